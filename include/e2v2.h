@@ -1,0 +1,188 @@
+/*
+ * e2v2 -- MI355X (gfx950) HIP library for the E2Former-V2 sparse equivariant
+ * attention path.  C ABI: plain pointers and sizes, no torch types.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer owned by the caller (the PyTorch caching
+ *     allocator in this repository).  The library never allocates or frees.
+ *   - Every call enqueues work on the given stream and returns 0 on success or
+ *     a nonzero code; e2v2_last_error() returns the message of the last failure
+ *     on the calling thread.
+ *   - Atoms of a batch are flattened; graph g owns atoms [graph_atom_ptr[g],
+ *     graph_atom_ptr[g+1]).  Edge e = (i <- j, shift s) lives in row i of the
+ *     query CSR; its source position is pos[j] + s . cell.
+ *   - Results are deterministic: no floating-point atomics; column sums use
+ *     the key CSR (edges of each source atom sorted by edge id).
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   e2v2_nbr_*          CellExpander.expand_includeself + construct_radius_neighbor
+ *                       src/molfm/models/e2former/module_utils.py:1065-1274, 3119-3242
+ *                       (FAISS twin: src/molfm/models/e2former/sp/dist_ner.py:27-86, 240-333)
+ *   e2v2_csr_transpose  prepare_sparse_qk_edge_index_metadata
+ *                       src/molfm/models/e2former/triton_dr/triton_sparse_qk_autograd.py:601-652
+ *   e2v2_mlp_fwd/bwd    GaussianSmearing + RadialProfile over x_edge = [rbf, tgt, src]
+ *                       src/molfm/models/e2former/e2former.py:258-266, 302 (fc_easy) and
+ *                       e2former.py:709-733 (gbf_projs); module_utils.py:1853-1869, 2151-2178
+ *   e2v2_attn_fwd       sparse_qk_edge_index_triton (triton_sparse_qk_autograd.py:839-871),
+ *                       segmented softmax e2former.py:327-367 with
+ *                       sparse_alpha_sum_edge_index_triton (sparse_alpha_sum_edge_index_autograd.py:207-213),
+ *                       sparse_v_agg_edge_index_triton_cblocked (sparse_v_agg_edge_index_cblocked_bench.py:428-449)
+ *                       and E2TensorProductSO2_FirstOrder.forward up to forward_linear
+ *                       (src/molfm/models/e2former/wigner6j/so2_tensor_product.py:341-385)
+ *   e2v2_attn_bwd       the first-order backward of the above autograd Functions
+ *                       (triton_sparse_qk_autograd.py:740-749, sparse_alpha_sum_edge_index_autograd.py:155-169,
+ *                        sparse_v_agg_edge_index_cblocked_bench.py:348-357)
+ *   e2v2_deg_fwd/bwd    edge_degree_outer_triton (triton_dr/edge_degree_outer_autograd.py:299-375) with the
+ *                       spherical harmonics and envelope of EdgeDegreeEmbeddingNetwork_higherorder.forward
+ *                       (e2former.py:689-753)
+ *   e2v2_edge_to_pos    autograd of f_edge_vec / f_dist w.r.t. positions (module_utils.py:3161-3206),
+ *                       consumed by GradientHead (src/molfm/pipeline/head.py:305-328)
+ */
+#ifndef E2V2_H
+#define E2V2_H
+
+#include <stdint.h>
+#include <stddef.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define E2V2_MAX_MLP 3
+
+const char* e2v2_last_error(void);
+int e2v2_version(void);
+
+/* ---- utilities -------------------------------------------------------- */
+int e2v2_fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s);
+int e2v2_fill_f32(float* p, float v, int64_t n, hipStream_t s);
+/* exclusive scan: out[0..n], out[n] = total; stats[0] = total, stats[1] = max(in) */
+int e2v2_scan_i32(const int32_t* in, int n, int32_t* out, int32_t* stats, hipStream_t s);
+
+/* ---- radius graph ------------------------------------------------------ */
+typedef struct e2v2_nbr_plan {
+  int32_t n_atoms, n_graphs, n_bins, n_shifts;
+  float rc, rmin;                   /* keep rmin <= d <= rc (both inclusive)                */
+  const float* pos;                 /* [n_atoms, 3]                                         */
+  const int32_t* atom_graph;        /* [n_atoms]                                            */
+  const int32_t* graph_atom_ptr;    /* [n_graphs + 1]                                       */
+  const int32_t* graph_shift_ptr;   /* [n_graphs + 1] rows of shift_off per graph            */
+  const int32_t* graph_periodic;    /* [n_graphs] 1 if any periodic direction               */
+  const float* shift_off;           /* [n_shifts, 3] fp32 offsets s . cell                  */
+  const float* grid_lo;             /* [n_graphs, 3] bin grid origin                        */
+  const float* grid_h;              /* [n_graphs, 3] bin edge (>= rc)                       */
+  const int32_t* grid_dim;          /* [n_graphs, 3]                                        */
+  const int32_t* bin_base;          /* [n_graphs] first bin of each graph                   */
+  int32_t* atom_bin;                /* workspace [n_atoms]                                  */
+  int32_t* bin_count;               /* workspace [n_bins]                                   */
+  int32_t* bin_start;               /* workspace [n_bins + 1]                               */
+  int32_t* bin_atoms;               /* workspace [n_atoms]                                  */
+  int32_t* stats;                   /* workspace [2] (scan total / max)                     */
+} e2v2_nbr_plan;
+
+int e2v2_nbr_bin(const e2v2_nbr_plan* plan, hipStream_t s);
+/* row_count [n_atoms]; row_ptr [n_atoms+1]; plan->stats = {E, max row} */
+int e2v2_nbr_count(const e2v2_nbr_plan* plan, int32_t* row_count, int32_t* row_ptr, hipStream_t s);
+/* rows sorted by (distance, j, shift); tmp_* are [E] (tmp_dvec [E,3]) scratch */
+int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, int64_t n_edges, int max_row,
+                  int32_t* tmp_col, int32_t* tmp_shift, float* tmp_dvec, float* tmp_dist, uint64_t* tmp_key,
+                  int32_t* col, int32_t* shift, float* dvec, float* dist, hipStream_t s);
+/* keep the k nearest of each sorted row: phase 0 counts + scans (stats = {E', max}), phase 1 compacts */
+int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* cnt, int32_t* new_ptr, int32_t* stats,
+                  const int32_t* col, const int32_t* shift, const float* dvec, const float* dist,
+                  int32_t* ocol, int32_t* oshift, float* odv, float* od, int phase, hipStream_t s);
+/* key CSR: phase 0 -> edge_row, key_ptr, stats = {E, max column}; phase 1 -> key_eid (sorted by edge id) */
+int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, int n_cols, int64_t n_edges,
+                       int32_t* edge_row, int32_t* key_cnt, int32_t* key_ptr, int32_t* stats,
+                       uint64_t* tmp_key, int32_t* key_eid, int phase, hipStream_t s);
+
+/* ---- edge radial MLP --------------------------------------------------- */
+typedef struct e2v2_mlp_weights {
+  const float* w1t;   /* [256][128]  rbf block of Linear1, transposed             */
+  const float* ttgt;  /* [types][128] target-type block of Linear1 + bias         */
+  const float* tsrc;  /* [types][128] source-type block of Linear1                */
+  const float* g1; const float* be1;   /* LayerNorm(128)                            */
+  const float* w2t;   /* [128][128] Linear2 transposed                            */
+  const float* b2;
+  const float* g2; const float* be2;
+  const float* w3t;   /* [128][256] Linear3 transposed                            */
+  const float* b3;
+  const float* w1;    /* [128][ldw1] Linear1 as stored (rbf block = columns 0..255) */
+  int32_t ldw1;
+  const float* w2;    /* [128][128] Linear2 as stored                             */
+  const float* w3;    /* [256][128] Linear3 as stored                             */
+} e2v2_mlp_weights;
+
+typedef struct e2v2_mlp_args {
+  int64_t n_edges;
+  int32_t n_mlp;                 /* 1..E2V2_MAX_MLP profiles sharing the edge input */
+  const float* dist;             /* [E]                                            */
+  const int32_t* edge_row;       /* [E] query atom                                 */
+  const int32_t* col;            /* [E] source atom                                */
+  const int32_t* node_type;      /* [N] atomic numbers                             */
+  const float* rbf_offset;       /* [256] Gaussian centres                         */
+  float rbf_coeff;               /* -0.5 / width^2                                 */
+  e2v2_mlp_weights w[E2V2_MAX_MLP];
+} e2v2_mlp_args;
+
+/* out[e, 256 m + c] for profile m */
+int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hipStream_t s);
+/* dd[e] (+)= sum_m dL/dout_m . dout_m/dd  (input gradient w.r.t. the edge distance only) */
+int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_dout, float* dd, int accumulate,
+                 hipStream_t s);
+
+/* ---- attention --------------------------------------------------------- */
+typedef struct e2v2_attn_args {
+  int32_t n_rows;                /* N query atoms (= source atoms)                  */
+  int64_t n_edges;
+  int32_t n_heads, head_dim, channels;   /* must be 128, 8, 256                     */
+  const int32_t* row_ptr;        /* [N+1] query CSR                                 */
+  const int32_t* col;            /* [E]                                             */
+  const int32_t* edge_row;       /* [E]                                             */
+  const int32_t* key_ptr;        /* [N+1] key CSR                                   */
+  const int32_t* key_eid;        /* [E]                                             */
+  const float* dvec;             /* [E,3] pos_i - (pos_j + s.cell)                   */
+  const float* dist;             /* [E]                                             */
+  const float* q;                /* [N,H,D]                                         */
+  const float* k;                /* [N,H,D]                                         */
+  const float* v;                /* [N,9,C]                                         */
+  const float* gi;               /* [E,2H] gate | inputhead                         */
+  float q_div;                   /* sqrt(D)                                         */
+  float rc, env_a, env_b, env_c; /* polynomial envelope                             */
+} e2v2_attn_args;
+
+/* out [N,20,C]; mrow/srow [N,H] softmax max / sum; cnt [N,H] number of maxima */
+int e2v2_attn_fwd(const e2v2_attn_args* args, float* out, float* mrow, float* srow, int32_t* cnt, hipStream_t s);
+/* grad_out, out [N,20,C] -> dgi [E,2H], ddvec [E,3], ddist [E], dq, dk [N,H,D], dv [N,9,C];
+   w_edge, dqk_edge [E,H] are outputs consumed by the column pass */
+int e2v2_attn_bwd(const e2v2_attn_args* args, const float* grad_out, const float* out, const float* mrow,
+                  const float* srow, const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq,
+                  float* dk, float* dv, float* w_edge, float* dqk_edge, hipStream_t s);
+
+/* ---- edge-degree embedding -------------------------------------------- */
+typedef struct e2v2_deg_args {
+  int32_t n_rows;
+  int64_t n_edges;
+  int32_t channels;              /* 256                                             */
+  const int32_t* row_ptr;
+  const float* dvec;             /* [E,3]                                           */
+  const float* dist;             /* [E]                                             */
+  const float* fea;              /* [E,3,C] radial-MLP outputs for l = 0, 1, 2      */
+  float avg;                     /* avg_aggregate_num                               */
+  float rc, env_a, env_b, env_c;
+} e2v2_deg_args;
+
+int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s);
+int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* dfea, float* ddvec, float* ddist,
+                 hipStream_t s);
+
+/* ---- positions --------------------------------------------------------- */
+int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,
+                     const float* dvec, const float* dist, const float* ddvec, const float* ddist, float* dpos,
+                     hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* E2V2_H */

@@ -1,0 +1,68 @@
+"""Plain-PyTorch references of the HIP operators (float64, CPU, autograd-able).
+
+Each one restates the reference's own torch formulation of the op:
+* ``mlp_ref``   RadialProfile(cat[rbf, tgt[z_i], src[z_j]])      e2former.py:258-266,302
+* ``attn_ref``  logits/softmax/aggregation of e2former.py:327-433 with the
+                first-order product written as the per-edge Cartesian coupling
+* ``deg_ref``   EdgeDegreeEmbeddingNetwork_higherorder fallback   e2former.py:689-753
+"""
+import math
+
+import numpy as np
+import torch
+
+ENV = (-21.0, 35.0, -15.0)
+
+
+def envelope(d, rc):
+    r = d / rc
+    return torch.where(r < 1, 1 + r ** 5 * (ENV[0] + r * (ENV[1] + ENV[2] * r)), torch.zeros_like(r))
+
+
+def rbf(d, offset, coeff):
+    return torch.exp(coeff * (d.view(-1, 1) - offset.view(1, -1)) ** 2)
+
+
+def mlp_ref(d, zi, zj, net, tgt_w, src_w, offset, coeff):
+    x = torch.cat([rbf(d, offset, coeff), tgt_w[zi], src_w[zj]], dim=-1)
+    return net(x)
+
+
+def attn_ref(q, k, v, dvec, dist, row, col, gi, T, rc, N):
+    E = row.shape[0]
+    H = q.shape[1]
+    qs = q / math.sqrt(q.shape[-1])
+    qk = (qs[row] * k[col]).sum(-1)
+    gate, ih = gi[:, :H], gi[:, H:]
+    a = gate * qk
+    rh = row.view(-1, 1).expand(-1, H)
+    amax = torch.full((N, H), -torch.inf, dtype=a.dtype).scatter_reduce(0, rh, a, "amax", include_self=True)
+    e = torch.exp(a - amax[row]) * envelope(dist, rc).unsqueeze(-1)
+    s = torch.zeros((N, H), dtype=a.dtype).scatter_add(0, rh, e)
+    alpha = e * ih / (s[row] + 1e-3)
+    w = alpha / dist.clamp_min(1e-6).unsqueeze(-1)
+    C = v.shape[-1]
+    wc = w[:, torch.arange(C) % H]                       # [E, C]
+    vj = v[col]                                          # [E, 9, C]
+    M = torch.einsum("trk,ek->etr", T, dvec)             # [E, 20, 9]
+    contrib = torch.einsum("etr,erc->etc", M, vj) * wc.unsqueeze(1)
+    out = torch.zeros((N, T.shape[0], C), dtype=contrib.dtype).index_add(0, row, contrib)
+    return out
+
+
+def raw_sh(u):
+    x, y, z = u[:, 0], u[:, 1], u[:, 2]
+    s3 = math.sqrt(3.0)
+    return torch.stack([torch.ones_like(x), x, y, z, s3 * x * z, s3 * x * y, y ** 2 - 0.5 * (x ** 2 + z ** 2),
+                        s3 * y * z, s3 / 2 * (z ** 2 - x ** 2)], dim=-1)
+
+
+def deg_ref(dvec, dist, row, fea, avg, rc, N):
+    u = torch.nn.functional.normalize(dvec, dim=-1)
+    Y = raw_sh(u)
+    p = envelope(dist, rc).unsqueeze(-1)
+    C = fea.shape[-1] // 3
+    f = fea.view(-1, 3, C) * p.unsqueeze(-1)
+    lidx = torch.tensor([0, 1, 1, 1, 2, 2, 2, 2, 2])
+    contrib = Y.unsqueeze(-1) * f[:, lidx, :]
+    return torch.zeros((N, 9, C), dtype=contrib.dtype).index_add(0, row, contrib) / avg

@@ -1,0 +1,96 @@
+"""Radius graph from the HIP cell-list builder vs the exact fp32 oracle.
+
+Bar: the canonical (i, j, shift) list is identical and dvec / d agree bitwise
+(both sides evaluate the same fp32 expression).  Edges within 2 ulp of the
+cutoff are counted and reported separately (their membership can differ from
+torch.linalg.norm rounding in the reference).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.neighbors import exact_neighbors
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(pkg, cuda, sysd, rc=6.0, label=""):
+    from ubio_molfm_amd import neighbors
+    pos = torch.as_tensor(sysd["pos"], device=cuda)
+    nl = neighbors.build_neighbors(pos, sysd["graph_ptr"], sysd["cell"], sysd["pbc"], rc)
+    got = nl.canonical()
+    ref = exact_neighbors(sysd["pos"], sysd["graph_ptr"], sysd["cell"], sysd["pbc"], rc)
+    shell = int(np.sum(np.abs(ref["d"] - np.float32(rc)) <= 2 * np.spacing(np.float32(rc))))
+    print(f"[nbr {label}] N={len(sysd['pos'])} E={nl.n_edges} oracle E={len(ref['i'])} "
+          f"max_row={nl.max_row} near-cutoff(2ulp)={shell}", flush=True)
+    assert nl.n_edges == len(ref["i"])
+    for k in ("i", "j", "s"):
+        assert np.array_equal(got[k], ref[k]), k
+    assert np.array_equal(got["dv"].view(np.uint32), ref["dv"].view(np.uint32))
+    assert np.array_equal(got["d"].view(np.uint32), ref["d"].view(np.uint32))
+    # rows sorted by distance
+    rp = nl.row_ptr.cpu().numpy(); d = nl.dist.cpu().numpy()
+    for r in range(min(len(rp) - 1, 200)):
+        seg = d[rp[r]:rp[r + 1]]
+        assert np.all(seg[1:] >= seg[:-1])
+    # key CSR is the exact transpose, sorted by edge id
+    kp = nl.key_ptr.cpu().numpy(); ke = nl.key_eid.cpu().numpy(); col = nl.col.cpu().numpy()
+    assert kp[-1] == nl.n_edges
+    for j in range(len(kp) - 1):
+        seg = ke[kp[j]:kp[j + 1]]
+        assert np.all(col[seg] == j) and np.all(np.diff(seg) > 0)
+    return nl
+
+
+def test_small_cell_below_cutoff(pkg, cuda):
+    from ubio_molfm_amd import systems
+    _check(pkg, cuda, systems.small_water(8, 6.2, seed=0), label="small")
+
+
+def test_water_cfg1(pkg, cuda):
+    from ubio_molfm_amd import systems
+    _check(pkg, cuda, systems.CONFIGS[1](), label="cfg1")
+
+
+def test_peptide_cfg3(pkg, cuda):
+    from ubio_molfm_amd import systems
+    _check(pkg, cuda, systems.CONFIGS[3](), label="cfg3")
+
+
+def test_ragged_organics_cfg2(pkg, cuda):
+    from ubio_molfm_amd import systems
+    _check(pkg, cuda, systems.CONFIGS[2](), label="cfg2")
+
+
+def test_triclinic_partial_pbc(pkg, cuda):
+    rng = np.random.default_rng(5)
+    cell = np.array([[9.0, 0.0, 0.0], [2.5, 8.0, 0.0], [1.0, -1.5, 10.0]], np.float32)
+    frac = rng.uniform(0, 1, size=(60, 3))
+    pos = (frac @ cell).astype(np.float32)
+    sysd = dict(pos=pos, Z=np.full(60, 6), graph_ptr=np.array([0, 60]), cell=cell[None],
+                pbc=np.array([[True, False, True]]))
+    _check(pkg, cuda, sysd, label="triclinic")
+
+
+def test_max_neighbors_keeps_nearest(pkg, cuda):
+    from ubio_molfm_amd import neighbors, systems
+    s = systems.CONFIGS[1]()
+    pos = torch.as_tensor(s["pos"], device=cuda)
+    full = neighbors.build_neighbors(pos, s["graph_ptr"], s["cell"], s["pbc"], 6.0)
+    top = neighbors.build_neighbors(pos, s["graph_ptr"], s["cell"], s["pbc"], 6.0, max_neighbors=32)
+    rp, rpt = full.row_ptr.cpu().numpy(), top.row_ptr.cpu().numpy()
+    d, dt = full.dist.cpu().numpy(), top.dist.cpu().numpy()
+    c, ct = full.col.cpu().numpy(), top.col.cpu().numpy()
+    for r in range(len(rp) - 1):
+        n = min(32, rp[r + 1] - rp[r])
+        assert rpt[r + 1] - rpt[r] == n
+        assert np.array_equal(d[rp[r]:rp[r] + n], dt[rpt[r]:rpt[r + 1]])
+        assert np.array_equal(c[rp[r]:rp[r] + n], ct[rpt[r]:rpt[r + 1]])
+
+
+def test_empty_and_isolated(pkg, cuda):
+    # two far-apart atoms in a non-periodic graph: no edges at all
+    sysd = dict(pos=np.array([[0, 0, 0], [50, 0, 0]], np.float32), Z=np.array([1, 1]), graph_ptr=np.array([0, 2]),
+                cell=np.zeros((1, 3, 3), np.float32), pbc=np.zeros((1, 3), bool))
+    nl = _check(pkg, cuda, sysd, label="isolated")
+    assert nl.n_edges == 0

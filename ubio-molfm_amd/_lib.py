@@ -1,0 +1,80 @@
+"""ctypes binding of libe2v2.so (the C ABI declared in include/e2v2.h).
+
+There is no fallback: if the library is missing or a call fails, a
+RuntimeError names the entry point and the library's own message.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libe2v2.so"
+
+i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
+
+EXPORTS = [
+    "e2v2_last_error", "e2v2_version", "e2v2_fill_i32", "e2v2_fill_f32", "e2v2_scan_i32",
+    "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose",
+    "e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
+    "e2v2_edge_to_pos",
+]
+
+
+class NbrPlan(C.Structure):
+    _fields_ = [("n_atoms", i32), ("n_graphs", i32), ("n_bins", i32), ("n_shifts", i32),
+                ("rc", f32), ("rmin", f32),
+                ("pos", vp), ("atom_graph", vp), ("graph_atom_ptr", vp), ("graph_shift_ptr", vp),
+                ("graph_periodic", vp), ("shift_off", vp), ("grid_lo", vp), ("grid_h", vp), ("grid_dim", vp),
+                ("bin_base", vp), ("atom_bin", vp), ("bin_count", vp), ("bin_start", vp), ("bin_atoms", vp),
+                ("stats", vp)]
+
+
+class MlpWeights(C.Structure):
+    _fields_ = [("w1t", vp), ("ttgt", vp), ("tsrc", vp), ("g1", vp), ("be1", vp), ("w2t", vp), ("b2", vp),
+                ("g2", vp), ("be2", vp), ("w3t", vp), ("b3", vp), ("w1", vp), ("ldw1", i32), ("w2", vp),
+                ("w3", vp)]
+
+
+class MlpArgs(C.Structure):
+    _fields_ = [("n_edges", i64), ("n_mlp", i32), ("dist", vp), ("edge_row", vp), ("col", vp),
+                ("node_type", vp), ("rbf_offset", vp), ("rbf_coeff", f32), ("w", MlpWeights * 3)]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [("n_rows", i32), ("n_edges", i64), ("n_heads", i32), ("head_dim", i32), ("channels", i32),
+                ("row_ptr", vp), ("col", vp), ("edge_row", vp), ("key_ptr", vp), ("key_eid", vp),
+                ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("gi", vp),
+                ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32)]
+
+
+class DegArgs(C.Structure):
+    _fields_ = [("n_rows", i32), ("n_edges", i64), ("channels", i32), ("row_ptr", vp), ("dvec", vp),
+                ("dist", vp), ("fea", vp), ("avg", f32), ("rc", f32), ("env_a", f32), ("env_b", f32),
+                ("env_c", f32)]
+
+
+_lib = None
+
+
+def load():
+    """Load libe2v2.so once; raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python ubio-molfm_amd/build.py` "
+                           "or __graft_entry__.build() (there is no CPU fallback)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name in EXPORTS:
+        getattr(lib, name)  # raises AttributeError if a symbol is absent
+    lib.e2v2_last_error.restype = C.c_char_p
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.e2v2_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (code {rc}): {msg}")

@@ -1,0 +1,406 @@
+// Sparse equivariant attention of one E2Former-V2 layer on the query CSR.
+//
+// Forward (one workgroup per query atom i, online segmented softmax):
+//   a_e[h]   = gate_e[h] * <q_i[h]/sqrt(D), k_j[h]>
+//   m[h]     = max_e a_e[h];  e_e = exp(a_e - m) p(d_e);  s = sum_e e_e
+//   w_e[h]   = e_e ih_e[h] / (s + 1e-3) / max(d_e, 1e-6)
+//   out[t,c] = sum_e w_e[h(c)] sum_{r,k} T[t,r,k] v_j[r,c] dvec_e[k]     (h(c) = c % 128)
+// which equals the reference's gather-scale-scatter of the merged node-frame
+// tensor followed by the SO(2) unrotation, h_a - h_b before forward_linear
+// (src/molfm/models/e2former/e2former.py:327-433,
+//  wigner6j/so2_tensor_product.py:341-385): TP(v, r_i) - TP(v, r_j) = TP(v, r_ij).
+// Backward: row pass (dq, dgate, dih, w, dqk, dvec/ddist partials; the softmax
+// row terms come from D_h = sum_{c in h} sum_t G[t,c] out[t,c]) and a column
+// pass over the key CSR (dv_j, dk_j) with no atomics.
+#include "common.h"
+#include "tp_table.h"
+#include "../../include/e2v2.h"
+
+namespace e2v2 {
+
+constexpr int kH = 128, kD = 8, kC = 256, kNV = 9, kNT = 20, kCH = 32, kCHB = 16;
+constexpr float kEps = 1e-3f;
+
+__device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
+  Envelope E;
+  E.rc = A.rc; E.a = A.env_a; E.b = A.env_b; E.c = A.env_c;
+  return E;
+}
+
+// <q_s, k_j[h]> with q_s already divided by sqrt(D); identical code in every pass
+__device__ __forceinline__ float qk_dot(const float (&qs)[kD], const float* __restrict__ kp) {
+  const float4 k0 = reinterpret_cast<const float4*>(kp)[0];
+  const float4 k1 = reinterpret_cast<const float4*>(kp)[1];
+  float s = qs[0] * k0.x;
+  s = fmaf(qs[1], k0.y, s);
+  s = fmaf(qs[2], k0.z, s);
+  s = fmaf(qs[3], k0.w, s);
+  s = fmaf(qs[4], k1.x, s);
+  s = fmaf(qs[5], k1.y, s);
+  s = fmaf(qs[6], k1.z, s);
+  s = fmaf(qs[7], k1.w, s);
+  return s;
+}
+
+__device__ __forceinline__ void load_qs(const e2v2_attn_args& A, int i, int h, float (&qs)[kD]) {
+  const float* qp = A.q + ((size_t)i * kH + h) * kD;
+#pragma unroll
+  for (int d = 0; d < kD; ++d) qs[d] = qp[d] / A.q_div;
+}
+
+struct ChunkEdges {
+  int j[kCH];
+  float dv[kCH][3];
+  float p[kCH];
+  float dp[kCH];
+  float R[kCH];
+  float d[kCH];
+};
+
+__device__ __forceinline__ void load_chunk(const e2v2_attn_args& A, const Envelope& env, int e0, int nc,
+                                           ChunkEdges& ce) {
+  const int t = threadIdx.x;
+  if (t < nc) {
+    const int64_t e = (int64_t)e0 + t;
+    ce.j[t] = A.col[e];
+    ce.dv[t][0] = A.dvec[3 * e];
+    ce.dv[t][1] = A.dvec[3 * e + 1];
+    ce.dv[t][2] = A.dvec[3 * e + 2];
+    const float d = A.dist[e];
+    ce.d[t] = d;
+    float p, dp;
+    env.eval(d, p, dp);
+    ce.p[t] = p;
+    ce.dp[t] = dp;
+    ce.R[t] = fmaxf(d, 1e-6f);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __restrict__ out, float* __restrict__ mrow,
+                                                  float* __restrict__ srow, int32_t* __restrict__ cnt) {
+  __shared__ float a_s[kCH][kH];
+  __shared__ float coef_s[kCH][kH];
+  __shared__ float scale_s[kH];
+  __shared__ float inv_s[kH];
+  __shared__ ChunkEdges ce;
+  const int i = blockIdx.x, t = threadIdx.x;
+  const int h = t & (kH - 1), half = t >> 7;
+  const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
+  const Envelope env = make_env(A);
+  float qs[kD];
+  load_qs(A, i, h, qs);
+  float m_run = -INFINITY, s_run = 0.f;
+  int c_run = 0;
+  float acc[kNV][3];
+#pragma unroll
+  for (int r = 0; r < kNV; ++r) acc[r][0] = acc[r][1] = acc[r][2] = 0.f;
+  const int hc = t & (kH - 1);  // head of channel c = t
+  for (int c0 = 0; c0 < n; c0 += kCH) {
+    const int nc = min(kCH, n - c0);
+    load_chunk(A, env, b + c0, nc, ce);
+    __syncthreads();
+    for (int el = half; el < nc; el += 2) {
+      const int64_t e = (int64_t)b + c0 + el;
+      const float qk = qk_dot(qs, A.k + ((size_t)ce.j[el] * kH + h) * kD);
+      a_s[el][h] = A.gi[e * (2 * kH) + h] * qk;
+    }
+    __syncthreads();
+    if (t < kH) {
+      float cm = -INFINITY;
+      for (int el = 0; el < nc; ++el) cm = fmaxf(cm, a_s[el][h]);
+      const float m_new = fmaxf(m_run, cm);
+      const float sc = (m_run == -INFINITY) ? 0.f : expf(m_run - m_new);
+      int cc = 0;
+      for (int el = 0; el < nc; ++el) cc += (a_s[el][h] == m_new);
+      c_run = (m_new == m_run) ? c_run + cc : cc;
+      s_run *= sc;
+      for (int el = 0; el < nc; ++el) {
+        const int64_t e = (int64_t)b + c0 + el;
+        const float ex = expf(a_s[el][h] - m_new);
+        const float ee = ex * ce.p[el];
+        s_run += ee;
+        const float ih = A.gi[e * (2 * kH) + kH + h];
+        coef_s[el][h] = (ee * ih) / ce.R[el];
+      }
+      m_run = m_new;
+      scale_s[h] = sc;
+    }
+    __syncthreads();
+    {
+      const float sc = scale_s[hc];
+      if (sc != 1.f) {
+#pragma unroll
+        for (int r = 0; r < kNV; ++r) {
+          acc[r][0] *= sc; acc[r][1] *= sc; acc[r][2] *= sc;
+        }
+      }
+      for (int el = 0; el < nc; ++el) {
+        const float w = coef_s[el][hc];
+        const float wx = w * ce.dv[el][0], wy = w * ce.dv[el][1], wz = w * ce.dv[el][2];
+        const float* vp = A.v + (size_t)ce.j[el] * (kNV * kC) + t;
+        float vv[kNV];
+#pragma unroll
+        for (int r = 0; r < kNV; ++r) vv[r] = vp[r * kC];
+#pragma unroll
+        for (int r = 0; r < kNV; ++r) {
+          acc[r][0] = fmaf(vv[r], wx, acc[r][0]);
+          acc[r][1] = fmaf(vv[r], wy, acc[r][1]);
+          acc[r][2] = fmaf(vv[r], wz, acc[r][2]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (t < kH) {
+    inv_s[h] = 1.0f / (s_run + kEps);
+    mrow[(size_t)i * kH + h] = m_run;
+    srow[(size_t)i * kH + h] = s_run;
+    cnt[(size_t)i * kH + h] = c_run;
+  }
+  __syncthreads();
+  const float inv = inv_s[hc];
+  float o[kNT];
+#pragma unroll
+  for (int q = 0; q < kNT; ++q) o[q] = 0.f;
+#pragma unroll
+  for (int z = 0; z < kTpNnz; ++z) o[kTp[z].t] = fmaf(kTp[z].c, acc[kTp[z].r][kTp[z].k], o[kTp[z].t]);
+  float* op = out + (size_t)i * (kNT * kC) + t;
+#pragma unroll
+  for (int q = 0; q < kNT; ++q) op[q * kC] = o[q] * inv;
+}
+
+// dA[r][k] = sum_t T[t][r][k] g[t] for one channel
+__device__ __forceinline__ void tp_transpose(const float (&g)[kNT], float (&dA)[kNV][3]) {
+#pragma unroll
+  for (int r = 0; r < kNV; ++r) dA[r][0] = dA[r][1] = dA[r][2] = 0.f;
+#pragma unroll
+  for (int z = 0; z < kTpNnz; ++z) dA[kTp[z].r][kTp[z].k] = fmaf(kTp[z].c, g[kTp[z].t], dA[kTp[z].r][kTp[z].k]);
+}
+
+__global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const float* __restrict__ G,
+                                                      const float* __restrict__ O, const float* __restrict__ mrow,
+                                                      const float* __restrict__ srow, const int32_t* __restrict__ cnt,
+                                                      float* __restrict__ dgi, float* __restrict__ ddv,
+                                                      float* __restrict__ dd, float* __restrict__ dq,
+                                                      float* __restrict__ w_out, float* __restrict__ dqk_out) {
+  __shared__ float a_s[kCHB][kH];
+  __shared__ float qk_s[kCHB][kH];
+  __shared__ float w_s[kCHB][kH];
+  __shared__ float dw_s[kCHB][kH];
+  __shared__ float ddv_s[kCHB][3];
+  __shared__ float dd_s[kCHB][2];
+  __shared__ float head_m[kH], head_inv[kH], head_dsum[kH], head_dmc[kH];
+  __shared__ float dq_s[kH][kD];
+  __shared__ ChunkEdges ce;
+  const int i = blockIdx.x, t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int h = t & (kH - 1), half = t >> 7;
+  const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
+  const Envelope env = make_env(A);
+  // ---- per-row prologue: dA for the lane's 4 channels c = lane + 64 q
+  float dA[4][kNV][3];
+  float gdot[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = lane + 64 * q;
+    float g[kNT];
+    float sdot = 0.f;
+#pragma unroll
+    for (int z = 0; z < kNT; ++z) {
+      g[z] = G[(size_t)i * (kNT * kC) + z * kC + c];
+      sdot = fmaf(g[z], O[(size_t)i * (kNT * kC) + z * kC + c], sdot);
+    }
+    tp_transpose(g, dA[q]);
+    gdot[q] = sdot;
+  }
+  if (wave == 0) {
+    // head lane: channels lane, lane+128; head lane+64: channels lane+64, lane+192
+    const float Dh0 = gdot[0] + gdot[2];
+    const float Dh1 = gdot[1] + gdot[3];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int hh = lane + 64 * u;
+      const float Dh = u ? Dh1 : Dh0;
+      const float s = srow[(size_t)i * kH + hh];
+      const float inv = 1.0f / (s + kEps);
+      const int cn = cnt[(size_t)i * kH + hh];
+      head_m[hh] = mrow[(size_t)i * kH + hh];
+      head_inv[hh] = inv;
+      head_dsum[hh] = Dh * inv;
+      head_dmc[hh] = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
+    }
+  }
+  float qs[kD];
+  load_qs(A, i, h, qs);
+  float dqa[kD];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) dqa[d] = 0.f;
+  __syncthreads();
+  for (int c0 = 0; c0 < n; c0 += kCHB) {
+    const int nc = min(kCHB, n - c0);
+    load_chunk(A, env, b + c0, nc, ce);
+    __syncthreads();
+    // recompute logits and final weights
+    for (int el = half; el < nc; el += 2) {
+      const int64_t e = (int64_t)b + c0 + el;
+      const float qk = qk_dot(qs, A.k + ((size_t)ce.j[el] * kH + h) * kD);
+      const float a = A.gi[e * (2 * kH) + h] * qk;
+      a_s[el][h] = a;
+      qk_s[el][h] = qk;
+      const float ee = expf(a - head_m[h]) * ce.p[el];
+      const float alpha = (ee * A.gi[e * (2 * kH) + kH + h]) * head_inv[h];
+      const float w = alpha / ce.R[el];
+      w_s[el][h] = w;
+      w_out[e * kH + h] = w;
+    }
+    __syncthreads();
+    // transposed aggregation: one wave per edge
+    for (int el = wave; el < nc; el += 4) {
+      const float dvx = ce.dv[el][0], dvy = ce.dv[el][1], dvz = ce.dv[el][2];
+      const float* vp = A.v + (size_t)ce.j[el] * (kNV * kC) + lane;
+      float gx = 0.f, gy = 0.f, gz = 0.f;
+      float dwc[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float ux = 0.f, uy = 0.f, uz = 0.f;
+#pragma unroll
+        for (int r = 0; r < kNV; ++r) {
+          const float vr = vp[r * kC + 64 * q];
+          ux = fmaf(dA[q][r][0], vr, ux);
+          uy = fmaf(dA[q][r][1], vr, uy);
+          uz = fmaf(dA[q][r][2], vr, uz);
+        }
+        dwc[q] = ux * dvx + uy * dvy + uz * dvz;
+        const float w = w_s[el][(lane + 64 * q) & (kH - 1)];
+        gx = fmaf(w, ux, gx);
+        gy = fmaf(w, uy, gy);
+        gz = fmaf(w, uz, gz);
+      }
+      dw_s[el][lane] = dwc[0] + dwc[2];
+      dw_s[el][lane + 64] = dwc[1] + dwc[3];
+      gx = wave_sum(gx);
+      gy = wave_sum(gy);
+      gz = wave_sum(gz);
+      if (lane == 0) {
+        ddv_s[el][0] = gx;
+        ddv_s[el][1] = gy;
+        ddv_s[el][2] = gz;
+      }
+    }
+    __syncthreads();
+    // softmax / gate / distance backward: thread per (head, edge parity)
+    for (int el = half; el < nc; el += 2) {
+      const int64_t e = (int64_t)b + c0 + el;
+      const float dw = dw_s[el][h];
+      const float a = a_s[el][h];
+      const float qk = qk_s[el][h];
+      const float gate = A.gi[e * (2 * kH) + h];
+      const float ih = A.gi[e * (2 * kH) + kH + h];
+      const float ex = expf(a - head_m[h]);
+      const float ee = ex * ce.p[el];
+      const float inv = head_inv[h];
+      const float alpha = (ee * ih) * inv;
+      const float R = ce.R[el];
+      const float dalpha = dw / R;
+      const float dR = (ce.d[el] > 1e-6f) ? -dw * alpha / (R * R) : 0.f;
+      const float dih = dalpha * ee * inv;
+      const float de = dalpha * ih * inv - head_dsum[h];
+      float da = de * ee;
+      if (a == head_m[h]) da += head_dmc[h];
+      const float dpv = de * ex;
+      const float dgate = da * qk;
+      const float dqk = da * gate;
+      dgi[e * (2 * kH) + h] = dgate;
+      dgi[e * (2 * kH) + kH + h] = dih;
+      dqk_out[e * kH + h] = dqk;
+      const float* kp = A.k + ((size_t)ce.j[el] * kH + h) * kD;
+#pragma unroll
+      for (int d = 0; d < kD; ++d) dqa[d] = fmaf(dqk, kp[d], dqa[d]);
+      float ddist = fmaf(dpv, ce.dp[el], dR);
+      ddist = wave_sum(ddist);
+      if (lane == 0) dd_s[el][(t & (kH - 1)) >> 6] = ddist;
+    }
+    __syncthreads();
+    if (t < nc) {
+      const int64_t e = (int64_t)b + c0 + t;
+      ddv[3 * e] = ddv_s[t][0];
+      ddv[3 * e + 1] = ddv_s[t][1];
+      ddv[3 * e + 2] = ddv_s[t][2];
+      dd[e] = dd_s[t][0] + dd_s[t][1];
+    }
+    __syncthreads();
+  }
+  if (half == 1) {
+#pragma unroll
+    for (int d = 0; d < kD; ++d) dq_s[h][d] = dqa[d];
+  }
+  __syncthreads();
+  if (half == 0) {
+#pragma unroll
+    for (int d = 0; d < kD; ++d) dq[((size_t)i * kH + h) * kD + d] = (dqa[d] + dq_s[h][d]) / A.q_div;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const float* __restrict__ G,
+                                                      const float* __restrict__ w_e, const float* __restrict__ dqk_e,
+                                                      float* __restrict__ dv_out, float* __restrict__ dk_out) {
+  const int j = blockIdx.x, t = threadIdx.x;
+  const int c = t, hc = t & (kH - 1);
+  const int hk = t >> 1, d0 = 4 * (t & 1);
+  float av[kNV];
+#pragma unroll
+  for (int r = 0; r < kNV; ++r) av[r] = 0.f;
+  float ak[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int p = A.key_ptr[j]; p < A.key_ptr[j + 1]; ++p) {
+    const int64_t e = A.key_eid[p];
+    const int i = A.edge_row[e];
+    const float dvx = A.dvec[3 * e], dvy = A.dvec[3 * e + 1], dvz = A.dvec[3 * e + 2];
+    float g[kNT];
+#pragma unroll
+    for (int z = 0; z < kNT; ++z) g[z] = G[(size_t)i * (kNT * kC) + z * kC + c];
+    float dA[kNV][3];
+    tp_transpose(g, dA);
+    const float w = w_e[e * kH + hc];
+#pragma unroll
+    for (int r = 0; r < kNV; ++r) av[r] = fmaf(w, dA[r][0] * dvx + dA[r][1] * dvy + dA[r][2] * dvz, av[r]);
+    const float dqk = dqk_e[e * kH + hk];
+    const float* qp = A.q + ((size_t)i * kH + hk) * kD + d0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) ak[d] = fmaf(dqk, qp[d] / A.q_div, ak[d]);
+  }
+#pragma unroll
+  for (int r = 0; r < kNV; ++r) dv_out[(size_t)j * (kNV * kC) + r * kC + c] = av[r];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) dk_out[((size_t)j * kH + hk) * kD + d0 + d] = ak[d];
+}
+
+}  // namespace e2v2
+
+using namespace e2v2;
+
+E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, float* out, float* mrow, float* srow, int32_t* cnt,
+                           hipStream_t s) {
+  const e2v2_attn_args& A = *args;
+  E2V2_REQUIRE(A.n_heads == kH && A.head_dim == kD && A.channels == kC,
+               "attn_fwd: built for H=%d D=%d C=%d, got H=%d D=%d C=%d", kH, kD, kC, A.n_heads, A.head_dim,
+               A.channels);
+  if (A.n_rows == 0) return 0;
+  hipLaunchKernelGGL(k_attn_fwd, dim3(A.n_rows), dim3(256), 0, s, A, out, mrow, srow, cnt);
+  E2V2_LAUNCHED("k_attn_fwd");
+  return 0;
+}
+
+E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const float* grad_out, const float* out, const float* mrow,
+                           const float* srow, const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq,
+                           float* dk, float* dv, float* w_edge, float* dqk_edge, hipStream_t s) {
+  const e2v2_attn_args& A = *args;
+  E2V2_REQUIRE(A.n_heads == kH && A.head_dim == kD && A.channels == kC,
+               "attn_bwd: built for H=%d D=%d C=%d", kH, kD, kC);
+  if (A.n_rows == 0) return 0;
+  hipLaunchKernelGGL(k_attn_bwd_row, dim3(A.n_rows), dim3(256), 0, s, A, grad_out, out, mrow, srow, cnt, dgi, ddvec,
+                     ddist, dq, w_edge, dqk_edge);
+  E2V2_LAUNCHED("k_attn_bwd_row");
+  hipLaunchKernelGGL(k_attn_bwd_col, dim3(A.n_rows), dim3(256), 0, s, A, grad_out, w_edge, dqk_edge, dv, dk);
+  E2V2_LAUNCHED("k_attn_bwd_col");
+  return 0;
+}

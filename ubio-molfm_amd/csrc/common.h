@@ -1,0 +1,89 @@
+// Shared helpers for the e2v2 HIP library (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <math.h>
+
+#define E2V2_API extern "C" __attribute__((visibility("default")))
+
+namespace e2v2 {
+
+int set_error(int code, const char* fmt, ...);
+
+#define E2V2_TRY_HIP(expr)                                                          \
+  do {                                                                              \
+    hipError_t e_ = (expr);                                                         \
+    if (e_ != hipSuccess)                                                           \
+      return ::e2v2::set_error((int)e_, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+#define E2V2_LAUNCHED(name)                                                         \
+  do {                                                                              \
+    hipError_t e_ = hipGetLastError();                                              \
+    if (e_ != hipSuccess)                                                           \
+      return ::e2v2::set_error((int)e_, "launch of %s failed: %s", name, hipGetErrorString(e_)); \
+  } while (0)
+
+#define E2V2_REQUIRE(cond, ...)                                                     \
+  do {                                                                              \
+    if (!(cond)) return ::e2v2::set_error(-1, __VA_ARGS__);                         \
+  } while (0)
+
+constexpr int kWave = 64;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// The one fp32 distance expression shared with the CPU oracle:
+// d = sqrt((dx*dx + dy*dy) + dz*dz), every op rounded to fp32 (no FMA
+// contraction; __builtin_sqrtf is correctly rounded under HIP's default
+// -fhip-fp32-correctly-rounded-divide-sqrt).
+__device__ __forceinline__ float exact_dist(float dx, float dy, float dz) {
+#pragma clang fp contract(off)
+  float xx = dx * dx;
+  float yy = dy * dy;
+  float zz = dz * dz;
+  float s = (xx + yy) + zz;
+  return __builtin_sqrtf(s);
+}
+
+// img = pos_j + off; dv = pos_i - img (component-wise, rounded)
+__device__ __forceinline__ void exact_edge(const float* pi, const float* pj, const float* off,
+                                           float& dx, float& dy, float& dz) {
+#pragma clang fp contract(off)
+  float ix = pj[0] + off[0];
+  float iy = pj[1] + off[1];
+  float iz = pj[2] + off[2];
+  dx = pi[0] - ix;
+  dy = pi[1] - iy;
+  dz = pi[2] - iz;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// polynomial envelope (exponent 5): p = 1 + r^5 (a + r (b + c r)), 0 for r >= 1
+struct Envelope {
+  float rc, a, b, c;
+  __device__ __forceinline__ void eval(float d, float& p, float& dp_dd) const {
+    float r = d / rc;
+    if (r < 1.0f) {
+      float r2 = r * r, r4 = r2 * r2, r5 = r4 * r;
+      p = 1.0f + r5 * (a + r * (b + c * r));
+      dp_dd = r4 * (5.0f * a + r * (6.0f * b + 7.0f * c * r)) / rc;
+    } else {
+      p = 0.0f;
+      dp_dd = 0.0f;
+    }
+  }
+};
+
+}  // namespace e2v2

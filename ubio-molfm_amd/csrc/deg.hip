@@ -1,0 +1,203 @@
+// Edge-degree embedding (src/molfm/models/e2former/e2former.py:689-753) and
+// the edge -> position gradient assembly.
+//
+// Forward, one workgroup per query atom i (thread per channel c):
+//   x0[i, m, c] = (1/avg) sum_e Y_m(dvec_e / |dvec_e|) * fea_e[l(m), c] * p(d_e)
+// with Y the e3nn raw real spherical harmonics of degree <= 2 (unit norm per
+// l block) and fea the three radial-MLP outputs [E, 3, 256].
+// Backward: dfea (for the MLP backward), plus dL/ddvec and dL/dd per edge.
+#include "common.h"
+#include "../../include/e2v2.h"
+
+namespace e2v2 {
+
+constexpr int kDC = 256;
+
+__device__ __forceinline__ void raw_sh2(float x, float y, float z, float (&Y)[9]) {
+  const float s3 = 1.7320508075688772f;
+  Y[0] = 1.f;
+  Y[1] = x; Y[2] = y; Y[3] = z;
+  Y[4] = s3 * x * z;
+  Y[5] = s3 * x * y;
+  Y[6] = y * y - 0.5f * (x * x + z * z);
+  Y[7] = s3 * y * z;
+  Y[8] = s3 / 2.0f * (z * z - x * x);
+}
+
+// dY/du for u = (x, y, z) given dL/dY -> dL/du
+__device__ __forceinline__ void raw_sh2_bwd(float x, float y, float z, const float (&g)[9], float& gx, float& gy,
+                                            float& gz) {
+  const float s3 = 1.7320508075688772f;
+  gx = g[1] + s3 * z * g[4] + s3 * y * g[5] - x * g[6] - s3 * x * g[8];
+  gy = g[2] + s3 * x * g[5] + 2.f * y * g[6] + s3 * z * g[7];
+  gz = g[3] + s3 * x * g[4] - z * g[6] + s3 * y * g[7] + s3 * z * g[8];
+}
+
+__device__ __forceinline__ int l_of(int m) { return m == 0 ? 0 : (m < 4 ? 1 : 2); }
+
+__global__ __launch_bounds__(256) void k_deg_fwd(e2v2_deg_args A, float* __restrict__ x0) {
+  __shared__ float sh_s[32][9];
+  __shared__ float p_s[32];
+  __shared__ int64_t e_s[32];
+  const int i = blockIdx.x, c = threadIdx.x;
+  const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
+  Envelope env;
+  env.rc = A.rc; env.a = A.env_a; env.b = A.env_b; env.c = A.env_c;
+  float acc[9];
+#pragma unroll
+  for (int m = 0; m < 9; ++m) acc[m] = 0.f;
+  for (int c0 = 0; c0 < n; c0 += 32) {
+    const int nc = min(32, n - c0);
+    if (c < nc) {
+      const int64_t e = (int64_t)b + c0 + c;
+      const float d = A.dist[e];
+      const float nrm = fmaxf(d, 1e-12f);
+      float Y[9];
+      raw_sh2(A.dvec[3 * e] / nrm, A.dvec[3 * e + 1] / nrm, A.dvec[3 * e + 2] / nrm, Y);
+#pragma unroll
+      for (int m = 0; m < 9; ++m) sh_s[c][m] = Y[m];
+      float p, dp;
+      env.eval(d, p, dp);
+      p_s[c] = p;
+      e_s[c] = e;
+    }
+    __syncthreads();
+    for (int el = 0; el < nc; ++el) {
+      const float* f = A.fea + e_s[el] * (3 * kDC) + c;
+      const float p = p_s[el];
+      const float f0 = f[0] * p, f1 = f[kDC] * p, f2 = f[2 * kDC] * p;
+      acc[0] = fmaf(sh_s[el][0], f0, acc[0]);
+#pragma unroll
+      for (int m = 1; m < 4; ++m) acc[m] = fmaf(sh_s[el][m], f1, acc[m]);
+#pragma unroll
+      for (int m = 4; m < 9; ++m) acc[m] = fmaf(sh_s[el][m], f2, acc[m]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < 9; ++m) x0[((size_t)i * 9 + m) * kDC + c] = acc[m] / A.avg;
+}
+
+// one workgroup per query atom; one wave per edge, lane owns channels lane + 64 q
+__global__ __launch_bounds__(256) void k_deg_bwd(e2v2_deg_args A, const float* __restrict__ G0,
+                                                 float* __restrict__ dfea, float* __restrict__ ddv,
+                                                 float* __restrict__ dd) {
+  const int i = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
+  Envelope env;
+  env.rc = A.rc; env.a = A.env_a; env.b = A.env_b; env.c = A.env_c;
+  float g[4][9];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int m = 0; m < 9; ++m) g[q][m] = G0[((size_t)i * 9 + m) * kDC + lane + 64 * q] / A.avg;
+  for (int el = wave; el < n; el += 4) {
+    const int64_t e = (int64_t)b + el;
+    const float d = A.dist[e];
+    const float nrm = fmaxf(d, 1e-12f);
+    const float ux = A.dvec[3 * e] / nrm, uy = A.dvec[3 * e + 1] / nrm, uz = A.dvec[3 * e + 2] / nrm;
+    float Y[9];
+    raw_sh2(ux, uy, uz, Y);
+    float p, dpdd;
+    env.eval(d, p, dpdd);
+    float dsh[9];
+#pragma unroll
+    for (int m = 0; m < 9; ++m) dsh[m] = 0.f;
+    float dp = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = lane + 64 * q;
+      const float* f = A.fea + e * (3 * kDC) + c;
+      const float f0 = f[0], f1 = f[kDC], f2 = f[2 * kDC];
+      // d(edge_fea_l) = sum_{m in l} Y_m g_m
+      const float d0 = Y[0] * g[q][0];
+      const float d1 = Y[1] * g[q][1] + Y[2] * g[q][2] + Y[3] * g[q][3];
+      const float d2 = Y[4] * g[q][4] + Y[5] * g[q][5] + Y[6] * g[q][6] + Y[7] * g[q][7] + Y[8] * g[q][8];
+      float* df = dfea + e * (3 * kDC) + c;
+      df[0] = d0 * p;
+      df[kDC] = d1 * p;
+      df[2 * kDC] = d2 * p;
+      dp = fmaf(d0, f0, dp);
+      dp = fmaf(d1, f1, dp);
+      dp = fmaf(d2, f2, dp);
+      const float e0 = f0 * p, e1 = f1 * p, e2 = f2 * p;
+      dsh[0] = fmaf(g[q][0], e0, dsh[0]);
+#pragma unroll
+      for (int m = 1; m < 4; ++m) dsh[m] = fmaf(g[q][m], e1, dsh[m]);
+#pragma unroll
+      for (int m = 4; m < 9; ++m) dsh[m] = fmaf(g[q][m], e2, dsh[m]);
+    }
+    dp = wave_sum(dp);
+#pragma unroll
+    for (int m = 1; m < 9; ++m) dsh[m] = wave_sum(dsh[m]);
+    if (lane == 0) {
+      float gx, gy, gz;
+      raw_sh2_bwd(ux, uy, uz, dsh, gx, gy, gz);
+      // u = v / |v|:  dv = (du - u (u . du)) / |v|
+      const float ud = ux * gx + uy * gy + uz * gz;
+      ddv[3 * e] = (gx - ux * ud) / nrm;
+      ddv[3 * e + 1] = (gy - uy * ud) / nrm;
+      ddv[3 * e + 2] = (gz - uz * ud) / nrm;
+      dd[e] = dp * dpdd;
+    }
+  }
+}
+
+// dpos[a] = sum_{e in row a} g_e - sum_{e in column a} g_e,  g_e = ddv_e + dd_e dvec_e / d_e
+__global__ void k_edge_to_pos(int n_atoms, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ key_ptr,
+                              const int32_t* __restrict__ key_eid, const float* __restrict__ dvec,
+                              const float* __restrict__ dist, const float* __restrict__ ddv,
+                              const float* __restrict__ dd, float* __restrict__ dpos) {
+  const int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a >= n_atoms) return;
+  float gx = 0.f, gy = 0.f, gz = 0.f;
+  for (int e = row_ptr[a]; e < row_ptr[a + 1]; ++e) {
+    const float s = dd[e] / dist[e];
+    gx += ddv[3 * e] + s * dvec[3 * e];
+    gy += ddv[3 * e + 1] + s * dvec[3 * e + 1];
+    gz += ddv[3 * e + 2] + s * dvec[3 * e + 2];
+  }
+  for (int p = key_ptr[a]; p < key_ptr[a + 1]; ++p) {
+    const int64_t e = key_eid[p];
+    const float s = dd[e] / dist[e];
+    gx -= ddv[3 * e] + s * dvec[3 * e];
+    gy -= ddv[3 * e + 1] + s * dvec[3 * e + 1];
+    gz -= ddv[3 * e + 2] + s * dvec[3 * e + 2];
+  }
+  dpos[3 * a] = gx;
+  dpos[3 * a + 1] = gy;
+  dpos[3 * a + 2] = gz;
+}
+
+}  // namespace e2v2
+
+using namespace e2v2;
+
+E2V2_API int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s) {
+  const e2v2_deg_args& A = *args;
+  E2V2_REQUIRE(A.channels == kDC, "deg_fwd: built for C=%d, got %d", kDC, A.channels);
+  if (A.n_rows == 0) return 0;
+  hipLaunchKernelGGL(k_deg_fwd, dim3(A.n_rows), dim3(256), 0, s, A, x0);
+  E2V2_LAUNCHED("k_deg_fwd");
+  return 0;
+}
+
+E2V2_API int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* dfea, float* ddvec, float* ddist,
+                          hipStream_t s) {
+  const e2v2_deg_args& A = *args;
+  E2V2_REQUIRE(A.channels == kDC, "deg_bwd: built for C=%d, got %d", kDC, A.channels);
+  if (A.n_rows == 0) return 0;
+  hipLaunchKernelGGL(k_deg_bwd, dim3(A.n_rows), dim3(256), 0, s, A, grad_x0, dfea, ddvec, ddist);
+  E2V2_LAUNCHED("k_deg_bwd");
+  return 0;
+}
+
+E2V2_API int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,
+                              const float* dvec, const float* dist, const float* ddvec, const float* ddist,
+                              float* dpos, hipStream_t s) {
+  if (n_atoms == 0) return 0;
+  hipLaunchKernelGGL(k_edge_to_pos, dim3((n_atoms + 127) / 128), dim3(128), 0, s, n_atoms, row_ptr, key_ptr, key_eid,
+                     dvec, dist, ddvec, ddist, dpos);
+  E2V2_LAUNCHED("k_edge_to_pos");
+  return 0;
+}

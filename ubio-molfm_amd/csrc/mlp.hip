@@ -1,0 +1,408 @@
+// Edge radial MLP (RadialProfile [K0 + types -> 128 -> LN -> SiLU -> 128 -> LN
+// -> SiLU -> OUT], src/molfm/models/e2former/module_utils.py:2151-2178) fused
+// with the Gaussian RBF of the edge distance (module_utils.py:1853-1869).
+//
+// The first Linear is split: W1 [rbf | tgt | src] x = W1r rbf + (W1t tgt[z_i] + b1)
+// + W1s src[z_j]; the two type terms arrive as per-type tables.  The RBF tile
+// lives in LDS only; the MLP runs as fp32 MFMA 16x16x4 GEMMs on 32-edge tiles.
+// The backward recomputes the forward and returns only dL/d(distance).
+#include "common.h"
+#include "../../include/e2v2.h"
+
+namespace e2v2 {
+
+constexpr int kT = 32;          // edges per tile
+constexpr int kK0 = 256;        // rbf basis
+constexpr int kH = 128;         // hidden width
+constexpr int kLdX = 258;       // LDS row stride for K=256 tiles (== 2 mod 32)
+constexpr int kLdY = 130;       // LDS row stride for K=128 tiles (== 2 mod 32)
+
+// C[32][N] = A[32][K] (LDS, row stride lda) x B[K][N] (global, row stride ldb).
+// Wave w owns columns [w*N/4, (w+1)*N/4).  acc[rt][ct] holds the 16x16 tile
+// (rows rt*16.., cols w*N/4 + ct*16..); lane l holds rows 4*(l/16)+r, col l%16.
+template <int K, int N>
+__device__ __forceinline__ void gemm32(const float* A, int lda, const float* __restrict__ B, int ldb,
+                                       floatx4 (&acc)[2][N / 64]) {
+  constexpr int CT = N / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15, lk = lane >> 4;
+  const int cbase = wave * (N / 4);
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const float* Bp = B + (size_t)lk * ldb + cbase + li;
+  float bn[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) bn[ct] = Bp[ct * 16];
+#pragma unroll 4
+  for (int k0 = 0; k0 < K; k0 += 4) {
+    float b[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) b[ct] = bn[ct];
+    if (k0 + 4 < K) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) bn[ct] = Bp[(size_t)(k0 + 4) * ldb + ct * 16];
+    }
+    float a0 = A[li * lda + k0 + lk];
+    float a1 = A[(16 + li) * lda + k0 + lk];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      acc[0][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b[ct], acc[0][ct], 0, 0, 0);
+      acc[1][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b[ct], acc[1][ct], 0, 0, 0);
+    }
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void acc_coord(int rt, int ct, int r, int& row, int& c) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  row = rt * 16 + 4 * (lane >> 4) + r;
+  c = wave * (N / 4) + ct * 16 + (lane & 15);
+}
+
+// Row-wise LayerNorm(128) + SiLU on Y (in place).  Saves nrm (normalised,
+// pre-affine) and rstd when requested.  8 threads per row.
+__device__ __forceinline__ void ln_silu_rows(float* Y, int ldy, const float* __restrict__ g, const float* __restrict__ b,
+                                             float* nrm, int ldn, float* rstd_out) {
+  const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
+  float* y = Y + row * ldy;
+  float v[16];
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    v[q] = y[sub + 8 * q];
+    s += v[q];
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 4, 64);
+  const float mean = s * (1.0f / kH);
+  float s2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    float dlt = v[q] - mean;
+    s2 += dlt * dlt;
+  }
+  s2 += __shfl_xor(s2, 1, 64);
+  s2 += __shfl_xor(s2, 2, 64);
+  s2 += __shfl_xor(s2, 4, 64);
+  const float rstd = 1.0f / sqrtf(s2 * (1.0f / kH) + 1e-5f);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int c = sub + 8 * q;
+    float n = (v[q] - mean) * rstd;
+    if (nrm) nrm[row * ldn + c] = n;
+    float a = n * g[c] + b[c];
+    y[c] = silu(a);
+  }
+  if (rstd_out && sub == 0) rstd_out[row] = rstd;
+}
+
+// dz = LN-backward(SiLU-backward(dy)) given the saved normalised input and rstd.
+__device__ __forceinline__ void ln_silu_bwd_rows(float* Y, int ldy, const float* nrm, int ldn, const float* rstd,
+                                                 const float* __restrict__ g, const float* __restrict__ b) {
+  const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
+  float* y = Y + row * ldy;
+  float dn[16], nn[16];
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int c = sub + 8 * q;
+    float n = nrm[row * ldn + c];
+    float a = n * g[c] + b[c];
+    float sg = sigmoidf_(a);
+    float da = y[c] * sg * (1.0f + a * (1.0f - sg));
+    dn[q] = da * g[c];
+    nn[q] = n;
+    s1 += dn[q];
+    s2 += dn[q] * n;
+  }
+  s1 += __shfl_xor(s1, 1, 64); s1 += __shfl_xor(s1, 2, 64); s1 += __shfl_xor(s1, 4, 64);
+  s2 += __shfl_xor(s2, 1, 64); s2 += __shfl_xor(s2, 2, 64); s2 += __shfl_xor(s2, 4, 64);
+  const float m1 = s1 * (1.0f / kH), m2 = s2 * (1.0f / kH), r = rstd[row];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) y[sub + 8 * q] = r * (dn[q] - m1 - nn[q] * m2);
+}
+
+struct TileEdges {
+  float d[kT];
+  int zi[kT], zj[kT];
+  int valid[kT];
+};
+
+__device__ __forceinline__ void load_tile_edges(const e2v2_mlp_args& A, int e0, TileEdges& te) {
+  const int t = threadIdx.x;
+  if (t < kT) {
+    const int64_t e = (int64_t)e0 + t;
+    const bool v = e < A.n_edges;
+    te.valid[t] = v;
+    te.d[t] = v ? A.dist[e] : 0.f;
+    te.zi[t] = v ? A.node_type[A.edge_row[e]] : 0;
+    te.zj[t] = v ? A.node_type[A.col[e]] : 0;
+  }
+}
+
+// rbf tile: X[r][k] = exp(coeff * (d_r - mu_k)^2); thread t owns basis k = t
+__device__ __forceinline__ void rbf_tile(const e2v2_mlp_args& A, const TileEdges& te, float* X) {
+  const int k = threadIdx.x;
+  const float mu = A.rbf_offset[k];
+#pragma unroll 4
+  for (int r = 0; r < kT; ++r) {
+    float x = te.d[r] - mu;
+    X[r * kLdX + k] = te.valid[r] ? expf(A.rbf_coeff * (x * x)) : 0.f;
+  }
+}
+
+// forward through LN2+SiLU.  On return: Y (ld kLdY) holds y1 (unused after),
+// H2 (ld kLdY) holds y2 = silu(LN2(h2)); optionally n1/n2 and rstds saved.
+__device__ __forceinline__ void mlp_trunk(const e2v2_mlp_args& A, const e2v2_mlp_weights& W, const TileEdges& te,
+                                          float* X, float* Y, float* H2, float* N1, float* N2, float* r1, float* r2) {
+  rbf_tile(A, te, X);
+  __syncthreads();
+  {
+    floatx4 acc[2][2];
+    gemm32<kK0, kH>(X, kLdX, W.w1t, kH, acc);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          int row, c;
+          acc_coord<kH>(rt, ct, r, row, c);
+          Y[row * kLdY + c] = acc[rt][ct][r] + W.ttgt[te.zi[row] * kH + c] + W.tsrc[te.zj[row] * kH + c];
+        }
+  }
+  __syncthreads();
+  ln_silu_rows(Y, kLdY, W.g1, W.be1, N1, kLdY, r1);
+  __syncthreads();
+  {
+    floatx4 acc[2][2];
+    gemm32<kH, kH>(Y, kLdY, W.w2t, kH, acc);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          int row, c;
+          acc_coord<kH>(rt, ct, r, row, c);
+          H2[row * kLdY + c] = acc[rt][ct][r] + W.b2[c];
+        }
+  }
+  __syncthreads();
+  ln_silu_rows(H2, kLdY, W.g2, W.be2, N2, kLdY, r2);
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
+  extern __shared__ float sm[];
+  float* X = sm;                    // [32][258]
+  float* Y = X + kT * kLdX;         // [32][130]
+  float* H2 = Y + kT * kLdY;        // [32][130]
+  __shared__ TileEdges te;
+  const int m = blockIdx.y;
+  const e2v2_mlp_weights& W = A.w[m];
+  const int e0 = blockIdx.x * kT;
+  load_tile_edges(A, e0, te);
+  __syncthreads();
+  mlp_trunk(A, W, te, X, Y, H2, nullptr, nullptr, nullptr, nullptr);
+  floatx4 acc[2][4];
+  gemm32<kH, 256>(H2, kLdY, W.w3t, 256, acc);
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int row, c;
+        acc_coord<256>(rt, ct, r, row, c);
+        if (te.valid[row]) out[(int64_t)(e0 + row) * ld_out + m * 256 + c] = acc[rt][ct][r] + W.b3[c];
+      }
+}
+
+// Normalise rows of Y in place (pre-affine LayerNorm(128)) and keep rstd.
+__device__ __forceinline__ void ln_normalize_rows(float* Y, int ldy, float* rstd_out) {
+  const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
+  float* y = Y + row * ldy;
+  float v[16], s = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) { v[q] = y[sub + 8 * q]; s += v[q]; }
+  s += __shfl_xor(s, 1, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 4, 64);
+  const float mean = s * (1.0f / kH);
+  float s2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) { float dl = v[q] - mean; s2 += dl * dl; }
+  s2 += __shfl_xor(s2, 1, 64); s2 += __shfl_xor(s2, 2, 64); s2 += __shfl_xor(s2, 4, 64);
+  const float rstd = 1.0f / sqrtf(s2 * (1.0f / kH) + 1e-5f);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) y[sub + 8 * q] = (v[q] - mean) * rstd;
+  if (sub == 0) rstd_out[row] = rstd;
+}
+
+template <int N>
+__device__ __forceinline__ void store_acc(const floatx4 (&acc)[2][N / 64], float* Y, int ldy,
+                                          const float* __restrict__ bias) {
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < N / 64; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int row, c;
+        acc_coord<N>(rt, ct, r, row, c);
+        Y[row * ldy + c] = acc[rt][ct][r] + (bias ? bias[c] : 0.f);
+      }
+}
+
+__global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
+                                                 float* __restrict__ dd, int accumulate) {
+  extern __shared__ float sm[];
+  float* X = sm;                    // [32][258]
+  float* Y = X + kT * kLdX;         // [32][130]
+  float* N1 = Y + kT * kLdY;        // [32][130]
+  float* N2 = N1 + kT * kLdY;       // [32][130]
+  __shared__ TileEdges te;
+  __shared__ float r1[kT], r2[kT];
+  __shared__ float part[4][kT];
+  const int e0 = blockIdx.x * kT;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  load_tile_edges(A, e0, te);
+  __syncthreads();
+  float dd_lane[2][4];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dd_lane[rt][r] = 0.f;
+  for (int m = 0; m < A.n_mlp; ++m) {
+    const e2v2_mlp_weights& W = A.w[m];
+    // ---- recompute the forward trunk: n1, r1, y1, n2, r2
+    rbf_tile(A, te, X);
+    __syncthreads();
+    {
+      floatx4 acc[2][2];
+      gemm32<kK0, kH>(X, kLdX, W.w1t, kH, acc);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            int row, c;
+            acc_coord<kH>(rt, ct, r, row, c);
+            Y[row * kLdY + c] = acc[rt][ct][r] + W.ttgt[te.zi[row] * kH + c] + W.tsrc[te.zj[row] * kH + c];
+          }
+    }
+    __syncthreads();
+    ln_silu_rows(Y, kLdY, W.g1, W.be1, N1, kLdY, r1);
+    __syncthreads();
+    {
+      floatx4 acc[2][2];
+      gemm32<kH, kH>(Y, kLdY, W.w2t, kH, acc);
+      store_acc<kH>(acc, N2, kLdY, W.b2);
+    }
+    __syncthreads();
+    ln_normalize_rows(N2, kLdY, r2);
+    // ---- backward
+    for (int idx = threadIdx.x; idx < kT * 256; idx += 256) {
+      const int row = idx >> 8, c = idx & 255;
+      X[row * kLdX + c] = te.valid[row] ? dout[(int64_t)(e0 + row) * ld_dout + m * 256 + c] : 0.f;
+    }
+    __syncthreads();
+    {  // dy2 = dOut . W3   (W3 [256][128] row-major = B[K=256][N=128])
+      floatx4 acc[2][2];
+      gemm32<256, kH>(X, kLdX, W.w3, kH, acc);
+      store_acc<kH>(acc, Y, kLdY, nullptr);
+    }
+    __syncthreads();
+    ln_silu_bwd_rows(Y, kLdY, N2, kLdY, r2, W.g2, W.be2);
+    __syncthreads();
+    {  // dy1 = dz2 . W2   (W2 [128][128])
+      floatx4 acc[2][2];
+      gemm32<kH, kH>(Y, kLdY, W.w2, kH, acc);
+      store_acc<kH>(acc, X, kLdY, nullptr);
+    }
+    __syncthreads();
+    ln_silu_bwd_rows(X, kLdY, N1, kLdY, r1, W.g1, W.be1);
+    __syncthreads();
+    {  // drbf = dz1 . W1r  (W1 [128][ldw1], rbf columns 0..255); dd += sum_k drbf * rbf * 2c(d - mu)
+      floatx4 acc[2][4];
+      gemm32<kH, 256>(X, kLdY, W.w1, W.ldw1, acc);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            int row, c;
+            acc_coord<256>(rt, ct, r, row, c);
+            float x = te.d[row] - A.rbf_offset[c];
+            float rb = expf(A.rbf_coeff * (x * x));
+            dd_lane[rt][r] += acc[rt][ct][r] * rb * (2.0f * A.rbf_coeff * x);
+          }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = dd_lane[rt][r];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      v += __shfl_xor(v, 8, 64);
+      if ((lane & 15) == 0) part[wave][rt * 16 + 4 * (lane >> 4) + r] = v;
+    }
+  __syncthreads();
+  if (threadIdx.x < kT && te.valid[threadIdx.x]) {
+    float v = part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] + part[3][threadIdx.x];
+    int64_t e = (int64_t)e0 + threadIdx.x;
+    dd[e] = accumulate ? dd[e] + v : v;
+  }
+}
+
+}  // namespace e2v2
+
+using namespace e2v2;
+
+static size_t mlp_fwd_lds() { return sizeof(float) * (kT * kLdX + 2 * kT * kLdY); }
+static size_t mlp_bwd_lds() { return sizeof(float) * (kT * kLdX + 3 * kT * kLdY); }
+
+E2V2_API int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hipStream_t s) {
+  const e2v2_mlp_args& A = *args;
+  E2V2_REQUIRE(A.n_mlp >= 1 && A.n_mlp <= E2V2_MAX_MLP, "mlp_fwd: n_mlp %d out of range", A.n_mlp);
+  E2V2_REQUIRE(ld_out >= 256 * A.n_mlp, "mlp_fwd: ld_out %d < 256*n_mlp", ld_out);
+  if (A.n_edges == 0) return 0;
+  static bool attr = false;
+  if (!attr) {
+    E2V2_TRY_HIP(hipFuncSetAttribute((const void*)k_mlp_fwd, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)mlp_fwd_lds()));
+    attr = true;
+  }
+  dim3 grid((unsigned)((A.n_edges + kT - 1) / kT), (unsigned)A.n_mlp);
+  hipLaunchKernelGGL(k_mlp_fwd, grid, dim3(256), mlp_fwd_lds(), s, A, out, ld_out);
+  E2V2_LAUNCHED("k_mlp_fwd");
+  return 0;
+}
+
+E2V2_API int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_dout, float* dd, int accumulate,
+                          hipStream_t s) {
+  const e2v2_mlp_args& A = *args;
+  E2V2_REQUIRE(A.n_mlp >= 1 && A.n_mlp <= E2V2_MAX_MLP, "mlp_bwd: n_mlp %d out of range", A.n_mlp);
+  E2V2_REQUIRE(ld_dout >= 256 * A.n_mlp, "mlp_bwd: ld_dout %d < 256*n_mlp", ld_dout);
+  if (A.n_edges == 0) return 0;
+  static bool attr = false;
+  if (!attr) {
+    E2V2_TRY_HIP(hipFuncSetAttribute((const void*)k_mlp_bwd, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)mlp_bwd_lds()));
+    attr = true;
+  }
+  dim3 grid((unsigned)((A.n_edges + kT - 1) / kT));
+  hipLaunchKernelGGL(k_mlp_bwd, grid, dim3(256), mlp_bwd_lds(), s, A, dout, ld_dout, dd, accumulate);
+  E2V2_LAUNCHED("k_mlp_bwd");
+  return 0;
+}

@@ -1,0 +1,435 @@
+// Periodic radius graph: cell-list binning -> per-row count -> exclusive scan
+// -> fill -> per-row sort by (distance, j, shift) -> key CSR (transpose).
+//
+// Replaces CellExpander.expand_includeself + construct_radius_neighbor
+// (src/molfm/models/e2former/module_utils.py:1065-1274,3119-3242) and the
+// CSR metadata of prepare_sparse_qk_edge_index_metadata
+// (src/molfm/models/e2former/triton_dr/triton_sparse_qk_autograd.py:601-652).
+#include "common.h"
+#include "../../include/e2v2.h"
+
+namespace e2v2 {
+
+__global__ void k_fill_i32(int32_t* __restrict__ p, int32_t v, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = v;
+}
+
+__global__ void k_fill_f32(float* __restrict__ p, float v, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = v;
+}
+
+// Single-workgroup exclusive scan: out[0..n] with out[n] = total;
+// stats[0] = total, stats[1] = max(in).
+__global__ __launch_bounds__(1024) void k_scan_i32(const int32_t* __restrict__ in, int n,
+                                                   int32_t* __restrict__ out, int32_t* __restrict__ stats) {
+  __shared__ int64_t part[1024];
+  __shared__ int32_t pmax[1024];
+  const int t = threadIdx.x;
+  const int per = (n + 1023) / 1024;
+  const int b = t * per;
+  const int e = min(n, b + per);
+  int64_t s = 0;
+  int32_t mx = 0;
+  for (int i = b; i < e; ++i) {
+    s += in[i];
+    mx = max(mx, in[i]);
+  }
+  part[t] = s;
+  pmax[t] = mx;
+  __syncthreads();
+  // Hillis-Steele inclusive scan over 1024 partials
+  for (int o = 1; o < 1024; o <<= 1) {
+    int64_t v = (t >= o) ? part[t - o] : 0;
+    int32_t m = (t >= o) ? pmax[t - o] : 0;
+    __syncthreads();
+    part[t] += v;
+    pmax[t] = max(pmax[t], m);
+    __syncthreads();
+  }
+  int64_t run = part[t] - s;
+  for (int i = b; i < e; ++i) {
+    out[i] = (int32_t)run;
+    run += in[i];
+  }
+  if (t == 1023) {
+    out[n] = (int32_t)part[1023];
+    stats[0] = (int32_t)part[1023];
+    stats[1] = pmax[1023];
+  }
+}
+
+__device__ __forceinline__ int bin_coord(float x, float lo, float h, int dim) {
+  int b = (int)floorf((x - lo) / h);
+  return min(max(b, 0), dim - 1);
+}
+
+__global__ void k_bin_assign(e2v2_nbr_plan P) {
+  int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a >= P.n_atoms) return;
+  int g = P.atom_graph[a];
+  const float* p = P.pos + 3 * a;
+  int bx = bin_coord(p[0], P.grid_lo[3 * g + 0], P.grid_h[3 * g + 0], P.grid_dim[3 * g + 0]);
+  int by = bin_coord(p[1], P.grid_lo[3 * g + 1], P.grid_h[3 * g + 1], P.grid_dim[3 * g + 1]);
+  int bz = bin_coord(p[2], P.grid_lo[3 * g + 2], P.grid_h[3 * g + 2], P.grid_dim[3 * g + 2]);
+  int bin = P.bin_base[g] + (bx * P.grid_dim[3 * g + 1] + by) * P.grid_dim[3 * g + 2] + bz;
+  P.atom_bin[a] = bin;
+  atomicAdd(&P.bin_count[bin], 1);
+}
+
+__global__ void k_bin_fill(e2v2_nbr_plan P, int32_t* __restrict__ cursor) {
+  int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a >= P.n_atoms) return;
+  int bin = P.atom_bin[a];
+  int slot = P.bin_start[bin] + atomicAdd(&cursor[bin], 1);
+  P.bin_atoms[slot] = a;
+}
+
+constexpr float kBinMargin = 1e-2f;
+
+// Does any atom of graph g lie strictly within rc of the image img?
+__device__ bool image_has_inner(const e2v2_nbr_plan& P, int g, const float* img) {
+  const float lo0 = P.grid_lo[3 * g], lo1 = P.grid_lo[3 * g + 1], lo2 = P.grid_lo[3 * g + 2];
+  const float h0 = P.grid_h[3 * g], h1 = P.grid_h[3 * g + 1], h2 = P.grid_h[3 * g + 2];
+  const int d0 = P.grid_dim[3 * g], d1 = P.grid_dim[3 * g + 1], d2 = P.grid_dim[3 * g + 2];
+  const float r = P.rc + kBinMargin;
+  int x0 = (int)floorf((img[0] - r - lo0) / h0), x1 = (int)floorf((img[0] + r - lo0) / h0);
+  int y0 = (int)floorf((img[1] - r - lo1) / h1), y1 = (int)floorf((img[1] + r - lo1) / h1);
+  int z0 = (int)floorf((img[2] - r - lo2) / h2), z1 = (int)floorf((img[2] + r - lo2) / h2);
+  x0 = max(x0, 0); y0 = max(y0, 0); z0 = max(z0, 0);
+  x1 = min(x1, d0 - 1); y1 = min(y1, d1 - 1); z1 = min(z1, d2 - 1);
+  const float zero[3] = {0.f, 0.f, 0.f};
+  for (int bx = x0; bx <= x1; ++bx)
+    for (int by = y0; by <= y1; ++by)
+      for (int bz = z0; bz <= z1; ++bz) {
+        int bin = P.bin_base[g] + (bx * d1 + by) * d2 + bz;
+        for (int s = P.bin_start[bin]; s < P.bin_start[bin + 1]; ++s) {
+          int k = P.bin_atoms[s];
+          float dx, dy, dz;
+          exact_edge(P.pos + 3 * k, img, zero, dx, dy, dz);
+          if (exact_dist(dx, dy, dz) < P.rc) return true;
+        }
+      }
+  return false;
+}
+
+// Visit every edge i <- (j, s) of atom i in a fixed traversal order.
+template <class Emit>
+__device__ void visit_edges(const e2v2_nbr_plan& P, int i, Emit&& emit) {
+  const int g = P.atom_graph[i];
+  const bool periodic = P.graph_periodic[g] != 0;
+  const float pi[3] = {P.pos[3 * i], P.pos[3 * i + 1], P.pos[3 * i + 2]};
+  const float lo0 = P.grid_lo[3 * g], lo1 = P.grid_lo[3 * g + 1], lo2 = P.grid_lo[3 * g + 2];
+  const float h0 = P.grid_h[3 * g], h1 = P.grid_h[3 * g + 1], h2 = P.grid_h[3 * g + 2];
+  const int d0 = P.grid_dim[3 * g], d1 = P.grid_dim[3 * g + 1], d2 = P.grid_dim[3 * g + 2];
+  const float r = P.rc + kBinMargin;
+  for (int s = P.graph_shift_ptr[g]; s < P.graph_shift_ptr[g + 1]; ++s) {
+    const float* off = P.shift_off + 3 * s;
+    const float q0 = pi[0] - off[0], q1 = pi[1] - off[1], q2 = pi[2] - off[2];
+    int x0 = (int)floorf((q0 - r - lo0) / h0), x1 = (int)floorf((q0 + r - lo0) / h0);
+    if (x1 < 0 || x0 > d0 - 1) continue;
+    int y0 = (int)floorf((q1 - r - lo1) / h1), y1 = (int)floorf((q1 + r - lo1) / h1);
+    if (y1 < 0 || y0 > d1 - 1) continue;
+    int z0 = (int)floorf((q2 - r - lo2) / h2), z1 = (int)floorf((q2 + r - lo2) / h2);
+    if (z1 < 0 || z0 > d2 - 1) continue;
+    x0 = max(x0, 0); y0 = max(y0, 0); z0 = max(z0, 0);
+    x1 = min(x1, d0 - 1); y1 = min(y1, d1 - 1); z1 = min(z1, d2 - 1);
+    for (int bx = x0; bx <= x1; ++bx)
+      for (int by = y0; by <= y1; ++by)
+        for (int bz = z0; bz <= z1; ++bz) {
+          int bin = P.bin_base[g] + (bx * d1 + by) * d2 + bz;
+          for (int t = P.bin_start[bin]; t < P.bin_start[bin + 1]; ++t) {
+            int j = P.bin_atoms[t];
+            float dx, dy, dz;
+            exact_edge(pi, P.pos + 3 * j, off, dx, dy, dz);
+            float d = exact_dist(dx, dy, dz);
+            if (!(d >= P.rmin && d <= P.rc)) continue;
+            if (periodic && !(d < P.rc)) {
+              float img[3];
+              {
+#pragma clang fp contract(off)
+                img[0] = P.pos[3 * j] + off[0];
+                img[1] = P.pos[3 * j + 1] + off[1];
+                img[2] = P.pos[3 * j + 2] + off[2];
+              }
+              if (!image_has_inner(P, g, img)) continue;
+            }
+            emit(j, s, dx, dy, dz, d);
+          }
+        }
+  }
+}
+
+__global__ void k_nbr_count(e2v2_nbr_plan P, int32_t* __restrict__ row_count) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P.n_atoms) return;
+  int c = 0;
+  visit_edges(P, i, [&](int, int, float, float, float, float) { ++c; });
+  row_count[i] = c;
+}
+
+__global__ void k_nbr_fill(e2v2_nbr_plan P, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ col,
+                           int32_t* __restrict__ shift, float* __restrict__ dvec, float* __restrict__ dist,
+                           uint64_t* __restrict__ key) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P.n_atoms) return;
+  int o = row_ptr[i];
+  const int o_end = row_ptr[i + 1];
+  const int g = P.atom_graph[i];
+  const int a0 = P.graph_atom_ptr[g];
+  const int s0 = P.graph_shift_ptr[g];
+  const int ns = P.graph_shift_ptr[g + 1] - s0;
+  visit_edges(P, i, [&](int j, int s, float dx, float dy, float dz, float d) {
+    if (o >= o_end) return;  // count and fill share one traversal; never write past the row
+    col[o] = j;
+    shift[o] = s;
+    dvec[3 * o] = dx;
+    dvec[3 * o + 1] = dy;
+    dvec[3 * o + 2] = dz;
+    dist[o] = d;
+    uint32_t lo = (uint32_t)(j - a0) * (uint32_t)ns + (uint32_t)(s - s0);
+    key[o] = ((uint64_t)__float_as_uint(d) << 32) | (uint64_t)lo;
+    ++o;
+  });
+}
+
+// Bitonic sort of one segment per workgroup (length <= kMaxSeg), returning
+// the sorted order as source positions.
+constexpr int kMaxSeg = 4096;
+
+__device__ void segment_sort(const uint64_t* __restrict__ key, int b, int n, uint64_t* sk, int32_t* sv) {
+  int p2 = 1;
+  while (p2 < n) p2 <<= 1;
+  for (int t = threadIdx.x; t < p2; t += blockDim.x) {
+    sk[t] = (t < n) ? key[b + t] : ~0ull;
+    sv[t] = (t < n) ? t : 0x7fffffff;
+  }
+  __syncthreads();
+  for (int k = 2; k <= p2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int t = threadIdx.x; t < p2; t += blockDim.x) {
+        int x = t ^ j;
+        if (x > t) {
+          bool up = ((t & k) == 0);
+          uint64_t a = sk[t], c = sk[x];
+          int32_t va = sv[t], vc = sv[x];
+          bool gt = (a > c) || (a == c && va > vc);
+          if (gt == up) {
+            sk[t] = c; sk[x] = a;
+            sv[t] = vc; sv[x] = va;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_sort_rows(const int32_t* __restrict__ row_ptr,
+                                                   const uint64_t* __restrict__ key,
+                                                   const int32_t* __restrict__ tcol, const int32_t* __restrict__ tshift,
+                                                   const float* __restrict__ tdv, const float* __restrict__ td,
+                                                   int32_t* __restrict__ col, int32_t* __restrict__ shift,
+                                                   float* __restrict__ dvec, float* __restrict__ dist) {
+  __shared__ uint64_t sk[kMaxSeg];
+  __shared__ int32_t sv[kMaxSeg];
+  const int r = blockIdx.x;
+  const int b = row_ptr[r], n = row_ptr[r + 1] - b;
+  if (n == 0) return;
+  segment_sort(key, b, n, sk, sv);
+  for (int t = threadIdx.x; t < n; t += blockDim.x) {
+    int src = b + sv[t], dst = b + t;
+    col[dst] = tcol[src];
+    shift[dst] = tshift[src];
+    dvec[3 * dst] = tdv[3 * src];
+    dvec[3 * dst + 1] = tdv[3 * src + 1];
+    dvec[3 * dst + 2] = tdv[3 * src + 2];
+    dist[dst] = td[src];
+  }
+}
+
+// edge -> row index
+__global__ void k_edge_rows(const int32_t* __restrict__ row_ptr, int n_rows, int32_t* __restrict__ edge_row) {
+  int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  for (int e = row_ptr[r]; e < row_ptr[r + 1]; ++e) edge_row[e] = r;
+}
+
+__global__ void k_col_count(const int32_t* __restrict__ col, int64_t n_edges, int32_t* __restrict__ cnt) {
+  int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  atomicAdd(&cnt[col[e]], 1);
+}
+
+__global__ void k_col_fill(const int32_t* __restrict__ col, int64_t n_edges, const int32_t* __restrict__ key_ptr,
+                           int32_t* __restrict__ cursor, uint64_t* __restrict__ tkey) {
+  int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n_edges) return;
+  int j = col[e];
+  int slot = key_ptr[j] + atomicAdd(&cursor[j], 1);
+  tkey[slot] = (uint64_t)e;
+}
+
+__global__ __launch_bounds__(256) void k_sort_cols(const int32_t* __restrict__ key_ptr,
+                                                   const uint64_t* __restrict__ tkey,
+                                                   int32_t* __restrict__ key_eid) {
+  __shared__ uint64_t sk[kMaxSeg];
+  __shared__ int32_t sv[kMaxSeg];
+  const int r = blockIdx.x;
+  const int b = key_ptr[r], n = key_ptr[r + 1] - b;
+  if (n == 0) return;
+  segment_sort(tkey, b, n, sk, sv);
+  for (int t = threadIdx.x; t < n; t += blockDim.x) key_eid[b + t] = (int32_t)sk[t];
+}
+
+// keep the first k entries of each row (rows already sorted by distance)
+__global__ void k_topk_count(const int32_t* __restrict__ row_ptr, int n_rows, int k, int32_t* __restrict__ cnt) {
+  int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  cnt[r] = min(row_ptr[r + 1] - row_ptr[r], k);
+}
+
+__global__ void k_topk_compact(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ new_ptr, int n_rows,
+                               const int32_t* __restrict__ col, const int32_t* __restrict__ shift,
+                               const float* __restrict__ dvec, const float* __restrict__ dist,
+                               int32_t* __restrict__ ocol, int32_t* __restrict__ oshift,
+                               float* __restrict__ odv, float* __restrict__ od) {
+  int r = blockIdx.x;
+  int b = row_ptr[r], nb = new_ptr[r], n = new_ptr[r + 1] - nb;
+  for (int t = threadIdx.x; t < n; t += blockDim.x) {
+    ocol[nb + t] = col[b + t];
+    oshift[nb + t] = shift[b + t];
+    odv[3 * (nb + t)] = dvec[3 * (b + t)];
+    odv[3 * (nb + t) + 1] = dvec[3 * (b + t) + 1];
+    odv[3 * (nb + t) + 2] = dvec[3 * (b + t) + 2];
+    od[nb + t] = dist[b + t];
+  }
+}
+
+static inline unsigned blocks_for(int64_t n, int bs) {
+  int64_t b = (n + bs - 1) / bs;
+  return (unsigned)(b < 1 ? 1 : (b > 1048576 ? 1048576 : b));
+}
+
+}  // namespace e2v2
+
+using namespace e2v2;
+
+E2V2_API int e2v2_fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(k_fill_i32, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
+  E2V2_LAUNCHED("k_fill_i32");
+  return 0;
+}
+
+E2V2_API int e2v2_fill_f32(float* p, float v, int64_t n, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(k_fill_f32, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
+  E2V2_LAUNCHED("k_fill_f32");
+  return 0;
+}
+
+E2V2_API int e2v2_scan_i32(const int32_t* in, int n, int32_t* out, int32_t* stats, hipStream_t s) {
+  E2V2_REQUIRE(n >= 0, "scan: negative length %d", n);
+  hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, in, n, out, stats);
+  E2V2_LAUNCHED("k_scan_i32");
+  return 0;
+}
+
+E2V2_API int e2v2_nbr_bin(const e2v2_nbr_plan* plan, hipStream_t s) {
+  const e2v2_nbr_plan& P = *plan;
+  E2V2_REQUIRE(P.n_atoms >= 0 && P.n_bins > 0, "nbr_bin: bad sizes (atoms %d, bins %d)", P.n_atoms, P.n_bins);
+  int rc = e2v2_fill_i32(P.bin_count, 0, P.n_bins, s);
+  if (rc) return rc;
+  if (P.n_atoms == 0) return e2v2_fill_i32(P.bin_start, 0, (int64_t)P.n_bins + 1, s);
+  hipLaunchKernelGGL(k_bin_assign, dim3(blocks_for(P.n_atoms, 256)), dim3(256), 0, s, P);
+  E2V2_LAUNCHED("k_bin_assign");
+  // bin_start = exclusive scan of counts; the count buffer becomes the fill cursor
+  hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, P.bin_count, P.n_bins, P.bin_start, P.stats);
+  E2V2_LAUNCHED("k_scan_i32");
+  rc = e2v2_fill_i32(P.bin_count, 0, P.n_bins, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_bin_fill, dim3(blocks_for(P.n_atoms, 256)), dim3(256), 0, s, P, P.bin_count);
+  E2V2_LAUNCHED("k_bin_fill");
+  return 0;
+}
+
+E2V2_API int e2v2_nbr_count(const e2v2_nbr_plan* plan, int32_t* row_count, int32_t* row_ptr, hipStream_t s) {
+  const e2v2_nbr_plan& P = *plan;
+  if (P.n_atoms > 0) {
+    hipLaunchKernelGGL(k_nbr_count, dim3(blocks_for(P.n_atoms, 64)), dim3(64), 0, s, P, row_count);
+    E2V2_LAUNCHED("k_nbr_count");
+  }
+  hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, row_count, P.n_atoms, row_ptr, P.stats);
+  E2V2_LAUNCHED("k_scan_i32");
+  return 0;
+}
+
+E2V2_API int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, int64_t n_edges, int max_row,
+                           int32_t* tmp_col, int32_t* tmp_shift, float* tmp_dvec, float* tmp_dist, uint64_t* tmp_key,
+                           int32_t* col, int32_t* shift, float* dvec, float* dist, hipStream_t s) {
+  const e2v2_nbr_plan& P = *plan;
+  E2V2_REQUIRE(max_row <= kMaxSeg, "nbr_fill: a row has %d neighbours; the per-row sort supports at most %d",
+               max_row, kMaxSeg);
+  if (P.n_atoms == 0 || n_edges == 0) return 0;
+  hipLaunchKernelGGL(k_nbr_fill, dim3(blocks_for(P.n_atoms, 64)), dim3(64), 0, s, P, row_ptr, tmp_col, tmp_shift,
+                     tmp_dvec, tmp_dist, tmp_key);
+  E2V2_LAUNCHED("k_nbr_fill");
+  hipLaunchKernelGGL(k_sort_rows, dim3(P.n_atoms), dim3(256), 0, s, row_ptr, tmp_key, tmp_col, tmp_shift, tmp_dvec,
+                     tmp_dist, col, shift, dvec, dist);
+  E2V2_LAUNCHED("k_sort_rows");
+  return 0;
+}
+
+E2V2_API int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* cnt, int32_t* new_ptr, int32_t* stats,
+                           const int32_t* col, const int32_t* shift, const float* dvec, const float* dist,
+                           int32_t* ocol, int32_t* oshift, float* odv, float* od, int phase, hipStream_t s) {
+  if (phase == 0) {
+    if (n_rows > 0) {
+      hipLaunchKernelGGL(k_topk_count, dim3(blocks_for(n_rows, 256)), dim3(256), 0, s, row_ptr, n_rows, k, cnt);
+      E2V2_LAUNCHED("k_topk_count");
+    }
+    hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, cnt, n_rows, new_ptr, stats);
+    E2V2_LAUNCHED("k_scan_i32");
+    return 0;
+  }
+  if (n_rows == 0) return 0;
+  hipLaunchKernelGGL(k_topk_compact, dim3(n_rows), dim3(128), 0, s, row_ptr, new_ptr, n_rows, col, shift, dvec, dist,
+                     ocol, oshift, odv, od);
+  E2V2_LAUNCHED("k_topk_compact");
+  return 0;
+}
+
+E2V2_API int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, int n_cols, int64_t n_edges,
+                                int32_t* edge_row, int32_t* key_cnt, int32_t* key_ptr, int32_t* stats,
+                                uint64_t* tmp_key, int32_t* key_eid, int phase, hipStream_t s) {
+  // phase 0: edge_row, column counts and key_ptr (host then reads stats[1] = max column)
+  // phase 1: fill and sort each column by edge id
+  if (phase == 0) {
+    if (n_rows > 0 && n_edges > 0) {
+      hipLaunchKernelGGL(k_edge_rows, dim3(blocks_for(n_rows, 256)), dim3(256), 0, s, row_ptr, n_rows, edge_row);
+      E2V2_LAUNCHED("k_edge_rows");
+    }
+    int rc = e2v2_fill_i32(key_cnt, 0, n_cols, s);
+    if (rc) return rc;
+    if (n_edges > 0) {
+      hipLaunchKernelGGL(k_col_count, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, col, n_edges, key_cnt);
+      E2V2_LAUNCHED("k_col_count");
+    }
+    hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, key_cnt, n_cols, key_ptr, stats);
+    E2V2_LAUNCHED("k_scan_i32");
+    return 0;
+  }
+  if (n_edges == 0) return 0;
+  int rc = e2v2_fill_i32(key_cnt, 0, n_cols, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_col_fill, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, col, n_edges, key_ptr, key_cnt,
+                     tmp_key);
+  E2V2_LAUNCHED("k_col_fill");
+  hipLaunchKernelGGL(k_sort_cols, dim3(n_cols), dim3(256), 0, s, key_ptr, tmp_key, key_eid);
+  E2V2_LAUNCHED("k_sort_cols");
+  return 0;
+}

@@ -1,0 +1,201 @@
+"""Drop-in model classes: E2FormerBackbone, MolfmAtomic, MDEnergyForceMultiHead.
+
+* ``E2FormerBackbone(**backbone_config).forward(batched_data)`` mirrors
+  src/molfm/models/e2former/e2former_wrapper.py:140-339 (same constructor
+  kwargs, same output keys ``node_featuresBxN``, ``node_vec_featuresBxN``,
+  ``node_irrepsBxN``, ``data``, ``neighbor_info``).  The neighbour list comes
+  from the HIP cell-list builder instead of CellExpander / FAISS.
+* ``MolfmAtomic`` mirrors src/molfm/tasks/pretrain_smallmol.py:170-251 with
+  the MLP energy head and the autograd force head
+  (src/molfm/pipeline/head.py:305-341,483-580).
+* ``Potential.energy_forces`` is the flat entry point used by the MD loop and
+  the benchmark: flattened atoms, graphs contiguous.
+"""
+from __future__ import annotations
+
+from types import SimpleNamespace
+from typing import Dict, Optional
+
+import numpy as np
+import torch
+from torch import nn
+
+from .modules import E2former, EdgeContext, parse_irreps
+from .neighbors import build_neighbors
+from .ops import EdgeGeometryFn
+
+
+def _as_int_or_none(v):
+    if v is None or (isinstance(v, str) and v.lower() == "none"):
+        return None
+    return int(v)
+
+
+class E2FormerBackbone(nn.Module):
+    def __init__(self, use_faiss: bool = False, **kwargs):
+        super().__init__()
+        self.kwargs = kwargs
+        self.use_faiss = use_faiss  # accepted for signature compatibility; the HIP builder replaces FAISS
+        C, lmax = parse_irreps(kwargs["irreps_node_embedding"])
+        self.scalar_dim = C
+        if kwargs.get("encoder", "default") != "default":
+            raise NotImplementedError("encoder != 'default' is outside the MI355X path")
+        self.embedding = nn.Embedding(256, C)
+        self.embedding_charge = nn.Embedding(30, C)
+        self.embedding_multiplicity = nn.Embedding(30, C)
+        self.mix_cm = nn.Sequential(nn.Linear(2 * C, C), nn.SiLU())
+        self.unifiedtokentoembedding = nn.Linear(C, C)
+        kw = dict(kwargs)
+        kw["max_neighbors"] = _as_int_or_none(kw.get("max_neighbors", None))
+        self.decoder = E2former(**kw)
+        self.max_neighbors = self.decoder.max_neighbors
+        self.max_radius = float(self.decoder.max_radius)
+        self.cells_per_direction = int(kwargs.get("pbc_expanded_num_cell_per_direction", 4))
+
+    # -- flat interface -------------------------------------------------------
+    def forward_flat(self, pos: torch.Tensor, Z: torch.Tensor, graph_ptr, cell, pbc, charge=None,
+                     multiplicity=None, nl=None):
+        """pos [N,3] (may require grad), Z [N] on the GPU; graph_ptr/cell/pbc on the host.
+        Returns (node_irreps [N,9,C], neighbour list)."""
+        if nl is None:
+            nl = build_neighbors(pos.detach(), graph_ptr, cell, pbc, self.max_radius, 1e-4, self.max_neighbors,
+                                 self.cells_per_direction)
+        dvec, dist = EdgeGeometryFn.apply(pos, nl)
+        node_type = Z.to(torch.int32).contiguous()
+        ctx = EdgeContext(nl, dvec, dist, node_type, self.decoder.rbf, self.max_radius)
+        sys_node = None
+        if charge is not None:
+            B = len(graph_ptr) - 1
+            sys_emb = self.mix_cm(torch.cat([self.embedding_charge(torch.clip(charge, -10, 10) + 10),
+                                             self.embedding_multiplicity(torch.clip(multiplicity, 0, 20))],
+                                            dim=-1)).reshape(B, -1)
+            counts = torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device)
+            sys_node = torch.repeat_interleave(sys_emb, counts, dim=0)
+        return self.decoder.forward_flat(ctx, sys_node), nl
+
+    # -- reference interface -------------------------------------------------
+    def forward(self, batched_data, **kwargs) -> Dict:
+        pos = batched_data["pos"]
+        mask = batched_data["atom_masks"].bool()
+        B, L = pos.shape[:2]
+        Z = batched_data["atomic_numbers"].reshape(B, L)
+        counts = mask.sum(-1).cpu().numpy()
+        graph_ptr = np.concatenate([[0], np.cumsum(counts)])
+        cell = batched_data.get("cell", None)
+        pbc = batched_data.get("pbc", None)
+        cell = np.zeros((B, 3, 3), np.float32) if cell is None else cell.detach().float().cpu().numpy()
+        pbc = np.zeros((B, 3), bool) if pbc is None else pbc.detach().cpu().numpy().astype(bool)
+        fpos = pos.float()[mask]
+        fZ = Z[mask]
+        charge = batched_data.get("charge", None)
+        mult = batched_data.get("multiplicity", None)
+        x, nl = self.forward_flat(fpos, fZ, graph_ptr, cell, pbc, charge, mult)
+        node_irreps = x.new_zeros((B, L, x.shape[1], x.shape[2]))
+        node_irreps = node_irreps.masked_scatter(mask[:, :, None, None], x)
+        return {"node_featuresBxN": node_irreps[:, :, 0], "node_vec_featuresBxN": node_irreps[:, :, 1:4],
+                "node_irrepsBxN": node_irreps, "data": batched_data, "neighbor_info": nl}
+
+
+class MLP_energy_head(nn.Module):
+    """head.py:330-341."""
+
+    def __init__(self, embedding_dim, lmax=2):
+        super().__init__()
+        self.mlp = nn.Sequential(nn.Linear(embedding_dim, embedding_dim), nn.SiLU(),
+                                 nn.Linear(embedding_dim, embedding_dim), nn.SiLU(), nn.Linear(embedding_dim, 1))
+
+    def forward(self, embedding, irreps=None):
+        return self.mlp(embedding)
+
+
+class GradientHead(nn.Module):
+    """head.py:305-328: forces = -dE/dpos (first order in eval)."""
+
+    def forward(self, pos, pred_energy):
+        if self.training:
+            raise NotImplementedError("training-mode (create_graph) forces are not supported by the HIP path")
+        return -torch.autograd.grad(pred_energy, pos, torch.ones_like(pred_energy))[0]
+
+
+class MDEnergyForceMultiHead(nn.Module):
+    """head.py:483-580 (MLP energy head + gradient force head)."""
+
+    def __init__(self, args):
+        super().__init__()
+        C, lmax = parse_irreps(args.backbone_config["irreps_node_embedding"])
+        self.energy_heads = nn.ModuleDict()
+        self.force_heads = nn.ModuleDict()
+        rename = {"svp-enhance": "tzvpd", "tzvpd-small": "tzvpd", "tzvpd-forceatomfilter": "tzvpd"}
+        if "share" in getattr(args, "head_cfg_str", ""):
+            rename.update({k: "omol25" for k in ("svp-enhance", "tzvpd-small", "tzvpd", "tzvpd-forceatomfilter")})
+        self.dataset_rename = rename
+        for name in str(args.dataset_name_list).split(","):
+            head = rename.get(name, name)
+            if head not in self.energy_heads:
+                self.energy_heads[head] = MLP_energy_head(C, lmax)
+                self.force_heads[head] = GradientHead()
+
+    def head_name(self, name: Optional[str]):
+        if name is None:
+            return next(iter(self.energy_heads.keys()))
+        return self.dataset_rename.get(name, name)
+
+
+class MolfmAtomic(nn.Module):
+    """pretrain_smallmol.py:170-251 restricted to energy + autograd forces."""
+
+    def __init__(self, args, loss_fn=None, not_init=False):
+        super().__init__()
+        if not_init:
+            return
+        self.args = args
+        name = args.backbone_config["name"]
+        if name not in {"e2former", "e2formerv2"}:
+            raise ValueError(f"Unsupported backbone: {name}")
+        cfg = dict(args.backbone_config)
+        cfg.pop("name", None)
+        self.decoder = E2FormerBackbone(**cfg)
+        self.head = MDEnergyForceMultiHead(args)
+
+    def energy_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None, nl=None):
+        x, nl = self.decoder.forward_flat(pos, Z, graph_ptr, cell, pbc, charge, multiplicity, nl)
+        h = self.head.head_name(head)
+        e_atom = self.head.energy_heads[h](x[:, 0]).squeeze(-1)
+        B = len(graph_ptr) - 1
+        gid = torch.repeat_interleave(torch.arange(B, device=pos.device),
+                                      torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device))
+        energy = torch.zeros(B, dtype=e_atom.dtype, device=pos.device).index_add(0, gid, e_atom)
+        return energy, nl
+
+    def energy_forces_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None):
+        pos = pos.detach().float().requires_grad_(True)
+        energy, nl = self.energy_flat(pos, Z, graph_ptr, cell, pbc, head, charge, multiplicity)
+        forces = -torch.autograd.grad(energy, pos, torch.ones_like(energy))[0]
+        return energy.detach(), forces, nl
+
+    def forward(self, batched_data, need_force=True, **unused):
+        pos = batched_data["pos"]
+        if need_force:
+            pos.requires_grad_(True)
+        out = self.decoder(dict(batched_data))
+        data_name = batched_data.get("data_name", [None])
+        h = self.head.head_name(data_name[0] if data_name else None)
+        mask = batched_data["atom_masks"].bool()
+        e_atom = self.head.energy_heads[h](out["node_featuresBxN"]).squeeze(-1).masked_fill(~mask, 0.0)
+        energy = e_atom.sum(dim=-1)
+        res = {"pred_energy": energy, "pred_energy_per_atom": energy / mask.sum(-1).reshape(-1)}
+        if need_force:
+            res["pred_forces"] = self.head.force_heads[h](pos, energy)
+        return res
+
+
+def default_args(max_radius=6.0, max_neighbors=None, num_layers=4, heads=("omol25",)):
+    """Backbone configuration of the benchmark, with the
+    reference's config keys (config_file/backbone_config/e2former.yaml)."""
+    bb = dict(name="e2former", irreps_node_embedding="256x0e+256x1e+256x2e", irreps_head="2x0e+2x1e+2x2e",
+              attn_scalar_head=8, num_attn_heads=128, number_of_basis=256, max_radius=max_radius,
+              max_neighbors=max_neighbors, num_layers=num_layers, alpha_drop=0.0, basis_type="gaussiansmear",
+              norm_layer="rms_norm_sh", attn_type="so2-first-order", tp_type="QK_alpha", edge_embedtype="default",
+              ffn_type="s3", encoder="default", with_cluster=False, pbc_expanded_num_cell_per_direction=4)
+    return SimpleNamespace(backbone_config=bb, dataset_name_list=",".join(heads), head_cfg_str="",
+                           AutoGradForce=True)

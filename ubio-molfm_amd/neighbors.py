@@ -1,0 +1,215 @@
+"""Periodic radius graph on the GPU -> query CSR + key CSR.
+
+Semantics follow the reference's CellExpander + construct_radius_neighbor
+(src/molfm/models/e2former/module_utils.py:953-988,1065-1274,3119-3242):
+
+* shifts s with |s_d| <= min(cells_per_direction, ceil(rc / h_d)) on periodic
+  dimensions (h_d = lattice height), 0 elsewhere; [0,0,0] first;
+* an image (j, s) exists iff some atom of the graph is strictly within rc of it;
+* edge i <- (j, s) iff rmin <= d <= rc (both inclusive);
+* rows sorted by ascending distance (ties by (j, s)); ``max_neighbors`` keeps
+  the nearest k of each row.
+
+fp32 expression (identical in the kernel): off = ((s0*a) + s1*b) + s2*c per
+component, img = pos_j + off, dvec = pos_i - img, d = sqrt((dx*dx + dy*dy) + dz*dz).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+
+F32 = np.float32
+BIN_MARGIN = 1e-2
+
+
+def _max_offsets(cell: np.ndarray, rc: float, cap: int):
+    c = torch.as_tensor(np.asarray(cell, F32)).reshape(1, 3, 3)
+    out = []
+    for dim in range(3):
+        lat = c[:, dim, :]
+        rest = c[:, [k for k in range(3) if k != dim], :]
+        nv = torch.cross(rest[:, 0, :], rest[:, 1, :], dim=-1)
+        nv = nv / nv.norm(dim=-1, keepdim=True)
+        try:
+            out.append(int(torch.max(torch.ceil(rc / torch.abs(torch.sum(nv * lat, dim=-1))))))
+        except (ValueError, RuntimeError, OverflowError):
+            out.append(cap)
+    return out
+
+
+def shift_table(cell: np.ndarray, pbc, rc: float, cap: int = 4) -> np.ndarray:
+    """Integer shifts of one graph, [0,0,0] first, then lexicographic."""
+    pbc = [bool(x) for x in np.asarray(pbc).reshape(3)]
+    if not any(pbc):
+        return np.zeros((1, 3), np.int32)
+    mo = _max_offsets(cell, rc, cap)
+    rows = [(0, 0, 0)]
+    for a in range(-cap, cap + 1):
+        for b in range(-cap, cap + 1):
+            for c in range(-cap, cap + 1):
+                s = (a, b, c)
+                if s == (0, 0, 0):
+                    continue
+                if any(abs(s[d]) > mo[d] or (s[d] != 0 and not pbc[d]) for d in range(3)):
+                    continue
+                rows.append(s)
+    return np.asarray(rows, np.int32)
+
+
+def shift_offsets(shifts: np.ndarray, cell: np.ndarray) -> np.ndarray:
+    A = np.asarray(cell, F32).reshape(3, 3)
+    s = shifts.astype(F32)
+    return ((s[:, 0:1] * A[0] + s[:, 1:2] * A[1]) + s[:, 2:3] * A[2]).astype(F32)
+
+
+@dataclass
+class NeighborList:
+    n_atoms: int
+    n_edges: int
+    row_ptr: torch.Tensor     # [N+1] int32
+    col: torch.Tensor         # [E] int32 source atom
+    shift_idx: torch.Tensor   # [E] int32 row of ``shifts``
+    shifts: torch.Tensor      # [S,3] int32 (host)
+    dvec: torch.Tensor        # [E,3] fp32
+    dist: torch.Tensor        # [E] fp32
+    edge_row: torch.Tensor    # [E] int32
+    key_ptr: torch.Tensor     # [N+1] int32
+    key_eid: torch.Tensor     # [E] int32
+    max_row: int = 0
+
+    def canonical(self):
+        """(i, j, s) sorted lexicographically, plus dvec/dist in that order (numpy)."""
+        i = self.edge_row.cpu().numpy().astype(np.int64)
+        j = self.col.cpu().numpy().astype(np.int64)
+        s = self.shifts.numpy()[self.shift_idx.cpu().numpy()]
+        dv = self.dvec.cpu().numpy()
+        d = self.dist.cpu().numpy()
+        o = np.lexsort((s[:, 2], s[:, 1], s[:, 0], j, i))
+        return dict(i=i[o], j=j[o], s=s[o], dv=dv[o], d=d[o])
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
+                    max_neighbors: Optional[int] = None, cells_per_direction: int = 4) -> NeighborList:
+    """pos [N,3] fp32 on the GPU (graphs contiguous); graph_ptr [B+1], cells
+    [B,3,3], pbcs [B,3] on the host."""
+    if not pos.is_cuda:
+        raise RuntimeError("build_neighbors runs on the GPU only (pos must be a CUDA/HIP tensor)")
+    dev = pos.device
+    pos = pos.detach().to(torch.float32).contiguous()
+    graph_ptr = np.asarray(graph_ptr, np.int64)
+    cells = np.asarray(cells, F32).reshape(-1, 3, 3)
+    pbcs = np.asarray(pbcs, bool).reshape(-1, 3)
+    N = int(pos.shape[0])
+    B = len(graph_ptr) - 1
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    i32 = dict(dtype=torch.int32, device=dev)
+    # per-graph bounding boxes (one host sync)
+    atom_graph = torch.repeat_interleave(torch.arange(B, device=dev, dtype=torch.int32),
+                                         torch.as_tensor(np.diff(graph_ptr), device=dev))
+    if N:
+        lo = torch.full((B, 3), float("inf"), device=dev).scatter_reduce(
+            0, atom_graph.long()[:, None].expand(-1, 3), pos, "amin", include_self=True)
+        hi = torch.full((B, 3), float("-inf"), device=dev).scatter_reduce(
+            0, atom_graph.long()[:, None].expand(-1, 3), pos, "amax", include_self=True)
+        bb = torch.stack([lo, hi]).cpu().numpy()
+    else:
+        bb = np.zeros((2, B, 3), F32)
+    shifts, sptr, periodic = [], [0], []
+    glo = np.zeros((B, 3), F32); gh = np.zeros((B, 3), F32); gdim = np.zeros((B, 3), np.int32)
+    base = np.zeros(B, np.int32)
+    nb = 0
+    h_min = F32(rc + BIN_MARGIN)
+    for g in range(B):
+        sh = shift_table(cells[g], pbcs[g], rc, cells_per_direction)
+        shifts.append(sh)
+        sptr.append(sptr[-1] + len(sh))
+        periodic.append(1 if pbcs[g].any() else 0)
+        if graph_ptr[g + 1] > graph_ptr[g]:
+            l, h = bb[0, g], bb[1, g]
+        else:
+            l, h = np.zeros(3, F32), np.zeros(3, F32)
+        ext = np.maximum(h - l, 0.0)
+        dims = np.maximum(1, np.floor(ext / h_min)).astype(np.int64)
+        while np.prod(dims) > (1 << 22):
+            dims = np.maximum(1, dims // 2)
+        glo[g] = l
+        gh[g] = np.maximum(ext / dims, h_min)
+        gdim[g] = dims
+        base[g] = nb
+        nb += int(np.prod(dims))
+    shifts_np = np.concatenate(shifts).astype(np.int32)
+    offs = np.concatenate([shift_offsets(s, cells[g]) for g, s in enumerate(shifts)]).astype(F32)
+    up = lambda a, dt: torch.as_tensor(np.ascontiguousarray(a), dtype=dt, device=dev)
+    t_gptr = up(graph_ptr.astype(np.int32), torch.int32)
+    t_sptr = up(np.asarray(sptr, np.int32), torch.int32)
+    t_per = up(np.asarray(periodic, np.int32), torch.int32)
+    t_off = up(offs.reshape(-1, 3), torch.float32)
+    t_lo = up(glo, torch.float32); t_h = up(gh, torch.float32); t_dim = up(gdim, torch.int32)
+    t_base = up(base, torch.int32)
+    atom_bin = torch.empty(max(N, 1), **i32)
+    bin_count = torch.empty(nb, **i32)
+    bin_start = torch.empty(nb + 1, **i32)
+    bin_atoms = torch.empty(max(N, 1), **i32)
+    stats = torch.zeros(2, **i32)
+    plan = _lib.NbrPlan(N, B, nb, len(offs), rc, rmin, pos.data_ptr(), atom_graph.data_ptr(), t_gptr.data_ptr(),
+                        t_sptr.data_ptr(), t_per.data_ptr(), t_off.data_ptr(), t_lo.data_ptr(), t_h.data_ptr(),
+                        t_dim.data_ptr(), t_base.data_ptr(), atom_bin.data_ptr(), bin_count.data_ptr(),
+                        bin_start.data_ptr(), bin_atoms.data_ptr(), stats.data_ptr())
+    _lib.call("e2v2_nbr_bin", _lib.C.byref(plan), _lib.vp(stream))
+    row_count = torch.empty(max(N, 1), **i32)
+    row_ptr = torch.empty(N + 1, **i32)
+    _lib.call("e2v2_nbr_count", _lib.C.byref(plan), _lib.vp(row_count.data_ptr()), _lib.vp(row_ptr.data_ptr()),
+              _lib.vp(stream))
+    E, max_row = (int(x) for x in stats.cpu())
+    f32t = dict(dtype=torch.float32, device=dev)
+    tcol = torch.empty(max(E, 1), **i32); tsh = torch.empty(max(E, 1), **i32)
+    tdv = torch.empty(max(E, 1), 3, **f32t); td = torch.empty(max(E, 1), **f32t)
+    tkey = torch.empty(max(E, 1), dtype=torch.int64, device=dev)
+    col = torch.empty(E, **i32); sh = torch.empty(E, **i32)
+    dvec = torch.empty(E, 3, **f32t); dist = torch.empty(E, **f32t)
+    _lib.call("e2v2_nbr_fill", _lib.C.byref(plan), _lib.vp(row_ptr.data_ptr()), _lib.i64(E), _lib.i32(max_row),
+              _lib.vp(tcol.data_ptr()), _lib.vp(tsh.data_ptr()), _lib.vp(tdv.data_ptr()), _lib.vp(td.data_ptr()),
+              _lib.vp(tkey.data_ptr()), _lib.vp(_ptr(col)), _lib.vp(_ptr(sh)), _lib.vp(_ptr(dvec)),
+              _lib.vp(_ptr(dist)), _lib.vp(stream))
+    del tcol, tsh, tdv, td
+    if max_neighbors is not None and E > 0 and max_row > max_neighbors:
+        cnt = torch.empty(max(N, 1), **i32)
+        new_ptr = torch.empty(N + 1, **i32)
+        _lib.call("e2v2_nbr_topk", _lib.vp(row_ptr.data_ptr()), _lib.i32(N), _lib.i32(int(max_neighbors)),
+                  _lib.vp(cnt.data_ptr()), _lib.vp(new_ptr.data_ptr()), _lib.vp(stats.data_ptr()),
+                  None, None, None, None, None, None, None, None, _lib.i32(0), _lib.vp(stream))
+        E2, max_row = (int(x) for x in stats.cpu())
+        col2 = torch.empty(E2, **i32); sh2 = torch.empty(E2, **i32)
+        dv2 = torch.empty(E2, 3, **f32t); d2 = torch.empty(E2, **f32t)
+        _lib.call("e2v2_nbr_topk", _lib.vp(row_ptr.data_ptr()), _lib.i32(N), _lib.i32(int(max_neighbors)),
+                  _lib.vp(cnt.data_ptr()), _lib.vp(new_ptr.data_ptr()), _lib.vp(stats.data_ptr()),
+                  _lib.vp(_ptr(col)), _lib.vp(_ptr(sh)), _lib.vp(_ptr(dvec)), _lib.vp(_ptr(dist)),
+                  _lib.vp(_ptr(col2)), _lib.vp(_ptr(sh2)), _lib.vp(_ptr(dv2)), _lib.vp(_ptr(d2)),
+                  _lib.i32(1), _lib.vp(stream))
+        row_ptr, col, sh, dvec, dist, E = new_ptr, col2, sh2, dv2, d2, E2
+    edge_row = torch.empty(E, **i32)
+    key_cnt = torch.empty(max(N, 1), **i32)
+    key_ptr = torch.empty(N + 1, **i32)
+    _lib.call("e2v2_csr_transpose", _lib.vp(row_ptr.data_ptr()), _lib.vp(_ptr(col)), _lib.i32(N), _lib.i32(N),
+              _lib.i64(E), _lib.vp(_ptr(edge_row)), _lib.vp(key_cnt.data_ptr()), _lib.vp(key_ptr.data_ptr()),
+              _lib.vp(stats.data_ptr()), None, None, _lib.i32(0), _lib.vp(stream))
+    max_col = int(stats.cpu()[1])
+    if max_col > 4096:
+        raise RuntimeError(f"an atom is the source of {max_col} edges; the column sort supports at most 4096")
+    key_eid = torch.empty(E, **i32)
+    _lib.call("e2v2_csr_transpose", _lib.vp(row_ptr.data_ptr()), _lib.vp(_ptr(col)), _lib.i32(N), _lib.i32(N),
+              _lib.i64(E), _lib.vp(_ptr(edge_row)), _lib.vp(key_cnt.data_ptr()), _lib.vp(key_ptr.data_ptr()),
+              _lib.vp(stats.data_ptr()), _lib.vp(tkey.data_ptr()), _lib.vp(_ptr(key_eid)), _lib.i32(1),
+              _lib.vp(stream))
+    return NeighborList(N, E, row_ptr, col, sh, torch.as_tensor(shifts_np), dvec, dist, edge_row, key_ptr, key_eid,
+                        max_row)

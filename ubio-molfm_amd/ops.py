@@ -1,0 +1,228 @@
+"""Autograd operators over libe2v2.so (HIP, gfx950).
+
+Each Function computes on the current stream of the input tensors' device and
+calls the C ABI of include/e2v2.h; there is no CPU or PyTorch fallback.
+Weights of the radial MLPs are constants of these Functions (inference and
+force evaluation need input gradients only); ``create_graph=True`` (double
+backward) raises NotImplementedError instead of returning wrong gradients.
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional
+
+import torch
+from torch import nn
+
+from . import _lib
+from .neighbors import NeighborList
+
+ENV_EXPONENT = 5
+ENV_A = -(ENV_EXPONENT + 1) * (ENV_EXPONENT + 2) / 2
+ENV_B = ENV_EXPONENT * (ENV_EXPONENT + 2)
+ENV_C = -ENV_EXPONENT * (ENV_EXPONENT + 1) / 2
+
+
+def _stream(t: torch.Tensor):
+    return _lib.vp(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else _lib.vp(t.data_ptr())
+
+
+def _need_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("the e2v2 HIP path needs GPU tensors (no CPU fallback)")
+
+
+def _no_double_backward():
+    if torch.is_grad_enabled():
+        raise NotImplementedError("the HIP E2Former path implements first-order input gradients only "
+                                  "(create_graph=True / double backward is not supported)")
+
+
+class PackedMLP:
+    """Device-ready weights of one RadialProfile [K0 + 2 E -> 128 -> 128 -> 256]
+    (src/molfm/models/e2former/module_utils.py:2151-2178) whose input is
+    [rbf(256), target_table[z_i], source_table[z_j]]."""
+
+    def __init__(self, net: nn.Sequential, tgt: torch.Tensor, src: torch.Tensor, n_rbf: int = 256):
+        lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
+        with torch.no_grad():
+            W1 = lin1.weight.detach().float().contiguous()
+            e = tgt.shape[1]
+            self.w1 = W1
+            self.w1t = W1[:, :n_rbf].t().contiguous()
+            self.ttgt = (tgt.detach().float() @ W1[:, n_rbf:n_rbf + e].t() + lin1.bias.detach().float()).contiguous()
+            self.tsrc = (src.detach().float() @ W1[:, n_rbf + e:n_rbf + 2 * e].t()).contiguous()
+            self.g1 = ln1.weight.detach().float().contiguous(); self.be1 = ln1.bias.detach().float().contiguous()
+            self.w2 = lin2.weight.detach().float().contiguous(); self.w2t = self.w2.t().contiguous()
+            self.b2 = lin2.bias.detach().float().contiguous()
+            self.g2 = ln2.weight.detach().float().contiguous(); self.be2 = ln2.bias.detach().float().contiguous()
+            self.w3 = lin3.weight.detach().float().contiguous(); self.w3t = self.w3.t().contiguous()
+            self.b3 = lin3.bias.detach().float().contiguous()
+        if not (abs(ln1.eps - 1e-5) < 1e-12 and abs(ln2.eps - 1e-5) < 1e-12):
+            raise NotImplementedError("RadialProfile LayerNorm eps must be 1e-5")
+        if self.w1t.shape != (256, 128) or self.w2.shape != (128, 128) or self.w3.shape != (256, 128):
+            raise NotImplementedError(f"RadialProfile shape {tuple(W1.shape)} -> {tuple(self.w3.shape)} "
+                                      "is not the [256+2E, 128, 128, 256] profile of the HIP kernels")
+
+    def struct(self) -> _lib.MlpWeights:
+        return _lib.MlpWeights(self.w1t.data_ptr(), self.ttgt.data_ptr(), self.tsrc.data_ptr(), self.g1.data_ptr(),
+                               self.be1.data_ptr(), self.w2t.data_ptr(), self.b2.data_ptr(), self.g2.data_ptr(),
+                               self.be2.data_ptr(), self.w3t.data_ptr(), self.b3.data_ptr(), self.w1.data_ptr(),
+                               int(self.w1.shape[1]), self.w2.data_ptr(), self.w3.data_ptr())
+
+
+def _version_key(params):
+    return tuple((p.data_ptr(), p._version, p.dtype, str(p.device)) for p in params)
+
+
+class MLPCache:
+    """Repack weights only when a parameter changed (MD loops reuse them)."""
+
+    def __init__(self):
+        self.key = None
+        self.packed: List[PackedMLP] = []
+
+    def get(self, nets, tgt_emb: nn.Embedding, src_emb: nn.Embedding):
+        params = [p for n in nets for p in n.parameters()] + [tgt_emb.weight, src_emb.weight]
+        key = _version_key(params)
+        if key != self.key:
+            self.packed = [PackedMLP(n, tgt_emb.weight, src_emb.weight) for n in nets]
+            self.key = key
+        return self.packed
+
+
+def mlp_args(nl: NeighborList, node_type: torch.Tensor, rbf_offset: torch.Tensor, rbf_coeff: float,
+             packed: List[PackedMLP]) -> _lib.MlpArgs:
+    ws = (_lib.MlpWeights * 3)()
+    for m, pk in enumerate(packed):
+        ws[m] = pk.struct()
+    return _lib.MlpArgs(nl.n_edges, len(packed), nl.dist.data_ptr(), nl.edge_row.data_ptr(), nl.col.data_ptr(),
+                        node_type.data_ptr(), rbf_offset.data_ptr(), float(rbf_coeff), ws)
+
+
+class EdgeGeometryFn(torch.autograd.Function):
+    """(dvec, dist) of every edge as a function of the positions; backward is the
+    deterministic row-minus-column reduction of e2v2_edge_to_pos."""
+
+    @staticmethod
+    def forward(ctx, pos, nl: NeighborList):
+        _need_cuda(pos)
+        ctx.nl = nl
+        return nl.dvec.clone(), nl.dist.clone()
+
+    @staticmethod
+    def backward(ctx, g_dvec, g_dist):
+        _no_double_backward()
+        nl = ctx.nl
+        dev = nl.dvec.device
+        if g_dvec is None:
+            g_dvec = torch.zeros_like(nl.dvec)
+        if g_dist is None:
+            g_dist = torch.zeros_like(nl.dist)
+        g_dvec = g_dvec.float().contiguous(); g_dist = g_dist.float().contiguous()
+        dpos = torch.empty(nl.n_atoms, 3, dtype=torch.float32, device=dev)
+        _lib.call("e2v2_edge_to_pos", _lib.i32(nl.n_atoms), _p(nl.row_ptr), _p(nl.key_ptr), _p(nl.key_eid),
+                  _p(nl.dvec), _p(nl.dist), _p(g_dvec), _p(g_dist), _p(dpos), _stream(dpos))
+        return dpos, None
+
+
+class DegreeEmbedFn(torch.autograd.Function):
+    """EdgeDegreeEmbeddingNetwork_higherorder.forward (e2former.py:689-753)."""
+
+    @staticmethod
+    def forward(ctx, dvec, dist, nl: NeighborList, node_type, rbf_offset, rbf_coeff: float, packed, avg: float,
+                rc: float):
+        _need_cuda(dvec, dist)
+        dev = dvec.device
+        E, N = nl.n_edges, nl.n_atoms
+        fea = torch.empty(max(E, 1), 3 * 256, dtype=torch.float32, device=dev)
+        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed)
+        _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(fea), _lib.i32(768), _stream(fea))
+        dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
+                             fea.data_ptr(), float(avg), float(rc), ENV_A, ENV_B, ENV_C)
+        x0 = torch.empty(N, 9, 256, dtype=torch.float32, device=dev)
+        _lib.call("e2v2_deg_fwd", _lib.C.byref(dargs), _p(x0), _stream(x0))
+        ctx.save_for_backward(fea)
+        ctx.nl, ctx.margs_src = nl, (node_type, rbf_offset, rbf_coeff, packed)
+        ctx.avg, ctx.rc = avg, rc
+        return x0
+
+    @staticmethod
+    def backward(ctx, gx0):
+        _no_double_backward()
+        (fea,) = ctx.saved_tensors
+        nl = ctx.nl
+        node_type, rbf_offset, rbf_coeff, packed = ctx.margs_src
+        dev = fea.device
+        E, N = nl.n_edges, nl.n_atoms
+        gx0 = gx0.float().contiguous()
+        dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
+                             fea.data_ptr(), float(ctx.avg), float(ctx.rc), ENV_A, ENV_B, ENV_C)
+        dfea = torch.empty_like(fea)
+        ddv = torch.empty(max(E, 1), 3, dtype=torch.float32, device=dev)
+        dd = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
+        _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(dfea), _p(ddv), _p(dd), _stream(gx0))
+        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed)
+        _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dfea), _lib.i32(768), _p(dd), _lib.i32(1), _stream(gx0))
+        return ddv[:E], dd[:E], None, None, None, None, None, None, None
+
+
+class AttentionFn(torch.autograd.Function):
+    """Edge part of E2AttentionArbOrder_sparse.forward (e2former.py:238-433) up to
+    the SO(2) product's forward_linear: returns the 20-row l3-sequential tensor
+    h_a - h_b of so2_tensor_product.py:385 for every query atom."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, dvec, dist, nl: NeighborList, node_type, rbf_offset, rbf_coeff: float, packed,
+                rc: float, q_div: float):
+        _need_cuda(q, k, v, dvec, dist)
+        dev = q.device
+        E, N = nl.n_edges, nl.n_atoms
+        q = q.float().contiguous(); k = k.float().contiguous(); v = v.float().contiguous()
+        gi = torch.empty(max(E, 1), 256, dtype=torch.float32, device=dev)
+        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed)
+        _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(gi), _lib.i32(256), _stream(q))
+        args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
+                             nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
+                             q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(q_div), float(rc),
+                             ENV_A, ENV_B, ENV_C)
+        out = torch.empty(N, 20, 256, dtype=torch.float32, device=dev)
+        mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
+        srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
+        cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
+        _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _p(out), _p(mrow), _p(srow), _p(cnt), _stream(q))
+        ctx.save_for_backward(q, k, v, gi, out, mrow, srow, cnt)
+        ctx.nl, ctx.margs_src, ctx.rc, ctx.q_div = nl, (node_type, rbf_offset, rbf_coeff, packed), rc, q_div
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        _no_double_backward()
+        q, k, v, gi, out, mrow, srow, cnt = ctx.saved_tensors
+        nl = ctx.nl
+        node_type, rbf_offset, rbf_coeff, packed = ctx.margs_src
+        dev = q.device
+        E, N = nl.n_edges, nl.n_atoms
+        gout = gout.float().contiguous()
+        args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
+                             nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
+                             q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(ctx.q_div),
+                             float(ctx.rc), ENV_A, ENV_B, ENV_C)
+        f = dict(dtype=torch.float32, device=dev)
+        dgi = torch.empty(max(E, 1), 256, **f)
+        ddv = torch.empty(max(E, 1), 3, **f)
+        dd = torch.empty(max(E, 1), **f)
+        dq = torch.empty_like(q); dk = torch.empty_like(k); dv = torch.empty_like(v)
+        w_e = torch.empty(max(E, 1), 128, **f)
+        dqk = torch.empty(max(E, 1), 128, **f)
+        _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(dgi),
+                  _p(ddv), _p(dd), _p(dq), _p(dk), _p(dv), _p(w_e), _p(dqk), _stream(gout))
+        del w_e, dqk
+        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed)
+        _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dgi), _lib.i32(256), _p(dd), _lib.i32(1), _stream(gout))
+        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None
