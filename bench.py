@@ -1,0 +1,183 @@
+"""Benchmark: fp32 energy + autograd forces of the E2Former-V2 stack on the
+10,000-atom periodic water/protein mix as a
+velocity-Verlet NVE loop at 1 fs with the neighbour list rebuilt every step.
+
+One step = neighbour rebuild + degree embedding + 4 attention layers, forward
+and force backward, + integrator update.  Prints ONE JSON line.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def load_package():
+    import importlib.util
+    if "ubio_molfm_amd" in sys.modules:
+        return sys.modules["ubio_molfm_amd"]
+    d = ROOT / "ubio-molfm_amd"
+    spec = importlib.util.spec_from_file_location("ubio_molfm_amd", d / "__init__.py",
+                                                  submodule_search_locations=[str(d)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["ubio_molfm_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+# algorithmic work per launch of each library entry point
+def mlp_fwd_flops(E, n_mlp):
+    return 2.0 * E * n_mlp * (256 * 128 + 128 * 128 + 128 * 256)
+
+
+def mlp_bwd_flops(E, n_mlp):
+    return 2.0 * E * n_mlp * (256 * 128 + 128 * 128 + 256 * 128 + 128 * 128 + 128 * 256)
+
+
+def attn_fwd_bytes(N, E):
+    return 4.0 * (N * (128 * 8 * 2 + 9 * 256 + 20 * 256 + 3 * 128) + E * (256 + 5) + N + 1)
+
+
+KERNEL_OF = {"e2v2_mlp_fwd": "k_mlp_fwd", "e2v2_mlp_bwd": "k_mlp_bwd", "e2v2_attn_fwd": "k_attn_fwd",
+             "e2v2_deg_fwd": "k_deg_fwd", "e2v2_deg_bwd": "k_deg_bwd", "e2v2_nbr_count": "k_nbr_count"}
+
+
+def traffic_from_profile(entry):
+    """HBM bytes per launch of the entry point's kernel from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated against a plain copy)."""
+    path = ROOT / "profiles" / "hbm_traffic_cfg4_md10k.txt"
+    k = KERNEL_OF.get(entry)
+    if k is None or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if parts and parts[0] == k and len(parts) == 4:
+            return float(parts[3]) * 1e9
+    return None
+
+
+def cpu_baseline(pkg):
+    """Oracle (restated reference path, torch CPU fp32) on a 300-atom periodic
+    water/protein mix built by the configs[3] recipe (same density and element
+    ratios); one evaluation after a warm-up on a 12-atom cell."""
+    import numpy as np
+    import torch
+    from ubio_molfm_amd import systems
+    from oracle.model import MolfmAtomic as OracleModel
+    from oracle.cpu_path import energy_forces_with_neighbors
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    torch.manual_seed(0)
+    om = OracleModel().eval()
+    energy_forces_with_neighbors(om, systems.small_water(4, 5.5, seed=1))
+    sysd = systems.solvated_chains(300, seed=0)
+    t0 = time.perf_counter()
+    e, f, n_edges = energy_forces_with_neighbors(om, sysd)
+    t = time.perf_counter() - t0
+    return {"value": n_edges / t, "unit": "edges/s", "cores": cores, "kind": "port",
+            "sample": f"300-atom periodic water/protein mix (configs[3] recipe, {n_edges} edges): one fp32 "
+                      f"energy+force evaluation of the restated reference path (oracle/, torch CPU) after a "
+                      f"warm-up; {t:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="run one plain 256 MiB device copy first (scale reference for FETCH_SIZE/WRITE_SIZE)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is described in DESIGN.md "
+                                   "and not launched", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+    pkg = load_package()
+    from ubio_molfm_amd import _lib, md, model, systems
+    dev = torch.device("cuda:0")
+    if args.pmc_calibration:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    torch.manual_seed(0)
+    m = model.MolfmAtomic(model.default_args()).eval().to(dev)
+    sysd = systems.CONFIGS[args.config]()
+    N = len(sysd["pos"])
+    integ = md.VelocityVerlet(m, sysd, dev, dt_fs=1.0, T=300.0, seed=0)
+    integ.e, integ.f = integ.forces()          # setup: forces at t = 0
+    for _ in range(args.warmup):
+        integ.step()
+    torch.cuda.synchronize()
+    timer = _lib.KernelTimer(["e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd",
+                              "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill"])
+    edges = []
+    e_start = integ.e.sum().item() + integ.kinetic()
+    _lib.set_timer(timer)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        integ.step()
+        edges.append(integ.n_edges)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.set_timer(None)
+    e_end = integ.e.sum().item() + integ.kinetic()
+    dt = t1 - t0
+    ms = dt / args.steps * 1e3
+    E_mean = float(np.mean(edges))
+    stats = timer.summary()
+    # dominant library call by total time
+    dom = max(stats.items(), key=lambda kv: kv[1]["total_ms"])
+    name, st = dom
+    n_mlp = {"e2v2_mlp_fwd": None, "e2v2_mlp_bwd": None}
+    if name in ("e2v2_mlp_fwd", "e2v2_mlp_bwd"):
+        # per launch: deg (3 profiles) once, attention (1 profile) 4 times per step
+        fl = mlp_fwd_flops if name == "e2v2_mlp_fwd" else mlp_bwd_flops
+        per_step = fl(E_mean, 3) + 4 * fl(E_mean, 1)
+        achieved = per_step / (st["count"] / args.steps) / (st["avg_ms"] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / FP32_PEAK_TFLOPS, "traffic": traffic_from_profile(name), "kernel": name}
+    else:
+        b = attn_fwd_bytes(N, E_mean)
+        achieved = b / (st["avg_ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profile(name), "kernel": name}
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(pkg)
+    out = {
+        "metric": "attn edges/s fwd+force-bwd & MD atom-steps/s at 10k atoms; % HBM roofline",
+        "value": E_mean * args.steps / dt,
+        "unit": "edges/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded generator, random-init weights)",
+        "config": {"workload": f"configs[{args.config - 1}] {sysd['name']}: {N} atoms, periodic, rc 6 A, "
+                               f"NVE velocity-Verlet 1 fs, neighbour rebuild every step, fp32 energy+forces",
+                   "atoms": N, "edges_per_step": E_mean, "layers": 4, "parallelism": "single GPU"},
+        "atom_steps_per_s": N * args.steps / dt,
+        "nve_energy_drift_ev_per_atom": (e_end - e_start) / N,
+        "kernels": {k: {"avg_ms": round(v["avg_ms"], 4), "count": v["count"], "total_ms": round(v["total_ms"], 3)}
+                    for k, v in stats.items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -72,9 +72,54 @@ def load():
     return lib
 
 
-def call(name: str, *args) -> None:
+class KernelTimer:
+    """HIP-event timing of selected entry points on the stream they run on
+    (torch's current stream, which every call in this package uses)."""
+
+    def __init__(self, names):
+        self.names = set(names)
+        self.events = {n: [] for n in names}
+
+    def wrap(self, name, fn):
+        import torch
+        if name not in self.names:
+            return fn()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        out = fn()
+        e.record()
+        self.events[name].append((s, e))
+        return out
+
+    def summary(self):
+        import torch
+        torch.cuda.synchronize()
+        out = {}
+        for n, evs in self.events.items():
+            if not evs:
+                continue
+            ts = [a.elapsed_time(b) for a, b in evs]
+            out[n] = {"count": len(ts), "avg_ms": sum(ts) / len(ts), "total_ms": sum(ts)}
+        return out
+
+
+_timer = None
+
+
+def set_timer(t):
+    global _timer
+    _timer = t
+
+
+def _call_raw(name, *args):
     lib = load()
     rc = getattr(lib, name)(*args)
     if rc != 0:
         msg = lib.e2v2_last_error().decode(errors="replace")
         raise RuntimeError(f"{name} failed (code {rc}): {msg}")
+
+
+def call(name: str, *args) -> None:  # noqa: F811  (timed variant)
+    if _timer is not None:
+        return _timer.wrap(name, lambda: _call_raw(name, *args))
+    return _call_raw(name, *args)
