@@ -114,7 +114,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     torch.manual_seed(0)
-    m = model.MolfmAtomic(model.default_args()).eval().to(dev)
+    m = model.MolfmAtomic(model.default_args()).eval().to(dev).requires_grad_(False)
     sysd = systems.CONFIGS[args.config]()
     N = len(sysd["pos"])
     integ = md.VelocityVerlet(m, sysd, dev, dt_fs=1.0, T=300.0, seed=0)

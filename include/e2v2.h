@@ -35,6 +35,8 @@
  *   e2v2_deg_fwd/bwd    edge_degree_outer_triton (triton_dr/edge_degree_outer_autograd.py:299-375) with the
  *                       spherical harmonics and envelope of EdgeDegreeEmbeddingNetwork_higherorder.forward
  *                       (e2former.py:689-753)
+ *   e2v2_rmsnorm_*      EquivariantRMSNormArraySphericalHarmonicsV2_BL (module_utils.py:1663-1772)
+ *   e2v2_gate_*         Gate_s3 activation (module_utils.py:2694-2746)
  *   e2v2_edge_to_pos    autograd of f_edge_vec / f_dist w.r.t. positions (module_utils.py:3161-3206),
  *                       consumed by GradientHead (src/molfm/pipeline/head.py:305-328)
  */
@@ -146,15 +148,16 @@ typedef struct e2v2_attn_args {
   const float* dist;             /* [E]                                             */
   const float* q;                /* [N,H,D]                                         */
   const float* k;                /* [N,H,D]                                         */
-  const float* v;                /* [N,9,C]                                         */
+  const float* v;                /* [9][N][C] m-major                               */
   const float* gi;               /* [E,2H] gate | inputhead                         */
   float q_div;                   /* sqrt(D)                                         */
   float rc, env_a, env_b, env_c; /* polynomial envelope                             */
 } e2v2_attn_args;
 
-/* out [N,20,C]; mrow/srow [N,H] softmax max / sum; cnt [N,H] number of maxima */
+/* v [9][N][C] and out [20][N][C] are m-major (row r of every atom contiguous);
+   out: h_a - h_b rows of the SO(2) product; mrow/srow [N,H] softmax max / sum; cnt [N,H] number of maxima */
 int e2v2_attn_fwd(const e2v2_attn_args* args, float* out, float* mrow, float* srow, int32_t* cnt, hipStream_t s);
-/* grad_out, out [N,20,C] -> dgi [E,2H], ddvec [E,3], ddist [E], dq, dk [N,H,D], dv [N,9,C];
+/* grad_out, out [20][N][C] -> dgi [E,2H], ddvec [E,3], ddist [E], dq, dk [N,H,D], dv [9][N][C];
    w_edge, dqk_edge [E,H] are outputs consumed by the column pass */
 int e2v2_attn_bwd(const e2v2_attn_args* args, const float* grad_out, const float* out, const float* mrow,
                   const float* srow, const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq,
@@ -173,9 +176,21 @@ typedef struct e2v2_deg_args {
   float rc, env_a, env_b, env_c;
 } e2v2_deg_args;
 
+/* x0 [9][N][C] m-major */
 int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s);
 int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* dfea, float* ddvec, float* ddist,
                  hipStream_t s);
+
+/* ---- per-node kernels (node layout m-major: x[9][N][256]) --------------- */
+/* rms_norm_sh: EquivariantRMSNormArraySphericalHarmonicsV2_BL
+ * (src/molfm/models/e2former/module_utils.py:1663-1772); w [3][256], b [256] */
+int e2v2_rmsnorm_fwd(const float* x, const float* w, const float* b, float* y, int n, float eps, hipStream_t s);
+int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, float* gx, int n, float eps, hipStream_t s);
+/* Gate_s3 activation (module_utils.py:2694-2746) from gate logits sc [N][768];
+ * k1, k2 = normalize2mom constants of SiLU and sigmoid */
+int e2v2_gate_fwd(const float* sc, const float* x, float* y, int n, float k1, float k2, hipStream_t s);
+int e2v2_gate_bwd(const float* sc, const float* x, const float* gy, float* gsc, float* gx, int n, float k1,
+                  float k2, hipStream_t s);
 
 /* ---- positions --------------------------------------------------------- */
 int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,

@@ -78,12 +78,13 @@ def test_attention_forward_backward(pkg, cuda):
     print(f"[attn] N={N} E={E}", flush=True)
     q, k, v, gi = _attn_inputs(nl, cuda)
     st = _lib.vp(torch.cuda.current_stream().cuda_stream)
-    qd, kd, vd, gid = (t.to(cuda).contiguous() for t in (q, k, v, gi))
+    qd, kd, gid = (t.to(cuda).contiguous() for t in (q, k, gi))
+    vd = v.permute(1, 0, 2).contiguous().to(cuda)        # m-major [9, N, C]
     args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
                          nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                          qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), gid.data_ptr(), math.sqrt(8.0), 6.0,
                          ops.ENV_A, ops.ENV_B, ops.ENV_C)
-    out = torch.empty(N, 20, 256, device=cuda); m = torch.empty(N, 128, device=cuda)
+    out = torch.empty(20, N, 256, device=cuda); m = torch.empty(N, 128, device=cuda)
     sr = torch.empty(N, 128, device=cuda); cnt = torch.empty(N, 128, dtype=torch.int32, device=cuda)
     _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _lib.vp(out.data_ptr()), _lib.vp(m.data_ptr()),
               _lib.vp(sr.data_ptr()), _lib.vp(cnt.data_ptr()), st)
@@ -91,10 +92,10 @@ def test_attention_forward_backward(pkg, cuda):
     row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()
     leaves = [t.double().requires_grad_(True) for t in (q, k, v, nl.dvec.cpu(), nl.dist.cpu(), gi)]
     ref = attn_ref(*leaves[:5], row, col, leaves[5], T, 6.0, N)
-    e_f = relerr(out, ref)
+    e_f = relerr(out.permute(1, 0, 2), ref)
     G = torch.randn(N, 20, 256, generator=torch.Generator().manual_seed(7))
     grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
-    Gd = G.to(cuda)
+    Gd = G.permute(1, 0, 2).contiguous().to(cuda)
     f = dict(device=cuda)
     dgi = torch.empty(E, 256, **f); ddv = torch.empty(E, 3, **f); dd = torch.empty(E, **f)
     dq = torch.empty_like(qd); dk = torch.empty_like(kd); dv = torch.empty_like(vd)
@@ -103,7 +104,8 @@ def test_attention_forward_backward(pkg, cuda):
               _lib.vp(m.data_ptr()), _lib.vp(sr.data_ptr()), _lib.vp(cnt.data_ptr()), _lib.vp(dgi.data_ptr()),
               _lib.vp(ddv.data_ptr()), _lib.vp(dd.data_ptr()), _lib.vp(dq.data_ptr()), _lib.vp(dk.data_ptr()),
               _lib.vp(dv.data_ptr()), _lib.vp(we.data_ptr()), _lib.vp(dqk.data_ptr()), st)
-    errs = dict(q=relerr(dq, grads[0]), k=relerr(dk, grads[1]), v=relerr(dv, grads[2]), dvec=relerr(ddv, grads[3]),
+    errs = dict(q=relerr(dq, grads[0]), k=relerr(dk, grads[1]), v=relerr(dv.permute(1, 0, 2), grads[2]),
+                dvec=relerr(ddv, grads[3]),
                 dist=relerr(dd, grads[4]), gi=relerr(dgi, grads[5]))
     print(f"[attn] fwd rel {e_f:.2e} bwd {errs}", flush=True)
     assert e_f < 2e-5
@@ -120,7 +122,7 @@ def test_degree_forward_backward(pkg, cuda):
     st = _lib.vp(torch.cuda.current_stream().cuda_stream)
     a = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(), feaD.data_ptr(),
                      23.01, 6.0, ops.ENV_A, ops.ENV_B, ops.ENV_C)
-    x0 = torch.empty(N, 9, 256, device=cuda)
+    x0 = torch.empty(9, N, 256, device=cuda)
     _lib.call("e2v2_deg_fwd", _lib.C.byref(a), _lib.vp(x0.data_ptr()), st)
     row = nl.edge_row.long().cpu()
     leaves = [nl.dvec.cpu().double().requires_grad_(True), nl.dist.cpu().double().requires_grad_(True),
@@ -128,11 +130,11 @@ def test_degree_forward_backward(pkg, cuda):
     ref = deg_ref(leaves[0], leaves[1], row, leaves[2], 23.01, 6.0, N)
     G = torch.randn(N, 9, 256, generator=torch.Generator().manual_seed(9))
     grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
-    Gd = G.to(cuda)
+    Gd = G.permute(1, 0, 2).contiguous().to(cuda)
     dfea = torch.empty_like(feaD); ddv = torch.empty(E, 3, device=cuda); dd = torch.empty(E, device=cuda)
     _lib.call("e2v2_deg_bwd", _lib.C.byref(a), _lib.vp(Gd.data_ptr()), _lib.vp(dfea.data_ptr()),
               _lib.vp(ddv.data_ptr()), _lib.vp(dd.data_ptr()), st)
-    errs = dict(fwd=relerr(x0, ref), dvec=relerr(ddv, grads[0]), dist=relerr(dd, grads[1]), fea=relerr(dfea, grads[2]))
+    errs = dict(fwd=relerr(x0.permute(1, 0, 2), ref), dvec=relerr(ddv, grads[0]), dist=relerr(dd, grads[1]), fea=relerr(dfea, grads[2]))
     print(f"[deg] {errs}", flush=True)
     assert errs["fwd"] < 2e-5
     for k_, e in errs.items():
@@ -159,3 +161,36 @@ def test_edge_to_pos(pkg, cuda):
     e = relerr(out, ref)
     print(f"[pos] rel {e:.2e}", flush=True)
     assert e < 1e-5
+
+
+def test_node_kernels_rmsnorm_gate(pkg, cuda):
+    """HIP rms_norm_sh and Gate_s3 (m-major) vs the oracle's torch modules."""
+    from ubio_molfm_amd import modules
+    from oracle.model import EquivariantRMSNormArraySphericalHarmonicsV2_BL as RefNorm, Gate_s3 as RefGate
+    torch.manual_seed(4)
+    N = 37
+    x = torch.randn(N, 9, 256, dtype=torch.float64)
+    ref_norm = RefNorm(2, 256).double()
+    ref_norm.affine_weight.data.uniform_(0.5, 1.5); ref_norm.affine_bias.data.uniform_(-0.3, 0.3)
+    xl = x.clone().requires_grad_(True)
+    yr = ref_norm(xl)
+    G = torch.randn_like(yr)
+    gr = torch.autograd.grad((yr * G).sum(), xl)[0]
+    norm = modules.EquivariantRMSNormArraySphericalHarmonicsV2_BL(2, 256).to(cuda)
+    norm.load_state_dict({k: v.float() for k, v in ref_norm.state_dict().items()})
+    xd = x.permute(1, 0, 2).float().contiguous().to(cuda).requires_grad_(True)
+    yd = norm(xd)
+    gd = torch.autograd.grad((yd * G.permute(1, 0, 2).float().to(cuda)).sum(), xd)[0]
+    e1, e2 = relerr(yd.permute(1, 0, 2), yr), relerr(gd.permute(1, 0, 2), gr)
+    ref_gate = RefGate(256, 2).double()
+    gate = modules.Gate_s3(256, 2).to(cuda)
+    gate.load_state_dict({k: v.float() for k, v in ref_gate.state_dict().items()})
+    xl = x.clone().requires_grad_(True)
+    yr = ref_gate(xl)
+    gr = torch.autograd.grad((yr * G).sum(), xl)[0]
+    xd = x.permute(1, 0, 2).float().contiguous().to(cuda).requires_grad_(True)
+    yd = gate(xd)
+    gd = torch.autograd.grad((yd * G.permute(1, 0, 2).float().to(cuda)).sum(), xd)[0]
+    e3, e4 = relerr(yd.permute(1, 0, 2), yr), relerr(gd.permute(1, 0, 2), gr)
+    print(f"[node] rms fwd {e1:.2e} bwd {e2:.2e} gate fwd {e3:.2e} bwd {e4:.2e}", flush=True)
+    assert max(e1, e3) < 2e-6 and max(e2, e4) < 1e-5

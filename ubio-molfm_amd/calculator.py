@@ -54,7 +54,7 @@ class E2FormerCalculator:
             if checkpoint_path not in (None, "none"):
                 sd = torch.load(checkpoint_path, map_location="cpu", weights_only=True)
                 model.load_state_dict(sd.get("model", sd), strict=False)
-        self.model = model.eval().to(self.device)
+        self.model = model.eval().to(self.device).requires_grad_(False)  # force evaluation only
         self.head_name = head_name
         self.ref_energy = None if ref_energy is None else torch.as_tensor(ref_energy, device=self.device)
 

@@ -83,7 +83,8 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
   __shared__ float scale_s[kH];
   __shared__ float inv_s[kH];
   __shared__ ChunkEdges ce;
-  const int i = blockIdx.x, t = threadIdx.x;
+  const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
+  if (i >= A.n_rows) return;
   const int h = t & (kH - 1), half = t >> 7;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   const Envelope env = make_env(A);
@@ -137,10 +138,11 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
       for (int el = 0; el < nc; ++el) {
         const float w = coef_s[el][hc];
         const float wx = w * ce.dv[el][0], wy = w * ce.dv[el][1], wz = w * ce.dv[el][2];
-        const float* vp = A.v + (size_t)ce.j[el] * (kNV * kC) + t;
+        const float* vp = A.v + (size_t)ce.j[el] * kC + t;
+        const size_t vs = (size_t)A.n_rows * kC;
         float vv[kNV];
 #pragma unroll
-        for (int r = 0; r < kNV; ++r) vv[r] = vp[r * kC];
+        for (int r = 0; r < kNV; ++r) vv[r] = vp[r * vs];
 #pragma unroll
         for (int r = 0; r < kNV; ++r) {
           acc[r][0] = fmaf(vv[r], wx, acc[r][0]);
@@ -164,9 +166,10 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
   for (int q = 0; q < kNT; ++q) o[q] = 0.f;
 #pragma unroll
   for (int z = 0; z < kTpNnz; ++z) o[kTp[z].t] = fmaf(kTp[z].c, acc[kTp[z].r][kTp[z].k], o[kTp[z].t]);
-  float* op = out + (size_t)i * (kNT * kC) + t;
+  float* op = out + (size_t)i * kC + t;
+  const size_t os = (size_t)A.n_rows * kC;
 #pragma unroll
-  for (int q = 0; q < kNT; ++q) op[q * kC] = o[q] * inv;
+  for (int q = 0; q < kNT; ++q) op[q * os] = o[q] * inv;
 }
 
 // dA[r][k] = sum_t T[t][r][k] g[t] for one channel
@@ -192,7 +195,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
   __shared__ float head_m[kH], head_inv[kH], head_dsum[kH], head_dmc[kH];
   __shared__ float dq_s[kH][kD];
   __shared__ ChunkEdges ce;
-  const int i = blockIdx.x, t = threadIdx.x;
+  const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
+  if (i >= A.n_rows) return;
   const int lane = t & 63, wave = t >> 6;
   const int h = t & (kH - 1), half = t >> 7;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
@@ -205,10 +209,11 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
     const int c = lane + 64 * q;
     float g[kNT];
     float sdot = 0.f;
+    const size_t os = (size_t)A.n_rows * kC;
 #pragma unroll
     for (int z = 0; z < kNT; ++z) {
-      g[z] = G[(size_t)i * (kNT * kC) + z * kC + c];
-      sdot = fmaf(g[z], O[(size_t)i * (kNT * kC) + z * kC + c], sdot);
+      g[z] = G[(size_t)i * kC + z * os + c];
+      sdot = fmaf(g[z], O[(size_t)i * kC + z * os + c], sdot);
     }
     tp_transpose(g, dA[q]);
     gdot[q] = sdot;
@@ -257,7 +262,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
     // transposed aggregation: one wave per edge
     for (int el = wave; el < nc; el += 4) {
       const float dvx = ce.dv[el][0], dvy = ce.dv[el][1], dvz = ce.dv[el][2];
-      const float* vp = A.v + (size_t)ce.j[el] * (kNV * kC) + lane;
+      const float* vp = A.v + (size_t)ce.j[el] * kC + lane;
+      const size_t vs = (size_t)A.n_rows * kC;
       float gx = 0.f, gy = 0.f, gz = 0.f;
       float dwc[4];
 #pragma unroll
@@ -265,7 +271,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
         float ux = 0.f, uy = 0.f, uz = 0.f;
 #pragma unroll
         for (int r = 0; r < kNV; ++r) {
-          const float vr = vp[r * kC + 64 * q];
+          const float vr = vp[r * vs + 64 * q];
           ux = fmaf(dA[q][r][0], vr, ux);
           uy = fmaf(dA[q][r][1], vr, uy);
           uz = fmaf(dA[q][r][2], vr, uz);
@@ -344,7 +350,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
 __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const float* __restrict__ G,
                                                       const float* __restrict__ w_e, const float* __restrict__ dqk_e,
                                                       float* __restrict__ dv_out, float* __restrict__ dk_out) {
-  const int j = blockIdx.x, t = threadIdx.x;
+  const int j = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
+  if (j >= A.n_rows) return;
   const int c = t, hc = t & (kH - 1);
   const int hk = t >> 1, d0 = 4 * (t & 1);
   float av[kNV];
@@ -356,8 +363,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const fl
     const int i = A.edge_row[e];
     const float dvx = A.dvec[3 * e], dvy = A.dvec[3 * e + 1], dvz = A.dvec[3 * e + 2];
     float g[kNT];
+    const size_t os = (size_t)A.n_rows * kC;
 #pragma unroll
-    for (int z = 0; z < kNT; ++z) g[z] = G[(size_t)i * (kNT * kC) + z * kC + c];
+    for (int z = 0; z < kNT; ++z) g[z] = G[(size_t)i * kC + z * os + c];
     float dA[kNV][3];
     tp_transpose(g, dA);
     const float w = w_e[e * kH + hc];
@@ -368,8 +376,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const fl
 #pragma unroll
     for (int d = 0; d < 4; ++d) ak[d] = fmaf(dqk, qp[d] / A.q_div, ak[d]);
   }
+  const size_t vs = (size_t)A.n_rows * kC;
 #pragma unroll
-  for (int r = 0; r < kNV; ++r) dv_out[(size_t)j * (kNV * kC) + r * kC + c] = av[r];
+  for (int r = 0; r < kNV; ++r) dv_out[(size_t)j * kC + r * vs + c] = av[r];
 #pragma unroll
   for (int d = 0; d < 4; ++d) dk_out[((size_t)j * kH + hk) * kD + d0 + d] = ak[d];
 }
@@ -385,7 +394,7 @@ E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, float* out, float* mrow, 
                "attn_fwd: built for H=%d D=%d C=%d, got H=%d D=%d C=%d", kH, kD, kC, A.n_heads, A.head_dim,
                A.channels);
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_attn_fwd, dim3(A.n_rows), dim3(256), 0, s, A, out, mrow, srow, cnt);
+  hipLaunchKernelGGL(k_attn_fwd, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, out, mrow, srow, cnt);
   E2V2_LAUNCHED("k_attn_fwd");
   return 0;
 }
@@ -397,10 +406,10 @@ E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const float* grad_out, co
   E2V2_REQUIRE(A.n_heads == kH && A.head_dim == kD && A.channels == kC,
                "attn_bwd: built for H=%d D=%d C=%d", kH, kD, kC);
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_attn_bwd_row, dim3(A.n_rows), dim3(256), 0, s, A, grad_out, out, mrow, srow, cnt, dgi, ddvec,
+  hipLaunchKernelGGL(k_attn_bwd_row, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, grad_out, out, mrow, srow, cnt, dgi, ddvec,
                      ddist, dq, w_edge, dqk_edge);
   E2V2_LAUNCHED("k_attn_bwd_row");
-  hipLaunchKernelGGL(k_attn_bwd_col, dim3(A.n_rows), dim3(256), 0, s, A, grad_out, w_edge, dqk_edge, dv, dk);
+  hipLaunchKernelGGL(k_attn_bwd_col, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, grad_out, w_edge, dqk_edge, dv, dk);
   E2V2_LAUNCHED("k_attn_bwd_col");
   return 0;
 }

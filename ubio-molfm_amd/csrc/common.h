@@ -67,6 +67,16 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X (each with
+// its own L2).  Give every XCD a contiguous range of rows so that spatially
+// adjacent rows (atoms are Morton-ordered by the host) share one L2.
+constexpr int kXcd = 8;
+__host__ __device__ __forceinline__ int xcd_grid(int n) { return ((n + kXcd - 1) / kXcd) * kXcd; }
+__device__ __forceinline__ int xcd_row(int b, int n) {
+  const int per = (n + kXcd - 1) / kXcd;
+  return (b % kXcd) * per + b / kXcd;
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 

@@ -39,7 +39,8 @@ __global__ __launch_bounds__(256) void k_deg_fwd(e2v2_deg_args A, float* __restr
   __shared__ float sh_s[32][9];
   __shared__ float p_s[32];
   __shared__ int64_t e_s[32];
-  const int i = blockIdx.x, c = threadIdx.x;
+  const int i = xcd_row(blockIdx.x, A.n_rows), c = threadIdx.x;
+  if (i >= A.n_rows) return;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   Envelope env;
   env.rc = A.rc; env.a = A.env_a; env.b = A.env_b; env.c = A.env_c;
@@ -75,14 +76,15 @@ __global__ __launch_bounds__(256) void k_deg_fwd(e2v2_deg_args A, float* __restr
     __syncthreads();
   }
 #pragma unroll
-  for (int m = 0; m < 9; ++m) x0[((size_t)i * 9 + m) * kDC + c] = acc[m] / A.avg;
+  for (int m = 0; m < 9; ++m) x0[((size_t)m * A.n_rows + i) * kDC + c] = acc[m] / A.avg;
 }
 
 // one workgroup per query atom; one wave per edge, lane owns channels lane + 64 q
 __global__ __launch_bounds__(256) void k_deg_bwd(e2v2_deg_args A, const float* __restrict__ G0,
                                                  float* __restrict__ dfea, float* __restrict__ ddv,
                                                  float* __restrict__ dd) {
-  const int i = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  if (i >= A.n_rows) return;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   Envelope env;
   env.rc = A.rc; env.a = A.env_a; env.b = A.env_b; env.c = A.env_c;
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(256) void k_deg_bwd(e2v2_deg_args A, const float* _
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
-    for (int m = 0; m < 9; ++m) g[q][m] = G0[((size_t)i * 9 + m) * kDC + lane + 64 * q] / A.avg;
+    for (int m = 0; m < 9; ++m) g[q][m] = G0[((size_t)m * A.n_rows + i) * kDC + lane + 64 * q] / A.avg;
   for (int el = wave; el < n; el += 4) {
     const int64_t e = (int64_t)b + el;
     const float d = A.dist[e];
@@ -177,7 +179,7 @@ E2V2_API int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s) {
   const e2v2_deg_args& A = *args;
   E2V2_REQUIRE(A.channels == kDC, "deg_fwd: built for C=%d, got %d", kDC, A.channels);
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_deg_fwd, dim3(A.n_rows), dim3(256), 0, s, A, x0);
+  hipLaunchKernelGGL(k_deg_fwd, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, x0);
   E2V2_LAUNCHED("k_deg_fwd");
   return 0;
 }
@@ -187,7 +189,7 @@ E2V2_API int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float
   const e2v2_deg_args& A = *args;
   E2V2_REQUIRE(A.channels == kDC, "deg_bwd: built for C=%d, got %d", kDC, A.channels);
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_deg_bwd, dim3(A.n_rows), dim3(256), 0, s, A, grad_x0, dfea, ddvec, ddist);
+  hipLaunchKernelGGL(k_deg_bwd, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, grad_x0, dfea, ddvec, ddist);
   E2V2_LAUNCHED("k_deg_bwd");
   return 0;
 }

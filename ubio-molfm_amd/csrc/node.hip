@@ -1,0 +1,173 @@
+// Per-node kernels on the m-major node layout x[9][N][C] (C = 256, l <= 2):
+//  * rms_norm_sh  = EquivariantRMSNormArraySphericalHarmonicsV2_BL
+//    (src/molfm/models/e2former/module_utils.py:1663-1772: centre the l = 0 row,
+//    degree-balanced mean square over all (m, c), affine per l, bias on l = 0)
+//  * Gate_s3 activation (module_utils.py:2694-2746) given the gate logits
+//    sc[N][3C] = gates(x[0]).
+// Backward passes return input gradients only (weights are constants for force
+// evaluation) and recompute the statistics.
+#include "common.h"
+#include "../../include/e2v2.h"
+
+namespace e2v2 {
+
+constexpr int kNC = 256;
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+__device__ __forceinline__ int lof(int m) { return m == 0 ? 0 : (m < 4 ? 1 : 2); }
+
+// balance weight of row m: 1 / ((2l+1) (lmax+1))
+__device__ __forceinline__ float bal(int m) {
+  const int l = lof(m);
+  return 1.0f / ((2.0f * l + 1.0f) * 3.0f);
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_fwd(const float* __restrict__ x, const float* __restrict__ w,
+                                                     const float* __restrict__ b, float* __restrict__ y, int n,
+                                                     float eps) {
+  __shared__ float red[4];
+  const int i = blockIdx.x, c = threadIdx.x;
+  const size_t st = (size_t)n * kNC;
+  const float* xp = x + (size_t)i * kNC + c;
+  float f[9];
+#pragma unroll
+  for (int m = 0; m < 9; ++m) f[m] = xp[m * st];
+  const float mean0 = block_sum256(f[0], red) * (1.0f / kNC);
+  f[0] -= mean0;
+  float ss = 0.f;
+#pragma unroll
+  for (int m = 0; m < 9; ++m) ss = fmaf(bal(m), f[m] * f[m], ss);
+  const float S = block_sum256(ss, red) * (1.0f / kNC);
+  const float r = 1.0f / sqrtf(S + eps);
+  float* yp = y + (size_t)i * kNC + c;
+#pragma unroll
+  for (int m = 0; m < 9; ++m) {
+    float v = f[m] * (r * w[lof(m) * kNC + c]);
+    if (m == 0) v += b[c];
+    yp[m * st] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w,
+                                                     const float* __restrict__ gy, float* __restrict__ gx, int n,
+                                                     float eps) {
+  __shared__ float red[4];
+  const int i = blockIdx.x, c = threadIdx.x;
+  const size_t st = (size_t)n * kNC;
+  const float* xp = x + (size_t)i * kNC + c;
+  const float* gp = gy + (size_t)i * kNC + c;
+  float f[9], g[9];
+#pragma unroll
+  for (int m = 0; m < 9; ++m) {
+    f[m] = xp[m * st];
+    g[m] = gp[m * st];
+  }
+  const float mean0 = block_sum256(f[0], red) * (1.0f / kNC);
+  f[0] -= mean0;
+  float ss = 0.f, dr = 0.f;
+#pragma unroll
+  for (int m = 0; m < 9; ++m) {
+    ss = fmaf(bal(m), f[m] * f[m], ss);
+    g[m] *= w[lof(m) * kNC + c];      // dL/d(f r) per element
+    dr = fmaf(g[m], f[m], dr);
+  }
+  const float S = block_sum256(ss, red) * (1.0f / kNC);
+  const float DR = block_sum256(dr, red);
+  const float r = 1.0f / sqrtf(S + eps);
+  const float dS = -0.5f * r * r * r * DR;
+  float gf[9];
+#pragma unroll
+  for (int m = 0; m < 9; ++m) gf[m] = g[m] * r + dS * 2.0f * bal(m) * f[m] * (1.0f / kNC);
+  const float gmean0 = block_sum256(gf[0], red) * (1.0f / kNC);
+  gf[0] -= gmean0;
+  float* op = gx + (size_t)i * kNC + c;
+#pragma unroll
+  for (int m = 0; m < 9; ++m) op[m * st] = gf[m];
+}
+
+__global__ void k_gate_fwd(const float* __restrict__ sc, const float* __restrict__ x, float* __restrict__ y, int n,
+                           float k1, float k2) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)n * kNC) return;
+  const int i = (int)(idx / kNC), c = (int)(idx % kNC);
+  const size_t st = (size_t)n * kNC;
+  const float* s = sc + (size_t)i * 3 * kNC;
+  y[idx] = silu(s[c]) * k1;
+  const float g1 = sigmoidf_(s[kNC + c]) * k2, g2 = sigmoidf_(s[2 * kNC + c]) * k2;
+#pragma unroll
+  for (int m = 1; m < 9; ++m) y[idx + m * st] = (m < 4 ? g1 : g2) * x[idx + m * st];
+}
+
+__global__ void k_gate_bwd(const float* __restrict__ sc, const float* __restrict__ x, const float* __restrict__ gy,
+                           float* __restrict__ gsc, float* __restrict__ gx, int n, float k1, float k2) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)n * kNC) return;
+  const int i = (int)(idx / kNC), c = (int)(idx % kNC);
+  const size_t st = (size_t)n * kNC;
+  const float* s = sc + (size_t)i * 3 * kNC;
+  float* gs = gsc + (size_t)i * 3 * kNC;
+  const float s0 = s[c];
+  const float sg0 = sigmoidf_(s0);
+  gs[c] = gy[idx] * k1 * sg0 * (1.0f + s0 * (1.0f - sg0));
+  gx[idx] = 0.f;
+  const float sg1 = sigmoidf_(s[kNC + c]), sg2 = sigmoidf_(s[2 * kNC + c]);
+  float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+  for (int m = 1; m < 9; ++m) {
+    const float g = gy[idx + m * st];
+    if (m < 4) {
+      a1 = fmaf(g, x[idx + m * st], a1);
+      gx[idx + m * st] = g * sg1 * k2;
+    } else {
+      a2 = fmaf(g, x[idx + m * st], a2);
+      gx[idx + m * st] = g * sg2 * k2;
+    }
+  }
+  gs[kNC + c] = a1 * k2 * sg1 * (1.0f - sg1);
+  gs[2 * kNC + c] = a2 * k2 * sg2 * (1.0f - sg2);
+}
+
+}  // namespace e2v2
+
+using namespace e2v2;
+
+E2V2_API int e2v2_rmsnorm_fwd(const float* x, const float* w, const float* b, float* y, int n, float eps,
+                              hipStream_t s) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_rmsnorm_fwd, dim3(n), dim3(256), 0, s, x, w, b, y, n, eps);
+  E2V2_LAUNCHED("k_rmsnorm_fwd");
+  return 0;
+}
+
+E2V2_API int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, float* gx, int n, float eps,
+                              hipStream_t s) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_rmsnorm_bwd, dim3(n), dim3(256), 0, s, x, w, gy, gx, n, eps);
+  E2V2_LAUNCHED("k_rmsnorm_bwd");
+  return 0;
+}
+
+E2V2_API int e2v2_gate_fwd(const float* sc, const float* x, float* y, int n, float k1, float k2, hipStream_t s) {
+  if (n == 0) return 0;
+  const int64_t tot = (int64_t)n * kNC;
+  hipLaunchKernelGGL(k_gate_fwd, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, sc, x, y, n, k1, k2);
+  E2V2_LAUNCHED("k_gate_fwd");
+  return 0;
+}
+
+E2V2_API int e2v2_gate_bwd(const float* sc, const float* x, const float* gy, float* gsc, float* gx, int n, float k1,
+                           float k2, hipStream_t s) {
+  if (n == 0) return 0;
+  const int64_t tot = (int64_t)n * kNC;
+  hipLaunchKernelGGL(k_gate_bwd, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, sc, x, gy, gsc, gx, n, k1, k2);
+  E2V2_LAUNCHED("k_gate_bwd");
+  return 0;
+}

@@ -25,6 +25,36 @@ from .neighbors import build_neighbors
 from .ops import EdgeGeometryFn
 
 
+def _spread_bits10(v: torch.Tensor) -> torch.Tensor:
+    v = v & 0x3FF
+    v = (v | (v << 16)) & 0x030000FF
+    v = (v | (v << 8)) & 0x0300F00F
+    v = (v | (v << 4)) & 0x030C30C3
+    v = (v | (v << 2)) & 0x09249249
+    return v
+
+
+def spatial_order(pos: torch.Tensor, graph_ptr) -> torch.Tensor:
+    """Permutation that sorts the atoms of every graph along a 30-bit Morton
+    (Z-order) curve of their positions; graphs stay contiguous and in order.
+    Neighbouring rows of the CSR then gather neighbouring source rows, which the
+    XCD-contiguous row mapping of the kernels keeps in one L2."""
+    N = pos.shape[0]
+    if N == 0:
+        return torch.zeros(0, dtype=torch.long, device=pos.device)
+    counts = torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device)
+    B = counts.shape[0]
+    gid = torch.repeat_interleave(torch.arange(B, device=pos.device), counts)
+    idx = gid[:, None].expand(-1, 3)
+    lo = torch.full((B, 3), float("inf"), device=pos.device).scatter_reduce(0, idx, pos, "amin", include_self=True)
+    hi = torch.full((B, 3), float("-inf"), device=pos.device).scatter_reduce(0, idx, pos, "amax", include_self=True)
+    span = (hi - lo).clamp_min(1e-6)
+    q = ((pos - lo[gid]) / span[gid] * 1023.0).clamp(0, 1023).to(torch.int64)
+    code = _spread_bits10(q[:, 0]) | (_spread_bits10(q[:, 1]) << 1) | (_spread_bits10(q[:, 2]) << 2)
+    key = (gid.to(torch.int64) << 32) | code
+    return torch.sort(key, stable=True).indices
+
+
 def _as_int_or_none(v):
     if v is None or (isinstance(v, str) and v.lower() == "none"):
         return None
@@ -54,9 +84,16 @@ class E2FormerBackbone(nn.Module):
 
     # -- flat interface -------------------------------------------------------
     def forward_flat(self, pos: torch.Tensor, Z: torch.Tensor, graph_ptr, cell, pbc, charge=None,
-                     multiplicity=None, nl=None):
+                     multiplicity=None, nl=None, reorder: bool = True):
         """pos [N,3] (may require grad), Z [N] on the GPU; graph_ptr/cell/pbc on the host.
-        Returns (node_irreps [N,9,C], neighbour list)."""
+        Returns (node_irreps [N,9,C], neighbour list, perm): rows of node_irreps and
+        the neighbour list refer to atoms ``perm`` (Morton order within each graph;
+        identity when ``reorder`` is False)."""
+        perm = None
+        if reorder and nl is None:
+            perm = spatial_order(pos.detach(), graph_ptr)
+            pos = pos[perm]
+            Z = Z[perm]
         if nl is None:
             nl = build_neighbors(pos.detach(), graph_ptr, cell, pbc, self.max_radius, 1e-4, self.max_neighbors,
                                  self.cells_per_direction)
@@ -71,7 +108,7 @@ class E2FormerBackbone(nn.Module):
                                             dim=-1)).reshape(B, -1)
             counts = torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device)
             sys_node = torch.repeat_interleave(sys_emb, counts, dim=0)
-        return self.decoder.forward_flat(ctx, sys_node), nl
+        return self.decoder.forward_flat(ctx, sys_node), nl, perm
 
     # -- reference interface -------------------------------------------------
     def forward(self, batched_data, **kwargs) -> Dict:
@@ -89,7 +126,10 @@ class E2FormerBackbone(nn.Module):
         fZ = Z[mask]
         charge = batched_data.get("charge", None)
         mult = batched_data.get("multiplicity", None)
-        x, nl = self.forward_flat(fpos, fZ, graph_ptr, cell, pbc, charge, mult)
+        x, nl, perm = self.forward_flat(fpos, fZ, graph_ptr, cell, pbc, charge, mult)
+        x = x.permute(1, 0, 2)                       # m-major -> [N, 9, C]
+        if perm is not None:
+            x = x.index_select(0, torch.argsort(perm))
         node_irreps = x.new_zeros((B, L, x.shape[1], x.shape[2]))
         node_irreps = node_irreps.masked_scatter(mask[:, :, None, None], x)
         return {"node_featuresBxN": node_irreps[:, :, 0], "node_vec_featuresBxN": node_irreps[:, :, 1:4],
@@ -158,9 +198,9 @@ class MolfmAtomic(nn.Module):
         self.head = MDEnergyForceMultiHead(args)
 
     def energy_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None, nl=None):
-        x, nl = self.decoder.forward_flat(pos, Z, graph_ptr, cell, pbc, charge, multiplicity, nl)
+        x, nl, _ = self.decoder.forward_flat(pos, Z, graph_ptr, cell, pbc, charge, multiplicity, nl)
         h = self.head.head_name(head)
-        e_atom = self.head.energy_heads[h](x[:, 0]).squeeze(-1)
+        e_atom = self.head.energy_heads[h](x[0]).squeeze(-1)     # x is m-major [9, N, C]
         B = len(graph_ptr) - 1
         gid = torch.repeat_interleave(torch.arange(B, device=pos.device),
                                       torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device))

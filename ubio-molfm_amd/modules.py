@@ -16,6 +16,7 @@ import torch
 from torch import nn
 
 from . import so3
+from . import _lib
 from .ops import AttentionFn, DegreeEmbedFn, MLPCache
 
 
@@ -35,12 +36,99 @@ def _expand_index(lmax: int) -> torch.Tensor:
     return torch.tensor([l for l in range(lmax + 1) for _ in range(2 * l + 1)], dtype=torch.long)
 
 
-def _per_l_matmul(x: torch.Tensor, weight: torch.Tensor, lmax: int) -> torch.Tensor:
-    """out[:, rows(l), :] = x[:, rows(l), :] @ weight[l].T (SO3 linear, no bias)."""
-    outs = []
-    for l in range(lmax + 1):
-        outs.append(torch.matmul(x[:, l * l:(l + 1) ** 2, :], weight[l].t()))
-    return torch.cat(outs, dim=1)
+def _stream():
+    return _lib.vp(torch.cuda.current_stream().cuda_stream)
+
+
+def _dp(t):
+    return _lib.vp(t.data_ptr())
+
+
+class SO3LinearFn(torch.autograd.Function):
+    """y[rows(l)] = x[rows(l)] W_l^T (+ bias on row 0) on the m-major layout
+    x[(lmax+1)^2, N, Cin]: each l block is one 2-D GEMM written in place.
+    W and bias are constants (input gradient only)."""
+
+    @staticmethod
+    def forward(ctx, x, W, bias, lmax: int):
+        x = x.contiguous()
+        L2, N, Cin = x.shape
+        O = W.shape[1]
+        y = x.new_empty(L2, N, O)
+        for l in range(lmax + 1):
+            a, b = l * l, (l + 1) ** 2
+            torch.mm(x[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
+        if bias is not None:
+            y[0].add_(bias)
+        ctx.save_for_backward(W)
+        ctx.lmax = lmax
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        (W,) = ctx.saved_tensors
+        gy = gy.contiguous()
+        L2, N, O = gy.shape
+        Cin = W.shape[2]
+        gx = gy.new_empty(L2, N, Cin)
+        for l in range(ctx.lmax + 1):
+            a, b = l * l, (l + 1) ** 2
+            torch.mm(gy[a:b].view(-1, O), W[l], out=gx[a:b].view(-1, Cin))
+        return gx, None, None, None
+
+
+class RMSNormFn(torch.autograd.Function):
+    """rms_norm_sh on x[9][N][256] through e2v2_rmsnorm_fwd/bwd."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, eps: float):
+        x = x.contiguous()
+        y = torch.empty_like(x)
+        _lib.call("e2v2_rmsnorm_fwd", _dp(x), _dp(w), _dp(b), _dp(y), _lib.i32(x.shape[1]), _lib.f32(eps),
+                  _stream())
+        ctx.save_for_backward(x, w)
+        ctx.eps = eps
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        gy = gy.contiguous()
+        gx = torch.empty_like(x)
+        _lib.call("e2v2_rmsnorm_bwd", _dp(x), _dp(w), _dp(gy), _dp(gx), _lib.i32(x.shape[1]), _lib.f32(ctx.eps),
+                  _stream())
+        return gx, None, None, None
+
+
+class GateFn(torch.autograd.Function):
+    """Gate_s3 activation from logits sc [N, 3C] and features x[9][N][C]."""
+
+    @staticmethod
+    def forward(ctx, sc, x, k1: float, k2: float):
+        sc = sc.contiguous(); x = x.contiguous()
+        y = torch.empty_like(x)
+        _lib.call("e2v2_gate_fwd", _dp(sc), _dp(x), _dp(y), _lib.i32(x.shape[1]), _lib.f32(k1), _lib.f32(k2),
+                  _stream())
+        ctx.save_for_backward(sc, x)
+        ctx.k = (k1, k2)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        sc, x = ctx.saved_tensors
+        gy = gy.contiguous()
+        gsc = torch.empty_like(sc); gx = torch.empty_like(x)
+        _lib.call("e2v2_gate_bwd", _dp(sc), _dp(x), _dp(gy), _dp(gsc), _dp(gx), _lib.i32(x.shape[1]),
+                  _lib.f32(ctx.k[0]), _lib.f32(ctx.k[1]), _stream())
+        return gsc, gx, None, None
+
+
+def _linear(x, lin: nn.Linear):
+    return torch.nn.functional.linear(x, lin.weight.detach(), None if lin.bias is None else lin.bias.detach())
+
+
+def _layer_norm(x, ln: nn.LayerNorm):
+    return torch.nn.functional.layer_norm(x, ln.normalized_shape, ln.weight.detach(), ln.bias.detach(), ln.eps)
 
 
 class GaussianSmearing(nn.Module):
@@ -79,7 +167,7 @@ class RadialProfile(nn.Module):
 
 
 class SO3_Linear_e2former(nn.Module):
-    """module_utils.py:2010-2052."""
+    """module_utils.py:2010-2052; input/output in the m-major layout [9, N, C]."""
 
     def __init__(self, in_features, out_features, lmax, bias=True):
         super().__init__()
@@ -91,12 +179,7 @@ class SO3_Linear_e2former(nn.Module):
         self.register_buffer("expand_index", _expand_index(lmax), persistent=False)
 
     def forward(self, x):
-        shp = x.shape[:-2]
-        ls = x.shape[-2]
-        x = x.reshape(-1, ls, x.shape[-1])
-        out = _per_l_matmul(x, self.weight, self.lmax)
-        out[:, 0, :] = out[:, 0, :] + self.bias
-        return out.reshape(shp + (ls, self.out_features))
+        return SO3LinearFn.apply(x, self.weight.detach(), self.bias.detach(), self.lmax)
 
 
 class SO3_Linear2Scalar_e2former(nn.Module):
@@ -117,28 +200,39 @@ class SO3_Linear2Scalar_e2former(nn.Module):
         self.final_linear = nn.Sequential(nn.Linear(hid * (lmax + 1), hid), nn.LayerNorm(hid), nn.SiLU(),
                                           nn.Linear(hid, out_features))
 
+    def stacked(self):
+        """[W | W2] and [bias | 0] for one fused GEMM."""
+        w = torch.cat([self.weight.detach(), self.weight2.detach()], dim=1)
+        b = torch.cat([self.bias.detach().view(-1), torch.zeros_like(self.bias.detach().view(-1))])
+        return w, b
+
+    def finish(self, a, b):
+        """a, b [9, N, hid] -> final_linear(cat_l sum_{m in l} a b) [N, out]."""
+        prod = a * b
+        parts = [prod[0]] + [prod[l * l:(l + 1) ** 2].sum(0) for l in range(1, self.lmax + 1)]
+        h = torch.cat(parts, dim=-1)
+        fl = self.final_linear
+        h = torch.nn.functional.silu(_layer_norm(_linear(h, fl[0]), fl[1]))
+        return _linear(h, fl[3])
+
     def forward(self, x):
-        shp = x.shape[:-2]
-        ls = x.shape[-2]
-        x = x.reshape(-1, ls, x.shape[-1])
+        w, b = self.stacked()
+        y = SO3LinearFn.apply(x, w, b, self.lmax)
         hid = self.weight.shape[1]
-        # both products in one GEMM per l: [rows, C] @ [C, 2 hid]
-        wcat = torch.cat([self.weight, self.weight2], dim=1)
-        o = _per_l_matmul(x, wcat, self.lmax)
-        a, b = o[..., :hid], o[..., hid:]
-        a = torch.cat([a[:, :1] + self.bias.view(1, 1, hid), a[:, 1:]], dim=1)
-        parts = [torch.sum(a[:, l * l:(l + 1) ** 2] * b[:, l * l:(l + 1) ** 2], dim=1) for l in range(self.lmax + 1)]
-        return self.final_linear(torch.cat(parts, dim=-1)).reshape(shp + (self.out_features,))
+        return self.finish(y[..., :hid], y[..., hid:])
 
 
 class EquivariantRMSNormArraySphericalHarmonicsV2_BL(nn.Module):
-    """module_utils.py:1663-1772 (rms_norm_sh: centering, balanced degrees)."""
+    """module_utils.py:1663-1772 (rms_norm_sh: centering, balanced degrees);
+    HIP kernel on the m-major layout."""
 
     def __init__(self, lmax, num_channels, eps=1e-5, affine=True, normalization="component", centering=True,
                  std_balance_degrees=True):
         super().__init__()
         if not (affine and centering and std_balance_degrees and normalization == "component"):
             raise NotImplementedError("only the rms_norm_sh configuration of the reference is implemented")
+        if lmax != 2 or num_channels != 256:
+            raise NotImplementedError("the HIP RMS norm is built for lmax 2 and 256 channels")
         self.lmax, self.num_channels, self.eps = lmax, num_channels, eps
         self.affine_weight = nn.Parameter(torch.ones(lmax + 1, num_channels))
         self.affine_bias = nn.Parameter(torch.zeros(num_channels))
@@ -149,20 +243,12 @@ class EquivariantRMSNormArraySphericalHarmonicsV2_BL(nn.Module):
         self.register_buffer("balance_degree_weight", bw / (lmax + 1))
 
     def forward(self, x, batch=None):
-        shp = x.shape[:-2]
-        f = x.reshape(-1, (self.lmax + 1) ** 2, self.num_channels)
-        f0 = f[:, :1] - f[:, :1].mean(dim=2, keepdim=True)
-        f = torch.cat([f0, f[:, 1:]], dim=1)
-        fn = (f.pow(2) * self.balance_degree_weight.view(1, -1, 1)).sum(dim=1, keepdim=True)
-        fn = (fn.mean(dim=2, keepdim=True) + self.eps).pow(-0.5)
-        w = self.affine_weight.index_select(0, self.expand_index).unsqueeze(0)
-        out = f * (fn * w)
-        out = torch.cat([out[:, :1] + self.affine_bias.view(1, 1, -1), out[:, 1:]], dim=1)
-        return out.reshape(shp + ((self.lmax + 1) ** 2, self.num_channels))
+        return RMSNormFn.apply(x, self.affine_weight.detach().float().contiguous(),
+                               self.affine_bias.detach().float().contiguous(), float(self.eps))
 
 
 class Gate_s3(nn.Module):
-    """module_utils.py:2694-2746."""
+    """module_utils.py:2694-2746 (HIP activation kernel)."""
 
     def __init__(self, sphere_channels, lmax, act_scalars="silu", act_vector="sigmoid"):
         super().__init__()
@@ -172,16 +258,8 @@ class Gate_s3(nn.Module):
         nn.init.uniform_(self.gates.weight, -bound, bound)
 
     def forward(self, x):
-        shp = x.shape
-        x = x.reshape(-1, shp[-2], shp[-1])
-        C = self.sphere_channels
-        sc = self.gates(x[:, 0:1])
-        out = [torch.nn.functional.silu(sc[:, :, :C]) * SILU_NORM]
-        st = 1
-        for l in range(1, self.lmax + 1):
-            out.append(torch.sigmoid(sc[:, :, l * C:(l + 1) * C]) * SIGMOID_NORM * x[:, st:st + 2 * l + 1])
-            st += 2 * l + 1
-        return torch.cat(out, dim=1).reshape(shp)
+        sc = _linear(x[0], self.gates)
+        return GateFn.apply(sc, x, SILU_NORM, SIGMOID_NORM)
 
 
 class FeedForwardNetwork_s3(nn.Module):
@@ -228,10 +306,23 @@ class SO2_TP_givenl2(nn.Module):
         self._canon_sel = sel
         self._canon_w = w
         self._rows = so3.path_rows(lmax)
+        self._scale_key = None
+        self._scale = None
 
     def path_scales(self) -> Optional[torch.Tensor]:
         """Per-row scale of the 20 output rows implied by the loaded CG_weight
-        relative to the canonical table, or None when they coincide."""
+        relative to the canonical table, or None when they coincide (cached on
+        the parameters' version counters: no host sync per call)."""
+        key = (self.selected_idx._version, self.CG_weight._version, self.CG_weight.data_ptr(),
+               self.selected_idx.data_ptr())
+        if key != self._scale_key:
+            self._scale = self._compute_scales()
+            if self._scale is not None:
+                self._scale = self._scale.to(self.CG_weight.device)
+            self._scale_key = key
+        return self._scale
+
+    def _compute_scales(self) -> Optional[torch.Tensor]:
         sel = self.selected_idx.detach().cpu().numpy()
         w = self.CG_weight.detach().float().cpu().numpy()
         if not np.array_equal(sel, self._canon_sel):
@@ -248,16 +339,40 @@ class SO2_TP_givenl2(nn.Module):
             scale[t0:t1] = r[0]
         return torch.from_numpy(scale)
 
-    def forward_linear(self, so2):
-        bs = so2.shape[0]
-        st = 0
-        outs = []
+    def folded_blocks(self):
+        """Per output l3: list of (input row start, rows, W_p^T) with path_norm and
+        loaded CG_weight path scales folded into W_p (cached on versions)."""
+        key = tuple((p.data_ptr(), p._version) for p in self.parameters())
+        if getattr(self, "_fold_key", None) == key:
+            return self._fold
+        sc = self._compute_scales()
+        pn = self.path_norm.detach().view(-1)
+        blocks, t0, o0 = [], 0, 0
         for idx, (l3, cnt) in enumerate(self.l3_sequential):
-            en = st + (2 * l3 + 1) * cnt
-            blk = so2[:, st:en].reshape(bs, cnt, 2 * l3 + 1, -1).permute(0, 2, 1, 3).reshape(bs, 2 * l3 + 1, -1)
-            outs.append(self.out_linear[idx](blk))
-            st = en
-        return torch.cat(outs, dim=1) * self.path_norm
+            W = self.out_linear[idx].weight.detach()
+            lst = []
+            for p in range(cnt):
+                Wp = W[:, p * self.in_c:(p + 1) * self.in_c] * pn[o0]
+                if sc is not None:
+                    Wp = Wp * float(sc[t0])
+                lst.append((t0, 2 * l3 + 1, Wp.t().contiguous()))
+                t0 += 2 * l3 + 1
+            blocks.append(lst)
+            o0 += 2 * l3 + 1
+        self._fold, self._fold_key = blocks, key
+        return blocks
+
+    def forward_linear(self, so2):
+        """so2 [20, N, C] (m-major, l3-sequential rows) -> [9, N, C_out]."""
+        N = so2.shape[1]
+        outs = []
+        for lst in self.folded_blocks():
+            acc = None
+            for (t0, nr, Wt) in lst:
+                xin = so2[t0:t0 + nr].reshape(nr * N, -1)
+                acc = torch.mm(xin, Wt) if acc is None else torch.addmm(acc, xin, Wt)
+            outs.append(acc.view(-1, N, acc.shape[-1]))
+        return torch.cat(outs, dim=0)
 
 
 class E2TensorProductSO2_FirstOrder(nn.Module):
@@ -317,21 +432,22 @@ class E2AttentionArbOrder_sparse(nn.Module):
         self._mlp = MLPCache()
 
     def forward(self, x: torch.Tensor, ctx: EdgeContext):
-        N = x.shape[0]
+        """x [9, N, C] (m-major) -> [9, N, C]."""
+        N = x.shape[1]
         H = self.num_attn_heads
         if self.training and self.alpha_dropout.p > 0:
             raise NotImplementedError("attention dropout in training mode is not supported by the HIP path")
-        q = self.query_linear(x).reshape(N, H, -1)
-        k = self.key_linear(x).reshape(N, H, -1)
+        wq, bq = self.query_linear.stacked()
+        wk, bk = self.key_linear.stacked()
+        hid = self.query_linear.weight.shape[1]
+        y = SO3LinearFn.apply(x, torch.cat([wq, wk], dim=1), torch.cat([bq, bk]), self.lmax)
+        q = self.query_linear.finish(y[..., :hid], y[..., hid:2 * hid]).reshape(N, H, -1)
+        k = self.key_linear.finish(y[..., 2 * hid:3 * hid], y[..., 3 * hid:]).reshape(N, H, -1)
         v = self.proj_value(x)
         packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding)
         so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
                                 packed, ctx.rc, math.sqrt(q.shape[-1]))
-        tp = self.first_order_tp.so2_tp
-        sc = tp.path_scales()
-        if sc is not None:
-            so2 = so2 * sc.to(so2.device).view(1, -1, 1)
-        return self.proj_first(tp.forward_linear(so2))
+        return self.proj_first(self.first_order_tp.so2_tp.forward_linear(so2))
 
 
 class TransBlock(nn.Module):
@@ -351,11 +467,11 @@ class TransBlock(nn.Module):
         self.ffn = FeedForwardNetwork_s3(C, C, C, lmax)
 
     def forward(self, x, ctx: EdgeContext, sys_node_embedding=None):
-        x = x[:, :(self.lmax + 1) ** 2]
+        """x [9, N, C] m-major."""
         res = x
         h = self.norm_1(x)
         if sys_node_embedding is not None:
-            h = torch.cat([h[:, :1] + sys_node_embedding.unsqueeze(1), h[:, 1:]], dim=1)
+            h = torch.cat([(h[0] + sys_node_embedding).unsqueeze(0), h[1:]], dim=0)
         x = self.ga(h, ctx) + res
         return x + self.ffn(self.norm_ffn(x))
 
@@ -416,6 +532,7 @@ class E2former(nn.Module):
         self.norm_final = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
 
     def forward_flat(self, ctx: EdgeContext, sys_node_embedding: Optional[torch.Tensor] = None):
+        """Returns the node irreps in the m-major layout [9, N, C]."""
         x = self.edge_deg_embed_dense(ctx)
         for blk in self.blocks:
             x = blk(x, ctx, sys_node_embedding)

@@ -145,7 +145,7 @@ class DegreeEmbedFn(torch.autograd.Function):
         _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(fea), _lib.i32(768), _stream(fea))
         dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                              fea.data_ptr(), float(avg), float(rc), ENV_A, ENV_B, ENV_C)
-        x0 = torch.empty(N, 9, 256, dtype=torch.float32, device=dev)
+        x0 = torch.empty(9, N, 256, dtype=torch.float32, device=dev)   # m-major
         _lib.call("e2v2_deg_fwd", _lib.C.byref(dargs), _p(x0), _stream(x0))
         ctx.save_for_backward(fea)
         ctx.nl, ctx.margs_src = nl, (node_type, rbf_offset, rbf_coeff, packed)
@@ -175,7 +175,8 @@ class DegreeEmbedFn(torch.autograd.Function):
 class AttentionFn(torch.autograd.Function):
     """Edge part of E2AttentionArbOrder_sparse.forward (e2former.py:238-433) up to
     the SO(2) product's forward_linear: returns the 20-row l3-sequential tensor
-    h_a - h_b of so2_tensor_product.py:385 for every query atom."""
+    h_a - h_b of so2_tensor_product.py:385 for every query atom, m-major
+    [20, N, 256]; q, k [N, 128, 8], v [9, N, 256]."""
 
     @staticmethod
     def forward(ctx, q, k, v, dvec, dist, nl: NeighborList, node_type, rbf_offset, rbf_coeff: float, packed,
@@ -191,7 +192,7 @@ class AttentionFn(torch.autograd.Function):
                              nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                              q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(q_div), float(rc),
                              ENV_A, ENV_B, ENV_C)
-        out = torch.empty(N, 20, 256, dtype=torch.float32, device=dev)
+        out = torch.empty(20, N, 256, dtype=torch.float32, device=dev)   # m-major
         mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
