@@ -39,7 +39,8 @@ def mlp_fwd_flops(E, n_mlp):
 
 
 def mlp_bwd_flops(E, n_mlp):
-    return 2.0 * E * n_mlp * (256 * 128 + 128 * 128 + 256 * 128 + 128 * 128 + 128 * 256)
+    # input-gradient backward of the three linear layers (the forward saves the LN inputs)
+    return 2.0 * E * n_mlp * (256 * 128 + 128 * 128 + 128 * 256)
 
 
 def attn_fwd_bytes(N, E):
@@ -47,6 +48,7 @@ def attn_fwd_bytes(N, E):
 
 
 KERNEL_OF = {"e2v2_mlp_fwd": "k_mlp_fwd", "e2v2_mlp_bwd": "k_mlp_bwd", "e2v2_attn_fwd": "k_attn_fwd",
+             "e2v2_attn_bwd": "k_attn_bwd_row",
              "e2v2_deg_fwd": "k_deg_fwd", "e2v2_deg_bwd": "k_deg_bwd", "e2v2_nbr_count": "k_nbr_count"}
 
 

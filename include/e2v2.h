@@ -37,6 +37,7 @@
  *                       (e2former.py:689-753)
  *   e2v2_rmsnorm_*      EquivariantRMSNormArraySphericalHarmonicsV2_BL (module_utils.py:1663-1772)
  *   e2v2_gate_*         Gate_s3 activation (module_utils.py:2694-2746)
+ *   e2v2_pairdot_*      per-l m-contraction of SO3_Linear2Scalar_e2former (module_utils.py:2241-2266)
  *   e2v2_edge_to_pos    autograd of f_edge_vec / f_dist w.r.t. positions (module_utils.py:3161-3206),
  *                       consumed by GradientHead (src/molfm/pipeline/head.py:305-328)
  */
@@ -125,12 +126,15 @@ typedef struct e2v2_mlp_args {
   const int32_t* node_type;      /* [N] atomic numbers                             */
   const float* rbf_offset;       /* [256] Gaussian centres                         */
   float rbf_coeff;               /* -0.5 / width^2                                 */
+  float* save_n;                 /* [n_mlp][E][256] normalised LN1 | LN2 inputs (written by fwd, read by bwd) */
+  float* save_r;                 /* [n_mlp][E][2]   their rstd                                                */
   e2v2_mlp_weights w[E2V2_MAX_MLP];
 } e2v2_mlp_args;
 
-/* out[e, 256 m + c] for profile m */
+/* out[e, 256 m + c] for profile m; fills save_n / save_r when they are non-null */
 int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hipStream_t s);
-/* dd[e] (+)= sum_m dL/dout_m . dout_m/dd  (input gradient w.r.t. the edge distance only) */
+/* dd[e] (+)= sum_m dL/dout_m . dout_m/dd  (input gradient w.r.t. the edge distance only);
+   requires save_n / save_r from the forward of the same edges and weights */
 int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_dout, float* dd, int accumulate,
                  hipStream_t s);
 
@@ -191,6 +195,11 @@ int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, float* gx,
 int e2v2_gate_fwd(const float* sc, const float* x, float* y, int n, float k1, float k2, hipStream_t s);
 int e2v2_gate_bwd(const float* sc, const float* x, const float* gy, float* gsc, float* gx, int n, float k1,
                   float k2, hipStream_t s);
+
+/* Q/K scalarisation of SO3_Linear2Scalar_e2former (module_utils.py:2241-2266):
+ * y [9][N][4 hid] = (q_a | q_b | k_a | k_b) -> hq, hk [N][3 hid], h[l hid + c] = sum_{m in l} a b */
+int e2v2_pairdot_fwd(const float* y, float* hq, float* hk, int n, int hid, hipStream_t s);
+int e2v2_pairdot_bwd(const float* y, const float* ghq, const float* ghk, float* gy, int n, int hid, hipStream_t s);
 
 /* ---- positions --------------------------------------------------------- */
 int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,

@@ -41,7 +41,8 @@ def test_mlp_forward_backward(pkg, cuda):
     rb = modules.GaussianSmearing(256, 6.0, 2.0)
     Z = torch.as_tensor(s["Z"], device=cuda).to(torch.int32)
     packed = [ops.PackedMLP(prof.to(cuda).net, tgt.weight.to(cuda), src.weight.to(cuda))]
-    args = ops.mlp_args(nl, Z, rb.offset.to(cuda), rb.coeff, packed)
+    sn, sr = ops.mlp_save_buffers(1, E, cuda)
+    args = ops.mlp_args(nl, Z, rb.offset.to(cuda), rb.coeff, packed, sn, sr)
     out = torch.empty(E, 256, device=cuda)
     from ubio_molfm_amd import _lib
     _lib.call("e2v2_mlp_fwd", _lib.C.byref(args), _lib.vp(out.data_ptr()), _lib.i32(256),

@@ -17,6 +17,7 @@ EXPORTS = [
     "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose",
     "e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
     "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd", "e2v2_gate_bwd",
+    "e2v2_pairdot_fwd", "e2v2_pairdot_bwd",
 ]
 
 
@@ -37,7 +38,8 @@ class MlpWeights(C.Structure):
 
 class MlpArgs(C.Structure):
     _fields_ = [("n_edges", i64), ("n_mlp", i32), ("dist", vp), ("edge_row", vp), ("col", vp),
-                ("node_type", vp), ("rbf_offset", vp), ("rbf_coeff", f32), ("w", MlpWeights * 3)]
+                ("node_type", vp), ("rbf_offset", vp), ("rbf_coeff", f32), ("save_n", vp), ("save_r", vp),
+                ("w", MlpWeights * 3)]
 
 
 class AttnArgs(C.Structure):

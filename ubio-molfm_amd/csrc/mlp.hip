@@ -5,7 +5,8 @@
 // The first Linear is split: W1 [rbf | tgt | src] x = W1r rbf + (W1t tgt[z_i] + b1)
 // + W1s src[z_j]; the two type terms arrive as per-type tables.  The RBF tile
 // lives in LDS only; the MLP runs as fp32 MFMA 16x16x4 GEMMs on 32-edge tiles.
-// The backward recomputes the forward and returns only dL/d(distance).
+// The forward saves the normalised LayerNorm inputs (n1, n2) and their rstd;
+// the backward uses them (no recompute) and returns only dL/d(distance).
 #include "common.h"
 #include "../../include/e2v2.h"
 
@@ -14,16 +15,19 @@ namespace e2v2 {
 constexpr int kT = 32;          // edges per tile
 constexpr int kK0 = 256;        // rbf basis
 constexpr int kH = 128;         // hidden width
-constexpr int kLdX = 258;       // LDS row stride for K=256 tiles (== 2 mod 32)
+constexpr int kLdX = 258;       // LDS row stride for K=256 tiles (== 2 mod 32: conflict-free A reads)
 constexpr int kLdY = 130;       // LDS row stride for K=128 tiles (== 2 mod 32)
+constexpr int kPF = 8;          // k-steps (of 4) per register-prefetched B chunk
 
 // C[32][N] = A[32][K] (LDS, row stride lda) x B[K][N] (global, row stride ldb).
 // Wave w owns columns [w*N/4, (w+1)*N/4).  acc[rt][ct] holds the 16x16 tile
 // (rows rt*16.., cols w*N/4 + ct*16..); lane l holds rows 4*(l/16)+r, col l%16.
+// B is streamed in chunks of 32 k-rows held in registers one chunk ahead.
 template <int K, int N>
 __device__ __forceinline__ void gemm32(const float* A, int lda, const float* __restrict__ B, int ldb,
                                        floatx4 (&acc)[2][N / 64]) {
   constexpr int CT = N / 64;
+  constexpr int NCH = K / (4 * kPF);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15, lk = lane >> 4;
@@ -33,24 +37,35 @@ __device__ __forceinline__ void gemm32(const float* A, int lda, const float* __r
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
   const float* Bp = B + (size_t)lk * ldb + cbase + li;
-  float bn[CT];
+  float bc[kPF][CT], bn[kPF][CT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) bn[ct] = Bp[ct * 16];
-#pragma unroll 4
-  for (int k0 = 0; k0 < K; k0 += 4) {
-    float b[CT];
+  for (int s = 0; s < kPF; ++s)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) b[ct] = bn[ct];
-    if (k0 + 4 < K) {
+    for (int ct = 0; ct < CT; ++ct) bc[s][ct] = Bp[(size_t)(4 * s) * ldb + ct * 16];
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) bn[ct] = Bp[(size_t)(k0 + 4) * ldb + ct * 16];
+  for (int ch = 0; ch < NCH; ++ch) {
+    if (ch + 1 < NCH) {
+#pragma unroll
+      for (int s = 0; s < kPF; ++s)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) bn[s][ct] = Bp[(size_t)((ch + 1) * 4 * kPF + 4 * s) * ldb + ct * 16];
     }
-    float a0 = A[li * lda + k0 + lk];
-    float a1 = A[(16 + li) * lda + k0 + lk];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      acc[0][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b[ct], acc[0][ct], 0, 0, 0);
-      acc[1][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b[ct], acc[1][ct], 0, 0, 0);
+    for (int s = 0; s < kPF; ++s) {
+      const int k0 = ch * 4 * kPF + 4 * s;
+      const float a0 = A[li * lda + k0 + lk];
+      const float a1 = A[(16 + li) * lda + k0 + lk];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        acc[0][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, bc[s][ct], acc[0][ct], 0, 0, 0);
+        acc[1][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, bc[s][ct], acc[1][ct], 0, 0, 0);
+      }
+    }
+    if (ch + 1 < NCH) {
+#pragma unroll
+      for (int s = 0; s < kPF; ++s)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) bc[s][ct] = bn[s][ct];
     }
   }
 }
@@ -63,10 +78,26 @@ __device__ __forceinline__ void acc_coord(int rt, int ct, int r, int& row, int& 
   c = wave * (N / 4) + ct * 16 + (lane & 15);
 }
 
-// Row-wise LayerNorm(128) + SiLU on Y (in place).  Saves nrm (normalised,
-// pre-affine) and rstd when requested.  8 threads per row.
-__device__ __forceinline__ void ln_silu_rows(float* Y, int ldy, const float* __restrict__ g, const float* __restrict__ b,
-                                             float* nrm, int ldn, float* rstd_out) {
+template <int N>
+__device__ __forceinline__ void store_acc(const floatx4 (&acc)[2][N / 64], float* Y, int ldy,
+                                          const float* __restrict__ bias) {
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < N / 64; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int row, c;
+        acc_coord<N>(rt, ct, r, row, c);
+        Y[row * ldy + c] = acc[rt][ct][r] + (bias ? bias[c] : 0.f);
+      }
+}
+
+// Row-wise LayerNorm(128) + SiLU on Y (in place), 8 threads per row.  Rows
+// below nsave also store the normalised (pre-affine) values and rstd.
+__device__ __forceinline__ void ln_silu_rows(float* Y, int ldy, const float* __restrict__ g,
+                                             const float* __restrict__ b, float* nrm, int ldn, float* rstd_out,
+                                             int rstd_stride, int nsave) {
   const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
   float* y = Y + row * ldy;
   float v[16];
@@ -90,28 +121,31 @@ __device__ __forceinline__ void ln_silu_rows(float* Y, int ldy, const float* __r
   s2 += __shfl_xor(s2, 2, 64);
   s2 += __shfl_xor(s2, 4, 64);
   const float rstd = 1.0f / sqrtf(s2 * (1.0f / kH) + 1e-5f);
+  const bool save = nrm != nullptr && row < nsave;
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int c = sub + 8 * q;
     float n = (v[q] - mean) * rstd;
-    if (nrm) nrm[row * ldn + c] = n;
+    if (save) nrm[(size_t)row * ldn + c] = n;
     float a = n * g[c] + b[c];
     y[c] = silu(a);
   }
-  if (rstd_out && sub == 0) rstd_out[row] = rstd;
+  if (save && sub == 0) rstd_out[(size_t)row * rstd_stride] = rstd;
 }
 
-// dz = LN-backward(SiLU-backward(dy)) given the saved normalised input and rstd.
-__device__ __forceinline__ void ln_silu_bwd_rows(float* Y, int ldy, const float* nrm, int ldn, const float* rstd,
+// dz = LN-backward(SiLU-backward(dy)) given the saved normalised input and rstd (global).
+__device__ __forceinline__ void ln_silu_bwd_rows(float* Y, int ldy, const float* __restrict__ nrm, int ldn,
+                                                 const float* __restrict__ rstd, int rstd_stride, int nvalid,
                                                  const float* __restrict__ g, const float* __restrict__ b) {
   const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
   float* y = Y + row * ldy;
+  const bool ok = row < nvalid;
   float dn[16], nn[16];
   float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int c = sub + 8 * q;
-    float n = nrm[row * ldn + c];
+    float n = ok ? nrm[(size_t)row * ldn + c] : 0.f;
     float a = n * g[c] + b[c];
     float sg = sigmoidf_(a);
     float da = y[c] * sg * (1.0f + a * (1.0f - sg));
@@ -122,7 +156,8 @@ __device__ __forceinline__ void ln_silu_bwd_rows(float* Y, int ldy, const float*
   }
   s1 += __shfl_xor(s1, 1, 64); s1 += __shfl_xor(s1, 2, 64); s1 += __shfl_xor(s1, 4, 64);
   s2 += __shfl_xor(s2, 1, 64); s2 += __shfl_xor(s2, 2, 64); s2 += __shfl_xor(s2, 4, 64);
-  const float m1 = s1 * (1.0f / kH), m2 = s2 * (1.0f / kH), r = rstd[row];
+  const float m1 = s1 * (1.0f / kH), m2 = s2 * (1.0f / kH);
+  const float r = ok ? rstd[(size_t)row * rstd_stride] : 0.f;
 #pragma unroll
   for (int q = 0; q < 16; ++q) y[sub + 8 * q] = r * (dn[q] - m1 - nn[q] * m2);
 }
@@ -133,10 +168,10 @@ struct TileEdges {
   int valid[kT];
 };
 
-__device__ __forceinline__ void load_tile_edges(const e2v2_mlp_args& A, int e0, TileEdges& te) {
+__device__ __forceinline__ void load_tile_edges(const e2v2_mlp_args& A, int64_t e0, TileEdges& te) {
   const int t = threadIdx.x;
   if (t < kT) {
-    const int64_t e = (int64_t)e0 + t;
+    const int64_t e = e0 + t;
     const bool v = e < A.n_edges;
     te.valid[t] = v;
     te.d[t] = v ? A.dist[e] : 0.f;
@@ -156,10 +191,19 @@ __device__ __forceinline__ void rbf_tile(const e2v2_mlp_args& A, const TileEdges
   }
 }
 
-// forward through LN2+SiLU.  On return: Y (ld kLdY) holds y1 (unused after),
-// H2 (ld kLdY) holds y2 = silu(LN2(h2)); optionally n1/n2 and rstds saved.
-__device__ __forceinline__ void mlp_trunk(const e2v2_mlp_args& A, const e2v2_mlp_weights& W, const TileEdges& te,
-                                          float* X, float* Y, float* H2, float* N1, float* N2, float* r1, float* r2) {
+__global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
+  extern __shared__ float sm[];
+  float* X = sm;                    // [32][258]: rbf tile, then h2 / y2 with stride kLdY
+  float* Y = X + kT * kLdX;         // [32][130]
+  __shared__ TileEdges te;
+  const int m = blockIdx.y;
+  const e2v2_mlp_weights& W = A.w[m];
+  const int64_t e0 = (int64_t)blockIdx.x * kT;
+  const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
+  float* sn = A.save_n ? A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH) : nullptr;
+  float* sr = A.save_r ? A.save_r + ((size_t)m * A.n_edges + e0) * 2 : nullptr;
+  load_tile_edges(A, e0, te);
+  __syncthreads();
   rbf_tile(A, te, X);
   __syncthreads();
   {
@@ -177,41 +221,18 @@ __device__ __forceinline__ void mlp_trunk(const e2v2_mlp_args& A, const e2v2_mlp
         }
   }
   __syncthreads();
-  ln_silu_rows(Y, kLdY, W.g1, W.be1, N1, kLdY, r1);
+  ln_silu_rows(Y, kLdY, W.g1, W.be1, sn, 2 * kH, sr, 2, nvalid);
   __syncthreads();
   {
     floatx4 acc[2][2];
     gemm32<kH, kH>(Y, kLdY, W.w2t, kH, acc);
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          int row, c;
-          acc_coord<kH>(rt, ct, r, row, c);
-          H2[row * kLdY + c] = acc[rt][ct][r] + W.b2[c];
-        }
+    store_acc<kH>(acc, X, kLdY, W.b2);
   }
   __syncthreads();
-  ln_silu_rows(H2, kLdY, W.g2, W.be2, N2, kLdY, r2);
+  ln_silu_rows(X, kLdY, W.g2, W.be2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2, nvalid);
   __syncthreads();
-}
-
-__global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
-  extern __shared__ float sm[];
-  float* X = sm;                    // [32][258]
-  float* Y = X + kT * kLdX;         // [32][130]
-  float* H2 = Y + kT * kLdY;        // [32][130]
-  __shared__ TileEdges te;
-  const int m = blockIdx.y;
-  const e2v2_mlp_weights& W = A.w[m];
-  const int e0 = blockIdx.x * kT;
-  load_tile_edges(A, e0, te);
-  __syncthreads();
-  mlp_trunk(A, W, te, X, Y, H2, nullptr, nullptr, nullptr, nullptr);
   floatx4 acc[2][4];
-  gemm32<kH, 256>(H2, kLdY, W.w3t, 256, acc);
+  gemm32<kH, 256>(X, kLdY, W.w3t, 256, acc);
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
@@ -220,41 +241,7 @@ __global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restr
       for (int r = 0; r < 4; ++r) {
         int row, c;
         acc_coord<256>(rt, ct, r, row, c);
-        if (te.valid[row]) out[(int64_t)(e0 + row) * ld_out + m * 256 + c] = acc[rt][ct][r] + W.b3[c];
-      }
-}
-
-// Normalise rows of Y in place (pre-affine LayerNorm(128)) and keep rstd.
-__device__ __forceinline__ void ln_normalize_rows(float* Y, int ldy, float* rstd_out) {
-  const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
-  float* y = Y + row * ldy;
-  float v[16], s = 0.f;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) { v[q] = y[sub + 8 * q]; s += v[q]; }
-  s += __shfl_xor(s, 1, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 4, 64);
-  const float mean = s * (1.0f / kH);
-  float s2 = 0.f;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) { float dl = v[q] - mean; s2 += dl * dl; }
-  s2 += __shfl_xor(s2, 1, 64); s2 += __shfl_xor(s2, 2, 64); s2 += __shfl_xor(s2, 4, 64);
-  const float rstd = 1.0f / sqrtf(s2 * (1.0f / kH) + 1e-5f);
-#pragma unroll
-  for (int q = 0; q < 16; ++q) y[sub + 8 * q] = (v[q] - mean) * rstd;
-  if (sub == 0) rstd_out[row] = rstd;
-}
-
-template <int N>
-__device__ __forceinline__ void store_acc(const floatx4 (&acc)[2][N / 64], float* Y, int ldy,
-                                          const float* __restrict__ bias) {
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < N / 64; ++ct)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int row, c;
-        acc_coord<N>(rt, ct, r, row, c);
-        Y[row * ldy + c] = acc[rt][ct][r] + (bias ? bias[c] : 0.f);
+        if (row < nvalid) out[(e0 + row) * ld_out + m * 256 + c] = acc[rt][ct][r] + W.b3[c];
       }
 }
 
@@ -263,12 +250,10 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
   extern __shared__ float sm[];
   float* X = sm;                    // [32][258]
   float* Y = X + kT * kLdX;         // [32][130]
-  float* N1 = Y + kT * kLdY;        // [32][130]
-  float* N2 = N1 + kT * kLdY;       // [32][130]
   __shared__ TileEdges te;
-  __shared__ float r1[kT], r2[kT];
   __shared__ float part[4][kT];
-  const int e0 = blockIdx.x * kT;
+  const int64_t e0 = (int64_t)blockIdx.x * kT;
+  const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   load_tile_edges(A, e0, te);
   __syncthreads();
@@ -279,37 +264,14 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
     for (int r = 0; r < 4; ++r) dd_lane[rt][r] = 0.f;
   for (int m = 0; m < A.n_mlp; ++m) {
     const e2v2_mlp_weights& W = A.w[m];
-    // ---- recompute the forward trunk: n1, r1, y1, n2, r2
-    rbf_tile(A, te, X);
-    __syncthreads();
-    {
-      floatx4 acc[2][2];
-      gemm32<kK0, kH>(X, kLdX, W.w1t, kH, acc);
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            int row, c;
-            acc_coord<kH>(rt, ct, r, row, c);
-            Y[row * kLdY + c] = acc[rt][ct][r] + W.ttgt[te.zi[row] * kH + c] + W.tsrc[te.zj[row] * kH + c];
-          }
-    }
-    __syncthreads();
-    ln_silu_rows(Y, kLdY, W.g1, W.be1, N1, kLdY, r1);
-    __syncthreads();
-    {
-      floatx4 acc[2][2];
-      gemm32<kH, kH>(Y, kLdY, W.w2t, kH, acc);
-      store_acc<kH>(acc, N2, kLdY, W.b2);
-    }
-    __syncthreads();
-    ln_normalize_rows(N2, kLdY, r2);
-    // ---- backward
-    for (int idx = threadIdx.x; idx < kT * 256; idx += 256) {
-      const int row = idx >> 8, c = idx & 255;
-      X[row * kLdX + c] = te.valid[row] ? dout[(int64_t)(e0 + row) * ld_dout + m * 256 + c] : 0.f;
+    const float* sn = A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH);
+    const float* sr = A.save_r + ((size_t)m * A.n_edges + e0) * 2;
+    for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {   // dOut tile, float4 loads
+      const int row = idx >> 6, c4 = idx & 63;
+      float4 v = row < nvalid ? reinterpret_cast<const float4*>(dout + (e0 + row) * ld_dout + m * 256)[c4]
+                              : float4{0.f, 0.f, 0.f, 0.f};
+      float* xr = X + row * kLdX + 4 * c4;
+      xr[0] = v.x; xr[1] = v.y; xr[2] = v.z; xr[3] = v.w;
     }
     __syncthreads();
     {  // dy2 = dOut . W3   (W3 [256][128] row-major = B[K=256][N=128])
@@ -318,15 +280,15 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
       store_acc<kH>(acc, Y, kLdY, nullptr);
     }
     __syncthreads();
-    ln_silu_bwd_rows(Y, kLdY, N2, kLdY, r2, W.g2, W.be2);
+    ln_silu_bwd_rows(Y, kLdY, sn + kH, 2 * kH, sr + 1, 2, nvalid, W.g2, W.be2);
     __syncthreads();
-    {  // dy1 = dz2 . W2   (W2 [128][128])
+    {  // dy1 = dz2 . W2   (W2 [128][128]) -> X with stride kLdY
       floatx4 acc[2][2];
       gemm32<kH, kH>(Y, kLdY, W.w2, kH, acc);
       store_acc<kH>(acc, X, kLdY, nullptr);
     }
     __syncthreads();
-    ln_silu_bwd_rows(X, kLdY, N1, kLdY, r1, W.g1, W.be1);
+    ln_silu_bwd_rows(X, kLdY, sn, 2 * kH, sr, 2, nvalid, W.g1, W.be1);
     __syncthreads();
     {  // drbf = dz1 . W1r  (W1 [128][ldw1], rbf columns 0..255); dd += sum_k drbf * rbf * 2c(d - mu)
       floatx4 acc[2][4];
@@ -358,9 +320,9 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
       if ((lane & 15) == 0) part[wave][rt * 16 + 4 * (lane >> 4) + r] = v;
     }
   __syncthreads();
-  if (threadIdx.x < kT && te.valid[threadIdx.x]) {
+  if (threadIdx.x < nvalid) {
     float v = part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] + part[3][threadIdx.x];
-    int64_t e = (int64_t)e0 + threadIdx.x;
+    int64_t e = e0 + threadIdx.x;
     dd[e] = accumulate ? dd[e] + v : v;
   }
 }
@@ -369,8 +331,7 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
 
 using namespace e2v2;
 
-static size_t mlp_fwd_lds() { return sizeof(float) * (kT * kLdX + 2 * kT * kLdY); }
-static size_t mlp_bwd_lds() { return sizeof(float) * (kT * kLdX + 3 * kT * kLdY); }
+static size_t mlp_lds() { return sizeof(float) * (kT * kLdX + kT * kLdY); }
 
 E2V2_API int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hipStream_t s) {
   const e2v2_mlp_args& A = *args;
@@ -380,11 +341,11 @@ E2V2_API int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hip
   static bool attr = false;
   if (!attr) {
     E2V2_TRY_HIP(hipFuncSetAttribute((const void*)k_mlp_fwd, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)mlp_fwd_lds()));
+                                     (int)mlp_lds()));
     attr = true;
   }
   dim3 grid((unsigned)((A.n_edges + kT - 1) / kT), (unsigned)A.n_mlp);
-  hipLaunchKernelGGL(k_mlp_fwd, grid, dim3(256), mlp_fwd_lds(), s, A, out, ld_out);
+  hipLaunchKernelGGL(k_mlp_fwd, grid, dim3(256), mlp_lds(), s, A, out, ld_out);
   E2V2_LAUNCHED("k_mlp_fwd");
   return 0;
 }
@@ -393,16 +354,18 @@ E2V2_API int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_d
                           hipStream_t s) {
   const e2v2_mlp_args& A = *args;
   E2V2_REQUIRE(A.n_mlp >= 1 && A.n_mlp <= E2V2_MAX_MLP, "mlp_bwd: n_mlp %d out of range", A.n_mlp);
-  E2V2_REQUIRE(ld_dout >= 256 * A.n_mlp, "mlp_bwd: ld_dout %d < 256*n_mlp", ld_dout);
+  E2V2_REQUIRE(ld_dout >= 256 * A.n_mlp && ld_dout % 4 == 0, "mlp_bwd: bad ld_dout %d", ld_dout);
+  E2V2_REQUIRE(A.save_n != nullptr && A.save_r != nullptr,
+               "mlp_bwd: needs the normalised activations saved by e2v2_mlp_fwd (save_n, save_r)");
   if (A.n_edges == 0) return 0;
   static bool attr = false;
   if (!attr) {
     E2V2_TRY_HIP(hipFuncSetAttribute((const void*)k_mlp_bwd, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)mlp_bwd_lds()));
+                                     (int)mlp_lds()));
     attr = true;
   }
   dim3 grid((unsigned)((A.n_edges + kT - 1) / kT));
-  hipLaunchKernelGGL(k_mlp_bwd, grid, dim3(256), mlp_bwd_lds(), s, A, dout, ld_dout, dd, accumulate);
+  hipLaunchKernelGGL(k_mlp_bwd, grid, dim3(256), mlp_lds(), s, A, dout, ld_dout, dd, accumulate);
   E2V2_LAUNCHED("k_mlp_bwd");
   return 0;
 }

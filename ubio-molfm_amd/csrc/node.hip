@@ -171,3 +171,75 @@ E2V2_API int e2v2_gate_bwd(const float* sc, const float* x, const float* gy, flo
   E2V2_LAUNCHED("k_gate_bwd");
   return 0;
 }
+
+// ---- Q/K scalarisation of SO3_Linear2Scalar_e2former (module_utils.py:2241-2266):
+// y [9][N][4*hid] holds (q_a, q_b, k_a, k_b) of the fused projection; for X in {q, k}:
+//   h_X[n][l*hid + c] = sum_{m in l} X_a[m][n][c] * X_b[m][n][c]        -> hq, hk [N][3*hid]
+namespace e2v2 {
+__global__ void k_pairdot_fwd(const float* __restrict__ y, float* __restrict__ hq, float* __restrict__ hk, int n,
+                              int hid) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)n * hid) return;
+  const int i = (int)(idx / hid), c = (int)(idx % hid);
+  const size_t st = (size_t)n * 4 * hid;
+  const float* p = y + (size_t)i * 4 * hid + c;
+  float q[3] = {0.f, 0.f, 0.f}, k[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 9; ++m) {
+    const int l = m == 0 ? 0 : (m < 4 ? 1 : 2);
+    const float* r = p + m * st;
+    q[l] = fmaf(r[0], r[hid], q[l]);
+    k[l] = fmaf(r[2 * hid], r[3 * hid], k[l]);
+  }
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    hq[(size_t)i * 3 * hid + l * hid + c] = q[l];
+    hk[(size_t)i * 3 * hid + l * hid + c] = k[l];
+  }
+}
+
+__global__ void k_pairdot_bwd(const float* __restrict__ y, const float* __restrict__ ghq,
+                              const float* __restrict__ ghk, float* __restrict__ gy, int n, int hid) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)n * hid) return;
+  const int i = (int)(idx / hid), c = (int)(idx % hid);
+  const size_t st = (size_t)n * 4 * hid;
+  const float* p = y + (size_t)i * 4 * hid + c;
+  float* g = gy + (size_t)i * 4 * hid + c;
+  float gq[3], gk[3];
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    gq[l] = ghq[(size_t)i * 3 * hid + l * hid + c];
+    gk[l] = ghk[(size_t)i * 3 * hid + l * hid + c];
+  }
+#pragma unroll
+  for (int m = 0; m < 9; ++m) {
+    const int l = m == 0 ? 0 : (m < 4 ? 1 : 2);
+    const float* r = p + m * st;
+    float* o = g + m * st;
+    const float qa = r[0], qb = r[hid], ka = r[2 * hid], kb = r[3 * hid];
+    o[0] = gq[l] * qb;
+    o[hid] = gq[l] * qa;
+    o[2 * hid] = gk[l] * kb;
+    o[3 * hid] = gk[l] * ka;
+  }
+}
+}  // namespace e2v2
+
+E2V2_API int e2v2_pairdot_fwd(const float* y, float* hq, float* hk, int n, int hid, hipStream_t s) {
+  if (n == 0) return 0;
+  const int64_t tot = (int64_t)n * hid;
+  hipLaunchKernelGGL(e2v2::k_pairdot_fwd, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, y, hq, hk, n, hid);
+  E2V2_LAUNCHED("k_pairdot_fwd");
+  return 0;
+}
+
+E2V2_API int e2v2_pairdot_bwd(const float* y, const float* ghq, const float* ghk, float* gy, int n, int hid,
+                              hipStream_t s) {
+  if (n == 0) return 0;
+  const int64_t tot = (int64_t)n * hid;
+  hipLaunchKernelGGL(e2v2::k_pairdot_bwd, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, y, ghq, ghk, gy, n,
+                     hid);
+  E2V2_LAUNCHED("k_pairdot_bwd");
+  return 0;
+}

@@ -45,23 +45,30 @@ def _dp(t):
 
 
 class SO3LinearFn(torch.autograd.Function):
-    """y[rows(l)] = x[rows(l)] W_l^T (+ bias on row 0) on the m-major layout
-    x[(lmax+1)^2, N, Cin]: each l block is one 2-D GEMM written in place.
-    W and bias are constants (input gradient only)."""
+    """y[rows(l)] = res[rows(l)] + x[rows(l)] W_l^T (+ bias on row 0) on the
+    m-major layout x[(lmax+1)^2, N, Cin]: each l block is one 2-D GEMM written in
+    place (addmm when a residual is fused).  W and bias are constants (input
+    gradients only)."""
 
     @staticmethod
-    def forward(ctx, x, W, bias, lmax: int):
+    def forward(ctx, x, W, bias, lmax: int, res=None):
         x = x.contiguous()
         L2, N, Cin = x.shape
         O = W.shape[1]
         y = x.new_empty(L2, N, O)
+        if res is not None:
+            res = res.contiguous()
         for l in range(lmax + 1):
             a, b = l * l, (l + 1) ** 2
-            torch.mm(x[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
+            if res is None:
+                torch.mm(x[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
+            else:
+                torch.addmm(res[a:b].view(-1, O), x[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
         if bias is not None:
             y[0].add_(bias)
         ctx.save_for_backward(W)
         ctx.lmax = lmax
+        ctx.has_res = res is not None
         return y
 
     @staticmethod
@@ -74,7 +81,97 @@ class SO3LinearFn(torch.autograd.Function):
         for l in range(ctx.lmax + 1):
             a, b = l * l, (l + 1) ** 2
             torch.mm(gy[a:b].view(-1, O), W[l], out=gx[a:b].view(-1, Cin))
-        return gx, None, None, None
+        return gx, None, None, None, (gy if ctx.has_res else None)
+
+
+class QKProjFn(torch.autograd.Function):
+    """Fused per-l GEMM of the query and key SO3_Linear2Scalar products and their
+    m-contraction: x[9][N][C] -> hq, hk [N][3 hid] (before final_linear)."""
+
+    @staticmethod
+    def forward(ctx, x, W, bias, lmax: int, hid: int):
+        x = x.contiguous()
+        L2, N, C = x.shape
+        y = x.new_empty(L2, N, 4 * hid)
+        for l in range(lmax + 1):
+            a, b = l * l, (l + 1) ** 2
+            torch.mm(x[a:b].view(-1, C), W[l].t(), out=y[a:b].view(-1, 4 * hid))
+        y[0].add_(bias)
+        hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
+        _lib.call("e2v2_pairdot_fwd", _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _stream())
+        ctx.save_for_backward(y, W)
+        ctx.lmax, ctx.hid = lmax, hid
+        return hq, hk
+
+    @staticmethod
+    def backward(ctx, ghq, ghk):
+        y, W = ctx.saved_tensors
+        L2, N, F = y.shape
+        hid = ctx.hid
+        ghq = torch.zeros(N, 3 * hid, device=y.device) if ghq is None else ghq.contiguous()
+        ghk = torch.zeros(N, 3 * hid, device=y.device) if ghk is None else ghk.contiguous()
+        gy = torch.empty_like(y)
+        _lib.call("e2v2_pairdot_bwd", _dp(y), _dp(ghq), _dp(ghk), _dp(gy), _lib.i32(N), _lib.i32(hid), _stream())
+        C = W.shape[2]
+        gx = y.new_empty(L2, N, C)
+        for l in range(ctx.lmax + 1):
+            a, b = l * l, (l + 1) ** 2
+            torch.mm(gy[a:b].view(-1, F), W[l], out=gx[a:b].view(-1, C))
+        return gx, None, None, None, None
+
+
+class SO2OutFn(torch.autograd.Function):
+    """y = res + proj_first(forward_linear(so2)): the SO(2) product's per-l3
+    output linears (path_norm and path scales folded into the blocks) followed by
+    the proj_first SO3 linear, GEMMs only (so2_tensor_product.py:276-290,
+    e2former.py:215-219,433)."""
+
+    @staticmethod
+    def forward(ctx, so2, res, blocks, Wp, bp):
+        so2 = so2.contiguous(); res = res.contiguous()
+        _, N, C = so2.shape
+        t = so2.new_empty(9, N, C)
+        o = 0
+        for lst in blocks:
+            nr = lst[0][1]
+            tv = t[o:o + nr].view(-1, C)
+            for idx, (t0, nr_, Wt) in enumerate(lst):
+                xin = so2[t0:t0 + nr_].view(-1, C)
+                if idx == 0:
+                    torch.mm(xin, Wt, out=tv)
+                else:
+                    tv.addmm_(xin, Wt)
+            o += nr
+        y = so2.new_empty(9, N, Wp.shape[1])
+        for l in range(3):
+            a, b = l * l, (l + 1) ** 2
+            torch.addmm(res[a:b].view(-1, Wp.shape[1]), t[a:b].view(-1, C), Wp[l].t(),
+                        out=y[a:b].view(-1, Wp.shape[1]))
+        y[0].add_(bp)
+        ctx.blocks = blocks
+        ctx.save_for_backward(Wp)
+        ctx.shape = so2.shape
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        (Wp,) = ctx.saved_tensors
+        gy = gy.contiguous()
+        _, N, O = gy.shape
+        C = Wp.shape[2]
+        gt = gy.new_empty(9, N, C)
+        for l in range(3):
+            a, b = l * l, (l + 1) ** 2
+            torch.mm(gy[a:b].view(-1, O), Wp[l], out=gt[a:b].view(-1, C))
+        gso2 = gy.new_empty(ctx.shape)
+        o = 0
+        for lst in ctx.blocks:
+            nr = lst[0][1]
+            gv = gt[o:o + nr].view(-1, C)
+            for (t0, nr_, Wt) in lst:
+                torch.mm(gv, Wt.t(), out=gso2[t0:t0 + nr_].view(-1, C))
+            o += nr
+        return gso2, gy, None, None, None
 
 
 class RMSNormFn(torch.autograd.Function):
@@ -101,26 +198,28 @@ class RMSNormFn(torch.autograd.Function):
 
 
 class GateFn(torch.autograd.Function):
-    """Gate_s3 activation from logits sc [N, 3C] and features x[9][N][C]."""
+    """Gate_s3: sc = x[0] Wg^T + bg, then the activation kernel on x[9][N][C]."""
 
     @staticmethod
-    def forward(ctx, sc, x, k1: float, k2: float):
-        sc = sc.contiguous(); x = x.contiguous()
+    def forward(ctx, x, Wg, bg, k1: float, k2: float):
+        x = x.contiguous()
+        sc = torch.addmm(bg, x[0], Wg.t())
         y = torch.empty_like(x)
         _lib.call("e2v2_gate_fwd", _dp(sc), _dp(x), _dp(y), _lib.i32(x.shape[1]), _lib.f32(k1), _lib.f32(k2),
                   _stream())
-        ctx.save_for_backward(sc, x)
+        ctx.save_for_backward(sc, x, Wg)
         ctx.k = (k1, k2)
         return y
 
     @staticmethod
     def backward(ctx, gy):
-        sc, x = ctx.saved_tensors
+        sc, x, Wg = ctx.saved_tensors
         gy = gy.contiguous()
         gsc = torch.empty_like(sc); gx = torch.empty_like(x)
         _lib.call("e2v2_gate_bwd", _dp(sc), _dp(x), _dp(gy), _dp(gsc), _dp(gx), _lib.i32(x.shape[1]),
                   _lib.f32(ctx.k[0]), _lib.f32(ctx.k[1]), _stream())
-        return gsc, gx, None, None
+        torch.mm(gsc, Wg, out=gx[0])            # the kernel leaves gx[0] = 0
+        return gx, None, None, None, None
 
 
 def _linear(x, lin: nn.Linear):
@@ -206,20 +305,18 @@ class SO3_Linear2Scalar_e2former(nn.Module):
         b = torch.cat([self.bias.detach().view(-1), torch.zeros_like(self.bias.detach().view(-1))])
         return w, b
 
-    def finish(self, a, b):
-        """a, b [9, N, hid] -> final_linear(cat_l sum_{m in l} a b) [N, out]."""
-        prod = a * b
-        parts = [prod[0]] + [prod[l * l:(l + 1) ** 2].sum(0) for l in range(1, self.lmax + 1)]
-        h = torch.cat(parts, dim=-1)
+    def head(self, h):
+        """final_linear on the m-contracted products h [N, (lmax+1) hid]."""
         fl = self.final_linear
         h = torch.nn.functional.silu(_layer_norm(_linear(h, fl[0]), fl[1]))
         return _linear(h, fl[3])
 
     def forward(self, x):
         w, b = self.stacked()
-        y = SO3LinearFn.apply(x, w, b, self.lmax)
         hid = self.weight.shape[1]
-        return self.finish(y[..., :hid], y[..., hid:])
+        # the pair kernel contracts (q_a, q_b) and (k_a, k_b); feed this product twice
+        hq, _ = QKProjFn.apply(x, torch.cat([w, w], dim=1), torch.cat([b, b]), self.lmax, hid)
+        return self.head(hq)
 
 
 class EquivariantRMSNormArraySphericalHarmonicsV2_BL(nn.Module):
@@ -258,8 +355,7 @@ class Gate_s3(nn.Module):
         nn.init.uniform_(self.gates.weight, -bound, bound)
 
     def forward(self, x):
-        sc = _linear(x[0], self.gates)
-        return GateFn.apply(sc, x, SILU_NORM, SIGMOID_NORM)
+        return GateFn.apply(x, self.gates.weight.detach(), self.gates.bias.detach(), SILU_NORM, SIGMOID_NORM)
 
 
 class FeedForwardNetwork_s3(nn.Module):
@@ -271,8 +367,10 @@ class FeedForwardNetwork_s3(nn.Module):
         self.gate = Gate_s3(hidden_channels, lmax=lmax)
         self.slinear_2 = SO3_Linear_e2former(hidden_channels, output_channels, lmax=lmax, bias=True)
 
-    def forward(self, x, **kw):
-        return self.slinear_2(self.gate(self.slinear_1(x)))
+    def forward(self, x, res=None, **kw):
+        h = self.gate(self.slinear_1(x))
+        s2 = self.slinear_2
+        return SO3LinearFn.apply(h, s2.weight.detach(), s2.bias.detach(), s2.lmax, res)
 
 
 class sph_fromxyz(nn.Module):
@@ -431,23 +529,37 @@ class E2AttentionArbOrder_sparse(nn.Module):
         self.proj_first = SO3_Linear_e2former(num_attn_heads * 2, C, lmax=lmax)
         self._mlp = MLPCache()
 
-    def forward(self, x: torch.Tensor, ctx: EdgeContext):
-        """x [9, N, C] (m-major) -> [9, N, C]."""
+    def qk_weights(self):
+        key = tuple((p.data_ptr(), p._version) for p in
+                    (self.query_linear.weight, self.query_linear.weight2, self.query_linear.bias,
+                     self.key_linear.weight, self.key_linear.weight2, self.key_linear.bias))
+        if getattr(self, "_qk_key", None) != key:
+            wq, bq = self.query_linear.stacked()
+            wk, bk = self.key_linear.stacked()
+            self._qk = (torch.cat([wq, wk], dim=1).contiguous(), torch.cat([bq, bk]).contiguous())
+            self._qk_key = key
+        return self._qk
+
+    def forward(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
+        """x [9, N, C] (m-major) -> res + attention(x), [9, N, C]."""
         N = x.shape[1]
         H = self.num_attn_heads
         if self.training and self.alpha_dropout.p > 0:
             raise NotImplementedError("attention dropout in training mode is not supported by the HIP path")
-        wq, bq = self.query_linear.stacked()
-        wk, bk = self.key_linear.stacked()
+        W, b = self.qk_weights()
         hid = self.query_linear.weight.shape[1]
-        y = SO3LinearFn.apply(x, torch.cat([wq, wk], dim=1), torch.cat([bq, bk]), self.lmax)
-        q = self.query_linear.finish(y[..., :hid], y[..., hid:2 * hid]).reshape(N, H, -1)
-        k = self.key_linear.finish(y[..., 2 * hid:3 * hid], y[..., 3 * hid:]).reshape(N, H, -1)
+        hq, hk = QKProjFn.apply(x, W, b, self.lmax, hid)
+        q = self.query_linear.head(hq).reshape(N, H, -1)
+        k = self.key_linear.head(hk).reshape(N, H, -1)
         v = self.proj_value(x)
         packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding)
         so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
                                 packed, ctx.rc, math.sqrt(q.shape[-1]))
-        return self.proj_first(self.first_order_tp.so2_tp.forward_linear(so2))
+        if res is None:
+            res = torch.zeros_like(x)
+        pf = self.proj_first
+        return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(), pf.weight.detach(),
+                              pf.bias.detach())
 
 
 class TransBlock(nn.Module):
@@ -472,8 +584,8 @@ class TransBlock(nn.Module):
         h = self.norm_1(x)
         if sys_node_embedding is not None:
             h = torch.cat([(h[0] + sys_node_embedding).unsqueeze(0), h[1:]], dim=0)
-        x = self.ga(h, ctx) + res
-        return x + self.ffn(self.norm_ffn(x))
+        x = self.ga(h, ctx, res=res)
+        return self.ffn(self.norm_ffn(x), res=x)
 
 
 class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):

@@ -97,12 +97,21 @@ class MLPCache:
 
 
 def mlp_args(nl: NeighborList, node_type: torch.Tensor, rbf_offset: torch.Tensor, rbf_coeff: float,
-             packed: List[PackedMLP]) -> _lib.MlpArgs:
+             packed: List[PackedMLP], save_n: Optional[torch.Tensor] = None,
+             save_r: Optional[torch.Tensor] = None) -> _lib.MlpArgs:
     ws = (_lib.MlpWeights * 3)()
     for m, pk in enumerate(packed):
         ws[m] = pk.struct()
     return _lib.MlpArgs(nl.n_edges, len(packed), nl.dist.data_ptr(), nl.edge_row.data_ptr(), nl.col.data_ptr(),
-                        node_type.data_ptr(), rbf_offset.data_ptr(), float(rbf_coeff), ws)
+                        node_type.data_ptr(), rbf_offset.data_ptr(), float(rbf_coeff),
+                        None if save_n is None else save_n.data_ptr(), None if save_r is None else save_r.data_ptr(),
+                        ws)
+
+
+def mlp_save_buffers(n_mlp: int, E: int, dev):
+    """Normalised LayerNorm inputs kept from the forward for the backward."""
+    return (torch.empty(n_mlp, max(E, 1), 256, dtype=torch.float32, device=dev),
+            torch.empty(n_mlp, max(E, 1), 2, dtype=torch.float32, device=dev))
 
 
 class EdgeGeometryFn(torch.autograd.Function):
@@ -141,13 +150,14 @@ class DegreeEmbedFn(torch.autograd.Function):
         dev = dvec.device
         E, N = nl.n_edges, nl.n_atoms
         fea = torch.empty(max(E, 1), 3 * 256, dtype=torch.float32, device=dev)
-        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed)
+        sn, sr = mlp_save_buffers(len(packed), E, dev)
+        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
         _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(fea), _lib.i32(768), _stream(fea))
         dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                              fea.data_ptr(), float(avg), float(rc), ENV_A, ENV_B, ENV_C)
         x0 = torch.empty(9, N, 256, dtype=torch.float32, device=dev)   # m-major
         _lib.call("e2v2_deg_fwd", _lib.C.byref(dargs), _p(x0), _stream(x0))
-        ctx.save_for_backward(fea)
+        ctx.save_for_backward(fea, sn, sr)
         ctx.nl, ctx.margs_src = nl, (node_type, rbf_offset, rbf_coeff, packed)
         ctx.avg, ctx.rc = avg, rc
         return x0
@@ -155,7 +165,7 @@ class DegreeEmbedFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gx0):
         _no_double_backward()
-        (fea,) = ctx.saved_tensors
+        fea, sn, sr = ctx.saved_tensors
         nl = ctx.nl
         node_type, rbf_offset, rbf_coeff, packed = ctx.margs_src
         dev = fea.device
@@ -167,7 +177,7 @@ class DegreeEmbedFn(torch.autograd.Function):
         ddv = torch.empty(max(E, 1), 3, dtype=torch.float32, device=dev)
         dd = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
         _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(dfea), _p(ddv), _p(dd), _stream(gx0))
-        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed)
+        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
         _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dfea), _lib.i32(768), _p(dd), _lib.i32(1), _stream(gx0))
         return ddv[:E], dd[:E], None, None, None, None, None, None, None
 
@@ -186,7 +196,8 @@ class AttentionFn(torch.autograd.Function):
         E, N = nl.n_edges, nl.n_atoms
         q = q.float().contiguous(); k = k.float().contiguous(); v = v.float().contiguous()
         gi = torch.empty(max(E, 1), 256, dtype=torch.float32, device=dev)
-        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed)
+        sn, sr = mlp_save_buffers(1, E, dev)
+        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
         _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(gi), _lib.i32(256), _stream(q))
         args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
                              nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
@@ -197,14 +208,14 @@ class AttentionFn(torch.autograd.Function):
         srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
         _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _p(out), _p(mrow), _p(srow), _p(cnt), _stream(q))
-        ctx.save_for_backward(q, k, v, gi, out, mrow, srow, cnt)
+        ctx.save_for_backward(q, k, v, gi, out, mrow, srow, cnt, sn, sr)
         ctx.nl, ctx.margs_src, ctx.rc, ctx.q_div = nl, (node_type, rbf_offset, rbf_coeff, packed), rc, q_div
         return out
 
     @staticmethod
     def backward(ctx, gout):
         _no_double_backward()
-        q, k, v, gi, out, mrow, srow, cnt = ctx.saved_tensors
+        q, k, v, gi, out, mrow, srow, cnt, sn, sr = ctx.saved_tensors
         nl = ctx.nl
         node_type, rbf_offset, rbf_coeff, packed = ctx.margs_src
         dev = q.device
@@ -224,6 +235,6 @@ class AttentionFn(torch.autograd.Function):
         _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(dgi),
                   _p(ddv), _p(dd), _p(dq), _p(dk), _p(dv), _p(w_e), _p(dqk), _stream(gout))
         del w_e, dqk
-        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed)
+        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
         _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dgi), _lib.i32(256), _p(dd), _lib.i32(1), _stream(gout))
         return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None
