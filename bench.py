@@ -44,7 +44,24 @@ def mlp_bwd_flops(E, n_mlp):
 
 
 def attn_fwd_bytes(N, E):
+    # read q, k, v, gate|inputhead, edge (col, dvec, dist), row_ptr; write out, m, s, cnt
     return 4.0 * (N * (128 * 8 * 2 + 9 * 256 + 20 * 256 + 3 * 128) + E * (256 + 5) + N + 1)
+
+
+def attn_bwd_bytes(N, E):
+    # row pass: read grad, out, q, k, v, gi, m/s/cnt, edges; write dgi, ddvec, ddist, dq, w, dqk
+    # column pass: read w, dqk, key CSR, grad rows, q; write dv, dk
+    row = N * (2 * 20 * 256 + 3 * 1024 + 9 * 256 + 3 * 128) + E * (256 + 5 + 256 + 4 + 2 * 128)
+    col = N * (20 * 256 + 1024 + 9 * 256 + 1024 + 2) + E * (2 * 128 + 2 + 3)
+    return 4.0 * (row + col)
+
+
+def deg_fwd_bytes(N, E):
+    return 4.0 * (E * (768 + 4) + N * 9 * 256)
+
+
+def deg_bwd_bytes(N, E):
+    return 4.0 * (E * (768 + 768 + 4 + 4) + N * 9 * 256)
 
 
 KERNEL_OF = {"e2v2_mlp_fwd": "k_mlp_fwd", "e2v2_mlp_bwd": "k_mlp_bwd", "e2v2_attn_fwd": "k_attn_fwd",
@@ -93,9 +110,12 @@ def cpu_baseline(pkg):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=4)
+    ap.add_argument("--mode", choices=["md", "eval"], default=None,
+                    help="md: NVE velocity-Verlet steps (default for configs 1-4); eval: repeated energy+force "
+                         "evaluations at fixed positions (default for config 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one plain 256 MiB device copy first (scale reference for FETCH_SIZE/WRITE_SIZE)")
@@ -119,7 +139,11 @@ def main():
     m = model.MolfmAtomic(model.default_args()).eval().to(dev).requires_grad_(False)
     sysd = systems.CONFIGS[args.config]()
     N = len(sysd["pos"])
+    mode = args.mode or ("eval" if args.config == 5 else "md")
     integ = md.VelocityVerlet(m, sysd, dev, dt_fs=1.0, T=300.0, seed=0)
+    if mode == "eval":
+        integ.step = lambda: integ.__setattr__("e", integ.forces()[0])
+        integ.kinetic = lambda: 0.0
     integ.e, integ.f = integ.forces()          # setup: forces at t = 0
     for _ in range(args.warmup):
         integ.step()
@@ -142,6 +166,7 @@ def main():
     ms = dt / args.steps * 1e3
     E_mean = float(np.mean(edges))
     stats = timer.summary()
+    peak_gb = torch.cuda.max_memory_allocated(dev) / 1e9
     # dominant library call by total time
     dom = max(stats.items(), key=lambda kv: kv[1]["total_ms"])
     name, st = dom
@@ -154,12 +179,14 @@ def main():
         roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / FP32_PEAK_TFLOPS, "traffic": traffic_from_profile(name), "kernel": name}
     else:
-        b = attn_fwd_bytes(N, E_mean)
+        fb = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
+              "e2v2_deg_bwd": deg_bwd_bytes}.get(name, attn_fwd_bytes)
+        b = fb(N, E_mean)
         achieved = b / (st["avg_ms"] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profile(name), "kernel": name}
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.config == 4:
         cpu = cpu_baseline(pkg)
     out = {
         "metric": "attn edges/s fwd+force-bwd & MD atom-steps/s at 10k atoms; % HBM roofline",
@@ -168,10 +195,14 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded generator, random-init weights)",
-        "config": {"workload": f"configs[{args.config - 1}] {sysd['name']}: {N} atoms, periodic, rc 6 A, "
-                               f"NVE velocity-Verlet 1 fs, neighbour rebuild every step, fp32 energy+forces",
+        "config": {"workload": f"configs[{args.config - 1}] {sysd['name']}: {N} atoms, rc 6 A, "
+                               + ("NVE velocity-Verlet 1 fs, neighbour rebuild every step, fp32 energy+forces"
+                                  if mode == "md" else "repeated fp32 energy+force evaluations (neighbour build "
+                                                       "included)"),
                    "atoms": N, "edges_per_step": E_mean, "layers": 4, "parallelism": "single GPU"},
         "atom_steps_per_s": N * args.steps / dt,
+        "mode": mode,
+        "peak_memory_gb": peak_gb,
         "nve_energy_drift_ev_per_atom": (e_end - e_start) / N,
         "kernels": {k: {"avg_ms": round(v["avg_ms"], 4), "count": v["count"], "total_ms": round(v["total_ms"], 3)}
                     for k, v in stats.items()},

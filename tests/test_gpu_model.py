@@ -68,3 +68,85 @@ def test_reference_interface_padded(pkg, cuda):
     mask = bd["atom_masks"]
     assert torch.allclose(res["pred_energy"].detach(), e, rtol=1e-6, atol=1e-6)
     assert torch.allclose(res["pred_forces"][mask], f, rtol=1e-5, atol=1e-7)
+
+
+def test_model_peptide_cfg3(pkg, cuda):
+    from ubio_molfm_amd import systems
+    m, om = _pair(cuda, seed=5)
+    _compare(m, om, systems.CONFIGS[3](), cuda, "cfg3")
+
+
+def test_deterministic_bitwise(pkg, cuda):
+    """Two evaluations of the same input give bit-identical energies and forces
+    (no floating-point atomics anywhere on the path)."""
+    from ubio_molfm_amd import systems
+    m, _ = _pair(cuda, seed=6)
+    s = systems.CONFIGS[1]()
+    pos = torch.as_tensor(s["pos"], device=cuda); Z = torch.as_tensor(s["Z"], device=cuda)
+    e1, f1, _ = m.energy_forces_flat(pos, Z, s["graph_ptr"], s["cell"], s["pbc"])
+    e2, f2, _ = m.energy_forces_flat(pos, Z, s["graph_ptr"], s["cell"], s["pbc"])
+    assert torch.equal(e1, e2) and torch.equal(f1, f2)
+
+
+def test_degenerate_frames_and_coincident_atoms(pkg, cuda):
+    """Atoms at the origin and on the +-y pole, where the reference's Wigner
+    frames are special-cased with detached angles (module_utils.py:188-221), and
+    a pair closer than min_dist = 1e-4 (no edge), non-periodic.
+
+    Energies match the oracle.  Forces match the oracle on every other atom; on
+    the origin/pole atoms the reference's detached angles drop the part of
+    dTP/dr perpendicular to r, so those forces are checked against central
+    finite differences of the fp64 oracle energy (the exact gradient)."""
+    from ubio_molfm_amd import systems
+    from oracle.model import MolfmAtomic as OracleModel
+    m, om = _pair(cuda, seed=7)
+    rng = np.random.default_rng(11)
+    p = rng.normal(size=(14, 3)) * 1.6
+    p[0] = [0.0, 0.0, 0.0]
+    p[1] = [0.0, 2.1, 0.0]
+    p[2] = [0.0, -1.7, 0.0]
+    p[3] = p[4] + np.array([3e-5, 0.0, 0.0])
+    sysd = dict(pos=p.astype(np.float32), Z=rng.choice([1, 6, 7, 8], size=14).astype(np.int64),
+                graph_ptr=np.array([0, 14]), cell=np.zeros((1, 3, 3), np.float32), pbc=np.zeros((1, 3), bool))
+    pos = torch.as_tensor(sysd["pos"], device=cuda)
+    e, f, nl = m.energy_forces_flat(pos, torch.as_tensor(sysd["Z"], device=cuda), sysd["graph_ptr"],
+                                    sysd["cell"], sysd["pbc"])
+    bd = systems.to_padded(sysd)
+    r = om(dict(bd))
+    assert abs(float(e.cpu()[0]) - float(r["pred_energy"][0])) / 14 < 1e-5
+    fo = r["pred_forces"][0].detach()
+    fc = f.cpu()
+    rel = float((fc[3:] - fo[3:]).norm() / fo[3:].norm())
+    m64 = OracleModel().eval().double()
+    m64.load_state_dict(om.state_dict())
+    b64 = {k: (v.double() if v.dtype == torch.float32 else v) for k, v in bd.items()}
+    h = 1e-5
+    fd = torch.zeros(3, 3, dtype=torch.float64)
+    for a in range(3):
+        for c in range(3):
+            bp = dict(b64); bp["pos"] = b64["pos"].clone(); bp["pos"][0, a, c] += h
+            bm = dict(b64); bm["pos"] = b64["pos"].clone(); bm["pos"][0, a, c] -= h
+            fd[a, c] = -(m64(bp, need_force=False)["pred_energy"] - m64(bm, need_force=False)["pred_energy"]) / (2 * h)
+    rel_fd = float((fc[:3].double() - fd).norm() / fd.norm())
+    rel_ref_fd = float((fo[:3].double() - fd).norm() / fd.norm())
+    print(f"[model degenerate] E={nl.n_edges} others relL2={rel:.2e} pole/origin vs FD={rel_fd:.2e} "
+          f"(reference autograd vs FD={rel_ref_fd:.2e})", flush=True)
+    assert rel < 1e-4 and rel_fd < 1e-3
+
+
+def test_translation_and_rotation_invariance(pkg, cuda):
+    """Energy is invariant and forces rotate with the frame (non-periodic)."""
+    from ubio_molfm_amd import systems
+    m, _ = _pair(cuda, seed=8)
+    s = systems.organics_batch(n_mol=2, nmin=20, nmax=30, seed=9)
+    q, _ = np.linalg.qr(np.random.default_rng(1).normal(size=(3, 3)))
+    if np.linalg.det(q) < 0:
+        q[:, 0] *= -1
+    s2 = dict(s); s2["pos"] = (s["pos"] @ q.T + np.array([3.0, -2.0, 5.0])).astype(np.float32)
+    Z = torch.as_tensor(s["Z"], device=cuda)
+    e1, f1, _ = m.energy_forces_flat(torch.as_tensor(s["pos"], device=cuda), Z, s["graph_ptr"], s["cell"], s["pbc"])
+    e2, f2, _ = m.energy_forces_flat(torch.as_tensor(s2["pos"], device=cuda), Z, s2["graph_ptr"], s2["cell"],
+                                     s2["pbc"])
+    qt = torch.as_tensor(q, dtype=torch.float32, device=cuda)
+    assert torch.allclose(e1, e2, rtol=1e-5, atol=1e-5)
+    assert float((f1 @ qt.T - f2).norm() / f1.norm()) < 1e-4

@@ -94,3 +94,14 @@ def test_empty_and_isolated(pkg, cuda):
                 cell=np.zeros((1, 3, 3), np.float32), pbc=np.zeros((1, 3), bool))
     nl = _check(pkg, cuda, sysd, label="isolated")
     assert nl.n_edges == 0
+
+
+def test_coincident_atoms_below_min_dist(pkg, cuda):
+    rng = np.random.default_rng(3)
+    pos = rng.uniform(0, 8, size=(30, 3)).astype(np.float32)
+    pos[7] = pos[3] + np.float32(5e-5)
+    sysd = dict(pos=pos, Z=np.full(30, 6), graph_ptr=np.array([0, 30]),
+                cell=(np.eye(3, dtype=np.float32) * 8.0)[None], pbc=np.ones((1, 3), bool))
+    nl = _check(pkg, cuda, sysd, label="coincident")
+    c = nl.canonical()
+    assert not np.any((c["i"] == 3) & (c["j"] == 7) & np.all(c["s"] == 0, axis=1))

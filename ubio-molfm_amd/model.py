@@ -34,6 +34,15 @@ def _spread_bits10(v: torch.Tensor) -> torch.Tensor:
     return v
 
 
+def graph_bounds(pos: torch.Tensor, counts: torch.Tensor):
+    """Per-graph coordinate minimum and maximum [B, 3] (graphs contiguous)."""
+    if counts.shape[0] == 1:
+        return pos.amin(0, keepdim=True), pos.amax(0, keepdim=True)
+    lo = torch.segment_reduce(pos, "min", lengths=counts, axis=0, unsafe=True)
+    hi = torch.segment_reduce(pos, "max", lengths=counts, axis=0, unsafe=True)
+    return lo, hi
+
+
 def spatial_order(pos: torch.Tensor, graph_ptr) -> torch.Tensor:
     """Permutation that sorts the atoms of every graph along a 30-bit Morton
     (Z-order) curve of their positions; graphs stay contiguous and in order.
@@ -45,9 +54,7 @@ def spatial_order(pos: torch.Tensor, graph_ptr) -> torch.Tensor:
     counts = torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device)
     B = counts.shape[0]
     gid = torch.repeat_interleave(torch.arange(B, device=pos.device), counts)
-    idx = gid[:, None].expand(-1, 3)
-    lo = torch.full((B, 3), float("inf"), device=pos.device).scatter_reduce(0, idx, pos, "amin", include_self=True)
-    hi = torch.full((B, 3), float("-inf"), device=pos.device).scatter_reduce(0, idx, pos, "amax", include_self=True)
+    lo, hi = graph_bounds(pos, counts)
     span = (hi - lo).clamp_min(1e-6)
     q = ((pos - lo[gid]) / span[gid] * 1023.0).clamp(0, 1023).to(torch.int64)
     code = _spread_bits10(q[:, 0]) | (_spread_bits10(q[:, 1]) << 1) | (_spread_bits10(q[:, 2]) << 2)

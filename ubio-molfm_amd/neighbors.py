@@ -117,10 +117,12 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     atom_graph = torch.repeat_interleave(torch.arange(B, device=dev, dtype=torch.int32),
                                          torch.as_tensor(np.diff(graph_ptr), device=dev))
     if N:
-        lo = torch.full((B, 3), float("inf"), device=dev).scatter_reduce(
-            0, atom_graph.long()[:, None].expand(-1, 3), pos, "amin", include_self=True)
-        hi = torch.full((B, 3), float("-inf"), device=dev).scatter_reduce(
-            0, atom_graph.long()[:, None].expand(-1, 3), pos, "amax", include_self=True)
+        counts = torch.as_tensor(np.diff(graph_ptr), device=dev)
+        if B == 1:
+            lo, hi = pos.amin(0, keepdim=True), pos.amax(0, keepdim=True)
+        else:
+            lo = torch.segment_reduce(pos, "min", lengths=counts, axis=0, unsafe=True)
+            hi = torch.segment_reduce(pos, "max", lengths=counts, axis=0, unsafe=True)
         bb = torch.stack([lo, hi]).cpu().numpy()
     else:
         bb = np.zeros((2, B, 3), F32)
