@@ -347,38 +347,101 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
   }
 }
 
+// Column pass: for every source atom j, sum over its key-CSR edges (ascending
+// edge id) -> dv_j and dk_j.  Edge metadata of a 32-edge chunk is staged in LDS
+// so the per-edge gathers of grad rows do not wait on index loads; two edges
+// are processed per iteration to overlap their 20-row gathers.
 __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const float* __restrict__ G,
                                                       const float* __restrict__ w_e, const float* __restrict__ dqk_e,
                                                       float* __restrict__ dv_out, float* __restrict__ dk_out) {
+  constexpr int CC = 32;
+  __shared__ int ci[CC];
+  __shared__ float cdv[CC][3];
+  __shared__ float cw[CC][kH];
+  __shared__ float cq[CC][kH];
   const int j = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
   if (j >= A.n_rows) return;
   const int c = t, hc = t & (kH - 1);
   const int hk = t >> 1, d0 = 4 * (t & 1);
+  const size_t os = (size_t)A.n_rows * kC;
   float av[kNV];
 #pragma unroll
   for (int r = 0; r < kNV; ++r) av[r] = 0.f;
   float ak[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int p = A.key_ptr[j]; p < A.key_ptr[j + 1]; ++p) {
-    const int64_t e = A.key_eid[p];
-    const int i = A.edge_row[e];
-    const float dvx = A.dvec[3 * e], dvy = A.dvec[3 * e + 1], dvz = A.dvec[3 * e + 2];
-    float g[kNT];
-    const size_t os = (size_t)A.n_rows * kC;
+  const int p0 = A.key_ptr[j], p1 = A.key_ptr[j + 1];
+  for (int c0 = p0; c0 < p1; c0 += CC) {
+    const int nc = min(CC, p1 - c0);
+    if (t < nc) {
+      const int64_t e = A.key_eid[c0 + t];
+      ci[t] = A.edge_row[e];
+      cdv[t][0] = A.dvec[3 * e];
+      cdv[t][1] = A.dvec[3 * e + 1];
+      cdv[t][2] = A.dvec[3 * e + 2];
+    }
+    // per-edge head weights: w and dqk rows are 512 B each; 2 edges x 128 heads per pass
+    for (int idx = t; idx < nc * kH; idx += 256) {
+      const int el = idx >> 7, h = idx & (kH - 1);
+      const int64_t e = A.key_eid[c0 + el];
+      cw[el][h] = w_e[e * kH + h];
+      cq[el][h] = dqk_e[e * kH + h];
+    }
+    __syncthreads();
+    int el = 0;
+    for (; el + 1 < nc; el += 2) {
+      const int i0 = ci[el], i1 = ci[el + 1];
+      float g0[kNT], g1[kNT];
 #pragma unroll
-    for (int z = 0; z < kNT; ++z) g[z] = G[(size_t)i * kC + z * os + c];
-    float dA[kNV][3];
-    tp_transpose(g, dA);
-    const float w = w_e[e * kH + hc];
+      for (int z = 0; z < kNT; ++z) {
+        g0[z] = G[(size_t)i0 * kC + z * os + c];
+        g1[z] = G[(size_t)i1 * kC + z * os + c];
+      }
+      const float* q0 = A.q + ((size_t)i0 * kH + hk) * kD + d0;
+      const float* q1 = A.q + ((size_t)i1 * kH + hk) * kD + d0;
+      float qa[4], qb[4];
 #pragma unroll
-    for (int r = 0; r < kNV; ++r) av[r] = fmaf(w, dA[r][0] * dvx + dA[r][1] * dvy + dA[r][2] * dvz, av[r]);
-    const float dqk = dqk_e[e * kH + hk];
-    const float* qp = A.q + ((size_t)i * kH + hk) * kD + d0;
+      for (int d = 0; d < 4; ++d) { qa[d] = q0[d]; qb[d] = q1[d]; }
+      float dA[kNV][3];
+      tp_transpose(g0, dA);
+      {
+        const float w = cw[el][hc];
+        const float x = cdv[el][0], y = cdv[el][1], zz = cdv[el][2];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) ak[d] = fmaf(dqk, qp[d] / A.q_div, ak[d]);
+        for (int r = 0; r < kNV; ++r) av[r] = fmaf(w, dA[r][0] * x + dA[r][1] * y + dA[r][2] * zz, av[r]);
+      }
+      tp_transpose(g1, dA);
+      {
+        const float w = cw[el + 1][hc];
+        const float x = cdv[el + 1][0], y = cdv[el + 1][1], zz = cdv[el + 1][2];
+#pragma unroll
+        for (int r = 0; r < kNV; ++r) av[r] = fmaf(w, dA[r][0] * x + dA[r][1] * y + dA[r][2] * zz, av[r]);
+      }
+      const float dq0 = cq[el][hk], dq1 = cq[el + 1][hk];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        ak[d] = fmaf(dq0, qa[d] / A.q_div, ak[d]);
+        ak[d] = fmaf(dq1, qb[d] / A.q_div, ak[d]);
+      }
+    }
+    if (el < nc) {
+      const int i0 = ci[el];
+      float g0[kNT];
+#pragma unroll
+      for (int z = 0; z < kNT; ++z) g0[z] = G[(size_t)i0 * kC + z * os + c];
+      float dA[kNV][3];
+      tp_transpose(g0, dA);
+      const float w = cw[el][hc];
+      const float x = cdv[el][0], y = cdv[el][1], zz = cdv[el][2];
+#pragma unroll
+      for (int r = 0; r < kNV; ++r) av[r] = fmaf(w, dA[r][0] * x + dA[r][1] * y + dA[r][2] * zz, av[r]);
+      const float dq0 = cq[el][hk];
+      const float* q0 = A.q + ((size_t)i0 * kH + hk) * kD + d0;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) ak[d] = fmaf(dq0, q0[d] / A.q_div, ak[d]);
+    }
+    __syncthreads();
   }
-  const size_t vs = (size_t)A.n_rows * kC;
 #pragma unroll
-  for (int r = 0; r < kNV; ++r) dv_out[(size_t)j * kC + r * vs + c] = av[r];
+  for (int r = 0; r < kNV; ++r) dv_out[(size_t)j * kC + r * os + c] = av[r];
 #pragma unroll
   for (int d = 0; d < 4; ++d) dk_out[((size_t)j * kH + hk) * kD + d0 + d] = ak[d];
 }

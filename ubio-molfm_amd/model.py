@@ -209,9 +209,11 @@ class MolfmAtomic(nn.Module):
         h = self.head.head_name(head)
         e_atom = self.head.energy_heads[h](x[0]).squeeze(-1)     # x is m-major [9, N, C]
         B = len(graph_ptr) - 1
-        gid = torch.repeat_interleave(torch.arange(B, device=pos.device),
-                                      torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device))
-        energy = torch.zeros(B, dtype=e_atom.dtype, device=pos.device).index_add(0, gid, e_atom)
+        if B == 1:
+            energy = e_atom.sum().reshape(1)
+        else:   # deterministic per-graph sums (no atomics)
+            counts = torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device)
+            energy = torch.segment_reduce(e_atom, "sum", lengths=counts, axis=0, unsafe=True)
         return energy, nl
 
     def energy_forces_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None):
