@@ -18,6 +18,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
+BF16_PEAK_TFLOPS = 2500.0
 
 
 def load_package():
@@ -69,11 +70,13 @@ KERNEL_OF = {"e2v2_mlp_fwd": "k_mlp_fwd", "e2v2_mlp_bwd": "k_mlp_bwd", "e2v2_att
              "e2v2_deg_fwd": "k_deg_fwd", "e2v2_deg_bwd": "k_deg_bwd", "e2v2_nbr_count": "k_nbr_count"}
 
 
-def traffic_from_profile(entry):
+def traffic_from_profile(entry, bf16=False):
     """HBM bytes per launch of the entry point's kernel from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated against a plain copy)."""
     path = ROOT / "profiles" / "hbm_traffic_cfg4_md10k.txt"
     k = KERNEL_OF.get(entry)
+    if bf16 and entry in ("e2v2_mlp_fwd", "e2v2_mlp_bwd"):
+        k = k + "_bf16"
     if k is None or not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -116,6 +119,9 @@ def main():
     ap.add_argument("--mode", choices=["md", "eval"], default=None,
                     help="md: NVE velocity-Verlet steps (default for configs 1-4); eval: repeated energy+force "
                          "evaluations at fixed positions (default for config 5)")
+    ap.add_argument("--dtype", choices=["fp32", "bf16"], default=None,
+                    help="GEMM operand precision (default: bf16 for configs 2 and 5, as they are specified, "
+                         "else fp32); accumulation, activations and reductions are fp32 in both")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one plain 256 MiB device copy first (scale reference for FETCH_SIZE/WRITE_SIZE)")
@@ -137,6 +143,9 @@ def main():
         del src, dst
     torch.manual_seed(0)
     m = model.MolfmAtomic(model.default_args()).eval().to(dev).requires_grad_(False)
+    dtype = args.dtype or ("bf16" if args.config in (2, 5) else "fp32")
+    m.decoder.set_compute_dtype(dtype)
+    bf16 = dtype == "bf16"
     sysd = systems.CONFIGS[args.config]()
     N = len(sysd["pos"])
     mode = args.mode or ("eval" if args.config == 5 else "md")
@@ -176,8 +185,9 @@ def main():
         fl = mlp_fwd_flops if name == "e2v2_mlp_fwd" else mlp_bwd_flops
         per_step = fl(E_mean, 3) + 4 * fl(E_mean, 1)
         achieved = per_step / (st["count"] / args.steps) / (st["avg_ms"] * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / FP32_PEAK_TFLOPS, "traffic": traffic_from_profile(name), "kernel": name}
+        peak = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
+        roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+                "frac": achieved / peak, "traffic": traffic_from_profile(name, bf16), "kernel": name}
     else:
         fb = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
               "e2v2_deg_bwd": deg_bwd_bytes}.get(name, attn_fwd_bytes)
@@ -193,12 +203,13 @@ def main():
         "value": E_mean * args.steps / dt,
         "unit": "edges/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 GEMM operands, f32 accumulate" if bf16 else "f32",
         "data": "synthetic (seeded generator, random-init weights)",
         "config": {"workload": f"configs[{args.config - 1}] {sysd['name']}: {N} atoms, rc 6 A, "
-                               + ("NVE velocity-Verlet 1 fs, neighbour rebuild every step, fp32 energy+forces"
-                                  if mode == "md" else "repeated fp32 energy+force evaluations (neighbour build "
-                                                       "included)"),
+                               + ("NVE velocity-Verlet 1 fs, neighbour rebuild every step, energy+forces"
+                                  if mode == "md" else "repeated energy+force evaluations (neighbour build "
+                                                       "included)") + f", {dtype}",
                    "atoms": N, "edges_per_step": E_mean, "layers": 4, "parallelism": "single GPU"},
         "atom_steps_per_s": N * args.steps / dt,
         "mode": mode,

@@ -115,11 +115,19 @@ typedef struct e2v2_mlp_weights {
   int32_t ldw1;
   const float* w2;    /* [128][128] Linear2 as stored                             */
   const float* w3;    /* [256][128] Linear3 as stored                             */
+  /* bf16 operands (compute_bf16 = 1), each as B^T row-major [N][K]:              */
+  const void* w1b;    /* [128][256] rbf block of Linear1 (forward)                */
+  const void* w2b;    /* [128][128] Linear2 (forward)                             */
+  const void* w3b;    /* [256][128] Linear3 (forward)                             */
+  const void* w3tb;   /* [128][256] Linear3^T (backward)                          */
+  const void* w2tb;   /* [128][128] Linear2^T (backward)                          */
+  const void* w1rtb;  /* [256][128] rbf block of Linear1, transposed (backward)   */
 } e2v2_mlp_weights;
 
 typedef struct e2v2_mlp_args {
   int64_t n_edges;
   int32_t n_mlp;                 /* 1..E2V2_MAX_MLP profiles sharing the edge input */
+  int32_t compute_bf16;          /* 1: bf16 GEMM operands, fp32 accumulation       */
   const float* dist;             /* [E]                                            */
   const int32_t* edge_row;       /* [E] query atom                                 */
   const int32_t* col;            /* [E] source atom                                */

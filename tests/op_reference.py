@@ -28,6 +28,54 @@ def mlp_ref(d, zi, zj, net, tgt_w, src_w, offset, coeff):
     return net(x)
 
 
+def bf16_round(x):
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
+class _RoundFwd(torch.autograd.Function):
+    """bf16 rounding of a GEMM operand; the gradient passes unchanged."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return bf16_round(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g
+
+
+class _RoundGrad(torch.autograd.Function):
+    """Identity whose incoming gradient is rounded to bf16 (a GEMM operand of the backward)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return x.clone()
+
+    @staticmethod
+    def backward(ctx, g):
+        return bf16_round(g)
+
+
+def mlp_ref_bf16(d, zi, zj, net, tgt_w, src_w, offset, coeff):
+    """RadialProfile with the rounding points of the bf16 edge kernels: the RBF
+    block, both LayerNorm+SiLU activations and the weights of the three GEMMs
+    are bf16 in the forward; the upstream gradient and the two LayerNorm input
+    gradients are bf16 in the backward; the per-type tables, LayerNorm
+    statistics and every accumulation stay at full precision."""
+    F = torch.nn.functional
+    lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
+    K0, e = offset.shape[0], tgt_w.shape[1]
+    W1 = lin1.weight
+    r = _RoundFwd.apply(rbf(d, offset, coeff))
+    y1 = (r @ bf16_round(W1[:, :K0]).t() + (tgt_w[zi] @ W1[:, K0:K0 + e].t() + lin1.bias)
+          + src_w[zj] @ W1[:, K0 + e:K0 + 2 * e].t())
+    y1 = _RoundGrad.apply(y1)
+    a1 = _RoundFwd.apply(F.silu(F.layer_norm(y1, ln1.normalized_shape, ln1.weight, ln1.bias, ln1.eps)))
+    y2 = _RoundGrad.apply(a1 @ bf16_round(lin2.weight).t() + lin2.bias)
+    a2 = _RoundFwd.apply(F.silu(F.layer_norm(y2, ln2.normalized_shape, ln2.weight, ln2.bias, ln2.eps)))
+    return _RoundGrad.apply(a2 @ bf16_round(lin3.weight).t() + lin3.bias)
+
+
 def attn_ref(q, k, v, dvec, dist, row, col, gi, T, rc, N):
     E = row.shape[0]
     H = q.shape[1]

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from op_reference import attn_ref, deg_ref, mlp_ref
+from op_reference import attn_ref, deg_ref, mlp_ref, mlp_ref_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -61,6 +61,49 @@ def test_mlp_forward_backward(pkg, cuda):
     e_b = relerr(dd, g)
     print(f"[mlp] fwd rel {e_f:.2e} bwd rel {e_b:.2e}", flush=True)
     assert e_f < 2e-5 and e_b < 1e-4
+
+
+def test_mlp_bf16_forward_backward(pkg, cuda):
+    """bf16-operand edge MLP.  Against a float64 restatement that rounds at the
+    kernel's rounding points: forward 3e-4, backward 1e-3 relative (fp32 and
+    float64 values on either side of a bf16 rounding boundary round apart).  Against the
+    plain float64 MLP (the whole bf16 error): forward and backward within 2e-2."""
+    from ubio_molfm_amd import _lib, modules, ops
+    torch.manual_seed(11)
+    s, pos, nl = _graph(pkg, cuda, seed=5)
+    E, N = nl.n_edges, nl.n_atoms
+    print(f"[mlp-bf16] N={N} E={E}", flush=True)
+    prof = modules.RadialProfile([768, 128, 128, 256])
+    for m in prof.modules():
+        if isinstance(m, torch.nn.LayerNorm):
+            m.weight.data.uniform_(0.5, 1.5); m.bias.data.uniform_(-0.2, 0.2)
+    tgt = torch.nn.Embedding(300, 256); src = torch.nn.Embedding(300, 256)
+    rb = modules.GaussianSmearing(256, 6.0, 2.0)
+    Z = torch.as_tensor(s["Z"], device=cuda).to(torch.int32)
+    packed = [ops.PackedMLP(prof.to(cuda).net, tgt.weight.to(cuda), src.weight.to(cuda), bf16=True)]
+    sn, sr = ops.mlp_save_buffers(1, E, cuda)
+    args = ops.mlp_args(nl, Z, rb.offset.to(cuda), rb.coeff, packed, sn, sr)
+    assert args.compute_bf16 == 1
+    st = _lib.vp(torch.cuda.current_stream().cuda_stream)
+    out = torch.empty(E, 256, device=cuda)
+    _lib.call("e2v2_mlp_fwd", _lib.C.byref(args), _lib.vp(out.data_ptr()), _lib.i32(256), st)
+    dout = torch.randn(E, 256, device=cuda)
+    dd = torch.empty(E, device=cuda)
+    _lib.call("e2v2_mlp_bwd", _lib.C.byref(args), _lib.vp(dout.data_ptr()), _lib.i32(256), _lib.vp(dd.data_ptr()),
+              _lib.i32(0), st)
+    zi = torch.as_tensor(s["Z"])[nl.edge_row.long().cpu()]
+    zj = torch.as_tensor(s["Z"])[nl.col.long().cpu()]
+    net64 = prof.cpu().double().net
+    errs = {}
+    for name, fn in (("emulated", mlp_ref_bf16), ("fp64", mlp_ref)):
+        d64 = nl.dist.double().cpu().requires_grad_(True)
+        ref = fn(d64, zi, zj, net64, tgt.weight.double(), src.weight.double(), rb.offset.double(), rb.coeff)
+        g = torch.autograd.grad((ref * dout.double().cpu()).sum(), d64)[0]
+        errs[name] = (relerr(out, ref), relerr(dd, g))
+    print(f"[mlp-bf16] vs emulated fwd {errs['emulated'][0]:.2e} bwd {errs['emulated'][1]:.2e}; "
+          f"vs fp64 fwd {errs['fp64'][0]:.2e} bwd {errs['fp64'][1]:.2e}", flush=True)
+    assert errs["emulated"][0] < 3e-4 and errs["emulated"][1] < 1e-3
+    assert errs["fp64"][0] < 2e-2 and errs["fp64"][1] < 2e-2
 
 
 def _attn_inputs(nl, cuda, seed=2):

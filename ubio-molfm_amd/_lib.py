@@ -33,11 +33,11 @@ class NbrPlan(C.Structure):
 class MlpWeights(C.Structure):
     _fields_ = [("w1t", vp), ("ttgt", vp), ("tsrc", vp), ("g1", vp), ("be1", vp), ("w2t", vp), ("b2", vp),
                 ("g2", vp), ("be2", vp), ("w3t", vp), ("b3", vp), ("w1", vp), ("ldw1", i32), ("w2", vp),
-                ("w3", vp)]
+                ("w3", vp), ("w1b", vp), ("w2b", vp), ("w3b", vp), ("w3tb", vp), ("w2tb", vp), ("w1rtb", vp)]
 
 
 class MlpArgs(C.Structure):
-    _fields_ = [("n_edges", i64), ("n_mlp", i32), ("dist", vp), ("edge_row", vp), ("col", vp),
+    _fields_ = [("n_edges", i64), ("n_mlp", i32), ("compute_bf16", i32), ("dist", vp), ("edge_row", vp), ("col", vp),
                 ("node_type", vp), ("rbf_offset", vp), ("rbf_coeff", f32), ("save_n", vp), ("save_r", vp),
                 ("w", MlpWeights * 3)]
 

@@ -88,6 +88,18 @@ class E2FormerBackbone(nn.Module):
         self.max_neighbors = self.decoder.max_neighbors
         self.max_radius = float(self.decoder.max_radius)
         self.cells_per_direction = int(kwargs.get("pbc_expanded_num_cell_per_direction", 4))
+        self.set_compute_dtype(kwargs.get("compute_dtype", "fp32"))
+
+    def set_compute_dtype(self, dtype) -> None:
+        """'fp32' (default) or 'bf16': in bf16 mode every GEMM of the stack (edge
+        radial MLPs, per-node irreps linears, Q/K heads, SO(2) output linears, gate)
+        takes bf16 operands with fp32 accumulation; parameters stay fp32 (bf16
+        copies are cached), and activations, softmax statistics, normalisations
+        and all reductions are fp32."""
+        name = {torch.float32: "fp32", torch.bfloat16: "bf16"}.get(dtype, dtype)
+        if name not in ("fp32", "float32", "bf16", "bfloat16"):
+            raise ValueError(f"compute_dtype must be 'fp32' or 'bf16', got {dtype!r}")
+        self.compute_bf16 = name in ("bf16", "bfloat16")
 
     # -- flat interface -------------------------------------------------------
     def forward_flat(self, pos: torch.Tensor, Z: torch.Tensor, graph_ptr, cell, pbc, charge=None,
@@ -106,7 +118,7 @@ class E2FormerBackbone(nn.Module):
                                  self.cells_per_direction)
         dvec, dist = EdgeGeometryFn.apply(pos, nl)
         node_type = Z.to(torch.int32).contiguous()
-        ctx = EdgeContext(nl, dvec, dist, node_type, self.decoder.rbf, self.max_radius)
+        ctx = EdgeContext(nl, dvec, dist, node_type, self.decoder.rbf, self.max_radius, self.compute_bf16)
         sys_node = None
         if charge is not None:
             B = len(graph_ptr) - 1

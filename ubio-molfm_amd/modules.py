@@ -44,6 +44,49 @@ def _dp(t):
     return _lib.vp(t.data_ptr())
 
 
+BF16 = torch.bfloat16
+
+
+def _bf(a):
+    return a if a.dtype == BF16 else a.to(BF16)
+
+
+def _mm_into(a, b, out):
+    """out = a @ b for an fp32 activation a and a weight operand b.  With a bf16
+    weight the activation is rounded to bf16 and the product is accumulated and
+    stored in fp32 (bf16 MFMA operands, fp32 result)."""
+    if b.dtype == BF16:
+        return torch.mm(_bf(a), b, out_dtype=torch.float32, out=out)
+    return torch.mm(a, b, out=out)
+
+
+def _addmm_into(c, a, b, out):
+    """out = c + a @ b with the operand rule of ``_mm_into``."""
+    if b.dtype == BF16:
+        return torch.addmm(c, _bf(a), b, out_dtype=torch.float32, out=out)
+    return torch.addmm(c, a, b, out=out)
+
+
+def cached(owner, name: str, params, build):
+    """Per-object cache of a tensor derived from ``params`` (rebuilt when any of
+    them is replaced or modified in place)."""
+    key = tuple((p.data_ptr(), p._version) for p in params)
+    ent = owner.__dict__.get("_c_" + name)
+    if ent is None or ent[0] != key:
+        ent = (key, build())
+        owner.__dict__["_c_" + name] = ent
+    return ent[1]
+
+
+def gemm_weight(mod, name: str, bf16: bool):
+    """A module's weight as a GEMM operand: the parameter itself in fp32 mode,
+    a cached bf16 copy in bf16 mode."""
+    p = getattr(mod, name)
+    if not bf16:
+        return p.detach()
+    return cached(mod, name + "_bf16", (p,), lambda: p.detach().to(BF16).contiguous())
+
+
 class SO3LinearFn(torch.autograd.Function):
     """y[rows(l)] = res[rows(l)] + x[rows(l)] W_l^T (+ bias on row 0) on the
     m-major layout x[(lmax+1)^2, N, Cin]: each l block is one 2-D GEMM written in
@@ -58,12 +101,13 @@ class SO3LinearFn(torch.autograd.Function):
         y = x.new_empty(L2, N, O)
         if res is not None:
             res = res.contiguous()
+        xa = _bf(x) if W.dtype == BF16 else x
         for l in range(lmax + 1):
             a, b = l * l, (l + 1) ** 2
             if res is None:
-                torch.mm(x[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
+                _mm_into(xa[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
             else:
-                torch.addmm(res[a:b].view(-1, O), x[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
+                _addmm_into(res[a:b].view(-1, O), xa[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
         if bias is not None:
             y[0].add_(bias)
         ctx.save_for_backward(W)
@@ -78,9 +122,10 @@ class SO3LinearFn(torch.autograd.Function):
         L2, N, O = gy.shape
         Cin = W.shape[2]
         gx = gy.new_empty(L2, N, Cin)
+        ga = _bf(gy) if W.dtype == BF16 else gy
         for l in range(ctx.lmax + 1):
             a, b = l * l, (l + 1) ** 2
-            torch.mm(gy[a:b].view(-1, O), W[l], out=gx[a:b].view(-1, Cin))
+            _mm_into(ga[a:b].view(-1, O), W[l], out=gx[a:b].view(-1, Cin))
         return gx, None, None, None, (gy if ctx.has_res else None)
 
 
@@ -93,9 +138,10 @@ class QKProjFn(torch.autograd.Function):
         x = x.contiguous()
         L2, N, C = x.shape
         y = x.new_empty(L2, N, 4 * hid)
+        xa = _bf(x) if W.dtype == BF16 else x
         for l in range(lmax + 1):
             a, b = l * l, (l + 1) ** 2
-            torch.mm(x[a:b].view(-1, C), W[l].t(), out=y[a:b].view(-1, 4 * hid))
+            _mm_into(xa[a:b].view(-1, C), W[l].t(), out=y[a:b].view(-1, 4 * hid))
         y[0].add_(bias)
         hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
         _lib.call("e2v2_pairdot_fwd", _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _stream())
@@ -114,9 +160,10 @@ class QKProjFn(torch.autograd.Function):
         _lib.call("e2v2_pairdot_bwd", _dp(y), _dp(ghq), _dp(ghk), _dp(gy), _lib.i32(N), _lib.i32(hid), _stream())
         C = W.shape[2]
         gx = y.new_empty(L2, N, C)
+        ga = _bf(gy) if W.dtype == BF16 else gy
         for l in range(ctx.lmax + 1):
             a, b = l * l, (l + 1) ** 2
-            torch.mm(gy[a:b].view(-1, F), W[l], out=gx[a:b].view(-1, C))
+            _mm_into(ga[a:b].view(-1, F), W[l], out=gx[a:b].view(-1, C))
         return gx, None, None, None, None
 
 
@@ -131,21 +178,23 @@ class SO2OutFn(torch.autograd.Function):
         so2 = so2.contiguous(); res = res.contiguous()
         _, N, C = so2.shape
         t = so2.new_empty(9, N, C)
+        sa = _bf(so2) if Wp.dtype == BF16 else so2
         o = 0
         for lst in blocks:
             nr = lst[0][1]
             tv = t[o:o + nr].view(-1, C)
             for idx, (t0, nr_, Wt) in enumerate(lst):
-                xin = so2[t0:t0 + nr_].view(-1, C)
+                xin = sa[t0:t0 + nr_].view(-1, C)
                 if idx == 0:
-                    torch.mm(xin, Wt, out=tv)
+                    _mm_into(xin, Wt, out=tv)
                 else:
-                    tv.addmm_(xin, Wt)
+                    _addmm_into(tv, xin, Wt, out=tv)
             o += nr
         y = so2.new_empty(9, N, Wp.shape[1])
+        ta = _bf(t) if Wp.dtype == BF16 else t
         for l in range(3):
             a, b = l * l, (l + 1) ** 2
-            torch.addmm(res[a:b].view(-1, Wp.shape[1]), t[a:b].view(-1, C), Wp[l].t(),
+            _addmm_into(res[a:b].view(-1, Wp.shape[1]), ta[a:b].view(-1, C), Wp[l].t(),
                         out=y[a:b].view(-1, Wp.shape[1]))
         y[0].add_(bp)
         ctx.blocks = blocks
@@ -160,16 +209,19 @@ class SO2OutFn(torch.autograd.Function):
         _, N, O = gy.shape
         C = Wp.shape[2]
         gt = gy.new_empty(9, N, C)
+        bf = Wp.dtype == BF16
+        ga = _bf(gy) if bf else gy
         for l in range(3):
             a, b = l * l, (l + 1) ** 2
-            torch.mm(gy[a:b].view(-1, O), Wp[l], out=gt[a:b].view(-1, C))
+            _mm_into(ga[a:b].view(-1, O), Wp[l], out=gt[a:b].view(-1, C))
         gso2 = gy.new_empty(ctx.shape)
+        gta = _bf(gt) if bf else gt
         o = 0
         for lst in ctx.blocks:
             nr = lst[0][1]
-            gv = gt[o:o + nr].view(-1, C)
+            gv = gta[o:o + nr].view(-1, C)
             for (t0, nr_, Wt) in lst:
-                torch.mm(gv, Wt.t(), out=gso2[t0:t0 + nr_].view(-1, C))
+                _mm_into(gv, Wt.t(), out=gso2[t0:t0 + nr_].view(-1, C))
             o += nr
         return gso2, gy, None, None, None
 
@@ -203,7 +255,10 @@ class GateFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, Wg, bg, k1: float, k2: float):
         x = x.contiguous()
-        sc = torch.addmm(bg, x[0], Wg.t())
+        if Wg.dtype == BF16:
+            sc = torch.mm(_bf(x[0]), Wg.t(), out_dtype=torch.float32).add_(bg)
+        else:
+            sc = torch.addmm(bg, x[0], Wg.t())
         y = torch.empty_like(x)
         _lib.call("e2v2_gate_fwd", _dp(sc), _dp(x), _dp(y), _lib.i32(x.shape[1]), _lib.f32(k1), _lib.f32(k2),
                   _stream())
@@ -218,8 +273,31 @@ class GateFn(torch.autograd.Function):
         gsc = torch.empty_like(sc); gx = torch.empty_like(x)
         _lib.call("e2v2_gate_bwd", _dp(sc), _dp(x), _dp(gy), _dp(gsc), _dp(gx), _lib.i32(x.shape[1]),
                   _lib.f32(ctx.k[0]), _lib.f32(ctx.k[1]), _stream())
-        torch.mm(gsc, Wg, out=gx[0])            # the kernel leaves gx[0] = 0
+        _mm_into(gsc, Wg, out=gx[0])            # the kernel leaves gx[0] = 0
         return gx, None, None, None, None
+
+
+class DenseFn(torch.autograd.Function):
+    """y = x W^T + b for a constant weight W [O, K] (fp32, or bf16 operands with
+    fp32 accumulation); input gradient only."""
+
+    @staticmethod
+    def forward(ctx, x, W, b):
+        x = x.contiguous()
+        y = x.new_empty(x.shape[0], W.shape[0])
+        _mm_into(x, W.t(), out=y)
+        if b is not None:
+            y.add_(b)
+        ctx.save_for_backward(W)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        (W,) = ctx.saved_tensors
+        gy = gy.contiguous()
+        gx = gy.new_empty(gy.shape[0], W.shape[1])
+        _mm_into(gy, W, out=gx)
+        return gx, None, None
 
 
 def _linear(x, lin: nn.Linear):
@@ -277,8 +355,8 @@ class SO3_Linear_e2former(nn.Module):
         self.bias = nn.Parameter(torch.zeros(out_features))
         self.register_buffer("expand_index", _expand_index(lmax), persistent=False)
 
-    def forward(self, x):
-        return SO3LinearFn.apply(x, self.weight.detach(), self.bias.detach(), self.lmax)
+    def forward(self, x, bf16: bool = False):
+        return SO3LinearFn.apply(x, gemm_weight(self, "weight", bf16), self.bias.detach(), self.lmax)
 
 
 class SO3_Linear2Scalar_e2former(nn.Module):
@@ -305,11 +383,15 @@ class SO3_Linear2Scalar_e2former(nn.Module):
         b = torch.cat([self.bias.detach().view(-1), torch.zeros_like(self.bias.detach().view(-1))])
         return w, b
 
-    def head(self, h):
+    def head(self, h, bf16: bool = False):
         """final_linear on the m-contracted products h [N, (lmax+1) hid]."""
         fl = self.final_linear
-        h = torch.nn.functional.silu(_layer_norm(_linear(h, fl[0]), fl[1]))
-        return _linear(h, fl[3])
+        if not bf16:
+            h = torch.nn.functional.silu(_layer_norm(_linear(h, fl[0]), fl[1]))
+            return _linear(h, fl[3])
+        h = DenseFn.apply(h, gemm_weight(fl[0], "weight", True), fl[0].bias.detach())
+        h = torch.nn.functional.silu(_layer_norm(h, fl[1]))
+        return DenseFn.apply(h, gemm_weight(fl[3], "weight", True), fl[3].bias.detach())
 
     def forward(self, x):
         w, b = self.stacked()
@@ -354,8 +436,9 @@ class Gate_s3(nn.Module):
         bound = 1 / math.sqrt(sphere_channels)
         nn.init.uniform_(self.gates.weight, -bound, bound)
 
-    def forward(self, x):
-        return GateFn.apply(x, self.gates.weight.detach(), self.gates.bias.detach(), SILU_NORM, SIGMOID_NORM)
+    def forward(self, x, bf16: bool = False):
+        return GateFn.apply(x, gemm_weight(self.gates, "weight", bf16), self.gates.bias.detach(), SILU_NORM,
+                            SIGMOID_NORM)
 
 
 class FeedForwardNetwork_s3(nn.Module):
@@ -367,10 +450,10 @@ class FeedForwardNetwork_s3(nn.Module):
         self.gate = Gate_s3(hidden_channels, lmax=lmax)
         self.slinear_2 = SO3_Linear_e2former(hidden_channels, output_channels, lmax=lmax, bias=True)
 
-    def forward(self, x, res=None, **kw):
-        h = self.gate(self.slinear_1(x))
+    def forward(self, x, res=None, bf16: bool = False, **kw):
+        h = self.gate(self.slinear_1(x, bf16), bf16)
         s2 = self.slinear_2
-        return SO3LinearFn.apply(h, s2.weight.detach(), s2.bias.detach(), s2.lmax, res)
+        return SO3LinearFn.apply(h, gemm_weight(s2, "weight", bf16), s2.bias.detach(), s2.lmax, res)
 
 
 class sph_fromxyz(nn.Module):
@@ -437,9 +520,14 @@ class SO2_TP_givenl2(nn.Module):
             scale[t0:t1] = r[0]
         return torch.from_numpy(scale)
 
-    def folded_blocks(self):
+    def folded_blocks(self, bf16: bool = False):
         """Per output l3: list of (input row start, rows, W_p^T) with path_norm and
-        loaded CG_weight path scales folded into W_p (cached on versions)."""
+        loaded CG_weight path scales folded into W_p (cached on versions); bf16
+        copies of the folded blocks in bf16 mode."""
+        if bf16:
+            return cached(self, "fold_bf16", list(self.parameters()),
+                          lambda: [[(t0, nr, Wt.to(BF16).contiguous()) for (t0, nr, Wt) in lst]
+                                   for lst in self.folded_blocks()])
         key = tuple((p.data_ptr(), p._version) for p in self.parameters())
         if getattr(self, "_fold_key", None) == key:
             return self._fold
@@ -494,12 +582,13 @@ class SmoothLeakyReLU(nn.Module):
 class EdgeContext:
     """Per-evaluation edge data shared by every layer."""
 
-    def __init__(self, nl, dvec, dist, node_type, rbf: GaussianSmearing, rc: float):
+    def __init__(self, nl, dvec, dist, node_type, rbf: GaussianSmearing, rc: float, bf16: bool = False):
         self.nl, self.dvec, self.dist = nl, dvec, dist
         self.node_type = node_type
         self.rbf_offset = rbf.offset.float().contiguous()
         self.rbf_coeff = float(rbf.coeff)
         self.rc = rc
+        self.bf16 = bf16          # bf16 GEMM operands, fp32 accumulation and storage
 
 
 class E2AttentionArbOrder_sparse(nn.Module):
@@ -529,16 +618,16 @@ class E2AttentionArbOrder_sparse(nn.Module):
         self.proj_first = SO3_Linear_e2former(num_attn_heads * 2, C, lmax=lmax)
         self._mlp = MLPCache()
 
-    def qk_weights(self):
-        key = tuple((p.data_ptr(), p._version) for p in
-                    (self.query_linear.weight, self.query_linear.weight2, self.query_linear.bias,
-                     self.key_linear.weight, self.key_linear.weight2, self.key_linear.bias))
-        if getattr(self, "_qk_key", None) != key:
+    def qk_weights(self, bf16: bool = False):
+        params = (self.query_linear.weight, self.query_linear.weight2, self.query_linear.bias,
+                  self.key_linear.weight, self.key_linear.weight2, self.key_linear.bias)
+
+        def build():
             wq, bq = self.query_linear.stacked()
             wk, bk = self.key_linear.stacked()
-            self._qk = (torch.cat([wq, wk], dim=1).contiguous(), torch.cat([bq, bk]).contiguous())
-            self._qk_key = key
-        return self._qk
+            w = torch.cat([wq, wk], dim=1)
+            return ((w.to(BF16) if bf16 else w).contiguous(), torch.cat([bq, bk]).float().contiguous())
+        return cached(self, "qk_bf16" if bf16 else "qk", params, build)
 
     def forward(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
         """x [9, N, C] (m-major) -> res + attention(x), [9, N, C]."""
@@ -546,20 +635,21 @@ class E2AttentionArbOrder_sparse(nn.Module):
         H = self.num_attn_heads
         if self.training and self.alpha_dropout.p > 0:
             raise NotImplementedError("attention dropout in training mode is not supported by the HIP path")
-        W, b = self.qk_weights()
+        bf16 = ctx.bf16
+        W, b = self.qk_weights(bf16)
         hid = self.query_linear.weight.shape[1]
         hq, hk = QKProjFn.apply(x, W, b, self.lmax, hid)
-        q = self.query_linear.head(hq).reshape(N, H, -1)
-        k = self.key_linear.head(hk).reshape(N, H, -1)
-        v = self.proj_value(x)
-        packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding)
+        q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
+        k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
+        v = self.proj_value(x, bf16)
+        packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding, bf16)
         so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
                                 packed, ctx.rc, math.sqrt(q.shape[-1]))
         if res is None:
             res = torch.zeros_like(x)
         pf = self.proj_first
-        return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(), pf.weight.detach(),
-                              pf.bias.detach())
+        return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16),
+                              gemm_weight(pf, "weight", bf16), pf.bias.detach())
 
 
 class TransBlock(nn.Module):
@@ -585,7 +675,7 @@ class TransBlock(nn.Module):
         if sys_node_embedding is not None:
             h = torch.cat([(h[0] + sys_node_embedding).unsqueeze(0), h[1:]], dim=0)
         x = self.ga(h, ctx, res=res)
-        return self.ffn(self.norm_ffn(x), res=x)
+        return self.ffn(self.norm_ffn(x), res=x, bf16=ctx.bf16)
 
 
 class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
@@ -609,7 +699,8 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
         self._mlp = MLPCache()
 
     def forward(self, ctx: EdgeContext):
-        packed = self._mlp.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding)
+        packed = self._mlp.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
+                               ctx.bf16)
         return DegreeEmbedFn.apply(ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff, packed,
                                    float(self.avg_aggregate_num), ctx.rc)
 

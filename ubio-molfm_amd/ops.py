@@ -48,8 +48,10 @@ class PackedMLP:
     (src/molfm/models/e2former/module_utils.py:2151-2178) whose input is
     [rbf(256), target_table[z_i], source_table[z_j]]."""
 
-    def __init__(self, net: nn.Sequential, tgt: torch.Tensor, src: torch.Tensor, n_rbf: int = 256):
+    def __init__(self, net: nn.Sequential, tgt: torch.Tensor, src: torch.Tensor, n_rbf: int = 256,
+                 bf16: bool = False):
         lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
+        self.bf16 = bf16
         with torch.no_grad():
             W1 = lin1.weight.detach().float().contiguous()
             e = tgt.shape[1]
@@ -63,6 +65,13 @@ class PackedMLP:
             self.g2 = ln2.weight.detach().float().contiguous(); self.be2 = ln2.bias.detach().float().contiguous()
             self.w3 = lin3.weight.detach().float().contiguous(); self.w3t = self.w3.t().contiguous()
             self.b3 = lin3.bias.detach().float().contiguous()
+            # bf16 GEMM operands as B^T row-major: forward W1r, W2, W3; backward W3^T, W2^T, W1r^T
+            self.bf = None
+            if bf16:
+                b = torch.bfloat16
+                self.bf = [W1[:, :n_rbf].to(b).contiguous(), self.w2.to(b).contiguous(), self.w3.to(b).contiguous(),
+                           self.w3.t().to(b).contiguous(), self.w2.t().to(b).contiguous(),
+                           W1[:, :n_rbf].t().to(b).contiguous()]
         if not (abs(ln1.eps - 1e-5) < 1e-12 and abs(ln2.eps - 1e-5) < 1e-12):
             raise NotImplementedError("RadialProfile LayerNorm eps must be 1e-5")
         if self.w1t.shape != (256, 128) or self.w2.shape != (128, 128) or self.w3.shape != (256, 128):
@@ -70,10 +79,11 @@ class PackedMLP:
                                       "is not the [256+2E, 128, 128, 256] profile of the HIP kernels")
 
     def struct(self) -> _lib.MlpWeights:
+        bf = [t.data_ptr() for t in self.bf] if self.bf is not None else [None] * 6
         return _lib.MlpWeights(self.w1t.data_ptr(), self.ttgt.data_ptr(), self.tsrc.data_ptr(), self.g1.data_ptr(),
                                self.be1.data_ptr(), self.w2t.data_ptr(), self.b2.data_ptr(), self.g2.data_ptr(),
                                self.be2.data_ptr(), self.w3t.data_ptr(), self.b3.data_ptr(), self.w1.data_ptr(),
-                               int(self.w1.shape[1]), self.w2.data_ptr(), self.w3.data_ptr())
+                               int(self.w1.shape[1]), self.w2.data_ptr(), self.w3.data_ptr(), *bf)
 
 
 def _version_key(params):
@@ -87,11 +97,11 @@ class MLPCache:
         self.key = None
         self.packed: List[PackedMLP] = []
 
-    def get(self, nets, tgt_emb: nn.Embedding, src_emb: nn.Embedding):
+    def get(self, nets, tgt_emb: nn.Embedding, src_emb: nn.Embedding, bf16: bool = False):
         params = [p for n in nets for p in n.parameters()] + [tgt_emb.weight, src_emb.weight]
-        key = _version_key(params)
+        key = (_version_key(params), bf16)
         if key != self.key:
-            self.packed = [PackedMLP(n, tgt_emb.weight, src_emb.weight) for n in nets]
+            self.packed = [PackedMLP(n, tgt_emb.weight, src_emb.weight, bf16=bf16) for n in nets]
             self.key = key
         return self.packed
 
@@ -102,8 +112,11 @@ def mlp_args(nl: NeighborList, node_type: torch.Tensor, rbf_offset: torch.Tensor
     ws = (_lib.MlpWeights * 3)()
     for m, pk in enumerate(packed):
         ws[m] = pk.struct()
-    return _lib.MlpArgs(nl.n_edges, len(packed), nl.dist.data_ptr(), nl.edge_row.data_ptr(), nl.col.data_ptr(),
-                        node_type.data_ptr(), rbf_offset.data_ptr(), float(rbf_coeff),
+    bf16 = packed[0].bf16
+    if any(pk.bf16 != bf16 for pk in packed):
+        raise ValueError("mixed fp32/bf16 RadialProfile packs in one launch")
+    return _lib.MlpArgs(nl.n_edges, len(packed), int(bf16), nl.dist.data_ptr(), nl.edge_row.data_ptr(),
+                        nl.col.data_ptr(), node_type.data_ptr(), rbf_offset.data_ptr(), float(rbf_coeff),
                         None if save_n is None else save_n.data_ptr(), None if save_r is None else save_r.data_ptr(),
                         ws)
 
