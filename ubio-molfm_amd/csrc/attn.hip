@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
     for (int el = half; el < nc; el += 2) {
       const int64_t e = (int64_t)b + c0 + el;
       const float qk = qk_dot(qs, A.k + ((size_t)ce.j[el] * kH + h) * kD);
-      a_s[el][h] = A.gi[e * (2 * kH) + h] * qk;
+      a_s[el][h] = ntload(A.gi + e * (2 * kH) + h) * qk;
     }
     __syncthreads();
     if (t < kH) {
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
         const float ex = expf(a_s[el][h] - m_new);
         const float ee = ex * ce.p[el];
         s_run += ee;
-        const float ih = A.gi[e * (2 * kH) + kH + h];
+        const float ih = ntload(A.gi + e * (2 * kH) + kH + h);
         coef_s[el][h] = (ee * ih) / ce.R[el];
       }
       m_run = m_new;
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
   float* op = out + (size_t)i * kC + t;
   const size_t os = (size_t)A.n_rows * kC;
 #pragma unroll
-  for (int q = 0; q < kNT; ++q) op[q * os] = o[q] * inv;
+  for (int q = 0; q < kNT; ++q) ntstore(o[q] * inv, op + q * os);
 }
 
 // dA[r][k] = sum_t T[t][r][k] g[t] for one channel
@@ -382,8 +382,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const fl
     for (int idx = t; idx < nc * kH; idx += 256) {
       const int el = idx >> 7, h = idx & (kH - 1);
       const int64_t e = A.key_eid[c0 + el];
-      cw[el][h] = w_e[e * kH + h];
-      cq[el][h] = dqk_e[e * kH + h];
+      cw[el][h] = ntload(w_e + e * kH + h);
+      cq[el][h] = ntload(dqk_e + e * kH + h);
     }
     __syncthreads();
     int el = 0;
@@ -441,9 +441,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const fl
     __syncthreads();
   }
 #pragma unroll
-  for (int r = 0; r < kNV; ++r) dv_out[(size_t)j * kC + r * os + c] = av[r];
+  for (int r = 0; r < kNV; ++r) ntstore(av[r], dv_out + (size_t)j * kC + r * os + c);
 #pragma unroll
-  for (int d = 0; d < 4; ++d) dk_out[((size_t)j * kH + hk) * kD + d0 + d] = ak[d];
+  for (int d = 0; d < 4; ++d) ntstore(ak[d], dk_out + ((size_t)j * kH + hk) * kD + d0 + d);
 }
 
 }  // namespace e2v2

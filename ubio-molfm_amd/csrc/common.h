@@ -77,8 +77,29 @@ __device__ __forceinline__ int xcd_row(int b, int n) {
   return (b % kXcd) * per + b / kXcd;
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// Streaming (non-temporal) global accesses for data touched once per kernel:
+// per-edge weights, row gradients, outputs.  They are marked for early L2
+// eviction so the 4 MB L2 of each XCD keeps the neighbour features that
+// many rows gather.
+template <typename T>
+__device__ __forceinline__ T ntload(const T* p) { return __builtin_nontemporal_load(p); }
+template <typename T>
+__device__ __forceinline__ void ntstore(T v, T* p) { __builtin_nontemporal_store(v, p); }
+
+// Native transcendental instructions (v_exp_f32 = 2^x, v_rcp_f32, v_rsq_f32),
+// one VALU op each and accurate to about 1 ulp, in place of the libm
+// sequences (range reduction, IEEE division) that dominate the VALU budget of
+// the per-edge MLP epilogues.  exp(x) = 2^(x log2 e): the rounding of the
+// product adds |x| * 6e-8 relative error, below fp32 rounding of the inputs
+// for the |x| < 20 that carry weight here.
+constexpr float kLog2e = 1.4426950408889634f;
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float frsq(float x) { return __builtin_amdgcn_rsqf(x); }
+
+__device__ __forceinline__ float sigmoidf_(float x) { return frcp(1.0f + fexp(-x)); }
+__device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
 
 // polynomial envelope (exponent 5): p = 1 + r^5 (a + r (b + c r)), 0 for r >= 1
 struct Envelope {

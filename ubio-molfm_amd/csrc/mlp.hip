@@ -4,9 +4,17 @@
 //
 // The first Linear is split: W1 [rbf | tgt | src] x = W1r rbf + (W1t tgt[z_i] + b1)
 // + W1s src[z_j]; the two type terms arrive as per-type tables.  The RBF tile
-// lives in LDS only; the MLP runs as fp32 MFMA 16x16x4 GEMMs on 32-edge tiles.
-// The forward saves the normalised LayerNorm inputs (n1, n2) and their rstd;
-// the backward uses them (no recompute) and returns only dL/d(distance).
+// lives in LDS only; the MLP runs as MFMA GEMMs on 32-edge tiles (fp32
+// 16x16x4, or bf16 16x16x32 operands with fp32 accumulation).  The forward saves
+// the normalised LayerNorm inputs (n1, n2) and their rstd; the backward uses
+// them (no recompute) and returns only dL/d(distance).
+//
+// Latency structure: each tile is a chain of three GEMMs separated by
+// LayerNorms, so every global access on that chain is issued a stage ahead of
+// its use.  LayerNorm affine parameters live in LDS for the whole block; the
+// bf16 kernels load a GEMM's entire per-wave B panel into registers while the
+// previous stage computes; the backward prefetches the saved LayerNorm inputs
+// before the GEMM whose output they normalise.
 #include "common.h"
 #include "../../include/e2v2.h"
 
@@ -15,14 +23,21 @@ namespace e2v2 {
 constexpr int kT = 32;          // edges per tile
 constexpr int kK0 = 256;        // rbf basis
 constexpr int kH = 128;         // hidden width
-constexpr int kLdX = 258;       // LDS row stride for K=256 tiles (== 2 mod 32: conflict-free A reads)
-constexpr int kLdY = 130;       // LDS row stride for K=128 tiles (== 2 mod 32)
-constexpr int kPF = 8;          // k-steps (of 4) per register-prefetched B chunk
+constexpr int kLdX = 258;       // fp32 LDS row stride for K=256 tiles (== 2 mod 32: conflict-free A reads)
+constexpr int kLdY = 130;       // fp32 LDS row stride for K=128 tiles (== 2 mod 32)
+constexpr int kLdXb = 264;      // bf16 row stride of K=256 tiles (16-byte aligned rows)
+constexpr int kLdYb = 136;      // bf16 row stride of K=128 tiles
+constexpr int kPF = 8;          // fp32 GEMM: k-steps (of 4) per register-prefetched B chunk
+constexpr float kFarDist = 1e18f;  // distance of padding rows: finite, and its RBF row is exactly 0
 
-// C[32][N] = A[32][K] (LDS, row stride lda) x B[K][N] (global, row stride ldb).
-// Wave w owns columns [w*N/4, (w+1)*N/4).  acc[rt][ct] holds the 16x16 tile
-// (rows rt*16.., cols w*N/4 + ct*16..); lane l holds rows 4*(l/16)+r, col l%16.
-// B is streamed in chunks of 32 k-rows held in registers one chunk ahead.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------
+// fp32 GEMM: C[32][N] = A[32][K] (LDS, row stride lda) x B[K][N] (global, row
+// stride ldb).  Wave w owns columns [w*N/4, (w+1)*N/4).  acc[rt][ct] holds the
+// 16x16 tile (rows rt*16.., cols w*N/4 + ct*16..); lane l holds rows
+// 4*(l/16)+r, col l%16.  B is streamed in chunks of 32 k-rows held in
+// registers one chunk ahead (the fp32 MFMA time per chunk covers the load).
 template <int K, int N>
 __device__ __forceinline__ void gemm32(const float* A, int lda, const float* __restrict__ B, int ldb,
                                        floatx4 (&acc)[2][N / 64]) {
@@ -70,36 +85,101 @@ __device__ __forceinline__ void gemm32(const float* A, int lda, const float* __r
   }
 }
 
-template <int N>
-__device__ __forceinline__ void acc_coord(int rt, int ct, int r, int& row, int& c) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  row = rt * 16 + 4 * (lane >> 4) + r;
-  c = wave * (N / 4) + ct * 16 + (lane & 15);
+// ---------------------------------------------------------------------------
+// bf16 GEMM on a register-resident B panel.  Bt is B^T row-major [N][K]; the
+// panel holds this wave's N/4 columns for all K (lane l: column l%16 of each
+// 16-column group, k values 8*(l/16)..+7 of each 32-k step), i.e. K/8 * N/64
+// VGPRs: 64 for K=256,N=128 or K=128,N=256.
+template <int K, int N>
+struct Panel {
+  bf16x8 v[K / 32][N / 64];
+};
+
+template <int K, int N>
+__device__ __forceinline__ void load_panel(Panel<K, N>& P, const __bf16* __restrict__ Bt) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const __bf16* p = Bt + (size_t)(wave * (N / 4) + (lane & 15)) * K + 8 * (lane >> 4);
+#pragma unroll
+  for (int ks = 0; ks < K / 32; ++ks)
+#pragma unroll
+    for (int ct = 0; ct < N / 64; ++ct)
+      P.v[ks][ct] = *reinterpret_cast<const bf16x8*>(p + (size_t)ct * 16 * K + ks * 32);
 }
 
-template <int N>
-__device__ __forceinline__ void store_acc(const floatx4 (&acc)[2][N / 64], float* Y, int ldy,
-                                          const float* __restrict__ bias) {
+template <int K, int N>
+__device__ __forceinline__ void gemm_panel(const __bf16* A, int lda, const Panel<K, N>& P,
+                                           floatx4 (&acc)[2][N / 64]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < N / 64; ++ct)
+    for (int ct = 0; ct < N / 64; ++ct) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int row, c;
-        acc_coord<N>(rt, ct, r, row, c);
-        Y[row * ldy + c] = acc[rt][ct][r] + (bias ? bias[c] : 0.f);
-      }
+  for (int ks = 0; ks < K / 32; ++ks) {
+    const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(A + li * lda + ks * 32 + 8 * lg);
+    const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(A + (16 + li) * lda + ks * 32 + 8 * lg);
+#pragma unroll
+    for (int ct = 0; ct < N / 64; ++ct) {
+      acc[0][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, P.v[ks][ct], acc[0][ct], 0, 0, 0);
+      acc[1][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, P.v[ks][ct], acc[1][ct], 0, 0, 0);
+    }
+  }
 }
 
-// Row-wise LayerNorm(128) + SiLU on Y (in place), 8 threads per row.  Rows
-// below nsave also store the normalised (pre-affine) values and rstd.
-__device__ __forceinline__ void ln_silu_rows(float* Y, int ldy, const float* __restrict__ g,
-                                             const float* __restrict__ b, float* nrm, int ldn, float* rstd_out,
-                                             int rstd_stride, int nsave) {
+// ---------------------------------------------------------------------------
+// Accumulator tile <-> LDS / global.  Lane l of wave w holds rows
+// rt*16 + 4*(l/16) + r and columns w*N/4 + ct*16 + l%16.
+__device__ __forceinline__ int acc_row(int rt, int r) { return rt * 16 + 4 * ((threadIdx.x & 63) >> 4) + r; }
+template <int N>
+__device__ __forceinline__ int acc_col0() { return (threadIdx.x >> 6) * (N / 4) + (threadIdx.x & 15); }
+
+template <int N>
+__device__ __forceinline__ void store_acc(const floatx4 (&acc)[2][N / 64], float* Y, int ldy,
+                                          const float (&bias)[N / 64]) {
+  const int c0 = acc_col0<N>();
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* y = Y + acc_row(rt, r) * ldy + c0;
+#pragma unroll
+      for (int ct = 0; ct < N / 64; ++ct) y[ct * 16] = acc[rt][ct][r] + bias[ct];
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void load_bias(const float* __restrict__ b, float (&bias)[N / 64]) {
+  const int c0 = acc_col0<N>();
+#pragma unroll
+  for (int ct = 0; ct < N / 64; ++ct) bias[ct] = b ? b[c0 + ct * 16] : 0.f;
+}
+
+// LayerNorm affine parameters of one profile, staged in LDS for the block
+struct LnParams {
+  float g1[kH], b1[kH], g2[kH], b2[kH];
+};
+
+__device__ __forceinline__ void load_ln_params(const e2v2_mlp_weights& W, LnParams& p) {
+  const int t = threadIdx.x;
+  if (t < kH) {
+    p.g1[t] = W.g1[t];
+    p.b1[t] = W.be1[t];
+  } else {
+    p.g2[t - kH] = W.g2[t - kH];
+    p.b2[t - kH] = W.be2[t - kH];
+  }
+}
+
+// Row-wise LayerNorm(128) + SiLU of the fp32 rows of Y (8 threads per row),
+// written to the next GEMM's A operand (fp32 in place, or bf16).  Rows below
+// nsave also store the normalised (pre-affine) values and rstd.
+template <typename OutT>
+__device__ __forceinline__ void ln_silu_rows(const float* Y, int ldy, OutT* Z, int ldz, const float* g,
+                                             const float* b, float* __restrict__ nrm, int ldn,
+                                             float* __restrict__ rstd_out, int rstd_stride, int nsave) {
   const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
-  float* y = Y + row * ldy;
+  const float* y = Y + row * ldy;
   float v[16];
   float s = 0.f;
 #pragma unroll
@@ -114,58 +194,71 @@ __device__ __forceinline__ void ln_silu_rows(float* Y, int ldy, const float* __r
   float s2 = 0.f;
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
-    float dlt = v[q] - mean;
+    const float dlt = v[q] - mean;
     s2 += dlt * dlt;
   }
   s2 += __shfl_xor(s2, 1, 64);
   s2 += __shfl_xor(s2, 2, 64);
   s2 += __shfl_xor(s2, 4, 64);
-  const float rstd = 1.0f / sqrtf(s2 * (1.0f / kH) + 1e-5f);
+  const float rstd = frsq(s2 * (1.0f / kH) + 1e-5f);
   const bool save = nrm != nullptr && row < nsave;
+  OutT* z = Z + row * ldz;
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int c = sub + 8 * q;
-    float n = (v[q] - mean) * rstd;
+    const float n = (v[q] - mean) * rstd;
     if (save) nrm[(size_t)row * ldn + c] = n;
-    float a = n * g[c] + b[c];
-    y[c] = silu(a);
+    z[c] = (OutT)silu(n * g[c] + b[c]);
   }
   if (save && sub == 0) rstd_out[(size_t)row * rstd_stride] = rstd;
 }
 
-// dz = LN-backward(SiLU-backward(dy)) given the saved normalised input and rstd (global).
-__device__ __forceinline__ void ln_silu_bwd_rows(float* Y, int ldy, const float* __restrict__ nrm, int ldn,
-                                                 const float* __restrict__ rstd, int rstd_stride, int nvalid,
-                                                 const float* __restrict__ g, const float* __restrict__ b) {
+// Saved LayerNorm input of this thread's row (8 threads per row, 16 columns each)
+struct SavedRow {
+  float n[16];
+  float rstd;
+};
+
+__device__ __forceinline__ void load_saved_row(const float* __restrict__ nrm, int ldn,
+                                               const float* __restrict__ rstd, int rstd_stride, int nvalid,
+                                               SavedRow& sr) {
   const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
-  float* y = Y + row * ldy;
   const bool ok = row < nvalid;
-  float dn[16], nn[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) sr.n[q] = ok ? nrm[(size_t)row * ldn + sub + 8 * q] : 0.f;
+  sr.rstd = ok ? rstd[(size_t)row * rstd_stride] : 0.f;
+}
+
+// dz = LN-backward(SiLU-backward(dy)) of the fp32 rows of Y, written to Z
+template <typename OutT>
+__device__ __forceinline__ void ln_silu_bwd_rows(const float* Y, int ldy, OutT* Z, int ldz, const SavedRow& sr,
+                                                 const float* g, const float* b) {
+  const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
+  const float* y = Y + row * ldy;
+  float dn[16];
   float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int c = sub + 8 * q;
-    float n = ok ? nrm[(size_t)row * ldn + c] : 0.f;
-    float a = n * g[c] + b[c];
-    float sg = sigmoidf_(a);
-    float da = y[c] * sg * (1.0f + a * (1.0f - sg));
+    const float a = sr.n[q] * g[c] + b[c];
+    const float sg = sigmoidf_(a);
+    const float da = y[c] * sg * (1.0f + a * (1.0f - sg));
     dn[q] = da * g[c];
-    nn[q] = n;
     s1 += dn[q];
-    s2 += dn[q] * n;
+    s2 += dn[q] * sr.n[q];
   }
   s1 += __shfl_xor(s1, 1, 64); s1 += __shfl_xor(s1, 2, 64); s1 += __shfl_xor(s1, 4, 64);
   s2 += __shfl_xor(s2, 1, 64); s2 += __shfl_xor(s2, 2, 64); s2 += __shfl_xor(s2, 4, 64);
   const float m1 = s1 * (1.0f / kH), m2 = s2 * (1.0f / kH);
-  const float r = ok ? rstd[(size_t)row * rstd_stride] : 0.f;
+  OutT* z = Z + row * ldz;
 #pragma unroll
-  for (int q = 0; q < 16; ++q) y[sub + 8 * q] = r * (dn[q] - m1 - nn[q] * m2);
+  for (int q = 0; q < 16; ++q) z[sub + 8 * q] = (OutT)(sr.rstd * (dn[q] - m1 - sr.n[q] * m2));
 }
 
+// ---------------------------------------------------------------------------
 struct TileEdges {
-  float d[kT];
+  alignas(16) float d[kT];   // padding rows hold kFarDist
   int zi[kT], zj[kT];
-  int valid[kT];
 };
 
 __device__ __forceinline__ void load_tile_edges(const e2v2_mlp_args& A, int64_t e0, TileEdges& te) {
@@ -173,141 +266,97 @@ __device__ __forceinline__ void load_tile_edges(const e2v2_mlp_args& A, int64_t 
   if (t < kT) {
     const int64_t e = e0 + t;
     const bool v = e < A.n_edges;
-    te.valid[t] = v;
-    te.d[t] = v ? A.dist[e] : 0.f;
+    te.d[t] = v ? A.dist[e] : kFarDist;
     te.zi[t] = v ? A.node_type[A.edge_row[e]] : 0;
     te.zj[t] = v ? A.node_type[A.col[e]] : 0;
   }
 }
 
 // rbf tile: X[r][k] = exp(coeff * (d_r - mu_k)^2); thread t owns basis k = t
-__device__ __forceinline__ void rbf_tile(const e2v2_mlp_args& A, const TileEdges& te, float* X) {
+template <typename T>
+__device__ __forceinline__ void rbf_tile(const TileEdges& te, float mu, float c2, T* X, int ldx) {
   const int k = threadIdx.x;
-  const float mu = A.rbf_offset[k];
-#pragma unroll 4
-  for (int r = 0; r < kT; ++r) {
-    float x = te.d[r] - mu;
-    X[r * kLdX + k] = te.valid[r] ? expf(A.rbf_coeff * (x * x)) : 0.f;
+#pragma unroll
+  for (int r4 = 0; r4 < kT / 4; ++r4) {
+    const float4 d4 = reinterpret_cast<const float4*>(te.d)[r4];
+    const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = dv[i] - mu;
+      X[(4 * r4 + i) * ldx + k] = (T)fexp2(c2 * (x * x));
+    }
   }
 }
 
-__global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
-  extern __shared__ float sm[];
-  float* X = sm;                    // [32][258]: rbf tile, then h2 / y2 with stride kLdY
-  float* Y = X + kT * kLdX;         // [32][130]
-  __shared__ TileEdges te;
-  const int m = blockIdx.y;
-  const e2v2_mlp_weights& W = A.w[m];
-  const int64_t e0 = (int64_t)blockIdx.x * kT;
-  const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
-  float* sn = A.save_n ? A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH) : nullptr;
-  float* sr = A.save_r ? A.save_r + ((size_t)m * A.n_edges + e0) * 2 : nullptr;
-  load_tile_edges(A, e0, te);
-  __syncthreads();
-  rbf_tile(A, te, X);
-  __syncthreads();
-  {
-    floatx4 acc[2][2];
-    gemm32<kK0, kH>(X, kLdX, W.w1t, kH, acc);
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          int row, c;
-          acc_coord<kH>(rt, ct, r, row, c);
-          Y[row * kLdY + c] = acc[rt][ct][r] + W.ttgt[te.zi[row] * kH + c] + W.tsrc[te.zj[row] * kH + c];
-        }
-  }
-  __syncthreads();
-  ln_silu_rows(Y, kLdY, W.g1, W.be1, sn, 2 * kH, sr, 2, nvalid);
-  __syncthreads();
-  {
-    floatx4 acc[2][2];
-    gemm32<kH, kH>(Y, kLdY, W.w2t, kH, acc);
-    store_acc<kH>(acc, X, kLdY, W.b2);
-  }
-  __syncthreads();
-  ln_silu_rows(X, kLdY, W.g2, W.be2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2, nvalid);
-  __syncthreads();
-  floatx4 acc[2][4];
-  gemm32<kH, 256>(X, kLdY, W.w3t, 256, acc);
+// Per-type table values of GEMM 1's epilogue, loaded ahead of the GEMM
+struct TypeTerms {
+  float t[2][4][2];
+};
+
+__device__ __forceinline__ void load_type_terms(const float* __restrict__ ttgt, const float* __restrict__ tsrc,
+                                                const TileEdges& te, TypeTerms& tt) {
+  const int c0 = acc_col0<kH>();
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
+    for (int r = 0; r < 4; ++r) {
+      const int row = acc_row(rt, r);
+      const float* pt = ttgt + te.zi[row] * kH + c0;
+      const float* ps = tsrc + te.zj[row] * kH + c0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int row, c;
-        acc_coord<256>(rt, ct, r, row, c);
-        if (row < nvalid) out[(e0 + row) * ld_out + m * 256 + c] = acc[rt][ct][r] + W.b3[c];
+      for (int ct = 0; ct < 2; ++ct) tt.t[rt][r][ct] = pt[ct * 16] + ps[ct * 16];
+    }
+}
+
+__device__ __forceinline__ void store_gemm1(const floatx4 (&acc)[2][2], const TypeTerms& tt, float* Y, int ldy) {
+  const int c0 = acc_col0<kH>();
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* y = Y + acc_row(rt, r) * ldy + c0;
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) y[ct * 16] = acc[rt][ct][r] + tt.t[rt][r][ct];
+    }
+}
+
+// GEMM-3 epilogue: out[e0 + row][m * 256 + c] = acc + b3[c] for the valid rows
+__device__ __forceinline__ void store_out(const floatx4 (&acc)[2][4], const float (&b3)[4], float* __restrict__ out,
+                                          int ld_out, int64_t e0, int nvalid, int m) {
+  const int c0 = acc_col0<256>();
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = acc_row(rt, r);
+      if (row < nvalid) {
+        float* o = out + (e0 + row) * (int64_t)ld_out + m * 256 + c0;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) o[ct * 16] = acc[rt][ct][r] + b3[ct];
       }
+    }
 }
 
-__global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
-                                                 float* __restrict__ dd, int accumulate) {
-  extern __shared__ float sm[];
-  float* X = sm;                    // [32][258]
-  float* Y = X + kT * kLdX;         // [32][130]
-  __shared__ TileEdges te;
-  __shared__ float part[4][kT];
-  const int64_t e0 = (int64_t)blockIdx.x * kT;
-  const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  load_tile_edges(A, e0, te);
-  __syncthreads();
-  float dd_lane[2][4];
+// dd += sum_c drbf[row][c] * d rbf_c / dd over this lane's 4 basis columns
+__device__ __forceinline__ void accumulate_dd(const floatx4 (&acc)[2][4], const TileEdges& te, const float (&mu)[4],
+                                              float c2, float coeff2, float (&dd_lane)[2][4]) {
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) dd_lane[rt][r] = 0.f;
-  for (int m = 0; m < A.n_mlp; ++m) {
-    const e2v2_mlp_weights& W = A.w[m];
-    const float* sn = A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH);
-    const float* sr = A.save_r + ((size_t)m * A.n_edges + e0) * 2;
-    for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {   // dOut tile, float4 loads
-      const int row = idx >> 6, c4 = idx & 63;
-      float4 v = row < nvalid ? reinterpret_cast<const float4*>(dout + (e0 + row) * ld_dout + m * 256)[c4]
-                              : float4{0.f, 0.f, 0.f, 0.f};
-      float* xr = X + row * kLdX + 4 * c4;
-      xr[0] = v.x; xr[1] = v.y; xr[2] = v.z; xr[3] = v.w;
-    }
-    __syncthreads();
-    {  // dy2 = dOut . W3   (W3 [256][128] row-major = B[K=256][N=128])
-      floatx4 acc[2][2];
-      gemm32<256, kH>(X, kLdX, W.w3, kH, acc);
-      store_acc<kH>(acc, Y, kLdY, nullptr);
-    }
-    __syncthreads();
-    ln_silu_bwd_rows(Y, kLdY, sn + kH, 2 * kH, sr + 1, 2, nvalid, W.g2, W.be2);
-    __syncthreads();
-    {  // dy1 = dz2 . W2   (W2 [128][128]) -> X with stride kLdY
-      floatx4 acc[2][2];
-      gemm32<kH, kH>(Y, kLdY, W.w2, kH, acc);
-      store_acc<kH>(acc, X, kLdY, nullptr);
-    }
-    __syncthreads();
-    ln_silu_bwd_rows(X, kLdY, sn, 2 * kH, sr, 2, nvalid, W.g1, W.be1);
-    __syncthreads();
-    {  // drbf = dz1 . W1r  (W1 [128][ldw1], rbf columns 0..255); dd += sum_k drbf * rbf * 2c(d - mu)
-      floatx4 acc[2][4];
-      gemm32<kH, 256>(X, kLdY, W.w1, W.ldw1, acc);
+    for (int r = 0; r < 4; ++r) {
+      const float d = te.d[acc_row(rt, r)];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            int row, c;
-            acc_coord<256>(rt, ct, r, row, c);
-            float x = te.d[row] - A.rbf_offset[c];
-            float rb = expf(A.rbf_coeff * (x * x));
-            dd_lane[rt][r] += acc[rt][ct][r] * rb * (2.0f * A.rbf_coeff * x);
-          }
+      for (int ct = 0; ct < 4; ++ct) {
+        const float x = d - mu[ct];
+        dd_lane[rt][r] += acc[rt][ct][r] * fexp2(c2 * (x * x)) * (coeff2 * x);
+      }
     }
-    __syncthreads();
-  }
+}
+
+// Row sums of dd_lane over the block's 4 waves and 16 lanes -> dd[e0 + row]
+__device__ __forceinline__ void reduce_dd(float (&dd_lane)[2][4], float (*part)[kT], float* __restrict__ dd,
+                                          int64_t e0, int nvalid, int accumulate) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
@@ -317,192 +366,180 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
       v += __shfl_xor(v, 2, 64);
       v += __shfl_xor(v, 4, 64);
       v += __shfl_xor(v, 8, 64);
-      if ((lane & 15) == 0) part[wave][rt * 16 + 4 * (lane >> 4) + r] = v;
+      if ((lane & 15) == 0) part[wave][acc_row(rt, r)] = v;
     }
   __syncthreads();
   if (threadIdx.x < nvalid) {
-    float v = part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] + part[3][threadIdx.x];
-    int64_t e = e0 + threadIdx.x;
+    const float v = part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] + part[3][threadIdx.x];
+    const int64_t e = e0 + threadIdx.x;
     dd[e] = accumulate ? dd[e] + v : v;
   }
 }
 
-
 // ---------------------------------------------------------------------------
-// bf16-operand variant (weights in bf16, fp32 accumulation): GEMMs on
-// v_mfma_f32_16x16x32_bf16; LayerNorm, SiLU, tables, saved statistics and all
-// outputs stay fp32.  B operands come as B^T row-major [N][K] in bf16 so each
-// lane loads its 8 consecutive k values with one 16-byte load.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-constexpr int kLdXb = 264;   // bf16 row stride of K=256 tiles (multiple of 8)
-constexpr int kLdYb = 136;   // bf16 row stride of K=128 tiles
+// fp32 kernels
+__global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
+  extern __shared__ float sm[];
+  float* X = sm;                    // [32][258]: rbf tile, then h2 / y2 with stride kLdY
+  float* Y = X + kT * kLdX;         // [32][130]
+  __shared__ TileEdges te;
+  __shared__ LnParams lp;
+  const int m = blockIdx.y;
+  const e2v2_mlp_weights& W = A.w[m];
+  const int64_t e0 = (int64_t)blockIdx.x * kT;
+  const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
+  float* sn = A.save_n ? A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH) : nullptr;
+  float* sr = A.save_r ? A.save_r + ((size_t)m * A.n_edges + e0) * 2 : nullptr;
+  const float mu = A.rbf_offset[threadIdx.x];
+  float b2[2], b3[4];
+  load_bias<kH>(W.b2, b2);
+  load_bias<256>(W.b3, b3);
+  load_tile_edges(A, e0, te);
+  load_ln_params(W, lp);
+  __syncthreads();
+  TypeTerms tt;
+  load_type_terms(W.ttgt, W.tsrc, te, tt);
+  rbf_tile(te, mu, A.rbf_coeff * kLog2e, X, kLdX);
+  __syncthreads();
+  {
+    floatx4 acc[2][2];
+    gemm32<kK0, kH>(X, kLdX, W.w1t, kH, acc);
+    store_gemm1(acc, tt, Y, kLdY);
+  }
+  __syncthreads();
+  ln_silu_rows(Y, kLdY, Y, kLdY, lp.g1, lp.b1, sn, 2 * kH, sr, 2, nvalid);
+  __syncthreads();
+  {
+    floatx4 acc[2][2];
+    gemm32<kH, kH>(Y, kLdY, W.w2t, kH, acc);
+    store_acc<kH>(acc, X, kLdY, b2);
+  }
+  __syncthreads();
+  ln_silu_rows(X, kLdY, X, kLdY, lp.g2, lp.b2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2, nvalid);
+  __syncthreads();
+  floatx4 acc[2][4];
+  gemm32<kH, 256>(X, kLdY, W.w3t, 256, acc);
+  store_out(acc, b3, out, ld_out, e0, nvalid, m);
+}
 
-template <int K, int N>
-__device__ __forceinline__ void gemm32_bf16(const __bf16* A, int lda, const __bf16* __restrict__ Bt, int ldb,
-                                            floatx4 (&acc)[2][N / 64]) {
-  constexpr int CT = N / 64;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int li = lane & 15, lg = lane >> 4;
-  const int cbase = wave * (N / 4);
+__global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
+                                                 float* __restrict__ dd, int accumulate) {
+  extern __shared__ float sm[];
+  float* X = sm;                    // [32][258]
+  float* Y = X + kT * kLdX;         // [32][130]
+  __shared__ TileEdges te;
+  __shared__ LnParams lp;
+  __shared__ float part[4][kT];
+  const int64_t e0 = (int64_t)blockIdx.x * kT;
+  const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
+  const float c2 = A.rbf_coeff * kLog2e, coeff2 = 2.0f * A.rbf_coeff;
+  float mu[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) mu[ct] = A.rbf_offset[acc_col0<256>() + ct * 16];
+  const float zero2[2] = {0.f, 0.f};
+  load_tile_edges(A, e0, te);
+  float dd_lane[2][4];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
-  bf16x8 bc[CT], bn[CT];
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct)
-    bc[ct] = *reinterpret_cast<const bf16x8*>(Bt + (size_t)(cbase + ct * 16 + li) * ldb + 8 * lg);
-#pragma unroll
-  for (int k0 = 0; k0 < K; k0 += 32) {
-    if (k0 + 32 < K) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-        bn[ct] = *reinterpret_cast<const bf16x8*>(Bt + (size_t)(cbase + ct * 16 + li) * ldb + k0 + 32 + 8 * lg);
+    for (int r = 0; r < 4; ++r) dd_lane[rt][r] = 0.f;
+  for (int m = 0; m < A.n_mlp; ++m) {
+    const e2v2_mlp_weights& W = A.w[m];
+    const float* sn = A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH);
+    const float* srs = A.save_r + ((size_t)m * A.n_edges + e0) * 2;
+    load_ln_params(W, lp);
+    for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {   // dOut tile, float4 loads
+      const int row = idx >> 6, c4 = idx & 63;
+      const floatx4 v = row < nvalid ? reinterpret_cast<const floatx4*>(dout + (e0 + row) * ld_dout + m * 256)[c4]
+                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+      float* xr = X + row * kLdX + 4 * c4;
+      xr[0] = v[0]; xr[1] = v[1]; xr[2] = v[2]; xr[3] = v[3];
     }
-    const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(A + li * lda + k0 + 8 * lg);
-    const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(A + (16 + li) * lda + k0 + 8 * lg);
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      acc[0][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bc[ct], acc[0][ct], 0, 0, 0);
-      acc[1][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bc[ct], acc[1][ct], 0, 0, 0);
+    SavedRow s2;
+    load_saved_row(sn + kH, 2 * kH, srs + 1, 2, nvalid, s2);
+    __syncthreads();
+    {  // dy2 = dOut . W3   (W3 [256][128] row-major = B[K=256][N=128])
+      floatx4 acc[2][2];
+      gemm32<256, kH>(X, kLdX, W.w3, kH, acc);
+      store_acc<kH>(acc, Y, kLdY, zero2);
     }
-    if (k0 + 32 < K) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) bc[ct] = bn[ct];
+    SavedRow s1;
+    load_saved_row(sn, 2 * kH, srs, 2, nvalid, s1);
+    __syncthreads();
+    ln_silu_bwd_rows(Y, kLdY, Y, kLdY, s2, lp.g2, lp.b2);
+    __syncthreads();
+    {  // dy1 = dz2 . W2   (W2 [128][128]) -> X with stride kLdY
+      floatx4 acc[2][2];
+      gemm32<kH, kH>(Y, kLdY, W.w2, kH, acc);
+      store_acc<kH>(acc, X, kLdY, zero2);
     }
+    __syncthreads();
+    ln_silu_bwd_rows(X, kLdY, X, kLdY, s1, lp.g1, lp.b1);
+    __syncthreads();
+    {  // drbf = dz1 . W1r  (W1 [128][ldw1], rbf columns 0..255)
+      floatx4 acc[2][4];
+      gemm32<kH, 256>(X, kLdY, W.w1, W.ldw1, acc);
+      accumulate_dd(acc, te, mu, c2, coeff2, dd_lane);
+    }
+    __syncthreads();
   }
+  reduce_dd(dd_lane, part, dd, e0, nvalid, accumulate);
 }
 
-// LayerNorm(128) + SiLU of the fp32 rows in Yf; writes the bf16 activation to Yb
-__device__ __forceinline__ void ln_silu_rows_bf16(const float* Yf, int ldf, __bf16* Yb, int ldb,
-                                                  const float* __restrict__ g, const float* __restrict__ b,
-                                                  float* nrm, int ldn, float* rstd_out, int rstd_stride, int nsave) {
-  const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
-  const float* y = Yf + row * ldf;
-  float v[16];
-  float s = 0.f;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) { v[q] = y[sub + 8 * q]; s += v[q]; }
-  s += __shfl_xor(s, 1, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 4, 64);
-  const float mean = s * (1.0f / kH);
-  float s2 = 0.f;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) { float dl = v[q] - mean; s2 += dl * dl; }
-  s2 += __shfl_xor(s2, 1, 64); s2 += __shfl_xor(s2, 2, 64); s2 += __shfl_xor(s2, 4, 64);
-  const float rstd = 1.0f / sqrtf(s2 * (1.0f / kH) + 1e-5f);
-  const bool save = nrm != nullptr && row < nsave;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int c = sub + 8 * q;
-    const float n = (v[q] - mean) * rstd;
-    if (save) nrm[(size_t)row * ldn + c] = n;
-    Yb[row * ldb + c] = (__bf16)silu(n * g[c] + b[c]);
-  }
-  if (save && sub == 0) rstd_out[(size_t)row * rstd_stride] = rstd;
-}
-
-// SiLU/LN backward on fp32 rows of Yf -> bf16 rows of Yb
-__device__ __forceinline__ void ln_silu_bwd_rows_bf16(const float* Yf, int ldf, __bf16* Yb, int ldb,
-                                                      const float* __restrict__ nrm, int ldn,
-                                                      const float* __restrict__ rstd, int rstd_stride, int nvalid,
-                                                      const float* __restrict__ g, const float* __restrict__ b) {
-  const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
-  const float* y = Yf + row * ldf;
-  const bool ok = row < nvalid;
-  float dn[16], nn[16];
-  float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int c = sub + 8 * q;
-    const float n = ok ? nrm[(size_t)row * ldn + c] : 0.f;
-    const float a = n * g[c] + b[c];
-    const float sg = sigmoidf_(a);
-    const float da = y[c] * sg * (1.0f + a * (1.0f - sg));
-    dn[q] = da * g[c];
-    nn[q] = n;
-    s1 += dn[q];
-    s2 += dn[q] * n;
-  }
-  s1 += __shfl_xor(s1, 1, 64); s1 += __shfl_xor(s1, 2, 64); s1 += __shfl_xor(s1, 4, 64);
-  s2 += __shfl_xor(s2, 1, 64); s2 += __shfl_xor(s2, 2, 64); s2 += __shfl_xor(s2, 4, 64);
-  const float m1 = s1 * (1.0f / kH), m2 = s2 * (1.0f / kH);
-  const float r = ok ? rstd[(size_t)row * rstd_stride] : 0.f;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) Yb[row * ldb + sub + 8 * q] = (__bf16)(r * (dn[q] - m1 - nn[q] * m2));
-}
-
-template <int N>
-__device__ __forceinline__ void store_acc_f32(const floatx4 (&acc)[2][N / 64], float* Y, int ldy,
-                                              const float* __restrict__ bias) {
-  store_acc<N>(acc, Y, ldy, bias);
-}
-
+// ---------------------------------------------------------------------------
+// bf16-operand kernels (fp32 accumulation; LayerNorm, SiLU, tables, saved
+// statistics and all outputs stay fp32).  B panels come as B^T row-major
+// [N][K] in bf16.
 __global__ __launch_bounds__(256) void k_mlp_fwd_bf16(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
   extern __shared__ float sm[];
   __bf16* Xb = reinterpret_cast<__bf16*>(sm);                 // [32][264] bf16
   float* Yf = sm + (kT * kLdXb) / 2;                           // [32][130] fp32
   __bf16* Yb = reinterpret_cast<__bf16*>(Yf + kT * kLdY);      // [32][136] bf16
   __shared__ TileEdges te;
+  __shared__ LnParams lp;
   const int m = blockIdx.y;
   const e2v2_mlp_weights& W = A.w[m];
-  const __bf16* w1b = static_cast<const __bf16*>(W.w1b);
-  const __bf16* w2b = static_cast<const __bf16*>(W.w2b);
-  const __bf16* w3b = static_cast<const __bf16*>(W.w3b);
   const int64_t e0 = (int64_t)blockIdx.x * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   float* sn = A.save_n ? A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH) : nullptr;
   float* sr = A.save_r ? A.save_r + ((size_t)m * A.n_edges + e0) * 2 : nullptr;
+  Panel<kK0, kH> P1;
+  load_panel(P1, static_cast<const __bf16*>(W.w1b));
+  const float mu = A.rbf_offset[threadIdx.x];
+  float b2[2], b3[4];
+  load_bias<kH>(W.b2, b2);
+  load_bias<256>(W.b3, b3);
   load_tile_edges(A, e0, te);
+  load_ln_params(W, lp);
   __syncthreads();
-  {
-    const int k = threadIdx.x;
-    const float mu = A.rbf_offset[k];
-#pragma unroll 4
-    for (int r = 0; r < kT; ++r) {
-      const float x = te.d[r] - mu;
-      Xb[r * kLdXb + k] = (__bf16)(te.valid[r] ? expf(A.rbf_coeff * (x * x)) : 0.f);
-    }
-  }
+  TypeTerms tt;
+  load_type_terms(W.ttgt, W.tsrc, te, tt);
+  rbf_tile(te, mu, A.rbf_coeff * kLog2e, Xb, kLdXb);
   __syncthreads();
+  Panel<kH, kH> P2;
   {
     floatx4 acc[2][2];
-    gemm32_bf16<kK0, kH>(Xb, kLdXb, w1b, kK0, acc);
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          int row, c;
-          acc_coord<kH>(rt, ct, r, row, c);
-          Yf[row * kLdY + c] = acc[rt][ct][r] + W.ttgt[te.zi[row] * kH + c] + W.tsrc[te.zj[row] * kH + c];
-        }
+    gemm_panel(Xb, kLdXb, P1, acc);
+    load_panel(P2, static_cast<const __bf16*>(W.w2b));
+    store_gemm1(acc, tt, Yf, kLdY);
   }
   __syncthreads();
-  ln_silu_rows_bf16(Yf, kLdY, Yb, kLdYb, W.g1, W.be1, sn, 2 * kH, sr, 2, nvalid);
+  ln_silu_rows(Yf, kLdY, Yb, kLdYb, lp.g1, lp.b1, sn, 2 * kH, sr, 2, nvalid);
   __syncthreads();
+  Panel<kH, 256> P3;
   {
     floatx4 acc[2][2];
-    gemm32_bf16<kH, kH>(Yb, kLdYb, w2b, kH, acc);
-    store_acc_f32<kH>(acc, Yf, kLdY, W.b2);
+    gemm_panel(Yb, kLdYb, P2, acc);
+    load_panel(P3, static_cast<const __bf16*>(W.w3b));
+    store_acc<kH>(acc, Yf, kLdY, b2);
   }
   __syncthreads();
-  ln_silu_rows_bf16(Yf, kLdY, Xb, kLdYb, W.g2, W.be2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2,
-                    nvalid);
+  ln_silu_rows(Yf, kLdY, Xb, kLdYb, lp.g2, lp.b2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2,
+               nvalid);
   __syncthreads();
   floatx4 acc[2][4];
-  gemm32_bf16<kH, 256>(Xb, kLdYb, w3b, kH, acc);
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int row, c;
-        acc_coord<256>(rt, ct, r, row, c);
-        if (row < nvalid) out[(e0 + row) * ld_out + m * 256 + c] = acc[rt][ct][r] + W.b3[c];
-      }
+  gemm_panel(Xb, kLdYb, P3, acc);
+  store_out(acc, b3, out, ld_out, e0, nvalid, m);
 }
 
 __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
@@ -512,12 +549,16 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const flo
   float* Yf = sm + (kT * kLdXb) / 2;                           // [32][130] fp32
   __bf16* Yb = reinterpret_cast<__bf16*>(Yf + kT * kLdY);      // [32][136] bf16
   __shared__ TileEdges te;
+  __shared__ LnParams lp;
   __shared__ float part[4][kT];
   const int64_t e0 = (int64_t)blockIdx.x * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float c2 = A.rbf_coeff * kLog2e, coeff2 = 2.0f * A.rbf_coeff;
+  float mu[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) mu[ct] = A.rbf_offset[acc_col0<256>() + ct * 16];
+  const float zero2[2] = {0.f, 0.f};
   load_tile_edges(A, e0, te);
-  __syncthreads();
   float dd_lane[2][4];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
@@ -525,70 +566,51 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const flo
     for (int r = 0; r < 4; ++r) dd_lane[rt][r] = 0.f;
   for (int m = 0; m < A.n_mlp; ++m) {
     const e2v2_mlp_weights& W = A.w[m];
-    const __bf16* w3tb = static_cast<const __bf16*>(W.w3tb);
-    const __bf16* w2tb = static_cast<const __bf16*>(W.w2tb);
-    const __bf16* w1rtb = static_cast<const __bf16*>(W.w1rtb);
     const float* sn = A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH);
-    const float* sr = A.save_r + ((size_t)m * A.n_edges + e0) * 2;
+    const float* srs = A.save_r + ((size_t)m * A.n_edges + e0) * 2;
+    Panel<256, kH> Pa;
+    load_panel(Pa, static_cast<const __bf16*>(W.w3tb));
+    load_ln_params(W, lp);
     for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {
       const int row = idx >> 6, c4 = idx & 63;
-      float4 v = row < nvalid ? reinterpret_cast<const float4*>(dout + (e0 + row) * ld_dout + m * 256)[c4]
-                              : float4{0.f, 0.f, 0.f, 0.f};
+      const floatx4 v = row < nvalid ? reinterpret_cast<const floatx4*>(dout + (e0 + row) * ld_dout + m * 256)[c4]
+                                     : floatx4{0.f, 0.f, 0.f, 0.f};
       __bf16* xr = Xb + row * kLdXb + 4 * c4;
-      xr[0] = (__bf16)v.x; xr[1] = (__bf16)v.y; xr[2] = (__bf16)v.z; xr[3] = (__bf16)v.w;
+      xr[0] = (__bf16)v[0]; xr[1] = (__bf16)v[1]; xr[2] = (__bf16)v[2]; xr[3] = (__bf16)v[3];
     }
+    SavedRow s2;
+    load_saved_row(sn + kH, 2 * kH, srs + 1, 2, nvalid, s2);
     __syncthreads();
+    Panel<kH, kH> Pb;
     {  // dy2 = dOut . W3   (B^T = W3^T [128][256])
       floatx4 acc[2][2];
-      gemm32_bf16<256, kH>(Xb, kLdXb, w3tb, 256, acc);
-      store_acc_f32<kH>(acc, Yf, kLdY, nullptr);
+      gemm_panel(Xb, kLdXb, Pa, acc);
+      load_panel(Pb, static_cast<const __bf16*>(W.w2tb));
+      store_acc<kH>(acc, Yf, kLdY, zero2);
     }
+    SavedRow s1;
+    load_saved_row(sn, 2 * kH, srs, 2, nvalid, s1);
     __syncthreads();
-    ln_silu_bwd_rows_bf16(Yf, kLdY, Yb, kLdYb, sn + kH, 2 * kH, sr + 1, 2, nvalid, W.g2, W.be2);
+    ln_silu_bwd_rows(Yf, kLdY, Yb, kLdYb, s2, lp.g2, lp.b2);
     __syncthreads();
+    Panel<kH, 256> Pc;
     {  // dy1 = dz2 . W2   (B^T = W2^T)
       floatx4 acc[2][2];
-      gemm32_bf16<kH, kH>(Yb, kLdYb, w2tb, kH, acc);
-      store_acc_f32<kH>(acc, Yf, kLdY, nullptr);
+      gemm_panel(Yb, kLdYb, Pb, acc);
+      load_panel(Pc, static_cast<const __bf16*>(W.w1rtb));
+      store_acc<kH>(acc, Yf, kLdY, zero2);
     }
     __syncthreads();
-    ln_silu_bwd_rows_bf16(Yf, kLdY, Xb, kLdYb, sn, 2 * kH, sr, 2, nvalid, W.g1, W.be1);
+    ln_silu_bwd_rows(Yf, kLdY, Xb, kLdYb, s1, lp.g1, lp.b1);
     __syncthreads();
     {  // drbf = dz1 . W1r   (B^T = W1r^T [256][128])
       floatx4 acc[2][4];
-      gemm32_bf16<kH, 256>(Xb, kLdYb, w1rtb, kH, acc);
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            int row, c;
-            acc_coord<256>(rt, ct, r, row, c);
-            float x = te.d[row] - A.rbf_offset[c];
-            float rb = expf(A.rbf_coeff * (x * x));
-            dd_lane[rt][r] += acc[rt][ct][r] * rb * (2.0f * A.rbf_coeff * x);
-          }
+      gemm_panel(Xb, kLdYb, Pc, acc);
+      accumulate_dd(acc, te, mu, c2, coeff2, dd_lane);
     }
     __syncthreads();
   }
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = dd_lane[rt][r];
-      v += __shfl_xor(v, 1, 64);
-      v += __shfl_xor(v, 2, 64);
-      v += __shfl_xor(v, 4, 64);
-      v += __shfl_xor(v, 8, 64);
-      if ((lane & 15) == 0) part[wave][rt * 16 + 4 * (lane >> 4) + r] = v;
-    }
-  __syncthreads();
-  if (threadIdx.x < nvalid) {
-    float v = part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] + part[3][threadIdx.x];
-    int64_t e = e0 + threadIdx.x;
-    dd[e] = accumulate ? dd[e] + v : v;
-  }
+  reduce_dd(dd_lane, part, dd, e0, nvalid, accumulate);
 }
 
 }  // namespace e2v2
