@@ -180,6 +180,12 @@ __device__ __forceinline__ void tp_transpose(const float (&g)[kNT], float (&dA)[
   for (int z = 0; z < kTpNnz; ++z) dA[kTp[z].r][kTp[z].k] = fmaf(kTp[z].c, g[kTp[z].t], dA[kTp[z].r][kTp[z].k]);
 }
 
+// Row pass.  One workgroup per query atom i.  Thread t owns channel c = t in
+// the transposed aggregation (dA_c = T^T G_i[:, c], 27 registers) and head
+// h = t % 128 with edge parity t / 128 in the logit and softmax phases.
+// Per-edge sums over the 256 channels (dL/d dvec) reduce by DPP within rows
+// of 16 lanes and then over the 16 row partials in LDS; the per-head dL/dw
+// adds the head's two channels (h, h + 128) in LDS.
 __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const float* __restrict__ G,
                                                       const float* __restrict__ O, const float* __restrict__ mrow,
                                                       const float* __restrict__ srow, const int32_t* __restrict__ cnt,
@@ -189,50 +195,43 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
   __shared__ float a_s[kCHB][kH];
   __shared__ float qk_s[kCHB][kH];
   __shared__ float w_s[kCHB][kH];
-  __shared__ float dw_s[kCHB][kH];
-  __shared__ float ddv_s[kCHB][3];
+  __shared__ float dwc_s[kCHB][kC];
+  __shared__ float gp_s[kCHB][16][3];
   __shared__ float dd_s[kCHB][2];
   __shared__ float head_m[kH], head_inv[kH], head_dsum[kH], head_dmc[kH];
+  __shared__ float gdot_s[kH];
   __shared__ float dq_s[kH][kD];
   __shared__ ChunkEdges ce;
   const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
   if (i >= A.n_rows) return;
   const int lane = t & 63, wave = t >> 6;
   const int h = t & (kH - 1), half = t >> 7;
+  const int c = t;                      // channel c; its head is c % 128 = h
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   const Envelope env = make_env(A);
-  // ---- per-row prologue: dA for the lane's 4 channels c = lane + 64 q
-  float dA[4][kNV][3];
-  float gdot[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int c = lane + 64 * q;
+  const size_t os = (size_t)A.n_rows * kC;
+  // ---- per-row prologue: dA of channel c and D_h = sum_{c in h} sum_t G out
+  float dA[kNV][3];
+  {
     float g[kNT];
     float sdot = 0.f;
-    const size_t os = (size_t)A.n_rows * kC;
 #pragma unroll
     for (int z = 0; z < kNT; ++z) {
       g[z] = G[(size_t)i * kC + z * os + c];
       sdot = fmaf(g[z], O[(size_t)i * kC + z * os + c], sdot);
     }
-    tp_transpose(g, dA[q]);
-    gdot[q] = sdot;
-  }
-  if (wave == 0) {
-    // head lane: channels lane, lane+128; head lane+64: channels lane+64, lane+192
-    const float Dh0 = gdot[0] + gdot[2];
-    const float Dh1 = gdot[1] + gdot[3];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int hh = lane + 64 * u;
-      const float Dh = u ? Dh1 : Dh0;
-      const float s = srow[(size_t)i * kH + hh];
+    tp_transpose(g, dA);
+    if (half) gdot_s[h] = sdot;
+    __syncthreads();
+    if (!half) {
+      const float Dh = sdot + gdot_s[h];
+      const float s = srow[(size_t)i * kH + h];
       const float inv = 1.0f / (s + kEps);
-      const int cn = cnt[(size_t)i * kH + hh];
-      head_m[hh] = mrow[(size_t)i * kH + hh];
-      head_inv[hh] = inv;
-      head_dsum[hh] = Dh * inv;
-      head_dmc[hh] = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
+      const int cn = cnt[(size_t)i * kH + h];
+      head_m[h] = mrow[(size_t)i * kH + h];
+      head_inv[h] = inv;
+      head_dsum[h] = Dh * inv;
+      head_dmc[h] = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
     }
   }
   float qs[kD];
@@ -245,7 +244,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
     const int nc = min(kCHB, n - c0);
     load_chunk(A, env, b + c0, nc, ce);
     __syncthreads();
-    // recompute logits and final weights
+    // ---- phase 1: recompute logits and final weights (thread per head, edge parity)
     for (int el = half; el < nc; el += 2) {
       const int64_t e = (int64_t)b + c0 + el;
       const float qk = qk_dot(qs, A.k + ((size_t)ce.j[el] * kH + h) * kD);
@@ -259,45 +258,55 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
       w_out[e * kH + h] = w;
     }
     __syncthreads();
-    // transposed aggregation: one wave per edge
-    for (int el = wave; el < nc; el += 4) {
-      const float dvx = ce.dv[el][0], dvy = ce.dv[el][1], dvz = ce.dv[el][2];
-      const float* vp = A.v + (size_t)ce.j[el] * kC + lane;
-      const size_t vs = (size_t)A.n_rows * kC;
-      float gx = 0.f, gy = 0.f, gz = 0.f;
-      float dwc[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float ux = 0.f, uy = 0.f, uz = 0.f;
+    // ---- phase 2: transposed aggregation, thread per channel, two edges per step
+    {
+      const float* vb = A.v + c;
+      auto edge = [&](int el, const float (&vr)[kNV]) {
+        float u0 = 0.f, u1 = 0.f, u2 = 0.f;
 #pragma unroll
         for (int r = 0; r < kNV; ++r) {
-          const float vr = vp[r * vs + 64 * q];
-          ux = fmaf(dA[q][r][0], vr, ux);
-          uy = fmaf(dA[q][r][1], vr, uy);
-          uz = fmaf(dA[q][r][2], vr, uz);
+          u0 = fmaf(dA[r][0], vr[r], u0);
+          u1 = fmaf(dA[r][1], vr[r], u1);
+          u2 = fmaf(dA[r][2], vr[r], u2);
         }
-        dwc[q] = ux * dvx + uy * dvy + uz * dvz;
-        const float w = w_s[el][(lane + 64 * q) & (kH - 1)];
-        gx = fmaf(w, ux, gx);
-        gy = fmaf(w, uy, gy);
-        gz = fmaf(w, uz, gz);
+        dwc_s[el][c] = u0 * ce.dv[el][0] + u1 * ce.dv[el][1] + u2 * ce.dv[el][2];
+        const float w = w_s[el][h];
+        const float g0 = dpp_row_sum16(w * u0);
+        const float g1 = dpp_row_sum16(w * u1);
+        const float g2 = dpp_row_sum16(w * u2);
+        if ((lane & 15) == 0) {
+          const int p = wave * 4 + (lane >> 4);
+          gp_s[el][p][0] = g0;
+          gp_s[el][p][1] = g1;
+          gp_s[el][p][2] = g2;
+        }
+      };
+      int el = 0;
+      for (; el + 1 < nc; el += 2) {
+        const float* v0 = vb + (size_t)ce.j[el] * kC;
+        const float* v1 = vb + (size_t)ce.j[el + 1] * kC;
+        float va[kNV], vc[kNV];
+#pragma unroll
+        for (int r = 0; r < kNV; ++r) {
+          va[r] = v0[r * os];
+          vc[r] = v1[r * os];
+        }
+        edge(el, va);
+        edge(el + 1, vc);
       }
-      dw_s[el][lane] = dwc[0] + dwc[2];
-      dw_s[el][lane + 64] = dwc[1] + dwc[3];
-      gx = wave_sum(gx);
-      gy = wave_sum(gy);
-      gz = wave_sum(gz);
-      if (lane == 0) {
-        ddv_s[el][0] = gx;
-        ddv_s[el][1] = gy;
-        ddv_s[el][2] = gz;
+      if (el < nc) {
+        const float* v0 = vb + (size_t)ce.j[el] * kC;
+        float va[kNV];
+#pragma unroll
+        for (int r = 0; r < kNV; ++r) va[r] = v0[r * os];
+        edge(el, va);
       }
     }
     __syncthreads();
-    // softmax / gate / distance backward: thread per (head, edge parity)
+    // ---- phase 3: softmax / gate / distance backward (thread per head, edge parity)
     for (int el = half; el < nc; el += 2) {
       const int64_t e = (int64_t)b + c0 + el;
-      const float dw = dw_s[el][h];
+      const float dw = dwc_s[el][h] + dwc_s[el][h + kH];
       const float a = a_s[el][h];
       const float qk = qk_s[el][h];
       const float gate = A.gi[e * (2 * kH) + h];
@@ -329,9 +338,16 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
     __syncthreads();
     if (t < nc) {
       const int64_t e = (int64_t)b + c0 + t;
-      ddv[3 * e] = ddv_s[t][0];
-      ddv[3 * e + 1] = ddv_s[t][1];
-      ddv[3 * e + 2] = ddv_s[t][2];
+      float gx = 0.f, gy = 0.f, gz = 0.f;
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        gx += gp_s[t][p][0];
+        gy += gp_s[t][p][1];
+        gz += gp_s[t][p][2];
+      }
+      ddv[3 * e] = gx;
+      ddv[3 * e + 1] = gy;
+      ddv[3 * e + 2] = gz;
       dd[e] = dd_s[t][0] + dd_s[t][1];
     }
     __syncthreads();

@@ -67,6 +67,21 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
+// Sum over each row of 16 lanes, left in every lane of the row, by four DPP
+// steps (lane ^ 1, lane ^ 2 via quad permutes; ^ 7 within 8 and ^ 15 within
+// 16 via the half-row and row mirrors) instead of LDS-crossbar shuffles.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_row_sum16(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return v;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X (each with
 // its own L2).  Give every XCD a contiguous range of rows so that spatially
 // adjacent rows (atoms are Morton-ordered by the host) share one L2.
