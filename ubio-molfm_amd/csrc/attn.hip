@@ -54,6 +54,7 @@ struct ChunkEdges {
   float p[kCH];
   float dp[kCH];
   float R[kCH];
+  float rR[kCH];
   float d[kCH];
 };
 
@@ -73,6 +74,7 @@ __device__ __forceinline__ void load_chunk(const e2v2_attn_args& A, const Envelo
     ce.p[t] = p;
     ce.dp[t] = dp;
     ce.R[t] = fmaxf(d, 1e-6f);
+    ce.rR[t] = 1.0f / ce.R[t];
   }
 }
 
@@ -104,6 +106,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
       const int64_t e = (int64_t)b + c0 + el;
       const float qk = qk_dot(qs, A.k + ((size_t)ce.j[el] * kH + h) * kD);
       a_s[el][h] = ntload(A.gi + e * (2 * kH) + h) * qk;
+      coef_s[el][h] = ntload(A.gi + e * (2 * kH) + kH + h);   // input head, scaled below
     }
     __syncthreads();
     if (t < kH) {
@@ -116,12 +119,10 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
       c_run = (m_new == m_run) ? c_run + cc : cc;
       s_run *= sc;
       for (int el = 0; el < nc; ++el) {
-        const int64_t e = (int64_t)b + c0 + el;
         const float ex = expf(a_s[el][h] - m_new);
         const float ee = ex * ce.p[el];
         s_run += ee;
-        const float ih = ntload(A.gi + e * (2 * kH) + kH + h);
-        coef_s[el][h] = (ee * ih) / ce.R[el];
+        coef_s[el][h] = (ee * coef_s[el][h]) * ce.rR[el];
       }
       m_run = m_new;
       scale_s[h] = sc;
@@ -253,7 +254,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
       qk_s[el][h] = qk;
       const float ee = expf(a - head_m[h]) * ce.p[el];
       const float alpha = (ee * A.gi[e * (2 * kH) + kH + h]) * head_inv[h];
-      const float w = alpha / ce.R[el];
+      const float w = alpha * ce.rR[el];
       w_s[el][h] = w;
       w_out[e * kH + h] = w;
     }
@@ -315,9 +316,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
       const float ee = ex * ce.p[el];
       const float inv = head_inv[h];
       const float alpha = (ee * ih) * inv;
-      const float R = ce.R[el];
-      const float dalpha = dw / R;
-      const float dR = (ce.d[el] > 1e-6f) ? -dw * alpha / (R * R) : 0.f;
+      const float rR = ce.rR[el];
+      const float dalpha = dw * rR;
+      const float dR = (ce.d[el] > 1e-6f) ? -dalpha * alpha * rR : 0.f;
       const float dih = dalpha * ee * inv;
       const float de = dalpha * ih * inv - head_dsum[h];
       float da = de * ee;

@@ -33,14 +33,14 @@ constexpr float kFarDist = 1e18f;  // distance of padding rows: finite, and its 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // ---------------------------------------------------------------------------
-// fp32 GEMM: C[32][N] = A[32][K] (LDS, row stride lda) x B[K][N] (global, row
-// stride ldb).  Wave w owns columns [w*N/4, (w+1)*N/4).  acc[rt][ct] holds the
-// 16x16 tile (rows rt*16.., cols w*N/4 + ct*16..); lane l holds rows
-// 4*(l/16)+r, col l%16.  B is streamed in chunks of 32 k-rows held in
+// fp32 GEMM: C[32][N] = A[32][K] x B[K][N] (global, row stride ldb).  Wave w
+// owns columns [w*N/4, (w+1)*N/4).  acc[rt][ct] holds the 16x16 tile (rows
+// rt*16.., cols w*N/4 + ct*16..); lane l holds rows 4*(l/16)+r, col l%16.
+// afn(k, a0, a1) supplies A[l%16][k] and A[16 + l%16][k] for this lane's
+// k = 4 s + l/16 of k-step s.  B is streamed in chunks of 32 k-rows held in
 // registers one chunk ahead (the fp32 MFMA time per chunk covers the load).
-template <int K, int N>
-__device__ __forceinline__ void gemm32(const float* A, int lda, const float* __restrict__ B, int ldb,
-                                       floatx4 (&acc)[2][N / 64]) {
+template <int K, int N, typename AFn>
+__device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, int ldb, floatx4 (&acc)[2][N / 64]) {
   constexpr int CT = N / 64;
   constexpr int NCH = K / (4 * kPF);
   const int lane = threadIdx.x & 63;
@@ -67,9 +67,8 @@ __device__ __forceinline__ void gemm32(const float* A, int lda, const float* __r
     }
 #pragma unroll
     for (int s = 0; s < kPF; ++s) {
-      const int k0 = ch * 4 * kPF + 4 * s;
-      const float a0 = A[li * lda + k0 + lk];
-      const float a1 = A[(16 + li) * lda + k0 + lk];
+      float a0, a1;
+      afn(ch * 4 * kPF + 4 * s + lk, a0, a1);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         acc[0][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, bc[s][ct], acc[0][ct], 0, 0, 0);
@@ -83,6 +82,32 @@ __device__ __forceinline__ void gemm32(const float* A, int lda, const float* __r
         for (int ct = 0; ct < CT; ++ct) bc[s][ct] = bn[s][ct];
     }
   }
+}
+
+// A from an LDS tile with row stride lda
+template <int K, int N>
+__device__ __forceinline__ void gemm32(const float* A, int lda, const float* __restrict__ B, int ldb,
+                                       floatx4 (&acc)[2][N / 64]) {
+  const int li = threadIdx.x & 15;
+  const float* A0 = A + li * lda;
+  const float* A1 = A + (16 + li) * lda;
+  gemm32f<K, N>([&](int k, float& a0, float& a1) { a0 = A0[k]; a1 = A1[k]; }, B, ldb, acc);
+}
+
+// A = the RBF tile exp(coeff (d_row - mu_k)^2), generated in registers: the
+// exponentials of a k-step issue under the previous k-step's MFMAs, and the
+// tile needs no LDS.
+template <int N>
+__device__ __forceinline__ void gemm32_rbf(float d0, float d1, const float* mu_s, float c2,
+                                           const float* __restrict__ B, int ldb, floatx4 (&acc)[2][N / 64]) {
+  gemm32f<kK0, N>(
+      [&](int k, float& a0, float& a1) {
+        const float mu = mu_s[k];
+        const float x0 = d0 - mu, x1 = d1 - mu;
+        a0 = fexp2(c2 * (x0 * x0));
+        a1 = fexp2(c2 * (x1 * x1));
+      },
+      B, ldb, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -380,17 +405,17 @@ __device__ __forceinline__ void reduce_dd(float (&dd_lane)[2][4], float (*part)[
 // fp32 kernels
 __global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
   extern __shared__ float sm[];
-  float* X = sm;                    // [32][258]: rbf tile, then h2 / y2 with stride kLdY
-  float* Y = X + kT * kLdX;         // [32][130]
+  float* Y = sm;                    // [32][130]: GEMM-1/2 outputs, LayerNorm in place
   __shared__ TileEdges te;
   __shared__ LnParams lp;
+  __shared__ float mu_s[kK0];
   const int m = blockIdx.y;
   const e2v2_mlp_weights& W = A.w[m];
   const int64_t e0 = (int64_t)blockIdx.x * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   float* sn = A.save_n ? A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH) : nullptr;
   float* sr = A.save_r ? A.save_r + ((size_t)m * A.n_edges + e0) * 2 : nullptr;
-  const float mu = A.rbf_offset[threadIdx.x];
+  mu_s[threadIdx.x] = A.rbf_offset[threadIdx.x];
   float b2[2], b3[4];
   load_bias<kH>(W.b2, b2);
   load_bias<256>(W.b3, b3);
@@ -399,11 +424,10 @@ __global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restr
   __syncthreads();
   TypeTerms tt;
   load_type_terms(W.ttgt, W.tsrc, te, tt);
-  rbf_tile(te, mu, A.rbf_coeff * kLog2e, X, kLdX);
-  __syncthreads();
   {
+    const int li = threadIdx.x & 15;
     floatx4 acc[2][2];
-    gemm32<kK0, kH>(X, kLdX, W.w1t, kH, acc);
+    gemm32_rbf<kH>(te.d[li], te.d[16 + li], mu_s, A.rbf_coeff * kLog2e, W.w1t, kH, acc);
     store_gemm1(acc, tt, Y, kLdY);
   }
   __syncthreads();
@@ -412,21 +436,22 @@ __global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restr
   {
     floatx4 acc[2][2];
     gemm32<kH, kH>(Y, kLdY, W.w2t, kH, acc);
-    store_acc<kH>(acc, X, kLdY, b2);
+    __syncthreads();
+    store_acc<kH>(acc, Y, kLdY, b2);
   }
   __syncthreads();
-  ln_silu_rows(X, kLdY, X, kLdY, lp.g2, lp.b2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2, nvalid);
+  ln_silu_rows(Y, kLdY, Y, kLdY, lp.g2, lp.b2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2, nvalid);
   __syncthreads();
   floatx4 acc[2][4];
-  gemm32<kH, 256>(X, kLdY, W.w3t, 256, acc);
+  gemm32<kH, 256>(Y, kLdY, W.w3t, 256, acc);
   store_out(acc, b3, out, ld_out, e0, nvalid, m);
 }
 
 __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
                                                  float* __restrict__ dd, int accumulate) {
   extern __shared__ float sm[];
-  float* X = sm;                    // [32][258]
-  float* Y = X + kT * kLdX;         // [32][130]
+  float* X = sm;                    // [32][258]: dOut tile; after GEMM a, the [32][130] LayerNorm rows
+  float* Y = sm;
   __shared__ TileEdges te;
   __shared__ LnParams lp;
   __shared__ float part[4][kT];
@@ -448,7 +473,7 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
     const float* sn = A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH);
     const float* srs = A.save_r + ((size_t)m * A.n_edges + e0) * 2;
     load_ln_params(W, lp);
-    for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {   // dOut tile, float4 loads
+    for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {   // dOut tile, 16-byte loads
       const int row = idx >> 6, c4 = idx & 63;
       const floatx4 v = row < nvalid ? reinterpret_cast<const floatx4*>(dout + (e0 + row) * ld_dout + m * 256)[c4]
                                      : floatx4{0.f, 0.f, 0.f, 0.f};
@@ -461,6 +486,7 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
     {  // dy2 = dOut . W3   (W3 [256][128] row-major = B[K=256][N=128])
       floatx4 acc[2][2];
       gemm32<256, kH>(X, kLdX, W.w3, kH, acc);
+      __syncthreads();
       store_acc<kH>(acc, Y, kLdY, zero2);
     }
     SavedRow s1;
@@ -468,17 +494,18 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
     __syncthreads();
     ln_silu_bwd_rows(Y, kLdY, Y, kLdY, s2, lp.g2, lp.b2);
     __syncthreads();
-    {  // dy1 = dz2 . W2   (W2 [128][128]) -> X with stride kLdY
+    {  // dy1 = dz2 . W2   (W2 [128][128])
       floatx4 acc[2][2];
       gemm32<kH, kH>(Y, kLdY, W.w2, kH, acc);
-      store_acc<kH>(acc, X, kLdY, zero2);
+      __syncthreads();
+      store_acc<kH>(acc, Y, kLdY, zero2);
     }
     __syncthreads();
-    ln_silu_bwd_rows(X, kLdY, X, kLdY, s1, lp.g1, lp.b1);
+    ln_silu_bwd_rows(Y, kLdY, Y, kLdY, s1, lp.g1, lp.b1);
     __syncthreads();
     {  // drbf = dz1 . W1r  (W1 [128][ldw1], rbf columns 0..255)
       floatx4 acc[2][4];
-      gemm32<kH, 256>(X, kLdY, W.w1, W.ldw1, acc);
+      gemm32<kH, 256>(Y, kLdY, W.w1, W.ldw1, acc);
       accumulate_dd(acc, te, mu, c2, coeff2, dd_lane);
     }
     __syncthreads();
@@ -617,7 +644,8 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const flo
 
 using namespace e2v2;
 
-static size_t mlp_lds() { return sizeof(float) * (kT * kLdX + kT * kLdY); }
+static size_t mlp_lds_fwd() { return sizeof(float) * kT * kLdY; }
+static size_t mlp_lds_bwd() { return sizeof(float) * kT * kLdX; }
 static size_t mlp_lds_bf16() { return sizeof(__bf16) * (kT * kLdXb + kT * kLdYb) + sizeof(float) * kT * kLdY; }
 
 E2V2_API int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hipStream_t s) {
@@ -633,13 +661,7 @@ E2V2_API int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hip
     E2V2_LAUNCHED("k_mlp_fwd_bf16");
     return 0;
   }
-  static bool attr = false;
-  if (!attr) {
-    E2V2_TRY_HIP(hipFuncSetAttribute((const void*)k_mlp_fwd, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)mlp_lds()));
-    attr = true;
-  }
-  hipLaunchKernelGGL(k_mlp_fwd, grid, dim3(256), mlp_lds(), s, A, out, ld_out);
+  hipLaunchKernelGGL(k_mlp_fwd, grid, dim3(256), mlp_lds_fwd(), s, A, out, ld_out);
   E2V2_LAUNCHED("k_mlp_fwd");
   return 0;
 }
@@ -660,13 +682,7 @@ E2V2_API int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_d
     E2V2_LAUNCHED("k_mlp_bwd_bf16");
     return 0;
   }
-  static bool attr = false;
-  if (!attr) {
-    E2V2_TRY_HIP(hipFuncSetAttribute((const void*)k_mlp_bwd, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)mlp_lds()));
-    attr = true;
-  }
-  hipLaunchKernelGGL(k_mlp_bwd, grid, dim3(256), mlp_lds(), s, A, dout, ld_dout, dd, accumulate);
+  hipLaunchKernelGGL(k_mlp_bwd, grid, dim3(256), mlp_lds_bwd(), s, A, dout, ld_dout, dd, accumulate);
   E2V2_LAUNCHED("k_mlp_bwd");
   return 0;
 }
