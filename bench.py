@@ -65,25 +65,36 @@ def deg_bwd_bytes(N, E):
     return 4.0 * (E * (768 + 768 + 4 + 4) + N * 9 * 256)
 
 
-KERNEL_OF = {"e2v2_mlp_fwd": "k_mlp_fwd", "e2v2_mlp_bwd": "k_mlp_bwd", "e2v2_attn_fwd": "k_attn_fwd",
-             "e2v2_attn_bwd": "k_attn_bwd_row",
-             "e2v2_deg_fwd": "k_deg_fwd", "e2v2_deg_bwd": "k_deg_bwd", "e2v2_nbr_count": "k_nbr_count"}
+def stack_flops(N, E):
+    """Algorithmic FLOPs of one energy + force evaluation, reference formulation:
+    2 x (1.88 MFLOP per edge + 4 layers x 22.7 MFLOP per node) (forward plus
+    first-order input-gradient backward)."""
+    return 2.0 * (E * 1.88e6 + N * 4 * 22.7e6)
+
+
+BYTES_OF = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
+            "e2v2_deg_bwd": deg_bwd_bytes}
+
+KERNELS_OF = {"e2v2_mlp_fwd": ["k_mlp_fwd"], "e2v2_mlp_bwd": ["k_mlp_bwd"], "e2v2_attn_fwd": ["k_attn_fwd"],
+              "e2v2_attn_bwd": ["k_attn_bwd_row", "k_attn_bwd_col"], "e2v2_deg_fwd": ["k_deg_fwd"],
+              "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"]}
 
 
 def traffic_from_profile(entry, bf16=False):
-    """HBM bytes per launch of the entry point's kernel from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated against a plain copy)."""
+    """HBM-side bytes per call of a library entry point (sum over its kernels)
+    from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the fp32
+    configs[3] workload, calibrated against a plain copy; None when the entry
+    point or its precision is not covered by the summary."""
     path = ROOT / "profiles" / "hbm_traffic_cfg4_md10k.txt"
-    k = KERNEL_OF.get(entry)
-    if bf16 and entry in ("e2v2_mlp_fwd", "e2v2_mlp_bwd"):
-        k = k + "_bf16"
-    if k is None or not path.exists():
+    ks = KERNELS_OF.get(entry)
+    if ks is None or not path.exists() or bf16:
         return None
+    found = {}
     for line in path.read_text().splitlines():
         parts = line.split()
-        if parts and parts[0] == k and len(parts) == 4:
-            return float(parts[3]) * 1e9
-    return None
+        if parts and parts[0] in ks and len(parts) == 4:
+            found[parts[0]] = float(parts[3]) * 1e9
+    return sum(found.values()) if len(found) == len(ks) else None
 
 
 def cpu_baseline(pkg):
@@ -195,6 +206,30 @@ def main():
         achieved = b / (st["avg_ms"] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profile(name), "kernel": name}
+    # per-kernel achieved rate against its own roofline
+    per_kernel = {}
+    for k, v in stats.items():
+        ent = {"avg_ms": round(v["avg_ms"], 4), "count": v["count"], "total_ms": round(v["total_ms"], 3)}
+        if k in BYTES_OF:
+            gbs = BYTES_OF[k](N, E_mean) / (v["avg_ms"] * 1e-3) / 1e9
+            ent.update(bound="hbm", achieved_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+        elif k in ("e2v2_mlp_fwd", "e2v2_mlp_bwd"):
+            fl = mlp_fwd_flops if k == "e2v2_mlp_fwd" else mlp_bwd_flops
+            tf = (fl(E_mean, 3) + 4 * fl(E_mean, 1)) / (v["count"] / args.steps) / (v["avg_ms"] * 1e-3) / 1e12
+            pk = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
+            ent.update(bound="mfma", achieved_tflops=round(tf, 2), frac=round(tf / pk, 4))
+        per_kernel[k] = ent
+    # stack: whole evaluation against the MFMA roofline; HBM-bound kernels time-weighted
+    peak_tf = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
+    stack_tf = stack_flops(N, E_mean) / (ms * 1e-3) / 1e12
+    hb = [k for k in BYTES_OF if k in stats]
+    hb_bytes = sum(BYTES_OF[k](N, E_mean) * stats[k]["count"] for k in hb)
+    hb_time = sum(stats[k]["total_ms"] for k in hb) * 1e-3
+    roof["stack"] = {"bound": "mfma", "achieved": round(stack_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
+                     "frac": round(stack_tf / peak_tf, 4), "flops_per_step": stack_flops(N, E_mean)}
+    roof["hbm_kernels_time_weighted"] = {"kernels": hb, "achieved": round(hb_bytes / hb_time / 1e9, 1),
+                                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                         "frac": round(hb_bytes / hb_time / 1e9 / HBM_PEAK_GBS, 4)}
     cpu = None
     if not args.no_cpu_baseline and args.config == 4:
         cpu = cpu_baseline(pkg)
@@ -215,8 +250,7 @@ def main():
         "mode": mode,
         "peak_memory_gb": peak_gb,
         "nve_energy_drift_ev_per_atom": (e_end - e_start) / N,
-        "kernels": {k: {"avg_ms": round(v["avg_ms"], 4), "count": v["count"], "total_ms": round(v["total_ms"], 3)}
-                    for k, v in stats.items()},
+        "kernels": per_kernel,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
