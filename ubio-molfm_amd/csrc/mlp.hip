@@ -57,6 +57,7 @@ __device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, in
   for (int s = 0; s < kPF; ++s)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) bc[s][ct] = Bp[(size_t)(4 * s) * ldb + ct * 16];
+  __builtin_amdgcn_s_setprio(1);   // MFMA-ready waves issue ahead of epilogue work of other waves
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     if (ch + 1 < NCH) {
@@ -82,6 +83,7 @@ __device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, in
         for (int ct = 0; ct < CT; ++ct) bc[s][ct] = bn[s][ct];
     }
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // A from an LDS tile with row stride lda
