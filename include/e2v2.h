@@ -158,20 +158,22 @@ typedef struct e2v2_attn_args {
   const int32_t* key_eid;        /* [E]                                             */
   const float* dvec;             /* [E,3] pos_i - (pos_j + s.cell)                   */
   const float* dist;             /* [E]                                             */
-  const float* q;                /* [N,H,D]                                         */
-  const float* k;                /* [N,H,D]                                         */
-  const float* v;                /* [9][N][C] m-major                               */
+  const void* q;                 /* [N,H,D]            float, or bf16 if act_bf16   */
+  const void* k;                 /* [N,H,D]            float, or bf16 if act_bf16   */
+  const void* v;                 /* [9][N][C] m-major  float, or bf16 if act_bf16   */
   const float* gi;               /* [E,2H] gate | inputhead                         */
   float q_div;                   /* sqrt(D)                                         */
   float rc, env_a, env_b, env_c; /* polynomial envelope                             */
+  int32_t act_bf16;              /* 1: q, k, v, out, grad_out stored as bf16 (fp32 math) */
 } e2v2_attn_args;
 
 /* v [9][N][C] and out [20][N][C] are m-major (row r of every atom contiguous);
-   out: h_a - h_b rows of the SO(2) product; mrow/srow [N,H] softmax max / sum; cnt [N,H] number of maxima */
-int e2v2_attn_fwd(const e2v2_attn_args* args, float* out, float* mrow, float* srow, int32_t* cnt, hipStream_t s);
-/* grad_out, out [20][N][C] -> dgi [E,2H], ddvec [E,3], ddist [E], dq, dk [N,H,D], dv [9][N][C];
-   w_edge, dqk_edge [E,H] are outputs consumed by the column pass */
-int e2v2_attn_bwd(const e2v2_attn_args* args, const float* grad_out, const float* out, const float* mrow,
+   out (float, or bf16 if act_bf16): h_a - h_b rows of the SO(2) product; mrow/srow [N,H] softmax max / sum;
+   cnt [N,H] number of maxima */
+int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, float* srow, int32_t* cnt, hipStream_t s);
+/* grad_out, out [20][N][C] (float, or bf16 if act_bf16) -> dgi [E,2H], ddvec [E,3], ddist [E], dq, dk [N,H,D],
+   dv [9][N][C] (all float); w_edge, dqk_edge [E,H] are outputs consumed by the column pass */
+int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, const void* out, const float* mrow,
                   const float* srow, const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq,
                   float* dk, float* dv, float* w_edge, float* dqk_edge, hipStream_t s);
 

@@ -115,20 +115,29 @@ def _attn_inputs(nl, cuda, seed=2):
     return q, k, v, gi
 
 
-def test_attention_forward_backward(pkg, cuda):
+def _attention_case(pkg, cuda, act_dtype):
+    """Attention fwd + bwd through the C ABI against the float64 reference.  With
+    bf16 storage the inputs (q, k, v, grad) are rounded to bf16 for both sides,
+    so the remaining differences are the bf16 output rows (also used by the
+    backward's D_h) and fp32 arithmetic."""
     from ubio_molfm_amd import _lib, ops, so3
     s, pos, nl = _graph(pkg, cuda, seed=4)
     N, E = nl.n_atoms, nl.n_edges
-    print(f"[attn] N={N} E={E}", flush=True)
+    bf = act_dtype == torch.bfloat16
+    print(f"[attn {act_dtype}] N={N} E={E}", flush=True)
     q, k, v, gi = _attn_inputs(nl, cuda)
+    G = torch.randn(N, 20, 256, generator=torch.Generator().manual_seed(7))
+    if bf:
+        q, k, v, G = (t.to(torch.bfloat16).float() for t in (q, k, v, G))
     st = _lib.vp(torch.cuda.current_stream().cuda_stream)
-    qd, kd, gid = (t.to(cuda).contiguous() for t in (q, k, gi))
-    vd = v.permute(1, 0, 2).contiguous().to(cuda)        # m-major [9, N, C]
+    qd, kd = (t.to(cuda).to(act_dtype).contiguous() for t in (q, k))
+    gid = gi.to(cuda).contiguous()
+    vd = v.permute(1, 0, 2).contiguous().to(cuda).to(act_dtype)        # m-major [9, N, C]
     args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
                          nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                          qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), gid.data_ptr(), math.sqrt(8.0), 6.0,
-                         ops.ENV_A, ops.ENV_B, ops.ENV_C)
-    out = torch.empty(20, N, 256, device=cuda); m = torch.empty(N, 128, device=cuda)
+                         ops.ENV_A, ops.ENV_B, ops.ENV_C, int(bf))
+    out = torch.empty(20, N, 256, device=cuda, dtype=act_dtype); m = torch.empty(N, 128, device=cuda)
     sr = torch.empty(N, 128, device=cuda); cnt = torch.empty(N, 128, dtype=torch.int32, device=cuda)
     _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _lib.vp(out.data_ptr()), _lib.vp(m.data_ptr()),
               _lib.vp(sr.data_ptr()), _lib.vp(cnt.data_ptr()), st)
@@ -136,13 +145,12 @@ def test_attention_forward_backward(pkg, cuda):
     row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()
     leaves = [t.double().requires_grad_(True) for t in (q, k, v, nl.dvec.cpu(), nl.dist.cpu(), gi)]
     ref = attn_ref(*leaves[:5], row, col, leaves[5], T, 6.0, N)
-    e_f = relerr(out.permute(1, 0, 2), ref)
-    G = torch.randn(N, 20, 256, generator=torch.Generator().manual_seed(7))
+    e_f = relerr(out.float().permute(1, 0, 2), ref)
     grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
-    Gd = G.permute(1, 0, 2).contiguous().to(cuda)
+    Gd = G.permute(1, 0, 2).contiguous().to(cuda).to(act_dtype)
     f = dict(device=cuda)
     dgi = torch.empty(E, 256, **f); ddv = torch.empty(E, 3, **f); dd = torch.empty(E, **f)
-    dq = torch.empty_like(qd); dk = torch.empty_like(kd); dv = torch.empty_like(vd)
+    dq = torch.empty(qd.shape, **f); dk = torch.empty(kd.shape, **f); dv = torch.empty(vd.shape, **f)
     we = torch.empty(E, 128, **f); dqk = torch.empty(E, 128, **f)
     _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _lib.vp(Gd.data_ptr()), _lib.vp(out.data_ptr()),
               _lib.vp(m.data_ptr()), _lib.vp(sr.data_ptr()), _lib.vp(cnt.data_ptr()), _lib.vp(dgi.data_ptr()),
@@ -151,10 +159,24 @@ def test_attention_forward_backward(pkg, cuda):
     errs = dict(q=relerr(dq, grads[0]), k=relerr(dk, grads[1]), v=relerr(dv.permute(1, 0, 2), grads[2]),
                 dvec=relerr(ddv, grads[3]),
                 dist=relerr(dd, grads[4]), gi=relerr(dgi, grads[5]))
-    print(f"[attn] fwd rel {e_f:.2e} bwd {errs}", flush=True)
+    print(f"[attn {act_dtype}] fwd rel {e_f:.2e} bwd {errs}", flush=True)
+    return e_f, errs
+
+
+def test_attention_forward_backward(pkg, cuda):
+    e_f, errs = _attention_case(pkg, cuda, torch.float32)
     assert e_f < 2e-5
     for name, e in errs.items():
         assert e < 1e-4, (name, e)
+
+
+def test_attention_bf16_storage(pkg, cuda):
+    """bf16 storage of q, k, v, out and grad (fp32 math): forward within 4e-3
+    (one bf16 rounding of the output rows), gradients within 1e-2."""
+    e_f, errs = _attention_case(pkg, cuda, torch.bfloat16)
+    assert e_f < 4e-3
+    for name, e in errs.items():
+        assert e < 1e-2, (name, e)
 
 
 def test_degree_forward_backward(pkg, cuda):

@@ -46,7 +46,7 @@ class AttnArgs(C.Structure):
     _fields_ = [("n_rows", i32), ("n_edges", i64), ("n_heads", i32), ("head_dim", i32), ("channels", i32),
                 ("row_ptr", vp), ("col", vp), ("edge_row", vp), ("key_ptr", vp), ("key_eid", vp),
                 ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("gi", vp),
-                ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32)]
+                ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32)]
 
 
 class DegArgs(C.Structure):

@@ -27,25 +27,64 @@ __device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
   return E;
 }
 
+// Node activations q, k, v, the output rows and their gradient are stored as TS
+// (float, or __bf16 in the bf16 mode); every load widens to fp32 and all
+// arithmetic, softmax statistics and reductions are fp32.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float f32(float x) { return x; }
+__device__ __forceinline__ float f32(__bf16 x) { return (float)x; }
+
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ void load8(const __bf16* p, float (&v)[8]) {
+  const bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)a[i];
+}
+__device__ __forceinline__ void load4(const float* p, float (&v)[4]) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+}
+__device__ __forceinline__ void load4(const __bf16* p, float (&v)[4]) {
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = (float)a[i];
+}
+// One activation through a 32-bit load of the aligned word that holds it: the
+// gathers of the column pass then schedule like their fp32 form (16-bit loads
+// are issued one edge at a time); the word lies inside the tensor because rows
+// have an even number of elements.
+__device__ __forceinline__ float ld_word(const float* p) { return *p; }
+__device__ __forceinline__ float ld_word(const __bf16* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+  return __uint_as_float((a & 2) ? (w & 0xffff0000u) : (w << 16));
+}
+__device__ __forceinline__ void store_act(float v, float* p) { ntstore(v, p); }
+__device__ __forceinline__ void store_act(float v, __bf16* p) { *p = (__bf16)v; }
+
 // <q_s, k_j[h]> with q_s already divided by sqrt(D); identical code in every pass
-__device__ __forceinline__ float qk_dot(const float (&qs)[kD], const float* __restrict__ kp) {
-  const float4 k0 = reinterpret_cast<const float4*>(kp)[0];
-  const float4 k1 = reinterpret_cast<const float4*>(kp)[1];
-  float s = qs[0] * k0.x;
-  s = fmaf(qs[1], k0.y, s);
-  s = fmaf(qs[2], k0.z, s);
-  s = fmaf(qs[3], k0.w, s);
-  s = fmaf(qs[4], k1.x, s);
-  s = fmaf(qs[5], k1.y, s);
-  s = fmaf(qs[6], k1.z, s);
-  s = fmaf(qs[7], k1.w, s);
+template <typename TS>
+__device__ __forceinline__ float qk_dot(const float (&qs)[kD], const TS* __restrict__ kp) {
+  float k[kD];
+  load8(kp, k);
+  float s = qs[0] * k[0];
+#pragma unroll
+  for (int d = 1; d < kD; ++d) s = fmaf(qs[d], k[d], s);
   return s;
 }
 
+template <typename TS>
 __device__ __forceinline__ void load_qs(const e2v2_attn_args& A, int i, int h, float (&qs)[kD]) {
-  const float* qp = A.q + ((size_t)i * kH + h) * kD;
+  float q[kD];
+  load8(static_cast<const TS*>(A.q) + ((size_t)i * kH + h) * kD, q);
 #pragma unroll
-  for (int d = 0; d < kD; ++d) qs[d] = qp[d] / A.q_div;
+  for (int d = 0; d < kD; ++d) qs[d] = q[d] / A.q_div;
 }
 
 struct ChunkEdges {
@@ -78,8 +117,11 @@ __device__ __forceinline__ void load_chunk(const e2v2_attn_args& A, const Envelo
   }
 }
 
-__global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __restrict__ out, float* __restrict__ mrow,
+template <typename TS>
+__global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, TS* __restrict__ out, float* __restrict__ mrow,
                                                   float* __restrict__ srow, int32_t* __restrict__ cnt) {
+  const TS* __restrict__ Kp = static_cast<const TS*>(A.k);
+  const TS* __restrict__ Vp = static_cast<const TS*>(A.v);
   __shared__ float a_s[kCH][kH];
   __shared__ float coef_s[kCH][kH];
   __shared__ float scale_s[kH];
@@ -91,7 +133,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   const Envelope env = make_env(A);
   float qs[kD];
-  load_qs(A, i, h, qs);
+  load_qs<TS>(A, i, h, qs);
   float m_run = -INFINITY, s_run = 0.f;
   int c_run = 0;
   float acc[kNV][3];
@@ -104,7 +146,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
     __syncthreads();
     for (int el = half; el < nc; el += 2) {
       const int64_t e = (int64_t)b + c0 + el;
-      const float qk = qk_dot(qs, A.k + ((size_t)ce.j[el] * kH + h) * kD);
+      const float qk = qk_dot(qs, Kp + ((size_t)ce.j[el] * kH + h) * kD);
       a_s[el][h] = ntload(A.gi + e * (2 * kH) + h) * qk;
       coef_s[el][h] = ntload(A.gi + e * (2 * kH) + kH + h);   // input head, scaled below
     }
@@ -139,11 +181,11 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
       for (int el = 0; el < nc; ++el) {
         const float w = coef_s[el][hc];
         const float wx = w * ce.dv[el][0], wy = w * ce.dv[el][1], wz = w * ce.dv[el][2];
-        const float* vp = A.v + (size_t)ce.j[el] * kC + t;
+        const TS* vp = Vp + (size_t)ce.j[el] * kC + t;
         const size_t vs = (size_t)A.n_rows * kC;
         float vv[kNV];
 #pragma unroll
-        for (int r = 0; r < kNV; ++r) vv[r] = vp[r * vs];
+        for (int r = 0; r < kNV; ++r) vv[r] = f32(vp[r * vs]);
 #pragma unroll
         for (int r = 0; r < kNV; ++r) {
           acc[r][0] = fmaf(vv[r], wx, acc[r][0]);
@@ -167,10 +209,10 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, float* __res
   for (int q = 0; q < kNT; ++q) o[q] = 0.f;
 #pragma unroll
   for (int z = 0; z < kTpNnz; ++z) o[kTp[z].t] = fmaf(kTp[z].c, acc[kTp[z].r][kTp[z].k], o[kTp[z].t]);
-  float* op = out + (size_t)i * kC + t;
+  TS* op = out + (size_t)i * kC + t;
   const size_t os = (size_t)A.n_rows * kC;
 #pragma unroll
-  for (int q = 0; q < kNT; ++q) ntstore(o[q] * inv, op + q * os);
+  for (int q = 0; q < kNT; ++q) store_act(o[q] * inv, op + q * os);
 }
 
 // dA[r][k] = sum_t T[t][r][k] g[t] for one channel
@@ -187,8 +229,9 @@ __device__ __forceinline__ void tp_transpose(const float (&g)[kNT], float (&dA)[
 // Per-edge sums over the 256 channels (dL/d dvec) reduce by DPP within rows
 // of 16 lanes and then over the 16 row partials in LDS; the per-head dL/dw
 // adds the head's two channels (h, h + 128) in LDS.
-__global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const float* __restrict__ G,
-                                                      const float* __restrict__ O, const float* __restrict__ mrow,
+template <typename TS>
+__global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const TS* __restrict__ G,
+                                                      const TS* __restrict__ O, const float* __restrict__ mrow,
                                                       const float* __restrict__ srow, const int32_t* __restrict__ cnt,
                                                       float* __restrict__ dgi, float* __restrict__ ddv,
                                                       float* __restrict__ dd, float* __restrict__ dq,
@@ -218,8 +261,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
     float sdot = 0.f;
 #pragma unroll
     for (int z = 0; z < kNT; ++z) {
-      g[z] = G[(size_t)i * kC + z * os + c];
-      sdot = fmaf(g[z], O[(size_t)i * kC + z * os + c], sdot);
+      g[z] = f32(G[(size_t)i * kC + z * os + c]);
+      sdot = fmaf(g[z], f32(O[(size_t)i * kC + z * os + c]), sdot);
     }
     tp_transpose(g, dA);
     if (half) gdot_s[h] = sdot;
@@ -235,8 +278,10 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
       head_dmc[h] = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
     }
   }
+  const TS* __restrict__ Kp = static_cast<const TS*>(A.k);
+  const TS* __restrict__ Vp = static_cast<const TS*>(A.v);
   float qs[kD];
-  load_qs(A, i, h, qs);
+  load_qs<TS>(A, i, h, qs);
   float dqa[kD];
 #pragma unroll
   for (int d = 0; d < kD; ++d) dqa[d] = 0.f;
@@ -248,7 +293,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
     // ---- phase 1: recompute logits and final weights (thread per head, edge parity)
     for (int el = half; el < nc; el += 2) {
       const int64_t e = (int64_t)b + c0 + el;
-      const float qk = qk_dot(qs, A.k + ((size_t)ce.j[el] * kH + h) * kD);
+      const float qk = qk_dot(qs, Kp + ((size_t)ce.j[el] * kH + h) * kD);
       const float a = A.gi[e * (2 * kH) + h] * qk;
       a_s[el][h] = a;
       qk_s[el][h] = qk;
@@ -261,7 +306,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
     __syncthreads();
     // ---- phase 2: transposed aggregation, thread per channel, two edges per step
     {
-      const float* vb = A.v + c;
+      const TS* vb = Vp + c;
       auto edge = [&](int el, const float (&vr)[kNV]) {
         float u0 = 0.f, u1 = 0.f, u2 = 0.f;
 #pragma unroll
@@ -284,22 +329,22 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
       };
       int el = 0;
       for (; el + 1 < nc; el += 2) {
-        const float* v0 = vb + (size_t)ce.j[el] * kC;
-        const float* v1 = vb + (size_t)ce.j[el + 1] * kC;
+        const TS* v0 = vb + (size_t)ce.j[el] * kC;
+        const TS* v1 = vb + (size_t)ce.j[el + 1] * kC;
         float va[kNV], vc[kNV];
 #pragma unroll
         for (int r = 0; r < kNV; ++r) {
-          va[r] = v0[r * os];
-          vc[r] = v1[r * os];
+          va[r] = f32(v0[r * os]);
+          vc[r] = f32(v1[r * os]);
         }
         edge(el, va);
         edge(el + 1, vc);
       }
       if (el < nc) {
-        const float* v0 = vb + (size_t)ce.j[el] * kC;
+        const TS* v0 = vb + (size_t)ce.j[el] * kC;
         float va[kNV];
 #pragma unroll
-        for (int r = 0; r < kNV; ++r) va[r] = v0[r * os];
+        for (int r = 0; r < kNV; ++r) va[r] = f32(v0[r * os]);
         edge(el, va);
       }
     }
@@ -329,9 +374,10 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
       dgi[e * (2 * kH) + h] = dgate;
       dgi[e * (2 * kH) + kH + h] = dih;
       dqk_out[e * kH + h] = dqk;
-      const float* kp = A.k + ((size_t)ce.j[el] * kH + h) * kD;
+      float kv[kD];
+      load8(Kp + ((size_t)ce.j[el] * kH + h) * kD, kv);
 #pragma unroll
-      for (int d = 0; d < kD; ++d) dqa[d] = fmaf(dqk, kp[d], dqa[d]);
+      for (int d = 0; d < kD; ++d) dqa[d] = fmaf(dqk, kv[d], dqa[d]);
       float ddist = fmaf(dpv, ce.dp[el], dR);
       ddist = wave_sum(ddist);
       if (lane == 0) dd_s[el][(t & (kH - 1)) >> 6] = ddist;
@@ -368,7 +414,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const fl
 // edge id) -> dv_j and dk_j.  Edge metadata of a 32-edge chunk is staged in LDS
 // so the per-edge gathers of grad rows do not wait on index loads; two edges
 // are processed per iteration to overlap their 20-row gathers.
-__global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const float* __restrict__ G,
+template <typename TS>
+__global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const TS* __restrict__ G,
                                                       const float* __restrict__ w_e, const float* __restrict__ dqk_e,
                                                       float* __restrict__ dv_out, float* __restrict__ dk_out) {
   constexpr int CC = 32;
@@ -386,6 +433,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const fl
   for (int r = 0; r < kNV; ++r) av[r] = 0.f;
   float ak[4] = {0.f, 0.f, 0.f, 0.f};
   const int p0 = A.key_ptr[j], p1 = A.key_ptr[j + 1];
+  const TS* __restrict__ Qp = static_cast<const TS*>(A.q);
   for (int c0 = p0; c0 < p1; c0 += CC) {
     const int nc = min(CC, p1 - c0);
     if (t < nc) {
@@ -403,93 +451,94 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const fl
       cq[el][h] = ntload(dqk_e + e * kH + h);
     }
     __syncthreads();
+    // dv_j[r] += sum_k dA[r][k] (w dvec_k), dA = T^T G_i[:, c]; dk_j += dqk q_i (scaled by 1/sqrt(D) once at the end)
+    auto edge = [&](int el, const float (&g)[kNT], const float (&q)[4]) {
+      float dA[kNV][3];
+      tp_transpose(g, dA);
+      const float w = cw[el][hc];
+      const float wx = w * cdv[el][0], wy = w * cdv[el][1], wz = w * cdv[el][2];
+#pragma unroll
+      for (int r = 0; r < kNV; ++r) av[r] = fmaf(dA[r][2], wz, fmaf(dA[r][1], wy, fmaf(dA[r][0], wx, av[r])));
+      const float dqv = cq[el][hk];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) ak[d] = fmaf(dqv, q[d], ak[d]);
+    };
     int el = 0;
     for (; el + 1 < nc; el += 2) {
       const int i0 = ci[el], i1 = ci[el + 1];
       float g0[kNT], g1[kNT];
 #pragma unroll
       for (int z = 0; z < kNT; ++z) {
-        g0[z] = G[(size_t)i0 * kC + z * os + c];
-        g1[z] = G[(size_t)i1 * kC + z * os + c];
+        g0[z] = ld_word(G + (size_t)i0 * kC + z * os + c);
+        g1[z] = ld_word(G + (size_t)i1 * kC + z * os + c);
       }
-      const float* q0 = A.q + ((size_t)i0 * kH + hk) * kD + d0;
-      const float* q1 = A.q + ((size_t)i1 * kH + hk) * kD + d0;
       float qa[4], qb[4];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) { qa[d] = q0[d]; qb[d] = q1[d]; }
-      float dA[kNV][3];
-      tp_transpose(g0, dA);
-      {
-        const float w = cw[el][hc];
-        const float x = cdv[el][0], y = cdv[el][1], zz = cdv[el][2];
-#pragma unroll
-        for (int r = 0; r < kNV; ++r) av[r] = fmaf(w, dA[r][0] * x + dA[r][1] * y + dA[r][2] * zz, av[r]);
-      }
-      tp_transpose(g1, dA);
-      {
-        const float w = cw[el + 1][hc];
-        const float x = cdv[el + 1][0], y = cdv[el + 1][1], zz = cdv[el + 1][2];
-#pragma unroll
-        for (int r = 0; r < kNV; ++r) av[r] = fmaf(w, dA[r][0] * x + dA[r][1] * y + dA[r][2] * zz, av[r]);
-      }
-      const float dq0 = cq[el][hk], dq1 = cq[el + 1][hk];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        ak[d] = fmaf(dq0, qa[d] / A.q_div, ak[d]);
-        ak[d] = fmaf(dq1, qb[d] / A.q_div, ak[d]);
-      }
+      load4(Qp + ((size_t)i0 * kH + hk) * kD + d0, qa);
+      load4(Qp + ((size_t)i1 * kH + hk) * kD + d0, qb);
+      edge(el, g0, qa);
+      edge(el + 1, g1, qb);
     }
     if (el < nc) {
       const int i0 = ci[el];
       float g0[kNT];
 #pragma unroll
-      for (int z = 0; z < kNT; ++z) g0[z] = G[(size_t)i0 * kC + z * os + c];
-      float dA[kNV][3];
-      tp_transpose(g0, dA);
-      const float w = cw[el][hc];
-      const float x = cdv[el][0], y = cdv[el][1], zz = cdv[el][2];
-#pragma unroll
-      for (int r = 0; r < kNV; ++r) av[r] = fmaf(w, dA[r][0] * x + dA[r][1] * y + dA[r][2] * zz, av[r]);
-      const float dq0 = cq[el][hk];
-      const float* q0 = A.q + ((size_t)i0 * kH + hk) * kD + d0;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) ak[d] = fmaf(dq0, q0[d] / A.q_div, ak[d]);
+      for (int z = 0; z < kNT; ++z) g0[z] = ld_word(G + (size_t)i0 * kC + z * os + c);
+      float qa[4];
+      load4(Qp + ((size_t)i0 * kH + hk) * kD + d0, qa);
+      edge(el, g0, qa);
     }
     __syncthreads();
   }
 #pragma unroll
   for (int r = 0; r < kNV; ++r) ntstore(av[r], dv_out + (size_t)j * kC + r * os + c);
 #pragma unroll
-  for (int d = 0; d < 4; ++d) ntstore(ak[d], dk_out + ((size_t)j * kH + hk) * kD + d0 + d);
+  for (int d = 0; d < 4; ++d) ntstore(ak[d] / A.q_div, dk_out + ((size_t)j * kH + hk) * kD + d0 + d);
 }
 
 }  // namespace e2v2
 
 using namespace e2v2;
 
-E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, float* out, float* mrow, float* srow, int32_t* cnt,
+E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, float* srow, int32_t* cnt,
                            hipStream_t s) {
   const e2v2_attn_args& A = *args;
   E2V2_REQUIRE(A.n_heads == kH && A.head_dim == kD && A.channels == kC,
                "attn_fwd: built for H=%d D=%d C=%d, got H=%d D=%d C=%d", kH, kD, kC, A.n_heads, A.head_dim,
                A.channels);
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_attn_fwd, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, out, mrow, srow, cnt);
+  const dim3 grid(xcd_grid(A.n_rows));
+  if (A.act_bf16) {
+    hipLaunchKernelGGL(k_attn_fwd<__bf16>, grid, dim3(256), 0, s, A, static_cast<__bf16*>(out), mrow, srow, cnt);
+  } else {
+    hipLaunchKernelGGL(k_attn_fwd<float>, grid, dim3(256), 0, s, A, static_cast<float*>(out), mrow, srow, cnt);
+  }
   E2V2_LAUNCHED("k_attn_fwd");
   return 0;
 }
 
-E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const float* grad_out, const float* out, const float* mrow,
+template <typename TS>
+static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, const float* mrow, const float* srow,
+                           const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
+                           float* w_edge, float* dqk_edge, hipStream_t s) {
+  const dim3 grid(xcd_grid(A.n_rows));
+  hipLaunchKernelGGL(k_attn_bwd_row<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, dgi, ddvec, ddist, dq,
+                     w_edge, dqk_edge);
+  E2V2_LAUNCHED("k_attn_bwd_row");
+  hipLaunchKernelGGL(k_attn_bwd_col<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
+  E2V2_LAUNCHED("k_attn_bwd_col");
+  return 0;
+}
+
+E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, const void* out, const float* mrow,
                            const float* srow, const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq,
                            float* dk, float* dv, float* w_edge, float* dqk_edge, hipStream_t s) {
   const e2v2_attn_args& A = *args;
   E2V2_REQUIRE(A.n_heads == kH && A.head_dim == kD && A.channels == kC,
                "attn_bwd: built for H=%d D=%d C=%d", kH, kD, kC);
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_attn_bwd_row, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, grad_out, out, mrow, srow, cnt, dgi, ddvec,
-                     ddist, dq, w_edge, dqk_edge);
-  E2V2_LAUNCHED("k_attn_bwd_row");
-  hipLaunchKernelGGL(k_attn_bwd_col, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, grad_out, w_edge, dqk_edge, dv, dk);
-  E2V2_LAUNCHED("k_attn_bwd_col");
-  return 0;
+  if (A.act_bf16)
+    return attn_bwd_launch(A, static_cast<const __bf16*>(grad_out), static_cast<const __bf16*>(out), mrow, srow,
+                           cnt, dgi, ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
+  return attn_bwd_launch(A, static_cast<const float*>(grad_out), static_cast<const float*>(out), mrow, srow, cnt,
+                         dgi, ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
 }

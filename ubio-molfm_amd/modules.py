@@ -53,9 +53,12 @@ def _bf(a):
 
 def _mm_into(a, b, out):
     """out = a @ b for an fp32 activation a and a weight operand b.  With a bf16
-    weight the activation is rounded to bf16 and the product is accumulated and
-    stored in fp32 (bf16 MFMA operands, fp32 result)."""
+    weight the activation is rounded to bf16 and the product is accumulated in
+    fp32 and stored in out's dtype (bf16 MFMA operands; fp32, or a bf16
+    activation consumed only by a bf16 kernel)."""
     if b.dtype == BF16:
+        if out.dtype == BF16:
+            return torch.mm(_bf(a), b, out=out)
         return torch.mm(_bf(a), b, out_dtype=torch.float32, out=out)
     return torch.mm(a, b, out=out)
 
@@ -177,7 +180,7 @@ class SO2OutFn(torch.autograd.Function):
     def forward(ctx, so2, res, blocks, Wp, bp):
         so2 = so2.contiguous(); res = res.contiguous()
         _, N, C = so2.shape
-        t = so2.new_empty(9, N, C)
+        t = so2.new_empty(9, N, C, dtype=torch.float32)
         sa = _bf(so2) if Wp.dtype == BF16 else so2
         o = 0
         for lst in blocks:
@@ -190,7 +193,7 @@ class SO2OutFn(torch.autograd.Function):
                 else:
                     _addmm_into(tv, xin, Wt, out=tv)
             o += nr
-        y = so2.new_empty(9, N, Wp.shape[1])
+        y = so2.new_empty(9, N, Wp.shape[1], dtype=torch.float32)
         ta = _bf(t) if Wp.dtype == BF16 else t
         for l in range(3):
             a, b = l * l, (l + 1) ** 2
@@ -199,7 +202,7 @@ class SO2OutFn(torch.autograd.Function):
         y[0].add_(bp)
         ctx.blocks = blocks
         ctx.save_for_backward(Wp)
-        ctx.shape = so2.shape
+        ctx.shape, ctx.so2_dtype = so2.shape, so2.dtype
         return y
 
     @staticmethod
@@ -214,7 +217,7 @@ class SO2OutFn(torch.autograd.Function):
         for l in range(3):
             a, b = l * l, (l + 1) ** 2
             _mm_into(ga[a:b].view(-1, O), Wp[l], out=gt[a:b].view(-1, C))
-        gso2 = gy.new_empty(ctx.shape)
+        gso2 = gy.new_empty(ctx.shape, dtype=ctx.so2_dtype)
         gta = _bf(gt) if bf else gt
         o = 0
         for lst in ctx.blocks:
@@ -644,7 +647,7 @@ class E2AttentionArbOrder_sparse(nn.Module):
         v = self.proj_value(x, bf16)
         packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding, bf16)
         so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
-                                packed, ctx.rc, math.sqrt(q.shape[-1]))
+                                packed, ctx.rc, math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
         if res is None:
             res = torch.zeros_like(x)
         pf = self.proj_first

@@ -203,11 +203,16 @@ class AttentionFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, dvec, dist, nl: NeighborList, node_type, rbf_offset, rbf_coeff: float, packed,
-                rc: float, q_div: float):
+                rc: float, q_div: float, act_dtype=torch.float32):
+        """act_dtype: storage of q, k, v and of the output rows (torch.float32, or
+        torch.bfloat16 in the bf16 mode: half the gather traffic, fp32 math)."""
         _need_cuda(q, k, v, dvec, dist)
+        if act_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"attention activations must be float32 or bfloat16, got {act_dtype}")
         dev = q.device
         E, N = nl.n_edges, nl.n_atoms
-        q = q.float().contiguous(); k = k.float().contiguous(); v = v.float().contiguous()
+        q = q.to(act_dtype).contiguous(); k = k.to(act_dtype).contiguous(); v = v.to(act_dtype).contiguous()
+        bf = int(act_dtype == torch.bfloat16)
         gi = torch.empty(max(E, 1), 256, dtype=torch.float32, device=dev)
         sn, sr = mlp_save_buffers(1, E, dev)
         margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
@@ -215,14 +220,15 @@ class AttentionFn(torch.autograd.Function):
         args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
                              nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                              q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(q_div), float(rc),
-                             ENV_A, ENV_B, ENV_C)
-        out = torch.empty(20, N, 256, dtype=torch.float32, device=dev)   # m-major
+                             ENV_A, ENV_B, ENV_C, bf)
+        out = torch.empty(20, N, 256, dtype=act_dtype, device=dev)   # m-major
         mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
         _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _p(out), _p(mrow), _p(srow), _p(cnt), _stream(q))
         ctx.save_for_backward(q, k, v, gi, out, mrow, srow, cnt, sn, sr)
         ctx.nl, ctx.margs_src, ctx.rc, ctx.q_div = nl, (node_type, rbf_offset, rbf_coeff, packed), rc, q_div
+        ctx.bf = bf
         return out
 
     @staticmethod
@@ -233,16 +239,16 @@ class AttentionFn(torch.autograd.Function):
         node_type, rbf_offset, rbf_coeff, packed = ctx.margs_src
         dev = q.device
         E, N = nl.n_edges, nl.n_atoms
-        gout = gout.float().contiguous()
+        gout = gout.to(out.dtype).contiguous()
         args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
                              nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                              q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(ctx.q_div),
-                             float(ctx.rc), ENV_A, ENV_B, ENV_C)
+                             float(ctx.rc), ENV_A, ENV_B, ENV_C, ctx.bf)
         f = dict(dtype=torch.float32, device=dev)
         dgi = torch.empty(max(E, 1), 256, **f)
         ddv = torch.empty(max(E, 1), 3, **f)
         dd = torch.empty(max(E, 1), **f)
-        dq = torch.empty_like(q); dk = torch.empty_like(k); dv = torch.empty_like(v)
+        dq = torch.empty(q.shape, **f); dk = torch.empty(k.shape, **f); dv = torch.empty(v.shape, **f)
         w_e = torch.empty(max(E, 1), 128, **f)
         dqk = torch.empty(max(E, 1), 128, **f)
         _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(dgi),
@@ -250,4 +256,4 @@ class AttentionFn(torch.autograd.Function):
         del w_e, dqk
         margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
         _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dgi), _lib.i32(256), _p(dd), _lib.i32(1), _stream(gout))
-        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None
+        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None, None
