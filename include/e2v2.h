@@ -102,7 +102,12 @@ int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, i
 
 /* ---- edge radial MLP --------------------------------------------------- */
 typedef struct e2v2_mlp_weights {
-  const float* w1t;   /* [256][128]  rbf block of Linear1, transposed             */
+  /* Linear1's rbf block as a function of the distance: rtab[n][k][c] =
+     h^k d^k/dd^k (W1[c, 0:256] . rbf(d)) at d = n h, k = 0..3 (float64-built by
+     e2v2_mlp_rbf_table); evaluated by quintic Hermite interpolation.            */
+  const float* rtab;  /* [rtab_n][4][128]                                          */
+  int32_t rtab_n;     /* nodes covering [0, rc]                                     */
+  float rtab_h;       /* node spacing, a power of two                               */
   const float* ttgt;  /* [types][128] target-type block of Linear1 + bias         */
   const float* tsrc;  /* [types][128] source-type block of Linear1                */
   const float* g1; const float* be1;   /* LayerNorm(128)                            */
@@ -111,17 +116,13 @@ typedef struct e2v2_mlp_weights {
   const float* g2; const float* be2;
   const float* w3t;   /* [128][256] Linear3 transposed                            */
   const float* b3;
-  const float* w1;    /* [128][ldw1] Linear1 as stored (rbf block = columns 0..255) */
-  int32_t ldw1;
   const float* w2;    /* [128][128] Linear2 as stored                             */
   const float* w3;    /* [256][128] Linear3 as stored                             */
   /* bf16 operands (compute_bf16 = 1), each as B^T row-major [N][K]:              */
-  const void* w1b;    /* [128][256] rbf block of Linear1 (forward)                */
   const void* w2b;    /* [128][128] Linear2 (forward)                             */
   const void* w3b;    /* [256][128] Linear3 (forward)                             */
   const void* w3tb;   /* [128][256] Linear3^T (backward)                          */
   const void* w2tb;   /* [128][128] Linear2^T (backward)                          */
-  const void* w1rtb;  /* [256][128] rbf block of Linear1, transposed (backward)   */
 } e2v2_mlp_weights;
 
 typedef struct e2v2_mlp_args {
@@ -132,12 +133,19 @@ typedef struct e2v2_mlp_args {
   const int32_t* edge_row;       /* [E] query atom                                 */
   const int32_t* col;            /* [E] source atom                                */
   const int32_t* node_type;      /* [N] atomic numbers                             */
-  const float* rbf_offset;       /* [256] Gaussian centres                         */
-  float rbf_coeff;               /* -0.5 / width^2                                 */
   float* save_n;                 /* [n_mlp][E][256] normalised LN1 | LN2 inputs (written by fwd, read by bwd) */
   float* save_r;                 /* [n_mlp][E][2]   their rstd                                                */
   e2v2_mlp_weights w[E2V2_MAX_MLP];
 } e2v2_mlp_args;
+
+/* Node count and spacing (a power of two, about 0.17 of the Gaussian width) of the
+   rbf-block table of a GaussianSmearing basis exp(rbf_coeff (d - mu)^2) over [0, rc]
+   (module_utils.py:1853-1869). */
+int e2v2_mlp_rbf_table_size(float rc, float rbf_coeff, int32_t* n_nodes, float* h);
+/* rtab [n_nodes][4][128] of Linear1's rbf block w1 [128][ldw1] (columns 0..255) with
+   centres rbf_offset [256]; float64 accumulation. */
+int e2v2_mlp_rbf_table(const float* w1, int ldw1, const float* rbf_offset, float rbf_coeff, int32_t n_nodes,
+                       float h, float* rtab, hipStream_t s);
 
 /* out[e, 256 m + c] for profile m; fills save_n / save_r when they are non-null */
 int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hipStream_t s);

@@ -57,19 +57,15 @@ class _RoundGrad(torch.autograd.Function):
 
 
 def mlp_ref_bf16(d, zi, zj, net, tgt_w, src_w, offset, coeff):
-    """RadialProfile with the rounding points of the bf16 edge kernels: the RBF
-    block, both LayerNorm+SiLU activations and the weights of the three GEMMs
-    are bf16 in the forward; the upstream gradient and the two LayerNorm input
-    gradients are bf16 in the backward; the per-type tables, LayerNorm
-    statistics and every accumulation stay at full precision."""
+    """RadialProfile with the rounding points of the bf16 edge kernels: Linear1
+    is evaluated at full precision (its rbf block comes from an fp32 table), the
+    two LayerNorm+SiLU activations and the weights of Linear2/3 are bf16 in the
+    forward; the upstream gradient and the LayerNorm-2 input gradient are bf16
+    in the backward; LayerNorm statistics, the LayerNorm-1 input gradient and
+    every accumulation stay at full precision."""
     F = torch.nn.functional
     lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
-    K0, e = offset.shape[0], tgt_w.shape[1]
-    W1 = lin1.weight
-    r = _RoundFwd.apply(rbf(d, offset, coeff))
-    y1 = (r @ bf16_round(W1[:, :K0]).t() + (tgt_w[zi] @ W1[:, K0:K0 + e].t() + lin1.bias)
-          + src_w[zj] @ W1[:, K0 + e:K0 + 2 * e].t())
-    y1 = _RoundGrad.apply(y1)
+    y1 = torch.cat([rbf(d, offset, coeff), tgt_w[zi], src_w[zj]], dim=-1) @ lin1.weight.t() + lin1.bias
     a1 = _RoundFwd.apply(F.silu(F.layer_norm(y1, ln1.normalized_shape, ln1.weight, ln1.bias, ln1.eps)))
     y2 = _RoundGrad.apply(a1 @ bf16_round(lin2.weight).t() + lin2.bias)
     a2 = _RoundFwd.apply(F.silu(F.layer_norm(y2, ln2.normalized_shape, ln2.weight, ln2.bias, ln2.eps)))

@@ -40,9 +40,10 @@ def test_mlp_forward_backward(pkg, cuda):
     tgt = torch.nn.Embedding(300, 256); src = torch.nn.Embedding(300, 256)
     rb = modules.GaussianSmearing(256, 6.0, 2.0)
     Z = torch.as_tensor(s["Z"], device=cuda).to(torch.int32)
-    packed = [ops.PackedMLP(prof.to(cuda).net, tgt.weight.to(cuda), src.weight.to(cuda))]
+    packed = [ops.PackedMLP(prof.to(cuda).net, tgt.weight.to(cuda), src.weight.to(cuda), rb.offset.to(cuda),
+                            rb.coeff, 6.0)]
     sn, sr = ops.mlp_save_buffers(1, E, cuda)
-    args = ops.mlp_args(nl, Z, rb.offset.to(cuda), rb.coeff, packed, sn, sr)
+    args = ops.mlp_args(nl, Z, packed, sn, sr)
     out = torch.empty(E, 256, device=cuda)
     from ubio_molfm_amd import _lib
     _lib.call("e2v2_mlp_fwd", _lib.C.byref(args), _lib.vp(out.data_ptr()), _lib.i32(256),
@@ -80,9 +81,10 @@ def test_mlp_bf16_forward_backward(pkg, cuda):
     tgt = torch.nn.Embedding(300, 256); src = torch.nn.Embedding(300, 256)
     rb = modules.GaussianSmearing(256, 6.0, 2.0)
     Z = torch.as_tensor(s["Z"], device=cuda).to(torch.int32)
-    packed = [ops.PackedMLP(prof.to(cuda).net, tgt.weight.to(cuda), src.weight.to(cuda), bf16=True)]
+    packed = [ops.PackedMLP(prof.to(cuda).net, tgt.weight.to(cuda), src.weight.to(cuda), rb.offset.to(cuda),
+                            rb.coeff, 6.0, bf16=True)]
     sn, sr = ops.mlp_save_buffers(1, E, cuda)
-    args = ops.mlp_args(nl, Z, rb.offset.to(cuda), rb.coeff, packed, sn, sr)
+    args = ops.mlp_args(nl, Z, packed, sn, sr)
     assert args.compute_bf16 == 1
     st = _lib.vp(torch.cuda.current_stream().cuda_stream)
     out = torch.empty(E, 256, device=cuda)
@@ -113,6 +115,63 @@ def _attn_inputs(nl, cuda, seed=2):
     v = torch.randn(N, 9, 256, generator=g)
     gi = torch.randn(E, 256, generator=g)
     return q, k, v, gi
+
+
+def _hermite5(t):
+    t2, t3, t4, t5 = t * t, t ** 3, t ** 4, t ** 5
+    return (1 - 10 * t3 + 15 * t4 - 6 * t5, t - 6 * t3 + 8 * t4 - 3 * t5, 0.5 * (t2 - 3 * t3 + 3 * t4 - t5),
+            10 * t3 - 15 * t4 + 6 * t5, -4 * t3 + 7 * t4 - 3 * t5, 0.5 * (t3 - 2 * t4 + t5))
+
+
+def test_rbf_block_table(pkg, cuda):
+    """The tabulated rbf block of Linear1 against its float64 closed form: node
+    values and scaled derivatives (to fp32 rounding), and the quintic Hermite
+    interpolant of the value and of the first derivative at 4000 random
+    distances in [0, rc] (evaluated here in float64 from the fp32 table, with
+    the kernel's interval arithmetic) -- relative to the function's scale."""
+    from ubio_molfm_amd import _lib, modules, ops
+    rc = 6.0
+    rb = modules.GaussianSmearing(256, rc, 2.0)
+    torch.manual_seed(5)
+    W1 = (torch.rand(128, 512) - 0.5) * 0.1
+    n, h = ops.rbf_table_size(rc, rb.coeff)
+    assert h == 2.0 ** round(math.log2(h)) and n == math.floor(rc / h) + 2
+    tab = torch.empty(n, 4, 128, device=cuda)
+    W1d, mu = W1.to(cuda).contiguous(), rb.offset.to(cuda).contiguous()
+    _lib.call("e2v2_mlp_rbf_table", _lib.vp(W1d.data_ptr()), _lib.i32(512), _lib.vp(mu.data_ptr()),
+              _lib.f32(rb.coeff), _lib.i32(n), _lib.f32(h), _lib.vp(tab.data_ptr()),
+              _lib.vp(torch.cuda.current_stream().cuda_stream))
+    T = tab.cpu().double().numpy()
+    c = float(np.float32(rb.coeff))
+    Wr = W1[:, :256].double().numpy()
+    m = rb.offset.double().numpy()
+
+    def exact(d):
+        x = d[:, None] - m[None, :]
+        r = np.exp(c * x * x)
+        return r @ Wr.T, (2 * c * x * r) @ Wr.T, ((2 * c + 4 * c * c * x * x) * r) @ Wr.T, \
+            ((12 * c * c * x + 8 * c ** 3 * x ** 3) * r) @ Wr.T
+    dn = np.arange(n) * h
+    f0, f1, f2, f3 = exact(dn)
+    scale = np.abs(f0).max()
+    for k, (fk, hk) in enumerate([(f0, 1), (f1, h), (f2, h * h), (f3, h ** 3)]):
+        err = np.abs(T[:, k, :] - fk * hk).max() / np.abs(fk * hk).max()
+        assert err < 1e-6, (k, err)
+    rng = np.random.default_rng(0)
+    d = np.concatenate([rng.uniform(0, rc, 3998), [0.0, rc]]).astype(np.float32)
+    u = np.minimum(d.astype(np.float32) * np.float32(1.0 / h), np.float32(n - 2))
+    nn_ = np.floor(u).astype(np.int64)
+    t = (u - nn_).astype(np.float64)
+    H = _hermite5(t[:, None])
+    val = (H[0] * T[nn_, 0] + H[1] * T[nn_, 1] + H[2] * T[nn_, 2] + H[3] * T[nn_ + 1, 0] + H[4] * T[nn_ + 1, 1]
+           + H[5] * T[nn_ + 1, 2])
+    der = (H[0] * T[nn_, 1] + H[1] * T[nn_, 2] + H[2] * T[nn_, 3] + H[3] * T[nn_ + 1, 1] + H[4] * T[nn_ + 1, 2]
+           + H[5] * T[nn_ + 1, 3]) / h
+    e0, e1, _, _ = exact(d.astype(np.float64))
+    ev = np.abs(val - e0).max() / scale
+    ed = np.abs(der - e1).max() / np.abs(e1).max()
+    print(f"[rbf table] n={n} h={h} value {ev:.2e} derivative {ed:.2e}", flush=True)
+    assert ev < 1e-6 and ed < 1e-6
 
 
 def _attention_case(pkg, cuda, act_dtype):

@@ -15,7 +15,7 @@ i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 EXPORTS = [
     "e2v2_last_error", "e2v2_version", "e2v2_fill_i32", "e2v2_fill_f32", "e2v2_scan_i32",
     "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose",
-    "e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
+    "e2v2_mlp_rbf_table_size", "e2v2_mlp_rbf_table", "e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
     "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd", "e2v2_gate_bwd",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd",
 ]
@@ -31,15 +31,14 @@ class NbrPlan(C.Structure):
 
 
 class MlpWeights(C.Structure):
-    _fields_ = [("w1t", vp), ("ttgt", vp), ("tsrc", vp), ("g1", vp), ("be1", vp), ("w2t", vp), ("b2", vp),
-                ("g2", vp), ("be2", vp), ("w3t", vp), ("b3", vp), ("w1", vp), ("ldw1", i32), ("w2", vp),
-                ("w3", vp), ("w1b", vp), ("w2b", vp), ("w3b", vp), ("w3tb", vp), ("w2tb", vp), ("w1rtb", vp)]
+    _fields_ = [("rtab", vp), ("rtab_n", i32), ("rtab_h", f32), ("ttgt", vp), ("tsrc", vp), ("g1", vp),
+                ("be1", vp), ("w2t", vp), ("b2", vp), ("g2", vp), ("be2", vp), ("w3t", vp), ("b3", vp), ("w2", vp),
+                ("w3", vp), ("w2b", vp), ("w3b", vp), ("w3tb", vp), ("w2tb", vp)]
 
 
 class MlpArgs(C.Structure):
-    _fields_ = [("n_edges", i64), ("n_mlp", i32), ("compute_bf16", i32), ("dist", vp), ("edge_row", vp), ("col", vp),
-                ("node_type", vp), ("rbf_offset", vp), ("rbf_coeff", f32), ("save_n", vp), ("save_r", vp),
-                ("w", MlpWeights * 3)]
+    _fields_ = [("n_edges", i64), ("n_mlp", i32), ("compute_bf16", i32), ("dist", vp), ("edge_row", vp),
+                ("col", vp), ("node_type", vp), ("save_n", vp), ("save_r", vp), ("w", MlpWeights * 3)]
 
 
 class AttnArgs(C.Structure):

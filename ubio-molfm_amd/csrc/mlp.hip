@@ -2,33 +2,41 @@
 // -> SiLU -> OUT], src/molfm/models/e2former/module_utils.py:2151-2178) fused
 // with the Gaussian RBF of the edge distance (module_utils.py:1853-1869).
 //
-// The first Linear is split: W1 [rbf | tgt | src] x = W1r rbf + (W1t tgt[z_i] + b1)
-// + W1s src[z_j]; the two type terms arrive as per-type tables.  The RBF tile
-// lives in LDS only; the MLP runs as MFMA GEMMs on 32-edge tiles (fp32
-// 16x16x4, or bf16 16x16x32 operands with fp32 accumulation).  The forward saves
-// the normalised LayerNorm inputs (n1, n2) and their rstd; the backward uses
-// them (no recompute) and returns only dL/d(distance).
+// Linear1 splits as W1 [rbf | tgt | src] x = W1r rbf(d) + (W1t tgt[z_i] + b1) +
+// W1s src[z_j].  The type terms are per-type tables.  W1r rbf(d) depends on the
+// scalar distance alone: it is tabulated per profile with its first three
+// derivatives (float64, node spacing h a power of two, about 0.17 of the
+// Gaussian width) and evaluated by quintic Hermite interpolation -- the
+// interpolation error, ~f^(6) h^6 / 46080, is ~1e-8 of the values, below the
+// fp32 rounding of the 256-term product it replaces.  The backward's
+// dL/dd = sum_c dz1[c] d/dd (W1r rbf(d))[c] is a 128-term dot with the
+// interpolated derivative.  Linear2 and Linear3 run as MFMA GEMMs on 32-edge
+// tiles (fp32 16x16x4, or bf16 16x16x32 operands with fp32 accumulation).  The
+// forward saves the normalised LayerNorm inputs (n1, n2) and their rstd; the
+// backward uses them (no recompute) and returns only dL/d(distance).
 //
-// Latency structure: each tile is a chain of three GEMMs separated by
-// LayerNorms, so every global access on that chain is issued a stage ahead of
-// its use.  LayerNorm affine parameters live in LDS for the whole block; the
-// bf16 kernels load a GEMM's entire per-wave B panel into registers while the
-// previous stage computes; the backward prefetches the saved LayerNorm inputs
-// before the GEMM whose output they normalise.
+// Latency structure: each tile is a chain of GEMMs separated by LayerNorms, so
+// every global access on that chain is issued a stage ahead of its use.
+// LayerNorm affine parameters live in LDS for the whole block; the bf16 kernels
+// load a GEMM's entire per-wave B panel into registers while the previous stage
+// computes; the backward prefetches the saved LayerNorm inputs before the GEMM
+// whose output they normalise.
+#include <cmath>
+
 #include "common.h"
 #include "../../include/e2v2.h"
 
 namespace e2v2 {
 
 constexpr int kT = 32;          // edges per tile
-constexpr int kK0 = 256;        // rbf basis
 constexpr int kH = 128;         // hidden width
 constexpr int kLdX = 258;       // fp32 LDS row stride for K=256 tiles (== 2 mod 32: conflict-free A reads)
 constexpr int kLdY = 130;       // fp32 LDS row stride for K=128 tiles (== 2 mod 32)
 constexpr int kLdXb = 264;      // bf16 row stride of K=256 tiles (16-byte aligned rows)
 constexpr int kLdYb = 136;      // bf16 row stride of K=128 tiles
 constexpr int kPF = 8;          // fp32 GEMM: k-steps (of 4) per register-prefetched B chunk
-constexpr float kFarDist = 1e18f;  // distance of padding rows: finite, and its RBF row is exactly 0
+constexpr int kTabRow = 4 * kH; // floats per table node: value and h, h^2, h^3 scaled derivatives
+constexpr float kFarDist = 1e18f;  // distance of padding rows (finite)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -94,22 +102,6 @@ __device__ __forceinline__ void gemm32(const float* A, int lda, const float* __r
   const float* A0 = A + li * lda;
   const float* A1 = A + (16 + li) * lda;
   gemm32f<K, N>([&](int k, float& a0, float& a1) { a0 = A0[k]; a1 = A1[k]; }, B, ldb, acc);
-}
-
-// A = the RBF tile exp(coeff (d_row - mu_k)^2), generated in registers: the
-// exponentials of a k-step issue under the previous k-step's MFMAs, and the
-// tile needs no LDS.
-template <int N>
-__device__ __forceinline__ void gemm32_rbf(float d0, float d1, const float* mu_s, float c2,
-                                           const float* __restrict__ B, int ldb, floatx4 (&acc)[2][N / 64]) {
-  gemm32f<kK0, N>(
-      [&](int k, float& a0, float& a1) {
-        const float mu = mu_s[k];
-        const float x0 = d0 - mu, x1 = d1 - mu;
-        a0 = fexp2(c2 * (x0 * x0));
-        a1 = fexp2(c2 * (x1 * x1));
-      },
-      B, ldb, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -284,7 +276,7 @@ __device__ __forceinline__ void ln_silu_bwd_rows(const float* Y, int ldy, OutT* 
 
 // ---------------------------------------------------------------------------
 struct TileEdges {
-  alignas(16) float d[kT];   // padding rows hold kFarDist
+  float d[kT];          // padding rows hold kFarDist
   int zi[kT], zj[kT];
 };
 
@@ -299,52 +291,112 @@ __device__ __forceinline__ void load_tile_edges(const e2v2_mlp_args& A, int64_t 
   }
 }
 
-// rbf tile: X[r][k] = exp(coeff * (d_r - mu_k)^2); thread t owns basis k = t
-template <typename T>
-__device__ __forceinline__ void rbf_tile(const TileEdges& te, float mu, float c2, T* X, int ldx) {
-  const int k = threadIdx.x;
+// ---------------------------------------------------------------------------
+// Linear1's rbf block from its table.  Quintic Hermite basis on t in [0, 1]:
+// node values and h-, h^2-scaled derivatives at both ends.
+struct Hermite5 {
+  float a0, a1, a2, b0, b1, b2;
+};
+
+__device__ __forceinline__ Hermite5 hermite5(float t) {
+  const float t2 = t * t, t3 = t2 * t, t4 = t3 * t, t5 = t4 * t;
+  Hermite5 H;
+  H.a0 = 1.f - 10.f * t3 + 15.f * t4 - 6.f * t5;
+  H.a1 = t - 6.f * t3 + 8.f * t4 - 3.f * t5;
+  H.a2 = 0.5f * (t2 - 3.f * t3 + 3.f * t4 - t5);
+  H.b0 = 10.f * t3 - 15.f * t4 + 6.f * t5;
+  H.b1 = -4.f * t3 + 7.f * t4 - 3.f * t5;
+  H.b2 = 0.5f * (t3 - 2.f * t4 + t5);
+  return H;
+}
+
+// Interval of distance d: d / h is exact (h is a power of two), so are its floor
+// and fraction; padding rows clamp to the last interval.
+__device__ __forceinline__ const float* table_interval(const e2v2_mlp_weights& W, float d, float& t) {
+  const float u = fminf(d * (1.0f / W.rtab_h), (float)(W.rtab_n - 2));
+  const float fn = floorf(u);
+  t = u - fn;
+  return W.rtab + (size_t)(int)fn * kTabRow;
+}
+
+// Y[row][c] = W1r rbf(d_row) + ttgt[z_i][c] + tsrc[z_j][c] (the pre-LayerNorm
+// activation of Linear1); thread t owns row t/8 and 16 consecutive columns.
+__device__ __forceinline__ void linear1_rows(const e2v2_mlp_weights& W, const TileEdges& te, float* Y, int ldy) {
+  const int row = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * 16;
+  float t;
+  const float* p = table_interval(W, te.d[row], t) + c0;
+  const Hermite5 H = hermite5(t);
+  const float* tt = W.ttgt + te.zi[row] * kH + c0;
+  const float* ts = W.tsrc + te.zj[row] * kH + c0;
+  float* y = Y + row * ldy + c0;
 #pragma unroll
-  for (int r4 = 0; r4 < kT / 4; ++r4) {
-    const float4 d4 = reinterpret_cast<const float4*>(te.d)[r4];
-    const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+  for (int q = 0; q < 4; ++q) {
+    const floatx4 f0 = reinterpret_cast<const floatx4*>(p + 4 * q)[0];
+    const floatx4 f1 = reinterpret_cast<const floatx4*>(p + kH + 4 * q)[0];
+    const floatx4 f2 = reinterpret_cast<const floatx4*>(p + 2 * kH + 4 * q)[0];
+    const floatx4 g0 = reinterpret_cast<const floatx4*>(p + kTabRow + 4 * q)[0];
+    const floatx4 g1 = reinterpret_cast<const floatx4*>(p + kTabRow + kH + 4 * q)[0];
+    const floatx4 g2 = reinterpret_cast<const floatx4*>(p + kTabRow + 2 * kH + 4 * q)[0];
+    const floatx4 a = reinterpret_cast<const floatx4*>(tt + 4 * q)[0];
+    const floatx4 b = reinterpret_cast<const floatx4*>(ts + 4 * q)[0];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = dv[i] - mu;
-      X[(4 * r4 + i) * ldx + k] = (T)fexp2(c2 * (x * x));
+      const float f = H.a0 * f0[i] + H.a1 * f1[i] + H.a2 * f2[i] + H.b0 * g0[i] + H.b1 * g1[i] + H.b2 * g2[i];
+      y[4 * q + i] = f + a[i] + b[i];
     }
   }
 }
 
-// Per-type table values of GEMM 1's epilogue, loaded ahead of the GEMM
-struct TypeTerms {
-  float t[2][4][2];
-};
-
-__device__ __forceinline__ void load_type_terms(const float* __restrict__ ttgt, const float* __restrict__ tsrc,
-                                                const TileEdges& te, TypeTerms& tt) {
-  const int c0 = acc_col0<kH>();
+// sum_c Z[row][c] d/dd (W1r rbf(d_row))[c], complete in each of the row's 8 threads
+__device__ __forceinline__ float linear1_dd(const e2v2_mlp_weights& W, const TileEdges& te, const float* Z, int ldz) {
+  const int row = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * 16;
+  float t;
+  const float* p = table_interval(W, te.d[row], t) + c0;
+  const Hermite5 H = hermite5(t);
+  const float* z = Z + row * ldz + c0;
+  float s = 0.f;
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int q = 0; q < 4; ++q) {
+    const floatx4 f1 = reinterpret_cast<const floatx4*>(p + kH + 4 * q)[0];
+    const floatx4 f2 = reinterpret_cast<const floatx4*>(p + 2 * kH + 4 * q)[0];
+    const floatx4 f3 = reinterpret_cast<const floatx4*>(p + 3 * kH + 4 * q)[0];
+    const floatx4 g1 = reinterpret_cast<const floatx4*>(p + kTabRow + kH + 4 * q)[0];
+    const floatx4 g2 = reinterpret_cast<const floatx4*>(p + kTabRow + 2 * kH + 4 * q)[0];
+    const floatx4 g3 = reinterpret_cast<const floatx4*>(p + kTabRow + 3 * kH + 4 * q)[0];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = acc_row(rt, r);
-      const float* pt = ttgt + te.zi[row] * kH + c0;
-      const float* ps = tsrc + te.zj[row] * kH + c0;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) tt.t[rt][r][ct] = pt[ct * 16] + ps[ct * 16];
+    for (int i = 0; i < 4; ++i) {
+      const float hd = H.a0 * f1[i] + H.a1 * f2[i] + H.a2 * f3[i] + H.b0 * g1[i] + H.b1 * g2[i] + H.b2 * g3[i];
+      s = fmaf(z[4 * q + i], hd, s);
     }
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 4, 64);
+  return s * (1.0f / W.rtab_h);
 }
 
-__device__ __forceinline__ void store_gemm1(const floatx4 (&acc)[2][2], const TypeTerms& tt, float* Y, int ldy) {
-  const int c0 = acc_col0<kH>();
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float* y = Y + acc_row(rt, r) * ldy + c0;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) y[ct * 16] = acc[rt][ct][r] + tt.t[rt][r][ct];
-    }
+// Table builder: one block per node n, thread c; float64 sums over the 256 centres of
+// h^k d^k/dd^k exp(c (d - mu)^2) W1r[c][mu] at d = n h.
+__global__ __launch_bounds__(kH) void k_rbf_table(const float* __restrict__ w1, int ldw1,
+                                                  const float* __restrict__ mu, float coeff, float h,
+                                                  float* __restrict__ rtab) {
+  const int n = blockIdx.x, c = threadIdx.x;
+  const double d = (double)n * (double)h, cf = (double)coeff, hh = (double)h;
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  for (int j = 0; j < 256; ++j) {
+    const double x = d - (double)mu[j];
+    const double r = exp(cf * x * x);
+    const double w = (double)w1[(size_t)c * ldw1 + j];
+    s0 += w * r;
+    s1 += w * (2.0 * cf * x) * r;
+    s2 += w * (2.0 * cf + 4.0 * cf * cf * x * x) * r;
+    s3 += w * (12.0 * cf * cf * x + 8.0 * cf * cf * cf * x * x * x) * r;
+  }
+  float* o = rtab + (size_t)n * kTabRow + c;
+  o[0] = (float)s0;
+  o[kH] = (float)(hh * s1);
+  o[2 * kH] = (float)(hh * hh * s2);
+  o[3 * kH] = (float)(hh * hh * hh * s3);
 }
 
 // GEMM-3 epilogue: out[e0 + row][m * 256 + c] = acc + b3[c] for the valid rows
@@ -364,74 +416,26 @@ __device__ __forceinline__ void store_out(const floatx4 (&acc)[2][4], const floa
     }
 }
 
-// dd += sum_c drbf[row][c] * d rbf_c / dd over this lane's 4 basis columns
-__device__ __forceinline__ void accumulate_dd(const floatx4 (&acc)[2][4], const TileEdges& te, const float (&mu)[4],
-                                              float c2, float coeff2, float (&dd_lane)[2][4]) {
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float d = te.d[acc_row(rt, r)];
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const float x = d - mu[ct];
-        dd_lane[rt][r] += acc[rt][ct][r] * fexp2(c2 * (x * x)) * (coeff2 * x);
-      }
-    }
-}
-
-// Row sums of dd_lane over the block's 4 waves and 16 lanes -> dd[e0 + row]
-__device__ __forceinline__ void reduce_dd(float (&dd_lane)[2][4], float (*part)[kT], float* __restrict__ dd,
-                                          int64_t e0, int nvalid, int accumulate) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = dd_lane[rt][r];
-      v += __shfl_xor(v, 1, 64);
-      v += __shfl_xor(v, 2, 64);
-      v += __shfl_xor(v, 4, 64);
-      v += __shfl_xor(v, 8, 64);
-      if ((lane & 15) == 0) part[wave][acc_row(rt, r)] = v;
-    }
-  __syncthreads();
-  if (threadIdx.x < nvalid) {
-    const float v = part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] + part[3][threadIdx.x];
-    const int64_t e = e0 + threadIdx.x;
-    dd[e] = accumulate ? dd[e] + v : v;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // fp32 kernels
 __global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
   extern __shared__ float sm[];
-  float* Y = sm;                    // [32][130]: GEMM-1/2 outputs, LayerNorm in place
+  float* Y = sm;                    // [32][130]: Linear1/2 outputs, LayerNorm in place
   __shared__ TileEdges te;
   __shared__ LnParams lp;
-  __shared__ float mu_s[kK0];
   const int m = blockIdx.y;
   const e2v2_mlp_weights& W = A.w[m];
   const int64_t e0 = (int64_t)blockIdx.x * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   float* sn = A.save_n ? A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH) : nullptr;
   float* sr = A.save_r ? A.save_r + ((size_t)m * A.n_edges + e0) * 2 : nullptr;
-  mu_s[threadIdx.x] = A.rbf_offset[threadIdx.x];
   float b2[2], b3[4];
   load_bias<kH>(W.b2, b2);
   load_bias<256>(W.b3, b3);
   load_tile_edges(A, e0, te);
   load_ln_params(W, lp);
   __syncthreads();
-  TypeTerms tt;
-  load_type_terms(W.ttgt, W.tsrc, te, tt);
-  {
-    const int li = threadIdx.x & 15;
-    floatx4 acc[2][2];
-    gemm32_rbf<kH>(te.d[li], te.d[16 + li], mu_s, A.rbf_coeff * kLog2e, W.w1t, kH, acc);
-    store_gemm1(acc, tt, Y, kLdY);
-  }
+  linear1_rows(W, te, Y, kLdY);
   __syncthreads();
   ln_silu_rows(Y, kLdY, Y, kLdY, lp.g1, lp.b1, sn, 2 * kH, sr, 2, nvalid);
   __syncthreads();
@@ -456,20 +460,11 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
   float* Y = sm;
   __shared__ TileEdges te;
   __shared__ LnParams lp;
-  __shared__ float part[4][kT];
   const int64_t e0 = (int64_t)blockIdx.x * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
-  const float c2 = A.rbf_coeff * kLog2e, coeff2 = 2.0f * A.rbf_coeff;
-  float mu[4];
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) mu[ct] = A.rbf_offset[acc_col0<256>() + ct * 16];
   const float zero2[2] = {0.f, 0.f};
   load_tile_edges(A, e0, te);
-  float dd_lane[2][4];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) dd_lane[rt][r] = 0.f;
+  float dd_row = 0.f;
   for (int m = 0; m < A.n_mlp; ++m) {
     const e2v2_mlp_weights& W = A.w[m];
     const float* sn = A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH);
@@ -505,14 +500,14 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
     __syncthreads();
     ln_silu_bwd_rows(Y, kLdY, Y, kLdY, s1, lp.g1, lp.b1);
     __syncthreads();
-    {  // drbf = dz1 . W1r  (W1 [128][ldw1], rbf columns 0..255)
-      floatx4 acc[2][4];
-      gemm32<kH, 256>(Y, kLdY, W.w1, W.ldw1, acc);
-      accumulate_dd(acc, te, mu, c2, coeff2, dd_lane);
-    }
+    dd_row += linear1_dd(W, te, Y, kLdY);
     __syncthreads();
   }
-  reduce_dd(dd_lane, part, dd, e0, nvalid, accumulate);
+  const int row = threadIdx.x >> 3;
+  if ((threadIdx.x & 7) == 0 && row < nvalid) {
+    const int64_t e = e0 + row;
+    dd[e] = accumulate ? dd[e] + dd_row : dd_row;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -521,9 +516,9 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* _
 // [N][K] in bf16.
 __global__ __launch_bounds__(256) void k_mlp_fwd_bf16(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
   extern __shared__ float sm[];
-  __bf16* Xb = reinterpret_cast<__bf16*>(sm);                 // [32][264] bf16
-  float* Yf = sm + (kT * kLdXb) / 2;                           // [32][130] fp32
+  float* Yf = sm;                                              // [32][130] fp32
   __bf16* Yb = reinterpret_cast<__bf16*>(Yf + kT * kLdY);      // [32][136] bf16
+  __bf16* Zb = Yb + kT * kLdYb;                                // [32][136] bf16
   __shared__ TileEdges te;
   __shared__ LnParams lp;
   const int m = blockIdx.y;
@@ -532,26 +527,15 @@ __global__ __launch_bounds__(256) void k_mlp_fwd_bf16(e2v2_mlp_args A, float* __
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   float* sn = A.save_n ? A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH) : nullptr;
   float* sr = A.save_r ? A.save_r + ((size_t)m * A.n_edges + e0) * 2 : nullptr;
-  Panel<kK0, kH> P1;
-  load_panel(P1, static_cast<const __bf16*>(W.w1b));
-  const float mu = A.rbf_offset[threadIdx.x];
+  Panel<kH, kH> P2;
+  load_panel(P2, static_cast<const __bf16*>(W.w2b));
   float b2[2], b3[4];
   load_bias<kH>(W.b2, b2);
   load_bias<256>(W.b3, b3);
   load_tile_edges(A, e0, te);
   load_ln_params(W, lp);
   __syncthreads();
-  TypeTerms tt;
-  load_type_terms(W.ttgt, W.tsrc, te, tt);
-  rbf_tile(te, mu, A.rbf_coeff * kLog2e, Xb, kLdXb);
-  __syncthreads();
-  Panel<kH, kH> P2;
-  {
-    floatx4 acc[2][2];
-    gemm_panel(Xb, kLdXb, P1, acc);
-    load_panel(P2, static_cast<const __bf16*>(W.w2b));
-    store_gemm1(acc, tt, Yf, kLdY);
-  }
+  linear1_rows(W, te, Yf, kLdY);
   __syncthreads();
   ln_silu_rows(Yf, kLdY, Yb, kLdYb, lp.g1, lp.b1, sn, 2 * kH, sr, 2, nvalid);
   __syncthreads();
@@ -563,11 +547,11 @@ __global__ __launch_bounds__(256) void k_mlp_fwd_bf16(e2v2_mlp_args A, float* __
     store_acc<kH>(acc, Yf, kLdY, b2);
   }
   __syncthreads();
-  ln_silu_rows(Yf, kLdY, Xb, kLdYb, lp.g2, lp.b2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2,
+  ln_silu_rows(Yf, kLdY, Zb, kLdYb, lp.g2, lp.b2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2,
                nvalid);
   __syncthreads();
   floatx4 acc[2][4];
-  gemm_panel(Xb, kLdYb, P3, acc);
+  gemm_panel(Zb, kLdYb, P3, acc);
   store_out(acc, b3, out, ld_out, e0, nvalid, m);
 }
 
@@ -579,20 +563,11 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const flo
   __bf16* Yb = reinterpret_cast<__bf16*>(Yf + kT * kLdY);      // [32][136] bf16
   __shared__ TileEdges te;
   __shared__ LnParams lp;
-  __shared__ float part[4][kT];
   const int64_t e0 = (int64_t)blockIdx.x * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
-  const float c2 = A.rbf_coeff * kLog2e, coeff2 = 2.0f * A.rbf_coeff;
-  float mu[4];
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) mu[ct] = A.rbf_offset[acc_col0<256>() + ct * 16];
   const float zero2[2] = {0.f, 0.f};
   load_tile_edges(A, e0, te);
-  float dd_lane[2][4];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) dd_lane[rt][r] = 0.f;
+  float dd_row = 0.f;
   for (int m = 0; m < A.n_mlp; ++m) {
     const e2v2_mlp_weights& W = A.w[m];
     const float* sn = A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH);
@@ -622,24 +597,22 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const flo
     __syncthreads();
     ln_silu_bwd_rows(Yf, kLdY, Yb, kLdYb, s2, lp.g2, lp.b2);
     __syncthreads();
-    Panel<kH, 256> Pc;
     {  // dy1 = dz2 . W2   (B^T = W2^T)
       floatx4 acc[2][2];
       gemm_panel(Yb, kLdYb, Pb, acc);
-      load_panel(Pc, static_cast<const __bf16*>(W.w1rtb));
       store_acc<kH>(acc, Yf, kLdY, zero2);
     }
     __syncthreads();
-    ln_silu_bwd_rows(Yf, kLdY, Xb, kLdYb, s1, lp.g1, lp.b1);
+    ln_silu_bwd_rows(Yf, kLdY, Yf, kLdY, s1, lp.g1, lp.b1);
     __syncthreads();
-    {  // drbf = dz1 . W1r   (B^T = W1r^T [256][128])
-      floatx4 acc[2][4];
-      gemm_panel(Xb, kLdYb, Pc, acc);
-      accumulate_dd(acc, te, mu, c2, coeff2, dd_lane);
-    }
+    dd_row += linear1_dd(W, te, Yf, kLdY);
     __syncthreads();
   }
-  reduce_dd(dd_lane, part, dd, e0, nvalid, accumulate);
+  const int row = threadIdx.x >> 3;
+  if ((threadIdx.x & 7) == 0 && row < nvalid) {
+    const int64_t e = e0 + row;
+    dd[e] = accumulate ? dd[e] + dd_row : dd_row;
+  }
 }
 
 }  // namespace e2v2
@@ -648,18 +621,47 @@ using namespace e2v2;
 
 static size_t mlp_lds_fwd() { return sizeof(float) * kT * kLdY; }
 static size_t mlp_lds_bwd() { return sizeof(float) * kT * kLdX; }
-static size_t mlp_lds_bf16() { return sizeof(__bf16) * (kT * kLdXb + kT * kLdYb) + sizeof(float) * kT * kLdY; }
+static size_t mlp_lds_fwd_bf16() { return sizeof(float) * kT * kLdY + 2 * sizeof(__bf16) * kT * kLdYb; }
+static size_t mlp_lds_bwd_bf16() { return sizeof(__bf16) * (kT * kLdXb + kT * kLdYb) + sizeof(float) * kT * kLdY; }
+
+static int check_tables(const e2v2_mlp_args& A, const char* who) {
+  for (int m = 0; m < A.n_mlp; ++m)
+    E2V2_REQUIRE(A.w[m].rtab != nullptr && A.w[m].rtab_n >= 2 && A.w[m].rtab_h > 0.f,
+                 "%s: profile %d has no rbf-block table (e2v2_mlp_rbf_table)", who, m);
+  return 0;
+}
+
+E2V2_API int e2v2_mlp_rbf_table_size(float rc, float rbf_coeff, int32_t* n_nodes, float* h) {
+  E2V2_REQUIRE(rc > 0.f && rbf_coeff < 0.f && n_nodes && h, "mlp_rbf_table_size: need rc > 0, rbf_coeff < 0");
+  const double sigma = std::sqrt(-0.5 / (double)rbf_coeff);
+  const double hh = std::ldexp(1.0, (int)std::floor(std::log2(0.2 * sigma)));
+  const double n = std::floor((double)rc / hh) + 2.0;
+  E2V2_REQUIRE(n <= 1 << 20, "mlp_rbf_table_size: %.0f nodes (rc %g, width %g) is too many", n, (double)rc, sigma);
+  *n_nodes = (int32_t)n;
+  *h = (float)hh;
+  return 0;
+}
+
+E2V2_API int e2v2_mlp_rbf_table(const float* w1, int ldw1, const float* rbf_offset, float rbf_coeff, int32_t n_nodes,
+                                float h, float* rtab, hipStream_t s) {
+  E2V2_REQUIRE(w1 && rbf_offset && rtab && ldw1 >= 256 && n_nodes >= 2 && h > 0.f,
+               "mlp_rbf_table: bad arguments (ldw1 %d, n_nodes %d)", ldw1, n_nodes);
+  hipLaunchKernelGGL(k_rbf_table, dim3((unsigned)n_nodes), dim3(kH), 0, s, w1, ldw1, rbf_offset, rbf_coeff, h, rtab);
+  E2V2_LAUNCHED("k_rbf_table");
+  return 0;
+}
 
 E2V2_API int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hipStream_t s) {
   const e2v2_mlp_args& A = *args;
   E2V2_REQUIRE(A.n_mlp >= 1 && A.n_mlp <= E2V2_MAX_MLP, "mlp_fwd: n_mlp %d out of range", A.n_mlp);
   E2V2_REQUIRE(ld_out >= 256 * A.n_mlp, "mlp_fwd: ld_out %d < 256*n_mlp", ld_out);
   if (A.n_edges == 0) return 0;
+  if (int rc = check_tables(A, "mlp_fwd")) return rc;
   dim3 grid((unsigned)((A.n_edges + kT - 1) / kT), (unsigned)A.n_mlp);
   if (A.compute_bf16) {
     for (int m = 0; m < A.n_mlp; ++m)
-      E2V2_REQUIRE(A.w[m].w1b && A.w[m].w2b && A.w[m].w3b, "mlp_fwd: bf16 weights missing for profile %d", m);
-    hipLaunchKernelGGL(k_mlp_fwd_bf16, grid, dim3(256), mlp_lds_bf16(), s, A, out, ld_out);
+      E2V2_REQUIRE(A.w[m].w2b && A.w[m].w3b, "mlp_fwd: bf16 weights missing for profile %d", m);
+    hipLaunchKernelGGL(k_mlp_fwd_bf16, grid, dim3(256), mlp_lds_fwd_bf16(), s, A, out, ld_out);
     E2V2_LAUNCHED("k_mlp_fwd_bf16");
     return 0;
   }
@@ -676,11 +678,12 @@ E2V2_API int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_d
   E2V2_REQUIRE(A.save_n != nullptr && A.save_r != nullptr,
                "mlp_bwd: needs the normalised activations saved by e2v2_mlp_fwd (save_n, save_r)");
   if (A.n_edges == 0) return 0;
+  if (int rc = check_tables(A, "mlp_bwd")) return rc;
   dim3 grid((unsigned)((A.n_edges + kT - 1) / kT));
   if (A.compute_bf16) {
     for (int m = 0; m < A.n_mlp; ++m)
-      E2V2_REQUIRE(A.w[m].w3tb && A.w[m].w2tb && A.w[m].w1rtb, "mlp_bwd: bf16 weights missing for profile %d", m);
-    hipLaunchKernelGGL(k_mlp_bwd_bf16, grid, dim3(256), mlp_lds_bf16(), s, A, dout, ld_dout, dd, accumulate);
+      E2V2_REQUIRE(A.w[m].w3tb && A.w[m].w2tb, "mlp_bwd: bf16 weights missing for profile %d", m);
+    hipLaunchKernelGGL(k_mlp_bwd_bf16, grid, dim3(256), mlp_lds_bwd_bf16(), s, A, dout, ld_dout, dd, accumulate);
     E2V2_LAUNCHED("k_mlp_bwd_bf16");
     return 0;
   }

@@ -645,7 +645,8 @@ class E2AttentionArbOrder_sparse(nn.Module):
         q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
         k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         v = self.proj_value(x, bf16)
-        packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding, bf16)
+        packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding, ctx.rbf_offset,
+                               ctx.rbf_coeff, ctx.rc, bf16)
         so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
                                 packed, ctx.rc, math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
         if res is None:
@@ -703,7 +704,7 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
 
     def forward(self, ctx: EdgeContext):
         packed = self._mlp.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
-                               ctx.bf16)
+                               ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.bf16)
         return DegreeEmbedFn.apply(ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff, packed,
                                    float(self.avg_aggregate_num), ctx.rc)
 

@@ -43,20 +43,30 @@ def _no_double_backward():
                                   "(create_graph=True / double backward is not supported)")
 
 
+def rbf_table_size(rc: float, rbf_coeff: float):
+    """(nodes, spacing) of the rbf-block table for this basis and cutoff."""
+    n = _lib.C.c_int32(); h = _lib.C.c_float()
+    _lib.call("e2v2_mlp_rbf_table_size", _lib.f32(rc), _lib.f32(rbf_coeff), _lib.C.byref(n), _lib.C.byref(h))
+    return n.value, h.value
+
+
 class PackedMLP:
     """Device-ready weights of one RadialProfile [K0 + 2 E -> 128 -> 128 -> 256]
     (src/molfm/models/e2former/module_utils.py:2151-2178) whose input is
-    [rbf(256), target_table[z_i], source_table[z_j]]."""
+    [rbf(256), target_table[z_i], source_table[z_j]]: the rbf block of Linear1
+    as an interpolation table over [0, rc] (e2v2_mlp_rbf_table), the type blocks
+    as per-type tables, Linear2/3 as GEMM operands."""
 
-    def __init__(self, net: nn.Sequential, tgt: torch.Tensor, src: torch.Tensor, n_rbf: int = 256,
-                 bf16: bool = False):
+    def __init__(self, net: nn.Sequential, tgt: torch.Tensor, src: torch.Tensor, rbf_offset: torch.Tensor,
+                 rbf_coeff: float, rc: float, n_rbf: int = 256, bf16: bool = False):
         lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
         self.bf16 = bf16
+        if n_rbf != 256 or rbf_offset.numel() != 256:
+            raise NotImplementedError("the HIP radial MLP is built for 256 Gaussian basis functions")
         with torch.no_grad():
             W1 = lin1.weight.detach().float().contiguous()
             e = tgt.shape[1]
             self.w1 = W1
-            self.w1t = W1[:, :n_rbf].t().contiguous()
             self.ttgt = (tgt.detach().float() @ W1[:, n_rbf:n_rbf + e].t() + lin1.bias.detach().float()).contiguous()
             self.tsrc = (src.detach().float() @ W1[:, n_rbf + e:n_rbf + 2 * e].t()).contiguous()
             self.g1 = ln1.weight.detach().float().contiguous(); self.be1 = ln1.bias.detach().float().contiguous()
@@ -65,25 +75,29 @@ class PackedMLP:
             self.g2 = ln2.weight.detach().float().contiguous(); self.be2 = ln2.bias.detach().float().contiguous()
             self.w3 = lin3.weight.detach().float().contiguous(); self.w3t = self.w3.t().contiguous()
             self.b3 = lin3.bias.detach().float().contiguous()
-            # bf16 GEMM operands as B^T row-major: forward W1r, W2, W3; backward W3^T, W2^T, W1r^T
+            # bf16 GEMM operands as B^T row-major: forward W2, W3; backward W3^T, W2^T
             self.bf = None
             if bf16:
                 b = torch.bfloat16
-                self.bf = [W1[:, :n_rbf].to(b).contiguous(), self.w2.to(b).contiguous(), self.w3.to(b).contiguous(),
-                           self.w3.t().to(b).contiguous(), self.w2.t().to(b).contiguous(),
-                           W1[:, :n_rbf].t().to(b).contiguous()]
+                self.bf = [self.w2.to(b).contiguous(), self.w3.to(b).contiguous(),
+                           self.w3.t().to(b).contiguous(), self.w2.t().to(b).contiguous()]
         if not (abs(ln1.eps - 1e-5) < 1e-12 and abs(ln2.eps - 1e-5) < 1e-12):
             raise NotImplementedError("RadialProfile LayerNorm eps must be 1e-5")
-        if self.w1t.shape != (256, 128) or self.w2.shape != (128, 128) or self.w3.shape != (256, 128):
+        if W1.shape[0] != 128 or self.w2.shape != (128, 128) or self.w3.shape != (256, 128):
             raise NotImplementedError(f"RadialProfile shape {tuple(W1.shape)} -> {tuple(self.w3.shape)} "
                                       "is not the [256+2E, 128, 128, 256] profile of the HIP kernels")
+        self.rtab_n, self.rtab_h = rbf_table_size(rc, rbf_coeff)
+        self.rtab = torch.empty(self.rtab_n, 4, 128, dtype=torch.float32, device=W1.device)
+        self.rbf_offset = rbf_offset.detach().float().contiguous()
+        _lib.call("e2v2_mlp_rbf_table", _p(W1), _lib.i32(W1.shape[1]), _p(self.rbf_offset), _lib.f32(rbf_coeff),
+                  _lib.i32(self.rtab_n), _lib.f32(self.rtab_h), _p(self.rtab), _stream(W1))
 
     def struct(self) -> _lib.MlpWeights:
-        bf = [t.data_ptr() for t in self.bf] if self.bf is not None else [None] * 6
-        return _lib.MlpWeights(self.w1t.data_ptr(), self.ttgt.data_ptr(), self.tsrc.data_ptr(), self.g1.data_ptr(),
-                               self.be1.data_ptr(), self.w2t.data_ptr(), self.b2.data_ptr(), self.g2.data_ptr(),
-                               self.be2.data_ptr(), self.w3t.data_ptr(), self.b3.data_ptr(), self.w1.data_ptr(),
-                               int(self.w1.shape[1]), self.w2.data_ptr(), self.w3.data_ptr(), *bf)
+        bf = [t.data_ptr() for t in self.bf] if self.bf is not None else [None] * 4
+        return _lib.MlpWeights(self.rtab.data_ptr(), self.rtab_n, self.rtab_h, self.ttgt.data_ptr(),
+                               self.tsrc.data_ptr(), self.g1.data_ptr(), self.be1.data_ptr(), self.w2t.data_ptr(),
+                               self.b2.data_ptr(), self.g2.data_ptr(), self.be2.data_ptr(), self.w3t.data_ptr(),
+                               self.b3.data_ptr(), self.w2.data_ptr(), self.w3.data_ptr(), *bf)
 
 
 def _version_key(params):
@@ -91,24 +105,25 @@ def _version_key(params):
 
 
 class MLPCache:
-    """Repack weights only when a parameter changed (MD loops reuse them)."""
+    """Repack weights only when a parameter (or the basis) changed (MD loops reuse them)."""
 
     def __init__(self):
         self.key = None
         self.packed: List[PackedMLP] = []
 
-    def get(self, nets, tgt_emb: nn.Embedding, src_emb: nn.Embedding, bf16: bool = False):
-        params = [p for n in nets for p in n.parameters()] + [tgt_emb.weight, src_emb.weight]
-        key = (_version_key(params), bf16)
+    def get(self, nets, tgt_emb: nn.Embedding, src_emb: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
+            rc: float, bf16: bool = False):
+        params = [p for n in nets for p in n.parameters()] + [tgt_emb.weight, src_emb.weight, rbf_offset]
+        key = (_version_key(params), float(rbf_coeff), float(rc), bf16)
         if key != self.key:
-            self.packed = [PackedMLP(n, tgt_emb.weight, src_emb.weight, bf16=bf16) for n in nets]
+            self.packed = [PackedMLP(n, tgt_emb.weight, src_emb.weight, rbf_offset, rbf_coeff, rc, bf16=bf16)
+                           for n in nets]
             self.key = key
         return self.packed
 
 
-def mlp_args(nl: NeighborList, node_type: torch.Tensor, rbf_offset: torch.Tensor, rbf_coeff: float,
-             packed: List[PackedMLP], save_n: Optional[torch.Tensor] = None,
-             save_r: Optional[torch.Tensor] = None) -> _lib.MlpArgs:
+def mlp_args(nl: NeighborList, node_type: torch.Tensor, packed: List[PackedMLP],
+             save_n: Optional[torch.Tensor] = None, save_r: Optional[torch.Tensor] = None) -> _lib.MlpArgs:
     ws = (_lib.MlpWeights * 3)()
     for m, pk in enumerate(packed):
         ws[m] = pk.struct()
@@ -116,7 +131,7 @@ def mlp_args(nl: NeighborList, node_type: torch.Tensor, rbf_offset: torch.Tensor
     if any(pk.bf16 != bf16 for pk in packed):
         raise ValueError("mixed fp32/bf16 RadialProfile packs in one launch")
     return _lib.MlpArgs(nl.n_edges, len(packed), int(bf16), nl.dist.data_ptr(), nl.edge_row.data_ptr(),
-                        nl.col.data_ptr(), node_type.data_ptr(), rbf_offset.data_ptr(), float(rbf_coeff),
+                        nl.col.data_ptr(), node_type.data_ptr(),
                         None if save_n is None else save_n.data_ptr(), None if save_r is None else save_r.data_ptr(),
                         ws)
 
@@ -164,7 +179,7 @@ class DegreeEmbedFn(torch.autograd.Function):
         E, N = nl.n_edges, nl.n_atoms
         fea = torch.empty(max(E, 1), 3 * 256, dtype=torch.float32, device=dev)
         sn, sr = mlp_save_buffers(len(packed), E, dev)
-        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
+        margs = mlp_args(nl, node_type, packed, sn, sr)
         _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(fea), _lib.i32(768), _stream(fea))
         dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                              fea.data_ptr(), float(avg), float(rc), ENV_A, ENV_B, ENV_C)
@@ -190,7 +205,7 @@ class DegreeEmbedFn(torch.autograd.Function):
         ddv = torch.empty(max(E, 1), 3, dtype=torch.float32, device=dev)
         dd = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
         _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(dfea), _p(ddv), _p(dd), _stream(gx0))
-        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
+        margs = mlp_args(nl, node_type, packed, sn, sr)
         _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dfea), _lib.i32(768), _p(dd), _lib.i32(1), _stream(gx0))
         return ddv[:E], dd[:E], None, None, None, None, None, None, None
 
@@ -215,7 +230,7 @@ class AttentionFn(torch.autograd.Function):
         bf = int(act_dtype == torch.bfloat16)
         gi = torch.empty(max(E, 1), 256, dtype=torch.float32, device=dev)
         sn, sr = mlp_save_buffers(1, E, dev)
-        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
+        margs = mlp_args(nl, node_type, packed, sn, sr)
         _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(gi), _lib.i32(256), _stream(q))
         args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
                              nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
@@ -254,6 +269,6 @@ class AttentionFn(torch.autograd.Function):
         _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(dgi),
                   _p(ddv), _p(dd), _p(dq), _p(dk), _p(dv), _p(w_e), _p(dqk), _stream(gout))
         del w_e, dqk
-        margs = mlp_args(nl, node_type, rbf_offset, rbf_coeff, packed, sn, sr)
+        margs = mlp_args(nl, node_type, packed, sn, sr)
         _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dgi), _lib.i32(256), _p(dd), _lib.i32(1), _stream(gout))
         return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None, None
