@@ -34,7 +34,8 @@ constexpr int kLdX = 258;       // fp32 LDS row stride for K=256 tiles (== 2 mod
 constexpr int kLdY = 130;       // fp32 LDS row stride for K=128 tiles (== 2 mod 32)
 constexpr int kLdXb = 264;      // bf16 row stride of K=256 tiles (16-byte aligned rows)
 constexpr int kLdYb = 136;      // bf16 row stride of K=128 tiles
-constexpr int kPF = 8;          // fp32 GEMM: k-steps (of 4) per register-prefetched B chunk
+constexpr int kPFNarrow = 8;    // fp32 GEMM: k-steps (of 4) per register-prefetched B chunk, N <= 128
+constexpr int kPFWide = 4;      //   and for N = 256 (same register footprint)
 constexpr int kTabRow = 4 * kH; // floats per table node: value and h, h^2, h^3 scaled derivatives
 constexpr float kFarDist = 1e18f;  // distance of padding rows (finite)
 
@@ -50,6 +51,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 template <int K, int N, typename AFn>
 __device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, int ldb, floatx4 (&acc)[2][N / 64]) {
   constexpr int CT = N / 64;
+  constexpr int kPF = N > 128 ? kPFWide : kPFNarrow;   // B registers per chunk: kPF * CT
   constexpr int NCH = K / (4 * kPF);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -329,7 +331,7 @@ __device__ __forceinline__ void linear1_rows(const e2v2_mlp_weights& W, const Ti
   const float* tt = W.ttgt + te.zi[row] * kH + c0;
   const float* ts = W.tsrc + te.zj[row] * kH + c0;
   float* y = Y + row * ldy + c0;
-#pragma unroll
+#pragma unroll 2
   for (int q = 0; q < 4; ++q) {
     const floatx4 f0 = reinterpret_cast<const floatx4*>(p + 4 * q)[0];
     const floatx4 f1 = reinterpret_cast<const floatx4*>(p + kH + 4 * q)[0];
@@ -355,7 +357,7 @@ __device__ __forceinline__ float linear1_dd(const e2v2_mlp_weights& W, const Til
   const Hermite5 H = hermite5(t);
   const float* z = Z + row * ldz + c0;
   float s = 0.f;
-#pragma unroll
+#pragma unroll 2
   for (int q = 0; q < 4; ++q) {
     const floatx4 f1 = reinterpret_cast<const floatx4*>(p + kH + 4 * q)[0];
     const floatx4 f2 = reinterpret_cast<const floatx4*>(p + 2 * kH + 4 * q)[0];
