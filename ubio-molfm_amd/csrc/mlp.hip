@@ -420,7 +420,8 @@ __device__ __forceinline__ void store_out(const floatx4 (&acc)[2][4], const floa
 
 // ---------------------------------------------------------------------------
 // fp32 kernels
-__global__ __launch_bounds__(256) void k_mlp_fwd(e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_mlp_fwd(
+    e2v2_mlp_args A, float* __restrict__ out, int ld_out) {
   extern __shared__ float sm[];
   float* Y = sm;                    // [32][130]: Linear1/2 outputs, LayerNorm in place
   __shared__ TileEdges te;
