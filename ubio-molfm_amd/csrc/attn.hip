@@ -410,12 +410,14 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const TS
   }
 }
 
-// Column pass: for every source atom j, sum over its key-CSR edges (ascending
-// edge id) -> dv_j and dk_j.  Edge metadata of a 32-edge chunk is staged in LDS
-// so the per-edge gathers of grad rows do not wait on index loads; two edges
-// are processed per iteration to overlap their 20-row gathers.
+// Column pass, one channel per thread (the fp32 form: a 4-byte gather per lane
+// is as cheap per byte for the address unit as a pair load): for every source
+// atom j, sum over its key-CSR edges (ascending edge id) -> dv_j and dk_j.
+// Edge metadata of a 32-edge chunk is staged in LDS so the per-edge gathers of
+// grad rows do not wait on index loads; two edges are processed per iteration
+// to overlap their 20-row gathers.
 template <typename TS>
-__global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const TS* __restrict__ G,
+__global__ __launch_bounds__(256) void k_attn_bwd_col_ch(e2v2_attn_args A, const TS* __restrict__ G,
                                                       const float* __restrict__ w_e, const float* __restrict__ dqk_e,
                                                       float* __restrict__ dv_out, float* __restrict__ dk_out) {
   constexpr int CC = 32;
@@ -495,6 +497,116 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col(e2v2_attn_args A, const TS
   for (int d = 0; d < 4; ++d) ntstore(ak[d] / A.q_div, dk_out + ((size_t)j * kH + hk) * kD + d0 + d);
 }
 
+// Column pass, channel pairs (the bf16 form: one 4-byte word carries two
+// channels): for every source atom j, sum over its key-CSR edges (ascending
+// edge id) -> dv_j and dk_j, no atomics.  Thread t owns the channel pair
+// (2u, 2u + 1), u = t % 128, and the chunk's edges of parity t / 128: every
+// gather instruction moves two channels per lane (the gathers, not the bytes,
+// bound this pass).  The two parities' partial sums are added once per column
+// in LDS (fixed order: deterministic).  Edge metadata of 32-edge chunks is
+// staged in LDS.
+__device__ __forceinline__ void ld_pair(const float* p, float& a, float& b) {
+  const float2 v = *reinterpret_cast<const float2*>(p);
+  a = v.x;
+  b = v.y;
+}
+__device__ __forceinline__ void ld_pair(const __bf16* p, float& a, float& b) {
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
+
+template <typename TS>
+__global__ __launch_bounds__(256) void k_attn_bwd_col_pair(e2v2_attn_args A, const TS* __restrict__ G,
+                                                           const float* __restrict__ w_e,
+                                                           const float* __restrict__ dqk_e, float* __restrict__ dv_out,
+                                                           float* __restrict__ dk_out) {
+  constexpr int CC = 32;
+  __shared__ int ci[CC];
+  __shared__ float cdv[CC][3];
+  __shared__ float cwq[2 * CC * kH];          // per-chunk w | dqk; after the loop, the parity partial sums
+  float (*cw)[kH] = reinterpret_cast<float (*)[kH]>(cwq);
+  float (*cq)[kH] = reinterpret_cast<float (*)[kH]>(cwq + CC * kH);
+  float (*red_v)[kC] = reinterpret_cast<float (*)[kC]>(cwq);
+  float (*red_k)[kD] = reinterpret_cast<float (*)[kD]>(cwq + kNV * kC);
+  static_assert(kNV * kC + kH * kD <= 2 * CC * kH, "partial sums fit the chunk buffers");
+  const int j = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
+  if (j >= A.n_rows) return;
+  const int u = t & (kH - 1), par = t >> 7;
+  const int c0 = 2 * u;                                     // channels c0, c0 + 1
+  const int h0 = c0 & (kH - 1), h1 = (c0 + 1) & (kH - 1);   // their heads
+  const size_t os = (size_t)A.n_rows * kC;
+  float av0[kNV], av1[kNV];
+#pragma unroll
+  for (int r = 0; r < kNV; ++r) av0[r] = av1[r] = 0.f;
+  float ak[kD];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) ak[d] = 0.f;
+  const int p0 = A.key_ptr[j], p1 = A.key_ptr[j + 1];
+  const TS* __restrict__ Qp = static_cast<const TS*>(A.q);
+  // dv[r] += sum_k dA[r][k] (w dvec_k), dA = T^T G_i[:, c]
+  auto channel = [&](int el, const float (&g)[kNT], int h, float (&av)[kNV]) {
+    float dA[kNV][3];
+    tp_transpose(g, dA);
+    const float w = cw[el][h];
+    const float wx = w * cdv[el][0], wy = w * cdv[el][1], wz = w * cdv[el][2];
+#pragma unroll
+    for (int r = 0; r < kNV; ++r) av[r] = fmaf(dA[r][2], wz, fmaf(dA[r][1], wy, fmaf(dA[r][0], wx, av[r])));
+  };
+  for (int c0e = p0; c0e < p1; c0e += CC) {
+    const int nc = min(CC, p1 - c0e);
+    if (t < nc) {
+      const int64_t e = A.key_eid[c0e + t];
+      ci[t] = A.edge_row[e];
+      cdv[t][0] = A.dvec[3 * e];
+      cdv[t][1] = A.dvec[3 * e + 1];
+      cdv[t][2] = A.dvec[3 * e + 2];
+    }
+    // per-edge head weights: w and dqk rows are 512 B each; 2 edges x 128 heads per pass
+    for (int idx = t; idx < nc * kH; idx += 256) {
+      const int el = idx >> 7, h = idx & (kH - 1);
+      const int64_t e = A.key_eid[c0e + el];
+      cw[el][h] = ntload(w_e + e * kH + h);
+      cq[el][h] = ntload(dqk_e + e * kH + h);
+    }
+    __syncthreads();
+    for (int el = par; el < nc; el += 2) {
+      const int i = ci[el];
+      float ga[kNT], gb[kNT];
+#pragma unroll
+      for (int z = 0; z < kNT; ++z) ld_pair(G + (size_t)i * kC + z * os + c0, ga[z], gb[z]);
+      float q[kD];
+      load8(Qp + ((size_t)i * kH + u) * kD, q);
+      channel(el, ga, h0, av0);
+      channel(el, gb, h1, av1);
+      const float dqv = cq[el][u];
+#pragma unroll
+      for (int d = 0; d < kD; ++d) ak[d] = fmaf(dqv, q[d], ak[d]);
+    }
+    __syncthreads();
+  }
+  if (par) {
+#pragma unroll
+    for (int r = 0; r < kNV; ++r) {
+      red_v[r][c0] = av0[r];
+      red_v[r][c0 + 1] = av1[r];
+    }
+#pragma unroll
+    for (int d = 0; d < kD; ++d) red_k[u][d] = ak[d];
+  }
+  __syncthreads();
+  if (!par) {
+#pragma unroll
+    for (int r = 0; r < kNV; ++r) {
+      const float2 v = make_float2(av0[r] + red_v[r][c0], av1[r] + red_v[r][c0 + 1]);
+      *reinterpret_cast<float2*>(dv_out + (size_t)j * kC + r * os + c0) = v;
+    }
+    float* kp = dk_out + ((size_t)j * kH + u) * kD;
+#pragma unroll
+    for (int d = 0; d < kD; ++d) kp[d] = (ak[d] + red_k[u][d]) / A.q_div;
+  }
+}
+
 }  // namespace e2v2
 
 using namespace e2v2;
@@ -524,7 +636,11 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
   hipLaunchKernelGGL(k_attn_bwd_row<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, dgi, ddvec, ddist, dq,
                      w_edge, dqk_edge);
   E2V2_LAUNCHED("k_attn_bwd_row");
-  hipLaunchKernelGGL(k_attn_bwd_col<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
+  if constexpr (sizeof(TS) == 2) {
+    hipLaunchKernelGGL(k_attn_bwd_col_pair<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
+  } else {
+    hipLaunchKernelGGL(k_attn_bwd_col_ch<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
+  }
   E2V2_LAUNCHED("k_attn_bwd_col");
   return 0;
 }
