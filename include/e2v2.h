@@ -95,6 +95,15 @@ int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, int64_t n_e
 int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* cnt, int32_t* new_ptr, int32_t* stats,
                   const int32_t* col, const int32_t* shift, const float* dvec, const float* dist,
                   int32_t* ocol, int32_t* oshift, float* odv, float* od, int phase, hipStream_t s);
+/* Clusters of `span` (1..8) consecutive segments of a CSR: seg_ptr = row_ptr with member = col and
+   item_eid = NULL (query rows), or seg_ptr = key_ptr with member = edge_row and item_eid = key_eid (key
+   columns).  Every distinct (member atom, occurrence) of a cluster becomes one slot, sorted by atom:
+   slot_member[slot] = the atom, slot_edge[slot * span + r] = the edge joining it to segment r of the
+   cluster or -1.  Slots of cluster c are stored from index seg_ptr[c * span] on; n_slots[c] counts them.
+   Sizes: slot_member [n_items], slot_edge [n_items * span], n_slots [ceil(n_seg / span)].
+   No reference counterpart: the layout the clustered edge kernels read. */
+int e2v2_cluster_slots(const int32_t* seg_ptr, int32_t n_seg, const int32_t* member, const int32_t* item_eid,
+                       int32_t span, int32_t* slot_member, int32_t* slot_edge, int32_t* n_slots, hipStream_t s);
 /* key CSR: phase 0 -> edge_row, key_ptr, stats = {E, max column}; phase 1 -> key_eid (sorted by edge id) */
 int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, int n_cols, int64_t n_edges,
                        int32_t* edge_row, int32_t* key_cnt, int32_t* key_ptr, int32_t* stats,
@@ -173,6 +182,11 @@ typedef struct e2v2_attn_args {
   float q_div;                   /* sqrt(D)                                         */
   float rc, env_a, env_b, env_c; /* polynomial envelope                             */
   int32_t act_bf16;              /* 1: q, k, v, out, grad_out stored as bf16 (fp32 math) */
+  /* Optional clusters from e2v2_cluster_slots (NULL: one workgroup per row / column):
+     query-CSR rows in clusters of row_span (4), key-CSR columns in clusters of col_span (4 or 8). */
+  int32_t row_span, col_span;
+  const int32_t* row_slot_member; const int32_t* row_slot_edge; const int32_t* row_n_slots;
+  const int32_t* col_slot_member; const int32_t* col_slot_edge; const int32_t* col_n_slots;
 } e2v2_attn_args;
 
 /* v [9][N][C] and out [20][N][C] are m-major (row r of every atom contiguous);

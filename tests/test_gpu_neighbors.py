@@ -39,7 +39,48 @@ def _check(pkg, cuda, sysd, rc=6.0, label=""):
     for j in range(len(kp) - 1):
         seg = ke[kp[j]:kp[j + 1]]
         assert np.all(col[seg] == j) and np.all(np.diff(seg) > 0)
+    if nl.n_edges:
+        er = nl.edge_row.cpu().numpy()
+        check_slots(kp, col, er, ke, nl.col_span, nl.col_slot_member, nl.col_slot_edge, nl.col_n_slots)
     return nl
+
+
+def check_slots(seg_ptr, seg_of_edge, member_of_edge, item_eid, span, sm, se, ns):
+    """Cluster slots (e2v2_cluster_slots) against their definition: every edge of
+    a cluster in exactly one slot, in the column of its segment, under its member
+    atom; slots sorted by atom with one slot per (atom, occurrence) unless the
+    cluster overflowed (then one slot per item)."""
+    sm, se, ns = sm.cpu().numpy(), se.cpu().numpy().reshape(-1, span), ns.cpu().numpy()
+    n_seg = len(seg_ptr) - 1
+    n_cl = (n_seg + span - 1) // span
+    assert len(ns) >= n_cl
+    E = len(seg_of_edge)
+    seen = np.zeros(E, np.int64)
+    for c in range(n_cl):
+        s0, s1 = c * span, min(c * span + span, n_seg)
+        b, n = seg_ptr[s0], seg_ptr[s1] - seg_ptr[s0]
+        k = ns[c]
+        assert 0 <= k <= n, (c, k, n)
+        m = sm[b:b + k]; ed = se[b:b + k]
+        rr, cc = np.nonzero(ed >= 0)
+        e = ed[rr, cc]
+        assert np.all(seg_of_edge[e] == s0 + cc)
+        assert np.all(member_of_edge[e] == m[rr])
+        seen[e] += 1
+        items = np.arange(b, b + n)
+        eids = items if item_eid is None else item_eid[items]
+        assert np.array_equal(np.sort(e), np.sort(eids))
+        if n <= 4096 and k:
+            assert np.all(np.diff(m) >= 0)
+            # one slot per (atom, occurrence): slots of an atom = its largest multiplicity in one segment
+            atoms, per_atom = np.unique(m, return_counts=True)
+            segm = seg_of_edge[eids] * (member_of_edge.max() + 1) + member_of_edge[eids]
+            mult_of = {}
+            for key, cnt in zip(*np.unique(segm, return_counts=True)):
+                a = key % (member_of_edge.max() + 1)
+                mult_of[a] = max(mult_of.get(a, 0), cnt)
+            assert all(mult_of[a] == pa for a, pa in zip(atoms, per_atom))
+    assert np.all(seen == 1)
 
 
 def test_small_cell_below_cutoff(pkg, cuda):
@@ -105,3 +146,31 @@ def test_coincident_atoms_below_min_dist(pkg, cuda):
     nl = _check(pkg, cuda, sysd, label="coincident")
     c = nl.canonical()
     assert not np.any((c["i"] == 3) & (c["j"] == 7) & np.all(c["s"] == 0, axis=1))
+
+
+def test_cluster_slots_rows_and_overflow(pkg, cuda):
+    """Row clusters (span 4 and 8) of a small periodic cell with many images, and
+    a dense cell whose 8-column clusters exceed the per-cluster sort capacity
+    (one slot per item)."""
+    from ubio_molfm_amd import neighbors, systems
+    s = systems.small_water(8, 6.2, seed=0)
+    rng = np.random.default_rng(5)
+    dense = dict(pos=rng.uniform(0, 10, size=(700, 3)).astype(np.float32), Z=np.full(700, 1),
+                 graph_ptr=np.array([0, 700]), cell=(np.eye(3, dtype=np.float32) * 10.0)[None],
+                 pbc=np.ones((1, 3), bool))
+    for sysd, label in ((s, "images"), (dense, "dense")):
+        pos = torch.as_tensor(sysd["pos"], device=cuda)
+        nl = neighbors.build_neighbors(pos, sysd["graph_ptr"], sysd["cell"], sysd["pbc"], 6.0)
+        rp = nl.row_ptr.cpu().numpy(); col = nl.col.cpu().numpy(); er = nl.edge_row.cpu().numpy()
+        kp = nl.key_ptr.cpu().numpy(); ke = nl.key_eid.cpu().numpy()
+        over = 0
+        for span in (4, 8):
+            sm, se, ns = neighbors.cluster_slots(nl.row_ptr, nl.n_atoms, nl.col, None, span)
+            check_slots(rp, er, col, None, span, sm, se, ns)
+            sm, se, ns = neighbors.cluster_slots(nl.key_ptr, nl.n_atoms, nl.edge_row, nl.key_eid, span)
+            check_slots(kp, col, er, ke, span, sm, se, ns)
+            over += int(np.sum(kp[np.minimum(np.arange(0, nl.n_atoms, span) + span, nl.n_atoms)]
+                               - kp[np.arange(0, nl.n_atoms, span)] > 4096))
+        print(f"[slots {label}] N={nl.n_atoms} E={nl.n_edges} overflowing clusters={over}", flush=True)
+        if label == "dense":
+            assert over > 0

@@ -174,7 +174,7 @@ def test_rbf_block_table(pkg, cuda):
     assert ev < 1e-6 and ed < 1e-6
 
 
-def _attention_case(pkg, cuda, act_dtype):
+def _attention_case(pkg, cuda, act_dtype, clusters=True):
     """Attention fwd + bwd through the C ABI against the float64 reference.  With
     bf16 storage the inputs (q, k, v, grad) are rounded to bf16 for both sides,
     so the remaining differences are the bf16 output rows (also used by the
@@ -192,10 +192,10 @@ def _attention_case(pkg, cuda, act_dtype):
     qd, kd = (t.to(cuda).to(act_dtype).contiguous() for t in (q, k))
     gid = gi.to(cuda).contiguous()
     vd = v.permute(1, 0, 2).contiguous().to(cuda).to(act_dtype)        # m-major [9, N, C]
-    args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
-                         nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
-                         qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), gid.data_ptr(), math.sqrt(8.0), 6.0,
-                         ops.ENV_A, ops.ENV_B, ops.ENV_C, int(bf))
+    args = ops.attn_args(nl, qd, kd, vd, gid, math.sqrt(8.0), 6.0, int(bf))
+    if not clusters:
+        args.col_slot_member = args.col_slot_edge = args.col_n_slots = None
+        args.row_slot_member = args.row_slot_edge = args.row_n_slots = None
     out = torch.empty(20, N, 256, device=cuda, dtype=act_dtype); m = torch.empty(N, 128, device=cuda)
     sr = torch.empty(N, 128, device=cuda); cnt = torch.empty(N, 128, dtype=torch.int32, device=cuda)
     _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _lib.vp(out.data_ptr()), _lib.vp(m.data_ptr()),
@@ -222,8 +222,9 @@ def _attention_case(pkg, cuda, act_dtype):
     return e_f, errs
 
 
-def test_attention_forward_backward(pkg, cuda):
-    e_f, errs = _attention_case(pkg, cuda, torch.float32)
+@pytest.mark.parametrize("clusters", [True, False], ids=["clusters", "per_row"])
+def test_attention_forward_backward(pkg, cuda, clusters):
+    e_f, errs = _attention_case(pkg, cuda, torch.float32, clusters)
     assert e_f < 2e-5
     for name, e in errs.items():
         assert e < 1e-4, (name, e)

@@ -14,7 +14,7 @@ i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
 EXPORTS = [
     "e2v2_last_error", "e2v2_version", "e2v2_fill_i32", "e2v2_fill_f32", "e2v2_scan_i32",
-    "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose",
+    "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose", "e2v2_cluster_slots",
     "e2v2_mlp_rbf_table_size", "e2v2_mlp_rbf_table", "e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
     "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd", "e2v2_gate_bwd",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd",
@@ -45,7 +45,10 @@ class AttnArgs(C.Structure):
     _fields_ = [("n_rows", i32), ("n_edges", i64), ("n_heads", i32), ("head_dim", i32), ("channels", i32),
                 ("row_ptr", vp), ("col", vp), ("edge_row", vp), ("key_ptr", vp), ("key_eid", vp),
                 ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("gi", vp),
-                ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32)]
+                ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32),
+                ("row_span", i32), ("col_span", i32),
+                ("row_slot_member", vp), ("row_slot_edge", vp), ("row_n_slots", vp),
+                ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp)]
 
 
 class DegArgs(C.Structure):

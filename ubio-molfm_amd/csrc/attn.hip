@@ -20,6 +20,24 @@ namespace e2v2 {
 
 constexpr int kH = 128, kD = 8, kC = 256, kNV = 9, kNT = 20, kCH = 32, kCHB = 16;
 constexpr float kEps = 1e-3f;
+// Channel groups of the clustered kernels: group g holds heads 32g..32g+31 and
+// their 64 channels (c and c + 128 share head c % 128).  Lane l of a wave owns
+// channel 32g + l (l < 32) or 128 + 32g + l - 32, i.e. head 32g + l % 32, and
+// dims 4 (l / 32) .. +3 of that head's q / k.
+constexpr int kGroups = 4, kGroupHeads = kH / kGroups;
+__device__ __forceinline__ int group_channel(int g, int lane) {
+  return (lane < 32) ? (kGroupHeads * g + lane) : (kH + kGroupHeads * g + lane - 32);
+}
+// (cluster, group) of a workgroup: the workgroups of one XCD (blockIdx % 8) run
+// its contiguous range of clusters group by group, so its L2 holds one group's
+// quarter of the gathered rows at a time.
+__device__ __forceinline__ bool cluster_group(int n_cl, int& cl, int& grp) {
+  const int per = (n_cl + kXcd - 1) / kXcd;
+  const int seq = blockIdx.x / kXcd, x = blockIdx.x % kXcd;
+  grp = seq / per;
+  cl = x * per + seq % per;
+  return grp < kGroups && cl < n_cl;
+}
 
 __device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
   Envelope E;
@@ -68,15 +86,21 @@ __device__ __forceinline__ float ld_word(const __bf16* p) {
 __device__ __forceinline__ void store_act(float v, float* p) { ntstore(v, p); }
 __device__ __forceinline__ void store_act(float v, __bf16* p) { *p = (__bf16)v; }
 
-// <q_s, k_j[h]> with q_s already divided by sqrt(D); identical code in every pass
+// <q_s, k_j[h]> with q_s already divided by sqrt(D), as the sum of the two
+// half-dots over dims 0..3 and 4..7: the clustered kernels hold one half per
+// lane and add the partner lane's, and every pass must round a logit the same
+// way (the softmax max is matched bitwise in the backward).
+__device__ __forceinline__ float half_dot(const float* q, const float* k) {
+  float s = q[0] * k[0];
+#pragma unroll
+  for (int d = 1; d < 4; ++d) s = fmaf(q[d], k[d], s);
+  return s;
+}
 template <typename TS>
 __device__ __forceinline__ float qk_dot(const float (&qs)[kD], const TS* __restrict__ kp) {
   float k[kD];
   load8(kp, k);
-  float s = qs[0] * k[0];
-#pragma unroll
-  for (int d = 1; d < kD; ++d) s = fmaf(qs[d], k[d], s);
-  return s;
+  return half_dot(qs, k) + half_dot(qs + 4, k + 4);
 }
 
 template <typename TS>
@@ -607,6 +631,159 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col_pair(e2v2_attn_args A, con
   }
 }
 
+// Column pass over clusters of R consecutive key-CSR columns and one of four
+// channel groups (fp32).  Group g holds the 64 channels of heads 32g..32g+31
+// (c and c + 128 share a head); the workgroups of one XCD run group by group,
+// so its L2 holds a quarter of each neighbour row at a time and the gathered
+// rows of a column window stay resident.  Wave w applies the slots s = w mod 4
+// of each chunk (lane = channel of the group; for dk lane = (head, half of the
+// head's dims)); the four waves' partial sums are added once per cluster in
+// LDS in a fixed order.  Every slot's G_i and q_i are loaded once and applied
+// to each column of the cluster that it joins.
+
+template <int R>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_bwd_col_grp(e2v2_attn_args A, const float* __restrict__ G,
+                                                          const float* __restrict__ w_e,
+                                                          const float* __restrict__ dqk_e, float* __restrict__ dv_out,
+                                                          float* __restrict__ dk_out) {
+  constexpr int S = 32;                        // slots per staged chunk
+  __shared__ int ci[S];
+  __shared__ int ce[S][R];
+  __shared__ float cdv[S][R][3];
+  __shared__ float red[2][R][kNV + 4][kWave];  // per-wave partial sums, added in two rounds
+  const int n_cl = (A.n_rows + R - 1) / R;
+  int cl, grp;
+  if (!cluster_group(n_cl, cl, grp)) return;
+  const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
+  const int c = group_channel(grp, lane);
+  const int hc = c & (kH - 1);
+  const int hk = kGroupHeads * grp + (lane >> 1), d0 = 4 * (lane & 1);
+  const int j0 = cl * R, nj = min(R, A.n_rows - j0);
+  const size_t os = (size_t)A.n_rows * kC;
+  const int64_t base = A.key_ptr[j0];
+  const int ns = A.col_n_slots[cl];
+  const int32_t* __restrict__ smem = A.col_slot_member + base;
+  const int32_t* __restrict__ sedge = A.col_slot_edge + base * R;
+  const float* __restrict__ Qp = static_cast<const float*>(A.q);
+  float av[R][kNV];
+  float ak[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int z = 0; z < kNV; ++z) av[r][z] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) ak[r][d] = 0.f;
+  }
+  struct Loads {
+    float g[kNT];
+    float q[4];
+    float w[R];
+    float dq[R];
+  };
+  auto issue = [&](int sl, Loads& L) {
+    const int i = ci[sl];
+#pragma unroll
+    for (int z = 0; z < kNT; ++z) L.g[z] = G[(size_t)i * kC + z * os + c];
+    load4(Qp + ((size_t)i * kH + hk) * kD + d0, L.q);
+    // unconditional (an absent edge reads edge 0, unused): every slot issues the
+    // same loads, so the wait before apply() counts only the older slot's
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t e = max(ce[sl][r], 0);
+      L.w[r] = ntload(w_e + e * kH + hc);
+      L.dq[r] = ntload(dqk_e + e * kH + hk);
+    }
+  };
+  auto apply = [&](int sl, const Loads& L) {
+    float dA[kNV][3];
+    tp_transpose(L.g, dA);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (ce[sl][r] >= 0) {
+        const float w = L.w[r];
+        const float wx = w * cdv[sl][r][0], wy = w * cdv[sl][r][1], wz = w * cdv[sl][r][2];
+#pragma unroll
+        for (int z = 0; z < kNV; ++z)
+          av[r][z] = fmaf(dA[z][2], wz, fmaf(dA[z][1], wy, fmaf(dA[z][0], wx, av[r][z])));
+#pragma unroll
+        for (int d = 0; d < 4; ++d) ak[r][d] = fmaf(L.dq[r], L.q[d], ak[r][d]);
+      }
+    }
+  };
+  for (int s0 = 0; s0 < ns; s0 += S) {
+    const int nc = min(S, ns - s0);
+    if (t < nc) ci[t] = smem[s0 + t];
+    for (int idx = t; idx < nc * R; idx += 256) {
+      const int sl = idx / R, r = idx % R;
+      const int e = sedge[(int64_t)(s0 + sl) * R + r];
+      ce[sl][r] = e;
+      if (e >= 0) {
+        cdv[sl][r][0] = A.dvec[3 * (int64_t)e];
+        cdv[sl][r][1] = A.dvec[3 * (int64_t)e + 1];
+        cdv[sl][r][2] = A.dvec[3 * (int64_t)e + 2];
+      }
+    }
+    __syncthreads();
+    int sl = wave;
+    if (sl < nc) {
+      Loads La, Lb;
+      issue(sl, La);
+      for (; sl + 8 < nc; sl += 8) {
+        issue(sl + 4, Lb);
+        apply(sl, La);
+        issue(sl + 8, La);
+        apply(sl + 4, Lb);
+      }
+      if (sl + 4 < nc) {
+        issue(sl + 4, Lb);
+        apply(sl, La);
+        apply(sl + 4, Lb);
+      } else {
+        apply(sl, La);
+      }
+    }
+    __syncthreads();
+  }
+  // (w0 + w2) + (w1 + w3)
+  auto put = [&](int b) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int z = 0; z < kNV; ++z) red[b][r][z][lane] = av[r][z];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) red[b][r][kNV + d][lane] = ak[r][d];
+    }
+  };
+  auto add = [&](int b) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int z = 0; z < kNV; ++z) av[r][z] += red[b][r][z][lane];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) ak[r][d] += red[b][r][kNV + d][lane];
+    }
+  };
+  if (wave >= 2) put(wave - 2);
+  __syncthreads();
+  if (wave < 2) add(wave);
+  __syncthreads();
+  if (wave == 1) put(0);
+  __syncthreads();
+  if (wave == 0) {
+    add(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r < nj) {
+        const int j = j0 + r;
+#pragma unroll
+        for (int z = 0; z < kNV; ++z) ntstore(av[r][z], dv_out + (size_t)j * kC + z * os + c);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) ntstore(ak[r][d] / A.q_div, dk_out + ((size_t)j * kH + hk) * kD + d0 + d);
+      }
+    }
+  }
+}
+
 }  // namespace e2v2
 
 using namespace e2v2;
@@ -636,7 +813,11 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
   hipLaunchKernelGGL(k_attn_bwd_row<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, dgi, ddvec, ddist, dq,
                      w_edge, dqk_edge);
   E2V2_LAUNCHED("k_attn_bwd_row");
-  if constexpr (sizeof(TS) == 2) {
+  if (A.col_slot_member && sizeof(TS) == 4) {
+    const int n_cl = (A.n_rows + 3) / 4;
+    hipLaunchKernelGGL(k_attn_bwd_col_grp<4>, dim3(xcd_grid(n_cl) * kGroups), dim3(256), 0, s, A,
+                       reinterpret_cast<const float*>(G), w_edge, dqk_edge, dv, dk);
+  } else if constexpr (sizeof(TS) == 2) {
     hipLaunchKernelGGL(k_attn_bwd_col_pair<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
   } else {
     hipLaunchKernelGGL(k_attn_bwd_col_ch<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
@@ -651,6 +832,8 @@ E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, con
   const e2v2_attn_args& A = *args;
   E2V2_REQUIRE(A.n_heads == kH && A.head_dim == kD && A.channels == kC,
                "attn_bwd: built for H=%d D=%d C=%d", kH, kD, kC);
+  E2V2_REQUIRE(!A.col_slot_member || (A.col_span == 4 && A.col_slot_edge && A.col_n_slots),
+               "attn_bwd: column clusters need span 4 and all three slot arrays (span %d)", A.col_span);
   if (A.n_rows == 0) return 0;
   if (A.act_bf16)
     return attn_bwd_launch(A, static_cast<const __bf16*>(grad_out), static_cast<const __bf16*>(out), mrow, srow,

@@ -285,6 +285,138 @@ __global__ __launch_bounds__(256) void k_sort_cols(const int32_t* __restrict__ k
   for (int t = threadIdx.x; t < n; t += blockDim.x) key_eid[b + t] = (int32_t)sk[t];
 }
 
+// Clusters of `span` consecutive segments of a CSR (rows of the query CSR, or
+// columns of the key CSR).  The edge kernels process one cluster per
+// workgroup and load the features of a neighbour atom once for every segment
+// of the cluster that it joins, so each distinct (member atom, occurrence)
+// pair of a cluster becomes one slot: slot_member = the atom, slot_edge[span] =
+// for every segment of the cluster the edge joining it to that atom (-1 when
+// absent).  Occurrence k > 0 exists only when one segment holds the same atom
+// more than once (periodic images).  Slots are sorted by (atom, occurrence)
+// and stored from the cluster's first item on (a cluster never has more slots
+// than items).  A cluster with more than kMaxClusterItems items keeps one
+// slot per item in CSR order (correct, without the reuse).
+constexpr int kMaxClusterItems = 4096;
+
+__global__ __launch_bounds__(256) void k_cluster_slots(const int32_t* __restrict__ seg_ptr, int n_seg, int span,
+                                                       const int32_t* __restrict__ member,
+                                                       const int32_t* __restrict__ item_eid,
+                                                       int32_t* __restrict__ slot_member,
+                                                       int32_t* __restrict__ slot_edge,
+                                                       int32_t* __restrict__ n_slots) {
+  __shared__ uint64_t sk[kMaxClusterItems];
+  __shared__ int32_t gbase[kMaxClusterItems];
+  __shared__ int32_t part[256];
+  const int cl = blockIdx.x, t = threadIdx.x;
+  const int s0 = cl * span, s1 = min(s0 + span, n_seg);
+  const int b = seg_ptr[s0], n = seg_ptr[s1] - b;
+  auto eid_of = [&](int p) { return item_eid ? item_eid[p] : p; };
+  if (n > kMaxClusterItems) {
+    for (int q = t; q < n; q += 256) {
+      const int p = b + q;
+      int sg = 0;
+      while (sg + 1 < s1 - s0 && seg_ptr[s0 + sg + 1] <= p) ++sg;
+      const int e = eid_of(p);
+      slot_member[p] = member[e];
+      for (int r = 0; r < span; ++r) slot_edge[(int64_t)p * span + r] = (r == sg) ? e : -1;
+    }
+    if (t == 0) n_slots[cl] = n;
+    return;
+  }
+  // keys (member, segment, position) sorted ascending
+  int p2 = 1;
+  while (p2 < n) p2 <<= 1;
+  for (int q = t; q < p2; q += 256) {
+    uint64_t k = ~0ull;
+    if (q < n) {
+      const int p = b + q;
+      int sg = 0;
+      while (sg + 1 < s1 - s0 && seg_ptr[s0 + sg + 1] <= p) ++sg;
+      k = ((uint64_t)(uint32_t)member[eid_of(p)] << 32) | ((uint64_t)sg << 16) | (uint64_t)q;
+    }
+    sk[q] = k;
+  }
+  __syncthreads();
+  for (int k = 2; k <= p2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int q = t; q < p2; q += 256) {
+        const int x = q ^ j;
+        if (x > q) {
+          const uint64_t a = sk[q], c = sk[x];
+          if ((a > c) == ((q & k) == 0)) {
+            sk[q] = c;
+            sk[x] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // per item: occurrence = rank among equal (member, segment); per member group: slot count
+  // = 1 + max occurrence, written at the group's first item
+  auto occ_of = [&](int q) {
+    int o = 0;
+    while (q - o - 1 >= 0 && (sk[q - o - 1] >> 16) == (sk[q] >> 16)) ++o;
+    return o;
+  };
+  constexpr int kPer = kMaxClusterItems / 256;
+  int local = 0;
+  for (int z = 0; z < kPer; ++z) {
+    const int q = t * kPer + z;
+    int cnt = 0;
+    if (q < n && (q == 0 || (sk[q - 1] >> 32) != (sk[q] >> 32))) {
+      int mx = 0;
+      for (int u = q; u < n && (sk[u] >> 32) == (sk[q] >> 32); ++u) mx = max(mx, occ_of(u));
+      cnt = mx + 1;
+    }
+    gbase[q] = cnt;
+    local += cnt;
+  }
+  part[t] = local;
+  __syncthreads();
+  __shared__ int total;
+  if (t == 0) {
+    int acc = 0;
+    for (int u = 0; u < 256; ++u) {
+      const int v = part[u];
+      part[u] = acc;
+      acc += v;
+    }
+    total = acc;
+    n_slots[cl] = acc;
+  }
+  __syncthreads();
+  int run = part[t];
+  for (int z = 0; z < kPer; ++z) {
+    const int q = t * kPer + z;
+    const int v = gbase[q];
+    gbase[q] = run;
+    run += v;
+  }
+  __syncthreads();
+  // group heads initialise their slots, then every item writes its edge
+  for (int q = t; q < n; q += 256) {
+    if (q == 0 || (sk[q - 1] >> 32) != (sk[q] >> 32)) {
+      // exclusive scan: the item after a group head carries the head's base + count
+      const int cnt = ((q + 1 < n) ? gbase[q + 1] : total) - gbase[q];
+      for (int o = 0; o < cnt; ++o) {
+        const int64_t sl = (int64_t)b + gbase[q] + o;
+        slot_member[sl] = (int32_t)(sk[q] >> 32);
+        for (int r = 0; r < span; ++r) slot_edge[sl * span + r] = -1;
+      }
+    }
+  }
+  __syncthreads();
+  for (int q = t; q < n; q += 256) {
+    int g = q;
+    while (g > 0 && (sk[g - 1] >> 32) == (sk[q] >> 32)) --g;
+    const int sg = (int)((sk[q] >> 16) & 0xffff);
+    const int pos = (int)(sk[q] & 0xffff);
+    const int64_t sl = (int64_t)b + gbase[g] + occ_of(q);
+    slot_edge[sl * span + sg] = eid_of(b + pos);
+  }
+}
+
 // keep the first k entries of each row (rows already sorted by distance)
 __global__ void k_topk_count(const int32_t* __restrict__ row_ptr, int n_rows, int k, int32_t* __restrict__ cnt) {
   int r = blockIdx.x * blockDim.x + threadIdx.x;
@@ -400,6 +532,18 @@ E2V2_API int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* c
   hipLaunchKernelGGL(k_topk_compact, dim3(n_rows), dim3(128), 0, s, row_ptr, new_ptr, n_rows, col, shift, dvec, dist,
                      ocol, oshift, odv, od);
   E2V2_LAUNCHED("k_topk_compact");
+  return 0;
+}
+
+E2V2_API int e2v2_cluster_slots(const int32_t* seg_ptr, int32_t n_seg, const int32_t* member,
+                                const int32_t* item_eid, int32_t span, int32_t* slot_member, int32_t* slot_edge,
+                                int32_t* n_slots, hipStream_t s) {
+  E2V2_REQUIRE(span >= 1 && span <= 16, "cluster_slots: span must be 1..16, got %d", span);
+  if (n_seg <= 0) return 0;
+  const int n_cl = (n_seg + span - 1) / span;
+  hipLaunchKernelGGL(k_cluster_slots, dim3(n_cl), dim3(256), 0, s, seg_ptr, n_seg, span, member, item_eid,
+                     slot_member, slot_edge, n_slots);
+  E2V2_LAUNCHED("k_cluster_slots");
   return 0;
 }
 

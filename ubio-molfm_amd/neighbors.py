@@ -82,6 +82,15 @@ class NeighborList:
     key_ptr: torch.Tensor     # [N+1] int32
     key_eid: torch.Tensor     # [E] int32
     max_row: int = 0
+    # clusters of consecutive query rows / key-CSR columns for the attention kernels
+    row_span: int = 0
+    row_slot_member: Optional[torch.Tensor] = None   # [E] int32
+    row_slot_edge: Optional[torch.Tensor] = None     # [E, row_span] int32
+    row_n_slots: Optional[torch.Tensor] = None       # [ceil(N / row_span)] int32
+    col_span: int = 0
+    col_slot_member: Optional[torch.Tensor] = None   # [E] int32
+    col_slot_edge: Optional[torch.Tensor] = None     # [E, col_span] int32
+    col_n_slots: Optional[torch.Tensor] = None       # [ceil(N / col_span)] int32
 
     def canonical(self):
         """(i, j, s) sorted lexicographically, plus dvec/dist in that order (numpy)."""
@@ -213,5 +222,29 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
               _lib.i64(E), _lib.vp(_ptr(edge_row)), _lib.vp(key_cnt.data_ptr()), _lib.vp(key_ptr.data_ptr()),
               _lib.vp(stats.data_ptr()), _lib.vp(tkey.data_ptr()), _lib.vp(_ptr(key_eid)), _lib.i32(1),
               _lib.vp(stream))
-    return NeighborList(N, E, row_ptr, col, sh, torch.as_tensor(shifts_np), dvec, dist, edge_row, key_ptr, key_eid,
-                        max_row)
+    nl = NeighborList(N, E, row_ptr, col, sh, torch.as_tensor(shifts_np), dvec, dist, edge_row, key_ptr, key_eid,
+                      max_row)
+    if N > 0 and E > 0:
+        nl.col_span = COL_SPAN
+        nl.col_slot_member, nl.col_slot_edge, nl.col_n_slots = cluster_slots(key_ptr, N, edge_row, key_eid,
+                                                                             COL_SPAN)
+    return nl
+
+
+COL_SPAN = 4
+
+
+def cluster_slots(seg_ptr: torch.Tensor, n_seg: int, member: torch.Tensor, item_eid: Optional[torch.Tensor],
+                  span: int):
+    """Slots of clusters of ``span`` consecutive CSR segments (e2v2_cluster_slots):
+    (slot_member [items], slot_edge [items, span], n_slots [clusters])."""
+    dev = seg_ptr.device
+    n_items = int(member.shape[0])
+    i32 = dict(dtype=torch.int32, device=dev)
+    sm = torch.empty(max(n_items, 1), **i32)
+    se = torch.empty(max(n_items, 1), span, **i32)
+    ns = torch.empty(max((n_seg + span - 1) // span, 1), **i32)
+    _lib.call("e2v2_cluster_slots", _lib.vp(seg_ptr.data_ptr()), _lib.i32(n_seg), _lib.vp(member.data_ptr()),
+              _lib.vp(_ptr(item_eid)), _lib.i32(span), _lib.vp(sm.data_ptr()), _lib.vp(se.data_ptr()),
+              _lib.vp(ns.data_ptr()), _lib.vp(torch.cuda.current_stream(dev).cuda_stream))
+    return sm, se, ns

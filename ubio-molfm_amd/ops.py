@@ -210,6 +210,25 @@ class DegreeEmbedFn(torch.autograd.Function):
         return ddv[:E], dd[:E], None, None, None, None, None, None, None
 
 
+def attn_args(nl: NeighborList, q, k, v, gi, q_div: float, rc: float, bf: int):
+    """e2v2_attn_args over the neighbour list (with its column clusters when built)."""
+    a = _lib.AttnArgs(nl.n_atoms, nl.n_edges, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(),
+                      nl.edge_row.data_ptr(), nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(),
+                      nl.dist.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(q_div),
+                      float(rc), ENV_A, ENV_B, ENV_C, int(bf))
+    if nl.row_slot_member is not None:
+        a.row_span = nl.row_span
+        a.row_slot_member = nl.row_slot_member.data_ptr()
+        a.row_slot_edge = nl.row_slot_edge.data_ptr()
+        a.row_n_slots = nl.row_n_slots.data_ptr()
+    if nl.col_slot_member is not None:
+        a.col_span = nl.col_span
+        a.col_slot_member = nl.col_slot_member.data_ptr()
+        a.col_slot_edge = nl.col_slot_edge.data_ptr()
+        a.col_n_slots = nl.col_n_slots.data_ptr()
+    return a
+
+
 class AttentionFn(torch.autograd.Function):
     """Edge part of E2AttentionArbOrder_sparse.forward (e2former.py:238-433) up to
     the SO(2) product's forward_linear: returns the 20-row l3-sequential tensor
@@ -232,10 +251,7 @@ class AttentionFn(torch.autograd.Function):
         sn, sr = mlp_save_buffers(1, E, dev)
         margs = mlp_args(nl, node_type, packed, sn, sr)
         _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(gi), _lib.i32(256), _stream(q))
-        args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
-                             nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
-                             q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(q_div), float(rc),
-                             ENV_A, ENV_B, ENV_C, bf)
+        args = attn_args(nl, q, k, v, gi, q_div, rc, bf)
         out = torch.empty(20, N, 256, dtype=act_dtype, device=dev)   # m-major
         mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
@@ -255,10 +271,7 @@ class AttentionFn(torch.autograd.Function):
         dev = q.device
         E, N = nl.n_edges, nl.n_atoms
         gout = gout.to(out.dtype).contiguous()
-        args = _lib.AttnArgs(N, E, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(), nl.edge_row.data_ptr(),
-                             nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
-                             q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(ctx.q_div),
-                             float(ctx.rc), ENV_A, ENV_B, ENV_C, ctx.bf)
+        args = attn_args(nl, q, k, v, gi, ctx.q_div, ctx.rc, ctx.bf)
         f = dict(dtype=torch.float32, device=dev)
         dgi = torch.empty(max(E, 1), 256, **f)
         ddv = torch.empty(max(E, 1), 3, **f)
