@@ -182,10 +182,9 @@ typedef struct e2v2_attn_args {
   float q_div;                   /* sqrt(D)                                         */
   float rc, env_a, env_b, env_c; /* polynomial envelope                             */
   int32_t act_bf16;              /* 1: q, k, v, out, grad_out stored as bf16 (fp32 math) */
-  /* Optional clusters from e2v2_cluster_slots (NULL: one workgroup per row / column):
-     query-CSR rows in clusters of row_span (4), key-CSR columns in clusters of col_span (4 or 8). */
-  int32_t row_span, col_span;
-  const int32_t* row_slot_member; const int32_t* row_slot_edge; const int32_t* row_n_slots;
+  /* Optional key-CSR column clusters from e2v2_cluster_slots with span col_span = 4 (NULL: one
+     workgroup per column); used by the fp32 column pass of e2v2_attn_bwd. */
+  int32_t col_span;
   const int32_t* col_slot_member; const int32_t* col_slot_edge; const int32_t* col_n_slots;
 } e2v2_attn_args;
 

@@ -195,7 +195,6 @@ def _attention_case(pkg, cuda, act_dtype, clusters=True):
     args = ops.attn_args(nl, qd, kd, vd, gid, math.sqrt(8.0), 6.0, int(bf))
     if not clusters:
         args.col_slot_member = args.col_slot_edge = args.col_n_slots = None
-        args.row_slot_member = args.row_slot_edge = args.row_n_slots = None
     out = torch.empty(20, N, 256, device=cuda, dtype=act_dtype); m = torch.empty(N, 128, device=cuda)
     sr = torch.empty(N, 128, device=cuda); cnt = torch.empty(N, 128, dtype=torch.int32, device=cuda)
     _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _lib.vp(out.data_ptr()), _lib.vp(m.data_ptr()),
@@ -222,7 +221,7 @@ def _attention_case(pkg, cuda, act_dtype, clusters=True):
     return e_f, errs
 
 
-@pytest.mark.parametrize("clusters", [True, False], ids=["clusters", "per_row"])
+@pytest.mark.parametrize("clusters", [True, False], ids=["clusters", "per_column"])
 def test_attention_forward_backward(pkg, cuda, clusters):
     e_f, errs = _attention_case(pkg, cuda, torch.float32, clusters)
     assert e_f < 2e-5

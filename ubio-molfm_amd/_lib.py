@@ -46,9 +46,7 @@ class AttnArgs(C.Structure):
                 ("row_ptr", vp), ("col", vp), ("edge_row", vp), ("key_ptr", vp), ("key_eid", vp),
                 ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("gi", vp),
                 ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32),
-                ("row_span", i32), ("col_span", i32),
-                ("row_slot_member", vp), ("row_slot_edge", vp), ("row_n_slots", vp),
-                ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp)]
+                ("col_span", i32), ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp)]
 
 
 class DegArgs(C.Structure):

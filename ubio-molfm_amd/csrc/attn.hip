@@ -247,193 +247,6 @@ __device__ __forceinline__ void tp_transpose(const float (&g)[kNT], float (&dA)[
   for (int z = 0; z < kTpNnz; ++z) dA[kTp[z].r][kTp[z].k] = fmaf(kTp[z].c, g[kTp[z].t], dA[kTp[z].r][kTp[z].k]);
 }
 
-// Row pass.  One workgroup per query atom i.  Thread t owns channel c = t in
-// the transposed aggregation (dA_c = T^T G_i[:, c], 27 registers) and head
-// h = t % 128 with edge parity t / 128 in the logit and softmax phases.
-// Per-edge sums over the 256 channels (dL/d dvec) reduce by DPP within rows
-// of 16 lanes and then over the 16 row partials in LDS; the per-head dL/dw
-// adds the head's two channels (h, h + 128) in LDS.
-template <typename TS>
-__global__ __launch_bounds__(256) void k_attn_bwd_row(e2v2_attn_args A, const TS* __restrict__ G,
-                                                      const TS* __restrict__ O, const float* __restrict__ mrow,
-                                                      const float* __restrict__ srow, const int32_t* __restrict__ cnt,
-                                                      float* __restrict__ dgi, float* __restrict__ ddv,
-                                                      float* __restrict__ dd, float* __restrict__ dq,
-                                                      float* __restrict__ w_out, float* __restrict__ dqk_out) {
-  __shared__ float a_s[kCHB][kH];
-  __shared__ float qk_s[kCHB][kH];
-  __shared__ float w_s[kCHB][kH];
-  __shared__ float dwc_s[kCHB][kC];
-  __shared__ float gp_s[kCHB][16][3];
-  __shared__ float dd_s[kCHB][2];
-  __shared__ float head_m[kH], head_inv[kH], head_dsum[kH], head_dmc[kH];
-  __shared__ float gdot_s[kH];
-  __shared__ float dq_s[kH][kD];
-  __shared__ ChunkEdges ce;
-  const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
-  if (i >= A.n_rows) return;
-  const int lane = t & 63, wave = t >> 6;
-  const int h = t & (kH - 1), half = t >> 7;
-  const int c = t;                      // channel c; its head is c % 128 = h
-  const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
-  const Envelope env = make_env(A);
-  const size_t os = (size_t)A.n_rows * kC;
-  // ---- per-row prologue: dA of channel c and D_h = sum_{c in h} sum_t G out
-  float dA[kNV][3];
-  {
-    float g[kNT];
-    float sdot = 0.f;
-#pragma unroll
-    for (int z = 0; z < kNT; ++z) {
-      g[z] = f32(G[(size_t)i * kC + z * os + c]);
-      sdot = fmaf(g[z], f32(O[(size_t)i * kC + z * os + c]), sdot);
-    }
-    tp_transpose(g, dA);
-    if (half) gdot_s[h] = sdot;
-    __syncthreads();
-    if (!half) {
-      const float Dh = sdot + gdot_s[h];
-      const float s = srow[(size_t)i * kH + h];
-      const float inv = 1.0f / (s + kEps);
-      const int cn = cnt[(size_t)i * kH + h];
-      head_m[h] = mrow[(size_t)i * kH + h];
-      head_inv[h] = inv;
-      head_dsum[h] = Dh * inv;
-      head_dmc[h] = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
-    }
-  }
-  const TS* __restrict__ Kp = static_cast<const TS*>(A.k);
-  const TS* __restrict__ Vp = static_cast<const TS*>(A.v);
-  float qs[kD];
-  load_qs<TS>(A, i, h, qs);
-  float dqa[kD];
-#pragma unroll
-  for (int d = 0; d < kD; ++d) dqa[d] = 0.f;
-  __syncthreads();
-  for (int c0 = 0; c0 < n; c0 += kCHB) {
-    const int nc = min(kCHB, n - c0);
-    load_chunk(A, env, b + c0, nc, ce);
-    __syncthreads();
-    // ---- phase 1: recompute logits and final weights (thread per head, edge parity)
-    for (int el = half; el < nc; el += 2) {
-      const int64_t e = (int64_t)b + c0 + el;
-      const float qk = qk_dot(qs, Kp + ((size_t)ce.j[el] * kH + h) * kD);
-      const float a = A.gi[e * (2 * kH) + h] * qk;
-      a_s[el][h] = a;
-      qk_s[el][h] = qk;
-      const float ee = expf(a - head_m[h]) * ce.p[el];
-      const float alpha = (ee * A.gi[e * (2 * kH) + kH + h]) * head_inv[h];
-      const float w = alpha * ce.rR[el];
-      w_s[el][h] = w;
-      w_out[e * kH + h] = w;
-    }
-    __syncthreads();
-    // ---- phase 2: transposed aggregation, thread per channel, two edges per step
-    {
-      const TS* vb = Vp + c;
-      auto edge = [&](int el, const float (&vr)[kNV]) {
-        float u0 = 0.f, u1 = 0.f, u2 = 0.f;
-#pragma unroll
-        for (int r = 0; r < kNV; ++r) {
-          u0 = fmaf(dA[r][0], vr[r], u0);
-          u1 = fmaf(dA[r][1], vr[r], u1);
-          u2 = fmaf(dA[r][2], vr[r], u2);
-        }
-        dwc_s[el][c] = u0 * ce.dv[el][0] + u1 * ce.dv[el][1] + u2 * ce.dv[el][2];
-        const float w = w_s[el][h];
-        const float g0 = dpp_row_sum16(w * u0);
-        const float g1 = dpp_row_sum16(w * u1);
-        const float g2 = dpp_row_sum16(w * u2);
-        if ((lane & 15) == 0) {
-          const int p = wave * 4 + (lane >> 4);
-          gp_s[el][p][0] = g0;
-          gp_s[el][p][1] = g1;
-          gp_s[el][p][2] = g2;
-        }
-      };
-      int el = 0;
-      for (; el + 1 < nc; el += 2) {
-        const TS* v0 = vb + (size_t)ce.j[el] * kC;
-        const TS* v1 = vb + (size_t)ce.j[el + 1] * kC;
-        float va[kNV], vc[kNV];
-#pragma unroll
-        for (int r = 0; r < kNV; ++r) {
-          va[r] = f32(v0[r * os]);
-          vc[r] = f32(v1[r * os]);
-        }
-        edge(el, va);
-        edge(el + 1, vc);
-      }
-      if (el < nc) {
-        const TS* v0 = vb + (size_t)ce.j[el] * kC;
-        float va[kNV];
-#pragma unroll
-        for (int r = 0; r < kNV; ++r) va[r] = f32(v0[r * os]);
-        edge(el, va);
-      }
-    }
-    __syncthreads();
-    // ---- phase 3: softmax / gate / distance backward (thread per head, edge parity)
-    for (int el = half; el < nc; el += 2) {
-      const int64_t e = (int64_t)b + c0 + el;
-      const float dw = dwc_s[el][h] + dwc_s[el][h + kH];
-      const float a = a_s[el][h];
-      const float qk = qk_s[el][h];
-      const float gate = A.gi[e * (2 * kH) + h];
-      const float ih = A.gi[e * (2 * kH) + kH + h];
-      const float ex = expf(a - head_m[h]);
-      const float ee = ex * ce.p[el];
-      const float inv = head_inv[h];
-      const float alpha = (ee * ih) * inv;
-      const float rR = ce.rR[el];
-      const float dalpha = dw * rR;
-      const float dR = (ce.d[el] > 1e-6f) ? -dalpha * alpha * rR : 0.f;
-      const float dih = dalpha * ee * inv;
-      const float de = dalpha * ih * inv - head_dsum[h];
-      float da = de * ee;
-      if (a == head_m[h]) da += head_dmc[h];
-      const float dpv = de * ex;
-      const float dgate = da * qk;
-      const float dqk = da * gate;
-      dgi[e * (2 * kH) + h] = dgate;
-      dgi[e * (2 * kH) + kH + h] = dih;
-      dqk_out[e * kH + h] = dqk;
-      float kv[kD];
-      load8(Kp + ((size_t)ce.j[el] * kH + h) * kD, kv);
-#pragma unroll
-      for (int d = 0; d < kD; ++d) dqa[d] = fmaf(dqk, kv[d], dqa[d]);
-      float ddist = fmaf(dpv, ce.dp[el], dR);
-      ddist = wave_sum(ddist);
-      if (lane == 0) dd_s[el][(t & (kH - 1)) >> 6] = ddist;
-    }
-    __syncthreads();
-    if (t < nc) {
-      const int64_t e = (int64_t)b + c0 + t;
-      float gx = 0.f, gy = 0.f, gz = 0.f;
-#pragma unroll
-      for (int p = 0; p < 16; ++p) {
-        gx += gp_s[t][p][0];
-        gy += gp_s[t][p][1];
-        gz += gp_s[t][p][2];
-      }
-      ddv[3 * e] = gx;
-      ddv[3 * e + 1] = gy;
-      ddv[3 * e + 2] = gz;
-      dd[e] = dd_s[t][0] + dd_s[t][1];
-    }
-    __syncthreads();
-  }
-  if (half == 1) {
-#pragma unroll
-    for (int d = 0; d < kD; ++d) dq_s[h][d] = dqa[d];
-  }
-  __syncthreads();
-  if (half == 0) {
-#pragma unroll
-    for (int d = 0; d < kD; ++d) dq[((size_t)i * kH + h) * kD + d] = (dqa[d] + dq_s[h][d]) / A.q_div;
-  }
-}
-
 // Column pass, one channel per thread (the fp32 form: a 4-byte gather per lane
 // is as cheap per byte for the address unit as a pair load): for every source
 // atom j, sum over its key-CSR edges (ascending edge id) -> dv_j and dk_j.
@@ -784,6 +597,187 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   }
 }
 
+template <typename TS>
+struct HeadEdge {
+  float k[kD];
+  float v0[kNV], v1[kNV];
+  float gate, ih;
+};
+
+// Backward row pass, one workgroup per query row; thread t owns head h = t % 128
+// with both of its channels (h, h + 128) and the row's edges of parity t / 128.
+// The edge index is uniform per wave (scalar loads of the edge record), and
+// the gathers of the next edge are issued before the current one is applied.
+// Per edge a thread recomputes its logit and
+// weight, forms u = dA^T v_j for both channels (dA = T^T G_i) and with it the
+// head's dL/dw, runs the softmax / gate / distance backward for its head and
+// accumulates dq from the k_j row it already holds, so nothing crosses threads
+// but the per-edge sums over heads (dL/d dvec, dL/dd): row sums by DPP, the
+// four rows of a wave by lane reads, the two waves of a parity in LDS, added
+// in a fixed order once per chunk of up to 128 edges.
+template <typename TS>
+__global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const TS* __restrict__ G,
+                                                         const TS* __restrict__ O, const float* __restrict__ mrow,
+                                                         const float* __restrict__ srow,
+                                                         const int32_t* __restrict__ cnt, float* __restrict__ dgi,
+                                                         float* __restrict__ ddv, float* __restrict__ dd,
+                                                         float* __restrict__ dq, float* __restrict__ w_out,
+                                                         float* __restrict__ dqk_out) {
+  constexpr int CH = 64;                      // edges per parity and reduction chunk
+  __shared__ float part[2 * CH][2][4];
+  __shared__ float dq_s[kH][kD];
+  const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
+  if (i >= A.n_rows) return;
+  const int h = t & (kH - 1), par = t >> 7, lane = t & (kWave - 1), wsub = (t >> 6) & 1;
+  const TS* __restrict__ Kp = static_cast<const TS*>(A.k);
+  const TS* __restrict__ Vp = static_cast<const TS*>(A.v);
+  const size_t os = (size_t)A.n_rows * kC;
+  const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
+  const Envelope env = make_env(A);
+  // per-row prologue: dA of both channels, D_h, softmax statistics of head h
+  float dA0[kNV][3], dA1[kNV][3];
+  float inv, dsum, dmc, m;
+  {
+    float g0[kNT], g1[kNT];
+    float Dh = 0.f;
+#pragma unroll
+    for (int z = 0; z < kNT; ++z) {
+      g0[z] = f32(G[(size_t)i * kC + z * os + h]);
+      g1[z] = f32(G[(size_t)i * kC + z * os + h + kH]);
+    }
+    // D_h = sum over the head's channels and the 20 rows, summed as channel h then h + 128
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int z = 0; z < kNT; ++z) {
+      d0 = fmaf(g0[z], f32(O[(size_t)i * kC + z * os + h]), d0);
+      d1 = fmaf(g1[z], f32(O[(size_t)i * kC + z * os + h + kH]), d1);
+    }
+    Dh = d1 + d0;
+    tp_transpose(g0, dA0);
+    tp_transpose(g1, dA1);
+    m = mrow[(size_t)i * kH + h];
+    const float s = srow[(size_t)i * kH + h];
+    const int cn = cnt[(size_t)i * kH + h];
+    inv = 1.0f / (s + kEps);
+    dsum = Dh * inv;
+    dmc = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
+  }
+  float qs[kD];
+  load_qs<TS>(A, i, h, qs);
+  float dqa[kD];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) dqa[d] = 0.f;
+  using L = HeadEdge<TS>;
+  auto issue = [&](int el, L& X) {
+    const int64_t e = (int64_t)b + el;
+    const int j = A.col[e];
+    load8(Kp + ((size_t)j * kH + h) * kD, X.k);
+    const TS* vp = Vp + (size_t)j * kC + h;
+#pragma unroll
+    for (int r = 0; r < kNV; ++r) {
+      X.v0[r] = f32(vp[r * os]);
+      X.v1[r] = f32(vp[r * os + kH]);
+    }
+    X.gate = A.gi[e * (2 * kH) + h];
+    X.ih = A.gi[e * (2 * kH) + kH + h];
+  };
+  auto apply = [&](int el, int slot, const L& X) {
+    const int64_t e = (int64_t)b + el;
+    const float d = A.dist[e];
+    float pe, dpe;
+    env.eval(d, pe, dpe);
+    const float rR = 1.0f / fmaxf(d, 1e-6f);
+    const float dvx = A.dvec[3 * e], dvy = A.dvec[3 * e + 1], dvz = A.dvec[3 * e + 2];
+    const float qk = half_dot(qs, X.k) + half_dot(qs + 4, X.k + 4);
+    const float a = X.gate * qk;
+    const float ex = expf(a - m);
+    const float ee = ex * pe;
+    const float alpha = (ee * X.ih) * inv;
+    const float w = alpha * rR;
+    float U[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      float u0 = 0.f, u1 = 0.f;
+#pragma unroll
+      for (int r = 0; r < kNV; ++r) {
+        u0 = fmaf(dA0[r][k], X.v0[r], u0);
+        u1 = fmaf(dA1[r][k], X.v1[r], u1);
+      }
+      U[k] = u0 + u1;
+    }
+    const float dw = U[0] * dvx + U[1] * dvy + U[2] * dvz;
+    const float dalpha = dw * rR;
+    const float dR = (d > 1e-6f) ? -dalpha * alpha * rR : 0.f;
+    const float dih = dalpha * ee * inv;
+    const float de = dalpha * X.ih * inv - dsum;
+    float da = de * ee;
+    if (a == m) da += dmc;
+    const float dpv = de * ex;
+    const float dqk = da * X.gate;
+    ntstore(w, w_out + e * kH + h);
+    ntstore(da * qk, dgi + e * (2 * kH) + h);
+    ntstore(dih, dgi + e * (2 * kH) + kH + h);
+    ntstore(dqk, dqk_out + e * kH + h);
+#pragma unroll
+    for (int q = 0; q < kD; ++q) dqa[q] = fmaf(dqk, X.k[q], dqa[q]);
+    // sums over the 64 heads of this wave: rows of 16 by DPP, then the four rows
+    float r4[4] = {w * U[0], w * U[1], w * U[2], fmaf(dpv, dpe, dR)};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float x = dpp_row_sum16(r4[k]);
+      r4[k] = ((__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0)) +
+                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16))) +
+               __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32))) +
+              __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48));
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) part[slot][wsub][k] = r4[k];
+    }
+  };
+  for (int c0 = 0; c0 < n; c0 += 2 * CH) {
+    const int nc = min(2 * CH, n - c0);
+    {
+      L Xa, Xb;
+      int el = par;
+      if (el < nc) {
+        issue(c0 + el, Xa);
+        for (; el + 4 < nc; el += 4) {
+          issue(c0 + el + 2, Xb);
+          apply(c0 + el, el, Xa);
+          issue(c0 + el + 4, Xa);
+          apply(c0 + el + 2, el + 2, Xb);
+        }
+        if (el + 2 < nc) {
+          issue(c0 + el + 2, Xb);
+          apply(c0 + el, el, Xa);
+          apply(c0 + el + 2, el + 2, Xb);
+        } else {
+          apply(c0 + el, el, Xa);
+        }
+      }
+    }
+    __syncthreads();
+    if (t < nc) {
+      const int64_t e = (int64_t)b + c0 + t;
+      ddv[3 * e] = part[t][0][0] + part[t][1][0];
+      ddv[3 * e + 1] = part[t][0][1] + part[t][1][1];
+      ddv[3 * e + 2] = part[t][0][2] + part[t][1][2];
+      dd[e] = part[t][0][3] + part[t][1][3];
+    }
+    __syncthreads();
+  }
+  if (par) {
+#pragma unroll
+    for (int q = 0; q < kD; ++q) dq_s[h][q] = dqa[q];
+  }
+  __syncthreads();
+  if (!par) {
+#pragma unroll
+    for (int q = 0; q < kD; ++q) dq[((size_t)i * kH + h) * kD + q] = (dqa[q] + dq_s[h][q]) / A.q_div;
+  }
+}
+
 }  // namespace e2v2
 
 using namespace e2v2;
@@ -810,7 +804,7 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
                            const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
                            float* w_edge, float* dqk_edge, hipStream_t s) {
   const dim3 grid(xcd_grid(A.n_rows));
-  hipLaunchKernelGGL(k_attn_bwd_row<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, dgi, ddvec, ddist, dq,
+  hipLaunchKernelGGL(k_attn_bwd_row_hp<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, dgi, ddvec, ddist, dq,
                      w_edge, dqk_edge);
   E2V2_LAUNCHED("k_attn_bwd_row");
   if (A.col_slot_member && sizeof(TS) == 4) {

@@ -82,11 +82,7 @@ class NeighborList:
     key_ptr: torch.Tensor     # [N+1] int32
     key_eid: torch.Tensor     # [E] int32
     max_row: int = 0
-    # clusters of consecutive query rows / key-CSR columns for the attention kernels
-    row_span: int = 0
-    row_slot_member: Optional[torch.Tensor] = None   # [E] int32
-    row_slot_edge: Optional[torch.Tensor] = None     # [E, row_span] int32
-    row_n_slots: Optional[torch.Tensor] = None       # [ceil(N / row_span)] int32
+    # clusters of consecutive key-CSR columns for the attention column pass
     col_span: int = 0
     col_slot_member: Optional[torch.Tensor] = None   # [E] int32
     col_slot_edge: Optional[torch.Tensor] = None     # [E, col_span] int32

@@ -216,11 +216,6 @@ def attn_args(nl: NeighborList, q, k, v, gi, q_div: float, rc: float, bf: int):
                       nl.edge_row.data_ptr(), nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(),
                       nl.dist.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(q_div),
                       float(rc), ENV_A, ENV_B, ENV_C, int(bf))
-    if nl.row_slot_member is not None:
-        a.row_span = nl.row_span
-        a.row_slot_member = nl.row_slot_member.data_ptr()
-        a.row_slot_edge = nl.row_slot_edge.data_ptr()
-        a.row_n_slots = nl.row_n_slots.data_ptr()
     if nl.col_slot_member is not None:
         a.col_span = nl.col_span
         a.col_slot_member = nl.col_slot_member.data_ptr()
