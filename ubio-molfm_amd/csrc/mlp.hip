@@ -21,6 +21,7 @@
 // load a GEMM's entire per-wave B panel into registers while the previous stage
 // computes; the backward prefetches the saved LayerNorm inputs before the GEMM
 // whose output they normalise.
+#include <algorithm>
 #include <cmath>
 
 #include "common.h"
@@ -194,7 +195,12 @@ __device__ __forceinline__ void load_ln_params(const e2v2_mlp_weights& W, LnPara
 
 // Row-wise LayerNorm(128) + SiLU of the fp32 rows of Y (8 threads per row),
 // written to the next GEMM's A operand (fp32 in place, or bf16).  Rows below
-// nsave also store the normalised (pre-affine) values and rstd.
+// nsave also store the normalised (pre-affine) values and rstd.  Thread sub of
+// a row owns columns ln_col(sub, q) = 4 sub + 32 (q / 4) + q % 4: for each q / 4
+// the row's 8 threads cover 128 contiguous bytes, so the saved rows are written
+// (and read back by the backward) as whole cache lines with 16-byte accesses.
+__device__ __forceinline__ int ln_col(int sub, int q) { return 4 * sub + 32 * (q >> 2) + (q & 3); }
+
 template <typename OutT>
 __device__ __forceinline__ void ln_silu_rows(const float* Y, int ldy, OutT* Z, int ldz, const float* g,
                                              const float* b, float* __restrict__ nrm, int ldn,
@@ -205,7 +211,7 @@ __device__ __forceinline__ void ln_silu_rows(const float* Y, int ldy, OutT* Z, i
   float s = 0.f;
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
-    v[q] = y[sub + 8 * q];
+    v[q] = y[ln_col(sub, q)];
     s += v[q];
   }
   s += __shfl_xor(s, 1, 64);
@@ -224,14 +230,20 @@ __device__ __forceinline__ void ln_silu_rows(const float* Y, int ldy, OutT* Z, i
   const float rstd = frsq(s2 * (1.0f / kH) + 1e-5f);
   const bool save = nrm != nullptr && row < nsave;
   OutT* z = Z + row * ldz;
+  float nv[16];
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
-    const int c = sub + 8 * q;
-    const float n = (v[q] - mean) * rstd;
-    if (save) nrm[(size_t)row * ldn + c] = n;
-    z[c] = (OutT)silu(n * g[c] + b[c]);
+    const int c = ln_col(sub, q);
+    nv[q] = (v[q] - mean) * rstd;
+    z[c] = (OutT)silu(nv[q] * g[c] + b[c]);
   }
-  if (save && sub == 0) rstd_out[(size_t)row * rstd_stride] = rstd;
+  if (save) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+      *reinterpret_cast<floatx4*>(nrm + (size_t)row * ldn + ln_col(sub, 4 * q4)) =
+          floatx4{nv[4 * q4], nv[4 * q4 + 1], nv[4 * q4 + 2], nv[4 * q4 + 3]};
+    if (sub == 0) rstd_out[(size_t)row * rstd_stride] = rstd;
+  }
 }
 
 // Saved LayerNorm input of this thread's row (8 threads per row, 16 columns each)
@@ -246,7 +258,12 @@ __device__ __forceinline__ void load_saved_row(const float* __restrict__ nrm, in
   const int row = threadIdx.x >> 3, sub = threadIdx.x & 7;
   const bool ok = row < nvalid;
 #pragma unroll
-  for (int q = 0; q < 16; ++q) sr.n[q] = ok ? nrm[(size_t)row * ldn + sub + 8 * q] : 0.f;
+  for (int q4 = 0; q4 < 4; ++q4) {
+    const floatx4 v = ok ? *reinterpret_cast<const floatx4*>(nrm + (size_t)row * ldn + ln_col(sub, 4 * q4))
+                         : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sr.n[4 * q4 + i] = v[i];
+  }
   sr.rstd = ok ? rstd[(size_t)row * rstd_stride] : 0.f;
 }
 
@@ -260,7 +277,7 @@ __device__ __forceinline__ void ln_silu_bwd_rows(const float* Y, int ldy, OutT* 
   float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
-    const int c = sub + 8 * q;
+    const int c = ln_col(sub, q);
     const float a = sr.n[q] * g[c] + b[c];
     const float sg = sigmoidf_(a);
     const float da = y[c] * sg * (1.0f + a * (1.0f - sg));
@@ -273,7 +290,7 @@ __device__ __forceinline__ void ln_silu_bwd_rows(const float* Y, int ldy, OutT* 
   const float m1 = s1 * (1.0f / kH), m2 = s2 * (1.0f / kH);
   OutT* z = Z + row * ldz;
 #pragma unroll
-  for (int q = 0; q < 16; ++q) z[sub + 8 * q] = (OutT)(sr.rstd * (dn[q] - m1 - sr.n[q] * m2));
+  for (int q = 0; q < 16; ++q) z[ln_col(sub, q)] = (OutT)(sr.rstd * (dn[q] - m1 - sr.n[q] * m2));
 }
 
 // ---------------------------------------------------------------------------
@@ -401,21 +418,33 @@ __global__ __launch_bounds__(kH) void k_rbf_table(const float* __restrict__ w1, 
   o[3 * kH] = (float)(hh * hh * hh * s3);
 }
 
-// GEMM-3 epilogue: out[e0 + row][m * 256 + c] = acc + b3[c] for the valid rows
-__device__ __forceinline__ void store_out(const floatx4 (&acc)[2][4], const float (&b3)[4], float* __restrict__ out,
-                                          int ld_out, int64_t e0, int nvalid, int m) {
+// GEMM-3 epilogue: out[e0 + row][m * 256 + c] = acc + b3[c] for the valid rows.
+// The tile goes through LDS (O, row stride kLdO; the caller has synchronised so
+// the buffer is free) and leaves as whole rows, one 16-byte store per lane and
+// 1 KB per wave instruction (the accumulator layout would write 64-byte pieces).
+constexpr int kLdO = 260;
+__device__ __forceinline__ void store_out(const floatx4 (&acc)[2][4], const float (&b3)[4], float* O,
+                                          float* __restrict__ out, int ld_out, int64_t e0, int nvalid, int m) {
   const int c0 = acc_col0<256>();
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = acc_row(rt, r);
-      if (row < nvalid) {
-        float* o = out + (e0 + row) * (int64_t)ld_out + m * 256 + c0;
+      float* o = O + acc_row(rt, r) * kLdO + c0;
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) o[ct * 16] = acc[rt][ct][r] + b3[ct];
-      }
+      for (int ct = 0; ct < 4; ++ct) o[ct * 16] = acc[rt][ct][r] + b3[ct];
     }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int rr = 0; rr < kT / 4; ++rr) {
+    const int row = wave + 4 * rr;
+    if (row < nvalid) {
+      const float* src = O + row * kLdO + 4 * lane;
+      *reinterpret_cast<floatx4*>(out + (e0 + row) * (int64_t)ld_out + m * 256 + 4 * lane) =
+          floatx4{src[0], src[1], src[2], src[3]};
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -453,10 +482,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   __syncthreads();
   floatx4 acc[2][4];
   gemm32<kH, 256>(Y, kLdY, W.w3t, 256, acc);
-  store_out(acc, b3, out, ld_out, e0, nvalid, m);
+  __syncthreads();
+  store_out(acc, b3, sm, out, ld_out, e0, nvalid, m);
 }
 
-__global__ __launch_bounds__(256) void k_mlp_bwd(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_mlp_bwd(
+    e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
                                                  float* __restrict__ dd, int accumulate) {
   extern __shared__ float sm[];
   float* X = sm;                    // [32][258]: dOut tile; after GEMM a, the [32][130] LayerNorm rows
@@ -555,7 +586,8 @@ __global__ __launch_bounds__(256) void k_mlp_fwd_bf16(e2v2_mlp_args A, float* __
   __syncthreads();
   floatx4 acc[2][4];
   gemm_panel(Zb, kLdYb, P3, acc);
-  store_out(acc, b3, out, ld_out, e0, nvalid, m);
+  __syncthreads();
+  store_out(acc, b3, sm, out, ld_out, e0, nvalid, m);
 }
 
 __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
@@ -622,9 +654,11 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const flo
 
 using namespace e2v2;
 
-static size_t mlp_lds_fwd() { return sizeof(float) * kT * kLdY; }
+static size_t mlp_lds_fwd() { return sizeof(float) * kT * kLdO; }
 static size_t mlp_lds_bwd() { return sizeof(float) * kT * kLdX; }
-static size_t mlp_lds_fwd_bf16() { return sizeof(float) * kT * kLdY + 2 * sizeof(__bf16) * kT * kLdYb; }
+static size_t mlp_lds_fwd_bf16() {
+  return std::max(sizeof(float) * kT * kLdY + 2 * sizeof(__bf16) * kT * kLdYb, sizeof(float) * kT * kLdO);
+}
 static size_t mlp_lds_bwd_bf16() { return sizeof(__bf16) * (kT * kLdXb + kT * kLdYb) + sizeof(float) * kT * kLdY; }
 
 static int check_tables(const e2v2_mlp_args& A, const char* who) {
