@@ -76,7 +76,7 @@ BYTES_OF = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e
             "e2v2_deg_bwd": deg_bwd_bytes}
 
 KERNELS_OF = {"e2v2_mlp_fwd": ["k_mlp_fwd"], "e2v2_mlp_bwd": ["k_mlp_bwd"], "e2v2_attn_fwd": ["k_attn_fwd"],
-              "e2v2_attn_bwd": ["k_attn_bwd_row", "k_attn_bwd_col_ch"], "e2v2_deg_fwd": ["k_deg_fwd"],
+              "e2v2_attn_bwd": ["k_attn_bwd_row_hp", "k_attn_bwd_col_grp"], "e2v2_deg_fwd": ["k_deg_fwd"],
               "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"]}
 
 
