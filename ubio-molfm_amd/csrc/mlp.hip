@@ -183,11 +183,11 @@ struct LnParams {
 };
 
 __device__ __forceinline__ void load_ln_params(const e2v2_mlp_weights& W, LnParams& p) {
-  const int t = threadIdx.x;
+  const int t = threadIdx.x;      // threads 256 and up (larger blocks) load nothing
   if (t < kH) {
     p.g1[t] = W.g1[t];
     p.b1[t] = W.be1[t];
-  } else {
+  } else if (t < 2 * kH) {
     p.g2[t - kH] = W.g2[t - kH];
     p.b2[t - kH] = W.be2[t - kH];
   }
