@@ -174,13 +174,13 @@ def test_rbf_block_table(pkg, cuda):
     assert ev < 1e-6 and ed < 1e-6
 
 
-def _attention_case(pkg, cuda, act_dtype, clusters=True):
+def _attention_case(pkg, cuda, act_dtype, clusters=True, graph=None):
     """Attention fwd + bwd through the C ABI against the float64 reference.  With
     bf16 storage the inputs (q, k, v, grad) are rounded to bf16 for both sides,
     so the remaining differences are the bf16 output rows (also used by the
     backward's D_h) and fp32 arithmetic."""
     from ubio_molfm_amd import _lib, ops, so3
-    s, pos, nl = _graph(pkg, cuda, seed=4)
+    s, pos, nl = graph if graph is not None else _graph(pkg, cuda, seed=4)
     N, E = nl.n_atoms, nl.n_edges
     bf = act_dtype == torch.bfloat16
     print(f"[attn {act_dtype}] N={N} E={E}", flush=True)
@@ -224,6 +224,27 @@ def _attention_case(pkg, cuda, act_dtype, clusters=True):
 @pytest.mark.parametrize("clusters", [True, False], ids=["clusters", "per_column"])
 def test_attention_forward_backward(pkg, cuda, clusters):
     e_f, errs = _attention_case(pkg, cuda, torch.float32, clusters)
+    assert e_f < 2e-5
+    for name, e in errs.items():
+        assert e < 1e-4, (name, e)
+
+
+def test_attention_ragged_clusters_isolated_atoms(pkg, cuda):
+    """Column clusters that end part-way (N = 23, not a multiple of 4) and atoms
+    with no edges at all (two atoms 100 A away, non-periodic): every row and
+    column still matches the float64 reference, isolated rows give zero output."""
+    from ubio_molfm_amd import neighbors
+    rng = np.random.default_rng(21)
+    p = rng.normal(size=(23, 3)) * 1.8
+    p[21] = [100.0, 0.0, 0.0]
+    p[22] = [0.0, -100.0, 0.0]
+    s = dict(pos=p.astype(np.float32), Z=np.full(23, 6), graph_ptr=np.array([0, 23]),
+             cell=np.zeros((1, 3, 3), np.float32), pbc=np.zeros((1, 3), bool))
+    pos = torch.as_tensor(s["pos"], device=cuda)
+    nl = neighbors.build_neighbors(pos, s["graph_ptr"], s["cell"], s["pbc"], 6.0)
+    deg = np.diff(nl.row_ptr.cpu().numpy())
+    assert deg[21] == 0 and deg[22] == 0 and nl.n_atoms % 4 != 0
+    e_f, errs = _attention_case(pkg, cuda, torch.float32, True, (s, pos, nl))
     assert e_f < 2e-5
     for name, e in errs.items():
         assert e < 1e-4, (name, e)
