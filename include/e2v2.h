@@ -104,7 +104,8 @@ int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* cnt, int32
    No reference counterpart: the layout the clustered edge kernels read. */
 int e2v2_cluster_slots(const int32_t* seg_ptr, int32_t n_seg, const int32_t* member, const int32_t* item_eid,
                        int32_t span, int32_t* slot_member, int32_t* slot_edge, int32_t* n_slots, hipStream_t s);
-/* key CSR: phase 0 -> edge_row, key_ptr, stats = {E, max column}; phase 1 -> key_eid (sorted by edge id) */
+/* key CSR: phase 0 -> edge_row, key_ptr, stats = {E, max column}; phase 1 -> key_eid (sorted by edge id;
+   columns of any length, no host check needed between the phases) */
 int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, int n_cols, int64_t n_edges,
                        int32_t* edge_row, int32_t* key_cnt, int32_t* key_ptr, int32_t* stats,
                        uint64_t* tmp_key, int32_t* key_eid, int phase, hipStream_t s);

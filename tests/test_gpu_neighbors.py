@@ -174,3 +174,41 @@ def test_cluster_slots_rows_and_overflow(pkg, cuda):
         print(f"[slots {label}] N={nl.n_atoms} E={nl.n_edges} overflowing clusters={over}", flush=True)
         if label == "dense":
             assert over > 0
+
+
+def test_key_csr_long_column(pkg, cuda):
+    """A column with more edges than the LDS sort holds (5000 rows point at atom
+    0) is sorted in place in global memory: the key CSR equals a stable numpy
+    sort of the edges by column."""
+    from ubio_molfm_amd import _lib
+    N = 6000
+    rng = np.random.default_rng(4)
+    rows, cols = [], []
+    for i in range(N):
+        if i < 5000:
+            rows.append(i); cols.append(0)
+        for j in rng.choice(N, size=3, replace=False):
+            rows.append(i); cols.append(int(j))
+    rows = np.asarray(rows, np.int32); cols = np.asarray(cols, np.int32)
+    o = np.lexsort((cols, rows)); rows, cols = rows[o], cols[o]
+    E = len(rows)
+    row_ptr = np.zeros(N + 1, np.int32); np.add.at(row_ptr, rows + 1, 1); row_ptr = np.cumsum(row_ptr).astype(np.int32)
+    i32 = dict(dtype=torch.int32, device=cuda)
+    d_rp = torch.as_tensor(row_ptr, device=cuda); d_col = torch.as_tensor(cols, device=cuda)
+    edge_row = torch.empty(E, **i32); kc = torch.empty(N, **i32); kp = torch.empty(N + 1, **i32)
+    stats = torch.zeros(2, **i32); tkey = torch.empty(E, dtype=torch.int64, device=cuda); ke = torch.empty(E, **i32)
+    st = _lib.vp(torch.cuda.current_stream().cuda_stream)
+    for phase in (0, 1):
+        _lib.call("e2v2_csr_transpose", _lib.vp(d_rp.data_ptr()), _lib.vp(d_col.data_ptr()), _lib.i32(N),
+                  _lib.i32(N), _lib.i64(E), _lib.vp(edge_row.data_ptr()), _lib.vp(kc.data_ptr()),
+                  _lib.vp(kp.data_ptr()), _lib.vp(stats.data_ptr()),
+                  _lib.vp(tkey.data_ptr()) if phase else None, _lib.vp(ke.data_ptr()) if phase else None,
+                  _lib.i32(phase), st)
+    torch.cuda.synchronize()
+    order = np.argsort(cols, kind="stable").astype(np.int32)
+    ref_ptr = np.zeros(N + 1, np.int64); np.add.at(ref_ptr, cols + 1, 1); ref_ptr = np.cumsum(ref_ptr)
+    print(f"[key csr] E={E} longest column={int(np.diff(ref_ptr).max())}", flush=True)
+    assert int(np.diff(ref_ptr).max()) > 4096
+    assert np.array_equal(kp.cpu().numpy(), ref_ptr.astype(np.int32))
+    assert np.array_equal(ke.cpu().numpy(), order)
+    assert np.array_equal(edge_row.cpu().numpy(), rows)

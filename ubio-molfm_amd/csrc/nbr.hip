@@ -273,14 +273,46 @@ __global__ void k_col_fill(const int32_t* __restrict__ col, int64_t n_edges, con
   tkey[slot] = (uint64_t)e;
 }
 
+// In-place ascending sort of n distinct keys in global memory by one workgroup,
+// for segments longer than the LDS sort holds.  Bitonic network in the form
+// whose comparators all put the minimum at the lower index (first step of each
+// merge pairs t with t ^ (k - 1), later steps t with t ^ j), so positions past
+// n act as +infinity and their comparators are skipped.
+__device__ void sort_global(uint64_t* __restrict__ k, int n) {
+  int p2 = 1;
+  while (p2 < n) p2 <<= 1;
+  for (int kk = 2; kk <= p2; kk <<= 1) {
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+      for (int t = threadIdx.x; t < p2; t += blockDim.x) {
+        const int x = (j == (kk >> 1)) ? (t ^ (kk - 1)) : (t ^ j);
+        if (x > t && x < n) {
+          const uint64_t a = k[t], c = k[x];
+          if (a > c) {
+            k[t] = c;
+            k[x] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Columns of any length: up to kMaxSeg in LDS, longer ones in place in global
+// memory (tkey is scratch), so the host needs no column-length check.
 __global__ __launch_bounds__(256) void k_sort_cols(const int32_t* __restrict__ key_ptr,
-                                                   const uint64_t* __restrict__ tkey,
+                                                   uint64_t* __restrict__ tkey,
                                                    int32_t* __restrict__ key_eid) {
   __shared__ uint64_t sk[kMaxSeg];
   __shared__ int32_t sv[kMaxSeg];
   const int r = blockIdx.x;
   const int b = key_ptr[r], n = key_ptr[r + 1] - b;
   if (n == 0) return;
+  if (n > kMaxSeg) {
+    sort_global(tkey + b, n);
+    for (int t = threadIdx.x; t < n; t += blockDim.x) key_eid[b + t] = (int32_t)tkey[b + t];
+    return;
+  }
   segment_sort(tkey, b, n, sk, sv);
   for (int t = threadIdx.x; t < n; t += blockDim.x) key_eid[b + t] = (int32_t)sk[t];
 }
@@ -550,8 +582,8 @@ E2V2_API int e2v2_cluster_slots(const int32_t* seg_ptr, int32_t n_seg, const int
 E2V2_API int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, int n_cols, int64_t n_edges,
                                 int32_t* edge_row, int32_t* key_cnt, int32_t* key_ptr, int32_t* stats,
                                 uint64_t* tmp_key, int32_t* key_eid, int phase, hipStream_t s) {
-  // phase 0: edge_row, column counts and key_ptr (host then reads stats[1] = max column)
-  // phase 1: fill and sort each column by edge id
+  // phase 0: edge_row, column counts and key_ptr (stats = {E, max column}, informational)
+  // phase 1: fill and sort each column by edge id (any column length)
   if (phase == 0) {
     if (n_rows > 0 && n_edges > 0) {
       hipLaunchKernelGGL(k_edge_rows, dim3(blocks_for(n_rows, 256)), dim3(256), 0, s, row_ptr, n_rows, edge_row);

@@ -210,9 +210,6 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     _lib.call("e2v2_csr_transpose", _lib.vp(row_ptr.data_ptr()), _lib.vp(_ptr(col)), _lib.i32(N), _lib.i32(N),
               _lib.i64(E), _lib.vp(_ptr(edge_row)), _lib.vp(key_cnt.data_ptr()), _lib.vp(key_ptr.data_ptr()),
               _lib.vp(stats.data_ptr()), None, None, _lib.i32(0), _lib.vp(stream))
-    max_col = int(stats.cpu()[1])
-    if max_col > 4096:
-        raise RuntimeError(f"an atom is the source of {max_col} edges; the column sort supports at most 4096")
     key_eid = torch.empty(E, **i32)
     _lib.call("e2v2_csr_transpose", _lib.vp(row_ptr.data_ptr()), _lib.vp(_ptr(col)), _lib.i32(N), _lib.i32(N),
               _lib.i64(E), _lib.vp(_ptr(edge_row)), _lib.vp(key_cnt.data_ptr()), _lib.vp(key_ptr.data_ptr()),
