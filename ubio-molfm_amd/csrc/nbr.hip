@@ -116,15 +116,24 @@ __device__ bool image_has_inner(const e2v2_nbr_plan& P, int g, const float* img)
   return false;
 }
 
-// Visit every edge i <- (j, s) of atom i in a fixed traversal order.
+// Visit every edge i <- (j, s) of atom i with one wavefront.  For each shift the
+// bins within rc + margin of pos_i - off span at most 3 bins per direction
+// (bin edge h >= rc + margin), so they form at most 3 x 3 columns of
+// z-consecutive bins, i.e. at most 9 contiguous runs of bin_atoms.  The runs are
+// concatenated and dealt out 64 candidates per round.  (A fourth bin that fp32
+// rounding of the bin range could add starts beyond q + rc + margin, so it holds
+// no edge.)  emit(ok, j, s, dx, dy, dz, d) is called by every lane of the wave in
+// each round (ok false on lanes without an edge) and may use wave-wide ballots.
 template <class Emit>
-__device__ void visit_edges(const e2v2_nbr_plan& P, int i, Emit&& emit) {
+__device__ void visit_edges_wave(const e2v2_nbr_plan& P, int i, Emit&& emit) {
+  const int lane = threadIdx.x & 63;
   const int g = P.atom_graph[i];
   const bool periodic = P.graph_periodic[g] != 0;
   const float pi[3] = {P.pos[3 * i], P.pos[3 * i + 1], P.pos[3 * i + 2]};
   const float lo0 = P.grid_lo[3 * g], lo1 = P.grid_lo[3 * g + 1], lo2 = P.grid_lo[3 * g + 2];
   const float h0 = P.grid_h[3 * g], h1 = P.grid_h[3 * g + 1], h2 = P.grid_h[3 * g + 2];
   const int d0 = P.grid_dim[3 * g], d1 = P.grid_dim[3 * g + 1], d2 = P.grid_dim[3 * g + 2];
+  const int bbase = P.bin_base[g];
   const float r = P.rc + kBinMargin;
   for (int s = P.graph_shift_ptr[g]; s < P.graph_shift_ptr[g + 1]; ++s) {
     const float* off = P.shift_off + 3 * s;
@@ -136,64 +145,97 @@ __device__ void visit_edges(const e2v2_nbr_plan& P, int i, Emit&& emit) {
     int z0 = (int)floorf((q2 - r - lo2) / h2), z1 = (int)floorf((q2 + r - lo2) / h2);
     if (z1 < 0 || z0 > d2 - 1) continue;
     x0 = max(x0, 0); y0 = max(y0, 0); z0 = max(z0, 0);
-    x1 = min(x1, d0 - 1); y1 = min(y1, d1 - 1); z1 = min(z1, d2 - 1);
-    for (int bx = x0; bx <= x1; ++bx)
-      for (int by = y0; by <= y1; ++by)
-        for (int bz = z0; bz <= z1; ++bz) {
-          int bin = P.bin_base[g] + (bx * d1 + by) * d2 + bz;
-          for (int t = P.bin_start[bin]; t < P.bin_start[bin + 1]; ++t) {
-            int j = P.bin_atoms[t];
-            float dx, dy, dz;
-            exact_edge(pi, P.pos + 3 * j, off, dx, dy, dz);
-            float d = exact_dist(dx, dy, dz);
-            if (!(d >= P.rmin && d <= P.rc)) continue;
-            if (periodic && !(d < P.rc)) {
-              float img[3];
-              {
-#pragma clang fp contract(off)
-                img[0] = P.pos[3 * j] + off[0];
-                img[1] = P.pos[3 * j + 1] + off[1];
-                img[2] = P.pos[3 * j + 2] + off[2];
-              }
-              if (!image_has_inner(P, g, img)) continue;
-            }
-            emit(j, s, dx, dy, dz, d);
-          }
+    x1 = min(min(x1, d0 - 1), x0 + 2); y1 = min(min(y1, d1 - 1), y0 + 2); z1 = min(min(z1, d2 - 1), z0 + 2);
+    // run r = (a, b) holds bins (x0 + a, y0 + b, z0..z1); pre = inclusive prefix of
+    // run lengths, base = run start - exclusive prefix
+    int pre[9], base[9];
+    int total = 0;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int b = 0; b < 3; ++b) {
+        int st = 0, len = 0;
+        if (x0 + a <= x1 && y0 + b <= y1) {
+          const int bin = bbase + ((x0 + a) * d1 + (y0 + b)) * d2;
+          st = P.bin_start[bin + z0];
+          len = P.bin_start[bin + z1 + 1] - st;
         }
+        base[3 * a + b] = st - total;
+        total += len;
+        pre[3 * a + b] = total;
+      }
+    for (int c0 = 0; c0 < total; c0 += 64) {
+      const int c = c0 + lane;
+      bool ok = false;
+      int j = 0;
+      float dx = 0.f, dy = 0.f, dz = 0.f, d = 0.f;
+      if (c < total) {
+        int t = 0;
+#pragma unroll
+        for (int q = 8; q >= 0; --q)
+          if (c < pre[q]) t = base[q] + c;
+        j = P.bin_atoms[t];
+        exact_edge(pi, P.pos + 3 * j, off, dx, dy, dz);
+        d = exact_dist(dx, dy, dz);
+        ok = d >= P.rmin && d <= P.rc;
+        if (ok && periodic && !(d < P.rc)) {
+          float img[3];
+          {
+#pragma clang fp contract(off)
+            img[0] = P.pos[3 * j] + off[0];
+            img[1] = P.pos[3 * j + 1] + off[1];
+            img[2] = P.pos[3 * j + 2] + off[2];
+          }
+          ok = image_has_inner(P, g, img);
+        }
+      }
+      emit(ok, j, s, dx, dy, dz, d);
+    }
   }
 }
 
-__global__ void k_nbr_count(e2v2_nbr_plan P, int32_t* __restrict__ row_count) {
-  int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= P.n_atoms) return;
-  int c = 0;
-  visit_edges(P, i, [&](int, int, float, float, float, float) { ++c; });
-  row_count[i] = c;
+// lanes below this one whose bit is set in m
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-__global__ void k_nbr_fill(e2v2_nbr_plan P, const int32_t* __restrict__ row_ptr, int32_t* __restrict__ col,
-                           int32_t* __restrict__ shift, float* __restrict__ dvec, float* __restrict__ dist,
-                           uint64_t* __restrict__ key) {
-  int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= P.n_atoms) return;
-  int o = row_ptr[i];
-  const int o_end = row_ptr[i + 1];
-  const int g = P.atom_graph[i];
-  const int a0 = P.graph_atom_ptr[g];
-  const int s0 = P.graph_shift_ptr[g];
-  const int ns = P.graph_shift_ptr[g + 1] - s0;
-  visit_edges(P, i, [&](int j, int s, float dx, float dy, float dz, float d) {
-    if (o >= o_end) return;  // count and fill share one traversal; never write past the row
-    col[o] = j;
-    shift[o] = s;
-    dvec[3 * o] = dx;
-    dvec[3 * o + 1] = dy;
-    dvec[3 * o + 2] = dz;
-    dist[o] = d;
-    uint32_t lo = (uint32_t)(j - a0) * (uint32_t)ns + (uint32_t)(s - s0);
-    key[o] = ((uint64_t)__float_as_uint(d) << 32) | (uint64_t)lo;
-    ++o;
-  });
+constexpr int kNbrWaves = 4;  // atoms (wavefronts) per workgroup of the count and fill kernels
+
+__global__ __launch_bounds__(64 * kNbrWaves) void k_nbr_count(e2v2_nbr_plan P, int32_t* __restrict__ row_count) {
+  for (int i = blockIdx.x * kNbrWaves + (int)(threadIdx.x >> 6); i < P.n_atoms; i += gridDim.x * kNbrWaves) {
+    int c = 0;
+    visit_edges_wave(P, i, [&](bool ok, int, int, float, float, float, float) { c += __popcll(__ballot(ok)); });
+    if ((threadIdx.x & 63) == 0) row_count[i] = c;
+  }
+}
+
+__global__ __launch_bounds__(64 * kNbrWaves) void k_nbr_fill(e2v2_nbr_plan P, const int32_t* __restrict__ row_ptr,
+                                                            int32_t* __restrict__ col, int32_t* __restrict__ shift,
+                                                            float* __restrict__ dvec, float* __restrict__ dist,
+                                                            uint64_t* __restrict__ key) {
+  for (int i = blockIdx.x * kNbrWaves + (int)(threadIdx.x >> 6); i < P.n_atoms; i += gridDim.x * kNbrWaves) {
+    int o = row_ptr[i];
+    const int o_end = row_ptr[i + 1];
+    const int g = P.atom_graph[i];
+    const int a0 = P.graph_atom_ptr[g];
+    const int s0 = P.graph_shift_ptr[g];
+    const int ns = P.graph_shift_ptr[g + 1] - s0;
+    visit_edges_wave(P, i, [&](bool ok, int j, int s, float dx, float dy, float dz, float d) {
+      const uint64_t m = __ballot(ok);
+      const int p = o + lanes_below(m);
+      if (ok && p < o_end) {  // count and fill share one traversal; never write past the row
+        col[p] = j;
+        shift[p] = s;
+        dvec[3 * p] = dx;
+        dvec[3 * p + 1] = dy;
+        dvec[3 * p + 2] = dz;
+        dist[p] = d;
+        uint32_t lo = (uint32_t)(j - a0) * (uint32_t)ns + (uint32_t)(s - s0);
+        key[p] = ((uint64_t)__float_as_uint(d) << 32) | (uint64_t)lo;
+      }
+      o += __popcll(m);
+    });
+  }
 }
 
 // Bitonic sort of one segment per workgroup (length <= kMaxSeg), returning
@@ -524,7 +566,8 @@ E2V2_API int e2v2_nbr_bin(const e2v2_nbr_plan* plan, hipStream_t s) {
 E2V2_API int e2v2_nbr_count(const e2v2_nbr_plan* plan, int32_t* row_count, int32_t* row_ptr, hipStream_t s) {
   const e2v2_nbr_plan& P = *plan;
   if (P.n_atoms > 0) {
-    hipLaunchKernelGGL(k_nbr_count, dim3(blocks_for(P.n_atoms, 64)), dim3(64), 0, s, P, row_count);
+    hipLaunchKernelGGL(k_nbr_count, dim3(blocks_for(P.n_atoms, kNbrWaves)), dim3(64 * kNbrWaves), 0, s, P,
+                       row_count);
     E2V2_LAUNCHED("k_nbr_count");
   }
   hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, row_count, P.n_atoms, row_ptr, P.stats);
@@ -539,8 +582,8 @@ E2V2_API int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, in
   E2V2_REQUIRE(max_row <= kMaxSeg, "nbr_fill: a row has %d neighbours; the per-row sort supports at most %d",
                max_row, kMaxSeg);
   if (P.n_atoms == 0 || n_edges == 0) return 0;
-  hipLaunchKernelGGL(k_nbr_fill, dim3(blocks_for(P.n_atoms, 64)), dim3(64), 0, s, P, row_ptr, tmp_col, tmp_shift,
-                     tmp_dvec, tmp_dist, tmp_key);
+  hipLaunchKernelGGL(k_nbr_fill, dim3(blocks_for(P.n_atoms, kNbrWaves)), dim3(64 * kNbrWaves), 0, s, P, row_ptr,
+                     tmp_col, tmp_shift, tmp_dvec, tmp_dist, tmp_key);
   E2V2_LAUNCHED("k_nbr_fill");
   hipLaunchKernelGGL(k_sort_rows, dim3(P.n_atoms), dim3(256), 0, s, row_ptr, tmp_key, tmp_col, tmp_shift, tmp_dvec,
                      tmp_dist, col, shift, dvec, dist);
