@@ -597,6 +597,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   }
 }
 
+// Sums of four values over the 64 lanes of a wave; every lane of row k (lanes
+// 16k .. 16k + 15) returns the sum of value k.  A swap across the wave halves
+// (lanes < 32 keep values 0 and 1, lanes >= 32 values 2 and 3), a swap across
+// the two rows of each half (even rows keep the first, odd rows the second),
+// then four DPP steps within each row of 16.
+__device__ __forceinline__ float wave_sum4(float v0, float v1, float v2, float v3, int lane) {
+  const bool hi = (lane & 32) != 0, odd = (lane & 16) != 0;
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v2), false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v1), __float_as_uint(v3), false, false);
+  // lane < 32: a[1] = v0 of lane + 32; lane >= 32: a[0] = v2 of lane - 32 (b likewise for v1, v3)
+  const float x = hi ? v2 + __uint_as_float(a[0]) : v0 + __uint_as_float(a[1]);
+  const float y = hi ? v3 + __uint_as_float(b[0]) : v1 + __uint_as_float(b[1]);
+  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  // even row: c[1] = x of the odd row beside it; odd row: c[0] = y of the even row
+  const float z = odd ? y + __uint_as_float(c[0]) : x + __uint_as_float(c[1]);
+  return dpp_row_sum16(z);
+}
+
 template <typename TS>
 struct HeadEdge {
   float k[kD];
@@ -612,9 +630,11 @@ struct HeadEdge {
 // weight, forms u = dA^T v_j for both channels (dA = T^T G_i) and with it the
 // head's dL/dw, runs the softmax / gate / distance backward for its head and
 // accumulates dq from the k_j row it already holds, so nothing crosses threads
-// but the per-edge sums over heads (dL/d dvec, dL/dd): row sums by DPP, the
-// four rows of a wave by lane reads, the two waves of a parity in LDS, added
-// in a fixed order once per chunk of up to 128 edges.
+// but the per-edge sums over heads (dL/d dvec, dL/dd): the 64 heads of a wave
+// by lane swaps and DPP (wave_sum4), the two waves of a parity in LDS, added
+// in a fixed order once per chunk of up to 128 edges.  The head-independent
+// edge terms (column, distance, envelope, 1/d, dvec) are formed once per edge
+// at the start of a chunk and read from LDS.
 template <typename TS>
 __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const TS* __restrict__ G,
                                                          const TS* __restrict__ O, const float* __restrict__ mrow,
@@ -626,6 +646,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
   constexpr int CH = 64;                      // edges per parity and reduction chunk
   __shared__ float part[2 * CH][2][4];
   __shared__ float dq_s[kH][kD];
+  __shared__ float4 er_a[2 * CH];             // per edge of the chunk: p, dp/dd, 1/max(d, 1e-6), d
+  __shared__ float4 er_b[2 * CH];             // dvec, column (int bits)
   const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
   if (i >= A.n_rows) return;
   const int h = t & (kH - 1), par = t >> 7, lane = t & (kWave - 1), wsub = (t >> 6) & 1;
@@ -668,26 +690,29 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
 #pragma unroll
   for (int d = 0; d < kD; ++d) dqa[d] = 0.f;
   using L = HeadEdge<TS>;
+  int c0 = 0;  // first edge of the current chunk
   auto issue = [&](int el, L& X) {
     const int64_t e = (int64_t)b + el;
-    const int j = A.col[e];
-    load8(Kp + ((size_t)j * kH + h) * kD, X.k);
-    const TS* vp = Vp + (size_t)j * kC + h;
+    const int j = __float_as_int(er_b[el - c0].w);
+    // 32-bit per-lane byte offsets from wave-uniform bases (n_rows * kH * kD *
+    // sizeof(TS) < 2^32 is checked by the host)
+    const uint32_t kof = ((uint32_t)j * kH + h) * (kD * sizeof(TS));
+    load8(reinterpret_cast<const TS*>(reinterpret_cast<const char*>(Kp) + kof), X.k);
+    const uint32_t vof = ((uint32_t)j * kC + h) * sizeof(TS);
 #pragma unroll
     for (int r = 0; r < kNV; ++r) {
-      X.v0[r] = f32(vp[r * os]);
-      X.v1[r] = f32(vp[r * os + kH]);
+      const char* vb = reinterpret_cast<const char*>(Vp + r * os);
+      X.v0[r] = f32(*reinterpret_cast<const TS*>(vb + vof));
+      X.v1[r] = f32(*reinterpret_cast<const TS*>(vb + vof + kH * sizeof(TS)));
     }
     X.gate = A.gi[e * (2 * kH) + h];
     X.ih = A.gi[e * (2 * kH) + kH + h];
   };
   auto apply = [&](int el, int slot, const L& X) {
     const int64_t e = (int64_t)b + el;
-    const float d = A.dist[e];
-    float pe, dpe;
-    env.eval(d, pe, dpe);
-    const float rR = 1.0f / fmaxf(d, 1e-6f);
-    const float dvx = A.dvec[3 * e], dvy = A.dvec[3 * e + 1], dvz = A.dvec[3 * e + 2];
+    const float4 ea = er_a[slot], eb = er_b[slot];
+    const float pe = ea.x, dpe = ea.y, rR = ea.z, d = ea.w;
+    const float dvx = eb.x, dvy = eb.y, dvz = eb.z;
     const float qk = half_dot(qs, X.k) + half_dot(qs + 4, X.k + 4);
     const float a = X.gate * qk;
     const float ex = expf(a - m);
@@ -720,23 +745,21 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
     ntstore(dqk, dqk_out + e * kH + h);
 #pragma unroll
     for (int q = 0; q < kD; ++q) dqa[q] = fmaf(dqk, X.k[q], dqa[q]);
-    // sums over the 64 heads of this wave: rows of 16 by DPP, then the four rows
-    float r4[4] = {w * U[0], w * U[1], w * U[2], fmaf(dpv, dpe, dR)};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float x = dpp_row_sum16(r4[k]);
-      r4[k] = ((__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0)) +
-                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16))) +
-               __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32))) +
-              __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48));
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) part[slot][wsub][k] = r4[k];
-    }
+    // sums over the 64 heads of this wave; lane 16k holds the sum of value k
+    const float sum = wave_sum4(w * U[0], w * U[1], w * U[2], fmaf(dpv, dpe, dR), lane);
+    if ((lane & 15) == 0) part[slot][wsub][lane >> 4] = sum;
   };
-  for (int c0 = 0; c0 < n; c0 += 2 * CH) {
+  for (c0 = 0; c0 < n; c0 += 2 * CH) {
     const int nc = min(2 * CH, n - c0);
+    if (t < nc) {
+      const int64_t e = (int64_t)b + c0 + t;
+      const float d = A.dist[e];
+      float pe, dpe;
+      env.eval(d, pe, dpe);
+      er_a[t] = make_float4(pe, dpe, 1.0f / fmaxf(d, 1e-6f), d);
+      er_b[t] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], __int_as_float(A.col[e]));
+    }
+    __syncthreads();
     {
       L Xa, Xb;
       int el = par;
@@ -829,6 +852,9 @@ E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, con
   E2V2_REQUIRE(!A.col_slot_member || (A.col_span == 4 && A.col_slot_edge && A.col_n_slots),
                "attn_bwd: column clusters need span 4 and all three slot arrays (span %d)", A.col_span);
   if (A.n_rows == 0) return 0;
+  // the row pass gathers k_j and v_j through 32-bit byte offsets within one row block
+  E2V2_REQUIRE((uint64_t)A.n_rows * kH * kD * (A.act_bf16 ? 2 : 4) < (1ull << 32),
+               "attn_bwd: %d rows exceed the 32-bit gather offsets of the row pass", A.n_rows);
   if (A.act_bf16)
     return attn_bwd_launch(A, static_cast<const __bf16*>(grad_out), static_cast<const __bf16*>(out), mrow, srow,
                            cnt, dgi, ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
