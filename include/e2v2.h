@@ -221,7 +221,9 @@ int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* dfea, f
 /* rms_norm_sh: EquivariantRMSNormArraySphericalHarmonicsV2_BL
  * (src/molfm/models/e2former/module_utils.py:1663-1772); w [3][256], b [256] */
 int e2v2_rmsnorm_fwd(const float* x, const float* w, const float* b, float* y, int n, float eps, hipStream_t s);
-int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, float* gx, int n, float eps, hipStream_t s);
+/* gx = d(rms_norm_sh)/dx^T gy (+ gres when gres is not NULL: the gradient of a residual branch that reads x) */
+int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, const float* gres, float* gx, int n, float eps,
+                     hipStream_t s);
 /* Gate_s3 activation (module_utils.py:2694-2746) from gate logits sc [N][768];
  * k1, k2 = normalize2mom constants of SiLU and sigmoid */
 int e2v2_gate_fwd(const float* sc, const float* x, float* y, int n, float k1, float k2, hipStream_t s);

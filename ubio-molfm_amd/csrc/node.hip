@@ -57,8 +57,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(const float* __restrict__ x
 }
 
 __global__ __launch_bounds__(256) void k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w,
-                                                     const float* __restrict__ gy, float* __restrict__ gx, int n,
-                                                     float eps) {
+                                                     const float* __restrict__ gy, const float* __restrict__ gres,
+                                                     float* __restrict__ gx, int n, float eps) {
   __shared__ float red[4];
   const int i = blockIdx.x, c = threadIdx.x;
   const size_t st = (size_t)n * kNC;
@@ -89,8 +89,14 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(const float* __restrict__ x
   const float gmean0 = block_sum256(gf[0], red) * (1.0f / kNC);
   gf[0] -= gmean0;
   float* op = gx + (size_t)i * kNC + c;
+  if (gres) {  // gradient of a residual branch that reads x directly
+    const float* rp = gres + (size_t)i * kNC + c;
 #pragma unroll
-  for (int m = 0; m < 9; ++m) op[m * st] = gf[m];
+    for (int m = 0; m < 9; ++m) op[m * st] = gf[m] + rp[m * st];
+  } else {
+#pragma unroll
+    for (int m = 0; m < 9; ++m) op[m * st] = gf[m];
+  }
 }
 
 __global__ void k_gate_fwd(const float* __restrict__ sc, const float* __restrict__ x, float* __restrict__ y, int n,
@@ -147,10 +153,10 @@ E2V2_API int e2v2_rmsnorm_fwd(const float* x, const float* w, const float* b, fl
   return 0;
 }
 
-E2V2_API int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, float* gx, int n, float eps,
-                              hipStream_t s) {
+E2V2_API int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, const float* gres, float* gx,
+                              int n, float eps, hipStream_t s) {
   if (n == 0) return 0;
-  hipLaunchKernelGGL(k_rmsnorm_bwd, dim3(n), dim3(256), 0, s, x, w, gy, gx, n, eps);
+  hipLaunchKernelGGL(k_rmsnorm_bwd, dim3(n), dim3(256), 0, s, x, w, gy, gres, gx, n, eps);
   E2V2_LAUNCHED("k_rmsnorm_bwd");
   return 0;
 }

@@ -63,6 +63,15 @@ def _mm_into(a, b, out):
     return torch.mm(a, b, out=out)
 
 
+def _mm_bias_into(a, b, bias, out):
+    """out = a @ b + bias (bias broadcast over rows; fused into the GEMM for fp32
+    operands) with the operand rule of ``_mm_into``."""
+    if b.dtype == BF16:
+        _mm_into(a, b, out)
+        return out.add_(bias)
+    return torch.addmm(bias, a, b, out=out)
+
+
 def _addmm_into(c, a, b, out):
     """out = c + a @ b with the operand rule of ``_mm_into``."""
     if b.dtype == BF16:
@@ -107,11 +116,13 @@ class SO3LinearFn(torch.autograd.Function):
         xa = _bf(x) if W.dtype == BF16 else x
         for l in range(lmax + 1):
             a, b = l * l, (l + 1) ** 2
-            if res is None:
-                _mm_into(xa[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
-            else:
+            if res is not None:
                 _addmm_into(res[a:b].view(-1, O), xa[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
-        if bias is not None:
+            elif l == 0 and bias is not None:
+                _mm_bias_into(xa[0], W[0].t(), bias, out=y[0])
+            else:
+                _mm_into(xa[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
+        if bias is not None and res is not None:
             y[0].add_(bias)
         ctx.save_for_backward(W)
         ctx.lmax = lmax
@@ -137,24 +148,40 @@ class QKProjFn(torch.autograd.Function):
     m-contraction: x[9][N][C] -> hq, hk [N][3 hid] (before final_linear)."""
 
     @staticmethod
-    def forward(ctx, x, W, bias, lmax: int, hid: int):
+    def forward(ctx, x, W, bias, lmax: int, hid: int, Wv=None, bv=None):
+        """With the value projection's weight Wv [lmax+1, Cv, C] and bias bv it
+        also returns v = SO3_Linear(x) [9, N, Cv] (else None), so that the
+        backward sums the two input gradients inside the GEMMs."""
         x = x.contiguous()
         L2, N, C = x.shape
         y = x.new_empty(L2, N, 4 * hid)
         xa = _bf(x) if W.dtype == BF16 else x
         for l in range(lmax + 1):
             a, b = l * l, (l + 1) ** 2
-            _mm_into(xa[a:b].view(-1, C), W[l].t(), out=y[a:b].view(-1, 4 * hid))
-        y[0].add_(bias)
+            if l == 0:
+                _mm_bias_into(xa[0], W[0].t(), bias, out=y[0])
+            else:
+                _mm_into(xa[a:b].view(-1, C), W[l].t(), out=y[a:b].view(-1, 4 * hid))
         hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
         _lib.call("e2v2_pairdot_fwd", _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _stream())
-        ctx.save_for_backward(y, W)
+        v = None
+        if Wv is not None:
+            Cv = Wv.shape[1]
+            v = x.new_empty(L2, N, Cv)
+            xv = _bf(x) if Wv.dtype == BF16 else x
+            for l in range(lmax + 1):
+                a, b = l * l, (l + 1) ** 2
+                if l == 0:
+                    _mm_bias_into(xv[0], Wv[0].t(), bv, out=v[0])
+                else:
+                    _mm_into(xv[a:b].view(-1, C), Wv[l].t(), out=v[a:b].view(-1, Cv))
+        ctx.save_for_backward(y, W, Wv)
         ctx.lmax, ctx.hid = lmax, hid
-        return hq, hk
+        return hq, hk, v
 
     @staticmethod
-    def backward(ctx, ghq, ghk):
-        y, W = ctx.saved_tensors
+    def backward(ctx, ghq, ghk, gv):
+        y, W, Wv = ctx.saved_tensors
         L2, N, F = y.shape
         hid = ctx.hid
         ghq = torch.zeros(N, 3 * hid, device=y.device) if ghq is None else ghq.contiguous()
@@ -167,7 +194,13 @@ class QKProjFn(torch.autograd.Function):
         for l in range(ctx.lmax + 1):
             a, b = l * l, (l + 1) ** 2
             _mm_into(ga[a:b].view(-1, F), W[l], out=gx[a:b].view(-1, C))
-        return gx, None, None, None, None
+        if Wv is not None and gv is not None:
+            gv = gv.contiguous()
+            Cv = Wv.shape[1]
+            for l in range(ctx.lmax + 1):
+                a, b = l * l, (l + 1) ** 2
+                _addmm_into(gx[a:b].view(-1, C), gv[a:b].view(-1, Cv), Wv[l], out=gx[a:b].view(-1, C))
+        return gx, None, None, None, None, None, None
 
 
 class SO2OutFn(torch.autograd.Function):
@@ -247,8 +280,37 @@ class RMSNormFn(torch.autograd.Function):
         x, w = ctx.saved_tensors
         gy = gy.contiguous()
         gx = torch.empty_like(x)
-        _lib.call("e2v2_rmsnorm_bwd", _dp(x), _dp(w), _dp(gy), _dp(gx), _lib.i32(x.shape[1]), _lib.f32(ctx.eps),
+        _lib.call("e2v2_rmsnorm_bwd", _dp(x), _dp(w), _dp(gy), None, _dp(gx), _lib.i32(x.shape[1]),
+                  _lib.f32(ctx.eps), _stream())
+        return gx, None, None, None
+
+
+class RMSNormResidualFn(torch.autograd.Function):
+    """(rms_norm_sh(x), x): the normed input of a block and x itself for the
+    block's residual branch, so that the backward adds the two gradients of x
+    inside the norm's kernel instead of a separate accumulation pass."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, eps: float):
+        x = x.contiguous()
+        y = torch.empty_like(x)
+        _lib.call("e2v2_rmsnorm_fwd", _dp(x), _dp(w), _dp(b), _dp(y), _lib.i32(x.shape[1]), _lib.f32(eps),
                   _stream())
+        ctx.save_for_backward(x, w)
+        ctx.eps = eps
+        ctx.set_materialize_grads(False)
+        return y, x
+
+    @staticmethod
+    def backward(ctx, gy, gres):
+        x, w = ctx.saved_tensors
+        if gy is None:
+            return gres, None, None, None
+        gy = gy.contiguous()
+        gres = None if gres is None else gres.contiguous()
+        gx = torch.empty_like(x)
+        _lib.call("e2v2_rmsnorm_bwd", _dp(x), _dp(w), _dp(gy), None if gres is None else _dp(gres), _dp(gx),
+                  _lib.i32(x.shape[1]), _lib.f32(ctx.eps), _stream())
         return gx, None, None, None
 
 
@@ -400,7 +462,7 @@ class SO3_Linear2Scalar_e2former(nn.Module):
         w, b = self.stacked()
         hid = self.weight.shape[1]
         # the pair kernel contracts (q_a, q_b) and (k_a, k_b); feed this product twice
-        hq, _ = QKProjFn.apply(x, torch.cat([w, w], dim=1), torch.cat([b, b]), self.lmax, hid)
+        hq, _, _ = QKProjFn.apply(x, torch.cat([w, w], dim=1), torch.cat([b, b]), self.lmax, hid)
         return self.head(hq)
 
 
@@ -427,6 +489,11 @@ class EquivariantRMSNormArraySphericalHarmonicsV2_BL(nn.Module):
     def forward(self, x, batch=None):
         return RMSNormFn.apply(x, self.affine_weight.detach().float().contiguous(),
                                self.affine_bias.detach().float().contiguous(), float(self.eps))
+
+    def forward_with_residual(self, x):
+        """(norm(x), x) with the residual gradient added in the norm's backward."""
+        return RMSNormResidualFn.apply(x, self.affine_weight.detach().float().contiguous(),
+                                       self.affine_bias.detach().float().contiguous(), float(self.eps))
 
 
 class Gate_s3(nn.Module):
@@ -641,10 +708,10 @@ class E2AttentionArbOrder_sparse(nn.Module):
         bf16 = ctx.bf16
         W, b = self.qk_weights(bf16)
         hid = self.query_linear.weight.shape[1]
-        hq, hk = QKProjFn.apply(x, W, b, self.lmax, hid)
+        pv = self.proj_value  # its GEMMs run inside QKProjFn (one input gradient)
+        hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, gemm_weight(pv, "weight", bf16), pv.bias.detach())
         q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
         k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
-        v = self.proj_value(x, bf16)
         packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding, ctx.rbf_offset,
                                ctx.rbf_coeff, ctx.rc, bf16)
         so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
@@ -674,12 +741,12 @@ class TransBlock(nn.Module):
 
     def forward(self, x, ctx: EdgeContext, sys_node_embedding=None):
         """x [9, N, C] m-major."""
-        res = x
-        h = self.norm_1(x)
+        h, res = self.norm_1.forward_with_residual(x)
         if sys_node_embedding is not None:
             h = torch.cat([(h[0] + sys_node_embedding).unsqueeze(0), h[1:]], dim=0)
         x = self.ga(h, ctx, res=res)
-        return self.ffn(self.norm_ffn(x), res=x, bf16=ctx.bf16)
+        h, res = self.norm_ffn.forward_with_residual(x)
+        return self.ffn(h, res=res, bf16=ctx.bf16)
 
 
 class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
