@@ -75,7 +75,8 @@ def stack_flops(N, E):
 BYTES_OF = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
             "e2v2_deg_bwd": deg_bwd_bytes}
 
-KERNELS_OF = {"e2v2_mlp_fwd": ["k_mlp_fwd"], "e2v2_mlp_bwd": ["k_mlp_bwd"], "e2v2_attn_fwd": ["k_attn_fwd"],
+KERNELS_OF = {"e2v2_mlp_fwd": ["k_mlp_fwd"], "e2v2_mlp_bwd": ["k_mlp_bwd"],
+              "e2v2_mlp_bwd_deg": ["k_mlp_bwd_deg"], "e2v2_attn_fwd": ["k_attn_fwd"],
               "e2v2_attn_bwd": ["k_attn_bwd_row_hp", "k_attn_bwd_col_grp"], "e2v2_deg_fwd": ["k_deg_fwd"],
               "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"]}
 
@@ -168,8 +169,8 @@ def main():
     for _ in range(args.warmup):
         integ.step()
     torch.cuda.synchronize()
-    timer = _lib.KernelTimer(["e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd",
-                              "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill"])
+    timer = _lib.KernelTimer(["e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_mlp_bwd_deg", "e2v2_attn_fwd", "e2v2_attn_bwd",
+                              "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill"])
     edges = []
     e_start = integ.e.sum().item() + integ.kinetic()
     _lib.set_timer(timer)
@@ -190,11 +191,14 @@ def main():
     # dominant library call by total time
     dom = max(stats.items(), key=lambda kv: kv[1]["total_ms"])
     name, st = dom
-    n_mlp = {"e2v2_mlp_fwd": None, "e2v2_mlp_bwd": None}
-    if name in ("e2v2_mlp_fwd", "e2v2_mlp_bwd"):
-        # per launch: deg (3 profiles) once, attention (1 profile) 4 times per step
-        fl = mlp_fwd_flops if name == "e2v2_mlp_fwd" else mlp_bwd_flops
-        per_step = fl(E_mean, 3) + 4 * fl(E_mean, 1)
+    # radial-MLP FLOPs per step of each entry point: the forward runs the degree
+    # embedding's 3 profiles once and one profile per attention layer (4); the
+    # backward splits them over e2v2_mlp_bwd (attention) and e2v2_mlp_bwd_deg
+    mlp_step_flops = {"e2v2_mlp_fwd": mlp_fwd_flops(E_mean, 3) + 4 * mlp_fwd_flops(E_mean, 1),
+                      "e2v2_mlp_bwd": 4 * mlp_bwd_flops(E_mean, 1),
+                      "e2v2_mlp_bwd_deg": mlp_bwd_flops(E_mean, 3)}
+    if name in mlp_step_flops:
+        per_step = mlp_step_flops[name]
         achieved = per_step / (st["count"] / args.steps) / (st["avg_ms"] * 1e-3) / 1e12
         peak = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
@@ -213,9 +217,8 @@ def main():
         if k in BYTES_OF:
             gbs = BYTES_OF[k](N, E_mean) / (v["avg_ms"] * 1e-3) / 1e9
             ent.update(bound="hbm", achieved_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
-        elif k in ("e2v2_mlp_fwd", "e2v2_mlp_bwd"):
-            fl = mlp_fwd_flops if k == "e2v2_mlp_fwd" else mlp_bwd_flops
-            tf = (fl(E_mean, 3) + 4 * fl(E_mean, 1)) / (v["count"] / args.steps) / (v["avg_ms"] * 1e-3) / 1e12
+        elif k in mlp_step_flops:
+            tf = mlp_step_flops[k] / (v["count"] / args.steps) / (v["avg_ms"] * 1e-3) / 1e12
             pk = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
             ent.update(bound="mfma", achieved_tflops=round(tf, 2), frac=round(tf / pk, 4))
         per_kernel[k] = ent

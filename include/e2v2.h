@@ -214,8 +214,15 @@ typedef struct e2v2_deg_args {
 
 /* x0 [9][N][C] m-major */
 int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s);
+/* dfea may be NULL (then only ddvec, ddist; e2v2_mlp_bwd_deg forms dfea itself) */
 int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* dfea, float* ddvec, float* ddist,
                  hipStream_t s);
+/* e2v2_mlp_bwd for the degree embedding's three l-profiles with dOut formed per edge tile from the
+   node gradient grad_x0 [9][N][256] (m-major) instead of a stored [E][3][256] tensor:
+   dOut[e, l, c] = p(d_e)/avg sum_{m in l} Y_m(u_e) grad_x0[m][i_e][c] (the transpose of the degree
+   embedding's CSR reduce, e2former.py:719-741); deg supplies dvec, dist, avg and the envelope. */
+int e2v2_mlp_bwd_deg(const e2v2_mlp_args* args, const e2v2_deg_args* deg, const float* grad_x0, float* dd,
+                     int accumulate, hipStream_t s);
 
 /* ---- per-node kernels (node layout m-major: x[9][N][256]) --------------- */
 /* rms_norm_sh: EquivariantRMSNormArraySphericalHarmonicsV2_BL

@@ -287,6 +287,53 @@ def test_degree_forward_backward(pkg, cuda):
         assert e < 1e-4, (k_, e)
 
 
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp32", "bf16"])
+def test_degree_mlp_backward_fused(pkg, cuda, bf16):
+    """e2v2_mlp_bwd_deg (dOut formed per edge tile from the node gradient) against
+    the stored-gradient path e2v2_deg_bwd(dfea) + e2v2_mlp_bwd(dfea) on the three
+    l-profiles of the degree embedding; e2v2_deg_bwd without dfea leaves ddvec and
+    ddist unchanged.  The two paths round p/avg at different points: fp32 within
+    1e-5, bf16 (dOut rounded to bf16 in the tile) within 2e-3."""
+    from ubio_molfm_amd import _lib, modules, ops
+    torch.manual_seed(5)
+    s, pos, nl = _graph(pkg, cuda, seed=8)
+    E, N = nl.n_edges, nl.n_atoms
+    profs = [modules.RadialProfile([768, 128, 128, 256]) for _ in range(3)]
+    for prof in profs:
+        for m in prof.modules():
+            if isinstance(m, torch.nn.LayerNorm):
+                m.weight.data.uniform_(0.5, 1.5); m.bias.data.uniform_(-0.2, 0.2)
+    tgt = torch.nn.Embedding(300, 256); src = torch.nn.Embedding(300, 256)
+    rb = modules.GaussianSmearing(256, 6.0, 2.0)
+    Z = torch.as_tensor(s["Z"], device=cuda).to(torch.int32)
+    packed = [ops.PackedMLP(p_.to(cuda).net, tgt.weight.to(cuda), src.weight.to(cuda), rb.offset.to(cuda),
+                            rb.coeff, 6.0, bf16=bf16) for p_ in profs]
+    sn, sr = ops.mlp_save_buffers(3, E, cuda)
+    margs = ops.mlp_args(nl, Z, packed, sn, sr)
+    st = _lib.vp(torch.cuda.current_stream().cuda_stream)
+    fea = torch.empty(E, 768, device=cuda)
+    _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _lib.vp(fea.data_ptr()), _lib.i32(768), st)
+    dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(), fea.data_ptr(),
+                         23.01, 6.0, ops.ENV_A, ops.ENV_B, ops.ENV_C)
+    G = torch.randn(9, N, 256, generator=torch.Generator().manual_seed(12)).to(cuda)
+    f = dict(device=cuda)
+    dfea = torch.empty(E, 768, **f); ddv0 = torch.empty(E, 3, **f); dd0 = torch.empty(E, **f)
+    _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _lib.vp(G.data_ptr()), _lib.vp(dfea.data_ptr()),
+              _lib.vp(ddv0.data_ptr()), _lib.vp(dd0.data_ptr()), st)
+    _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _lib.vp(dfea.data_ptr()), _lib.i32(768),
+              _lib.vp(dd0.data_ptr()), _lib.i32(1), st)
+    ddv1 = torch.empty(E, 3, **f); dd1 = torch.empty(E, **f)
+    _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _lib.vp(G.data_ptr()), None, _lib.vp(ddv1.data_ptr()),
+              _lib.vp(dd1.data_ptr()), st)
+    _lib.call("e2v2_mlp_bwd_deg", _lib.C.byref(margs), _lib.C.byref(dargs), _lib.vp(G.data_ptr()),
+              _lib.vp(dd1.data_ptr()), _lib.i32(1), st)
+    e_dd = relerr(dd1, dd0)
+    print(f"[deg-mlp {'bf16' if bf16 else 'fp32'}] E={E} ddvec equal {torch.equal(ddv1, ddv0)} dd rel {e_dd:.2e}",
+          flush=True)
+    assert torch.equal(ddv1, ddv0)
+    assert e_dd < (2e-3 if bf16 else 1e-5)
+
+
 def test_edge_to_pos(pkg, cuda):
     from ubio_molfm_amd import _lib
     s, pos, nl = _graph(pkg, cuda, seed=6)

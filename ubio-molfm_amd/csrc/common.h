@@ -116,6 +116,20 @@ __device__ __forceinline__ float frsq(float x) { return __builtin_amdgcn_rsqf(x)
 __device__ __forceinline__ float sigmoidf_(float x) { return frcp(1.0f + fexp(-x)); }
 __device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
 
+// e3nn's raw real spherical harmonics of degree <= 2 at a unit vector (x, y, z)
+// (each l block of unit norm up to the l = 0 scale), as used by the edge-degree
+// embedding (src/molfm/models/e2former/e2former.py:719-726).
+__device__ __forceinline__ void raw_sh2(float x, float y, float z, float (&Y)[9]) {
+  const float s3 = 1.7320508075688772f;
+  Y[0] = 1.f;
+  Y[1] = x; Y[2] = y; Y[3] = z;
+  Y[4] = s3 * x * z;
+  Y[5] = s3 * x * y;
+  Y[6] = y * y - 0.5f * (x * x + z * z);
+  Y[7] = s3 * y * z;
+  Y[8] = s3 / 2.0f * (z * z - x * x);
+}
+
 // polynomial envelope (exponent 5): p = 1 + r^5 (a + r (b + c r)), 0 for r >= 1
 struct Envelope {
   float rc, a, b, c;

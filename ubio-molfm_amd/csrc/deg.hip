@@ -5,24 +5,14 @@
 //   x0[i, m, c] = (1/avg) sum_e Y_m(dvec_e / |dvec_e|) * fea_e[l(m), c] * p(d_e)
 // with Y the e3nn raw real spherical harmonics of degree <= 2 (unit norm per
 // l block) and fea the three radial-MLP outputs [E, 3, 256].
-// Backward: dfea (for the MLP backward), plus dL/ddvec and dL/dd per edge.
+// Backward: dL/ddvec and dL/dd per edge, and optionally dfea (the MLP
+// backward can form dfea from G0 itself: e2v2_mlp_bwd_deg).
 #include "common.h"
 #include "../../include/e2v2.h"
 
 namespace e2v2 {
 
 constexpr int kDC = 256;
-
-__device__ __forceinline__ void raw_sh2(float x, float y, float z, float (&Y)[9]) {
-  const float s3 = 1.7320508075688772f;
-  Y[0] = 1.f;
-  Y[1] = x; Y[2] = y; Y[3] = z;
-  Y[4] = s3 * x * z;
-  Y[5] = s3 * x * y;
-  Y[6] = y * y - 0.5f * (x * x + z * z);
-  Y[7] = s3 * y * z;
-  Y[8] = s3 / 2.0f * (z * z - x * x);
-}
 
 // dY/du for u = (x, y, z) given dL/dY -> dL/du
 __device__ __forceinline__ void raw_sh2_bwd(float x, float y, float z, const float (&g)[9], float& gx, float& gy,
@@ -115,10 +105,12 @@ __global__ __launch_bounds__(256) void k_deg_bwd(e2v2_deg_args A, const float* _
       const float d0 = Y[0] * g[q][0];
       const float d1 = Y[1] * g[q][1] + Y[2] * g[q][2] + Y[3] * g[q][3];
       const float d2 = Y[4] * g[q][4] + Y[5] * g[q][5] + Y[6] * g[q][6] + Y[7] * g[q][7] + Y[8] * g[q][8];
-      float* df = dfea + e * (3 * kDC) + c;
-      df[0] = d0 * p;
-      df[kDC] = d1 * p;
-      df[2 * kDC] = d2 * p;
+      if (dfea) {  // NULL when the MLP backward forms these from G0 itself
+        float* df = dfea + e * (3 * kDC) + c;
+        df[0] = d0 * p;
+        df[kDC] = d1 * p;
+        df[2 * kDC] = d2 * p;
+      }
       dp = fmaf(d0, f0, dp);
       dp = fmaf(d1, f1, dp);
       dp = fmaf(d2, f2, dp);

@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include <type_traits>
 #include "common.h"
 #include "../../include/e2v2.h"
 
@@ -310,6 +311,78 @@ __device__ __forceinline__ void load_tile_edges(const e2v2_mlp_args& A, int64_t 
   }
 }
 
+// dOut of the backward as the edge-degree embedding's gradient, formed per tile
+// instead of read from a stored [E][3][256] tensor:
+//   dOut[e, l, c] = p(d_e) / avg * sum_{m in l} Y_m(u_e) G0[m][i_e][c]
+// (the transpose of the CSR outer-product reduce of e2former.py:719-741, Y the
+// raw spherical harmonics of the unit edge vector, p the envelope).
+struct DegTile {
+  float y[kT][9];
+  float pa[kT];         // p(d) / avg; 0 on padding rows
+  int row[kT];
+};
+
+__device__ __forceinline__ void load_deg_tile(const e2v2_mlp_args& A, const e2v2_deg_args& D, int64_t e0,
+                                              DegTile& dt) {
+  const int t = threadIdx.x;
+  if (t < kT) {
+    const int64_t e = e0 + t;
+    if (e < A.n_edges) {
+      const float d = D.dist[e];
+      const float nrm = fmaxf(d, 1e-12f);
+      float Y[9];
+      raw_sh2(D.dvec[3 * e] / nrm, D.dvec[3 * e + 1] / nrm, D.dvec[3 * e + 2] / nrm, Y);
+#pragma unroll
+      for (int m = 0; m < 9; ++m) dt.y[t][m] = Y[m];
+      Envelope env;
+      env.rc = D.rc; env.a = D.env_a; env.b = D.env_b; env.c = D.env_c;
+      float p, dp;
+      env.eval(d, p, dp);
+      dt.pa[t] = p / D.avg;
+      dt.row[t] = A.edge_row[e];
+    } else {
+#pragma unroll
+      for (int m = 0; m < 9; ++m) dt.y[t][m] = 0.f;
+      dt.pa[t] = 0.f;
+      dt.row[t] = 0;
+    }
+  }
+}
+
+// Four consecutive channels (4 c4 .. 4 c4 + 3) of dOut row `row`, profile m: a
+// dense load, or (kDeg) the degree-embedding gradient of profile l = m.
+template <bool kDeg>
+__device__ __forceinline__ floatx4 dout4(const float* __restrict__ dout, int ld_dout, int64_t e0, int row,
+                                         int nvalid, int m, int c4, const float* __restrict__ g0, int n_rows,
+                                         const DegTile& dt) {
+  floatx4 v = {0.f, 0.f, 0.f, 0.f};
+  if (row >= nvalid) return v;
+  if constexpr (kDeg) {
+    const floatx4* gp = reinterpret_cast<const floatx4*>(g0 + (size_t)dt.row[row] * 256) + c4;
+    const size_t gs = (size_t)n_rows * 64;   // one m-row of g0, in floatx4
+    // the 2l + 1 rows of profile l = m, loaded together
+    auto acc = [&](int q0, auto nq) {
+      floatx4 g[decltype(nq)::value];
+#pragma unroll
+      for (int q = 0; q < decltype(nq)::value; ++q) g[q] = gp[(q0 + q) * gs];
+#pragma unroll
+      for (int q = 0; q < decltype(nq)::value; ++q) {
+        const float y = dt.y[row][q0 + q];
+        v[0] = fmaf(y, g[q][0], v[0]); v[1] = fmaf(y, g[q][1], v[1]);
+        v[2] = fmaf(y, g[q][2], v[2]); v[3] = fmaf(y, g[q][3], v[3]);
+      }
+    };
+    if (m == 0) acc(0, std::integral_constant<int, 1>{});
+    else if (m == 1) acc(1, std::integral_constant<int, 3>{});
+    else acc(4, std::integral_constant<int, 5>{});
+    const float pa = dt.pa[row];
+    v[0] *= pa; v[1] *= pa; v[2] *= pa; v[3] *= pa;
+    return v;
+  } else {
+    return reinterpret_cast<const floatx4*>(dout + (e0 + row) * ld_dout + m * 256)[c4];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Linear1's rbf block from its table.  Quintic Hermite basis on t in [0, 1]:
 // node values and h-, h^2-scaled derivatives at both ends.
@@ -486,18 +559,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   store_out(acc, b3, sm, out, ld_out, e0, nvalid, m);
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_mlp_bwd(
-    e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
-                                                 float* __restrict__ dd, int accumulate) {
+template <bool kDeg>
+__device__ __forceinline__ void mlp_bwd_body(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
+                                             float* __restrict__ dd, int accumulate, e2v2_deg_args D,
+                                             const float* __restrict__ g0) {
   extern __shared__ float sm[];
   float* X = sm;                    // [32][258]: dOut tile; after GEMM a, the [32][130] LayerNorm rows
   float* Y = sm;
   __shared__ TileEdges te;
   __shared__ LnParams lp;
+  __shared__ DegTile dt;
   const int64_t e0 = (int64_t)blockIdx.x * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   const float zero2[2] = {0.f, 0.f};
   load_tile_edges(A, e0, te);
+  if constexpr (kDeg) load_deg_tile(A, D, e0, dt);
+  __syncthreads();
   float dd_row = 0.f;
   for (int m = 0; m < A.n_mlp; ++m) {
     const e2v2_mlp_weights& W = A.w[m];
@@ -506,8 +583,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     load_ln_params(W, lp);
     for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {   // dOut tile, 16-byte loads
       const int row = idx >> 6, c4 = idx & 63;
-      const floatx4 v = row < nvalid ? reinterpret_cast<const floatx4*>(dout + (e0 + row) * ld_dout + m * 256)[c4]
-                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+      const floatx4 v = dout4<kDeg>(dout, ld_dout, e0, row, nvalid, m, c4, g0, D.n_rows, dt);
       float* xr = X + row * kLdX + 4 * c4;
       xr[0] = v[0]; xr[1] = v[1]; xr[2] = v[2]; xr[3] = v[3];
     }
@@ -542,6 +618,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const int64_t e = e0 + row;
     dd[e] = accumulate ? dd[e] + dd_row : dd_row;
   }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_mlp_bwd(
+    e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout, float* __restrict__ dd, int accumulate) {
+  mlp_bwd_body<false>(A, dout, ld_dout, dd, accumulate, e2v2_deg_args{}, nullptr);
+}
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_mlp_bwd_deg(
+    e2v2_mlp_args A, float* __restrict__ dd, int accumulate, e2v2_deg_args D, const float* __restrict__ g0) {
+  mlp_bwd_body<true>(A, nullptr, 0, dd, accumulate, D, g0);
 }
 
 // ---------------------------------------------------------------------------
@@ -590,18 +675,23 @@ __global__ __launch_bounds__(256) void k_mlp_fwd_bf16(e2v2_mlp_args A, float* __
   store_out(acc, b3, sm, out, ld_out, e0, nvalid, m);
 }
 
-__global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
-                                                      float* __restrict__ dd, int accumulate) {
+template <bool kDeg>
+__device__ __forceinline__ void mlp_bwd_bf16_body(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
+                                                  float* __restrict__ dd, int accumulate, e2v2_deg_args D,
+                                                  const float* __restrict__ g0) {
   extern __shared__ float sm[];
   __bf16* Xb = reinterpret_cast<__bf16*>(sm);                 // [32][264] bf16
   float* Yf = sm + (kT * kLdXb) / 2;                           // [32][130] fp32
   __bf16* Yb = reinterpret_cast<__bf16*>(Yf + kT * kLdY);      // [32][136] bf16
   __shared__ TileEdges te;
   __shared__ LnParams lp;
+  __shared__ DegTile dt;
   const int64_t e0 = (int64_t)blockIdx.x * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   const float zero2[2] = {0.f, 0.f};
   load_tile_edges(A, e0, te);
+  if constexpr (kDeg) load_deg_tile(A, D, e0, dt);
+  __syncthreads();
   float dd_row = 0.f;
   for (int m = 0; m < A.n_mlp; ++m) {
     const e2v2_mlp_weights& W = A.w[m];
@@ -612,8 +702,7 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const flo
     load_ln_params(W, lp);
     for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {
       const int row = idx >> 6, c4 = idx & 63;
-      const floatx4 v = row < nvalid ? reinterpret_cast<const floatx4*>(dout + (e0 + row) * ld_dout + m * 256)[c4]
-                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+      const floatx4 v = dout4<kDeg>(dout, ld_dout, e0, row, nvalid, m, c4, g0, D.n_rows, dt);
       __bf16* xr = Xb + row * kLdXb + 4 * c4;
       xr[0] = (__bf16)v[0]; xr[1] = (__bf16)v[1]; xr[2] = (__bf16)v[2]; xr[3] = (__bf16)v[3];
     }
@@ -648,6 +737,15 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const flo
     const int64_t e = e0 + row;
     dd[e] = accumulate ? dd[e] + dd_row : dd_row;
   }
+}
+
+__global__ __launch_bounds__(256) void k_mlp_bwd_bf16(e2v2_mlp_args A, const float* __restrict__ dout, int ld_dout,
+                                                      float* __restrict__ dd, int accumulate) {
+  mlp_bwd_bf16_body<false>(A, dout, ld_dout, dd, accumulate, e2v2_deg_args{}, nullptr);
+}
+__global__ __launch_bounds__(256) void k_mlp_bwd_deg_bf16(e2v2_mlp_args A, float* __restrict__ dd, int accumulate,
+                                                          e2v2_deg_args D, const float* __restrict__ g0) {
+  mlp_bwd_bf16_body<true>(A, nullptr, 0, dd, accumulate, D, g0);
 }
 
 }  // namespace e2v2
@@ -707,11 +805,9 @@ E2V2_API int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hip
   return 0;
 }
 
-E2V2_API int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_dout, float* dd, int accumulate,
-                          hipStream_t s) {
-  const e2v2_mlp_args& A = *args;
+static int mlp_bwd_launch(const e2v2_mlp_args& A, const float* dout, int ld_dout, float* dd, int accumulate,
+                          const e2v2_deg_args* D, const float* g0, hipStream_t s) {
   E2V2_REQUIRE(A.n_mlp >= 1 && A.n_mlp <= E2V2_MAX_MLP, "mlp_bwd: n_mlp %d out of range", A.n_mlp);
-  E2V2_REQUIRE(ld_dout >= 256 * A.n_mlp && ld_dout % 4 == 0, "mlp_bwd: bad ld_dout %d", ld_dout);
   E2V2_REQUIRE(A.save_n != nullptr && A.save_r != nullptr,
                "mlp_bwd: needs the normalised activations saved by e2v2_mlp_fwd (save_n, save_r)");
   if (A.n_edges == 0) return 0;
@@ -720,11 +816,35 @@ E2V2_API int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_d
   if (A.compute_bf16) {
     for (int m = 0; m < A.n_mlp; ++m)
       E2V2_REQUIRE(A.w[m].w3tb && A.w[m].w2tb, "mlp_bwd: bf16 weights missing for profile %d", m);
-    hipLaunchKernelGGL(k_mlp_bwd_bf16, grid, dim3(256), mlp_lds_bwd_bf16(), s, A, dout, ld_dout, dd, accumulate);
-    E2V2_LAUNCHED("k_mlp_bwd_bf16");
+    if (D) {
+      hipLaunchKernelGGL(k_mlp_bwd_deg_bf16, grid, dim3(256), mlp_lds_bwd_bf16(), s, A, dd, accumulate, *D, g0);
+      E2V2_LAUNCHED("k_mlp_bwd_deg_bf16");
+    } else {
+      hipLaunchKernelGGL(k_mlp_bwd_bf16, grid, dim3(256), mlp_lds_bwd_bf16(), s, A, dout, ld_dout, dd, accumulate);
+      E2V2_LAUNCHED("k_mlp_bwd_bf16");
+    }
     return 0;
   }
-  hipLaunchKernelGGL(k_mlp_bwd, grid, dim3(256), mlp_lds_bwd(), s, A, dout, ld_dout, dd, accumulate);
-  E2V2_LAUNCHED("k_mlp_bwd");
+  if (D) {
+    hipLaunchKernelGGL(k_mlp_bwd_deg, grid, dim3(256), mlp_lds_bwd(), s, A, dd, accumulate, *D, g0);
+    E2V2_LAUNCHED("k_mlp_bwd_deg");
+  } else {
+    hipLaunchKernelGGL(k_mlp_bwd, grid, dim3(256), mlp_lds_bwd(), s, A, dout, ld_dout, dd, accumulate);
+    E2V2_LAUNCHED("k_mlp_bwd");
+  }
   return 0;
+}
+
+E2V2_API int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_dout, float* dd, int accumulate,
+                          hipStream_t s) {
+  E2V2_REQUIRE(ld_dout >= 256 * args->n_mlp && ld_dout % 4 == 0, "mlp_bwd: bad ld_dout %d", ld_dout);
+  return mlp_bwd_launch(*args, dout, ld_dout, dd, accumulate, nullptr, nullptr, s);
+}
+
+E2V2_API int e2v2_mlp_bwd_deg(const e2v2_mlp_args* args, const e2v2_deg_args* deg, const float* grad_x0, float* dd,
+                              int accumulate, hipStream_t s) {
+  E2V2_REQUIRE(args->n_mlp == 3 && deg && grad_x0 && deg->channels == 256 && deg->n_edges == args->n_edges,
+               "mlp_bwd_deg: needs the three l-profiles of the degree embedding (n_mlp %d) and its edges",
+               args->n_mlp);
+  return mlp_bwd_launch(*args, nullptr, 0, dd, accumulate, deg, grad_x0, s);
 }

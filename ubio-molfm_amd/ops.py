@@ -201,12 +201,13 @@ class DegreeEmbedFn(torch.autograd.Function):
         gx0 = gx0.float().contiguous()
         dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                              fea.data_ptr(), float(ctx.avg), float(ctx.rc), ENV_A, ENV_B, ENV_C)
-        dfea = torch.empty_like(fea)
         ddv = torch.empty(max(E, 1), 3, dtype=torch.float32, device=dev)
         dd = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
-        _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(dfea), _p(ddv), _p(dd), _stream(gx0))
+        _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), None, _p(ddv), _p(dd), _stream(gx0))
         margs = mlp_args(nl, node_type, packed, sn, sr)
-        _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dfea), _lib.i32(768), _p(dd), _lib.i32(1), _stream(gx0))
+        # the MLP backward forms the [E, 3, 256] feature gradient per edge tile from gx0
+        _lib.call("e2v2_mlp_bwd_deg", _lib.C.byref(margs), _lib.C.byref(dargs), _p(gx0), _p(dd), _lib.i32(1),
+                  _stream(gx0))
         return ddv[:E], dd[:E], None, None, None, None, None, None, None
 
 
