@@ -228,6 +228,10 @@ int e2v2_mlp_bwd_deg(const e2v2_mlp_args* args, const e2v2_deg_args* deg, const 
 /* rms_norm_sh: EquivariantRMSNormArraySphericalHarmonicsV2_BL
  * (src/molfm/models/e2former/module_utils.py:1663-1772); w [3][256], b [256] */
 int e2v2_rmsnorm_fwd(const float* x, const float* w, const float* b, float* y, int n, float eps, hipStream_t s);
+/* The residual add of the producing block fused in: xs = x + delta (written) and y = rms_norm_sh(xs);
+   delta = NULL is e2v2_rmsnorm_fwd (xs unused). */
+int e2v2_add_rmsnorm_fwd(const float* x, const float* delta, const float* w, const float* b, float* xs, float* y,
+                         int n, float eps, hipStream_t s);
 /* gx = d(rms_norm_sh)/dx^T gy (+ gres when gres is not NULL: the gradient of a residual branch that reads x) */
 int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, const float* gres, float* gx, int n, float eps,
                      hipStream_t s);

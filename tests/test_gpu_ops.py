@@ -341,10 +341,12 @@ def test_edge_to_pos(pkg, cuda):
     g = torch.Generator().manual_seed(1)
     gdv = torch.randn(E, 3, generator=g); gd = torch.randn(E, generator=g)
     out = torch.empty(N, 3, device=cuda)
+    gdv_d, gd_d = gdv.to(cuda), gd.to(cuda)   # held until the kernel has run
     _lib.call("e2v2_edge_to_pos", _lib.i32(N), _lib.vp(nl.row_ptr.data_ptr()), _lib.vp(nl.key_ptr.data_ptr()),
               _lib.vp(nl.key_eid.data_ptr()), _lib.vp(nl.dvec.data_ptr()), _lib.vp(nl.dist.data_ptr()),
-              _lib.vp(gdv.to(cuda).data_ptr()), _lib.vp(gd.to(cuda).data_ptr()), _lib.vp(out.data_ptr()),
+              _lib.vp(gdv_d.data_ptr()), _lib.vp(gd_d.data_ptr()), _lib.vp(out.data_ptr()),
               _lib.vp(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
     p64 = torch.as_tensor(s["pos"], dtype=torch.float64).requires_grad_(True)
     off = torch.as_tensor((nl.shifts.numpy()[nl.shift_idx.cpu().numpy()] @ s["cell"][0].astype(np.float64)))
     row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()

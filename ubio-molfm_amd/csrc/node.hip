@@ -30,8 +30,11 @@ __device__ __forceinline__ float bal(int m) {
   return 1.0f / ((2.0f * l + 1.0f) * 3.0f);
 }
 
-__global__ __launch_bounds__(256) void k_rmsnorm_fwd(const float* __restrict__ x, const float* __restrict__ w,
-                                                     const float* __restrict__ b, float* __restrict__ y, int n,
+// y = rms_norm_sh(x), or with delta: xs = x + delta (the residual add of the
+// producing block, written out) and y = rms_norm_sh(xs)
+__global__ __launch_bounds__(256) void k_rmsnorm_fwd(const float* __restrict__ x, const float* __restrict__ delta,
+                                                     const float* __restrict__ w, const float* __restrict__ b,
+                                                     float* __restrict__ xs, float* __restrict__ y, int n,
                                                      float eps) {
   __shared__ float red[4];
   const int i = blockIdx.x, c = threadIdx.x;
@@ -40,6 +43,15 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(const float* __restrict__ x
   float f[9];
 #pragma unroll
   for (int m = 0; m < 9; ++m) f[m] = xp[m * st];
+  if (delta) {
+    const float* dp = delta + (size_t)i * kNC + c;
+    float* sp = xs + (size_t)i * kNC + c;
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      f[m] += dp[m * st];
+      sp[m * st] = f[m];
+    }
+  }
   const float mean0 = block_sum256(f[0], red) * (1.0f / kNC);
   f[0] -= mean0;
   float ss = 0.f;
@@ -147,8 +159,14 @@ using namespace e2v2;
 
 E2V2_API int e2v2_rmsnorm_fwd(const float* x, const float* w, const float* b, float* y, int n, float eps,
                               hipStream_t s) {
+  return e2v2_add_rmsnorm_fwd(x, nullptr, w, b, nullptr, y, n, eps, s);
+}
+
+E2V2_API int e2v2_add_rmsnorm_fwd(const float* x, const float* delta, const float* w, const float* b, float* xs,
+                                  float* y, int n, float eps, hipStream_t s) {
+  E2V2_REQUIRE(!delta || xs, "add_rmsnorm_fwd: the sum x + delta needs an output buffer");
   if (n == 0) return 0;
-  hipLaunchKernelGGL(k_rmsnorm_fwd, dim3(n), dim3(256), 0, s, x, w, b, y, n, eps);
+  hipLaunchKernelGGL(k_rmsnorm_fwd, dim3(n), dim3(256), 0, s, x, delta, w, b, xs, y, n, eps);
   E2V2_LAUNCHED("k_rmsnorm_fwd");
   return 0;
 }

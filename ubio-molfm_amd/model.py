@@ -51,10 +51,15 @@ def spatial_order(pos: torch.Tensor, graph_ptr) -> torch.Tensor:
     N = pos.shape[0]
     if N == 0:
         return torch.zeros(0, dtype=torch.long, device=pos.device)
-    counts = torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device)
-    B = counts.shape[0]
-    gid = torch.repeat_interleave(torch.arange(B, device=pos.device), counts)
-    lo, hi = graph_bounds(pos, counts)
+    counts_np = np.diff(np.asarray(graph_ptr))
+    B = len(counts_np)
+    if B == 1:   # no host copies or syncs for a single graph
+        gid = torch.zeros(N, dtype=torch.long, device=pos.device)
+        lo, hi = pos.amin(0, keepdim=True), pos.amax(0, keepdim=True)
+    else:
+        counts = torch.as_tensor(counts_np, device=pos.device)
+        gid = torch.repeat_interleave(torch.arange(B, device=pos.device), counts, output_size=N)
+        lo, hi = graph_bounds(pos, counts)
     span = (hi - lo).clamp_min(1e-6)
     q = ((pos - lo[gid]) / span[gid] * 1023.0).clamp(0, 1023).to(torch.int64)
     code = _spread_bits10(q[:, 0]) | (_spread_bits10(q[:, 1]) << 1) | (_spread_bits10(q[:, 2]) << 2)

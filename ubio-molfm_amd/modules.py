@@ -211,7 +211,8 @@ class SO2OutFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, so2, res, blocks, Wp, bp):
-        so2 = so2.contiguous(); res = res.contiguous()
+        so2 = so2.contiguous()
+        res = None if res is None else res.contiguous()
         _, N, C = so2.shape
         t = so2.new_empty(9, N, C, dtype=torch.float32)
         sa = _bf(so2) if Wp.dtype == BF16 else so2
@@ -228,11 +229,18 @@ class SO2OutFn(torch.autograd.Function):
             o += nr
         y = so2.new_empty(9, N, Wp.shape[1], dtype=torch.float32)
         ta = _bf(t) if Wp.dtype == BF16 else t
+        O = Wp.shape[1]
         for l in range(3):
             a, b = l * l, (l + 1) ** 2
-            _addmm_into(res[a:b].view(-1, Wp.shape[1]), ta[a:b].view(-1, C), Wp[l].t(),
-                        out=y[a:b].view(-1, Wp.shape[1]))
-        y[0].add_(bp)
+            if res is not None:
+                _addmm_into(res[a:b].view(-1, O), ta[a:b].view(-1, C), Wp[l].t(), out=y[a:b].view(-1, O))
+            elif l == 0:
+                _mm_bias_into(ta[0], Wp[0].t(), bp, out=y[0])
+            else:
+                _mm_into(ta[a:b].view(-1, C), Wp[l].t(), out=y[a:b].view(-1, O))
+        if res is not None:
+            y[0].add_(bp)
+        ctx.has_res = res is not None
         ctx.blocks = blocks
         ctx.save_for_backward(Wp)
         ctx.shape, ctx.so2_dtype = so2.shape, so2.dtype
@@ -259,7 +267,7 @@ class SO2OutFn(torch.autograd.Function):
             for (t0, nr_, Wt) in lst:
                 _mm_into(gv, Wt.t(), out=gso2[t0:t0 + nr_].view(-1, C))
             o += nr
-        return gso2, gy, None, None, None
+        return gso2, (gy if ctx.has_res else None), None, None, None
 
 
 class RMSNormFn(torch.autograd.Function):
@@ -285,33 +293,43 @@ class RMSNormFn(torch.autograd.Function):
         return gx, None, None, None
 
 
-class RMSNormResidualFn(torch.autograd.Function):
-    """(rms_norm_sh(x), x): the normed input of a block and x itself for the
-    block's residual branch, so that the backward adds the two gradients of x
-    inside the norm's kernel instead of a separate accumulation pass."""
+class AddRMSNormFn(torch.autograd.Function):
+    """(rms_norm_sh(xs), xs) with xs = x + delta (delta None: xs = x): the
+    residual add of the producing block fused into the norm that follows it,
+    and xs returned for the next residual branch, so that the backward adds the
+    two gradients of xs inside the norm's kernel (no accumulation pass, no
+    residual operand in the GEMMs)."""
 
     @staticmethod
-    def forward(ctx, x, w, b, eps: float):
+    def forward(ctx, x, delta, w, b, eps: float):
         x = x.contiguous()
         y = torch.empty_like(x)
-        _lib.call("e2v2_rmsnorm_fwd", _dp(x), _dp(w), _dp(b), _dp(y), _lib.i32(x.shape[1]), _lib.f32(eps),
-                  _stream())
-        ctx.save_for_backward(x, w)
-        ctx.eps = eps
+        if delta is None:
+            xs = x
+            _lib.call("e2v2_rmsnorm_fwd", _dp(x), _dp(w), _dp(b), _dp(y), _lib.i32(x.shape[1]), _lib.f32(eps),
+                      _stream())
+        else:
+            delta = delta.contiguous()
+            xs = torch.empty_like(x)
+            _lib.call("e2v2_add_rmsnorm_fwd", _dp(x), _dp(delta), _dp(w), _dp(b), _dp(xs), _dp(y),
+                      _lib.i32(x.shape[1]), _lib.f32(eps), _stream())
+        ctx.save_for_backward(xs, w)
+        ctx.eps, ctx.has_delta = eps, delta is not None
         ctx.set_materialize_grads(False)
-        return y, x
+        return y, xs
 
     @staticmethod
     def backward(ctx, gy, gres):
-        x, w = ctx.saved_tensors
+        xs, w = ctx.saved_tensors
         if gy is None:
-            return gres, None, None, None
-        gy = gy.contiguous()
-        gres = None if gres is None else gres.contiguous()
-        gx = torch.empty_like(x)
-        _lib.call("e2v2_rmsnorm_bwd", _dp(x), _dp(w), _dp(gy), None if gres is None else _dp(gres), _dp(gx),
-                  _lib.i32(x.shape[1]), _lib.f32(ctx.eps), _stream())
-        return gx, None, None, None
+            gx = gres
+        else:
+            gy = gy.contiguous()
+            gres = None if gres is None else gres.contiguous()
+            gx = torch.empty_like(xs)
+            _lib.call("e2v2_rmsnorm_bwd", _dp(xs), _dp(w), _dp(gy), None if gres is None else _dp(gres), _dp(gx),
+                      _lib.i32(xs.shape[1]), _lib.f32(ctx.eps), _stream())
+        return gx, (gx if ctx.has_delta else None), None, None, None
 
 
 class GateFn(torch.autograd.Function):
@@ -490,10 +508,11 @@ class EquivariantRMSNormArraySphericalHarmonicsV2_BL(nn.Module):
         return RMSNormFn.apply(x, self.affine_weight.detach().float().contiguous(),
                                self.affine_bias.detach().float().contiguous(), float(self.eps))
 
-    def forward_with_residual(self, x):
-        """(norm(x), x) with the residual gradient added in the norm's backward."""
-        return RMSNormResidualFn.apply(x, self.affine_weight.detach().float().contiguous(),
-                                       self.affine_bias.detach().float().contiguous(), float(self.eps))
+    def add_forward(self, x, delta=None):
+        """(norm(x + delta), x + delta); the gradient of the returned sum is added
+        in the norm's backward."""
+        return AddRMSNormFn.apply(x, delta, self.affine_weight.detach().float().contiguous(),
+                                  self.affine_bias.detach().float().contiguous(), float(self.eps))
 
 
 class Gate_s3(nn.Module):
@@ -700,7 +719,7 @@ class E2AttentionArbOrder_sparse(nn.Module):
         return cached(self, "qk_bf16" if bf16 else "qk", params, build)
 
     def forward(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
-        """x [9, N, C] (m-major) -> res + attention(x), [9, N, C]."""
+        """x [9, N, C] (m-major) -> attention(x) (+ res when given), [9, N, C]."""
         N = x.shape[1]
         H = self.num_attn_heads
         if self.training and self.alpha_dropout.p > 0:
@@ -716,8 +735,6 @@ class E2AttentionArbOrder_sparse(nn.Module):
                                ctx.rbf_coeff, ctx.rc, bf16)
         so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
                                 packed, ctx.rc, math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
-        if res is None:
-            res = torch.zeros_like(x)
         pf = self.proj_first
         return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16),
                               gemm_weight(pf, "weight", bf16), pf.bias.detach())
@@ -740,13 +757,19 @@ class TransBlock(nn.Module):
         self.ffn = FeedForwardNetwork_s3(C, C, C, lmax)
 
     def forward(self, x, ctx: EdgeContext, sys_node_embedding=None):
-        """x [9, N, C] m-major."""
-        h, res = self.norm_1.forward_with_residual(x)
+        """x [9, N, C] m-major -> the block output."""
+        x, d = self.forward_deferred(x, None, ctx, sys_node_embedding)
+        return x + d
+
+    def forward_deferred(self, x, delta, ctx: EdgeContext, sys_node_embedding=None):
+        """(x', d) with block output x' + d for the input x + delta: each residual
+        add is left to the RMS norm that reads its result next."""
+        h, x = self.norm_1.add_forward(x, delta)
         if sys_node_embedding is not None:
             h = torch.cat([(h[0] + sys_node_embedding).unsqueeze(0), h[1:]], dim=0)
-        x = self.ga(h, ctx, res=res)
-        h, res = self.norm_ffn.forward_with_residual(x)
-        return self.ffn(h, res=res, bf16=ctx.bf16)
+        d = self.ga(h, ctx)
+        h, x = self.norm_ffn.add_forward(x, d)
+        return x, self.ffn(h, bf16=ctx.bf16)
 
 
 class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
@@ -808,9 +831,10 @@ class E2former(nn.Module):
     def forward_flat(self, ctx: EdgeContext, sys_node_embedding: Optional[torch.Tensor] = None):
         """Returns the node irreps in the m-major layout [9, N, C]."""
         x = self.edge_deg_embed_dense(ctx)
+        d = None
         for blk in self.blocks:
-            x = blk(x, ctx, sys_node_embedding)
-        return self.norm_final(x)
+            x, d = blk.forward_deferred(x, d, ctx, sys_node_embedding)
+        return self.norm_final.add_forward(x, d)[0]
 
 
 def parse_irreps(s: str):

@@ -119,13 +119,11 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     stream = torch.cuda.current_stream(dev).cuda_stream
     i32 = dict(dtype=torch.int32, device=dev)
     # per-graph bounding boxes (one host sync)
-    atom_graph = torch.repeat_interleave(torch.arange(B, device=dev, dtype=torch.int32),
-                                         torch.as_tensor(np.diff(graph_ptr), device=dev))
     if N:
-        counts = torch.as_tensor(np.diff(graph_ptr), device=dev)
         if B == 1:
             lo, hi = pos.amin(0, keepdim=True), pos.amax(0, keepdim=True)
         else:
+            counts = torch.as_tensor(np.diff(graph_ptr), device=dev)
             lo = torch.segment_reduce(pos, "min", lengths=counts, axis=0, unsafe=True)
             hi = torch.segment_reduce(pos, "max", lengths=counts, axis=0, unsafe=True)
         bb = torch.stack([lo, hi]).cpu().numpy()
@@ -156,13 +154,15 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
         nb += int(np.prod(dims))
     shifts_np = np.concatenate(shifts).astype(np.int32)
     offs = np.concatenate([shift_offsets(s, cells[g]) for g, s in enumerate(shifts)]).astype(F32)
-    up = lambda a, dt: torch.as_tensor(np.ascontiguousarray(a), dtype=dt, device=dev)
-    t_gptr = up(graph_ptr.astype(np.int32), torch.int32)
-    t_sptr = up(np.asarray(sptr, np.int32), torch.int32)
-    t_per = up(np.asarray(periodic, np.int32), torch.int32)
-    t_off = up(offs.reshape(-1, 3), torch.float32)
-    t_lo = up(glo, torch.float32); t_h = up(gh, torch.float32); t_dim = up(gdim, torch.int32)
-    t_base = up(base, torch.int32)
+    # the plan's small tables in one host-to-device copy per type
+    ints = [graph_ptr.astype(np.int32), np.asarray(sptr, np.int32), np.asarray(periodic, np.int32),
+            gdim.reshape(-1), base, np.repeat(np.arange(B, dtype=np.int32), np.diff(graph_ptr))]
+    floats = [offs.reshape(-1), glo.reshape(-1), gh.reshape(-1)]
+    ti = torch.as_tensor(np.concatenate(ints).astype(np.int32), device=dev)
+    tf = torch.as_tensor(np.concatenate(floats).astype(F32), device=dev)
+    ti_parts = torch.split(ti, [len(a) for a in ints])
+    t_gptr, t_sptr, t_per, t_dim, t_base, atom_graph = ti_parts
+    t_off, t_lo, t_h = torch.split(tf, [len(a) for a in floats])
     atom_bin = torch.empty(max(N, 1), **i32)
     bin_count = torch.empty(nb, **i32)
     bin_start = torch.empty(nb + 1, **i32)
