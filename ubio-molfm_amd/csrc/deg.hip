@@ -7,6 +7,7 @@
 // l block) and fea the three radial-MLP outputs [E, 3, 256].
 // Backward: dL/ddvec and dL/dd per edge, and optionally dfea (the MLP
 // backward can form dfea from G0 itself: e2v2_mlp_bwd_deg).
+#include <algorithm>
 #include "common.h"
 #include "../../include/e2v2.h"
 
@@ -137,30 +138,40 @@ __global__ __launch_bounds__(256) void k_deg_bwd(e2v2_deg_args A, const float* _
   }
 }
 
-// dpos[a] = sum_{e in row a} g_e - sum_{e in column a} g_e,  g_e = ddv_e + dd_e dvec_e / d_e
-__global__ void k_edge_to_pos(int n_atoms, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ key_ptr,
-                              const int32_t* __restrict__ key_eid, const float* __restrict__ dvec,
-                              const float* __restrict__ dist, const float* __restrict__ ddv,
-                              const float* __restrict__ dd, float* __restrict__ dpos) {
-  const int a = blockIdx.x * blockDim.x + threadIdx.x;
-  if (a >= n_atoms) return;
-  float gx = 0.f, gy = 0.f, gz = 0.f;
-  for (int e = row_ptr[a]; e < row_ptr[a + 1]; ++e) {
-    const float s = dd[e] / dist[e];
-    gx += ddv[3 * e] + s * dvec[3 * e];
-    gy += ddv[3 * e + 1] + s * dvec[3 * e + 1];
-    gz += ddv[3 * e + 2] + s * dvec[3 * e + 2];
+// dpos[a] = sum_{e in row a} g_e - sum_{e in column a} g_e,  g_e = ddv_e + dd_e dvec_e / d_e.
+// One wavefront per atom: lanes stride over the row's and the column's edges,
+// then a fixed-order wave reduction (deterministic).
+constexpr int kPosWaves = 4;
+
+__device__ __forceinline__ void edge_grad(int64_t e, const float* __restrict__ dvec, const float* __restrict__ dist,
+                                          const float* __restrict__ ddv, const float* __restrict__ dd, float sign,
+                                          float& gx, float& gy, float& gz) {
+  const float s = dd[e] / dist[e];
+  gx += sign * (ddv[3 * e] + s * dvec[3 * e]);
+  gy += sign * (ddv[3 * e + 1] + s * dvec[3 * e + 1]);
+  gz += sign * (ddv[3 * e + 2] + s * dvec[3 * e + 2]);
+}
+
+__global__ __launch_bounds__(64 * kPosWaves) void k_edge_to_pos(int n_atoms, const int32_t* __restrict__ row_ptr,
+                                                                const int32_t* __restrict__ key_ptr,
+                                                                const int32_t* __restrict__ key_eid,
+                                                                const float* __restrict__ dvec,
+                                                                const float* __restrict__ dist,
+                                                                const float* __restrict__ ddv,
+                                                                const float* __restrict__ dd, float* __restrict__ dpos) {
+  const int lane = threadIdx.x & 63;
+  for (int a = blockIdx.x * kPosWaves + (int)(threadIdx.x >> 6); a < n_atoms; a += gridDim.x * kPosWaves) {
+    float gx = 0.f, gy = 0.f, gz = 0.f;
+    for (int e = row_ptr[a] + lane; e < row_ptr[a + 1]; e += 64) edge_grad(e, dvec, dist, ddv, dd, 1.f, gx, gy, gz);
+    for (int p = key_ptr[a] + lane; p < key_ptr[a + 1]; p += 64)
+      edge_grad(key_eid[p], dvec, dist, ddv, dd, -1.f, gx, gy, gz);
+    gx = wave_sum(gx); gy = wave_sum(gy); gz = wave_sum(gz);
+    if (lane == 0) {
+      dpos[3 * a] = gx;
+      dpos[3 * a + 1] = gy;
+      dpos[3 * a + 2] = gz;
+    }
   }
-  for (int p = key_ptr[a]; p < key_ptr[a + 1]; ++p) {
-    const int64_t e = key_eid[p];
-    const float s = dd[e] / dist[e];
-    gx -= ddv[3 * e] + s * dvec[3 * e];
-    gy -= ddv[3 * e + 1] + s * dvec[3 * e + 1];
-    gz -= ddv[3 * e + 2] + s * dvec[3 * e + 2];
-  }
-  dpos[3 * a] = gx;
-  dpos[3 * a + 1] = gy;
-  dpos[3 * a + 2] = gz;
 }
 
 }  // namespace e2v2
@@ -190,7 +201,8 @@ E2V2_API int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t
                               const float* dvec, const float* dist, const float* ddvec, const float* ddist,
                               float* dpos, hipStream_t s) {
   if (n_atoms == 0) return 0;
-  hipLaunchKernelGGL(k_edge_to_pos, dim3((n_atoms + 127) / 128), dim3(128), 0, s, n_atoms, row_ptr, key_ptr, key_eid,
+  const int blocks = (int)std::min<int64_t>(((int64_t)n_atoms + kPosWaves - 1) / kPosWaves, 1 << 20);
+  hipLaunchKernelGGL(k_edge_to_pos, dim3(blocks), dim3(64 * kPosWaves), 0, s, n_atoms, row_ptr, key_ptr, key_eid,
                      dvec, dist, ddvec, ddist, dpos);
   E2V2_LAUNCHED("k_edge_to_pos");
   return 0;

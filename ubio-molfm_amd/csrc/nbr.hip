@@ -270,14 +270,18 @@ __device__ void segment_sort(const uint64_t* __restrict__ key, int b, int n, uin
   }
 }
 
-__global__ __launch_bounds__(256) void k_sort_rows(const int32_t* __restrict__ row_ptr,
-                                                   const uint64_t* __restrict__ key,
-                                                   const int32_t* __restrict__ tcol, const int32_t* __restrict__ tshift,
-                                                   const float* __restrict__ tdv, const float* __restrict__ td,
-                                                   int32_t* __restrict__ col, int32_t* __restrict__ shift,
-                                                   float* __restrict__ dvec, float* __restrict__ dist) {
-  __shared__ uint64_t sk[kMaxSeg];
-  __shared__ int32_t sv[kMaxSeg];
+// One wavefront per row (column); LDS holds cap keys and positions (cap = the
+// longest row rounded up to a power of two, sized by the host).
+extern __shared__ uint64_t seg_lds[];
+
+__global__ __launch_bounds__(64) void k_sort_rows(const int32_t* __restrict__ row_ptr,
+                                                  const uint64_t* __restrict__ key,
+                                                  const int32_t* __restrict__ tcol, const int32_t* __restrict__ tshift,
+                                                  const float* __restrict__ tdv, const float* __restrict__ td,
+                                                  int32_t* __restrict__ col, int32_t* __restrict__ shift,
+                                                  float* __restrict__ dvec, float* __restrict__ dist, int cap) {
+  uint64_t* sk = seg_lds;
+  int32_t* sv = reinterpret_cast<int32_t*>(seg_lds + cap);
   const int r = blockIdx.x;
   const int b = row_ptr[r], n = row_ptr[r + 1] - b;
   if (n == 0) return;
@@ -340,17 +344,17 @@ __device__ void sort_global(uint64_t* __restrict__ k, int n) {
   }
 }
 
-// Columns of any length: up to kMaxSeg in LDS, longer ones in place in global
+// Columns of any length: up to cap in LDS, longer ones in place in global
 // memory (tkey is scratch), so the host needs no column-length check.
-__global__ __launch_bounds__(256) void k_sort_cols(const int32_t* __restrict__ key_ptr,
-                                                   uint64_t* __restrict__ tkey,
-                                                   int32_t* __restrict__ key_eid) {
-  __shared__ uint64_t sk[kMaxSeg];
-  __shared__ int32_t sv[kMaxSeg];
+__global__ __launch_bounds__(64) void k_sort_cols(const int32_t* __restrict__ key_ptr,
+                                                  uint64_t* __restrict__ tkey,
+                                                  int32_t* __restrict__ key_eid, int cap) {
+  uint64_t* sk = seg_lds;
+  int32_t* sv = reinterpret_cast<int32_t*>(seg_lds + cap);
   const int r = blockIdx.x;
   const int b = key_ptr[r], n = key_ptr[r + 1] - b;
   if (n == 0) return;
-  if (n > kMaxSeg) {
+  if (n > cap) {
     sort_global(tkey + b, n);
     for (int t = threadIdx.x; t < n; t += blockDim.x) key_eid[b + t] = (int32_t)tkey[b + t];
     return;
@@ -515,6 +519,14 @@ __global__ void k_topk_compact(const int32_t* __restrict__ row_ptr, const int32_
   }
 }
 
+// LDS capacity (power of two, 64 .. kMaxSeg) of the per-segment sorts for segments of up to n items
+static inline int seg_cap(int n) {
+  int c = 64;
+  while (c < n && c < kMaxSeg) c <<= 1;
+  return c;
+}
+static inline size_t seg_lds_bytes(int cap) { return (size_t)cap * (sizeof(uint64_t) + sizeof(int32_t)); }
+
 static inline unsigned blocks_for(int64_t n, int bs) {
   int64_t b = (n + bs - 1) / bs;
   return (unsigned)(b < 1 ? 1 : (b > 1048576 ? 1048576 : b));
@@ -585,8 +597,9 @@ E2V2_API int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, in
   hipLaunchKernelGGL(k_nbr_fill, dim3(blocks_for(P.n_atoms, kNbrWaves)), dim3(64 * kNbrWaves), 0, s, P, row_ptr,
                      tmp_col, tmp_shift, tmp_dvec, tmp_dist, tmp_key);
   E2V2_LAUNCHED("k_nbr_fill");
-  hipLaunchKernelGGL(k_sort_rows, dim3(P.n_atoms), dim3(256), 0, s, row_ptr, tmp_key, tmp_col, tmp_shift, tmp_dvec,
-                     tmp_dist, col, shift, dvec, dist);
+  const int cap = seg_cap(max_row);
+  hipLaunchKernelGGL(k_sort_rows, dim3(P.n_atoms), dim3(64), seg_lds_bytes(cap), s, row_ptr, tmp_key, tmp_col,
+                     tmp_shift, tmp_dvec, tmp_dist, col, shift, dvec, dist, cap);
   E2V2_LAUNCHED("k_sort_rows");
   return 0;
 }
@@ -648,7 +661,10 @@ E2V2_API int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int 
   hipLaunchKernelGGL(k_col_fill, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, col, n_edges, key_ptr, key_cnt,
                      tmp_key);
   E2V2_LAUNCHED("k_col_fill");
-  hipLaunchKernelGGL(k_sort_cols, dim3(n_cols), dim3(256), 0, s, key_ptr, tmp_key, key_eid);
+  // columns of up to 256 edges sort in LDS (at liquid density and a 6 A cutoff a column
+  // holds about 90), longer ones in place in global memory
+  const int cap = 256;
+  hipLaunchKernelGGL(k_sort_cols, dim3(n_cols), dim3(64), seg_lds_bytes(cap), s, key_ptr, tmp_key, key_eid, cap);
   E2V2_LAUNCHED("k_sort_cols");
   return 0;
 }
