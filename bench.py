@@ -62,7 +62,9 @@ def deg_fwd_bytes(N, E):
 
 
 def deg_bwd_bytes(N, E):
-    return 4.0 * (E * (768 + 768 + 4 + 4) + N * 9 * 256)
+    # read fea, dvec, dist and the node gradient; write ddvec, ddist (the feature
+    # gradient is formed inside e2v2_mlp_bwd_deg, never stored)
+    return 4.0 * (E * (768 + 4 + 4) + N * 9 * 256)
 
 
 def stack_flops(N, E):

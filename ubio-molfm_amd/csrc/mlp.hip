@@ -569,7 +569,12 @@ __device__ __forceinline__ void mlp_bwd_body(e2v2_mlp_args A, const float* __res
   __shared__ TileEdges te;
   __shared__ LnParams lp;
   __shared__ DegTile dt;
-  const int64_t e0 = (int64_t)blockIdx.x * kT;
+  // degree mode: each XCD takes a contiguous range of tiles, so the node-gradient
+  // rows that neighbouring tiles share stay in one L2
+  const int64_t n_tiles = (A.n_edges + kT - 1) / kT;
+  const int64_t tile = kDeg ? (int64_t)xcd_row(blockIdx.x, (int)n_tiles) : (int64_t)blockIdx.x;
+  if (tile >= n_tiles) return;
+  const int64_t e0 = tile * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   const float zero2[2] = {0.f, 0.f};
   load_tile_edges(A, e0, te);
@@ -686,7 +691,12 @@ __device__ __forceinline__ void mlp_bwd_bf16_body(e2v2_mlp_args A, const float* 
   __shared__ TileEdges te;
   __shared__ LnParams lp;
   __shared__ DegTile dt;
-  const int64_t e0 = (int64_t)blockIdx.x * kT;
+  // degree mode: each XCD takes a contiguous range of tiles, so the node-gradient
+  // rows that neighbouring tiles share stay in one L2
+  const int64_t n_tiles = (A.n_edges + kT - 1) / kT;
+  const int64_t tile = kDeg ? (int64_t)xcd_row(blockIdx.x, (int)n_tiles) : (int64_t)blockIdx.x;
+  if (tile >= n_tiles) return;
+  const int64_t e0 = tile * kT;
   const int nvalid = (int)min<int64_t>(kT, A.n_edges - e0);
   const float zero2[2] = {0.f, 0.f};
   load_tile_edges(A, e0, te);
@@ -817,7 +827,8 @@ static int mlp_bwd_launch(const e2v2_mlp_args& A, const float* dout, int ld_dout
     for (int m = 0; m < A.n_mlp; ++m)
       E2V2_REQUIRE(A.w[m].w3tb && A.w[m].w2tb, "mlp_bwd: bf16 weights missing for profile %d", m);
     if (D) {
-      hipLaunchKernelGGL(k_mlp_bwd_deg_bf16, grid, dim3(256), mlp_lds_bwd_bf16(), s, A, dd, accumulate, *D, g0);
+      hipLaunchKernelGGL(k_mlp_bwd_deg_bf16, dim3((unsigned)xcd_grid((int)((A.n_edges + kT - 1) / kT))), dim3(256),
+                         mlp_lds_bwd_bf16(), s, A, dd, accumulate, *D, g0);
       E2V2_LAUNCHED("k_mlp_bwd_deg_bf16");
     } else {
       hipLaunchKernelGGL(k_mlp_bwd_bf16, grid, dim3(256), mlp_lds_bwd_bf16(), s, A, dout, ld_dout, dd, accumulate);
@@ -825,8 +836,9 @@ static int mlp_bwd_launch(const e2v2_mlp_args& A, const float* dout, int ld_dout
     }
     return 0;
   }
+  const dim3 grid_deg((unsigned)xcd_grid((int)((A.n_edges + kT - 1) / kT)));
   if (D) {
-    hipLaunchKernelGGL(k_mlp_bwd_deg, grid, dim3(256), mlp_lds_bwd(), s, A, dd, accumulate, *D, g0);
+    hipLaunchKernelGGL(k_mlp_bwd_deg, grid_deg, dim3(256), mlp_lds_bwd(), s, A, dd, accumulate, *D, g0);
     E2V2_LAUNCHED("k_mlp_bwd_deg");
   } else {
     hipLaunchKernelGGL(k_mlp_bwd, grid, dim3(256), mlp_lds_bwd(), s, A, dout, ld_dout, dd, accumulate);
