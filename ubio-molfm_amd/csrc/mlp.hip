@@ -50,25 +50,47 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // afn(k, a0, a1) supplies A[l%16][k] and A[16 + l%16][k] for this lane's
 // k = 4 s + l/16 of k-step s.  B is streamed in chunks of 32 k-rows held in
 // registers one chunk ahead (the fp32 MFMA time per chunk covers the load).
+// The first B chunk of a GEMM, loaded ahead (before the stage that precedes the
+// GEMM) so that its L2 round trip overlaps that stage.
+template <int N>
+struct BChunk {
+  float v[N > 128 ? kPFWide : kPFNarrow][N / 64];
+};
+
+template <int N>
+__device__ __forceinline__ const float* b_lane_ptr(const float* __restrict__ B, int ldb) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  return B + (size_t)(lane >> 4) * ldb + wave * (N / 4) + (lane & 15);
+}
+
+template <int N>
+__device__ __forceinline__ void load_first_chunk(const float* __restrict__ B, int ldb, BChunk<N>& c) {
+  constexpr int kPF = N > 128 ? kPFWide : kPFNarrow;
+  const float* Bp = b_lane_ptr<N>(B, ldb);
+#pragma unroll
+  for (int s = 0; s < kPF; ++s)
+#pragma unroll
+    for (int ct = 0; ct < N / 64; ++ct) c.v[s][ct] = Bp[(size_t)(4 * s) * ldb + ct * 16];
+}
+
 template <int K, int N, typename AFn>
-__device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, int ldb, floatx4 (&acc)[2][N / 64]) {
+__device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, int ldb, const BChunk<N>& first,
+                                        floatx4 (&acc)[2][N / 64]) {
   constexpr int CT = N / 64;
   constexpr int kPF = N > 128 ? kPFWide : kPFNarrow;   // B registers per chunk: kPF * CT
   constexpr int NCH = K / (4 * kPF);
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int li = lane & 15, lk = lane >> 4;
-  const int cbase = wave * (N / 4);
+  const int lk = lane >> 4;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const float* Bp = B + (size_t)lk * ldb + cbase + li;
+  const float* Bp = b_lane_ptr<N>(B, ldb);
   float bc[kPF][CT], bn[kPF][CT];
 #pragma unroll
   for (int s = 0; s < kPF; ++s)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) bc[s][ct] = Bp[(size_t)(4 * s) * ldb + ct * 16];
+    for (int ct = 0; ct < CT; ++ct) bc[s][ct] = first.v[s][ct];
   __builtin_amdgcn_s_setprio(1);   // MFMA-ready waves issue ahead of epilogue work of other waves
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
@@ -98,14 +120,14 @@ __device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, in
   __builtin_amdgcn_s_setprio(0);
 }
 
-// A from an LDS tile with row stride lda
+// A from an LDS tile with row stride lda; the first B chunk already loaded
 template <int K, int N>
 __device__ __forceinline__ void gemm32(const float* A, int lda, const float* __restrict__ B, int ldb,
-                                       floatx4 (&acc)[2][N / 64]) {
+                                       const BChunk<N>& first, floatx4 (&acc)[2][N / 64]) {
   const int li = threadIdx.x & 15;
   const float* A0 = A + li * lda;
   const float* A1 = A + (16 + li) * lda;
-  gemm32f<K, N>([&](int k, float& a0, float& a1) { a0 = A0[k]; a1 = A1[k]; }, B, ldb, acc);
+  gemm32f<K, N>([&](int k, float& a0, float& a1) { a0 = A0[k]; a1 = A1[k]; }, B, ldb, first, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -539,14 +561,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   load_bias<256>(W.b3, b3);
   load_tile_edges(A, e0, te);
   load_ln_params(W, lp);
+  BChunk<kH> f2;
+  load_first_chunk<kH>(W.w2t, kH, f2);      // in flight during Linear1 and LayerNorm 1
   __syncthreads();
   linear1_rows(W, te, Y, kLdY);
   __syncthreads();
   ln_silu_rows(Y, kLdY, Y, kLdY, lp.g1, lp.b1, sn, 2 * kH, sr, 2, nvalid);
   __syncthreads();
+  BChunk<256> f3;
   {
     floatx4 acc[2][2];
-    gemm32<kH, kH>(Y, kLdY, W.w2t, kH, acc);
+    gemm32<kH, kH>(Y, kLdY, W.w2t, kH, f2, acc);
+    load_first_chunk<256>(W.w3t, 256, f3);  // in flight during LayerNorm 2
     __syncthreads();
     store_acc<kH>(acc, Y, kLdY, b2);
   }
@@ -554,7 +580,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   ln_silu_rows(Y, kLdY, Y, kLdY, lp.g2, lp.b2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2, nvalid);
   __syncthreads();
   floatx4 acc[2][4];
-  gemm32<kH, 256>(Y, kLdY, W.w3t, 256, acc);
+  gemm32<kH, 256>(Y, kLdY, W.w3t, 256, f3, acc);
   __syncthreads();
   store_out(acc, b3, sm, out, ld_out, e0, nvalid, m);
 }
@@ -586,6 +612,8 @@ __device__ __forceinline__ void mlp_bwd_body(e2v2_mlp_args A, const float* __res
     const float* sn = A.save_n + ((size_t)m * A.n_edges + e0) * (2 * kH);
     const float* srs = A.save_r + ((size_t)m * A.n_edges + e0) * 2;
     load_ln_params(W, lp);
+    BChunk<kH> fa;
+    load_first_chunk<kH>(W.w3, kH, fa);       // in flight during the dOut tile load
     for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {   // dOut tile, 16-byte loads
       const int row = idx >> 6, c4 = idx & 63;
       const floatx4 v = dout4<kDeg>(dout, ld_dout, e0, row, nvalid, m, c4, g0, D.n_rows, dt);
@@ -595,9 +623,11 @@ __device__ __forceinline__ void mlp_bwd_body(e2v2_mlp_args A, const float* __res
     SavedRow s2;
     load_saved_row(sn + kH, 2 * kH, srs + 1, 2, nvalid, s2);
     __syncthreads();
+    BChunk<kH> fb;
     {  // dy2 = dOut . W3   (W3 [256][128] row-major = B[K=256][N=128])
       floatx4 acc[2][2];
-      gemm32<256, kH>(X, kLdX, W.w3, kH, acc);
+      gemm32<256, kH>(X, kLdX, W.w3, kH, fa, acc);
+      load_first_chunk<kH>(W.w2, kH, fb);     // in flight during the LayerNorm-2 backward
       __syncthreads();
       store_acc<kH>(acc, Y, kLdY, zero2);
     }
@@ -608,7 +638,7 @@ __device__ __forceinline__ void mlp_bwd_body(e2v2_mlp_args A, const float* __res
     __syncthreads();
     {  // dy1 = dz2 . W2   (W2 [128][128])
       floatx4 acc[2][2];
-      gemm32<kH, kH>(Y, kLdY, W.w2, kH, acc);
+      gemm32<kH, kH>(Y, kLdY, W.w2, kH, fb, acc);
       __syncthreads();
       store_acc<kH>(acc, Y, kLdY, zero2);
     }
