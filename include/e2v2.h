@@ -245,6 +245,13 @@ int e2v2_gate_bwd(const float* sc, const float* x, const float* gy, float* gsc, 
  * y [9][N][4 hid] = (q_a | q_b | k_a | k_b) -> hq, hk [N][3 hid], h[l hid + c] = sum_{m in l} a b */
 int e2v2_pairdot_fwd(const float* y, float* hq, float* hk, int n, int hid, hipStream_t s);
 int e2v2_pairdot_bwd(const float* y, const float* ghq, const float* ghk, float* gy, int n, int hid, hipStream_t s);
+/* y = silu(LayerNorm(x) * g + b) on rows x [n][w] (w % 64 == 0, w <= 1024), the LayerNorm + SiLU of the
+   Q/K head (final_linear of SO3_Linear2Scalar_e2former, module_utils.py:2230-2233,2268); stats [n][2] =
+   (mean, rstd) kept for the backward, which returns the input gradient only. */
+int e2v2_ln_silu_fwd(const float* x, const float* g, const float* b, float* y, float* stats, int n, int w, float eps,
+                     hipStream_t s);
+int e2v2_ln_silu_bwd(const float* x, const float* g, const float* b, const float* stats, const float* gy, float* gx,
+                     int n, int w, hipStream_t s);
 
 /* ---- positions --------------------------------------------------------- */
 int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,

@@ -358,6 +358,30 @@ def test_edge_to_pos(pkg, cuda):
     assert e < 1e-5
 
 
+@pytest.mark.parametrize("n,w", [(37, 512), (8, 128), (1, 1024)])
+def test_ln_silu(pkg, cuda, n, w):
+    """LayerNorm + SiLU of the Q/K head (LNSiLUFn) against float64 torch: forward
+    and input gradient within 2e-6 relative; rows not a multiple of the four
+    rows per workgroup."""
+    from ubio_molfm_amd import modules
+    torch.manual_seed(3)
+    x = torch.randn(n, w, dtype=torch.float64) * 2.0 + 0.5
+    ln = torch.nn.LayerNorm(w).double()
+    ln.weight.data.uniform_(0.5, 1.5); ln.bias.data.uniform_(-0.3, 0.3)
+    xl = x.clone().requires_grad_(True)
+    yr = torch.nn.functional.silu(ln(xl))
+    G = torch.randn_like(yr)
+    gr = torch.autograd.grad((yr * G).sum(), xl)[0]
+    lnd = torch.nn.LayerNorm(w).to(cuda)
+    lnd.load_state_dict({k: v.float() for k, v in ln.state_dict().items()})
+    xd = x.float().to(cuda).requires_grad_(True)
+    yd = modules._ln_silu(xd, lnd)
+    gd = torch.autograd.grad((yd * G.float().to(cuda)).sum(), xd)[0]
+    ef, eb = relerr(yd, yr), relerr(gd, gr)
+    print(f"[ln-silu {n}x{w}] fwd {ef:.2e} bwd {eb:.2e}", flush=True)
+    assert ef < 2e-6 and eb < 2e-6
+
+
 def test_node_kernels_rmsnorm_gate(pkg, cuda):
     """HIP rms_norm_sh and Gate_s3 (m-major) vs the oracle's torch modules."""
     from ubio_molfm_amd import modules

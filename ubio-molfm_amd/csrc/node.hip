@@ -267,3 +267,103 @@ E2V2_API int e2v2_pairdot_bwd(const float* y, const float* ghq, const float* ghk
   E2V2_LAUNCHED("k_pairdot_bwd");
   return 0;
 }
+
+// ---- LayerNorm + SiLU of the Q/K head (final_linear of SO3_Linear2Scalar_e2former,
+// module_utils.py:2230-2233,2268): y = silu(LN(x) * g + b) on rows x[N][w], one
+// wavefront per row (w a multiple of 64, at most 1024: w / 64 values per lane).
+// The forward keeps (mean, rstd) per row; the backward recomputes the rest.
+namespace e2v2 {
+constexpr int kLnMaxPerLane = 16;
+
+__global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ x, const float* __restrict__ g,
+                                                     const float* __restrict__ b, float* __restrict__ y,
+                                                     float* __restrict__ stats, int n, int w, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (row >= n) return;
+  const int nq = w >> 6;
+  const float* xr = x + (size_t)row * w;
+  float v[kLnMaxPerLane];
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < kLnMaxPerLane; ++q) {
+    v[q] = q < nq ? xr[q * 64 + lane] : 0.f;
+    s += v[q];
+  }
+  const float mean = wave_sum(s) / (float)w;
+  float s2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < kLnMaxPerLane; ++q) {
+    const float d = q < nq ? v[q] - mean : 0.f;
+    s2 = fmaf(d, d, s2);
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(s2) / (float)w + eps);
+  float* yr = y + (size_t)row * w;
+#pragma unroll
+  for (int q = 0; q < kLnMaxPerLane; ++q) {
+    if (q < nq) {
+      const int c = q * 64 + lane;
+      const float a = (v[q] - mean) * rstd * g[c] + b[c];
+      yr[c] = a / (1.0f + expf(-a));
+    }
+  }
+  if (lane == 0) {
+    stats[2 * (size_t)row] = mean;
+    stats[2 * (size_t)row + 1] = rstd;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ x, const float* __restrict__ g,
+                                                     const float* __restrict__ b, const float* __restrict__ stats,
+                                                     const float* __restrict__ gy, float* __restrict__ gx, int n,
+                                                     int w) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (row >= n) return;
+  const int nq = w >> 6;
+  const float mean = stats[2 * (size_t)row], rstd = stats[2 * (size_t)row + 1];
+  const float* xr = x + (size_t)row * w;
+  const float* gr = gy + (size_t)row * w;
+  float nv[kLnMaxPerLane], dn[kLnMaxPerLane];
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < kLnMaxPerLane; ++q) {
+    nv[q] = 0.f;
+    dn[q] = 0.f;
+    if (q < nq) {
+      const int c = q * 64 + lane;
+      nv[q] = (xr[c] - mean) * rstd;
+      const float a = nv[q] * g[c] + b[c];
+      const float sg = 1.0f / (1.0f + expf(-a));
+      dn[q] = gr[c] * sg * (1.0f + a * (1.0f - sg)) * g[c];
+      s1 += dn[q];
+      s2 = fmaf(dn[q], nv[q], s2);
+    }
+  }
+  const float m1 = wave_sum(s1) / (float)w, m2 = wave_sum(s2) / (float)w;
+  float* o = gx + (size_t)row * w;
+#pragma unroll
+  for (int q = 0; q < kLnMaxPerLane; ++q)
+    if (q < nq) o[q * 64 + lane] = rstd * (dn[q] - m1 - nv[q] * m2);
+}
+}  // namespace e2v2
+
+E2V2_API int e2v2_ln_silu_fwd(const float* x, const float* g, const float* b, float* y, float* stats, int n, int w,
+                              float eps, hipStream_t s) {
+  E2V2_REQUIRE(w > 0 && w % 64 == 0 && w <= 64 * e2v2::kLnMaxPerLane, "ln_silu_fwd: width %d", w);
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(e2v2::k_ln_silu_fwd, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, x, g, b, y, stats, n, w,
+                     eps);
+  E2V2_LAUNCHED("k_ln_silu_fwd");
+  return 0;
+}
+
+E2V2_API int e2v2_ln_silu_bwd(const float* x, const float* g, const float* b, const float* stats, const float* gy,
+                              float* gx, int n, int w, hipStream_t s) {
+  E2V2_REQUIRE(w > 0 && w % 64 == 0 && w <= 64 * e2v2::kLnMaxPerLane, "ln_silu_bwd: width %d", w);
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(e2v2::k_ln_silu_bwd, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, x, g, b, stats, gy, gx, n,
+                     w);
+  E2V2_LAUNCHED("k_ln_silu_bwd");
+  return 0;
+}

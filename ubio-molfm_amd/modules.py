@@ -332,6 +332,37 @@ class AddRMSNormFn(torch.autograd.Function):
         return gx, (gx if ctx.has_delta else None), None, None, None
 
 
+class LNSiLUFn(torch.autograd.Function):
+    """silu(LayerNorm(x)) on rows x [N, w] (the LayerNorm + SiLU of the Q/K head,
+    module_utils.py:2230-2233) through e2v2_ln_silu_fwd/bwd; the LayerNorm
+    affine parameters are constants (input gradient only)."""
+
+    @staticmethod
+    def forward(ctx, x, g, b, eps: float):
+        x = x.contiguous()
+        n, w = x.shape
+        y = torch.empty_like(x)
+        st = x.new_empty(n, 2)
+        _lib.call("e2v2_ln_silu_fwd", _dp(x), _dp(g), _dp(b), _dp(y), _dp(st), _lib.i32(n), _lib.i32(w),
+                  _lib.f32(eps), _stream())
+        ctx.save_for_backward(x, g, b, st)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, g, b, st = ctx.saved_tensors
+        gy = gy.contiguous()
+        gx = torch.empty_like(x)
+        _lib.call("e2v2_ln_silu_bwd", _dp(x), _dp(g), _dp(b), _dp(st), _dp(gy), _dp(gx), _lib.i32(x.shape[0]),
+                  _lib.i32(x.shape[1]), _stream())
+        return gx, None, None, None
+
+
+def _ln_silu(x, ln: nn.LayerNorm):
+    return LNSiLUFn.apply(x, ln.weight.detach().float().contiguous(), ln.bias.detach().float().contiguous(),
+                          float(ln.eps))
+
+
 class GateFn(torch.autograd.Function):
     """Gate_s3: sc = x[0] Wg^T + bg, then the activation kernel on x[9][N][C]."""
 
@@ -470,10 +501,9 @@ class SO3_Linear2Scalar_e2former(nn.Module):
         """final_linear on the m-contracted products h [N, (lmax+1) hid]."""
         fl = self.final_linear
         if not bf16:
-            h = torch.nn.functional.silu(_layer_norm(_linear(h, fl[0]), fl[1]))
-            return _linear(h, fl[3])
+            return _linear(_ln_silu(_linear(h, fl[0]), fl[1]), fl[3])
         h = DenseFn.apply(h, gemm_weight(fl[0], "weight", True), fl[0].bias.detach())
-        h = torch.nn.functional.silu(_layer_norm(h, fl[1]))
+        h = _ln_silu(h, fl[1])
         return DenseFn.apply(h, gemm_weight(fl[3], "weight", True), fl[3].bias.detach())
 
     def forward(self, x):
