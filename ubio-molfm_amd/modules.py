@@ -99,6 +99,42 @@ def gemm_weight(mod, name: str, bf16: bool):
     return cached(mod, name + "_bf16", (p,), lambda: p.detach().to(BF16).contiguous())
 
 
+class MRowWeight:
+    """Per-l weight W [lmax+1, O, Cin] of an SO(3) linear as GEMM operands: ``w``
+    for per-l GEMMs (fp32, or a bf16 copy), and in fp32 its per-m-row expansions
+    for one batched GEMM over the (lmax+1)^2 m-rows (one launch instead of lmax+1,
+    fewer partial tiles): ``fwd`` [M, Cin, O] and ``bwd`` [M, O, Cin]."""
+    __slots__ = ("w", "fwd", "bwd")
+
+    def __init__(self, w, fwd=None, bwd=None):
+        self.w, self.fwd, self.bwd = w, fwd, bwd
+
+
+def _m_index(lmax: int, device):
+    return torch.tensor([l for l in range(lmax + 1) for _ in range(2 * l + 1)], device=device)
+
+
+def mrow_weight(owner, name: str, w, bf16: bool, lmax: int):
+    """MRowWeight of the weight tensor w (a parameter of ``owner`` or a tensor built
+    from its parameters; cached under ``name`` until w changes)."""
+    if bf16:
+        return cached(owner, name + "_mrow_bf16", (w,), lambda: MRowWeight(w.detach().to(BF16).contiguous()))
+
+    def build():
+        wd = w.detach()
+        e = wd[_m_index(lmax, wd.device)]
+        return MRowWeight(wd, e.transpose(1, 2).contiguous(), e.contiguous())
+    return cached(owner, name + "_mrow", (w,), build)
+
+
+def _mrow_gemm(x, Wop: MRowWeight, bias):
+    """y[m] = x[m] W_l(m)^T (+ bias on row 0) for x [M, N, Cin] (fp32, batched)."""
+    y = torch.bmm(x, Wop.fwd)
+    if bias is not None:
+        y[0].add_(bias)
+    return y
+
+
 class SO3LinearFn(torch.autograd.Function):
     """y[rows(l)] = res[rows(l)] + x[rows(l)] W_l^T (+ bias on row 0) on the
     m-major layout x[(lmax+1)^2, N, Cin]: each l block is one 2-D GEMM written in
@@ -106,8 +142,12 @@ class SO3LinearFn(torch.autograd.Function):
     gradients only)."""
 
     @staticmethod
-    def forward(ctx, x, W, bias, lmax: int, res=None):
+    def forward(ctx, x, Wop, bias, lmax: int, res=None):
         x = x.contiguous()
+        ctx.Wop, ctx.lmax, ctx.has_res = Wop, lmax, res is not None
+        if Wop.fwd is not None and res is None:
+            return _mrow_gemm(x, Wop, bias)
+        W = Wop.w
         L2, N, Cin = x.shape
         O = W.shape[1]
         y = x.new_empty(L2, N, O)
@@ -124,15 +164,15 @@ class SO3LinearFn(torch.autograd.Function):
                 _mm_into(xa[a:b].view(-1, Cin), W[l].t(), out=y[a:b].view(-1, O))
         if bias is not None and res is not None:
             y[0].add_(bias)
-        ctx.save_for_backward(W)
-        ctx.lmax = lmax
-        ctx.has_res = res is not None
         return y
 
     @staticmethod
     def backward(ctx, gy):
-        (W,) = ctx.saved_tensors
+        Wop = ctx.Wop
         gy = gy.contiguous()
+        if Wop.bwd is not None:
+            return torch.bmm(gy, Wop.bwd), None, None, None, (gy if ctx.has_res else None)
+        W = Wop.w
         L2, N, O = gy.shape
         Cin = W.shape[2]
         gx = gy.new_empty(L2, N, Cin)
@@ -148,58 +188,77 @@ class QKProjFn(torch.autograd.Function):
     m-contraction: x[9][N][C] -> hq, hk [N][3 hid] (before final_linear)."""
 
     @staticmethod
-    def forward(ctx, x, W, bias, lmax: int, hid: int, Wv=None, bv=None):
-        """With the value projection's weight Wv [lmax+1, Cv, C] and bias bv it
-        also returns v = SO3_Linear(x) [9, N, Cv] (else None), so that the
-        backward sums the two input gradients inside the GEMMs."""
+    def forward(ctx, x, Wop, bias, lmax: int, hid: int, Wvop=None, bv=None):
+        """Wop, Wvop: MRowWeight.  With the value projection's weight Wvop
+        ([lmax+1, Cv, C]) and bias bv it also returns v = SO3_Linear(x) [9, N, Cv]
+        (else None), so that the backward sums the two input gradients inside the
+        GEMMs."""
         x = x.contiguous()
         L2, N, C = x.shape
-        y = x.new_empty(L2, N, 4 * hid)
-        xa = _bf(x) if W.dtype == BF16 else x
-        for l in range(lmax + 1):
-            a, b = l * l, (l + 1) ** 2
-            if l == 0:
-                _mm_bias_into(xa[0], W[0].t(), bias, out=y[0])
-            else:
-                _mm_into(xa[a:b].view(-1, C), W[l].t(), out=y[a:b].view(-1, 4 * hid))
-        hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
-        _lib.call("e2v2_pairdot_fwd", _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _stream())
-        v = None
-        if Wv is not None:
-            Cv = Wv.shape[1]
-            v = x.new_empty(L2, N, Cv)
-            xv = _bf(x) if Wv.dtype == BF16 else x
+        W = Wop.w
+        if Wop.fwd is not None:
+            y = _mrow_gemm(x, Wop, bias)
+        else:
+            y = x.new_empty(L2, N, 4 * hid)
+            xa = _bf(x) if W.dtype == BF16 else x
             for l in range(lmax + 1):
                 a, b = l * l, (l + 1) ** 2
                 if l == 0:
-                    _mm_bias_into(xv[0], Wv[0].t(), bv, out=v[0])
+                    _mm_bias_into(xa[0], W[0].t(), bias, out=y[0])
                 else:
-                    _mm_into(xv[a:b].view(-1, C), Wv[l].t(), out=v[a:b].view(-1, Cv))
-        ctx.save_for_backward(y, W, Wv)
+                    _mm_into(xa[a:b].view(-1, C), W[l].t(), out=y[a:b].view(-1, 4 * hid))
+        hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
+        _lib.call("e2v2_pairdot_fwd", _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _stream())
+        v = None
+        if Wvop is not None:
+            Wv = Wvop.w
+            Cv = Wv.shape[1]
+            if Wvop.fwd is not None:
+                v = _mrow_gemm(x, Wvop, bv)
+            else:
+                v = x.new_empty(L2, N, Cv)
+                xv = _bf(x) if Wv.dtype == BF16 else x
+                for l in range(lmax + 1):
+                    a, b = l * l, (l + 1) ** 2
+                    if l == 0:
+                        _mm_bias_into(xv[0], Wv[0].t(), bv, out=v[0])
+                    else:
+                        _mm_into(xv[a:b].view(-1, C), Wv[l].t(), out=v[a:b].view(-1, Cv))
+        ctx.save_for_backward(y)
+        ctx.Wop, ctx.Wvop = Wop, Wvop
         ctx.lmax, ctx.hid = lmax, hid
         return hq, hk, v
 
     @staticmethod
     def backward(ctx, ghq, ghk, gv):
-        y, W, Wv = ctx.saved_tensors
+        (y,) = ctx.saved_tensors
+        Wop, Wvop = ctx.Wop, ctx.Wvop
         L2, N, F = y.shape
         hid = ctx.hid
         ghq = torch.zeros(N, 3 * hid, device=y.device) if ghq is None else ghq.contiguous()
         ghk = torch.zeros(N, 3 * hid, device=y.device) if ghk is None else ghk.contiguous()
         gy = torch.empty_like(y)
         _lib.call("e2v2_pairdot_bwd", _dp(y), _dp(ghq), _dp(ghk), _dp(gy), _lib.i32(N), _lib.i32(hid), _stream())
+        W = Wop.w
         C = W.shape[2]
-        gx = y.new_empty(L2, N, C)
-        ga = _bf(gy) if W.dtype == BF16 else gy
-        for l in range(ctx.lmax + 1):
-            a, b = l * l, (l + 1) ** 2
-            _mm_into(ga[a:b].view(-1, F), W[l], out=gx[a:b].view(-1, C))
-        if Wv is not None and gv is not None:
-            gv = gv.contiguous()
-            Cv = Wv.shape[1]
+        if Wop.bwd is not None:
+            gx = torch.bmm(gy, Wop.bwd)
+        else:
+            gx = y.new_empty(L2, N, C)
+            ga = _bf(gy) if W.dtype == BF16 else gy
             for l in range(ctx.lmax + 1):
                 a, b = l * l, (l + 1) ** 2
-                _addmm_into(gx[a:b].view(-1, C), gv[a:b].view(-1, Cv), Wv[l], out=gx[a:b].view(-1, C))
+                _mm_into(ga[a:b].view(-1, F), W[l], out=gx[a:b].view(-1, C))
+        if Wvop is not None and gv is not None:
+            gv = gv.contiguous()
+            if Wvop.bwd is not None:
+                gx.baddbmm_(gv, Wvop.bwd)
+            else:
+                Wv = Wvop.w
+                Cv = Wv.shape[1]
+                for l in range(ctx.lmax + 1):
+                    a, b = l * l, (l + 1) ** 2
+                    _addmm_into(gx[a:b].view(-1, C), gv[a:b].view(-1, Cv), Wv[l], out=gx[a:b].view(-1, C))
         return gx, None, None, None, None, None, None
 
 
@@ -210,9 +269,10 @@ class SO2OutFn(torch.autograd.Function):
     e2former.py:215-219,433)."""
 
     @staticmethod
-    def forward(ctx, so2, res, blocks, Wp, bp):
+    def forward(ctx, so2, res, blocks, Wpop, bp):
         so2 = so2.contiguous()
         res = None if res is None else res.contiguous()
+        Wp = Wpop.w
         _, N, C = so2.shape
         t = so2.new_empty(9, N, C, dtype=torch.float32)
         sa = _bf(so2) if Wp.dtype == BF16 else so2
@@ -227,37 +287,43 @@ class SO2OutFn(torch.autograd.Function):
                 else:
                     _addmm_into(tv, xin, Wt, out=tv)
             o += nr
-        y = so2.new_empty(9, N, Wp.shape[1], dtype=torch.float32)
-        ta = _bf(t) if Wp.dtype == BF16 else t
         O = Wp.shape[1]
-        for l in range(3):
-            a, b = l * l, (l + 1) ** 2
+        if Wpop.fwd is not None and res is None:
+            y = _mrow_gemm(t, Wpop, bp)
+        else:
+            y = so2.new_empty(9, N, O, dtype=torch.float32)
+            ta = _bf(t) if Wp.dtype == BF16 else t
+            for l in range(3):
+                a, b = l * l, (l + 1) ** 2
+                if res is not None:
+                    _addmm_into(res[a:b].view(-1, O), ta[a:b].view(-1, C), Wp[l].t(), out=y[a:b].view(-1, O))
+                elif l == 0:
+                    _mm_bias_into(ta[0], Wp[0].t(), bp, out=y[0])
+                else:
+                    _mm_into(ta[a:b].view(-1, C), Wp[l].t(), out=y[a:b].view(-1, O))
             if res is not None:
-                _addmm_into(res[a:b].view(-1, O), ta[a:b].view(-1, C), Wp[l].t(), out=y[a:b].view(-1, O))
-            elif l == 0:
-                _mm_bias_into(ta[0], Wp[0].t(), bp, out=y[0])
-            else:
-                _mm_into(ta[a:b].view(-1, C), Wp[l].t(), out=y[a:b].view(-1, O))
-        if res is not None:
-            y[0].add_(bp)
+                y[0].add_(bp)
         ctx.has_res = res is not None
-        ctx.blocks = blocks
-        ctx.save_for_backward(Wp)
+        ctx.blocks, ctx.Wpop = blocks, Wpop
         ctx.shape, ctx.so2_dtype = so2.shape, so2.dtype
         return y
 
     @staticmethod
     def backward(ctx, gy):
-        (Wp,) = ctx.saved_tensors
+        Wpop = ctx.Wpop
+        Wp = Wpop.w
         gy = gy.contiguous()
         _, N, O = gy.shape
         C = Wp.shape[2]
-        gt = gy.new_empty(9, N, C)
         bf = Wp.dtype == BF16
-        ga = _bf(gy) if bf else gy
-        for l in range(3):
-            a, b = l * l, (l + 1) ** 2
-            _mm_into(ga[a:b].view(-1, O), Wp[l], out=gt[a:b].view(-1, C))
+        if Wpop.bwd is not None:
+            gt = torch.bmm(gy, Wpop.bwd)
+        else:
+            gt = gy.new_empty(9, N, C)
+            ga = _bf(gy) if bf else gy
+            for l in range(3):
+                a, b = l * l, (l + 1) ** 2
+                _mm_into(ga[a:b].view(-1, O), Wp[l], out=gt[a:b].view(-1, C))
         gso2 = gy.new_empty(ctx.shape, dtype=ctx.so2_dtype)
         gta = _bf(gt) if bf else gt
         o = 0
@@ -470,7 +536,8 @@ class SO3_Linear_e2former(nn.Module):
         self.register_buffer("expand_index", _expand_index(lmax), persistent=False)
 
     def forward(self, x, bf16: bool = False):
-        return SO3LinearFn.apply(x, gemm_weight(self, "weight", bf16), self.bias.detach(), self.lmax)
+        return SO3LinearFn.apply(x, mrow_weight(self, "weight", self.weight, bf16, self.lmax), self.bias.detach(),
+                                 self.lmax)
 
 
 class SO3_Linear2Scalar_e2former(nn.Module):
@@ -510,7 +577,7 @@ class SO3_Linear2Scalar_e2former(nn.Module):
         w, b = self.stacked()
         hid = self.weight.shape[1]
         # the pair kernel contracts (q_a, q_b) and (k_a, k_b); feed this product twice
-        hq, _, _ = QKProjFn.apply(x, torch.cat([w, w], dim=1), torch.cat([b, b]), self.lmax, hid)
+        hq, _, _ = QKProjFn.apply(x, MRowWeight(torch.cat([w, w], dim=1)), torch.cat([b, b]), self.lmax, hid)
         return self.head(hq)
 
 
@@ -572,7 +639,8 @@ class FeedForwardNetwork_s3(nn.Module):
     def forward(self, x, res=None, bf16: bool = False, **kw):
         h = self.gate(self.slinear_1(x, bf16), bf16)
         s2 = self.slinear_2
-        return SO3LinearFn.apply(h, gemm_weight(s2, "weight", bf16), s2.bias.detach(), s2.lmax, res)
+        return SO3LinearFn.apply(h, mrow_weight(s2, "weight", s2.weight, bf16, s2.lmax), s2.bias.detach(), s2.lmax,
+                                 res)
 
 
 class sph_fromxyz(nn.Module):
@@ -744,9 +812,10 @@ class E2AttentionArbOrder_sparse(nn.Module):
         def build():
             wq, bq = self.query_linear.stacked()
             wk, bk = self.key_linear.stacked()
-            w = torch.cat([wq, wk], dim=1)
-            return ((w.to(BF16) if bf16 else w).contiguous(), torch.cat([bq, bk]).float().contiguous())
-        return cached(self, "qk_bf16" if bf16 else "qk", params, build)
+            w = torch.cat([wq, wk], dim=1).contiguous()
+            return w, torch.cat([bq, bk]).float().contiguous()
+        w, b = cached(self, "qk", params, build)
+        return mrow_weight(self, "qk", w, bf16, self.lmax), b
 
     def forward(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
         """x [9, N, C] (m-major) -> attention(x) (+ res when given), [9, N, C]."""
@@ -758,7 +827,8 @@ class E2AttentionArbOrder_sparse(nn.Module):
         W, b = self.qk_weights(bf16)
         hid = self.query_linear.weight.shape[1]
         pv = self.proj_value  # its GEMMs run inside QKProjFn (one input gradient)
-        hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, gemm_weight(pv, "weight", bf16), pv.bias.detach())
+        hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight", pv.weight, bf16, pv.lmax),
+                                   pv.bias.detach())
         q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
         k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding, ctx.rbf_offset,
@@ -767,7 +837,7 @@ class E2AttentionArbOrder_sparse(nn.Module):
                                 packed, ctx.rc, math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
         pf = self.proj_first
         return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16),
-                              gemm_weight(pf, "weight", bf16), pf.bias.detach())
+                              mrow_weight(pf, "weight", pf.weight, bf16, pf.lmax), pf.bias.detach())
 
 
 class TransBlock(nn.Module):
