@@ -95,6 +95,12 @@ int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, int64_t n_e
 int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* cnt, int32_t* new_ptr, int32_t* stats,
                   const int32_t* col, const int32_t* shift, const float* dvec, const float* dist,
                   int32_t* ocol, int32_t* oshift, float* odv, float* od, int phase, hipStream_t s);
+/* 30-bit Morton (Z-order) keys of atoms within their graph's bounding box, for the spatial
+   ordering of the rows: key[i] = g << 32 | interleave(q) with q = clamp((pos - lo[g]) / span[g]
+   * 1023, 0, 1023) truncated; gid [n] the graph of each atom (NULL: one graph), lo/span [B][3].
+   No reference counterpart: the row order that keeps a workgroup's neighbours in one L2. */
+int e2v2_morton_keys(const float* pos, const int32_t* gid, const float* lo, const float* span, int n, int64_t* key,
+                     hipStream_t s);
 /* Clusters of `span` (1..8) consecutive segments of a CSR: seg_ptr = row_ptr with member = col and
    item_eid = NULL (query rows), or seg_ptr = key_ptr with member = edge_row and item_eid = key_eid (key
    columns).  Every distinct (member atom, occurrence) of a cluster becomes one slot, sorted by atom:

@@ -527,6 +527,33 @@ static inline int seg_cap(int n) {
 }
 static inline size_t seg_lds_bytes(int cap) { return (size_t)cap * (sizeof(uint64_t) + sizeof(int32_t)); }
 
+// 30-bit Morton (Z-order) key of each atom within its graph's bounding box:
+// key = graph << 32 | interleave(q_x, q_y, q_z), q = clamp((pos - lo) / span * 1023, 0, 1023)
+// truncated, graphs given by gid (NULL: one graph).
+__device__ __forceinline__ uint64_t spread_bits10(uint64_t v) {
+  v &= 0x3FF;
+  v = (v | (v << 16)) & 0x030000FF;
+  v = (v | (v << 8)) & 0x0300F00F;
+  v = (v | (v << 4)) & 0x030C30C3;
+  v = (v | (v << 2)) & 0x09249249;
+  return v;
+}
+
+__global__ void k_morton_keys(const float* __restrict__ pos, const int32_t* __restrict__ gid,
+                              const float* __restrict__ lo, const float* __restrict__ span, int n,
+                              uint64_t* __restrict__ key) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int g = gid ? gid[i] : 0;
+  uint64_t code = 0;
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    const float u = (pos[3 * i + d] - lo[3 * g + d]) / span[3 * g + d] * 1023.0f;
+    code |= spread_bits10((uint64_t)fminf(fmaxf(u, 0.0f), 1023.0f)) << d;
+  }
+  key[i] = ((uint64_t)(uint32_t)g << 32) | code;
+}
+
 static inline unsigned blocks_for(int64_t n, int bs) {
   int64_t b = (n + bs - 1) / bs;
   return (unsigned)(b < 1 ? 1 : (b > 1048576 ? 1048576 : b));
@@ -620,6 +647,16 @@ E2V2_API int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* c
   hipLaunchKernelGGL(k_topk_compact, dim3(n_rows), dim3(128), 0, s, row_ptr, new_ptr, n_rows, col, shift, dvec, dist,
                      ocol, oshift, odv, od);
   E2V2_LAUNCHED("k_topk_compact");
+  return 0;
+}
+
+E2V2_API int e2v2_morton_keys(const float* pos, const int32_t* gid, const float* lo, const float* span, int n,
+                              int64_t* key, hipStream_t s) {
+  E2V2_REQUIRE(n >= 0, "morton_keys: negative count %d", n);
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_morton_keys, dim3(blocks_for(n, 256)), dim3(256), 0, s, pos, gid, lo, span, n,
+                     reinterpret_cast<uint64_t*>(key));
+  E2V2_LAUNCHED("k_morton_keys");
   return 0;
 }
 

@@ -20,18 +20,10 @@ import numpy as np
 import torch
 from torch import nn
 
+from . import _lib
 from .modules import E2former, EdgeContext, parse_irreps
 from .neighbors import build_neighbors
 from .ops import EdgeGeometryFn
-
-
-def _spread_bits10(v: torch.Tensor) -> torch.Tensor:
-    v = v & 0x3FF
-    v = (v | (v << 16)) & 0x030000FF
-    v = (v | (v << 8)) & 0x0300F00F
-    v = (v | (v << 4)) & 0x030C30C3
-    v = (v | (v << 2)) & 0x09249249
-    return v
 
 
 def graph_bounds(pos: torch.Tensor, counts: torch.Tensor):
@@ -53,17 +45,21 @@ def spatial_order(pos: torch.Tensor, graph_ptr) -> torch.Tensor:
         return torch.zeros(0, dtype=torch.long, device=pos.device)
     counts_np = np.diff(np.asarray(graph_ptr))
     B = len(counts_np)
+    pos = pos.detach().float().contiguous()
+    gid = None
     if B == 1:   # no host copies or syncs for a single graph
-        gid = torch.zeros(N, dtype=torch.long, device=pos.device)
         lo, hi = pos.amin(0, keepdim=True), pos.amax(0, keepdim=True)
     else:
         counts = torch.as_tensor(counts_np, device=pos.device)
-        gid = torch.repeat_interleave(torch.arange(B, device=pos.device), counts, output_size=N)
+        gid = torch.repeat_interleave(torch.arange(B, device=pos.device, dtype=torch.int32), counts,
+                                      output_size=N)
         lo, hi = graph_bounds(pos, counts)
-    span = (hi - lo).clamp_min(1e-6)
-    q = ((pos - lo[gid]) / span[gid] * 1023.0).clamp(0, 1023).to(torch.int64)
-    code = _spread_bits10(q[:, 0]) | (_spread_bits10(q[:, 1]) << 1) | (_spread_bits10(q[:, 2]) << 2)
-    key = (gid.to(torch.int64) << 32) | code
+    lo = lo.contiguous()
+    span = (hi - lo).clamp_min(1e-6).contiguous()
+    key = torch.empty(N, dtype=torch.int64, device=pos.device)
+    _lib.call("e2v2_morton_keys", _lib.vp(pos.data_ptr()), None if gid is None else _lib.vp(gid.data_ptr()),
+              _lib.vp(lo.data_ptr()), _lib.vp(span.data_ptr()), _lib.i32(N), _lib.vp(key.data_ptr()),
+              _lib.vp(torch.cuda.current_stream(pos.device).cuda_stream))
     return torch.sort(key, stable=True).indices
 
 
