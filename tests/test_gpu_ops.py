@@ -334,6 +334,39 @@ def test_degree_mlp_backward_fused(pkg, cuda, bf16):
     assert e_dd < (2e-3 if bf16 else 1e-5)
 
 
+def test_morton_keys(pkg, cuda):
+    """e2v2_morton_keys against a numpy restatement (fp32 quantisation, 10-bit
+    interleave), one graph and a ragged batch of three graphs."""
+    from ubio_molfm_amd import _lib
+
+    def spread(v):
+        v = v.astype(np.uint64) & np.uint64(0x3FF)
+        for sh, mask in ((16, 0x030000FF), (8, 0x0300F00F), (4, 0x030C30C3), (2, 0x09249249)):
+            v = (v | (v << np.uint64(sh))) & np.uint64(mask)
+        return v
+
+    rng = np.random.default_rng(3)
+    for counts in ([500], [7, 300, 41]):
+        n = sum(counts)
+        pos = (rng.normal(size=(n, 3)) * 5).astype(np.float32)
+        gid = np.repeat(np.arange(len(counts)), counts).astype(np.int32)
+        lo = np.stack([pos[gid == g].min(0) for g in range(len(counts))]).astype(np.float32)
+        hi = np.stack([pos[gid == g].max(0) for g in range(len(counts))]).astype(np.float32)
+        span = np.maximum(hi - lo, np.float32(1e-6)).astype(np.float32)
+        u = (pos - lo[gid]) / span[gid] * np.float32(1023.0)
+        q = np.clip(u, 0, 1023).astype(np.int64)
+        ref = (gid.astype(np.uint64) << np.uint64(32)) | spread(q[:, 0]) | (spread(q[:, 1]) << np.uint64(1)) \
+            | (spread(q[:, 2]) << np.uint64(2))
+        t = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=cuda)
+        pd, gd, ld, sd = t(pos), t(gid), t(lo), t(span)
+        key = torch.empty(n, dtype=torch.int64, device=cuda)
+        _lib.call("e2v2_morton_keys", _lib.vp(pd.data_ptr()), None if len(counts) == 1 else _lib.vp(gd.data_ptr()),
+                  _lib.vp(ld.data_ptr()), _lib.vp(sd.data_ptr()), _lib.i32(n), _lib.vp(key.data_ptr()),
+                  _lib.vp(torch.cuda.current_stream().cuda_stream))
+        got = key.cpu().numpy().view(np.uint64)
+        assert np.array_equal(got, ref), (counts, int((got != ref).sum()))
+
+
 def test_edge_to_pos(pkg, cuda):
     from ubio_molfm_amd import _lib
     s, pos, nl = _graph(pkg, cuda, seed=6)
