@@ -26,48 +26,52 @@ __device__ __forceinline__ void raw_sh2_bwd(float x, float y, float z, const flo
 
 __device__ __forceinline__ int l_of(int m) { return m == 0 ? 0 : (m < 4 ? 1 : 2); }
 
-__global__ __launch_bounds__(256) void k_deg_fwd(e2v2_deg_args A, float* __restrict__ x0) {
-  __shared__ float sh_s[32][9];
-  __shared__ float p_s[32];
-  __shared__ int64_t e_s[32];
-  const int i = xcd_row(blockIdx.x, A.n_rows), c = threadIdx.x;
+// One wavefront per query atom; lane owns channels 4 lane .. 4 lane + 3 (16-byte
+// loads of each edge's three feature rows); the edge's SH and envelope are
+// wave-uniform.
+constexpr int kDegWaves = 4;
+
+__global__ __launch_bounds__(64 * kDegWaves) void k_deg_fwd(e2v2_deg_args A, float* __restrict__ x0) {
+  const int w = (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int i = xcd_row(blockIdx.x, (A.n_rows + kDegWaves - 1) / kDegWaves) * kDegWaves + w;
   if (i >= A.n_rows) return;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   Envelope env;
   env.rc = A.rc; env.a = A.env_a; env.b = A.env_b; env.c = A.env_c;
-  float acc[9];
+  floatx4 acc[9];
 #pragma unroll
-  for (int m = 0; m < 9; ++m) acc[m] = 0.f;
-  for (int c0 = 0; c0 < n; c0 += 32) {
-    const int nc = min(32, n - c0);
-    if (c < nc) {
-      const int64_t e = (int64_t)b + c0 + c;
-      const float d = A.dist[e];
-      const float nrm = fmaxf(d, 1e-12f);
-      float Y[9];
-      raw_sh2(A.dvec[3 * e] / nrm, A.dvec[3 * e + 1] / nrm, A.dvec[3 * e + 2] / nrm, Y);
+  for (int m = 0; m < 9; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int c = 4 * lane;
+#pragma unroll 2
+  for (int el = 0; el < n; ++el) {
+    const int64_t e = (int64_t)b + el;
+    const float d = A.dist[e];
+    const float nrm = fmaxf(d, 1e-12f);
+    float Y[9];
+    raw_sh2(A.dvec[3 * e] / nrm, A.dvec[3 * e + 1] / nrm, A.dvec[3 * e + 2] / nrm, Y);
+    float p, dp;
+    env.eval(d, p, dp);
+    const float* f = A.fea + e * (3 * kDC) + c;
+    const floatx4 fa = *reinterpret_cast<const floatx4*>(f);
+    const floatx4 fb = *reinterpret_cast<const floatx4*>(f + kDC);
+    const floatx4 fc = *reinterpret_cast<const floatx4*>(f + 2 * kDC);
 #pragma unroll
-      for (int m = 0; m < 9; ++m) sh_s[c][m] = Y[m];
-      float p, dp;
-      env.eval(d, p, dp);
-      p_s[c] = p;
-      e_s[c] = e;
+    for (int u = 0; u < 4; ++u) {
+      const float f0 = fa[u] * p, f1 = fb[u] * p, f2 = fc[u] * p;
+      acc[0][u] = fmaf(Y[0], f0, acc[0][u]);
+#pragma unroll
+      for (int m = 1; m < 4; ++m) acc[m][u] = fmaf(Y[m], f1, acc[m][u]);
+#pragma unroll
+      for (int m = 4; m < 9; ++m) acc[m][u] = fmaf(Y[m], f2, acc[m][u]);
     }
-    __syncthreads();
-    for (int el = 0; el < nc; ++el) {
-      const float* f = A.fea + e_s[el] * (3 * kDC) + c;
-      const float p = p_s[el];
-      const float f0 = f[0] * p, f1 = f[kDC] * p, f2 = f[2 * kDC] * p;
-      acc[0] = fmaf(sh_s[el][0], f0, acc[0]);
-#pragma unroll
-      for (int m = 1; m < 4; ++m) acc[m] = fmaf(sh_s[el][m], f1, acc[m]);
-#pragma unroll
-      for (int m = 4; m < 9; ++m) acc[m] = fmaf(sh_s[el][m], f2, acc[m]);
-    }
-    __syncthreads();
   }
 #pragma unroll
-  for (int m = 0; m < 9; ++m) x0[((size_t)m * A.n_rows + i) * kDC + c] = acc[m] / A.avg;
+  for (int m = 0; m < 9; ++m) {
+    floatx4 o;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) o[u] = acc[m][u] / A.avg;
+    *reinterpret_cast<floatx4*>(x0 + ((size_t)m * A.n_rows + i) * kDC + c) = o;
+  }
 }
 
 // one workgroup per query atom; one wave per edge, lane owns channels lane + 64 q
@@ -182,7 +186,8 @@ E2V2_API int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s) {
   const e2v2_deg_args& A = *args;
   E2V2_REQUIRE(A.channels == kDC, "deg_fwd: built for C=%d, got %d", kDC, A.channels);
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_deg_fwd, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, x0);
+  hipLaunchKernelGGL(k_deg_fwd, dim3(xcd_grid((A.n_rows + kDegWaves - 1) / kDegWaves)), dim3(64 * kDegWaves), 0, s,
+                     A, x0);
   E2V2_LAUNCHED("k_deg_fwd");
   return 0;
 }
