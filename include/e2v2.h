@@ -38,6 +38,7 @@
  *   e2v2_rmsnorm_*      EquivariantRMSNormArraySphericalHarmonicsV2_BL (module_utils.py:1663-1772)
  *   e2v2_gate_*         Gate_s3 activation (module_utils.py:2694-2746)
  *   e2v2_pairdot_*      per-l m-contraction of SO3_Linear2Scalar_e2former (module_utils.py:2241-2266)
+ *   e2v2_qk_proj_*      its projection GEMMs with the contraction fused (module_utils.py:2198-2266)
  *   e2v2_edge_to_pos    autograd of f_edge_vec / f_dist w.r.t. positions (module_utils.py:3161-3206),
  *                       consumed by GradientHead (src/molfm/pipeline/head.py:305-328)
  */
@@ -251,6 +252,18 @@ int e2v2_gate_bwd(const float* sc, const float* x, const float* gy, float* gsc, 
  * y [9][N][4 hid] = (q_a | q_b | k_a | k_b) -> hq, hk [N][3 hid], h[l hid + c] = sum_{m in l} a b */
 int e2v2_pairdot_fwd(const float* y, float* hq, float* hk, int n, int hid, hipStream_t s);
 int e2v2_pairdot_bwd(const float* y, const float* ghq, const float* ghk, float* gy, int n, int hid, hipStream_t s);
+/* The Q/K projection of SO3_Linear2Scalar_e2former with the above contraction fused (module_utils.py:2198-2266,
+ * called for query and key at e2former.py:300-303), fp32 MFMA:
+ *   fwd: y[m][n][o] = sum_k x[m][n][k] w[l(m)][o][k] (+ bias[o] on m = 0; bias may be NULL), x [9][N][C],
+ *        w [3][4 hid][C]; writes y (kept for the backward) and hq, hk [N][3 hid].
+ *   bwd: gx [9][N][C] = gy W with gy the contraction's gradient (formed from y, ghq, ghk; never stored),
+ *        wt [9][C][4 hid] = w[l(m)]^T per m-row; with gv (NULL for none) also + gv Wv, gv [9][N][cv],
+ *        wvt [9][C][cv] = Wv[l(m)]^T (the value projection, which reads the same x).
+ * Requires hid % 64 == 0, C % 128 == 0 (bwd; C % 32 fwd), cv % 32 == 0. */
+int e2v2_qk_proj_fwd(const float* x, const float* w, const float* bias, float* y, float* hq, float* hk, int n, int hid,
+                     int c, hipStream_t s);
+int e2v2_qk_proj_bwd(const float* y, const float* ghq, const float* ghk, const float* wt, const float* gv,
+                     const float* wvt, float* gx, int n, int hid, int c, int cv, hipStream_t s);
 /* y = silu(LayerNorm(x) * g + b) on rows x [n][w] (w % 64 == 0, w <= 1024), the LayerNorm + SiLU of the
    Q/K head (final_linear of SO3_Linear2Scalar_e2former, module_utils.py:2230-2233,2268); stats [n][2] =
    (mean, rstd) kept for the backward, which returns the input gradient only. */

@@ -446,3 +446,58 @@ def test_node_kernels_rmsnorm_gate(pkg, cuda):
     e3, e4 = relerr(yd.permute(1, 0, 2), yr), relerr(gd.permute(1, 0, 2), gr)
     print(f"[node] rms fwd {e1:.2e} bwd {e2:.2e} gate fwd {e3:.2e} bwd {e4:.2e}", flush=True)
     assert max(e1, e3) < 2e-6 and max(e2, e4) < 1e-5
+
+
+@pytest.mark.parametrize("n,with_v,with_bias", [(1, True, True), (200, False, True), (1000, True, False)])
+def test_qk_proj_fused(pkg, cuda, n, with_v, with_bias):
+    """Fused Q/K projection + m-contraction (forward) and its input gradient with the
+    value projection's gradient folded in (backward) against float64 GEMMs."""
+    from ubio_molfm_amd import _lib
+    torch.manual_seed(7)
+    hid, C, Cv = 512, 256, 256
+    print(f"[qk_proj] n={n} with_v={with_v} bias={with_bias}", flush=True)
+    idx = torch.tensor([0, 1, 1, 1, 2, 2, 2, 2, 2], device=cuda)
+    x = torch.randn(9, n, C, device=cuda)
+    W = torch.randn(3, 4 * hid, C, device=cuda) / 16
+    bias = torch.randn(4 * hid, device=cuda) if with_bias else None
+    Wv = torch.randn(3, Cv, C, device=cuda) / 16
+    Wt = W[idx].transpose(1, 2).contiguous()
+    Wvt = Wv[idx].transpose(1, 2).contiguous()
+    y = torch.empty(9, n, 4 * hid, device=cuda)
+    hq = torch.empty(n, 3 * hid, device=cuda); hk = torch.empty_like(hq)
+    st = _lib.vp(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: _lib.vp(t.data_ptr() if t is not None else 0)
+    _lib.call("e2v2_qk_proj_fwd", p(x), p(W), p(bias), p(y), p(hq), p(hk), _lib.i32(n), _lib.i32(hid),
+              _lib.i32(C), st)
+    # float64 reference: per-m GEMM with the degree's weight, bias on m = 0, then the per-l pair sums
+    yd = torch.bmm(x.double(), Wt.double())
+    if with_bias:
+        yd[0] += bias.double()
+    a_q, b_q, a_k, b_k = yd.split(hid, dim=2)
+    L = [slice(0, 1), slice(1, 4), slice(4, 9)]
+    hqd = torch.cat([(a_q[s] * b_q[s]).sum(0) for s in L], dim=1)
+    hkd = torch.cat([(a_k[s] * b_k[s]).sum(0) for s in L], dim=1)
+    e_y, e_q, e_k = relerr(y, yd), relerr(hq, hqd), relerr(hk, hkd)
+    ghq = torch.randn(n, 3 * hid, device=cuda); ghk = torch.randn(n, 3 * hid, device=cuda)
+    gv = torch.randn(9, n, Cv, device=cuda) if with_v else None
+    gx = torch.empty(9, n, C, device=cuda)
+    _lib.call("e2v2_qk_proj_bwd", p(y), p(ghq), p(ghk), p(Wt), p(gv), p(Wvt if with_v else None), p(gx),
+              _lib.i32(n), _lib.i32(hid), _lib.i32(C), _lib.i32(Cv if with_v else 0), st)
+    # reference gradient: autograd through the float64 forward
+    xd = x.double().requires_grad_(True)
+    yr = torch.bmm(xd, Wt.double())
+    if with_bias:
+        shift = torch.zeros(9, 1, 4 * hid, device=cuda, dtype=torch.float64)
+        shift[0, 0] = bias.double()
+        yr = yr + shift
+    aq, bq, ak, bk = yr.split(hid, dim=2)
+    hq_r = torch.cat([(aq[s] * bq[s]).sum(0) for s in L], dim=1)
+    hk_r = torch.cat([(ak[s] * bk[s]).sum(0) for s in L], dim=1)
+    obj = (hq_r * ghq.double()).sum() + (hk_r * ghk.double()).sum()
+    if with_v:
+        obj = obj + (torch.bmm(xd, Wvt.double()) * gv.double()).sum()
+    gxd, = torch.autograd.grad(obj, xd)
+    e_g = relerr(gx, gxd)
+    print(f"[qk_proj] n={n} y {e_y:.2e} hq {e_q:.2e} hk {e_k:.2e} gx {e_g:.2e}", flush=True)
+    assert e_y < 2e-5 and e_q < 2e-5 and e_k < 2e-5
+    assert e_g < 1e-4

@@ -183,6 +183,16 @@ class SO3LinearFn(torch.autograd.Function):
         return gx, None, None, None, (gy if ctx.has_res else None)
 
 
+def _qk_fused(Wop: MRowWeight, Wvop, C: int, hid: int, lmax: int) -> bool:
+    """The fused HIP projection (``e2v2_qk_proj_fwd/bwd``) covers fp32 weights with
+    per-m expansions, lmax 2, C a multiple of 128, hid of 64 and the value width of 32."""
+    ok = (Wop.fwd is not None and Wop.w.dtype == torch.float32 and lmax == 2 and C % 128 == 0
+          and hid % 64 == 0)
+    if Wvop is not None:
+        ok = ok and Wvop.fwd is not None and Wvop.fwd.shape[2] % 32 == 0
+    return ok
+
+
 class QKProjFn(torch.autograd.Function):
     """Fused per-l GEMM of the query and key SO3_Linear2Scalar products and their
     m-contraction: x[9][N][C] -> hq, hk [N][3 hid] (before final_linear)."""
@@ -196,7 +206,15 @@ class QKProjFn(torch.autograd.Function):
         x = x.contiguous()
         L2, N, C = x.shape
         W = Wop.w
-        if Wop.fwd is not None:
+        fused = _qk_fused(Wop, Wvop, C, hid, lmax)
+        ctx.fused = fused
+        if fused:
+            # projection GEMM with the m-contraction on its accumulators (HIP, MFMA)
+            y = x.new_empty(L2, N, 4 * hid)
+            hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
+            _lib.call("e2v2_qk_proj_fwd", _dp(x), _dp(W), _lib.vp(bias.data_ptr() if bias is not None else 0),
+                      _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _lib.i32(C), _stream())
+        elif Wop.fwd is not None:
             y = _mrow_gemm(x, Wop, bias)
         else:
             y = x.new_empty(L2, N, 4 * hid)
@@ -207,8 +225,9 @@ class QKProjFn(torch.autograd.Function):
                     _mm_bias_into(xa[0], W[0].t(), bias, out=y[0])
                 else:
                     _mm_into(xa[a:b].view(-1, C), W[l].t(), out=y[a:b].view(-1, 4 * hid))
-        hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
-        _lib.call("e2v2_pairdot_fwd", _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _stream())
+        if not fused:
+            hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
+            _lib.call("e2v2_pairdot_fwd", _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _stream())
         v = None
         if Wvop is not None:
             Wv = Wvop.w
@@ -237,6 +256,18 @@ class QKProjFn(torch.autograd.Function):
         hid = ctx.hid
         ghq = torch.zeros(N, 3 * hid, device=y.device) if ghq is None else ghq.contiguous()
         ghk = torch.zeros(N, 3 * hid, device=y.device) if ghk is None else ghk.contiguous()
+        if ctx.fused:
+            # gy = the m-contraction's gradient, formed while the GEMM stages it; the
+            # value projection's gradient gv W_v enters as further K stages
+            C = Wop.w.shape[2]
+            gx = y.new_empty(L2, N, C)
+            with_v = Wvop is not None and gv is not None
+            gvc = gv.contiguous() if with_v else None
+            _lib.call("e2v2_qk_proj_bwd", _dp(y), _dp(ghq), _dp(ghk), _dp(Wop.fwd),
+                      _lib.vp(gvc.data_ptr() if with_v else 0), _lib.vp(Wvop.fwd.data_ptr() if with_v else 0),
+                      _dp(gx), _lib.i32(N), _lib.i32(hid), _lib.i32(C),
+                      _lib.i32(Wvop.fwd.shape[2] if with_v else 0), _stream())
+            return gx, None, None, None, None, None, None
         gy = torch.empty_like(y)
         _lib.call("e2v2_pairdot_bwd", _dp(y), _dp(ghq), _dp(ghk), _dp(gy), _lib.i32(N), _lib.i32(hid), _stream())
         W = Wop.w
