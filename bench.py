@@ -74,13 +74,19 @@ def stack_flops(N, E):
     return 2.0 * (E * 1.88e6 + N * 4 * 22.7e6)
 
 
+# fused Q/K projection (fp32), FLOPs per call: 9 m-rows x N nodes x C=256 inputs x 4 hid=2048 outputs,
+# the backward also folds in the value projection's input gradient (256 more K columns)
+PROJ_FLOPS = {"e2v2_qk_proj_fwd": lambda N: 2.0 * 9 * N * 256 * 2048,
+              "e2v2_qk_proj_bwd": lambda N: 2.0 * 9 * N * 256 * (2048 + 256)}
+
 BYTES_OF = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
             "e2v2_deg_bwd": deg_bwd_bytes}
 
 KERNELS_OF = {"e2v2_mlp_fwd": ["k_mlp_fwd"], "e2v2_mlp_bwd": ["k_mlp_bwd"],
               "e2v2_mlp_bwd_deg": ["k_mlp_bwd_deg"], "e2v2_attn_fwd": ["k_attn_fwd"],
               "e2v2_attn_bwd": ["k_attn_bwd_row_hp", "k_attn_bwd_col_grp"], "e2v2_deg_fwd": ["k_deg_fwd"],
-              "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"]}
+              "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"],
+              "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"]}
 
 
 def traffic_from_profile(entry, bf16=False):
@@ -172,7 +178,8 @@ def main():
         integ.step()
     torch.cuda.synchronize()
     timer = _lib.KernelTimer(["e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_mlp_bwd_deg", "e2v2_attn_fwd", "e2v2_attn_bwd",
-                              "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill"])
+                              "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill",
+                              "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd"])
     edges = []
     e_start = integ.e.sum().item() + integ.kinetic()
     _lib.set_timer(timer)
@@ -223,6 +230,9 @@ def main():
             tf = mlp_step_flops[k] / (v["count"] / args.steps) / (v["avg_ms"] * 1e-3) / 1e12
             pk = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
             ent.update(bound="mfma", achieved_tflops=round(tf, 2), frac=round(tf / pk, 4))
+        elif k in PROJ_FLOPS:
+            tf = PROJ_FLOPS[k](N) / (v["avg_ms"] * 1e-3) / 1e12
+            ent.update(bound="mfma", achieved_tflops=round(tf, 2), frac=round(tf / FP32_PEAK_TFLOPS, 4))
         per_kernel[k] = ent
     # stack: whole evaluation against the MFMA roofline; HBM-bound kernels time-weighted
     peak_tf = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
