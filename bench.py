@@ -212,6 +212,10 @@ def main():
         peak = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                 "frac": achieved / peak, "traffic": traffic_from_profile(name, bf16), "kernel": name}
+    elif name in PROJ_FLOPS:
+        achieved = PROJ_FLOPS[name](N) / (st["avg_ms"] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / FP32_PEAK_TFLOPS, "traffic": traffic_from_profile(name), "kernel": name}
     else:
         fb = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
               "e2v2_deg_bwd": deg_bwd_bytes}.get(name, attn_fwd_bytes)
