@@ -128,13 +128,16 @@ typedef struct e2v2_mlp_weights {
   const float* ttgt;  /* [types][128] target-type block of Linear1 + bias         */
   const float* tsrc;  /* [types][128] source-type block of Linear1                */
   const float* g1; const float* be1;   /* LayerNorm(128)                            */
-  const float* w2t;   /* [128][128] Linear2 transposed                            */
+  /* fp32 GEMM operands B[K][N], lane-packed: one float4 per (wave w < 4, column group
+     ct < N/64, k block b < K/16, lane l < 64) in that order, holding
+     B[16 b + 4 (l / 16) + s][w N/4 + 16 ct + l % 16], s = 0..3.                  */
+  const float* w2t;   /* B = Linear2^T [128][128] (forward)                       */
   const float* b2;
   const float* g2; const float* be2;
-  const float* w3t;   /* [128][256] Linear3 transposed                            */
+  const float* w3t;   /* B = Linear3^T [128][256] (forward)                       */
   const float* b3;
-  const float* w2;    /* [128][128] Linear2 as stored                             */
-  const float* w3;    /* [256][128] Linear3 as stored                             */
+  const float* w2;    /* B = Linear2 [128][128] (backward)                        */
+  const float* w3;    /* B = Linear3 [256][128] (backward)                        */
   /* bf16 operands (compute_bf16 = 1), each as B^T row-major [N][K]:              */
   const void* w2b;    /* [128][128] Linear2 (forward)                             */
   const void* w3b;    /* [256][128] Linear3 (forward)                             */

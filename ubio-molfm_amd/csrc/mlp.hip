@@ -44,40 +44,44 @@ constexpr float kFarDist = 1e18f;  // distance of padding rows (finite)
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // ---------------------------------------------------------------------------
-// fp32 GEMM: C[32][N] = A[32][K] x B[K][N] (global, row stride ldb).  Wave w
-// owns columns [w*N/4, (w+1)*N/4).  acc[rt][ct] holds the 16x16 tile (rows
-// rt*16.., cols w*N/4 + ct*16..); lane l holds rows 4*(l/16)+r, col l%16.
-// afn(k, a0, a1) supplies A[l%16][k] and A[16 + l%16][k] for this lane's
-// k = 4 s + l/16 of k-step s.  B is streamed in chunks of 32 k-rows held in
-// registers one chunk ahead (the fp32 MFMA time per chunk covers the load).
+// fp32 GEMM: C[32][N] = A[32][K] x B[K][N].  Wave w owns columns
+// [w*N/4, (w+1)*N/4).  acc[rt][ct] holds the 16x16 tile (rows rt*16.., cols
+// w*N/4 + ct*16..); lane l holds rows 4*(l/16)+r, col l%16.  Within each block
+// of 16 k the four k-steps s take k = 16 blk + 4 (l/16) + s, so a lane's B values
+// for a block are four consecutive k of one column: B is stored lane-packed,
+// one float4 per (wave, ct, blk, lane), B[16 blk + 4 (l/16) + s][w N/4 + 16 ct + l%16]
+// at ((w (N/64) + ct) (K/16) + blk) 64 + l (16-byte loads, a wave's 1 KB contiguous).
+// afn(k, a0, a1) supplies A[l%16][k] and A[16 + l%16][k].  B is streamed in chunks
+// held in registers one chunk ahead (the fp32 MFMA time per chunk covers the load).
 // The first B chunk of a GEMM, loaded ahead (before the stage that precedes the
 // GEMM) so that its L2 round trip overlaps that stage.
 template <int N>
 struct BChunk {
-  float v[N > 128 ? kPFWide : kPFNarrow][N / 64];
+  floatx4 v[(N > 128 ? kPFWide : kPFNarrow) / 4][N / 64];
 };
 
-template <int N>
-__device__ __forceinline__ const float* b_lane_ptr(const float* __restrict__ B, int ldb) {
+template <int K, int N>
+__device__ __forceinline__ const floatx4* b_lane_ptr(const float* __restrict__ B) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  return B + (size_t)(lane >> 4) * ldb + wave * (N / 4) + (lane & 15);
+  return reinterpret_cast<const floatx4*>(B) + (size_t)wave * (N / 64) * (K / 16) * 64 + lane;
 }
 
-template <int N>
-__device__ __forceinline__ void load_first_chunk(const float* __restrict__ B, int ldb, BChunk<N>& c) {
-  constexpr int kPF = N > 128 ? kPFWide : kPFNarrow;
-  const float* Bp = b_lane_ptr<N>(B, ldb);
+template <int K, int N>
+__device__ __forceinline__ void load_first_chunk(const float* __restrict__ B, BChunk<N>& c) {
+  constexpr int kBl = (N > 128 ? kPFWide : kPFNarrow) / 4;
+  const floatx4* Bp = b_lane_ptr<K, N>(B);
 #pragma unroll
-  for (int s = 0; s < kPF; ++s)
+  for (int b = 0; b < kBl; ++b)
 #pragma unroll
-    for (int ct = 0; ct < N / 64; ++ct) c.v[s][ct] = Bp[(size_t)(4 * s) * ldb + ct * 16];
+    for (int ct = 0; ct < N / 64; ++ct) c.v[b][ct] = Bp[(ct * (K / 16) + b) * 64];
 }
 
-template <int K, int N, typename AFn>
-__device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, int ldb, const BChunk<N>& first,
+template <int K, int N, bool kPin, typename AFn>
+__device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, const BChunk<N>& first,
                                         floatx4 (&acc)[2][N / 64]) {
   constexpr int CT = N / 64;
-  constexpr int kPF = N > 128 ? kPFWide : kPFNarrow;   // B registers per chunk: kPF * CT
+  constexpr int kPF = N > 128 ? kPFWide : kPFNarrow;   // k-steps per chunk (kPF / 4 blocks of 16 k)
+  constexpr int kBl = kPF / 4;
   constexpr int NCH = K / (4 * kPF);
   const int lane = threadIdx.x & 63;
   const int lk = lane >> 4;
@@ -85,49 +89,53 @@ __device__ __forceinline__ void gemm32f(AFn afn, const float* __restrict__ B, in
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const float* Bp = b_lane_ptr<N>(B, ldb);
-  float bc[kPF][CT], bn[kPF][CT];
+  const floatx4* Bp = b_lane_ptr<K, N>(B);
+  floatx4 bc[kBl][CT], bn[kBl][CT];
 #pragma unroll
-  for (int s = 0; s < kPF; ++s)
+  for (int b = 0; b < kBl; ++b)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) bc[s][ct] = first.v[s][ct];
+    for (int ct = 0; ct < CT; ++ct) bc[b][ct] = first.v[b][ct];
   __builtin_amdgcn_s_setprio(1);   // MFMA-ready waves issue ahead of epilogue work of other waves
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     if (ch + 1 < NCH) {
 #pragma unroll
-      for (int s = 0; s < kPF; ++s)
+      for (int b = 0; b < kBl; ++b)
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) bn[s][ct] = Bp[(size_t)((ch + 1) * 4 * kPF + 4 * s) * ldb + ct * 16];
+        for (int ct = 0; ct < CT; ++ct) bn[b][ct] = Bp[(ct * (K / 16) + (ch + 1) * kBl + b) * 64];
     }
+    // kPin: keep the next chunk's loads here, a chunk of MFMAs ahead of their use
+    // (the scheduler would otherwise sink them next to the first use and wait on
+    // them); costs registers, so kernels under a 128-VGPR cap leave it off
+    if constexpr (kPin) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < kPF; ++s) {
       float a0, a1;
-      afn(ch * 4 * kPF + 4 * s + lk, a0, a1);
+      afn(16 * (ch * kBl + s / 4) + 4 * lk + (s & 3), a0, a1);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        acc[0][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, bc[s][ct], acc[0][ct], 0, 0, 0);
-        acc[1][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, bc[s][ct], acc[1][ct], 0, 0, 0);
+        acc[0][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, bc[s / 4][ct][s & 3], acc[0][ct], 0, 0, 0);
+        acc[1][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, bc[s / 4][ct][s & 3], acc[1][ct], 0, 0, 0);
       }
     }
     if (ch + 1 < NCH) {
 #pragma unroll
-      for (int s = 0; s < kPF; ++s)
+      for (int b = 0; b < kBl; ++b)
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) bc[s][ct] = bn[s][ct];
+        for (int ct = 0; ct < CT; ++ct) bc[b][ct] = bn[b][ct];
     }
   }
   __builtin_amdgcn_s_setprio(0);
 }
 
 // A from an LDS tile with row stride lda; the first B chunk already loaded
-template <int K, int N>
-__device__ __forceinline__ void gemm32(const float* A, int lda, const float* __restrict__ B, int ldb,
+template <int K, int N, bool kPin = false>
+__device__ __forceinline__ void gemm32(const float* A, int lda, const float* __restrict__ B,
                                        const BChunk<N>& first, floatx4 (&acc)[2][N / 64]) {
   const int li = threadIdx.x & 15;
   const float* A0 = A + li * lda;
   const float* A1 = A + (16 + li) * lda;
-  gemm32f<K, N>([&](int k, float& a0, float& a1) { a0 = A0[k]; a1 = A1[k]; }, B, ldb, first, acc);
+  gemm32f<K, N, kPin>([&](int k, float& a0, float& a1) { a0 = A0[k]; a1 = A1[k]; }, B, first, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -562,7 +570,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   load_tile_edges(A, e0, te);
   load_ln_params(W, lp);
   BChunk<kH> f2;
-  load_first_chunk<kH>(W.w2t, kH, f2);      // in flight during Linear1 and LayerNorm 1
+  load_first_chunk<kH, kH>(W.w2t, f2);      // in flight during Linear1 and LayerNorm 1
   __syncthreads();
   linear1_rows(W, te, Y, kLdY);
   __syncthreads();
@@ -571,8 +579,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   BChunk<256> f3;
   {
     floatx4 acc[2][2];
-    gemm32<kH, kH>(Y, kLdY, W.w2t, kH, f2, acc);
-    load_first_chunk<256>(W.w3t, 256, f3);  // in flight during LayerNorm 2
+    gemm32<kH, kH, true>(Y, kLdY, W.w2t, f2, acc);
+    load_first_chunk<kH, 256>(W.w3t, f3);  // in flight during LayerNorm 2
     __syncthreads();
     store_acc<kH>(acc, Y, kLdY, b2);
   }
@@ -580,7 +588,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   ln_silu_rows(Y, kLdY, Y, kLdY, lp.g2, lp.b2, sn ? sn + kH : nullptr, 2 * kH, sr ? sr + 1 : nullptr, 2, nvalid);
   __syncthreads();
   floatx4 acc[2][4];
-  gemm32<kH, 256>(Y, kLdY, W.w3t, 256, f3, acc);
+  gemm32<kH, 256, true>(Y, kLdY, W.w3t, f3, acc);
   __syncthreads();
   store_out(acc, b3, sm, out, ld_out, e0, nvalid, m);
 }
@@ -613,7 +621,7 @@ __device__ __forceinline__ void mlp_bwd_body(e2v2_mlp_args A, const float* __res
     const float* srs = A.save_r + ((size_t)m * A.n_edges + e0) * 2;
     load_ln_params(W, lp);
     BChunk<kH> fa;
-    load_first_chunk<kH>(W.w3, kH, fa);       // in flight during the dOut tile load
+    load_first_chunk<256, kH>(W.w3, fa);       // in flight during the dOut tile load
     for (int idx = threadIdx.x; idx < kT * 64; idx += 256) {   // dOut tile, 16-byte loads
       const int row = idx >> 6, c4 = idx & 63;
       const floatx4 v = dout4<kDeg>(dout, ld_dout, e0, row, nvalid, m, c4, g0, D.n_rows, dt);
@@ -626,8 +634,8 @@ __device__ __forceinline__ void mlp_bwd_body(e2v2_mlp_args A, const float* __res
     BChunk<kH> fb;
     {  // dy2 = dOut . W3   (W3 [256][128] row-major = B[K=256][N=128])
       floatx4 acc[2][2];
-      gemm32<256, kH>(X, kLdX, W.w3, kH, fa, acc);
-      load_first_chunk<kH>(W.w2, kH, fb);     // in flight during the LayerNorm-2 backward
+      gemm32<256, kH>(X, kLdX, W.w3, fa, acc);
+      load_first_chunk<kH, kH>(W.w2, fb);     // in flight during the LayerNorm-2 backward
       __syncthreads();
       store_acc<kH>(acc, Y, kLdY, zero2);
     }
@@ -638,7 +646,7 @@ __device__ __forceinline__ void mlp_bwd_body(e2v2_mlp_args A, const float* __res
     __syncthreads();
     {  // dy1 = dz2 . W2   (W2 [128][128])
       floatx4 acc[2][2];
-      gemm32<kH, kH>(Y, kLdY, W.w2, kH, fb, acc);
+      gemm32<kH, kH>(Y, kLdY, W.w2, fb, acc);
       __syncthreads();
       store_acc<kH>(acc, Y, kLdY, zero2);
     }

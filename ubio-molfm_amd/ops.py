@@ -70,10 +70,12 @@ class PackedMLP:
             self.ttgt = (tgt.detach().float() @ W1[:, n_rbf:n_rbf + e].t() + lin1.bias.detach().float()).contiguous()
             self.tsrc = (src.detach().float() @ W1[:, n_rbf + e:n_rbf + 2 * e].t()).contiguous()
             self.g1 = ln1.weight.detach().float().contiguous(); self.be1 = ln1.bias.detach().float().contiguous()
-            self.w2 = lin2.weight.detach().float().contiguous(); self.w2t = self.w2.t().contiguous()
+            self.w2 = lin2.weight.detach().float().contiguous(); self.w2t = _lane_pack(self.w2.t())
             self.b2 = lin2.bias.detach().float().contiguous()
             self.g2 = ln2.weight.detach().float().contiguous(); self.be2 = ln2.bias.detach().float().contiguous()
-            self.w3 = lin3.weight.detach().float().contiguous(); self.w3t = self.w3.t().contiguous()
+            self.w3 = lin3.weight.detach().float().contiguous(); self.w3t = _lane_pack(self.w3.t())
+            # fp32 GEMM B operands, lane-packed: forward W2^T, W3^T; backward W3, W2
+            self.w2p = _lane_pack(self.w2); self.w3p = _lane_pack(self.w3)
             self.b3 = lin3.bias.detach().float().contiguous()
             # bf16 GEMM operands as B^T row-major: forward W2, W3; backward W3^T, W2^T
             self.bf = None
@@ -97,7 +99,15 @@ class PackedMLP:
         return _lib.MlpWeights(self.rtab.data_ptr(), self.rtab_n, self.rtab_h, self.ttgt.data_ptr(),
                                self.tsrc.data_ptr(), self.g1.data_ptr(), self.be1.data_ptr(), self.w2t.data_ptr(),
                                self.b2.data_ptr(), self.g2.data_ptr(), self.be2.data_ptr(), self.w3t.data_ptr(),
-                               self.b3.data_ptr(), self.w2.data_ptr(), self.w3.data_ptr(), *bf)
+                               self.b3.data_ptr(), self.w2p.data_ptr(), self.w3p.data_ptr(), *bf)
+
+
+def _lane_pack(B: torch.Tensor) -> torch.Tensor:
+    """B [K][N] (fp32) in the lane-packed order of the HIP MLP's fp32 GEMMs: one
+    float4 per (wave w, 16-column group ct, 16-k block b, lane l), holding
+    B[16 b + 4 (l // 16) + s][w N/4 + 16 ct + l % 16] for s = 0..3."""
+    K, N = B.shape
+    return B.contiguous().view(K // 16, 4, 4, 4, N // 64, 16).permute(3, 4, 0, 1, 5, 2).contiguous()
 
 
 def _version_key(params):
