@@ -109,7 +109,8 @@ def traffic_from_profile(entry, bf16=False):
 def cpu_baseline(pkg):
     """Oracle (restated reference path, torch CPU fp32) on a 300-atom periodic
     water/protein mix built by the configs[3] recipe (same density and element
-    ratios); one evaluation after a warm-up on a 12-atom cell."""
+    ratios): repeated energy+force evaluations for at least 10 s (bounded at 20)
+    after a warm-up on a 12-atom cell."""
     import numpy as np
     import torch
     from ubio_molfm_amd import systems
@@ -121,13 +122,17 @@ def cpu_baseline(pkg):
     om = OracleModel().eval()
     energy_forces_with_neighbors(om, systems.small_water(4, 5.5, seed=1))
     sysd = systems.solvated_chains(300, seed=0)
+    reps, edges_total = 0, 0
     t0 = time.perf_counter()
-    e, f, n_edges = energy_forces_with_neighbors(om, sysd)
+    while reps < 20 and (reps == 0 or time.perf_counter() - t0 < 10.0):
+        e, f, n_edges = energy_forces_with_neighbors(om, sysd)
+        reps += 1
+        edges_total += n_edges
     t = time.perf_counter() - t0
-    return {"value": n_edges / t, "unit": "edges/s", "cores": cores, "kind": "port",
-            "sample": f"300-atom periodic water/protein mix (configs[3] recipe, {n_edges} edges): one fp32 "
-                      f"energy+force evaluation of the restated reference path (oracle/, torch CPU) after a "
-                      f"warm-up; {t:.1f} s"}
+    return {"value": edges_total / t, "unit": "edges/s", "cores": cores, "kind": "port",
+            "sample": f"300-atom periodic water/protein mix (configs[3] recipe, {n_edges} edges): {reps} fp32 "
+                      f"energy+force evaluations (neighbour build included) of the restated reference path "
+                      f"(oracle/, torch CPU) after a warm-up; {t:.1f} s"}
 
 
 def main():
