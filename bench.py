@@ -78,6 +78,8 @@ def stack_flops(N, E):
 # the backward also folds in the value projection's input gradient (256 more K columns)
 PROJ_FLOPS = {"e2v2_qk_proj_fwd": lambda N: 2.0 * 9 * N * 256 * 2048,
               "e2v2_qk_proj_bwd": lambda N: 2.0 * 9 * N * 256 * (2048 + 256)}
+PROJ_FLOPS["e2v2_qk_proj_fwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
+PROJ_FLOPS["e2v2_qk_proj_bwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
 
 BYTES_OF = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
             "e2v2_deg_bwd": deg_bwd_bytes}
@@ -184,7 +186,8 @@ def main():
     torch.cuda.synchronize()
     timer = _lib.KernelTimer(["e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_mlp_bwd_deg", "e2v2_attn_fwd", "e2v2_attn_bwd",
                               "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill",
-                              "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd"])
+                              "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd", "e2v2_qk_proj_fwd_bf16",
+                              "e2v2_qk_proj_bwd_bf16"])
     edges = []
     e_start = integ.e.sum().item() + integ.kinetic()
     _lib.set_timer(timer)
@@ -219,8 +222,9 @@ def main():
                 "frac": achieved / peak, "traffic": traffic_from_profile(name, bf16), "kernel": name}
     elif name in PROJ_FLOPS:
         achieved = PROJ_FLOPS[name](N) / (st["avg_ms"] * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / FP32_PEAK_TFLOPS, "traffic": traffic_from_profile(name), "kernel": name}
+        pk = BF16_PEAK_TFLOPS if name.endswith("_bf16") else FP32_PEAK_TFLOPS
+        roof = {"bound": "mfma", "achieved": achieved, "peak": pk, "unit": "TFLOP/s",
+                "frac": achieved / pk, "traffic": traffic_from_profile(name, bf16), "kernel": name}
     else:
         fb = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
               "e2v2_deg_bwd": deg_bwd_bytes}.get(name, attn_fwd_bytes)
@@ -241,7 +245,8 @@ def main():
             ent.update(bound="mfma", achieved_tflops=round(tf, 2), frac=round(tf / pk, 4))
         elif k in PROJ_FLOPS:
             tf = PROJ_FLOPS[k](N) / (v["avg_ms"] * 1e-3) / 1e12
-            ent.update(bound="mfma", achieved_tflops=round(tf, 2), frac=round(tf / FP32_PEAK_TFLOPS, 4))
+            pk = BF16_PEAK_TFLOPS if k.endswith("_bf16") else FP32_PEAK_TFLOPS
+            ent.update(bound="mfma", achieved_tflops=round(tf, 2), frac=round(tf / pk, 4))
         per_kernel[k] = ent
     # stack: whole evaluation against the MFMA roofline; HBM-bound kernels time-weighted
     peak_tf = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS

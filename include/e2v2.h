@@ -267,6 +267,14 @@ int e2v2_qk_proj_fwd(const float* x, const float* w, const float* bias, float* y
                      int c, hipStream_t s);
 int e2v2_qk_proj_bwd(const float* y, const float* ghq, const float* ghk, const float* wt, const float* gv,
                      const float* wvt, float* gx, int n, int hid, int c, int cv, hipStream_t s);
+/* The same with bf16 MFMA operands (bf16 compute mode): x, bias, hq, hk, ghq, ghk, gv and gx stay fp32 (x and gv
+ * are rounded to bf16 as they are staged); w [3][4 hid][C], wt [3][C][4 hid] (per degree l, not per m-row),
+ * wvt [3][C][cv] and the kept product y [9][N][4 hid] are bf16.  Requires hid % 64 == 0, C % 64 == 0 (fwd) /
+ * C % 128 == 0 (bwd), cv % 64 == 0. */
+int e2v2_qk_proj_fwd_bf16(const float* x, const void* w, const float* bias, void* y, float* hq, float* hk, int n,
+                          int hid, int c, hipStream_t s);
+int e2v2_qk_proj_bwd_bf16(const void* y, const float* ghq, const float* ghk, const void* wt, const float* gv,
+                          const void* wvt, float* gx, int n, int hid, int c, int cv, hipStream_t s);
 /* y = silu(LayerNorm(x) * g + b) on rows x [n][w] (w % 64 == 0, w <= 1024), the LayerNorm + SiLU of the
    Q/K head (final_linear of SO3_Linear2Scalar_e2former, module_utils.py:2230-2233,2268); stats [n][2] =
    (mean, rstd) kept for the backward, which returns the input gradient only. */

@@ -501,3 +501,57 @@ def test_qk_proj_fused(pkg, cuda, n, with_v, with_bias):
     print(f"[qk_proj] n={n} y {e_y:.2e} hq {e_q:.2e} hk {e_k:.2e} gx {e_g:.2e}", flush=True)
     assert e_y < 2e-5 and e_q < 2e-5 and e_k < 2e-5
     assert e_g < 1e-4
+
+
+@pytest.mark.parametrize("n,with_v", [(1, True), (300, False), (1000, True)])
+def test_qk_proj_fused_bf16(pkg, cuda, n, with_v):
+    """bf16-operand form of the fused projection against float64 GEMMs of the
+    bf16-rounded operands.  Tolerances: y is stored in bf16 (2^-9 relative, test
+    4e-3); hq / hk come from the fp32 accumulators (1e-4); the backward rounds its
+    formed gradient operand to bf16 (1e-2)."""
+    from ubio_molfm_amd import _lib
+    torch.manual_seed(11)
+    hid, C, Cv = 512, 256, 256
+    print(f"[qk_proj bf16] n={n} with_v={with_v}", flush=True)
+    bf = torch.bfloat16
+    x = torch.randn(9, n, C, device=cuda)
+    W = (torch.randn(3, 4 * hid, C, device=cuda) / 16).to(bf)
+    Wv = (torch.randn(3, Cv, C, device=cuda) / 16).to(bf)
+    bias = torch.randn(4 * hid, device=cuda)
+    Wt = W.transpose(1, 2).contiguous(); Wvt = Wv.transpose(1, 2).contiguous()
+    y = torch.empty(9, n, 4 * hid, device=cuda, dtype=bf)
+    hq = torch.empty(n, 3 * hid, device=cuda); hk = torch.empty_like(hq)
+    st = _lib.vp(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: _lib.vp(t.data_ptr() if t is not None else 0)
+    _lib.call("e2v2_qk_proj_fwd_bf16", p(x), p(W), p(bias), p(y), p(hq), p(hk), _lib.i32(n), _lib.i32(hid),
+              _lib.i32(C), st)
+    idx = torch.tensor([0, 1, 1, 1, 2, 2, 2, 2, 2], device=cuda)
+    xr = x.to(bf).double()
+    yd = torch.bmm(xr, Wt.double()[idx])
+    yd[0] += bias.double()
+    L = [slice(0, 1), slice(1, 4), slice(4, 9)]
+    a_q, b_q, a_k, b_k = yd.split(hid, dim=2)
+    hqd = torch.cat([(a_q[s] * b_q[s]).sum(0) for s in L], dim=1)
+    hkd = torch.cat([(a_k[s] * b_k[s]).sum(0) for s in L], dim=1)
+    e_y, e_q, e_k = relerr(y.float(), yd), relerr(hq, hqd), relerr(hk, hkd)
+    ghq = torch.randn(n, 3 * hid, device=cuda); ghk = torch.randn(n, 3 * hid, device=cuda)
+    gv = torch.randn(9, n, Cv, device=cuda) if with_v else None
+    gx = torch.empty(9, n, C, device=cuda)
+    _lib.call("e2v2_qk_proj_bwd_bf16", p(y), p(ghq), p(ghk), p(Wt), p(gv), p(Wvt if with_v else None), p(gx),
+              _lib.i32(n), _lib.i32(hid), _lib.i32(C), _lib.i32(Cv if with_v else 0), st)
+    yy = y.double()
+    gyd = torch.empty_like(yy)
+    gq3 = ghq.double().view(n, 3, hid); gk3 = ghk.double().view(n, 3, hid)
+    for m in range(9):
+        l = 0 if m == 0 else (1 if m < 4 else 2)
+        gyd[m, :, :hid] = gq3[:, l] * yy[m, :, hid:2 * hid]
+        gyd[m, :, hid:2 * hid] = gq3[:, l] * yy[m, :, :hid]
+        gyd[m, :, 2 * hid:3 * hid] = gk3[:, l] * yy[m, :, 3 * hid:]
+        gyd[m, :, 3 * hid:] = gk3[:, l] * yy[m, :, 2 * hid:3 * hid]
+    gxd = torch.bmm(gyd, W.double()[idx])
+    if with_v:
+        gxd = gxd + torch.bmm(gv.to(bf).double(), Wv.double()[idx])
+    e_g = relerr(gx, gxd)
+    print(f"[qk_proj bf16] n={n} y {e_y:.2e} hq {e_q:.2e} hk {e_k:.2e} gx {e_g:.2e}", flush=True)
+    assert e_y < 4e-3 and e_q < 1e-4 and e_k < 1e-4
+    assert e_g < 1e-2

@@ -18,6 +18,7 @@ EXPORTS = [
     "e2v2_mlp_rbf_table_size", "e2v2_mlp_rbf_table", "e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
     "e2v2_edge_to_pos", "e2v2_mlp_bwd_deg", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd", "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd", "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd",
+    "e2v2_qk_proj_fwd_bf16", "e2v2_qk_proj_bwd_bf16",
 ]
 
 

@@ -103,11 +103,12 @@ class MRowWeight:
     """Per-l weight W [lmax+1, O, Cin] of an SO(3) linear as GEMM operands: ``w``
     for per-l GEMMs (fp32, or a bf16 copy), and in fp32 its per-m-row expansions
     for one batched GEMM over the (lmax+1)^2 m-rows (one launch instead of lmax+1,
-    fewer partial tiles): ``fwd`` [M, Cin, O] and ``bwd`` [M, O, Cin]."""
-    __slots__ = ("w", "fwd", "bwd")
+    fewer partial tiles): ``fwd`` [M, Cin, O] and ``bwd`` [M, O, Cin]; in bf16 the
+    per-l transpose ``wt`` [lmax+1, Cin, O] (B operand of the fused projection's backward)."""
+    __slots__ = ("w", "fwd", "bwd", "wt")
 
-    def __init__(self, w, fwd=None, bwd=None):
-        self.w, self.fwd, self.bwd = w, fwd, bwd
+    def __init__(self, w, fwd=None, bwd=None, wt=None):
+        self.w, self.fwd, self.bwd, self.wt = w, fwd, bwd, wt
 
 
 def _m_index(lmax: int, device):
@@ -118,7 +119,10 @@ def mrow_weight(owner, name: str, w, bf16: bool, lmax: int):
     """MRowWeight of the weight tensor w (a parameter of ``owner`` or a tensor built
     from its parameters; cached under ``name`` until w changes)."""
     if bf16:
-        return cached(owner, name + "_mrow_bf16", (w,), lambda: MRowWeight(w.detach().to(BF16).contiguous()))
+        def build_bf16():
+            wb = w.detach().to(BF16).contiguous()
+            return MRowWeight(wb, wt=wb.transpose(1, 2).contiguous())
+        return cached(owner, name + "_mrow_bf16", (w,), build_bf16)
 
     def build():
         wd = w.detach()
@@ -183,14 +187,20 @@ class SO3LinearFn(torch.autograd.Function):
         return gx, None, None, None, (gy if ctx.has_res else None)
 
 
-def _qk_fused(Wop: MRowWeight, Wvop, C: int, hid: int, lmax: int) -> bool:
-    """The fused HIP projection (``e2v2_qk_proj_fwd/bwd``) covers fp32 weights with
-    per-m expansions, lmax 2, C a multiple of 128, hid of 64 and the value width of 32."""
-    ok = (Wop.fwd is not None and Wop.w.dtype == torch.float32 and lmax == 2 and C % 128 == 0
-          and hid % 64 == 0)
-    if Wvop is not None:
-        ok = ok and Wvop.fwd is not None and Wvop.fwd.shape[2] % 32 == 0
-    return ok
+def _qk_fused(x, Wop: MRowWeight, Wvop, C: int, hid: int, lmax: int):
+    """Which fused HIP projection covers this call: "fp32" (``e2v2_qk_proj_fwd/bwd``:
+    fp32 weights with per-m expansions) or "bf16" (``e2v2_qk_proj_*_bf16``: bf16
+    weights with per-l transposes), for an fp32 input, lmax 2, C a multiple of 128,
+    hid of 64 and a value width of 64; else None (per-l GEMMs + pair-dot kernels)."""
+    if not (x.dtype == torch.float32 and lmax == 2 and C % 128 == 0 and hid % 64 == 0):
+        return None
+    if Wop.fwd is not None and Wop.w.dtype == torch.float32:
+        if Wvop is None or (Wvop.fwd is not None and Wvop.fwd.shape[2] % 64 == 0):
+            return "fp32"
+    if Wop.wt is not None and Wop.w.dtype == BF16:
+        if Wvop is None or (Wvop.wt is not None and Wvop.wt.shape[2] % 64 == 0):
+            return "bf16"
+    return None
 
 
 class QKProjFn(torch.autograd.Function):
@@ -206,14 +216,16 @@ class QKProjFn(torch.autograd.Function):
         x = x.contiguous()
         L2, N, C = x.shape
         W = Wop.w
-        fused = _qk_fused(Wop, Wvop, C, hid, lmax)
+        fused = _qk_fused(x, Wop, Wvop, C, hid, lmax)
         ctx.fused = fused
         if fused:
-            # projection GEMM with the m-contraction on its accumulators (HIP, MFMA)
-            y = x.new_empty(L2, N, 4 * hid)
+            # projection GEMM with the m-contraction on its accumulators (HIP, MFMA);
+            # the bf16 form rounds x while staging it and keeps y in bf16
+            y = x.new_empty(L2, N, 4 * hid, dtype=BF16 if fused == "bf16" else torch.float32)
             hq = x.new_empty(N, 3 * hid); hk = x.new_empty(N, 3 * hid)
-            _lib.call("e2v2_qk_proj_fwd", _dp(x), _dp(W), _lib.vp(bias.data_ptr() if bias is not None else 0),
-                      _dp(y), _dp(hq), _dp(hk), _lib.i32(N), _lib.i32(hid), _lib.i32(C), _stream())
+            _lib.call("e2v2_qk_proj_fwd" if fused == "fp32" else "e2v2_qk_proj_fwd_bf16", _dp(x), _dp(W),
+                      _lib.vp(bias.data_ptr() if bias is not None else 0), _dp(y), _dp(hq), _dp(hk),
+                      _lib.i32(N), _lib.i32(hid), _lib.i32(C), _stream())
         elif Wop.fwd is not None:
             y = _mrow_gemm(x, Wop, bias)
         else:
@@ -260,13 +272,15 @@ class QKProjFn(torch.autograd.Function):
             # gy = the m-contraction's gradient, formed while the GEMM stages it; the
             # value projection's gradient gv W_v enters as further K stages
             C = Wop.w.shape[2]
-            gx = y.new_empty(L2, N, C)
+            gx = y.new_empty(L2, N, C, dtype=torch.float32)
             with_v = Wvop is not None and gv is not None
-            gvc = gv.contiguous() if with_v else None
-            _lib.call("e2v2_qk_proj_bwd", _dp(y), _dp(ghq), _dp(ghk), _dp(Wop.fwd),
-                      _lib.vp(gvc.data_ptr() if with_v else 0), _lib.vp(Wvop.fwd.data_ptr() if with_v else 0),
-                      _dp(gx), _lib.i32(N), _lib.i32(hid), _lib.i32(C),
-                      _lib.i32(Wvop.fwd.shape[2] if with_v else 0), _stream())
+            gvc = gv.float().contiguous() if with_v else None
+            bt = Wop.fwd if ctx.fused == "fp32" else Wop.wt            # [M or lmax+1, C, 4 hid]
+            bvt = (Wvop.fwd if ctx.fused == "fp32" else Wvop.wt) if with_v else None
+            _lib.call("e2v2_qk_proj_bwd" if ctx.fused == "fp32" else "e2v2_qk_proj_bwd_bf16", _dp(y), _dp(ghq),
+                      _dp(ghk), _dp(bt), _lib.vp(gvc.data_ptr() if with_v else 0),
+                      _lib.vp(bvt.data_ptr() if with_v else 0), _dp(gx), _lib.i32(N), _lib.i32(hid), _lib.i32(C),
+                      _lib.i32(bvt.shape[2] if with_v else 0), _stream())
             return gx, None, None, None, None, None, None
         gy = torch.empty_like(y)
         _lib.call("e2v2_pairdot_bwd", _dp(y), _dp(ghq), _dp(ghk), _dp(gy), _lib.i32(N), _lib.i32(hid), _stream())
