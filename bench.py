@@ -108,33 +108,54 @@ def traffic_from_profile(entry, bf16=False):
     return sum(found.values()) if len(found) == len(ks) else None
 
 
-def cpu_baseline(pkg):
-    """Oracle (restated reference path, torch CPU fp32) on a 300-atom periodic
-    water/protein mix built by the configs[3] recipe (same density and element
-    ratios): repeated energy+force evaluations for at least 10 s (bounded at 20)
-    after a warm-up on a 12-atom cell."""
+def cpu_baseline(pkg, config: int = 4, n_edges_gpu: float = 0.0):
+    """The restated reference path (oracle/, torch CPU fp32) timed on the host
+    cores, repeated for at least 10 s (bounded at 20 evaluations) after a warm-up
+    on a 12-atom cell, with the exact cell-list neighbour list.  Bounded samples of
+    each workload (a full configs[0] evaluation takes about 90 s on 8 cores):
+    config 1: a 64-molecule water box at the same density; config 2: the full
+    64-molecule batch, graph by graph; configs 3 and 4: a 300-atom periodic
+    water/protein mix built by their recipe (same density and element ratios);
+    config 5: not run (about 9 minutes per evaluation), None."""
     import numpy as np
     import torch
     from ubio_molfm_amd import systems
     from oracle.model import MolfmAtomic as OracleModel
     from oracle.cpu_path import energy_forces_with_neighbors
+    if config == 5:
+        return None
     cores = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(cores)
     torch.manual_seed(0)
     om = OracleModel().eval()
     energy_forces_with_neighbors(om, systems.small_water(4, 5.5, seed=1))
-    sysd = systems.solvated_chains(300, seed=0)
+    if config in (3, 4):
+        graphs = [systems.solvated_chains(300, seed=0)]
+        what = f"300-atom periodic water/protein mix (configs[{config - 1}] recipe, {{e}} edges)"
+    elif config == 1:
+        graphs = [systems.water_box(64, 18.64 * (64 / 216) ** (1 / 3), seed=0)]
+        what = "64-molecule periodic water box at the configs[0] density ({e} edges)"
+    else:
+        full = systems.CONFIGS[config]()
+        ptr = np.asarray(full["graph_ptr"])
+        graphs = [dict(pos=full["pos"][ptr[g]:ptr[g + 1]], Z=full["Z"][ptr[g]:ptr[g + 1]],
+                       graph_ptr=np.array([0, ptr[g + 1] - ptr[g]]), cell=full["cell"][g:g + 1],
+                       pbc=full["pbc"][g:g + 1], name=full["name"]) for g in range(len(ptr) - 1)]
+        what = (f"the full configs[{config - 1}] system ({len(full['pos'])} atoms in {len(graphs)} graph(s), "
+                "{e} edges, fp32)")
+
+    def run():
+        return sum(energy_forces_with_neighbors(om, g)[2] for g in graphs)
     reps, edges_total = 0, 0
     t0 = time.perf_counter()
     while reps < 20 and (reps == 0 or time.perf_counter() - t0 < 10.0):
-        e, f, n_edges = energy_forces_with_neighbors(om, sysd)
+        n_edges = run()
         reps += 1
         edges_total += n_edges
     t = time.perf_counter() - t0
     return {"value": edges_total / t, "unit": "edges/s", "cores": cores, "kind": "port",
-            "sample": f"300-atom periodic water/protein mix (configs[3] recipe, {n_edges} edges): {reps} fp32 "
-                      f"energy+force evaluations (neighbour build included) of the restated reference path "
-                      f"(oracle/, torch CPU) after a warm-up; {t:.1f} s"}
+            "sample": what.format(e=n_edges) + f": {reps} energy+force evaluations (neighbour build included) of "
+                      f"the restated reference path (oracle/, torch CPU) after a warm-up; {t:.1f} s"}
 
 
 def main():
@@ -260,8 +281,8 @@ def main():
                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                          "frac": round(hb_bytes / hb_time / 1e9 / HBM_PEAK_GBS, 4)}
     cpu = None
-    if not args.no_cpu_baseline and args.config == 4:
-        cpu = cpu_baseline(pkg)
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(pkg, args.config, E_mean)
     out = {
         "metric": "attn edges/s fwd+force-bwd & MD atom-steps/s at 10k atoms; % HBM roofline",
         "value": E_mean * args.steps / dt,
