@@ -34,7 +34,8 @@ def load_package():
     return mod
 
 
-# algorithmic work per launch of each library entry point
+# algorithmic work per launch of each library entry point: reference-formulation FLOPs for
+# the radial MLPs, compulsory bytes for the gather kernels
 def mlp_fwd_flops(E, n_mlp):
     return 2.0 * E * n_mlp * (256 * 128 + 128 * 128 + 128 * 256)
 
@@ -175,8 +176,8 @@ def main():
                     help="run one plain 256 MiB device copy first (scale reference for FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is described in DESIGN.md "
-                                   "and not launched", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU: the spatial sharding over several GPUs is "
+                                   "designed but not launched", "n_gpus": args.gpus}))
         sys.exit(2)
     import numpy as np
     import torch
