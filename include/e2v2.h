@@ -82,7 +82,8 @@ typedef struct e2v2_nbr_plan {
   int32_t* bin_count;               /* workspace [n_bins]                                   */
   int32_t* bin_start;               /* workspace [n_bins + 1]                               */
   int32_t* bin_atoms;               /* workspace [n_atoms]                                  */
-  int32_t* stats;                   /* workspace [2] (scan total / max)                     */
+  int32_t* stats;                   /* workspace [3], zeroed by the caller: scan total / max;
+                                       [2] != 0 if an atom lies outside its graph's grid box */
 } e2v2_nbr_plan;
 
 int e2v2_nbr_bin(const e2v2_nbr_plan* plan, hipStream_t s);

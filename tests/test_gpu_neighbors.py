@@ -212,3 +212,25 @@ def test_key_csr_long_column(pkg, cuda):
     assert np.array_equal(kp.cpu().numpy(), ref_ptr.astype(np.int32))
     assert np.array_equal(ke.cpu().numpy(), order)
     assert np.array_equal(edge_row.cpu().numpy(), rows)
+
+
+@pytest.mark.parametrize("box", ["cell", "padded", "shrunk", "shifted"])
+def test_caller_grid_box_gives_same_edges(pkg, cuda, box):
+    """A caller-supplied bin grid (the MD loop passes the cell of its wrapped
+    positions) yields the same neighbour list as the read-back bounding box; a box
+    that misses atoms ("shrunk", "shifted") is detected and the list rebuilt."""
+    from ubio_molfm_amd import neighbors, systems
+    s = systems.CONFIGS[1]()
+    pos = torch.as_tensor(s["pos"], device=cuda)
+    L = np.diag(s["cell"][0]).astype(np.float32)
+    lo, hi = {"cell": (np.zeros(3, np.float32), L),
+              "padded": (-0.2 * L, 1.3 * L),
+              "shrunk": (0.3 * L, 0.6 * L),
+              "shifted": (-0.5 * L, 0.7 * L)}[box]
+    ref = neighbors.build_neighbors(pos, s["graph_ptr"], s["cell"], s["pbc"], 6.0)
+    got = neighbors.build_neighbors(pos, s["graph_ptr"], s["cell"], s["pbc"], 6.0,
+                                    grid_box=np.stack([lo, hi])[:, None, :])
+    print(f"[grid_box {box}] E={ref.n_edges}/{got.n_edges}", flush=True)
+    assert ref.n_edges == got.n_edges
+    for name in ("row_ptr", "col", "shift_idx", "dist", "dvec", "key_ptr", "key_eid"):
+        assert torch.equal(getattr(ref, name), getattr(got, name)), name

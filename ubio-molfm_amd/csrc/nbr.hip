@@ -67,6 +67,14 @@ __device__ __forceinline__ int bin_coord(float x, float lo, float h, int dim) {
   return min(max(b, 0), dim - 1);
 }
 
+// An atom outside its graph's grid box (possible only with a caller-supplied box):
+// the cell search tolerates atoms up to the bin margin (0.01 A) outside, so one
+// further out than 1e-3 A is flagged in stats[2] for the host to rebuild with
+// the atoms' own bounding box.
+__device__ __forceinline__ bool outside_box(float x, float lo, float h, int dim) {
+  return !(x >= lo - 1e-3f && x <= lo + h * (float)dim + 1e-3f);
+}
+
 __global__ void k_bin_assign(e2v2_nbr_plan P) {
   int a = blockIdx.x * blockDim.x + threadIdx.x;
   if (a >= P.n_atoms) return;
@@ -75,6 +83,10 @@ __global__ void k_bin_assign(e2v2_nbr_plan P) {
   int bx = bin_coord(p[0], P.grid_lo[3 * g + 0], P.grid_h[3 * g + 0], P.grid_dim[3 * g + 0]);
   int by = bin_coord(p[1], P.grid_lo[3 * g + 1], P.grid_h[3 * g + 1], P.grid_dim[3 * g + 1]);
   int bz = bin_coord(p[2], P.grid_lo[3 * g + 2], P.grid_h[3 * g + 2], P.grid_dim[3 * g + 2]);
+  bool out = false;
+#pragma unroll
+  for (int d = 0; d < 3; ++d) out |= outside_box(p[d], P.grid_lo[3 * g + d], P.grid_h[3 * g + d], P.grid_dim[3 * g + d]);
+  if (out) atomicOr(&P.stats[2], 1);
   int bin = P.bin_base[g] + (bx * P.grid_dim[3 * g + 1] + by) * P.grid_dim[3 * g + 2] + bz;
   P.atom_bin[a] = bin;
   atomicAdd(&P.bin_count[bin], 1);

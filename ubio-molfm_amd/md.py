@@ -45,6 +45,10 @@ class VelocityVerlet:
         self.cell = np.asarray(sysd["cell"], np.float32)
         self.wrap = wrap and bool(np.all(sysd["pbc"]))
         self.L = torch.as_tensor(np.diag(self.cell[0]).astype(np.float64), device=device)
+        # wrapped positions lie in [0, L): the neighbour grid is the cell (no bounding-box readback)
+        ortho = np.count_nonzero(self.cell[0] - np.diag(np.diag(self.cell[0]))) == 0
+        self.grid_box = (np.stack([np.zeros(3), np.diag(self.cell[0])])[:, None, :].astype(np.float32)
+                         if self.wrap and ortho else None)
         self.f = None
         self.e = None
         self.n_edges = 0
@@ -55,7 +59,7 @@ class VelocityVerlet:
 
     def forces(self):
         e, f, nl = self.model.energy_forces_flat(self.x.float(), self.Z, self.sys["graph_ptr"], self.cell,
-                                                 self.sys["pbc"])
+                                                 self.sys["pbc"], grid_box=self.grid_box)
         self.n_edges = nl.n_edges
         return e, f.double()
 

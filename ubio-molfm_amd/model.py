@@ -104,11 +104,11 @@ class E2FormerBackbone(nn.Module):
 
     # -- flat interface -------------------------------------------------------
     def forward_flat(self, pos: torch.Tensor, Z: torch.Tensor, graph_ptr, cell, pbc, charge=None,
-                     multiplicity=None, nl=None, reorder: bool = True):
+                     multiplicity=None, nl=None, reorder: bool = True, grid_box=None):
         """pos [N,3] (may require grad), Z [N] on the GPU; graph_ptr/cell/pbc on the host.
         Returns (node_irreps [N,9,C], neighbour list, perm): rows of node_irreps and
         the neighbour list refer to atoms ``perm`` (Morton order within each graph;
-        identity when ``reorder`` is False)."""
+        identity when ``reorder`` is False).  grid_box: see ``build_neighbors``."""
         perm = None
         if reorder and nl is None:
             perm = spatial_order(pos.detach(), graph_ptr)
@@ -116,7 +116,7 @@ class E2FormerBackbone(nn.Module):
             Z = Z[perm]
         if nl is None:
             nl = build_neighbors(pos.detach(), graph_ptr, cell, pbc, self.max_radius, 1e-4, self.max_neighbors,
-                                 self.cells_per_direction)
+                                 self.cells_per_direction, grid_box=grid_box)
         dvec, dist = EdgeGeometryFn.apply(pos, nl)
         node_type = Z.to(torch.int32).contiguous()
         ctx = EdgeContext(nl, dvec, dist, node_type, self.decoder.rbf, self.max_radius, self.compute_bf16)
@@ -217,8 +217,10 @@ class MolfmAtomic(nn.Module):
         self.decoder = E2FormerBackbone(**cfg)
         self.head = MDEnergyForceMultiHead(args)
 
-    def energy_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None, nl=None):
-        x, nl, _ = self.decoder.forward_flat(pos, Z, graph_ptr, cell, pbc, charge, multiplicity, nl)
+    def energy_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None, nl=None,
+                    grid_box=None):
+        x, nl, _ = self.decoder.forward_flat(pos, Z, graph_ptr, cell, pbc, charge, multiplicity, nl,
+                                             grid_box=grid_box)
         h = self.head.head_name(head)
         e_atom = self.head.energy_heads[h](x[0]).squeeze(-1)     # x is m-major [9, N, C]
         B = len(graph_ptr) - 1
@@ -229,9 +231,10 @@ class MolfmAtomic(nn.Module):
             energy = torch.segment_reduce(e_atom, "sum", lengths=counts, axis=0, unsafe=True)
         return energy, nl
 
-    def energy_forces_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None):
+    def energy_forces_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None,
+                           grid_box=None):
         pos = pos.detach().float().requires_grad_(True)
-        energy, nl = self.energy_flat(pos, Z, graph_ptr, cell, pbc, head, charge, multiplicity)
+        energy, nl = self.energy_flat(pos, Z, graph_ptr, cell, pbc, head, charge, multiplicity, grid_box=grid_box)
         forces = -torch.autograd.grad(energy, pos, torch.ones_like(energy))[0]
         return energy.detach(), forces, nl
 

@@ -104,9 +104,15 @@ def _ptr(t: Optional[torch.Tensor]):
 
 
 def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
-                    max_neighbors: Optional[int] = None, cells_per_direction: int = 4) -> NeighborList:
+                    max_neighbors: Optional[int] = None, cells_per_direction: int = 4,
+                    grid_box=None) -> NeighborList:
     """pos [N,3] fp32 on the GPU (graphs contiguous); graph_ptr [B+1], cells
-    [B,3,3], pbcs [B,3] on the host."""
+    [B,3,3], pbcs [B,3] on the host.  grid_box [2,B,3] (optional, host): per-graph
+    (lo, hi) corners of the bin grid that contain every atom, e.g. the cell of
+    positions wrapped into it; without it the atoms' bounding boxes are read back
+    (one host sync).  The edge list does not depend on the grid.  An atom outside
+    the supplied box is detected on the device (read back with the edge count)
+    and the list is rebuilt with the bounding boxes."""
     if not pos.is_cuda:
         raise RuntimeError("build_neighbors runs on the GPU only (pos must be a CUDA/HIP tensor)")
     dev = pos.device
@@ -118,8 +124,10 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     B = len(graph_ptr) - 1
     stream = torch.cuda.current_stream(dev).cuda_stream
     i32 = dict(dtype=torch.int32, device=dev)
-    # per-graph bounding boxes (one host sync)
-    if N:
+    # per-graph bounding boxes (one host sync unless the caller supplies the grid box)
+    if grid_box is not None:
+        bb = np.asarray(grid_box, F32).reshape(2, B, 3)
+    elif N:
         if B == 1:
             lo, hi = pos.amin(0, keepdim=True), pos.amax(0, keepdim=True)
         else:
@@ -167,7 +175,7 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     bin_count = torch.empty(nb, **i32)
     bin_start = torch.empty(nb + 1, **i32)
     bin_atoms = torch.empty(max(N, 1), **i32)
-    stats = torch.zeros(2, **i32)
+    stats = torch.zeros(3, **i32)
     plan = _lib.NbrPlan(N, B, nb, len(offs), rc, rmin, pos.data_ptr(), atom_graph.data_ptr(), t_gptr.data_ptr(),
                         t_sptr.data_ptr(), t_per.data_ptr(), t_off.data_ptr(), t_lo.data_ptr(), t_h.data_ptr(),
                         t_dim.data_ptr(), t_base.data_ptr(), atom_bin.data_ptr(), bin_count.data_ptr(),
@@ -177,7 +185,11 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     row_ptr = torch.empty(N + 1, **i32)
     _lib.call("e2v2_nbr_count", _lib.C.byref(plan), _lib.vp(row_count.data_ptr()), _lib.vp(row_ptr.data_ptr()),
               _lib.vp(stream))
-    E, max_row = (int(x) for x in stats.cpu())
+    E, max_row, outside = (int(x) for x in stats.cpu())
+    if outside:
+        if grid_box is None:
+            raise RuntimeError("neighbour build: an atom lies outside its own bounding box")
+        return build_neighbors(pos, graph_ptr, cells, pbcs, rc, rmin, max_neighbors, cells_per_direction)
     f32t = dict(dtype=torch.float32, device=dev)
     tcol = torch.empty(max(E, 1), **i32); tsh = torch.empty(max(E, 1), **i32)
     tdv = torch.empty(max(E, 1), 3, **f32t); td = torch.empty(max(E, 1), **f32t)
@@ -195,7 +207,7 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
         _lib.call("e2v2_nbr_topk", _lib.vp(row_ptr.data_ptr()), _lib.i32(N), _lib.i32(int(max_neighbors)),
                   _lib.vp(cnt.data_ptr()), _lib.vp(new_ptr.data_ptr()), _lib.vp(stats.data_ptr()),
                   None, None, None, None, None, None, None, None, _lib.i32(0), _lib.vp(stream))
-        E2, max_row = (int(x) for x in stats.cpu())
+        E2, max_row = (int(x) for x in stats[:2].cpu())
         col2 = torch.empty(E2, **i32); sh2 = torch.empty(E2, **i32)
         dv2 = torch.empty(E2, 3, **f32t); d2 = torch.empty(E2, **f32t)
         _lib.call("e2v2_nbr_topk", _lib.vp(row_ptr.data_ptr()), _lib.i32(N), _lib.i32(int(max_neighbors)),
