@@ -16,9 +16,10 @@
 // A operand is staged, so it is never written; optionally + sum_j gv[m][n][j] Wv_l[j][k]
 // (the value projection's input gradient, same x) as further K stages.
 //
-// Tiling: 128 nodes x 128 GEMM columns per workgroup, four wavefronts of 64 x 64
-// (2 x 2 tiles of v_mfma_f32_32x32x2f32), K staged through LDS 32 at a time in two
-// buffers (32 KB each).  In LDS a row keeps its 32 k as eight 16-byte granules,
+// Tiling: 128 nodes x 128 GEMM columns per workgroup, eight wavefronts of 32 x 64
+// (4 x 2; two 32x32 tiles of v_mfma_f32_32x32x2f32 each, at most 128 VGPRs so that
+// two workgroups, four waves per SIMD, share a CU), K staged through LDS 32 at a
+// time in two buffers (32 KB each).  In LDS a row keeps its 32 k as eight 16-byte granules,
 // granule g of row r at slot g ^ (r & 7), so the eight lanes of a 128-byte
 // ds_read_b128 phase read eight different bank groups.  An MFMA k-step s of an
 // 8-k group takes k = 4 (lane / 32) + s in both operands: one 16-byte LDS read per
@@ -32,9 +33,9 @@ constexpr int kPjRows = 128;                    // nodes per workgroup
 constexpr int kPjCols = 128;                    // GEMM columns per workgroup
 constexpr int kPjK = 32;                        // K per LDS stage (16 or 32)
 constexpr int kPjG = kPjK / 4;                  // 16-byte granules per row and stage
-constexpr int kPjPer = kPjRows * kPjG / 256;    // granules per thread and operand
+constexpr int kPjT = 512;                       // threads per workgroup (8 waves, 4 x 2)
+constexpr int kPjPer = kPjRows * kPjG / kPjT;    // granules per thread and operand
 constexpr int kPjStage = (kPjRows + kPjCols) * kPjK;  // floats per stage buffer
-constexpr int kPjWgPerCu = kPjK == 16 ? 3 : 2;  // LDS: 2 stages of 16 or 32 KB
 
 __device__ __forceinline__ int pj_l(int m) { return m == 0 ? 0 : (m < 4 ? 1 : 2); }
 // LDS float offset of granule g of row r: 128-byte lines of 8 granules (one row of
@@ -44,26 +45,29 @@ __device__ __forceinline__ int pj_slot(int r, int g) {
   return (r >> 1) * 32 + (((((r & 1) << 2) | g) ^ ((r >> 1) & 7)) << 2);
 }
 
-// 32 k of one stage: four 8-k groups, each four k-steps on the 2 x 2 tiles of the wave.
+// kPjK k of one stage: 8-k groups, each four k-steps on the wave's 1 x 2 tiles (rows
+// 32 wr.., columns 64 wc + 32 j..).
 __device__ __forceinline__ void pj_mma(const float* __restrict__ As, const float* __restrict__ Bs,
-                                       floatx16 (&acc)[2][2], int wr, int wc, int lane) {
-  const int r0 = wr * 64 + (lane & 31), c0 = wc * 64 + (lane & 31), h = lane >> 5;
+                                       floatx16 (&acc)[2], int wr, int wc, int lane) {
+  const int r0 = wr * 32 + (lane & 31), c0 = wc * 64 + (lane & 31), h = lane >> 5;
 #pragma unroll
   for (int grp = 0; grp < kPjK / 8; ++grp) {
-    floatx4 a[2], b[2];
+    const floatx4 a = *reinterpret_cast<const floatx4*>(As + pj_slot(r0, 2 * grp + h));
+    floatx4 b[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      a[i] = *reinterpret_cast<const floatx4*>(As + pj_slot(r0 + 32 * i, 2 * grp + h));
-      b[i] = *reinterpret_cast<const floatx4*>(Bs + pj_slot(c0 + 32 * i, 2 * grp + h));
-    }
+    for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const floatx4*>(Bs + pj_slot(c0 + 32 * j, 2 * grp + h));
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[j][s], acc[j], 0, 0, 0);
   }
+}
+
+__device__ __forceinline__ void pj_zero(floatx16 (&acc)[2]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
 }
 
 __device__ __forceinline__ void pj_zero(floatx16 (&acc)[2][2]) {
@@ -86,7 +90,7 @@ __device__ __forceinline__ int pj_pair_col(int p, int ab, int hid) {
   return p < hid ? (ab ? hid + p : p) : (ab ? 2 * hid + p : hid + p);
 }
 
-__global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_fwd(const float* __restrict__ x, const float* __restrict__ w,
+__global__ __launch_bounds__(kPjT) __attribute__((amdgpu_waves_per_eu(4))) void k_qk_proj_fwd(const float* __restrict__ x, const float* __restrict__ w,
                                                         const float* __restrict__ bias, float* __restrict__ y,
                                                         float* __restrict__ hq, float* __restrict__ hk, int n,
                                                         int hid, int c) {
@@ -101,13 +105,13 @@ __global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_fwd(const float* __
   const int row0 = (tile / n_cb) * kPjRows, p0 = (tile % n_cb) * 64;
   const int O = 4 * hid, nk = c / kPjK, m0 = L * L, n_it = (2 * L + 1) * nk;
 
-  // staging assignment: granule g of rows / columns t / kPjG + (256 / kPjG) i
+  // staging assignment: granule g of rows / columns t / kPjG + (kPjT / kPjG) i
   const int g = t % kPjG;
   int a_row[kPjPer], b_col[kPjPer];
 #pragma unroll
   for (int i = 0; i < kPjPer; ++i) {
-    a_row[i] = row0 + t / kPjG + (256 / kPjG) * i;
-    const int cl = t / kPjG + (256 / kPjG) * i;
+    a_row[i] = row0 + t / kPjG + (kPjT / kPjG) * i;
+    const int cl = t / kPjG + (kPjT / kPjG) * i;
     b_col[i] = pj_pair_col(p0 + 32 * (cl >> 6) + (cl & 31), (cl >> 5) & 1, hid);
   }
   // 32-bit element offsets from wave-uniform bases (per m / per l)
@@ -134,7 +138,7 @@ __global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_fwd(const float* __
     float* Bs = As + kPjRows * kPjK;
 #pragma unroll
     for (int i = 0; i < kPjPer; ++i) {
-      const int r = t / kPjG + (256 / kPjG) * i;
+      const int r = t / kPjG + (kPjT / kPjG) * i;
       *reinterpret_cast<floatx4*>(As + pj_slot(r, g)) = R.a[i];
       *reinterpret_cast<floatx4*>(Bs + pj_slot(r, g)) = R.b[i];
     }
@@ -144,18 +148,16 @@ __global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_fwd(const float* __
   // first accumulator row is erow, register (i, r) adds pj_acc_row(r, 0) + 32 i
   const int p = p0 + 32 * wc + (lane & 31);
   const int oa = pj_pair_col(p, 0, hid), ob = pj_pair_col(p, 1, hid);
-  const int erow = row0 + wr * 64 + 4 * (lane >> 5);
+  const int erow = row0 + wr * 32 + 4 * (lane >> 5);
   const uint32_t y_off = (uint32_t)erow * O + oa, h_off = (uint32_t)erow * 3 * hid + (p < hid ? p : p - hid);
   float* hbase = p < hid ? hq : hk;
   const float ba = bias ? bias[oa] : 0.f, bb = bias ? bias[ob] : 0.f;
 
-  floatx16 acc[2][2];
+  floatx16 acc[2];   // the a- and b-columns of the wave's 32 channels
   pj_zero(acc);
-  float s[2][16];
+  float s[16];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[i][r] = 0.f;
+  for (int r = 0; r < 16; ++r) s[r] = 0.f;
 
   // stages: LDS buffer it & 1; the next stage's global loads are in flight during the MFMAs
   Regs R;
@@ -171,29 +173,25 @@ __global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_fwd(const float* __
       const float a0 = m == 0 ? ba : 0.f, b0 = m == 0 ? bb : 0.f;
       float* ym = y + (size_t)m * n * O;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dr = 32 * i + pj_acc_row(r, 0);
-          const float va = acc[i][0][r] + a0, vb = acc[i][1][r] + b0;
-          s[i][r] = fmaf(va, vb, s[i][r]);
-          if (erow + dr < n) {
-            float* yr = ym + (size_t)dr * O;
-            yr[y_off] = va;
-            yr[y_off + (ob - oa)] = vb;
-          }
+      for (int r = 0; r < 16; ++r) {
+        const int dr = pj_acc_row(r, 0);
+        const float va = acc[0][r] + a0, vb = acc[1][r] + b0;
+        s[r] = fmaf(va, vb, s[r]);
+        if (erow + dr < n) {
+          float* yr = ym + (size_t)dr * O;
+          yr[y_off] = va;
+          yr[y_off + (ob - oa)] = vb;
         }
+      }
       pj_zero(acc);
       if (it == n_it - 1) {
         float* hl = hbase + L * hid;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int dr = 32 * i + pj_acc_row(r, 0);
-            if (erow + dr < n) hl[(size_t)dr * 3 * hid + h_off] = s[i][r];
-            s[i][r] = 0.f;
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int dr = pj_acc_row(r, 0);
+          if (erow + dr < n) hl[(size_t)dr * 3 * hid + h_off] = s[r];
+          s[r] = 0.f;
+        }
       }
     }
     if (it + 1 < n_it) store(it + 1, R);
@@ -205,7 +203,7 @@ __global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_fwd(const float* __
 // Backward.  Workgroup tile: m-row m, nodes row0 .. row0+127, input channels
 // k0 .. k0+127.  K stages: the 4 hid columns of gy (formed from y and ghq/ghk),
 // then the cv columns of gv when given.
-__global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_bwd(const float* __restrict__ y, const float* __restrict__ ghq,
+__global__ __launch_bounds__(kPjT) __attribute__((amdgpu_waves_per_eu(4))) void k_qk_proj_bwd(const float* __restrict__ y, const float* __restrict__ ghq,
                                                         const float* __restrict__ ghk,
                                                         const float* __restrict__ wt,
                                                         const float* __restrict__ gv,
@@ -226,12 +224,12 @@ __global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_bwd(const float* __
   uint32_t y_off[kPjPer], g_off[kPjPer], v_off[kPjPer], b_off[kPjPer], bv_off[kPjPer];
 #pragma unroll
   for (int i = 0; i < kPjPer; ++i) {
-    a_row[i] = row0 + t / kPjG + (256 / kPjG) * i;
+    a_row[i] = row0 + t / kPjG + (kPjT / kPjG) * i;
     y_off[i] = (uint32_t)a_row[i] * O + 4 * g;
     g_off[i] = (uint32_t)a_row[i] * 3 * hid + 4 * g;
     v_off[i] = (uint32_t)a_row[i] * cv + 4 * g;
-    b_off[i] = (uint32_t)(col0 + t / kPjG + (256 / kPjG) * i) * O + 4 * g;
-    bv_off[i] = (uint32_t)(col0 + t / kPjG + (256 / kPjG) * i) * cv + 4 * g;
+    b_off[i] = (uint32_t)(col0 + t / kPjG + (kPjT / kPjG) * i) * O + 4 * g;
+    bv_off[i] = (uint32_t)(col0 + t / kPjG + (kPjT / kPjG) * i) * cv + 4 * g;
   }
   const float* ym = y + (size_t)m * n * O;
   const float* wt_m = wt + (size_t)m * c * O;
@@ -266,13 +264,13 @@ __global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_bwd(const float* __
     float* Bs = As + kPjRows * kPjK;
 #pragma unroll
     for (int i = 0; i < kPjPer; ++i) {
-      const int r = t / kPjG + (256 / kPjG) * i;
+      const int r = t / kPjG + (kPjT / kPjG) * i;
       *reinterpret_cast<floatx4*>(As + pj_slot(r, g)) = R.a[i] * R.g[i];
       *reinterpret_cast<floatx4*>(Bs + pj_slot(r, g)) = R.b[i];
     }
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[2];
   pj_zero(acc);
   // stages: LDS buffer it & 1; the next stage's global loads are in flight during the MFMAs
   Regs R;
@@ -287,16 +285,14 @@ __global__ __launch_bounds__(256, kPjWgPerCu) void k_qk_proj_bwd(const float* __
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = row0 + wr * 64 + 32 * i + pj_acc_row(r, lane);
-      if (row < n) {
-        float* gr = gx + ((size_t)m * n + row) * c + col0 + wc * 64 + (lane & 31);
-        gr[0] = acc[i][0][r];
-        gr[32] = acc[i][1][r];
-      }
+  for (int r = 0; r < 16; ++r) {
+    const int row = row0 + wr * 32 + pj_acc_row(r, lane);
+    if (row < n) {
+      float* gr = gx + ((size_t)m * n + row) * c + col0 + wc * 64 + (lane & 31);
+      gr[0] = acc[0][r];
+      gr[32] = acc[1][r];
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -562,7 +558,7 @@ E2V2_API int e2v2_qk_proj_fwd(const float* x, const float* w, const float* bias,
   E2V2_REQUIRE(n >= 0 && pj_offsets_fit(n, 4 * hid) && pj_offsets_fit(n, c), "qk_proj_fwd: n=%d too large", n);
   if (n == 0) return 0;
   const int tiles = ((n + kPjRows - 1) / kPjRows) * (2 * hid / 64);
-  hipLaunchKernelGGL(k_qk_proj_fwd, dim3(3 * xcd_grid(tiles)), dim3(256), 0, s, x, w, bias, y, hq, hk, n, hid, c);
+  hipLaunchKernelGGL(k_qk_proj_fwd, dim3(3 * xcd_grid(tiles)), dim3(kPjT), 0, s, x, w, bias, y, hq, hk, n, hid, c);
   E2V2_LAUNCHED("k_qk_proj_fwd");
   return 0;
 }
@@ -578,7 +574,7 @@ E2V2_API int e2v2_qk_proj_bwd(const float* y, const float* ghq, const float* ghk
                "qk_proj_bwd: n=%d too large", n);
   if (n == 0) return 0;
   const int tiles = 9 * ((n + kPjRows - 1) / kPjRows) * (c / kPjCols);
-  hipLaunchKernelGGL(k_qk_proj_bwd, dim3(xcd_grid(tiles)), dim3(256), 0, s, y, ghq, ghk, wt, gv, wvt, gx, n, hid, c,
+  hipLaunchKernelGGL(k_qk_proj_bwd, dim3(xcd_grid(tiles)), dim3(kPjT), 0, s, y, ghq, ghk, wt, gv, wvt, gx, n, hid, c,
                      cv);
   E2V2_LAUNCHED("k_qk_proj_bwd");
   return 0;
