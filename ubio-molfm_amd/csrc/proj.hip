@@ -301,7 +301,10 @@ __global__ __launch_bounds__(kPjT) __attribute__((amdgpu_waves_per_eu(4))) void 
 // same XOR swizzle); an MFMA step takes 16 k, granule 2 s + lane / 32 of both
 // operands.  Activations are read in fp32 and rounded to bf16 as they are staged
 // (no separate cast pass); the forward keeps y in bf16 for the backward, hq / hk
-// are formed from the fp32 accumulators.
+// are formed from the fp32 accumulators.  The backward uses the eight-wave 32 x 64
+// layout of the fp32 kernels; the forward keeps four waves of 64 x 64 (256 threads,
+// two workgroups per CU): on eight waves its staging registers and per-pair sums no
+// longer fit in 128 VGPRs and it spills.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kPbK = 64;   // bf16 K per LDS stage
 
@@ -317,7 +320,8 @@ __device__ __forceinline__ bf16x8 pb_round(floatx4 a, floatx4 b) {
   return r;
 }
 
-__device__ __forceinline__ void pb_mma(const bf16x8* __restrict__ As, const bf16x8* __restrict__ Bs,
+// 64x64 wave tile (forward, four waves of 256 threads)
+__device__ __forceinline__ void pb_mma64(const bf16x8* __restrict__ As, const bf16x8* __restrict__ Bs,
                                        floatx16 (&acc)[2][2], int wr, int wc, int lane) {
   const int r0 = wr * 64 + (lane & 31), c0 = wc * 64 + (lane & 31), h = lane >> 5;
 #pragma unroll
@@ -333,6 +337,21 @@ __device__ __forceinline__ void pb_mma(const bf16x8* __restrict__ As, const bf16
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// 32x64 wave tile (backward, eight waves of 512 threads)
+__device__ __forceinline__ void pb_mma(const bf16x8* __restrict__ As, const bf16x8* __restrict__ Bs,
+                                       floatx16 (&acc)[2], int wr, int wc, int lane) {
+  const int r0 = wr * 32 + (lane & 31), c0 = wc * 64 + (lane & 31), h = lane >> 5;
+#pragma unroll
+  for (int ks = 0; ks < kPbK / 16; ++ks) {
+    const bf16x8 a = As[pb_slot(r0, 2 * ks + h)];
+    bf16x8 b[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b[j] = Bs[pb_slot(c0 + 32 * j, 2 * ks + h)];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], acc[j], 0, 0, 0);
   }
 }
 
@@ -405,7 +424,7 @@ __global__ __launch_bounds__(256, 2) void k_qk_proj_fwd_bf16(const float* __rest
   for (int it = 0; it < n_it; ++it) {
     if (it + 1 < n_it) load(it + 1, R);
     const bf16x8* As = lds + (it & 1) * (kPjRows + kPjCols) * 8;
-    pb_mma(As, As + kPjRows * 8, acc, wr, wc, lane);
+    pb_mma64(As, As + kPjRows * 8, acc, wr, wc, lane);
     if (it % nk == nk - 1) {
       const int m = m0 + it / nk;
       const float a0 = m == 0 ? ba : 0.f, b0 = m == 0 ? bb : 0.f;
@@ -442,7 +461,7 @@ __global__ __launch_bounds__(256, 2) void k_qk_proj_fwd_bf16(const float* __rest
 
 // Backward with bf16 operands: gy formed in fp32 from the bf16 y and ghq / ghk and
 // rounded as it is staged; wt / wvt are per degree l: [3][C][4 hid] and [3][C][cv].
-__global__ __launch_bounds__(256, 2) void k_qk_proj_bwd_bf16(const __bf16* __restrict__ y,
+__global__ __launch_bounds__(kPjT) __attribute__((amdgpu_waves_per_eu(4))) void k_qk_proj_bwd_bf16(const __bf16* __restrict__ y,
                                                              const float* __restrict__ ghq,
                                                              const float* __restrict__ ghk,
                                                              const __bf16* __restrict__ wt,
@@ -460,12 +479,12 @@ __global__ __launch_bounds__(256, 2) void k_qk_proj_bwd_bf16(const __bf16* __res
   const int O = 4 * hid, nkq = O / kPbK, n_it = nkq + (gv ? cv / kPbK : 0);
 
   const int g = t & 7;
-  const int r_base = row0 + (t >> 3);                  // staged rows r_base + 32 i, i < 4
-  const uint32_t c_base = (uint32_t)(col0 + (t >> 3));  // staged columns c_base + 32 i
+  const int r_base = row0 + (t >> 3);                  // staged rows r_base + 64 i, i < 2
+  const uint32_t c_base = (uint32_t)(col0 + (t >> 3));  // staged columns c_base + 64 i
   const __bf16* ym = y + (size_t)m * n * O;
   const __bf16* wt_l = wt + (size_t)l * c * O;
   // a: the fp32 factor (g or gv); yb: 8 bf16 of y as four 32-bit words
-  struct Regs { floatx4 a[4][2]; uint4 yb[4]; bf16x8 b[4]; };
+  struct Regs { floatx4 a[2][2]; uint4 yb[2]; bf16x8 b[2]; };
   auto load = [&](int it, Regs& R) {
     if (it < nkq) {
       const int j0 = it * kPbK, q = j0 / hid;
@@ -473,28 +492,28 @@ __global__ __launch_bounds__(256, 2) void k_qk_proj_bwd_bf16(const __bf16* __res
       const float* gs = (q < 2 ? ghq : ghk) + l * hid + (j0 - q * hid) + 8 * g;
       const __bf16* wp = wt_l + j0 + 8 * g;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = r_base + 32 * i;
+      for (int i = 0; i < 2; ++i) {
+        const int row = r_base + 64 * i;
         const bool ok = row < n;
         // rows past n read row n - 1 of y (their gradient factor is 0)
         R.yb[i] = *reinterpret_cast<const uint4*>(yp + (uint32_t)min(row, n - 1) * O);
         const float* gr = gs + (uint32_t)row * 3 * hid;
         R.a[i][0] = ok ? *reinterpret_cast<const floatx4*>(gr) : floatx4{0.f, 0.f, 0.f, 0.f};
         R.a[i][1] = ok ? *reinterpret_cast<const floatx4*>(gr + 4) : floatx4{0.f, 0.f, 0.f, 0.f};
-        R.b[i] = *reinterpret_cast<const bf16x8*>(wp + (c_base + 32 * i) * O);
+        R.b[i] = *reinterpret_cast<const bf16x8*>(wp + (c_base + 64 * i) * O);
       }
     } else {
       const int j0 = (it - nkq) * kPbK;
       const float* vp = gv + (size_t)m * n * cv + j0 + 8 * g;
       const __bf16* wp = wvt + (size_t)l * c * cv + j0 + 8 * g;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = r_base + 32 * i;
+      for (int i = 0; i < 2; ++i) {
+        const int row = r_base + 64 * i;
         const bool ok = row < n;
         const float* vr = vp + (uint32_t)row * cv;
         R.a[i][0] = ok ? *reinterpret_cast<const floatx4*>(vr) : floatx4{0.f, 0.f, 0.f, 0.f};
         R.a[i][1] = ok ? *reinterpret_cast<const floatx4*>(vr + 4) : floatx4{0.f, 0.f, 0.f, 0.f};
-        R.b[i] = *reinterpret_cast<const bf16x8*>(wp + (c_base + 32 * i) * cv);
+        R.b[i] = *reinterpret_cast<const bf16x8*>(wp + (c_base + 64 * i) * cv);
       }
     }
   };
@@ -503,8 +522,8 @@ __global__ __launch_bounds__(256, 2) void k_qk_proj_bwd_bf16(const __bf16* __res
     bf16x8* Bs = As + kPjRows * 8;
     const bool gy_stage = it < nkq;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = (t >> 3) + 32 * i;
+    for (int i = 0; i < 2; ++i) {
+      const int r = (t >> 3) + 64 * i;
       floatx4 lo = R.a[i][0], hi = R.a[i][1];
       if (gy_stage) {   // bf16 -> fp32: the 16 bits are the fp32's upper half
         const uint4 w = R.yb[i];
@@ -518,7 +537,7 @@ __global__ __launch_bounds__(256, 2) void k_qk_proj_bwd_bf16(const __bf16* __res
     }
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[2];
   pj_zero(acc);
   Regs R;
   load(0, R);
@@ -532,16 +551,14 @@ __global__ __launch_bounds__(256, 2) void k_qk_proj_bwd_bf16(const __bf16* __res
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = row0 + wr * 64 + 32 * i + pj_acc_row(r, lane);
-      if (row < n) {
-        float* gr = gx + ((size_t)m * n + row) * c + col0 + wc * 64 + (lane & 31);
-        gr[0] = acc[i][0][r];
-        gr[32] = acc[i][1][r];
-      }
+  for (int r = 0; r < 16; ++r) {
+    const int row = row0 + wr * 32 + pj_acc_row(r, lane);
+    if (row < n) {
+      float* gr = gx + ((size_t)m * n + row) * c + col0 + wc * 64 + (lane & 31);
+      gr[0] = acc[0][r];
+      gr[32] = acc[1][r];
     }
+  }
 }
 
 // Staging and epilogue offsets are 32-bit element offsets from per-m bases.
@@ -605,7 +622,7 @@ E2V2_API int e2v2_qk_proj_bwd_bf16(const void* y, const float* ghq, const float*
                "qk_proj_bwd_bf16: n=%d too large", n);
   if (n == 0) return 0;
   const int tiles = 9 * ((n + kPjRows - 1) / kPjRows) * (c / kPjCols);
-  hipLaunchKernelGGL(k_qk_proj_bwd_bf16, dim3(xcd_grid(tiles)), dim3(256), 0, s, static_cast<const __bf16*>(y), ghq,
+  hipLaunchKernelGGL(k_qk_proj_bwd_bf16, dim3(xcd_grid(tiles)), dim3(kPjT), 0, s, static_cast<const __bf16*>(y), ghq,
                      ghk, static_cast<const __bf16*>(wt), gv, static_cast<const __bf16*>(wvt), gx, n, hid, c, cv);
   E2V2_LAUNCHED("k_qk_proj_bwd_bf16");
   return 0;
