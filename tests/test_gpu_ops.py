@@ -250,10 +250,12 @@ def test_attention_ragged_clusters_isolated_atoms(pkg, cuda):
         assert e < 1e-4, (name, e)
 
 
-def test_attention_bf16_storage(pkg, cuda):
+@pytest.mark.parametrize("clusters", [True, False], ids=["col_clusters", "col_rows"])
+def test_attention_bf16_storage(pkg, cuda, clusters):
     """bf16 storage of q, k, v, out and grad (fp32 math): forward within 4e-3
-    (one bf16 rounding of the output rows), gradients within 1e-2."""
-    e_f, errs = _attention_case(pkg, cuda, torch.bfloat16)
+    (one bf16 rounding of the output rows), gradients within 1e-2; the column
+    pass over key-column clusters and the one-column-per-workgroup form."""
+    e_f, errs = _attention_case(pkg, cuda, torch.bfloat16, clusters=clusters)
     assert e_f < 4e-3
     for name, e in errs.items():
         assert e < 1e-2, (name, e)

@@ -445,7 +445,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col_pair(e2v2_attn_args A, con
 }
 
 // Column pass over clusters of R consecutive key-CSR columns and one of four
-// channel groups (fp32).  Group g holds the 64 channels of heads 32g..32g+31
+// channel groups (G and q in fp32 or bf16, sums in fp32).  Group g holds the 64 channels of heads 32g..32g+31
 // (c and c + 128 share a head); the workgroups of one XCD run group by group,
 // so its L2 holds a quarter of each neighbour row at a time and the gathered
 // rows of a column window stay resident.  Wave w applies the slots s = w mod 4
@@ -454,8 +454,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col_pair(e2v2_attn_args A, con
 // LDS in a fixed order.  Every slot's G_i and q_i are loaded once and applied
 // to each column of the cluster that it joins.
 
-template <int R>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_bwd_col_grp(e2v2_attn_args A, const float* __restrict__ G,
+template <int R, typename TS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_bwd_col_grp(e2v2_attn_args A, const TS* __restrict__ G,
                                                           const float* __restrict__ w_e,
                                                           const float* __restrict__ dqk_e, float* __restrict__ dv_out,
                                                           float* __restrict__ dk_out) {
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   const int ns = A.col_n_slots[cl];
   const int32_t* __restrict__ smem = A.col_slot_member + base;
   const int32_t* __restrict__ sedge = A.col_slot_edge + base * R;
-  const float* __restrict__ Qp = static_cast<const float*>(A.q);
+  const TS* __restrict__ Qp = static_cast<const TS*>(A.q);
   float av[R][kNV];
   float ak[R][4];
 #pragma unroll
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     for (int d = 0; d < 4; ++d) ak[r][d] = 0.f;
   }
   struct Loads {
-    float g[kNT];
+    TS g[kNT];   // converted to fp32 in apply()
     float q[4];
     float w[R];
     float dq[R];
@@ -508,8 +508,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     }
   };
   auto apply = [&](int sl, const Loads& L) {
-    float dA[kNV][3];
-    tp_transpose(L.g, dA);
+    float g[kNT], dA[kNV][3];
+#pragma unroll
+    for (int z = 0; z < kNT; ++z) g[z] = static_cast<float>(L.g[z]);
+    tp_transpose(g, dA);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (ce[sl][r] >= 0) {
@@ -830,10 +832,10 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
   hipLaunchKernelGGL(k_attn_bwd_row_hp<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, dgi, ddvec, ddist, dq,
                      w_edge, dqk_edge);
   E2V2_LAUNCHED("k_attn_bwd_row");
-  if (A.col_slot_member && sizeof(TS) == 4) {
+  if (A.col_slot_member) {
     const int n_cl = (A.n_rows + 3) / 4;
-    hipLaunchKernelGGL(k_attn_bwd_col_grp<4>, dim3(xcd_grid(n_cl) * kGroups), dim3(256), 0, s, A,
-                       reinterpret_cast<const float*>(G), w_edge, dqk_edge, dv, dk);
+    hipLaunchKernelGGL((k_attn_bwd_col_grp<4, TS>), dim3(xcd_grid(n_cl) * kGroups), dim3(256), 0, s, A, G, w_edge,
+                       dqk_edge, dv, dk);
   } else if constexpr (sizeof(TS) == 2) {
     hipLaunchKernelGGL(k_attn_bwd_col_pair<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
   } else {
