@@ -617,12 +617,20 @@ __device__ __forceinline__ float wave_sum4(float v0, float v1, float v2, float v
   return dpp_row_sum16(z);
 }
 
+// One edge's gathered operands for a head, kept in the storage type until the
+// edge is applied (bf16: half the staging registers of converted values).
 template <typename TS>
 struct HeadEdge {
-  float k[kD];
-  float v0[kNV], v1[kNV];
+  TS k[kD];
+  TS v0[kNV], v1[kNV];
   float gate, ih;
 };
+__device__ __forceinline__ void load8_raw(const float* p, float (&v)[8]) { load8(p, v); }
+__device__ __forceinline__ void load8_raw(const __bf16* p, __bf16 (&v)[8]) {
+  const bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = a[i];
+}
 
 // Backward row pass, one workgroup per query row; thread t owns head h = t % 128
 // with both of its channels (h, h + 128) and the row's edges of parity t / 128.
@@ -699,13 +707,13 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
     // 32-bit per-lane byte offsets from wave-uniform bases (n_rows * kH * kD *
     // sizeof(TS) < 2^32 is checked by the host)
     const uint32_t kof = ((uint32_t)j * kH + h) * (kD * sizeof(TS));
-    load8(reinterpret_cast<const TS*>(reinterpret_cast<const char*>(Kp) + kof), X.k);
+    load8_raw(reinterpret_cast<const TS*>(reinterpret_cast<const char*>(Kp) + kof), X.k);
     const uint32_t vof = ((uint32_t)j * kC + h) * sizeof(TS);
 #pragma unroll
     for (int r = 0; r < kNV; ++r) {
       const char* vb = reinterpret_cast<const char*>(Vp + r * os);
-      X.v0[r] = f32(*reinterpret_cast<const TS*>(vb + vof));
-      X.v1[r] = f32(*reinterpret_cast<const TS*>(vb + vof + kH * sizeof(TS)));
+      X.v0[r] = *reinterpret_cast<const TS*>(vb + vof);
+      X.v1[r] = *reinterpret_cast<const TS*>(vb + vof + kH * sizeof(TS));
     }
     X.gate = A.gi[e * (2 * kH) + h];
     X.ih = A.gi[e * (2 * kH) + kH + h];
@@ -715,7 +723,10 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
     const float4 ea = er_a[slot], eb = er_b[slot];
     const float pe = ea.x, dpe = ea.y, rR = ea.z, d = ea.w;
     const float dvx = eb.x, dvy = eb.y, dvz = eb.z;
-    const float qk = half_dot(qs, X.k) + half_dot(qs + 4, X.k + 4);
+    float kf[kD];
+#pragma unroll
+    for (int q = 0; q < kD; ++q) kf[q] = f32(X.k[q]);
+    const float qk = half_dot(qs, kf) + half_dot(qs + 4, kf + 4);
     const float a = X.gate * qk;
     const float ex = expf(a - m);
     const float ee = ex * pe;
@@ -727,8 +738,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
       float u0 = 0.f, u1 = 0.f;
 #pragma unroll
       for (int r = 0; r < kNV; ++r) {
-        u0 = fmaf(dA0[r][k], X.v0[r], u0);
-        u1 = fmaf(dA1[r][k], X.v1[r], u1);
+        u0 = fmaf(dA0[r][k], f32(X.v0[r]), u0);
+        u1 = fmaf(dA1[r][k], f32(X.v1[r]), u1);
       }
       U[k] = u0 + u1;
     }
@@ -746,7 +757,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
     ntstore(dih, dgi + e * (2 * kH) + kH + h);
     ntstore(dqk, dqk_out + e * kH + h);
 #pragma unroll
-    for (int q = 0; q < kD; ++q) dqa[q] = fmaf(dqk, X.k[q], dqa[q]);
+    for (int q = 0; q < kD; ++q) dqa[q] = fmaf(dqk, kf[q], dqa[q]);
     // sums over the 64 heads of this wave; lane 16k holds the sum of value k
     const float sum = wave_sum4(w * U[0], w * U[1], w * U[2], fmaf(dpv, dpe, dR), lane);
     if ((lane & 15) == 0) part[slot][wsub][lane >> 4] = sum;
