@@ -45,24 +45,28 @@ def mlp_bwd_flops(E, n_mlp):
     return 2.0 * E * n_mlp * (256 * 128 + 128 * 128 + 128 * 256)
 
 
-def attn_fwd_bytes(N, E):
+# act = bytes per element of the attention activations q, k, v, out and grad
+# (4 in fp32, 2 in the bf16 mode); everything else is fp32 / int32 in both modes.
+def attn_fwd_bytes(N, E, act=4):
     # read q, k, v, gate|inputhead, edge (col, dvec, dist), row_ptr; write out, m, s, cnt
-    return 4.0 * (N * (128 * 8 * 2 + 9 * 256 + 20 * 256 + 3 * 128) + E * (256 + 5) + N + 1)
+    return (act * N * (128 * 8 * 2 + 9 * 256 + 20 * 256)
+            + 4.0 * (N * 3 * 128 + E * (256 + 5) + N + 1))
 
 
-def attn_bwd_bytes(N, E):
+def attn_bwd_bytes(N, E, act=4):
     # row pass: read grad, out, q, k, v, gi, m/s/cnt, edges; write dgi, ddvec, ddist, dq, w, dqk
     # column pass: read w, dqk, key CSR, grad rows, q; write dv, dk
-    row = N * (2 * 20 * 256 + 3 * 1024 + 9 * 256 + 3 * 128) + E * (256 + 5 + 256 + 4 + 2 * 128)
-    col = N * (20 * 256 + 1024 + 9 * 256 + 1024 + 2) + E * (2 * 128 + 2 + 3)
-    return 4.0 * (row + col)
+    row = (act * N * (2 * 20 * 256 + 2 * 1024 + 9 * 256)
+           + 4.0 * (N * (1024 + 3 * 128) + E * (256 + 5 + 256 + 4 + 2 * 128)))
+    col = act * N * (20 * 256 + 1024) + 4.0 * (N * (9 * 256 + 1024 + 2) + E * (2 * 128 + 2 + 3))
+    return row + col
 
 
-def deg_fwd_bytes(N, E):
+def deg_fwd_bytes(N, E, act=4):
     return 4.0 * (E * (768 + 4) + N * 9 * 256)
 
 
-def deg_bwd_bytes(N, E):
+def deg_bwd_bytes(N, E, act=4):
     # read fea, dvec, dist and the node gradient; write ddvec, ddist (the feature
     # gradient is formed inside e2v2_mlp_bwd_deg, never stored)
     return 4.0 * (E * (768 + 4 + 4) + N * 9 * 256)
@@ -92,14 +96,14 @@ KERNELS_OF = {"e2v2_mlp_fwd": ["k_mlp_fwd"], "e2v2_mlp_bwd": ["k_mlp_bwd"],
               "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"]}
 
 
-def traffic_from_profile(entry, bf16=False):
+def traffic_from_profile(entry, bf16=False, config=4):
     """HBM-side bytes per call of a library entry point (sum over its kernels)
     from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the fp32
-    configs[3] workload, calibrated against a plain copy; None when the entry
-    point or its precision is not covered by the summary."""
+    configs[3] workload (--config 4), calibrated against a plain copy; None when
+    the entry point, its precision or the workload is not covered by the summary."""
     path = ROOT / "profiles" / "hbm_traffic_cfg4_md10k.txt"
     ks = KERNELS_OF.get(entry)
-    if ks is None or not path.exists() or bf16:
+    if ks is None or not path.exists() or bf16 or config != 4:
         return None
     found = {}
     for line in path.read_text().splitlines():
@@ -227,6 +231,7 @@ def main():
     E_mean = float(np.mean(edges))
     stats = timer.summary()
     peak_gb = torch.cuda.max_memory_allocated(dev) / 1e9
+    act = 2 if bf16 else 4   # bytes per attention activation element
     # dominant library call by total time
     dom = max(stats.items(), key=lambda kv: kv[1]["total_ms"])
     name, st = dom
@@ -241,25 +246,25 @@ def main():
         achieved = per_step / (st["count"] / args.steps) / (st["avg_ms"] * 1e-3) / 1e12
         peak = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
-                "frac": achieved / peak, "traffic": traffic_from_profile(name, bf16), "kernel": name}
+                "frac": achieved / peak, "traffic": traffic_from_profile(name, bf16, args.config), "kernel": name}
     elif name in PROJ_FLOPS:
         achieved = PROJ_FLOPS[name](N) / (st["avg_ms"] * 1e-3) / 1e12
         pk = BF16_PEAK_TFLOPS if name.endswith("_bf16") else FP32_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": achieved, "peak": pk, "unit": "TFLOP/s",
-                "frac": achieved / pk, "traffic": traffic_from_profile(name, bf16), "kernel": name}
+                "frac": achieved / pk, "traffic": traffic_from_profile(name, bf16, args.config), "kernel": name}
     else:
         fb = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
               "e2v2_deg_bwd": deg_bwd_bytes}.get(name, attn_fwd_bytes)
-        b = fb(N, E_mean)
+        b = fb(N, E_mean, act)
         achieved = b / (st["avg_ms"] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profile(name), "kernel": name}
+                "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profile(name, bf16, args.config), "kernel": name}
     # per-kernel achieved rate against its own roofline
     per_kernel = {}
     for k, v in stats.items():
         ent = {"avg_ms": round(v["avg_ms"], 4), "count": v["count"], "total_ms": round(v["total_ms"], 3)}
         if k in BYTES_OF:
-            gbs = BYTES_OF[k](N, E_mean) / (v["avg_ms"] * 1e-3) / 1e9
+            gbs = BYTES_OF[k](N, E_mean, act) / (v["avg_ms"] * 1e-3) / 1e9
             ent.update(bound="hbm", achieved_gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
         elif k in mlp_step_flops:
             tf = mlp_step_flops[k] / (v["count"] / args.steps) / (v["avg_ms"] * 1e-3) / 1e12
@@ -274,7 +279,7 @@ def main():
     peak_tf = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
     stack_tf = stack_flops(N, E_mean) / (ms * 1e-3) / 1e12
     hb = [k for k in BYTES_OF if k in stats]
-    hb_bytes = sum(BYTES_OF[k](N, E_mean) * stats[k]["count"] for k in hb)
+    hb_bytes = sum(BYTES_OF[k](N, E_mean, act) * stats[k]["count"] for k in hb)
     hb_time = sum(stats[k]["total_ms"] for k in hb) * 1e-3
     roof["stack"] = {"bound": "mfma", "achieved": round(stack_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
                      "frac": round(stack_tf / peak_tf, 4), "flops_per_step": stack_flops(N, E_mean)}
