@@ -364,7 +364,9 @@ class SO2OutFn(torch.autograd.Function):
         if Wpop.bwd is not None:
             gt = torch.bmm(gy, Wpop.bwd)
         else:
-            gt = gy.new_empty(9, N, C)
+            # bf16: gt feeds only the bf16 GEMMs below, so it is produced in bf16
+            # (one rounding of the fp32 accumulators, no separate cast pass)
+            gt = gy.new_empty(9, N, C, dtype=BF16 if bf else gy.dtype)
             ga = _bf(gy) if bf else gy
             for l in range(3):
                 a, b = l * l, (l + 1) ** 2
