@@ -31,6 +31,7 @@ import torch
 from torch import nn
 
 from . import cg as _cg
+from . import sparse_ops
 from .neighbors import expand_includeself, construct_radius_neighbor, polynomial
 
 
@@ -39,6 +40,11 @@ def _normalize2mom_cst(f) -> float:
     z = torch.randn(1_000_000, generator=gen, dtype=torch.float64)
     return f(z).pow(2).mean().pow(-0.5).item()
 
+
+# above this many edges the attention's QK and value aggregation run edge-chunked
+# (sparse_ops: same sums, without the all-edge gathers); below it the reference's
+# own torch fallbacks run as written
+CHUNKED_EDGES = 1 << 18
 
 SILU_2MOM = _normalize2mom_cst(torch.nn.functional.silu)
 SIGMOID_2MOM = _normalize2mom_cst(torch.sigmoid)
@@ -296,6 +302,21 @@ class SmoothLeakyReLU(nn.Module):
         return (1 - self.alpha) * x * torch.sigmoid(x) + self.alpha * x
 
 
+def segment_alpha(logit, poly, inputhead, qi, n_rows):
+    """Segmented softmax of ``e2former.py:327-367`` (torch fallback): row max
+    by ``scatter_reduce(amax, include_self)`` from -inf (its gradient goes to the
+    row's maxima, split evenly over ties), e = exp(a - m) * p with the envelope
+    inside, s = sum over the row, alpha = e * inputhead / (s + 1e-3)."""
+    H = logit.shape[1]
+    qih = qi.unsqueeze(-1).expand(-1, H)
+    amax = torch.full((n_rows, H), -torch.inf, dtype=logit.dtype)
+    amax.scatter_reduce_(0, qih, logit, reduce="amax", include_self=True)
+    e = torch.exp(logit - amax[qi]) * poly.unsqueeze(-1)
+    asum = torch.zeros((n_rows, H), dtype=logit.dtype)
+    asum.scatter_add_(0, qih, e)
+    return e * inputhead / (asum[qi] + 1e-3)
+
+
 class E2AttentionArbOrder_sparse(nn.Module):
     """``e2former.py:80-436`` for tp_type=QK_alpha, attn_type=so2-first-order,
     with the torch fallbacks (``use_triton`` False)."""
@@ -335,20 +356,18 @@ class E2AttentionArbOrder_sparse(nn.Module):
         inputhead = eg[:, H:].reshape(E, H)
         key = key.reshape(-1, H, key.shape[-1] // H)
         q_scaled = query / math.sqrt(query.shape[-1])
-        qk = torch.sum(q_scaled[qi] * key[nj], dim=-1)
-        alpha = gate * qk
-        qih = qi.unsqueeze(-1).expand(-1, H)
-        amax = torch.full((f_N1, H), -torch.inf, dtype=alpha.dtype)
-        amax.scatter_reduce_(0, qih, alpha, reduce="amax", include_self=True)
-        alpha = alpha - amax[qi]
-        alpha = torch.exp(alpha) * poly_dist.unsqueeze(-1)
-        asum = torch.zeros((f_N1, H), dtype=alpha.dtype)
-        asum.scatter_add_(0, qih, alpha)
-        alpha = alpha * inputhead / (asum[qi] + 1e-3)
+        chunked = E > CHUNKED_EDGES
+        if chunked:
+            qk = sparse_ops.sparse_qk(q_scaled, key, qi, nj)
+        else:
+            qk = torch.sum(q_scaled[qi] * key[nj], dim=-1)
+        alpha = segment_alpha(gate * qk, poly_dist, inputhead, qi, f_N1)
         value = self.proj_value(x)[bd["f_outcell_index"]]
         alpha_div_r = alpha / edge_dis.unsqueeze(-1).clamp_min(1e-6)
 
         def agg(v, a):
+            if chunked:
+                return sparse_ops.sparse_v_agg(v, a, qi, nj, f_N1)
             ev = v[nj] * a.unsqueeze(1)
             out = torch.zeros((f_N1, ev.shape[1], ev.shape[2]), dtype=ev.dtype)
             out.scatter_add_(0, qi.view(-1, 1, 1).expand_as(ev), ev)

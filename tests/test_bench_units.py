@@ -1,5 +1,7 @@
-"""CPU checks of bench.py's accounting: algorithmic byte counts per activation
-storage type, the profile-traffic lookup's coverage, and the one-GPU guard."""
+"""CPU checks of bench.py's accounting: the compulsory (reference-formulation)
+bytes and FLOPs the roofline uses, the implementation byte counts per
+activation storage type, the profile-traffic lookup's coverage, and the
+one-GPU guard."""
 import json
 import subprocess
 import sys
@@ -41,3 +43,41 @@ def test_more_than_one_gpu_exits_with_message():
     assert r.returncode == 2
     msg = json.loads(r.stdout.strip().splitlines()[-1])
     assert msg["n_gpus"] == 2 and "one GPU" in msg["error"]
+
+
+def test_compulsory_bytes_reference_formulation():
+    """One attention layer's forward at configs[3] (N = 10,000, M = 19,400
+    expanded nodes, E = 0.86 M edges) moves about 0.96 GB: Q and K (2 N 1024),
+    the merged value rows (M 29 256) and the output (N 29 256) in fp32, plus
+    8 bytes per edge; the backward about twice that."""
+    N, M, E = 10_000, 19_400, 860_000
+    b = bench.attn_fwd_compulsory(N, M, E)
+    assert abs(b - (4 * (2 * N * 1024 + M * 7424 + N * 7424) + 8 * E + 4 * (N + 1))) < 1
+    assert 0.94e9 < b < 0.98e9
+    assert bench.attn_bwd_compulsory(N, M, E) == 2 * b
+    # bf16 activations halve exactly the activation terms
+    assert b - bench.attn_fwd_compulsory(N, M, E, 2) == 2 * (2 * N * 1024 + M * 7424 + N * 7424)
+    assert bench.deg_compulsory(N, M, E) == 4 * N * 9 * 256 + 8 * E
+
+
+def test_mlp_flops_executed_and_reference():
+    """Per edge and evaluation: the reference formulation runs fc_easy
+    (2 (512 128 + 128 128 + 128 256) = 229,376 FLOP) in each of 4 layers and three
+    degree profiles (294,912 each); the kernels execute Linear2/3 only
+    (98,304 FLOP per profile forward)."""
+    ref, exe = bench.mlp_step_flops(1.0)
+    assert ref["e2v2_mlp_fwd"] == 4 * 229_376 + 3 * 294_912
+    assert ref["e2v2_mlp_bwd"] == 4 * 229_376 and ref["e2v2_mlp_bwd_deg"] == 3 * 294_912
+    assert exe["e2v2_mlp_fwd"] == 7 * 98_304
+    assert exe["e2v2_mlp_bwd"] == 4 * (98_304 + 256)
+
+
+def test_expanded_nodes_counts_distinct_images():
+    """M = real atoms + distinct (atom, nonzero shift) images carrying edges."""
+    import numpy as np
+    import torch
+    from types import SimpleNamespace
+    col = torch.tensor([1, 1, 2, 0, 1, 2, 2], dtype=torch.int32)
+    sidx = torch.tensor([0, 3, 3, 0, 3, 5, 5], dtype=torch.int32)
+    nl = SimpleNamespace(n_atoms=3, n_edges=7, col=col, shift_idx=sidx, shift_ptr=np.array([0, 27]))
+    assert bench.expanded_nodes(nl) == 3 + 3          # (3,1), (3,2), (5,2)

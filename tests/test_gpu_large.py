@@ -1,0 +1,132 @@
+"""Full-size configurations on the GPU: configs[3] (10,000 atoms, the benchmark
+workload) and configs[4] (100,000 atoms).
+
+At these sizes the CPU oracle model takes minutes per evaluation, so the
+model is checked through size-independent properties (bitwise determinism,
+translation / rotation invariance, zero net force, a directional
+finite-difference derivative of the energy) and, for bf16 at 100k atoms,
+against the fp32 HIP path on the same input; the neighbour lists are checked
+bit-exactly against the oracle's exact fp32 radius graph."""
+import numpy as np
+import pytest
+import torch
+
+from oracle.neighbors import exact_neighbors
+
+pytestmark = pytest.mark.gpu
+
+
+def _nbr_exact(pkg, cuda, sysd, label):
+    from ubio_molfm_amd import neighbors
+    pos = torch.as_tensor(sysd["pos"], device=cuda)
+    nl = neighbors.build_neighbors(pos, sysd["graph_ptr"], sysd["cell"], sysd["pbc"], 6.0)
+    got = nl.canonical()
+    ref = exact_neighbors(sysd["pos"], sysd["graph_ptr"], sysd["cell"], sysd["pbc"], 6.0)
+    rc = np.float32(6.0)
+    shell = int(np.sum(np.abs(ref["d"] - rc) <= 2 * np.spacing(rc)))
+    print(f"[nbr {label}] N={len(sysd['pos'])} E={nl.n_edges} oracle E={len(ref['i'])} max_row={nl.max_row} "
+          f"edges within 2 ulp of rc: {shell}", flush=True)
+    assert nl.n_edges == len(ref["i"])
+    for k in ("i", "j", "s"):
+        assert np.array_equal(got[k], ref[k]), k
+    assert np.array_equal(got["dv"].view(np.uint32), ref["dv"].view(np.uint32))
+    assert np.array_equal(got["d"].view(np.uint32), ref["d"].view(np.uint32))
+    kp = nl.key_ptr.cpu().numpy()
+    assert kp[-1] == nl.n_edges and np.array_equal(np.diff(kp), np.bincount(got["j"], minlength=len(sysd["pos"])))
+
+
+def test_neighbors_cfg4_bit_exact(pkg, cuda):
+    from ubio_molfm_amd import systems
+    _nbr_exact(pkg, cuda, systems.CONFIGS[4](), "cfg4")
+
+
+def test_neighbors_cfg5_bit_exact(pkg, cuda):
+    from ubio_molfm_amd import systems
+    _nbr_exact(pkg, cuda, systems.CONFIGS[5](), "cfg5")
+
+
+def _model(cuda, seed=21):
+    from ubio_molfm_amd import model
+    torch.manual_seed(seed)
+    return model.MolfmAtomic(model.default_args()).eval().to(cuda).requires_grad_(False)
+
+
+def _ef(m, pos, s, cell=None):
+    Z = torch.as_tensor(s["Z"], device=pos.device)
+    e, f, nl = m.energy_forces_flat(pos, Z, s["graph_ptr"], s["cell"] if cell is None else cell, s["pbc"])
+    return e.double(), f.double(), nl
+
+
+def test_cfg4_properties(pkg, cuda):
+    """configs[3] (10,000 atoms, periodic, fp32): two evaluations are bitwise
+    identical; a rigid translation and a rotation of atoms and cell leave the
+    energy unchanged (1e-6 relative) and rotate the forces (1e-4 rel-L2); the
+    net force vanishes (|sum F| below 1e-4 of sqrt(N) * rms F); and the central
+    difference of the energy along a random direction over 64 atoms equals
+    -F . u (2% + 2e-3 eV)."""
+    from ubio_molfm_amd import systems
+    s = systems.CONFIGS[4]()
+    m = _model(cuda)
+    pos = torch.as_tensor(s["pos"], device=cuda)
+    e1, f1, nl = _ef(m, pos, s)
+    e2, f2, _ = _ef(m, pos, s)
+    assert torch.equal(e1, e2) and torch.equal(f1, f2), "evaluations differ bitwise"
+    N = pos.shape[0]
+    rms = float(f1.pow(2).mean().sqrt())
+    net = float(f1.sum(0).norm())
+    e_t, f_t, _ = _ef(m, pos + torch.tensor([0.37, -0.21, 0.55], device=cuda), s)
+    q, _ = np.linalg.qr(np.random.default_rng(5).normal(size=(3, 3)))
+    if np.linalg.det(q) < 0:
+        q[:, 0] *= -1
+    qt = torch.as_tensor(q, dtype=torch.float32, device=cuda)
+    cell_r = (np.asarray(s["cell"], np.float64) @ q.T).astype(np.float32)
+    e_r, f_r, _ = _ef(m, pos @ qt.T, s, cell=cell_r)
+    rel_t = float((f_t - f1).norm() / f1.norm())
+    rel_r = float((f1 @ qt.double().T - f_r).norm() / f1.norm())
+    rng = np.random.default_rng(6)
+    idx = torch.as_tensor(rng.choice(N, 64, replace=False), device=cuda)
+    u = torch.zeros(N, 3, dtype=torch.float64, device=cuda)
+    u[idx] = torch.as_tensor(rng.normal(size=(64, 3)), device=cuda)
+    u /= u.norm()
+    h = 5e-3
+    ep, _, _ = _ef(m, (pos.double() + h * u).float(), s)
+    em, _, _ = _ef(m, (pos.double() - h * u).float(), s)
+    fd = float(ep - em) / (2 * h)
+    dirder = -float((f1 * u).sum())
+    print(f"[cfg4 props] N={N} E={nl.n_edges} energy={float(e1):.6f} |dE_trans|={abs(float(e_t - e1)):.3e} "
+          f"|dE_rot|={abs(float(e_r - e1)):.3e} F relL2 trans={rel_t:.2e} rot={rel_r:.2e} "
+          f"|sum F|={net:.3e} (sqrt(N) rms F={np.sqrt(N) * rms:.3e}) FD={fd:.6f} -F.u={dirder:.6f}", flush=True)
+    assert abs(float(e_t - e1)) <= 1e-6 * abs(float(e1)) + 1e-4
+    assert abs(float(e_r - e1)) <= 1e-6 * abs(float(e1)) + 1e-4
+    assert rel_t < 1e-4 and rel_r < 1e-4
+    assert net < 1e-4 * np.sqrt(N) * rms
+    assert abs(fd - dirder) <= 0.02 * abs(dirder) + 2e-3
+
+
+def test_cfg5_bf16_against_fp32_and_memory(pkg, cuda):
+    """configs[4] (100,000 atoms, periodic): one bf16 energy + force
+    evaluation (bf16 activations and GEMM operands, fp32 reductions) records its
+    peak device memory and agrees with the fp32 HIP evaluation of the same
+    input within the stated bf16 tolerance (1e-3 eV/atom, 2e-2 force rel-L2)."""
+    from ubio_molfm_amd import systems
+    s = systems.CONFIGS[5]()
+    m = _model(cuda, seed=22)
+    pos = torch.as_tensor(s["pos"], device=cuda)
+    N = pos.shape[0]
+    torch.cuda.synchronize(); torch.cuda.empty_cache(); torch.cuda.reset_peak_memory_stats(cuda)
+    e32, f32, nl = _ef(m, pos, s)
+    torch.cuda.synchronize()
+    peak32 = torch.cuda.max_memory_allocated(cuda) / 1e9
+    E = nl.n_edges
+    del nl
+    torch.cuda.empty_cache(); torch.cuda.reset_peak_memory_stats(cuda)
+    m.decoder.set_compute_dtype("bf16")
+    e16, f16, nl = _ef(m, pos, s)
+    torch.cuda.synchronize()
+    peak16 = torch.cuda.max_memory_allocated(cuda) / 1e9
+    de = abs(float(e16 - e32)) / N
+    rel = float((f16 - f32).norm() / f32.norm())
+    print(f"[cfg5] N={N} E={E} peak fp32={peak32:.1f} GB bf16={peak16:.1f} GB ({peak16 * 1e9 / E:.0f} B/edge) "
+          f"bf16 vs fp32: |dE|/atom={de:.3e} force relL2={rel:.3e}", flush=True)
+    assert de < 1e-3 and rel < 2e-2
+    assert peak16 < 288.0

@@ -152,8 +152,69 @@ class E2FormerBackbone(nn.Module):
             x = x.index_select(0, torch.argsort(perm))
         node_irreps = x.new_zeros((B, L, x.shape[1], x.shape[2]))
         node_irreps = node_irreps.masked_scatter(mask[:, :, None, None], x)
+        info = neighbor_info(nl, perm, fpos.detach(), graph_ptr, cell, self.max_radius)
+        batched_data.update(f_exp_node_pos=info.pop("f_exp_node_pos"), f_outcell_index=info.pop("f_outcell_index"))
         return {"node_featuresBxN": node_irreps[:, :, 0], "node_vec_featuresBxN": node_irreps[:, :, 1:4],
-                "node_irrepsBxN": node_irreps, "data": batched_data, "neighbor_info": nl}
+                "node_irrepsBxN": node_irreps, "data": batched_data, "neighbor_info": info}
+
+
+def _segment_metadata(row_index: torch.Tensor, col_index: torch.Tensor, num_rows: int):
+    """(row_ptr, sorted col_index, edge_perm) int32 of a stable sort by row
+    (triton_sparse_qk_autograd.py:617-633)."""
+    perm = torch.argsort(row_index, stable=True)
+    counts = torch.bincount(row_index.long(), minlength=num_rows)
+    row_ptr = torch.zeros(num_rows + 1, dtype=torch.int32, device=row_index.device)
+    row_ptr[1:] = counts.cumsum(0).to(torch.int32)
+    return row_ptr, col_index[perm].to(torch.int32).contiguous(), perm.to(torch.int32).contiguous()
+
+
+def neighbor_info(nl, perm: Optional[torch.Tensor], pos: torch.Tensor, graph_ptr, cells, rc: float) -> Dict:
+    """The neighbour list as the reference's ``construct_neighbor`` dict
+    (module_utils.py:3233-3242) in the caller's atom order: ``query_idx``
+    ascending with each row ordered by distance, ``neighbor_idx`` into the
+    flattened expanded nodes, the 6-tuple CSR ``metadata``
+    (triton_sparse_qk_autograd.py:635-652), ``f_edge_vec``, ``f_dist``,
+    ``f_poly_dist``; plus the expanded nodes themselves (``f_exp_node_pos``,
+    ``f_outcell_index``, e2former_wrapper.py:213-216).  Expanded nodes are, per
+    graph, every real atom (the [0,0,0] cell, atom order) followed by the images
+    that carry edges, in (cell, atom) order; images of the reference's expansion
+    that carry no edge (within 1e-4 of an atom but no other atom in range) are
+    not listed.  ``shift`` [E,3] gives each edge's integer cell offset."""
+    from .ops import ENV_A, ENV_B, ENV_C
+    dev = pos.device
+    N, E = nl.n_atoms, nl.n_edges
+    graph_ptr = np.asarray(graph_ptr, np.int64)
+    cells = torch.as_tensor(np.asarray(cells, np.float32).reshape(-1, 3, 3), device=dev)
+    to_in = perm if perm is not None else torch.arange(N, device=dev)
+    qi = to_in[nl.edge_row.long()]
+    order = torch.argsort(qi, stable=True)            # rows keep their distance order
+    qi = qi[order]
+    j = to_in[nl.col.long()][order]
+    sidx = nl.shift_idx.long()[order]
+    shifts = nl.shifts.to(dev)
+    # per-graph [0,0,0] row of the shift table, and the graph of every atom
+    counts = torch.as_tensor(np.diff(graph_ptr), device=dev)
+    gid = torch.repeat_interleave(torch.arange(len(counts), device=dev), counts, output_size=N)
+    sptr0 = torch.as_tensor(np.asarray(nl.shift_ptr, np.int64)[:-1], device=dev)
+    key_real = sptr0[gid] * N + torch.arange(N, device=dev)
+    key_edge = sidx * N + j
+    exp_keys, inv = torch.unique(torch.cat([key_real, key_edge]), sorted=True, return_inverse=True)
+    nbr = inv[N:]
+    out_j = exp_keys % N
+    out_s = exp_keys // N
+    off = shifts[out_s].float()
+    cg = cells[gid[out_j]]
+    img_off = (off[:, 0:1] * cg[:, 0] + off[:, 1:2] * cg[:, 1]) + off[:, 2:3] * cg[:, 2]
+    exp_pos = pos[out_j] + img_off
+    vec = nl.dvec[order]
+    dist = nl.dist[order]
+    ratio = dist / rc                                   # module_utils.py:1946-1954
+    poly = torch.where(ratio < 1, 1 + ratio ** 5 * (ENV_A + ratio * (ENV_B + ENV_C * ratio)), 0)
+    q_ptr, q_col, q_perm = _segment_metadata(qi, nbr, N)
+    k_ptr, k_col, k_perm = _segment_metadata(nbr, qi, exp_keys.shape[0])
+    return {"query_idx": qi, "neighbor_idx": nbr, "metadata": (q_ptr, q_col, q_perm, k_ptr, k_col, k_perm),
+            "f_edge_vec": vec, "f_dist": dist, "f_poly_dist": poly, "shift": shifts[sidx],
+            "f_exp_node_pos": exp_pos, "f_outcell_index": out_j}
 
 
 class MLP_energy_head(nn.Module):

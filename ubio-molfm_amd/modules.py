@@ -14,6 +14,7 @@ from typing import Optional
 import numpy as np
 import torch
 from torch import nn
+from torch.profiler import record_function
 
 from . import so3
 from . import _lib
@@ -684,10 +685,11 @@ class FeedForwardNetwork_s3(nn.Module):
         self.slinear_2 = SO3_Linear_e2former(hidden_channels, output_channels, lmax=lmax, bias=True)
 
     def forward(self, x, res=None, bf16: bool = False, **kw):
-        h = self.gate(self.slinear_1(x, bf16), bf16)
-        s2 = self.slinear_2
-        return SO3LinearFn.apply(h, mrow_weight(s2, "weight", s2.weight, bf16, s2.lmax), s2.bias.detach(), s2.lmax,
-                                 res)
+        with record_function("FeedForwardFunction"):
+            h = self.gate(self.slinear_1(x, bf16), bf16)
+            s2 = self.slinear_2
+            return SO3LinearFn.apply(h, mrow_weight(s2, "weight", s2.weight, bf16, s2.lmax), s2.bias.detach(),
+                                     s2.lmax, res)
 
 
 class sph_fromxyz(nn.Module):
@@ -874,17 +876,22 @@ class E2AttentionArbOrder_sparse(nn.Module):
         W, b = self.qk_weights(bf16)
         hid = self.query_linear.weight.shape[1]
         pv = self.proj_value  # its GEMMs run inside QKProjFn (one input gradient)
-        hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight", pv.weight, bf16, pv.lmax),
-                                   pv.bias.detach())
-        q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
-        k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
+        with record_function("query key linear function"):
+            hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight", pv.weight, bf16, pv.lmax),
+                                       pv.bias.detach())
+            q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
+            k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding, ctx.rbf_offset,
                                ctx.rbf_coeff, ctx.rc, bf16)
-        so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
-                                packed, ctx.rc, math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
+        # the radial profile ("rbf function-a") runs inside the attention launches
+        with record_function("qk attention"):
+            so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset,
+                                    ctx.rbf_coeff, packed, ctx.rc, math.sqrt(q.shape[-1]),
+                                    BF16 if bf16 else torch.float32)
         pf = self.proj_first
-        return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16),
-                              mrow_weight(pf, "weight", pf.weight, bf16, pf.lmax), pf.bias.detach())
+        with record_function("first-order"):
+            return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16),
+                                  mrow_weight(pf, "weight", pf.weight, bf16, pf.lmax), pf.bias.detach())
 
 
 class TransBlock(nn.Module):
@@ -942,8 +949,10 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
     def forward(self, ctx: EdgeContext):
         packed = self._mlp.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
                                ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.bf16)
-        return DegreeEmbedFn.apply(ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff, packed,
-                                   float(self.avg_aggregate_num), ctx.rc)
+        # the edge spherical harmonics ("e3nn sph") are formed inside the degree kernels
+        with record_function("e3nn sph"):
+            return DegreeEmbedFn.apply(ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
+                                       packed, float(self.avg_aggregate_num), ctx.rc)
 
 
 class E2former(nn.Module):
@@ -977,10 +986,12 @@ class E2former(nn.Module):
 
     def forward_flat(self, ctx: EdgeContext, sys_node_embedding: Optional[torch.Tensor] = None):
         """Returns the node irreps in the m-major layout [9, N, C]."""
-        x = self.edge_deg_embed_dense(ctx)
+        with record_function("node_initiliation"):
+            x = self.edge_deg_embed_dense(ctx)
         d = None
-        for blk in self.blocks:
-            x, d = blk.forward_deferred(x, d, ctx, sys_node_embedding)
+        for i, blk in enumerate(self.blocks):
+            with record_function(f"tranblock {i}"):
+                x, d = blk.forward_deferred(x, d, ctx, sys_node_embedding)
         return self.norm_final.add_forward(x, d)[0]
 
 

@@ -87,6 +87,7 @@ class NeighborList:
     col_slot_member: Optional[torch.Tensor] = None   # [E] int32
     col_slot_edge: Optional[torch.Tensor] = None     # [E, col_span] int32
     col_n_slots: Optional[torch.Tensor] = None       # [ceil(N / col_span)] int32
+    shift_ptr: Optional[np.ndarray] = None           # [B+1] rows of ``shifts`` per graph (host)
 
     def canonical(self):
         """(i, j, s) sorted lexicographically, plus dvec/dist in that order (numpy)."""
@@ -228,7 +229,7 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
               _lib.vp(stats.data_ptr()), _lib.vp(tkey.data_ptr()), _lib.vp(_ptr(key_eid)), _lib.i32(1),
               _lib.vp(stream))
     nl = NeighborList(N, E, row_ptr, col, sh, torch.as_tensor(shifts_np), dvec, dist, edge_row, key_ptr, key_eid,
-                      max_row)
+                      max_row, shift_ptr=np.asarray(sptr, np.int64))
     if N > 0 and E > 0:
         nl.col_span = COL_SPAN
         nl.col_slot_member, nl.col_slot_edge, nl.col_n_slots = cluster_slots(key_ptr, N, edge_row, key_eid,
