@@ -65,56 +65,54 @@ COMPULSORY = {"e2v2_attn_fwd": attn_fwd_compulsory, "e2v2_attn_bwd": attn_bwd_co
               "e2v2_deg_fwd": deg_compulsory, "e2v2_deg_bwd": deg_compulsory}
 
 
-# Bytes the implementation's kernels move per launch (inputs they must read and outputs they
-# must write, including the per-edge tensors this implementation keeps); the excess over the
-# compulsory bytes is the per-edge overhead.
+# Bytes the implementation's kernels read and write per launch, split into node / edge-list traffic
+# and the radial-table reads (rows of the per-type-pair distance tables, mostly served by the L2 and
+# the Infinity Cache: an attention layer's table is 16 pairs x 770 nodes x 4 KB = 50 MB at configs[3]).
 def attn_fwd_bytes(N, E, act=4):
-    # read q, k, v, gate|inputhead, edge (col, dvec, dist), row_ptr; write out, m, s, cnt
-    return (act * N * (128 * 8 * 2 + 9 * 256 + 20 * 256)
-            + 4.0 * (N * 3 * 128 + E * (256 + 5) + N + 1))
+    # read q, k, v, edge (col, dvec, dist, source type), row_ptr; write out, m, s, cnt
+    node_edge = (act * N * (128 * 8 * 2 + 9 * 256 + 20 * 256) + 4.0 * (N * 3 * 128 + E * 6 + N + 1))
+    return node_edge + attn_fwd_table_bytes(E)
+
+
+def attn_fwd_table_bytes(E):
+    return 4.0 * E * 256 * 6          # gate | inputhead, rows 0..2 at two nodes
 
 
 def attn_bwd_bytes(N, E, act=4):
-    # row pass: read grad, out, q, k, v, gi, m/s/cnt, edges; write dgi, ddvec, ddist, dq, w, dqk
+    # row pass: read grad, out, q, k, v, m/s/cnt, edges; write ddvec, ddist, dq, w, dqk
     # column pass: read w, dqk, key CSR, grad rows, q; write dv, dk
     row = (act * N * (2 * 20 * 256 + 2 * 1024 + 9 * 256)
-           + 4.0 * (N * (1024 + 3 * 128) + E * (256 + 5 + 256 + 4 + 2 * 128)))
+           + 4.0 * (N * (1024 + 3 * 128) + E * (6 + 4 + 2 * 128)))
     col = act * N * (20 * 256 + 1024) + 4.0 * (N * (9 * 256 + 1024 + 2) + E * (2 * 128 + 2 + 3))
-    return row + col
+    return row + col + attn_bwd_table_bytes(E)
+
+
+def attn_bwd_table_bytes(E):
+    return 4.0 * E * 256 * 8          # rows 0..3 at two nodes (value and distance derivative)
 
 
 def deg_fwd_bytes(N, E, act=4):
-    return 4.0 * (E * (768 + 4) + N * 9 * 256)
+    return 4.0 * (E * 6 + N * 9 * 256) + deg_fwd_table_bytes(E)
+
+
+def deg_fwd_table_bytes(E):
+    return 4.0 * E * 768 * 6
 
 
 def deg_bwd_bytes(N, E, act=4):
-    # read fea, dvec, dist and the node gradient; write ddvec, ddist (the feature
-    # gradient is formed inside e2v2_mlp_bwd_deg, never stored)
-    return 4.0 * (E * (768 + 4 + 4) + N * 9 * 256)
+    # read dvec, dist, col, types and the node gradient; write ddvec, ddist
+    return 4.0 * (E * (6 + 4) + N * 9 * 256) + deg_bwd_table_bytes(E)
+
+
+def deg_bwd_table_bytes(E):
+    return 4.0 * E * 768 * 8
 
 
 IMPL_BYTES = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
               "e2v2_deg_bwd": deg_bwd_bytes}
+TABLE_BYTES = {"e2v2_attn_fwd": attn_fwd_table_bytes, "e2v2_attn_bwd": attn_bwd_table_bytes,
+               "e2v2_deg_fwd": deg_fwd_table_bytes, "e2v2_deg_bwd": deg_bwd_table_bytes}
 BYTES_OF = IMPL_BYTES
-
-# Radial MLP FLOPs per edge per profile.  Reference formulation: fc_easy 512 -> 128 -> 128 -> 256
-# (attention), the degree embedding's profiles 768 -> 128 -> 128 -> 256.  Executed here: Linear2 and
-# Linear3 only (Linear1 is per-type tables plus an interpolated table of its rbf block), and in the
-# backward the two input-gradient GEMMs plus the 128-term table dot.
-MLP_REF_FLOPS = {"attn": 2.0 * (512 * 128 + 128 * 128 + 128 * 256), "deg": 2.0 * (768 * 128 + 128 * 128 + 128 * 256)}
-MLP_EXEC_FWD = 2.0 * (128 * 128 + 128 * 256)
-MLP_EXEC_BWD = 2.0 * (128 * 128 + 128 * 256) + 2.0 * 128
-
-
-def mlp_step_flops(E):
-    """Per MD step / evaluation: the degree embedding's 3 profiles and one profile per attention
-    layer (4) in the forward; their backward split over e2v2_mlp_bwd (attention) and
-    e2v2_mlp_bwd_deg (degree)."""
-    ref = {"e2v2_mlp_fwd": E * (3 * MLP_REF_FLOPS["deg"] + 4 * MLP_REF_FLOPS["attn"]),
-           "e2v2_mlp_bwd": E * 4 * MLP_REF_FLOPS["attn"], "e2v2_mlp_bwd_deg": E * 3 * MLP_REF_FLOPS["deg"]}
-    exe = {"e2v2_mlp_fwd": E * 7 * MLP_EXEC_FWD, "e2v2_mlp_bwd": E * 4 * MLP_EXEC_BWD,
-           "e2v2_mlp_bwd_deg": E * 3 * MLP_EXEC_BWD}
-    return ref, exe
 
 
 def stack_flops(N, E):
@@ -131,10 +129,8 @@ PROJ_FLOPS = {"e2v2_qk_proj_fwd": lambda N: 2.0 * 9 * N * 256 * 2048,
 PROJ_FLOPS["e2v2_qk_proj_fwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
 PROJ_FLOPS["e2v2_qk_proj_bwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
 
-KERNELS_OF = {"e2v2_mlp_fwd": ["k_mlp_fwd"], "e2v2_mlp_bwd": ["k_mlp_bwd"],
-              "e2v2_mlp_bwd_deg": ["k_mlp_bwd_deg"], "e2v2_attn_fwd": ["k_attn_fwd"],
-              "e2v2_attn_bwd": ["k_attn_bwd_row_hp", "k_attn_bwd_col_grp"], "e2v2_deg_fwd": ["k_deg_fwd"],
-              "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"],
+KERNELS_OF = {"e2v2_attn_fwd": ["k_attn_fwd"], "e2v2_attn_bwd": ["k_attn_bwd_row_hp", "k_attn_bwd_col_grp"],
+              "e2v2_deg_fwd": ["k_deg_fwd"], "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"],
               "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"]}
 
 
@@ -286,7 +282,7 @@ def main():
     for _ in range(args.warmup):
         integ.step()
     torch.cuda.synchronize()
-    timer = _lib.KernelTimer(["e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_mlp_bwd_deg", "e2v2_attn_fwd", "e2v2_attn_bwd",
+    timer = _lib.KernelTimer(["e2v2_attn_fwd", "e2v2_attn_bwd",
                               "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill",
                               "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd", "e2v2_qk_proj_fwd_bf16",
                               "e2v2_qk_proj_bwd_bf16"])
@@ -310,7 +306,6 @@ def main():
     act = 2 if bf16 else 4   # bytes per attention activation element
     M = expanded_nodes(integ.last_nl)     # reference formulation's expanded nodes (last step's list)
     peak_tf = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
-    mlp_ref, mlp_exe = mlp_step_flops(E_mean)
     per_kernel = {}
     for k, v in stats.items():
         ent = {"avg_ms": round(v["avg_ms"], 4), "count": v["count"], "total_ms": round(v["total_ms"], 3)}
@@ -318,19 +313,11 @@ def main():
         if k in COMPULSORY:
             b_alg = COMPULSORY[k](N, M, E_mean, act)
             b_imp = IMPL_BYTES[k](N, E_mean, act)
+            b_tab = TABLE_BYTES[k](E_mean)
             ent.update(bound="hbm", bytes_per_launch=b_alg, achieved_gbs=round(b_alg / sec / 1e9, 1),
                        frac=round(b_alg / sec / 1e9 / HBM_PEAK_GBS, 4), impl_bytes_per_launch=b_imp,
                        impl_gbs=round(b_imp / sec / 1e9, 1), impl_frac=round(b_imp / sec / 1e9 / HBM_PEAK_GBS, 4),
-                       per_edge_overhead_bytes=max(0.0, b_imp - b_alg))
-        elif k in mlp_exe:
-            calls = v["count"] / args.steps
-            tf_exe = mlp_exe[k] / calls / sec / 1e12
-            tf_ref = mlp_ref[k] / calls / sec / 1e12
-            ent.update(bound="mfma", flops_per_launch=mlp_exe[k] / calls, achieved_tflops=round(tf_exe, 2),
-                       frac=round(tf_exe / peak_tf, 4), reference_flops_per_launch=mlp_ref[k] / calls,
-                       reference_tflops=round(tf_ref, 2), reference_frac=round(tf_ref / peak_tf, 4),
-                       note="frac: executed FLOPs (Linear2/3; Linear1 by tables); reference_frac counts the "
-                            "reference formulation's Linear1 work too")
+                       impl_table_bytes_per_launch=b_tab)
         elif k in PROJ_FLOPS:
             tf = PROJ_FLOPS[k](N) / sec / 1e12
             pk = BF16_PEAK_TFLOPS if k.endswith("_bf16") else FP32_PEAK_TFLOPS
@@ -356,8 +343,8 @@ def main():
     hb_imp = sum(IMPL_BYTES[k](N, E_mean, act) * stats[k]["count"] for k in hb)
     roof["stack"] = {"bound": "mfma", "achieved": round(stack_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
                      "frac": round(stack_tf / peak_tf, 4), "flops_per_step": stack_flops(N, E_mean),
-                     "note": "reference-formulation FLOPs (includes the radial MLPs' Linear1 work that per-type "
-                             "and interpolation tables replace here)"}
+                     "note": "reference-formulation FLOPs; the per-edge radial MLPs (about 70% of them) run here "
+                             "as distance-table interpolation, so this is an equivalent rate, not MFMA utilisation"}
     roof["hbm_kernels_time_weighted"] = {"kernels": hb, "achieved": round(hb_alg / hb_time / 1e9, 1),
                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                          "frac": round(hb_alg / hb_time / 1e9 / HBM_PEAK_GBS, 4),

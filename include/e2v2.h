@@ -20,9 +20,10 @@
  *                       (FAISS twin: src/molfm/models/e2former/sp/dist_ner.py:27-86, 240-333)
  *   e2v2_csr_transpose  prepare_sparse_qk_edge_index_metadata
  *                       src/molfm/models/e2former/triton_dr/triton_sparse_qk_autograd.py:601-652
- *   e2v2_mlp_fwd/bwd    GaussianSmearing + RadialProfile over x_edge = [rbf, tgt, src]
+ *   e2v2_radial_table*  GaussianSmearing + RadialProfile over x_edge = [rbf, tgt, src]
  *                       src/molfm/models/e2former/e2former.py:258-266, 302 (fc_easy) and
- *                       e2former.py:709-733 (gbf_projs); module_utils.py:1853-1869, 2151-2178
+ *                       e2former.py:709-733 (gbf_projs); module_utils.py:1853-1869, 2151-2178,
+ *                       as per-type-pair tables of the distance (the edge kernels interpolate them)
  *   e2v2_attn_fwd       sparse_qk_edge_index_triton (triton_sparse_qk_autograd.py:839-871),
  *                       segmented softmax e2former.py:327-367 with
  *                       sparse_alpha_sum_edge_index_triton (sparse_alpha_sum_edge_index_autograd.py:207-213),
@@ -52,8 +53,6 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
-
-#define E2V2_MAX_MLP 3
 
 const char* e2v2_last_error(void);
 int e2v2_version(void);
@@ -118,62 +117,42 @@ int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, i
                        int32_t* edge_row, int32_t* key_cnt, int32_t* key_ptr, int32_t* stats,
                        uint64_t* tmp_key, int32_t* key_eid, int phase, hipStream_t s);
 
-/* ---- edge radial MLP --------------------------------------------------- */
-typedef struct e2v2_mlp_weights {
-  /* Linear1's rbf block as a function of the distance: rtab[n][k][c] =
-     h^k d^k/dd^k (W1[c, 0:256] . rbf(d)) at d = n h, k = 0..3 (float64-built by
-     e2v2_mlp_rbf_table); evaluated by quintic Hermite interpolation.            */
-  const float* rtab;  /* [rtab_n][4][128]                                          */
-  int32_t rtab_n;     /* nodes covering [0, rc]                                     */
-  float rtab_h;       /* node spacing, a power of two                               */
-  const float* ttgt;  /* [types][128] target-type block of Linear1 + bias         */
-  const float* tsrc;  /* [types][128] source-type block of Linear1                */
-  const float* g1; const float* be1;   /* LayerNorm(128)                            */
-  /* fp32 GEMM operands B[K][N], lane-packed: one float4 per (wave w < 4, column group
-     ct < N/64, k block b < K/16, lane l < 64) in that order, holding
-     B[16 b + 4 (l / 16) + s][w N/4 + 16 ct + l % 16], s = 0..3.                  */
-  const float* w2t;   /* B = Linear2^T [128][128] (forward)                       */
-  const float* b2;
-  const float* g2; const float* be2;
-  const float* w3t;   /* B = Linear3^T [128][256] (forward)                       */
-  const float* b3;
-  const float* w2;    /* B = Linear2 [128][128] (backward)                        */
-  const float* w3;    /* B = Linear3 [256][128] (backward)                        */
-  /* bf16 operands (compute_bf16 = 1), each as B^T row-major [N][K]:              */
-  const void* w2b;    /* [128][128] Linear2 (forward)                             */
-  const void* w3b;    /* [256][128] Linear3 (forward)                             */
-  const void* w3tb;   /* [128][256] Linear3^T (backward)                          */
-  const void* w2tb;   /* [128][128] Linear2^T (backward)                          */
-} e2v2_mlp_weights;
+/* ---- radial profiles as distance tables ------------------------------- */
+/* A RadialProfile [256 + 2 n_emb -> 128 -> LayerNorm -> SiLU -> 128 -> LayerNorm -> SiLU -> 256] over
+   x_edge = [rbf(d), tgt[z_i], src[z_j]] is, for one pair of atom types, a function of the edge distance d
+   alone.  Its table, for a set of n_types atom types (type slot a has atomic number type_z[a]), holds per
+   type pair p = a * n_types + b (a: the query atom's type, b: the source atom's) and node n (d = n h, h a
+   power of two) four rows of nc channels: row k = h^k d^k f / dd^k (k = 0..3), float64-built by exact
+   Taylor-series propagation through every op.  Layout tab[p][n][k][nc]; one profile fills the 256
+   channels [col0, col0 + 256) of each row (nc = 256 for an attention layer's fc_easy, whose channels
+   are gate | inputhead; nc = 768 for the degree embedding's three profiles, l = 0, 1, 2).  The edge
+   kernels interpolate rows 0..2 (value) and rows 1..3 (derivative) with quintic Hermite polynomials. */
+#define E2V2_MAX_TYPES 32
+typedef struct e2v2_radial_net {
+  const float* w1;  int32_t ld_w1;    /* Linear1 weight [128][ld_w1], ld_w1 = 256 + 2 n_emb     */
+  int32_t n_emb;                      /* width of the type embeddings                           */
+  const float* b1;                    /* [128]                                                  */
+  const float* g1; const float* be1;  /* LayerNorm(128), eps 1e-5                               */
+  const float* w2; const float* b2;   /* [128][128], [128]                                      */
+  const float* g2; const float* be2;  /* LayerNorm(128)                                         */
+  const float* w3; const float* b3;   /* [256][128], [256]                                      */
+  const float* tgt;                   /* [n_types_max][n_emb] target (query atom) embedding     */
+  const float* src;                   /* [n_types_max][n_emb] source atom embedding             */
+} e2v2_radial_net;
 
-typedef struct e2v2_mlp_args {
-  int64_t n_edges;
-  int32_t n_mlp;                 /* 1..E2V2_MAX_MLP profiles sharing the edge input */
-  int32_t compute_bf16;          /* 1: bf16 GEMM operands, fp32 accumulation       */
-  const float* dist;             /* [E]                                            */
-  const int32_t* edge_row;       /* [E] query atom                                 */
-  const int32_t* col;            /* [E] source atom                                */
-  const int32_t* node_type;      /* [N] atomic numbers                             */
-  float* save_n;                 /* [n_mlp][E][256] normalised LN1 | LN2 inputs (written by fwd, read by bwd) */
-  float* save_r;                 /* [n_mlp][E][2]   their rstd                                                */
-  e2v2_mlp_weights w[E2V2_MAX_MLP];
-} e2v2_mlp_args;
-
-/* Node count and spacing (a power of two, about 0.17 of the Gaussian width) of the
-   rbf-block table of a GaussianSmearing basis exp(rbf_coeff (d - mu)^2) over [0, rc]
-   (module_utils.py:1853-1869). */
-int e2v2_mlp_rbf_table_size(float rc, float rbf_coeff, int32_t* n_nodes, float* h);
-/* rtab [n_nodes][4][128] of Linear1's rbf block w1 [128][ldw1] (columns 0..255) with
-   centres rbf_offset [256]; float64 accumulation. */
-int e2v2_mlp_rbf_table(const float* w1, int ldw1, const float* rbf_offset, float rbf_coeff, int32_t n_nodes,
-                       float h, float* rtab, hipStream_t s);
-
-/* out[e, 256 m + c] for profile m; fills save_n / save_r when they are non-null */
-int e2v2_mlp_fwd(const e2v2_mlp_args* args, float* out, int ld_out, hipStream_t s);
-/* dd[e] (+)= sum_m dL/dout_m . dout_m/dd  (input gradient w.r.t. the edge distance only);
-   requires save_n / save_r from the forward of the same edges and weights */
-int e2v2_mlp_bwd(const e2v2_mlp_args* args, const float* dout, int ld_dout, float* dd, int accumulate,
-                 hipStream_t s);
+/* Node spacing h = 2^(floor(log2(0.2 sigma)) - refine) of a GaussianSmearing basis exp(coeff (d - mu)^2)
+   (sigma = sqrt(-0.5 / coeff)) and the node count covering [0, rc]. */
+int e2v2_radial_table_size(float rc, float rbf_coeff, int32_t refine, int32_t* n_nodes, float* h);
+/* Build one profile's channels of tab (device type_z [n_types], rbf_offset [256] = mu). */
+int e2v2_radial_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff, const int32_t* type_z,
+                      int32_t n_types, int32_t n_nodes, float h, float* tab, int32_t nc, int32_t col0,
+                      hipStream_t s);
+/* Interpolation error of one profile's table at every interval midpoint against the float64 profile:
+   err (uint32 [4], zeroed by the caller) receives the float bits of max |f - f~|, max |f|,
+   max h |f' - f~'|, max h |f'|. */
+int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                            const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h, const float* tab,
+                            int32_t nc, int32_t col0, uint32_t* err, hipStream_t s);
 
 /* ---- attention --------------------------------------------------------- */
 typedef struct e2v2_attn_args {
@@ -190,7 +169,10 @@ typedef struct e2v2_attn_args {
   const void* q;                 /* [N,H,D]            float, or bf16 if act_bf16   */
   const void* k;                 /* [N,H,D]            float, or bf16 if act_bf16   */
   const void* v;                 /* [9][N][C] m-major  float, or bf16 if act_bf16   */
-  const float* gi;               /* [E,2H] gate | inputhead                         */
+  const float* rtab;             /* fc_easy table [T*T][rtab_n][4][2H] (gate | inputhead), e2v2_radial_table */
+  const int32_t* atom_type;      /* [N] type slot of each atom, 0 .. n_types - 1     */
+  int32_t n_types, rtab_n;       /* T, table nodes                                  */
+  float rtab_h;                  /* node spacing (a power of two)                   */
   float q_div;                   /* sqrt(D)                                         */
   float rc, env_a, env_b, env_c; /* polynomial envelope                             */
   int32_t act_bf16;              /* 1: q, k, v, out, grad_out stored as bf16 (fp32 math) */
@@ -202,13 +184,15 @@ typedef struct e2v2_attn_args {
 
 /* v [9][N][C] and out [20][N][C] are m-major (row r of every atom contiguous);
    out (float, or bf16 if act_bf16): h_a - h_b rows of the SO(2) product; mrow/srow [N,H] softmax max / sum;
-   cnt [N,H] number of maxima */
+   cnt [N,H] number of maxima.  gate and inputhead of every edge are interpolated from rtab in the kernel
+   (nothing per edge is stored). */
 int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, float* srow, int32_t* cnt, hipStream_t s);
-/* grad_out, out [20][N][C] (float, or bf16 if act_bf16) -> dgi [E,2H], ddvec [E,3], ddist [E], dq, dk [N,H,D],
-   dv [9][N][C] (all float); w_edge, dqk_edge [E,H] are outputs consumed by the column pass */
+/* grad_out, out [20][N][C] (float, or bf16 if act_bf16) -> ddvec [E,3], ddist [E] (including the radial
+   profile's distance derivative, from the table), dq, dk [N,H,D], dv [9][N][C] (all float); w_edge, dqk_edge
+   [E,H] are scratch written by the row pass and read by the column pass of this call */
 int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, const void* out, const float* mrow,
-                  const float* srow, const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq,
-                  float* dk, float* dv, float* w_edge, float* dqk_edge, hipStream_t s);
+                  const float* srow, const int32_t* cnt, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
+                  float* w_edge, float* dqk_edge, hipStream_t s);
 
 /* ---- edge-degree embedding -------------------------------------------- */
 typedef struct e2v2_deg_args {
@@ -218,22 +202,20 @@ typedef struct e2v2_deg_args {
   const int32_t* row_ptr;
   const float* dvec;             /* [E,3]                                           */
   const float* dist;             /* [E]                                             */
-  const float* fea;              /* [E,3,C] radial-MLP outputs for l = 0, 1, 2      */
+  const int32_t* col;            /* [E] source atom                                 */
+  const float* rtab;             /* gbf_projs table [T*T][rtab_n][4][3C] (profiles l = 0, 1, 2) */
+  const int32_t* atom_type;      /* [N] type slot of each atom                      */
+  int32_t n_types, rtab_n;
+  float rtab_h;
   float avg;                     /* avg_aggregate_num                               */
   float rc, env_a, env_b, env_c;
 } e2v2_deg_args;
 
 /* x0 [9][N][C] m-major */
 int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s);
-/* dfea may be NULL (then only ddvec, ddist; e2v2_mlp_bwd_deg forms dfea itself) */
-int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* dfea, float* ddvec, float* ddist,
-                 hipStream_t s);
-/* e2v2_mlp_bwd for the degree embedding's three l-profiles with dOut formed per edge tile from the
-   node gradient grad_x0 [9][N][256] (m-major) instead of a stored [E][3][256] tensor:
-   dOut[e, l, c] = p(d_e)/avg sum_{m in l} Y_m(u_e) grad_x0[m][i_e][c] (the transpose of the degree
-   embedding's CSR reduce, e2former.py:719-741); deg supplies dvec, dist, avg and the envelope. */
-int e2v2_mlp_bwd_deg(const e2v2_mlp_args* args, const e2v2_deg_args* deg, const float* grad_x0, float* dd,
-                     int accumulate, hipStream_t s);
+/* grad_x0 [9][N][C] -> ddvec [E,3], ddist [E] (spherical harmonics, envelope and the profiles' distance
+   derivative from the table) */
+int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* ddvec, float* ddist, hipStream_t s);
 
 /* ---- per-node kernels (node layout m-major: x[9][N][256]) --------------- */
 /* rms_norm_sh: EquivariantRMSNormArraySphericalHarmonicsV2_BL

@@ -1,7 +1,7 @@
 """Plain-PyTorch references of the HIP operators (float64, CPU, autograd-able).
 
 Each one restates the reference's own torch formulation of the op:
-* ``mlp_ref``   RadialProfile(cat[rbf, tgt[z_i], src[z_j]])      e2former.py:258-266,302
+* ``mlp_ref``   RadialProfile(cat[rbf, tgt[z_i], src[z_j]])      e2former.py:258-266,302 (and 709-733)
 * ``attn_ref``  logits/softmax/aggregation of e2former.py:327-433 with the
                 first-order product written as the per-edge Cartesian coupling
 * ``deg_ref``   EdgeDegreeEmbeddingNetwork_higherorder fallback   e2former.py:689-753
@@ -26,50 +26,6 @@ def rbf(d, offset, coeff):
 def mlp_ref(d, zi, zj, net, tgt_w, src_w, offset, coeff):
     x = torch.cat([rbf(d, offset, coeff), tgt_w[zi], src_w[zj]], dim=-1)
     return net(x)
-
-
-def bf16_round(x):
-    return x.to(torch.bfloat16).to(x.dtype)
-
-
-class _RoundFwd(torch.autograd.Function):
-    """bf16 rounding of a GEMM operand; the gradient passes unchanged."""
-
-    @staticmethod
-    def forward(ctx, x):
-        return bf16_round(x)
-
-    @staticmethod
-    def backward(ctx, g):
-        return g
-
-
-class _RoundGrad(torch.autograd.Function):
-    """Identity whose incoming gradient is rounded to bf16 (a GEMM operand of the backward)."""
-
-    @staticmethod
-    def forward(ctx, x):
-        return x.clone()
-
-    @staticmethod
-    def backward(ctx, g):
-        return bf16_round(g)
-
-
-def mlp_ref_bf16(d, zi, zj, net, tgt_w, src_w, offset, coeff):
-    """RadialProfile with the rounding points of the bf16 edge kernels: Linear1
-    is evaluated at full precision (its rbf block comes from an fp32 table), the
-    two LayerNorm+SiLU activations and the weights of Linear2/3 are bf16 in the
-    forward; the upstream gradient and the LayerNorm-2 input gradient are bf16
-    in the backward; LayerNorm statistics, the LayerNorm-1 input gradient and
-    every accumulation stay at full precision."""
-    F = torch.nn.functional
-    lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
-    y1 = torch.cat([rbf(d, offset, coeff), tgt_w[zi], src_w[zj]], dim=-1) @ lin1.weight.t() + lin1.bias
-    a1 = _RoundFwd.apply(F.silu(F.layer_norm(y1, ln1.normalized_shape, ln1.weight, ln1.bias, ln1.eps)))
-    y2 = _RoundGrad.apply(a1 @ bf16_round(lin2.weight).t() + lin2.bias)
-    a2 = _RoundFwd.apply(F.silu(F.layer_norm(y2, ln2.normalized_shape, ln2.weight, ln2.bias, ln2.eps)))
-    return _RoundGrad.apply(a2 @ bf16_round(lin3.weight).t() + lin3.bias)
 
 
 def attn_ref(q, k, v, dvec, dist, row, col, gi, T, rc, N):

@@ -1,7 +1,6 @@
 """CPU checks of bench.py's accounting: the compulsory (reference-formulation)
-bytes and FLOPs the roofline uses, the implementation byte counts per
-activation storage type, the profile-traffic lookup's coverage, and the
-one-GPU guard."""
+bytes the roofline uses, the implementation byte counts per activation
+storage type, the profile-traffic lookup's coverage, and the one-GPU guard."""
 import json
 import subprocess
 import sys
@@ -14,19 +13,21 @@ import bench  # noqa: E402
 
 def test_attention_bytes_split_by_activation_type():
     N, E = 7, 53
-    # fp32: every term at 4 bytes, counted tensor by tensor
-    fwd32 = 4 * (N * 128 * 8 * 2 + N * 9 * 256 + N * 20 * 256 + N * 3 * 128 + E * 256 + E * 5 + N + 1)
-    assert bench.attn_fwd_bytes(N, E) == fwd32
-    row32 = 4 * (N * 20 * 256 * 2 + N * 1024 * 3 + N * 9 * 256 + N * 3 * 128 + E * (256 + 5 + 256 + 4 + 256))
+    # fp32: every node / edge-list term at 4 bytes, plus the radial-table rows (6 per channel forward,
+    # 8 backward, 256 channels)
+    fwd32 = 4 * (N * 128 * 8 * 2 + N * 9 * 256 + N * 20 * 256 + N * 3 * 128 + E * 6 + N + 1)
+    assert bench.attn_fwd_bytes(N, E) == fwd32 + 4 * E * 256 * 6
+    row32 = 4 * (N * 20 * 256 * 2 + N * 1024 * 3 + N * 9 * 256 + N * 3 * 128 + E * (6 + 4 + 256))
     col32 = 4 * (N * 20 * 256 + N * 1024 * 2 + N * 9 * 256 + 2 * N + E * (256 + 5))
-    assert bench.attn_bwd_bytes(N, E) == row32 + col32
+    assert bench.attn_bwd_bytes(N, E) == row32 + col32 + 4 * E * 256 * 8
     # bf16 storage halves exactly the activation terms: q, k, v, out, grad
     act_fwd = N * (128 * 8 * 2 + 9 * 256 + 20 * 256)
-    assert fwd32 - bench.attn_fwd_bytes(N, E, 2) == 2 * act_fwd
+    assert bench.attn_fwd_bytes(N, E) - bench.attn_fwd_bytes(N, E, 2) == 2 * act_fwd
     act_bwd = N * (2 * 20 * 256 + 2 * 1024 + 9 * 256) + N * (20 * 256 + 1024)
-    assert row32 + col32 - bench.attn_bwd_bytes(N, E, 2) == 2 * act_bwd
+    assert bench.attn_bwd_bytes(N, E) - bench.attn_bwd_bytes(N, E, 2) == 2 * act_bwd
     # the degree kernels read and write fp32 in both modes
     assert bench.deg_fwd_bytes(N, E, 2) == bench.deg_fwd_bytes(N, E)
+    assert bench.deg_fwd_table_bytes(E) == 4 * E * 768 * 6 and bench.deg_bwd_table_bytes(E) == 4 * E * 768 * 8
 
 
 def test_profile_traffic_only_for_the_profiled_workload():
@@ -58,18 +59,6 @@ def test_compulsory_bytes_reference_formulation():
     # bf16 activations halve exactly the activation terms
     assert b - bench.attn_fwd_compulsory(N, M, E, 2) == 2 * (2 * N * 1024 + M * 7424 + N * 7424)
     assert bench.deg_compulsory(N, M, E) == 4 * N * 9 * 256 + 8 * E
-
-
-def test_mlp_flops_executed_and_reference():
-    """Per edge and evaluation: the reference formulation runs fc_easy
-    (2 (512 128 + 128 128 + 128 256) = 229,376 FLOP) in each of 4 layers and three
-    degree profiles (294,912 each); the kernels execute Linear2/3 only
-    (98,304 FLOP per profile forward)."""
-    ref, exe = bench.mlp_step_flops(1.0)
-    assert ref["e2v2_mlp_fwd"] == 4 * 229_376 + 3 * 294_912
-    assert ref["e2v2_mlp_bwd"] == 4 * 229_376 and ref["e2v2_mlp_bwd_deg"] == 3 * 294_912
-    assert exe["e2v2_mlp_fwd"] == 7 * 98_304
-    assert exe["e2v2_mlp_bwd"] == 4 * (98_304 + 256)
 
 
 def test_expanded_nodes_counts_distinct_images():

@@ -62,8 +62,8 @@ def test_cfg4_properties(pkg, cuda):
     identical; a rigid translation and a rotation of atoms and cell leave the
     energy unchanged (1e-6 relative) and rotate the forces (1e-4 rel-L2); the
     net force vanishes (|sum F| below 1e-4 of sqrt(N) * rms F); and the central
-    difference of the energy along a random direction over 64 atoms equals
-    -F . u (2% + 2e-3 eV)."""
+    difference of the energy along the forces of 64 atoms equals -F . u (3% plus
+    8 float32 ulps of the total energy over 2h)."""
     from ubio_molfm_amd import systems
     s = systems.CONFIGS[4]()
     m = _model(cuda)
@@ -83,12 +83,14 @@ def test_cfg4_properties(pkg, cuda):
     e_r, f_r, _ = _ef(m, pos @ qt.T, s, cell=cell_r)
     rel_t = float((f_t - f1).norm() / f1.norm())
     rel_r = float((f1 @ qt.double().T - f_r).norm() / f1.norm())
+    # direction: the forces on 64 random atoms (so the energy change is ~|F_sel| 2h, hundreds of
+    # float32 ulps of the total energy), step 0.02 A
     rng = np.random.default_rng(6)
     idx = torch.as_tensor(rng.choice(N, 64, replace=False), device=cuda)
     u = torch.zeros(N, 3, dtype=torch.float64, device=cuda)
-    u[idx] = torch.as_tensor(rng.normal(size=(64, 3)), device=cuda)
+    u[idx] = f1[idx]
     u /= u.norm()
-    h = 5e-3
+    h = 2e-2
     ep, _, _ = _ef(m, (pos.double() + h * u).float(), s)
     em, _, _ = _ef(m, (pos.double() - h * u).float(), s)
     fd = float(ep - em) / (2 * h)
@@ -100,7 +102,8 @@ def test_cfg4_properties(pkg, cuda):
     assert abs(float(e_r - e1)) <= 1e-6 * abs(float(e1)) + 1e-4
     assert rel_t < 1e-4 and rel_r < 1e-4
     assert net < 1e-4 * np.sqrt(N) * rms
-    assert abs(fd - dirder) <= 0.02 * abs(dirder) + 2e-3
+    ulp = float(np.spacing(np.float32(abs(float(e1)))))
+    assert abs(fd - dirder) <= 0.03 * abs(dirder) + 8 * ulp / (2 * h)
 
 
 def test_cfg5_bf16_against_fp32_and_memory(pkg, cuda):

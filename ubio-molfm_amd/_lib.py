@@ -14,9 +14,11 @@ i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
 EXPORTS = [
     "e2v2_last_error", "e2v2_version", "e2v2_fill_i32", "e2v2_fill_f32", "e2v2_scan_i32",
-    "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose", "e2v2_cluster_slots", "e2v2_morton_keys",
-    "e2v2_mlp_rbf_table_size", "e2v2_mlp_rbf_table", "e2v2_mlp_fwd", "e2v2_mlp_bwd", "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
-    "e2v2_edge_to_pos", "e2v2_mlp_bwd_deg", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd", "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd",
+    "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose", "e2v2_cluster_slots",
+    "e2v2_morton_keys", "e2v2_radial_table_size", "e2v2_radial_table", "e2v2_radial_table_check",
+    "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
+    "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd",
+    "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd", "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd",
     "e2v2_qk_proj_fwd_bf16", "e2v2_qk_proj_bwd_bf16",
 ]
@@ -31,29 +33,23 @@ class NbrPlan(C.Structure):
                 ("stats", vp)]
 
 
-class MlpWeights(C.Structure):
-    _fields_ = [("rtab", vp), ("rtab_n", i32), ("rtab_h", f32), ("ttgt", vp), ("tsrc", vp), ("g1", vp),
-                ("be1", vp), ("w2t", vp), ("b2", vp), ("g2", vp), ("be2", vp), ("w3t", vp), ("b3", vp), ("w2", vp),
-                ("w3", vp), ("w2b", vp), ("w3b", vp), ("w3tb", vp), ("w2tb", vp)]
-
-
-class MlpArgs(C.Structure):
-    _fields_ = [("n_edges", i64), ("n_mlp", i32), ("compute_bf16", i32), ("dist", vp), ("edge_row", vp),
-                ("col", vp), ("node_type", vp), ("save_n", vp), ("save_r", vp), ("w", MlpWeights * 3)]
+class RadialNet(C.Structure):
+    _fields_ = [("w1", vp), ("ld_w1", i32), ("n_emb", i32), ("b1", vp), ("g1", vp), ("be1", vp), ("w2", vp),
+                ("b2", vp), ("g2", vp), ("be2", vp), ("w3", vp), ("b3", vp), ("tgt", vp), ("src", vp)]
 
 
 class AttnArgs(C.Structure):
     _fields_ = [("n_rows", i32), ("n_edges", i64), ("n_heads", i32), ("head_dim", i32), ("channels", i32),
                 ("row_ptr", vp), ("col", vp), ("edge_row", vp), ("key_ptr", vp), ("key_eid", vp),
-                ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("gi", vp),
-                ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32),
+                ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("rtab", vp), ("atom_type", vp),
+                ("n_types", i32), ("rtab_n", i32), ("rtab_h", f32), ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32),
                 ("col_span", i32), ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp)]
 
 
 class DegArgs(C.Structure):
     _fields_ = [("n_rows", i32), ("n_edges", i64), ("channels", i32), ("row_ptr", vp), ("dvec", vp),
-                ("dist", vp), ("fea", vp), ("avg", f32), ("rc", f32), ("env_a", f32), ("env_b", f32),
-                ("env_c", f32)]
+                ("dist", vp), ("col", vp), ("rtab", vp), ("atom_type", vp), ("n_types", i32), ("rtab_n", i32),
+                ("rtab_h", f32), ("avg", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32)]
 
 
 _lib = None

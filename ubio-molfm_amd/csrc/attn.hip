@@ -9,10 +9,15 @@
 // tensor followed by the SO(2) unrotation, h_a - h_b before forward_linear
 // (src/molfm/models/e2former/e2former.py:327-433,
 //  wigner6j/so2_tensor_product.py:341-385): TP(v, r_i) - TP(v, r_j) = TP(v, r_ij).
-// Backward: row pass (dq, dgate, dih, w, dqk, dvec/ddist partials; the softmax
-// row terms come from D_h = sum_{c in h} sum_t G[t,c] out[t,c]) and a column
-// pass over the key CSR (dv_j, dk_j) with no atomics.
+// gate and inputhead of every edge are the fc_easy radial profile of
+// (d, z_i, z_j), interpolated from its per-type-pair distance table (radial.h)
+// where they are used; no per-edge tensor is read from or written to memory
+// except the column pass's inputs below.
+// Backward: row pass (dq, w, dqk, dvec/ddist with the profile's distance
+// derivative; the softmax row terms come from D_h = sum_{c in h} sum_t G[t,c]
+// out[t,c]) and a column pass over the key CSR (dv_j, dk_j) with no atomics.
 #include "common.h"
+#include "radial.h"
 #include "tp_table.h"
 #include "../../include/e2v2.h"
 
@@ -43,6 +48,14 @@ __device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
   Envelope E;
   E.rc = A.rc; E.a = A.env_a; E.b = A.env_b; E.c = A.env_c;
   return E;
+}
+
+// the fc_easy table: channels h (gate) and 128 + h (inputhead) of each row
+constexpr int kTabC = 2 * kH;
+__device__ __forceinline__ RadialTab make_tab(const e2v2_attn_args& A) {
+  RadialTab R;
+  R.tab = A.rtab; R.n_types = A.n_types; R.n_nodes = A.rtab_n; R.nc = kTabC; R.inv_h = 1.0f / A.rtab_h;
+  return R;
 }
 
 // Node activations q, k, v, the output rows and their gradient are stored as TS
@@ -112,6 +125,7 @@ __device__ __forceinline__ void load_qs(const e2v2_attn_args& A, int i, int h, f
 }
 
 struct ChunkEdges {
+  int64_t toff[kCH];   // table offset of the edge's lower node
   int j[kCH];
   float dv[kCH][3];
   float p[kCH];
@@ -119,14 +133,16 @@ struct ChunkEdges {
   float R[kCH];
   float rR[kCH];
   float d[kCH];
+  float tt[kCH];       // fraction of the distance in its node interval
 };
 
-__device__ __forceinline__ void load_chunk(const e2v2_attn_args& A, const Envelope& env, int e0, int nc,
-                                           ChunkEdges& ce) {
+__device__ __forceinline__ void load_chunk(const e2v2_attn_args& A, const Envelope& env, const RadialTab& R, int ti,
+                                           int e0, int nc, ChunkEdges& ce) {
   const int t = threadIdx.x;
   if (t < nc) {
     const int64_t e = (int64_t)e0 + t;
-    ce.j[t] = A.col[e];
+    const int j = A.col[e];
+    ce.j[t] = j;
     ce.dv[t][0] = A.dvec[3 * e];
     ce.dv[t][1] = A.dvec[3 * e + 1];
     ce.dv[t][2] = A.dvec[3 * e + 2];
@@ -138,6 +154,9 @@ __device__ __forceinline__ void load_chunk(const e2v2_attn_args& A, const Envelo
     ce.dp[t] = dp;
     ce.R[t] = fmaxf(d, 1e-6f);
     ce.rR[t] = 1.0f / ce.R[t];
+    float tt;
+    ce.toff[t] = radial_node(R, ti * R.n_types + A.atom_type[j], d, tt);
+    ce.tt[t] = tt;
   }
 }
 
@@ -156,6 +175,8 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, TS* __restri
   const int h = t & (kH - 1), half = t >> 7;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   const Envelope env = make_env(A);
+  const RadialTab R = make_tab(A);
+  const int ti = A.atom_type[i];
   float qs[kD];
   load_qs<TS>(A, i, h, qs);
   float m_run = -INFINITY, s_run = 0.f;
@@ -166,13 +187,20 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, TS* __restri
   const int hc = t & (kH - 1);  // head of channel c = t
   for (int c0 = 0; c0 < n; c0 += kCH) {
     const int nc = min(kCH, n - c0);
-    load_chunk(A, env, b + c0, nc, ce);
+    load_chunk(A, env, R, ti, b + c0, nc, ce);
     __syncthreads();
     for (int el = half; el < nc; el += 2) {
-      const int64_t e = (int64_t)b + c0 + el;
       const float qk = qk_dot(qs, Kp + ((size_t)ce.j[el] * kH + h) * kD);
-      a_s[el][h] = ntload(A.gi + e * (2 * kH) + h) * qk;
-      coef_s[el][h] = ntload(A.gi + e * (2 * kH) + kH + h);   // input head, scaled below
+      // gate (channel h) and inputhead (channel 128 + h): rows 0..2 at the two nodes
+      const float* tb = R.tab + ce.toff[el] + h;
+      const Hermite5 Hw = hermite5(ce.tt[el]);
+      constexpr int nb = 4 * kTabC;
+      const float gate = herm_value(Hw, tb[0], tb[kTabC], tb[2 * kTabC], tb[nb], tb[nb + kTabC], tb[nb + 2 * kTabC]);
+      const float* tb2 = tb + kH;
+      const float ih = herm_value(Hw, tb2[0], tb2[kTabC], tb2[2 * kTabC], tb2[nb], tb2[nb + kTabC],
+                                  tb2[nb + 2 * kTabC]);
+      a_s[el][h] = gate * qk;
+      coef_s[el][h] = ih;   // input head, scaled below
     }
     __syncthreads();
     if (t < kH) {
@@ -623,7 +651,7 @@ template <typename TS>
 struct HeadEdge {
   TS k[kD];
   TS v0[kNV], v1[kNV];
-  float gate, ih;
+  float tg[8], ti[8];   // table rows 0..3 at the lower and upper node: gate, inputhead
 };
 __device__ __forceinline__ void load8_raw(const float* p, float (&v)[8]) { load8(p, v); }
 __device__ __forceinline__ void load8_raw(const __bf16* p, __bf16 (&v)[8]) {
@@ -635,21 +663,24 @@ __device__ __forceinline__ void load8_raw(const __bf16* p, __bf16 (&v)[8]) {
 // Backward row pass, one workgroup per query row; thread t owns head h = t % 128
 // with both of its channels (h, h + 128) and the row's edges of parity t / 128.
 // The edge index is uniform per wave (scalar loads of the edge record), and
-// the gathers of the next edge are issued before the current one is applied.
-// Per edge a thread recomputes its logit and
-// weight, forms u = dA^T v_j for both channels (dA = T^T G_i) and with it the
-// head's dL/dw, runs the softmax / gate / distance backward for its head and
-// accumulates dq from the k_j row it already holds, so nothing crosses threads
-// but the per-edge sums over heads (dL/d dvec, dL/dd): the 64 heads of a wave
-// by lane swaps and DPP (wave_sum4), the two waves of a parity in LDS, added
-// in a fixed order once per chunk of up to 128 edges.  The head-independent
-// edge terms (column, distance, envelope, 1/d, dvec) are formed once per edge
-// at the start of a chunk and read from LDS.
+// the gathers of the next edge (k_j, v_j and the head's gate / inputhead table
+// rows) are issued before the current one is applied.  Per edge a thread
+// interpolates the head's gate and inputhead and their distance derivatives,
+// recomputes its logit and weight, forms u = dA^T v_j for both channels
+// (dA = T^T G_i) and with it the head's dL/dw, runs the softmax / gate /
+// distance backward for its head (the profile's part dL/dgate gate' +
+// dL/dih ih' included) and accumulates dq from the k_j row it already holds,
+// so nothing crosses threads but the per-edge sums over heads (dL/d dvec,
+// dL/dd): the 64 heads of a wave by lane swaps and DPP (wave_sum4), the two
+// waves of a parity in LDS, added in a fixed order once per chunk of up to 128
+// edges.  The head-independent edge terms (column, distance, envelope, 1/d,
+// dvec, table node and fraction) are formed once per edge at the start of a
+// chunk and read from LDS.
 template <typename TS>
 __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const TS* __restrict__ G,
                                                          const TS* __restrict__ O, const float* __restrict__ mrow,
                                                          const float* __restrict__ srow,
-                                                         const int32_t* __restrict__ cnt, float* __restrict__ dgi,
+                                                         const int32_t* __restrict__ cnt,
                                                          float* __restrict__ ddv, float* __restrict__ dd,
                                                          float* __restrict__ dq, float* __restrict__ w_out,
                                                          float* __restrict__ dqk_out) {
@@ -658,8 +689,12 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
   __shared__ float dq_s[kH][kD];
   __shared__ float4 er_a[2 * CH];             // per edge of the chunk: p, dp/dd, 1/max(d, 1e-6), d
   __shared__ float4 er_b[2 * CH];             // dvec, column (int bits)
+  __shared__ int64_t er_toff[2 * CH];         // table offset of the lower node
+  __shared__ float er_t[2 * CH];              // fraction in the node interval
   const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
   if (i >= A.n_rows) return;
+  const RadialTab R = make_tab(A);
+  const int ti = A.atom_type[i];
   const int h = t & (kH - 1), par = t >> 7, lane = t & (kWave - 1), wsub = (t >> 6) & 1;
   const TS* __restrict__ Kp = static_cast<const TS*>(A.k);
   const TS* __restrict__ Vp = static_cast<const TS*>(A.v);
@@ -715,22 +750,33 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
       X.v0[r] = *reinterpret_cast<const TS*>(vb + vof);
       X.v1[r] = *reinterpret_cast<const TS*>(vb + vof + kH * sizeof(TS));
     }
-    X.gate = A.gi[e * (2 * kH) + h];
-    X.ih = A.gi[e * (2 * kH) + kH + h];
+    const float* tb = R.tab + er_toff[el - c0] + h;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      X.tg[q] = tb[q * kTabC];
+      X.tg[4 + q] = tb[(4 + q) * kTabC];
+      X.ti[q] = tb[q * kTabC + kH];
+      X.ti[4 + q] = tb[(4 + q) * kTabC + kH];
+    }
   };
   auto apply = [&](int el, int slot, const L& X) {
     const int64_t e = (int64_t)b + el;
     const float4 ea = er_a[slot], eb = er_b[slot];
     const float pe = ea.x, dpe = ea.y, rR = ea.z, d = ea.w;
     const float dvx = eb.x, dvy = eb.y, dvz = eb.z;
+    const Hermite5 Hw = hermite5(er_t[slot]);
+    const float gate = herm_value(Hw, X.tg[0], X.tg[1], X.tg[2], X.tg[4], X.tg[5], X.tg[6]);
+    const float ih = herm_value(Hw, X.ti[0], X.ti[1], X.ti[2], X.ti[4], X.ti[5], X.ti[6]);
+    const float gate_d = herm_value(Hw, X.tg[1], X.tg[2], X.tg[3], X.tg[5], X.tg[6], X.tg[7]) * R.inv_h;
+    const float ih_d = herm_value(Hw, X.ti[1], X.ti[2], X.ti[3], X.ti[5], X.ti[6], X.ti[7]) * R.inv_h;
     float kf[kD];
 #pragma unroll
     for (int q = 0; q < kD; ++q) kf[q] = f32(X.k[q]);
     const float qk = half_dot(qs, kf) + half_dot(qs + 4, kf + 4);
-    const float a = X.gate * qk;
+    const float a = gate * qk;
     const float ex = expf(a - m);
     const float ee = ex * pe;
-    const float alpha = (ee * X.ih) * inv;
+    const float alpha = (ee * ih) * inv;
     const float w = alpha * rR;
     float U[3];
 #pragma unroll
@@ -747,19 +793,19 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
     const float dalpha = dw * rR;
     const float dR = (d > 1e-6f) ? -dalpha * alpha * rR : 0.f;
     const float dih = dalpha * ee * inv;
-    const float de = dalpha * X.ih * inv - dsum;
+    const float de = dalpha * ih * inv - dsum;
     float da = de * ee;
     if (a == m) da += dmc;
     const float dpv = de * ex;
-    const float dqk = da * X.gate;
+    const float dqk = da * gate;
     ntstore(w, w_out + e * kH + h);
-    ntstore(da * qk, dgi + e * (2 * kH) + h);
-    ntstore(dih, dgi + e * (2 * kH) + kH + h);
     ntstore(dqk, dqk_out + e * kH + h);
 #pragma unroll
     for (int q = 0; q < kD; ++q) dqa[q] = fmaf(dqk, kf[q], dqa[q]);
+    // dL/dd of this head: envelope, 1/d, and the profile (dL/dgate gate' + dL/dih ih')
+    const float ddh = fmaf(da * qk, gate_d, fmaf(dih, ih_d, fmaf(dpv, dpe, dR)));
     // sums over the 64 heads of this wave; lane 16k holds the sum of value k
-    const float sum = wave_sum4(w * U[0], w * U[1], w * U[2], fmaf(dpv, dpe, dR), lane);
+    const float sum = wave_sum4(w * U[0], w * U[1], w * U[2], ddh, lane);
     if ((lane & 15) == 0) part[slot][wsub][lane >> 4] = sum;
   };
   for (c0 = 0; c0 < n; c0 += 2 * CH) {
@@ -770,7 +816,11 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
       float pe, dpe;
       env.eval(d, pe, dpe);
       er_a[t] = make_float4(pe, dpe, 1.0f / fmaxf(d, 1e-6f), d);
-      er_b[t] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], __int_as_float(A.col[e]));
+      const int j = A.col[e];
+      er_b[t] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], __int_as_float(j));
+      float tt;
+      er_toff[t] = radial_node(R, ti * R.n_types + A.atom_type[j], d, tt);
+      er_t[t] = tt;
     }
     __syncthreads();
     {
@@ -818,6 +868,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
 
 using namespace e2v2;
 
+static int check_table(const e2v2_attn_args& A, const char* who);
+
 E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, float* srow, int32_t* cnt,
                            hipStream_t s) {
   const e2v2_attn_args& A = *args;
@@ -825,6 +877,7 @@ E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, f
                "attn_fwd: built for H=%d D=%d C=%d, got H=%d D=%d C=%d", kH, kD, kC, A.n_heads, A.head_dim,
                A.channels);
   if (A.n_rows == 0) return 0;
+  if (int rc = check_table(A, "attn_fwd")) return rc;
   const dim3 grid(xcd_grid(A.n_rows));
   if (A.act_bf16) {
     hipLaunchKernelGGL(k_attn_fwd<__bf16>, grid, dim3(256), 0, s, A, static_cast<__bf16*>(out), mrow, srow, cnt);
@@ -837,10 +890,10 @@ E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, f
 
 template <typename TS>
 static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, const float* mrow, const float* srow,
-                           const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
+                           const int32_t* cnt, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
                            float* w_edge, float* dqk_edge, hipStream_t s) {
   const dim3 grid(xcd_grid(A.n_rows));
-  hipLaunchKernelGGL(k_attn_bwd_row_hp<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, dgi, ddvec, ddist, dq,
+  hipLaunchKernelGGL(k_attn_bwd_row_hp<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, ddvec, ddist, dq,
                      w_edge, dqk_edge);
   E2V2_LAUNCHED("k_attn_bwd_row");
   if (A.col_slot_member) {
@@ -856,9 +909,19 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
   return 0;
 }
 
+static int check_table(const e2v2_attn_args& A, const char* who) {
+  E2V2_REQUIRE(A.rtab && A.atom_type && A.n_types >= 1 && A.n_types <= E2V2_MAX_TYPES && A.rtab_n >= 2 &&
+                   A.rtab_h > 0.f,
+               "%s: needs the fc_easy table and atom types (n_types %d, rtab_n %d)", who, A.n_types, A.rtab_n);
+  E2V2_REQUIRE((double)A.rc * (1.0 / A.rtab_h) <= (double)(A.rtab_n - 1),
+               "%s: table of %d nodes (h %g) does not cover the cutoff %g", who, A.rtab_n, (double)A.rtab_h,
+               (double)A.rc);
+  return 0;
+}
+
 E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, const void* out, const float* mrow,
-                           const float* srow, const int32_t* cnt, float* dgi, float* ddvec, float* ddist, float* dq,
-                           float* dk, float* dv, float* w_edge, float* dqk_edge, hipStream_t s) {
+                           const float* srow, const int32_t* cnt, float* ddvec, float* ddist, float* dq, float* dk,
+                           float* dv, float* w_edge, float* dqk_edge, hipStream_t s) {
   const e2v2_attn_args& A = *args;
   E2V2_REQUIRE(A.n_heads == kH && A.head_dim == kD && A.channels == kC,
                "attn_bwd: built for H=%d D=%d C=%d", kH, kD, kC);
@@ -868,9 +931,10 @@ E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, con
   // the row pass gathers k_j and v_j through 32-bit byte offsets within one row block
   E2V2_REQUIRE((uint64_t)A.n_rows * kH * kD * (A.act_bf16 ? 2 : 4) < (1ull << 32),
                "attn_bwd: %d rows exceed the 32-bit gather offsets of the row pass", A.n_rows);
+  if (int rc = check_table(A, "attn_bwd")) return rc;
   if (A.act_bf16)
     return attn_bwd_launch(A, static_cast<const __bf16*>(grad_out), static_cast<const __bf16*>(out), mrow, srow,
-                           cnt, dgi, ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
+                           cnt, ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
   return attn_bwd_launch(A, static_cast<const float*>(grad_out), static_cast<const float*>(out), mrow, srow, cnt,
-                         dgi, ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
+                         ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
 }

@@ -1,0 +1,315 @@
+// Radial profiles as distance tables, built in float64.
+//
+// RadialProfile [K0 + 2 E -> 128 -> LN -> SiLU -> 128 -> LN -> SiLU -> 256]
+// (src/molfm/models/e2former/module_utils.py:2151-2178) applied to
+// x_edge = [rbf(d), tgt[z_i], src[z_j]] (e2former.py:258-266 for fc_easy,
+// e2former.py:709-733 for the degree embedding's gbf_projs) with the Gaussian
+// basis rbf_k(d) = exp(coeff (d - mu_k)^2) (module_utils.py:1853-1869) is, for
+// one pair of atom types, a function of the scalar distance d only.  Every
+// (type pair, node d = n h) gets the truncated Taylor series of the profile
+// output in delta = d - n h to third order, propagated exactly through each op
+// in float64 ("jets": value and three derivatives), and stored as the rows
+// h^k d^k f/dd^k, k = 0..3, of the table the edge kernels interpolate
+// (quintic Hermite, radial.h).  e2v2_radial_table_check evaluates the profile
+// at every interval midpoint and reports the interpolation error, so the host
+// can halve h until the table meets its tolerance.
+#include <cmath>
+
+#include "common.h"
+#include "radial.h"
+#include "../../include/e2v2.h"
+
+namespace e2v2 {
+
+constexpr int kRH = 128;   // hidden width of the profiles
+constexpr int kRO = 256;   // output width of one profile
+constexpr int kNB = 256;   // Gaussian basis functions
+
+struct Jet {
+  double c[4];
+};
+
+__device__ __forceinline__ Jet jconst(double v) { return Jet{{v, 0.0, 0.0, 0.0}}; }
+
+__device__ __forceinline__ Jet jmul(const Jet& a, const Jet& b) {
+  Jet r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j <= k; ++j) s += a.c[j] * b.c[k - j];
+    r.c[k] = s;
+  }
+  return r;
+}
+
+// y = exp(a): y' = y a'  ->  k y_k = sum_{j=1..k} j a_j y_{k-j}
+__device__ __forceinline__ Jet jexp(const Jet& a) {
+  Jet y;
+  y.c[0] = exp(a.c[0]);
+#pragma unroll
+  for (int k = 1; k < 4; ++k) {
+    double s = 0.0;
+#pragma unroll
+    for (int j = 1; j <= k; ++j) s += j * a.c[j] * y.c[k - j];
+    y.c[k] = s / k;
+  }
+  return y;
+}
+
+// y = a^p: a y' = p a' y  ->  k a_0 y_k = sum_{j=1..k} (p j - (k - j)) a_j y_{k-j}
+__device__ __forceinline__ Jet jpow(const Jet& a, double p) {
+  Jet y;
+  y.c[0] = pow(a.c[0], p);
+#pragma unroll
+  for (int k = 1; k < 4; ++k) {
+    double s = 0.0;
+#pragma unroll
+    for (int j = 1; j <= k; ++j) s += (p * j - (k - j)) * a.c[j] * y.c[k - j];
+    y.c[k] = s / (k * a.c[0]);
+  }
+  return y;
+}
+
+// silu(a) = a sigma(a); sigma' = sigma (1 - sigma) a'  ->  k s_k = sum_j j a_j u_{k-j}, u = s - s^2
+__device__ __forceinline__ Jet jsilu(const Jet& a) {
+  Jet s, u;
+  const double a0 = a.c[0];
+  s.c[0] = a0 >= 0.0 ? 1.0 / (1.0 + exp(-a0)) : exp(a0) / (1.0 + exp(a0));
+  u.c[0] = s.c[0] - s.c[0] * s.c[0];
+#pragma unroll
+  for (int k = 1; k < 4; ++k) {
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 1; j <= k; ++j) acc += j * a.c[j] * u.c[k - j];
+    s.c[k] = acc / k;
+    double sq = 0.0;
+#pragma unroll
+    for (int j = 0; j <= k; ++j) sq += s.c[j] * s.c[k - j];
+    u.c[k] = s.c[k] - sq;
+  }
+  return jmul(a, s);
+}
+
+// Sum over the 128 threads of the block, every order at once (fixed order).
+__device__ __forceinline__ Jet block_sum128(Jet v, double (*red)[4]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) red[t][k] = v.c[k];
+  __syncthreads();
+  for (int s = kRH / 2; s > 0; s >>= 1) {
+    if (t < s) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) red[t][k] += red[t + s][k];
+    }
+    __syncthreads();
+  }
+  Jet r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.c[k] = red[0][k];
+  __syncthreads();
+  return r;
+}
+
+// LayerNorm(128) with affine (g, b), eps 1e-5, of this thread's channel
+__device__ __forceinline__ Jet jlayernorm(const Jet& x, double g, double b, double (*red)[4]) {
+  Jet mean = block_sum128(x, red);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) mean.c[k] *= 1.0 / kRH;
+  Jet u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) u.c[k] = x.c[k] - mean.c[k];
+  Jet var = block_sum128(jmul(u, u), red);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) var.c[k] *= 1.0 / kRH;
+  var.c[0] += 1e-5;
+  const Jet r = jpow(var, -0.5);
+  Jet n = jmul(u, r);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) n.c[k] *= g;
+  n.c[0] += b;
+  return n;
+}
+
+// Output jets of one profile at d = d0 (type pair (ta, tb)) for channels t and t + 128.
+__device__ void profile_jets(const e2v2_radial_net& W, const float* __restrict__ mu, double coeff, int za, int zb,
+                             double d0, Jet (&out)[2]) {
+  __shared__ double rbf_s[kNB][4];
+  __shared__ double hid_s[kRH][4];
+  __shared__ double red[kRH][4];
+  const int t = threadIdx.x;
+  for (int k = t; k < kNB; k += kRH) {   // rbf_k(d0 + delta) = exp(coeff (x + delta)^2), x = d0 - mu_k
+    const double x = d0 - (double)mu[k];
+    const Jet a{{coeff * x * x, 2.0 * coeff * x, coeff, 0.0}};
+    const Jet y = jexp(a);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rbf_s[k][q] = y.c[q];
+  }
+  __syncthreads();
+  // Linear1: rbf block + the constant type blocks and bias
+  const float* w1 = W.w1 + (size_t)t * W.ld_w1;
+  Jet z = jconst((double)W.b1[t]);
+  for (int k = 0; k < kNB; ++k) {
+    const double w = (double)w1[k];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) z.c[q] += w * rbf_s[k][q];
+  }
+  const float* tg = W.tgt + (size_t)za * W.n_emb;
+  const float* sr = W.src + (size_t)zb * W.n_emb;
+  double cst = 0.0;
+  for (int e = 0; e < W.n_emb; ++e)
+    cst += (double)w1[kNB + e] * (double)tg[e] + (double)w1[kNB + W.n_emb + e] * (double)sr[e];
+  z.c[0] += cst;
+  Jet s1 = jsilu(jlayernorm(z, (double)W.g1[t], (double)W.be1[t], red));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) hid_s[t][q] = s1.c[q];
+  __syncthreads();
+  // Linear2
+  const float* w2 = W.w2 + (size_t)t * kRH;
+  z = jconst((double)W.b2[t]);
+  for (int j = 0; j < kRH; ++j) {
+    const double w = (double)w2[j];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) z.c[q] += w * hid_s[j][q];
+  }
+  __syncthreads();
+  const Jet s2 = jsilu(jlayernorm(z, (double)W.g2[t], (double)W.be2[t], red));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) hid_s[t][q] = s2.c[q];
+  __syncthreads();
+  // Linear3: outputs t and t + 128
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int o = t + h * kRH;
+    const float* w3 = W.w3 + (size_t)o * kRH;
+    Jet y = jconst((double)W.b3[o]);
+    for (int j = 0; j < kRH; ++j) {
+      const double w = (double)w3[j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) y.c[q] += w * hid_s[j][q];
+    }
+    out[h] = y;
+  }
+  __syncthreads();
+}
+
+// Rows h^k f^(k) = h^k k! c_k of the jets
+__device__ __forceinline__ void jet_rows(const Jet& y, double h, double (&r)[4]) {
+  r[0] = y.c[0];
+  r[1] = h * y.c[1];
+  r[2] = h * h * 2.0 * y.c[2];
+  r[3] = h * h * h * 6.0 * y.c[3];
+}
+
+// one block per (node, pair); writes channels [col0, col0 + 256) of rows k = 0..3
+__global__ __launch_bounds__(kRH) void k_radial_table(e2v2_radial_net W, const float* __restrict__ mu, double coeff,
+                                                      const int32_t* __restrict__ type_z, int n_types, int n_nodes,
+                                                      double h, float* __restrict__ tab, int nc, int col0) {
+  const int n = blockIdx.x, p = blockIdx.y;
+  const int za = type_z[p / n_types], zb = type_z[p % n_types];
+  Jet y[2];
+  profile_jets(W, mu, coeff, za, zb, (double)n * h, y);
+  float* base = tab + ((int64_t)p * n_nodes + n) * (4 * nc) + col0;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    double r[4];
+    jet_rows(y[hh], h, r);
+    const int o = threadIdx.x + hh * kRH;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) base[k * nc + o] = (float)r[k];
+  }
+}
+
+// Interpolation error at the midpoint of every node interval: err[0] = max |f - f~|,
+// err[1] = max |f|, err[2] = max h |f' - f~'|, err[3] = max h |f'| (float bits; non-negative
+// floats order like their bit patterns, so the unsigned atomic max is exact and deterministic).
+__global__ __launch_bounds__(kRH) void k_radial_check(e2v2_radial_net W, const float* __restrict__ mu, double coeff,
+                                                      const int32_t* __restrict__ type_z, int n_types, int n_nodes,
+                                                      double h, const float* __restrict__ tab, int nc, int col0,
+                                                      uint32_t* __restrict__ err) {
+  const int n = blockIdx.x, p = blockIdx.y;
+  const int za = type_z[p / n_types], zb = type_z[p % n_types];
+  Jet y[2];
+  profile_jets(W, mu, coeff, za, zb, ((double)n + 0.5) * h, y);
+  const float* A = tab + ((int64_t)p * n_nodes + n) * (4 * nc) + col0;
+  const float* B = A + 4 * nc;
+  const Hermite5 H = hermite5(0.5f);
+  float e_v = 0.f, m_v = 0.f, e_d = 0.f, m_d = 0.f;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int o = threadIdx.x + hh * kRH;
+    const float v = herm_value(H, A[o], A[nc + o], A[2 * nc + o], B[o], B[nc + o], B[2 * nc + o]);
+    const float dv = herm_value(H, A[nc + o], A[2 * nc + o], A[3 * nc + o], B[nc + o], B[2 * nc + o],
+                                B[3 * nc + o]);
+    e_v = fmaxf(e_v, (float)fabs((double)v - y[hh].c[0]));
+    m_v = fmaxf(m_v, (float)fabs(y[hh].c[0]));
+    e_d = fmaxf(e_d, (float)fabs((double)dv - h * y[hh].c[1]));
+    m_d = fmaxf(m_d, (float)fabs(h * y[hh].c[1]));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    e_v = fmaxf(e_v, __shfl_xor(e_v, o, kWave));
+    m_v = fmaxf(m_v, __shfl_xor(m_v, o, kWave));
+    e_d = fmaxf(e_d, __shfl_xor(e_d, o, kWave));
+    m_d = fmaxf(m_d, __shfl_xor(m_d, o, kWave));
+  }
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    atomicMax(err + 0, __float_as_uint(e_v));
+    atomicMax(err + 1, __float_as_uint(m_v));
+    atomicMax(err + 2, __float_as_uint(e_d));
+    atomicMax(err + 3, __float_as_uint(m_d));
+  }
+}
+
+}  // namespace e2v2
+
+using namespace e2v2;
+
+static int check_net(const e2v2_radial_net* W, const char* who) {
+  E2V2_REQUIRE(W && W->w1 && W->b1 && W->g1 && W->be1 && W->w2 && W->b2 && W->g2 && W->be2 && W->w3 && W->b3 &&
+                   W->tgt && W->src,
+               "%s: incomplete radial profile weights", who);
+  E2V2_REQUIRE(W->n_emb > 0 && W->ld_w1 == kNB + 2 * W->n_emb,
+               "%s: Linear1 must read [rbf(256) | tgt(n_emb) | src(n_emb)] (ld_w1 %d, n_emb %d)", who, W->ld_w1,
+               W->n_emb);
+  return 0;
+}
+
+E2V2_API int e2v2_radial_table_size(float rc, float rbf_coeff, int32_t refine, int32_t* n_nodes, float* h) {
+  E2V2_REQUIRE(rc > 0.f && rbf_coeff < 0.f && n_nodes && h && refine >= 0 && refine <= 6,
+               "radial_table_size: need rc > 0, rbf_coeff < 0, 0 <= refine <= 6");
+  const double sigma = std::sqrt(-0.5 / (double)rbf_coeff);
+  const double hh = std::ldexp(1.0, (int)std::floor(std::log2(0.2 * sigma)) - refine);
+  const double n = std::floor((double)rc / hh) + 2.0;
+  E2V2_REQUIRE(n <= 1 << 20, "radial_table_size: %.0f nodes (rc %g, width %g) is too many", n, (double)rc, sigma);
+  *n_nodes = (int32_t)n;
+  *h = (float)hh;
+  return 0;
+}
+
+E2V2_API int e2v2_radial_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                               const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h, float* tab,
+                               int32_t nc, int32_t col0, hipStream_t s) {
+  if (int rc = check_net(net, "radial_table")) return rc;
+  E2V2_REQUIRE(rbf_offset && type_z && tab && n_types >= 1 && n_types <= E2V2_MAX_TYPES && n_nodes >= 2 && h > 0.f,
+               "radial_table: bad arguments (n_types %d, n_nodes %d)", n_types, n_nodes);
+  E2V2_REQUIRE(nc % kRO == 0 && col0 % kRO == 0 && col0 + kRO <= nc,
+               "radial_table: channel block [%d, %d) outside rows of %d", col0, col0 + kRO, nc);
+  hipLaunchKernelGGL(k_radial_table, dim3((unsigned)n_nodes, (unsigned)(n_types * n_types)), dim3(kRH), 0, s, *net,
+                     rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, col0);
+  E2V2_LAUNCHED("k_radial_table");
+  return 0;
+}
+
+E2V2_API int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                                     const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h,
+                                     const float* tab, int32_t nc, int32_t col0, uint32_t* err, hipStream_t s) {
+  if (int rc = check_net(net, "radial_table_check")) return rc;
+  E2V2_REQUIRE(rbf_offset && type_z && tab && err && n_types >= 1 && n_types <= E2V2_MAX_TYPES && n_nodes >= 2,
+               "radial_table_check: bad arguments");
+  E2V2_REQUIRE(nc % kRO == 0 && col0 % kRO == 0 && col0 + kRO <= nc, "radial_table_check: bad channel block");
+  hipLaunchKernelGGL(k_radial_check, dim3((unsigned)(n_nodes - 1), (unsigned)(n_types * n_types)), dim3(kRH), 0, s,
+                     *net, rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, col0, err);
+  E2V2_LAUNCHED("k_radial_check");
+  return 0;
+}

@@ -13,6 +13,7 @@
 """
 from __future__ import annotations
 
+import weakref
 from types import SimpleNamespace
 from typing import Dict, Optional
 
@@ -89,18 +90,38 @@ class E2FormerBackbone(nn.Module):
         self.max_neighbors = self.decoder.max_neighbors
         self.max_radius = float(self.decoder.max_radius)
         self.cells_per_direction = int(kwargs.get("pbc_expanded_num_cell_per_direction", 4))
+        self._types = None
         self.set_compute_dtype(kwargs.get("compute_dtype", "fp32"))
 
     def set_compute_dtype(self, dtype) -> None:
-        """'fp32' (default) or 'bf16': in bf16 mode every GEMM of the stack (edge
-        radial MLPs, per-node irreps linears, Q/K heads, SO(2) output linears, gate)
-        takes bf16 operands with fp32 accumulation; parameters stay fp32 (bf16
-        copies are cached), and activations, softmax statistics, normalisations
+        """'fp32' (default) or 'bf16': in bf16 mode every GEMM of the stack (per-node
+        irreps linears, Q/K projections and heads, SO(2) output linears, gate) takes
+        bf16 operands with fp32 accumulation and the attention's gathered
+        activations are stored in bf16; parameters stay fp32 (bf16 copies are
+        cached), the radial-profile tables, softmax statistics, normalisations
         and all reductions are fp32."""
         name = {torch.float32: "fp32", torch.bfloat16: "bf16"}.get(dtype, dtype)
         if name not in ("fp32", "float32", "bf16", "bfloat16"):
             raise ValueError(f"compute_dtype must be 'fp32' or 'bf16', got {dtype!r}")
         self.compute_bf16 = name in ("bf16", "bfloat16")
+
+    def type_slots(self, Z: torch.Tensor):
+        """(type_z [T] int32: the atomic numbers present, ascending; type_key: the
+        same as a host tuple; slot [N] int32: each atom's index into type_z).  One
+        host readback per new Z tensor; repeated calls with the same live tensor
+        (an MD loop) reuse the result."""
+        cached = self._types
+        if cached is not None and cached[0]() is Z and cached[1] == Z._version:
+            return cached[2]
+        zs = torch.unique(Z.long())
+        key = tuple(int(z) for z in zs.cpu())
+        if key and (key[0] < 0 or key[-1] > 255):
+            raise ValueError(f"atomic numbers must lie in [0, 255], got {key[0]}..{key[-1]}")
+        lut = torch.zeros(256, dtype=torch.int32, device=Z.device)
+        lut[zs] = torch.arange(len(key), dtype=torch.int32, device=Z.device)
+        out = (zs.to(torch.int32).contiguous(), key, lut[Z.long()].contiguous())
+        self._types = (weakref.ref(Z), Z._version, out)
+        return out
 
     # -- flat interface -------------------------------------------------------
     def forward_flat(self, pos: torch.Tensor, Z: torch.Tensor, graph_ptr, cell, pbc, charge=None,
@@ -110,16 +131,17 @@ class E2FormerBackbone(nn.Module):
         the neighbour list refer to atoms ``perm`` (Morton order within each graph;
         identity when ``reorder`` is False).  grid_box: see ``build_neighbors``."""
         perm = None
+        type_z, type_key, slot = self.type_slots(Z)
         if reorder and nl is None:
             perm = spatial_order(pos.detach(), graph_ptr)
             pos = pos[perm]
-            Z = Z[perm]
+            slot = slot[perm]
         if nl is None:
             nl = build_neighbors(pos.detach(), graph_ptr, cell, pbc, self.max_radius, 1e-4, self.max_neighbors,
                                  self.cells_per_direction, grid_box=grid_box)
         dvec, dist = EdgeGeometryFn.apply(pos, nl)
-        node_type = Z.to(torch.int32).contiguous()
-        ctx = EdgeContext(nl, dvec, dist, node_type, self.decoder.rbf, self.max_radius, self.compute_bf16)
+        ctx = EdgeContext(nl, dvec, dist, slot.contiguous(), type_z, type_key, self.decoder.rbf, self.max_radius,
+                          self.compute_bf16)
         sys_node = None
         if charge is not None:
             B = len(graph_ptr) - 1

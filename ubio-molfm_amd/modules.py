@@ -18,7 +18,7 @@ from torch.profiler import record_function
 
 from . import so3
 from . import _lib
-from .ops import AttentionFn, DegreeEmbedFn, MLPCache
+from .ops import AttentionFn, DegreeEmbedFn, RadialCache
 
 
 def _e3nn_normalize2mom(f) -> float:
@@ -551,7 +551,7 @@ class GaussianSmearing(nn.Module):
 
 
 class RadialProfile(nn.Module):
-    """module_utils.py:2151-2178 (parameters only; evaluated by e2v2_mlp_*)."""
+    """module_utils.py:2151-2178 (parameters only; evaluated through its distance table, ops.RadialTable)."""
 
     def __init__(self, ch_list, use_layer_norm=True, use_offset=True):
         super().__init__()
@@ -816,11 +816,14 @@ class SmoothLeakyReLU(nn.Module):
 
 
 class EdgeContext:
-    """Per-evaluation edge data shared by every layer."""
+    """Per-evaluation edge data shared by every layer: the neighbour list, the edge
+    geometry, each atom's type slot (atom_type [N], into type_z [T], the atomic
+    numbers present; type_key the host tuple of type_z) for the radial tables."""
 
-    def __init__(self, nl, dvec, dist, node_type, rbf: GaussianSmearing, rc: float, bf16: bool = False):
+    def __init__(self, nl, dvec, dist, atom_type, type_z, type_key, rbf: GaussianSmearing, rc: float,
+                 bf16: bool = False):
         self.nl, self.dvec, self.dist = nl, dvec, dist
-        self.node_type = node_type
+        self.atom_type, self.type_z, self.type_key = atom_type, type_z, type_key
         self.rbf_offset = rbf.offset.float().contiguous()
         self.rbf_coeff = float(rbf.coeff)
         self.rc = rc
@@ -852,7 +855,7 @@ class E2AttentionArbOrder_sparse(nn.Module):
         self.first_order_tp = E2TensorProductSO2_FirstOrder(None, None, head=num_attn_heads, order=1, lmax=lmax,
                                                             in_c=C, out_c=C)
         self.proj_first = SO3_Linear_e2former(num_attn_heads * 2, C, lmax=lmax)
-        self._mlp = MLPCache()
+        self._radial = RadialCache()
 
     def qk_weights(self, bf16: bool = False):
         params = (self.query_linear.weight, self.query_linear.weight2, self.query_linear.bias,
@@ -881,13 +884,12 @@ class E2AttentionArbOrder_sparse(nn.Module):
                                        pv.bias.detach())
             q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
             k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
-        packed = self._mlp.get([self.fc_easy.net], self.target_embedding, self.source_embedding, ctx.rbf_offset,
-                               ctx.rbf_coeff, ctx.rc, bf16)
-        # the radial profile ("rbf function-a") runs inside the attention launches
+        with record_function("rbf function-a"):   # fc_easy as a distance table, built once per weight version
+            table = self._radial.get([self.fc_easy.net], self.target_embedding, self.source_embedding,
+                                     ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key)
         with record_function("qk attention"):
-            so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset,
-                                    ctx.rbf_coeff, packed, ctx.rc, math.sqrt(q.shape[-1]),
-                                    BF16 if bf16 else torch.float32)
+            so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table, ctx.rc,
+                                    math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
         pf = self.proj_first
         with record_function("first-order"):
             return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16),
@@ -944,15 +946,15 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
         self.target_embedding = nn.Embedding(300, number_of_basis)
         self.sph = sph_fromxyz(lmax)
         self.proj = SO3_Linear_e2former(2 * C, C, lmax=lmax)
-        self._mlp = MLPCache()
+        self._radial = RadialCache()
 
     def forward(self, ctx: EdgeContext):
-        packed = self._mlp.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
-                               ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.bf16)
+        table = self._radial.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
+                                 ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key)
         # the edge spherical harmonics ("e3nn sph") are formed inside the degree kernels
         with record_function("e3nn sph"):
-            return DegreeEmbedFn.apply(ctx.dvec, ctx.dist, ctx.nl, ctx.node_type, ctx.rbf_offset, ctx.rbf_coeff,
-                                       packed, float(self.avg_aggregate_num), ctx.rc)
+            return DegreeEmbedFn.apply(ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table,
+                                       float(self.avg_aggregate_num), ctx.rc)
 
 
 class E2former(nn.Module):

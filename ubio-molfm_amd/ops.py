@@ -43,113 +43,96 @@ def _no_double_backward():
                                   "(create_graph=True / double backward is not supported)")
 
 
-def rbf_table_size(rc: float, rbf_coeff: float):
-    """(nodes, spacing) of the rbf-block table for this basis and cutoff."""
-    n = _lib.C.c_int32(); h = _lib.C.c_float()
-    _lib.call("e2v2_mlp_rbf_table_size", _lib.f32(rc), _lib.f32(rbf_coeff), _lib.C.byref(n), _lib.C.byref(h))
-    return n.value, h.value
+class RadialTable:
+    """Distance table of radial profiles RadialProfile [256 + 2E -> 128 -> 128 -> 256]
+    (src/molfm/models/e2former/module_utils.py:2151-2178) over
+    x_edge = [rbf(d), tgt[z_i], src[z_j]] for the atom types ``type_z``: one
+    profile (an attention layer's fc_easy, 256 channels gate | inputhead) or the
+    degree embedding's three (768 channels).  Built in float64 on the device
+    (e2v2_radial_table), then checked at every interval midpoint against the
+    float64 profile (e2v2_radial_table_check); the node spacing is halved until
+    the interpolation error is at most ``tol_value`` of the largest |f| and
+    ``tol_deriv`` of the largest |f'| (one host readback per build)."""
 
-
-class PackedMLP:
-    """Device-ready weights of one RadialProfile [K0 + 2 E -> 128 -> 128 -> 256]
-    (src/molfm/models/e2former/module_utils.py:2151-2178) whose input is
-    [rbf(256), target_table[z_i], source_table[z_j]]: the rbf block of Linear1
-    as an interpolation table over [0, rc] (e2v2_mlp_rbf_table), the type blocks
-    as per-type tables, Linear2/3 as GEMM operands."""
-
-    def __init__(self, net: nn.Sequential, tgt: torch.Tensor, src: torch.Tensor, rbf_offset: torch.Tensor,
-                 rbf_coeff: float, rc: float, n_rbf: int = 256, bf16: bool = False):
-        lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
-        self.bf16 = bf16
-        if n_rbf != 256 or rbf_offset.numel() != 256:
-            raise NotImplementedError("the HIP radial MLP is built for 256 Gaussian basis functions")
+    def __init__(self, nets, tgt: nn.Embedding, src: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
+                 rc: float, type_z: torch.Tensor, tol_value: float = 1e-6, tol_deriv: float = 1e-5,
+                 max_refine: int = 3):
+        dev = type_z.device
+        self.nc = 256 * len(nets)
+        self.n_types = int(type_z.numel())
+        if self.n_types < 1 or self.n_types > MAX_TYPES:
+            raise NotImplementedError(f"{self.n_types} atom types: the radial tables hold at most {MAX_TYPES}")
         with torch.no_grad():
-            W1 = lin1.weight.detach().float().contiguous()
-            e = tgt.shape[1]
-            self.w1 = W1
-            self.ttgt = (tgt.detach().float() @ W1[:, n_rbf:n_rbf + e].t() + lin1.bias.detach().float()).contiguous()
-            self.tsrc = (src.detach().float() @ W1[:, n_rbf + e:n_rbf + 2 * e].t()).contiguous()
-            self.g1 = ln1.weight.detach().float().contiguous(); self.be1 = ln1.bias.detach().float().contiguous()
-            self.w2 = lin2.weight.detach().float().contiguous(); self.w2t = _lane_pack(self.w2.t())
-            self.b2 = lin2.bias.detach().float().contiguous()
-            self.g2 = ln2.weight.detach().float().contiguous(); self.be2 = ln2.bias.detach().float().contiguous()
-            self.w3 = lin3.weight.detach().float().contiguous(); self.w3t = _lane_pack(self.w3.t())
-            # fp32 GEMM B operands, lane-packed: forward W2^T, W3^T; backward W3, W2
-            self.w2p = _lane_pack(self.w2); self.w3p = _lane_pack(self.w3)
-            self.b3 = lin3.bias.detach().float().contiguous()
-            # bf16 GEMM operands as B^T row-major: forward W2, W3; backward W3^T, W2^T
-            self.bf = None
-            if bf16:
-                b = torch.bfloat16
-                self.bf = [self.w2.to(b).contiguous(), self.w3.to(b).contiguous(),
-                           self.w3.t().to(b).contiguous(), self.w2.t().to(b).contiguous()]
+            self._keep = [t.detach().float().contiguous() for t in (tgt.weight, src.weight, rbf_offset)]
+            tgt_w, src_w, mu = self._keep
+            self._structs = [self._net(n, tgt_w, src_w) for n in nets]
+        self.type_z = type_z.to(torch.int32).contiguous()
+        st = _stream(type_z)
+        for refine in range(max_refine + 1):
+            n = _lib.C.c_int32(); h = _lib.C.c_float()
+            _lib.call("e2v2_radial_table_size", _lib.f32(rc), _lib.f32(rbf_coeff), _lib.i32(refine), _lib.C.byref(n),
+                      _lib.C.byref(h))
+            self.n_nodes, self.h = n.value, h.value
+            self.tab = torch.empty(self.n_types ** 2, self.n_nodes, 4, self.nc, dtype=torch.float32, device=dev)
+            err = torch.zeros(len(nets), 4, dtype=torch.int32, device=dev)
+            for m, W in enumerate(self._structs):
+                args = (_lib.C.byref(W), _p(mu), _lib.f32(rbf_coeff), _p(self.type_z), _lib.i32(self.n_types),
+                        _lib.i32(self.n_nodes), _lib.f32(self.h))
+                _lib.call("e2v2_radial_table", *args, _p(self.tab), _lib.i32(self.nc), _lib.i32(256 * m), st)
+                _lib.call("e2v2_radial_table_check", *args, _p(self.tab), _lib.i32(self.nc), _lib.i32(256 * m),
+                          _lib.vp(err[m].data_ptr()), st)
+            e = err.cpu().view(torch.float32).double()
+            self.value_err = float((e[:, 0] / e[:, 1].clamp_min(1e-30)).max())
+            self.deriv_err = float((e[:, 2] / e[:, 3].clamp_min(1e-30)).max())
+            if self.value_err <= tol_value and self.deriv_err <= tol_deriv:
+                break
+        else:
+            raise RuntimeError(f"radial table: interpolation error {self.value_err:.2e} (value) / "
+                               f"{self.deriv_err:.2e} (derivative) above tolerance after {max_refine} refinements")
+
+    def _net(self, net: nn.Sequential, tgt_w: torch.Tensor, src_w: torch.Tensor) -> _lib.RadialNet:
+        lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
+        if not (isinstance(net[2], nn.SiLU) and isinstance(net[5], nn.SiLU)):
+            raise NotImplementedError("RadialProfile activations must be SiLU")
         if not (abs(ln1.eps - 1e-5) < 1e-12 and abs(ln2.eps - 1e-5) < 1e-12):
             raise NotImplementedError("RadialProfile LayerNorm eps must be 1e-5")
-        if W1.shape[0] != 128 or self.w2.shape != (128, 128) or self.w3.shape != (256, 128):
-            raise NotImplementedError(f"RadialProfile shape {tuple(W1.shape)} -> {tuple(self.w3.shape)} "
-                                      "is not the [256+2E, 128, 128, 256] profile of the HIP kernels")
-        self.rtab_n, self.rtab_h = rbf_table_size(rc, rbf_coeff)
-        self.rtab = torch.empty(self.rtab_n, 4, 128, dtype=torch.float32, device=W1.device)
-        self.rbf_offset = rbf_offset.detach().float().contiguous()
-        _lib.call("e2v2_mlp_rbf_table", _p(W1), _lib.i32(W1.shape[1]), _p(self.rbf_offset), _lib.f32(rbf_coeff),
-                  _lib.i32(self.rtab_n), _lib.f32(self.rtab_h), _p(self.rtab), _stream(W1))
-
-    def struct(self) -> _lib.MlpWeights:
-        bf = [t.data_ptr() for t in self.bf] if self.bf is not None else [None] * 4
-        return _lib.MlpWeights(self.rtab.data_ptr(), self.rtab_n, self.rtab_h, self.ttgt.data_ptr(),
-                               self.tsrc.data_ptr(), self.g1.data_ptr(), self.be1.data_ptr(), self.w2t.data_ptr(),
-                               self.b2.data_ptr(), self.g2.data_ptr(), self.be2.data_ptr(), self.w3t.data_ptr(),
-                               self.b3.data_ptr(), self.w2p.data_ptr(), self.w3p.data_ptr(), *bf)
+        E = tgt_w.shape[1]
+        if (lin1.weight.shape != (128, 256 + 2 * E) or lin2.weight.shape != (128, 128)
+                or lin3.weight.shape != (256, 128) or src_w.shape[1] != E):
+            raise NotImplementedError(f"RadialProfile {tuple(lin1.weight.shape)} -> {tuple(lin3.weight.shape)} is "
+                                      "not the [256 + 2E, 128, 128, 256] profile the radial tables are built for")
+        ts = [t.detach().float().contiguous() for t in (lin1.weight, lin1.bias, ln1.weight, ln1.bias, lin2.weight,
+                                                         lin2.bias, ln2.weight, ln2.bias, lin3.weight, lin3.bias)]
+        self._keep += ts
+        w1, b1, g1, be1, w2, b2, g2, be2, w3, b3 = [t.data_ptr() for t in ts]
+        return _lib.RadialNet(w1, 256 + 2 * E, E, b1, g1, be1, w2, b2, g2, be2, w3, b3, tgt_w.data_ptr(),
+                              src_w.data_ptr())
 
 
-def _lane_pack(B: torch.Tensor) -> torch.Tensor:
-    """B [K][N] (fp32) in the lane-packed order of the HIP MLP's fp32 GEMMs: one
-    float4 per (wave w, 16-column group ct, 16-k block b, lane l), holding
-    B[16 b + 4 (l // 16) + s][w N/4 + 16 ct + l % 16] for s = 0..3."""
-    K, N = B.shape
-    return B.contiguous().view(K // 16, 4, 4, 4, N // 64, 16).permute(3, 4, 0, 1, 5, 2).contiguous()
+MAX_TYPES = 32
 
 
 def _version_key(params):
     return tuple((p.data_ptr(), p._version, p.dtype, str(p.device)) for p in params)
 
 
-class MLPCache:
-    """Repack weights only when a parameter (or the basis) changed (MD loops reuse them)."""
+class RadialCache:
+    """Rebuild a RadialTable only when a parameter, the basis or the type set changed
+    (an MD loop builds each table once)."""
 
     def __init__(self):
         self.key = None
-        self.packed: List[PackedMLP] = []
+        self.table: Optional[RadialTable] = None
 
     def get(self, nets, tgt_emb: nn.Embedding, src_emb: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
-            rc: float, bf16: bool = False):
+            rc: float, type_z: torch.Tensor, type_key: tuple):
         params = [p for n in nets for p in n.parameters()] + [tgt_emb.weight, src_emb.weight, rbf_offset]
-        key = (_version_key(params), float(rbf_coeff), float(rc), bf16)
+        key = (_version_key(params), float(rbf_coeff), float(rc), type_key)
         if key != self.key:
-            self.packed = [PackedMLP(n, tgt_emb.weight, src_emb.weight, rbf_offset, rbf_coeff, rc, bf16=bf16)
-                           for n in nets]
+            self.table = None
+            self.table = RadialTable(nets, tgt_emb, src_emb, rbf_offset, rbf_coeff, rc, type_z)
             self.key = key
-        return self.packed
-
-
-def mlp_args(nl: NeighborList, node_type: torch.Tensor, packed: List[PackedMLP],
-             save_n: Optional[torch.Tensor] = None, save_r: Optional[torch.Tensor] = None) -> _lib.MlpArgs:
-    ws = (_lib.MlpWeights * 3)()
-    for m, pk in enumerate(packed):
-        ws[m] = pk.struct()
-    bf16 = packed[0].bf16
-    if any(pk.bf16 != bf16 for pk in packed):
-        raise ValueError("mixed fp32/bf16 RadialProfile packs in one launch")
-    return _lib.MlpArgs(nl.n_edges, len(packed), int(bf16), nl.dist.data_ptr(), nl.edge_row.data_ptr(),
-                        nl.col.data_ptr(), node_type.data_ptr(),
-                        None if save_n is None else save_n.data_ptr(), None if save_r is None else save_r.data_ptr(),
-                        ws)
-
-
-def mlp_save_buffers(n_mlp: int, E: int, dev):
-    """Normalised LayerNorm inputs kept from the forward for the backward."""
-    return (torch.empty(n_mlp, max(E, 1), 256, dtype=torch.float32, device=dev),
-            torch.empty(n_mlp, max(E, 1), 2, dtype=torch.float32, device=dev))
+        return self.table
 
 
 class EdgeGeometryFn(torch.autograd.Function):
@@ -179,54 +162,51 @@ class EdgeGeometryFn(torch.autograd.Function):
 
 
 class DegreeEmbedFn(torch.autograd.Function):
-    """EdgeDegreeEmbeddingNetwork_higherorder.forward (e2former.py:689-753)."""
+    """EdgeDegreeEmbeddingNetwork_higherorder.forward (e2former.py:689-753): the three
+    gbf_projs profiles interpolated from their table inside the kernels; nothing per
+    edge is saved."""
 
     @staticmethod
-    def forward(ctx, dvec, dist, nl: NeighborList, node_type, rbf_offset, rbf_coeff: float, packed, avg: float,
-                rc: float):
+    def forward(ctx, dvec, dist, nl: NeighborList, atom_type, table: RadialTable, avg: float, rc: float):
         _need_cuda(dvec, dist)
         dev = dvec.device
-        E, N = nl.n_edges, nl.n_atoms
-        fea = torch.empty(max(E, 1), 3 * 256, dtype=torch.float32, device=dev)
-        sn, sr = mlp_save_buffers(len(packed), E, dev)
-        margs = mlp_args(nl, node_type, packed, sn, sr)
-        _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(fea), _lib.i32(768), _stream(fea))
-        dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
-                             fea.data_ptr(), float(avg), float(rc), ENV_A, ENV_B, ENV_C)
-        x0 = torch.empty(9, N, 256, dtype=torch.float32, device=dev)   # m-major
+        dargs = deg_args(nl, atom_type, table, avg, rc)
+        x0 = torch.empty(9, nl.n_atoms, 256, dtype=torch.float32, device=dev)   # m-major
         _lib.call("e2v2_deg_fwd", _lib.C.byref(dargs), _p(x0), _stream(x0))
-        ctx.save_for_backward(fea, sn, sr)
-        ctx.nl, ctx.margs_src = nl, (node_type, rbf_offset, rbf_coeff, packed)
-        ctx.avg, ctx.rc = avg, rc
+        ctx.nl, ctx.atom_type, ctx.table, ctx.avg, ctx.rc = nl, atom_type, table, avg, rc
         return x0
 
     @staticmethod
     def backward(ctx, gx0):
         _no_double_backward()
-        fea, sn, sr = ctx.saved_tensors
         nl = ctx.nl
-        node_type, rbf_offset, rbf_coeff, packed = ctx.margs_src
-        dev = fea.device
-        E, N = nl.n_edges, nl.n_atoms
+        dev = nl.dvec.device
+        E = nl.n_edges
         gx0 = gx0.float().contiguous()
-        dargs = _lib.DegArgs(N, E, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
-                             fea.data_ptr(), float(ctx.avg), float(ctx.rc), ENV_A, ENV_B, ENV_C)
+        dargs = deg_args(nl, ctx.atom_type, ctx.table, ctx.avg, ctx.rc)
         ddv = torch.empty(max(E, 1), 3, dtype=torch.float32, device=dev)
         dd = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
-        _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), None, _p(ddv), _p(dd), _stream(gx0))
-        margs = mlp_args(nl, node_type, packed, sn, sr)
-        # the MLP backward forms the [E, 3, 256] feature gradient per edge tile from gx0
-        _lib.call("e2v2_mlp_bwd_deg", _lib.C.byref(margs), _lib.C.byref(dargs), _p(gx0), _p(dd), _lib.i32(1),
-                  _stream(gx0))
-        return ddv[:E], dd[:E], None, None, None, None, None, None, None
+        _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(ddv), _p(dd), _stream(gx0))
+        return ddv[:E], dd[:E], None, None, None, None, None
 
 
-def attn_args(nl: NeighborList, q, k, v, gi, q_div: float, rc: float, bf: int):
+def deg_args(nl: NeighborList, atom_type: torch.Tensor, table: RadialTable, avg: float, rc: float):
+    if table.nc != 768:
+        raise ValueError("the degree embedding needs the table of its three profiles (768 channels)")
+    return _lib.DegArgs(nl.n_atoms, nl.n_edges, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
+                        nl.col.data_ptr(), table.tab.data_ptr(), atom_type.data_ptr(), table.n_types, table.n_nodes,
+                        table.h, float(avg), float(rc), ENV_A, ENV_B, ENV_C)
+
+
+def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: float, rc: float, bf: int):
     """e2v2_attn_args over the neighbour list (with its column clusters when built)."""
+    if table.nc != 256:
+        raise ValueError("the attention needs the table of its fc_easy profile (256 channels)")
     a = _lib.AttnArgs(nl.n_atoms, nl.n_edges, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(),
                       nl.edge_row.data_ptr(), nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(),
-                      nl.dist.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), gi.data_ptr(), float(q_div),
-                      float(rc), ENV_A, ENV_B, ENV_C, int(bf))
+                      nl.dist.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.tab.data_ptr(),
+                      atom_type.data_ptr(), table.n_types, table.n_nodes, table.h, float(q_div), float(rc), ENV_A,
+                      ENV_B, ENV_C, int(bf))
     if nl.col_slot_member is not None:
         a.col_span = nl.col_span
         a.col_slot_member = nl.col_slot_member.data_ptr()
@@ -239,55 +219,49 @@ class AttentionFn(torch.autograd.Function):
     """Edge part of E2AttentionArbOrder_sparse.forward (e2former.py:238-433) up to
     the SO(2) product's forward_linear: returns the 20-row l3-sequential tensor
     h_a - h_b of so2_tensor_product.py:385 for every query atom, m-major
-    [20, N, 256]; q, k [N, 128, 8], v [9, N, 256]."""
+    [20, N, 256]; q, k [N, 128, 8], v [9, N, 256].  gate and inputhead
+    (fc_easy, e2former.py:258-306) are interpolated from the layer's radial table
+    inside the kernels: only node-level tensors are saved."""
 
     @staticmethod
-    def forward(ctx, q, k, v, dvec, dist, nl: NeighborList, node_type, rbf_offset, rbf_coeff: float, packed,
-                rc: float, q_div: float, act_dtype=torch.float32):
+    def forward(ctx, q, k, v, dvec, dist, nl: NeighborList, atom_type, table: RadialTable, rc: float,
+                q_div: float, act_dtype=torch.float32):
         """act_dtype: storage of q, k, v and of the output rows (torch.float32, or
         torch.bfloat16 in the bf16 mode: half the gather traffic, fp32 math)."""
         _need_cuda(q, k, v, dvec, dist)
         if act_dtype not in (torch.float32, torch.bfloat16):
             raise ValueError(f"attention activations must be float32 or bfloat16, got {act_dtype}")
         dev = q.device
-        E, N = nl.n_edges, nl.n_atoms
+        N = nl.n_atoms
         q = q.to(act_dtype).contiguous(); k = k.to(act_dtype).contiguous(); v = v.to(act_dtype).contiguous()
         bf = int(act_dtype == torch.bfloat16)
-        gi = torch.empty(max(E, 1), 256, dtype=torch.float32, device=dev)
-        sn, sr = mlp_save_buffers(1, E, dev)
-        margs = mlp_args(nl, node_type, packed, sn, sr)
-        _lib.call("e2v2_mlp_fwd", _lib.C.byref(margs), _p(gi), _lib.i32(256), _stream(q))
-        args = attn_args(nl, q, k, v, gi, q_div, rc, bf)
+        args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf)
         out = torch.empty(20, N, 256, dtype=act_dtype, device=dev)   # m-major
         mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
         _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _p(out), _p(mrow), _p(srow), _p(cnt), _stream(q))
-        ctx.save_for_backward(q, k, v, gi, out, mrow, srow, cnt, sn, sr)
-        ctx.nl, ctx.margs_src, ctx.rc, ctx.q_div = nl, (node_type, rbf_offset, rbf_coeff, packed), rc, q_div
-        ctx.bf = bf
+        ctx.save_for_backward(q, k, v, out, mrow, srow, cnt)
+        ctx.nl, ctx.atom_type, ctx.table, ctx.rc, ctx.q_div, ctx.bf = nl, atom_type, table, rc, q_div, bf
         return out
 
     @staticmethod
     def backward(ctx, gout):
         _no_double_backward()
-        q, k, v, gi, out, mrow, srow, cnt, sn, sr = ctx.saved_tensors
+        q, k, v, out, mrow, srow, cnt = ctx.saved_tensors
         nl = ctx.nl
-        node_type, rbf_offset, rbf_coeff, packed = ctx.margs_src
         dev = q.device
-        E, N = nl.n_edges, nl.n_atoms
+        E = nl.n_edges
         gout = gout.to(out.dtype).contiguous()
-        args = attn_args(nl, q, k, v, gi, ctx.q_div, ctx.rc, ctx.bf)
+        args = attn_args(nl, q, k, v, ctx.atom_type, ctx.table, ctx.q_div, ctx.rc, ctx.bf)
         f = dict(dtype=torch.float32, device=dev)
-        dgi = torch.empty(max(E, 1), 256, **f)
         ddv = torch.empty(max(E, 1), 3, **f)
         dd = torch.empty(max(E, 1), **f)
         dq = torch.empty(q.shape, **f); dk = torch.empty(k.shape, **f); dv = torch.empty(v.shape, **f)
+        # scratch of this call: per-edge weights and logit gradients handed from the row pass to the column pass
         w_e = torch.empty(max(E, 1), 128, **f)
         dqk = torch.empty(max(E, 1), 128, **f)
-        _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(dgi),
-                  _p(ddv), _p(dd), _p(dq), _p(dk), _p(dv), _p(w_e), _p(dqk), _stream(gout))
+        _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(ddv),
+                  _p(dd), _p(dq), _p(dk), _p(dv), _p(w_e), _p(dqk), _stream(gout))
         del w_e, dqk
-        margs = mlp_args(nl, node_type, packed, sn, sr)
-        _lib.call("e2v2_mlp_bwd", _lib.C.byref(margs), _p(dgi), _lib.i32(256), _p(dd), _lib.i32(1), _stream(gout))
-        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None, None
+        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None
