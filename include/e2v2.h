@@ -96,6 +96,18 @@ int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, int64_t n_e
 int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* cnt, int32_t* new_ptr, int32_t* stats,
                   const int32_t* col, const int32_t* shift, const float* dvec, const float* dist,
                   int32_t* ocol, int32_t* oshift, float* odv, float* od, int phase, hipStream_t s);
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph
+   capture, tight serving loops).  e2v2_nbr_bin + e2v2_nbr_count in one call with the plan's workspace
+   (atom_bin, bin_count, bin_start, bin_atoms, stats; those pointers are ignored) replaced by a static device
+   array of the library (16 MB per GPU, held until the process ends): at most E2V2_NOALLOC_MAX_ATOMS atoms
+   and E2V2_NOALLOC_MAX_BINS bins, larger plans are rejected before any launch.  Outputs as e2v2_nbr_count:
+   row_count [n_atoms], row_ptr [n_atoms + 1]; stats_out [3] = {E, max row, 1 if an atom lies outside its
+   graph's grid box} (cleared by the call).  Calls no allocator.  The array keeps the last call's contents
+   and every call on a GPU shares it: calls that overlap on one device (other streams or threads) race. */
+#define E2V2_NOALLOC_MAX_ATOMS (1 << 20)
+#define E2V2_NOALLOC_MAX_BINS (1 << 20)
+int e2v2_nbr_count_noalloc(const e2v2_nbr_plan* plan, int32_t* row_count, int32_t* row_ptr, int32_t* stats_out,
+                           hipStream_t s);
 /* 30-bit Morton (Z-order) keys of atoms within their graph's bounding box, for the spatial
    ordering of the rows: key[i] = g << 32 | interleave(q) with q = clamp((pos - lo[g]) / span[g]
    * 1023, 0, 1023) truncated; gid [n] the graph of each atom (NULL: one graph), lo/span [B][3].

@@ -32,3 +32,17 @@ def test_error_path_reports_message(pkg):
     # a negative length is rejected on the host before any launch
     rc = lib.e2v2_scan_i32(None, ctypes.c_int(-1), None, None, None)
     assert rc != 0 and b"negative" in lib.e2v2_last_error()
+
+
+def test_noalloc_rejects_oversized_plan(pkg):
+    """e2v2_nbr_count_noalloc checks the plan against its static scratch before any
+    HIP call: more atoms than E2V2_NOALLOC_MAX_ATOMS is an error with a message."""
+    from ubio_molfm_amd import _lib
+    import ctypes
+    lib = _lib.load()
+    plan = _lib.NbrPlan()
+    plan.n_atoms = (1 << 20) + 1
+    plan.n_bins = 8
+    dummy = ctypes.c_void_p(16)          # never dereferenced: the size check fails first
+    rc = lib.e2v2_nbr_count_noalloc(ctypes.byref(plan), dummy, dummy, dummy, None)
+    assert rc != 0 and b"exceed the static scratch" in lib.e2v2_last_error()

@@ -5,6 +5,8 @@
 // (src/molfm/models/e2former/module_utils.py:1065-1274,3119-3242) and the
 // CSR metadata of prepare_sparse_qk_edge_index_metadata
 // (src/molfm/models/e2former/triton_dr/triton_sparse_qk_autograd.py:601-652).
+#include <mutex>
+
 #include "common.h"
 #include "../../include/e2v2.h"
 
@@ -571,6 +573,37 @@ static inline unsigned blocks_for(int64_t n, int bs) {
   return (unsigned)(b < 1 ? 1 : (b > 1048576 ? 1048576 : b));
 }
 
+// ---------------------------------------------------------------------------
+// No-allocation variant of e2v2_nbr_bin + e2v2_nbr_count: the bin workspace lives
+// in this file-scope device array instead of the plan's workspace buffers.  In
+// host code `scratch` only names the symbol; its device address (one copy per
+// GPU) comes from hipGetSymbolAddress, taken once per device on first use.
+constexpr int64_t kNoAllocAtoms = E2V2_NOALLOC_MAX_ATOMS;
+constexpr int64_t kNoAllocBins = E2V2_NOALLOC_MAX_BINS;
+// atom_bin [atoms] | bin_atoms [atoms] | bin_count [bins] | bin_start [bins + 1]
+constexpr int64_t kScratchInts = 2 * kNoAllocAtoms + 2 * kNoAllocBins + 1;
+static __device__ __align__(256) int32_t scratch[kScratchInts];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static int32_t* g_scratch_ptr[kMaxDevices] = {};
+
+static int scratch_for_current_device(int32_t** out) {
+  int dev = 0;
+  E2V2_TRY_HIP(hipGetDevice(&dev));
+  E2V2_REQUIRE(dev >= 0 && dev < kMaxDevices, "nbr_count_noalloc: device %d beyond the %d supported", dev,
+               kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    E2V2_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    E2V2_REQUIRE(p != nullptr, "nbr_count_noalloc: no device address for the scratch array on device %d", dev);
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace e2v2
 
 using namespace e2v2;
@@ -716,4 +749,26 @@ E2V2_API int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int 
   hipLaunchKernelGGL(k_sort_cols, dim3(n_cols), dim3(64), seg_lds_bytes(cap), s, key_ptr, tmp_key, key_eid, cap);
   E2V2_LAUNCHED("k_sort_cols");
   return 0;
+}
+
+E2V2_API int e2v2_nbr_count_noalloc(const e2v2_nbr_plan* plan, int32_t* row_count, int32_t* row_ptr,
+                                    int32_t* stats_out, hipStream_t s) {
+  E2V2_REQUIRE(plan && row_ptr && stats_out && (row_count || plan->n_atoms == 0),
+               "nbr_count_noalloc: plan, row_count, row_ptr and stats_out are required");
+  const e2v2_nbr_plan& P0 = *plan;
+  E2V2_REQUIRE(P0.n_atoms >= 0 && P0.n_atoms <= kNoAllocAtoms && P0.n_bins > 0 && P0.n_bins <= kNoAllocBins,
+               "nbr_count_noalloc: %d atoms / %d bins exceed the static scratch (at most %lld atoms, %lld bins)",
+               P0.n_atoms, P0.n_bins, (long long)kNoAllocAtoms, (long long)kNoAllocBins);
+  int32_t* sc = nullptr;
+  if (int rc = scratch_for_current_device(&sc)) return rc;
+  e2v2_nbr_plan P = P0;
+  P.atom_bin = sc;
+  P.bin_atoms = sc + kNoAllocAtoms;
+  P.bin_count = sc + 2 * kNoAllocAtoms;
+  P.bin_start = P.bin_count + kNoAllocBins;
+  P.stats = stats_out;
+  // the outside flag accumulates by atomic OR: start from zero (a fill kernel, not a memset)
+  if (int rc = e2v2_fill_i32(stats_out, 0, 3, s)) return rc;
+  if (int rc = e2v2_nbr_bin(&P, s)) return rc;
+  return e2v2_nbr_count(&P, row_count, row_ptr, s);
 }

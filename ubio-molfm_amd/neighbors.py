@@ -104,26 +104,19 @@ def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
 
-def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
-                    max_neighbors: Optional[int] = None, cells_per_direction: int = 4,
-                    grid_box=None) -> NeighborList:
-    """pos [N,3] fp32 on the GPU (graphs contiguous); graph_ptr [B+1], cells
-    [B,3,3], pbcs [B,3] on the host.  grid_box [2,B,3] (optional, host): per-graph
-    (lo, hi) corners of the bin grid that contain every atom, e.g. the cell of
-    positions wrapped into it; without it the atoms' bounding boxes are read back
-    (one host sync).  The edge list does not depend on the grid.  An atom outside
-    the supplied box is detected on the device (read back with the edge count)
-    and the list is rebuilt with the bounding boxes."""
-    if not pos.is_cuda:
-        raise RuntimeError("build_neighbors runs on the GPU only (pos must be a CUDA/HIP tensor)")
+def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
+              cells_per_direction: int = 4, grid_box=None, workspace: bool = True):
+    """The e2v2_nbr_plan of a batch (pos [N,3] fp32 on the GPU, graphs contiguous;
+    graph_ptr, cells, pbcs on the host): per-graph shift tables, bin grids and,
+    with ``workspace``, the bin workspace tensors.  Returns (plan, tensors kept
+    alive for it, the shift table, its per-graph row pointers).  Without
+    ``grid_box`` the atoms' bounding boxes are read back (one host sync)."""
     dev = pos.device
-    pos = pos.detach().to(torch.float32).contiguous()
     graph_ptr = np.asarray(graph_ptr, np.int64)
     cells = np.asarray(cells, F32).reshape(-1, 3, 3)
     pbcs = np.asarray(pbcs, bool).reshape(-1, 3)
     N = int(pos.shape[0])
     B = len(graph_ptr) - 1
-    stream = torch.cuda.current_stream(dev).cuda_stream
     i32 = dict(dtype=torch.int32, device=dev)
     # per-graph bounding boxes (one host sync unless the caller supplies the grid box)
     if grid_box is not None:
@@ -172,15 +165,41 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     ti_parts = torch.split(ti, [len(a) for a in ints])
     t_gptr, t_sptr, t_per, t_dim, t_base, atom_graph = ti_parts
     t_off, t_lo, t_h = torch.split(tf, [len(a) for a in floats])
-    atom_bin = torch.empty(max(N, 1), **i32)
-    bin_count = torch.empty(nb, **i32)
-    bin_start = torch.empty(nb + 1, **i32)
-    bin_atoms = torch.empty(max(N, 1), **i32)
-    stats = torch.zeros(3, **i32)
+    keep = dict(pos=pos, ti=ti, tf=tf)
+    ws = [None] * 5
+    if workspace:
+        keep.update(atom_bin=torch.empty(max(N, 1), **i32), bin_count=torch.empty(nb, **i32),
+                    bin_start=torch.empty(nb + 1, **i32), bin_atoms=torch.empty(max(N, 1), **i32),
+                    stats=torch.zeros(3, **i32))
+        ws = [keep[k].data_ptr() for k in ("atom_bin", "bin_count", "bin_start", "bin_atoms", "stats")]
     plan = _lib.NbrPlan(N, B, nb, len(offs), rc, rmin, pos.data_ptr(), atom_graph.data_ptr(), t_gptr.data_ptr(),
                         t_sptr.data_ptr(), t_per.data_ptr(), t_off.data_ptr(), t_lo.data_ptr(), t_h.data_ptr(),
-                        t_dim.data_ptr(), t_base.data_ptr(), atom_bin.data_ptr(), bin_count.data_ptr(),
-                        bin_start.data_ptr(), bin_atoms.data_ptr(), stats.data_ptr())
+                        t_dim.data_ptr(), t_base.data_ptr(), *ws)
+    return plan, keep, shifts_np, sptr
+
+
+def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
+                    max_neighbors: Optional[int] = None, cells_per_direction: int = 4,
+                    grid_box=None) -> NeighborList:
+    """pos [N,3] fp32 on the GPU (graphs contiguous); graph_ptr [B+1], cells
+    [B,3,3], pbcs [B,3] on the host.  grid_box [2,B,3] (optional, host): per-graph
+    (lo, hi) corners of the bin grid that contain every atom, e.g. the cell of
+    positions wrapped into it; without it the atoms' bounding boxes are read back
+    (one host sync).  The edge list does not depend on the grid.  An atom outside
+    the supplied box is detected on the device (read back with the edge count)
+    and the list is rebuilt with the bounding boxes."""
+    if not pos.is_cuda:
+        raise RuntimeError("build_neighbors runs on the GPU only (pos must be a CUDA/HIP tensor)")
+    dev = pos.device
+    pos = pos.detach().to(torch.float32).contiguous()
+    graph_ptr = np.asarray(graph_ptr, np.int64)
+    cells = np.asarray(cells, F32).reshape(-1, 3, 3)
+    pbcs = np.asarray(pbcs, bool).reshape(-1, 3)
+    N = int(pos.shape[0])
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    i32 = dict(dtype=torch.int32, device=dev)
+    plan, keep, shifts_np, sptr = make_plan(pos, graph_ptr, cells, pbcs, rc, rmin, cells_per_direction, grid_box)
+    stats = keep["stats"]
     _lib.call("e2v2_nbr_bin", _lib.C.byref(plan), _lib.vp(stream))
     row_count = torch.empty(max(N, 1), **i32)
     row_ptr = torch.empty(N + 1, **i32)
@@ -254,3 +273,25 @@ def cluster_slots(seg_ptr: torch.Tensor, n_seg: int, member: torch.Tensor, item_
               _lib.vp(_ptr(item_eid)), _lib.i32(span), _lib.vp(sm.data_ptr()), _lib.vp(se.data_ptr()),
               _lib.vp(ns.data_ptr()), _lib.vp(torch.cuda.current_stream(dev).cuda_stream))
     return sm, se, ns
+
+
+def count_neighbors_noalloc(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
+                            cells_per_direction: int = 4, grid_box=None):
+    """Neighbour counts of every row through e2v2_nbr_count_noalloc (the library's
+    static bin scratch instead of workspace buffers): (row_count [N], row_ptr [N+1],
+    stats [3] = E, max row, outside flag), all int32 on the device.  The outputs and
+    the plan's small tables are allocated here; the library call allocates nothing."""
+    if not pos.is_cuda:
+        raise RuntimeError("count_neighbors_noalloc runs on the GPU only")
+    pos = pos.detach().to(torch.float32).contiguous()
+    plan, keep, _, _ = make_plan(pos, graph_ptr, cells, pbcs, rc, rmin, cells_per_direction, grid_box,
+                                 workspace=False)
+    N = int(pos.shape[0])
+    i32 = dict(dtype=torch.int32, device=pos.device)
+    row_count = torch.empty(max(N, 1), **i32)
+    row_ptr = torch.empty(N + 1, **i32)
+    stats = torch.empty(3, **i32)
+    _lib.call("e2v2_nbr_count_noalloc", _lib.C.byref(plan), _lib.vp(row_count.data_ptr()),
+              _lib.vp(row_ptr.data_ptr()), _lib.vp(stats.data_ptr()),
+              _lib.vp(torch.cuda.current_stream(pos.device).cuda_stream))
+    return row_count[:N], row_ptr, stats
