@@ -183,11 +183,12 @@ def cpu_baseline(pkg, config: int = 4, sample: str = "default"):
     cell-list neighbour list.  Samples of each workload (default):
     config 1: the full 648-atom water box, one evaluation;
     config 2: the full 64-molecule batch, graph by graph;
-    configs 3 and 4: a 2,000-atom periodic water/protein mix built by their
-    recipe (same density and element ratios), one evaluation;
+    config 3: the full 1,500-atom system, one evaluation;
+    config 4: a 2,000-atom periodic water/protein mix built by its recipe (same
+    density and element ratios), one evaluation;
     config 5: not run (hours per evaluation on the host), None.
-    ``sample="full"`` evaluates the configuration's own system once (configs
-    3 and 4; at 10,000 atoms that is minutes of host time and ~100 GB of RAM)."""
+    ``sample="full"`` evaluates configs[3]'s own 10,000-atom system once
+    (minutes of host time and ~100 GB of RAM)."""
     import numpy as np
     import torch
     from ubio_molfm_amd import systems
@@ -200,13 +201,12 @@ def cpu_baseline(pkg, config: int = 4, sample: str = "default"):
     torch.manual_seed(0)
     om = OracleModel().eval()
     energy_forces_with_neighbors(om, systems.small_water(4, 5.5, seed=1))
-    if config in (3, 4):
-        if sample == "full":
-            graphs = [systems.CONFIGS[config]()]
-            what = f"the full configs[{config - 1}] system ({len(graphs[0]['pos'])} atoms, {{e}} edges)"
-        else:
-            graphs = [systems.solvated_chains(2000, seed=0)]
-            what = f"2,000-atom periodic water/protein mix (configs[{config - 1}] recipe, {{e}} edges)"
+    if config == 3 or (config == 4 and sample == "full"):
+        graphs = [systems.CONFIGS[config]()]
+        what = f"the full configs[{config - 1}] system ({len(graphs[0]['pos'])} atoms, {{e}} edges)"
+    elif config == 4:
+        graphs = [systems.solvated_chains(2000, seed=0)]
+        what = f"2,000-atom periodic water/protein mix (configs[{config - 1}] recipe, {{e}} edges)"
     elif config == 1:
         graphs = [systems.CONFIGS[1]()]
         what = "the full configs[0] water box (648 atoms, {e} edges)"
@@ -220,7 +220,10 @@ def cpu_baseline(pkg, config: int = 4, sample: str = "default"):
                 "{e} edges, fp32)")
     n_atoms = sum(len(g["pos"]) for g in graphs)
     t0 = time.perf_counter()
-    n_edges = sum(energy_forces_with_neighbors(om, g)[2] for g in graphs)
+
+    def progress(msg):
+        print(f"[cpu baseline] {msg} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+    n_edges = sum(energy_forces_with_neighbors(om, g, progress if len(graphs) == 1 else None)[2] for g in graphs)
     t = time.perf_counter() - t0
     out = {"value": n_edges / t, "unit": "edges/s", "cores": cores, "kind": "port",
            "cpu": _cpu_model(), "atoms": n_atoms, "edges": int(n_edges), "seconds": round(t, 2),

@@ -39,10 +39,14 @@ def reference_batch(om, sysd, pos: torch.Tensor):
                 f_exp_node_pos=exp_pos, f_outcell_index=exp_j), len(nb["i"])
 
 
-def energy_forces_with_neighbors(om, sysd):
+def energy_forces_with_neighbors(om, sysd, progress=None):
+    """(energy, forces, edge count) of one graph; ``progress(msg)`` is called after
+    the neighbour list, the forward and the backward when given."""
     pos = torch.as_tensor(np.asarray(sysd["pos"], np.float32)).clone().requires_grad_(True)
     Z = torch.as_tensor(np.asarray(sysd["Z"]))
     nbinfo, n_edges = reference_batch(om, sysd, pos)
+    if progress:
+        progress(f"neighbour list: {n_edges} edges")
     bd = dict(pos=pos.unsqueeze(0), atomic_numbers=Z.unsqueeze(0),
               atom_masks=torch.ones(1, len(Z), dtype=torch.bool),
               pbc=torch.as_tensor(np.asarray(sysd["pbc"])), cell=torch.as_tensor(np.asarray(sysd["cell"])))
@@ -51,5 +55,9 @@ def energy_forces_with_neighbors(om, sysd):
     tok = dec.embedding(bd["atomic_numbers"])
     a, v, irr = dec.decoder(bd, tok, None)
     e = om.head(dict(node_featuresBxN=a), bd, next(iter(om.head.energy_heads.keys())))[0]
+    if progress:
+        progress("forward done")
     f = -torch.autograd.grad(e, pos, torch.ones_like(e))[0]
+    if progress:
+        progress("backward done")
     return e.detach(), f, n_edges
