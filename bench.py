@@ -68,9 +68,14 @@ COMPULSORY = {"e2v2_attn_fwd": attn_fwd_compulsory, "e2v2_attn_bwd": attn_bwd_co
 # Bytes the implementation's kernels read and write per launch, split into node / edge-list traffic
 # and the radial-table reads (rows of the per-type-pair distance tables, mostly served by the L2 and
 # the Infinity Cache: an attention layer's table is 16 pairs x 770 nodes x 4 KB = 50 MB at configs[3]).
+# The forward and the backward row pass run one wavefront per (row, 16-head slice): every slice reads
+# the edge list (col, dvec, dist, source type: 6 words per edge) once, 8 times in all.
+SLICES = 8
+
+
 def attn_fwd_bytes(N, E, act=4):
-    # read q, k, v, edge (col, dvec, dist, source type), row_ptr; write out, m, s, cnt
-    node_edge = (act * N * (128 * 8 * 2 + 9 * 256 + 20 * 256) + 4.0 * (N * 3 * 128 + E * 6 + N + 1))
+    # read q, k, v, edge list per slice, row_ptr; write out, m, s, cnt
+    node_edge = (act * N * (128 * 8 * 2 + 9 * 256 + 20 * 256) + 4.0 * (N * 3 * 128 + SLICES * E * 6 + N + 1))
     return node_edge + attn_fwd_table_bytes(E)
 
 
@@ -79,12 +84,14 @@ def attn_fwd_table_bytes(E):
 
 
 def attn_bwd_bytes(N, E, act=4):
-    # row pass: read grad, out, q, k, v, m/s/cnt, edges; write ddvec, ddist, dq, w, dqk
+    # row pass: read grad, out, q, k, v, m/s/cnt, edge list per slice; write dq, w, dqk, slice partials
     # column pass: read w, dqk, key CSR, grad rows, q; write dv, dk
+    # partial sum: read the 8 slice partials, write ddvec, ddist
     row = (act * N * (2 * 20 * 256 + 2 * 1024 + 9 * 256)
-           + 4.0 * (N * (1024 + 3 * 128) + E * (6 + 4 + 2 * 128)))
+           + 4.0 * (N * (1024 + 3 * 128) + E * (SLICES * 6 + 2 * 128 + SLICES * 4)))
     col = act * N * (20 * 256 + 1024) + 4.0 * (N * (9 * 256 + 1024 + 2) + E * (2 * 128 + 2 + 3))
-    return row + col + attn_bwd_table_bytes(E)
+    part = 4.0 * E * (SLICES * 4 + 4)
+    return row + col + part + attn_bwd_table_bytes(E)
 
 
 def attn_bwd_table_bytes(E):
@@ -129,7 +136,8 @@ PROJ_FLOPS = {"e2v2_qk_proj_fwd": lambda N: 2.0 * 9 * N * 256 * 2048,
 PROJ_FLOPS["e2v2_qk_proj_fwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
 PROJ_FLOPS["e2v2_qk_proj_bwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
 
-KERNELS_OF = {"e2v2_attn_fwd": ["k_attn_fwd"], "e2v2_attn_bwd": ["k_attn_bwd_row_hp", "k_attn_bwd_col_grp"],
+KERNELS_OF = {"e2v2_attn_fwd": ["k_attn_fwd_sl"],
+              "e2v2_attn_bwd": ["k_attn_bwd_row_sl", "k_attn_bwd_col_grp", "k_edge_part_sum"],
               "e2v2_deg_fwd": ["k_deg_fwd"], "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"],
               "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"]}
 

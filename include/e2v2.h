@@ -135,10 +135,18 @@ int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, i
    alone.  Its table, for a set of n_types atom types (type slot a has atomic number type_z[a]), holds per
    type pair p = a * n_types + b (a: the query atom's type, b: the source atom's) and node n (d = n h, h a
    power of two) four rows of nc channels: row k = h^k d^k f / dd^k (k = 0..3), float64-built by exact
-   Taylor-series propagation through every op.  Layout tab[p][n][k][nc]; one profile fills the 256
-   channels [col0, col0 + 256) of each row (nc = 256 for an attention layer's fc_easy, whose channels
-   are gate | inputhead; nc = 768 for the degree embedding's three profiles, l = 0, 1, 2).  The edge
-   kernels interpolate rows 0..2 (value) and rows 1..3 (derivative) with quintic Hermite polynomials. */
+   Taylor-series propagation through every op.  Layout tab[p][n][k][nc]; a profile's 256 output
+   channels are placed in each row by an e2v2_radial_layout.  The edge kernels interpolate rows 0..2
+   (value) and rows 1..3 (derivative) with quintic Hermite polynomials, and read the tables in these
+   layouts:
+     attention (nc = 256, fc_easy = gate | inputhead): the slice order below, i.e. the gate and the
+       inputhead of head h at positions E2V2_POS0(h) and E2V2_POS1(h), stored slice-major;
+       layout {col0 0, split 128, block 16, block_stride 32, split_stride 16, slice_width 32};
+     degree embedding (nc = 768, profiles l = 0, 1, 2): channel c of profile l at
+       96 (c / 32) + 32 l + c % 32 (each 32-channel slice of the three profiles contiguous);
+       layout {col0 32 l, split 256, block 32, block_stride 96, split_stride 0, slice_width 0};
+     contiguous (any other caller): channel c of profile m at 256 m + c;
+       layout {col0 256 m, split 256, block 256, block_stride 0, split_stride 0, slice_width 0}. */
 #define E2V2_MAX_TYPES 32
 typedef struct e2v2_radial_net {
   const float* w1;  int32_t ld_w1;    /* Linear1 weight [128][ld_w1], ld_w1 = 256 + 2 n_emb     */
@@ -155,18 +163,33 @@ typedef struct e2v2_radial_net {
 /* Node spacing h = 2^(floor(log2(0.2 sigma)) - refine) of a GaussianSmearing basis exp(coeff (d - mu)^2)
    (sigma = sqrt(-0.5 / coeff)) and the node count covering [0, rc]. */
 int e2v2_radial_table_size(float rc, float rbf_coeff, int32_t refine, int32_t* n_nodes, float* h);
+/* Position of output channel o (0..255) of a profile in a table row:
+   pos = col0 + ((o % split) / block) * block_stride + (o / split) * split_stride + o % block
+   (checked on the host: every channel inside the row, no two at one position).  slice_width = 0: the
+   table is tab[p][n][k][nc], rows contiguous; slice_width = w > 0: it is tab[p][nc / w][n][k][w], channel
+   position pos in slice pos / w at column pos % w (each slice of a pair contiguous, its four rows at a node
+   4 w floats apart). */
+typedef struct e2v2_radial_layout {
+  int32_t col0, split, block, block_stride, split_stride, slice_width;
+} e2v2_radial_layout;
 /* Build one profile's channels of tab (device type_z [n_types], rbf_offset [256] = mu). */
 int e2v2_radial_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff, const int32_t* type_z,
-                      int32_t n_types, int32_t n_nodes, float h, float* tab, int32_t nc, int32_t col0,
-                      hipStream_t s);
+                      int32_t n_types, int32_t n_nodes, float h, float* tab, int32_t nc,
+                      const e2v2_radial_layout* layout, hipStream_t s);
 /* Interpolation error of one profile's table at every interval midpoint against the float64 profile:
    err (uint32 [4], zeroed by the caller) receives the float bits of max |f - f~|, max |f|,
    max h |f' - f~'|, max h |f'|. */
 int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
                             const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h, const float* tab,
-                            int32_t nc, int32_t col0, uint32_t* err, hipStream_t s);
+                            int32_t nc, const e2v2_radial_layout* layout, uint32_t* err, hipStream_t s);
 
 /* ---- attention --------------------------------------------------------- */
+/* Channel order of v, out, grad_out, dv and of the fc_easy table rows ("slice order"): position p of a
+   row holds the first (model channel h, the gate in the table) or second (model channel 128 + h, the
+   inputhead) channel of head h, at E2V2_POS0(h) and E2V2_POS1(h); slice s = p / 32 holds heads
+   16 s .. 16 s + 15.  Callers fold the permutation into the producing and consuming weights. */
+#define E2V2_POS0(h) (32 * ((h) / 16) + (h) % 16)
+#define E2V2_POS1(h) (E2V2_POS0(h) + 16)
 typedef struct e2v2_attn_args {
   int32_t n_rows;                /* N query atoms (= source atoms)                  */
   int64_t n_edges;
@@ -181,7 +204,7 @@ typedef struct e2v2_attn_args {
   const void* q;                 /* [N,H,D]            float, or bf16 if act_bf16   */
   const void* k;                 /* [N,H,D]            float, or bf16 if act_bf16   */
   const void* v;                 /* [9][N][C] m-major  float, or bf16 if act_bf16   */
-  const float* rtab;             /* fc_easy table [T*T][rtab_n][4][2H] (gate | inputhead), e2v2_radial_table */
+  const float* rtab;             /* fc_easy table [T*T][8][rtab_n][4][32]: slice order, slice-major */
   const int32_t* atom_type;      /* [N] type slot of each atom, 0 .. n_types - 1     */
   int32_t n_types, rtab_n;       /* T, table nodes                                  */
   float rtab_h;                  /* node spacing (a power of two)                   */
@@ -194,17 +217,20 @@ typedef struct e2v2_attn_args {
   const int32_t* col_slot_member; const int32_t* col_slot_edge; const int32_t* col_n_slots;
 } e2v2_attn_args;
 
-/* v [9][N][C] and out [20][N][C] are m-major (row r of every atom contiguous);
+/* v [9][N][C] and out [20][N][C] are m-major (row r of every atom contiguous), channels in slice order;
    out (float, or bf16 if act_bf16): h_a - h_b rows of the SO(2) product; mrow/srow [N,H] softmax max / sum;
    cnt [N,H] number of maxima.  gate and inputhead of every edge are interpolated from rtab in the kernel
    (nothing per edge is stored). */
 int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, float* srow, int32_t* cnt, hipStream_t s);
+/* Bytes of device workspace e2v2_attn_bwd needs for n_edges edges (per-edge weights handed from the row
+   pass to the column pass and per-slice partial edge gradients, alive during the call only). */
+size_t e2v2_attn_bwd_workspace(int64_t n_edges);
 /* grad_out, out [20][N][C] (float, or bf16 if act_bf16) -> ddvec [E,3], ddist [E] (including the radial
-   profile's distance derivative, from the table), dq, dk [N,H,D], dv [9][N][C] (all float); w_edge, dqk_edge
-   [E,H] are scratch written by the row pass and read by the column pass of this call */
+   profile's distance derivative, from the table), dq, dk [N,H,D], dv [9][N][C] (all float, dv in slice
+   order); workspace: e2v2_attn_bwd_workspace(E) bytes, 16-byte aligned */
 int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, const void* out, const float* mrow,
                   const float* srow, const int32_t* cnt, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
-                  float* w_edge, float* dqk_edge, hipStream_t s);
+                  void* workspace, size_t workspace_bytes, hipStream_t s);
 
 /* ---- edge-degree embedding -------------------------------------------- */
 typedef struct e2v2_deg_args {

@@ -8,7 +8,7 @@ ROOT = Path(__file__).resolve().parents[1]
 
 def declared():
     text = (ROOT / "include" / "e2v2.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(e2v2_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(e2v2_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_api():

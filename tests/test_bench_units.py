@@ -13,13 +13,14 @@ import bench  # noqa: E402
 
 def test_attention_bytes_split_by_activation_type():
     N, E = 7, 53
-    # fp32: every node / edge-list term at 4 bytes, plus the radial-table rows (6 per channel forward,
-    # 8 backward, 256 channels)
-    fwd32 = 4 * (N * 128 * 8 * 2 + N * 9 * 256 + N * 20 * 256 + N * 3 * 128 + E * 6 + N + 1)
+    # fp32: every node / edge-list term at 4 bytes (the edge list once per 16-head slice, 8 slices), plus
+    # the radial-table rows (6 per channel forward, 8 backward, 256 channels)
+    fwd32 = 4 * (N * 128 * 8 * 2 + N * 9 * 256 + N * 20 * 256 + N * 3 * 128 + 8 * E * 6 + N + 1)
     assert bench.attn_fwd_bytes(N, E) == fwd32 + 4 * E * 256 * 6
-    row32 = 4 * (N * 20 * 256 * 2 + N * 1024 * 3 + N * 9 * 256 + N * 3 * 128 + E * (6 + 4 + 256))
+    row32 = 4 * (N * 20 * 256 * 2 + N * 1024 * 3 + N * 9 * 256 + N * 3 * 128 + E * (8 * 6 + 256 + 8 * 4))
     col32 = 4 * (N * 20 * 256 + N * 1024 * 2 + N * 9 * 256 + 2 * N + E * (256 + 5))
-    assert bench.attn_bwd_bytes(N, E) == row32 + col32 + 4 * E * 256 * 8
+    part32 = 4 * E * (8 * 4 + 4)
+    assert bench.attn_bwd_bytes(N, E) == row32 + col32 + part32 + 4 * E * 256 * 8
     # bf16 storage halves exactly the activation terms: q, k, v, out, grad
     act_fwd = N * (128 * 8 * 2 + 9 * 256 + 20 * 256)
     assert bench.attn_fwd_bytes(N, E) - bench.attn_fwd_bytes(N, E, 2) == 2 * act_fwd

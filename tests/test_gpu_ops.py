@@ -164,10 +164,14 @@ def _attention_case(pkg, cuda, act_dtype, clusters=True, graph=None):
     net64 = copy.deepcopy(prof).double().net
     tw, sw = tgt.weight.detach().double().clone(), src.weight.detach().double().clone()
     type_z, slot = _types(pkg, cuda, s["Z"])
-    tab = ops.RadialTable([prof.to(cuda).net], tgt.to(cuda), src.to(cuda), rb.offset.to(cuda), rb.coeff, 6.0, type_z)
+    tab = ops.RadialTable([prof.to(cuda).net], tgt.to(cuda), src.to(cuda), rb.offset.to(cuda), rb.coeff, 6.0, type_z,
+                          layout="attn")
     st = _lib.vp(torch.cuda.current_stream().cuda_stream)
+    # the kernels hold v, out and their gradients in slice order: position p holds model channel P[p]
+    P = modules.slice_perm(cuda)
+    Pinv = torch.argsort(P)
     qd, kd = (t.to(cuda).to(act_dtype).contiguous() for t in (q, k))
-    vd = v.permute(1, 0, 2).contiguous().to(cuda).to(act_dtype)        # m-major [9, N, C]
+    vd = v.permute(1, 0, 2).to(cuda)[:, :, P].contiguous().to(act_dtype)          # m-major [9, N, C]
     args = ops.attn_args(nl, qd, kd, vd, slot, tab, math.sqrt(8.0), 6.0, int(bf))
     if not clusters:
         args.col_slot_member = args.col_slot_edge = args.col_n_slots = None
@@ -181,18 +185,19 @@ def _attention_case(pkg, cuda, act_dtype, clusters=True, graph=None):
     leaves = [t.double().requires_grad_(True) for t in (q, k, v, nl.dvec.cpu(), nl.dist.cpu())]
     gi = mlp_ref(leaves[4], Z[row], Z[col], net64, tw, sw, rb.offset.double(), float(np.float32(rb.coeff)))
     ref = attn_ref(*leaves[:5], row, col, gi, T, 6.0, N)
-    e_f = relerr(out.float().permute(1, 0, 2), ref)
+    e_f = relerr(out.float()[:, :, Pinv].permute(1, 0, 2), ref)
     grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
-    Gd = G.permute(1, 0, 2).contiguous().to(cuda).to(act_dtype)
+    Gd = G.permute(1, 0, 2).to(cuda)[:, :, P].contiguous().to(act_dtype)
     f = dict(device=cuda)
     ddv = torch.empty(E, 3, **f); dd = torch.empty(E, **f)
     dq = torch.empty(qd.shape, **f); dk = torch.empty(kd.shape, **f); dv = torch.empty(vd.shape, **f)
-    we = torch.empty(E, 128, **f); dqk = torch.empty(E, 128, **f)
+    nb = int(_lib.load().e2v2_attn_bwd_workspace(E))
+    ws = torch.empty(nb, dtype=torch.uint8, device=cuda)
     _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _lib.vp(Gd.data_ptr()), _lib.vp(out.data_ptr()),
               _lib.vp(m.data_ptr()), _lib.vp(sr.data_ptr()), _lib.vp(cnt.data_ptr()),
               _lib.vp(ddv.data_ptr()), _lib.vp(dd.data_ptr()), _lib.vp(dq.data_ptr()), _lib.vp(dk.data_ptr()),
-              _lib.vp(dv.data_ptr()), _lib.vp(we.data_ptr()), _lib.vp(dqk.data_ptr()), st)
-    errs = dict(q=relerr(dq, grads[0]), k=relerr(dk, grads[1]), v=relerr(dv.permute(1, 0, 2), grads[2]),
+              _lib.vp(dv.data_ptr()), _lib.vp(ws.data_ptr()), _lib.C.c_size_t(nb), st)
+    errs = dict(q=relerr(dq, grads[0]), k=relerr(dk, grads[1]), v=relerr(dv[:, :, Pinv].permute(1, 0, 2), grads[2]),
                 dvec=relerr(ddv, grads[3]), dist=relerr(dd, grads[4]))
     print(f"[attn {act_dtype}] fwd rel {e_f:.2e} bwd {errs}", flush=True)
     return e_f, errs

@@ -16,7 +16,7 @@ EXPORTS = [
     "e2v2_last_error", "e2v2_version", "e2v2_fill_i32", "e2v2_fill_f32", "e2v2_scan_i32",
     "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_count_noalloc", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose", "e2v2_cluster_slots",
     "e2v2_morton_keys", "e2v2_radial_table_size", "e2v2_radial_table", "e2v2_radial_table_check",
-    "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_deg_fwd", "e2v2_deg_bwd",
+    "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_attn_bwd_workspace", "e2v2_deg_fwd", "e2v2_deg_bwd",
     "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd",
     "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd", "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd",
@@ -36,6 +36,14 @@ class NbrPlan(C.Structure):
 class RadialNet(C.Structure):
     _fields_ = [("w1", vp), ("ld_w1", i32), ("n_emb", i32), ("b1", vp), ("g1", vp), ("be1", vp), ("w2", vp),
                 ("b2", vp), ("g2", vp), ("be2", vp), ("w3", vp), ("b3", vp), ("tgt", vp), ("src", vp)]
+
+
+class RadialLayout(C.Structure):
+    """Position of output channel o of a profile in a table row:
+    col0 + ((o % split) // block) * block_stride + (o // split) * split_stride + o % block;
+    slice_width w > 0 stores the table slice-major, [pairs][nc / w][nodes][4][w]."""
+    _fields_ = [("col0", i32), ("split", i32), ("block", i32), ("block_stride", i32), ("split_stride", i32),
+                ("slice_width", i32)]
 
 
 class AttnArgs(C.Structure):
@@ -67,6 +75,8 @@ def load():
     for name in EXPORTS:
         getattr(lib, name)  # raises AttributeError if a symbol is absent
     lib.e2v2_last_error.restype = C.c_char_p
+    lib.e2v2_attn_bwd_workspace.restype = C.c_size_t
+    lib.e2v2_attn_bwd_workspace.argtypes = [C.c_int64]
     _lib = lib
     return lib
 

@@ -1,6 +1,6 @@
 // Sparse equivariant attention of one E2Former-V2 layer on the query CSR.
 //
-// Forward (one workgroup per query atom i, online segmented softmax):
+// Forward (online segmented softmax per query atom i and head h):
 //   a_e[h]   = gate_e[h] * <q_i[h]/sqrt(D), k_j[h]>
 //   m[h]     = max_e a_e[h];  e_e = exp(a_e - m) p(d_e);  s = sum_e e_e
 //   w_e[h]   = e_e ih_e[h] / (s + 1e-3) / max(d_e, 1e-6)
@@ -11,11 +11,22 @@
 //  wigner6j/so2_tensor_product.py:341-385): TP(v, r_i) - TP(v, r_j) = TP(v, r_ij).
 // gate and inputhead of every edge are the fc_easy radial profile of
 // (d, z_i, z_j), interpolated from its per-type-pair distance table (radial.h)
-// where they are used; no per-edge tensor is read from or written to memory
-// except the column pass's inputs below.
-// Backward: row pass (dq, w, dqk, dvec/ddist with the profile's distance
-// derivative; the softmax row terms come from D_h = sum_{c in h} sum_t G[t,c]
-// out[t,c]) and a column pass over the key CSR (dv_j, dk_j) with no atomics.
+// where they are used.
+//
+// Head slices: the 128 heads form 8 slices of 16.  The forward and the
+// backward row pass run one wavefront per (query row, slice), slice =
+// blockIdx % 8; workgroups are dispatched round-robin over the 8 XCDs, so XCD
+// s runs every row of slice s in Morton order and its L2 holds slice s of the
+// table and of the gathered k and v rows (a whole layer's table does not fit
+// one XCD's 4 MB L2; one slice of its frequent type pairs does).  Channels of
+// v, out, their gradients and the table are stored in slice order (position
+// p holds the first or second channel of head pos_head(p); the header's
+// E2V2_POS0 / E2V2_POS1), so a slice is one 128-byte run of every row.
+// Backward: row pass (dq, the edge weights w and dL/dqk, dvec/ddist partials
+// per slice with the profile's distance derivative; the softmax row terms
+// come from D_h = sum_{c in h} sum_t G[t,c] out[t,c]), a column pass over the
+// key CSR (dv_j, dk_j) with no atomics, and the slice partials added per edge
+// in slice order.
 #include "common.h"
 #include "radial.h"
 #include "tp_table.h"
@@ -23,16 +34,20 @@
 
 namespace e2v2 {
 
-constexpr int kH = 128, kD = 8, kC = 256, kNV = 9, kNT = 20, kCH = 32, kCHB = 16;
+constexpr int kH = 128, kD = 8, kC = 256, kNV = 9, kNT = 20;
 constexpr float kEps = 1e-3f;
-// Channel groups of the clustered kernels: group g holds heads 32g..32g+31 and
-// their 64 channels (c and c + 128 share head c % 128).  Lane l of a wave owns
-// channel 32g + l (l < 32) or 128 + 32g + l - 32, i.e. head 32g + l % 32, and
-// dims 4 (l / 32) .. +3 of that head's q / k.
-constexpr int kGroups = 4, kGroupHeads = kH / kGroups;
-__device__ __forceinline__ int group_channel(int g, int lane) {
-  return (lane < 32) ? (kGroupHeads * g + lane) : (kH + kGroupHeads * g + lane - 32);
-}
+// Slice order of channel positions: position p holds the first (p % 32 < 16,
+// model channel h) or second (model channel 128 + h) channel of head
+// h = pos_head(p); slice s = p / 32 holds heads 16 s .. 16 s + 15.  In the
+// fc_easy table the first channel of a head is its gate, the second its
+// inputhead.
+constexpr int kSl = 8, kSlH = kH / kSl, kSlC = kC / kSl;
+__device__ __forceinline__ int pos_head(int p) { return ((p >> 5) << 4) | (p & 15); }
+// Channel groups of the clustered column pass: group g holds heads
+// 32 g .. 32 g + 31, i.e. the 64 positions 64 g .. 64 g + 63 (slices 2 g and
+// 2 g + 1).  Lane l of a wave owns position 64 g + l, and dims 4 (l % 2) .. +3
+// of head 32 g + l / 2 for dk.
+constexpr int kGroups = 4, kGroupHeads = kH / kGroups, kGroupC = kC / kGroups;
 // (cluster, group) of a workgroup: the workgroups of one XCD (blockIdx % 8) run
 // its contiguous range of clusters group by group, so its L2 holds one group's
 // quarter of the gathered rows at a time.
@@ -50,7 +65,7 @@ __device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
   return E;
 }
 
-// the fc_easy table: channels h (gate) and 128 + h (inputhead) of each row
+// the fc_easy table: 256 channels per row in slice order (gate, inputhead of each head)
 constexpr int kTabC = 2 * kH;
 __device__ __forceinline__ RadialTab make_tab(const e2v2_attn_args& A) {
   RadialTab R;
@@ -124,55 +139,76 @@ __device__ __forceinline__ void load_qs(const e2v2_attn_args& A, int i, int h, f
   for (int d = 0; d < kD; ++d) qs[d] = q[d] / A.q_div;
 }
 
-struct ChunkEdges {
-  int64_t toff[kCH];   // table offset of the edge's lower node
-  int j[kCH];
-  float dv[kCH][3];
-  float p[kCH];
-  float dp[kCH];
-  float R[kCH];
-  float rR[kCH];
-  float d[kCH];
-  float tt[kCH];       // fraction of the distance in its node interval
-};
 
-__device__ __forceinline__ void load_chunk(const e2v2_attn_args& A, const Envelope& env, const RadialTab& R, int ti,
-                                           int e0, int nc, ChunkEdges& ce) {
-  const int t = threadIdx.x;
-  if (t < nc) {
-    const int64_t e = (int64_t)e0 + t;
-    const int j = A.col[e];
-    ce.j[t] = j;
-    ce.dv[t][0] = A.dvec[3 * e];
-    ce.dv[t][1] = A.dvec[3 * e + 1];
-    ce.dv[t][2] = A.dvec[3 * e + 2];
-    const float d = A.dist[e];
-    ce.d[t] = d;
-    float p, dp;
-    env.eval(d, p, dp);
-    ce.p[t] = p;
-    ce.dp[t] = dp;
-    ce.R[t] = fmaxf(d, 1e-6f);
-    ce.rR[t] = 1.0f / ce.R[t];
-    float tt;
-    ce.toff[t] = radial_node(R, ti * R.n_types + A.atom_type[j], d, tt);
-    ce.tt[t] = tt;
-  }
+// One edge's gathered operands for a head, kept in the storage type until the
+// edge is applied (bf16: half the staging registers of converted values).
+template <typename TS>
+struct HeadEdge {
+  TS k[kD];
+  TS v0[kNV], v1[kNV];
+  float tg[8], ti[8];   // table rows 0..3 at the lower and upper node: gate, inputhead
+};
+__device__ __forceinline__ void load8_raw(const float* p, float (&v)[8]) { load8(p, v); }
+__device__ __forceinline__ void load8_raw(const __bf16* p, __bf16 (&v)[8]) {
+  const bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = a[i];
 }
 
+
+// Buffer resource over [base, base + bytes): vector loads at a 32-bit byte
+// offset plus a wave-uniform scalar offset, no per-lane address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float buf_act(float*, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ float buf_act(__bf16*, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0) << 16);
+}
+
+// Forward, one wavefront per (query row i, slice s), i = blockIdx / 8,
+// s = blockIdx % 8.  Per chunk of up to 32 edges: lane t < nc forms edge t's
+// gather offsets, dvec, envelope, 1/d, table node and Hermite weights in LDS;
+// lane (sub, hh) = (lane / 16, lane % 16) computes the logits of head 16 s + hh
+// for the chunk's edges sub, sub + 4, ... (gate and inputhead interpolated from
+// the slice-major table; a partial chunk repeats its last edge and masks it)
+// and the head's online-softmax update (chunk max, count of maxima and sum
+// combined over the four subs by lane swaps, the same order in every lane) and
+// stages the edge weights ee ih / d; then lane (par, u) = (lane / 32, lane % 32)
+// accumulates position 32 s + u over the chunk's edges of parity par (27
+// accumulators: 9 rows of v times xyz).  In both loops the next edge's gathers
+// are issued before the current edge is applied.  The two parities are added
+// once per row in LDS, the coupling table is applied and the slice's 20
+// output rows are written.
 template <typename TS>
-__global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, TS* __restrict__ out, float* __restrict__ mrow,
-                                                  float* __restrict__ srow, int32_t* __restrict__ cnt) {
-  const TS* __restrict__ Kp = static_cast<const TS*>(A.k);
-  const TS* __restrict__ Vp = static_cast<const TS*>(A.v);
-  __shared__ float a_s[kCH][kH];
-  __shared__ float coef_s[kCH][kH];
-  __shared__ float scale_s[kH];
-  __shared__ float inv_s[kH];
-  __shared__ ChunkEdges ce;
-  const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
+__global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __restrict__ out, float* __restrict__ mrow,
+                                                    float* __restrict__ srow, int32_t* __restrict__ cnt) {
+  constexpr int CH = 32;               // edges per chunk
+  __shared__ uint32_t ckof[CH];        // byte offsets of the edge's k row (head 16 s) and v rows (position 32 s)
+  __shared__ uint32_t cvof[CH];
+  __shared__ float4 cg[CH];            // dvec, envelope p
+  __shared__ float crR[CH];            // 1 / max(d, 1e-6)
+  __shared__ int64_t ctoff[CH];        // slice-s table offset of the lower node
+  __shared__ float chw[6][CH];         // quintic Hermite weights of the edge's fraction in its node interval
+  __shared__ float a_s[CH][kSlH];      // logits per (edge, head)
+  __shared__ float coef_s[CH][kSlH];   // inputhead, then ee ih / d per (edge, head)
+  __shared__ float sc_s[kSlH];         // rescale of the running sums per head
+  __shared__ float red[kNV * 3][kSlC];
+  const int s = blockIdx.x % kSl, i = blockIdx.x / kSl;
   if (i >= A.n_rows) return;
-  const int h = t & (kH - 1), half = t >> 7;
+  const int lane = threadIdx.x;
+  const int hh = lane & (kSlH - 1), sub = lane >> 4;
+  const int u = lane & (kSlC - 1), par = lane >> 5, hu = u & (kSlH - 1);
+  const int h = kSlH * s + hh;
+  const int pu = kSlC * s + u;
+  // gathers at 32-bit byte offsets: k through its base (n_rows * kH * kD * sizeof(TS) < 2^32 and
+  // 9 n_rows * kC * sizeof(TS) < 2^32 are checked by the host), v through a buffer resource
+  const char* __restrict__ Kb = static_cast<const char*>(A.k) + (size_t)hh * kD * sizeof(TS);
+  const uint32_t vsb = (uint32_t)A.n_rows * kC * sizeof(TS);
+  const __amdgpu_buffer_rsrc_t Vr = buf_rsrc(A.v, kNV * vsb);   // uniform base; the lane's column in voffset
+  const uint32_t ub = (uint32_t)u * sizeof(TS);
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   const Envelope env = make_env(A);
   const RadialTab R = make_tab(A);
@@ -184,87 +220,176 @@ __global__ __launch_bounds__(256) void k_attn_fwd(e2v2_attn_args A, TS* __restri
   float acc[kNV][3];
 #pragma unroll
   for (int r = 0; r < kNV; ++r) acc[r][0] = acc[r][1] = acc[r][2] = 0.f;
-  const int hc = t & (kH - 1);  // head of channel c = t
-  for (int c0 = 0; c0 < n; c0 += kCH) {
-    const int nc = min(kCH, n - c0);
-    load_chunk(A, env, R, ti, b + c0, nc, ce);
-    __syncthreads();
-    for (int el = half; el < nc; el += 2) {
-      const float qk = qk_dot(qs, Kp + ((size_t)ce.j[el] * kH + h) * kD);
-      // gate (channel h) and inputhead (channel 128 + h): rows 0..2 at the two nodes
-      const float* tb = R.tab + ce.toff[el] + h;
-      const Hermite5 Hw = hermite5(ce.tt[el]);
-      constexpr int nb = 4 * kTabC;
-      const float gate = herm_value(Hw, tb[0], tb[kTabC], tb[2 * kTabC], tb[nb], tb[nb + kTabC], tb[nb + 2 * kTabC]);
-      const float* tb2 = tb + kH;
-      const float ih = herm_value(Hw, tb2[0], tb2[kTabC], tb2[2 * kTabC], tb2[nb], tb2[nb + kTabC],
-                                  tb2[nb + 2 * kTabC]);
-      a_s[el][h] = gate * qk;
-      coef_s[el][h] = ih;   // input head, scaled below
+  struct LogitIn {
+    TS k[kD];
+    float t[12];   // gate rows 0..2 at the two nodes, then inputhead
+  };
+  for (int c0 = 0; c0 < n; c0 += CH) {
+    const int nc = min(CH, n - c0);
+    if (lane < nc) {
+      const int64_t e = (int64_t)b + c0 + lane;
+      const int j = A.col[e];
+      const float d = A.dist[e];
+      float p, dp;
+      env.eval(d, p, dp);
+      ckof[lane] = ((uint32_t)j * kH + kSlH * s) * (kD * sizeof(TS));
+      cvof[lane] = ((uint32_t)j * kC + kSlC * s) * sizeof(TS);
+      cg[lane] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], p);
+      crR[lane] = 1.0f / fmaxf(d, 1e-6f);
+      float tt;
+      ctoff[lane] = radial_node_sliced(R, ti * R.n_types + A.atom_type[j], s, kSl, kSlC, d, tt);
+      const Hermite5 Hw = hermite5(tt);
+      chw[0][lane] = Hw.a0; chw[1][lane] = Hw.a1; chw[2][lane] = Hw.a2;
+      chw[3][lane] = Hw.b0; chw[4][lane] = Hw.b1; chw[5][lane] = Hw.b2;
     }
     __syncthreads();
-    if (t < kH) {
-      float cm = -INFINITY;
-      for (int el = 0; el < nc; ++el) cm = fmaxf(cm, a_s[el][h]);
-      const float m_new = fmaxf(m_run, cm);
-      const float sc = (m_run == -INFINITY) ? 0.f : expf(m_run - m_new);
-      int cc = 0;
-      for (int el = 0; el < nc; ++el) cc += (a_s[el][h] == m_new);
-      c_run = (m_new == m_run) ? c_run + cc : cc;
-      s_run *= sc;
-      for (int el = 0; el < nc; ++el) {
-        const float ex = expf(a_s[el][h] - m_new);
-        const float ee = ex * ce.p[el];
-        s_run += ee;
-        coef_s[el][h] = (ee * coef_s[el][h]) * ce.rR[el];
+    // logits of head h for the edges sub, sub + 4, ... of the chunk (a missing edge repeats the last one and
+    // is not stored)
+    auto lload = [&](int k, LogitIn& X) {
+      const int el = min(sub + 4 * k, nc - 1);
+      load8_raw(reinterpret_cast<const TS*>(Kb + ckof[el]), X.k);
+      // slice-s table: gate of head hh in column hh, inputhead in column 16 + hh; rows 0..2 at the two nodes
+      const float* tg = R.tab + ctoff[el] + hh;
+      constexpr int rs = kSlC, nb = 4 * kSlC;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        X.t[q] = tg[q * rs];
+        X.t[3 + q] = tg[nb + q * rs];
+        X.t[6 + q] = tg[kSlH + q * rs];
+        X.t[9 + q] = tg[kSlH + nb + q * rs];
       }
-      m_run = m_new;
-      scale_s[h] = sc;
-    }
-    __syncthreads();
+    };
+    auto lapply = [&](int k, const LogitIn& X) {
+      const int el = sub + 4 * k;
+      if (el >= nc) return;
+      float kf[kD];
+#pragma unroll
+      for (int q = 0; q < kD; ++q) kf[q] = f32(X.k[q]);
+      const float qk = half_dot(qs, kf) + half_dot(qs + 4, kf + 4);
+      Hermite5 Hw;
+      Hw.a0 = chw[0][el]; Hw.a1 = chw[1][el]; Hw.a2 = chw[2][el];
+      Hw.b0 = chw[3][el]; Hw.b1 = chw[4][el]; Hw.b2 = chw[5][el];
+      const float gate = herm_value(Hw, X.t[0], X.t[1], X.t[2], X.t[3], X.t[4], X.t[5]);
+      a_s[el][hh] = gate * qk;
+      coef_s[el][hh] = herm_value(Hw, X.t[6], X.t[7], X.t[8], X.t[9], X.t[10], X.t[11]);
+    };
     {
-      const float sc = scale_s[hc];
-      if (sc != 1.f) {
-#pragma unroll
-        for (int r = 0; r < kNV; ++r) {
-          acc[r][0] *= sc; acc[r][1] *= sc; acc[r][2] *= sc;
-        }
+      const int ke = (nc + 3) / 4;   // logit steps of this chunk (the subs of a step share it)
+      LogitIn Xa, Xb;
+      lload(0, Xa);
+      int k = 0;
+      for (; k + 2 < ke; k += 2) {
+        lload(k + 1, Xb);
+        lapply(k, Xa);
+        lload(k + 2, Xa);
+        lapply(k + 1, Xb);
       }
-      for (int el = 0; el < nc; ++el) {
-        const float w = coef_s[el][hc];
-        const float wx = w * ce.dv[el][0], wy = w * ce.dv[el][1], wz = w * ce.dv[el][2];
-        const TS* vp = Vp + (size_t)ce.j[el] * kC + t;
-        const size_t vs = (size_t)A.n_rows * kC;
-        float vv[kNV];
+      if (k + 1 < ke) {
+        lload(k + 1, Xb);
+        lapply(k, Xa);
+        lapply(k + 1, Xb);
+      } else {
+        lapply(k, Xa);
+      }
+    }
+    // online softmax of head h over the chunk (each lane reads back the logits it wrote)
+    float cm = -INFINITY;
+    for (int el = sub; el < nc; el += 4) cm = fmaxf(cm, a_s[el][hh]);
+    cm = fmaxf(cm, __shfl_xor(cm, 16, kWave));
+    cm = fmaxf(cm, __shfl_xor(cm, 32, kWave));
+    const float m_new = fmaxf(m_run, cm);
+    const float sc = (m_run == -INFINITY) ? 0.f : fexp(m_run - m_new);
+    int cc = 0;
+    float ls = 0.f;
+    for (int el = sub; el < nc; el += 4) {
+      const float av = a_s[el][hh];
+      cc += (av == m_new);
+      const float ee = fexp(av - m_new) * cg[el].w;
+      ls += ee;
+      coef_s[el][hh] = (ee * coef_s[el][hh]) * crR[el];
+    }
+    cc += __shfl_xor(cc, 16, kWave);
+    cc += __shfl_xor(cc, 32, kWave);
+    ls += __shfl_xor(ls, 16, kWave);
+    ls += __shfl_xor(ls, 32, kWave);
+    c_run = (m_new == m_run) ? c_run + cc : cc;
+    s_run = s_run * sc + ls;
+    m_run = m_new;
+    if (sub == 0) sc_s[hh] = sc;
+    __syncthreads();
+    // value aggregation of position 32 s + u over the edges of parity par
+    const float scu = sc_s[hu];
+    if (scu != 1.f) {
 #pragma unroll
-        for (int r = 0; r < kNV; ++r) vv[r] = f32(vp[r * vs]);
+      for (int r = 0; r < kNV; ++r) {
+        acc[r][0] *= scu; acc[r][1] *= scu; acc[r][2] *= scu;
+      }
+    }
+    auto vload = [&](int el, float (&vv)[kNV]) {
+      const uint32_t vof = cvof[el] + ub;
 #pragma unroll
-        for (int r = 0; r < kNV; ++r) {
-          acc[r][0] = fmaf(vv[r], wx, acc[r][0]);
-          acc[r][1] = fmaf(vv[r], wy, acc[r][1]);
-          acc[r][2] = fmaf(vv[r], wz, acc[r][2]);
-        }
+      for (int r = 0; r < kNV; ++r) vv[r] = buf_act(static_cast<TS*>(nullptr), Vr, vof, (uint32_t)r * vsb);
+    };
+    auto vapply = [&](int el, const float (&vv)[kNV]) {
+      const float w = coef_s[el][hu];
+      const float4 g = cg[el];
+      const float wx = w * g.x, wy = w * g.y, wz = w * g.z;
+#pragma unroll
+      for (int r = 0; r < kNV; ++r) {
+        acc[r][0] = fmaf(vv[r], wx, acc[r][0]);
+        acc[r][1] = fmaf(vv[r], wy, acc[r][1]);
+        acc[r][2] = fmaf(vv[r], wz, acc[r][2]);
+      }
+    };
+    int el = par;
+    if (el < nc) {
+      float va[kNV], vb[kNV];
+      vload(el, va);
+      for (; el + 4 < nc; el += 4) {
+        vload(el + 2, vb);
+        vapply(el, va);
+        vload(el + 4, va);
+        vapply(el + 2, vb);
+      }
+      if (el + 2 < nc) {
+        vload(el + 2, vb);
+        vapply(el, va);
+        vapply(el + 2, vb);
+      } else {
+        vapply(el, va);
       }
     }
     __syncthreads();
   }
-  if (t < kH) {
-    inv_s[h] = 1.0f / (s_run + kEps);
+  if (par) {
+#pragma unroll
+    for (int r = 0; r < kNV; ++r) {
+      red[3 * r][u] = acc[r][0]; red[3 * r + 1][u] = acc[r][1]; red[3 * r + 2][u] = acc[r][2];
+    }
+  }
+  __syncthreads();
+  if (!par) {
+#pragma unroll
+    for (int r = 0; r < kNV; ++r) {
+      acc[r][0] += red[3 * r][u]; acc[r][1] += red[3 * r + 1][u]; acc[r][2] += red[3 * r + 2][u];
+    }
+    // this lane (sub = u / 16, hh = u % 16) holds the statistics of head 16 s + hu
+    const float inv = 1.0f / (s_run + kEps);
+    float o[kNT];
+#pragma unroll
+    for (int q = 0; q < kNT; ++q) o[q] = 0.f;
+#pragma unroll
+    for (int z = 0; z < kTpNnz; ++z) o[kTp[z].t] = fmaf(kTp[z].c, acc[kTp[z].r][kTp[z].k], o[kTp[z].t]);
+    TS* op = out + (size_t)i * kC + pu;
+    const size_t os = (size_t)A.n_rows * kC;
+#pragma unroll
+    for (int q = 0; q < kNT; ++q) store_act(o[q] * inv, op + q * os);
+  }
+  if (lane < kSlH) {
     mrow[(size_t)i * kH + h] = m_run;
     srow[(size_t)i * kH + h] = s_run;
     cnt[(size_t)i * kH + h] = c_run;
   }
-  __syncthreads();
-  const float inv = inv_s[hc];
-  float o[kNT];
-#pragma unroll
-  for (int q = 0; q < kNT; ++q) o[q] = 0.f;
-#pragma unroll
-  for (int z = 0; z < kTpNnz; ++z) o[kTp[z].t] = fmaf(kTp[z].c, acc[kTp[z].r][kTp[z].k], o[kTp[z].t]);
-  TS* op = out + (size_t)i * kC + t;
-  const size_t os = (size_t)A.n_rows * kC;
-#pragma unroll
-  for (int q = 0; q < kNT; ++q) store_act(o[q] * inv, op + q * os);
 }
 
 // dA[r][k] = sum_t T[t][r][k] g[t] for one channel
@@ -292,7 +417,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col_ch(e2v2_attn_args A, const
   __shared__ float cq[CC][kH];
   const int j = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
   if (j >= A.n_rows) return;
-  const int c = t, hc = t & (kH - 1);
+  const int c = t, hc = pos_head(t);
   const int hk = t >> 1, d0 = 4 * (t & 1);
   const size_t os = (size_t)A.n_rows * kC;
   float av[kNV];
@@ -365,7 +490,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col_ch(e2v2_attn_args A, const
 // Column pass, channel pairs (the bf16 form: one 4-byte word carries two
 // channels): for every source atom j, sum over its key-CSR edges (ascending
 // edge id) -> dv_j and dk_j, no atomics.  Thread t owns the channel pair
-// (2u, 2u + 1), u = t % 128, and the chunk's edges of parity t / 128: every
+// positions (2u, 2u + 1), u = t % 128, and the chunk's edges of parity t / 128: every
 // gather instruction moves two channels per lane (the gathers, not the bytes,
 // bound this pass).  The two parities' partial sums are added once per column
 // in LDS (fixed order: deterministic).  Edge metadata of 32-edge chunks is
@@ -399,7 +524,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col_pair(e2v2_attn_args A, con
   if (j >= A.n_rows) return;
   const int u = t & (kH - 1), par = t >> 7;
   const int c0 = 2 * u;                                     // channels c0, c0 + 1
-  const int h0 = c0 & (kH - 1), h1 = (c0 + 1) & (kH - 1);   // their heads
+  const int h0 = pos_head(c0), h1 = pos_head(c0 + 1);       // their heads
   const size_t os = (size_t)A.n_rows * kC;
   float av0[kNV], av1[kNV];
 #pragma unroll
@@ -473,8 +598,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_col_pair(e2v2_attn_args A, con
 }
 
 // Column pass over clusters of R consecutive key-CSR columns and one of four
-// channel groups (G and q in fp32 or bf16, sums in fp32).  Group g holds the 64 channels of heads 32g..32g+31
-// (c and c + 128 share a head); the workgroups of one XCD run group by group,
+// channel groups (G and q in fp32 or bf16, sums in fp32).  Group g holds the 64 channel positions of heads
+// 32g..32g+31 (positions 64g..64g+63); the workgroups of one XCD run group by group,
 // so its L2 holds a quarter of each neighbour row at a time and the gathered
 // rows of a column window stay resident.  Wave w applies the slots s = w mod 4
 // of each chunk (lane = channel of the group; for dk lane = (head, half of the
@@ -496,8 +621,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   int cl, grp;
   if (!cluster_group(n_cl, cl, grp)) return;
   const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
-  const int c = group_channel(grp, lane);
-  const int hc = c & (kH - 1);
+  const int c = kGroupC * grp + lane;   // channel position
+  const int hc = pos_head(c);
   const int hk = kGroupHeads * grp + (lane >> 1), d0 = 4 * (lane & 1);
   const int j0 = cl * R, nj = min(R, A.n_rows - j0);
   const size_t os = (size_t)A.n_rows * kC;
@@ -627,75 +752,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   }
 }
 
-// Sums of four values over the 64 lanes of a wave; every lane of row k (lanes
-// 16k .. 16k + 15) returns the sum of value k.  A swap across the wave halves
-// (lanes < 32 keep values 0 and 1, lanes >= 32 values 2 and 3), a swap across
-// the two rows of each half (even rows keep the first, odd rows the second),
-// then four DPP steps within each row of 16.
-__device__ __forceinline__ float wave_sum4(float v0, float v1, float v2, float v3, int lane) {
-  const bool hi = (lane & 32) != 0, odd = (lane & 16) != 0;
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v2), false, false);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v1), __float_as_uint(v3), false, false);
-  // lane < 32: a[1] = v0 of lane + 32; lane >= 32: a[0] = v2 of lane - 32 (b likewise for v1, v3)
-  const float x = hi ? v2 + __uint_as_float(a[0]) : v0 + __uint_as_float(a[1]);
-  const float y = hi ? v3 + __uint_as_float(b[0]) : v1 + __uint_as_float(b[1]);
-  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-  // even row: c[1] = x of the odd row beside it; odd row: c[0] = y of the even row
-  const float z = odd ? y + __uint_as_float(c[0]) : x + __uint_as_float(c[1]);
-  return dpp_row_sum16(z);
+// Sums over the 16 lanes of each row of the wave of four values: quad q of the
+// row (lanes 4 q .. 4 q + 3) returns the sum of value q.  Lanes 0..7 of a row
+// keep values 0, 1 and lanes 8..15 values 2, 3, each adding its partner's
+// (lane ^ 8: row rotation by 8); then within each half row lanes 0..3 keep the
+// first and lanes 4..7 the second (partner 7 - lane: half-row mirror); two
+// quad permutes finish the sums.  Fixed order, the same in every row.
+__device__ __forceinline__ float row_sum4(float v0, float v1, float v2, float v3, int lane) {
+  const bool hi8 = (lane & 8) != 0, hi4 = (lane & 4) != 0;
+  const float k0 = hi8 ? v2 : v0, k1 = hi8 ? v3 : v1;
+  const float s0 = hi8 ? v0 : v2, s1 = hi8 ? v1 : v3;
+  const float x0 = k0 + dpp_mov<0x128>(s0);   // row_ror:8
+  const float x1 = k1 + dpp_mov<0x128>(s1);
+  float y = (hi4 ? x1 : x0) + dpp_mov<0x141>(hi4 ? x0 : x1);   // row_half_mirror
+  y += dpp_mov<0x4E>(y);   // quad_perm [2,3,0,1]
+  y += dpp_mov<0xB1>(y);   // quad_perm [1,0,3,2]
+  return y;
 }
 
-// One edge's gathered operands for a head, kept in the storage type until the
-// edge is applied (bf16: half the staging registers of converted values).
+// Backward row pass, one wavefront per (query row i, slice s) as in the
+// forward.  Lane (sub, hh) owns head h = 16 s + hh with both of its channel
+// positions and the row's edges sub, sub + 4, ...  Per edge it interpolates the
+// head's gate and inputhead and their distance derivatives, recomputes the
+// logit and weight, forms u = dA^T v_j for both channels (dA = T^T G_i, formed
+// once per row) and with it the head's dL/dw, runs the softmax / gate /
+// distance backward (dL/dgate gate' + dL/dih ih' included; the softmax row
+// terms from D_h and the exact amax gradient split over ties), accumulates dq
+// from the k_j row it already holds and writes the edge's w and dL/dqk for the
+// column pass.  The sums over the slice's 16 heads of dL/d dvec and dL/dd are
+// formed within each 16-lane row (row_sum4) and written as the slice's partial
+// part[s][e][0..3].  The head-independent terms of up to 64 edges (column,
+// distance, envelope, 1/d, dvec, table node and fraction) are formed once per
+// chunk in LDS, and the next edge's gathers are issued before the current one
+// is applied.
 template <typename TS>
-struct HeadEdge {
-  TS k[kD];
-  TS v0[kNV], v1[kNV];
-  float tg[8], ti[8];   // table rows 0..3 at the lower and upper node: gate, inputhead
-};
-__device__ __forceinline__ void load8_raw(const float* p, float (&v)[8]) { load8(p, v); }
-__device__ __forceinline__ void load8_raw(const __bf16* p, __bf16 (&v)[8]) {
-  const bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = a[i];
-}
-
-// Backward row pass, one workgroup per query row; thread t owns head h = t % 128
-// with both of its channels (h, h + 128) and the row's edges of parity t / 128.
-// The edge index is uniform per wave (scalar loads of the edge record), and
-// the gathers of the next edge (k_j, v_j and the head's gate / inputhead table
-// rows) are issued before the current one is applied.  Per edge a thread
-// interpolates the head's gate and inputhead and their distance derivatives,
-// recomputes its logit and weight, forms u = dA^T v_j for both channels
-// (dA = T^T G_i) and with it the head's dL/dw, runs the softmax / gate /
-// distance backward for its head (the profile's part dL/dgate gate' +
-// dL/dih ih' included) and accumulates dq from the k_j row it already holds,
-// so nothing crosses threads but the per-edge sums over heads (dL/d dvec,
-// dL/dd): the 64 heads of a wave by lane swaps and DPP (wave_sum4), the two
-// waves of a parity in LDS, added in a fixed order once per chunk of up to 128
-// edges.  The head-independent edge terms (column, distance, envelope, 1/d,
-// dvec, table node and fraction) are formed once per edge at the start of a
-// chunk and read from LDS.
-template <typename TS>
-__global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const TS* __restrict__ G,
-                                                         const TS* __restrict__ O, const float* __restrict__ mrow,
-                                                         const float* __restrict__ srow,
-                                                         const int32_t* __restrict__ cnt,
-                                                         float* __restrict__ ddv, float* __restrict__ dd,
-                                                         float* __restrict__ dq, float* __restrict__ w_out,
-                                                         float* __restrict__ dqk_out) {
-  constexpr int CH = 64;                      // edges per parity and reduction chunk
-  __shared__ float part[2 * CH][2][4];
-  __shared__ float dq_s[kH][kD];
-  __shared__ float4 er_a[2 * CH];             // per edge of the chunk: p, dp/dd, 1/max(d, 1e-6), d
-  __shared__ float4 er_b[2 * CH];             // dvec, column (int bits)
-  __shared__ int64_t er_toff[2 * CH];         // table offset of the lower node
-  __shared__ float er_t[2 * CH];              // fraction in the node interval
-  const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
+__global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const TS* __restrict__ G,
+                                                        const TS* __restrict__ O, const float* __restrict__ mrow,
+                                                        const float* __restrict__ srow,
+                                                        const int32_t* __restrict__ cnt, float* __restrict__ part,
+                                                        float* __restrict__ dq, float* __restrict__ w_out,
+                                                        float* __restrict__ dqk_out) {
+  constexpr int CH = 64;
+  __shared__ float4 er_a[CH];      // p, dp/dd, 1/max(d, 1e-6), d
+  __shared__ float4 er_b[CH];      // dvec, column (int bits)
+  __shared__ int64_t er_toff[CH];  // slice-s table offset of the lower node
+  __shared__ float er_hw[6][CH];   // quintic Hermite weights of the fraction in the node interval
+  const int s = blockIdx.x % kSl, i = blockIdx.x / kSl;
   if (i >= A.n_rows) return;
+  const int lane = threadIdx.x, hh = lane & (kSlH - 1), sub = lane >> 4;
+  const int h = kSlH * s + hh;
+  const int p0 = kSlC * s + hh, p1 = p0 + kSlH;   // the head's two channel positions
   const RadialTab R = make_tab(A);
   const int ti = A.atom_type[i];
-  const int h = t & (kH - 1), par = t >> 7, lane = t & (kWave - 1), wsub = (t >> 6) & 1;
   const TS* __restrict__ Kp = static_cast<const TS*>(A.k);
   const TS* __restrict__ Vp = static_cast<const TS*>(A.v);
   const size_t os = (size_t)A.n_rows * kC;
@@ -706,26 +814,25 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
   float inv, dsum, dmc, m;
   {
     float g0[kNT], g1[kNT];
-    float Dh = 0.f;
 #pragma unroll
     for (int z = 0; z < kNT; ++z) {
-      g0[z] = f32(G[(size_t)i * kC + z * os + h]);
-      g1[z] = f32(G[(size_t)i * kC + z * os + h + kH]);
+      g0[z] = f32(G[(size_t)i * kC + z * os + p0]);
+      g1[z] = f32(G[(size_t)i * kC + z * os + p1]);
     }
-    // D_h = sum over the head's channels and the 20 rows, summed as channel h then h + 128
+    // D_h = sum over the head's two channels and the 20 rows, summed as the first channel then the second
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int z = 0; z < kNT; ++z) {
-      d0 = fmaf(g0[z], f32(O[(size_t)i * kC + z * os + h]), d0);
-      d1 = fmaf(g1[z], f32(O[(size_t)i * kC + z * os + h + kH]), d1);
+      d0 = fmaf(g0[z], f32(O[(size_t)i * kC + z * os + p0]), d0);
+      d1 = fmaf(g1[z], f32(O[(size_t)i * kC + z * os + p1]), d1);
     }
-    Dh = d1 + d0;
+    const float Dh = d1 + d0;
     tp_transpose(g0, dA0);
     tp_transpose(g1, dA1);
     m = mrow[(size_t)i * kH + h];
-    const float s = srow[(size_t)i * kH + h];
+    const float sr = srow[(size_t)i * kH + h];
     const int cn = cnt[(size_t)i * kH + h];
-    inv = 1.0f / (s + kEps);
+    inv = 1.0f / (sr + kEps);
     dsum = Dh * inv;
     dmc = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
   }
@@ -736,35 +843,37 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
   for (int d = 0; d < kD; ++d) dqa[d] = 0.f;
   using L = HeadEdge<TS>;
   int c0 = 0;  // first edge of the current chunk
-  auto issue = [&](int el, L& X) {
-    const int64_t e = (int64_t)b + el;
-    const int j = __float_as_int(er_b[el - c0].w);
-    // 32-bit per-lane byte offsets from wave-uniform bases (n_rows * kH * kD *
-    // sizeof(TS) < 2^32 is checked by the host)
+  auto issue = [&](int sl, L& X) {
+    const int j = __float_as_int(er_b[sl].w);
+    // 32-bit per-lane byte offsets from wave-uniform bases (n_rows * kH * kD * sizeof(TS) < 2^32, which
+    // bounds the v offsets too, is checked by the host)
     const uint32_t kof = ((uint32_t)j * kH + h) * (kD * sizeof(TS));
     load8_raw(reinterpret_cast<const TS*>(reinterpret_cast<const char*>(Kp) + kof), X.k);
-    const uint32_t vof = ((uint32_t)j * kC + h) * sizeof(TS);
+    const uint32_t vof = ((uint32_t)j * kC + p0) * sizeof(TS);
 #pragma unroll
     for (int r = 0; r < kNV; ++r) {
       const char* vb = reinterpret_cast<const char*>(Vp + r * os);
       X.v0[r] = *reinterpret_cast<const TS*>(vb + vof);
-      X.v1[r] = *reinterpret_cast<const TS*>(vb + vof + kH * sizeof(TS));
+      X.v1[r] = *reinterpret_cast<const TS*>(vb + vof + kSlH * sizeof(TS));
     }
-    const float* tb = R.tab + er_toff[el - c0] + h;
+    // slice-s table: gate of head hh in column hh, inputhead in column 16 + hh; rows 0..3 at the two nodes
+    const float* tb = R.tab + er_toff[sl] + hh;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      X.tg[q] = tb[q * kTabC];
-      X.tg[4 + q] = tb[(4 + q) * kTabC];
-      X.ti[q] = tb[q * kTabC + kH];
-      X.ti[4 + q] = tb[(4 + q) * kTabC + kH];
+      X.tg[q] = tb[q * kSlC];
+      X.tg[4 + q] = tb[(4 + q) * kSlC];
+      X.ti[q] = tb[q * kSlC + kSlH];
+      X.ti[4 + q] = tb[(4 + q) * kSlC + kSlH];
     }
   };
-  auto apply = [&](int el, int slot, const L& X) {
-    const int64_t e = (int64_t)b + el;
-    const float4 ea = er_a[slot], eb = er_b[slot];
+  auto apply = [&](int sl, const L& X) {
+    const int64_t e = (int64_t)b + c0 + sl;
+    const float4 ea = er_a[sl], eb = er_b[sl];
     const float pe = ea.x, dpe = ea.y, rR = ea.z, d = ea.w;
     const float dvx = eb.x, dvy = eb.y, dvz = eb.z;
-    const Hermite5 Hw = hermite5(er_t[slot]);
+    Hermite5 Hw;
+    Hw.a0 = er_hw[0][sl]; Hw.a1 = er_hw[1][sl]; Hw.a2 = er_hw[2][sl];
+    Hw.b0 = er_hw[3][sl]; Hw.b1 = er_hw[4][sl]; Hw.b2 = er_hw[5][sl];
     const float gate = herm_value(Hw, X.tg[0], X.tg[1], X.tg[2], X.tg[4], X.tg[5], X.tg[6]);
     const float ih = herm_value(Hw, X.ti[0], X.ti[1], X.ti[2], X.ti[4], X.ti[5], X.ti[6]);
     const float gate_d = herm_value(Hw, X.tg[1], X.tg[2], X.tg[3], X.tg[5], X.tg[6], X.tg[7]) * R.inv_h;
@@ -774,7 +883,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
     for (int q = 0; q < kD; ++q) kf[q] = f32(X.k[q]);
     const float qk = half_dot(qs, kf) + half_dot(qs + 4, kf + 4);
     const float a = gate * qk;
-    const float ex = expf(a - m);
+    const float ex = fexp(a - m);
     const float ee = ex * pe;
     const float alpha = (ee * ih) * inv;
     const float w = alpha * rR;
@@ -804,71 +913,98 @@ __global__ __launch_bounds__(256) void k_attn_bwd_row_hp(e2v2_attn_args A, const
     for (int q = 0; q < kD; ++q) dqa[q] = fmaf(dqk, kf[q], dqa[q]);
     // dL/dd of this head: envelope, 1/d, and the profile (dL/dgate gate' + dL/dih ih')
     const float ddh = fmaf(da * qk, gate_d, fmaf(dih, ih_d, fmaf(dpv, dpe, dR)));
-    // sums over the 64 heads of this wave; lane 16k holds the sum of value k
-    const float sum = wave_sum4(w * U[0], w * U[1], w * U[2], ddh, lane);
-    if ((lane & 15) == 0) part[slot][wsub][lane >> 4] = sum;
+    // sums over the slice's 16 heads (this row of 16 lanes); quad q holds value q
+    const float sum = row_sum4(w * U[0], w * U[1], w * U[2], ddh, lane);
+    if ((lane & 3) == 0) part[((size_t)s * A.n_edges + e) * 4 + (hh >> 2)] = sum;
   };
-  for (c0 = 0; c0 < n; c0 += 2 * CH) {
-    const int nc = min(2 * CH, n - c0);
-    if (t < nc) {
-      const int64_t e = (int64_t)b + c0 + t;
+  for (c0 = 0; c0 < n; c0 += CH) {
+    const int nc = min(CH, n - c0);
+    if (lane < nc) {
+      const int64_t e = (int64_t)b + c0 + lane;
       const float d = A.dist[e];
       float pe, dpe;
       env.eval(d, pe, dpe);
-      er_a[t] = make_float4(pe, dpe, 1.0f / fmaxf(d, 1e-6f), d);
+      er_a[lane] = make_float4(pe, dpe, 1.0f / fmaxf(d, 1e-6f), d);
       const int j = A.col[e];
-      er_b[t] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], __int_as_float(j));
+      er_b[lane] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], __int_as_float(j));
       float tt;
-      er_toff[t] = radial_node(R, ti * R.n_types + A.atom_type[j], d, tt);
-      er_t[t] = tt;
+      er_toff[lane] = radial_node_sliced(R, ti * R.n_types + A.atom_type[j], s, kSl, kSlC, d, tt);
+      const Hermite5 Hw = hermite5(tt);
+      er_hw[0][lane] = Hw.a0; er_hw[1][lane] = Hw.a1; er_hw[2][lane] = Hw.a2;
+      er_hw[3][lane] = Hw.b0; er_hw[4][lane] = Hw.b1; er_hw[5][lane] = Hw.b2;
     }
     __syncthreads();
     {
+      // the 16 lanes of a row share their edges (sub), so the row sums see whole rows
       L Xa, Xb;
-      int el = par;
+      int el = sub;
       if (el < nc) {
-        issue(c0 + el, Xa);
-        for (; el + 4 < nc; el += 4) {
-          issue(c0 + el + 2, Xb);
-          apply(c0 + el, el, Xa);
-          issue(c0 + el + 4, Xa);
-          apply(c0 + el + 2, el + 2, Xb);
+        issue(el, Xa);
+        for (; el + 8 < nc; el += 8) {
+          issue(el + 4, Xb);
+          apply(el, Xa);
+          issue(el + 8, Xa);
+          apply(el + 4, Xb);
         }
-        if (el + 2 < nc) {
-          issue(c0 + el + 2, Xb);
-          apply(c0 + el, el, Xa);
-          apply(c0 + el + 2, el + 2, Xb);
+        if (el + 4 < nc) {
+          issue(el + 4, Xb);
+          apply(el, Xa);
+          apply(el + 4, Xb);
         } else {
-          apply(c0 + el, el, Xa);
+          apply(el, Xa);
         }
       }
     }
     __syncthreads();
-    if (t < nc) {
-      const int64_t e = (int64_t)b + c0 + t;
-      ddv[3 * e] = part[t][0][0] + part[t][1][0];
-      ddv[3 * e + 1] = part[t][0][1] + part[t][1][1];
-      ddv[3 * e + 2] = part[t][0][2] + part[t][1][2];
-      dd[e] = part[t][0][3] + part[t][1][3];
-    }
-    __syncthreads();
   }
-  if (par) {
+  // dq of head h: the four subs added in a fixed order
 #pragma unroll
-    for (int q = 0; q < kD; ++q) dq_s[h][q] = dqa[q];
+  for (int q = 0; q < kD; ++q) {
+    dqa[q] += __shfl_xor(dqa[q], 16, kWave);
+    dqa[q] += __shfl_xor(dqa[q], 32, kWave);
   }
-  __syncthreads();
-  if (!par) {
+  if (sub == 0) {
 #pragma unroll
-    for (int q = 0; q < kD; ++q) dq[((size_t)i * kH + h) * kD + q] = (dqa[q] + dq_s[h][q]) / A.q_div;
+    for (int q = 0; q < kD; ++q) dq[((size_t)i * kH + h) * kD + q] = dqa[q] / A.q_div;
   }
+}
+
+// dL/d dvec and dL/dd of every edge: the 8 slices' partials part[s][e] added in slice order.
+__global__ __launch_bounds__(256) void k_edge_part_sum(const float4* __restrict__ part, int64_t n_edges,
+                                                       float* __restrict__ ddv, float* __restrict__ dd) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n_edges) return;
+  float4 a = part[e];
+#pragma unroll
+  for (int s = 1; s < kSl; ++s) {
+    const float4 q = part[(int64_t)s * n_edges + e];
+    a.x += q.x; a.y += q.y; a.z += q.z; a.w += q.w;
+  }
+  ddv[3 * e] = a.x;
+  ddv[3 * e + 1] = a.y;
+  ddv[3 * e + 2] = a.z;
+  dd[e] = a.w;
 }
 
 }  // namespace e2v2
 
 using namespace e2v2;
 
-static int check_table(const e2v2_attn_args& A, const char* who);
+static int check_table(const e2v2_attn_args& A, const char* who) {
+  E2V2_REQUIRE(A.rtab && A.atom_type && A.n_types >= 1 && A.n_types <= E2V2_MAX_TYPES && A.rtab_n >= 2 &&
+                   A.rtab_h > 0.f,
+               "%s: needs the fc_easy table and atom types (n_types %d, rtab_n %d)", who, A.n_types, A.rtab_n);
+  E2V2_REQUIRE((double)A.rc * (1.0 / A.rtab_h) <= (double)(A.rtab_n - 1),
+               "%s: table of %d nodes (h %g) does not cover the cutoff %g", who, A.rtab_n, (double)A.rtab_h,
+               (double)A.rc);
+  // one wavefront per (row, slice): the grid holds 8 n_rows workgroups
+  E2V2_REQUIRE(A.n_rows < (1 << 27), "%s: %d rows exceed the slice grid", who, A.n_rows);
+  // the forward and the row pass gather k_j and v_j through 32-bit byte offsets (v: all 9 rows)
+  E2V2_REQUIRE((uint64_t)A.n_rows * kH * kD * (A.act_bf16 ? 2 : 4) < (1ull << 32) &&
+                   (uint64_t)A.n_rows * kNV * kC * (A.act_bf16 ? 2 : 4) < (1ull << 32),
+               "%s: %d rows exceed the 32-bit gather offsets", who, A.n_rows);
+  return 0;
+}
 
 E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, float* srow, int32_t* cnt,
                            hipStream_t s) {
@@ -878,63 +1014,74 @@ E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, f
                A.channels);
   if (A.n_rows == 0) return 0;
   if (int rc = check_table(A, "attn_fwd")) return rc;
-  const dim3 grid(xcd_grid(A.n_rows));
+  const dim3 grid((unsigned)A.n_rows * kSl);
   if (A.act_bf16) {
-    hipLaunchKernelGGL(k_attn_fwd<__bf16>, grid, dim3(256), 0, s, A, static_cast<__bf16*>(out), mrow, srow, cnt);
+    hipLaunchKernelGGL(k_attn_fwd_sl<__bf16>, grid, dim3(kWave), 0, s, A, static_cast<__bf16*>(out), mrow, srow,
+                       cnt);
   } else {
-    hipLaunchKernelGGL(k_attn_fwd<float>, grid, dim3(256), 0, s, A, static_cast<float*>(out), mrow, srow, cnt);
+    hipLaunchKernelGGL(k_attn_fwd_sl<float>, grid, dim3(kWave), 0, s, A, static_cast<float*>(out), mrow, srow, cnt);
   }
-  E2V2_LAUNCHED("k_attn_fwd");
+  E2V2_LAUNCHED("k_attn_fwd_sl");
   return 0;
+}
+
+// workspace of e2v2_attn_bwd: w [E][H] and dL/dqk [E][H] handed from the row pass to the column pass, and the
+// slice partials of dL/d dvec, dL/dd [8][E][4]
+static size_t bwd_ws_floats(int64_t n_edges) { return (size_t)n_edges * (2 * kH + 4 * kSl); }
+
+E2V2_API size_t e2v2_attn_bwd_workspace(int64_t n_edges) {
+  return n_edges > 0 ? bwd_ws_floats(n_edges) * sizeof(float) : 0;
 }
 
 template <typename TS>
 static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, const float* mrow, const float* srow,
                            const int32_t* cnt, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
-                           float* w_edge, float* dqk_edge, hipStream_t s) {
-  const dim3 grid(xcd_grid(A.n_rows));
-  hipLaunchKernelGGL(k_attn_bwd_row_hp<TS>, grid, dim3(256), 0, s, A, G, O, mrow, srow, cnt, ddvec, ddist, dq,
-                     w_edge, dqk_edge);
-  E2V2_LAUNCHED("k_attn_bwd_row");
+                           float* ws, hipStream_t s) {
+  const int64_t E = A.n_edges;
+  float* w_edge = ws;
+  float* dqk_edge = ws + (size_t)E * kH;
+  float* part = ws + (size_t)E * 2 * kH;
+  hipLaunchKernelGGL(k_attn_bwd_row_sl<TS>, dim3((unsigned)A.n_rows * kSl), dim3(kWave), 0, s, A, G, O, mrow, srow,
+                     cnt, part, dq, w_edge, dqk_edge);
+  E2V2_LAUNCHED("k_attn_bwd_row_sl");
   if (A.col_slot_member) {
     const int n_cl = (A.n_rows + 3) / 4;
     hipLaunchKernelGGL((k_attn_bwd_col_grp<4, TS>), dim3(xcd_grid(n_cl) * kGroups), dim3(256), 0, s, A, G, w_edge,
                        dqk_edge, dv, dk);
   } else if constexpr (sizeof(TS) == 2) {
-    hipLaunchKernelGGL(k_attn_bwd_col_pair<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
+    hipLaunchKernelGGL(k_attn_bwd_col_pair<TS>, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_edge, dqk_edge,
+                       dv, dk);
   } else {
-    hipLaunchKernelGGL(k_attn_bwd_col_ch<TS>, grid, dim3(256), 0, s, A, G, w_edge, dqk_edge, dv, dk);
+    hipLaunchKernelGGL(k_attn_bwd_col_ch<TS>, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_edge, dqk_edge, dv,
+                       dk);
   }
   E2V2_LAUNCHED("k_attn_bwd_col");
-  return 0;
-}
-
-static int check_table(const e2v2_attn_args& A, const char* who) {
-  E2V2_REQUIRE(A.rtab && A.atom_type && A.n_types >= 1 && A.n_types <= E2V2_MAX_TYPES && A.rtab_n >= 2 &&
-                   A.rtab_h > 0.f,
-               "%s: needs the fc_easy table and atom types (n_types %d, rtab_n %d)", who, A.n_types, A.rtab_n);
-  E2V2_REQUIRE((double)A.rc * (1.0 / A.rtab_h) <= (double)(A.rtab_n - 1),
-               "%s: table of %d nodes (h %g) does not cover the cutoff %g", who, A.rtab_n, (double)A.rtab_h,
-               (double)A.rc);
+  if (E > 0) {
+    hipLaunchKernelGGL(k_edge_part_sum, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<const float4*>(part), E, ddvec, ddist);
+    E2V2_LAUNCHED("k_edge_part_sum");
+  }
   return 0;
 }
 
 E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, const void* out, const float* mrow,
                            const float* srow, const int32_t* cnt, float* ddvec, float* ddist, float* dq, float* dk,
-                           float* dv, float* w_edge, float* dqk_edge, hipStream_t s) {
+                           float* dv, void* workspace, size_t workspace_bytes, hipStream_t s) {
   const e2v2_attn_args& A = *args;
   E2V2_REQUIRE(A.n_heads == kH && A.head_dim == kD && A.channels == kC,
                "attn_bwd: built for H=%d D=%d C=%d", kH, kD, kC);
   E2V2_REQUIRE(!A.col_slot_member || (A.col_span == 4 && A.col_slot_edge && A.col_n_slots),
                "attn_bwd: column clusters need span 4 and all three slot arrays (span %d)", A.col_span);
   if (A.n_rows == 0) return 0;
-  // the row pass gathers k_j and v_j through 32-bit byte offsets within one row block
-  E2V2_REQUIRE((uint64_t)A.n_rows * kH * kD * (A.act_bf16 ? 2 : 4) < (1ull << 32),
-               "attn_bwd: %d rows exceed the 32-bit gather offsets of the row pass", A.n_rows);
   if (int rc = check_table(A, "attn_bwd")) return rc;
+  const size_t need = e2v2_attn_bwd_workspace(A.n_edges);
+  E2V2_REQUIRE(workspace_bytes >= need && (need == 0 || workspace) &&
+                   reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "attn_bwd: workspace of %zu bytes (16-byte aligned) needed, got %zu", need, workspace_bytes);
+  float* ws = static_cast<float*>(workspace);
   if (A.act_bf16)
     return attn_bwd_launch(A, static_cast<const __bf16*>(grad_out), static_cast<const __bf16*>(out), mrow, srow,
-                           cnt, ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
+                           cnt, ddvec, ddist, dq, dk, dv, ws, s);
   return attn_bwd_launch(A, static_cast<const float*>(grad_out), static_cast<const float*>(out), mrow, srow, cnt,
-                         ddvec, ddist, dq, dk, dv, w_edge, dqk_edge, s);
+                         ddvec, ddist, dq, dk, dv, ws, s);
 }

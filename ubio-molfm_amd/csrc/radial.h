@@ -47,6 +47,16 @@ __device__ __forceinline__ int64_t radial_node(const RadialTab& R, int pair, flo
   return ((int64_t)pair * R.n_nodes + (int64_t)fn) * (4 * R.nc);
 }
 
+// Offset (floats) of node n of the interval holding d for pair p in a slice-major
+// table ([pairs][n_slices][nodes][4][w]) of slice `slice`, and the fraction t.
+__device__ __forceinline__ int64_t radial_node_sliced(const RadialTab& R, int pair, int slice, int n_slices, int w,
+                                                      float d, float& t) {
+  const float u = fminf(d * R.inv_h, (float)(R.n_nodes - 2));
+  const float fn = floorf(u);
+  t = u - fn;
+  return (((int64_t)pair * n_slices + slice) * R.n_nodes + (int64_t)fn) * (4 * w);
+}
+
 // Interpolated value of channel c from its six node rows (f0, f1, f2 at n and at n + 1)
 __device__ __forceinline__ float herm_value(const Hermite5& H, float f0, float f1, float f2, float g0, float g1,
                                             float g2) {

@@ -193,6 +193,18 @@ __device__ void profile_jets(const e2v2_radial_net& W, const float* __restrict__
   __syncthreads();
 }
 
+// Table position of output channel o of a profile (e2v2_radial_layout)
+__device__ __forceinline__ int layout_pos(const e2v2_radial_layout& Lo, int o) {
+  return Lo.col0 + ((o % Lo.split) / Lo.block) * Lo.block_stride + (o / Lo.split) * Lo.split_stride + o % Lo.block;
+}
+// Index of (pair p, node n, row k, channel position pos) in a table of nc positions per row
+__device__ __forceinline__ int64_t tab_index(const e2v2_radial_layout& Lo, int p, int n_nodes, int n, int k, int nc,
+                                             int pos) {
+  if (Lo.slice_width == 0) return (((int64_t)p * n_nodes + n) * 4 + k) * nc + pos;
+  const int w = Lo.slice_width, ns = nc / w;
+  return ((((int64_t)p * ns + pos / w) * n_nodes + n) * 4 + k) * w + pos % w;
+}
+
 // Rows h^k f^(k) = h^k k! c_k of the jets
 __device__ __forceinline__ void jet_rows(const Jet& y, double h, double (&r)[4]) {
   r[0] = y.c[0];
@@ -201,22 +213,22 @@ __device__ __forceinline__ void jet_rows(const Jet& y, double h, double (&r)[4])
   r[3] = h * h * h * 6.0 * y.c[3];
 }
 
-// one block per (node, pair); writes channels [col0, col0 + 256) of rows k = 0..3
+// one block per (node, pair); writes the profile's 256 channels of rows k = 0..3 at their layout positions
 __global__ __launch_bounds__(kRH) void k_radial_table(e2v2_radial_net W, const float* __restrict__ mu, double coeff,
                                                       const int32_t* __restrict__ type_z, int n_types, int n_nodes,
-                                                      double h, float* __restrict__ tab, int nc, int col0) {
+                                                      double h, float* __restrict__ tab, int nc,
+                                                      e2v2_radial_layout Lo) {
   const int n = blockIdx.x, p = blockIdx.y;
   const int za = type_z[p / n_types], zb = type_z[p % n_types];
   Jet y[2];
   profile_jets(W, mu, coeff, za, zb, (double)n * h, y);
-  float* base = tab + ((int64_t)p * n_nodes + n) * (4 * nc) + col0;
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
     double r[4];
     jet_rows(y[hh], h, r);
-    const int o = threadIdx.x + hh * kRH;
+    const int o = layout_pos(Lo, threadIdx.x + hh * kRH);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) base[k * nc + o] = (float)r[k];
+    for (int k = 0; k < 4; ++k) tab[tab_index(Lo, p, n_nodes, n, k, nc, o)] = (float)r[k];
   }
 }
 
@@ -225,22 +237,25 @@ __global__ __launch_bounds__(kRH) void k_radial_table(e2v2_radial_net W, const f
 // floats order like their bit patterns, so the unsigned atomic max is exact and deterministic).
 __global__ __launch_bounds__(kRH) void k_radial_check(e2v2_radial_net W, const float* __restrict__ mu, double coeff,
                                                       const int32_t* __restrict__ type_z, int n_types, int n_nodes,
-                                                      double h, const float* __restrict__ tab, int nc, int col0,
-                                                      uint32_t* __restrict__ err) {
+                                                      double h, const float* __restrict__ tab, int nc,
+                                                      e2v2_radial_layout Lo, uint32_t* __restrict__ err) {
   const int n = blockIdx.x, p = blockIdx.y;
   const int za = type_z[p / n_types], zb = type_z[p % n_types];
   Jet y[2];
   profile_jets(W, mu, coeff, za, zb, ((double)n + 0.5) * h, y);
-  const float* A = tab + ((int64_t)p * n_nodes + n) * (4 * nc) + col0;
-  const float* B = A + 4 * nc;
   const Hermite5 H = hermite5(0.5f);
   float e_v = 0.f, m_v = 0.f, e_d = 0.f, m_d = 0.f;
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
-    const int o = threadIdx.x + hh * kRH;
-    const float v = herm_value(H, A[o], A[nc + o], A[2 * nc + o], B[o], B[nc + o], B[2 * nc + o]);
-    const float dv = herm_value(H, A[nc + o], A[2 * nc + o], A[3 * nc + o], B[nc + o], B[2 * nc + o],
-                                B[3 * nc + o]);
+    const int o = layout_pos(Lo, threadIdx.x + hh * kRH);
+    float a[4], b[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a[k] = tab[tab_index(Lo, p, n_nodes, n, k, nc, o)];
+      b[k] = tab[tab_index(Lo, p, n_nodes, n + 1, k, nc, o)];
+    }
+    const float v = herm_value(H, a[0], a[1], a[2], b[0], b[1], b[2]);
+    const float dv = herm_value(H, a[1], a[2], a[3], b[1], b[2], b[3]);
     e_v = fmaxf(e_v, (float)fabs((double)v - y[hh].c[0]));
     m_v = fmaxf(m_v, (float)fabs(y[hh].c[0]));
     e_d = fmaxf(e_d, (float)fabs((double)dv - h * y[hh].c[1]));
@@ -287,29 +302,49 @@ E2V2_API int e2v2_radial_table_size(float rc, float rbf_coeff, int32_t refine, i
   return 0;
 }
 
+// Every output channel of the profile lands inside the row, at a distinct position.
+static int check_layout(const e2v2_radial_layout* Lo, int32_t nc, const char* who) {
+  E2V2_REQUIRE(Lo, "%s: no channel layout", who);
+  E2V2_REQUIRE(nc >= kRO && nc <= 4 * kRO && Lo->split >= 1 && kRO % Lo->split == 0 && Lo->block >= 1 &&
+                   Lo->split % Lo->block == 0 && Lo->col0 >= 0 && Lo->block_stride >= 0 && Lo->split_stride >= 0 &&
+                   Lo->slice_width >= 0 && (Lo->slice_width == 0 || nc % Lo->slice_width == 0),
+               "%s: bad channel layout (nc %d, col0 %d, split %d, block %d, slice width %d)", who, nc, Lo->col0,
+               Lo->split, Lo->block, Lo->slice_width);
+  uint64_t used[4 * kRO / 64] = {};
+  for (int o = 0; o < kRO; ++o) {
+    const int64_t p = (int64_t)Lo->col0 + (int64_t)((o % Lo->split) / Lo->block) * Lo->block_stride +
+                      (int64_t)(o / Lo->split) * Lo->split_stride + o % Lo->block;
+    E2V2_REQUIRE(p >= 0 && p < nc, "%s: channel %d maps to position %lld outside rows of %d", who, o, (long long)p,
+                 nc);
+    E2V2_REQUIRE(!((used[p / 64] >> (p % 64)) & 1), "%s: two channels map to position %lld", who, (long long)p);
+    used[p / 64] |= 1ull << (p % 64);
+  }
+  return 0;
+}
+
 E2V2_API int e2v2_radial_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
                                const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h, float* tab,
-                               int32_t nc, int32_t col0, hipStream_t s) {
+                               int32_t nc, const e2v2_radial_layout* layout, hipStream_t s) {
   if (int rc = check_net(net, "radial_table")) return rc;
   E2V2_REQUIRE(rbf_offset && type_z && tab && n_types >= 1 && n_types <= E2V2_MAX_TYPES && n_nodes >= 2 && h > 0.f,
                "radial_table: bad arguments (n_types %d, n_nodes %d)", n_types, n_nodes);
-  E2V2_REQUIRE(nc % kRO == 0 && col0 % kRO == 0 && col0 + kRO <= nc,
-               "radial_table: channel block [%d, %d) outside rows of %d", col0, col0 + kRO, nc);
+  if (int rc = check_layout(layout, nc, "radial_table")) return rc;
   hipLaunchKernelGGL(k_radial_table, dim3((unsigned)n_nodes, (unsigned)(n_types * n_types)), dim3(kRH), 0, s, *net,
-                     rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, col0);
+                     rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, *layout);
   E2V2_LAUNCHED("k_radial_table");
   return 0;
 }
 
 E2V2_API int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
                                      const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h,
-                                     const float* tab, int32_t nc, int32_t col0, uint32_t* err, hipStream_t s) {
+                                     const float* tab, int32_t nc, const e2v2_radial_layout* layout, uint32_t* err,
+                                     hipStream_t s) {
   if (int rc = check_net(net, "radial_table_check")) return rc;
   E2V2_REQUIRE(rbf_offset && type_z && tab && err && n_types >= 1 && n_types <= E2V2_MAX_TYPES && n_nodes >= 2,
                "radial_table_check: bad arguments");
-  E2V2_REQUIRE(nc % kRO == 0 && col0 % kRO == 0 && col0 + kRO <= nc, "radial_table_check: bad channel block");
+  if (int rc = check_layout(layout, nc, "radial_table_check")) return rc;
   hipLaunchKernelGGL(k_radial_check, dim3((unsigned)(n_nodes - 1), (unsigned)(n_types * n_types)), dim3(kRH), 0, s,
-                     *net, rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, col0, err);
+                     *net, rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, *layout, err);
   E2V2_LAUNCHED("k_radial_check");
   return 0;
 }

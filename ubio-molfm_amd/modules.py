@@ -91,6 +91,23 @@ def cached(owner, name: str, params, build):
     return ent[1]
 
 
+_SLICE_PERM = {}
+
+
+def slice_perm(device) -> torch.Tensor:
+    """Channel order of the attention kernels (the header's slice order): the
+    model channel held at each position p of a v / output row, P[p].  Position p
+    belongs to head h = 16 (p // 32) + p % 16 and holds its first channel (h)
+    for p % 32 < 16, its second (128 + h) otherwise, so the 16 heads of slice
+    s = p // 32 occupy one contiguous 32-channel run."""
+    key = str(device)
+    if key not in _SLICE_PERM:
+        p = np.arange(256)
+        h = 16 * (p // 32) + p % 16
+        _SLICE_PERM[key] = torch.as_tensor(np.where(p % 32 < 16, h, 128 + h), device=device)
+    return _SLICE_PERM[key]
+
+
 def gemm_weight(mod, name: str, bf16: bool):
     """A module's weight as a GEMM operand: the parameter itself in fp32 mode,
     a cached bf16 copy in bf16 mode."""
@@ -756,10 +773,16 @@ class SO2_TP_givenl2(nn.Module):
             scale[t0:t1] = r[0]
         return torch.from_numpy(scale)
 
-    def folded_blocks(self, bf16: bool = False):
+    def folded_blocks(self, bf16: bool = False, sliced: bool = False):
         """Per output l3: list of (input row start, rows, W_p^T) with path_norm and
         loaded CG_weight path scales folded into W_p (cached on versions); bf16
-        copies of the folded blocks in bf16 mode."""
+        copies of the folded blocks in bf16 mode.  ``sliced``: the rows of W_p^T
+        permuted to the attention kernels' slice order of the input channels."""
+        if sliced:
+            def build_sliced():
+                P = slice_perm(self.path_norm.device)
+                return [[(t0, nr, Wt[P].contiguous()) for (t0, nr, Wt) in lst] for lst in self.folded_blocks(bf16)]
+            return cached(self, "fold_sl_bf16" if bf16 else "fold_sl", list(self.parameters()), build_sliced)
         if bf16:
             return cached(self, "fold_bf16", list(self.parameters()),
                           lambda: [[(t0, nr, Wt.to(BF16).contiguous()) for (t0, nr, Wt) in lst]
@@ -869,8 +892,21 @@ class E2AttentionArbOrder_sparse(nn.Module):
         w, b = cached(self, "qk", params, build)
         return mrow_weight(self, "qk", w, bf16, self.lmax), b
 
+    def value_weights_sliced(self):
+        """proj_value's weight and bias with the output channels in the attention
+        kernels' slice order (cached per weight version)."""
+        pv = self.proj_value
+
+        def build():
+            P = slice_perm(pv.weight.device)
+            return pv.weight.detach()[:, P, :].contiguous(), pv.bias.detach()[P].contiguous()
+        return cached(self, "v_sliced", (pv.weight, pv.bias), build)
+
     def forward(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
-        """x [9, N, C] (m-major) -> attention(x) (+ res when given), [9, N, C]."""
+        """x [9, N, C] (m-major) -> attention(x) (+ res when given), [9, N, C].
+        v, the attention rows and their gradients run in the kernels' slice order
+        of channels: the permutation is folded into proj_value (output rows) and
+        forward_linear (input rows), so the layer's output is in model order."""
         N = x.shape[1]
         H = self.num_attn_heads
         if self.training and self.alpha_dropout.p > 0:
@@ -879,20 +915,20 @@ class E2AttentionArbOrder_sparse(nn.Module):
         W, b = self.qk_weights(bf16)
         hid = self.query_linear.weight.shape[1]
         pv = self.proj_value  # its GEMMs run inside QKProjFn (one input gradient)
+        wv, bv = self.value_weights_sliced()
         with record_function("query key linear function"):
-            hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight", pv.weight, bf16, pv.lmax),
-                                       pv.bias.detach())
+            hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight_sl", wv, bf16, pv.lmax), bv)
             q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
             k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         with record_function("rbf function-a"):   # fc_easy as a distance table, built once per weight version
             table = self._radial.get([self.fc_easy.net], self.target_embedding, self.source_embedding,
-                                     ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key)
+                                     ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="attn")
         with record_function("qk attention"):
             so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table, ctx.rc,
                                     math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
         pf = self.proj_first
         with record_function("first-order"):
-            return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16),
+            return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16, sliced=True),
                                   mrow_weight(pf, "weight", pf.weight, bf16, pf.lmax), pf.bias.detach())
 
 

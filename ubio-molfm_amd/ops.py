@@ -52,12 +52,28 @@ class RadialTable:
     (e2v2_radial_table), then checked at every interval midpoint against the
     float64 profile (e2v2_radial_table_check); the node spacing is halved until
     the interpolation error is at most ``tol_value`` of the largest |f| and
-    ``tol_deriv`` of the largest |f'| (one host readback per build)."""
+    ``tol_deriv`` of the largest |f'| (one host readback per build).
+
+    ``layout`` places the channels: "plain" (rows [pairs][nodes][4][nc], profile
+    m at 256 m + c), "attn" (one fc_easy profile in the attention kernels' slice
+    order, gate and inputhead of head h at 32 (h // 16) + h % 16 and 16 positions
+    on, stored slice-major [pairs][8][nodes][4][32]) or "deg" (three profiles,
+    channel c of profile l at 96 (c // 32) + 32 l + c % 32)."""
+
+    LAYOUTS = {
+        "plain": lambda m: (256 * m, 256, 256, 0, 0, 0),
+        "attn": lambda m: (0, 128, 16, 32, 16, 32),
+        "deg": lambda m: (32 * m, 256, 32, 96, 0, 0),
+    }
 
     def __init__(self, nets, tgt: nn.Embedding, src: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
                  rc: float, type_z: torch.Tensor, tol_value: float = 1e-6, tol_deriv: float = 1e-5,
-                 max_refine: int = 3):
+                 max_refine: int = 3, layout: str = "plain"):
         dev = type_z.device
+        if layout not in self.LAYOUTS or (layout == "attn" and len(nets) != 1) or (layout == "deg" and len(nets) != 3):
+            raise ValueError(f"radial table layout {layout!r} does not fit {len(nets)} profiles")
+        self.layout = layout
+        self._layouts = [_lib.RadialLayout(*self.LAYOUTS[layout](m)) for m in range(len(nets))]
         self.nc = 256 * len(nets)
         self.n_types = int(type_z.numel())
         if self.n_types < 1 or self.n_types > MAX_TYPES:
@@ -78,8 +94,9 @@ class RadialTable:
             for m, W in enumerate(self._structs):
                 args = (_lib.C.byref(W), _p(mu), _lib.f32(rbf_coeff), _p(self.type_z), _lib.i32(self.n_types),
                         _lib.i32(self.n_nodes), _lib.f32(self.h))
-                _lib.call("e2v2_radial_table", *args, _p(self.tab), _lib.i32(self.nc), _lib.i32(256 * m), st)
-                _lib.call("e2v2_radial_table_check", *args, _p(self.tab), _lib.i32(self.nc), _lib.i32(256 * m),
+                lo = _lib.C.byref(self._layouts[m])
+                _lib.call("e2v2_radial_table", *args, _p(self.tab), _lib.i32(self.nc), lo, st)
+                _lib.call("e2v2_radial_table_check", *args, _p(self.tab), _lib.i32(self.nc), lo,
                           _lib.vp(err[m].data_ptr()), st)
             e = err.cpu().view(torch.float32).double()
             self.value_err = float((e[:, 0] / e[:, 1].clamp_min(1e-30)).max())
@@ -125,12 +142,12 @@ class RadialCache:
         self.table: Optional[RadialTable] = None
 
     def get(self, nets, tgt_emb: nn.Embedding, src_emb: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
-            rc: float, type_z: torch.Tensor, type_key: tuple):
+            rc: float, type_z: torch.Tensor, type_key: tuple, layout: str = "plain"):
         params = [p for n in nets for p in n.parameters()] + [tgt_emb.weight, src_emb.weight, rbf_offset]
-        key = (_version_key(params), float(rbf_coeff), float(rc), type_key)
+        key = (_version_key(params), float(rbf_coeff), float(rc), type_key, layout)
         if key != self.key:
             self.table = None
-            self.table = RadialTable(nets, tgt_emb, src_emb, rbf_offset, rbf_coeff, rc, type_z)
+            self.table = RadialTable(nets, tgt_emb, src_emb, rbf_offset, rbf_coeff, rc, type_z, layout=layout)
             self.key = key
         return self.table
 
@@ -200,8 +217,8 @@ def deg_args(nl: NeighborList, atom_type: torch.Tensor, table: RadialTable, avg:
 
 def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: float, rc: float, bf: int):
     """e2v2_attn_args over the neighbour list (with its column clusters when built)."""
-    if table.nc != 256:
-        raise ValueError("the attention needs the table of its fc_easy profile (256 channels)")
+    if table.nc != 256 or table.layout != "attn":
+        raise ValueError("the attention needs the table of its fc_easy profile in slice order (layout 'attn')")
     a = _lib.AttnArgs(nl.n_atoms, nl.n_edges, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(),
                       nl.edge_row.data_ptr(), nl.key_ptr.data_ptr(), nl.key_eid.data_ptr(), nl.dvec.data_ptr(),
                       nl.dist.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.tab.data_ptr(),
@@ -219,7 +236,8 @@ class AttentionFn(torch.autograd.Function):
     """Edge part of E2AttentionArbOrder_sparse.forward (e2former.py:238-433) up to
     the SO(2) product's forward_linear: returns the 20-row l3-sequential tensor
     h_a - h_b of so2_tensor_product.py:385 for every query atom, m-major
-    [20, N, 256]; q, k [N, 128, 8], v [9, N, 256].  gate and inputhead
+    [20, N, 256]; q, k [N, 128, 8], v [9, N, 256], the channels of v and of the
+    output in the kernels' slice order (modules.slice_perm).  gate and inputhead
     (fc_easy, e2former.py:258-306) are interpolated from the layer's radial table
     inside the kernels: only node-level tensors are saved."""
 
@@ -258,10 +276,11 @@ class AttentionFn(torch.autograd.Function):
         ddv = torch.empty(max(E, 1), 3, **f)
         dd = torch.empty(max(E, 1), **f)
         dq = torch.empty(q.shape, **f); dk = torch.empty(k.shape, **f); dv = torch.empty(v.shape, **f)
-        # scratch of this call: per-edge weights and logit gradients handed from the row pass to the column pass
-        w_e = torch.empty(max(E, 1), 128, **f)
-        dqk = torch.empty(max(E, 1), 128, **f)
+        # workspace of this call (per-edge weights handed from the row pass to the column pass, per-slice
+        # partial edge gradients), freed when the call returns
+        nb = int(_lib.load().e2v2_attn_bwd_workspace(E))
+        ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
         _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(ddv),
-                  _p(dd), _p(dq), _p(dk), _p(dv), _p(w_e), _p(dqk), _stream(gout))
-        del w_e, dqk
+                  _p(dd), _p(dq), _p(dk), _p(dv), _p(ws), _lib.C.c_size_t(ws.numel()), _stream(gout))
+        del ws
         return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None
