@@ -99,7 +99,8 @@ def attn_bwd_table_bytes(E):
 
 
 def deg_fwd_bytes(N, E, act=4):
-    return 4.0 * (E * 6 + N * 9 * 256) + deg_fwd_table_bytes(E)
+    # the edge list (dvec, dist, col, source type) once per slice; write x0
+    return 4.0 * (SLICES * E * 6 + N * 9 * 256) + deg_fwd_table_bytes(E)
 
 
 def deg_fwd_table_bytes(E):
@@ -107,8 +108,8 @@ def deg_fwd_table_bytes(E):
 
 
 def deg_bwd_bytes(N, E, act=4):
-    # read dvec, dist, col, types and the node gradient; write ddvec, ddist
-    return 4.0 * (E * (6 + 4) + N * 9 * 256) + deg_bwd_table_bytes(E)
+    # read the edge list per slice and the node gradient; write the slice partials; sum them into ddvec, ddist
+    return 4.0 * (SLICES * E * 6 + N * 9 * 256 + SLICES * E * 4 + SLICES * E * 4 + E * 4) + deg_bwd_table_bytes(E)
 
 
 def deg_bwd_table_bytes(E):
@@ -138,7 +139,8 @@ PROJ_FLOPS["e2v2_qk_proj_bwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
 
 KERNELS_OF = {"e2v2_attn_fwd": ["k_attn_fwd_sl"],
               "e2v2_attn_bwd": ["k_attn_bwd_row_sl", "k_attn_bwd_col_grp", "k_edge_part_sum"],
-              "e2v2_deg_fwd": ["k_deg_fwd"], "e2v2_deg_bwd": ["k_deg_bwd"], "e2v2_nbr_count": ["k_nbr_count"],
+              "e2v2_deg_fwd": ["k_deg_fwd_sl"], "e2v2_deg_bwd": ["k_deg_bwd_sl", "k_edge_part_sum"],
+              "e2v2_nbr_count": ["k_nbr_count"],
               "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"]}
 
 

@@ -143,8 +143,9 @@ int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, i
        inputhead of head h at positions E2V2_POS0(h) and E2V2_POS1(h), stored slice-major;
        layout {col0 0, split 128, block 16, block_stride 32, split_stride 16, slice_width 32};
      degree embedding (nc = 768, profiles l = 0, 1, 2): channel c of profile l at
-       96 (c / 32) + 32 l + c % 32 (each 32-channel slice of the three profiles contiguous);
-       layout {col0 32 l, split 256, block 32, block_stride 96, split_stride 0, slice_width 0};
+       96 (c / 32) + 32 l + c % 32, stored slice-major (each 32-channel slice of the three profiles
+       contiguous); layout {col0 32 l, split 256, block 32, block_stride 96, split_stride 0,
+       slice_width 96};
      contiguous (any other caller): channel c of profile m at 256 m + c;
        layout {col0 256 m, split 256, block 256, block_stride 0, split_stride 0, slice_width 0}. */
 #define E2V2_MAX_TYPES 32
@@ -241,7 +242,7 @@ typedef struct e2v2_deg_args {
   const float* dvec;             /* [E,3]                                           */
   const float* dist;             /* [E]                                             */
   const int32_t* col;            /* [E] source atom                                 */
-  const float* rtab;             /* gbf_projs table [T*T][rtab_n][4][3C] (profiles l = 0, 1, 2) */
+  const float* rtab;             /* gbf_projs table [T*T][8][rtab_n][4][96] (slice-major, profiles l = 0, 1, 2) */
   const int32_t* atom_type;      /* [N] type slot of each atom                      */
   int32_t n_types, rtab_n;
   float rtab_h;
@@ -251,9 +252,12 @@ typedef struct e2v2_deg_args {
 
 /* x0 [9][N][C] m-major */
 int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s);
+/* Bytes of device workspace e2v2_deg_bwd needs for n_edges edges (per-slice partial edge gradients). */
+size_t e2v2_deg_bwd_workspace(int64_t n_edges);
 /* grad_x0 [9][N][C] -> ddvec [E,3], ddist [E] (spherical harmonics, envelope and the profiles' distance
-   derivative from the table) */
-int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* ddvec, float* ddist, hipStream_t s);
+   derivative from the table); workspace: e2v2_deg_bwd_workspace(E) bytes, 16-byte aligned */
+int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* ddvec, float* ddist, void* workspace,
+                 size_t workspace_bytes, hipStream_t s);
 
 /* ---- per-node kernels (node layout m-major: x[9][N][256]) --------------- */
 /* rms_norm_sh: EquivariantRMSNormArraySphericalHarmonicsV2_BL

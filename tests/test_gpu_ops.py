@@ -257,7 +257,7 @@ def test_degree_forward_backward(pkg, cuda):
     tw, sw = tgt.weight.detach().double().clone(), src.weight.detach().double().clone()
     type_z, slot = _types(pkg, cuda, s["Z"])
     tab = ops.RadialTable([p_.to(cuda).net for p_ in profs], tgt.to(cuda), src.to(cuda), rb.offset.to(cuda),
-                          rb.coeff, 6.0, type_z)
+                          rb.coeff, 6.0, type_z, layout="deg")
     st = _lib.vp(torch.cuda.current_stream().cuda_stream)
     a = ops.deg_args(nl, slot, tab, 23.01, 6.0)
     x0 = torch.empty(9, N, 256, device=cuda)
@@ -273,8 +273,10 @@ def test_degree_forward_backward(pkg, cuda):
     grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
     Gd = G.permute(1, 0, 2).contiguous().to(cuda)
     ddv = torch.empty(E, 3, device=cuda); dd = torch.empty(E, device=cuda)
+    nb = int(_lib.load().e2v2_deg_bwd_workspace(E))
+    ws = torch.empty(nb, dtype=torch.uint8, device=cuda)
     _lib.call("e2v2_deg_bwd", _lib.C.byref(a), _lib.vp(Gd.data_ptr()), _lib.vp(ddv.data_ptr()),
-              _lib.vp(dd.data_ptr()), st)
+              _lib.vp(dd.data_ptr()), _lib.vp(ws.data_ptr()), _lib.C.c_size_t(nb), st)
     errs = dict(fwd=relerr(x0.permute(1, 0, 2), ref), dvec=relerr(ddv, grads[0]), dist=relerr(dd, grads[1]))
     print(f"[deg] {errs}", flush=True)
     assert errs["fwd"] < 2e-5

@@ -17,6 +17,7 @@ EXPORTS = [
     "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_count_noalloc", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose", "e2v2_cluster_slots",
     "e2v2_morton_keys", "e2v2_radial_table_size", "e2v2_radial_table", "e2v2_radial_table_check",
     "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_attn_bwd_workspace", "e2v2_deg_fwd", "e2v2_deg_bwd",
+    "e2v2_deg_bwd_workspace",
     "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd",
     "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd", "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd",
@@ -77,6 +78,8 @@ def load():
     lib.e2v2_last_error.restype = C.c_char_p
     lib.e2v2_attn_bwd_workspace.restype = C.c_size_t
     lib.e2v2_attn_bwd_workspace.argtypes = [C.c_int64]
+    lib.e2v2_deg_bwd_workspace.restype = C.c_size_t
+    lib.e2v2_deg_bwd_workspace.argtypes = [C.c_int64]
     _lib = lib
     return lib
 

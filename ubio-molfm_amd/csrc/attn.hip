@@ -969,23 +969,6 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
   }
 }
 
-// dL/d dvec and dL/dd of every edge: the 8 slices' partials part[s][e] added in slice order.
-__global__ __launch_bounds__(256) void k_edge_part_sum(const float4* __restrict__ part, int64_t n_edges,
-                                                       float* __restrict__ ddv, float* __restrict__ dd) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= n_edges) return;
-  float4 a = part[e];
-#pragma unroll
-  for (int s = 1; s < kSl; ++s) {
-    const float4 q = part[(int64_t)s * n_edges + e];
-    a.x += q.x; a.y += q.y; a.z += q.z; a.w += q.w;
-  }
-  ddv[3 * e] = a.x;
-  ddv[3 * e + 1] = a.y;
-  ddv[3 * e + 2] = a.z;
-  dd[e] = a.w;
-}
-
 }  // namespace e2v2
 
 using namespace e2v2;
@@ -1056,12 +1039,7 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
                        dk);
   }
   E2V2_LAUNCHED("k_attn_bwd_col");
-  if (E > 0) {
-    hipLaunchKernelGGL(k_edge_part_sum, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, s,
-                       reinterpret_cast<const float4*>(part), E, ddvec, ddist);
-    E2V2_LAUNCHED("k_edge_part_sum");
-  }
-  return 0;
+  return launch_edge_part_sum(part, E, ddvec, ddist, s);
 }
 
 E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, const void* out, const float* mrow,

@@ -1,7 +1,7 @@
 // Edge-degree embedding (src/molfm/models/e2former/e2former.py:689-753) and
 // the edge -> position gradient assembly.
 //
-// Forward, one wavefront per query atom i (lane owns channels 4 lane .. + 3):
+// Forward:
 //   x0[i, m, c] = (1/avg) sum_e Y_m(dvec_e / |dvec_e|) * fea_l(m)(d_e)[c] * p(d_e)
 // with Y the e3nn raw real spherical harmonics of degree <= 2 (unit norm per
 // l block) and fea_l the three radial profiles (gbf_projs, l = 0, 1, 2) of
@@ -36,85 +36,167 @@ __device__ __forceinline__ RadialTab make_deg_tab(const e2v2_deg_args& A) {
   return R;
 }
 
-// Four consecutive channels of profile l from rows r0 .. r0 + 2 at both nodes (node block p):
-// the quintic Hermite interpolant.
+// Channel slices: slice s = 32 channels 32 s .. 32 s + 31 of every profile.  The
+// kernels run one wavefront per (query row, slice), slice = blockIdx % 8, so
+// XCD s (workgroups are dispatched round-robin over the 8 XCDs) keeps slice s of
+// the table (96 channels per row: profiles l = 0, 1, 2) in its L2.  The table is
+// stored slice-major, [pairs][8][nodes][4][96], column 32 l + u holding channel
+// 32 s + u of profile l.  Lane (sub, q) = (lane / 8, lane % 8) owns channels
+// 32 s + 4 q .. + 3 (16-byte table loads) and the row's edges sub, sub + 8, ...
+constexpr int kDSl = 8, kDSlC = kDC / kDSl, kDRow = 3 * kDSlC, kDNode = 4 * kDRow;
+
+// Four consecutive channels of one profile from rows r0 .. r0 + 2 at both nodes
+// (p: the profile's columns of the lower node): the quintic Hermite interpolant.
 __device__ __forceinline__ floatx4 deg_interp(const float* p, const Hermite5& H, int r0) {
-  const floatx4 f0 = *reinterpret_cast<const floatx4*>(p + r0 * kDegC);
-  const floatx4 f1 = *reinterpret_cast<const floatx4*>(p + (r0 + 1) * kDegC);
-  const floatx4 f2 = *reinterpret_cast<const floatx4*>(p + (r0 + 2) * kDegC);
-  const floatx4 g0 = *reinterpret_cast<const floatx4*>(p + (4 + r0) * kDegC);
-  const floatx4 g1 = *reinterpret_cast<const floatx4*>(p + (5 + r0) * kDegC);
-  const floatx4 g2 = *reinterpret_cast<const floatx4*>(p + (6 + r0) * kDegC);
+  const floatx4 f0 = *reinterpret_cast<const floatx4*>(p + r0 * kDRow);
+  const floatx4 f1 = *reinterpret_cast<const floatx4*>(p + (r0 + 1) * kDRow);
+  const floatx4 f2 = *reinterpret_cast<const floatx4*>(p + (r0 + 2) * kDRow);
+  const floatx4 g0 = *reinterpret_cast<const floatx4*>(p + kDNode + r0 * kDRow);
+  const floatx4 g1 = *reinterpret_cast<const floatx4*>(p + kDNode + (r0 + 1) * kDRow);
+  const floatx4 g2 = *reinterpret_cast<const floatx4*>(p + kDNode + (r0 + 2) * kDRow);
   floatx4 v;
 #pragma unroll
   for (int u = 0; u < 4; ++u) v[u] = herm_value(H, f0[u], f1[u], f2[u], g0[u], g1[u], g2[u]);
   return v;
 }
 
-// One wavefront per query atom; lane owns channels 4 lane .. 4 lane + 3 (16-byte
-// loads of each edge's table rows); the edge's SH, envelope and table node are
-// wave-uniform.
-constexpr int kDegWaves = 4;
+// Per-edge terms of a chunk of up to 64 edges, formed by thread-per-edge into LDS.
+struct DegChunk {
+  float Y[9][64];        // raw SH of the unit vector
+  float u[3][64];        // unit vector
+  float nrm[64];         // max(d, 1e-12)
+  float p[64], dp[64];   // envelope and its derivative
+  int64_t toff[64];      // slice-s table offset of the lower node
+  float hw[6][64];       // quintic Hermite weights of the fraction in the node interval
+};
 
-__global__ __launch_bounds__(64 * kDegWaves) void k_deg_fwd(e2v2_deg_args A, float* __restrict__ x0) {
-  const int w = (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int i = xcd_row(blockIdx.x, (A.n_rows + kDegWaves - 1) / kDegWaves) * kDegWaves + w;
-  if (i >= A.n_rows) return;
-  const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
+__device__ __forceinline__ void deg_chunk(const e2v2_deg_args& A, const Envelope& env, const RadialTab& R, int ti,
+                                          int s, int64_t e0, int nc, DegChunk& C) {
+  const int t = threadIdx.x;
+  if (t < nc) {
+    const int64_t e = e0 + t;
+    const float d = A.dist[e];
+    const float nrm = fmaxf(d, 1e-12f);
+    const float ux = A.dvec[3 * e] / nrm, uy = A.dvec[3 * e + 1] / nrm, uz = A.dvec[3 * e + 2] / nrm;
+    float Y[9];
+    raw_sh2(ux, uy, uz, Y);
+#pragma unroll
+    for (int m = 0; m < 9; ++m) C.Y[m][t] = Y[m];
+    C.u[0][t] = ux; C.u[1][t] = uy; C.u[2][t] = uz;
+    C.nrm[t] = nrm;
+    float p, dp;
+    env.eval(d, p, dp);
+    C.p[t] = p; C.dp[t] = dp;
+    float tt;
+    C.toff[t] = radial_node_sliced(R, ti * R.n_types + A.atom_type[A.col[e]], s, kDSl, kDRow, d, tt);
+    const Hermite5 H = hermite5(tt);
+    C.hw[0][t] = H.a0; C.hw[1][t] = H.a1; C.hw[2][t] = H.a2;
+    C.hw[3][t] = H.b0; C.hw[4][t] = H.b1; C.hw[5][t] = H.b2;
+  }
+}
+
+__device__ __forceinline__ Hermite5 chunk_hermite(const DegChunk& C, int el) {
+  Hermite5 H;
+  H.a0 = C.hw[0][el]; H.a1 = C.hw[1][el]; H.a2 = C.hw[2][el];
+  H.b0 = C.hw[3][el]; H.b1 = C.hw[4][el]; H.b2 = C.hw[5][el];
+  return H;
+}
+
+__device__ __forceinline__ Envelope deg_env(const e2v2_deg_args& A) {
   Envelope env;
   env.rc = A.rc; env.a = A.env_a; env.b = A.env_b; env.c = A.env_c;
+  return env;
+}
+
+// Forward: x0[m][i][c] = (1/avg) sum_e Y_m(e) p(e) fea_l(m)(e)[c]; the eight edge
+// subsets are added by lane swaps (lane ^ 8, ^ 16, ^ 32, a fixed order).
+__global__ __launch_bounds__(64) void k_deg_fwd_sl(e2v2_deg_args A, float* __restrict__ x0) {
+  constexpr int CH = 64;
+  __shared__ DegChunk C;
+  const int s = blockIdx.x % kDSl, i = blockIdx.x / kDSl;
+  if (i >= A.n_rows) return;
+  const int lane = threadIdx.x, sub = lane >> 3, q = lane & 7;
+  const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
+  const Envelope env = deg_env(A);
   const RadialTab R = make_deg_tab(A);
   const int ti = A.atom_type[i];
   floatx4 acc[9];
 #pragma unroll
   for (int m = 0; m < 9; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int c = 4 * lane;
-  for (int el = 0; el < n; ++el) {
-    const int64_t e = (int64_t)b + el;
-    const float d = A.dist[e];
-    const float nrm = fmaxf(d, 1e-12f);
-    float Y[9];
-    raw_sh2(A.dvec[3 * e] / nrm, A.dvec[3 * e + 1] / nrm, A.dvec[3 * e + 2] / nrm, Y);
-    float p, dp;
-    env.eval(d, p, dp);
-    float t;
-    const float* tb = R.tab + radial_node(R, ti * R.n_types + A.atom_type[A.col[e]], d, t) + c;
-    const Hermite5 H = hermite5(t);
-    const floatx4 fa = deg_interp(tb, H, 0);
-    const floatx4 fb = deg_interp(tb + kDC, H, 0);
-    const floatx4 fc = deg_interp(tb + 2 * kDC, H, 0);
+  for (int c0 = 0; c0 < n; c0 += CH) {
+    const int nc = min(CH, n - c0);
+    deg_chunk(A, env, R, ti, s, (int64_t)b + c0, nc, C);
+    __syncthreads();
+    for (int el = sub; el < nc; el += 8) {
+      const float* tb = R.tab + C.toff[el] + 4 * q;
+      const Hermite5 H = chunk_hermite(C, el);
+      const float p = C.p[el];
+      float Y[9];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float f0 = fa[u] * p, f1 = fb[u] * p, f2 = fc[u] * p;
-      acc[0][u] = fmaf(Y[0], f0, acc[0][u]);
+      for (int m = 0; m < 9; ++m) Y[m] = C.Y[m][el];
+      const floatx4 fa = deg_interp(tb, H, 0);
+      const floatx4 fb = deg_interp(tb + kDSlC, H, 0);
+      const floatx4 fc = deg_interp(tb + 2 * kDSlC, H, 0);
 #pragma unroll
-      for (int m = 1; m < 4; ++m) acc[m][u] = fmaf(Y[m], f1, acc[m][u]);
+      for (int u = 0; u < 4; ++u) {
+        const float f0 = fa[u] * p, f1 = fb[u] * p, f2 = fc[u] * p;
+        acc[0][u] = fmaf(Y[0], f0, acc[0][u]);
 #pragma unroll
-      for (int m = 4; m < 9; ++m) acc[m][u] = fmaf(Y[m], f2, acc[m][u]);
+        for (int m = 1; m < 4; ++m) acc[m][u] = fmaf(Y[m], f1, acc[m][u]);
+#pragma unroll
+        for (int m = 4; m < 9; ++m) acc[m][u] = fmaf(Y[m], f2, acc[m][u]);
+      }
     }
+    __syncthreads();
   }
 #pragma unroll
   for (int m = 0; m < 9; ++m) {
-    floatx4 o;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) o[u] = acc[m][u] / A.avg;
-    *reinterpret_cast<floatx4*>(x0 + ((size_t)m * A.n_rows + i) * kDC + c) = o;
+    for (int u = 0; u < 4; ++u) {
+      float v = acc[m][u];
+      v += __shfl_xor(v, 8, kWave);
+      v += __shfl_xor(v, 16, kWave);
+      v += __shfl_xor(v, 32, kWave);
+      acc[m][u] = v;
+    }
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      floatx4 o;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o[u] = acc[m][u] / A.avg;
+      *reinterpret_cast<floatx4*>(x0 + ((size_t)m * A.n_rows + i) * kDC + kDSlC * s + 4 * q) = o;
+    }
   }
 }
 
-// One workgroup per query atom; one wave per edge, lane owns channels 4 lane .. + 3.
-// Per edge: dfea_l[c] = p/avg sum_{m in l} Y_m G0[m][i][c]; dL/dd = sum_{l,c} dfea_l[c]
-// (p' fea_l[c] / p + fea_l'[c]) (envelope and profile derivative) and dL/dY -> dL/ddvec.
-__global__ __launch_bounds__(256) void k_deg_bwd(e2v2_deg_args A, const float* __restrict__ G0,
-                                                 float* __restrict__ ddv, float* __restrict__ dd) {
-  const int i = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x, lane = t & 63, wave = t >> 6;
+// Sum over each group of 8 lanes (lanes 8 k .. 8 k + 7), left in every lane of the
+// group: two quad permutes and the half-row mirror (fixed order).
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);   // row_half_mirror
+  return v;
+}
+
+// Backward: per edge and slice, dfea_l[c] = p/avg sum_{m in l} Y_m G0[m][i][c];
+// dL/dd = sum_{l,c} dfea_l[c] (p' fea_l[c] / p + fea_l'[c]) (envelope and profile
+// derivative) and dL/dY -> dL/ddvec.  The 8 lanes of an edge add their channel
+// quads' sums (sum8) and lane q = 0 writes the slice's partial part[s][e] =
+// (dL/ddvec, dL/dd); e2v2_deg_bwd adds the 8 partials of every edge in slice order.
+__global__ __launch_bounds__(64) void k_deg_bwd_sl(e2v2_deg_args A, const float* __restrict__ G0,
+                                                   float4* __restrict__ part) {
+  constexpr int CH = 64;
+  __shared__ DegChunk C;
+  const int s = blockIdx.x % kDSl, i = blockIdx.x / kDSl;
   if (i >= A.n_rows) return;
+  const int lane = threadIdx.x, sub = lane >> 3, q = lane & 7;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
-  Envelope env;
-  env.rc = A.rc; env.a = A.env_a; env.b = A.env_b; env.c = A.env_c;
+  const Envelope env = deg_env(A);
   const RadialTab R = make_deg_tab(A);
   const int ti = A.atom_type[i];
-  const int c = 4 * lane;
+  const int c = kDSlC * s + 4 * q;
   floatx4 g[9];
 #pragma unroll
   for (int m = 0; m < 9; ++m) {
@@ -122,57 +204,83 @@ __global__ __launch_bounds__(256) void k_deg_bwd(e2v2_deg_args A, const float* _
 #pragma unroll
     for (int u = 0; u < 4; ++u) g[m][u] = v[u] / A.avg;
   }
-  for (int el = wave; el < n; el += 4) {
-    const int64_t e = (int64_t)b + el;
-    const float d = A.dist[e];
-    const float nrm = fmaxf(d, 1e-12f);
-    const float ux = A.dvec[3 * e] / nrm, uy = A.dvec[3 * e + 1] / nrm, uz = A.dvec[3 * e + 2] / nrm;
-    float Y[9];
-    raw_sh2(ux, uy, uz, Y);
-    float p, dpdd;
-    env.eval(d, p, dpdd);
-    float tt;
-    const float* tb = R.tab + radial_node(R, ti * R.n_types + A.atom_type[A.col[e]], d, tt) + c;
-    const Hermite5 H = hermite5(tt);
-    float dsh[9];
+  for (int c0 = 0; c0 < n; c0 += CH) {
+    const int nc = min(CH, n - c0);
+    deg_chunk(A, env, R, ti, s, (int64_t)b + c0, nc, C);
+    __syncthreads();
+    for (int el = sub; el < nc; el += 8) {
+      const float* tb = R.tab + C.toff[el] + 4 * q;
+      const Hermite5 H = chunk_hermite(C, el);
+      const float p = C.p[el];
+      float Y[9];
 #pragma unroll
-    for (int m = 0; m < 9; ++m) dsh[m] = 0.f;
-    float s_val = 0.f, s_der = 0.f;   // sum dfea_l fea_l / p and sum dfea_l fea_l' / p
-    // one degree block l (rows m0 .. m0 + 2l) at compile-time indices (the arrays stay in registers)
-    auto block = [&](auto lc) {
-      constexpr int l = decltype(lc)::value, m0 = l * l, m1 = (l + 1) * (l + 1);
-      const floatx4 f = deg_interp(tb + l * kDC, H, 0);
-      const floatx4 fd = deg_interp(tb + l * kDC, H, 1);
+      for (int m = 0; m < 9; ++m) Y[m] = C.Y[m][el];
+      float dsh[9];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float dl = 0.f;
+      for (int m = 0; m < 9; ++m) dsh[m] = 0.f;
+      float s_val = 0.f, s_der = 0.f;   // sum dfea_l fea_l / p and sum dfea_l fea_l' / p
+      // one degree block l (rows m0 .. m0 + 2l) at compile-time indices (the arrays stay in registers)
+      auto block = [&](auto lc) {
+        constexpr int l = decltype(lc)::value, m0 = l * l, m1 = (l + 1) * (l + 1);
+        const floatx4 f = deg_interp(tb + l * kDSlC, H, 0);
+        const floatx4 fd = deg_interp(tb + l * kDSlC, H, 1);
 #pragma unroll
-        for (int m = m0; m < m1; ++m) {
-          dl = fmaf(Y[m], g[m][u], dl);
-          dsh[m] = fmaf(g[m][u], f[u] * p, dsh[m]);
+        for (int u = 0; u < 4; ++u) {
+          float dl = 0.f;
+#pragma unroll
+          for (int m = m0; m < m1; ++m) {
+            dl = fmaf(Y[m], g[m][u], dl);
+            dsh[m] = fmaf(g[m][u], f[u] * p, dsh[m]);
+          }
+          s_val = fmaf(dl, f[u], s_val);
+          s_der = fmaf(dl, fd[u], s_der);
         }
-        s_val = fmaf(dl, f[u], s_val);
-        s_der = fmaf(dl, fd[u], s_der);
-      }
-    };
-    block(std::integral_constant<int, 0>{});
-    block(std::integral_constant<int, 1>{});
-    block(std::integral_constant<int, 2>{});
-    s_val = wave_sum(s_val);
-    s_der = wave_sum(s_der);
+      };
+      block(std::integral_constant<int, 0>{});
+      block(std::integral_constant<int, 1>{});
+      block(std::integral_constant<int, 2>{});
+      s_val = sum8(s_val);
+      s_der = sum8(s_der);
 #pragma unroll
-    for (int m = 1; m < 9; ++m) dsh[m] = wave_sum(dsh[m]);
-    if (lane == 0) {
-      float gx, gy, gz;
-      raw_sh2_bwd(ux, uy, uz, dsh, gx, gy, gz);
-      // u = v / |v|:  dv = (du - u (u . du)) / |v|
-      const float ud = ux * gx + uy * gy + uz * gz;
-      ddv[3 * e] = (gx - ux * ud) / nrm;
-      ddv[3 * e + 1] = (gy - uy * ud) / nrm;
-      ddv[3 * e + 2] = (gz - uz * ud) / nrm;
-      dd[e] = s_val * dpdd + p * s_der * R.inv_h;
+      for (int m = 1; m < 9; ++m) dsh[m] = sum8(dsh[m]);
+      if (q == 0) {
+        const float ux = C.u[0][el], uy = C.u[1][el], uz = C.u[2][el], nrm = C.nrm[el];
+        float gx, gy, gz;
+        raw_sh2_bwd(ux, uy, uz, dsh, gx, gy, gz);
+        // u = v / |v|:  dv = (du - u (u . du)) / |v|
+        const float ud = ux * gx + uy * gy + uz * gz;
+        part[(size_t)s * A.n_edges + b + c0 + el] =
+            make_float4((gx - ux * ud) / nrm, (gy - uy * ud) / nrm, (gz - uz * ud) / nrm,
+                        s_val * C.dp[el] + p * s_der * R.inv_h);
+      }
     }
+    __syncthreads();
   }
+}
+
+// dL/d dvec and dL/dd of every edge: the 8 slices' partials part[s][e] added in slice order.
+__global__ __launch_bounds__(256) void k_edge_part_sum(const float4* __restrict__ part, int64_t n_edges,
+                                                       float* __restrict__ ddv, float* __restrict__ dd) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n_edges) return;
+  float4 a = part[e];
+#pragma unroll
+  for (int s = 1; s < kDSl; ++s) {
+    const float4 v = part[(int64_t)s * n_edges + e];
+    a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+  }
+  ddv[3 * e] = a.x;
+  ddv[3 * e + 1] = a.y;
+  ddv[3 * e + 2] = a.z;
+  dd[e] = a.w;
+}
+
+int launch_edge_part_sum(const float* part, int64_t n_edges, float* ddv, float* dd, hipStream_t st) {
+  if (n_edges <= 0) return 0;
+  hipLaunchKernelGGL(k_edge_part_sum, dim3((unsigned)((n_edges + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<const float4*>(part), n_edges, ddv, dd);
+  E2V2_LAUNCHED("k_edge_part_sum");
+  return 0;
 }
 
 // dpos[a] = sum_{e in row a} g_e - sum_{e in column a} g_e,  g_e = ddv_e + dd_e dvec_e / d_e.
@@ -221,6 +329,8 @@ static int check_deg_table(const e2v2_deg_args& A, const char* who) {
                    A.rtab_h > 0.f && (double)A.rc * (1.0 / A.rtab_h) <= (double)(A.rtab_n - 1),
                "%s: needs the gbf_projs table covering the cutoff and the atom types (n_types %d, rtab_n %d)", who,
                A.n_types, A.rtab_n);
+  // one wavefront per (row, slice): the grid holds 8 n_rows workgroups
+  E2V2_REQUIRE(A.n_rows < (1 << 27), "%s: %d rows exceed the slice grid", who, A.n_rows);
   return 0;
 }
 
@@ -228,20 +338,28 @@ E2V2_API int e2v2_deg_fwd(const e2v2_deg_args* args, float* x0, hipStream_t s) {
   const e2v2_deg_args& A = *args;
   if (int rc = check_deg_table(A, "deg_fwd")) return rc;
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_deg_fwd, dim3(xcd_grid((A.n_rows + kDegWaves - 1) / kDegWaves)), dim3(64 * kDegWaves), 0, s,
-                     A, x0);
-  E2V2_LAUNCHED("k_deg_fwd");
+  hipLaunchKernelGGL(k_deg_fwd_sl, dim3((unsigned)A.n_rows * kDSl), dim3(kWave), 0, s, A, x0);
+  E2V2_LAUNCHED("k_deg_fwd_sl");
   return 0;
 }
 
+E2V2_API size_t e2v2_deg_bwd_workspace(int64_t n_edges) {
+  return n_edges > 0 ? (size_t)n_edges * kDSl * sizeof(float4) : 0;
+}
+
 E2V2_API int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* ddvec, float* ddist,
-                          hipStream_t s) {
+                          void* workspace, size_t workspace_bytes, hipStream_t s) {
   const e2v2_deg_args& A = *args;
   if (int rc = check_deg_table(A, "deg_bwd")) return rc;
   if (A.n_rows == 0) return 0;
-  hipLaunchKernelGGL(k_deg_bwd, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, grad_x0, ddvec, ddist);
-  E2V2_LAUNCHED("k_deg_bwd");
-  return 0;
+  const size_t need = e2v2_deg_bwd_workspace(A.n_edges);
+  E2V2_REQUIRE(workspace_bytes >= need && (need == 0 || workspace) &&
+                   reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "deg_bwd: workspace of %zu bytes (16-byte aligned) needed, got %zu", need, workspace_bytes);
+  float4* part = static_cast<float4*>(workspace);
+  hipLaunchKernelGGL(k_deg_bwd_sl, dim3((unsigned)A.n_rows * kDSl), dim3(kWave), 0, s, A, grad_x0, part);
+  E2V2_LAUNCHED("k_deg_bwd_sl");
+  return launch_edge_part_sum(reinterpret_cast<const float*>(part), A.n_edges, ddvec, ddist, s);
 }
 
 E2V2_API int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,

@@ -986,7 +986,7 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
 
     def forward(self, ctx: EdgeContext):
         table = self._radial.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
-                                 ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key)
+                                 ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="deg")
         # the edge spherical harmonics ("e3nn sph") are formed inside the degree kernels
         with record_function("e3nn sph"):
             return DegreeEmbedFn.apply(ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table,

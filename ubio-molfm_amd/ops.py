@@ -58,12 +58,13 @@ class RadialTable:
     m at 256 m + c), "attn" (one fc_easy profile in the attention kernels' slice
     order, gate and inputhead of head h at 32 (h // 16) + h % 16 and 16 positions
     on, stored slice-major [pairs][8][nodes][4][32]) or "deg" (three profiles,
-    channel c of profile l at 96 (c // 32) + 32 l + c % 32)."""
+    channel c of profile l at 96 (c // 32) + 32 l + c % 32, stored slice-major
+    [pairs][8][nodes][4][96])."""
 
     LAYOUTS = {
         "plain": lambda m: (256 * m, 256, 256, 0, 0, 0),
         "attn": lambda m: (0, 128, 16, 32, 16, 32),
-        "deg": lambda m: (32 * m, 256, 32, 96, 0, 0),
+        "deg": lambda m: (32 * m, 256, 32, 96, 0, 96),
     }
 
     def __init__(self, nets, tgt: nn.Embedding, src: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
@@ -203,13 +204,17 @@ class DegreeEmbedFn(torch.autograd.Function):
         dargs = deg_args(nl, ctx.atom_type, ctx.table, ctx.avg, ctx.rc)
         ddv = torch.empty(max(E, 1), 3, dtype=torch.float32, device=dev)
         dd = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
-        _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(ddv), _p(dd), _stream(gx0))
+        nb = int(_lib.load().e2v2_deg_bwd_workspace(E))     # per-slice partials of this call
+        ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
+        _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(ddv), _p(dd), _p(ws), _lib.C.c_size_t(ws.numel()),
+                  _stream(gx0))
+        del ws
         return ddv[:E], dd[:E], None, None, None, None, None
 
 
 def deg_args(nl: NeighborList, atom_type: torch.Tensor, table: RadialTable, avg: float, rc: float):
-    if table.nc != 768:
-        raise ValueError("the degree embedding needs the table of its three profiles (768 channels)")
+    if table.nc != 768 or table.layout != "deg":
+        raise ValueError("the degree embedding needs the table of its three profiles in slices (layout 'deg')")
     return _lib.DegArgs(nl.n_atoms, nl.n_edges, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                         nl.col.data_ptr(), table.tab.data_ptr(), atom_type.data_ptr(), table.n_types, table.n_nodes,
                         table.h, float(avg), float(rc), ENV_A, ENV_B, ENV_C)
