@@ -22,11 +22,12 @@
 // v, out, their gradients and the table are stored in slice order (position
 // p holds the first or second channel of head pos_head(p); the header's
 // E2V2_POS0 / E2V2_POS1), so a slice is one 128-byte run of every row.
-// Backward: row pass (dq, the edge weights w and dL/dqk, dvec/ddist partials
-// per slice with the profile's distance derivative; the softmax row terms
-// come from D_h = sum_{c in h} sum_t G[t,c] out[t,c]), a column pass over the
-// key CSR (dv_j, dk_j) with no atomics, and the slice partials added per edge
-// in slice order.
+// Backward, one head group (32 heads, two slices) at a time: row pass (dq, the
+// group's edge weights w and dL/dqk, dvec/ddist partials per slice with the
+// profile's distance derivative; the softmax row terms come from
+// D_h = sum_{c in h} sum_t G[t,c] out[t,c]) and the group's column pass over the
+// key CSR (dv_j, dk_j) with no atomics; then the slice partials are added per
+// edge in slice order.
 #include "common.h"
 #include "radial.h"
 #include "tp_table.h"
@@ -48,17 +49,6 @@ __device__ __forceinline__ int pos_head(int p) { return ((p >> 5) << 4) | (p & 1
 // 2 g + 1).  Lane l of a wave owns position 64 g + l, and dims 4 (l % 2) .. +3
 // of head 32 g + l / 2 for dk.
 constexpr int kGroups = 4, kGroupHeads = kH / kGroups, kGroupC = kC / kGroups;
-// (cluster, group) of a workgroup: the workgroups of one XCD (blockIdx % 8) run
-// its contiguous range of clusters group by group, so its L2 holds one group's
-// quarter of the gathered rows at a time.
-__device__ __forceinline__ bool cluster_group(int n_cl, int& cl, int& grp) {
-  const int per = (n_cl + kXcd - 1) / kXcd;
-  const int seq = blockIdx.x / kXcd, x = blockIdx.x % kXcd;
-  grp = seq / per;
-  cl = x * per + seq % per;
-  return grp < kGroups && cl < n_cl;
-}
-
 __device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
   Envelope E;
   E.rc = A.rc; E.a = A.env_a; E.b = A.env_b; E.c = A.env_c;
@@ -100,16 +90,6 @@ __device__ __forceinline__ void load4(const __bf16* p, float (&v)[4]) {
   const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = (float)a[i];
-}
-// One activation through a 32-bit load of the aligned word that holds it: the
-// gathers of the column pass then schedule like their fp32 form (16-bit loads
-// are issued one edge at a time); the word lies inside the tensor because rows
-// have an even number of elements.
-__device__ __forceinline__ float ld_word(const float* p) { return *p; }
-__device__ __forceinline__ float ld_word(const __bf16* p) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-  return __uint_as_float((a & 2) ? (w & 0xffff0000u) : (w << 16));
 }
 __device__ __forceinline__ void store_act(float v, float* p) { ntstore(v, p); }
 __device__ __forceinline__ void store_act(float v, __bf16* p) { *p = (__bf16)v; }
@@ -400,236 +380,40 @@ __device__ __forceinline__ void tp_transpose(const float (&g)[kNT], float (&dA)[
   for (int z = 0; z < kTpNnz; ++z) dA[kTp[z].r][kTp[z].k] = fmaf(kTp[z].c, g[kTp[z].t], dA[kTp[z].r][kTp[z].k]);
 }
 
-// Column pass, one channel per thread (the fp32 form: a 4-byte gather per lane
-// is as cheap per byte for the address unit as a pair load): for every source
-// atom j, sum over its key-CSR edges (ascending edge id) -> dv_j and dk_j.
-// Edge metadata of a 32-edge chunk is staged in LDS so the per-edge gathers of
-// grad rows do not wait on index loads; two edges are processed per iteration
-// to overlap their 20-row gathers.
-template <typename TS>
-__global__ __launch_bounds__(256) void k_attn_bwd_col_ch(e2v2_attn_args A, const TS* __restrict__ G,
-                                                      const float* __restrict__ w_e, const float* __restrict__ dqk_e,
-                                                      float* __restrict__ dv_out, float* __restrict__ dk_out) {
-  constexpr int CC = 32;
-  __shared__ int ci[CC];
-  __shared__ float cdv[CC][3];
-  __shared__ float cw[CC][kH];
-  __shared__ float cq[CC][kH];
-  const int j = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
-  if (j >= A.n_rows) return;
-  const int c = t, hc = pos_head(t);
-  const int hk = t >> 1, d0 = 4 * (t & 1);
-  const size_t os = (size_t)A.n_rows * kC;
-  float av[kNV];
-#pragma unroll
-  for (int r = 0; r < kNV; ++r) av[r] = 0.f;
-  float ak[4] = {0.f, 0.f, 0.f, 0.f};
-  const int p0 = A.key_ptr[j], p1 = A.key_ptr[j + 1];
-  const TS* __restrict__ Qp = static_cast<const TS*>(A.q);
-  for (int c0 = p0; c0 < p1; c0 += CC) {
-    const int nc = min(CC, p1 - c0);
-    if (t < nc) {
-      const int64_t e = A.key_eid[c0 + t];
-      ci[t] = A.edge_row[e];
-      cdv[t][0] = A.dvec[3 * e];
-      cdv[t][1] = A.dvec[3 * e + 1];
-      cdv[t][2] = A.dvec[3 * e + 2];
-    }
-    // per-edge head weights: w and dqk rows are 512 B each; 2 edges x 128 heads per pass
-    for (int idx = t; idx < nc * kH; idx += 256) {
-      const int el = idx >> 7, h = idx & (kH - 1);
-      const int64_t e = A.key_eid[c0 + el];
-      cw[el][h] = ntload(w_e + e * kH + h);
-      cq[el][h] = ntload(dqk_e + e * kH + h);
-    }
-    __syncthreads();
-    // dv_j[r] += sum_k dA[r][k] (w dvec_k), dA = T^T G_i[:, c]; dk_j += dqk q_i (scaled by 1/sqrt(D) once at the end)
-    auto edge = [&](int el, const float (&g)[kNT], const float (&q)[4]) {
-      float dA[kNV][3];
-      tp_transpose(g, dA);
-      const float w = cw[el][hc];
-      const float wx = w * cdv[el][0], wy = w * cdv[el][1], wz = w * cdv[el][2];
-#pragma unroll
-      for (int r = 0; r < kNV; ++r) av[r] = fmaf(dA[r][2], wz, fmaf(dA[r][1], wy, fmaf(dA[r][0], wx, av[r])));
-      const float dqv = cq[el][hk];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) ak[d] = fmaf(dqv, q[d], ak[d]);
-    };
-    int el = 0;
-    for (; el + 1 < nc; el += 2) {
-      const int i0 = ci[el], i1 = ci[el + 1];
-      float g0[kNT], g1[kNT];
-#pragma unroll
-      for (int z = 0; z < kNT; ++z) {
-        g0[z] = ld_word(G + (size_t)i0 * kC + z * os + c);
-        g1[z] = ld_word(G + (size_t)i1 * kC + z * os + c);
-      }
-      float qa[4], qb[4];
-      load4(Qp + ((size_t)i0 * kH + hk) * kD + d0, qa);
-      load4(Qp + ((size_t)i1 * kH + hk) * kD + d0, qb);
-      edge(el, g0, qa);
-      edge(el + 1, g1, qb);
-    }
-    if (el < nc) {
-      const int i0 = ci[el];
-      float g0[kNT];
-#pragma unroll
-      for (int z = 0; z < kNT; ++z) g0[z] = ld_word(G + (size_t)i0 * kC + z * os + c);
-      float qa[4];
-      load4(Qp + ((size_t)i0 * kH + hk) * kD + d0, qa);
-      edge(el, g0, qa);
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int r = 0; r < kNV; ++r) ntstore(av[r], dv_out + (size_t)j * kC + r * os + c);
-#pragma unroll
-  for (int d = 0; d < 4; ++d) ntstore(ak[d] / A.q_div, dk_out + ((size_t)j * kH + hk) * kD + d0 + d);
-}
-
-// Column pass, channel pairs (the bf16 form: one 4-byte word carries two
-// channels): for every source atom j, sum over its key-CSR edges (ascending
-// edge id) -> dv_j and dk_j, no atomics.  Thread t owns the channel pair
-// positions (2u, 2u + 1), u = t % 128, and the chunk's edges of parity t / 128: every
-// gather instruction moves two channels per lane (the gathers, not the bytes,
-// bound this pass).  The two parities' partial sums are added once per column
-// in LDS (fixed order: deterministic).  Edge metadata of 32-edge chunks is
-// staged in LDS.
-__device__ __forceinline__ void ld_pair(const float* p, float& a, float& b) {
-  const float2 v = *reinterpret_cast<const float2*>(p);
-  a = v.x;
-  b = v.y;
-}
-__device__ __forceinline__ void ld_pair(const __bf16* p, float& a, float& b) {
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-  a = __uint_as_float(w << 16);
-  b = __uint_as_float(w & 0xffff0000u);
-}
-
-template <typename TS>
-__global__ __launch_bounds__(256) void k_attn_bwd_col_pair(e2v2_attn_args A, const TS* __restrict__ G,
-                                                           const float* __restrict__ w_e,
-                                                           const float* __restrict__ dqk_e, float* __restrict__ dv_out,
-                                                           float* __restrict__ dk_out) {
-  constexpr int CC = 32;
-  __shared__ int ci[CC];
-  __shared__ float cdv[CC][3];
-  __shared__ float cwq[2 * CC * kH];          // per-chunk w | dqk; after the loop, the parity partial sums
-  float (*cw)[kH] = reinterpret_cast<float (*)[kH]>(cwq);
-  float (*cq)[kH] = reinterpret_cast<float (*)[kH]>(cwq + CC * kH);
-  float (*red_v)[kC] = reinterpret_cast<float (*)[kC]>(cwq);
-  float (*red_k)[kD] = reinterpret_cast<float (*)[kD]>(cwq + kNV * kC);
-  static_assert(kNV * kC + kH * kD <= 2 * CC * kH, "partial sums fit the chunk buffers");
-  const int j = xcd_row(blockIdx.x, A.n_rows), t = threadIdx.x;
-  if (j >= A.n_rows) return;
-  const int u = t & (kH - 1), par = t >> 7;
-  const int c0 = 2 * u;                                     // channels c0, c0 + 1
-  const int h0 = pos_head(c0), h1 = pos_head(c0 + 1);       // their heads
-  const size_t os = (size_t)A.n_rows * kC;
-  float av0[kNV], av1[kNV];
-#pragma unroll
-  for (int r = 0; r < kNV; ++r) av0[r] = av1[r] = 0.f;
-  float ak[kD];
-#pragma unroll
-  for (int d = 0; d < kD; ++d) ak[d] = 0.f;
-  const int p0 = A.key_ptr[j], p1 = A.key_ptr[j + 1];
-  const TS* __restrict__ Qp = static_cast<const TS*>(A.q);
-  // dv[r] += sum_k dA[r][k] (w dvec_k), dA = T^T G_i[:, c]
-  auto channel = [&](int el, const float (&g)[kNT], int h, float (&av)[kNV]) {
-    float dA[kNV][3];
-    tp_transpose(g, dA);
-    const float w = cw[el][h];
-    const float wx = w * cdv[el][0], wy = w * cdv[el][1], wz = w * cdv[el][2];
-#pragma unroll
-    for (int r = 0; r < kNV; ++r) av[r] = fmaf(dA[r][2], wz, fmaf(dA[r][1], wy, fmaf(dA[r][0], wx, av[r])));
-  };
-  for (int c0e = p0; c0e < p1; c0e += CC) {
-    const int nc = min(CC, p1 - c0e);
-    if (t < nc) {
-      const int64_t e = A.key_eid[c0e + t];
-      ci[t] = A.edge_row[e];
-      cdv[t][0] = A.dvec[3 * e];
-      cdv[t][1] = A.dvec[3 * e + 1];
-      cdv[t][2] = A.dvec[3 * e + 2];
-    }
-    // per-edge head weights: w and dqk rows are 512 B each; 2 edges x 128 heads per pass
-    for (int idx = t; idx < nc * kH; idx += 256) {
-      const int el = idx >> 7, h = idx & (kH - 1);
-      const int64_t e = A.key_eid[c0e + el];
-      cw[el][h] = ntload(w_e + e * kH + h);
-      cq[el][h] = ntload(dqk_e + e * kH + h);
-    }
-    __syncthreads();
-    for (int el = par; el < nc; el += 2) {
-      const int i = ci[el];
-      float ga[kNT], gb[kNT];
-#pragma unroll
-      for (int z = 0; z < kNT; ++z) ld_pair(G + (size_t)i * kC + z * os + c0, ga[z], gb[z]);
-      float q[kD];
-      load8(Qp + ((size_t)i * kH + u) * kD, q);
-      channel(el, ga, h0, av0);
-      channel(el, gb, h1, av1);
-      const float dqv = cq[el][u];
-#pragma unroll
-      for (int d = 0; d < kD; ++d) ak[d] = fmaf(dqv, q[d], ak[d]);
-    }
-    __syncthreads();
-  }
-  if (par) {
-#pragma unroll
-    for (int r = 0; r < kNV; ++r) {
-      red_v[r][c0] = av0[r];
-      red_v[r][c0 + 1] = av1[r];
-    }
-#pragma unroll
-    for (int d = 0; d < kD; ++d) red_k[u][d] = ak[d];
-  }
-  __syncthreads();
-  if (!par) {
-#pragma unroll
-    for (int r = 0; r < kNV; ++r) {
-      const float2 v = make_float2(av0[r] + red_v[r][c0], av1[r] + red_v[r][c0 + 1]);
-      *reinterpret_cast<float2*>(dv_out + (size_t)j * kC + r * os + c0) = v;
-    }
-    float* kp = dk_out + ((size_t)j * kH + u) * kD;
-#pragma unroll
-    for (int d = 0; d < kD; ++d) kp[d] = (ak[d] + red_k[u][d]) / A.q_div;
-  }
-}
-
-// Column pass over clusters of R consecutive key-CSR columns and one of four
-// channel groups (G and q in fp32 or bf16, sums in fp32).  Group g holds the 64 channel positions of heads
-// 32g..32g+31 (positions 64g..64g+63); the workgroups of one XCD run group by group,
-// so its L2 holds a quarter of each neighbour row at a time and the gathered
-// rows of a column window stay resident.  Wave w applies the slots s = w mod 4
-// of each chunk (lane = channel of the group; for dk lane = (head, half of the
-// head's dims)); the four waves' partial sums are added once per cluster in
-// LDS in a fixed order.  Every slot's G_i and q_i are loaded once and applied
-// to each column of the cluster that it joins.
-
-template <int R, typename TS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_bwd_col_grp(e2v2_attn_args A, const TS* __restrict__ G,
-                                                          const float* __restrict__ w_e,
-                                                          const float* __restrict__ dqk_e, float* __restrict__ dv_out,
-                                                          float* __restrict__ dk_out) {
+// Column pass of channel group g (heads 32 g .. 32 g + 31, positions 64 g .. 64 g
+// + 63; G and q in fp32 or bf16, sums in fp32) over clusters of R consecutive
+// key-CSR columns: the workgroups of one XCD run a contiguous range of clusters,
+// so the gathered rows of a column window stay in its L2.  Wave w applies the
+// slots s = w mod 4 of each chunk (lane = channel of the group; for dk lane =
+// (head, half of the head's dims)); the four waves' partial sums are added once
+// per cluster in LDS in a fixed order.  Every slot's G_i and q_i are loaded once
+// and applied to each column of the cluster that it joins.  With kSlots the
+// slots come from e2v2_cluster_slots (R = 4); without, R = 1 and the slots of
+// column j are its key-CSR edges.  w_g and dqk_g hold the group's 32 heads per
+// edge ([E][32]), written by the row pass of the same group.
+template <int R, typename TS, bool kSlots>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_bwd_col_grp(
+    e2v2_attn_args A, const TS* __restrict__ G, const float* __restrict__ w_g, const float* __restrict__ dqk_g,
+    float* __restrict__ dv_out, float* __restrict__ dk_out, int grp) {
+  static_assert(kSlots || R == 1, "columns without slots are clusters of one");
   constexpr int S = 32;                        // slots per staged chunk
   __shared__ int ci[S];
   __shared__ int ce[S][R];
   __shared__ float cdv[S][R][3];
   __shared__ float red[2][R][kNV + 4][kWave];  // per-wave partial sums, added in two rounds
   const int n_cl = (A.n_rows + R - 1) / R;
-  int cl, grp;
-  if (!cluster_group(n_cl, cl, grp)) return;
+  const int cl = xcd_row(blockIdx.x, n_cl);
+  if (cl >= n_cl) return;
   const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
   const int c = kGroupC * grp + lane;   // channel position
-  const int hc = pos_head(c);
-  const int hk = kGroupHeads * grp + (lane >> 1), d0 = 4 * (lane & 1);
+  const int hc = pos_head(c) - kGroupHeads * grp;                     // its head within the group
+  const int hkg = lane >> 1, hk = kGroupHeads * grp + hkg, d0 = 4 * (lane & 1);
   const int j0 = cl * R, nj = min(R, A.n_rows - j0);
   const size_t os = (size_t)A.n_rows * kC;
   const int64_t base = A.key_ptr[j0];
-  const int ns = A.col_n_slots[cl];
-  const int32_t* __restrict__ smem = A.col_slot_member + base;
-  const int32_t* __restrict__ sedge = A.col_slot_edge + base * R;
+  const int ns = kSlots ? A.col_n_slots[cl] : A.key_ptr[j0 + 1] - (int)base;
+  const int32_t* __restrict__ smem = kSlots ? A.col_slot_member + base : nullptr;
+  const int32_t* __restrict__ sedge = kSlots ? A.col_slot_edge + base * R : nullptr;
   const TS* __restrict__ Qp = static_cast<const TS*>(A.q);
   float av[R][kNV];
   float ak[R][4];
@@ -656,8 +440,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t e = max(ce[sl][r], 0);
-      L.w[r] = ntload(w_e + e * kH + hc);
-      L.dq[r] = ntload(dqk_e + e * kH + hk);
+      L.w[r] = ntload(w_g + e * kGroupHeads + hc);
+      L.dq[r] = ntload(dqk_g + e * kGroupHeads + hkg);
     }
   };
   auto apply = [&](int sl, const Loads& L) {
@@ -680,10 +464,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   };
   for (int s0 = 0; s0 < ns; s0 += S) {
     const int nc = min(S, ns - s0);
-    if (t < nc) ci[t] = smem[s0 + t];
+    if (t < nc) ci[t] = kSlots ? smem[s0 + t] : A.edge_row[A.key_eid[base + s0 + t]];
     for (int idx = t; idx < nc * R; idx += 256) {
       const int sl = idx / R, r = idx % R;
-      const int e = sedge[(int64_t)(s0 + sl) * R + r];
+      const int e = kSlots ? sedge[(int64_t)(s0 + sl) * R + r] : A.key_eid[base + s0 + sl];
       ce[sl][r] = e;
       if (e >= 0) {
         cdv[sl][r][0] = A.dvec[3 * (int64_t)e];
@@ -791,16 +575,18 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
                                                         const float* __restrict__ srow,
                                                         const int32_t* __restrict__ cnt, float* __restrict__ part,
                                                         float* __restrict__ dq, float* __restrict__ w_out,
-                                                        float* __restrict__ dqk_out) {
+                                                        float* __restrict__ dqk_out, int grp) {
   constexpr int CH = 64;
   __shared__ float4 er_a[CH];      // p, dp/dd, 1/max(d, 1e-6), d
   __shared__ float4 er_b[CH];      // dvec, column (int bits)
   __shared__ int64_t er_toff[CH];  // slice-s table offset of the lower node
   __shared__ float er_hw[6][CH];   // quintic Hermite weights of the fraction in the node interval
-  const int s = blockIdx.x % kSl, i = blockIdx.x / kSl;
+  // slices 2 grp (even blockIdx: XCDs 0, 2, 4, 6) and 2 grp + 1 (odd: XCDs 1, 3, 5, 7), rows in order
+  const int s = 2 * grp + (blockIdx.x & 1), i = blockIdx.x >> 1;
   if (i >= A.n_rows) return;
   const int lane = threadIdx.x, hh = lane & (kSlH - 1), sub = lane >> 4;
   const int h = kSlH * s + hh;
+  const int hg = h - kGroupHeads * grp;   // head within the group (w, dqk columns)
   const int p0 = kSlC * s + hh, p1 = p0 + kSlH;   // the head's two channel positions
   const RadialTab R = make_tab(A);
   const int ti = A.atom_type[i];
@@ -907,8 +693,8 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
     if (a == m) da += dmc;
     const float dpv = de * ex;
     const float dqk = da * gate;
-    ntstore(w, w_out + e * kH + h);
-    ntstore(dqk, dqk_out + e * kH + h);
+    ntstore(w, w_out + e * kGroupHeads + hg);
+    ntstore(dqk, dqk_out + e * kGroupHeads + hg);
 #pragma unroll
     for (int q = 0; q < kD; ++q) dqa[q] = fmaf(dqk, kf[q], dqa[q]);
     // dL/dd of this head: envelope, 1/d, and the profile (dL/dgate gate' + dL/dih ih')
@@ -1008,37 +794,38 @@ E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, f
   return 0;
 }
 
-// workspace of e2v2_attn_bwd: w [E][H] and dL/dqk [E][H] handed from the row pass to the column pass, and the
-// slice partials of dL/d dvec, dL/dd [8][E][4]
-static size_t bwd_ws_floats(int64_t n_edges) { return (size_t)n_edges * (2 * kH + 4 * kSl); }
+// workspace of e2v2_attn_bwd: w [E][32] and dL/dqk [E][32] of one head group, handed from that group's row
+// pass to its column pass, and the slice partials of dL/d dvec, dL/dd [8][E][4]
+static size_t bwd_ws_floats(int64_t n_edges) { return (size_t)n_edges * (2 * kGroupHeads + 4 * kSl); }
 
 E2V2_API size_t e2v2_attn_bwd_workspace(int64_t n_edges) {
   return n_edges > 0 ? bwd_ws_floats(n_edges) * sizeof(float) : 0;
 }
 
+// The four head groups in turn: the row pass of the group's two slices, then its column pass (clusters when
+// given, else one column per workgroup); finally the slice partials are added per edge.
 template <typename TS>
 static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, const float* mrow, const float* srow,
                            const int32_t* cnt, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
                            float* ws, hipStream_t s) {
   const int64_t E = A.n_edges;
-  float* w_edge = ws;
-  float* dqk_edge = ws + (size_t)E * kH;
-  float* part = ws + (size_t)E * 2 * kH;
-  hipLaunchKernelGGL(k_attn_bwd_row_sl<TS>, dim3((unsigned)A.n_rows * kSl), dim3(kWave), 0, s, A, G, O, mrow, srow,
-                     cnt, part, dq, w_edge, dqk_edge);
-  E2V2_LAUNCHED("k_attn_bwd_row_sl");
-  if (A.col_slot_member) {
-    const int n_cl = (A.n_rows + 3) / 4;
-    hipLaunchKernelGGL((k_attn_bwd_col_grp<4, TS>), dim3(xcd_grid(n_cl) * kGroups), dim3(256), 0, s, A, G, w_edge,
-                       dqk_edge, dv, dk);
-  } else if constexpr (sizeof(TS) == 2) {
-    hipLaunchKernelGGL(k_attn_bwd_col_pair<TS>, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_edge, dqk_edge,
-                       dv, dk);
-  } else {
-    hipLaunchKernelGGL(k_attn_bwd_col_ch<TS>, dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_edge, dqk_edge, dv,
-                       dk);
+  float* w_g = ws;
+  float* dqk_g = ws + (size_t)E * kGroupHeads;
+  float* part = ws + (size_t)E * 2 * kGroupHeads;
+  for (int g = 0; g < kGroups; ++g) {
+    hipLaunchKernelGGL(k_attn_bwd_row_sl<TS>, dim3((unsigned)A.n_rows * 2), dim3(kWave), 0, s, A, G, O, mrow, srow,
+                       cnt, part, dq, w_g, dqk_g, g);
+    E2V2_LAUNCHED("k_attn_bwd_row_sl");
+    if (A.col_slot_member) {
+      const int n_cl = (A.n_rows + 3) / 4;
+      hipLaunchKernelGGL((k_attn_bwd_col_grp<4, TS, true>), dim3(xcd_grid(n_cl)), dim3(256), 0, s, A, G, w_g, dqk_g,
+                         dv, dk, g);
+    } else {
+      hipLaunchKernelGGL((k_attn_bwd_col_grp<1, TS, false>), dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_g,
+                         dqk_g, dv, dk, g);
+    }
+    E2V2_LAUNCHED("k_attn_bwd_col_grp");
   }
-  E2V2_LAUNCHED("k_attn_bwd_col");
   return launch_edge_part_sum(part, E, ddvec, ddist, s);
 }
 
