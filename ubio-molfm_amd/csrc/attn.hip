@@ -581,9 +581,11 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
   __shared__ float4 er_b[CH];      // dvec, column (int bits)
   __shared__ int64_t er_toff[CH];  // slice-s table offset of the lower node
   __shared__ float er_hw[6][CH];   // quintic Hermite weights of the fraction in the node interval
-  // slices 2 grp (even blockIdx: XCDs 0, 2, 4, 6) and 2 grp + 1 (odd: XCDs 1, 3, 5, 7), rows in order
-  const int s = 2 * grp + (blockIdx.x & 1), i = blockIdx.x >> 1;
-  if (i >= A.n_rows) return;
+  // slice 2 grp on the even XCDs (blockIdx % 8 = 0, 2, 4, 6), 2 grp + 1 on the odd ones; the four XCDs of a
+  // slice take contiguous quarters of the rows, each in order, so an XCD's rows stay spatially compact
+  const int x = blockIdx.x % kXcd, quarter = (A.n_rows + 3) / 4;
+  const int s = 2 * grp + (x & 1), i = (x >> 1) * quarter + (int)(blockIdx.x / kXcd);
+  if (blockIdx.x / kXcd >= (unsigned)quarter || i >= A.n_rows) return;
   const int lane = threadIdx.x, hh = lane & (kSlH - 1), sub = lane >> 4;
   const int h = kSlH * s + hh;
   const int hg = h - kGroupHeads * grp;   // head within the group (w, dqk columns)
@@ -813,8 +815,8 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
   float* dqk_g = ws + (size_t)E * kGroupHeads;
   float* part = ws + (size_t)E * 2 * kGroupHeads;
   for (int g = 0; g < kGroups; ++g) {
-    hipLaunchKernelGGL(k_attn_bwd_row_sl<TS>, dim3((unsigned)A.n_rows * 2), dim3(kWave), 0, s, A, G, O, mrow, srow,
-                       cnt, part, dq, w_g, dqk_g, g);
+    hipLaunchKernelGGL(k_attn_bwd_row_sl<TS>, dim3((unsigned)((A.n_rows + 3) / 4) * kXcd), dim3(kWave), 0, s, A, G, O,
+                       mrow, srow, cnt, part, dq, w_g, dqk_g, g);
     E2V2_LAUNCHED("k_attn_bwd_row_sl");
     if (A.col_slot_member) {
       const int n_cl = (A.n_rows + 3) / 4;
