@@ -19,7 +19,13 @@
  *                       src/molfm/models/e2former/module_utils.py:1065-1274, 3119-3242
  *                       (FAISS twin: src/molfm/models/e2former/sp/dist_ner.py:27-86, 240-333)
  *   e2v2_csr_transpose  prepare_sparse_qk_edge_index_metadata
- *                       src/molfm/models/e2former/triton_dr/triton_sparse_qk_autograd.py:601-652
+ *   e2v2_segment_metadata src/molfm/models/e2former/triton_dr/triton_sparse_qk_autograd.py:601-652
+ *   e2v2_pair_*         construct_radius_neighbor in its padded-batch form (module_utils.py:3119-3242)
+ *   e2v2_seg_*, e2v2_gather_rows, e2v2_outer_*
+ *                       the op-level Triton kernels of src/molfm/models/e2former/triton_dr/ behind
+ *                       sparse_qk_edge_index_triton, sparse_alpha_sum_edge_index_triton,
+ *                       sparse_v_agg_edge_index_triton_cblocked and edge_degree_outer_triton, first and
+ *                       second order
  *   e2v2_radial_table*  GaussianSmearing + RadialProfile over x_edge = [rbf, tgt, src]
  *                       src/molfm/models/e2former/e2former.py:258-266, 302 (fc_easy) and
  *                       e2former.py:709-733 (gbf_projs); module_utils.py:1853-1869, 2151-2178,
@@ -128,6 +134,85 @@ int e2v2_cluster_slots(const int32_t* seg_ptr, int32_t n_seg, const int32_t* mem
 int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, int n_cols, int64_t n_edges,
                        int32_t* edge_row, int32_t* key_cnt, int32_t* key_ptr, int32_t* stats,
                        uint64_t* tmp_key, int32_t* key_eid, int phase, hipStream_t s);
+/* Segment metadata of an edge list in any order, the (row_ptr, col_index, alpha_index) triple of
+   _prepare_segment_metadata (src/molfm/models/e2former/triton_dr/triton_sparse_qk_autograd.py:615-632):
+   the edges of row r in ascending edge order (a stable sort by row_index), col_index[p] =
+   other_index[alpha_index[p]].  Phase 0: row_ptr [n_rows + 1] and stats [3] = {edges counted, longest
+   row, entries of row_index outside [0, n_rows)}; the caller reads stats[2] and runs phase 1 (col_index,
+   alpha_index [n_edges]) only when it is 0.  cnt [n_rows] and tmp_key [n_edges] are scratch. */
+int e2v2_segment_metadata(const int32_t* row_index, const int32_t* other_index, int64_t n_edges, int n_rows,
+                          int32_t* row_ptr, int32_t* col_index, int32_t* alpha_index, int32_t* cnt,
+                          uint64_t* tmp_key, int32_t* stats, int phase, hipStream_t s);
+
+/* Padded-batch radius search by direct distance evaluation: construct_radius_neighbor
+   (src/molfm/models/e2former/module_utils.py:3119-3242).  Query q (a real atom, node_pos[node_mask]
+   flattened) of batch row qgraph[q] meets all l2 padded expanded positions of that row (padding
+   included, as in the reference); the pair (q, k) is kept when min_dist <= d <= max_dist and
+   include[row][k] (NULL: all), d = sqrt((dx dx + dy dy) + dz dz) in fp32 of dv = node_pos - expand_pos.
+   Rows are sorted by (d, k) and cut to their k_keep nearest; neighbor_idx = min(sbase[row] + k,
+   n_flat - 1) indexes the flattened expanded nodes sflat (expand_node_pos[expand_node_mask]),
+   f_edge_vec = qpos[q] - sflat[neighbor_idx], f_poly_dist = polynomial(d, max_dist) (poly 0,
+   module_utils.py:1946-1954) or smooth_polynomial_bell(d, min_dist, max_dist, 2) (poly 1, :1956-1985). */
+typedef struct e2v2_pair_plan {
+  int32_t n_query, n_graphs, l2, n_flat;
+  float max_dist, min_dist;
+  int32_t poly;                     /* 0 polynomial envelope (exponent 5), 1 smooth bell (exponent 2)   */
+  const float* qpos;                /* [n_query, 3]                                                     */
+  const int32_t* qgraph;            /* [n_query] batch row of each query                                */
+  const float* spos;                /* [n_graphs, l2, 3] padded expanded positions                      */
+  const uint8_t* include;           /* [n_graphs, l2] or NULL                                           */
+  const int32_t* sbase;             /* [n_graphs] flattened index of each row's first expanded node     */
+  const float* sflat;               /* [n_flat, 3]                                                      */
+} e2v2_pair_plan;
+/* row_count [n_query], row_ptr [n_query + 1]; stats [2] = {pairs, longest row} */
+int e2v2_pair_count(const e2v2_pair_plan* plan, int32_t* row_count, int32_t* row_ptr, int32_t* stats,
+                    hipStream_t s);
+/* new_ptr [n_query + 1]: the kept pairs per row, from e2v2_nbr_topk phase 0 over row_ptr with
+   k_keep (rows are cut to their first new_ptr[q+1] - new_ptr[q] pairs); tmp_key [n_pairs] scratch;
+   outputs of new_ptr[n_query] entries: query_idx, neighbor_idx (int64), edge_vec [., 3], dist, poly. */
+int e2v2_pair_emit(const e2v2_pair_plan* plan, const int32_t* row_ptr, int64_t n_pairs, int max_row,
+                   const int32_t* new_ptr, uint64_t* tmp_key, int64_t* query_idx, int64_t* neighbor_idx,
+                   float* edge_vec, float* dist, float* poly, hipStream_t s);
+
+/* ---- op-level sparse edge kernels -------------------------------------- */
+/* The segment layout of the reference's Triton kernels: slot p of row r (row_ptr[r] <= p <
+   row_ptr[r+1]) carries edge alpha_index[p] and partner row col_index[p].  Slots whose partner row is
+   outside [0, n_cols) or whose edge is outside [0, n_edges) are skipped; row bounds are clamped to
+   [0, n_slots].  Rows are summed in slot order by one workgroup each (deterministic).  Operands are
+   fp32 with element strides: a logical [rows, H, D] operand A has A[r, h, d] at r s[0] + h s[1] + d s[2]. */
+typedef struct e2v2_segments {
+  const int32_t* row_ptr;           /* [n_rows + 1]                                                     */
+  const int32_t* col_index;         /* [n_slots] (may be NULL where no partner operand is read)          */
+  const int32_t* alpha_index;       /* [n_slots]                                                        */
+  int32_t n_rows, n_cols;
+  int64_t n_slots, n_edges;
+} e2v2_segments;
+/* out[alpha_index[p], h] = sum_d A[r, h, d] B[col_index[p], h, d] over the slots of every row r:
+   _edge_qk_fwd_csr_kernel (triton_sparse_qk_autograd.py:52-130) and, with A, B viewed [M, H, C] from
+   [M, C, H], _edge_dot_cblocked (sparse_v_agg_edge_index_cblocked_bench.py:133-161).  Slots not written
+   keep their value. */
+int e2v2_seg_dot(const e2v2_segments* seg, const float* A, const int64_t* a_strides, const float* B,
+                 const int64_t* b_strides, int H, int D, float* out, const int64_t* out_strides, hipStream_t s);
+/* out[r, h, d] = sum_p W[alpha_index[p], h] X[col_index[p], h, d] (every row written):
+   _edge_grouped_reduce_triton / _bwdk_n_tiled_spmv (triton_sparse_qk_autograd.py:388-435, 655-673),
+   _edge_index_cblocked_kernel and _edge_grouped_reduce_cblocked (sparse_v_agg_edge_index_cblocked_bench.py:
+   164-294).  X NULL (D = 1): out[r, h] = sum_p W[alpha_index[p], h], _fwd_alpha_sum_edge_index
+   (sparse_alpha_sum_edge_index_autograd.py:28-67, 112-126). */
+int e2v2_seg_reduce(const e2v2_segments* seg, const float* W, const int64_t* w_strides, const float* X,
+                    const int64_t* x_strides, int H, int D, float* out, const int64_t* out_strides, hipStream_t s);
+/* out[e, :K] = in[index[e], :K] (zero rows for an index outside [0, n_in)): _bwd_alpha_sum_edge_index
+   (sparse_alpha_sum_edge_index_autograd.py:70-99). */
+int e2v2_gather_rows(const float* in, int64_t n_in, const int32_t* index, int64_t n, int K, float* out,
+                     hipStream_t s);
+/* out[r, l, h] = sum_p sh[alpha_index[p], l] fea[alpha_index[p], h], contiguous [E, L], [E, H], [R, L, H]:
+   _edge_outer_reduce_kernel (triton_dr/edge_degree_outer_autograd.py:25-70, 181-204). */
+int e2v2_outer_reduce(const e2v2_segments* seg, const float* sh, const float* fea, int L, int H, float* out,
+                      hipStream_t s);
+/* dsh[e, l] = sum_h grad[q_e, l, h] fea[e, h] and dfea[e, h] = sum_l grad[q_e, l, h] sh[e, l] (either
+   output may be NULL; q_e outside [0, n_rows) gives 0): _edge_dsh_kernel / _edge_dfea_kernel
+   (edge_degree_outer_autograd.py:81-178, 207-256). */
+int e2v2_outer_bwd(const float* grad, int n_rows, const float* sh, const float* fea, const int32_t* query_index,
+                   int64_t n_edges, int L, int H, float* dsh, float* dfea, hipStream_t s);
 
 /* ---- radial profiles as distance tables ------------------------------- */
 /* A RadialProfile [256 + 2 n_emb -> 128 -> LayerNorm -> SiLU -> 128 -> LayerNorm -> SiLU -> 256] over

@@ -241,16 +241,41 @@ def expand_includeself(pos, pbc, atomic_numbers, cell, rc, cap=4, padding_mask=N
                 expand_shift=exp_shift)
 
 
+def smooth_polynomial_bell(dist, cutoff_min, cutoff_max, exponent=2):
+    """``module_utils.py:1956-1985``: (1 - t^2)^exponent with t the distance
+    mapped linearly from [cutoff_min, cutoff_max] onto [-1, 1] and clamped."""
+    cmin = torch.tensor(cutoff_min, dtype=dist.dtype)
+    cmax = torch.maximum(torch.tensor(cutoff_max, dtype=dist.dtype), cmin + 1e-8)
+    t = (2 * dist - (cmin + cmax)) / (cmax - cmin)
+    t = torch.clamp(t, -1.0, 1.0)
+    return (1.0 - t ** 2) ** exponent
+
+
+def _fixed_norm(v):
+    """The fp32 expression sqrt((dx*dx + dy*dy) + dz*dz), each op rounded (the
+    build's fixed form of torch.linalg.norm for fp32 vectors).  The square root
+    is taken in float64 and rounded once to fp32, which is the correctly rounded
+    fp32 root (torch's CPU fp32 sqrt is not correctly rounded in every case)."""
+    a = v.to(torch.float32)
+    s = (a[..., 0] * a[..., 0] + a[..., 1] * a[..., 1]) + a[..., 2] * a[..., 2]
+    return torch.sqrt(s.double()).float()
+
+
 def construct_radius_neighbor(node_pos, node_mask, expand_node_pos, expand_node_mask,
-                              max_dist, min_dist=1e-4, max_neighbors=None):
-    """``module_utils.py:3119-3242`` (poly='poly', no include_mask); metadata
-    omitted (the CSR is rebuilt where needed)."""
+                              max_dist, min_dist=1e-4, max_neighbors=None, include_mask=None,
+                              poly="poly", fixed_norm=False):
+    """``module_utils.py:3119-3242`` (metadata omitted: the CSR is rebuilt where
+    needed).  ``fixed_norm`` replaces torch.linalg.norm by the fixed fp32
+    expression (the two agree to about one ulp); ties in the per-row sort keep
+    the expanded-slot order (a stable sort)."""
     B, L = node_pos.shape[:2]
     expand_ptr = torch.cat([torch.zeros(1, dtype=torch.int64),
                             torch.cumsum(torch.sum(expand_node_mask, dim=-1), dim=-1)])
     edge_vec = node_pos.unsqueeze(2) - expand_node_pos.unsqueeze(1)
-    dist = torch.linalg.norm(edge_vec, dim=-1, keepdim=False)
+    dist = _fixed_norm(edge_vec) if fixed_norm else torch.linalg.norm(edge_vec, dim=-1, keepdim=False)
     dist = torch.where(dist >= min_dist, dist, max_dist + 1000)
+    if include_mask is not None:
+        dist = torch.where(include_mask.unsqueeze(1), dist, max_dist + 1000)
     within = torch.max(torch.sum(dist <= max_dist, dim=-1)[node_mask])
     _, nidx = dist.sort(dim=-1, descending=False, stable=True)
     if max_neighbors is not None:
@@ -261,7 +286,12 @@ def construct_radius_neighbor(node_pos, node_mask, expand_node_pos, expand_node_
     dist = torch.gather(dist, dim=-1, index=nidx)
     f_dist = dist[node_mask]
     f_attn_mask = (f_dist > max_dist).unsqueeze(-1)
-    f_poly = polynomial(f_dist, max_dist)
+    if poly == "poly":
+        f_poly = polynomial(f_dist, max_dist)
+    elif poly == "poly_bell":
+        f_poly = smooth_polynomial_bell(f_dist, min_dist, max_dist, exponent=2)
+    else:
+        raise ValueError("sorry, you must set poly or poly_bell")
     f_poly = torch.where(f_attn_mask.squeeze(-1), 0, f_poly)
     f_sparse = (nidx + expand_ptr[:B, None, None])[node_mask]
     f_sparse = torch.clamp(f_sparse, max=int(expand_ptr[B]) - 1)

@@ -14,9 +14,16 @@ E x 58 x 128 floats = 25 GB):
   e2former.py:393-407).
 
 Backward passes recompute the gathers chunk by chunk (first order only).
+
+``segment_metadata`` / ``qk_metadata``: the CSR metadata of
+``_prepare_segment_metadata`` / ``prepare_sparse_qk_edge_index_metadata``
+(triton_dr/triton_sparse_qk_autograd.py:607-652) in numpy: row_ptr from a
+bincount and cumulative sum, alpha_index the stable argsort of the row index,
+col_index permuted by it.  Pinned by a per-row brute-force listing.
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 CHUNK = 1 << 15
@@ -72,3 +79,21 @@ def sparse_qk(q, k, qi, nj):
 
 def sparse_v_agg(v, a, qi, nj, n_rows: int):
     return _SparseVAgg.apply(v, a, qi, nj, n_rows)
+
+
+def segment_metadata(row_index, col_index, num_rows: int):
+    """(row_ptr, col_index, alpha_index), int32 numpy (triton_sparse_qk_autograd.py:607-632)."""
+    row = np.asarray(row_index, np.int64).reshape(-1)
+    col = np.asarray(col_index, np.int64).reshape(-1)
+    if row.size and (row.min() < 0 or row.max() >= num_rows):
+        raise ValueError("row index outside [0, num_rows)")
+    perm = np.argsort(row, kind="stable")
+    row_ptr = np.zeros(num_rows + 1, np.int64)
+    row_ptr[1:] = np.cumsum(np.bincount(row, minlength=num_rows))
+    return row_ptr.astype(np.int32), col[perm].astype(np.int32), perm.astype(np.int32)
+
+
+def qk_metadata(query_index, neighbor_index, num_queries: int, num_keys: int):
+    """The 6-tuple of prepare_sparse_qk_edge_index_metadata (triton_sparse_qk_autograd.py:635-652)."""
+    return (*segment_metadata(query_index, neighbor_index, num_queries),
+            *segment_metadata(neighbor_index, query_index, num_keys))

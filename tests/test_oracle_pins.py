@@ -222,3 +222,97 @@ def test_chunked_sparse_ops_equal_fallbacks(monkeypatch):
     r1 = m(dict(bd))
     assert torch.allclose(r0["pred_energy"], r1["pred_energy"], rtol=1e-12, atol=0)
     assert torch.allclose(r0["pred_forces"], r1["pred_forces"], rtol=0, atol=1e-12)
+
+
+def test_segment_metadata_brute_force():
+    """The numpy CSR metadata against a per-row listing of the edges in id order."""
+    from oracle.sparse_ops import qk_metadata, segment_metadata
+    rng = np.random.default_rng(3)
+    for n_rows, E in ((7, 40), (1, 5), (5, 0), (50, 600)):
+        row = rng.integers(0, n_rows, E)
+        col = rng.integers(0, 11, E)
+        ptr, c, perm = segment_metadata(row, col, n_rows)
+        want_perm = [e for r in range(n_rows) for e in range(E) if row[e] == r]
+        want_ptr = [0]
+        for r in range(n_rows):
+            want_ptr.append(want_ptr[-1] + sum(1 for e in range(E) if row[e] == r))
+        assert perm.tolist() == want_perm and ptr.tolist() == want_ptr
+        assert c.tolist() == [int(col[e]) for e in want_perm]
+    srt = np.sort(rng.integers(0, 9, 30))
+    assert segment_metadata(srt, srt, 9)[2].tolist() == list(range(30))   # sorted input: identity
+    md = qk_metadata([0, 2, 1, 0], [3, 0, 3, 1], 3, 4)
+    assert md[3].tolist() == [0, 1, 2, 2, 4] and md[5].tolist() == [1, 3, 0, 2] and md[4].tolist() == [2, 0, 0, 1]
+    with pytest.raises(ValueError):
+        segment_metadata([0, 3], [0, 0], 3)
+
+
+def test_envelopes_closed_forms():
+    """polynomial: 1 at 0, 0 from the cutoff on, value and first two derivatives
+    vanishing at the cutoff (the exponent-5 form); bell: 0 at both ends, 1 at the
+    midpoint, symmetric."""
+    from oracle.neighbors import polynomial, smooth_polynomial_bell
+    d = torch.tensor([0.0, 3.0, 6.0, 7.0], dtype=torch.float64)
+    p = polynomial(d, 6.0)
+    assert p[0] == 1 and p[2] == 0 and p[3] == 0
+    r = torch.tensor(1.0 - 1e-4, dtype=torch.float64)
+    assert abs(float(polynomial(r * 6.0, 6.0))) < 1e-15 * 1e6
+    x = torch.tensor([2.0 - 1e-6, 2.0 + 1e-6], dtype=torch.float64)
+    b = smooth_polynomial_bell(torch.tensor([2.0, 4.0, 6.0], dtype=torch.float64), 2.0, 6.0)
+    assert b.tolist() == [0.0, 1.0, 0.0]
+    t = torch.tensor([2.5, 5.5], dtype=torch.float64)
+    bt = smooth_polynomial_bell(t, 2.0, 6.0)
+    assert abs(float(bt[0] - bt[1])) < 1e-15 and abs(float(bt[0]) - (1 - 0.75 ** 2) ** 2) < 1e-15
+    assert smooth_polynomial_bell(x, 2.0, 6.0).max() < 1e-11
+
+
+def test_construct_radius_neighbor_brute_force():
+    """The dense restatement (include mask, bell envelope, max_neighbors, padding)
+    against a pure-Python listing on a tiny padded batch."""
+    from oracle.neighbors import construct_radius_neighbor, polynomial, _fixed_norm
+    g = torch.Generator().manual_seed(5)
+    B, L, L2 = 2, 5, 9
+    pos = torch.rand(B, L, 3, generator=g) * 4.0
+    mask = torch.ones(B, L, dtype=torch.bool)
+    mask[1, 3:] = False
+    pos[~mask] = 999.0
+    epos = torch.cat([pos, pos[:, :4] + torch.tensor([4.0, 0.0, 0.0])], 1)
+    emask = torch.ones(B, L2, dtype=torch.bool)
+    emask[1, 3:5] = False
+    epos[~emask] = 999.0
+    # valid expanded nodes first in every row, as the reference assumes
+    order = torch.argsort((~emask).to(torch.int64), dim=1, stable=True)
+    epos = torch.gather(epos, 1, order.unsqueeze(-1).expand(-1, -1, 3))
+    emask = torch.gather(emask, 1, order)
+    inc = torch.rand(B, L2, generator=g) > 0.2
+    rc, rmin = 3.0, 0.5
+    for kw in (dict(), dict(include_mask=inc), dict(max_neighbors=2), dict(poly="poly_bell", include_mask=inc)):
+        nb = construct_radius_neighbor(pos, mask, epos, emask, rc, rmin, fixed_norm=True, **kw)
+        flat = epos[emask]
+        base = torch.cat([torch.zeros(1, dtype=torch.int64), emask.sum(1).cumsum(0)])
+        rows = []
+        q = 0
+        for b in range(B):
+            for i in range(L):
+                if not mask[b, i]:
+                    continue
+                cand = []
+                for k in range(L2):
+                    d = float(_fixed_norm(pos[b, i] - epos[b, k]))
+                    ok = rmin <= d <= rc and (kw.get("include_mask") is None or bool(inc[b, k]))
+                    if ok:
+                        cand.append((d, k))
+                cand.sort()
+                rows.append((q, b, cand))
+                q += 1
+        longest = max(len(c) for _, _, c in rows)
+        K = max(min(L2, kw.get("max_neighbors", 10 ** 9), longest), 1)
+        want = [(q, min(int(base[b]) + k, int(base[B]) - 1), d) for q, b, c in rows for d, k in c[:K]]
+        assert nb["query_idx"].tolist() == [w[0] for w in want]
+        assert nb["neighbor_idx"].tolist() == [w[1] for w in want]
+        assert torch.equal(nb["f_dist"], torch.tensor([w[2] for w in want], dtype=torch.float32))
+        assert torch.equal(nb["f_edge_vec"], pos[mask][nb["query_idx"]] - flat[nb["neighbor_idx"]])
+        if kw.get("poly") == "poly_bell":
+            t = (2 * nb["f_dist"].double() - (rmin + rc)) / (rc - rmin)
+            assert torch.allclose(nb["f_poly_dist"].double(), (1 - t ** 2) ** 2, atol=1e-6)
+        else:
+            assert torch.allclose(nb["f_poly_dist"], polynomial(nb["f_dist"], rc))

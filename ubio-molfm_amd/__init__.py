@@ -9,7 +9,9 @@ csrc/          HIP kernels for gfx950 and the extern "C" API (libe2v2.so)
 _lib.py        ctypes binding of libe2v2.so (fails loudly when it is missing)
 build.py       hipcc build of libe2v2.so (in-tree)
 ops.py         torch-facing operators and autograd Functions over the C-ABI
-neighbors.py   periodic radius graph -> CSR (query rows, key columns)
+sparse_ops.py  the reference's op-level sparse edge functions (first and second order)
+neighbors.py   periodic radius graph -> CSR (query rows, key columns); the reference's
+               padded-batch construct_radius_neighbor
 modules.py     E2former module tree (reference names) on the HIP edge path
 model.py       E2FormerBackbone / MolfmAtomic / energy head / forces
 calculator.py  E2FormerCalculator-style batched energy+forces entry point

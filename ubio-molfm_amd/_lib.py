@@ -22,6 +22,8 @@ EXPORTS = [
     "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd", "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd",
     "e2v2_qk_proj_fwd_bf16", "e2v2_qk_proj_bwd_bf16",
+    "e2v2_segment_metadata", "e2v2_pair_count", "e2v2_pair_emit", "e2v2_seg_dot", "e2v2_seg_reduce",
+    "e2v2_gather_rows", "e2v2_outer_reduce", "e2v2_outer_bwd",
 ]
 
 
@@ -32,6 +34,17 @@ class NbrPlan(C.Structure):
                 ("graph_periodic", vp), ("shift_off", vp), ("grid_lo", vp), ("grid_h", vp), ("grid_dim", vp),
                 ("bin_base", vp), ("atom_bin", vp), ("bin_count", vp), ("bin_start", vp), ("bin_atoms", vp),
                 ("stats", vp)]
+
+
+class PairPlan(C.Structure):
+    _fields_ = [("n_query", i32), ("n_graphs", i32), ("l2", i32), ("n_flat", i32), ("max_dist", f32),
+                ("min_dist", f32), ("poly", i32), ("qpos", vp), ("qgraph", vp), ("spos", vp), ("include", vp),
+                ("sbase", vp), ("sflat", vp)]
+
+
+class Segments(C.Structure):
+    _fields_ = [("row_ptr", vp), ("col_index", vp), ("alpha_index", vp), ("n_rows", i32), ("n_cols", i32),
+                ("n_slots", i64), ("n_edges", i64)]
 
 
 class RadialNet(C.Structure):

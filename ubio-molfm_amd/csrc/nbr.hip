@@ -574,6 +574,134 @@ static inline unsigned blocks_for(int64_t n, int bs) {
 }
 
 // ---------------------------------------------------------------------------
+// Segment metadata of an edge list in any order (COO -> CSR): entries of row r
+// in ascending edge order (a stable sort by row).  Row indices outside
+// [0, n_rows) are counted in *bad and left out.
+__global__ void k_coo_count(const int32_t* __restrict__ row, int64_t n, int n_rows, int32_t* __restrict__ cnt,
+                            int32_t* __restrict__ bad) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int r = row[e];
+  if (r < 0 || r >= n_rows) {
+    atomicAdd(bad, 1);
+    return;
+  }
+  atomicAdd(&cnt[r], 1);
+}
+
+__global__ void k_gather_i32(const int32_t* __restrict__ src, const int32_t* __restrict__ index, int64_t n,
+                             int32_t* __restrict__ out) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  out[p] = src[index[p]];
+}
+
+// ---------------------------------------------------------------------------
+// Query -> source pairs of padded batches by direct distance evaluation (the
+// reference's dense construct_radius_neighbor form): query q of graph b meets
+// every one of the l2 padded source positions of b.  A pair is kept when
+// min_dist <= d <= max_dist (a NaN distance fails both) and the source is
+// included; each row is sorted by (distance, source slot) and cut to its k
+// nearest.
+__device__ __forceinline__ bool pair_dist(const e2v2_pair_plan& P, int q, int b, int k, float& d) {
+#pragma clang fp contract(off)
+  const float* a = P.qpos + 3 * (int64_t)q;
+  const float* c = P.spos + ((int64_t)b * P.l2 + k) * 3;
+  d = exact_dist(a[0] - c[0], a[1] - c[1], a[2] - c[2]);
+  const bool inc = P.include == nullptr || P.include[(int64_t)b * P.l2 + k] != 0;
+  return inc && d >= P.min_dist && d <= P.max_dist;
+}
+
+__global__ __launch_bounds__(64 * kNbrWaves) void k_pair_count(e2v2_pair_plan P, int32_t* __restrict__ row_count) {
+  const int lane = threadIdx.x & 63;
+  for (int q = blockIdx.x * kNbrWaves + (int)(threadIdx.x >> 6); q < P.n_query; q += gridDim.x * kNbrWaves) {
+    const int b = P.qgraph[q];
+    int c = 0;
+    for (int k0 = 0; k0 < P.l2; k0 += 64) {
+      const int k = k0 + lane;
+      float d;
+      const bool ok = k < P.l2 && pair_dist(P, q, b, k, d);
+      c += __popcll(__ballot(ok));
+    }
+    if (lane == 0) row_count[q] = c;
+  }
+}
+
+__global__ __launch_bounds__(64 * kNbrWaves) void k_pair_fill(e2v2_pair_plan P, const int32_t* __restrict__ row_ptr,
+                                                             uint64_t* __restrict__ key) {
+  const int lane = threadIdx.x & 63;
+  for (int q = blockIdx.x * kNbrWaves + (int)(threadIdx.x >> 6); q < P.n_query; q += gridDim.x * kNbrWaves) {
+    const int b = P.qgraph[q];
+    int o = row_ptr[q];
+    const int o_end = row_ptr[q + 1];
+    for (int k0 = 0; k0 < P.l2; k0 += 64) {
+      const int k = k0 + lane;
+      float d = 0.f;
+      const bool ok = k < P.l2 && pair_dist(P, q, b, k, d);
+      const uint64_t m = __ballot(ok);
+      const int p = o + lanes_below(m);
+      if (ok && p < o_end) key[p] = ((uint64_t)__float_as_uint(d) << 32) | (uint64_t)(uint32_t)k;
+      o += __popcll(m);
+    }
+  }
+}
+
+// module_utils.py:1946-1954 (kind 0, exponent 5) and :1956-1985 (kind 1, exponent 2), fp32, unfused
+__device__ __forceinline__ float pair_envelope(const e2v2_pair_plan& P, float d) {
+#pragma clang fp contract(off)
+  if (P.poly == 0) {
+    const float r = d / P.max_dist;
+    if (!(r < 1.0f)) return 0.0f;
+    const float r2 = r * r, r4 = r2 * r2, r5 = r4 * r;
+    return 1.0f + r5 * (-21.0f + r * (35.0f + -15.0f * r));
+  }
+  const float lo = P.min_dist, hi = fmaxf(P.max_dist, P.min_dist + 1e-8f);
+  float t = (2.0f * d - (lo + hi)) / (hi - lo);
+  t = fminf(fmaxf(t, -1.0f), 1.0f);
+  const float u = 1.0f - t * t;
+  return u * u;
+}
+
+// One workgroup per query row: sort its keys (LDS up to cap, longer rows in place in
+// global memory) and write the first new_ptr[q+1] - new_ptr[q] of them.
+__global__ __launch_bounds__(64) void k_pair_emit(e2v2_pair_plan P, const int32_t* __restrict__ row_ptr,
+                                                  const int32_t* __restrict__ new_ptr, uint64_t* __restrict__ key,
+                                                  int cap, int64_t* __restrict__ query_idx,
+                                                  int64_t* __restrict__ neighbor_idx, float* __restrict__ edge_vec,
+                                                  float* __restrict__ dist, float* __restrict__ poly) {
+#pragma clang fp contract(off)
+  uint64_t* sk = seg_lds;
+  int32_t* sv = reinterpret_cast<int32_t*>(seg_lds + cap);
+  const int q = blockIdx.x;
+  const int b0 = row_ptr[q], n = row_ptr[q + 1] - b0;
+  const int o0 = new_ptr[q], nk = new_ptr[q + 1] - o0;
+  if (n == 0 || nk == 0) return;
+  const bool in_lds = n <= cap;
+  if (in_lds)
+    segment_sort(key, b0, n, sk, sv);
+  else
+    sort_global(key + b0, n);
+  const int g = P.qgraph[q];
+  const float* a = P.qpos + 3 * (int64_t)q;
+  for (int t = threadIdx.x; t < nk; t += blockDim.x) {
+    const uint64_t kv = in_lds ? sk[t] : key[b0 + t];
+    const int k = (int)(uint32_t)kv;
+    const float d = __uint_as_float((uint32_t)(kv >> 32));
+    int64_t j = (int64_t)P.sbase[g] + k;
+    if (j > (int64_t)P.n_flat - 1) j = (int64_t)P.n_flat - 1;
+    const int64_t o = o0 + t;
+    query_idx[o] = q;
+    neighbor_idx[o] = j;
+    const float* c = P.sflat + 3 * j;
+    edge_vec[3 * o] = a[0] - c[0];
+    edge_vec[3 * o + 1] = a[1] - c[1];
+    edge_vec[3 * o + 2] = a[2] - c[2];
+    dist[o] = d;
+    poly[o] = pair_envelope(P, d);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // No-allocation variant of e2v2_nbr_bin + e2v2_nbr_count: the bin workspace lives
 // in this file-scope device array instead of the plan's workspace buffers.  In
 // host code `scratch` only names the symbol; its device address (one copy per
@@ -771,4 +899,87 @@ E2V2_API int e2v2_nbr_count_noalloc(const e2v2_nbr_plan* plan, int32_t* row_coun
   if (int rc = e2v2_fill_i32(stats_out, 0, 3, s)) return rc;
   if (int rc = e2v2_nbr_bin(&P, s)) return rc;
   return e2v2_nbr_count(&P, row_count, row_ptr, s);
+}
+
+E2V2_API int e2v2_segment_metadata(const int32_t* row_index, const int32_t* other_index, int64_t n_edges, int n_rows,
+                                   int32_t* row_ptr, int32_t* col_index, int32_t* alpha_index, int32_t* cnt,
+                                   uint64_t* tmp_key, int32_t* stats, int phase, hipStream_t s) {
+  E2V2_REQUIRE(n_edges >= 0 && n_edges < (1ll << 31) && n_rows >= 0,
+               "segment_metadata: bad sizes (%lld edges, %d rows)", (long long)n_edges, n_rows);
+  E2V2_REQUIRE(row_ptr && stats && (cnt || n_rows == 0), "segment_metadata: null row_ptr / stats / cnt");
+  if (phase == 0) {
+    if (int rc = e2v2_fill_i32(cnt, 0, n_rows, s)) return rc;
+    if (int rc = e2v2_fill_i32(stats + 2, 0, 1, s)) return rc;
+    if (n_edges > 0) {
+      E2V2_REQUIRE(row_index, "segment_metadata: null row_index");
+      hipLaunchKernelGGL(k_coo_count, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, row_index, n_edges, n_rows,
+                         cnt, stats + 2);
+      E2V2_LAUNCHED("k_coo_count");
+    }
+    hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, cnt, n_rows, row_ptr, stats);
+    E2V2_LAUNCHED("k_scan_i32");
+    return 0;
+  }
+  // phase 1: only after phase 0 reported no out-of-range row (stats[2] == 0)
+  if (n_edges == 0) return 0;
+  E2V2_REQUIRE(n_rows > 0, "segment_metadata: %lld edges but no row", (long long)n_edges);
+  E2V2_REQUIRE(row_index && other_index && col_index && alpha_index && tmp_key, "segment_metadata: null pointer");
+  if (int rc = e2v2_fill_i32(cnt, 0, n_rows, s)) return rc;
+  hipLaunchKernelGGL(k_col_fill, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, row_index, n_edges, row_ptr, cnt,
+                     tmp_key);
+  E2V2_LAUNCHED("k_col_fill");
+  const int cap = 256;
+  hipLaunchKernelGGL(k_sort_cols, dim3(n_rows), dim3(64), seg_lds_bytes(cap), s, row_ptr, tmp_key, alpha_index, cap);
+  E2V2_LAUNCHED("k_sort_cols");
+  hipLaunchKernelGGL(k_gather_i32, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, other_index, alpha_index,
+                     n_edges, col_index);
+  E2V2_LAUNCHED("k_gather_i32");
+  return 0;
+}
+
+static int check_pair_plan(const e2v2_pair_plan* P) {
+  E2V2_REQUIRE(P != nullptr, "pair search: null plan");
+  E2V2_REQUIRE(P->n_query >= 0 && P->n_graphs >= 0 && P->l2 >= 0 && P->n_flat >= 0,
+               "pair search: negative size (queries %d, graphs %d, l2 %d, flat %d)", P->n_query, P->n_graphs, P->l2,
+               P->n_flat);
+  E2V2_REQUIRE(P->poly == 0 || P->poly == 1, "pair search: envelope kind %d (0 polynomial, 1 bell)", P->poly);
+  E2V2_REQUIRE(P->n_query == 0 || (P->qpos && P->qgraph && P->n_graphs > 0), "pair search: null query arrays");
+  E2V2_REQUIRE(P->l2 == 0 || P->spos, "pair search: null source positions");
+  return 0;
+}
+
+E2V2_API int e2v2_pair_count(const e2v2_pair_plan* plan, int32_t* row_count, int32_t* row_ptr, int32_t* stats,
+                             hipStream_t s) {
+  if (int rc = check_pair_plan(plan)) return rc;
+  E2V2_REQUIRE(row_ptr && stats && (row_count || plan->n_query == 0), "pair_count: null output");
+  const e2v2_pair_plan& P = *plan;
+  if (P.n_query > 0) {
+    hipLaunchKernelGGL(k_pair_count, dim3(blocks_for(P.n_query, kNbrWaves)), dim3(64 * kNbrWaves), 0, s, P,
+                       row_count);
+    E2V2_LAUNCHED("k_pair_count");
+  }
+  hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, row_count, P.n_query, row_ptr, stats);
+  E2V2_LAUNCHED("k_scan_i32");
+  return 0;
+}
+
+E2V2_API int e2v2_pair_emit(const e2v2_pair_plan* plan, const int32_t* row_ptr, int64_t n_pairs, int max_row,
+                            const int32_t* new_ptr, uint64_t* tmp_key, int64_t* query_idx, int64_t* neighbor_idx,
+                            float* edge_vec, float* dist, float* poly, hipStream_t s) {
+  if (int rc = check_pair_plan(plan)) return rc;
+  const e2v2_pair_plan& P = *plan;
+  E2V2_REQUIRE(n_pairs >= 0 && n_pairs < (1ll << 31) && max_row >= 0, "pair_emit: bad sizes (%lld pairs, row %d)",
+               (long long)n_pairs, max_row);
+  if (n_pairs == 0 || P.n_query == 0) return 0;
+  E2V2_REQUIRE(P.n_flat > 0 && P.sflat && P.sbase, "pair_emit: pairs found but no flattened source nodes");
+  E2V2_REQUIRE(row_ptr && new_ptr && tmp_key && query_idx && neighbor_idx && edge_vec && dist && poly,
+               "pair_emit: null pointer");
+  hipLaunchKernelGGL(k_pair_fill, dim3(blocks_for(P.n_query, kNbrWaves)), dim3(64 * kNbrWaves), 0, s, P, row_ptr,
+                     tmp_key);
+  E2V2_LAUNCHED("k_pair_fill");
+  const int cap = seg_cap(max_row);
+  hipLaunchKernelGGL(k_pair_emit, dim3(P.n_query), dim3(64), seg_lds_bytes(cap), s, P, row_ptr, new_ptr, tmp_key,
+                     cap, query_idx, neighbor_idx, edge_vec, dist, poly);
+  E2V2_LAUNCHED("k_pair_emit");
+  return 0;
 }

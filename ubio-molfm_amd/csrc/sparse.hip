@@ -1,0 +1,243 @@
+// Segment (CSR) kernels behind the reference's op-level sparse edge functions
+// (src/molfm/models/e2former/triton_dr/): edge-indexed dot products, their
+// grouped reductions (the QK logits, the value aggregation and both of their
+// gradients), the segmented alpha sum, row gathers and the edge-degree outer
+// product with its gradient.  A segment layout is the reference's
+// (row_ptr [R+1], col_index, alpha_index): slot p of row r carries edge
+// alpha_index[p] and its partner row col_index[p].  Every row is summed in
+// slot order by one workgroup (deterministic, no atomics).  Tensors are fp32
+// with explicit element strides, so [R, H, D] and [M, C, H] operands share
+// the kernels.  Slots whose partner row or edge id is out of range are skipped
+// and row bounds are clamped to the slot arrays, so malformed metadata cannot
+// make a kernel read or write outside its operands.  The attention and degree
+// paths of the model run fused in attn.hip and deg.hip; these serve callers of
+// the reference's op-level interfaces.
+#include "common.h"
+#include "../../include/e2v2.h"
+
+namespace e2v2 {
+
+constexpr int kSegThreads = 256;
+
+struct SegRow {
+  int p0, p1;
+};
+
+__device__ __forceinline__ SegRow seg_row(const e2v2_segments& S, int r) {
+  const int64_t n = S.n_slots;
+  int64_t a = S.row_ptr[r], b = S.row_ptr[r + 1];
+  a = a < 0 ? 0 : (a > n ? n : a);
+  b = b < a ? a : (b > n ? n : b);
+  return {(int)a, (int)b};
+}
+
+__device__ __forceinline__ bool slot_ok(const e2v2_segments& S, int c, int e) {
+  return c >= 0 && c < S.n_cols && e >= 0 && (int64_t)e < S.n_edges;
+}
+
+// out[alpha_index[p], h] = sum_d A[r, h, d] B[col_index[p], h, d] for the slots p of row r
+__global__ __launch_bounds__(kSegThreads) void k_seg_dot(e2v2_segments S, const float* __restrict__ A, int64_t sa_r,
+                                                         int64_t sa_h, int64_t sa_d, const float* __restrict__ B,
+                                                         int64_t sb_r, int64_t sb_h, int64_t sb_d, int H, int D,
+                                                         float* __restrict__ out, int64_t so_e, int64_t so_h) {
+  const int r = blockIdx.x;
+  const SegRow R = seg_row(S, r);
+  const unsigned n = (unsigned)(R.p1 - R.p0) * (unsigned)H;
+  const float* a = A + (int64_t)r * sa_r;
+  for (unsigned idx = threadIdx.x; idx < n; idx += kSegThreads) {
+    const int p = R.p0 + (int)(idx / (unsigned)H), h = (int)(idx % (unsigned)H);
+    const int c = S.col_index[p], e = S.alpha_index[p];
+    if (!slot_ok(S, c, e)) continue;
+    const float* b = B + (int64_t)c * sb_r + (int64_t)h * sb_h;
+    const float* ah = a + (int64_t)h * sa_h;
+    float s = 0.f;
+    for (int d = 0; d < D; ++d) s = fmaf(ah[d * sa_d], b[d * sb_d], s);
+    out[(int64_t)e * so_e + (int64_t)h * so_h] = s;
+  }
+}
+
+// out[r, h, d] = sum_{p in row r} W[alpha_index[p], h] X[col_index[p], h, d]; X NULL: the plain
+// sum of W (D = 1).  Threads walk (h, d) with the operand's unit-stride index fastest.
+__global__ __launch_bounds__(kSegThreads) void k_seg_reduce(e2v2_segments S, const float* __restrict__ W,
+                                                            int64_t sw_e, int64_t sw_h, const float* __restrict__ X,
+                                                            int64_t sx_r, int64_t sx_h, int64_t sx_d, int H, int D,
+                                                            bool h_fast, float* __restrict__ out, int64_t so_r,
+                                                            int64_t so_h, int64_t so_d) {
+  const int r = blockIdx.x;
+  const SegRow R = seg_row(S, r);
+  for (int idx = threadIdx.x; idx < H * D; idx += kSegThreads) {
+    const int h = h_fast ? idx % H : idx / D, d = h_fast ? idx / H : idx % D;
+    float s = 0.f;
+    for (int p = R.p0; p < R.p1; ++p) {
+      const int e = S.alpha_index[p];
+      if (e < 0 || (int64_t)e >= S.n_edges) continue;
+      const float w = W[(int64_t)e * sw_e + (int64_t)h * sw_h];
+      if (X) {
+        const int c = S.col_index[p];
+        if (c < 0 || c >= S.n_cols) continue;
+        s = fmaf(w, X[(int64_t)c * sx_r + (int64_t)h * sx_h + (int64_t)d * sx_d], s);
+      } else {
+        s += w;
+      }
+    }
+    out[(int64_t)r * so_r + (int64_t)h * so_h + (int64_t)d * so_d] = s;
+  }
+}
+
+// out[e, k] = in[index[e], k] (rows of K contiguous floats; an index outside [0, n_in) gives a zero row)
+__global__ void k_gather_rows(const float* __restrict__ in, int64_t n_in, const int32_t* __restrict__ index,
+                              int64_t n, int K, float* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * K) return;
+  const int64_t e = t / K;
+  const int64_t i = index[e];
+  out[t] = (i >= 0 && i < n_in) ? in[i * K + t % K] : 0.f;
+}
+
+// out[r, l, h] = sum_{p in row r} sh[e, l] fea[e, h], e = alpha_index[p]
+__global__ __launch_bounds__(kSegThreads) void k_outer_reduce(e2v2_segments S, const float* __restrict__ sh,
+                                                              const float* __restrict__ fea, int L, int H,
+                                                              float* __restrict__ out) {
+  const int r = blockIdx.x;
+  const SegRow R = seg_row(S, r);
+  for (int idx = threadIdx.x; idx < L * H; idx += kSegThreads) {
+    const int l = idx / H, h = idx % H;
+    float s = 0.f;
+    for (int p = R.p0; p < R.p1; ++p) {
+      const int64_t e = S.alpha_index[p];
+      if (e < 0 || e >= S.n_edges) continue;
+      s = fmaf(sh[e * L + l], fea[e * H + h], s);
+    }
+    out[(int64_t)r * L * H + idx] = s;
+  }
+}
+
+// dsh[e, l] = sum_h g[q[e], l, h] fea[e, h]  (q[e] outside [0, n_rows): 0)
+__global__ void k_outer_dsh(const float* __restrict__ g, int n_rows, const float* __restrict__ fea,
+                            const int32_t* __restrict__ qidx, int64_t n_edges, int L, int H, float* __restrict__ dsh) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_edges * L) return;
+  const int64_t e = t / L;
+  const int l = (int)(t % L);
+  const int q = qidx[e];
+  float s = 0.f;
+  if (q >= 0 && q < n_rows) {
+    const float* gr = g + ((int64_t)q * L + l) * H;
+    const float* f = fea + e * H;
+    for (int h = 0; h < H; ++h) s = fmaf(gr[h], f[h], s);
+  }
+  dsh[t] = s;
+}
+
+// dfea[e, h] = sum_l g[q[e], l, h] sh[e, l]  (q[e] outside [0, n_rows): 0)
+__global__ void k_outer_dfea(const float* __restrict__ g, int n_rows, const float* __restrict__ sh,
+                             const int32_t* __restrict__ qidx, int64_t n_edges, int L, int H,
+                             float* __restrict__ dfea) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_edges * H) return;
+  const int64_t e = t / H;
+  const int h = (int)(t % H);
+  const int q = qidx[e];
+  float s = 0.f;
+  if (q >= 0 && q < n_rows) {
+    const float* gr = g + (int64_t)q * L * H + h;
+    const float* s_e = sh + e * L;
+    for (int l = 0; l < L; ++l) s = fmaf(gr[(int64_t)l * H], s_e[l], s);
+  }
+  dfea[t] = s;
+}
+
+static inline unsigned blocks_of(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+static int check_segments(const e2v2_segments* S, bool need_col, const char* what) {
+  E2V2_REQUIRE(S != nullptr, "%s: null segment layout", what);
+  E2V2_REQUIRE(S->n_rows >= 0 && S->n_slots >= 0 && S->n_edges >= 0 && S->n_cols >= 0,
+               "%s: negative size (rows %d, cols %d, slots %lld, edges %lld)", what, S->n_rows, S->n_cols,
+               (long long)S->n_slots, (long long)S->n_edges);
+  E2V2_REQUIRE(S->n_slots < (1ll << 31), "%s: %lld slots exceed the 32-bit slot index", what,
+               (long long)S->n_slots);
+  E2V2_REQUIRE(S->n_rows == 0 || S->row_ptr, "%s: null row_ptr", what);
+  E2V2_REQUIRE(S->n_slots == 0 || (S->alpha_index && (!need_col || S->col_index)),
+               "%s: null col_index / alpha_index", what);
+  return 0;
+}
+
+}  // namespace e2v2
+
+using namespace e2v2;
+
+E2V2_API int e2v2_seg_dot(const e2v2_segments* S, const float* A, const int64_t* a_strides, const float* B,
+                          const int64_t* b_strides, int H, int D, float* out, const int64_t* out_strides,
+                          hipStream_t s) {
+  if (int rc = check_segments(S, true, "seg_dot")) return rc;
+  E2V2_REQUIRE(H >= 1 && D >= 1 && a_strides && b_strides && out_strides, "seg_dot: bad sizes (H %d, D %d)", H, D);
+  if (S->n_rows == 0 || S->n_slots == 0) return 0;
+  E2V2_REQUIRE(A && B && out, "seg_dot: null operand");
+  E2V2_REQUIRE((int64_t)S->n_slots * H < (1ll << 32), "seg_dot: rows of up to 2^32 / H slots");
+  hipLaunchKernelGGL(k_seg_dot, dim3(S->n_rows), dim3(kSegThreads), 0, s, *S, A, a_strides[0], a_strides[1],
+                     a_strides[2], B, b_strides[0], b_strides[1], b_strides[2], H, D, out, out_strides[0],
+                     out_strides[1]);
+  E2V2_LAUNCHED("k_seg_dot");
+  return 0;
+}
+
+E2V2_API int e2v2_seg_reduce(const e2v2_segments* S, const float* W, const int64_t* w_strides, const float* X,
+                             const int64_t* x_strides, int H, int D, float* out, const int64_t* out_strides,
+                             hipStream_t s) {
+  if (int rc = check_segments(S, X != nullptr, "seg_reduce")) return rc;
+  E2V2_REQUIRE(H >= 1 && D >= 1 && (int64_t)H * D < (1ll << 31) && w_strides && out_strides &&
+                   (X == nullptr || x_strides),
+               "seg_reduce: bad sizes (H %d, D %d)", H, D);
+  E2V2_REQUIRE(X != nullptr || D == 1, "seg_reduce: a plain sum (X NULL) has D = 1");
+  if (S->n_rows == 0) return 0;
+  E2V2_REQUIRE(W && out, "seg_reduce: null operand");
+  const int64_t z = 0;
+  const bool h_fast = X ? (x_strides[1] <= x_strides[2]) : true;
+  hipLaunchKernelGGL(k_seg_reduce, dim3(S->n_rows), dim3(kSegThreads), 0, s, *S, W, w_strides[0], w_strides[1], X,
+                     X ? x_strides[0] : z, X ? x_strides[1] : z, X ? x_strides[2] : z, H, D, h_fast, out,
+                     out_strides[0], out_strides[1], out_strides[2]);
+  E2V2_LAUNCHED("k_seg_reduce");
+  return 0;
+}
+
+E2V2_API int e2v2_gather_rows(const float* in, int64_t n_in, const int32_t* index, int64_t n, int K, float* out,
+                              hipStream_t s) {
+  E2V2_REQUIRE(n >= 0 && n_in >= 0 && K >= 1, "gather_rows: bad sizes (n %lld, K %d)", (long long)n, K);
+  if (n == 0) return 0;
+  E2V2_REQUIRE(in && index && out, "gather_rows: null pointer");
+  hipLaunchKernelGGL(k_gather_rows, dim3(blocks_of(n * K, 256)), dim3(256), 0, s, in, n_in, index, n, K, out);
+  E2V2_LAUNCHED("k_gather_rows");
+  return 0;
+}
+
+E2V2_API int e2v2_outer_reduce(const e2v2_segments* S, const float* sh, const float* fea, int L, int H, float* out,
+                               hipStream_t s) {
+  if (int rc = check_segments(S, false, "outer_reduce")) return rc;
+  E2V2_REQUIRE(L >= 1 && H >= 1 && (int64_t)L * H < (1ll << 31), "outer_reduce: bad sizes (L %d, H %d)", L, H);
+  if (S->n_rows == 0) return 0;
+  E2V2_REQUIRE(sh && fea && out, "outer_reduce: null operand");
+  hipLaunchKernelGGL(k_outer_reduce, dim3(S->n_rows), dim3(kSegThreads), 0, s, *S, sh, fea, L, H, out);
+  E2V2_LAUNCHED("k_outer_reduce");
+  return 0;
+}
+
+E2V2_API int e2v2_outer_bwd(const float* grad, int n_rows, const float* sh, const float* fea,
+                            const int32_t* query_index, int64_t n_edges, int L, int H, float* dsh, float* dfea,
+                            hipStream_t s) {
+  E2V2_REQUIRE(n_rows >= 0 && n_edges >= 0 && L >= 1 && H >= 1, "outer_bwd: bad sizes (E %lld, L %d, H %d)",
+               (long long)n_edges, L, H);
+  if (n_edges == 0) return 0;
+  E2V2_REQUIRE(grad && query_index && (dsh == nullptr || fea) && (dfea == nullptr || sh),
+               "outer_bwd: null operand");
+  if (dsh) {
+    hipLaunchKernelGGL(k_outer_dsh, dim3(blocks_of(n_edges * L, 256)), dim3(256), 0, s, grad, n_rows, fea,
+                       query_index, n_edges, L, H, dsh);
+    E2V2_LAUNCHED("k_outer_dsh");
+  }
+  if (dfea) {
+    hipLaunchKernelGGL(k_outer_dfea, dim3(blocks_of(n_edges * H, 256)), dim3(256), 0, s, grad, n_rows, sh,
+                       query_index, n_edges, L, H, dfea);
+    E2V2_LAUNCHED("k_outer_dfea");
+  }
+  return 0;
+}

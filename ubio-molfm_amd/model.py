@@ -22,7 +22,7 @@ import torch
 from torch import nn
 
 from . import _lib
-from .modules import E2former, EdgeContext, parse_irreps
+from .modules import E2former, EdgeContext, atom_type_slots, parse_irreps
 from .neighbors import build_neighbors
 from .ops import EdgeGeometryFn
 
@@ -113,13 +113,7 @@ class E2FormerBackbone(nn.Module):
         cached = self._types
         if cached is not None and cached[0]() is Z and cached[1] == Z._version:
             return cached[2]
-        zs = torch.unique(Z.long())
-        key = tuple(int(z) for z in zs.cpu())
-        if key and (key[0] < 0 or key[-1] > 255):
-            raise ValueError(f"atomic numbers must lie in [0, 255], got {key[0]}..{key[-1]}")
-        lut = torch.zeros(256, dtype=torch.int32, device=Z.device)
-        lut[zs] = torch.arange(len(key), dtype=torch.int32, device=Z.device)
-        out = (zs.to(torch.int32).contiguous(), key, lut[Z.long()].contiguous())
+        out = atom_type_slots(Z)
         self._types = (weakref.ref(Z), Z._version, out)
         return out
 

@@ -853,6 +853,52 @@ class EdgeContext:
         self.bf16 = bf16          # bf16 GEMM operands, fp32 accumulation and storage
 
 
+def atom_type_slots(Z: torch.Tensor):
+    """(type_z [T] int32: the atomic numbers present, ascending; type_key: the
+    same as a host tuple; slot [N] int32: each atom's index into type_z).  One
+    host read."""
+    zs = torch.unique(Z.long())
+    key = tuple(int(z) for z in zs.cpu())
+    if key and (key[0] < 0 or key[-1] > 255):
+        raise ValueError(f"atomic numbers must lie in [0, 255], got {key[0]}..{key[-1]}")
+    lut = torch.zeros(256, dtype=torch.int32, device=Z.device)
+    lut[zs] = torch.arange(len(key), dtype=torch.int32, device=Z.device)
+    return zs.to(torch.int32).contiguous(), key, lut[Z.long()].contiguous()
+
+
+_REF_CTX_KEY = "_e2v2_edge_context"
+
+
+def reference_edge_context(batched_data, edge_vec, edge_dis, atomic_numbers, rbf, rc: float,
+                           bf16: bool = False) -> EdgeContext:
+    """EdgeContext from the per-forward edge inputs of the reference's layers:
+    batched_data's construct_radius_neighbor dict (query_idx, neighbor_idx,
+    metadata) and f_outcell_index (expanded node -> atom), the edge vectors and
+    distances (f_edge_vec, f_dist; gradients flow back to them), the flattened
+    atomic numbers, the E2former's GaussianSmearing and cutoff.  Edges are taken
+    in query-row order (the metadata's q_alpha_index, the identity for the
+    reference's sorted lists).  Built once per batched_data and reused by every
+    layer (kept in batched_data under "_e2v2_edge_context")."""
+    ent = batched_data.get(_REF_CTX_KEY)
+    if ent is not None and ent[0] is batched_data["query_idx"] and ent[1] is edge_vec and ent[2] is edge_dis \
+            and ent[3] is atomic_numbers:
+        return ent[4]
+    from .neighbors import neighbor_list_from_edges
+    md = batched_data["metadata"]
+    if len(md) != 6:
+        raise ValueError("metadata must be a 6-tuple from prepare_sparse_qk_edge_index_metadata")
+    order = md[2].long()
+    src = batched_data["f_outcell_index"].long()[batched_data["neighbor_idx"].long().index_select(0, order)]
+    dvec = edge_vec.index_select(0, order).float()
+    dist = edge_dis.reshape(-1).index_select(0, order).float()
+    N = int(atomic_numbers.shape[0])
+    nl = neighbor_list_from_edges(md[0], src, dvec, dist, N)
+    type_z, type_key, slot = atom_type_slots(atomic_numbers)
+    ctx = EdgeContext(nl, dvec, dist, slot, type_z, type_key, rbf, float(rc), bf16)
+    batched_data[_REF_CTX_KEY] = (batched_data["query_idx"], edge_vec, edge_dis, atomic_numbers, ctx)
+    return ctx
+
+
 class E2AttentionArbOrder_sparse(nn.Module):
     """e2former.py:80-436 for tp_type=QK_alpha, attn_type=so2-first-order."""
 
@@ -902,7 +948,45 @@ class E2AttentionArbOrder_sparse(nn.Module):
             return pv.weight.detach()[:, P, :].contiguous(), pv.bias.detach()[P].contiguous()
         return cached(self, "v_sliced", (pv.weight, pv.bias), build)
 
-    def forward(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
+    def bind_edge_basis(self, rbf, max_radius: float):
+        """The E2former's GaussianSmearing and cutoff, for calls with the
+        reference's signature (attn_weight = rbf(edge_dis) is evaluated inside
+        the kernels from the distance, as is poly_dist)."""
+        self._edge_basis = (rbf, float(max_radius))
+        return self
+
+    def forward(self, *args, **kwargs):
+        """forward(x [9, N, C], ctx: EdgeContext, res=None) -> [9, N, C] (the fused
+        path of this package), or the reference's signature (e2former.py:223-236)
+        -> (node_output [N, 9, C], attn_weight)."""
+        if len(args) >= 2 and isinstance(args[1], EdgeContext):
+            return self.forward_fused(*args, **kwargs)
+        return self.forward_reference(*args, **kwargs)
+
+    def forward_reference(self, node_pos, node_irreps_input, edge_dis, edge_vec, attn_weight, atomic_numbers,
+                          poly_dist=None, attn_mask=None, batch=None, batched_data=None, rbf=None, max_radius=None,
+                          **kwargs):
+        """E2AttentionArbOrder_sparse.forward (e2former.py:223-436) with its
+        arguments: node_irreps_input [N, 9, C]; batched_data holds query_idx,
+        neighbor_idx, metadata and f_outcell_index; edge_vec / edge_dis are
+        f_edge_vec / f_dist.  attn_weight must be rbf(edge_dis) and poly_dist
+        polynomial(edge_dis, max_radius), both re-evaluated inside the kernels from
+        the distance; rbf and max_radius come from the keywords or
+        bind_edge_basis.  Returns (node_output [N, 9, C], attn_weight)."""
+        if batched_data is None:
+            raise ValueError("batched_data with the neighbour dict is required")
+        if rbf is None or max_radius is None:
+            basis = getattr(self, "_edge_basis", None)
+            if basis is None:
+                raise ValueError("pass rbf= and max_radius= (the E2former's GaussianSmearing and cutoff) or call "
+                                 "bind_edge_basis(rbf, max_radius) once")
+            rbf, max_radius = basis
+        ctx = reference_edge_context(batched_data, edge_vec, edge_dis, atomic_numbers, rbf, max_radius)
+        x = node_irreps_input.float().transpose(0, 1).contiguous()
+        out = self.forward_fused(x, ctx)
+        return out.transpose(0, 1).contiguous(), attn_weight
+
+    def forward_fused(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
         """x [9, N, C] (m-major) -> attention(x) (+ res when given), [9, N, C].
         v, the attention rows and their gradients run in the kernels' slice order
         of channels: the permutation is folded into proj_value (output rows) and
@@ -984,7 +1068,35 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
         self.proj = SO3_Linear_e2former(2 * C, C, lmax=lmax)
         self._radial = RadialCache()
 
-    def forward(self, ctx: EdgeContext):
+    def forward(self, *args, **kwargs):
+        """forward(ctx: EdgeContext) -> [9, N, C] (the fused path of this package), or
+        the reference's signature (e2former.py:689-753) -> node_features [N, 9, C]."""
+        if len(args) == 1 and isinstance(args[0], EdgeContext) and not kwargs:
+            return self.forward_fused(args[0])
+        if not args and isinstance(kwargs.get("ctx"), EdgeContext):
+            return self.forward_fused(kwargs["ctx"])
+        return self.forward_reference(*args, **kwargs)
+
+    def forward_reference(self, node_input, node_pos, edge_dis, atomic_numbers, edge_vec, batched_data,
+                          attn_mask=None, poly_dist=None, edge_scalars=None, rbf=None, max_radius=None, **kwargs):
+        """EdgeDegreeEmbeddingNetwork_higherorder.forward (e2former.py:689-753) with
+        its arguments; edge_scalars must be rbf(edge_dis) and poly_dist
+        polynomial(edge_dis, cutoff), both evaluated inside the kernels.  rbf
+        defaults to GaussianSmearing(number_of_basis, cutoff, 2), the E2former's
+        own (e2former.py:831-834), max_radius to this module's cutoff."""
+        if rbf is None:
+            rbf = getattr(self, "_default_rbf", None)
+            if rbf is None or rbf.offset.device != edge_dis.device:
+                rbf = GaussianSmearing(self.number_of_basis, cutoff=self.cutoff, basis_width_scalar=2.0)
+                rbf = rbf.to(edge_dis.device)
+                self._default_rbf = rbf
+        rc = self.cutoff if max_radius is None else float(max_radius)
+        ctx = reference_edge_context(batched_data, edge_vec, edge_dis, atomic_numbers, rbf, rc)
+        if int(node_input.shape[0]) != ctx.nl.n_atoms:
+            raise ValueError(f"node_input has {node_input.shape[0]} rows for {ctx.nl.n_atoms} atoms")
+        return self.forward_fused(ctx).transpose(0, 1).contiguous()
+
+    def forward_fused(self, ctx: EdgeContext):
         table = self._radial.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
                                  ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="deg")
         # the edge spherical harmonics ("e3nn sph") are formed inside the degree kernels

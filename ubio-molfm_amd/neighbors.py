@@ -104,6 +104,10 @@ def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
 
+def _vp(t: Optional[torch.Tensor]):
+    return None if t is None or t.numel() == 0 else _lib.vp(t.data_ptr())
+
+
 def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
               cells_per_direction: int = 4, grid_box=None, workspace: bool = True):
     """The e2v2_nbr_plan of a batch (pos [N,3] fp32 on the GPU, graphs contiguous;
@@ -295,3 +299,152 @@ def count_neighbors_noalloc(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float
               _lib.vp(row_ptr.data_ptr()), _lib.vp(stats.data_ptr()),
               _lib.vp(torch.cuda.current_stream(pos.device).cuda_stream))
     return row_count[:N], row_ptr, stats
+
+
+def construct_radius_neighbor(node_pos, node_mask, expand_node_pos, expand_node_mask, max_dist, include_mask=None,
+                              min_dist=-1, max_neighbors=None, error_check=False, poly="poly", toy_config=None):
+    """The reference's padded-batch neighbour search with its signature and
+    output dict (module_utils.py:3119-3242), on the HIP pair kernels.
+
+    node_pos [B, L, 3], node_mask [B, L] (True = atom), expand_node_pos
+    [B, L2, 3], expand_node_mask [B, L2], include_mask [B, L2] or None.  Query
+    q is the q-th real atom (node_pos[node_mask]); it meets every padded
+    expanded position of its batch row (padding included, as in the
+    reference, whose callers place padding at 999 A).  Pairs with
+    min_dist <= d <= max_dist (and included) are kept, each row sorted by
+    (d, expanded slot) and cut to topK = max(min(L2, max_neighbors, longest
+    row), 1).  Returns query_idx, neighbor_idx (int64, the index into
+    expand_node_pos[expand_node_mask], clamped to its last row), metadata
+    (the 6-tuple of prepare_sparse_qk_edge_index_metadata), f_edge_vec
+    (node_pos[q] - the indexed expanded node), f_dist, f_poly_dist
+    (polynomial(d, max_dist), or smooth_polynomial_bell(d, min_dist, max_dist)
+    for poly="poly_bell").  Positions are evaluated in fp32 with d =
+    sqrt((dx dx + dy dy) + dz dz).  toy_config {"prob": p} drops each kept
+    edge with probability p (the reference's random attention mask, drawn per
+    edge here).  A batch with no real atom raises, as the reference's max over
+    an empty selection does."""
+    from .sparse_ops import prepare_sparse_qk_edge_index_metadata
+    import logging
+
+    if poly not in ("poly", "poly_bell"):
+        raise ValueError("sorry, you must set poly or poly_bell")
+    for t in (node_pos, expand_node_pos):
+        if not t.is_cuda:
+            raise RuntimeError("construct_radius_neighbor runs on the GPU only (HIP library, no CPU path)")
+    dev = node_pos.device
+    B, L = node_pos.shape[:2]
+    L2 = expand_node_pos.shape[1]
+    node_mask = node_mask.to(torch.bool)
+    expand_node_mask = expand_node_mask.to(torch.bool)
+    if tuple(node_mask.shape) != (B, L) or tuple(expand_node_mask.shape) != (B, L2) \
+            or expand_node_pos.shape[0] != B:
+        raise ValueError(f"shapes: node_pos {tuple(node_pos.shape)}, node_mask {tuple(node_mask.shape)}, "
+                         f"expand_node_pos {tuple(expand_node_pos.shape)}, "
+                         f"expand_node_mask {tuple(expand_node_mask.shape)}")
+    pos32 = node_pos.detach().to(torch.float32)
+    qpos = pos32[node_mask].contiguous()
+    qgraph = node_mask.nonzero()[:, 0].to(torch.int32).contiguous()
+    N = qpos.shape[0]
+    if N == 0:
+        raise RuntimeError("construct_radius_neighbor: node_mask selects no atom")
+    spos = expand_node_pos.detach().to(torch.float32).contiguous()
+    sflat = spos[expand_node_mask].contiguous()
+    n_flat = sflat.shape[0]
+    expand_ptr = torch.zeros(B + 1, dtype=torch.int64, device=dev)
+    expand_ptr[1:] = torch.cumsum(expand_node_mask.sum(-1), 0)
+    sbase = expand_ptr[:B].to(torch.int32).contiguous()
+    inc = None
+    if include_mask is not None:
+        inc = include_mask.to(torch.bool).reshape(B, L2).to(torch.uint8).contiguous()
+    plan = _lib.PairPlan(N, B, L2, n_flat, float(max_dist), float(min_dist), 0 if poly == "poly" else 1,
+                         _vp(qpos), _vp(qgraph), _vp(spos), _vp(inc), _vp(sbase), _vp(sflat))
+    stream = _lib.vp(torch.cuda.current_stream(dev).cuda_stream)
+    i32 = dict(dtype=torch.int32, device=dev)
+    row_count = torch.empty(N, **i32)
+    row_ptr = torch.empty(N + 1, **i32)
+    stats = torch.zeros(3, **i32)
+    _lib.call("e2v2_pair_count", _lib.C.byref(plan), _vp(row_count), _vp(row_ptr), _vp(stats), stream)
+    n_pairs, longest = (int(x) for x in stats[:2].cpu())
+    top_k = max(min(L2, longest) if max_neighbors is None else min(L2, int(max_neighbors), longest), 1)
+    new_ptr, E = row_ptr, n_pairs
+    if top_k < longest:
+        cnt = torch.empty(N, **i32)
+        new_ptr = torch.empty(N + 1, **i32)
+        _lib.call("e2v2_nbr_topk", _vp(row_ptr), _lib.i32(N), _lib.i32(top_k), _vp(cnt), _vp(new_ptr),
+                  _vp(stats), None, None, None, None, None, None, None, None, _lib.i32(0), stream)
+        E = int(stats[0].item())
+    query_idx = torch.empty(E, dtype=torch.int64, device=dev)
+    neighbor_idx = torch.empty(E, dtype=torch.int64, device=dev)
+    f_edge_vec = torch.empty(E, 3, dtype=torch.float32, device=dev)
+    f_dist = torch.empty(E, dtype=torch.float32, device=dev)
+    f_poly = torch.empty(E, dtype=torch.float32, device=dev)
+    if E > 0:
+        tkey = torch.empty(n_pairs, dtype=torch.int64, device=dev)
+        _lib.call("e2v2_pair_emit", _lib.C.byref(plan), _vp(row_ptr), _lib.i64(n_pairs), _lib.i32(longest),
+                  _vp(new_ptr), _vp(tkey), _vp(query_idx), _vp(neighbor_idx), _vp(f_edge_vec), _vp(f_dist),
+                  _vp(f_poly), stream)
+    if toy_config is not None and E > 0:
+        keep = torch.rand(E, device=dev) >= float(toy_config.get("prob", 0))
+        query_idx, neighbor_idx = query_idx[keep].contiguous(), neighbor_idx[keep].contiguous()
+        f_edge_vec, f_dist, f_poly = f_edge_vec[keep].contiguous(), f_dist[keep].contiguous(), f_poly[keep].contiguous()
+    if error_check:
+        log = logging.getLogger(__name__)
+        if f_dist.numel() and torch.max(torch.linalg.norm(f_edge_vec, dim=-1) - f_dist) != 0:
+            log.error("Please verify your code, neighbor selection error happened")
+        if torch.sum(node_pos[~node_mask] == 0):
+            log.warning("node padding part is zero, will lead to some neighbor dist sort error")
+        if torch.sum(expand_node_pos[~expand_node_mask] == 0):
+            log.warning("expand_node_pos padding part is zero, will lead to some neighbor dist sort error")
+    return {
+        "query_idx": query_idx,
+        "neighbor_idx": neighbor_idx,
+        "metadata": prepare_sparse_qk_edge_index_metadata(query_idx, neighbor_idx, N, n_flat),
+        "f_edge_vec": f_edge_vec,
+        "f_dist": f_dist,
+        "f_poly_dist": f_poly,
+    }
+
+
+def neighbor_list_from_edges(row_ptr: torch.Tensor, src_atom: torch.Tensor, dvec: torch.Tensor, dist: torch.Tensor,
+                             n_atoms: int, clusters: bool = True) -> NeighborList:
+    """A NeighborList over an edge list already in query-row order (row_ptr
+    [n_atoms + 1] int32, the source atom of every edge, its dvec [E,3] and
+    dist [E]), for callers that bring their own edges (the reference's
+    construct_radius_neighbor dict): key CSR by source atom (edges of each
+    column in edge order) and the column clusters of the attention backward
+    built on the GPU.  Shifts are not tracked (shift_idx zero)."""
+    dev = dvec.device
+    N = int(n_atoms)
+    E = int(src_atom.shape[0])
+    i32 = dict(dtype=torch.int32, device=dev)
+    row_ptr = row_ptr.to(torch.int32).contiguous()
+    col = src_atom.to(torch.int32).contiguous()
+    dvec = dvec.detach().to(torch.float32).contiguous()
+    dist = dist.detach().to(torch.float32).contiguous()
+    if row_ptr.numel() != N + 1 or dvec.shape != (E, 3) or dist.shape != (E,):
+        raise ValueError(f"edge list shapes: row_ptr {tuple(row_ptr.shape)} for {N} atoms, dvec {tuple(dvec.shape)}, "
+                         f"dist {tuple(dist.shape)}, {E} edges")
+    if E > 0:   # the CSR kernels index with these: one host read to check them
+        lo, hi, p0, pe, bad = (int(x) for x in torch.stack([
+            col.min(), col.max(), row_ptr[0], row_ptr[-1], (row_ptr[1:] < row_ptr[:-1]).sum().to(torch.int32)]).cpu())
+        if lo < 0 or hi >= N or p0 != 0 or pe != E or bad:
+            raise ValueError(f"edge list: source atoms in [{lo}, {hi}] for {N} atoms, row_ptr from {p0} to {pe} "
+                             f"for {E} edges, {bad} decreasing steps")
+    stream = _lib.vp(torch.cuda.current_stream(dev).cuda_stream)
+    stats = torch.zeros(3, **i32)
+    edge_row = torch.empty(E, **i32)
+    key_cnt = torch.empty(max(N, 1), **i32)
+    key_ptr = torch.empty(N + 1, **i32)
+    key_eid = torch.empty(E, **i32)
+    tkey = torch.empty(max(E, 1), dtype=torch.int64, device=dev)
+    for phase in (0, 1):
+        _lib.call("e2v2_csr_transpose", _vp(row_ptr), _vp(col), _lib.i32(N), _lib.i32(N), _lib.i64(E),
+                  _vp(edge_row), _vp(key_cnt), _vp(key_ptr), _vp(stats), _vp(tkey) if phase else None,
+                  _vp(key_eid) if phase else None, _lib.i32(phase), stream)
+    nl = NeighborList(N, E, row_ptr, col, torch.zeros(E, **i32), torch.zeros(1, 3, dtype=torch.int32), dvec, dist,
+                      edge_row, key_ptr, key_eid, 0)
+    if clusters and N > 0 and E > 0:
+        nl.col_span = COL_SPAN
+        nl.col_slot_member, nl.col_slot_edge, nl.col_n_slots = cluster_slots(key_ptr, N, edge_row, key_eid,
+                                                                             COL_SPAN)
+    return nl
