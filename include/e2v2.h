@@ -246,8 +246,8 @@ typedef struct e2v2_radial_net {
   const float* src;                   /* [n_types_max][n_emb] source atom embedding             */
 } e2v2_radial_net;
 
-/* Node spacing h = 2^(floor(log2(0.2 sigma)) - refine) of a GaussianSmearing basis exp(coeff (d - mu)^2)
-   (sigma = sqrt(-0.5 / coeff)) and the node count covering [0, rc]. */
+/* Node spacing h = 2^(floor(log2(0.2 sigma)) - refine) (-3 <= refine <= 6) of a GaussianSmearing basis
+   exp(coeff (d - mu)^2) (sigma = sqrt(-0.5 / coeff)) and the node count covering [0, rc]. */
 int e2v2_radial_table_size(float rc, float rbf_coeff, int32_t refine, int32_t* n_nodes, float* h);
 /* Position of output channel o (0..255) of a profile in a table row:
    pos = col0 + ((o % split) / block) * block_stride + (o / split) * split_stride + o % block

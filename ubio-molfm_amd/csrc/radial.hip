@@ -291,8 +291,8 @@ static int check_net(const e2v2_radial_net* W, const char* who) {
 }
 
 E2V2_API int e2v2_radial_table_size(float rc, float rbf_coeff, int32_t refine, int32_t* n_nodes, float* h) {
-  E2V2_REQUIRE(rc > 0.f && rbf_coeff < 0.f && n_nodes && h && refine >= 0 && refine <= 6,
-               "radial_table_size: need rc > 0, rbf_coeff < 0, 0 <= refine <= 6");
+  E2V2_REQUIRE(rc > 0.f && rbf_coeff < 0.f && n_nodes && h && refine >= -3 && refine <= 6,
+               "radial_table_size: need rc > 0, rbf_coeff < 0, -3 <= refine <= 6");
   const double sigma = std::sqrt(-0.5 / (double)rbf_coeff);
   const double hh = std::ldexp(1.0, (int)std::floor(std::log2(0.2 * sigma)) - refine);
   const double n = std::floor((double)rc / hh) + 2.0;

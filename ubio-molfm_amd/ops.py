@@ -50,9 +50,12 @@ class RadialTable:
     profile (an attention layer's fc_easy, 256 channels gate | inputhead) or the
     degree embedding's three (768 channels).  Built in float64 on the device
     (e2v2_radial_table), then checked at every interval midpoint against the
-    float64 profile (e2v2_radial_table_check); the node spacing is halved until
-    the interpolation error is at most ``tol_value`` of the largest |f| and
-    ``tol_deriv`` of the largest |f'| (one host readback per build).
+    float64 profile (e2v2_radial_table_check); starting from the spacing of
+    ``min_refine`` (-1: 2^(floor(log2(0.2 sigma)) + 1), 0.0156 A for the 256-basis
+    RBF at 6 A) the node spacing is halved until the interpolation error is at
+    most ``tol_value`` of the largest |f| and ``tol_deriv`` of the largest |f'|
+    (one host readback per build).  The coarsest passing table keeps the edge
+    kernels' table reads in L2.
 
     ``layout`` places the channels: "plain" (rows [pairs][nodes][4][nc], profile
     m at 256 m + c), "attn" (one fc_easy profile in the attention kernels' slice
@@ -69,7 +72,7 @@ class RadialTable:
 
     def __init__(self, nets, tgt: nn.Embedding, src: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
                  rc: float, type_z: torch.Tensor, tol_value: float = 1e-6, tol_deriv: float = 1e-5,
-                 max_refine: int = 3, layout: str = "plain"):
+                 max_refine: int = 3, layout: str = "plain", min_refine: int = -1):
         dev = type_z.device
         if layout not in self.LAYOUTS or (layout == "attn" and len(nets) != 1) or (layout == "deg" and len(nets) != 3):
             raise ValueError(f"radial table layout {layout!r} does not fit {len(nets)} profiles")
@@ -85,7 +88,7 @@ class RadialTable:
             self._structs = [self._net(n, tgt_w, src_w) for n in nets]
         self.type_z = type_z.to(torch.int32).contiguous()
         st = _stream(type_z)
-        for refine in range(max_refine + 1):
+        for refine in range(min_refine, max_refine + 1):
             n = _lib.C.c_int32(); h = _lib.C.c_float()
             _lib.call("e2v2_radial_table_size", _lib.f32(rc), _lib.f32(rbf_coeff), _lib.i32(refine), _lib.C.byref(n),
                       _lib.C.byref(h))
