@@ -303,15 +303,23 @@ typedef struct e2v2_attn_args {
   const int32_t* col_slot_member; const int32_t* col_slot_edge; const int32_t* col_n_slots;
 } e2v2_attn_args;
 
-/* v [9][N][C] and out [20][N][C] are m-major (row r of every atom contiguous), channels in slice order;
-   out (float, or bf16 if act_bf16): h_a - h_b rows of the SO(2) product; mrow/srow [N,H] softmax max / sum;
-   cnt [N,H] number of maxima.  gate and inputhead of every edge are interpolated from rtab in the kernel
-   (nothing per edge is stored). */
+/* v [9][N][C] is m-major (row r of every atom contiguous), channels in slice order.  out holds the 20
+   l3-sequential rows h_a - h_b of the SO(2) product (float, or bf16 if act_bf16; 20 N C values, channels in
+   slice order) in the l3-grouped layout: the 2 l3 + 1 rows of output degree l3 keep their cnt coupling
+   paths side by side, a block [2 l3 + 1][N][cnt C] (blocks in l3 order: l3 = 0 with 1 path, 1 with 3,
+   2 with 2), so that each block is the [(2 l3 + 1) N, cnt C] operand of the per-l3 output Linear
+   (so2_tensor_product.py:276-290).  Row t (path p, order m of degree l3) of channel c of atom i sits at
+   N E2V2_SO2_A(t) + i E2V2_SO2_LD(t) + E2V2_SO2_COL(t) + c.  mrow/srow [N,H] softmax max / sum; cnt [N,H]
+   number of maxima.  gate and inputhead of every edge are interpolated from rtab in the kernel (nothing
+   per edge is stored). */
+#define E2V2_SO2_A(t) ((t) == 0 ? 0 : (t) < 10 ? 256 + 768 * (((t) - 1) % 3) : 2560 + 512 * (((t) - 10) % 5))
+#define E2V2_SO2_LD(t) ((t) == 0 ? 256 : (t) < 10 ? 768 : 512)
+#define E2V2_SO2_COL(t) ((t) == 0 ? 0 : (t) < 10 ? 256 * (((t) - 1) / 3) : 256 * (((t) - 10) / 5))
 int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, float* srow, int32_t* cnt, hipStream_t s);
 /* Bytes of device workspace e2v2_attn_bwd needs for n_edges edges (per-edge weights handed from the row
    pass to the column pass and per-slice partial edge gradients, alive during the call only). */
 size_t e2v2_attn_bwd_workspace(int64_t n_edges);
-/* grad_out, out [20][N][C] (float, or bf16 if act_bf16) -> ddvec [E,3], ddist [E] (including the radial
+/* grad_out, out (l3-grouped as above; float, or bf16 if act_bf16) -> ddvec [E,3], ddist [E] (including the radial
    profile's distance derivative, from the table), dq, dk [N,H,D], dv [9][N][C] (all float, dv in slice
    order); workspace: e2v2_attn_bwd_workspace(E) bytes, 16-byte aligned */
 int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, const void* out, const float* mrow,

@@ -3,6 +3,8 @@ include/e2v2.h declares; the Python binding lists the same set."""
 import re
 from pathlib import Path
 
+import pytest
+
 ROOT = Path(__file__).resolve().parents[1]
 
 
@@ -46,3 +48,26 @@ def test_noalloc_rejects_oversized_plan(pkg):
     dummy = ctypes.c_void_p(16)          # never dereferenced: the size check fails first
     rc = lib.e2v2_nbr_count_noalloc(ctypes.byref(plan), dummy, dummy, dummy, None)
     assert rc != 0 and b"exceed the static scratch" in lib.e2v2_last_error()
+
+
+def test_header_so2_layout_macros_match_generated_tables(tmp_path):
+    """E2V2_SO2_A / _LD / _COL of include/e2v2.h (compiled with gcc) equal the
+    l3-grouped row placement the kernels are generated with (so3.so2_row_layout)."""
+    import shutil
+    import subprocess
+    import sys
+    if shutil.which("gcc") is None or not Path("/opt/rocm/include/hip/hip_runtime_api.h").exists():
+        pytest.skip("gcc or the HIP headers are not available")
+    src = tmp_path / "m.c"
+    src.write_text('#include <stdio.h>\n#include "e2v2.h"\nint main(void) {\n'
+                   '  for (int t = 0; t < 20; ++t) printf("%d %d %d\\n", E2V2_SO2_A(t), E2V2_SO2_LD(t), '
+                   'E2V2_SO2_COL(t));\n  return 0;\n}\n')
+    exe = tmp_path / "m"
+    subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", "-I", str(ROOT / "include"), "-I", "/opt/rocm/include",
+                    str(src), "-o", str(exe)], check=True, capture_output=True)
+    got = [tuple(int(x) for x in line.split()) for line in subprocess.run([str(exe)], check=True,
+                                                                          capture_output=True, text=True).stdout.split("\n") if line]
+    sys.path.insert(0, str(ROOT / "ubio-molfm_amd"))
+    import so3
+    a, ld, col, _ = so3.so2_row_layout()
+    assert got == list(zip(a, ld, col))

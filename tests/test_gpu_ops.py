@@ -175,7 +175,8 @@ def _attention_case(pkg, cuda, act_dtype, clusters=True, graph=None):
     args = ops.attn_args(nl, qd, kd, vd, slot, tab, math.sqrt(8.0), 6.0, int(bf))
     if not clusters:
         args.col_slot_member = args.col_slot_edge = args.col_n_slots = None
-    out = torch.empty(20, N, 256, device=cuda, dtype=act_dtype); m = torch.empty(N, 128, device=cuda)
+    out = torch.empty(20 * N * 256, device=cuda, dtype=act_dtype)   # l3-grouped rows
+    m = torch.empty(N, 128, device=cuda)
     sr = torch.empty(N, 128, device=cuda); cnt = torch.empty(N, 128, dtype=torch.int32, device=cuda)
     _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _lib.vp(out.data_ptr()), _lib.vp(m.data_ptr()),
               _lib.vp(sr.data_ptr()), _lib.vp(cnt.data_ptr()), st)
@@ -185,9 +186,9 @@ def _attention_case(pkg, cuda, act_dtype, clusters=True, graph=None):
     leaves = [t.double().requires_grad_(True) for t in (q, k, v, nl.dvec.cpu(), nl.dist.cpu())]
     gi = mlp_ref(leaves[4], Z[row], Z[col], net64, tw, sw, rb.offset.double(), float(np.float32(rb.coeff)))
     ref = attn_ref(*leaves[:5], row, col, gi, T, 6.0, N)
-    e_f = relerr(out.float()[:, :, Pinv].permute(1, 0, 2), ref)
+    e_f = relerr(ops.so2_rows(out, N).float()[:, :, Pinv].permute(1, 0, 2), ref)
     grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
-    Gd = G.permute(1, 0, 2).to(cuda)[:, :, P].contiguous().to(act_dtype)
+    Gd = ops.so2_grouped(G.permute(1, 0, 2).to(cuda)[:, :, P].contiguous()).to(act_dtype)
     f = dict(device=cuda)
     ddv = torch.empty(E, 3, **f); dd = torch.empty(E, **f)
     dq = torch.empty(qd.shape, **f); dk = torch.empty(kd.shape, **f); dv = torch.empty(vd.shape, **f)

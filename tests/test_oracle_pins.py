@@ -316,3 +316,30 @@ def test_construct_radius_neighbor_brute_force():
             assert torch.allclose(nb["f_poly_dist"].double(), (1 - t ** 2) ** 2, atol=1e-6)
         else:
             assert torch.allclose(nb["f_poly_dist"], polynomial(nb["f_dist"], rc))
+
+
+def test_so2_grouped_layout_is_a_permutation():
+    """The l3-grouped placement of the 20 SO(2) rows covers 20 N 256 slots once
+    each, and the rows of one output degree sit side by side as the K blocks of
+    its forward_linear operand (path p of row m at column p 256)."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "ubio-molfm_amd"))
+    import so3
+    a, ld, col, groups = so3.so2_row_layout()
+    N = 7
+    seen = np.zeros(20 * N * 256, np.int32)
+    for t in range(20):
+        for i in range(N):
+            base = N * a[t] + i * ld[t] + col[t]
+            seen[base:base + 256] += 1
+    assert np.all(seen == 1)
+    _, seq, _, _, _ = so3.so2_gather_tables()
+    t = 0
+    for (l3, cnt, start), (l3b, cntb) in zip(groups, seq):
+        assert (l3, cnt) == (l3b, cntb)
+        for p in range(cnt):
+            for m in range(2 * l3 + 1):
+                assert a[t] == start + m * cnt * 256 and ld[t] == cnt * 256 and col[t] == p * 256
+                t += 1
+    assert t == 20

@@ -36,6 +36,7 @@
 namespace e2v2 {
 
 constexpr int kH = 128, kD = 8, kC = 256, kNV = 9, kNT = 20;
+static_assert(kNT == kTpRows, "the coupling table's output rows");
 constexpr float kEps = 1e-3f;
 // Slice order of channel positions: position p holds the first (p % 32 < 16,
 // model channel h) or second (model channel 128 + h) channel of head
@@ -360,10 +361,10 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
     for (int q = 0; q < kNT; ++q) o[q] = 0.f;
 #pragma unroll
     for (int z = 0; z < kTpNnz; ++z) o[kTp[z].t] = fmaf(kTp[z].c, acc[kTp[z].r][kTp[z].k], o[kTp[z].t]);
-    TS* op = out + (size_t)i * kC + pu;
-    const size_t os = (size_t)A.n_rows * kC;
+    const size_t nr = (size_t)A.n_rows;
 #pragma unroll
-    for (int q = 0; q < kNT; ++q) store_act(o[q] * inv, op + q * os);
+    for (int q = 0; q < kNT; ++q)
+      store_act(o[q] * inv, out + nr * kRowA[q] + (size_t)i * kRowLd[q] + kRowCol[q] + pu);
   }
   if (lane < kSlH) {
     mrow[(size_t)i * kH + h] = m_run;
@@ -433,7 +434,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   auto issue = [&](int sl, Loads& L) {
     const int i = ci[sl];
 #pragma unroll
-    for (int z = 0; z < kNT; ++z) L.g[z] = G[(size_t)i * kC + z * os + c];
+    for (int z = 0; z < kNT; ++z) L.g[z] = G[(size_t)A.n_rows * kRowA[z] + (size_t)i * kRowLd[z] + kRowCol[z] + c];
     load4(Qp + ((size_t)i * kH + hk) * kD + d0, L.q);
     // unconditional (an absent edge reads edge 0, unused): every slot issues the
     // same loads, so the wait before apply() counts only the older slot's
@@ -602,17 +603,20 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
   float inv, dsum, dmc, m;
   {
     float g0[kNT], g1[kNT];
+    const size_t nr = (size_t)A.n_rows;
 #pragma unroll
     for (int z = 0; z < kNT; ++z) {
-      g0[z] = f32(G[(size_t)i * kC + z * os + p0]);
-      g1[z] = f32(G[(size_t)i * kC + z * os + p1]);
+      const size_t rz = nr * kRowA[z] + (size_t)i * kRowLd[z] + kRowCol[z];
+      g0[z] = f32(G[rz + p0]);
+      g1[z] = f32(G[rz + p1]);
     }
     // D_h = sum over the head's two channels and the 20 rows, summed as the first channel then the second
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int z = 0; z < kNT; ++z) {
-      d0 = fmaf(g0[z], f32(O[(size_t)i * kC + z * os + p0]), d0);
-      d1 = fmaf(g1[z], f32(O[(size_t)i * kC + z * os + p1]), d1);
+      const size_t rz = nr * kRowA[z] + (size_t)i * kRowLd[z] + kRowCol[z];
+      d0 = fmaf(g0[z], f32(O[rz + p0]), d0);
+      d1 = fmaf(g1[z], f32(O[rz + p1]), d1);
     }
     const float Dh = d1 + d0;
     tp_transpose(g0, dA0);

@@ -326,78 +326,44 @@ class QKProjFn(torch.autograd.Function):
 
 
 class SO2OutFn(torch.autograd.Function):
-    """y = res + proj_first(forward_linear(so2)): the SO(2) product's per-l3
-    output linears (path_norm and path scales folded into the blocks) followed by
-    the proj_first SO3 linear, GEMMs only (so2_tensor_product.py:276-290,
-    e2former.py:215-219,433)."""
+    """y = res + proj_first(forward_linear(so2)) as one GEMM per output degree l3
+    (so2_tensor_product.py:276-290, e2former.py:215-219,433).  so2 is the
+    attention output in its l3-grouped layout: the 2 l3 + 1 rows of degree l3
+    hold their cnt coupling paths side by side, [2 l3 + 1][N][cnt C], the
+    operand of forward_linear's Linear(cnt C -> C); its weight (path_norm and the
+    path scales folded, input rows in the kernels' slice order) times
+    proj_first's W_l3^T is one [cnt C, O] weight (``so2_out_weights``)."""
 
     @staticmethod
-    def forward(ctx, so2, res, blocks, Wpop, bp):
+    def forward(ctx, so2, res, Wc, bias, N: int):
         so2 = so2.contiguous()
         res = None if res is None else res.contiguous()
-        Wp = Wpop.w
-        _, N, C = so2.shape
-        t = so2.new_empty(9, N, C, dtype=torch.float32)
-        sa = _bf(so2) if Wp.dtype == BF16 else so2
-        o = 0
-        for lst in blocks:
-            nr = lst[0][1]
-            tv = t[o:o + nr].view(-1, C)
-            for idx, (t0, nr_, Wt) in enumerate(lst):
-                xin = sa[t0:t0 + nr_].view(-1, C)
-                if idx == 0:
-                    _mm_into(xin, Wt, out=tv)
-                else:
-                    _addmm_into(tv, xin, Wt, out=tv)
-            o += nr
-        O = Wp.shape[1]
-        if Wpop.fwd is not None and res is None:
-            y = _mrow_gemm(t, Wpop, bp)
-        else:
-            y = so2.new_empty(9, N, O, dtype=torch.float32)
-            ta = _bf(t) if Wp.dtype == BF16 else t
-            for l in range(3):
-                a, b = l * l, (l + 1) ** 2
-                if res is not None:
-                    _addmm_into(res[a:b].view(-1, O), ta[a:b].view(-1, C), Wp[l].t(), out=y[a:b].view(-1, O))
-                elif l == 0:
-                    _mm_bias_into(ta[0], Wp[0].t(), bp, out=y[0])
-                else:
-                    _mm_into(ta[a:b].view(-1, C), Wp[l].t(), out=y[a:b].view(-1, O))
+        O = Wc[0][3].shape[1]
+        y = so2.new_empty(9, N, O, dtype=torch.float32)
+        for (l3, cnt, start, W, _) in Wc:
+            K = W.shape[0]
+            A = so2[start * N:(start + (2 * l3 + 1) * K) * N].view(-1, K)
+            a, b = l3 * l3, (l3 + 1) ** 2
             if res is not None:
-                y[0].add_(bp)
+                _addmm_into(res[a:b].view(-1, O), A, W, out=y[a:b].view(-1, O))
+            else:
+                _mm_into(A, W, out=y[a:b].view(-1, O))
+        y[0].add_(bias)
         ctx.has_res = res is not None
-        ctx.blocks, ctx.Wpop = blocks, Wpop
+        ctx.Wc, ctx.N = Wc, N
         ctx.shape, ctx.so2_dtype = so2.shape, so2.dtype
         return y
 
     @staticmethod
     def backward(ctx, gy):
-        Wpop = ctx.Wpop
-        Wp = Wpop.w
         gy = gy.contiguous()
-        _, N, O = gy.shape
-        C = Wp.shape[2]
-        bf = Wp.dtype == BF16
-        if Wpop.bwd is not None:
-            gt = torch.bmm(gy, Wpop.bwd)
-        else:
-            # bf16: gt feeds only the bf16 GEMMs below, so it is produced in bf16
-            # (one rounding of the fp32 accumulators, no separate cast pass)
-            gt = gy.new_empty(9, N, C, dtype=BF16 if bf else gy.dtype)
-            ga = _bf(gy) if bf else gy
-            for l in range(3):
-                a, b = l * l, (l + 1) ** 2
-                _mm_into(ga[a:b].view(-1, O), Wp[l], out=gt[a:b].view(-1, C))
+        N = ctx.N
+        O = gy.shape[2]
         gso2 = gy.new_empty(ctx.shape, dtype=ctx.so2_dtype)
-        gta = _bf(gt) if bf else gt
-        o = 0
-        for lst in ctx.blocks:
-            nr = lst[0][1]
-            gv = gta[o:o + nr].view(-1, C)
-            for (t0, nr_, Wt) in lst:
-                _mm_into(gv, Wt.t(), out=gso2[t0:t0 + nr_].view(-1, C))
-            o += nr
+        for (l3, cnt, start, _, WT) in ctx.Wc:
+            K = WT.shape[1]
+            a, b = l3 * l3, (l3 + 1) ** 2
+            _mm_into(gy[a:b].view(-1, O), WT, out=gso2[start * N:(start + (2 * l3 + 1) * K) * N].view(-1, K))
         return gso2, (gy if ctx.has_res else None), None, None, None
 
 
@@ -986,6 +952,27 @@ class E2AttentionArbOrder_sparse(nn.Module):
         out = self.forward_fused(x, ctx)
         return out.transpose(0, 1).contiguous(), attn_weight
 
+    def so2_out_weights(self, bf16: bool = False):
+        """Per output degree l3 (l3 order): (l3, cnt, start, W, W^T) with W [cnt 256, O]
+        = forward_linear's folded blocks of that degree stacked along K (input rows
+        in the kernels' slice order, path_norm and path scales folded) times
+        proj_first's W_l3^T, formed in float64 and rounded once (bf16 copies in bf16
+        mode); start = the block's offset / N in the l3-grouped attention output.
+        Cached on the parameters' versions."""
+        tp = self.first_order_tp.so2_tp
+        pf = self.proj_first
+        params = list(tp.parameters()) + [pf.weight]
+
+        def build():
+            out = []
+            for (l3, cnt, start), lst in zip(so3.so2_row_layout()[3], tp.folded_blocks(False, sliced=True)):
+                Wcat = torch.cat([Wt.double() for (_, _, Wt) in lst], dim=0)
+                W = Wcat @ pf.weight.detach()[l3].double().t()
+                dt = BF16 if bf16 else torch.float32
+                out.append((l3, cnt, start, W.to(dt).contiguous(), W.t().to(dt).contiguous()))
+            return out
+        return cached(self, "so2_out_bf16" if bf16 else "so2_out", params, build)
+
     def forward_fused(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
         """x [9, N, C] (m-major) -> attention(x) (+ res when given), [9, N, C].
         v, the attention rows and their gradients run in the kernels' slice order
@@ -1012,8 +999,7 @@ class E2AttentionArbOrder_sparse(nn.Module):
                                     math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
         pf = self.proj_first
         with record_function("first-order"):
-            return SO2OutFn.apply(so2, res, self.first_order_tp.so2_tp.folded_blocks(bf16, sliced=True),
-                                  mrow_weight(pf, "weight", pf.weight, bf16, pf.lmax), pf.bias.detach())
+            return SO2OutFn.apply(so2, res, self.so2_out_weights(bf16), pf.bias.detach(), N)
 
 
 class TransBlock(nn.Module):

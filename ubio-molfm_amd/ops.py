@@ -14,13 +14,37 @@ from typing import List, Optional
 import torch
 from torch import nn
 
-from . import _lib
+from . import _lib, so3
 from .neighbors import NeighborList
 
 ENV_EXPONENT = 5
 ENV_A = -(ENV_EXPONENT + 1) * (ENV_EXPONENT + 2) / 2
 ENV_B = ENV_EXPONENT * (ENV_EXPONENT + 2)
 ENV_C = -ENV_EXPONENT * (ENV_EXPONENT + 1) / 2
+
+
+# Placement of the 20 SO(2) output rows in the attention kernels' l3-grouped layout (so3.so2_row_layout):
+# row t of channel c of atom i at N SO2_A[t] + i SO2_LD[t] + SO2_COL[t] + c; per output degree l3 a block
+# [2 l3 + 1][N][cnt 256] starting at N start (SO2_GROUPS = [(l3, cnt, start)]).
+SO2_A, SO2_LD, SO2_COL, SO2_GROUPS = so3.so2_row_layout()
+
+
+def so2_rows(flat: torch.Tensor, n_atoms: int) -> torch.Tensor:
+    """[20, N, 256] l3-sequential rows (a copy) of an l3-grouped attention output."""
+    N = int(n_atoms)
+    out = flat.new_empty(len(SO2_A), N, 256)
+    for t in range(len(SO2_A)):
+        out[t] = torch.as_strided(flat, (N, 256), (SO2_LD[t], 1), N * SO2_A[t] + SO2_COL[t])
+    return out
+
+
+def so2_grouped(rows: torch.Tensor) -> torch.Tensor:
+    """The l3-grouped layout (flat) of [20, N, 256] l3-sequential rows."""
+    N = rows.shape[1]
+    flat = rows.new_empty(rows.numel())
+    for t in range(len(SO2_A)):
+        torch.as_strided(flat, (N, 256), (SO2_LD[t], 1), N * SO2_A[t] + SO2_COL[t]).copy_(rows[t])
+    return flat
 
 
 def _stream(t: torch.Tensor):
@@ -242,10 +266,11 @@ def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: f
 
 class AttentionFn(torch.autograd.Function):
     """Edge part of E2AttentionArbOrder_sparse.forward (e2former.py:238-433) up to
-    the SO(2) product's forward_linear: returns the 20-row l3-sequential tensor
-    h_a - h_b of so2_tensor_product.py:385 for every query atom, m-major
-    [20, N, 256]; q, k [N, 128, 8], v [9, N, 256], the channels of v and of the
-    output in the kernels' slice order (modules.slice_perm).  gate and inputhead
+    the SO(2) product's forward_linear: returns the 20 l3-sequential rows of
+    h_a - h_b of so2_tensor_product.py:385 for every query atom in the
+    l3-grouped layout (flat, 20 N 256 values; ``so2_rows`` gives [20, N, 256]);
+    q, k [N, 128, 8], v [9, N, 256], the channels of v and of the output in the
+    kernels' slice order (modules.slice_perm).  gate and inputhead
     (fc_easy, e2former.py:258-306) are interpolated from the layer's radial table
     inside the kernels: only node-level tensors are saved."""
 
@@ -262,7 +287,7 @@ class AttentionFn(torch.autograd.Function):
         q = q.to(act_dtype).contiguous(); k = k.to(act_dtype).contiguous(); v = v.to(act_dtype).contiguous()
         bf = int(act_dtype == torch.bfloat16)
         args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf)
-        out = torch.empty(20, N, 256, dtype=act_dtype, device=dev)   # m-major
+        out = torch.empty(20 * N * 256, dtype=act_dtype, device=dev)   # l3-grouped rows
         mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)

@@ -123,6 +123,28 @@ def wigner_J(lmax: int = 11) -> list:
     return [np.ones((1, 1))] + [((-1) ** l) * D[l] for l in range(1, lmax + 1)]
 
 
+def so2_row_layout(lmax: int = 2, C: int = 256):
+    """Placement of the SO(2) product's l3-sequential output rows in the
+    l3-grouped layout of the attention kernels' output: the rows of output degree
+    l3 hold their cnt coupling paths side by side, a [2 l3 + 1][N][cnt C] block
+    (the input of the per-l3 Linear(cnt C -> C) of so2_tensor_product.py:276-290
+    as one GEMM operand); the blocks follow in l3 order.  Row t = (l3, path p,
+    order m) of channel c of atom i sits at N a[t] + i ld[t] + col[t] + c.
+    Returns (a, ld, col, groups) with groups = [(l3, cnt, start / N)]."""
+    _, seq, _, _, _ = so2_gather_tables(lmax)
+    a, ld, col, groups = [], [], [], []
+    start = 0
+    for l3, cnt in seq:
+        groups.append((l3, cnt, start))
+        for p in range(cnt):
+            for m in range(2 * l3 + 1):
+                a.append(start + m * cnt * C)
+                ld.append(cnt * C)
+                col.append(p * C)
+        start += (2 * l3 + 1) * cnt * C
+    return a, ld, col, groups
+
+
 def render_tp_header(lmax: int = 2) -> str:
     """C++ header with the nonzeros of the Cartesian table (generated)."""
     T = cartesian_tp_table(lmax)
@@ -139,6 +161,11 @@ def render_tp_header(lmax: int = 2) -> str:
     for (t, r, k, c) in nz:
         lines.append(f"    {{{t}, {r}, {k}, {float(np.float32(c))!r}f}},")
     lines.append("};")
+    a, ld, col, _ = so2_row_layout(lmax)
+    lines.append("// l3-grouped output rows: row t of channel c of atom i at N kRowA[t] + i kRowLd[t] + kRowCol[t] + c")
+    lines.append("constexpr int kRowA[kTpRows] = {" + ", ".join(str(x) for x in a) + "};")
+    lines.append("constexpr int kRowLd[kTpRows] = {" + ", ".join(str(x) for x in ld) + "};")
+    lines.append("constexpr int kRowCol[kTpRows] = {" + ", ".join(str(x) for x in col) + "};")
     lines.append("}  // namespace e2v2")
     return "\n".join(lines) + "\n"
 
