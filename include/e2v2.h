@@ -89,6 +89,9 @@ typedef struct e2v2_nbr_plan {
   int32_t* bin_atoms;               /* workspace [n_atoms]                                  */
   int32_t* stats;                   /* workspace [3], zeroed by the caller: scan total / max;
                                        [2] != 0 if an atom lies outside its graph's grid box */
+  const uint8_t* src_include;       /* [n_atoms] or NULL: only atoms j with src_include[j] != 0 are
+                                       edge sources (the long-range list's include_mask,
+                                       e2former_wrapper.py:225-231); images exist as before */
 } e2v2_nbr_plan;
 
 int e2v2_nbr_bin(const e2v2_nbr_plan* plan, hipStream_t s);
@@ -301,6 +304,14 @@ typedef struct e2v2_attn_args {
      workgroup per column); used by the fp32 column pass of e2v2_attn_bwd. */
   int32_t col_span;
   const int32_t* col_slot_member; const int32_t* col_slot_edge; const int32_t* col_n_slots;
+  /* zero_order 0: the SO(2) first-order product ("so2-first-order", weights alpha / r, 20 output rows);
+     1: the zero-order aggregation ("zero-order", e2former.py:411-416: out[r][i][c] = sum_e
+     alpha_e,h(c) v_j[r][c], weights alpha, 9 output rows [9][N][C] m-major) */
+  int32_t zero_order;
+  /* envelope of the weights: env_kind 0 the polynomial (rc, env_a/b/c), 1 the smooth bell on
+     [env_lo, rc] (module_utils.py:1956-1985, exponent 2) */
+  int32_t env_kind;
+  float env_lo;
 } e2v2_attn_args;
 
 /* v [9][N][C] is m-major (row r of every atom contiguous), channels in slice order.  out holds the 20

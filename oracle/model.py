@@ -318,12 +318,13 @@ def segment_alpha(logit, poly, inputhead, qi, n_rows):
 
 
 class E2AttentionArbOrder_sparse(nn.Module):
-    """``e2former.py:80-436`` for tp_type=QK_alpha, attn_type=so2-first-order,
-    with the torch fallbacks (``use_triton`` False)."""
+    """``e2former.py:80-436`` for tp_type=QK_alpha, attn_type so2-first-order
+    or zero-order, with the torch fallbacks (``use_triton`` False)."""
 
     def __init__(self, C=256, attn_weight_input_dim=256, num_attn_heads=128, attn_scalar_head=8,
-                 lmax=2, atom_type_cnt=256):
+                 lmax=2, atom_type_cnt=256, attn_type="so2-first-order"):
         super().__init__()
+        self.attn_type = attn_type
         self.num_attn_heads, self.attn_scalar_head, self.lmax = num_attn_heads, attn_scalar_head, lmax
         self.node_embed_dim = 128
         self.source_embedding = nn.Embedding(atom_type_cnt, 128)
@@ -337,8 +338,11 @@ class E2AttentionArbOrder_sparse(nn.Module):
         self.query_linear = SO3_Linear2Scalar_e2former(C, num_attn_heads * attn_scalar_head, lmax=lmax)
         self.key_linear = SO3_Linear2Scalar_e2former(C, num_attn_heads * attn_scalar_head, lmax=lmax)
         self.proj_value = SO3_Linear_e2former(C, C, lmax=lmax)
-        self.first_order_tp = E2TensorProductSO2_FirstOrder(lmax, C, C, num_attn_heads)
-        self.proj_first = SO3_Linear_e2former(C, C, lmax=lmax)
+        if attn_type == "zero-order":                       # e2former.py:199-204
+            self.proj_zero = SO3_Linear_e2former(C, C, lmax=lmax)
+        else:
+            self.first_order_tp = E2TensorProductSO2_FirstOrder(lmax, C, C, num_attn_heads)
+            self.proj_first = SO3_Linear_e2former(C, C, lmax=lmax)
 
     def forward(self, node_pos, x, edge_dis, edge_vec, attn_weight, atomic_numbers, poly_dist, bd):
         f_N1 = x.shape[0]
@@ -373,6 +377,11 @@ class E2AttentionArbOrder_sparse(nn.Module):
             out.scatter_add_(0, qi.view(-1, 1, 1).expand_as(ev), ev)
             return out
 
+        if self.attn_type == "zero-order":                  # e2former.py:411-416
+            f_N2 = value.shape[0]
+            agg_out = agg(value.reshape(f_N2, -1, H), alpha)   # [N, 9 C / H, H]: head of channel c is c % H
+            agg_out = agg_out.reshape(f_N1, (self.lmax + 1) ** 2, x.shape[-1])
+            return self.proj_zero(agg_out), attn_weight
         out = self.first_order_tp(node_pos, bd["f_exp_node_pos"], value, alpha_div_r, agg, bd)
         return self.proj_first(out), attn_weight
 
@@ -380,11 +389,13 @@ class E2AttentionArbOrder_sparse(nn.Module):
 class TransBlock(nn.Module):
     """``e2former.py:440-620``."""
 
-    def __init__(self, C=256, lmax=2, num_attn_heads=128, attn_scalar_head=8, number_of_basis=256):
+    def __init__(self, C=256, lmax=2, num_attn_heads=128, attn_scalar_head=8, number_of_basis=256,
+                 attn_type="so2-first-order"):
         super().__init__()
         self.lmax = lmax
         self.norm_1 = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
-        self.ga = E2AttentionArbOrder_sparse(C, number_of_basis, num_attn_heads, attn_scalar_head, lmax)
+        self.ga = E2AttentionArbOrder_sparse(C, number_of_basis, num_attn_heads, attn_scalar_head, lmax,
+                                             attn_type=attn_type)
         self.norm_ffn = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
         self.ffn = FeedForwardNetwork_s3(C, C, C, lmax)
 
@@ -482,11 +493,15 @@ def _wigner_pair(pos64, J64, lmax, l3_seq):
 
 
 class E2former(nn.Module):
-    """``e2former.py:758-1145`` (with_cluster off)."""
+    """``e2former.py:758-1145``, with the long-range blocks of
+    with_cluster="node*" (``e2former.py:887-929,1088-1117``)."""
 
     def __init__(self, C=256, lmax=2, num_layers=4, max_radius=6.0, number_of_basis=256,
-                 num_attn_heads=128, attn_scalar_head=8, avg_degree=23.01, atom_type_cnt=256):
+                 num_attn_heads=128, attn_scalar_head=8, avg_degree=23.01, atom_type_cnt=256,
+                 attn_type="so2-first-order", with_cluster=False, long_range_layers=2, long_cutoff_lower=0.1,
+                 long_cutoff_upper=12):
         super().__init__()
+        types = attn_type.split("+") if "+" in attn_type else [attn_type, attn_type]
         self.lmax, self.max_radius, self.num_layers = lmax, max_radius, num_layers
         self._node_scalar_dim = C
         self.default_node_embedding = nn.Embedding(atom_type_cnt, C)
@@ -495,12 +510,25 @@ class E2former(nn.Module):
         self.Jd_list = nn.ParameterList([nn.Parameter(torch.from_numpy(j).float(), requires_grad=False)
                                          for j in _cg.j_from_cg(11)])
         self.edge_deg_embed_dense = EdgeDegreeEmbeddingNetwork_higherorder(C, lmax, avg_degree, number_of_basis)
-        self.blocks = nn.ModuleList([TransBlock(C, lmax, num_attn_heads, attn_scalar_head, number_of_basis)
-                                     for _ in range(num_layers)])
-        self.l3_sequential = self.blocks[0].ga.first_order_tp.so2_tp.l3_sequential
+        self.blocks = nn.ModuleList([TransBlock(C, lmax, num_attn_heads, attn_scalar_head, number_of_basis,
+                                                types[0] if i < num_layers // 2 else types[1])
+                                     for i in range(num_layers)])
+        ga0 = self.blocks[0].ga
+        self.l3_sequential = (ga0.first_order_tp.so2_tp.l3_sequential if hasattr(ga0, "first_order_tp")
+                              else [(l, 1) for l in range(lmax + 1)])
         self.norm_final = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
+        self.long_cutoff_lower, self.long_cutoff_upper = long_cutoff_lower, long_cutoff_upper
+        self.with_cluster = str(with_cluster)
+        if "node" in self.with_cluster:
+            self.pre_norm_node = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
+            self.norm_cluster = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
+            self.final_linear = SO3_Linear_e2former(2 * C, C, lmax=lmax, bias=True)
+            self.rbf_long = GaussianSmearing(number_of_basis, cutoff=long_cutoff_upper, basis_width_scalar=2)
+            self.long_blocks = nn.ModuleList([TransBlock(C, lmax, num_attn_heads, attn_scalar_head, number_of_basis,
+                                                         "zero-order") for _ in range(long_range_layers)])
+            self.norm_final = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
 
-    def forward(self, bd, token_embedding, sys_embedding):
+    def forward(self, bd, token_embedding, sys_embedding, cluster_neighbor_info=None):
         B, L = bd["pos"].shape[:2]
         node_mask = bd["atom_masks"]
         node_pos = torch.where((~node_mask).unsqueeze(-1).repeat(1, 1, 3), 999.0, bd["pos"])
@@ -520,10 +548,21 @@ class E2former(nn.Module):
         f_dist, f_vec, f_poly = bd["f_dist"], bd["f_edge_vec"], bd["f_poly_dist"]
         rbf = self.rbf(f_dist)
         x = self.edge_deg_embed_dense(f_pos.shape[0], f_Z, f_vec, bd, f_poly, rbf)
+        sys_node = None if sys_embedding is None else sys_embedding[f_batch]
         for blk in self.blocks:
-            x, rbf = blk(f_pos, x, None if sys_embedding is None else sys_embedding[f_batch],
-                         f_dist, f_vec, rbf, f_Z, f_poly, bd)
-        x = self.norm_final(x)
+            x, rbf = blk(f_pos, x, sys_node, f_dist, f_vec, rbf, f_Z, f_poly, bd)
+        if "node" in self.with_cluster:
+            short = x
+            x = self.pre_norm_node(x)
+            bd.update(cluster_neighbor_info)
+            cn = cluster_neighbor_info
+            rbf = self.rbf_long(cn["f_dist"])
+            for blk in self.long_blocks:
+                x, rbf = blk(f_pos, x, sys_node, cn["f_dist"], cn["f_edge_vec"], rbf, f_Z, cn["f_poly_dist"], bd)
+            x = self.norm_cluster(x)
+            x = self.final_linear(torch.cat([short, x], dim=-1))
+        else:
+            x = self.norm_final(x)
         node_irreps = torch.zeros((B, L, (self.lmax + 1) ** 2, self._node_scalar_dim), dtype=x.dtype)
         node_irreps[node_mask] = x
         return node_irreps[:, :, 0], node_irreps[:, :, 1:4], node_irreps
@@ -533,7 +572,7 @@ class E2FormerBackbone(nn.Module):
     """``e2former_wrapper.py:35-339`` (dense neighbour path, encoder=default)."""
 
     def __init__(self, C=256, lmax=2, num_layers=4, max_radius=6.0, number_of_basis=256, num_attn_heads=128,
-                 attn_scalar_head=8, max_neighbors=None, pbc_cells=4, avg_degree=23.01):
+                 attn_scalar_head=8, max_neighbors=None, pbc_cells=4, avg_degree=23.01, **decoder_kw):
         super().__init__()
         self.max_radius, self.max_neighbors, self.pbc_cells = max_radius, max_neighbors, pbc_cells
         self.embedding = nn.Embedding(256, C)
@@ -542,7 +581,7 @@ class E2FormerBackbone(nn.Module):
         self.mix_cm = nn.Sequential(nn.Linear(2 * C, C), nn.SiLU())
         self.unifiedtokentoembedding = nn.Linear(C, C)
         self.decoder = E2former(C, lmax, num_layers, max_radius, number_of_basis, num_attn_heads,
-                                attn_scalar_head, avg_degree)
+                                attn_scalar_head, avg_degree, **decoder_kw)
 
     def forward(self, bd):
         Z = bd["atomic_numbers"]
@@ -552,8 +591,11 @@ class E2FormerBackbone(nn.Module):
         bd["pos"] = torch.where(pad.unsqueeze(-1).repeat(1, 1, 3), 999.0, bd["pos"].to(dt))
         pos = bd["pos"]
         B, L = pos.shape[:2]
+        cluster = "node" in self.decoder.with_cluster
+        # the cell expansion covers the long-range cutoff (e2former_wrapper.py:94-99,199)
+        r_exp = self.decoder.long_cutoff_upper if cluster else self.max_radius
         if torch.any(bd["pbc"]):
-            ex = expand_includeself(pos, bd["pbc"], Z, bd["cell"], self.max_radius, self.pbc_cells, pad, dt)
+            ex = expand_includeself(pos, bd["pbc"], Z, bd["cell"], r_exp, self.pbc_cells, pad, dt)
             bd.update(ex)
         else:
             bd.update(dict(expand_node_pos=pos, outcell_index=torch.arange(L).unsqueeze(0).repeat(B, 1),
@@ -565,6 +607,15 @@ class E2FormerBackbone(nn.Module):
         bd["f_outcell_index"] = (bd["outcell_index"] + ptr[:B, None])[bd["expand_node_mask"]]
         nb = construct_radius_neighbor(pos, node_mask, en, bd["expand_node_mask"], self.max_radius,
                                        1e-4, self.max_neighbors)
+        cn = None
+        if cluster:                                                  # e2former_wrapper.py:223-243
+            exp_z = torch.gather(Z, dim=1, index=bd["outcell_index"])
+            include = ~torch.isin(exp_z, torch.tensor([0, 1]))
+            dec = self.decoder
+            cn = construct_radius_neighbor(
+                pos, node_mask, en, bd["expand_node_mask"], dec.long_cutoff_upper, dec.long_cutoff_lower,
+                None if self.max_neighbors is None else int(2.5 * self.max_neighbors), include_mask=include,
+                poly="poly_bell" if "bell" in dec.with_cluster else "poly")
         bd.update(nb)
         tok = self.embedding(Z)
         if "charge" in bd:
@@ -574,7 +625,7 @@ class E2FormerBackbone(nn.Module):
             tok = self.unifiedtokentoembedding(tok + sys_emb.unsqueeze(1))
         else:
             sys_emb = None
-        a, v, irr = self.decoder(bd, tok, sys_emb)
+        a, v, irr = self.decoder(bd, tok, sys_emb, cn)
         return {"node_featuresBxN": a, "node_vec_featuresBxN": v, "node_irrepsBxN": irr, "data": bd}
 
 

@@ -92,11 +92,13 @@ def fp32_dist(pi: np.ndarray, pj: np.ndarray, off: np.ndarray):
     return dv, np.sqrt(sq).astype(F32)
 
 
-def exact_neighbors(pos, graph_ptr, cells, pbcs, rc=6.0, rmin=1e-4, cap=4):
+def exact_neighbors(pos, graph_ptr, cells, pbcs, rc=6.0, rmin=1e-4, cap=4, include=None):
     """Canonical exact edge list.  pos [N,3] fp32 (real atoms, graphs contiguous),
     graph_ptr [B+1], cells [B,3,3], pbcs [B,3].  Returns dict with
     i, j (int64), s (int32 [E,3]), dv (fp32 [E,3]), d (fp32 [E]) sorted
-    lexicographically by (i, j, s)."""
+    lexicographically by (i, j, s).  include [N] bool (or None): only atoms j
+    with include[j] are sources, the include_mask of module_utils.py:3165-3166
+    applied to the expanded nodes (which image exists does not depend on it)."""
     from scipy.spatial import cKDTree
     pos = np.asarray(pos, F32)
     rc32, rmin32 = F32(rc), F32(rmin)
@@ -126,6 +128,8 @@ def exact_neighbors(pos, graph_ptr, cells, pbcs, rc=6.0, rmin=1e-4, cap=4):
                 has = np.zeros(n, bool)
                 np.logical_or.at(has, jj[strict], True)
                 ok &= has[jj]
+            if include is not None:
+                ok &= np.asarray(include, bool)[p0:p1][jj]
             I.append(ii[ok] + p0); Jn.append(jj[ok] + p0)
             S.append(np.repeat(shifts[si][None], ok.sum(), 0)); DV.append(dv[ok]); D.append(d[ok])
     if not I:

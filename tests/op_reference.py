@@ -5,6 +5,9 @@ Each one restates the reference's own torch formulation of the op:
 * ``attn_ref``  logits/softmax/aggregation of e2former.py:327-433 with the
                 first-order product written as the per-edge Cartesian coupling
 * ``deg_ref``   EdgeDegreeEmbeddingNetwork_higherorder fallback   e2former.py:689-753
+* ``attn0_ref`` zero-order aggregation of e2former.py:393-416 (value reshaped to
+                [M, 9 C / H, H]: channel c weighted by head c mod H), with the
+                polynomial or the bell envelope (module_utils.py:1946-1985)
 """
 import math
 
@@ -66,3 +69,28 @@ def deg_ref(dvec, dist, row, fea, avg, rc, N):
     lidx = torch.tensor([0, 1, 1, 1, 2, 2, 2, 2, 2])
     contrib = Y.unsqueeze(-1) * f[:, lidx, :]
     return torch.zeros((N, 9, C), dtype=contrib.dtype).index_add(0, row, contrib) / avg
+
+
+def bell(d, lo, hi):
+    """(1 - t^2)^2, t = (2 d - (lo + hi)) / (hi - lo) clamped to [-1, 1]."""
+    hi = max(hi, lo + 1e-8)
+    t = torch.clamp((2 * d - (lo + hi)) / (hi - lo), -1.0, 1.0)
+    return (1 - t * t) ** 2
+
+
+def attn0_ref(q, k, v, dist, row, col, gi, env, N):
+    """Zero-order aggregation: out[i, r, c] = sum over edges (i, j) of
+    alpha_e,(c mod H) v[j, r, c], alpha the row softmax with the envelope env(d)."""
+    H = q.shape[1]
+    qs = q / math.sqrt(q.shape[-1])
+    qk = (qs[row] * k[col]).sum(-1)
+    gate, ih = gi[:, :H], gi[:, H:]
+    a = gate * qk
+    rh = row.view(-1, 1).expand(-1, H)
+    amax = torch.full((N, H), -torch.inf, dtype=a.dtype).scatter_reduce(0, rh, a, "amax", include_self=True)
+    e = torch.exp(a - amax[row]) * env(dist).unsqueeze(-1)
+    s = torch.zeros((N, H), dtype=a.dtype).scatter_add(0, rh, e)
+    alpha = e * ih / (s[row] + 1e-3)
+    C = v.shape[-1]
+    contrib = v[col] * alpha[:, torch.arange(C) % H].unsqueeze(1)     # [E, 9, C]
+    return torch.zeros((N, v.shape[1], C), dtype=contrib.dtype).index_add(0, row, contrib)

@@ -19,6 +19,20 @@ def _pair(cuda, seed=0):
     return m, om
 
 
+def _pair_variant(cuda, seed, **cfg):
+    """Product and oracle on one state dict for a backbone variant (attn_type
+    "a+b", with_cluster "node" / "node_bell" and its long-range settings)."""
+    from ubio_molfm_amd import model
+    from oracle.model import MolfmAtomic as OracleModel
+    torch.manual_seed(seed)
+    args = model.default_args()
+    args.backbone_config.update(cfg)
+    m = model.MolfmAtomic(args).eval().to(cuda)
+    om = OracleModel(**cfg).eval()
+    om.load_state_dict({k: v.cpu() for k, v in m.state_dict().items()}, strict=True)
+    return m, om
+
+
 def _compare(m, om, sysd, cuda, label, tol_e=1e-5, tol_f=1e-4):
     from ubio_molfm_amd import systems
     pos = torch.as_tensor(sysd["pos"], device=cuda)
@@ -42,6 +56,39 @@ def test_model_small_water(pkg, cuda):
     from ubio_molfm_amd import systems
     m, om = _pair(cuda)
     _compare(m, om, systems.small_water(8, 6.2, seed=2), cuda, "small-water")
+
+
+@pytest.mark.parametrize("with_cluster", ["node", "node_bell"])
+def test_model_long_range_cluster(pkg, cuda, with_cluster):
+    """with_cluster="node*" (e2former.py:887-929,1088-1117): the four short blocks,
+    then pre_norm_node, two zero-order long-range blocks on the 12 A list of
+    non-hydrogen sources (lower cutoff 0.1 A, rbf_long, the polynomial or the
+    bell envelope), norm_cluster and final_linear over [short, long]; periodic
+    water, same gates as the base model."""
+    from ubio_molfm_amd import systems
+    m, om = _pair_variant(cuda, 11, with_cluster=with_cluster)
+    assert len(m.decoder.decoder.long_blocks) == 2
+    _compare(m, om, systems.small_water(8, 6.2, seed=7), cuda, f"cluster-{with_cluster}")
+
+
+def test_model_long_range_cluster_organics(pkg, cuda):
+    """The bell cluster variant on a ragged non-periodic batch with
+    max_neighbors 12 (long-range list cut to 30 per atom), long cutoffs 0.5-9 A
+    and one long-range layer."""
+    from ubio_molfm_amd import systems
+    m, om = _pair_variant(cuda, 12, with_cluster="node_bell", max_neighbors=12, long_range_layers=1,
+                          long_cutoff_lower=0.5, long_cutoff_upper=9.0)
+    _compare(m, om, systems.organics_batch(n_mol=3, nmin=12, nmax=30, seed=9), cuda, "cluster-organics")
+
+
+def test_model_zero_order_short_blocks(pkg, cuda):
+    """attn_type "so2-first-order+zero-order": the last num_layers - num_layers // 2
+    short blocks aggregate with the zero-order attention (e2former.py:792-795,863)."""
+    from ubio_molfm_amd import systems
+    m, om = _pair_variant(cuda, 13, attn_type="so2-first-order+zero-order")
+    assert m.decoder.decoder.blocks[1].ga.attn_type == "so2-first-order"
+    assert m.decoder.decoder.blocks[2].ga.attn_type == "zero-order"
+    _compare(m, om, systems.small_water(8, 6.2, seed=8), cuda, "zero+first")
 
 
 def test_model_ragged_batch(pkg, cuda):

@@ -14,12 +14,13 @@ from oracle.neighbors import exact_neighbors
 pytestmark = pytest.mark.gpu
 
 
-def _check(pkg, cuda, sysd, rc=6.0, label=""):
+def _check(pkg, cuda, sysd, rc=6.0, label="", rmin=1e-4, include=None):
     from ubio_molfm_amd import neighbors
     pos = torch.as_tensor(sysd["pos"], device=cuda)
-    nl = neighbors.build_neighbors(pos, sysd["graph_ptr"], sysd["cell"], sysd["pbc"], rc)
+    inc = None if include is None else torch.as_tensor(include, device=cuda)
+    nl = neighbors.build_neighbors(pos, sysd["graph_ptr"], sysd["cell"], sysd["pbc"], rc, rmin, src_include=inc)
     got = nl.canonical()
-    ref = exact_neighbors(sysd["pos"], sysd["graph_ptr"], sysd["cell"], sysd["pbc"], rc)
+    ref = exact_neighbors(sysd["pos"], sysd["graph_ptr"], sysd["cell"], sysd["pbc"], rc, rmin, include=include)
     shell = int(np.sum(np.abs(ref["d"] - np.float32(rc)) <= 2 * np.spacing(np.float32(rc))))
     print(f"[nbr {label}] N={len(sysd['pos'])} E={nl.n_edges} oracle E={len(ref['i'])} "
           f"max_row={nl.max_row} near-cutoff(2ulp)={shell}", flush=True)
@@ -234,3 +235,18 @@ def test_caller_grid_box_gives_same_edges(pkg, cuda, box):
     assert ref.n_edges == got.n_edges
     for name in ("row_ptr", "col", "shift_idx", "dist", "dvec", "key_ptr", "key_eid"):
         assert torch.equal(getattr(ref, name), getattr(got, name)), name
+
+
+@pytest.mark.parametrize("case", ["water_pbc", "organics"])
+def test_long_range_source_mask(pkg, cuda, case):
+    """The long-range cluster list (e2former_wrapper.py:223-243): cutoff 12 A,
+    lower cutoff 0.1 A, sources restricted to atoms whose atomic number is
+    neither 0 nor 1 -- the same exact edge set, shifts and fp32 geometry as the
+    oracle with the include mask."""
+    from ubio_molfm_amd import systems
+    s = systems.small_water(8, 6.2, seed=3) if case == "water_pbc" else \
+        systems.organics_batch(n_mol=3, nmin=10, nmax=24, seed=8)
+    include = ~np.isin(np.asarray(s["Z"]), [0, 1])
+    nl = _check(pkg, cuda, s, rc=12.0, rmin=0.1, include=include, label=f"long-{case}")
+    col = nl.col.cpu().numpy()
+    assert nl.n_edges > 0 and np.all(include[col])

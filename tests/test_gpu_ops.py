@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from op_reference import attn_ref, deg_ref, mlp_ref
+from op_reference import attn0_ref, attn_ref, bell, deg_ref, envelope, mlp_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -242,6 +242,67 @@ def test_attention_bf16_storage(pkg, cuda, clusters):
     assert e_f < 4e-3
     for name, e in errs.items():
         assert e < 1e-2, (name, e)
+
+
+@pytest.mark.parametrize("env", ["poly", "bell"])
+@pytest.mark.parametrize("act", ["fp32", "bf16"])
+def test_zero_order_attention(pkg, cuda, env, act):
+    """The zero-order attention of the long-range blocks through AttentionFn
+    (e2v2_attn_fwd / e2v2_attn_bwd with zero_order set) on the long-range list
+    (12 A, lower cutoff 0.1 A, sources O only), against the float64 reference
+    with the profile evaluated per edge: the polynomial envelope on [0, 12] or
+    the bell on [0.1, 12].  The output does not depend on dvec: its gradient is
+    exactly zero; the distance gradient carries the envelope, the profile and
+    the softmax.  fp32: forward 2e-5, gradients 1e-4; bf16 storage (inputs and
+    output gradient rounded to bf16 on both sides): 4e-3 and 1e-2."""
+    from ubio_molfm_amd import modules, neighbors, ops, systems
+    rc, lo = 12.0, 0.1
+    bf = act == "bf16"
+    adt = torch.bfloat16 if bf else torch.float32
+    s = systems.small_water(8, 6.2, seed=6)
+    pos = torch.as_tensor(s["pos"], device=cuda)
+    inc = torch.as_tensor(np.asarray(s["Z"]) != 1, device=cuda)
+    nl = neighbors.build_neighbors(pos, s["graph_ptr"], s["cell"], s["pbc"], rc, lo, src_include=inc)
+    N, E = nl.n_atoms, nl.n_edges
+    print(f"[attn zero-order {env} {act}] N={N} E={E}", flush=True)
+    q, k, v = _attn_inputs(nl, cuda, seed=12)
+    G = torch.randn(N, 9, 256, generator=torch.Generator().manual_seed(13))
+    if bf:
+        q, k, v, G = (t.to(torch.bfloat16).float() for t in (q, k, v, G))
+    rb = modules.GaussianSmearing(256, rc, 2.0)
+    prof = _profile(14, 512)
+    tgt, src = _embeddings(15, 256, 128)
+    net64 = copy.deepcopy(prof).double().net
+    tw, sw = tgt.weight.detach().double().clone(), src.weight.detach().double().clone()
+    type_z, slot = _types(pkg, cuda, s["Z"])
+    tab = ops.RadialTable([prof.to(cuda).net], tgt.to(cuda), src.to(cuda), rb.offset.to(cuda), rb.coeff, rc, type_z,
+                          layout="attn")
+    P = modules.slice_perm(cuda)
+    Pinv = torch.argsort(P)
+    env_t = (1, lo) if env == "bell" else (0, 0.0)
+    dvec = nl.dvec.clone().requires_grad_(True)
+    dist = nl.dist.clone().requires_grad_(True)
+    qd = q.to(cuda).requires_grad_(True); kd = k.to(cuda).requires_grad_(True)
+    vd = v.permute(1, 0, 2).to(cuda)[:, :, P].contiguous().requires_grad_(True)
+    out = ops.AttentionFn.apply(qd, kd, vd, dvec, dist, nl, slot, tab, rc, math.sqrt(8.0), adt, True, env_t)
+    assert out.shape == (9, N, 256)
+    Gd = G.permute(1, 0, 2).to(cuda)[:, :, P].contiguous()
+    out.backward(Gd.to(out.dtype))
+    row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()
+    Z = torch.as_tensor(np.asarray(s["Z"]))
+    leaves = [t.double().requires_grad_(True) for t in (q, k, v, nl.dist.cpu())]
+    gi = mlp_ref(leaves[3], Z[row], Z[col], net64, tw, sw, rb.offset.double(), float(np.float32(rb.coeff)))
+    env_fn = (lambda d: bell(d, lo, rc)) if env == "bell" else (lambda d: envelope(d, rc))
+    ref = attn0_ref(*leaves[:3], leaves[3], row, col, gi, env_fn, N)
+    e_f = relerr(out.float()[:, :, Pinv].permute(1, 0, 2), ref)
+    grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
+    errs = dict(q=relerr(qd.grad, grads[0]), k=relerr(kd.grad, grads[1]),
+                v=relerr(vd.grad[:, :, Pinv].permute(1, 0, 2), grads[2]), dist=relerr(dist.grad, grads[3]))
+    print(f"[attn zero-order {env} {act}] fwd rel {e_f:.2e} bwd {errs}", flush=True)
+    assert torch.count_nonzero(dvec.grad) == 0
+    assert e_f < (4e-3 if bf else 2e-5)
+    for name, e in errs.items():
+        assert e < (1e-2 if bf else 1e-4), (name, e)
 
 
 def test_degree_forward_backward(pkg, cuda):

@@ -206,6 +206,48 @@ def test_degree_embedding_single_edge_pair():
             assert torch.allclose(out[row, l * l:(l + 1) ** 2], expect, rtol=1e-12, atol=1e-15), (row, l)
 
 
+def test_zero_order_attention_head_of_channel():
+    """Zero-order attention (e2former.py:411-416) on two atoms with one edge per
+    row, proj_value and proj_zero the identity, and a profile whose gate is 0 and
+    whose inputhead is 1 on head h0 only: the value of the neighbour comes
+    through on every one of the 9 rows exactly in the channels whose head is
+    h0 (channels h0 and h0 + H, the reshape of the value row to [9 C / H, H]),
+    scaled by alpha = p ih / (p + 1e-3).  Catches: heads taken as contiguous
+    channel pairs (channels 2 h0, 2 h0 + 1), the value reshaped head-major
+    ([H, 9 C / H]), alpha divided by the distance (the first-order weight),
+    the aggregation reading the query's own value."""
+    torch.manual_seed(4)
+    H, C = 4, 8
+    ga = om.E2AttentionArbOrder_sparse(C=C, attn_weight_input_dim=6, num_attn_heads=H, attn_scalar_head=2,
+                                       attn_type="zero-order").double()
+    with torch.no_grad():
+        for lin in (ga.proj_value, ga.proj_zero):
+            lin.weight.copy_(torch.eye(C, dtype=D64).expand(3, C, C))
+            lin.bias.zero_()
+        last = ga.fc_easy.net[-1]
+        last.weight.zero_()
+        last.bias.zero_()
+        h0 = 1
+        last.bias[H + h0] = 1.0                    # inputhead of head h0; gate 0
+    Z = torch.tensor([8, 6])
+    pos = torch.tensor([[0.0, 0.0, 2.5], [0.0, 0.0, 0.0]], dtype=D64)
+    qi, nj = torch.tensor([0, 1]), torch.tensor([1, 0])
+    vec = pos[qi] - pos[nj]
+    dist = vec.norm(dim=-1)
+    poly = om.polynomial(dist, 6.0)
+    rbf = om.GaussianSmearing(6, cutoff=6.0).double()(dist)
+    x = torch.randn(2, 9, C, dtype=D64)
+    bd = dict(query_idx=qi, neighbor_idx=nj, f_outcell_index=torch.arange(2), f_exp_node_pos=pos)
+    out, _ = ga(pos, x, dist, vec, rbf, Z, poly, bd)
+    p = float(poly[0])
+    alpha = p / (p + 1e-3)
+    chans = torch.tensor([h0, h0 + H])
+    for row in (0, 1):
+        expect = torch.zeros(9, C, dtype=D64)
+        expect[:, chans] = alpha * x[1 - row][:, chans]
+        assert torch.allclose(out[row], expect, rtol=1e-13, atol=1e-15), row
+
+
 def test_chunked_sparse_ops_equal_fallbacks(monkeypatch):
     """The edge-chunked QK / value aggregation (used by the oracle above
     CHUNKED_EDGES edges, e.g. for the CPU baseline at 10k atoms) give the same

@@ -1,0 +1,57 @@
+"""Backbone variants on the CPU (construction only, no GPU calls): attention
+types per block ("a+b", e2former.py:792-795,863), the long-range cluster
+modules of with_cluster="node*" (e2former.py:887-929) with the reference's
+parameter names, and the configurations the reference rejects."""
+import pytest
+import torch
+
+
+def _cfg(**over):
+    from ubio_molfm_amd import model
+    args = model.default_args(num_layers=4)
+    args.backbone_config.update(over)
+    return args
+
+
+def test_cluster_modules_and_state_dict_names(pkg):
+    from ubio_molfm_amd import model
+    from oracle.model import MolfmAtomic as OracleModel
+    m = model.MolfmAtomic(_cfg(with_cluster="node_bell", long_range_layers=3, long_cutoff_lower=0.2,
+                               long_cutoff_upper=10.0))
+    dec = m.decoder.decoder
+    assert dec.cluster and len(dec.long_blocks) == 3
+    assert all(b.ga.attn_type == "zero-order" and hasattr(b.ga, "proj_zero") for b in dec.long_blocks)
+    assert dec.long_envelope() == (1, 0.2)
+    assert float(dec.rbf_long.offset[-1]) == 10.0
+    assert dec.final_linear.weight.shape == (3, 256, 512)
+    om = OracleModel(with_cluster="node_bell", long_range_layers=3, long_cutoff_lower=0.2, long_cutoff_upper=10.0)
+    om.load_state_dict(m.state_dict(), strict=True)
+    m.load_state_dict(om.state_dict(), strict=True)
+
+
+def test_block_attention_types(pkg):
+    from ubio_molfm_amd import model
+    m = model.MolfmAtomic(_cfg(attn_type="so2-first-order+zero-order"))
+    types = [b.ga.attn_type for b in m.decoder.decoder.blocks]
+    assert types == ["so2-first-order", "so2-first-order", "zero-order", "zero-order"]
+    m0 = model.MolfmAtomic(_cfg(attn_type="zero-order"))
+    assert m0.decoder.decoder.l3_sequential == [(0, 1), (1, 1), (2, 1)]
+    assert not m0.decoder.decoder.cluster
+
+
+@pytest.mark.parametrize("over, err", [
+    (dict(attn_type="zero-order+so2-first-order"), ValueError),
+    (dict(with_cluster="edge"), ValueError),
+    (dict(attn_type="first-order"), NotImplementedError),
+])
+def test_rejected_configurations(pkg, over, err):
+    from ubio_molfm_amd import model
+    with pytest.raises(err):
+        model.MolfmAtomic(_cfg(**over))
+
+
+def test_cluster_polynomial_envelope(pkg):
+    from ubio_molfm_amd import model
+    dec = model.MolfmAtomic(_cfg(with_cluster="node")).decoder.decoder
+    assert dec.cluster and dec.long_envelope() == (0, 0.0)
+    assert (dec.long_cutoff_lower, dec.long_cutoff_upper) == (0.1, 12)

@@ -33,7 +33,7 @@ class NbrPlan(C.Structure):
                 ("pos", vp), ("atom_graph", vp), ("graph_atom_ptr", vp), ("graph_shift_ptr", vp),
                 ("graph_periodic", vp), ("shift_off", vp), ("grid_lo", vp), ("grid_h", vp), ("grid_dim", vp),
                 ("bin_base", vp), ("atom_bin", vp), ("bin_count", vp), ("bin_start", vp), ("bin_atoms", vp),
-                ("stats", vp)]
+                ("stats", vp), ("src_include", vp)]
 
 
 class PairPlan(C.Structure):
@@ -65,7 +65,8 @@ class AttnArgs(C.Structure):
                 ("row_ptr", vp), ("col", vp), ("edge_row", vp), ("key_ptr", vp), ("key_eid", vp),
                 ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("rtab", vp), ("atom_type", vp),
                 ("n_types", i32), ("rtab_n", i32), ("rtab_h", f32), ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32),
-                ("col_span", i32), ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp)]
+                ("col_span", i32), ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp),
+                ("zero_order", i32), ("env_kind", i32), ("env_lo", f32)]
 
 
 class DegArgs(C.Structure):

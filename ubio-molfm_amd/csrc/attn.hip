@@ -53,6 +53,7 @@ constexpr int kGroups = 4, kGroupHeads = kH / kGroups, kGroupC = kC / kGroups;
 __device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
   Envelope E;
   E.rc = A.rc; E.a = A.env_a; E.b = A.env_b; E.c = A.env_c;
+  E.lo = A.env_lo;
   return E;
 }
 
@@ -163,9 +164,11 @@ __device__ __forceinline__ float buf_act(__bf16*, __amdgpu_buffer_rsrc_t r, uint
 // are issued before the current edge is applied.  The two parities are added
 // once per row in LDS, the coupling table is applied and the slice's 20
 // output rows are written.
-template <typename TS>
+// kMode: 0 first order (polynomial envelope), 1 zero order (polynomial), 2 zero order (bell)
+template <typename TS, int kMode>
 __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __restrict__ out, float* __restrict__ mrow,
                                                     float* __restrict__ srow, int32_t* __restrict__ cnt) {
+  constexpr bool kZ = kMode != 0, kBell = kMode == 2;
   constexpr int CH = 32;               // edges per chunk
   __shared__ uint32_t ckof[CH];        // byte offsets of the edge's k row (head 16 s) and v rows (position 32 s)
   __shared__ uint32_t cvof[CH];
@@ -212,7 +215,7 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
       const int j = A.col[e];
       const float d = A.dist[e];
       float p, dp;
-      env.eval(d, p, dp);
+      env.template eval<kBell>(d, p, dp);
       ckof[lane] = ((uint32_t)j * kH + kSlH * s) * (kD * sizeof(TS));
       cvof[lane] = ((uint32_t)j * kC + kSlC * s) * sizeof(TS);
       cg[lane] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], p);
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
       cc += (av == m_new);
       const float ee = fexp(av - m_new) * cg[el].w;
       ls += ee;
-      coef_s[el][hh] = (ee * coef_s[el][hh]) * crR[el];
+      coef_s[el][hh] = kZ ? ee * coef_s[el][hh] : (ee * coef_s[el][hh]) * crR[el];
     }
     cc += __shfl_xor(cc, 16, kWave);
     cc += __shfl_xor(cc, 32, kWave);
@@ -313,13 +316,18 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
     };
     auto vapply = [&](int el, const float (&vv)[kNV]) {
       const float w = coef_s[el][hu];
-      const float4 g = cg[el];
-      const float wx = w * g.x, wy = w * g.y, wz = w * g.z;
+      if constexpr (kZ) {
 #pragma unroll
-      for (int r = 0; r < kNV; ++r) {
-        acc[r][0] = fmaf(vv[r], wx, acc[r][0]);
-        acc[r][1] = fmaf(vv[r], wy, acc[r][1]);
-        acc[r][2] = fmaf(vv[r], wz, acc[r][2]);
+        for (int r = 0; r < kNV; ++r) acc[r][0] = fmaf(vv[r], w, acc[r][0]);
+      } else {
+        const float4 g = cg[el];
+        const float wx = w * g.x, wy = w * g.y, wz = w * g.z;
+#pragma unroll
+        for (int r = 0; r < kNV; ++r) {
+          acc[r][0] = fmaf(vv[r], wx, acc[r][0]);
+          acc[r][1] = fmaf(vv[r], wy, acc[r][1]);
+          acc[r][2] = fmaf(vv[r], wz, acc[r][2]);
+        }
       }
     };
     int el = par;
@@ -356,15 +364,22 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
     }
     // this lane (sub = u / 16, hh = u % 16) holds the statistics of head 16 s + hu
     const float inv = 1.0f / (s_run + kEps);
-    float o[kNT];
+    if constexpr (kZ) {
+      // zero order: the aggregated rows themselves, m-major [9][N][C]
+      const size_t os = (size_t)A.n_rows * kC;
 #pragma unroll
-    for (int q = 0; q < kNT; ++q) o[q] = 0.f;
+      for (int r = 0; r < kNV; ++r) store_act(acc[r][0] * inv, out + r * os + (size_t)i * kC + pu);
+    } else {
+      float o[kNT];
 #pragma unroll
-    for (int z = 0; z < kTpNnz; ++z) o[kTp[z].t] = fmaf(kTp[z].c, acc[kTp[z].r][kTp[z].k], o[kTp[z].t]);
-    const size_t nr = (size_t)A.n_rows;
+      for (int q = 0; q < kNT; ++q) o[q] = 0.f;
 #pragma unroll
-    for (int q = 0; q < kNT; ++q)
-      store_act(o[q] * inv, out + nr * kRowA[q] + (size_t)i * kRowLd[q] + kRowCol[q] + pu);
+      for (int z = 0; z < kTpNnz; ++z) o[kTp[z].t] = fmaf(kTp[z].c, acc[kTp[z].r][kTp[z].k], o[kTp[z].t]);
+      const size_t nr = (size_t)A.n_rows;
+#pragma unroll
+      for (int q = 0; q < kNT; ++q)
+        store_act(o[q] * inv, out + nr * kRowA[q] + (size_t)i * kRowLd[q] + kRowCol[q] + pu);
+    }
   }
   if (lane < kSlH) {
     mrow[(size_t)i * kH + h] = m_run;
@@ -392,10 +407,11 @@ __device__ __forceinline__ void tp_transpose(const float (&g)[kNT], float (&dA)[
 // slots come from e2v2_cluster_slots (R = 4); without, R = 1 and the slots of
 // column j are its key-CSR edges.  w_g and dqk_g hold the group's 32 heads per
 // edge ([E][32]), written by the row pass of the same group.
-template <int R, typename TS, bool kSlots>
+template <int R, typename TS, bool kSlots, int kMode>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_bwd_col_grp(
     e2v2_attn_args A, const TS* __restrict__ G, const float* __restrict__ w_g, const float* __restrict__ dqk_g,
     float* __restrict__ dv_out, float* __restrict__ dk_out, int grp) {
+  constexpr bool kZ = kMode != 0;
   static_assert(kSlots || R == 1, "columns without slots are clusters of one");
   constexpr int S = 32;                        // slots per staged chunk
   __shared__ int ci[S];
@@ -425,8 +441,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 #pragma unroll
     for (int d = 0; d < 4; ++d) ak[r][d] = 0.f;
   }
+  constexpr int NG = kZ ? kNV : kNT;   // rows of the output gradient
   struct Loads {
-    TS g[kNT];   // converted to fp32 in apply()
+    TS g[NG];   // converted to fp32 in apply()
     float q[4];
     float w[R];
     float dq[R];
@@ -434,7 +451,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   auto issue = [&](int sl, Loads& L) {
     const int i = ci[sl];
 #pragma unroll
-    for (int z = 0; z < kNT; ++z) L.g[z] = G[(size_t)A.n_rows * kRowA[z] + (size_t)i * kRowLd[z] + kRowCol[z] + c];
+    for (int z = 0; z < NG; ++z)
+      L.g[z] = kZ ? G[z * os + (size_t)i * kC + c]
+                  : G[(size_t)A.n_rows * kRowA[z] + (size_t)i * kRowLd[z] + kRowCol[z] + c];
     load4(Qp + ((size_t)i * kH + hk) * kD + d0, L.q);
     // unconditional (an absent edge reads edge 0, unused): every slot issues the
     // same loads, so the wait before apply() counts only the older slot's
@@ -446,18 +465,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     }
   };
   auto apply = [&](int sl, const Loads& L) {
-    float g[kNT], dA[kNV][3];
+    float g[NG], dA[kNV][3];
 #pragma unroll
-    for (int z = 0; z < kNT; ++z) g[z] = static_cast<float>(L.g[z]);
-    tp_transpose(g, dA);
+    for (int z = 0; z < NG; ++z) g[z] = static_cast<float>(L.g[z]);
+    if constexpr (!kZ) tp_transpose(g, dA);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (ce[sl][r] >= 0) {
         const float w = L.w[r];
-        const float wx = w * cdv[sl][r][0], wy = w * cdv[sl][r][1], wz = w * cdv[sl][r][2];
+        if constexpr (kZ) {
 #pragma unroll
-        for (int z = 0; z < kNV; ++z)
-          av[r][z] = fmaf(dA[z][2], wz, fmaf(dA[z][1], wy, fmaf(dA[z][0], wx, av[r][z])));
+          for (int z = 0; z < kNV; ++z) av[r][z] = fmaf(g[z], w, av[r][z]);
+        } else {
+          const float wx = w * cdv[sl][r][0], wy = w * cdv[sl][r][1], wz = w * cdv[sl][r][2];
+#pragma unroll
+          for (int z = 0; z < kNV; ++z)
+            av[r][z] = fmaf(dA[z][2], wz, fmaf(dA[z][1], wy, fmaf(dA[z][0], wx, av[r][z])));
+        }
 #pragma unroll
         for (int d = 0; d < 4; ++d) ak[r][d] = fmaf(L.dq[r], L.q[d], ak[r][d]);
       }
@@ -470,7 +494,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
       const int sl = idx / R, r = idx % R;
       const int e = kSlots ? sedge[(int64_t)(s0 + sl) * R + r] : A.key_eid[base + s0 + sl];
       ce[sl][r] = e;
-      if (e >= 0) {
+      if (!kZ && e >= 0) {
         cdv[sl][r][0] = A.dvec[3 * (int64_t)e];
         cdv[sl][r][1] = A.dvec[3 * (int64_t)e + 1];
         cdv[sl][r][2] = A.dvec[3 * (int64_t)e + 2];
@@ -570,13 +594,14 @@ __device__ __forceinline__ float row_sum4(float v0, float v1, float v2, float v3
 // distance, envelope, 1/d, dvec, table node and fraction) are formed once per
 // chunk in LDS, and the next edge's gathers are issued before the current one
 // is applied.
-template <typename TS>
+template <typename TS, int kMode>
 __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const TS* __restrict__ G,
                                                         const TS* __restrict__ O, const float* __restrict__ mrow,
                                                         const float* __restrict__ srow,
                                                         const int32_t* __restrict__ cnt, float* __restrict__ part,
                                                         float* __restrict__ dq, float* __restrict__ w_out,
                                                         float* __restrict__ dqk_out, int grp) {
+  constexpr bool kZ = kMode != 0, kBell = kMode == 2;
   constexpr int CH = 64;
   __shared__ float4 er_a[CH];      // p, dp/dd, 1/max(d, 1e-6), d
   __shared__ float4 er_b[CH];      // dvec, column (int bits)
@@ -602,25 +627,38 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
   float dA0[kNV][3], dA1[kNV][3];
   float inv, dsum, dmc, m;
   {
-    float g0[kNT], g1[kNT];
+    constexpr int NG = kZ ? kNV : kNT;   // output rows: 9 (zero order) or the 20 l3-grouped ones
+    float g0[NG], g1[NG];
     const size_t nr = (size_t)A.n_rows;
+    auto row_at = [&](int z) -> size_t {
+      return kZ ? z * os + (size_t)i * kC : nr * kRowA[z] + (size_t)i * kRowLd[z] + kRowCol[z];
+    };
 #pragma unroll
-    for (int z = 0; z < kNT; ++z) {
-      const size_t rz = nr * kRowA[z] + (size_t)i * kRowLd[z] + kRowCol[z];
+    for (int z = 0; z < NG; ++z) {
+      const size_t rz = row_at(z);
       g0[z] = f32(G[rz + p0]);
       g1[z] = f32(G[rz + p1]);
     }
-    // D_h = sum over the head's two channels and the 20 rows, summed as the first channel then the second
+    // D_h = sum over the head's two channels and the output rows, summed as the first channel then the second
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
-    for (int z = 0; z < kNT; ++z) {
-      const size_t rz = nr * kRowA[z] + (size_t)i * kRowLd[z] + kRowCol[z];
+    for (int z = 0; z < NG; ++z) {
+      const size_t rz = row_at(z);
       d0 = fmaf(g0[z], f32(O[rz + p0]), d0);
       d1 = fmaf(g1[z], f32(O[rz + p1]), d1);
     }
     const float Dh = d1 + d0;
-    tp_transpose(g0, dA0);
-    tp_transpose(g1, dA1);
+    if constexpr (kZ) {
+      // zero order: u = G_i . v_j per channel, dA = G itself (component 0)
+#pragma unroll
+      for (int r = 0; r < kNV; ++r) {
+        dA0[r][0] = g0[r]; dA0[r][1] = dA0[r][2] = 0.f;
+        dA1[r][0] = g1[r]; dA1[r][1] = dA1[r][2] = 0.f;
+      }
+    } else {
+      tp_transpose(g0, dA0);
+      tp_transpose(g1, dA1);
+    }
     m = mrow[(size_t)i * kH + h];
     const float sr = srow[(size_t)i * kH + h];
     const int cn = cnt[(size_t)i * kH + h];
@@ -678,10 +716,10 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
     const float ex = fexp(a - m);
     const float ee = ex * pe;
     const float alpha = (ee * ih) * inv;
-    const float w = alpha * rR;
+    const float w = kZ ? alpha : alpha * rR;
     float U[3];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
+    for (int k = 0; k < (kZ ? 1 : 3); ++k) {
       float u0 = 0.f, u1 = 0.f;
 #pragma unroll
       for (int r = 0; r < kNV; ++r) {
@@ -690,9 +728,11 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
       }
       U[k] = u0 + u1;
     }
-    const float dw = U[0] * dvx + U[1] * dvy + U[2] * dvz;
-    const float dalpha = dw * rR;
-    const float dR = (d > 1e-6f) ? -dalpha * alpha * rR : 0.f;
+    if constexpr (kZ) U[1] = U[2] = 0.f;
+    // zero order: the weight is alpha itself and the output does not depend on dvec directly
+    const float dw = kZ ? U[0] : U[0] * dvx + U[1] * dvy + U[2] * dvz;
+    const float dalpha = kZ ? dw : dw * rR;
+    const float dR = (!kZ && d > 1e-6f) ? -dalpha * alpha * rR : 0.f;
     const float dih = dalpha * ee * inv;
     const float de = dalpha * ih * inv - dsum;
     float da = de * ee;
@@ -706,7 +746,7 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
     // dL/dd of this head: envelope, 1/d, and the profile (dL/dgate gate' + dL/dih ih')
     const float ddh = fmaf(da * qk, gate_d, fmaf(dih, ih_d, fmaf(dpv, dpe, dR)));
     // sums over the slice's 16 heads (this row of 16 lanes); quad q holds value q
-    const float sum = row_sum4(w * U[0], w * U[1], w * U[2], ddh, lane);
+    const float sum = row_sum4(kZ ? 0.f : w * U[0], w * U[1], w * U[2], ddh, lane);
     if ((lane & 3) == 0) part[((size_t)s * A.n_edges + e) * 4 + (hh >> 2)] = sum;
   };
   for (c0 = 0; c0 < n; c0 += CH) {
@@ -715,7 +755,7 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
       const int64_t e = (int64_t)b + c0 + lane;
       const float d = A.dist[e];
       float pe, dpe;
-      env.eval(d, pe, dpe);
+      env.template eval<kBell>(d, pe, dpe);
       er_a[lane] = make_float4(pe, dpe, 1.0f / fmaxf(d, 1e-6f), d);
       const int j = A.col[e];
       er_b[lane] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], __int_as_float(j));
@@ -765,7 +805,15 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
 
 using namespace e2v2;
 
+// kernel instantiation: 0 first order with the polynomial envelope, 1 zero order with the polynomial,
+// 2 zero order with the bell (checked by check_table)
+static int kernel_mode(const e2v2_attn_args& A) { return A.zero_order ? 1 + A.env_kind : 0; }
+
 static int check_table(const e2v2_attn_args& A, const char* who) {
+  E2V2_REQUIRE((A.zero_order == 0 || A.zero_order == 1) && (A.env_kind == 0 || A.env_kind == 1) &&
+                   (A.env_kind == 0 || (A.zero_order == 1 && A.env_lo >= 0.f && A.env_lo < A.rc)),
+               "%s: zero_order %d with envelope kind %d (lo %g, rc %g) is not supported (the bell envelope is "
+               "built for the zero-order layers)", who, A.zero_order, A.env_kind, (double)A.env_lo, (double)A.rc);
   E2V2_REQUIRE(A.rtab && A.atom_type && A.n_types >= 1 && A.n_types <= E2V2_MAX_TYPES && A.rtab_n >= 2 &&
                    A.rtab_h > 0.f,
                "%s: needs the fc_easy table and atom types (n_types %d, rtab_n %d)", who, A.n_types, A.rtab_n);
@@ -790,11 +838,17 @@ E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, f
   if (A.n_rows == 0) return 0;
   if (int rc = check_table(A, "attn_fwd")) return rc;
   const dim3 grid((unsigned)A.n_rows * kSl);
+  const int mode = kernel_mode(A);
   if (A.act_bf16) {
-    hipLaunchKernelGGL(k_attn_fwd_sl<__bf16>, grid, dim3(kWave), 0, s, A, static_cast<__bf16*>(out), mrow, srow,
-                       cnt);
+    auto* o = static_cast<__bf16*>(out);
+    if (mode == 2) hipLaunchKernelGGL((k_attn_fwd_sl<__bf16, 2>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
+    else if (mode == 1) hipLaunchKernelGGL((k_attn_fwd_sl<__bf16, 1>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
+    else hipLaunchKernelGGL((k_attn_fwd_sl<__bf16, 0>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
   } else {
-    hipLaunchKernelGGL(k_attn_fwd_sl<float>, grid, dim3(kWave), 0, s, A, static_cast<float*>(out), mrow, srow, cnt);
+    auto* o = static_cast<float*>(out);
+    if (mode == 2) hipLaunchKernelGGL((k_attn_fwd_sl<float, 2>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
+    else if (mode == 1) hipLaunchKernelGGL((k_attn_fwd_sl<float, 1>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
+    else hipLaunchKernelGGL((k_attn_fwd_sl<float, 0>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
   }
   E2V2_LAUNCHED("k_attn_fwd_sl");
   return 0;
@@ -810,7 +864,7 @@ E2V2_API size_t e2v2_attn_bwd_workspace(int64_t n_edges) {
 
 // The four head groups in turn: the row pass of the group's two slices, then its column pass (clusters when
 // given, else one column per workgroup); finally the slice partials are added per edge.
-template <typename TS>
+template <typename TS, int kMode>
 static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, const float* mrow, const float* srow,
                            const int32_t* cnt, float* ddvec, float* ddist, float* dq, float* dk, float* dv,
                            float* ws, hipStream_t s) {
@@ -819,15 +873,15 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
   float* dqk_g = ws + (size_t)E * kGroupHeads;
   float* part = ws + (size_t)E * 2 * kGroupHeads;
   for (int g = 0; g < kGroups; ++g) {
-    hipLaunchKernelGGL(k_attn_bwd_row_sl<TS>, dim3((unsigned)((A.n_rows + 3) / 4) * kXcd), dim3(kWave), 0, s, A, G, O,
+    hipLaunchKernelGGL((k_attn_bwd_row_sl<TS, kMode>), dim3((unsigned)((A.n_rows + 3) / 4) * kXcd), dim3(kWave), 0, s, A, G, O,
                        mrow, srow, cnt, part, dq, w_g, dqk_g, g);
     E2V2_LAUNCHED("k_attn_bwd_row_sl");
     if (A.col_slot_member) {
       const int n_cl = (A.n_rows + 3) / 4;
-      hipLaunchKernelGGL((k_attn_bwd_col_grp<4, TS, true>), dim3(xcd_grid(n_cl)), dim3(256), 0, s, A, G, w_g, dqk_g,
+      hipLaunchKernelGGL((k_attn_bwd_col_grp<4, TS, true, kMode>), dim3(xcd_grid(n_cl)), dim3(256), 0, s, A, G, w_g, dqk_g,
                          dv, dk, g);
     } else {
-      hipLaunchKernelGGL((k_attn_bwd_col_grp<1, TS, false>), dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_g,
+      hipLaunchKernelGGL((k_attn_bwd_col_grp<1, TS, false, kMode>), dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_g,
                          dqk_g, dv, dk, g);
     }
     E2V2_LAUNCHED("k_attn_bwd_col_grp");
@@ -850,9 +904,17 @@ E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, con
                    reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
                "attn_bwd: workspace of %zu bytes (16-byte aligned) needed, got %zu", need, workspace_bytes);
   float* ws = static_cast<float*>(workspace);
-  if (A.act_bf16)
-    return attn_bwd_launch(A, static_cast<const __bf16*>(grad_out), static_cast<const __bf16*>(out), mrow, srow,
-                           cnt, ddvec, ddist, dq, dk, dv, ws, s);
-  return attn_bwd_launch(A, static_cast<const float*>(grad_out), static_cast<const float*>(out), mrow, srow, cnt,
-                         ddvec, ddist, dq, dk, dv, ws, s);
+  const auto* Gb = static_cast<const __bf16*>(grad_out);
+  const auto* Ob = static_cast<const __bf16*>(out);
+  const auto* Gf = static_cast<const float*>(grad_out);
+  const auto* Of = static_cast<const float*>(out);
+  const int mode = kernel_mode(A);
+  if (A.act_bf16) {
+    if (mode == 2) return attn_bwd_launch<__bf16, 2>(A, Gb, Ob, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
+    if (mode == 1) return attn_bwd_launch<__bf16, 1>(A, Gb, Ob, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
+    return attn_bwd_launch<__bf16, 0>(A, Gb, Ob, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
+  }
+  if (mode == 2) return attn_bwd_launch<float, 2>(A, Gf, Of, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
+  if (mode == 1) return attn_bwd_launch<float, 1>(A, Gf, Of, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
+  return attn_bwd_launch<float, 0>(A, Gf, Of, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
 }

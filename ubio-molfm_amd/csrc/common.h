@@ -132,10 +132,28 @@ __device__ __forceinline__ void raw_sh2(float x, float y, float z, float (&Y)[9]
   Y[8] = s3 / 2.0f * (z * z - x * x);
 }
 
-// polynomial envelope (exponent 5): p = 1 + r^5 (a + r (b + c r)), 0 for r >= 1
+// Distance envelope of the attention weights.  kind 0: the polynomial of exponent 5,
+// p = 1 + r^5 (a + r (b + c r)), r = d / rc, 0 for r >= 1 (module_utils.py:1946-1954);
+// kind 1: the smooth bell (1 - t^2)^2, t = (2 d - (lo + hi)) / (hi - lo) clamped to
+// [-1, 1], hi = max(rc, lo + 1e-8) (module_utils.py:1956-1985, exponent 2).
 struct Envelope {
   float rc, a, b, c;
+  float lo = 0.f;   // lower end of the bell
+  template <bool kBell = false>
   __device__ __forceinline__ void eval(float d, float& p, float& dp_dd) const {
+    if constexpr (kBell) {
+      const float hi = fmaxf(rc, lo + 1e-8f);
+      const float t = (2.0f * d - (lo + hi)) / (hi - lo);
+      if (t > -1.0f && t < 1.0f) {
+        const float u = 1.0f - t * t;
+        p = u * u;
+        dp_dd = -8.0f * u * t / (hi - lo);
+      } else {
+        p = 0.0f;
+        dp_dd = 0.0f;
+      }
+      return;
+    }
     float r = d / rc;
     if (r < 1.0f) {
       float r2 = r * r, r4 = r2 * r2, r5 = r4 * r;

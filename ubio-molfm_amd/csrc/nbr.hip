@@ -191,7 +191,7 @@ __device__ void visit_edges_wave(const e2v2_nbr_plan& P, int i, Emit&& emit) {
         j = P.bin_atoms[t];
         exact_edge(pi, P.pos + 3 * j, off, dx, dy, dz);
         d = exact_dist(dx, dy, dz);
-        ok = d >= P.rmin && d <= P.rc;
+        ok = d >= P.rmin && d <= P.rc && (P.src_include == nullptr || P.src_include[j] != 0);
         if (ok && periodic && !(d < P.rc)) {
           float img[3];
           {

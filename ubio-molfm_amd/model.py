@@ -136,6 +136,10 @@ class E2FormerBackbone(nn.Module):
         dvec, dist = EdgeGeometryFn.apply(pos, nl)
         ctx = EdgeContext(nl, dvec, dist, slot.contiguous(), type_z, type_key, self.decoder.rbf, self.max_radius,
                           self.compute_bf16)
+        long_ctx = None
+        if self.decoder.cluster:
+            long_ctx = self.long_range_context(pos, Z if perm is None else Z[perm], graph_ptr, cell, pbc, slot,
+                                               type_z, type_key)
         sys_node = None
         if charge is not None:
             B = len(graph_ptr) - 1
@@ -144,7 +148,24 @@ class E2FormerBackbone(nn.Module):
                                             dim=-1)).reshape(B, -1)
             counts = torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device)
             sys_node = torch.repeat_interleave(sys_emb, counts, dim=0)
-        return self.decoder.forward_flat(ctx, sys_node), nl, perm
+        return self.decoder.forward_flat(ctx, sys_node, long_ctx), nl, perm
+
+    def long_range_context(self, pos, Z, graph_ptr, cell, pbc, slot, type_z, type_key) -> EdgeContext:
+        """Edge context of the long-range cluster blocks (e2former_wrapper.py:223-243):
+        neighbours j with long_cutoff_lower <= d <= long_cutoff_upper whose atomic
+        number is neither 0 nor 1, at most 2.5 max_neighbors per atom (all when
+        max_neighbors is None), rbf_long as the distance basis and the bell or
+        polynomial envelope of with_cluster."""
+        dec = self.decoder
+        lo, hi = float(dec.long_cutoff_lower), float(dec.long_cutoff_upper)
+        include = (Z != 0) & (Z != 1)
+        mx = None if self.max_neighbors is None else int(2.5 * self.max_neighbors)
+        nl = build_neighbors(pos.detach(), graph_ptr, cell, pbc, hi, lo, mx, self.cells_per_direction,
+                             src_include=include.contiguous())
+        dvec, dist = EdgeGeometryFn.apply(pos, nl)
+        kind, env_lo = dec.long_envelope()
+        return EdgeContext(nl, dvec, dist, slot.contiguous(), type_z, type_key, dec.rbf_long, hi, self.compute_bf16,
+                           kind, env_lo)
 
     # -- reference interface -------------------------------------------------
     def forward(self, batched_data, **kwargs) -> Dict:

@@ -332,7 +332,9 @@ class SO2OutFn(torch.autograd.Function):
     hold their cnt coupling paths side by side, [2 l3 + 1][N][cnt C], the
     operand of forward_linear's Linear(cnt C -> C); its weight (path_norm and the
     path scales folded, input rows in the kernels' slice order) times
-    proj_first's W_l3^T is one [cnt C, O] weight (``so2_out_weights``)."""
+    proj_first's W_l3^T is one [cnt C, O] weight (``so2_out_weights``).  The
+    zero-order rows [9][N][C] are the case cnt = 1 with proj_zero's W_l^T
+    (``zero_out_weights``, e2former.py:411-416)."""
 
     @staticmethod
     def forward(ctx, so2, res, Wc, bias, N: int):
@@ -807,16 +809,22 @@ class SmoothLeakyReLU(nn.Module):
 class EdgeContext:
     """Per-evaluation edge data shared by every layer: the neighbour list, the edge
     geometry, each atom's type slot (atom_type [N], into type_z [T], the atomic
-    numbers present; type_key the host tuple of type_z) for the radial tables."""
+    numbers present; type_key the host tuple of type_z) for the radial tables, and
+    the distance envelope of the attention weights (poly_dist): env_kind 0 the
+    polynomial on [0, rc] (module_utils.py:1946-1954), 1 the smooth bell on
+    [env_lo, rc] (module_utils.py:1956-1985), the long-range list's "poly_bell"."""
 
     def __init__(self, nl, dvec, dist, atom_type, type_z, type_key, rbf: GaussianSmearing, rc: float,
-                 bf16: bool = False):
+                 bf16: bool = False, env_kind: int = 0, env_lo: float = 0.0):
         self.nl, self.dvec, self.dist = nl, dvec, dist
         self.atom_type, self.type_z, self.type_key = atom_type, type_z, type_key
         self.rbf_offset = rbf.offset.float().contiguous()
         self.rbf_coeff = float(rbf.coeff)
         self.rc = rc
         self.bf16 = bf16          # bf16 GEMM operands, fp32 accumulation and storage
+        if env_kind not in (0, 1) or (env_kind == 1 and not 0.0 <= env_lo < rc):
+            raise ValueError(f"envelope kind {env_kind} on [{env_lo}, {rc}] is not supported")
+        self.env_kind, self.env_lo = int(env_kind), float(env_lo)
 
 
 def atom_type_slots(Z: torch.Tensor):
@@ -836,18 +844,19 @@ _REF_CTX_KEY = "_e2v2_edge_context"
 
 
 def reference_edge_context(batched_data, edge_vec, edge_dis, atomic_numbers, rbf, rc: float,
-                           bf16: bool = False) -> EdgeContext:
+                           bf16: bool = False, env=(0, 0.0)) -> EdgeContext:
     """EdgeContext from the per-forward edge inputs of the reference's layers:
     batched_data's construct_radius_neighbor dict (query_idx, neighbor_idx,
     metadata) and f_outcell_index (expanded node -> atom), the edge vectors and
     distances (f_edge_vec, f_dist; gradients flow back to them), the flattened
     atomic numbers, the E2former's GaussianSmearing and cutoff.  Edges are taken
     in query-row order (the metadata's q_alpha_index, the identity for the
-    reference's sorted lists).  Built once per batched_data and reused by every
-    layer (kept in batched_data under "_e2v2_edge_context")."""
+    reference's sorted lists).  env: the envelope (kind, lower end) of
+    EdgeContext.  Built once per batched_data and reused by every layer (kept in
+    batched_data under "_e2v2_edge_context")."""
     ent = batched_data.get(_REF_CTX_KEY)
     if ent is not None and ent[0] is batched_data["query_idx"] and ent[1] is edge_vec and ent[2] is edge_dis \
-            and ent[3] is atomic_numbers:
+            and ent[3] is atomic_numbers and ent[5] == (float(rc), int(env[0]), float(env[1]), bool(bf16)):
         return ent[4]
     from .neighbors import neighbor_list_from_edges
     md = batched_data["metadata"]
@@ -860,13 +869,16 @@ def reference_edge_context(batched_data, edge_vec, edge_dis, atomic_numbers, rbf
     N = int(atomic_numbers.shape[0])
     nl = neighbor_list_from_edges(md[0], src, dvec, dist, N)
     type_z, type_key, slot = atom_type_slots(atomic_numbers)
-    ctx = EdgeContext(nl, dvec, dist, slot, type_z, type_key, rbf, float(rc), bf16)
-    batched_data[_REF_CTX_KEY] = (batched_data["query_idx"], edge_vec, edge_dis, atomic_numbers, ctx)
+    ctx = EdgeContext(nl, dvec, dist, slot, type_z, type_key, rbf, float(rc), bf16, env[0], env[1])
+    batched_data[_REF_CTX_KEY] = (batched_data["query_idx"], edge_vec, edge_dis, atomic_numbers, ctx,
+                                  (float(rc), int(env[0]), float(env[1]), bool(bf16)))
     return ctx
 
 
 class E2AttentionArbOrder_sparse(nn.Module):
-    """e2former.py:80-436 for tp_type=QK_alpha, attn_type=so2-first-order."""
+    """e2former.py:80-436 for tp_type=QK_alpha, attn_type so2-first-order or
+    zero-order (proj_zero on the alpha-weighted sum of the neighbours' values,
+    e2former.py:199-204,411-416)."""
 
     def __init__(self, irreps_node_input="256x0e+256x1e+256x2e", attn_weight_input_dim=256, num_attn_heads=128,
                  attn_scalar_head=8, irreps_head="2x0e+2x1e+2x2e", alpha_drop=0.0, tp_type="QK_alpha",
@@ -887,9 +899,15 @@ class E2AttentionArbOrder_sparse(nn.Module):
         self.query_linear = SO3_Linear2Scalar_e2former(C, num_attn_heads * attn_scalar_head, lmax=lmax)
         self.key_linear = SO3_Linear2Scalar_e2former(C, num_attn_heads * attn_scalar_head, lmax=lmax)
         self.proj_value = SO3_Linear_e2former(C, C, lmax=lmax)
-        self.first_order_tp = E2TensorProductSO2_FirstOrder(None, None, head=num_attn_heads, order=1, lmax=lmax,
-                                                            in_c=C, out_c=C)
-        self.proj_first = SO3_Linear_e2former(num_attn_heads * 2, C, lmax=lmax)
+        if attn_type == "zero-order":
+            self.proj_zero = SO3_Linear_e2former(C, C, lmax=lmax)
+        elif attn_type == "so2-first-order":
+            self.first_order_tp = E2TensorProductSO2_FirstOrder(None, None, head=num_attn_heads, order=1,
+                                                                lmax=lmax, in_c=C, out_c=C)
+            self.proj_first = SO3_Linear_e2former(num_attn_heads * 2, C, lmax=lmax)
+        else:
+            raise NotImplementedError(f"attn_type {attn_type!r}: the HIP path implements so2-first-order and "
+                                      "zero-order")
         self._radial = RadialCache()
 
     def qk_weights(self, bf16: bool = False):
@@ -914,11 +932,13 @@ class E2AttentionArbOrder_sparse(nn.Module):
             return pv.weight.detach()[:, P, :].contiguous(), pv.bias.detach()[P].contiguous()
         return cached(self, "v_sliced", (pv.weight, pv.bias), build)
 
-    def bind_edge_basis(self, rbf, max_radius: float):
+    def bind_edge_basis(self, rbf, max_radius: float, poly: str = "poly", min_dist: float = 0.0):
         """The E2former's GaussianSmearing and cutoff, for calls with the
         reference's signature (attn_weight = rbf(edge_dis) is evaluated inside
-        the kernels from the distance, as is poly_dist)."""
-        self._edge_basis = (rbf, float(max_radius))
+        the kernels from the distance, as is poly_dist: poly "poly" for
+        polynomial(d, max_radius), "poly_bell" for the bell on [min_dist,
+        max_radius] of the long-range list)."""
+        self._edge_basis = (rbf, float(max_radius), _env_of(poly, min_dist))
         return self
 
     def forward(self, *args, **kwargs):
@@ -931,26 +951,49 @@ class E2AttentionArbOrder_sparse(nn.Module):
 
     def forward_reference(self, node_pos, node_irreps_input, edge_dis, edge_vec, attn_weight, atomic_numbers,
                           poly_dist=None, attn_mask=None, batch=None, batched_data=None, rbf=None, max_radius=None,
-                          **kwargs):
+                          poly=None, min_dist=None, **kwargs):
         """E2AttentionArbOrder_sparse.forward (e2former.py:223-436) with its
         arguments: node_irreps_input [N, 9, C]; batched_data holds query_idx,
         neighbor_idx, metadata and f_outcell_index; edge_vec / edge_dis are
         f_edge_vec / f_dist.  attn_weight must be rbf(edge_dis) and poly_dist
-        polynomial(edge_dis, max_radius), both re-evaluated inside the kernels from
-        the distance; rbf and max_radius come from the keywords or
-        bind_edge_basis.  Returns (node_output [N, 9, C], attn_weight)."""
+        polynomial(edge_dis, max_radius) (poly="poly", the default) or
+        smooth_polynomial_bell(edge_dis, min_dist, max_radius) (poly="poly_bell"),
+        both re-evaluated inside the kernels from the distance; rbf, max_radius,
+        poly and min_dist come from the keywords or bind_edge_basis.  Returns
+        (node_output [N, 9, C], attn_weight)."""
         if batched_data is None:
             raise ValueError("batched_data with the neighbour dict is required")
+        basis = getattr(self, "_edge_basis", None)
         if rbf is None or max_radius is None:
-            basis = getattr(self, "_edge_basis", None)
             if basis is None:
                 raise ValueError("pass rbf= and max_radius= (the E2former's GaussianSmearing and cutoff) or call "
                                  "bind_edge_basis(rbf, max_radius) once")
-            rbf, max_radius = basis
-        ctx = reference_edge_context(batched_data, edge_vec, edge_dis, atomic_numbers, rbf, max_radius)
+            rbf, max_radius = basis[:2]
+        if poly is None and min_dist is None and basis is not None:
+            env = basis[2]
+        else:
+            env = _env_of(poly or "poly", 0.0 if min_dist is None else min_dist)
+        ctx = reference_edge_context(batched_data, edge_vec, edge_dis, atomic_numbers, rbf, max_radius, env=env)
         x = node_irreps_input.float().transpose(0, 1).contiguous()
         out = self.forward_fused(x, ctx)
         return out.transpose(0, 1).contiguous(), attn_weight
+
+    def zero_out_weights(self, bf16: bool = False):
+        """proj_zero as the operand list of SO2OutFn for the zero-order rows
+        [9, N, C]: per degree l, (l, 1, C l^2, W, W^T) with W = W_l^T [C, O], input
+        rows in the kernels' slice order (bf16 copies in bf16 mode)."""
+        pz = self.proj_zero
+
+        def build():
+            P = slice_perm(pz.weight.device)
+            C = pz.weight.shape[2]
+            dt = BF16 if bf16 else torch.float32
+            out = []
+            for l in range(self.lmax + 1):
+                W = pz.weight.detach()[l][:, P].t()
+                out.append((l, 1, C * l * l, W.to(dt).contiguous(), W.t().to(dt).contiguous()))
+            return out
+        return cached(self, "zero_out_bf16" if bf16 else "zero_out", (pz.weight,), build)
 
     def so2_out_weights(self, bf16: bool = False):
         """Per output degree l3 (l3 order): (l3, cnt, start, W, W^T) with W [cnt 256, O]
@@ -994,12 +1037,28 @@ class E2AttentionArbOrder_sparse(nn.Module):
         with record_function("rbf function-a"):   # fc_easy as a distance table, built once per weight version
             table = self._radial.get([self.fc_easy.net], self.target_embedding, self.source_embedding,
                                      ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="attn")
+        zero = self.attn_type == "zero-order"
         with record_function("qk attention"):
             so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table, ctx.rc,
-                                    math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32)
+                                    math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32, zero,
+                                    (ctx.env_kind, ctx.env_lo))
+        if zero:
+            with record_function("zero-order"):
+                return SO2OutFn.apply(so2.view(-1), res, self.zero_out_weights(bf16), self.proj_zero.bias.detach(),
+                                      N)
         pf = self.proj_first
         with record_function("first-order"):
             return SO2OutFn.apply(so2, res, self.so2_out_weights(bf16), pf.bias.detach(), N)
+
+
+def _env_of(poly: str, min_dist: float):
+    """EdgeContext's envelope (kind, lower end) of construct_radius_neighbor's
+    ``poly`` argument (module_utils.py:3184-3191)."""
+    if poly == "poly":
+        return (0, 0.0)
+    if poly == "poly_bell":
+        return (1, float(min_dist))
+    raise ValueError("sorry, you must set poly or poly_bell")
 
 
 class TransBlock(nn.Module):
@@ -1092,19 +1151,23 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
 
 
 class E2former(nn.Module):
-    """e2former.py:758-1145 (with_cluster off) on flattened atoms."""
+    """e2former.py:758-1145 on flattened atoms, with the long-range cluster
+    blocks of with_cluster="node*" (e2former.py:887-929,1088-1117)."""
 
     def __init__(self, irreps_node_embedding="256x0e+256x1e+256x2e", num_layers=4, max_neighbors=None,
                  max_radius=6.0, basis_type="gaussiansmear", number_of_basis=256, num_attn_heads=128,
                  attn_scalar_head=8, irreps_head="2x0e+2x1e+2x2e", norm_layer="rms_norm_sh", alpha_drop=0.0,
                  tp_type="QK_alpha", attn_type="so2-first-order", atom_type_cnt=256, edge_embedtype="default",
-                 ffn_type="s3", avg_degree=23.01, with_cluster=False, **kwargs):
+                 ffn_type="s3", avg_degree=23.01, with_cluster=False, long_range_layers=2, long_cutoff_lower=0.1,
+                 long_cutoff_upper=12, **kwargs):
         super().__init__()
         C, lmax = parse_irreps(irreps_node_embedding)
         check_supported(C, lmax, num_attn_heads, attn_scalar_head, number_of_basis, irreps_head, norm_layer,
                         tp_type, attn_type, ffn_type, basis_type, with_cluster, edge_embedtype)
         self.max_neighbors, self.max_radius, self.number_of_basis = max_neighbors, max_radius, number_of_basis
         self.num_layers, self.num_attn_heads, self.lmax = num_layers, num_attn_heads, lmax
+        # "a+b": type a for the first num_layers // 2 blocks, b for the rest (e2former.py:792-795,863)
+        self.attn_type = attn_type.split("+") if "+" in attn_type else [attn_type, attn_type]
         self._node_scalar_dim = C
         self.default_node_embedding = nn.Embedding(atom_type_cnt, C)
         self.heads2basis = nn.Linear(num_attn_heads, number_of_basis, bias=True)
@@ -1115,20 +1178,63 @@ class E2former(nn.Module):
             irreps_node_embedding, avg_degree, number_of_basis, max_radius, C=C, lmax=lmax)
         self.blocks = nn.ModuleList([
             TransBlock(irreps_node_embedding, irreps_node_embedding, number_of_basis, num_attn_heads,
-                       attn_scalar_head, irreps_head, alpha_drop, tp_type, attn_type, atom_type_cnt, norm_layer,
+                       attn_scalar_head, irreps_head, alpha_drop, tp_type,
+                       self.attn_type[0] if i < num_layers // 2 else self.attn_type[1], 256, norm_layer,
                        ffn_type, i, C=C, lmax=lmax) for i in range(num_layers)])
-        self.l3_sequential = self.blocks[0].ga.first_order_tp.so2_tp.l3_sequential
+        ga0 = self.blocks[0].ga
+        self.l3_sequential = (ga0.first_order_tp.so2_tp.l3_sequential if hasattr(ga0, "first_order_tp")
+                              else [(l, 1) for l in range(lmax + 1)])
+        if self.attn_type[0] == "zero-order" and "so2-first-order" in self.attn_type and num_layers > 1:
+            # the node frames are sized from block 0's product (e2former.py:877-881,991-1002): with a zero-order
+            # block 0 the reference's first-order blocks get the 9-row frames and fail in their forward
+            raise ValueError("attn_type 'zero-order+so2-first-order' is not runnable in the reference (its "
+                             "first-order blocks take the frames sized for a zero-order block 0); use "
+                             "'so2-first-order+zero-order'")
         self.norm_final = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
+        self.long_cutoff_lower, self.long_cutoff_upper = long_cutoff_lower, long_cutoff_upper
+        self.with_cluster = str(with_cluster)
+        if "node" in self.with_cluster:
+            self.pre_norm_node = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
+            self.norm_cluster = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
+            self.final_linear = SO3_Linear_e2former(2 * C, C, lmax=lmax, bias=True)
+            self.rbf_long = GaussianSmearing(number_of_basis, cutoff=long_cutoff_upper, basis_width_scalar=2)
+            self.long_blocks = nn.ModuleList([
+                TransBlock(irreps_node_embedding, irreps_node_embedding, number_of_basis, num_attn_heads,
+                           attn_scalar_head, irreps_head, alpha_drop, tp_type, "zero-order", 256, norm_layer,
+                           ffn_type, i, C=C, lmax=lmax) for i in range(long_range_layers)])
+            self.norm_final = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
 
-    def forward_flat(self, ctx: EdgeContext, sys_node_embedding: Optional[torch.Tensor] = None):
-        """Returns the node irreps in the m-major layout [9, N, C]."""
+    @property
+    def cluster(self) -> bool:
+        return "node" in self.with_cluster
+
+    def long_envelope(self):
+        """(kind, lower end) of the long-range list's envelope: the bell on
+        [long_cutoff_lower, long_cutoff_upper] when with_cluster names "bell",
+        else the polynomial on [0, long_cutoff_upper] (e2former_wrapper.py:240)."""
+        return (1, float(self.long_cutoff_lower)) if "bell" in self.with_cluster else (0, 0.0)
+
+    def forward_flat(self, ctx: EdgeContext, sys_node_embedding: Optional[torch.Tensor] = None,
+                     long_ctx: Optional[EdgeContext] = None):
+        """Returns the node irreps in the m-major layout [9, N, C].  long_ctx: the
+        long-range neighbour list's edge context (with_cluster only)."""
         with record_function("node_initiliation"):
             x = self.edge_deg_embed_dense(ctx)
         d = None
         for i, blk in enumerate(self.blocks):
             with record_function(f"tranblock {i}"):
                 x, d = blk.forward_deferred(x, d, ctx, sys_node_embedding)
-        return self.norm_final.add_forward(x, d)[0]
+        if not self.cluster:
+            return self.norm_final.add_forward(x, d)[0]
+        if long_ctx is None:
+            raise ValueError("cluster_neighbor_info is required when with_cluster contains 'node'.")
+        x, short = self.pre_norm_node.add_forward(x, d)
+        d = None
+        for i, blk in enumerate(self.long_blocks):
+            with record_function(f"long-tranblock {i}"):
+                x, d = blk.forward_deferred(x, d, long_ctx, sys_node_embedding)
+        x = self.norm_cluster.add_forward(x, d)[0]
+        return self.final_linear(torch.cat([short, x], dim=-1), bf16=ctx.bf16)
 
 
 def parse_irreps(s: str):
@@ -1147,11 +1253,14 @@ def check_supported(C, lmax, heads, head_dim, n_basis, irreps_head, norm_layer, 
     hc, hl = parse_irreps(irreps_head)
     ok = (C == 256 and lmax == 2 and heads == 128 and head_dim == 8 and n_basis == 256 and hc * heads == C
           and hl == lmax and norm_layer in ("rms_norm_sh", "rms_norm_sh_BL") and tp_type.split("+")[0] == "QK_alpha"
-          and attn_type == "so2-first-order" and ("s3" in ffn_type or "default" in ffn_type)
-          and basis_type == "gaussiansmear" and str(with_cluster) in ("False", "false", "0", "None", "none")
-          and "wolayernorm" not in edge_embedtype)
+          and all(a in ("so2-first-order", "zero-order") for a in attn_type.split("+"))
+          and len(attn_type.split("+")) <= 2 and ("s3" in ffn_type or "default" in ffn_type)
+          and basis_type == "gaussiansmear" and "wolayernorm" not in edge_embedtype)
     if not ok:
         raise NotImplementedError(
             "the MI355X path implements the E2Former-V2 production configuration: irreps 256x0e+256x1e+256x2e, "
             "irreps_head 2x0e+2x1e+2x2e, 128 heads, attn_scalar_head 8, 256 basis, rms_norm_sh, tp_type QK_alpha, "
-            "attn_type so2-first-order, ffn s3, no cluster blocks")
+            "attn_type so2-first-order / zero-order (or 'a+b' of the two), ffn s3")
+    if "node" not in str(with_cluster) and str(with_cluster) not in ("False", "false", "0", "None", "none"):
+        raise ValueError("Only with_cluster='node*' is restored in this release tree. "
+                         "Other cluster modes require removed modules.")

@@ -109,12 +109,15 @@ def _vp(t: Optional[torch.Tensor]):
 
 
 def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
-              cells_per_direction: int = 4, grid_box=None, workspace: bool = True):
+              cells_per_direction: int = 4, grid_box=None, workspace: bool = True,
+              src_include: Optional[torch.Tensor] = None):
     """The e2v2_nbr_plan of a batch (pos [N,3] fp32 on the GPU, graphs contiguous;
     graph_ptr, cells, pbcs on the host): per-graph shift tables, bin grids and,
     with ``workspace``, the bin workspace tensors.  Returns (plan, tensors kept
     alive for it, the shift table, its per-graph row pointers).  Without
-    ``grid_box`` the atoms' bounding boxes are read back (one host sync)."""
+    ``grid_box`` the atoms' bounding boxes are read back (one host sync).
+    ``src_include`` ([N] bool on the GPU, or None) restricts the edge sources
+    (neighbour atoms j) to the marked atoms."""
     dev = pos.device
     graph_ptr = np.asarray(graph_ptr, np.int64)
     cells = np.asarray(cells, F32).reshape(-1, 3, 3)
@@ -176,22 +179,30 @@ def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float 
                     bin_start=torch.empty(nb + 1, **i32), bin_atoms=torch.empty(max(N, 1), **i32),
                     stats=torch.zeros(3, **i32))
         ws = [keep[k].data_ptr() for k in ("atom_bin", "bin_count", "bin_start", "bin_atoms", "stats")]
+    inc = None
+    if src_include is not None:
+        if src_include.shape != (N,) or src_include.device != dev:
+            raise ValueError(f"src_include must be a [{N}] tensor on {dev}")
+        keep["src_include"] = src_include.to(torch.uint8).contiguous()
+        inc = keep["src_include"].data_ptr() if N else None
     plan = _lib.NbrPlan(N, B, nb, len(offs), rc, rmin, pos.data_ptr(), atom_graph.data_ptr(), t_gptr.data_ptr(),
                         t_sptr.data_ptr(), t_per.data_ptr(), t_off.data_ptr(), t_lo.data_ptr(), t_h.data_ptr(),
-                        t_dim.data_ptr(), t_base.data_ptr(), *ws)
+                        t_dim.data_ptr(), t_base.data_ptr(), *ws, inc)
     return plan, keep, shifts_np, sptr
 
 
 def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
                     max_neighbors: Optional[int] = None, cells_per_direction: int = 4,
-                    grid_box=None) -> NeighborList:
+                    grid_box=None, src_include: Optional[torch.Tensor] = None) -> NeighborList:
     """pos [N,3] fp32 on the GPU (graphs contiguous); graph_ptr [B+1], cells
     [B,3,3], pbcs [B,3] on the host.  grid_box [2,B,3] (optional, host): per-graph
     (lo, hi) corners of the bin grid that contain every atom, e.g. the cell of
     positions wrapped into it; without it the atoms' bounding boxes are read back
     (one host sync).  The edge list does not depend on the grid.  An atom outside
     the supplied box is detected on the device (read back with the edge count)
-    and the list is rebuilt with the bounding boxes."""
+    and the list is rebuilt with the bounding boxes.  src_include ([N] bool on
+    the GPU, or None): only marked atoms are edge sources (every atom is still a
+    query row)."""
     if not pos.is_cuda:
         raise RuntimeError("build_neighbors runs on the GPU only (pos must be a CUDA/HIP tensor)")
     dev = pos.device
@@ -202,7 +213,8 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     N = int(pos.shape[0])
     stream = torch.cuda.current_stream(dev).cuda_stream
     i32 = dict(dtype=torch.int32, device=dev)
-    plan, keep, shifts_np, sptr = make_plan(pos, graph_ptr, cells, pbcs, rc, rmin, cells_per_direction, grid_box)
+    plan, keep, shifts_np, sptr = make_plan(pos, graph_ptr, cells, pbcs, rc, rmin, cells_per_direction, grid_box,
+                                            src_include=src_include)
     stats = keep["stats"]
     _lib.call("e2v2_nbr_bin", _lib.C.byref(plan), _lib.vp(stream))
     row_count = torch.empty(max(N, 1), **i32)
@@ -213,7 +225,8 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     if outside:
         if grid_box is None:
             raise RuntimeError("neighbour build: an atom lies outside its own bounding box")
-        return build_neighbors(pos, graph_ptr, cells, pbcs, rc, rmin, max_neighbors, cells_per_direction)
+        return build_neighbors(pos, graph_ptr, cells, pbcs, rc, rmin, max_neighbors, cells_per_direction,
+                               src_include=src_include)
     f32t = dict(dtype=torch.float32, device=dev)
     tcol = torch.empty(max(E, 1), **i32); tsh = torch.empty(max(E, 1), **i32)
     tdv = torch.empty(max(E, 1), 3, **f32t); td = torch.empty(max(E, 1), **f32t)

@@ -247,8 +247,11 @@ def deg_args(nl: NeighborList, atom_type: torch.Tensor, table: RadialTable, avg:
                         table.h, float(avg), float(rc), ENV_A, ENV_B, ENV_C)
 
 
-def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: float, rc: float, bf: int):
-    """e2v2_attn_args over the neighbour list (with its column clusters when built)."""
+def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: float, rc: float, bf: int,
+              zero_order: bool = False, env=(0, 0.0)):
+    """e2v2_attn_args over the neighbour list (with its column clusters when built).
+    zero_order selects the zero-order aggregation; env = (kind, lower end): kind 0
+    the polynomial envelope on [0, rc], 1 the smooth bell on [lower end, rc]."""
     if table.nc != 256 or table.layout != "attn":
         raise ValueError("the attention needs the table of its fc_easy profile in slice order (layout 'attn')")
     a = _lib.AttnArgs(nl.n_atoms, nl.n_edges, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(),
@@ -256,6 +259,8 @@ def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: f
                       nl.dist.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.tab.data_ptr(),
                       atom_type.data_ptr(), table.n_types, table.n_nodes, table.h, float(q_div), float(rc), ENV_A,
                       ENV_B, ENV_C, int(bf))
+    a.zero_order = int(bool(zero_order))
+    a.env_kind, a.env_lo = int(env[0]), float(env[1])
     if nl.col_slot_member is not None:
         a.col_span = nl.col_span
         a.col_slot_member = nl.col_slot_member.data_ptr()
@@ -272,13 +277,18 @@ class AttentionFn(torch.autograd.Function):
     q, k [N, 128, 8], v [9, N, 256], the channels of v and of the output in the
     kernels' slice order (modules.slice_perm).  gate and inputhead
     (fc_easy, e2former.py:258-306) are interpolated from the layer's radial table
-    inside the kernels: only node-level tensors are saved."""
+    inside the kernels: only node-level tensors are saved.
+
+    With ``zero_order`` the edge part of the zero-order attention
+    (e2former.py:411-416) instead: the 9 rows sum_j alpha_ij,h(c) v_j (no 1/r, no
+    SO(2) product), [9, N, 256] m-major in the same slice order of channels."""
 
     @staticmethod
     def forward(ctx, q, k, v, dvec, dist, nl: NeighborList, atom_type, table: RadialTable, rc: float,
-                q_div: float, act_dtype=torch.float32):
+                q_div: float, act_dtype=torch.float32, zero_order: bool = False, env=(0, 0.0)):
         """act_dtype: storage of q, k, v and of the output rows (torch.float32, or
-        torch.bfloat16 in the bf16 mode: half the gather traffic, fp32 math)."""
+        torch.bfloat16 in the bf16 mode: half the gather traffic, fp32 math).
+        env: the distance envelope (kind, lower end), see attn_args."""
         _need_cuda(q, k, v, dvec, dist)
         if act_dtype not in (torch.float32, torch.bfloat16):
             raise ValueError(f"attention activations must be float32 or bfloat16, got {act_dtype}")
@@ -286,14 +296,18 @@ class AttentionFn(torch.autograd.Function):
         N = nl.n_atoms
         q = q.to(act_dtype).contiguous(); k = k.to(act_dtype).contiguous(); v = v.to(act_dtype).contiguous()
         bf = int(act_dtype == torch.bfloat16)
-        args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf)
-        out = torch.empty(20 * N * 256, dtype=act_dtype, device=dev)   # l3-grouped rows
+        args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env)
+        if zero_order:
+            out = torch.empty(9, N, 256, dtype=act_dtype, device=dev)
+        else:
+            out = torch.empty(20 * N * 256, dtype=act_dtype, device=dev)   # l3-grouped rows
         mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
         _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _p(out), _p(mrow), _p(srow), _p(cnt), _stream(q))
         ctx.save_for_backward(q, k, v, out, mrow, srow, cnt)
         ctx.nl, ctx.atom_type, ctx.table, ctx.rc, ctx.q_div, ctx.bf = nl, atom_type, table, rc, q_div, bf
+        ctx.zero_order, ctx.env = zero_order, env
         return out
 
     @staticmethod
@@ -304,7 +318,7 @@ class AttentionFn(torch.autograd.Function):
         dev = q.device
         E = nl.n_edges
         gout = gout.to(out.dtype).contiguous()
-        args = attn_args(nl, q, k, v, ctx.atom_type, ctx.table, ctx.q_div, ctx.rc, ctx.bf)
+        args = attn_args(nl, q, k, v, ctx.atom_type, ctx.table, ctx.q_div, ctx.rc, ctx.bf, ctx.zero_order, ctx.env)
         f = dict(dtype=torch.float32, device=dev)
         ddv = torch.empty(max(E, 1), 3, **f)
         dd = torch.empty(max(E, 1), **f)
@@ -316,4 +330,4 @@ class AttentionFn(torch.autograd.Function):
         _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(ddv),
                   _p(dd), _p(dq), _p(dk), _p(dv), _p(ws), _lib.C.c_size_t(ws.numel()), _stream(gout))
         del ws
-        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None
+        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None, None
