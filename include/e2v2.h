@@ -272,6 +272,27 @@ int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset,
                             const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h, const float* tab,
                             int32_t nc, const e2v2_radial_layout* layout, uint32_t* err, hipStream_t s);
 
+/* Per-edge values of a "plain"-layout table ([pairs][n_nodes][4][nc], nc channels): out [E][nc] =
+   f_c(dist[e]) for the pair (atom_type[edge_row[e]], atom_type[col[e]]), the quintic Hermite interpolant.
+   Replaces the per-edge RadialProfile calls of the QKdot gates, rad_func_m0(x_edge) (e2former.py:278)
+   and fc_easy(x_edge)[:, H:] (e2former.py:293-294). */
+int e2v2_radial_eval(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
+                     const int32_t* atom_type, const int32_t* edge_row, const int32_t* col, const float* dist,
+                     int64_t n_edges, float* out, hipStream_t s);
+/* ddist [E] = sum_c grad[e][c] f_c'(dist[e]) (fixed summation order). */
+int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
+                         const int32_t* atom_type, const int32_t* edge_row, const int32_t* col, const float* dist,
+                         int64_t n_edges, const float* grad, float* ddist, hipStream_t s);
+/* x0 [E][3][C] = sum_{m in l} Y[e][m] xn[m][row(e)][C] for l = 0, 1, 2 (Y [E][9], xn [9][n_rows][C]
+   m-major, edges of a row contiguous by row_ptr [n_rows + 1], C <= 256): the x_0_extra of QKdot_alpha
+   (e2former.py:271-276, Y the normalised spherical harmonics) and of QKdotS_alpha (e2former.py:288-296,
+   the raw polynomials of edge_vec with sum_vec's l blocks). */
+int e2v2_sh_contract(const float* Y, const float* xn, const int32_t* row_ptr, int32_t n_rows, int32_t C,
+                     float* x0, hipStream_t s);
+/* Its backward for the gradient g [E][3][C]: dY [E][9], dxn [9][n_rows][C] (per-row sums, no atomics). */
+int e2v2_sh_contract_bwd(const float* Y, const float* xn, const int32_t* row_ptr, int32_t n_rows, int32_t C,
+                         const float* g, float* dY, float* dxn, hipStream_t s);
+
 /* ---- attention --------------------------------------------------------- */
 /* Channel order of v, out, grad_out, dv and of the fc_easy table rows ("slice order"): position p of a
    row holds the first (model channel h, the gate in the table) or second (model channel 128 + h, the
@@ -312,6 +333,12 @@ typedef struct e2v2_attn_args {
      [env_lo, rc] (module_utils.py:1956-1985, exponent 2) */
   int32_t env_kind;
   float env_lo;
+  /* ext_gate [E][H] fp32 or NULL: the gate of every (edge, head) given by the caller (the QKdot_alpha /
+     QKdotS_alpha logits gates, e2former.py:270-300) instead of the table's gate rows, which are then not
+     read; with it e2v2_attn_bwd writes dL/dgate of every (edge, head) to ext_dgate [E][H] and leaves the
+     gate's distance derivative out of ddist */
+  const float* ext_gate;
+  float* ext_dgate;
 } e2v2_attn_args;
 
 /* v [9][N][C] is m-major (row r of every atom contiguous), channels in slice order.  out holds the 20

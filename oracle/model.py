@@ -317,14 +317,25 @@ def segment_alpha(logit, poly, inputhead, qi, n_rows):
     return e * inputhead / (asum[qi] + 1e-3)
 
 
+def e3nn_sh(l, vec, normalize=True):
+    """``e3nn.o3.spherical_harmonics(l, vec, normalize)`` with its default
+    normalization="integral" (e2former.py:274): the raw polynomials of the unit
+    vector scaled by sqrt(2 l + 1) / sqrt(4 pi)."""
+    u = vec / vec.norm(dim=-1, keepdim=True) if normalize else vec
+    raw = e3nn_raw_sh_l2(u[..., 0], u[..., 1], u[..., 2])
+    return raw[..., l * l:(l + 1) ** 2] * (math.sqrt(2 * l + 1) / math.sqrt(4 * math.pi))
+
+
 class E2AttentionArbOrder_sparse(nn.Module):
-    """``e2former.py:80-436`` for tp_type=QK_alpha, attn_type so2-first-order
-    or zero-order, with the torch fallbacks (``use_triton`` False)."""
+    """``e2former.py:80-436`` for tp_type QK_alpha, QKdot_alpha or QKdotS_alpha
+    and attn_type so2-first-order or zero-order, with the torch fallbacks
+    (``use_triton`` False)."""
 
     def __init__(self, C=256, attn_weight_input_dim=256, num_attn_heads=128, attn_scalar_head=8,
-                 lmax=2, atom_type_cnt=256, attn_type="so2-first-order"):
+                 lmax=2, atom_type_cnt=256, attn_type="so2-first-order", tp_type="QK_alpha"):
         super().__init__()
         self.attn_type = attn_type
+        self.tp_type = tp_type.split("+")[0]
         self.num_attn_heads, self.attn_scalar_head, self.lmax = num_attn_heads, attn_scalar_head, lmax
         self.node_embed_dim = 128
         self.source_embedding = nn.Embedding(atom_type_cnt, 128)
@@ -334,7 +345,22 @@ class E2AttentionArbOrder_sparse(nn.Module):
         self.alpha_act = SmoothLeakyReLU(0.2)
         ecl = [attn_weight_input_dim + 256, min(128, attn_weight_input_dim // 2), min(128, attn_weight_input_dim // 2)]
         self.alpha_dropout = nn.Dropout(0.0)
-        self.fc_easy = RadialProfile(ecl + [2 * num_attn_heads])
+        H = num_attn_heads
+        if self.tp_type == "QKdot_alpha":                   # e2former.py:143-154
+            self.dot_linear = SO3_Linear_e2former(C, attn_weight_input_dim, lmax=lmax)
+            self.rad_func_m0 = RadialProfile(ecl + [attn_weight_input_dim * (lmax + 1)])
+            self.fc_m0 = nn.Linear(attn_weight_input_dim * (lmax + 1), H)
+            self.fc_easy = RadialProfile(ecl + [H])
+        elif self.tp_type == "QKdotS_alpha":                # e2former.py:155-167
+            sv = torch.zeros([(lmax + 1) ** 2, lmax + 1])
+            for l in range(lmax + 1):
+                sv[l ** 2:(l + 1) ** 2, l] = 1
+            self.sum_vec = nn.Parameter(sv, requires_grad=False)
+            self.dot_linear = SO3_Linear_e2former(C, H // (lmax + 1) + 1, lmax=lmax)
+            self.direction_linear = nn.Sequential(nn.Linear(H, H), nn.LayerNorm(H), nn.SiLU(), nn.Linear(H, H))
+            self.fc_easy = RadialProfile(ecl + [2 * H])
+        else:
+            self.fc_easy = RadialProfile(ecl + [2 * H])
         self.query_linear = SO3_Linear2Scalar_e2former(C, num_attn_heads * attn_scalar_head, lmax=lmax)
         self.key_linear = SO3_Linear2Scalar_e2former(C, num_attn_heads * attn_scalar_head, lmax=lmax)
         self.proj_value = SO3_Linear_e2former(C, C, lmax=lmax)
@@ -355,9 +381,23 @@ class E2AttentionArbOrder_sparse(nn.Module):
         query = self.query_linear(x).reshape(f_N1, H, -1)
         key = self.key_linear(x)[bd["f_outcell_index"]]
         x_edge = torch.cat([attn_weight, tgt[qi], src[nj]], dim=-1)
-        eg = self.fc_easy(x_edge)
-        gate = eg[:, :H]
-        inputhead = eg[:, H:].reshape(E, H)
+        if self.tp_type == "QKdot_alpha":                   # e2former.py:270-283
+            xd = self.dot_linear(x)
+            x0 = [torch.sum(e3nn_sh(l, edge_vec).unsqueeze(-1) * xd[qi, l * l:(l + 1) ** 2], dim=-2)
+                  for l in range(self.lmax + 1)]
+            gate = self.fc_m0(torch.cat(x0, dim=-1) * self.rad_func_m0(x_edge))
+            inputhead = self.fc_easy(x_edge).reshape(E, H)
+        elif self.tp_type == "QKdotS_alpha":                # e2former.py:284-300
+            lxs = e3nn_raw_sh_l2(edge_vec[..., 0], edge_vec[..., 1], edge_vec[..., 2])
+            xd = self.dot_linear(x)
+            x0 = torch.einsum("elc,el,ls->esc", xd[qi], lxs, self.sum_vec).reshape(E, -1)[:, :H]
+            eg = self.fc_easy(x_edge)
+            gate = self.direction_linear(x0 * eg[:, H:])
+            inputhead = eg[:, :H].reshape(E, H)
+        else:
+            eg = self.fc_easy(x_edge)
+            gate = eg[:, :H]
+            inputhead = eg[:, H:].reshape(E, H)
         key = key.reshape(-1, H, key.shape[-1] // H)
         q_scaled = query / math.sqrt(query.shape[-1])
         chunked = E > CHUNKED_EDGES
@@ -390,12 +430,12 @@ class TransBlock(nn.Module):
     """``e2former.py:440-620``."""
 
     def __init__(self, C=256, lmax=2, num_attn_heads=128, attn_scalar_head=8, number_of_basis=256,
-                 attn_type="so2-first-order"):
+                 attn_type="so2-first-order", tp_type="QK_alpha"):
         super().__init__()
         self.lmax = lmax
         self.norm_1 = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
         self.ga = E2AttentionArbOrder_sparse(C, number_of_basis, num_attn_heads, attn_scalar_head, lmax,
-                                             attn_type=attn_type)
+                                             attn_type=attn_type, tp_type=tp_type)
         self.norm_ffn = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
         self.ffn = FeedForwardNetwork_s3(C, C, C, lmax)
 
@@ -499,7 +539,7 @@ class E2former(nn.Module):
     def __init__(self, C=256, lmax=2, num_layers=4, max_radius=6.0, number_of_basis=256,
                  num_attn_heads=128, attn_scalar_head=8, avg_degree=23.01, atom_type_cnt=256,
                  attn_type="so2-first-order", with_cluster=False, long_range_layers=2, long_cutoff_lower=0.1,
-                 long_cutoff_upper=12):
+                 long_cutoff_upper=12, tp_type="QK_alpha"):
         super().__init__()
         types = attn_type.split("+") if "+" in attn_type else [attn_type, attn_type]
         self.lmax, self.max_radius, self.num_layers = lmax, max_radius, num_layers
@@ -511,7 +551,7 @@ class E2former(nn.Module):
                                          for j in _cg.j_from_cg(11)])
         self.edge_deg_embed_dense = EdgeDegreeEmbeddingNetwork_higherorder(C, lmax, avg_degree, number_of_basis)
         self.blocks = nn.ModuleList([TransBlock(C, lmax, num_attn_heads, attn_scalar_head, number_of_basis,
-                                                types[0] if i < num_layers // 2 else types[1])
+                                                types[0] if i < num_layers // 2 else types[1], tp_type)
                                      for i in range(num_layers)])
         ga0 = self.blocks[0].ga
         self.l3_sequential = (ga0.first_order_tp.so2_tp.l3_sequential if hasattr(ga0, "first_order_tp")
@@ -525,7 +565,7 @@ class E2former(nn.Module):
             self.final_linear = SO3_Linear_e2former(2 * C, C, lmax=lmax, bias=True)
             self.rbf_long = GaussianSmearing(number_of_basis, cutoff=long_cutoff_upper, basis_width_scalar=2)
             self.long_blocks = nn.ModuleList([TransBlock(C, lmax, num_attn_heads, attn_scalar_head, number_of_basis,
-                                                         "zero-order") for _ in range(long_range_layers)])
+                                                         "zero-order", tp_type) for _ in range(long_range_layers)])
             self.norm_final = EquivariantRMSNormArraySphericalHarmonicsV2_BL(lmax, C)
 
     def forward(self, bd, token_embedding, sys_embedding, cluster_neighbor_info=None):

@@ -305,6 +305,111 @@ def test_zero_order_attention(pkg, cuda, env, act):
         assert e < (1e-2 if bf else 1e-4), (name, e)
 
 
+def test_attention_external_gate(pkg, cuda):
+    """The attention kernels with the caller's gate per (edge, head) (the QKdot
+    variants): forward and gradients against the float64 reference fed the same
+    gate and the table's inputhead; the gate's gradient comes back as dL/dgate
+    [E, H] and the distance gradient carries only the inputhead, envelope and 1/d
+    terms.  fp32: forward 2e-5, gradients 1e-4."""
+    from ubio_molfm_amd import modules, ops, so3
+    s, pos, nl = _graph(pkg, cuda, seed=5)
+    N, E = nl.n_atoms, nl.n_edges
+    print(f"[attn ext gate] N={N} E={E}", flush=True)
+    q, k, v = _attn_inputs(nl, cuda, seed=16)
+    gate = torch.randn(E, 128, generator=torch.Generator().manual_seed(17), dtype=torch.float64)
+    G = torch.randn(N, 20, 256, generator=torch.Generator().manual_seed(18))
+    rb = modules.GaussianSmearing(256, 6.0, 2.0)
+    prof = _profile(19, 512)
+    tgt, src = _embeddings(20, 256, 128)
+    net64 = copy.deepcopy(prof).double().net
+    tw, sw = tgt.weight.detach().double().clone(), src.weight.detach().double().clone()
+    type_z, slot = _types(pkg, cuda, s["Z"])
+    tab = ops.RadialTable([prof.to(cuda).net], tgt.to(cuda), src.to(cuda), rb.offset.to(cuda), rb.coeff, 6.0, type_z,
+                          layout="attn")
+    P = modules.slice_perm(cuda)
+    Pinv = torch.argsort(P)
+    dvec = nl.dvec.clone().requires_grad_(True)
+    dist = nl.dist.clone().requires_grad_(True)
+    qd = q.to(cuda).requires_grad_(True); kd = k.to(cuda).requires_grad_(True)
+    vd = v.permute(1, 0, 2).to(cuda)[:, :, P].contiguous().requires_grad_(True)
+    gd = gate.float().to(cuda).requires_grad_(True)
+    out = ops.AttentionFn.apply(qd, kd, vd, dvec, dist, nl, slot, tab, 6.0, math.sqrt(8.0), torch.float32, False,
+                                (0, 0.0), gd)
+    out.backward(ops.so2_grouped(G.permute(1, 0, 2).to(cuda)[:, :, P].contiguous()))
+    T = torch.as_tensor(so3.cartesian_tp_table())
+    row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()
+    Z = torch.as_tensor(np.asarray(s["Z"]))
+    leaves = [t.double().requires_grad_(True) for t in (q, k, v, nl.dvec.cpu(), nl.dist.cpu())] + \
+        [gate.clone().requires_grad_(True)]
+    gi = mlp_ref(leaves[4], Z[row], Z[col], net64, tw, sw, rb.offset.double(), float(np.float32(rb.coeff)))
+    gi = torch.cat([leaves[5], gi[:, 128:]], dim=1)
+    ref = attn_ref(*leaves[:5], row, col, gi, T, 6.0, N)
+    e_f = relerr(ops.so2_rows(out.detach(), N)[:, :, Pinv].permute(1, 0, 2), ref)
+    grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
+    errs = dict(q=relerr(qd.grad, grads[0]), k=relerr(kd.grad, grads[1]),
+                v=relerr(vd.grad[:, :, Pinv].permute(1, 0, 2), grads[2]), dvec=relerr(dvec.grad, grads[3]),
+                dist=relerr(dist.grad, grads[4]), gate=relerr(gd.grad, grads[5]))
+    print(f"[attn ext gate] fwd rel {e_f:.2e} bwd {errs}", flush=True)
+    assert e_f < 2e-5
+    for name, e in errs.items():
+        assert e < 1e-4, (name, e)
+
+
+def test_radial_eval_per_edge(pkg, cuda):
+    """e2v2_radial_eval / _bwd: three profiles in the plain layout (768 channels)
+    at every edge against the float64 profiles, value within 2e-6 of the scale,
+    and dL/dd for a random weighting against float64 autograd (1e-5)."""
+    from ubio_molfm_amd import modules, ops
+    s, pos, nl = _graph(pkg, cuda, seed=6)
+    E = nl.n_edges
+    rb = modules.GaussianSmearing(256, 6.0, 2.0)
+    profs = [_profile(30 + m, 512) for m in range(3)]
+    tgt, src = _embeddings(33, 256, 128)
+    tw, sw = tgt.weight.detach().double().clone(), src.weight.detach().double().clone()
+    type_z, slot = _types(pkg, cuda, s["Z"])
+    tab = ops.RadialTable([copy.deepcopy(p).to(cuda).net for p in profs], tgt.to(cuda), src.to(cuda),
+                          rb.offset.to(cuda), rb.coeff, 6.0, type_z, layout="plain")
+    dist = nl.dist.clone().requires_grad_(True)
+    out = ops.RadialEvalFn.apply(dist, nl, slot, tab)
+    g = torch.randn(E, 768, generator=torch.Generator().manual_seed(34))
+    out.backward(g.to(cuda))
+    row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()
+    Z = torch.as_tensor(np.asarray(s["Z"]))
+    d64 = nl.dist.cpu().double().requires_grad_(True)
+    ref = torch.cat([mlp_ref(d64, Z[row], Z[col], copy.deepcopy(p).double().net, tw, sw, rb.offset.double(),
+                             float(np.float32(rb.coeff))) for p in profs], dim=1)
+    (dref,) = torch.autograd.grad((ref * g.double()).sum(), [d64])
+    ev = float((out.detach().cpu().double() - ref).abs().max() / ref.abs().max())
+    ed = relerr(dist.grad, dref)
+    print(f"[radial eval] E={E} value {ev:.2e} ddist relL2 {ed:.2e}", flush=True)
+    assert ev < 2e-6 and ed < 1e-5
+
+
+@pytest.mark.parametrize("C", [256, 43])
+def test_sh_contract(pkg, cuda, C):
+    """e2v2_sh_contract / _bwd: x0[e, l] = sum_{m in l} Y[e, m] xn[m, row(e)] and
+    its gradients (dY per edge, dxn summed over each row's edges) against
+    float64; C = 256 (QKdot_alpha) and 43 (QKdotS_alpha's H // 3 + 1)."""
+    from ubio_molfm_amd import ops
+    s, pos, nl = _graph(pkg, cuda, seed=7)
+    N, E = nl.n_atoms, nl.n_edges
+    gen = torch.Generator().manual_seed(40 + C)
+    Y = torch.randn(E, 9, generator=gen); xn = torch.randn(9, N, C, generator=gen)
+    g = torch.randn(E, 3, C, generator=gen)
+    Yd = Y.to(cuda).requires_grad_(True); xd = xn.to(cuda).requires_grad_(True)
+    x0 = ops.ShContractFn.apply(Yd, xd, nl)
+    x0.backward(g.to(cuda))
+    row = nl.edge_row.long().cpu()
+    Y64, x64 = Y.double().requires_grad_(True), xn.double().requires_grad_(True)
+    blocks = [(0, 1), (1, 4), (4, 9)]
+    ref = torch.stack([torch.einsum("em,mec->ec", Y64[:, a:b], x64[a:b][:, row]) for a, b in blocks], dim=1)
+    gY, gx = torch.autograd.grad((ref * g.double()).sum(), [Y64, x64])
+    errs = dict(x0=relerr(x0, ref), dY=relerr(Yd.grad, gY), dxn=relerr(xd.grad, gx))
+    print(f"[sh contract C={C}] E={E} {errs}", flush=True)
+    for name, e in errs.items():
+        assert e < 1e-6, (name, e)
+
+
 def test_degree_forward_backward(pkg, cuda):
     """Degree embedding fwd + bwd through the C ABI against the float64 restated
     fallback, with the three gbf_projs profiles evaluated in float64 per edge

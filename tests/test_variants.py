@@ -55,3 +55,31 @@ def test_cluster_polynomial_envelope(pkg):
     dec = model.MolfmAtomic(_cfg(with_cluster="node")).decoder.decoder
     assert dec.cluster and dec.long_envelope() == (0, 0.0)
     assert (dec.long_cutoff_lower, dec.long_cutoff_upper) == (0.1, 12)
+
+
+@pytest.mark.parametrize("tp", ["QKdot_alpha", "QKdotS_alpha"])
+def test_qkdot_variants_state_dict_names(pkg, tp):
+    """QKdot_alpha (dot_linear to attn_weight_input_dim, rad_func_m0 with 768
+    outputs, fc_m0, an fc_easy of 128) and QKdotS_alpha (sum_vec, dot_linear to
+    H // 3 + 1, direction_linear, fc_easy of 256) with the reference's names
+    and shapes (e2former.py:143-167): state dicts load both ways, strict."""
+    from ubio_molfm_amd import model
+    from oracle.model import MolfmAtomic as OracleModel
+    m = model.MolfmAtomic(_cfg(tp_type=tp))
+    ga = m.decoder.decoder.blocks[0].ga
+    if tp == "QKdot_alpha":
+        assert ga.dot_linear.weight.shape == (3, 256, 256) and ga.fc_m0.weight.shape == (128, 768)
+        assert ga.rad_func_m0.net[6].weight.shape == (768, 128) and ga.fc_easy.net[6].weight.shape == (128, 128)
+    else:
+        assert ga.dot_linear.weight.shape == (3, 43, 256) and ga.sum_vec.shape == (9, 3)
+        assert not ga.sum_vec.requires_grad and ga.fc_easy.net[6].weight.shape == (256, 128)
+    om = OracleModel(tp_type=tp)
+    om.load_state_dict(m.state_dict(), strict=True)
+    m.load_state_dict(om.state_dict(), strict=True)
+
+
+@pytest.mark.parametrize("tp", ["QK_alpha+softplus", "QK_alpha+sigmoid", "QKdot_alpha+softplus"])
+def test_non_softmax_weights_rejected(pkg, tp):
+    from ubio_molfm_amd import model
+    with pytest.raises(NotImplementedError):
+        model.MolfmAtomic(_cfg(tp_type=tp))

@@ -24,6 +24,7 @@ EXPORTS = [
     "e2v2_qk_proj_fwd_bf16", "e2v2_qk_proj_bwd_bf16",
     "e2v2_segment_metadata", "e2v2_pair_count", "e2v2_pair_emit", "e2v2_seg_dot", "e2v2_seg_reduce",
     "e2v2_gather_rows", "e2v2_outer_reduce", "e2v2_outer_bwd",
+    "e2v2_radial_eval", "e2v2_radial_eval_bwd", "e2v2_sh_contract", "e2v2_sh_contract_bwd",
 ]
 
 
@@ -66,7 +67,7 @@ class AttnArgs(C.Structure):
                 ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("rtab", vp), ("atom_type", vp),
                 ("n_types", i32), ("rtab_n", i32), ("rtab_h", f32), ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32),
                 ("col_span", i32), ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp),
-                ("zero_order", i32), ("env_kind", i32), ("env_lo", f32)]
+                ("zero_order", i32), ("env_kind", i32), ("env_lo", f32), ("ext_gate", vp), ("ext_dgate", vp)]
 
 
 class DegArgs(C.Structure):

@@ -28,6 +28,8 @@
 // D_h = sum_{c in h} sum_t G[t,c] out[t,c]) and the group's column pass over the
 // key CSR (dv_j, dk_j) with no atomics; then the slice partials are added per
 // edge in slice order.
+#include <type_traits>
+
 #include "common.h"
 #include "radial.h"
 #include "tp_table.h"
@@ -50,6 +52,8 @@ __device__ __forceinline__ int pos_head(int p) { return ((p >> 5) << 4) | (p & 1
 // 2 g + 1).  Lane l of a wave owns position 64 g + l, and dims 4 (l % 2) .. +3
 // of head 32 g + l / 2 for dk.
 constexpr int kGroups = 4, kGroupHeads = kH / kGroups, kGroupC = kC / kGroups;
+// kernel variants (template bits): zero-order aggregation, bell envelope, the caller's gate
+constexpr int kModeZero = 1, kModeBell = 2, kModeExt = 4;
 __device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
   Envelope E;
   E.rc = A.rc; E.a = A.env_a; E.b = A.env_b; E.c = A.env_c;
@@ -129,6 +133,7 @@ struct HeadEdge {
   TS k[kD];
   TS v0[kNV], v1[kNV];
   float tg[8], ti[8];   // table rows 0..3 at the lower and upper node: gate, inputhead
+  float gx;             // the caller's gate (external-gate mode)
 };
 __device__ __forceinline__ void load8_raw(const float* p, float (&v)[8]) { load8(p, v); }
 __device__ __forceinline__ void load8_raw(const __bf16* p, __bf16 (&v)[8]) {
@@ -164,11 +169,12 @@ __device__ __forceinline__ float buf_act(__bf16*, __amdgpu_buffer_rsrc_t r, uint
 // are issued before the current edge is applied.  The two parities are added
 // once per row in LDS, the coupling table is applied and the slice's 20
 // output rows are written.
-// kMode: 0 first order (polynomial envelope), 1 zero order (polynomial), 2 zero order (bell)
+// kMode: bit kModeZero the zero-order aggregation (else first order), bit kModeBell the bell envelope (else
+// the polynomial), bit kModeExt the caller's gate per (edge, head) (else the table's gate rows)
 template <typename TS, int kMode>
 __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __restrict__ out, float* __restrict__ mrow,
                                                     float* __restrict__ srow, int32_t* __restrict__ cnt) {
-  constexpr bool kZ = kMode != 0, kBell = kMode == 2;
+  constexpr bool kZ = kMode & kModeZero, kBell = kMode & kModeBell, kExt = kMode & kModeExt;
   constexpr int CH = 32;               // edges per chunk
   __shared__ uint32_t ckof[CH];        // byte offsets of the edge's k row (head 16 s) and v rows (position 32 s)
   __shared__ uint32_t cvof[CH];
@@ -207,6 +213,7 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
   struct LogitIn {
     TS k[kD];
     float t[12];   // gate rows 0..2 at the two nodes, then inputhead
+    float g;       // the caller's gate (external-gate mode)
   };
   for (int c0 = 0; c0 < n; c0 += CH) {
     const int nc = min(CH, n - c0);
@@ -237,11 +244,14 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
       constexpr int rs = kSlC, nb = 4 * kSlC;
 #pragma unroll
       for (int q = 0; q < 3; ++q) {
-        X.t[q] = tg[q * rs];
-        X.t[3 + q] = tg[nb + q * rs];
+        if constexpr (!kExt) {
+          X.t[q] = tg[q * rs];
+          X.t[3 + q] = tg[nb + q * rs];
+        }
         X.t[6 + q] = tg[kSlH + q * rs];
         X.t[9 + q] = tg[kSlH + nb + q * rs];
       }
+      if constexpr (kExt) X.g = A.ext_gate[((int64_t)b + c0 + el) * kH + h];
     };
     auto lapply = [&](int k, const LogitIn& X) {
       const int el = sub + 4 * k;
@@ -253,7 +263,7 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
       Hermite5 Hw;
       Hw.a0 = chw[0][el]; Hw.a1 = chw[1][el]; Hw.a2 = chw[2][el];
       Hw.b0 = chw[3][el]; Hw.b1 = chw[4][el]; Hw.b2 = chw[5][el];
-      const float gate = herm_value(Hw, X.t[0], X.t[1], X.t[2], X.t[3], X.t[4], X.t[5]);
+      const float gate = kExt ? X.g : herm_value(Hw, X.t[0], X.t[1], X.t[2], X.t[3], X.t[4], X.t[5]);
       a_s[el][hh] = gate * qk;
       coef_s[el][hh] = herm_value(Hw, X.t[6], X.t[7], X.t[8], X.t[9], X.t[10], X.t[11]);
     };
@@ -411,7 +421,7 @@ template <int R, typename TS, bool kSlots, int kMode>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_bwd_col_grp(
     e2v2_attn_args A, const TS* __restrict__ G, const float* __restrict__ w_g, const float* __restrict__ dqk_g,
     float* __restrict__ dv_out, float* __restrict__ dk_out, int grp) {
-  constexpr bool kZ = kMode != 0;
+  constexpr bool kZ = kMode & kModeZero;
   static_assert(kSlots || R == 1, "columns without slots are clusters of one");
   constexpr int S = 32;                        // slots per staged chunk
   __shared__ int ci[S];
@@ -601,7 +611,7 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
                                                         const int32_t* __restrict__ cnt, float* __restrict__ part,
                                                         float* __restrict__ dq, float* __restrict__ w_out,
                                                         float* __restrict__ dqk_out, int grp) {
-  constexpr bool kZ = kMode != 0, kBell = kMode == 2;
+  constexpr bool kZ = kMode & kModeZero, kBell = kMode & kModeBell, kExt = kMode & kModeExt;
   constexpr int CH = 64;
   __shared__ float4 er_a[CH];      // p, dp/dd, 1/max(d, 1e-6), d
   __shared__ float4 er_b[CH];      // dvec, column (int bits)
@@ -690,11 +700,14 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
     const float* tb = R.tab + er_toff[sl] + hh;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      X.tg[q] = tb[q * kSlC];
-      X.tg[4 + q] = tb[(4 + q) * kSlC];
+      if constexpr (!kExt) {
+        X.tg[q] = tb[q * kSlC];
+        X.tg[4 + q] = tb[(4 + q) * kSlC];
+      }
       X.ti[q] = tb[q * kSlC + kSlH];
       X.ti[4 + q] = tb[(4 + q) * kSlC + kSlH];
     }
+    if constexpr (kExt) X.gx = A.ext_gate[((int64_t)b + c0 + sl) * kH + h];
   };
   auto apply = [&](int sl, const L& X) {
     const int64_t e = (int64_t)b + c0 + sl;
@@ -704,9 +717,10 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
     Hermite5 Hw;
     Hw.a0 = er_hw[0][sl]; Hw.a1 = er_hw[1][sl]; Hw.a2 = er_hw[2][sl];
     Hw.b0 = er_hw[3][sl]; Hw.b1 = er_hw[4][sl]; Hw.b2 = er_hw[5][sl];
-    const float gate = herm_value(Hw, X.tg[0], X.tg[1], X.tg[2], X.tg[4], X.tg[5], X.tg[6]);
+    const float gate = kExt ? X.gx : herm_value(Hw, X.tg[0], X.tg[1], X.tg[2], X.tg[4], X.tg[5], X.tg[6]);
     const float ih = herm_value(Hw, X.ti[0], X.ti[1], X.ti[2], X.ti[4], X.ti[5], X.ti[6]);
-    const float gate_d = herm_value(Hw, X.tg[1], X.tg[2], X.tg[3], X.tg[5], X.tg[6], X.tg[7]) * R.inv_h;
+    const float gate_d =
+        kExt ? 0.f : herm_value(Hw, X.tg[1], X.tg[2], X.tg[3], X.tg[5], X.tg[6], X.tg[7]) * R.inv_h;
     const float ih_d = herm_value(Hw, X.ti[1], X.ti[2], X.ti[3], X.ti[5], X.ti[6], X.ti[7]) * R.inv_h;
     float kf[kD];
 #pragma unroll
@@ -741,10 +755,12 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
     const float dqk = da * gate;
     ntstore(w, w_out + e * kGroupHeads + hg);
     ntstore(dqk, dqk_out + e * kGroupHeads + hg);
+    if constexpr (kExt) ntstore(da * qk, A.ext_dgate + e * kH + h);   // dL/dgate
 #pragma unroll
     for (int q = 0; q < kD; ++q) dqa[q] = fmaf(dqk, kf[q], dqa[q]);
     // dL/dd of this head: envelope, 1/d, and the profile (dL/dgate gate' + dL/dih ih')
-    const float ddh = fmaf(da * qk, gate_d, fmaf(dih, ih_d, fmaf(dpv, dpe, dR)));
+    // (external gate: its distance dependence is the caller's)
+    const float ddh = kExt ? fmaf(dih, ih_d, fmaf(dpv, dpe, dR)) : fmaf(da * qk, gate_d, fmaf(dih, ih_d, fmaf(dpv, dpe, dR)));
     // sums over the slice's 16 heads (this row of 16 lanes); quad q holds value q
     const float sum = row_sum4(kZ ? 0.f : w * U[0], w * U[1], w * U[2], ddh, lane);
     if ((lane & 3) == 0) part[((size_t)s * A.n_edges + e) * 4 + (hh >> 2)] = sum;
@@ -805,9 +821,24 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
 
 using namespace e2v2;
 
-// kernel instantiation: 0 first order with the polynomial envelope, 1 zero order with the polynomial,
-// 2 zero order with the bell (checked by check_table)
-static int kernel_mode(const e2v2_attn_args& A) { return A.zero_order ? 1 + A.env_kind : 0; }
+// kernel variant of the arguments (combinations checked by check_table): the bell only with zero order
+static int kernel_mode(const e2v2_attn_args& A) {
+  return (A.zero_order ? kModeZero : 0) | (A.env_kind ? kModeBell : 0) | (A.ext_gate ? kModeExt : 0);
+}
+
+// Calls f(integral_constant<int, mode>) for the instantiated variants 0, 1, 3, 4, 5, 7.
+template <typename F>
+static int with_mode(int mode, F&& f) {
+  switch (mode) {
+    case 0: return f(std::integral_constant<int, 0>{});
+    case kModeZero: return f(std::integral_constant<int, kModeZero>{});
+    case kModeZero | kModeBell: return f(std::integral_constant<int, kModeZero | kModeBell>{});
+    case kModeExt: return f(std::integral_constant<int, kModeExt>{});
+    case kModeExt | kModeZero: return f(std::integral_constant<int, kModeExt | kModeZero>{});
+    case kModeExt | kModeZero | kModeBell: return f(std::integral_constant<int, kModeExt | kModeZero | kModeBell>{});
+    default: return ::e2v2::set_error(-1, "attention variant %d is not built", mode);
+  }
+}
 
 static int check_table(const e2v2_attn_args& A, const char* who) {
   E2V2_REQUIRE((A.zero_order == 0 || A.zero_order == 1) && (A.env_kind == 0 || A.env_kind == 1) &&
@@ -838,20 +869,17 @@ E2V2_API int e2v2_attn_fwd(const e2v2_attn_args* args, void* out, float* mrow, f
   if (A.n_rows == 0) return 0;
   if (int rc = check_table(A, "attn_fwd")) return rc;
   const dim3 grid((unsigned)A.n_rows * kSl);
-  const int mode = kernel_mode(A);
-  if (A.act_bf16) {
-    auto* o = static_cast<__bf16*>(out);
-    if (mode == 2) hipLaunchKernelGGL((k_attn_fwd_sl<__bf16, 2>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
-    else if (mode == 1) hipLaunchKernelGGL((k_attn_fwd_sl<__bf16, 1>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
-    else hipLaunchKernelGGL((k_attn_fwd_sl<__bf16, 0>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
-  } else {
-    auto* o = static_cast<float*>(out);
-    if (mode == 2) hipLaunchKernelGGL((k_attn_fwd_sl<float, 2>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
-    else if (mode == 1) hipLaunchKernelGGL((k_attn_fwd_sl<float, 1>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
-    else hipLaunchKernelGGL((k_attn_fwd_sl<float, 0>), grid, dim3(kWave), 0, s, A, o, mrow, srow, cnt);
-  }
-  E2V2_LAUNCHED("k_attn_fwd_sl");
-  return 0;
+  return with_mode(kernel_mode(A), [&](auto md) -> int {
+    constexpr int kM = decltype(md)::value;
+    if (A.act_bf16)
+      hipLaunchKernelGGL((k_attn_fwd_sl<__bf16, kM>), grid, dim3(kWave), 0, s, A, static_cast<__bf16*>(out), mrow,
+                         srow, cnt);
+    else
+      hipLaunchKernelGGL((k_attn_fwd_sl<float, kM>), grid, dim3(kWave), 0, s, A, static_cast<float*>(out), mrow,
+                         srow, cnt);
+    E2V2_LAUNCHED("k_attn_fwd_sl");
+    return 0;
+  });
 }
 
 // workspace of e2v2_attn_bwd: w [E][32] and dL/dqk [E][32] of one head group, handed from that group's row
@@ -878,10 +906,10 @@ static int attn_bwd_launch(const e2v2_attn_args& A, const TS* G, const TS* O, co
     E2V2_LAUNCHED("k_attn_bwd_row_sl");
     if (A.col_slot_member) {
       const int n_cl = (A.n_rows + 3) / 4;
-      hipLaunchKernelGGL((k_attn_bwd_col_grp<4, TS, true, kMode>), dim3(xcd_grid(n_cl)), dim3(256), 0, s, A, G, w_g, dqk_g,
+      hipLaunchKernelGGL((k_attn_bwd_col_grp<4, TS, true, kMode & kModeZero>), dim3(xcd_grid(n_cl)), dim3(256), 0, s, A, G, w_g, dqk_g,
                          dv, dk, g);
     } else {
-      hipLaunchKernelGGL((k_attn_bwd_col_grp<1, TS, false, kMode>), dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_g,
+      hipLaunchKernelGGL((k_attn_bwd_col_grp<1, TS, false, kMode & kModeZero>), dim3(xcd_grid(A.n_rows)), dim3(256), 0, s, A, G, w_g,
                          dqk_g, dv, dk, g);
     }
     E2V2_LAUNCHED("k_attn_bwd_col_grp");
@@ -908,13 +936,10 @@ E2V2_API int e2v2_attn_bwd(const e2v2_attn_args* args, const void* grad_out, con
   const auto* Ob = static_cast<const __bf16*>(out);
   const auto* Gf = static_cast<const float*>(grad_out);
   const auto* Of = static_cast<const float*>(out);
-  const int mode = kernel_mode(A);
-  if (A.act_bf16) {
-    if (mode == 2) return attn_bwd_launch<__bf16, 2>(A, Gb, Ob, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
-    if (mode == 1) return attn_bwd_launch<__bf16, 1>(A, Gb, Ob, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
-    return attn_bwd_launch<__bf16, 0>(A, Gb, Ob, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
-  }
-  if (mode == 2) return attn_bwd_launch<float, 2>(A, Gf, Of, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
-  if (mode == 1) return attn_bwd_launch<float, 1>(A, Gf, Of, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
-  return attn_bwd_launch<float, 0>(A, Gf, Of, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
+  E2V2_REQUIRE(!A.ext_gate || A.ext_dgate, "attn_bwd: the external gate needs ext_dgate for its gradient");
+  return with_mode(kernel_mode(A), [&](auto md) -> int {
+    constexpr int kM = decltype(md)::value;
+    if (A.act_bf16) return attn_bwd_launch<__bf16, kM>(A, Gb, Ob, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
+    return attn_bwd_launch<float, kM>(A, Gf, Of, mrow, srow, cnt, ddvec, ddist, dq, dk, dv, ws, s);
+  });
 }

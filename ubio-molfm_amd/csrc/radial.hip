@@ -276,6 +276,55 @@ __global__ __launch_bounds__(kRH) void k_radial_check(e2v2_radial_net W, const f
   }
 }
 
+// Per-edge evaluation of a plain-layout table ([pairs][nodes][4][nc]): one
+// wavefront per edge, lanes over channels.  The forward interpolates rows 0..2
+// (values), the backward rows 1..3 (h-scaled derivatives) and sums
+// grad[e][c] f_c'(d) over the channels in a fixed order (lane partials, then a
+// butterfly), so the result does not depend on the launch.
+constexpr int kEvWaves = 4;
+
+__global__ __launch_bounds__(64 * kEvWaves) void k_radial_eval(RadialTab R, const int32_t* __restrict__ atom_type,
+                                                               const int32_t* __restrict__ edge_row,
+                                                               const int32_t* __restrict__ col,
+                                                               const float* __restrict__ dist, int64_t n_edges,
+                                                               float* __restrict__ out) {
+  const int64_t e = (int64_t)blockIdx.x * kEvWaves + (threadIdx.x >> 6);
+  if (e >= n_edges) return;
+  const int lane = threadIdx.x & 63;
+  const int pair = atom_type[edge_row[e]] * R.n_types + atom_type[col[e]];
+  float t;
+  const float* a = R.tab + radial_node(R, pair, dist[e], t);
+  const float* b = a + 4 * R.nc;
+  const Hermite5 H = hermite5(t);
+  const int nc = R.nc;
+  for (int c = lane; c < nc; c += 64)
+    out[e * nc + c] = herm_value(H, a[c], a[nc + c], a[2 * nc + c], b[c], b[nc + c], b[2 * nc + c]);
+}
+
+__global__ __launch_bounds__(64 * kEvWaves) void k_radial_eval_bwd(RadialTab R, const int32_t* __restrict__ atom_type,
+                                                                   const int32_t* __restrict__ edge_row,
+                                                                   const int32_t* __restrict__ col,
+                                                                   const float* __restrict__ dist, int64_t n_edges,
+                                                                   const float* __restrict__ grad,
+                                                                   float* __restrict__ ddist) {
+  const int64_t e = (int64_t)blockIdx.x * kEvWaves + (threadIdx.x >> 6);
+  if (e >= n_edges) return;
+  const int lane = threadIdx.x & 63;
+  const int pair = atom_type[edge_row[e]] * R.n_types + atom_type[col[e]];
+  float t;
+  const float* a = R.tab + radial_node(R, pair, dist[e], t);
+  const float* b = a + 4 * R.nc;
+  const Hermite5 H = hermite5(t);
+  const int nc = R.nc;
+  float acc = 0.f;
+  for (int c = lane; c < nc; c += 64)
+    acc = fmaf(grad[e * nc + c],
+               herm_value(H, a[nc + c], a[2 * nc + c], a[3 * nc + c], b[nc + c], b[2 * nc + c], b[3 * nc + c]), acc);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, kWave);
+  if (lane == 0) ddist[e] = acc * R.inv_h;
+}
+
 }  // namespace e2v2
 
 using namespace e2v2;
@@ -346,5 +395,45 @@ E2V2_API int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rb
   hipLaunchKernelGGL(k_radial_check, dim3((unsigned)(n_nodes - 1), (unsigned)(n_types * n_types)), dim3(kRH), 0, s,
                      *net, rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, *layout, err);
   E2V2_LAUNCHED("k_radial_check");
+  return 0;
+}
+
+static int radial_eval_check(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
+                             const int32_t* atom_type, const int32_t* edge_row, const int32_t* col, const float* dist,
+                             int64_t n_edges, const char* who) {
+  E2V2_REQUIRE(n_edges >= 0 && (n_edges == 0 || (tab && atom_type && edge_row && col && dist)) && n_types >= 1 &&
+                   n_types <= E2V2_MAX_TYPES && n_nodes >= 2 && h > 0.f && nc >= 1 && nc <= 4096,
+               "%s: bad arguments (n_types %d, n_nodes %d, nc %d)", who, n_types, n_nodes, nc);
+  return 0;
+}
+
+E2V2_API int e2v2_radial_eval(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
+                              const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
+                              const float* dist, int64_t n_edges, float* out, hipStream_t s) {
+  if (int rc = radial_eval_check(tab, n_types, n_nodes, h, nc, atom_type, edge_row, col, dist, n_edges,
+                                 "radial_eval"))
+    return rc;
+  if (n_edges == 0) return 0;
+  E2V2_REQUIRE(out, "radial_eval: out is NULL");
+  const RadialTab R{tab, n_types, n_nodes, nc, 1.0f / h};
+  hipLaunchKernelGGL(k_radial_eval, dim3((unsigned)((n_edges + kEvWaves - 1) / kEvWaves)), dim3(64 * kEvWaves), 0, s,
+                     R, atom_type, edge_row, col, dist, n_edges, out);
+  E2V2_LAUNCHED("k_radial_eval");
+  return 0;
+}
+
+E2V2_API int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
+                                  const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
+                                  const float* dist, int64_t n_edges, const float* grad, float* ddist,
+                                  hipStream_t s) {
+  if (int rc = radial_eval_check(tab, n_types, n_nodes, h, nc, atom_type, edge_row, col, dist, n_edges,
+                                 "radial_eval_bwd"))
+    return rc;
+  if (n_edges == 0) return 0;
+  E2V2_REQUIRE(grad && ddist, "radial_eval_bwd: grad or ddist is NULL");
+  const RadialTab R{tab, n_types, n_nodes, nc, 1.0f / h};
+  hipLaunchKernelGGL(k_radial_eval_bwd, dim3((unsigned)((n_edges + kEvWaves - 1) / kEvWaves)), dim3(64 * kEvWaves),
+                     0, s, R, atom_type, edge_row, col, dist, n_edges, grad, ddist);
+  E2V2_LAUNCHED("k_radial_eval_bwd");
   return 0;
 }

@@ -162,6 +162,116 @@ static int check_segments(const e2v2_segments* S, bool need_col, const char* wha
   return 0;
 }
 
+// Per-edge contraction of a query node's irreps with the edge's spherical
+// harmonics, l by l: x0[e][l][c] = sum_{m in l} Y[e][m] xn[m][row(e)][c] (the
+// x_0_extra of the QKdot_alpha / QKdotS_alpha gates, e2former.py:271-277 and
+// 288-296), for lmax = 2 (9 m-rows, 3 l-blocks) and C <= 256 channels.  One
+// wavefront per query row (edges of a row contiguous, CSR row_ptr), lanes over
+// channels (up to four each), the row's node values held in registers.  The
+// backward of the same row forms dxn[m][i][c] = sum_e Y[e][m] g[e][l(m)][c]
+// in registers (no atomics) and dY[e][m] = sum_c g[e][l(m)][c] xn[m][i][c] by a
+// fixed-order butterfly over the lanes.
+constexpr int kShWaves = 4, kShPer = 4;
+
+__device__ __forceinline__ int sh_l(int m) { return m == 0 ? 0 : (m < 4 ? 1 : 2); }
+
+__global__ __launch_bounds__(64 * kShWaves) void k_sh_contract(const float* __restrict__ Y,
+                                                               const float* __restrict__ xn,
+                                                               const int32_t* __restrict__ row_ptr, int32_t n_rows,
+                                                               int32_t C, float* __restrict__ x0) {
+  const int i = blockIdx.x * kShWaves + (threadIdx.x >> 6);
+  if (i >= n_rows) return;
+  const int lane = threadIdx.x & 63;
+  const size_t ms = (size_t)n_rows * C;
+  float xr[kShPer][9];
+#pragma unroll
+  for (int q = 0; q < kShPer; ++q) {
+    const int c = lane + 64 * q;
+#pragma unroll
+    for (int m = 0; m < 9; ++m) xr[q][m] = c < C ? xn[m * ms + (size_t)i * C + c] : 0.f;
+  }
+  const int b = row_ptr[i], n = row_ptr[i + 1] - b;
+  for (int k = 0; k < n; ++k) {
+    const int64_t e = (int64_t)b + k;
+    float y[9];
+#pragma unroll
+    for (int m = 0; m < 9; ++m) y[m] = Y[e * 9 + m];
+#pragma unroll
+    for (int q = 0; q < kShPer; ++q) {
+      const int c = lane + 64 * q;
+      if (c < C) {
+        float* o = x0 + (size_t)e * 3 * C + c;
+        o[0] = y[0] * xr[q][0];
+        o[C] = fmaf(y[3], xr[q][3], fmaf(y[2], xr[q][2], y[1] * xr[q][1]));
+        o[2 * C] = fmaf(y[8], xr[q][8], fmaf(y[7], xr[q][7], fmaf(y[6], xr[q][6], fmaf(y[5], xr[q][5],
+                   y[4] * xr[q][4]))));
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(64 * kShWaves) void k_sh_contract_bwd(const float* __restrict__ Y,
+                                                                   const float* __restrict__ xn,
+                                                                   const int32_t* __restrict__ row_ptr,
+                                                                   int32_t n_rows, int32_t C,
+                                                                   const float* __restrict__ g,
+                                                                   float* __restrict__ dY, float* __restrict__ dxn) {
+  const int i = blockIdx.x * kShWaves + (threadIdx.x >> 6);
+  if (i >= n_rows) return;
+  const int lane = threadIdx.x & 63;
+  const size_t ms = (size_t)n_rows * C;
+  float xr[kShPer][9], dx[kShPer][9];
+#pragma unroll
+  for (int q = 0; q < kShPer; ++q) {
+    const int c = lane + 64 * q;
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      xr[q][m] = c < C ? xn[m * ms + (size_t)i * C + c] : 0.f;
+      dx[q][m] = 0.f;
+    }
+  }
+  const int b = row_ptr[i], n = row_ptr[i + 1] - b;
+  for (int k = 0; k < n; ++k) {
+    const int64_t e = (int64_t)b + k;
+    float y[9], p[9];
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      y[m] = Y[e * 9 + m];
+      p[m] = 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < kShPer; ++q) {
+      const int c = lane + 64 * q;
+      const float* gp = g + (size_t)e * 3 * C + c;
+      const float gl[3] = {c < C ? gp[0] : 0.f, c < C ? gp[C] : 0.f, c < C ? gp[2 * C] : 0.f};
+#pragma unroll
+      for (int m = 0; m < 9; ++m) {
+        dx[q][m] = fmaf(y[m], gl[sh_l(m)], dx[q][m]);
+        p[m] = fmaf(gl[sh_l(m)], xr[q][m], p[m]);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) p[m] += __shfl_xor(p[m], o, kWave);
+    }
+    if (lane < 9) {
+      float v = p[0];
+#pragma unroll
+      for (int m = 1; m < 9; ++m) v = lane == m ? p[m] : v;
+      dY[e * 9 + lane] = v;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kShPer; ++q) {
+    const int c = lane + 64 * q;
+    if (c < C) {
+#pragma unroll
+      for (int m = 0; m < 9; ++m) dxn[m * ms + (size_t)i * C + c] = dx[q][m];
+    }
+  }
+}
+
 }  // namespace e2v2
 
 using namespace e2v2;
@@ -239,5 +349,28 @@ E2V2_API int e2v2_outer_bwd(const float* grad, int n_rows, const float* sh, cons
                        query_index, n_edges, L, H, dfea);
     E2V2_LAUNCHED("k_outer_dfea");
   }
+  return 0;
+}
+
+E2V2_API int e2v2_sh_contract(const float* Y, const float* xn, const int32_t* row_ptr, int32_t n_rows, int32_t C,
+                              float* x0, hipStream_t s) {
+  E2V2_REQUIRE(n_rows >= 0 && C >= 1 && C <= 64 * kShPer && (n_rows == 0 || (Y && xn && row_ptr && x0)),
+               "sh_contract: bad arguments (n_rows %d, C %d; C must be 1..%d)", n_rows, C, 64 * kShPer);
+  if (n_rows == 0) return 0;
+  hipLaunchKernelGGL(k_sh_contract, dim3((unsigned)((n_rows + kShWaves - 1) / kShWaves)), dim3(64 * kShWaves), 0, s,
+                     Y, xn, row_ptr, n_rows, C, x0);
+  E2V2_LAUNCHED("k_sh_contract");
+  return 0;
+}
+
+E2V2_API int e2v2_sh_contract_bwd(const float* Y, const float* xn, const int32_t* row_ptr, int32_t n_rows, int32_t C,
+                                  const float* g, float* dY, float* dxn, hipStream_t s) {
+  E2V2_REQUIRE(n_rows >= 0 && C >= 1 && C <= 64 * kShPer &&
+                   (n_rows == 0 || (Y && xn && row_ptr && g && dY && dxn)),
+               "sh_contract_bwd: bad arguments (n_rows %d, C %d; C must be 1..%d)", n_rows, C, 64 * kShPer);
+  if (n_rows == 0) return 0;
+  hipLaunchKernelGGL(k_sh_contract_bwd, dim3((unsigned)((n_rows + kShWaves - 1) / kShWaves)), dim3(64 * kShWaves), 0,
+                     s, Y, xn, row_ptr, n_rows, C, g, dY, dxn);
+  E2V2_LAUNCHED("k_sh_contract_bwd");
   return 0;
 }

@@ -18,7 +18,7 @@ from torch.profiler import record_function
 
 from . import so3
 from . import _lib
-from .ops import AttentionFn, DegreeEmbedFn, RadialCache
+from .ops import AttentionFn, DegreeEmbedFn, RadialCache, RadialEvalFn, ShContractFn
 
 
 def _e3nn_normalize2mom(f) -> float:
@@ -875,10 +875,49 @@ def reference_edge_context(batched_data, edge_vec, edge_dis, atomic_numbers, rbf
     return ctx
 
 
+def _raw_sh(v: torch.Tensor) -> torch.Tensor:
+    """The raw real spherical-harmonic polynomials l <= 2 of e3nn's
+    ``_spherical_harmonics`` (y the polar axis) of the vector v [E, 3] itself,
+    [E, 9]: 1 | x, y, z | sqrt3 x z, sqrt3 x y, y^2 - (x^2 + z^2) / 2, sqrt3 y z,
+    sqrt3 / 2 (z^2 - x^2)."""
+    x, y, z = v[:, 0], v[:, 1], v[:, 2]
+    s3 = math.sqrt(3.0)
+    return torch.stack([torch.ones_like(x), x, y, z, s3 * x * z, s3 * x * y, y * y - 0.5 * (x * x + z * z),
+                        s3 * y * z, s3 / 2 * (z * z - x * x)], dim=-1)
+
+
+_SH_INTEGRAL = [math.sqrt(2 * l + 1) / math.sqrt(4 * math.pi) for l in (0, 1, 1, 1, 2, 2, 2, 2, 2)]
+
+
+def _sh_integral(v: torch.Tensor) -> torch.Tensor:
+    """e3nn.o3.spherical_harmonics(l, v, normalize=True) for l = 0, 1, 2
+    concatenated, [E, 9]: the raw polynomials of v / |v| times
+    sqrt(2 l + 1) / sqrt(4 pi) (e3nn's default "integral" normalisation)."""
+    u = v / v.norm(dim=-1, keepdim=True)
+    return _raw_sh(u) * torch.tensor(_SH_INTEGRAL, dtype=v.dtype, device=v.device)
+
+
+def _profile_with_rows(net: nn.Sequential, w3: torch.Tensor, b3: torch.Tensor) -> nn.Sequential:
+    """A RadialProfile net with the first five layers of ``net`` and a last Linear
+    of the given rows (w3 [256, 128], b3 [256]): the 256-channel profiles the
+    radial tables are built from, for profiles of another width (rows taken out
+    of them, or zero rows for channels a table must hold but nothing reads)."""
+    lin = nn.Linear(w3.shape[1], w3.shape[0]).to(w3.device)
+    with torch.no_grad():
+        lin.weight.copy_(w3)
+        lin.bias.copy_(b3)
+    return nn.Sequential(net[0], net[1], net[2], net[3], net[4], net[5], lin)
+
+
 class E2AttentionArbOrder_sparse(nn.Module):
-    """e2former.py:80-436 for tp_type=QK_alpha, attn_type so2-first-order or
-    zero-order (proj_zero on the alpha-weighted sum of the neighbours' values,
-    e2former.py:199-204,411-416)."""
+    """e2former.py:80-436 for attn_type so2-first-order or zero-order
+    (proj_zero on the alpha-weighted sum of the neighbours' values,
+    e2former.py:199-204,411-416) and tp_type QK_alpha, QKdot_alpha (gate from
+    the spherical harmonics of the edge against dot_linear of the query node,
+    e2former.py:143-154,270-283) or QKdotS_alpha (e2former.py:155-167,284-300).
+    The QKdot gates are formed per edge (e2v2_sh_contract, e2v2_radial_eval,
+    the gate's small dense layers) and handed to the attention kernels as their
+    gate; the inputhead stays a table inside the kernels."""
 
     def __init__(self, irreps_node_input="256x0e+256x1e+256x2e", attn_weight_input_dim=256, num_attn_heads=128,
                  attn_scalar_head=8, irreps_head="2x0e+2x1e+2x2e", alpha_drop=0.0, tp_type="QK_alpha",
@@ -895,7 +934,26 @@ class E2AttentionArbOrder_sparse(nn.Module):
         ecl = [attn_weight_input_dim + 256, min(128, attn_weight_input_dim // 2),
                min(128, attn_weight_input_dim // 2)]
         self.alpha_dropout = nn.Dropout(alpha_drop)
-        self.fc_easy = RadialProfile(ecl + [2 * num_attn_heads])
+        H = num_attn_heads
+        if self.tp_type == "QKdot_alpha":
+            self.dot_linear = SO3_Linear_e2former(C, attn_weight_input_dim, lmax=lmax)
+            self.rad_func_m0 = RadialProfile(ecl + [attn_weight_input_dim * (lmax + 1)])
+            self.fc_m0 = nn.Linear(attn_weight_input_dim * (lmax + 1), H)
+            self.fc_easy = RadialProfile(ecl + [H])
+        elif self.tp_type == "QKdotS_alpha":
+            sv = torch.zeros((lmax + 1) ** 2, lmax + 1)
+            for l in range(lmax + 1):
+                sv[l * l:(l + 1) ** 2, l] = 1
+            self.sum_vec = nn.Parameter(sv, requires_grad=False)
+            self.dot_linear = SO3_Linear_e2former(C, H // (lmax + 1) + 1, lmax=lmax)
+            self.direction_linear = nn.Sequential(nn.Linear(H, H), nn.LayerNorm(H), nn.SiLU(), nn.Linear(H, H))
+            self.fc_easy = RadialProfile(ecl + [2 * H])
+        elif self.tp_type == "QK_alpha":
+            self.fc_easy = RadialProfile(ecl + [2 * H])
+        else:
+            raise NotImplementedError(f"tp_type {tp_type!r}: the HIP path implements QK_alpha, QKdot_alpha and "
+                                      "QKdotS_alpha")
+        self._radial_m0 = RadialCache()
         self.query_linear = SO3_Linear2Scalar_e2former(C, num_attn_heads * attn_scalar_head, lmax=lmax)
         self.key_linear = SO3_Linear2Scalar_e2former(C, num_attn_heads * attn_scalar_head, lmax=lmax)
         self.proj_value = SO3_Linear_e2former(C, C, lmax=lmax)
@@ -978,6 +1036,71 @@ class E2AttentionArbOrder_sparse(nn.Module):
         out = self.forward_fused(x, ctx)
         return out.transpose(0, 1).contiguous(), attn_weight
 
+    def _attn_profile(self):
+        """The net of the attention kernels' table (256 channels: gate | inputhead):
+        fc_easy itself for QK_alpha; for the QKdot variants, whose gate comes from
+        outside, zero gate rows and the inputhead rows of fc_easy (all of its 128
+        for QKdot_alpha, its first 128 for QKdotS_alpha)."""
+        net = self.fc_easy.net
+        if self.tp_type == "QK_alpha":
+            return net
+
+        def build():
+            w3, b3 = net[6].weight.detach(), net[6].bias.detach()
+            H = self.num_attn_heads
+            w = torch.cat([torch.zeros(H, w3.shape[1], device=w3.device), w3[:H]])
+            b = torch.cat([torch.zeros(H, device=b3.device), b3[:H]])
+            return _profile_with_rows(net, w, b)
+        return cached(self, "attn_profile", list(self.fc_easy.parameters()), build)
+
+    def _m0_profiles(self):
+        """Nets of the per-edge radial profile of the QKdot gate, 256 channels each:
+        rad_func_m0's 768 outputs in three (QKdot_alpha), or the second half of
+        fc_easy then zero rows (QKdotS_alpha)."""
+        if self.tp_type == "QKdot_alpha":
+            net = self.rad_func_m0.net
+
+            def build():
+                w3, b3 = net[6].weight.detach(), net[6].bias.detach()
+                return [_profile_with_rows(net, w3[256 * m:256 * (m + 1)], b3[256 * m:256 * (m + 1)])
+                        for m in range(w3.shape[0] // 256)]
+            return cached(self, "m0_profiles", list(self.rad_func_m0.parameters()), build)
+        net = self.fc_easy.net
+
+        def build_s():
+            w3, b3 = net[6].weight.detach(), net[6].bias.detach()
+            H = self.num_attn_heads
+            w = torch.cat([w3[H:], torch.zeros(256 - H, w3.shape[1], device=w3.device)])
+            b = torch.cat([b3[H:], torch.zeros(256 - H, device=b3.device)])
+            return [_profile_with_rows(net, w, b)]
+        return cached(self, "m0_profiles", list(self.fc_easy.parameters()), build_s)
+
+    def qkdot_gate(self, x: torch.Tensor, ctx: EdgeContext) -> torch.Tensor:
+        """The gate [E, H] of the QKdot variants in the edge order of ctx.nl, from
+        the layer input x [9, N, C] (e2former.py:270-300)."""
+        nl = ctx.nl
+        E, H = nl.n_edges, self.num_attn_heads
+        xd = self.dot_linear(x, ctx.bf16)                                     # [9, N, Cd]
+        tab = self._radial_m0.get(self._m0_profiles(), self.target_embedding, self.source_embedding,
+                                  ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="plain")
+        rad = RadialEvalFn.apply(ctx.dist, nl, ctx.atom_type, tab)
+        if self.tp_type == "QKdot_alpha":
+            x0 = ShContractFn.apply(_sh_integral(ctx.dvec), xd, nl).reshape(E, -1)    # [E, 3 Cd]
+            return _linear(x0 * rad, self.fc_m0)
+        sv = self.sum_vec.detach()
+        if not torch.equal(sv.cpu(), self._sum_vec_blocks()):
+            raise NotImplementedError("QKdotS_alpha: sum_vec must keep its l-block indicator values")
+        x0 = ShContractFn.apply(_raw_sh(ctx.dvec), xd, nl).reshape(E, -1)[:, :H]     # [E, H]
+        dl = self.direction_linear
+        return _linear(_ln_silu(_linear(x0 * rad[:, :H], dl[0]), dl[1]), dl[3])
+
+    def _sum_vec_blocks(self):
+        L = self.lmax + 1
+        sv = torch.zeros(L * L, L)
+        for l in range(L):
+            sv[l * l:(l + 1) ** 2, l] = 1
+        return sv
+
     def zero_out_weights(self, bf16: bool = False):
         """proj_zero as the operand list of SO2OutFn for the zero-order rows
         [9, N, C]: per degree l, (l, 1, C l^2, W, W^T) with W = W_l^T [C, O], input
@@ -1035,13 +1158,14 @@ class E2AttentionArbOrder_sparse(nn.Module):
             q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
             k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         with record_function("rbf function-a"):   # fc_easy as a distance table, built once per weight version
-            table = self._radial.get([self.fc_easy.net], self.target_embedding, self.source_embedding,
+            table = self._radial.get([self._attn_profile()], self.target_embedding, self.source_embedding,
                                      ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="attn")
         zero = self.attn_type == "zero-order"
         with record_function("qk attention"):
+            gate = None if self.tp_type == "QK_alpha" else self.qkdot_gate(x, ctx)
             so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table, ctx.rc,
                                     math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32, zero,
-                                    (ctx.env_kind, ctx.env_lo))
+                                    (ctx.env_kind, ctx.env_lo), gate)
         if zero:
             with record_function("zero-order"):
                 return SO2OutFn.apply(so2.view(-1), res, self.zero_out_weights(bf16), self.proj_zero.bias.detach(),
@@ -1252,15 +1376,18 @@ def check_supported(C, lmax, heads, head_dim, n_basis, irreps_head, norm_layer, 
                     basis_type, with_cluster, edge_embedtype):
     hc, hl = parse_irreps(irreps_head)
     ok = (C == 256 and lmax == 2 and heads == 128 and head_dim == 8 and n_basis == 256 and hc * heads == C
-          and hl == lmax and norm_layer in ("rms_norm_sh", "rms_norm_sh_BL") and tp_type.split("+")[0] == "QK_alpha"
+          and hl == lmax and norm_layer in ("rms_norm_sh", "rms_norm_sh_BL")
+          and tp_type.split("+")[0] in ("QK_alpha", "QKdot_alpha", "QKdotS_alpha")
+          and "softplus" not in tp_type and "sigmoid" not in tp_type
           and all(a in ("so2-first-order", "zero-order") for a in attn_type.split("+"))
           and len(attn_type.split("+")) <= 2 and ("s3" in ffn_type or "default" in ffn_type)
           and basis_type == "gaussiansmear" and "wolayernorm" not in edge_embedtype)
     if not ok:
         raise NotImplementedError(
             "the MI355X path implements the E2Former-V2 production configuration: irreps 256x0e+256x1e+256x2e, "
-            "irreps_head 2x0e+2x1e+2x2e, 128 heads, attn_scalar_head 8, 256 basis, rms_norm_sh, tp_type QK_alpha, "
-            "attn_type so2-first-order / zero-order (or 'a+b' of the two), ffn s3")
+            "irreps_head 2x0e+2x1e+2x2e, 128 heads, attn_scalar_head 8, 256 basis, rms_norm_sh, tp_type QK_alpha / "
+            "QKdot_alpha / QKdotS_alpha (softmax weights), attn_type so2-first-order / zero-order (or 'a+b' of the "
+            "two), ffn s3")
     if "node" not in str(with_cluster) and str(with_cluster) not in ("False", "false", "0", "None", "none"):
         raise ValueError("Only with_cluster='node*' is restored in this release tree. "
                          "Other cluster modes require removed modules.")

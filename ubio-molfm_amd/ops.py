@@ -248,10 +248,12 @@ def deg_args(nl: NeighborList, atom_type: torch.Tensor, table: RadialTable, avg:
 
 
 def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: float, rc: float, bf: int,
-              zero_order: bool = False, env=(0, 0.0)):
+              zero_order: bool = False, env=(0, 0.0), ext_gate=None, ext_dgate=None):
     """e2v2_attn_args over the neighbour list (with its column clusters when built).
     zero_order selects the zero-order aggregation; env = (kind, lower end): kind 0
-    the polynomial envelope on [0, rc], 1 the smooth bell on [lower end, rc]."""
+    the polynomial envelope on [0, rc], 1 the smooth bell on [lower end, rc];
+    ext_gate [E, 128] fp32 (or None) replaces the table's gate rows, ext_dgate
+    [E, 128] receives its gradient in the backward."""
     if table.nc != 256 or table.layout != "attn":
         raise ValueError("the attention needs the table of its fc_easy profile in slice order (layout 'attn')")
     a = _lib.AttnArgs(nl.n_atoms, nl.n_edges, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(),
@@ -261,6 +263,11 @@ def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: f
                       ENV_B, ENV_C, int(bf))
     a.zero_order = int(bool(zero_order))
     a.env_kind, a.env_lo = int(env[0]), float(env[1])
+    if ext_gate is not None:
+        if ext_gate.shape != (nl.n_edges, 128) or ext_gate.dtype != torch.float32 or not ext_gate.is_contiguous():
+            raise ValueError(f"ext_gate must be a contiguous float32 [{nl.n_edges}, 128] tensor")
+        a.ext_gate = ext_gate.data_ptr() if nl.n_edges else None
+        a.ext_dgate = None if ext_dgate is None or nl.n_edges == 0 else ext_dgate.data_ptr()
     if nl.col_slot_member is not None:
         a.col_span = nl.col_span
         a.col_slot_member = nl.col_slot_member.data_ptr()
@@ -285,10 +292,12 @@ class AttentionFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, dvec, dist, nl: NeighborList, atom_type, table: RadialTable, rc: float,
-                q_div: float, act_dtype=torch.float32, zero_order: bool = False, env=(0, 0.0)):
+                q_div: float, act_dtype=torch.float32, zero_order: bool = False, env=(0, 0.0), ext_gate=None):
         """act_dtype: storage of q, k, v and of the output rows (torch.float32, or
         torch.bfloat16 in the bf16 mode: half the gather traffic, fp32 math).
-        env: the distance envelope (kind, lower end), see attn_args."""
+        env: the distance envelope (kind, lower end), see attn_args.  ext_gate
+        [E, 128]: the gate of every (edge, head) (the QKdot variants' gates, in the
+        edge order of nl); the table then only supplies the inputhead."""
         _need_cuda(q, k, v, dvec, dist)
         if act_dtype not in (torch.float32, torch.bfloat16):
             raise ValueError(f"attention activations must be float32 or bfloat16, got {act_dtype}")
@@ -296,7 +305,9 @@ class AttentionFn(torch.autograd.Function):
         N = nl.n_atoms
         q = q.to(act_dtype).contiguous(); k = k.to(act_dtype).contiguous(); v = v.to(act_dtype).contiguous()
         bf = int(act_dtype == torch.bfloat16)
-        args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env)
+        if ext_gate is not None:
+            ext_gate = ext_gate.float().contiguous()
+        args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env, ext_gate)
         if zero_order:
             out = torch.empty(9, N, 256, dtype=act_dtype, device=dev)
         else:
@@ -305,7 +316,7 @@ class AttentionFn(torch.autograd.Function):
         srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
         cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
         _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _p(out), _p(mrow), _p(srow), _p(cnt), _stream(q))
-        ctx.save_for_backward(q, k, v, out, mrow, srow, cnt)
+        ctx.save_for_backward(q, k, v, out, mrow, srow, cnt, ext_gate)
         ctx.nl, ctx.atom_type, ctx.table, ctx.rc, ctx.q_div, ctx.bf = nl, atom_type, table, rc, q_div, bf
         ctx.zero_order, ctx.env = zero_order, env
         return out
@@ -313,12 +324,14 @@ class AttentionFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gout):
         _no_double_backward()
-        q, k, v, out, mrow, srow, cnt = ctx.saved_tensors
+        q, k, v, out, mrow, srow, cnt, ext_gate = ctx.saved_tensors
         nl = ctx.nl
         dev = q.device
         E = nl.n_edges
         gout = gout.to(out.dtype).contiguous()
-        args = attn_args(nl, q, k, v, ctx.atom_type, ctx.table, ctx.q_div, ctx.rc, ctx.bf, ctx.zero_order, ctx.env)
+        dgate = None if ext_gate is None else torch.empty(E, 128, dtype=torch.float32, device=dev)
+        args = attn_args(nl, q, k, v, ctx.atom_type, ctx.table, ctx.q_div, ctx.rc, ctx.bf, ctx.zero_order, ctx.env,
+                         ext_gate, dgate)
         f = dict(dtype=torch.float32, device=dev)
         ddv = torch.empty(max(E, 1), 3, **f)
         dd = torch.empty(max(E, 1), **f)
@@ -330,4 +343,75 @@ class AttentionFn(torch.autograd.Function):
         _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(ddv),
                   _p(dd), _p(dq), _p(dk), _p(dv), _p(ws), _lib.C.c_size_t(ws.numel()), _stream(gout))
         del ws
-        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None, None
+        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None, None, dgate
+
+
+class RadialEvalFn(torch.autograd.Function):
+    """Per-edge values [E, nc] of a "plain"-layout RadialTable (e2v2_radial_eval):
+    the radial profiles of the QKdot gates (rad_func_m0, e2former.py:278; the
+    second half of fc_easy, e2former.py:293-294) at every edge of nl, for the
+    type pair (atom_type[row], atom_type[col]).  Gradient: dist only (the table
+    is a constant of the weights)."""
+
+    @staticmethod
+    def forward(ctx, dist, nl: NeighborList, atom_type, table: RadialTable):
+        _need_cuda(dist)
+        if table.layout != "plain":
+            raise ValueError("RadialEvalFn needs a table in the 'plain' layout")
+        E = nl.n_edges
+        dist = dist.float().contiguous()
+        out = torch.empty(E, table.nc, dtype=torch.float32, device=dist.device)
+        _lib.call("e2v2_radial_eval", *_radial_eval_args(nl, atom_type, table, dist), _p(out), _stream(dist))
+        ctx.save_for_backward(dist)
+        ctx.nl, ctx.atom_type, ctx.table = nl, atom_type, table
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        _no_double_backward()
+        (dist,) = ctx.saved_tensors
+        g = g.float().contiguous()
+        dd = torch.empty_like(dist)
+        _lib.call("e2v2_radial_eval_bwd", *_radial_eval_args(ctx.nl, ctx.atom_type, ctx.table, dist), _p(g), _p(dd),
+                  _stream(dist))
+        return dd, None, None, None
+
+
+def _radial_eval_args(nl: NeighborList, atom_type, table: RadialTable, dist):
+    return (_p(table.tab), _lib.i32(table.n_types), _lib.i32(table.n_nodes), _lib.f32(table.h),
+            _lib.i32(table.nc), _p(atom_type), _p(nl.edge_row), _p(nl.col), _p(dist), _lib.i64(nl.n_edges))
+
+
+class ShContractFn(torch.autograd.Function):
+    """x0 [E, 3, C] with x0[e, l] = sum_{m in l} Y[e, m] xn[m, row(e)] (e2v2_sh_contract):
+    the per-edge x_0_extra of the QKdot gates (e2former.py:271-276, 288-296).  Y
+    [E, 9] in the edge order of nl (rows contiguous), xn [9, N, C] m-major,
+    C <= 256.  Gradients to Y and xn (per-row sums, deterministic)."""
+
+    @staticmethod
+    def forward(ctx, Y, xn, nl: NeighborList):
+        _need_cuda(Y, xn)
+        Y = Y.float().contiguous()
+        xn = xn.float().contiguous()
+        C = xn.shape[-1]
+        if Y.shape != (nl.n_edges, 9) or xn.shape[:2] != (9, nl.n_atoms):
+            raise ValueError(f"ShContractFn: Y {tuple(Y.shape)}, xn {tuple(xn.shape)} for {nl.n_edges} edges and "
+                             f"{nl.n_atoms} rows")
+        x0 = torch.empty(nl.n_edges, 3, C, dtype=torch.float32, device=Y.device)
+        _lib.call("e2v2_sh_contract", _p(Y), _p(xn), _p(nl.row_ptr), _lib.i32(nl.n_atoms), _lib.i32(C), _p(x0),
+                  _stream(Y))
+        ctx.save_for_backward(Y, xn)
+        ctx.nl = nl
+        return x0
+
+    @staticmethod
+    def backward(ctx, g):
+        _no_double_backward()
+        Y, xn = ctx.saved_tensors
+        nl = ctx.nl
+        g = g.float().contiguous()
+        dY = torch.empty_like(Y)
+        dxn = torch.empty_like(xn)
+        _lib.call("e2v2_sh_contract_bwd", _p(Y), _p(xn), _p(nl.row_ptr), _lib.i32(nl.n_atoms), _lib.i32(xn.shape[-1]),
+                  _p(g), _p(dY), _p(dxn), _stream(Y))
+        return dY, dxn, None
