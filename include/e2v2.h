@@ -439,6 +439,40 @@ int e2v2_ln_silu_fwd(const float* x, const float* g, const float* b, float* y, f
 int e2v2_ln_silu_bwd(const float* x, const float* g, const float* b, const float* stats, const float* gy, float* gx,
                      int n, int w, hipStream_t s);
 
+/* ---- per-node dense layers: fp32 GEMMs on bf16 MFMA by the exact three-piece split ----
+ * Replaces the GEMMs (forward and input gradient) of SO3_Linear_e2former (module_utils.py:2010-2052) and so of
+ * FeedForwardNetwork_s3 (module_utils.py:2755-2797), the value projection and proj_first (e2former.py:215-219,
+ * 300-303, 433), forward_linear (wigner6j/so2_tensor_product.py:276-290), the final_linear of
+ * SO3_Linear2Scalar_e2former (module_utils.py:2230-2233) and the gate logits of Gate_s3 (module_utils.py:2694-2746).
+ * Each fp32 operand x is split as x0 + x1 + x2 (bf16, round to nearest even, exact remainders) and a product is
+ * the sum of the six piece products of order <= 2, accumulated in fp32: an fp32 GEMM to within a few units of
+ * fp32 rounding (measured against float64: below the error of the fp32 MFMA GEMM of the same operands).
+ *   c[b][i][j] = sum_k a[b][i][k] W_{widx[b]}[j][k] (+ bias[j] for b < bias_batches) (+ r[b][i][j])
+ * a: fp32, row stride lda (lda >= k, lda % 4 == 0, 16-byte aligned), batch stride a_bs (elements);
+ * b: n_w weights packed by e2v2_gemm_pack; c (and r, which may equal c): fp32 with row / batch strides.
+ * Requires n % 128 == 0, k % 16 == 0, 1 <= batch <= 16, 0 <= widx[b] < n_w <= 16. */
+typedef struct {
+  const float* a;
+  int64_t lda, a_bs;
+  const void* b;
+  int n_w;
+  float* c;
+  int64_t ldc, c_bs;
+  const float* r;
+  int64_t ldr, r_bs;
+  const float* bias;
+  int bias_batches;
+  int m, n, k, batch;
+  int widx[16];
+} e2v2_gemm_args;
+int e2v2_gemm_s3(const e2v2_gemm_args* args, hipStream_t s);
+/* Pack n_w weights W_w[j][k] = w[w w_stride + j ld_n + k ld_k] (j < n, k < k; so W or W^T of a row-major matrix
+ * without a copy) into e2v2_gemm_packed_bytes(n_w, n, k) bytes at packed (16-byte aligned); the bytes needed,
+ * or -1 for an unsupported shape. */
+int64_t e2v2_gemm_packed_bytes(int n_w, int n, int k);
+int e2v2_gemm_pack(const float* w, int64_t ld_n, int64_t ld_k, int64_t w_stride, int n_w, int n, int k, void* packed,
+                   hipStream_t s);
+
 /* ---- positions --------------------------------------------------------- */
 int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,
                      const float* dvec, const float* dist, const float* ddvec, const float* ddist, float* dpos,

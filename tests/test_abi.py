@@ -10,7 +10,7 @@ ROOT = Path(__file__).resolve().parents[1]
 
 def declared():
     text = (ROOT / "include" / "e2v2.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(e2v2_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(e2v2_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_api():
@@ -71,3 +71,19 @@ def test_header_so2_layout_macros_match_generated_tables(tmp_path):
     import so3
     a, ld, col, _ = so3.so2_row_layout()
     assert got == list(zip(a, ld, col))
+
+
+def test_split_gemm_host_checks(pkg):
+    """e2v2_gemm_s3 / e2v2_gemm_packed_bytes validate shapes and weight indices on
+    the host, before any HIP call."""
+    from ubio_molfm_amd import _lib
+    lib = _lib.load()
+    assert lib.e2v2_gemm_packed_bytes(3, 256, 64) == 3 * 2 * 2 * 3 * 512 * 16
+    assert lib.e2v2_gemm_packed_bytes(1, 100, 64) == -1 and lib.e2v2_gemm_packed_bytes(1, 128, 40) == -1
+    g = _lib.GemmArgs()
+    g.a = g.b = g.c = 16                 # never dereferenced: the checks fail first
+    g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w = 64, 128, 10, 128, 64, 2, 1
+    g.widx[1] = 1                         # only weight 0 exists
+    assert lib.e2v2_gemm_s3(_lib.C.byref(g), None) != 0 and b"widx[1]" in lib.e2v2_last_error()
+    g.widx[1], g.n = 0, 100
+    assert lib.e2v2_gemm_s3(_lib.C.byref(g), None) != 0 and b"multiple of 128" in lib.e2v2_last_error()

@@ -1,0 +1,108 @@
+"""The split-bf16 fp32 GEMM (e2v2_gemm_s3) against float64 products and against
+the native fp32 GEMM of the same operands (torch.mm on the GPU: hipBLASLt on fp32
+MFMA).
+
+Error measure: |C - C64| elementwise over the GEMM's own scale sum_k |a_ik| |b_kj|
+(the quantity fp32 rounding error is proportional to).  The bar: the maximum of
+that measure within 2x of the native fp32 GEMM's on the same operands, and below
+8 units of fp32 rounding (2^-24) times sqrt(k)."""
+import math
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+
+
+def _scaled_err(c, a64, w64, res64=None, bias64=None):
+    ref = a64 @ w64.transpose(-1, -2)
+    scale = a64.abs() @ w64.abs().transpose(-1, -2)
+    if bias64 is not None:
+        ref = ref + bias64
+        scale = scale + bias64.abs()
+    if res64 is not None:
+        ref = ref + res64
+        scale = scale + res64.abs()
+    return float(((c.double().cpu() - ref).abs() / (scale + 1e-300)).max())
+
+
+def _wide_range(shape, gen, spread=8.0):
+    """Random values with magnitudes over 2^-spread .. 2^spread and both signs."""
+    mag = torch.exp2((torch.rand(shape, generator=gen) * 2 - 1) * spread)
+    return (torch.randn(shape, generator=gen).sign() * mag).float()
+
+
+@pytest.mark.parametrize("m,n,k,batch", [(1000, 256, 256, 9), (130, 128, 32, 1), (1, 768, 1536, 1),
+                                         (2048, 512, 768, 3), (517, 1024, 512, 1)])
+def test_split_gemm_against_float64_and_native_fp32(pkg, cuda, m, n, k, batch):
+    from ubio_molfm_amd import gemm
+    g = torch.Generator().manual_seed(m + n + k)
+    n_w = min(batch, 3)
+    a = torch.randn(batch, m, k, generator=g)
+    w = torch.randn(n_w, n, k, generator=g) / math.sqrt(k)
+    widx = [b % n_w for b in range(batch)]
+    pw = gemm.pack(w.to(cuda))
+    out = torch.empty(batch, m, n, device=cuda)
+    gemm.gemm(a.to(cuda), pw, out, widx)
+    wb = w[widx].double()
+    err = _scaled_err(out, a.double(), wb)
+    native = torch.stack([a[b].to(cuda) @ w[widx[b]].to(cuda).t() for b in range(batch)])
+    err_native = _scaled_err(native, a.double(), wb)
+    print(f"m={m} n={n} k={k} batch={batch}: split {err / U:.2f} u, native fp32 {err_native / U:.2f} u")
+    assert err <= max(2.0 * err_native, 2 * U) and err <= 8 * U * math.sqrt(k), (err / U, err_native / U)
+
+
+def test_split_gemm_wide_range_bias_residual_strides(pkg, cuda):
+    """Operands over 2^-8..2^8 (every piece matters), a bias on the first batch
+    only, the residual read from the output buffer itself, rows of A strided
+    (a column slice of a wider matrix) and the weight packed from its transpose."""
+    from ubio_molfm_amd import gemm
+    g = torch.Generator().manual_seed(7)
+    batch, m, n, k = 3, 300, 256, 512
+    a_wide = _wide_range((batch, m, k + 64), g)
+    a = a_wide[:, :, 32:32 + k]
+    wt = _wide_range((2, k, n), g) / k            # packed transposed: W_w = wt[w]^T
+    bias = _wide_range((n,), g)
+    res = _wide_range((batch, m, n), g)
+    widx = [1, 0, 1]
+    pw = gemm.pack(wt.to(cuda), transpose=True)
+    a_dev = a_wide.to(cuda)[:, :, 32:32 + k]
+    assert a_dev.stride(1) == k + 64
+    out = res.to(cuda).clone()
+    gemm.gemm(a_dev, pw, out, widx, bias=bias.to(cuda), bias_batches=1, res=out)
+    w64 = wt[widx].double().transpose(1, 2)
+    b64 = torch.zeros(batch, 1, n, dtype=torch.float64)
+    b64[0, 0] = bias.double()
+    err = _scaled_err(out, a.double(), w64, res64=res.double(), bias64=b64)
+    print(f"wide range: {err / U:.2f} u")
+    assert err <= 8 * U * math.sqrt(k)
+
+
+def test_split_gemm_exact_on_representable_products(pkg, cuda):
+    """Integer operands whose products and sums are exact in fp32: the split
+    GEMM must return them exactly (any dropped piece product or wrong piece
+    pairing shows as an integer error)."""
+    from ubio_molfm_amd import gemm
+    g = torch.Generator().manual_seed(3)
+    m, n, k = 257, 128, 64
+    a = torch.randint(-2 ** 11, 2 ** 11, (m, k), generator=g).float()      # 12-bit: needs two bf16 pieces
+    w = torch.randint(-2 ** 5, 2 ** 5, (n, k), generator=g).float()
+    pw = gemm.pack(w.to(cuda))
+    out = torch.empty(m, n, device=cuda)
+    gemm.gemm(a.to(cuda), pw, out)
+    ref = (a.double() @ w.double().t())
+    assert ref.abs().max() < 2 ** 24
+    assert torch.equal(out.cpu().double(), ref)
+
+
+def test_split_gemm_rejects_bad_shapes(pkg, cuda):
+    from ubio_molfm_amd import gemm
+    with pytest.raises(ValueError):
+        gemm.pack(torch.randn(100, 64, device=cuda))              # n not a multiple of 128
+    pw = gemm.pack(torch.randn(128, 64, device=cuda))
+    with pytest.raises(ValueError):
+        gemm.gemm(torch.randn(10, 32, device=cuda), pw, torch.empty(10, 128, device=cuda))
+    out = torch.empty(0, 128, device=cuda)
+    gemm.gemm(torch.empty(0, 64, device=cuda), pw, out)            # no rows: nothing to do

@@ -25,6 +25,7 @@ EXPORTS = [
     "e2v2_segment_metadata", "e2v2_pair_count", "e2v2_pair_emit", "e2v2_seg_dot", "e2v2_seg_reduce",
     "e2v2_gather_rows", "e2v2_outer_reduce", "e2v2_outer_bwd",
     "e2v2_radial_eval", "e2v2_radial_eval_bwd", "e2v2_sh_contract", "e2v2_sh_contract_bwd",
+    "e2v2_gemm_s3", "e2v2_gemm_pack", "e2v2_gemm_packed_bytes",
 ]
 
 
@@ -76,6 +77,12 @@ class DegArgs(C.Structure):
                 ("rtab_h", f32), ("avg", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32)]
 
 
+class GemmArgs(C.Structure):
+    _fields_ = [("a", vp), ("lda", i64), ("a_bs", i64), ("b", vp), ("n_w", i32), ("c", vp), ("ldc", i64), ("c_bs", i64),
+                ("r", vp), ("ldr", i64), ("r_bs", i64), ("bias", vp), ("bias_batches", i32),
+                ("m", i32), ("n", i32), ("k", i32), ("batch", i32), ("widx", i32 * 16)]
+
+
 _lib = None
 
 
@@ -95,6 +102,8 @@ def load():
     lib.e2v2_attn_bwd_workspace.argtypes = [C.c_int64]
     lib.e2v2_deg_bwd_workspace.restype = C.c_size_t
     lib.e2v2_deg_bwd_workspace.argtypes = [C.c_int64]
+    lib.e2v2_gemm_packed_bytes.restype = C.c_int64
+    lib.e2v2_gemm_packed_bytes.argtypes = [C.c_int32, C.c_int32, C.c_int32]
     _lib = lib
     return lib
 

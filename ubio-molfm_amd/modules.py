@@ -3,12 +3,16 @@
 Class names, constructor arguments, parameter/buffer names and shapes follow the
 reference (src/molfm/models/e2former/e2former.py, module_utils.py,
 wigner6j/so2_tensor_product.py), so a reference state_dict loads with
-``strict=True``.  Dense per-node algebra stays in PyTorch (hipBLASLt GEMMs);
-every edge-level operation runs in libe2v2.so through ``ops``.
+``strict=True``.  Every edge-level operation runs in libe2v2.so through ``ops``;
+the per-node dense layers run as fp32 GEMMs on bf16 MFMA by the exact
+three-piece operand split of ``gemm`` (e2v2_gemm_s3) in fp32 mode, and as bf16
+hipBLASLt GEMMs in bf16 mode.  ``E2V2_FP32_GEMM=native`` in the environment
+selects hipBLASLt's fp32 GEMMs instead of the split ones (a measurement switch).
 """
 from __future__ import annotations
 
 import math
+import os
 from typing import Optional
 
 import numpy as np
@@ -18,6 +22,7 @@ from torch.profiler import record_function
 
 from . import so3
 from . import _lib
+from . import gemm as s3gemm
 from .ops import AttentionFn, DegreeEmbedFn, RadialCache, RadialEvalFn, ShContractFn
 
 
@@ -35,6 +40,14 @@ SIGMOID_NORM = _e3nn_normalize2mom(torch.sigmoid)
 
 def _expand_index(lmax: int) -> torch.Tensor:
     return torch.tensor([l for l in range(lmax + 1) for _ in range(2 * l + 1)], dtype=torch.long)
+
+
+FP32_GEMM = os.environ.get("E2V2_FP32_GEMM", "split")
+
+
+def split_gemm_on() -> bool:
+    """fp32 per-node GEMMs on the split-bf16 kernel (else hipBLASLt fp32)."""
+    return FP32_GEMM != "native"
 
 
 def _stream():
@@ -122,15 +135,37 @@ class MRowWeight:
     for per-l GEMMs (fp32, or a bf16 copy), and in fp32 its per-m-row expansions
     for one batched GEMM over the (lmax+1)^2 m-rows (one launch instead of lmax+1,
     fewer partial tiles): ``fwd`` [M, Cin, O] and ``bwd`` [M, O, Cin]; in bf16 the
-    per-l transpose ``wt`` [lmax+1, Cin, O] (B operand of the fused projection's backward)."""
-    __slots__ = ("w", "fwd", "bwd", "wt")
+    per-l transpose ``wt`` [lmax+1, Cin, O] (B operand of the fused projection's backward).
+    In fp32, ``s3f()`` / ``s3b()``: the per-l weights packed for the split GEMM
+    (W_l for y = x W_l^T, W_l^T for the input gradient), packed on first use."""
+    __slots__ = ("w", "fwd", "bwd", "wt", "_s3f", "_s3b")
 
     def __init__(self, w, fwd=None, bwd=None, wt=None):
         self.w, self.fwd, self.bwd, self.wt = w, fwd, bwd, wt
+        self._s3f = self._s3b = None
+
+    def split_ok(self) -> bool:
+        w = self.w
+        return (split_gemm_on() and w.dtype == torch.float32 and w.is_cuda
+                and s3gemm.supported(w.shape[1], w.shape[2]) and s3gemm.supported(w.shape[2], w.shape[1]))
+
+    def s3f(self):
+        if self._s3f is None:
+            self._s3f = s3gemm.pack(self.w)
+        return self._s3f
+
+    def s3b(self):
+        if self._s3b is None:
+            self._s3b = s3gemm.pack(self.w, transpose=True)
+        return self._s3b
 
 
 def _m_index(lmax: int, device):
     return torch.tensor([l for l in range(lmax + 1) for _ in range(2 * l + 1)], device=device)
+
+
+def _m_degrees(lmax: int):
+    return [l for l in range(lmax + 1) for _ in range(2 * l + 1)]
 
 
 def mrow_weight(owner, name: str, w, bf16: bool, lmax: int):
@@ -151,6 +186,9 @@ def mrow_weight(owner, name: str, w, bf16: bool, lmax: int):
 
 def _mrow_gemm(x, Wop: MRowWeight, bias):
     """y[m] = x[m] W_l(m)^T (+ bias on row 0) for x [M, N, Cin] (fp32, batched)."""
+    if Wop.split_ok():
+        y = x.new_empty(x.shape[0], x.shape[1], Wop.w.shape[1])
+        return s3gemm.gemm(x, Wop.s3f(), y, _m_degrees(Wop.w.shape[0] - 1), bias=bias, bias_batches=1)
     y = torch.bmm(x, Wop.fwd)
     if bias is not None:
         y[0].add_(bias)
@@ -167,6 +205,10 @@ class SO3LinearFn(torch.autograd.Function):
     def forward(ctx, x, Wop, bias, lmax: int, res=None):
         x = x.contiguous()
         ctx.Wop, ctx.lmax, ctx.has_res = Wop, lmax, res is not None
+        if Wop.split_ok():
+            y = x.new_empty(x.shape[0], x.shape[1], Wop.w.shape[1])
+            return s3gemm.gemm(x, Wop.s3f(), y, _m_degrees(lmax), bias=bias, bias_batches=1,
+                               res=None if res is None else res.contiguous())
         if Wop.fwd is not None and res is None:
             return _mrow_gemm(x, Wop, bias)
         W = Wop.w
@@ -192,6 +234,10 @@ class SO3LinearFn(torch.autograd.Function):
     def backward(ctx, gy):
         Wop = ctx.Wop
         gy = gy.contiguous()
+        if Wop.split_ok():
+            gx = gy.new_empty(gy.shape[0], gy.shape[1], Wop.w.shape[2])
+            return (s3gemm.gemm(gy, Wop.s3b(), gx, _m_degrees(ctx.lmax)), None, None, None,
+                    (gy if ctx.has_res else None))
         if Wop.bwd is not None:
             return torch.bmm(gy, Wop.bwd), None, None, None, (gy if ctx.has_res else None)
         W = Wop.w
@@ -342,15 +388,20 @@ class SO2OutFn(torch.autograd.Function):
         res = None if res is None else res.contiguous()
         O = Wc[0][3].shape[1]
         y = so2.new_empty(9, N, O, dtype=torch.float32)
-        for (l3, cnt, start, W, _) in Wc:
+        split = all(e[5] is not None for e in Wc) and so2.dtype == torch.float32
+        for (l3, cnt, start, W, _, PF, _) in Wc:
             K = W.shape[0]
             A = so2[start * N:(start + (2 * l3 + 1) * K) * N].view(-1, K)
             a, b = l3 * l3, (l3 + 1) ** 2
-            if res is not None:
+            if split:
+                s3gemm.gemm(A, PF, y[a:b].view(-1, O), bias=bias if l3 == 0 else None,
+                            res=None if res is None else res[a:b].view(-1, O))
+            elif res is not None:
                 _addmm_into(res[a:b].view(-1, O), A, W, out=y[a:b].view(-1, O))
             else:
                 _mm_into(A, W, out=y[a:b].view(-1, O))
-        y[0].add_(bias)
+        if not split:
+            y[0].add_(bias)
         ctx.has_res = res is not None
         ctx.Wc, ctx.N = Wc, N
         ctx.shape, ctx.so2_dtype = so2.shape, so2.dtype
@@ -362,10 +413,15 @@ class SO2OutFn(torch.autograd.Function):
         N = ctx.N
         O = gy.shape[2]
         gso2 = gy.new_empty(ctx.shape, dtype=ctx.so2_dtype)
-        for (l3, cnt, start, _, WT) in ctx.Wc:
+        split = all(e[6] is not None for e in ctx.Wc) and ctx.so2_dtype == torch.float32
+        for (l3, cnt, start, _, WT, _, PB) in ctx.Wc:
             K = WT.shape[1]
             a, b = l3 * l3, (l3 + 1) ** 2
-            _mm_into(gy[a:b].view(-1, O), WT, out=gso2[start * N:(start + (2 * l3 + 1) * K) * N].view(-1, K))
+            dst = gso2[start * N:(start + (2 * l3 + 1) * K) * N].view(-1, K)
+            if split:
+                s3gemm.gemm(gy[a:b].view(-1, O), PB, dst)
+            else:
+                _mm_into(gy[a:b].view(-1, O), WT, out=dst)
         return gso2, (gy if ctx.has_res else None), None, None, None
 
 
@@ -466,9 +522,13 @@ class GateFn(torch.autograd.Function):
     """Gate_s3: sc = x[0] Wg^T + bg, then the activation kernel on x[9][N][C]."""
 
     @staticmethod
-    def forward(ctx, x, Wg, bg, k1: float, k2: float):
+    def forward(ctx, x, Wg, bg, k1: float, k2: float, packs=None):
         x = x.contiguous()
-        if Wg.dtype == BF16:
+        ctx.packs = packs
+        if packs is not None:
+            sc = x.new_empty(x.shape[1], packs[0].n)
+            s3gemm.gemm(x[0], packs[0], sc, bias=bg)
+        elif Wg.dtype == BF16:
             sc = torch.mm(_bf(x[0]), Wg.t(), out_dtype=torch.float32).add_(bg)
         else:
             sc = torch.addmm(bg, x[0], Wg.t())
@@ -486,8 +546,11 @@ class GateFn(torch.autograd.Function):
         gsc = torch.empty_like(sc); gx = torch.empty_like(x)
         _lib.call("e2v2_gate_bwd", _dp(sc), _dp(x), _dp(gy), _dp(gsc), _dp(gx), _lib.i32(x.shape[1]),
                   _lib.f32(ctx.k[0]), _lib.f32(ctx.k[1]), _stream())
-        _mm_into(gsc, Wg, out=gx[0])            # the kernel leaves gx[0] = 0
-        return gx, None, None, None, None
+        if ctx.packs is not None:                # the kernel leaves gx[0] = 0
+            s3gemm.gemm(gsc, ctx.packs[1], gx[0])
+        else:
+            _mm_into(gsc, Wg, out=gx[0])
+        return gx, None, None, None, None, None
 
 
 class DenseFn(torch.autograd.Function):
@@ -513,7 +576,43 @@ class DenseFn(torch.autograd.Function):
         return gx, None, None
 
 
+class DenseS3Fn(torch.autograd.Function):
+    """y = x W^T + b for a constant fp32 weight on the split GEMM (packs of W for
+    the forward and of W^T for the input gradient); input gradient only."""
+
+    @staticmethod
+    def forward(ctx, x, packs, b):
+        x = x.contiguous()
+        pf, pb = packs
+        y = x.new_empty(x.shape[0], pf.n)
+        s3gemm.gemm(x, pf, y, bias=b)
+        ctx.pb = pb
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        gy = gy.contiguous()
+        gx = gy.new_empty(gy.shape[0], ctx.pb.n)
+        s3gemm.gemm(gy, ctx.pb, gx)
+        return gx, None, None
+
+
+def dense_packs(lin: nn.Linear):
+    """Split-GEMM packs (W, W^T) of an nn.Linear's weight (cached per version), or
+    None when the split GEMM does not apply."""
+    w = lin.weight
+    if not (split_gemm_on() and w.is_cuda and w.dtype == torch.float32
+            and s3gemm.supported(w.shape[0], w.shape[1]) and s3gemm.supported(w.shape[1], w.shape[0])):
+        return None
+    return cached(lin, "s3_packs", (w,), lambda: (s3gemm.pack(w.detach()), s3gemm.pack(w.detach(), transpose=True)))
+
+
 def _linear(x, lin: nn.Linear):
+    if x.dim() == 2 and x.dtype == torch.float32:
+        packs = dense_packs(lin)
+        if packs is not None:
+            b = None if lin.bias is None else lin.bias.detach().float().contiguous()
+            return DenseS3Fn.apply(x, packs, b)
     return torch.nn.functional.linear(x, lin.weight.detach(), None if lin.bias is None else lin.bias.detach())
 
 
@@ -656,8 +755,9 @@ class Gate_s3(nn.Module):
         nn.init.uniform_(self.gates.weight, -bound, bound)
 
     def forward(self, x, bf16: bool = False):
+        packs = None if bf16 else dense_packs(self.gates)
         return GateFn.apply(x, gemm_weight(self.gates, "weight", bf16), self.gates.bias.detach(), SILU_NORM,
-                            SIGMOID_NORM)
+                            SIGMOID_NORM, packs)
 
 
 class FeedForwardNetwork_s3(nn.Module):
@@ -1114,9 +1214,10 @@ class E2AttentionArbOrder_sparse(nn.Module):
             out = []
             for l in range(self.lmax + 1):
                 W = pz.weight.detach()[l][:, P].t()
-                out.append((l, 1, C * l * l, W.to(dt).contiguous(), W.t().to(dt).contiguous()))
+                out.append((l, 1, C * l * l, W.to(dt).contiguous(), W.t().to(dt).contiguous()) + _so2_packs(W, bf16))
             return out
-        return cached(self, "zero_out_bf16" if bf16 else "zero_out", (pz.weight,), build)
+        key = "zero_out_bf16" if bf16 else ("zero_out_s3" if split_gemm_on() else "zero_out")
+        return cached(self, key, (pz.weight,), build)
 
     def so2_out_weights(self, bf16: bool = False):
         """Per output degree l3 (l3 order): (l3, cnt, start, W, W^T) with W [cnt 256, O]
@@ -1135,9 +1236,11 @@ class E2AttentionArbOrder_sparse(nn.Module):
                 Wcat = torch.cat([Wt.double() for (_, _, Wt) in lst], dim=0)
                 W = Wcat @ pf.weight.detach()[l3].double().t()
                 dt = BF16 if bf16 else torch.float32
-                out.append((l3, cnt, start, W.to(dt).contiguous(), W.t().to(dt).contiguous()))
+                Wf = W.float()
+                out.append((l3, cnt, start, W.to(dt).contiguous(), W.t().to(dt).contiguous()) + _so2_packs(Wf, bf16))
             return out
-        return cached(self, "so2_out_bf16" if bf16 else "so2_out", params, build)
+        key = "so2_out_bf16" if bf16 else ("so2_out_s3" if split_gemm_on() else "so2_out")
+        return cached(self, key, params, build)
 
     def forward_fused(self, x: torch.Tensor, ctx: EdgeContext, res: Optional[torch.Tensor] = None):
         """x [9, N, C] (m-major) -> attention(x) (+ res when given), [9, N, C].
@@ -1173,6 +1276,17 @@ class E2AttentionArbOrder_sparse(nn.Module):
         pf = self.proj_first
         with record_function("first-order"):
             return SO2OutFn.apply(so2, res, self.so2_out_weights(bf16), pf.bias.detach(), N)
+
+
+def _so2_packs(W: torch.Tensor, bf16: bool):
+    """(forward, backward) split-GEMM packs of an SO2OutFn operand W [K, O] (y = A W,
+    gA = gy W^T), or (None, None) in bf16 mode, with the split GEMM off, or for an
+    unsupported shape."""
+    K, O = W.shape
+    if bf16 or not split_gemm_on() or not W.is_cuda or not (s3gemm.supported(O, K) and s3gemm.supported(K, O)):
+        return (None, None)
+    W = W.float().contiguous()
+    return (s3gemm.pack(W, transpose=True), s3gemm.pack(W))
 
 
 def _env_of(poly: str, min_dist: float):
