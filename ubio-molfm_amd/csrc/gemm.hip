@@ -35,7 +35,8 @@
 // LDS destination (no staging registers; rows past m read as zero through the
 // buffer's bound).  A wavefront splits its A fragment of the next stage while the
 // 24 MFMAs of the current one run (B by piece: b0 with a0, a1, a2; b1 with a0,
-// a1; b2 with a0).  Outputs are written with streaming stores.
+// a1; b2 with a0).  Outputs are written with ordinary stores, so that they stay
+// in the L2 / Infinity Cache for the kernel that consumes them.
 // In LDS (64 banks of 4 bytes: a 16-byte granule's bank group is its index mod 16)
 // an A row keeps its 16 k as four granules, granule g of row r in slot
 // g ^ ((r / 4) & 3); a B piece keeps a column's 16 k as two granules, granule g of
@@ -190,7 +191,7 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
         float v = acc[j][r];
         if (with_bias) v += bv;
         if (rb) v += rb[(size_t)row * G.ldr + col];
-        ntstore(v, cb + (size_t)row * G.ldc + col);
+        cb[(size_t)row * G.ldc + col] = v;
       }
     }
   }
