@@ -470,6 +470,20 @@ int e2v2_gemm_s3(const e2v2_gemm_args* args, hipStream_t s);
  * without a copy) into e2v2_gemm_packed_bytes(n_w, n, k) bytes at packed (16-byte aligned); the bytes needed,
  * or -1 for an unsupported shape. */
 int64_t e2v2_gemm_packed_bytes(int n_w, int n, int k);
+/* The Q/K projection with its m-contraction (as e2v2_qk_proj_fwd / _bwd above) on the split GEMM.  Pairs
+ * p < 2 hid: (q_a, q_b) columns p of the stacked w for p < hid, else (k_a, k_b) columns p - hid.
+ *   fwd: wp = the three per-l [4 hid][C] weights packed with their columns in the tile-paired order (128-column
+ *        tile t: the a-columns of pairs 64 t .. +63, then their b-columns), bias [4 hid] in that order (m = 0
+ *        only; may be NULL); writes hq, hk [N][3 hid] and y [9][N][4 hid] with column 16 (p / 8) + 8 ab + p % 8
+ *        holding side ab of pair p (kept for the backward).
+ *   bwd: gx [9][N][C] = gy W (+ gv Wv when gv != NULL, gv [9][N][cv]), gy the contraction's gradient formed
+ *        from y, ghq, ghk as the operand is read; wp = per l the packed [W rows in y's order ; Wv_l]^T
+ *        ([C][4 hid + cv]).
+ * Requires hid % 64 == 0, C % 16 (fwd) / % 128 (bwd), cv % 16 == 0; operands 16-byte aligned. */
+int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bias, float* y, float* hq, float* hk, int n,
+                        int hid, int c, hipStream_t s);
+int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* ghk, const void* wp, const float* gv,
+                        float* gx, int n, int hid, int c, int cv, hipStream_t s);
 int e2v2_gemm_pack(const float* w, int64_t ld_n, int64_t ld_k, int64_t w_stride, int n_w, int n, int k, void* packed,
                    hipStream_t s);
 

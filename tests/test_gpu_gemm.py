@@ -106,3 +106,47 @@ def test_split_gemm_rejects_bad_shapes(pkg, cuda):
         gemm.gemm(torch.randn(10, 32, device=cuda), pw, torch.empty(10, 128, device=cuda))
     out = torch.empty(0, 128, device=cuda)
     gemm.gemm(torch.empty(0, 64, device=cuda), pw, out)            # no rows: nothing to do
+
+
+@pytest.mark.parametrize("n,with_v,with_bias", [(1, True, True), (300, False, True), (1000, True, False)])
+def test_qk_proj_split(pkg, cuda, n, with_v, with_bias):
+    """Split-GEMM Q/K projection + m-contraction (forward) and its input gradient
+    with the value projection's gradient folded in (backward) against float64, at
+    the fp32 fused kernel's tolerances (2e-5 forward, 1e-4 gradient)."""
+    from ubio_molfm_amd import gemm
+    torch.manual_seed(7)
+    hid, C, Cv = 512, 256, 256
+    print(f"[qk_proj s3] n={n} with_v={with_v} bias={with_bias}", flush=True)
+    idx = torch.tensor([0, 1, 1, 1, 2, 2, 2, 2, 2], device=cuda)
+    x = torch.randn(9, n, C, device=cuda)
+    W = torch.randn(3, 4 * hid, C, device=cuda) / 16
+    bias = torch.randn(4 * hid, device=cuda) if with_bias else None
+    Wv = torch.randn(3, Cv, C, device=cuda) / 16
+    P = gemm.pack_qk(W, bias, Wv)
+    hq, hk, y = gemm.qk_forward(x, P)
+    _, bwd_order = gemm.qk_orders(hid)
+    y_model = torch.empty_like(y)
+    y_model[:, :, torch.as_tensor(bwd_order, device=cuda)] = y        # back to W's column order
+    L = [slice(0, 1), slice(1, 4), slice(4, 9)]
+    xd = x.double().requires_grad_(True)
+    yd = torch.bmm(xd, W.double()[idx].transpose(1, 2))
+    if with_bias:
+        shift = torch.zeros(9, 1, 4 * hid, device=cuda, dtype=torch.float64)
+        shift[0, 0] = bias.double()
+        yd = yd + shift
+    aq, bq, ak, bk = yd.split(hid, dim=2)
+    hqd = torch.cat([(aq[s] * bq[s]).sum(0) for s in L], dim=1)
+    hkd = torch.cat([(ak[s] * bk[s]).sum(0) for s in L], dim=1)
+    rel = lambda a, b: float((a.double() - b).norm() / (b.norm() + 1e-30))
+    e_y, e_q, e_k = rel(y_model, yd.detach()), rel(hq, hqd.detach()), rel(hk, hkd.detach())
+    ghq = torch.randn(n, 3 * hid, device=cuda); ghk = torch.randn(n, 3 * hid, device=cuda)
+    gv = torch.randn(9, n, Cv, device=cuda) if with_v else None
+    gx = gemm.qk_backward(y, ghq, ghk, gv, P)
+    obj = (hqd * ghq.double()).sum() + (hkd * ghk.double()).sum()
+    if with_v:
+        obj = obj + (torch.bmm(xd, Wv.double()[idx].transpose(1, 2)) * gv.double()).sum()
+    gxd, = torch.autograd.grad(obj, xd)
+    e_g = rel(gx, gxd)
+    print(f"[qk_proj s3] n={n} y {e_y:.2e} hq {e_q:.2e} hk {e_k:.2e} gx {e_g:.2e}", flush=True)
+    assert e_y < 2e-5 and e_q < 2e-5 and e_k < 2e-5
+    assert e_g < 1e-4

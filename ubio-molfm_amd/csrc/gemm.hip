@@ -94,79 +94,83 @@ __device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, bf1
   for (int k = 0; k < 3; ++k) p[k] = __builtin_bit_cast(bf16x8, (uint32x4){u[k][0], u[k][1], u[k][2], u[k][3]});
 }
 
-__global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
-  const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
-  const int n_mt = (G.m + kGM - 1) / kGM, n_nt = G.n / kGN, n_tiles = G.batch * n_mt * n_nt;
-  const int tile = xcd_row(blockIdx.x, n_tiles);
-  if (tile >= n_tiles) return;
-  const int nt = tile % n_nt, mt = (tile / n_nt) % n_mt, bi = tile / (n_nt * n_mt);
-  const int row0 = mt * kGM, nks = G.k / kGK;
-
-  // A: buffer over this batch's rows row0 .. m-1 (reads past m return zero).  Load
-  // instruction ii (= wv, wv + 4) fills LDS granules 64 ii .. +63, i.e. rows
-  // 16 ii + lane / 4, slot lane % 4, from the source granule that belongs there.
-  const float* abase = G.a + (size_t)bi * G.a_bs + (size_t)row0 * G.lda;
-  const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(abase), (short)0, (int)((uint32_t)(G.m - row0) * (uint32_t)G.lda * 4u), 0x00020000);
-  uint32_t a_voff[kGAi / 4];
+// LDS-direct load offsets of an fp32 A tile of 128 rows (row stride lda floats):
+// this wavefront's two loads per stage (ii = wv, wv + 4) fill LDS granules
+// 64 ii .. +63, i.e. rows 16 ii + lane / 4, slot lane % 4, from the source
+// granule that belongs there; byte offsets from the tile's first row.
+__device__ __forceinline__ void a_offsets(int wv, int lane, int lda, uint32_t (&voff)[kGAi / 4]) {
 #pragma unroll
   for (int i = 0; i < kGAi / 4; ++i) {
     const int r = (wv + 4 * i) * 16 + (lane >> 2), sl = lane & 3;
-    a_voff[i] = (uint32_t)(r * G.lda + 4 * (sl ^ ((r >> 2) & 3))) * 4u;
+    voff[i] = (uint32_t)(r * lda + 4 * (sl ^ ((r >> 2) & 3))) * 4u;
   }
-  // B: contiguous packed stages of this weight and column tile
-  const char* bbase = static_cast<const char*>(G.b) + ((size_t)G.widx[bi] * n_nt + nt) * (size_t)nks * kGBStage * 16;
-  const __amdgpu_buffer_rsrc_t br =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(bbase), (short)0, nks * kGBStage * 16, 0x00020000);
-
-  auto load = [&](int ks, int buf) {
-    char* As = lds + buf * kGStage;
-    char* Bs = As + kGAg * 16;
-    const uint32_t koff = (uint32_t)(ks * kGK) * 4u;
+}
+// Buffer resource over rows row0 .. m-1 of a row-major fp32 matrix (reads past
+// row m - 1 return zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, int row0, int m, int ld) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + (size_t)row0 * ld), (short)0,
+                                           (int)((uint32_t)(m - row0) * (uint32_t)ld * 4u), 0x00020000);
+}
+__device__ __forceinline__ void load_a(__amdgpu_buffer_rsrc_t r, const uint32_t (&voff)[kGAi / 4], uint32_t koff,
+                                       char* As, int wv) {
 #pragma unroll
-    for (int i = 0; i < kGAi / 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void*)(As + (wv + 4 * i) * 1024), 16, a_voff[i] + koff, 0, 0, 0);
-    const uint32_t bst = (uint32_t)ks * kGBStage * 16u;
+  for (int i = 0; i < kGAi / 4; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(As + (wv + 4 * i) * 1024), 16, voff[i] + koff, 0, 0, 0);
+}
+// The packed B stage ks (contiguous 12 KB from the weight's column-tile base).
+__device__ __forceinline__ void load_b(__amdgpu_buffer_rsrc_t r, int ks, char* Bs, int wv, int lane) {
+  const uint32_t bst = (uint32_t)ks * kGBStage * 16u;
 #pragma unroll
-    for (int i = 0; i < kGBi / 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (lds_void*)(Bs + (wv + 4 * i) * 1024), 16,
-                                               bst + (uint32_t)((wv + 4 * i) * 1024 + 16 * lane), 0, 0, 0);
-  };
-  // wavefront wv: rows 32 wv .. +31 of the tile, all 128 columns (four 32x32 tiles j)
-  const int ra = wv * 32 + (lane & 31);
-  auto a_lds = [&](int buf) { return reinterpret_cast<const floatx4*>(lds + buf * kGStage); };
-  auto b_lds = [&](int buf) { return reinterpret_cast<const bf16x8*>(lds + buf * kGStage + kGAg * 16); };
+  for (int i = 0; i < kGBi / 4; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(Bs + (wv + 4 * i) * 1024), 16,
+                                             bst + (uint32_t)((wv + 4 * i) * 1024 + 16 * lane), 0, 0, 0);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t b_rsrc(const void* packed, int w, int n_nt, int nt, int nks) {
+  const char* base = static_cast<const char*>(packed) + ((size_t)w * n_nt + nt) * (size_t)nks * kGBStage * 16;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nks * kGBStage * 16, 0x00020000);
+}
 
-  floatx16 acc[4];
+// The pipelined K loop of every kernel here: stage ks sits in LDS buffer ks & 1
+// (A at offset 0, the three B pieces at 16 kGAg, any extra region after them);
+// stage ks + 2 is loaded into it (load(ks, buf)) once every wavefront has read
+// it.  read_a(ks, buf, x0, x1) gives this lane's eight fp32 A values of stage ks
+// (row 32 wv + lane % 32, k 8 (lane / 32) .. +7); they are split while the 24
+// MFMAs of the previous stage run.  The wavefront accumulates rows 32 wv .. +31
+// of the tile over all 128 columns (four 32x32 tiles j).
+template <typename Load, typename ReadA>
+__device__ __forceinline__ void kloop(const char* lds, int stage_bytes, int nks, int lane, Load&& load,
+                                      ReadA&& read_a, floatx16 (&acc)[4]) {
+  const int h = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-
-  // Stage ks sits in buffer ks & 1; stage ks + 2 is loaded into it once every
-  // wavefront has read it.  The A fragment of stage ks + 1 is split while the
-  // MFMAs of stage ks run.
   load(0, 0);
   if (nks > 1) load(1, 1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   bf16x8 a_cur[3];
-  split8(a_lds(0)[a_slot(ra, 2 * h)], a_lds(0)[a_slot(ra, 2 * h + 1)], a_cur);
+  {
+    floatx4 x0, x1;
+    read_a(0, 0, x0, x1);
+    split8(x0, x1, a_cur);
+  }
   for (int ks = 0; ks < nks; ++ks) {
     const int buf = ks & 1;
+    const bf16x8* Bs = reinterpret_cast<const bf16x8*>(lds + buf * stage_bytes + kGAg * 16);
     bf16x8 b[3][4];
 #pragma unroll
     for (int p = 0; p < 3; ++p)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[p][j] = b_lds(buf)[p * kGBg + b_slot(32 * j + (lane & 31), h)];
+      for (int j = 0; j < 4; ++j) b[p][j] = Bs[p * kGBg + b_slot(32 * j + (lane & 31), h)];
     if (ks + 1 < nks) {
       __builtin_amdgcn_s_waitcnt(0);      // stage ks + 1 landed; this wavefront's reads of buf are done
       __syncthreads();
       if (ks + 2 < nks) load(ks + 2, buf);
     }
-    // (after the last stage this reads the other buffer's stale A: a value never used)
-    const floatx4 x0 = a_lds(buf ^ 1)[a_slot(ra, 2 * h)], x1 = a_lds(buf ^ 1)[a_slot(ra, 2 * h + 1)];
+    // (after the last stage this reads the other buffer's stale contents: values never used)
+    floatx4 x0, x1;
+    read_a(ks + 1, buf ^ 1, x0, x1);
     constexpr int kPa[6] = {0, 1, 2, 0, 1, 0}, kPb[6] = {0, 0, 0, 1, 1, 2};
 #pragma unroll
     for (int q = 0; q < 6; ++q)
@@ -175,6 +179,33 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_cur[kPa[q]], b[kPb[q]][j], acc[j], 0, 0, 0);
     split8(x0, x1, a_cur);
   }
+}
+
+__global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
+  const int n_mt = (G.m + kGM - 1) / kGM, n_nt = G.n / kGN, n_tiles = G.batch * n_mt * n_nt;
+  const int tile = xcd_row(blockIdx.x, n_tiles);
+  if (tile >= n_tiles) return;
+  const int nt = tile % n_nt, mt = (tile / n_nt) % n_mt, bi = tile / (n_nt * n_mt);
+  const int row0 = mt * kGM, nks = G.k / kGK;
+  const __amdgpu_buffer_rsrc_t ar = rows_rsrc(G.a + (size_t)bi * G.a_bs, row0, G.m, (int)G.lda);
+  uint32_t a_voff[kGAi / 4];
+  a_offsets(wv, lane, (int)G.lda, a_voff);
+  const __amdgpu_buffer_rsrc_t br = b_rsrc(G.b, G.widx[bi], n_nt, nt, nks);
+  const int ra = wv * 32 + (lane & 31);
+  floatx16 acc[4];
+  kloop(lds, kGStage, nks, lane,
+        [&](int ks, int buf) {
+          load_a(ar, a_voff, (uint32_t)(ks * kGK) * 4u, lds + buf * kGStage, wv);
+          load_b(br, ks, lds + buf * kGStage + kGAg * 16, wv, lane);
+        },
+        [&](int, int buf, floatx4& x0, floatx4& x1) {
+          const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * kGStage);
+          x0 = As[a_slot(ra, 2 * h)];
+          x1 = As[a_slot(ra, 2 * h + 1)];
+        },
+        acc);
 
   // epilogue: C = acc (+ bias) (+ R)
   const bool with_bias = G.bias && bi < G.bias_batches;
@@ -193,6 +224,162 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
         if (rb) v += rb[(size_t)row * G.ldr + col];
         cb[(size_t)row * G.ldc + col] = v;
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Q/K projection of SO3_Linear2Scalar_e2former (module_utils.py:2198-2266, query
+// and key at e2former.py:300-303) with its m-contraction, on the split GEMM.
+// Pairs p < 2 hid: the query pairs (q_a, q_b) = (weight, weight2) columns p, then
+// the key pairs; hq[n][l hid + p] = sum_{m in l} y[m][n][a(p)] y[m][n][b(p)].
+// Forward: the packed weight's 128-column tile t holds the a-columns of pairs
+// 64 t .. +63 then their b-columns, so a wavefront's tiles j and j + 2 hold the
+// a- and b-values of the same 32 pairs in the same accumulator layout; a
+// workgroup runs the m-rows of its degree l in turn and adds a b to its pair
+// sums.  y is kept for the backward in the paired order:
+//   y[m][n][16 (p / 8) + 8 ab + p % 8]  (ab = 0: a-column, 1: b-column)
+// so that within every 16-k stage of the backward the partner of column k is k ^ 8.
+__device__ __forceinline__ int pair_pos(int p, int ab) { return 16 * (p >> 3) + 8 * ab + (p & 7); }
+
+__global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ x, const void* __restrict__ wp,
+                                                      const float* __restrict__ bias, float* __restrict__ y,
+                                                      float* __restrict__ hq, float* __restrict__ hk, int n,
+                                                      int hid, int c) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
+  const int n_mt = (n + kGM - 1) / kGM, n_pt = 2 * hid / 64, tiles = n_mt * n_pt;
+  // three groups of xcd_grid(tiles) workgroups, l = 2, 1, 0 (5, 3, 1 m-rows): long tiles first
+  const int grp = blockIdx.x / xcd_grid(tiles), L = 2 - grp;
+  const int tile = xcd_row(blockIdx.x - grp * xcd_grid(tiles), tiles);
+  if (tile >= tiles) return;
+  const int mt = tile / n_pt, pt = tile % n_pt, row0 = mt * kGM, nks = c / kGK, O = 4 * hid;
+  uint32_t a_voff[kGAi / 4];
+  a_offsets(wv, lane, c, a_voff);
+  const __amdgpu_buffer_rsrc_t br = b_rsrc(wp, L, n_pt, pt, nks);
+  const int ra = wv * 32 + (lane & 31);
+  float s[2][16];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[j][r] = 0.f;
+  for (int m = L * L; m < (L + 1) * (L + 1); ++m) {
+    if (m != L * L) __syncthreads();      // every wavefront is done with the previous row's LDS stages
+    const __amdgpu_buffer_rsrc_t ar = rows_rsrc(x + (size_t)m * n * c, row0, n, c);
+    floatx16 acc[4];
+    kloop(lds, kGStage, nks, lane,
+          [&](int ks, int buf) {
+            load_a(ar, a_voff, (uint32_t)(ks * kGK) * 4u, lds + buf * kGStage, wv);
+            load_b(br, ks, lds + buf * kGStage + kGAg * 16, wv, lane);
+          },
+          [&](int, int buf, floatx4& x0, floatx4& x1) {
+            const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * kGStage);
+            x0 = As[a_slot(ra, 2 * h)];
+            x1 = As[a_slot(ra, 2 * h + 1)];
+          },
+          acc);
+    float* ym = y + (size_t)m * n * O;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = 64 * pt + 32 * (j & 1) + (lane & 31), ab = j >> 1;
+      const float bv = m == 0 && bias ? bias[128 * pt + 32 * j + (lane & 31)] : 0.f;
+      const int col = pair_pos(p, ab);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = row0 + wv * 32 + acc_row(r, lane);
+        acc[j][r] += bv;
+        if (row < n) ym[(size_t)row * O + col] = acc[j][r];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[j][r] = fmaf(acc[j][r], acc[j + 2][r], s[j][r]);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = 64 * pt + 32 * j + (lane & 31);
+    float* out = p < hid ? hq + L * hid + p : hk + L * hid + (p - hid);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + wv * 32 + acc_row(r, lane);
+      if (row < n) out[(size_t)row * 3 * hid] = s[j][r];
+    }
+  }
+}
+
+// Backward: gx[m][n][k] = sum_o gy[m][n][o] W_l[o][k] + sum_j gv[m][n][j] Wv_l[j][k]
+// with gy at a- / b-column of pair p = g(n, l, p) times the partner's y
+// (g = ghq or ghk at [n][l hid + p']), formed as the A operand is read: the stage
+// holds y[m] of 8 pairs (a then b columns: the partner granules are those of the
+// other half) and their 8 g values (a G tile of 128 rows x 8 fp32 after the B
+// pieces, granule g of row r in slot g ^ ((r / 8) & 1)).  The packed weight is
+// [W_l (rows in the paired order) ; Wv_l]^T per l: the value projection's input
+// gradient enters as cv / 16 further stages with A = gv[m].
+constexpr int kGStageQ = kGStage + 128 * 8 * 4;      // + the G tile: 24 KB
+__device__ __forceinline__ int g_slot(int r, int g) { return r * 2 + (g ^ ((r >> 3) & 1)); }
+
+__global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const float* __restrict__ y, const float* __restrict__ ghq,
+                                                      const float* __restrict__ ghk, const void* __restrict__ wp,
+                                                      const float* __restrict__ gv, float* __restrict__ gx, int n,
+                                                      int hid, int c, int cv) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kGStageQ];
+  const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
+  const int n_mt = (n + kGM - 1) / kGM, n_ct = c / kGN, tiles = 9 * n_mt * n_ct;
+  const int tile = xcd_row(blockIdx.x, tiles);
+  if (tile >= tiles) return;
+  const int ct = tile % n_ct, mt = (tile / n_ct) % n_mt, m = tile / (n_ct * n_mt);
+  const int l = m == 0 ? 0 : (m < 4 ? 1 : 2);
+  const int O = 4 * hid, row0 = mt * kGM, nk1 = O / kGK, nks = nk1 + (gv ? cv / kGK : 0);
+  const int nks_w = nk1 + cv / kGK;                                // stages of the packed weight
+  uint32_t y_voff[kGAi / 4], v_voff[kGAi / 4];
+  a_offsets(wv, lane, O, y_voff);
+  a_offsets(wv, lane, cv, v_voff);
+  const __amdgpu_buffer_rsrc_t yr = rows_rsrc(y + (size_t)m * n * O, row0, n, O);
+  const __amdgpu_buffer_rsrc_t vr = gv ? rows_rsrc(gv + (size_t)m * n * cv, row0, n, cv) : yr;
+  const __amdgpu_buffer_rsrc_t qr = rows_rsrc(ghq, row0, n, 3 * hid), kr = rows_rsrc(ghk, row0, n, 3 * hid);
+  const char* wbase = static_cast<const char*>(wp) + ((size_t)l * n_ct + ct) * (size_t)nks_w * kGBStage * 16;
+  const __amdgpu_buffer_rsrc_t br =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wbase), (short)0, nks_w * kGBStage * 16, 0x00020000);
+  // G tile load: one instruction per wavefront, LDS granules 64 wv .. +63 = rows 32 wv + lane / 2, slot lane % 2
+  const int g_r = 32 * wv + (lane >> 1);
+  const uint32_t g_voff = (uint32_t)(g_r * 3 * hid + 4 * ((lane & 1) ^ ((g_r >> 3) & 1))) * 4u;
+  const int ra = wv * 32 + (lane & 31);
+  floatx16 acc[4];
+  kloop(lds, kGStageQ, nks, lane,
+        [&](int ks, int buf) {
+          char* As = lds + buf * kGStageQ;
+          if (ks < nk1) {
+            load_a(yr, y_voff, (uint32_t)(ks * kGK) * 4u, As, wv);
+            const int p0 = 8 * ks;                                     // first pair of the stage
+            const uint32_t goff = (uint32_t)(l * hid + (p0 < hid ? p0 : p0 - hid)) * 4u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(p0 < hid ? qr : kr, (lds_void*)(As + kGStage + wv * 1024), 16,
+                                                     g_voff + goff, 0, 0, 0);
+          } else {
+            load_a(vr, v_voff, (uint32_t)((ks - nk1) * kGK) * 4u, As, wv);
+          }
+          load_b(br, ks, As + kGAg * 16, wv, lane);
+        },
+        [&](int ks, int buf, floatx4& x0, floatx4& x1) {
+          const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * kGStageQ);
+          if (ks < nk1) {
+            const floatx4* Gs = reinterpret_cast<const floatx4*>(lds + buf * kGStageQ + kGStage);
+            x0 = As[a_slot(ra, 2 - 2 * h)] * Gs[g_slot(ra, 0)];
+            x1 = As[a_slot(ra, 3 - 2 * h)] * Gs[g_slot(ra, 1)];
+          } else {
+            x0 = As[a_slot(ra, 2 * h)];
+            x1 = As[a_slot(ra, 2 * h + 1)];
+          }
+        },
+        acc);
+  float* gm = gx + (size_t)m * n * c;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int col = ct * kGN + 32 * j + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + wv * 32 + acc_row(r, lane);
+      if (row < n) gm[(size_t)row * c + col] = acc[j][r];
     }
   }
 }
@@ -267,5 +454,45 @@ E2V2_API int e2v2_gemm_s3(const e2v2_gemm_args* g, hipStream_t s) {
   const int tiles = G.batch * ((G.m + kGM - 1) / kGM) * (G.n / kGN);
   hipLaunchKernelGGL(k_gemm_s3, dim3(xcd_grid(tiles)), dim3(kGT), 0, s, G);
   E2V2_LAUNCHED("k_gemm_s3");
+  return 0;
+}
+
+// hq, hk [n][3 hid] and the kept y [9][n][4 hid] (paired order) from x [9][n][c];
+// wp: the three per-l weights packed with their columns in the tile-paired order
+// (n = 4 hid, k = c), bias [4 hid] in the same order (m = 0 rows only; may be NULL).
+E2V2_API int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bias, float* y, float* hq, float* hk,
+                                 int n, int hid, int c, hipStream_t s) {
+  using namespace e2v2;
+  E2V2_REQUIRE(hid > 0 && hid % 64 == 0, "qk_proj_fwd_s3: hid=%d must be a positive multiple of 64", hid);
+  E2V2_REQUIRE(c > 0 && c % kGK == 0, "qk_proj_fwd_s3: C=%d must be a positive multiple of %d", c, kGK);
+  E2V2_REQUIRE(x && wp && y && hq && hk, "qk_proj_fwd_s3: null operand");
+  E2V2_REQUIRE(((uintptr_t)x & 15) == 0, "qk_proj_fwd_s3: x must be 16-byte aligned");
+  E2V2_REQUIRE(n >= 0 && (uint64_t)(n + kGM) * (uint64_t)c * 4u < (1ull << 31) &&
+                   (uint64_t)(n + kGM) * 4u * hid < (1ull << 32), "qk_proj_fwd_s3: n=%d too large", n);
+  if (n == 0) return 0;
+  const int tiles = ((n + kGM - 1) / kGM) * (2 * hid / 64);
+  hipLaunchKernelGGL(k_qk_s3_fwd, dim3(3 * xcd_grid(tiles)), dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
+  E2V2_LAUNCHED("k_qk_s3_fwd");
+  return 0;
+}
+
+// gx [9][n][c] from y (paired order), ghq, ghk [n][3 hid] and, when gv != NULL,
+// gv [9][n][cv]; wp: per l the packed [W_l (rows in the paired order) ; Wv_l]^T
+// (n = c, k = 4 hid + cv).
+E2V2_API int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* ghk, const void* wp, const float* gv,
+                                 float* gx, int n, int hid, int c, int cv, hipStream_t s) {
+  using namespace e2v2;
+  E2V2_REQUIRE(hid > 0 && hid % 64 == 0, "qk_proj_bwd_s3: hid=%d must be a positive multiple of 64", hid);
+  E2V2_REQUIRE(c > 0 && c % kGN == 0, "qk_proj_bwd_s3: C=%d must be a positive multiple of %d", c, kGN);
+  E2V2_REQUIRE(cv > 0 && cv % kGK == 0, "qk_proj_bwd_s3: Cv=%d must be a positive multiple of %d", cv, kGK);
+  E2V2_REQUIRE(y && ghq && ghk && wp && gx, "qk_proj_bwd_s3: null operand");
+  E2V2_REQUIRE(((uintptr_t)y & 15) == 0 && ((uintptr_t)ghq & 15) == 0 && ((uintptr_t)ghk & 15) == 0 &&
+                   ((uintptr_t)gv & 15) == 0 && hid % 4 == 0, "qk_proj_bwd_s3: operands must be 16-byte aligned");
+  E2V2_REQUIRE(n >= 0 && (uint64_t)(n + kGM) * 4u * hid * 4u < (1ull << 31) &&
+                   (uint64_t)(n + kGM) * (uint64_t)cv * 4u < (1ull << 31), "qk_proj_bwd_s3: n=%d too large", n);
+  if (n == 0) return 0;
+  const int tiles = 9 * ((n + kGM - 1) / kGM) * (c / kGN);
+  hipLaunchKernelGGL(k_qk_s3_bwd, dim3(xcd_grid(tiles)), dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
+  E2V2_LAUNCHED("k_qk_s3_bwd");
   return 0;
 }

@@ -103,3 +103,86 @@ def gemm(a: torch.Tensor, pw: PackedWeight, out: torch.Tensor, widx: Optional[Se
         g.widx[b] = int(i)
     _lib.call("e2v2_gemm_s3", _lib.C.byref(g), _lib.vp(torch.cuda.current_stream(a.device).cuda_stream))
     return out
+
+
+# ---------------------------------------------------------------------------------------------
+# Q/K projection of SO3_Linear2Scalar_e2former with its m-contraction (e2v2_qk_proj_fwd_s3 /
+# e2v2_qk_proj_bwd_s3).  The stacked weight W [3, 4 hid, C] has the columns
+# [q_a | q_b | k_a | k_b] (hid each); pair p < 2 hid is (q_a, q_b) column p for p < hid, else
+# (k_a, k_b) column p - hid.
+
+def pair_col(p: int, ab: int, hid: int) -> int:
+    """Column of W holding the a- (ab = 0) or b-side (ab = 1) of pair p."""
+    if p < hid:
+        return hid + p if ab else p
+    return 2 * hid + p if ab else hid + p
+
+
+def qk_orders(hid: int):
+    """(forward, backward) column orders: the forward's packed column i is W column
+    fwd[i] (128-column tile t = a-sides of pairs 64 t .. +63, then their b-sides);
+    the kept y and the backward's K index s hold W column bwd[s]
+    (s = 16 (p // 8) + 8 ab + p % 8)."""
+    fwd = [pair_col(64 * (i // 128) + (i % 128) % 64, (i % 128) // 64, hid) for i in range(4 * hid)]
+    bwd = [0] * (4 * hid)
+    for p in range(2 * hid):
+        for ab in (0, 1):
+            bwd[16 * (p // 8) + 8 * ab + p % 8] = pair_col(p, ab, hid)
+    return fwd, bwd
+
+
+class QKPacks:
+    """Packed operands of the split Q/K projection: ``fwd`` (W in the forward order),
+    ``bias`` (in the same order), ``bwd`` ([W rows in the backward order ; Wv]^T per
+    l), hid, C and Cv."""
+    __slots__ = ("fwd", "bias", "bwd", "hid", "c", "cv")
+
+
+def qk_supported(hid: int, c: int, cv: int) -> bool:
+    return hid > 0 and hid % 64 == 0 and c > 0 and c % TILE_N == 0 and cv > 0 and cv % TILE_K == 0
+
+
+def pack_qk(W: torch.Tensor, bias: Optional[torch.Tensor], Wv: torch.Tensor) -> QKPacks:
+    """W [3, 4 hid, C] (stacked query and key weights), bias [4 hid] or None, Wv
+    [3, Cv, C] (the value projection, whose input gradient the backward adds)."""
+    W = W.detach().float()
+    Wv = Wv.detach().float()
+    hid, c, cv = W.shape[1] // 4, W.shape[2], Wv.shape[1]
+    if not qk_supported(hid, c, cv) or W.shape[0] != 3 or Wv.shape[0] != 3 or Wv.shape[2] != c:
+        raise ValueError(f"pack_qk: unsupported shapes W {tuple(W.shape)} Wv {tuple(Wv.shape)}")
+    fwd, bwd = qk_orders(hid)
+    fi = torch.as_tensor(fwd, device=W.device)
+    bi = torch.as_tensor(bwd, device=W.device)
+    P = QKPacks()
+    P.fwd = pack(W[:, fi, :].contiguous())
+    P.bias = None if bias is None else bias.detach().float()[fi].contiguous()
+    P.bwd = pack(torch.cat([W[:, bi, :], Wv], dim=1).contiguous(), transpose=True)
+    P.hid, P.c, P.cv = hid, c, cv
+    return P
+
+
+def qk_forward(x: torch.Tensor, P: QKPacks):
+    """(hq, hk [N, 3 hid], y [9, N, 4 hid] in the backward order) from x [9, N, C]."""
+    x = x.contiguous()
+    _, n, c = x.shape
+    y = x.new_empty(9, n, 4 * P.hid)
+    hq = x.new_empty(n, 3 * P.hid)
+    hk = x.new_empty(n, 3 * P.hid)
+    st = _lib.vp(torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.call("e2v2_qk_proj_fwd_s3", _lib.vp(x.data_ptr()), _lib.vp(P.fwd.buf.data_ptr()),
+              _lib.vp(0 if P.bias is None else P.bias.data_ptr()), _lib.vp(y.data_ptr()), _lib.vp(hq.data_ptr()),
+              _lib.vp(hk.data_ptr()), _lib.i32(n), _lib.i32(P.hid), _lib.i32(c), st)
+    return hq, hk, y
+
+
+def qk_backward(y: torch.Tensor, ghq: torch.Tensor, ghk: torch.Tensor, gv: Optional[torch.Tensor], P: QKPacks):
+    """gx [9, N, C] (with gv [9, N, Cv] W_v added when gv is given)."""
+    n = y.shape[1]
+    gx = y.new_empty(9, n, P.c)
+    ghq, ghk = ghq.contiguous(), ghk.contiguous()
+    gv = None if gv is None else gv.float().contiguous()
+    st = _lib.vp(torch.cuda.current_stream(y.device).cuda_stream)
+    _lib.call("e2v2_qk_proj_bwd_s3", _lib.vp(y.data_ptr()), _lib.vp(ghq.data_ptr()), _lib.vp(ghk.data_ptr()),
+              _lib.vp(P.bwd.buf.data_ptr()), _lib.vp(0 if gv is None else gv.data_ptr()), _lib.vp(gx.data_ptr()),
+              _lib.i32(n), _lib.i32(P.hid), _lib.i32(P.c), _lib.i32(P.cv), st)
+    return gx

@@ -272,17 +272,22 @@ class QKProjFn(torch.autograd.Function):
     m-contraction: x[9][N][C] -> hq, hk [N][3 hid] (before final_linear)."""
 
     @staticmethod
-    def forward(ctx, x, Wop, bias, lmax: int, hid: int, Wvop=None, bv=None):
+    def forward(ctx, x, Wop, bias, lmax: int, hid: int, Wvop=None, bv=None, s3=None):
         """Wop, Wvop: MRowWeight.  With the value projection's weight Wvop
         ([lmax+1, Cv, C]) and bias bv it also returns v = SO3_Linear(x) [9, N, Cv]
         (else None), so that the backward sums the two input gradients inside the
-        GEMMs."""
+        GEMMs.  s3: the split-GEMM packs of the same weights (gemm.QKPacks), which
+        take the fp32 projection when given."""
         x = x.contiguous()
         L2, N, C = x.shape
         W = Wop.w
-        fused = _qk_fused(x, Wop, Wvop, C, hid, lmax)
-        ctx.fused = fused
-        if fused:
+        fused = "s3" if s3 is not None and x.dtype == torch.float32 and lmax == 2 else _qk_fused(x, Wop, Wvop, C,
+                                                                                                   hid, lmax)
+        ctx.fused, ctx.s3 = fused, s3
+        if fused == "s3":
+            # split-GEMM projection, the m-contraction in its epilogue; y kept in the paired column order
+            hq, hk, y = s3gemm.qk_forward(x, s3)
+        elif fused:
             # projection GEMM with the m-contraction on its accumulators (HIP, MFMA);
             # the bf16 form rounds x while staging it and keeps y in bf16
             y = x.new_empty(L2, N, 4 * hid, dtype=BF16 if fused == "bf16" else torch.float32)
@@ -332,6 +337,8 @@ class QKProjFn(torch.autograd.Function):
         hid = ctx.hid
         ghq = torch.zeros(N, 3 * hid, device=y.device) if ghq is None else ghq.contiguous()
         ghk = torch.zeros(N, 3 * hid, device=y.device) if ghk is None else ghk.contiguous()
+        if ctx.fused == "s3":
+            return s3gemm.qk_backward(y, ghq, ghk, gv, ctx.s3), None, None, None, None, None, None, None
         if ctx.fused:
             # gy = the m-contraction's gradient, formed while the GEMM stages it; the
             # value projection's gradient gv W_v enters as further K stages
@@ -345,7 +352,7 @@ class QKProjFn(torch.autograd.Function):
                       _dp(ghk), _dp(bt), _lib.vp(gvc.data_ptr() if with_v else 0),
                       _lib.vp(bvt.data_ptr() if with_v else 0), _dp(gx), _lib.i32(N), _lib.i32(hid), _lib.i32(C),
                       _lib.i32(bvt.shape[2] if with_v else 0), _stream())
-            return gx, None, None, None, None, None, None
+            return gx, None, None, None, None, None, None, None
         gy = torch.empty_like(y)
         _lib.call("e2v2_pairdot_bwd", _dp(y), _dp(ghq), _dp(ghk), _dp(gy), _lib.i32(N), _lib.i32(hid), _stream())
         W = Wop.w
@@ -368,7 +375,7 @@ class QKProjFn(torch.autograd.Function):
                 for l in range(ctx.lmax + 1):
                     a, b = l * l, (l + 1) ** 2
                     _addmm_into(gx[a:b].view(-1, C), gv[a:b].view(-1, Cv), Wv[l], out=gx[a:b].view(-1, C))
-        return gx, None, None, None, None, None, None
+        return gx, None, None, None, None, None, None, None
 
 
 class SO2OutFn(torch.autograd.Function):
@@ -1080,6 +1087,21 @@ class E2AttentionArbOrder_sparse(nn.Module):
         w, b = cached(self, "qk", params, build)
         return mrow_weight(self, "qk", w, bf16, self.lmax), b
 
+    def qk_s3_packs(self):
+        """The split-GEMM packs of the Q/K projection (query and key weights, their
+        bias, and the sliced value projection whose input gradient the backward
+        adds), or None when the split GEMM does not apply (cached per version)."""
+        Wop, b = self.qk_weights(False)
+        wv, _ = self.value_weights_sliced()
+        W = Wop.w
+        if not (split_gemm_on() and W.is_cuda and W.dtype == torch.float32
+                and s3gemm.qk_supported(W.shape[1] // 4, W.shape[2], wv.shape[1])):
+            return None
+        pv = self.proj_value
+        params = (self.query_linear.weight, self.query_linear.weight2, self.query_linear.bias,
+                  self.key_linear.weight, self.key_linear.weight2, self.key_linear.bias, pv.weight, pv.bias)
+        return cached(self, "qk_s3", params, lambda: s3gemm.pack_qk(W, b, wv))
+
     def value_weights_sliced(self):
         """proj_value's weight and bias with the output channels in the attention
         kernels' slice order (cached per weight version)."""
@@ -1257,7 +1279,9 @@ class E2AttentionArbOrder_sparse(nn.Module):
         pv = self.proj_value  # its GEMMs run inside QKProjFn (one input gradient)
         wv, bv = self.value_weights_sliced()
         with record_function("query key linear function"):
-            hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight_sl", wv, bf16, pv.lmax), bv)
+            s3 = None if bf16 else self.qk_s3_packs()
+            hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight_sl", wv, bf16, pv.lmax), bv,
+                                       s3)
             q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
             k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         with record_function("rbf function-a"):   # fc_easy as a distance table, built once per weight version
