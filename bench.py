@@ -136,12 +136,19 @@ PROJ_FLOPS = {"e2v2_qk_proj_fwd": lambda N: 2.0 * 9 * N * 256 * 2048,
               "e2v2_qk_proj_bwd": lambda N: 2.0 * 9 * N * 256 * (2048 + 256)}
 PROJ_FLOPS["e2v2_qk_proj_fwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
 PROJ_FLOPS["e2v2_qk_proj_bwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
+PROJ_FLOPS["e2v2_qk_proj_fwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
+PROJ_FLOPS["e2v2_qk_proj_bwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
+# fp32 GEMMs on the split kernels execute six bf16 MFMA products per fp32 multiply-add
+SPLIT_PRODUCTS = 6
+SPLIT_ENTRIES = ("e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3", "e2v2_gemm_s3")
 
 KERNELS_OF = {"e2v2_attn_fwd": ["k_attn_fwd_sl"],
               "e2v2_attn_bwd": ["k_attn_bwd_row_sl", "k_attn_bwd_col_grp", "k_edge_part_sum"],
               "e2v2_deg_fwd": ["k_deg_fwd_sl"], "e2v2_deg_bwd": ["k_deg_bwd_sl", "k_edge_part_sum"],
               "e2v2_nbr_count": ["k_nbr_count"],
-              "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"]}
+              "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"],
+              "e2v2_qk_proj_fwd_s3": ["k_qk_s3_fwd"], "e2v2_qk_proj_bwd_s3": ["k_qk_s3_bwd"],
+              "e2v2_gemm_s3": ["k_gemm_s3"]}
 
 
 def expanded_nodes(nl) -> int:
@@ -298,7 +305,8 @@ def main():
     timer = _lib.KernelTimer(["e2v2_attn_fwd", "e2v2_attn_bwd",
                               "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill",
                               "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd", "e2v2_qk_proj_fwd_bf16",
-                              "e2v2_qk_proj_bwd_bf16"])
+                              "e2v2_qk_proj_bwd_bf16", "e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3",
+                              "e2v2_gemm_s3"])
     edges = []
     e_start = integ.e.sum().item() + integ.kinetic()
     _lib.set_timer(timer)
@@ -331,11 +339,16 @@ def main():
                        frac=round(b_alg / sec / 1e9 / HBM_PEAK_GBS, 4), impl_bytes_per_launch=b_imp,
                        impl_gbs=round(b_imp / sec / 1e9, 1), impl_frac=round(b_imp / sec / 1e9 / HBM_PEAK_GBS, 4),
                        impl_table_bytes_per_launch=b_tab)
-        elif k in PROJ_FLOPS:
-            tf = PROJ_FLOPS[k](N) / sec / 1e12
+        elif k in PROJ_FLOPS or k in SPLIT_ENTRIES:
+            fl = PROJ_FLOPS[k](N) if k in PROJ_FLOPS else v["work"] / v["count"]
+            tf = fl / sec / 1e12
             pk = BF16_PEAK_TFLOPS if k.endswith("_bf16") else FP32_PEAK_TFLOPS
-            ent.update(bound="mfma", flops_per_launch=PROJ_FLOPS[k](N), achieved_tflops=round(tf, 2),
-                       frac=round(tf / pk, 4))
+            ent.update(bound="mfma", flops_per_launch=fl, achieved_tflops=round(tf, 2), frac=round(tf / pk, 4))
+            if k in SPLIT_ENTRIES:
+                # fp32 work against the fp32 MFMA peak (frac); the bf16 MFMA work it executes against
+                # the bf16 peak (executed_frac, comparable with SQ_VALU_MFMA_BUSY)
+                ent.update(executed_bf16_tflops=round(SPLIT_PRODUCTS * tf, 2),
+                           executed_frac=round(SPLIT_PRODUCTS * tf / BF16_PEAK_TFLOPS, 4))
         per_kernel[k] = ent
     # headline: the library entry point with the largest total time, at its algorithmic work per launch
     name = max(stats.items(), key=lambda kv: kv[1]["total_ms"])[0]

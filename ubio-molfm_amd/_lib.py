@@ -115,6 +115,12 @@ class KernelTimer:
     def __init__(self, names):
         self.names = set(names)
         self.events = {n: [] for n in names}
+        self.work = {n: 0.0 for n in names}
+
+    def add_work(self, name, amount):
+        """Algorithmic work (e.g. FLOPs) of one timed call whose size varies per call."""
+        if name in self.work:
+            self.work[name] += amount
 
     def wrap(self, name, fn):
         import torch
@@ -135,7 +141,7 @@ class KernelTimer:
             if not evs:
                 continue
             ts = [a.elapsed_time(b) for a, b in evs]
-            out[n] = {"count": len(ts), "avg_ms": sum(ts) / len(ts), "total_ms": sum(ts)}
+            out[n] = {"count": len(ts), "avg_ms": sum(ts) / len(ts), "total_ms": sum(ts), "work": self.work[n]}
         return out
 
 

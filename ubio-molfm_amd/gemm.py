@@ -102,6 +102,8 @@ def gemm(a: torch.Tensor, pw: PackedWeight, out: torch.Tensor, widx: Optional[Se
     for b, i in enumerate(widx):
         g.widx[b] = int(i)
     _lib.call("e2v2_gemm_s3", _lib.C.byref(g), _lib.vp(torch.cuda.current_stream(a.device).cuda_stream))
+    if _lib._timer is not None:
+        _lib._timer.add_work("e2v2_gemm_s3", 2.0 * batch * m * pw.n * pw.k)
     return out
 
 
