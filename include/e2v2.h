@@ -101,6 +101,11 @@ int e2v2_nbr_count(const e2v2_nbr_plan* plan, int32_t* row_count, int32_t* row_p
 int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, int64_t n_edges, int max_row,
                   int32_t* tmp_col, int32_t* tmp_shift, float* tmp_dvec, float* tmp_dist, uint64_t* tmp_key,
                   int32_t* col, int32_t* shift, float* dvec, float* dist, hipStream_t s);
+/* Capacity build, for callers that size the edge arrays without reading the count back (the MD loop):
+ * after e2v2_nbr_count, clamp row_ptr to the first cap_edges edge slots and set stats[3] = 1 when the list
+ * needs more than cap_edges edges or a row longer than cap_row (then it is truncated and must be rebuilt);
+ * e2v2_nbr_fill is then called with n_edges = cap_edges, max_row = cap_row.  stats holds 4 ints. */
+int e2v2_nbr_cap(int32_t* row_ptr, int n_rows, int64_t cap_edges, int cap_row, int32_t* stats, hipStream_t s);
 /* keep the k nearest of each sorted row: phase 0 counts + scans (stats = {E', max}), phase 1 compacts */
 int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* cnt, int32_t* new_ptr, int32_t* stats,
                   const int32_t* col, const int32_t* shift, const float* dvec, const float* dist,
@@ -133,7 +138,8 @@ int e2v2_morton_keys(const float* pos, const int32_t* gid, const float* lo, cons
 int e2v2_cluster_slots(const int32_t* seg_ptr, int32_t n_seg, const int32_t* member, const int32_t* item_eid,
                        int32_t span, int32_t* slot_member, int32_t* slot_edge, int32_t* n_slots, hipStream_t s);
 /* key CSR: phase 0 -> edge_row, key_ptr, stats = {E, max column}; phase 1 -> key_eid (sorted by edge id;
-   columns of any length, no host check needed between the phases) */
+   columns of any length, no host check needed between the phases).  The edges are those below
+   min(n_edges, row_ptr[n_rows]) (the arrays may be sized for more, as in a capacity build). */
 int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int n_rows, int n_cols, int64_t n_edges,
                        int32_t* edge_row, int32_t* key_cnt, int32_t* key_ptr, int32_t* stats,
                        uint64_t* tmp_key, int32_t* key_eid, int phase, hipStream_t s);

@@ -181,6 +181,7 @@ def test_md_matches_oracle_nve_step(pkg, cuda):
     f = fn(x)
     for step in range(5):
         integ.step()
+        integ.sync()
         x, p, f = omd.nve_step(x, p, mass, f, fn, integ.dt, fixcom=True)
         dx = float((integ.x - x).abs().max()); dp = float((integ.p - p).abs().max())
         print(f"[md vs oracle step {step}] |dx|={dx:.2e} |dp|={dp:.2e}", flush=True)
@@ -188,3 +189,31 @@ def test_md_matches_oracle_nve_step(pkg, cuda):
     cm = (integ.m * integ.x).sum(0) / integ.m.sum()
     cm0 = (integ.m * torch.as_tensor(np.asarray(s["pos"], np.float64), device=cuda)).sum(0) / integ.m.sum()
     assert float((cm - cm0).abs().max()) < 1e-10 and float(integ.p.sum(0).abs().max()) < 1e-10
+
+
+def test_md_capacity_builds_match_exact_and_recover_from_overflow(pkg, cuda):
+    """The MD loop's capacity builds (edge arrays sized from the previous count,
+    counters checked one step later: no host readback per step) give bitwise the
+    trajectory of exact builds; a capacity too small for the list is detected at
+    the next step and that step recomputed with an exact build."""
+    from ubio_molfm_amd import md, systems
+    m, _ = _pair(cuda, seed=14)
+    s = systems.small_water(8, 6.2, seed=9)
+    ref = md.VelocityVerlet(m, s, cuda, dt_fs=1.0, T=300.0, seed=2, lagged=False)
+    lag = md.VelocityVerlet(m, s, cuda, dt_fs=1.0, T=300.0, seed=2)
+    small = md.VelocityVerlet(m, s, cuda, dt_fs=1.0, T=300.0, seed=2)
+    for k in range(6):
+        ref.step(); lag.step(); small.step()
+        if k == 1:
+            small.sync()
+            small.capacity = (small.n_edges - 10, small.capacity[1])      # the next build overflows
+        if k == 3:
+            small.sync()
+            small.capacity = (small.capacity[0], 8)                        # rows longer than 8 overflow
+    lag.sync(); small.sync()
+    print(f"[md capacity] edges {lag.edge_counts} redone {lag.redone} / {small.redone}", flush=True)
+    assert lag.last_nl.stats is not None and ref.last_nl.stats is None
+    assert torch.equal(ref.x, lag.x) and torch.equal(ref.p, lag.p) and torch.equal(ref.f, lag.f)
+    assert torch.equal(ref.x, small.x) and torch.equal(ref.p, small.p) and torch.equal(ref.f, small.f)
+    assert ref.edge_counts == lag.edge_counts == small.edge_counts
+    assert lag.redone == 0 and small.redone == 2

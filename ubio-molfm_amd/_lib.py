@@ -14,7 +14,7 @@ i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
 EXPORTS = [
     "e2v2_last_error", "e2v2_version", "e2v2_fill_i32", "e2v2_fill_f32", "e2v2_scan_i32",
-    "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_count_noalloc", "e2v2_nbr_fill", "e2v2_nbr_topk", "e2v2_csr_transpose", "e2v2_cluster_slots",
+    "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_count_noalloc", "e2v2_nbr_fill", "e2v2_nbr_cap", "e2v2_nbr_topk", "e2v2_csr_transpose", "e2v2_cluster_slots",
     "e2v2_morton_keys", "e2v2_radial_table_size", "e2v2_radial_table", "e2v2_radial_table_check",
     "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_attn_bwd_workspace", "e2v2_deg_fwd", "e2v2_deg_bwd",
     "e2v2_deg_bwd_workspace",

@@ -297,11 +297,14 @@ __global__ __launch_bounds__(64) void k_sort_rows(const int32_t* __restrict__ ro
   uint64_t* sk = seg_lds;
   int32_t* sv = reinterpret_cast<int32_t*>(seg_lds + cap);
   const int r = blockIdx.x;
-  const int b = row_ptr[r], n = row_ptr[r + 1] - b;
-  if (n == 0) return;
+  const int b = row_ptr[r], n_row = row_ptr[r + 1] - b, n = min(n_row, cap);
+  if (n_row == 0) return;
   segment_sort(key, b, n, sk, sv);
-  for (int t = threadIdx.x; t < n; t += blockDim.x) {
-    int src = b + sv[t], dst = b + t;
+  // A row longer than cap exists only in a capacity build that overflowed (the caller
+  // rebuilds the list): its first cap entries are sorted and the rest copied unsorted, so
+  // that every entry of the row is still one of its edges for the kernels that read it.
+  for (int t = threadIdx.x; t < n_row; t += blockDim.x) {
+    int src = t < n ? b + sv[t] : b + t, dst = b + t;
     col[dst] = tcol[src];
     shift[dst] = tshift[src];
     dvec[3 * dst] = tdv[3 * src];
@@ -311,6 +314,16 @@ __global__ __launch_bounds__(64) void k_sort_rows(const int32_t* __restrict__ ro
   }
 }
 
+// Capacity build: stats = {E, longest row} of the scan; rows are clamped to the
+// first cap_edges edge slots and stats[3] = 1 when the list needs more edges or a
+// longer row than the caller sized for (the list is then truncated).
+__global__ void k_cap_rows(int32_t* __restrict__ row_ptr, int n_rows, int64_t cap_edges, int cap_row,
+                           int32_t* __restrict__ stats) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0) stats[3] = ((int64_t)stats[0] > cap_edges || stats[1] > cap_row) ? 1 : 0;
+  if (i <= n_rows) row_ptr[i] = (int32_t)min((int64_t)row_ptr[i], cap_edges);
+}
+
 // edge -> row index
 __global__ void k_edge_rows(const int32_t* __restrict__ row_ptr, int n_rows, int32_t* __restrict__ edge_row) {
   int r = blockIdx.x * blockDim.x + threadIdx.x;
@@ -318,16 +331,20 @@ __global__ void k_edge_rows(const int32_t* __restrict__ row_ptr, int n_rows, int
   for (int e = row_ptr[r]; e < row_ptr[r + 1]; ++e) edge_row[e] = r;
 }
 
-__global__ void k_col_count(const int32_t* __restrict__ col, int64_t n_edges, int32_t* __restrict__ cnt) {
+// e_end (NULL: n_edges) bounds the edges on the device: the query CSR's row_ptr[n_rows],
+// which is below n_edges in a capacity build (arrays sized for more edges than exist)
+__global__ void k_col_count(const int32_t* __restrict__ col, int64_t n_edges, const int32_t* __restrict__ e_end,
+                            int32_t* __restrict__ cnt) {
   int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n_edges) return;
+  if (e >= n_edges || (e_end && e >= *e_end)) return;
   atomicAdd(&cnt[col[e]], 1);
 }
 
-__global__ void k_col_fill(const int32_t* __restrict__ col, int64_t n_edges, const int32_t* __restrict__ key_ptr,
-                           int32_t* __restrict__ cursor, uint64_t* __restrict__ tkey) {
+__global__ void k_col_fill(const int32_t* __restrict__ col, int64_t n_edges, const int32_t* __restrict__ e_end,
+                           const int32_t* __restrict__ key_ptr, int32_t* __restrict__ cursor,
+                           uint64_t* __restrict__ tkey) {
   int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n_edges) return;
+  if (e >= n_edges || (e_end && e >= *e_end)) return;
   int j = col[e];
   int slot = key_ptr[j] + atomicAdd(&cursor[j], 1);
   tkey[slot] = (uint64_t)e;
@@ -804,6 +821,17 @@ E2V2_API int e2v2_nbr_fill(const e2v2_nbr_plan* plan, const int32_t* row_ptr, in
   return 0;
 }
 
+E2V2_API int e2v2_nbr_cap(int32_t* row_ptr, int n_rows, int64_t cap_edges, int cap_row, int32_t* stats,
+                          hipStream_t s) {
+  E2V2_REQUIRE(row_ptr && stats && n_rows >= 0, "nbr_cap: null row_ptr / stats or negative row count");
+  E2V2_REQUIRE(cap_edges >= 0 && cap_edges < (1ll << 31) && cap_row > 0 && cap_row <= kMaxSeg,
+               "nbr_cap: capacity %lld edges / %d per row outside the supported range", (long long)cap_edges, cap_row);
+  hipLaunchKernelGGL(k_cap_rows, dim3(blocks_for(n_rows + 1, 256)), dim3(256), 0, s, row_ptr, n_rows, cap_edges,
+                     cap_row, stats);
+  E2V2_LAUNCHED("k_cap_rows");
+  return 0;
+}
+
 E2V2_API int e2v2_nbr_topk(const int32_t* row_ptr, int n_rows, int k, int32_t* cnt, int32_t* new_ptr, int32_t* stats,
                            const int32_t* col, const int32_t* shift, const float* dvec, const float* dist,
                            int32_t* ocol, int32_t* oshift, float* odv, float* od, int phase, hipStream_t s) {
@@ -858,7 +886,8 @@ E2V2_API int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int 
     int rc = e2v2_fill_i32(key_cnt, 0, n_cols, s);
     if (rc) return rc;
     if (n_edges > 0) {
-      hipLaunchKernelGGL(k_col_count, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, col, n_edges, key_cnt);
+      hipLaunchKernelGGL(k_col_count, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, col, n_edges,
+                         row_ptr + n_rows, key_cnt);
       E2V2_LAUNCHED("k_col_count");
     }
     hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, key_cnt, n_cols, key_ptr, stats);
@@ -868,8 +897,8 @@ E2V2_API int e2v2_csr_transpose(const int32_t* row_ptr, const int32_t* col, int 
   if (n_edges == 0) return 0;
   int rc = e2v2_fill_i32(key_cnt, 0, n_cols, s);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_col_fill, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, col, n_edges, key_ptr, key_cnt,
-                     tmp_key);
+  hipLaunchKernelGGL(k_col_fill, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, col, n_edges, row_ptr + n_rows,
+                     key_ptr, key_cnt, tmp_key);
   E2V2_LAUNCHED("k_col_fill");
   // columns of up to 256 edges sort in LDS (at liquid density and a 6 A cutoff a column
   // holds about 90), longer ones in place in global memory
@@ -925,7 +954,8 @@ E2V2_API int e2v2_segment_metadata(const int32_t* row_index, const int32_t* othe
   E2V2_REQUIRE(n_rows > 0, "segment_metadata: %lld edges but no row", (long long)n_edges);
   E2V2_REQUIRE(row_index && other_index && col_index && alpha_index && tmp_key, "segment_metadata: null pointer");
   if (int rc = e2v2_fill_i32(cnt, 0, n_rows, s)) return rc;
-  hipLaunchKernelGGL(k_col_fill, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, row_index, n_edges, row_ptr, cnt,
+  hipLaunchKernelGGL(k_col_fill, dim3(blocks_for(n_edges, 256)), dim3(256), 0, s, row_index, n_edges,
+                     (const int32_t*)nullptr, row_ptr, cnt,
                      tmp_key);
   E2V2_LAUNCHED("k_col_fill");
   const int cap = 256;

@@ -15,6 +15,16 @@ periodic cell the positions handed to the model are wrapped into the cell
 through fractional coordinates (a lattice translation per atom, so energy and
 forces are unchanged); the neighbour grid is then the cell's bounding box and
 the builder needs no bounding-box readback.
+
+No host readback per step: after the first (exact) neighbour build, each step
+builds its list into arrays sized from the previous count plus a margin (the
+capacity build of ``neighbors.build_neighbors``).  The build's counters (edge
+count, longest row, atom outside the grid box, overflow) are copied to pinned
+host memory without waiting, and checked when the next step starts, by which
+time the device has long finished that build; a step whose list overflowed is
+recomputed from its saved starting state with an exact build (bitwise the same
+result, since the capacity only pads the edge arrays).  ``sync()`` resolves the
+last step; until then the state after ``step()`` is provisional.
 """
 from __future__ import annotations
 
@@ -62,13 +72,20 @@ def wrappable(cell: np.ndarray, pbc) -> bool:
     return bool(np.all(np.asarray(pbc).reshape(3))) and abs(np.linalg.det(cell)) > 1e-9
 
 
-def wrap_positions(x: torch.Tensor, cell) -> torch.Tensor:
+def cell_matrices(cell, device):
+    """(A, A^-1) float64 on the device for the cell spanned by the rows of ``cell``
+    (the inverse taken on the host: no device solver and no host sync)."""
+    A = np.asarray(cell, np.float64).reshape(3, 3)
+    return (torch.as_tensor(A, device=device), torch.as_tensor(np.linalg.inv(A), device=device))
+
+
+def wrap_positions(x: torch.Tensor, cell=None, mats=None) -> torch.Tensor:
     """Positions mapped into the cell spanned by the rows of ``cell`` through
     fractional coordinates (frac - floor(frac)): each atom moves by a lattice
     vector, so every periodic pair distance is unchanged (triclinic cells
-    included)."""
-    A = torch.as_tensor(np.asarray(cell, np.float64).reshape(3, 3), device=x.device, dtype=torch.float64)
-    frac = x.to(torch.float64) @ torch.linalg.inv(A)
+    included).  mats: the cell's ``cell_matrices``, if already on the device."""
+    A, Ainv = cell_matrices(cell, x.device) if mats is None else mats
+    frac = x.to(torch.float64) @ Ainv
     return (frac - torch.floor(frac)) @ A
 
 
@@ -84,7 +101,10 @@ class VelocityVerlet:
     ``sysd``); ``fixcm`` applies the FixCom projections to the whole system, as
     the reference does for its one ``TorchAtoms`` object."""
 
-    def __init__(self, model, sysd, device, dt_fs=1.0, T=300.0, seed=0, fixcm=True, wrap=True):
+    # capacity of the next build: the last count plus this fraction and a fixed margin
+    CAP_FRAC, CAP_EDGES, CAP_ROW = 0.04, 4096, 64
+
+    def __init__(self, model, sysd, device, dt_fs=1.0, T=300.0, seed=0, fixcm=True, wrap=True, lagged=True):
         self.model = model
         self.sys = sysd
         self.dev = device
@@ -103,10 +123,17 @@ class VelocityVerlet:
         if self.wrap:
             bb = np.stack([cell_bounding_box(c) for c in self.cells], axis=1)     # [2, B, 3]
             self.grid_box = bb.astype(np.float32)
+            self.cell_mats = [cell_matrices(c, device) for c in self.cells]
         self.f = None
         self.e = None
         self.n_edges = 0
         self.last_nl = None
+        # the capacity build needs the cell's grid box (wrapped positions)
+        self.lagged = lagged and self.wrap and device.type == "cuda"
+        self.capacity = None          # (edges, longest row) of the next capacity build
+        self.pending = None           # (pinned counters, event, state before the step) of the last one
+        self.edge_counts = []         # edges of every step's build, in order (complete after sync())
+        self.redone = 0               # steps recomputed after an overflowing capacity build
 
     @property
     def v(self) -> torch.Tensor:
@@ -116,16 +143,47 @@ class VelocityVerlet:
         """float32 positions given to the model (wrapped copy for periodic cells)."""
         if not self.wrap:
             return x.float()
-        parts = [wrap_positions(x[self.ptr[g]:self.ptr[g + 1]], self.cells[g]) for g in range(len(self.ptr) - 1)]
+        parts = [wrap_positions(x[self.ptr[g]:self.ptr[g + 1]], mats=self.cell_mats[g]) for g in range(len(self.ptr) - 1)]
         return (parts[0] if len(parts) == 1 else torch.cat(parts)).float()
 
-    def forces_at(self, x: torch.Tensor):
-        """(energy per graph, raw model forces float64) at positions x."""
+    def forces_at(self, x: torch.Tensor, capacity=None):
+        """(energy per graph, raw model forces float64) at positions x; with
+        ``capacity`` the neighbour list is a capacity build whose counters the
+        caller checks (``self.last_nl.stats``)."""
+        kw = {} if capacity is None else {"nbr_capacity": capacity}
         e, f, nl = self.model.energy_forces_flat(self.model_positions(x), self.Z, self.ptr, self.cells, self.pbcs,
-                                                 grid_box=self.grid_box)
-        self.n_edges = nl.n_edges
+                                                 grid_box=self.grid_box, **kw)
+        if capacity is None:
+            self.n_edges = nl.n_edges
+            self._size_from(nl.n_edges, getattr(nl, "max_row", 0))
         self.last_nl = nl
         return e, f.double()
+
+    def _size_from(self, n_edges: int, longest: int):
+        self.capacity = (int(n_edges * (1 + self.CAP_FRAC)) + self.CAP_EDGES, min(longest + self.CAP_ROW, 4096))
+
+    def _resolve(self):
+        """Check the last capacity build (waits for that build only, not the step)."""
+        if self.pending is None:
+            return
+        host, ev, state = self.pending
+        self.pending = None
+        ev.synchronize()
+        E, longest, outside, overflow = (int(v) for v in host.tolist())
+        if outside or overflow:
+            # recompute the step from its starting state with an exact build
+            self.x, self.p, self.e, self.f = state
+            self.redone += 1
+            self._advance(None)
+            return
+        self.n_edges = E
+        self.edge_counts.append(E)
+        if E > self.capacity[0] - self.CAP_EDGES // 2 or longest > self.capacity[1] - self.CAP_ROW // 2:
+            self._size_from(E, longest)
+
+    def sync(self):
+        """Resolve the last step (after it the state is final)."""
+        self._resolve()
 
     def forces(self):
         return self.forces_at(self.x)
@@ -134,17 +192,26 @@ class VelocityVerlet:
         return 0.5 * float((self.p * self.p / self.m).sum())
 
     def step(self):
+        self._resolve()
         if self.f is None:
             self.e, self.f = self.forces()
+        self._advance(self.capacity if self.lagged else None)
+        return self.e
+
+    def _advance(self, capacity):
+        state = (self.x, self.p, self.e, self.f)
         m, dt, c1 = self.m, self.dt, 0.5 * self.dt
         f = fixcom_forces(self.f, m) if self.fixcm else self.f
         x_new = self.x + dt * (self.p / m + c1 * f / m)
         if self.fixcm:
             x_new = fixcom_positions(self.x, x_new, m)
-        e_new, f_new = self.forces_at(x_new)
+        e_new, f_new = self.forces_at(x_new, capacity)
+        if capacity is not None:
+            self.pending = (self.last_nl.stats_host, self.last_nl.stats_event, state)
+        else:
+            self.edge_counts.append(self.n_edges)
         fn = fixcom_forces(f_new, m) if self.fixcm else f_new
         p_new = ((x_new - self.x) / dt + c1 * fn / m) * m
         if self.fixcm:
             p_new = fixcom_momenta(p_new, m)
         self.x, self.p, self.e, self.f = x_new, p_new, e_new, f_new
-        return self.e

@@ -119,11 +119,12 @@ class E2FormerBackbone(nn.Module):
 
     # -- flat interface -------------------------------------------------------
     def forward_flat(self, pos: torch.Tensor, Z: torch.Tensor, graph_ptr, cell, pbc, charge=None,
-                     multiplicity=None, nl=None, reorder: bool = True, grid_box=None):
+                     multiplicity=None, nl=None, reorder: bool = True, grid_box=None, nbr_capacity=None):
         """pos [N,3] (may require grad), Z [N] on the GPU; graph_ptr/cell/pbc on the host.
         Returns (node_irreps [N,9,C], neighbour list, perm): rows of node_irreps and
         the neighbour list refer to atoms ``perm`` (Morton order within each graph;
-        identity when ``reorder`` is False).  grid_box: see ``build_neighbors``."""
+        identity when ``reorder`` is False).  grid_box, nbr_capacity (the capacity
+        build, no host readback): see ``build_neighbors``."""
         perm = None
         type_z, type_key, slot = self.type_slots(Z)
         if reorder and nl is None:
@@ -132,7 +133,7 @@ class E2FormerBackbone(nn.Module):
             slot = slot[perm]
         if nl is None:
             nl = build_neighbors(pos.detach(), graph_ptr, cell, pbc, self.max_radius, 1e-4, self.max_neighbors,
-                                 self.cells_per_direction, grid_box=grid_box)
+                                 self.cells_per_direction, grid_box=grid_box, capacity=nbr_capacity)
         dvec, dist = EdgeGeometryFn.apply(pos, nl)
         ctx = EdgeContext(nl, dvec, dist, slot.contiguous(), type_z, type_key, self.decoder.rbf, self.max_radius,
                           self.compute_bf16)
@@ -316,9 +317,9 @@ class MolfmAtomic(nn.Module):
         self.head = MDEnergyForceMultiHead(args)
 
     def energy_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None, nl=None,
-                    grid_box=None):
+                    grid_box=None, nbr_capacity=None):
         x, nl, _ = self.decoder.forward_flat(pos, Z, graph_ptr, cell, pbc, charge, multiplicity, nl,
-                                             grid_box=grid_box)
+                                             grid_box=grid_box, nbr_capacity=nbr_capacity)
         h = self.head.head_name(head)
         e_atom = self.head.energy_heads[h](x[0]).squeeze(-1)     # x is m-major [9, N, C]
         B = len(graph_ptr) - 1
@@ -330,9 +331,10 @@ class MolfmAtomic(nn.Module):
         return energy, nl
 
     def energy_forces_flat(self, pos, Z, graph_ptr, cell, pbc, head=None, charge=None, multiplicity=None,
-                           grid_box=None):
+                           grid_box=None, nbr_capacity=None):
         pos = pos.detach().float().requires_grad_(True)
-        energy, nl = self.energy_flat(pos, Z, graph_ptr, cell, pbc, head, charge, multiplicity, grid_box=grid_box)
+        energy, nl = self.energy_flat(pos, Z, graph_ptr, cell, pbc, head, charge, multiplicity, grid_box=grid_box,
+                                      nbr_capacity=nbr_capacity)
         forces = -torch.autograd.grad(energy, pos, torch.ones_like(energy))[0]
         return energy.detach(), forces, nl
 

@@ -16,6 +16,7 @@ component, img = pos_j + off, dvec = pos_i - img, d = sqrt((dx*dx + dy*dy) + dz*
 from __future__ import annotations
 
 import math
+from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Optional
 
@@ -88,6 +89,13 @@ class NeighborList:
     col_slot_edge: Optional[torch.Tensor] = None     # [E, col_span] int32
     col_n_slots: Optional[torch.Tensor] = None       # [ceil(N / col_span)] int32
     shift_ptr: Optional[np.ndarray] = None           # [B+1] rows of ``shifts`` per graph (host)
+    # capacity build (build_neighbors(capacity=...)): the edge arrays hold n_edges slots of which
+    # the first stats[0] are edges; stats [4] int32 on the device = {E, longest row, an atom outside
+    # the grid box, overflow}; the list is valid only when stats[2] == stats[3] == 0
+    stats: Optional[torch.Tensor] = None
+    # ... copied without waiting to pinned host memory (stats_host), complete once stats_event has
+    stats_host: Optional[torch.Tensor] = None
+    stats_event: Optional[object] = None
 
     def canonical(self):
         """(i, j, s) sorted lexicographically, plus dvec/dist in that order (numpy)."""
@@ -106,6 +114,59 @@ def _ptr(t: Optional[torch.Tensor]):
 
 def _vp(t: Optional[torch.Tensor]):
     return None if t is None or t.numel() == 0 else _lib.vp(t.data_ptr())
+
+
+_PLAN_TABLES: "OrderedDict" = OrderedDict()
+
+
+def _plan_tables(dev, graph_ptr, cells, pbcs, rc, cells_per_direction, bb):
+    """The plan's device tables (graph pointers, shift tables and offsets, bin
+    grids) and host sizes, built once per distinct input: an MD loop with a fixed
+    grid box reuses them (no host-to-device copy, hence no host sync, per build)."""
+    key = (str(dev), graph_ptr.tobytes(), cells.tobytes(), pbcs.tobytes(), float(rc), int(cells_per_direction),
+           np.asarray(bb, F32).tobytes())
+    hit = _PLAN_TABLES.get(key)
+    if hit is not None:
+        _PLAN_TABLES.move_to_end(key)
+        return hit
+    B = len(graph_ptr) - 1
+    shifts, sptr, periodic = [], [0], []
+    glo = np.zeros((B, 3), F32); gh = np.zeros((B, 3), F32); gdim = np.zeros((B, 3), np.int32)
+    base = np.zeros(B, np.int32)
+    nb = 0
+    h_min = F32(rc + BIN_MARGIN)
+    for g in range(B):
+        sh = shift_table(cells[g], pbcs[g], rc, cells_per_direction)
+        shifts.append(sh)
+        sptr.append(sptr[-1] + len(sh))
+        periodic.append(1 if pbcs[g].any() else 0)
+        if graph_ptr[g + 1] > graph_ptr[g]:
+            l, h = bb[0, g], bb[1, g]
+        else:
+            l, h = np.zeros(3, F32), np.zeros(3, F32)
+        ext = np.maximum(h - l, 0.0)
+        dims = np.maximum(1, np.floor(ext / h_min)).astype(np.int64)
+        while np.prod(dims) > (1 << 22):
+            dims = np.maximum(1, dims // 2)
+        glo[g] = l
+        gh[g] = np.maximum(ext / dims, h_min)
+        gdim[g] = dims
+        base[g] = nb
+        nb += int(np.prod(dims))
+    shifts_np = np.concatenate(shifts).astype(np.int32)
+    offs = np.concatenate([shift_offsets(s, cells[g]) for g, s in enumerate(shifts)]).astype(F32)
+    # the small tables in one host-to-device copy per type
+    ints = [graph_ptr.astype(np.int32), np.asarray(sptr, np.int32), np.asarray(periodic, np.int32),
+            gdim.reshape(-1), base, np.repeat(np.arange(B, dtype=np.int32), np.diff(graph_ptr))]
+    floats = [offs.reshape(-1), glo.reshape(-1), gh.reshape(-1)]
+    ti = torch.as_tensor(np.concatenate(ints).astype(np.int32), device=dev)
+    tf = torch.as_tensor(np.concatenate(floats).astype(F32), device=dev)
+    tensors = (ti, tf) + tuple(torch.split(ti, [len(a) for a in ints])) + tuple(torch.split(tf, [len(a) for a in floats]))
+    out = (tensors, shifts_np, sptr, nb, len(offs))
+    _PLAN_TABLES[key] = out
+    while len(_PLAN_TABLES) > 16:
+        _PLAN_TABLES.popitem(last=False)
+    return out
 
 
 def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
@@ -138,46 +199,14 @@ def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float 
         bb = torch.stack([lo, hi]).cpu().numpy()
     else:
         bb = np.zeros((2, B, 3), F32)
-    shifts, sptr, periodic = [], [0], []
-    glo = np.zeros((B, 3), F32); gh = np.zeros((B, 3), F32); gdim = np.zeros((B, 3), np.int32)
-    base = np.zeros(B, np.int32)
-    nb = 0
-    h_min = F32(rc + BIN_MARGIN)
-    for g in range(B):
-        sh = shift_table(cells[g], pbcs[g], rc, cells_per_direction)
-        shifts.append(sh)
-        sptr.append(sptr[-1] + len(sh))
-        periodic.append(1 if pbcs[g].any() else 0)
-        if graph_ptr[g + 1] > graph_ptr[g]:
-            l, h = bb[0, g], bb[1, g]
-        else:
-            l, h = np.zeros(3, F32), np.zeros(3, F32)
-        ext = np.maximum(h - l, 0.0)
-        dims = np.maximum(1, np.floor(ext / h_min)).astype(np.int64)
-        while np.prod(dims) > (1 << 22):
-            dims = np.maximum(1, dims // 2)
-        glo[g] = l
-        gh[g] = np.maximum(ext / dims, h_min)
-        gdim[g] = dims
-        base[g] = nb
-        nb += int(np.prod(dims))
-    shifts_np = np.concatenate(shifts).astype(np.int32)
-    offs = np.concatenate([shift_offsets(s, cells[g]) for g, s in enumerate(shifts)]).astype(F32)
-    # the plan's small tables in one host-to-device copy per type
-    ints = [graph_ptr.astype(np.int32), np.asarray(sptr, np.int32), np.asarray(periodic, np.int32),
-            gdim.reshape(-1), base, np.repeat(np.arange(B, dtype=np.int32), np.diff(graph_ptr))]
-    floats = [offs.reshape(-1), glo.reshape(-1), gh.reshape(-1)]
-    ti = torch.as_tensor(np.concatenate(ints).astype(np.int32), device=dev)
-    tf = torch.as_tensor(np.concatenate(floats).astype(F32), device=dev)
-    ti_parts = torch.split(ti, [len(a) for a in ints])
-    t_gptr, t_sptr, t_per, t_dim, t_base, atom_graph = ti_parts
-    t_off, t_lo, t_h = torch.split(tf, [len(a) for a in floats])
+    tabs = _plan_tables(dev, graph_ptr, cells, pbcs, rc, cells_per_direction, bb)
+    (ti, tf, t_gptr, t_sptr, t_per, t_dim, t_base, atom_graph, t_off, t_lo, t_h), shifts_np, sptr, nb, n_off = tabs
     keep = dict(pos=pos, ti=ti, tf=tf)
     ws = [None] * 5
     if workspace:
         keep.update(atom_bin=torch.empty(max(N, 1), **i32), bin_count=torch.empty(nb, **i32),
                     bin_start=torch.empty(nb + 1, **i32), bin_atoms=torch.empty(max(N, 1), **i32),
-                    stats=torch.zeros(3, **i32))
+                    stats=torch.zeros(4, **i32))
         ws = [keep[k].data_ptr() for k in ("atom_bin", "bin_count", "bin_start", "bin_atoms", "stats")]
     inc = None
     if src_include is not None:
@@ -185,7 +214,7 @@ def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float 
             raise ValueError(f"src_include must be a [{N}] tensor on {dev}")
         keep["src_include"] = src_include.to(torch.uint8).contiguous()
         inc = keep["src_include"].data_ptr() if N else None
-    plan = _lib.NbrPlan(N, B, nb, len(offs), rc, rmin, pos.data_ptr(), atom_graph.data_ptr(), t_gptr.data_ptr(),
+    plan = _lib.NbrPlan(N, B, nb, n_off, rc, rmin, pos.data_ptr(), atom_graph.data_ptr(), t_gptr.data_ptr(),
                         t_sptr.data_ptr(), t_per.data_ptr(), t_off.data_ptr(), t_lo.data_ptr(), t_h.data_ptr(),
                         t_dim.data_ptr(), t_base.data_ptr(), *ws, inc)
     return plan, keep, shifts_np, sptr
@@ -193,7 +222,8 @@ def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float 
 
 def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
                     max_neighbors: Optional[int] = None, cells_per_direction: int = 4,
-                    grid_box=None, src_include: Optional[torch.Tensor] = None) -> NeighborList:
+                    grid_box=None, src_include: Optional[torch.Tensor] = None,
+                    capacity: Optional[tuple] = None) -> NeighborList:
     """pos [N,3] fp32 on the GPU (graphs contiguous); graph_ptr [B+1], cells
     [B,3,3], pbcs [B,3] on the host.  grid_box [2,B,3] (optional, host): per-graph
     (lo, hi) corners of the bin grid that contain every atom, e.g. the cell of
@@ -202,7 +232,14 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     the supplied box is detected on the device (read back with the edge count)
     and the list is rebuilt with the bounding boxes.  src_include ([N] bool on
     the GPU, or None): only marked atoms are edge sources (every atom is still a
-    query row)."""
+    query row).
+
+    capacity = (edges, longest row): build into arrays of that many edge slots with
+    no host readback at all (the kernels bound the edges on the device); the
+    returned list carries ``stats`` = {E, longest row, atom outside the grid box,
+    overflow} on the device, and the caller must check (later, asynchronously) that
+    entries 2 and 3 are zero, else rebuild: the list is then truncated.  Needs a
+    grid box, no max_neighbors."""
     if not pos.is_cuda:
         raise RuntimeError("build_neighbors runs on the GPU only (pos must be a CUDA/HIP tensor)")
     dev = pos.device
@@ -221,7 +258,20 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     row_ptr = torch.empty(N + 1, **i32)
     _lib.call("e2v2_nbr_count", _lib.C.byref(plan), _lib.vp(row_count.data_ptr()), _lib.vp(row_ptr.data_ptr()),
               _lib.vp(stream))
-    E, max_row, outside = (int(x) for x in stats.cpu())
+    if capacity is not None:
+        if grid_box is None or max_neighbors is not None or N == 0:
+            raise ValueError("a capacity build needs a grid box, no max_neighbors and at least one atom")
+        E, max_row = int(capacity[0]), int(capacity[1])
+        _lib.call("e2v2_nbr_cap", _lib.vp(row_ptr.data_ptr()), _lib.i32(N), _lib.i64(E), _lib.i32(max_row),
+                  _lib.vp(stats.data_ptr()), _lib.vp(stream))
+        # the counters are final here: start their copy to the host now, not after the evaluation
+        stats_host = torch.empty(4, dtype=torch.int32, pin_memory=True)
+        stats_host.copy_(stats, non_blocking=True)
+        stats_event = torch.cuda.Event()
+        stats_event.record(torch.cuda.current_stream(dev))
+        outside = 0
+    else:
+        E, max_row, outside = (int(x) for x in stats[:3].cpu())
     if outside:
         if grid_box is None:
             raise RuntimeError("neighbour build: an atom lies outside its own bounding box")
@@ -256,16 +306,19 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     edge_row = torch.empty(E, **i32)
     key_cnt = torch.empty(max(N, 1), **i32)
     key_ptr = torch.empty(N + 1, **i32)
+    tstats = torch.empty(2, **i32)        # the key scan's {E, longest column} (informational)
     _lib.call("e2v2_csr_transpose", _lib.vp(row_ptr.data_ptr()), _lib.vp(_ptr(col)), _lib.i32(N), _lib.i32(N),
               _lib.i64(E), _lib.vp(_ptr(edge_row)), _lib.vp(key_cnt.data_ptr()), _lib.vp(key_ptr.data_ptr()),
-              _lib.vp(stats.data_ptr()), None, None, _lib.i32(0), _lib.vp(stream))
+              _lib.vp(tstats.data_ptr()), None, None, _lib.i32(0), _lib.vp(stream))
     key_eid = torch.empty(E, **i32)
     _lib.call("e2v2_csr_transpose", _lib.vp(row_ptr.data_ptr()), _lib.vp(_ptr(col)), _lib.i32(N), _lib.i32(N),
               _lib.i64(E), _lib.vp(_ptr(edge_row)), _lib.vp(key_cnt.data_ptr()), _lib.vp(key_ptr.data_ptr()),
-              _lib.vp(stats.data_ptr()), _lib.vp(tkey.data_ptr()), _lib.vp(_ptr(key_eid)), _lib.i32(1),
+              _lib.vp(tstats.data_ptr()), _lib.vp(tkey.data_ptr()), _lib.vp(_ptr(key_eid)), _lib.i32(1),
               _lib.vp(stream))
     nl = NeighborList(N, E, row_ptr, col, sh, torch.as_tensor(shifts_np), dvec, dist, edge_row, key_ptr, key_eid,
                       max_row, shift_ptr=np.asarray(sptr, np.int64))
+    if capacity is not None:
+        nl.stats, nl.stats_host, nl.stats_event = stats, stats_host, stats_event
     if N > 0 and E > 0:
         nl.col_span = COL_SPAN
         nl.col_slot_member, nl.col_slot_edge, nl.col_n_slots = cluster_slots(key_ptr, N, edge_row, key_eid,
