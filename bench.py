@@ -348,16 +348,20 @@ def main():
                        frac=round(b_alg / sec / 1e9 / HBM_PEAK_GBS, 4), impl_bytes_per_launch=b_imp,
                        impl_gbs=round(b_imp / sec / 1e9, 1), impl_frac=round(b_imp / sec / 1e9 / HBM_PEAK_GBS, 4),
                        impl_table_bytes_per_launch=b_tab)
-        elif k in PROJ_FLOPS or k in SPLIT_ENTRIES:
+        elif k in SPLIT_ENTRIES:
+            # fp32 GEMMs executed as six bf16 MFMA products each: the executed bf16 rate against the bf16
+            # peak (frac, comparable with SQ_VALU_MFMA_BUSY), and the fp32 work rate beside the fp32 peak
             fl = PROJ_FLOPS[k](N) if k in PROJ_FLOPS else v["work"] / v["count"]
             tf = fl / sec / 1e12
+            ent.update(bound="mfma", flops_per_launch=fl, executed_flops_per_launch=SPLIT_PRODUCTS * fl,
+                       achieved_tflops=round(SPLIT_PRODUCTS * tf, 2), peak_tflops=BF16_PEAK_TFLOPS,
+                       frac=round(SPLIT_PRODUCTS * tf / BF16_PEAK_TFLOPS, 4),
+                       fp32_equivalent_tflops=round(tf, 2), fp32_equivalent_over_fp32_peak=round(tf / FP32_PEAK_TFLOPS, 4))
+        elif k in PROJ_FLOPS:
+            tf = PROJ_FLOPS[k](N) / sec / 1e12
             pk = BF16_PEAK_TFLOPS if k.endswith("_bf16") else FP32_PEAK_TFLOPS
-            ent.update(bound="mfma", flops_per_launch=fl, achieved_tflops=round(tf, 2), frac=round(tf / pk, 4))
-            if k in SPLIT_ENTRIES:
-                # fp32 work against the fp32 MFMA peak (frac); the bf16 MFMA work it executes against
-                # the bf16 peak (executed_frac, comparable with SQ_VALU_MFMA_BUSY)
-                ent.update(executed_bf16_tflops=round(SPLIT_PRODUCTS * tf, 2),
-                           executed_frac=round(SPLIT_PRODUCTS * tf / BF16_PEAK_TFLOPS, 4))
+            ent.update(bound="mfma", flops_per_launch=PROJ_FLOPS[k](N), achieved_tflops=round(tf, 2),
+                       peak_tflops=pk, frac=round(tf / pk, 4))
         per_kernel[k] = ent
     # headline: the library entry point with the largest total time, at its algorithmic work per launch
     name = max(stats.items(), key=lambda kv: kv[1]["total_ms"])[0]
@@ -367,7 +371,7 @@ def main():
                 "frac": ent["frac"], "traffic": traffic_from_profile(name, bf16, args.config), "kernel": name,
                 "algorithmic_bytes_per_launch": ent["bytes_per_launch"], "expanded_nodes": M}
     else:
-        pk = BF16_PEAK_TFLOPS if (bf16 or name.endswith("_bf16")) else FP32_PEAK_TFLOPS
+        pk = ent.get("peak_tflops", FP32_PEAK_TFLOPS)
         roof = {"bound": "mfma", "achieved": ent.get("achieved_tflops"), "peak": pk, "unit": "TFLOP/s",
                 "frac": ent.get("frac"), "traffic": traffic_from_profile(name, bf16, args.config), "kernel": name}
     # stack: whole evaluation against the MFMA roofline; HBM-bound kernels time-weighted
