@@ -453,8 +453,9 @@ int e2v2_ln_silu_bwd(const float* x, const float* g, const float* b, const float
  * Each fp32 operand x is split as x0 + x1 + x2 (bf16, round to nearest even, exact remainders) and a product is
  * the sum of the six piece products of order <= 2, accumulated in fp32: an fp32 GEMM to within a few units of
  * fp32 rounding (measured against float64: below the error of the fp32 MFMA GEMM of the same operands).
- *   c[b][i][j] = sum_k a[b][i][k] W_{widx[b]}[j][k] (+ bias[j] for b < bias_batches) (+ r[b][i][j])
- * a: fp32, row stride lda (lda >= k, lda % 4 == 0, 16-byte aligned), batch stride a_bs (elements);
+ *   c[b][i][j] = sum_k a[b][i][k] W_{widx[b]}[j][k] (+ bias[b bias_bs + j] for b < bias_batches) (+ r[b][i][j])
+ * a: fp32, row stride lda (lda >= k, lda % 4 == 0, 16-byte aligned), batch b at a + b a_bs (elements; any
+ * distance, so two separate matrices of the same layout form a batch);
  * b: n_w weights packed by e2v2_gemm_pack; c (and r, which may equal c): fp32 with row / batch strides.
  * Requires n % 128 == 0, k % 16 == 0, 1 <= batch <= 16, 0 <= widx[b] < n_w <= 16. */
 typedef struct {
@@ -467,6 +468,7 @@ typedef struct {
   const float* r;
   int64_t ldr, r_bs;
   const float* bias;
+  int64_t bias_bs;      /* elements between the bias vectors of consecutive batches (0: one shared vector) */
   int bias_batches;
   int m, n, k, batch;
   int widx[16];

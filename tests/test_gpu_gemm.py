@@ -150,3 +150,38 @@ def test_qk_proj_split(pkg, cuda, n, with_v, with_bias):
     print(f"[qk_proj s3] n={n} y {e_y:.2e} hq {e_q:.2e} hk {e_k:.2e} gx {e_g:.2e}", flush=True)
     assert e_y < 2e-5 and e_q < 2e-5 and e_k < 2e-5
     assert e_g < 1e-4
+
+
+@pytest.mark.parametrize("n", [1, 700])
+def test_qk_heads_batched_split(pkg, cuda, n):
+    """The query and key final_linear stacks (Linear 1536->512, LayerNorm, SiLU,
+    Linear 512->1024) run as two-batch split GEMMs: outputs and input gradients
+    against the two stacks evaluated separately in float64."""
+    import copy
+    from ubio_molfm_amd import modules
+    torch.manual_seed(11)
+    print(f"[qk heads s3] n={n}", flush=True)
+    mk = lambda: torch.nn.Sequential(torch.nn.Linear(1536, 512), torch.nn.LayerNorm(512), torch.nn.SiLU(),
+                                     torch.nn.Linear(512, 1024))
+    fq, fk = mk(), mk()
+    with torch.no_grad():                      # LayerNorm affine away from its (1, 0) init
+        for f in (fq, fk):
+            f[1].weight.uniform_(0.5, 1.5)
+            f[1].bias.uniform_(-0.5, 0.5)
+    fq, fk = fq.to(cuda), fk.to(cuda)
+    P = modules.head_pair_packs(fq, fk, fq)
+    assert P is not None
+    hq = torch.randn(n, 1536, device=cuda, requires_grad=True)
+    hk = torch.randn(n, 1536, device=cuda, requires_grad=True)
+    q, k = modules.QKHeadsS3Fn.apply(hq, hk, P)
+    gq, gk = torch.randn_like(q), torch.randn_like(k)
+    gxq, gxk = torch.autograd.grad((q * gq).sum() + (k * gk).sum(), (hq, hk))
+    fqd, fkd = copy.deepcopy(fq).double(), copy.deepcopy(fk).double()
+    hqd = hq.detach().double().requires_grad_(True)
+    hkd = hk.detach().double().requires_grad_(True)
+    qd, kd = fqd(hqd), fkd(hkd)
+    gqd, gkd = torch.autograd.grad((qd * gq.double()).sum() + (kd * gk.double()).sum(), (hqd, hkd))
+    rel = lambda a, b: float((a.double() - b).norm() / (b.norm() + 1e-30))
+    errs = [rel(q, qd.detach()), rel(k, kd.detach()), rel(gxq, gqd), rel(gxk, gkd)]
+    print(f"[qk heads s3] n={n} q {errs[0]:.2e} k {errs[1]:.2e} gq {errs[2]:.2e} gk {errs[3]:.2e}", flush=True)
+    assert max(errs[:2]) < 2e-6 and max(errs[2:]) < 1e-5

@@ -79,7 +79,7 @@ class DegArgs(C.Structure):
 
 class GemmArgs(C.Structure):
     _fields_ = [("a", vp), ("lda", i64), ("a_bs", i64), ("b", vp), ("n_w", i32), ("c", vp), ("ldc", i64), ("c_bs", i64),
-                ("r", vp), ("ldr", i64), ("r_bs", i64), ("bias", vp), ("bias_batches", i32),
+                ("r", vp), ("ldr", i64), ("r_bs", i64), ("bias", vp), ("bias_bs", i64), ("bias_batches", i32),
                 ("m", i32), ("n", i32), ("k", i32), ("batch", i32), ("widx", i32 * 16)]
 
 

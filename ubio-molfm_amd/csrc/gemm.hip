@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int col = nt * kGN + 32 * j + (lane & 31);
-    const float bv = with_bias ? G.bias[col] : 0.f;
+    const float bv = with_bias ? G.bias[(size_t)bi * G.bias_bs + col] : 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = row0 + wv * 32 + acc_row(r, lane);

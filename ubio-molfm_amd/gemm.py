@@ -68,40 +68,63 @@ def _as3(t: torch.Tensor) -> torch.Tensor:
     return t.unsqueeze(0) if t.dim() == 2 else t
 
 
-def gemm(a: torch.Tensor, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] = None,
+def _batch_view(a):
+    """(base pointer, row stride, batch stride, batch, m, k) of an A operand given as a tensor
+    [batch, m, k] / [m, k] or as a list of same-layout 2-D tensors (batch b at base + b * bs)."""
+    if isinstance(a, (list, tuple)):
+        t0 = a[0]
+        for t in a:
+            if (t.dim() != 2 or t.shape != t0.shape or t.stride() != t0.stride() or t.dtype != torch.float32
+                    or t.stride(1) != 1 or t.stride(0) % 4 or t.data_ptr() % 16):
+                raise ValueError("gemm: batch matrices must share shape and a 16-byte aligned row layout")
+        steps = {(a[b + 1].data_ptr() - a[b].data_ptr()) for b in range(len(a) - 1)}
+        if len(steps) > 1 or any(d % 4 for d in steps):
+            raise ValueError("gemm: batch matrices must be evenly spaced in memory")
+        bs = steps.pop() // 4 if steps else 0
+        return t0.data_ptr(), t0.stride(0), bs, len(a), t0.shape[0], t0.shape[1]
+    a3 = _as3(a)
+    if a3.stride(2) != 1 or a3.stride(1) % 4 or a3.data_ptr() % 16:
+        a3 = a3.contiguous()
+    return a3.data_ptr(), a3.stride(1), a3.stride(0), a3.shape[0], a3.shape[1], a3.shape[2]
+
+
+def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] = None,
          bias: Optional[torch.Tensor] = None, bias_batches: int = 1, res: Optional[torch.Tensor] = None):
     """out[b] = a[b] W_{widx[b]}^T (+ bias for b < bias_batches) (+ res[b]).
-    a [batch, m, k] or [m, k] fp32 (rows may be strided, k contiguous), out and
-    res [batch, m, n] (res may be out)."""
-    a3, o3 = _as3(a), _as3(out)
+    a [batch, m, k] or [m, k] fp32 (rows may be strided, k contiguous), or a list of
+    same-layout [m, k] matrices; out and res [batch, m, n] (res may be out); bias [n]
+    (shared) or [batch, n] (one per batch)."""
+    o3 = _as3(out)
     r3 = None if res is None else _as3(res)
-    batch, m, k = a3.shape
-    if k != pw.k or o3.shape != (batch, m, pw.n) or a3.dtype != torch.float32 or o3.dtype != torch.float32:
-        raise ValueError(f"gemm: a {tuple(a3.shape)} / out {tuple(o3.shape)} do not fit W [{pw.n}, {pw.k}]")
-    if a3.stride(2) != 1 or o3.stride(2) != 1 or (r3 is not None and (r3.shape != o3.shape or r3.stride(2) != 1)):
+    keep = a    # the operand stays referenced until the launch is enqueued
+    a_ptr, lda, a_bs, batch, m, k = _batch_view(a)
+    if k != pw.k or o3.shape != (batch, m, pw.n) or o3.dtype != torch.float32:
+        raise ValueError(f"gemm: a [{batch}, {m}, {k}] / out {tuple(o3.shape)} do not fit W [{pw.n}, {pw.k}]")
+    if o3.stride(2) != 1 or (r3 is not None and (r3.shape != o3.shape or r3.stride(2) != 1)):
         raise ValueError("gemm: operands need a contiguous last dimension")
-    if a3.stride(1) % 4 or a3.data_ptr() % 16:
-        a3 = a3.contiguous()
     widx = list(range(batch)) if widx is None else list(widx)
     if len(widx) != batch or batch > MAX_BATCH or any(not 0 <= i < pw.n_w for i in widx):
         raise ValueError(f"gemm: weight index {widx} for {pw.n_w} weights")
     if m == 0:
         return out
     g = _lib.GemmArgs()
-    g.a, g.lda, g.a_bs = a3.data_ptr(), a3.stride(1), a3.stride(0)
+    g.a, g.lda, g.a_bs = a_ptr, lda, a_bs
     g.b, g.n_w = pw.buf.data_ptr(), pw.n_w
     g.c, g.ldc, g.c_bs = o3.data_ptr(), o3.stride(1), o3.stride(0)
     if r3 is not None:
         g.r, g.ldr, g.r_bs = r3.data_ptr(), r3.stride(1), r3.stride(0)
     if bias is not None:
-        bias = bias.detach().reshape(-1)
-        if bias.numel() != pw.n or bias.dtype != torch.float32 or not bias.is_contiguous():
-            raise ValueError("gemm: bias must be a contiguous fp32 [n]")
-        g.bias, g.bias_batches = bias.data_ptr(), int(bias_batches)
+        bias = bias.detach()
+        per_batch = bias.dim() == 2
+        if (bias.shape[-1] != pw.n or bias.dtype != torch.float32 or not bias.is_contiguous()
+                or (per_batch and bias.shape[0] < min(bias_batches, batch))):
+            raise ValueError("gemm: bias must be a contiguous fp32 [n] or [batch, n]")
+        g.bias, g.bias_bs, g.bias_batches = bias.data_ptr(), (pw.n if per_batch else 0), int(bias_batches)
     g.m, g.n, g.k, g.batch = m, pw.n, pw.k, batch
     for b, i in enumerate(widx):
         g.widx[b] = int(i)
-    _lib.call("e2v2_gemm_s3", _lib.C.byref(g), _lib.vp(torch.cuda.current_stream(a.device).cuda_stream))
+    _lib.call("e2v2_gemm_s3", _lib.C.byref(g), _lib.vp(torch.cuda.current_stream(out.device).cuda_stream))
+    del keep
     if _lib._timer is not None:
         _lib._timer.add_work("e2v2_gemm_s3", 2.0 * batch * m * pw.n * pw.k)
     return out

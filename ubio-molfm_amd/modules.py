@@ -520,6 +520,74 @@ class LNSiLUFn(torch.autograd.Function):
         return gx, None, None, None
 
 
+class QKHeadsS3Fn(torch.autograd.Function):
+    """final_linear of the query and of the key SO3_Linear2Scalar_e2former
+    (module_utils.py:2230-2233: Linear(3 hid -> hid) -> LayerNorm -> SiLU ->
+    Linear(hid -> out)) for both at once on the split GEMM: each Linear is one
+    launch with the two heads as batches (per-head weights and biases), which fills
+    twice the tiles of two separate launches.  Input gradients only."""
+
+    @staticmethod
+    def forward(ctx, hq, hk, P):
+        hq, hk = hq.contiguous(), hk.contiguous()
+        N = hq.shape[0]
+        h1 = hq.new_empty(2, N, P["p1f"].n)
+        s3gemm.gemm([hq, hk], P["p1f"], h1, [0, 1], bias=P["b1"], bias_batches=2)
+        a = torch.empty_like(h1)
+        st = hq.new_empty(2, N, 2)
+        for b in range(2):
+            g, be, eps = P["ln"][b]
+            _lib.call("e2v2_ln_silu_fwd", _dp(h1[b]), _dp(g), _dp(be), _dp(a[b]), _dp(st[b]), _lib.i32(N),
+                      _lib.i32(h1.shape[2]), _lib.f32(eps), _stream())
+        out = hq.new_empty(2, N, P["p2f"].n)
+        s3gemm.gemm(a, P["p2f"], out, [0, 1], bias=P["b2"], bias_batches=2)
+        ctx.save_for_backward(h1, st)
+        ctx.P = P
+        return out[0], out[1]
+
+    @staticmethod
+    def backward(ctx, gq, gk):
+        h1, st = ctx.saved_tensors
+        P = ctx.P
+        N = h1.shape[1]
+        gq = torch.zeros(N, P["p2f"].n, device=h1.device) if gq is None else gq.float().contiguous()
+        gk = torch.zeros(N, P["p2f"].n, device=h1.device) if gk is None else gk.float().contiguous()
+        ga = torch.empty_like(h1)
+        s3gemm.gemm([gq, gk], P["p2b"], ga, [0, 1])
+        gh1 = torch.empty_like(h1)
+        for b in range(2):
+            g, be, _ = P["ln"][b]
+            _lib.call("e2v2_ln_silu_bwd", _dp(h1[b]), _dp(g), _dp(be), _dp(st[b]), _dp(ga[b]), _dp(gh1[b]),
+                      _lib.i32(N), _lib.i32(h1.shape[2]), _stream())
+        gh = h1.new_empty(2, N, P["p1f"].k)
+        s3gemm.gemm(gh1, P["p1b"], gh, [0, 1])
+        return gh[0], gh[1], None
+
+
+def head_pair_packs(fq: nn.Sequential, fk: nn.Sequential, owner):
+    """Operands of QKHeadsS3Fn for two final_linear stacks (Linear, LayerNorm,
+    SiLU, Linear) of the same shapes: each Linear's two weights stacked and packed
+    for the forward and (transposed) for the input gradient, the biases as
+    [2, n], the LayerNorm parameters per head.  Cached on ``owner`` per weight
+    version; None when the split GEMM does not apply."""
+    w1, w2 = fq[0].weight, fq[3].weight
+    if not (split_gemm_on() and w1.is_cuda and w1.dtype == torch.float32
+            and all(s3gemm.supported(*w.shape) and s3gemm.supported(*w.shape[::-1]) for w in (w1, w2))):
+        return None
+    params = [p for f in (fq, fk) for i in (0, 1, 3) for p in (f[i].weight, f[i].bias)]
+
+    def build():
+        W1 = torch.stack([fq[0].weight.detach(), fk[0].weight.detach()]).float().contiguous()
+        W2 = torch.stack([fq[3].weight.detach(), fk[3].weight.detach()]).float().contiguous()
+        ln = [(f[1].weight.detach().float().contiguous(), f[1].bias.detach().float().contiguous(),
+               float(f[1].eps)) for f in (fq, fk)]
+        return {"p1f": s3gemm.pack(W1), "p1b": s3gemm.pack(W1, transpose=True),
+                "b1": torch.stack([fq[0].bias.detach(), fk[0].bias.detach()]).float().contiguous(),
+                "p2f": s3gemm.pack(W2), "p2b": s3gemm.pack(W2, transpose=True),
+                "b2": torch.stack([fq[3].bias.detach(), fk[3].bias.detach()]).float().contiguous(), "ln": ln}
+    return cached(owner, "head_pair_s3", params, build)
+
+
 def _ln_silu(x, ln: nn.LayerNorm):
     return LNSiLUFn.apply(x, ln.weight.detach().float().contiguous(), ln.bias.detach().float().contiguous(),
                           float(ln.eps))
@@ -1102,6 +1170,11 @@ class E2AttentionArbOrder_sparse(nn.Module):
                   self.key_linear.weight, self.key_linear.weight2, self.key_linear.bias, pv.weight, pv.bias)
         return cached(self, "qk_s3", params, lambda: s3gemm.pack_qk(W, b, wv))
 
+    def qk_head_packs(self):
+        """Split-GEMM packs of the query and key final_linear (cached per version),
+        or None when the split GEMM does not apply."""
+        return head_pair_packs(self.query_linear.final_linear, self.key_linear.final_linear, self)
+
     def value_weights_sliced(self):
         """proj_value's weight and bias with the output channels in the attention
         kernels' slice order (cached per weight version)."""
@@ -1282,8 +1355,13 @@ class E2AttentionArbOrder_sparse(nn.Module):
             s3 = None if bf16 else self.qk_s3_packs()
             hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight_sl", wv, bf16, pv.lmax), bv,
                                        s3)
-            q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
-            k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
+            heads = None if bf16 else self.qk_head_packs()
+            if heads is not None:
+                q, k = QKHeadsS3Fn.apply(hq, hk, heads)
+                q, k = q.reshape(N, H, -1), k.reshape(N, H, -1)
+            else:
+                q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
+                k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         with record_function("rbf function-a"):   # fc_easy as a distance table, built once per weight version
             table = self._radial.get([self._attn_profile()], self.target_embedding, self.source_embedding,
                                      ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="attn")
