@@ -474,6 +474,12 @@ typedef struct {
   int widx[16];
 } e2v2_gemm_args;
 int e2v2_gemm_s3(const e2v2_gemm_args* args, hipStream_t s);
+/* Up to four independent GEMMs (each as e2v2_gemm_s3, with its own shapes, operands and packed weight) in one
+ * launch: the groups' tiles share the GPU instead of running one small launch after another; groups are
+ * dispatched in the order given (put the longest k first).  Used for the per-degree GEMMs of forward_linear +
+ * proj_first (so2_tensor_product.py:276-290, e2former.py:433) and their input gradients, which replace three
+ * launches of 160-800 tiles. */
+int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hipStream_t s);
 /* Pack n_w weights W_w[j][k] = w[w w_stride + j ld_n + k ld_k] (j < n, k < k; so W or W^T of a row-major matrix
  * without a copy) into e2v2_gemm_packed_bytes(n_w, n, k) bytes at packed (16-byte aligned); the bytes needed,
  * or -1 for an unsupported shape. */

@@ -87,3 +87,18 @@ def test_split_gemm_host_checks(pkg):
     assert lib.e2v2_gemm_s3(_lib.C.byref(g), None) != 0 and b"widx[1]" in lib.e2v2_last_error()
     g.widx[1], g.n = 0, 100
     assert lib.e2v2_gemm_s3(_lib.C.byref(g), None) != 0 and b"multiple of 128" in lib.e2v2_last_error()
+
+
+def test_grouped_gemm_host_checks(pkg):
+    """e2v2_gemm_s3_grouped takes 1 .. 4 groups and checks each group as
+    e2v2_gemm_s3 does, on the host, before any HIP call."""
+    from ubio_molfm_amd import _lib
+    lib = _lib.load()
+    arr = (_lib.GemmArgs * 4)()
+    for g in arr:
+        g.a = g.b = g.c = 16                 # never dereferenced: the checks fail first
+        g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w = 64, 128, 10, 128, 64, 1, 1
+    assert lib.e2v2_gemm_s3_grouped(arr, 0, None) != 0 and b"groups" in lib.e2v2_last_error()
+    assert lib.e2v2_gemm_s3_grouped(arr, 5, None) != 0 and b"groups" in lib.e2v2_last_error()
+    arr[2].k = 40
+    assert lib.e2v2_gemm_s3_grouped(arr, 3, None) != 0 and b"multiple of 16" in lib.e2v2_last_error()

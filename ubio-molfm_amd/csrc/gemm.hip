@@ -181,12 +181,14 @@ __device__ __forceinline__ void kloop(const char* lds, int stage_bytes, int nks,
   }
 }
 
-__global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+__device__ __forceinline__ int gemm_tiles(const e2v2_gemm_args& G) {
+  return G.batch * ((G.m + kGM - 1) / kGM) * (G.n / kGN);
+}
+
+// One 128 x 128 output tile (batch-major, then row tile, then column tile).
+__device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, char* lds) {
   const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
-  const int n_mt = (G.m + kGM - 1) / kGM, n_nt = G.n / kGN, n_tiles = G.batch * n_mt * n_nt;
-  const int tile = xcd_row(blockIdx.x, n_tiles);
-  if (tile >= n_tiles) return;
+  const int n_mt = (G.m + kGM - 1) / kGM, n_nt = G.n / kGN;
   const int nt = tile % n_nt, mt = (tile / n_nt) % n_mt, bi = tile / (n_nt * n_mt);
   const int row0 = mt * kGM, nks = G.k / kGK;
   const __amdgpu_buffer_rsrc_t ar = rows_rsrc(G.a + (size_t)bi * G.a_bs, row0, G.m, (int)G.lda);
@@ -224,6 +226,40 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
         if (rb) v += rb[(size_t)row * G.ldr + col];
         cb[(size_t)row * G.ldc + col] = v;
       }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  const int n_tiles = gemm_tiles(G);
+  const int tile = xcd_row(blockIdx.x, n_tiles);
+  if (tile >= n_tiles) return;
+  gemm_tile(G, tile, lds);
+}
+
+// Independent GEMMs in one launch: group g owns workgroups block0[g] ..
+// block0[g + 1] - 1 (xcd_grid of its tile count, in the order given, so the
+// caller puts the longest tiles first), its tiles spread over the XCDs as in a
+// launch of its own.  The group is selected with constant indices so that its
+// arguments stay in the kernel-argument segment.
+constexpr int kGGroups = 4;
+struct GemmGroups {
+  e2v2_gemm_args g[kGGroups];
+  int block0[kGGroups + 1];
+  int n;
+};
+
+__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp(GemmGroups P) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  const int b = blockIdx.x;
+#pragma unroll
+  for (int gi = 0; gi < kGGroups; ++gi) {
+    if (gi < P.n && b >= P.block0[gi] && b < P.block0[gi + 1]) {
+      const int n_tiles = gemm_tiles(P.g[gi]);
+      const int tile = xcd_row(b - P.block0[gi], n_tiles);
+      if (tile < n_tiles) gemm_tile(P.g[gi], tile, lds);
+      return;
     }
   }
 }
@@ -434,10 +470,9 @@ E2V2_API int e2v2_gemm_pack(const float* w, int64_t ld_n, int64_t ld_k, int64_t 
   return 0;
 }
 
-E2V2_API int e2v2_gemm_s3(const e2v2_gemm_args* g, hipStream_t s) {
-  using namespace e2v2;
-  E2V2_REQUIRE(g, "gemm_s3: null arguments");
-  const e2v2_gemm_args& G = *g;
+namespace e2v2 {
+namespace {
+int check_gemm_args(const e2v2_gemm_args& G) {
   E2V2_REQUIRE(G.batch > 0 && G.batch <= 16, "gemm_s3: batch=%d (1 .. 16)", G.batch);
   E2V2_REQUIRE(G.m >= 0 && G.n > 0 && G.n % kGN == 0 && G.k > 0 && G.k % kGK == 0,
                "gemm_s3: m=%d, n=%d (multiple of %d), k=%d (multiple of %d)", G.m, G.n, kGN, G.k, kGK);
@@ -450,10 +485,40 @@ E2V2_API int e2v2_gemm_s3(const e2v2_gemm_args* g, hipStream_t s) {
   E2V2_REQUIRE(G.n_w > 0 && G.n_w <= 16, "gemm_s3: n_w=%d (1 .. 16)", G.n_w);
   for (int b = 0; b < G.batch; ++b)
     E2V2_REQUIRE(G.widx[b] >= 0 && G.widx[b] < G.n_w, "gemm_s3: widx[%d]=%d outside 0 .. %d", b, G.widx[b], G.n_w - 1);
+  return 0;
+}
+int host_tiles(const e2v2_gemm_args& G) { return G.batch * ((G.m + kGM - 1) / kGM) * (G.n / kGN); }
+}  // namespace
+}  // namespace e2v2
+
+E2V2_API int e2v2_gemm_s3(const e2v2_gemm_args* g, hipStream_t s) {
+  using namespace e2v2;
+  E2V2_REQUIRE(g, "gemm_s3: null arguments");
+  const e2v2_gemm_args& G = *g;
+  if (int rc = check_gemm_args(G)) return rc;
   if (G.m == 0) return 0;
-  const int tiles = G.batch * ((G.m + kGM - 1) / kGM) * (G.n / kGN);
-  hipLaunchKernelGGL(k_gemm_s3, dim3(xcd_grid(tiles)), dim3(kGT), 0, s, G);
+  hipLaunchKernelGGL(k_gemm_s3, dim3(xcd_grid(host_tiles(G))), dim3(kGT), 0, s, G);
   E2V2_LAUNCHED("k_gemm_s3");
+  return 0;
+}
+
+E2V2_API int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hipStream_t s) {
+  using namespace e2v2;
+  E2V2_REQUIRE(groups && n_groups >= 1 && n_groups <= kGGroups, "gemm_s3_grouped: %d groups (1 .. %d)", n_groups,
+               kGGroups);
+  GemmGroups P{};
+  P.block0[0] = 0;
+  for (int i = 0; i < n_groups; ++i) {
+    if (int rc = check_gemm_args(groups[i])) return rc;
+    P.g[i] = groups[i];
+    P.block0[i + 1] = P.block0[i] + xcd_grid(host_tiles(groups[i]));
+    E2V2_REQUIRE(P.block0[i + 1] >= P.block0[i], "gemm_s3_grouped: too many tiles");
+  }
+  for (int i = n_groups; i < kGGroups; ++i) P.block0[i + 1] = P.block0[n_groups];
+  P.n = n_groups;
+  if (P.block0[n_groups] == 0) return 0;
+  hipLaunchKernelGGL(k_gemm_s3_grp, dim3(P.block0[n_groups]), dim3(kGT), 0, s, P);
+  E2V2_LAUNCHED("k_gemm_s3_grp");
   return 0;
 }
 

@@ -88,15 +88,10 @@ def _batch_view(a):
     return a3.data_ptr(), a3.stride(1), a3.stride(0), a3.shape[0], a3.shape[1], a3.shape[2]
 
 
-def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] = None,
-         bias: Optional[torch.Tensor] = None, bias_batches: int = 1, res: Optional[torch.Tensor] = None):
-    """out[b] = a[b] W_{widx[b]}^T (+ bias for b < bias_batches) (+ res[b]).
-    a [batch, m, k] or [m, k] fp32 (rows may be strided, k contiguous), or a list of
-    same-layout [m, k] matrices; out and res [batch, m, n] (res may be out); bias [n]
-    (shared) or [batch, n] (one per batch)."""
+def _args(a, pw: PackedWeight, out: torch.Tensor, widx=None, bias=None, bias_batches: int = 1, res=None):
+    """(e2v2_gemm_args, fp32 work) of one GEMM (None for an empty one); checks the operands."""
     o3 = _as3(out)
     r3 = None if res is None else _as3(res)
-    keep = a    # the operand stays referenced until the launch is enqueued
     a_ptr, lda, a_bs, batch, m, k = _batch_view(a)
     if k != pw.k or o3.shape != (batch, m, pw.n) or o3.dtype != torch.float32:
         raise ValueError(f"gemm: a [{batch}, {m}, {k}] / out {tuple(o3.shape)} do not fit W [{pw.n}, {pw.k}]")
@@ -106,7 +101,7 @@ def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] =
     if len(widx) != batch or batch > MAX_BATCH or any(not 0 <= i < pw.n_w for i in widx):
         raise ValueError(f"gemm: weight index {widx} for {pw.n_w} weights")
     if m == 0:
-        return out
+        return None, 0.0
     g = _lib.GemmArgs()
     g.a, g.lda, g.a_bs = a_ptr, lda, a_bs
     g.b, g.n_w = pw.buf.data_ptr(), pw.n_w
@@ -123,11 +118,51 @@ def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] =
     g.m, g.n, g.k, g.batch = m, pw.n, pw.k, batch
     for b, i in enumerate(widx):
         g.widx[b] = int(i)
+    return g, 2.0 * batch * m * pw.n * pw.k
+
+
+def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] = None,
+         bias: Optional[torch.Tensor] = None, bias_batches: int = 1, res: Optional[torch.Tensor] = None):
+    """out[b] = a[b] W_{widx[b]}^T (+ bias for b < bias_batches) (+ res[b]).
+    a [batch, m, k] or [m, k] fp32 (rows may be strided, k contiguous), or a list of
+    same-layout [m, k] matrices; out and res [batch, m, n] (res may be out); bias [n]
+    (shared) or [batch, n] (one per batch)."""
+    keep = a    # the operand stays referenced until the launch is enqueued
+    g, work = _args(a, pw, out, widx, bias, bias_batches, res)
+    if g is None:
+        return out
     _lib.call("e2v2_gemm_s3", _lib.C.byref(g), _lib.vp(torch.cuda.current_stream(out.device).cuda_stream))
     del keep
     if _lib._timer is not None:
-        _lib._timer.add_work("e2v2_gemm_s3", 2.0 * batch * m * pw.n * pw.k)
+        _lib._timer.add_work("e2v2_gemm_s3", work)
     return out
+
+
+MAX_GROUPS = 4
+
+
+def gemm_grouped(problems):
+    """Up to four independent GEMMs in one launch (``e2v2_gemm_s3_grouped``):
+    ``problems`` is a sequence of dicts with the arguments of :func:`gemm`
+    (a, pw, out and optionally widx, bias, bias_batches, res).  Put the problems
+    with the longest k first: their tiles are dispatched first."""
+    if not 0 < len(problems) <= MAX_GROUPS:
+        raise ValueError(f"gemm_grouped: {len(problems)} problems (1 .. {MAX_GROUPS})")
+    keep = [p["a"] for p in problems]
+    arr = (_lib.GemmArgs * MAX_GROUPS)()
+    n, work, dev = 0, 0.0, problems[0]["out"].device
+    for p in problems:
+        g, w = _args(p["a"], p["pw"], p["out"], p.get("widx"), p.get("bias"), p.get("bias_batches", 1),
+                     p.get("res"))
+        if g is not None:
+            arr[n] = g
+            n += 1
+            work += w
+    if n:
+        _lib.call("e2v2_gemm_s3_grouped", arr, _lib.i32(n), _lib.vp(torch.cuda.current_stream(dev).cuda_stream))
+        if _lib._timer is not None:
+            _lib._timer.add_work("e2v2_gemm_s3_grouped", work)
+    del keep
 
 
 # ---------------------------------------------------------------------------------------------

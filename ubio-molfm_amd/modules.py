@@ -396,18 +396,21 @@ class SO2OutFn(torch.autograd.Function):
         O = Wc[0][3].shape[1]
         y = so2.new_empty(9, N, O, dtype=torch.float32)
         split = all(e[5] is not None for e in Wc) and so2.dtype == torch.float32
+        problems = []
         for (l3, cnt, start, W, _, PF, _) in Wc:
             K = W.shape[0]
             A = so2[start * N:(start + (2 * l3 + 1) * K) * N].view(-1, K)
             a, b = l3 * l3, (l3 + 1) ** 2
             if split:
-                s3gemm.gemm(A, PF, y[a:b].view(-1, O), bias=bias if l3 == 0 else None,
-                            res=None if res is None else res[a:b].view(-1, O))
+                problems.append({"a": A, "pw": PF, "out": y[a:b].view(-1, O), "bias": bias if l3 == 0 else None,
+                                 "res": None if res is None else res[a:b].view(-1, O)})
             elif res is not None:
                 _addmm_into(res[a:b].view(-1, O), A, W, out=y[a:b].view(-1, O))
             else:
                 _mm_into(A, W, out=y[a:b].view(-1, O))
-        if not split:
+        if split:                                # one launch, the longest k first
+            s3gemm.gemm_grouped(sorted(problems, key=lambda p: -p["pw"].k))
+        else:
             y[0].add_(bias)
         ctx.has_res = res is not None
         ctx.Wc, ctx.N = Wc, N
@@ -421,14 +424,17 @@ class SO2OutFn(torch.autograd.Function):
         O = gy.shape[2]
         gso2 = gy.new_empty(ctx.shape, dtype=ctx.so2_dtype)
         split = all(e[6] is not None for e in ctx.Wc) and ctx.so2_dtype == torch.float32
+        problems = []
         for (l3, cnt, start, _, WT, _, PB) in ctx.Wc:
             K = WT.shape[1]
             a, b = l3 * l3, (l3 + 1) ** 2
             dst = gso2[start * N:(start + (2 * l3 + 1) * K) * N].view(-1, K)
             if split:
-                s3gemm.gemm(gy[a:b].view(-1, O), PB, dst)
+                problems.append({"a": gy[a:b].view(-1, O), "pw": PB, "out": dst})
             else:
                 _mm_into(gy[a:b].view(-1, O), WT, out=dst)
+        if split:                                # one launch, the most tiles first
+            s3gemm.gemm_grouped(sorted(problems, key=lambda p: -p["out"].numel()))
         return gso2, (gy if ctx.has_res else None), None, None, None
 
 
