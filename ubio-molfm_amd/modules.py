@@ -526,6 +526,39 @@ class LNSiLUFn(torch.autograd.Function):
         return gx, None, None, None
 
 
+def _heads_tail(h1, P):
+    """LayerNorm + SiLU of each head's first Linear output h1 [2, N, hid] and the
+    second Linear (one two-batch launch): (out [2, N, n_out], LayerNorm stats)."""
+    N = h1.shape[1]
+    a = torch.empty_like(h1)
+    st = h1.new_empty(2, N, 2)
+    for b in range(2):
+        g, be, eps = P["ln"][b]
+        _lib.call("e2v2_ln_silu_fwd", _dp(h1[b]), _dp(g), _dp(be), _dp(a[b]), _dp(st[b]), _lib.i32(N),
+                  _lib.i32(h1.shape[2]), _lib.f32(eps), _stream())
+    out = h1.new_empty(2, N, P["p2f"].n)
+    s3gemm.gemm(a, P["p2f"], out, [0, 1], bias=P["b2"], bias_batches=2)
+    return out, st
+
+
+def _heads_backward(h1, st, gq, gk, P):
+    """Input gradients [2, N, 3 hid] of the two final_linear stacks given the
+    output gradients gq, gk [N, n_out] (None: zero)."""
+    N = h1.shape[1]
+    gq = torch.zeros(N, P["p2f"].n, device=h1.device) if gq is None else gq.float().contiguous()
+    gk = torch.zeros(N, P["p2f"].n, device=h1.device) if gk is None else gk.float().contiguous()
+    ga = torch.empty_like(h1)
+    s3gemm.gemm([gq, gk], P["p2b"], ga, [0, 1])
+    gh1 = torch.empty_like(h1)
+    for b in range(2):
+        g, be, _ = P["ln"][b]
+        _lib.call("e2v2_ln_silu_bwd", _dp(h1[b]), _dp(g), _dp(be), _dp(st[b]), _dp(ga[b]), _dp(gh1[b]),
+                  _lib.i32(N), _lib.i32(h1.shape[2]), _stream())
+    gh = h1.new_empty(2, N, P["p1f"].k)
+    s3gemm.gemm(gh1, P["p1b"], gh, [0, 1])
+    return gh
+
+
 class QKHeadsS3Fn(torch.autograd.Function):
     """final_linear of the query and of the key SO3_Linear2Scalar_e2former
     (module_utils.py:2230-2233: Linear(3 hid -> hid) -> LayerNorm -> SiLU ->
@@ -536,17 +569,9 @@ class QKHeadsS3Fn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hq, hk, P):
         hq, hk = hq.contiguous(), hk.contiguous()
-        N = hq.shape[0]
-        h1 = hq.new_empty(2, N, P["p1f"].n)
+        h1 = hq.new_empty(2, hq.shape[0], P["p1f"].n)
         s3gemm.gemm([hq, hk], P["p1f"], h1, [0, 1], bias=P["b1"], bias_batches=2)
-        a = torch.empty_like(h1)
-        st = hq.new_empty(2, N, 2)
-        for b in range(2):
-            g, be, eps = P["ln"][b]
-            _lib.call("e2v2_ln_silu_fwd", _dp(h1[b]), _dp(g), _dp(be), _dp(a[b]), _dp(st[b]), _lib.i32(N),
-                      _lib.i32(h1.shape[2]), _lib.f32(eps), _stream())
-        out = hq.new_empty(2, N, P["p2f"].n)
-        s3gemm.gemm(a, P["p2f"], out, [0, 1], bias=P["b2"], bias_batches=2)
+        out, st = _heads_tail(h1, P)
         ctx.save_for_backward(h1, st)
         ctx.P = P
         return out[0], out[1]
@@ -554,20 +579,39 @@ class QKHeadsS3Fn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gq, gk):
         h1, st = ctx.saved_tensors
-        P = ctx.P
-        N = h1.shape[1]
-        gq = torch.zeros(N, P["p2f"].n, device=h1.device) if gq is None else gq.float().contiguous()
-        gk = torch.zeros(N, P["p2f"].n, device=h1.device) if gk is None else gk.float().contiguous()
-        ga = torch.empty_like(h1)
-        s3gemm.gemm([gq, gk], P["p2b"], ga, [0, 1])
-        gh1 = torch.empty_like(h1)
-        for b in range(2):
-            g, be, _ = P["ln"][b]
-            _lib.call("e2v2_ln_silu_bwd", _dp(h1[b]), _dp(g), _dp(be), _dp(st[b]), _dp(ga[b]), _dp(gh1[b]),
-                      _lib.i32(N), _lib.i32(h1.shape[2]), _stream())
-        gh = h1.new_empty(2, N, P["p1f"].k)
-        s3gemm.gemm(gh1, P["p1b"], gh, [0, 1])
+        gh = _heads_backward(h1, st, gq, gk, ctx.P)
         return gh[0], gh[1], None
+
+
+class AttnProjS3Fn(torch.autograd.Function):
+    """The attention's node projections on the split GEMMs, fp32: the query / key
+    SO3_Linear2Scalar_e2former (module_utils.py:2198-2266) with its final_linear
+    for both (QKHeadsS3Fn) and the value SO3_Linear (e2former.py:300-303).  The
+    value GEMM shares a launch with the heads' first Linear, which alone fills
+    too few tiles to occupy the GPU; the backward folds the value gradient into
+    the projection's backward GEMM.  Returns q, k [N, H D] and v [9, N, Cv]."""
+
+    @staticmethod
+    def forward(ctx, x, s3, P, Wvop, bv):
+        x = x.contiguous()
+        N = x.shape[1]
+        hq, hk, y = s3gemm.qk_forward(x, s3)
+        h1 = x.new_empty(2, N, P["p1f"].n)
+        v = x.new_empty(x.shape[0], N, Wvop.w.shape[1])
+        s3gemm.gemm_grouped([
+            {"a": [hq, hk], "pw": P["p1f"], "out": h1, "widx": [0, 1], "bias": P["b1"], "bias_batches": 2},
+            {"a": x, "pw": Wvop.s3f(), "out": v, "widx": _m_degrees(Wvop.w.shape[0] - 1), "bias": bv}])
+        out, st = _heads_tail(h1, P)
+        ctx.save_for_backward(y, h1, st)
+        ctx.s3, ctx.P = s3, P
+        return out[0], out[1], v
+
+    @staticmethod
+    def backward(ctx, gq, gk, gv):
+        y, h1, st = ctx.saved_tensors
+        gh = _heads_backward(h1, st, gq, gk, ctx.P)
+        gx = s3gemm.qk_backward(y, gh[0], gh[1], None if gv is None else gv.contiguous(), ctx.s3)
+        return gx, None, None, None, None
 
 
 def head_pair_packs(fq: nn.Sequential, fk: nn.Sequential, owner):
@@ -1359,13 +1403,17 @@ class E2AttentionArbOrder_sparse(nn.Module):
         wv, bv = self.value_weights_sliced()
         with record_function("query key linear function"):
             s3 = None if bf16 else self.qk_s3_packs()
-            hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, mrow_weight(pv, "weight_sl", wv, bf16, pv.lmax), bv,
-                                       s3)
+            Wvop = mrow_weight(pv, "weight_sl", wv, bf16, pv.lmax)
             heads = None if bf16 else self.qk_head_packs()
-            if heads is not None:
+            if s3 is not None and heads is not None and Wvop.split_ok():
+                q, k, v = AttnProjS3Fn.apply(x, s3, heads, Wvop, bv)
+                q, k = q.reshape(N, H, -1), k.reshape(N, H, -1)
+            elif heads is not None:
+                hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, Wvop, bv, s3)
                 q, k = QKHeadsS3Fn.apply(hq, hk, heads)
                 q, k = q.reshape(N, H, -1), k.reshape(N, H, -1)
             else:
+                hq, hk, v = QKProjFn.apply(x, W, b, self.lmax, hid, Wvop, bv, s3)
                 q = self.query_linear.head(hq, bf16).reshape(N, H, -1)
                 k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         with record_function("rbf function-a"):   # fc_easy as a distance table, built once per weight version
