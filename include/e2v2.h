@@ -480,6 +480,13 @@ int e2v2_gemm_s3(const e2v2_gemm_args* args, hipStream_t s);
  * proj_first (so2_tensor_product.py:276-290, e2former.py:433) and their input gradients, which replace three
  * launches of 160-800 tiles. */
 int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hipStream_t s);
+/* e2v2_gemm_s3 with the activation of Gate_s3 (module_utils.py:2694-2746) applied to A as it is read, so that
+ * the second Linear of FeedForwardNetwork_s3 (module_utils.py:2755-2797) takes the gate's inputs instead of its
+ * output: batch 0's operand is silu(s[i][kk]) k1 (kk < k; args->a is not read for it), batch b >= 1's is
+ * a[b][i][kk] sigmoid(s[i][k widx[b] + kk]) k2, with s the gate logits [m][ld_s] (16-byte aligned, ld_s % 4 == 0,
+ * k (widx[b] + 1) <= ld_s).  The products are those of the gate kernel (e2v2_gate_fwd), so the result equals that
+ * kernel followed by e2v2_gemm_s3. */
+int e2v2_gemm_s3_gated(const e2v2_gemm_args* args, const float* s, int64_t ld_s, float k1, float k2, hipStream_t st);
 /* Pack n_w weights W_w[j][k] = w[w w_stride + j ld_n + k ld_k] (j < n, k < k; so W or W^T of a row-major matrix
  * without a copy) into e2v2_gemm_packed_bytes(n_w, n, k) bytes at packed (16-byte aligned); the bytes needed,
  * or -1 for an unsupported shape. */

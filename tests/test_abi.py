@@ -102,3 +102,19 @@ def test_grouped_gemm_host_checks(pkg):
     assert lib.e2v2_gemm_s3_grouped(arr, 5, None) != 0 and b"groups" in lib.e2v2_last_error()
     arr[2].k = 40
     assert lib.e2v2_gemm_s3_grouped(arr, 3, None) != 0 and b"multiple of 16" in lib.e2v2_last_error()
+
+
+def test_gated_gemm_host_checks(pkg):
+    """e2v2_gemm_s3_gated checks the gate logits' layout against the batches'
+    weight indices on the host, before any HIP call."""
+    from ubio_molfm_amd import _lib
+    lib = _lib.load()
+    g = _lib.GemmArgs()
+    g.a = g.b = g.c = 16                 # never dereferenced: the checks fail first
+    g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w = 64, 128, 10, 128, 64, 3, 3
+    g.widx[0], g.widx[1], g.widx[2] = 0, 1, 2
+    f = _lib.C.c_float
+    assert lib.e2v2_gemm_s3_gated(_lib.C.byref(g), _lib.C.c_void_p(16), _lib.C.c_int64(128), f(1.0), f(1.0),
+                                  None) != 0 and b"past ld_s" in lib.e2v2_last_error()
+    assert lib.e2v2_gemm_s3_gated(_lib.C.byref(g), _lib.C.c_void_p(0), _lib.C.c_int64(192), f(1.0), f(1.0),
+                                  None) != 0 and b"alignment" in lib.e2v2_last_error()

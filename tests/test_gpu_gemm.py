@@ -209,3 +209,30 @@ def test_grouped_gemm_matches_separate_launches(pkg, cuda):
     gemm.gemm_grouped(probs)
     for p, ref in zip(probs, refs):
         assert torch.equal(p["out"], ref)
+
+
+@pytest.mark.parametrize("n", [1, 1000])
+def test_gated_gemm_equals_gate_kernel_then_gemm(pkg, cuda, n):
+    """The FFN's gate applied inside the split GEMM's operand read
+    (e2v2_gemm_s3_gated) against the gate kernel (e2v2_gate_fwd) followed by the
+    plain split GEMM: the same products, so the outputs are bitwise equal; a
+    bias on row 0 and a residual included."""
+    from ubio_molfm_amd import _lib, gemm, modules
+    g = torch.Generator().manual_seed(9)
+    C = 256
+    h = torch.randn(9, n, C, generator=g).to(cuda)
+    sc = (2 * torch.randn(n, 3 * C, generator=g)).to(cuda)
+    w = (torch.randn(3, C, C, generator=g) / 16).to(cuda)
+    b2 = torch.randn(C, generator=g).to(cuda)
+    res = torch.randn(9, n, C, generator=g).to(cuda)
+    widx = [0, 1, 1, 1, 2, 2, 2, 2, 2]
+    pw = gemm.pack(w)
+    y = torch.empty_like(h)
+    k1, k2 = modules.SILU_NORM, modules.SIGMOID_NORM
+    _lib.call("e2v2_gate_fwd", _lib.vp(sc.data_ptr()), _lib.vp(h.data_ptr()), _lib.vp(y.data_ptr()), _lib.i32(n),
+              _lib.f32(k1), _lib.f32(k2), _lib.vp(torch.cuda.current_stream().cuda_stream))
+    ref = torch.empty(9, n, C, device=cuda)
+    gemm.gemm(y, pw, ref, widx, bias=b2, res=res)
+    out = torch.empty(9, n, C, device=cuda)
+    gemm.gemm(h, pw, out, widx, bias=b2, res=res, gate=(sc, k1, k2))
+    assert torch.equal(out, ref)

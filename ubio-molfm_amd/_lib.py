@@ -25,7 +25,7 @@ EXPORTS = [
     "e2v2_segment_metadata", "e2v2_pair_count", "e2v2_pair_emit", "e2v2_seg_dot", "e2v2_seg_reduce",
     "e2v2_gather_rows", "e2v2_outer_reduce", "e2v2_outer_bwd",
     "e2v2_radial_eval", "e2v2_radial_eval_bwd", "e2v2_sh_contract", "e2v2_sh_contract_bwd",
-    "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_pack", "e2v2_gemm_packed_bytes", "e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3",
+    "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated", "e2v2_gemm_pack", "e2v2_gemm_packed_bytes", "e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3",
 ]
 
 

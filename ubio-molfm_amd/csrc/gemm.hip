@@ -185,27 +185,72 @@ __device__ __forceinline__ int gemm_tiles(const e2v2_gemm_args& G) {
   return G.batch * ((G.m + kGM - 1) / kGM) * (G.n / kGN);
 }
 
+// Gate_s3 (module_utils.py:2694-2746) applied to the A operand as it is read:
+// batch 0 reads silu(s[i][kk]) k1 from the gate logits themselves, batch b >= 1
+// reads a[b][i][kk] sigmoid(s[i][k widx[b] + kk]) k2 (the same products, rounded
+// the same way, as the gate kernel's output).
+struct GateOp {
+  const float* s;
+  int64_t ld;
+  float k1, k2;
+};
+
 // One 128 x 128 output tile (batch-major, then row tile, then column tile).
-__device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, char* lds) {
+template <bool kGate>
+__device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, char* lds, const GateOp& gt) {
   const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
   const int n_mt = (G.m + kGM - 1) / kGM, n_nt = G.n / kGN;
   const int nt = tile % n_nt, mt = (tile / n_nt) % n_mt, bi = tile / (n_nt * n_mt);
   const int row0 = mt * kGM, nks = G.k / kGK;
-  const __amdgpu_buffer_rsrc_t ar = rows_rsrc(G.a + (size_t)bi * G.a_bs, row0, G.m, (int)G.lda);
+  const bool g0 = kGate && bi == 0;                      // batch 0 of a gated call: silu of the logits
+  const int lda = g0 ? (int)gt.ld : (int)G.lda;
+  const __amdgpu_buffer_rsrc_t ar = rows_rsrc(g0 ? gt.s : G.a + (size_t)bi * G.a_bs, row0, G.m, lda);
   uint32_t a_voff[kGAi / 4];
-  a_offsets(wv, lane, (int)G.lda, a_voff);
+  a_offsets(wv, lane, lda, a_voff);
   const __amdgpu_buffer_rsrc_t br = b_rsrc(G.b, G.widx[bi], n_nt, nt, nks);
   const int ra = wv * 32 + (lane & 31);
+  // gate logits of this lane's A values (row ra, k 8 h .. +7 of each stage), one stage ahead
+  // (32-bit byte offsets from the uniform base: (m + 128) ld_s 4 < 2^31 is checked by the host)
+  const char* sb = reinterpret_cast<const char*>(gt.s);
+  const bool mok = kGate && !g0 && row0 + ra < G.m;
+  const uint32_t moff = mok ? (uint32_t)(((uint32_t)(row0 + ra) * (uint32_t)gt.ld + (uint32_t)(G.k * G.widx[bi]) +
+                                          8u * h) * 4u)
+                            : 0u;
+  floatx4 mv0 = {0.f, 0.f, 0.f, 0.f}, mv1 = {0.f, 0.f, 0.f, 0.f};
+  if (mok) {
+    mv0 = *reinterpret_cast<const floatx4*>(sb + moff);
+    mv1 = *reinterpret_cast<const floatx4*>(sb + moff + 16u);
+  }
   floatx16 acc[4];
   kloop(lds, kGStage, nks, lane,
         [&](int ks, int buf) {
           load_a(ar, a_voff, (uint32_t)(ks * kGK) * 4u, lds + buf * kGStage, wv);
           load_b(br, ks, lds + buf * kGStage + kGAg * 16, wv, lane);
         },
-        [&](int, int buf, floatx4& x0, floatx4& x1) {
+        [&](int ks, int buf, floatx4& x0, floatx4& x1) {
           const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * kGStage);
           x0 = As[a_slot(ra, 2 * h)];
           x1 = As[a_slot(ra, 2 * h + 1)];
+          if constexpr (kGate) {
+            if (g0) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                x0[e] = silu(x0[e]) * gt.k1;
+                x1[e] = silu(x1[e]) * gt.k1;
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                x0[e] = sigmoidf_(mv0[e]) * gt.k2 * x0[e];
+                x1[e] = sigmoidf_(mv1[e]) * gt.k2 * x1[e];
+              }
+              if (mok && ks + 1 < nks) {
+                const uint32_t o = moff + (uint32_t)(ks + 1) * (kGK * 4u);
+                mv0 = *reinterpret_cast<const floatx4*>(sb + o);
+                mv1 = *reinterpret_cast<const floatx4*>(sb + o + 16u);
+              }
+            }
+          }
         },
         acc);
 
@@ -235,7 +280,15 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
   const int n_tiles = gemm_tiles(G);
   const int tile = xcd_row(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
-  gemm_tile(G, tile, lds);
+  gemm_tile<false>(G, tile, lds, GateOp{});
+}
+
+__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_gate(e2v2_gemm_args G, GateOp gt) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  const int n_tiles = gemm_tiles(G);
+  const int tile = xcd_row(blockIdx.x, n_tiles);
+  if (tile >= n_tiles) return;
+  gemm_tile<true>(G, tile, lds, gt);
 }
 
 // Independent GEMMs in one launch: group g owns workgroups block0[g] ..
@@ -258,7 +311,7 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp(GemmGroups P) {
     if (gi < P.n && b >= P.block0[gi] && b < P.block0[gi + 1]) {
       const int n_tiles = gemm_tiles(P.g[gi]);
       const int tile = xcd_row(b - P.block0[gi], n_tiles);
-      if (tile < n_tiles) gemm_tile(P.g[gi], tile, lds);
+      if (tile < n_tiles) gemm_tile<false>(P.g[gi], tile, lds, GateOp{});
       return;
     }
   }
@@ -499,6 +552,25 @@ E2V2_API int e2v2_gemm_s3(const e2v2_gemm_args* g, hipStream_t s) {
   if (G.m == 0) return 0;
   hipLaunchKernelGGL(k_gemm_s3, dim3(xcd_grid(host_tiles(G))), dim3(kGT), 0, s, G);
   E2V2_LAUNCHED("k_gemm_s3");
+  return 0;
+}
+
+E2V2_API int e2v2_gemm_s3_gated(const e2v2_gemm_args* g, const float* s, int64_t ld_s, float k1, float k2,
+                                hipStream_t st) {
+  using namespace e2v2;
+  E2V2_REQUIRE(g, "gemm_s3_gated: null arguments");
+  const e2v2_gemm_args& G = *g;
+  if (int rc = check_gemm_args(G)) return rc;
+  E2V2_REQUIRE(s && ((uintptr_t)s & 15) == 0 && ld_s % 4 == 0,
+               "gemm_s3_gated: the gate logits need 16-byte alignment and ld_s %% 4 == 0");
+  for (int b = 0; b < G.batch; ++b)
+    E2V2_REQUIRE((int64_t)G.k * (G.widx[b] + 1) <= ld_s, "gemm_s3_gated: batch %d reads logit columns past ld_s=%lld",
+                 b, (long long)ld_s);
+  E2V2_REQUIRE((uint64_t)(G.m + kGM) * (uint64_t)ld_s * 4u < (1ull << 31), "gemm_s3_gated: logits too large (m=%d)",
+               G.m);
+  if (G.m == 0) return 0;
+  hipLaunchKernelGGL(k_gemm_s3_gate, dim3(xcd_grid(host_tiles(G))), dim3(kGT), 0, st, G, GateOp{s, ld_s, k1, k2});
+  E2V2_LAUNCHED("k_gemm_s3_gate");
   return 0;
 }
 

@@ -122,16 +122,27 @@ def _args(a, pw: PackedWeight, out: torch.Tensor, widx=None, bias=None, bias_bat
 
 
 def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] = None,
-         bias: Optional[torch.Tensor] = None, bias_batches: int = 1, res: Optional[torch.Tensor] = None):
+         bias: Optional[torch.Tensor] = None, bias_batches: int = 1, res: Optional[torch.Tensor] = None,
+         gate=None):
     """out[b] = a[b] W_{widx[b]}^T (+ bias for b < bias_batches) (+ res[b]).
     a [batch, m, k] or [m, k] fp32 (rows may be strided, k contiguous), or a list of
     same-layout [m, k] matrices; out and res [batch, m, n] (res may be out); bias [n]
-    (shared) or [batch, n] (one per batch)."""
+    (shared) or [batch, n] (one per batch).  gate = (s, k1, k2): Gate_s3's activation
+    applied to A as it is read (``e2v2_gemm_s3_gated``): batch 0 takes silu(s[:, :k]) k1,
+    batch b >= 1 takes a[b] * sigmoid(s[:, k widx[b]:k (widx[b] + 1)]) k2."""
     keep = a    # the operand stays referenced until the launch is enqueued
     g, work = _args(a, pw, out, widx, bias, bias_batches, res)
     if g is None:
         return out
-    _lib.call("e2v2_gemm_s3", _lib.C.byref(g), _lib.vp(torch.cuda.current_stream(out.device).cuda_stream))
+    st = _lib.vp(torch.cuda.current_stream(out.device).cuda_stream)
+    if gate is not None:
+        sg, k1, k2 = gate
+        if sg.dtype != torch.float32 or sg.dim() != 2 or sg.stride(1) != 1 or sg.shape[0] != _as3(out).shape[1]:
+            raise ValueError("gemm: gate logits must be fp32 [m, ld] with contiguous rows")
+        _lib.call("e2v2_gemm_s3_gated", _lib.C.byref(g), _lib.vp(sg.data_ptr()), _lib.i64(sg.stride(0)),
+                  _lib.f32(k1), _lib.f32(k2), st)
+    else:
+        _lib.call("e2v2_gemm_s3", _lib.C.byref(g), st)
     del keep
     if _lib._timer is not None:
         _lib._timer.add_work("e2v2_gemm_s3", work)

@@ -885,6 +885,39 @@ class Gate_s3(nn.Module):
                             SIGMOID_NORM, packs)
 
 
+class GatedLinearS3Fn(torch.autograd.Function):
+    """Gate_s3 followed by the FFN's second SO3_Linear_e2former
+    (module_utils.py:2694-2746, 2755-2797) on the split GEMMs, fp32: the gate logits
+    sc = h[0] Wg^T + bg, then y = res + gate(sc, h) W2 (+ b2 on row 0) with the gate
+    applied while the GEMM reads its operand (``e2v2_gemm_s3_gated``), so the gated
+    activation is never written.  The backward is GateFn's and SO3LinearFn's.  Input
+    gradients only."""
+
+    @staticmethod
+    def forward(ctx, h, gpacks, bg, k1: float, k2: float, W2op, b2, lmax: int, res=None):
+        h = h.contiguous()
+        sc = h.new_empty(h.shape[1], gpacks[0].n)
+        s3gemm.gemm(h[0], gpacks[0], sc, bias=bg)
+        y = h.new_empty(h.shape[0], h.shape[1], W2op.w.shape[1])
+        s3gemm.gemm(h, W2op.s3f(), y, _m_degrees(lmax), bias=b2, bias_batches=1,
+                    res=None if res is None else res.contiguous(), gate=(sc, k1, k2))
+        ctx.save_for_backward(sc, h)
+        ctx.gpacks, ctx.k, ctx.W2op, ctx.lmax, ctx.has_res = gpacks, (k1, k2), W2op, lmax, res is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gout):
+        sc, h = ctx.saved_tensors
+        gout = gout.contiguous()
+        gy = torch.empty_like(h)
+        s3gemm.gemm(gout, ctx.W2op.s3b(), gy, _m_degrees(ctx.lmax))
+        gsc = torch.empty_like(sc); gh = torch.empty_like(h)
+        _lib.call("e2v2_gate_bwd", _dp(sc), _dp(h), _dp(gy), _dp(gsc), _dp(gh), _lib.i32(h.shape[1]),
+                  _lib.f32(ctx.k[0]), _lib.f32(ctx.k[1]), _stream())
+        s3gemm.gemm(gsc, ctx.gpacks[1], gh[0])        # the gate kernel leaves gh[0] = 0
+        return gh, None, None, None, None, None, None, None, (gout if ctx.has_res else None)
+
+
 class FeedForwardNetwork_s3(nn.Module):
     """module_utils.py:2755-2797."""
 
@@ -896,10 +929,15 @@ class FeedForwardNetwork_s3(nn.Module):
 
     def forward(self, x, res=None, bf16: bool = False, **kw):
         with record_function("FeedForwardFunction"):
-            h = self.gate(self.slinear_1(x, bf16), bf16)
+            h = self.slinear_1(x, bf16)
             s2 = self.slinear_2
-            return SO3LinearFn.apply(h, mrow_weight(s2, "weight", s2.weight, bf16, s2.lmax), s2.bias.detach(),
-                                     s2.lmax, res)
+            W2op = mrow_weight(s2, "weight", s2.weight, bf16, s2.lmax)
+            gpacks = None if bf16 else dense_packs(self.gate.gates)
+            if gpacks is not None and W2op.split_ok() and h.dtype == torch.float32 and h.shape[2] == s2.weight.shape[2]:
+                return GatedLinearS3Fn.apply(h, gpacks, self.gate.gates.bias.detach(), SILU_NORM, SIGMOID_NORM, W2op,
+                                             s2.bias.detach(), s2.lmax, res)
+            h = self.gate(h, bf16)
+            return SO3LinearFn.apply(h, W2op, s2.bias.detach(), s2.lmax, res)
 
 
 class sph_fromxyz(nn.Module):
