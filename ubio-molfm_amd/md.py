@@ -51,20 +51,29 @@ def maxwell_boltzmann(Z, T=300.0, seed=0):
     return v
 
 
-def fixcom_forces(f: torch.Tensor, m: torch.Tensor) -> torch.Tensor:
-    """F - m (sum m F) / (sum m^2); m is [N, 1]."""
-    return f - m * ((m * f).sum(0) / (m * m).sum())
+# The projections below are written as few fused elementwise operations, with
+# the constant mass sums passed in as numbers when known, so that a step
+# launches about 25 small kernels instead of about 45.  (Mass-weighted sums as
+# [1, N] x [N, 3] float64 GEMMs were measured far slower: the library runs such
+# a shape's whole K loop in one tile.)
+
+def fixcom_forces(f: torch.Tensor, m: torch.Tensor, mm: float = None) -> torch.Tensor:
+    """F - m (sum m F) / (sum m^2); m is [N, 1], mm = sum m^2 when known."""
+    mm = float((m * m).sum()) if mm is None else mm
+    return torch.addcmul(f, m, (m * f).sum(0), value=-1.0 / mm)
 
 
-def fixcom_positions(x_old: torch.Tensor, x_new: torch.Tensor, m: torch.Tensor) -> torch.Tensor:
-    """Shift x_new so that its mass-weighted centre equals that of x_old."""
-    ms = m.sum()
-    return x_new + ((m * x_old).sum(0) / ms - (m * x_new).sum(0) / ms)
+def fixcom_positions(x_old: torch.Tensor, x_new: torch.Tensor, m: torch.Tensor, ms: float = None) -> torch.Tensor:
+    """Shift x_new so that its mass-weighted centre equals that of x_old
+    (ms = sum m when known)."""
+    ms = float(m.sum()) if ms is None else ms
+    return torch.add(x_new, (m * (x_old - x_new)).sum(0), alpha=1.0 / ms)
 
 
-def fixcom_momenta(p: torch.Tensor, m: torch.Tensor) -> torch.Tensor:
+def fixcom_momenta(p: torch.Tensor, m: torch.Tensor, ms: float = None) -> torch.Tensor:
     """p - m (sum p) / (sum m)."""
-    return p - m * (p.sum(0) / m.sum())
+    ms = float(m.sum()) if ms is None else ms
+    return torch.addcmul(p, m, p.sum(0), value=-1.0 / ms)
 
 
 def wrappable(cell: np.ndarray, pbc) -> bool:
@@ -86,7 +95,7 @@ def wrap_positions(x: torch.Tensor, cell=None, mats=None) -> torch.Tensor:
     included).  mats: the cell's ``cell_matrices``, if already on the device."""
     A, Ainv = cell_matrices(cell, x.device) if mats is None else mats
     frac = x.to(torch.float64) @ Ainv
-    return (frac - torch.floor(frac)) @ A
+    return torch.remainder(frac, 1.0) @ A          # frac - floor(frac), one kernel
 
 
 def cell_bounding_box(cell) -> np.ndarray:
@@ -112,7 +121,10 @@ class VelocityVerlet:
         self.fixcm = fixcm
         Z = np.asarray(sysd["Z"])
         self.Z = torch.as_tensor(Z, device=device)
-        self.m = torch.as_tensor(masses_for(Z), device=device, dtype=torch.float64)[:, None]
+        mnp = masses_for(Z)
+        self.m = torch.as_tensor(mnp, device=device, dtype=torch.float64)[:, None]
+        self.inv_m = 1.0 / self.m
+        self.msum, self.mmsum = float(mnp.sum()), float((mnp * mnp).sum())
         self.x = torch.as_tensor(np.asarray(sysd["pos"], np.float64), device=device)
         self.p = torch.as_tensor(maxwell_boltzmann(Z, T, seed), device=device) * self.m
         self.cells = np.asarray(sysd["cell"], np.float32).reshape(-1, 3, 3)
@@ -201,17 +213,19 @@ class VelocityVerlet:
     def _advance(self, capacity):
         state = (self.x, self.p, self.e, self.f)
         m, dt, c1 = self.m, self.dt, 0.5 * self.dt
-        f = fixcom_forces(self.f, m) if self.fixcm else self.f
-        x_new = self.x + dt * (self.p / m + c1 * f / m)
+        f = fixcom_forces(self.f, m, self.mmsum) if self.fixcm else self.f
+        # x + dt (p / m + c1 f / m)
+        x_new = torch.addcmul(self.x, self.inv_m, self.p, value=dt).addcmul_(self.inv_m, f, value=dt * c1)
         if self.fixcm:
-            x_new = fixcom_positions(self.x, x_new, m)
+            x_new = fixcom_positions(self.x, x_new, m, self.msum)
         e_new, f_new = self.forces_at(x_new, capacity)
         if capacity is not None:
             self.pending = (self.last_nl.stats_host, self.last_nl.stats_event, state)
         else:
             self.edge_counts.append(self.n_edges)
-        fn = fixcom_forces(f_new, m) if self.fixcm else f_new
-        p_new = ((x_new - self.x) / dt + c1 * fn / m) * m
+        fn = fixcom_forces(f_new, m, self.mmsum) if self.fixcm else f_new
+        # ((x_new - x) / dt + c1 fn / m) m
+        p_new = torch.addcmul(fn * c1, x_new - self.x, m, value=1.0 / dt)
         if self.fixcm:
-            p_new = fixcom_momenta(p_new, m)
+            p_new = fixcom_momenta(p_new, m, self.msum)
         self.x, self.p, self.e, self.f = x_new, p_new, e_new, f_new
