@@ -236,3 +236,27 @@ def test_gated_gemm_equals_gate_kernel_then_gemm(pkg, cuda, n):
     out = torch.empty(9, n, C, device=cuda)
     gemm.gemm(h, pw, out, widx, bias=b2, res=res, gate=(sc, k1, k2))
     assert torch.equal(out, ref)
+
+
+def test_list_operands_either_order(pkg, cuda):
+    """Two separately allocated matrices as a two-batch A operand (batch stride =
+    their address difference, of either sign, per-batch bias): bitwise equal to
+    two single launches."""
+    from ubio_molfm_amd import gemm
+    g = torch.Generator().manual_seed(13)
+    m, n, k = 700, 256, 512
+    x0 = torch.randn(m, k, generator=g).to(cuda)
+    x1 = torch.randn(m, k, generator=g).to(cuda)
+    w = (torch.randn(2, n, k, generator=g) / math.sqrt(k)).to(cuda)
+    bias = torch.randn(2, n, generator=g).to(cuda)
+    pw = gemm.pack(w)
+    refs = []
+    for b, x in enumerate((x0, x1)):
+        r = torch.empty(m, n, device=cuda)
+        gemm.gemm(x, pw, r, [b], bias=bias[b].contiguous())
+        refs.append(r)
+    for order in ((0, 1), (1, 0)):
+        xs = [(x0, x1)[i] for i in order]
+        out = torch.empty(2, m, n, device=cuda)
+        gemm.gemm(xs, pw, out, list(order), bias=bias[list(order)].contiguous(), bias_batches=2)
+        assert torch.equal(out[0], refs[order[0]]) and torch.equal(out[1], refs[order[1]])

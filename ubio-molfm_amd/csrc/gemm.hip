@@ -204,7 +204,7 @@ __device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, cha
   const int row0 = mt * kGM, nks = G.k / kGK;
   const bool g0 = kGate && bi == 0;                      // batch 0 of a gated call: silu of the logits
   const int lda = g0 ? (int)gt.ld : (int)G.lda;
-  const __amdgpu_buffer_rsrc_t ar = rows_rsrc(g0 ? gt.s : G.a + (size_t)bi * G.a_bs, row0, G.m, lda);
+  const __amdgpu_buffer_rsrc_t ar = rows_rsrc(g0 ? gt.s : G.a + (int64_t)bi * G.a_bs, row0, G.m, lda);
   uint32_t a_voff[kGAi / 4];
   a_offsets(wv, lane, lda, a_voff);
   const __amdgpu_buffer_rsrc_t br = b_rsrc(G.b, G.widx[bi], n_nt, nt, nks);
@@ -256,12 +256,12 @@ __device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, cha
 
   // epilogue: C = acc (+ bias) (+ R)
   const bool with_bias = G.bias && bi < G.bias_batches;
-  float* cb = G.c + (size_t)bi * G.c_bs;
-  const float* rb = G.r ? G.r + (size_t)bi * G.r_bs : nullptr;
+  float* cb = G.c + (int64_t)bi * G.c_bs;
+  const float* rb = G.r ? G.r + (int64_t)bi * G.r_bs : nullptr;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int col = nt * kGN + 32 * j + (lane & 31);
-    const float bv = with_bias ? G.bias[(size_t)bi * G.bias_bs + col] : 0.f;
+    const float bv = with_bias ? G.bias[(int64_t)bi * G.bias_bs + col] : 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = row0 + wv * 32 + acc_row(r, lane);

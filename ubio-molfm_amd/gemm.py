@@ -69,8 +69,9 @@ def _as3(t: torch.Tensor) -> torch.Tensor:
 
 
 def _batch_view(a):
-    """(base pointer, row stride, batch stride, batch, m, k) of an A operand given as a tensor
-    [batch, m, k] / [m, k] or as a list of same-layout 2-D tensors (batch b at base + b * bs)."""
+    """(base pointer, row stride, batch stride, batch, m, k, holder) of an A operand given as a
+    tensor [batch, m, k] / [m, k] or as a list of same-layout 2-D tensors (batch b at base + b * bs,
+    bs of either sign); holder is what must stay referenced until the launch is enqueued."""
     if isinstance(a, (list, tuple)):
         t0 = a[0]
         for t in a:
@@ -81,18 +82,19 @@ def _batch_view(a):
         if len(steps) > 1 or any(d % 4 for d in steps):
             raise ValueError("gemm: batch matrices must be evenly spaced in memory")
         bs = steps.pop() // 4 if steps else 0
-        return t0.data_ptr(), t0.stride(0), bs, len(a), t0.shape[0], t0.shape[1]
+        return t0.data_ptr(), t0.stride(0), bs, len(a), t0.shape[0], t0.shape[1], a
     a3 = _as3(a)
     if a3.stride(2) != 1 or a3.stride(1) % 4 or a3.data_ptr() % 16:
         a3 = a3.contiguous()
-    return a3.data_ptr(), a3.stride(1), a3.stride(0), a3.shape[0], a3.shape[1], a3.shape[2]
+    return a3.data_ptr(), a3.stride(1), a3.stride(0), a3.shape[0], a3.shape[1], a3.shape[2], a3
 
 
 def _args(a, pw: PackedWeight, out: torch.Tensor, widx=None, bias=None, bias_batches: int = 1, res=None):
-    """(e2v2_gemm_args, fp32 work) of one GEMM (None for an empty one); checks the operands."""
+    """(e2v2_gemm_args, fp32 work, operand holder) of one GEMM (None for an empty one); checks
+    the operands."""
     o3 = _as3(out)
     r3 = None if res is None else _as3(res)
-    a_ptr, lda, a_bs, batch, m, k = _batch_view(a)
+    a_ptr, lda, a_bs, batch, m, k, holder = _batch_view(a)
     if k != pw.k or o3.shape != (batch, m, pw.n) or o3.dtype != torch.float32:
         raise ValueError(f"gemm: a [{batch}, {m}, {k}] / out {tuple(o3.shape)} do not fit W [{pw.n}, {pw.k}]")
     if o3.stride(2) != 1 or (r3 is not None and (r3.shape != o3.shape or r3.stride(2) != 1)):
@@ -101,7 +103,7 @@ def _args(a, pw: PackedWeight, out: torch.Tensor, widx=None, bias=None, bias_bat
     if len(widx) != batch or batch > MAX_BATCH or any(not 0 <= i < pw.n_w for i in widx):
         raise ValueError(f"gemm: weight index {widx} for {pw.n_w} weights")
     if m == 0:
-        return None, 0.0
+        return None, 0.0, holder
     g = _lib.GemmArgs()
     g.a, g.lda, g.a_bs = a_ptr, lda, a_bs
     g.b, g.n_w = pw.buf.data_ptr(), pw.n_w
@@ -118,7 +120,7 @@ def _args(a, pw: PackedWeight, out: torch.Tensor, widx=None, bias=None, bias_bat
     g.m, g.n, g.k, g.batch = m, pw.n, pw.k, batch
     for b, i in enumerate(widx):
         g.widx[b] = int(i)
-    return g, 2.0 * batch * m * pw.n * pw.k
+    return g, 2.0 * batch * m * pw.n * pw.k, holder
 
 
 def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] = None,
@@ -130,8 +132,7 @@ def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] =
     (shared) or [batch, n] (one per batch).  gate = (s, k1, k2): Gate_s3's activation
     applied to A as it is read (``e2v2_gemm_s3_gated``): batch 0 takes silu(s[:, :k]) k1,
     batch b >= 1 takes a[b] * sigmoid(s[:, k widx[b]:k (widx[b] + 1)]) k2."""
-    keep = a    # the operand stays referenced until the launch is enqueued
-    g, work = _args(a, pw, out, widx, bias, bias_batches, res)
+    g, work, keep = _args(a, pw, out, widx, bias, bias_batches, res)   # keep: referenced until the launch
     if g is None:
         return out
     st = _lib.vp(torch.cuda.current_stream(out.device).cuda_stream)
@@ -159,12 +160,13 @@ def gemm_grouped(problems):
     with the longest k first: their tiles are dispatched first."""
     if not 0 < len(problems) <= MAX_GROUPS:
         raise ValueError(f"gemm_grouped: {len(problems)} problems (1 .. {MAX_GROUPS})")
-    keep = [p["a"] for p in problems]
+    keep = []   # operands (and any contiguous copies) referenced until the launch is enqueued
     arr = (_lib.GemmArgs * MAX_GROUPS)()
     n, work, dev = 0, 0.0, problems[0]["out"].device
     for p in problems:
-        g, w = _args(p["a"], p["pw"], p["out"], p.get("widx"), p.get("bias"), p.get("bias_batches", 1),
-                     p.get("res"))
+        g, w, holder = _args(p["a"], p["pw"], p["out"], p.get("widx"), p.get("bias"), p.get("bias_batches", 1),
+                             p.get("res"))
+        keep.append(holder)
         if g is not None:
             arr[n] = g
             n += 1
