@@ -140,7 +140,7 @@ PROJ_FLOPS["e2v2_qk_proj_fwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
 PROJ_FLOPS["e2v2_qk_proj_bwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
 # fp32 GEMMs on the split kernels execute six bf16 MFMA products per fp32 multiply-add
 SPLIT_PRODUCTS = 6
-SPLIT_ENTRIES = ("e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3", "e2v2_gemm_s3", "e2v2_gemm_s3_grouped")
+SPLIT_ENTRIES = ("e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3", "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated")
 
 KERNELS_OF = {"e2v2_attn_fwd": ["k_attn_fwd_sl"],
               "e2v2_attn_bwd": ["k_attn_bwd_row_sl", "k_attn_bwd_col_grp", "k_edge_part_sum"],
@@ -148,7 +148,8 @@ KERNELS_OF = {"e2v2_attn_fwd": ["k_attn_fwd_sl"],
               "e2v2_nbr_count": ["k_nbr_count"],
               "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"],
               "e2v2_qk_proj_fwd_s3": ["k_qk_s3_fwd"], "e2v2_qk_proj_bwd_s3": ["k_qk_s3_bwd"],
-              "e2v2_gemm_s3": ["k_gemm_s3"], "e2v2_gemm_s3_grouped": ["k_gemm_s3_grp"]}
+              "e2v2_gemm_s3": ["k_gemm_s3"], "e2v2_gemm_s3_grouped": ["k_gemm_s3_grp"],
+              "e2v2_gemm_s3_gated": ["k_gemm_s3_gate"]}
 
 
 def expanded_nodes(nl) -> int:
@@ -309,7 +310,7 @@ def main():
                               "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill",
                               "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd", "e2v2_qk_proj_fwd_bf16",
                               "e2v2_qk_proj_bwd_bf16", "e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3",
-                              "e2v2_gemm_s3", "e2v2_gemm_s3_grouped"])
+                              "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated"])
     edges = []
     e_start = integ.e.sum().item() + integ.kinetic()
     _lib.set_timer(timer)

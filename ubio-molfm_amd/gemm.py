@@ -136,6 +136,7 @@ def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] =
     if g is None:
         return out
     st = _lib.vp(torch.cuda.current_stream(out.device).cuda_stream)
+    entry = "e2v2_gemm_s3" if gate is None else "e2v2_gemm_s3_gated"
     if gate is not None:
         sg, k1, k2 = gate
         if sg.dtype != torch.float32 or sg.dim() != 2 or sg.stride(1) != 1 or sg.shape[0] != _as3(out).shape[1]:
@@ -146,7 +147,7 @@ def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] =
         _lib.call("e2v2_gemm_s3", _lib.C.byref(g), st)
     del keep
     if _lib._timer is not None:
-        _lib._timer.add_work("e2v2_gemm_s3", work)
+        _lib._timer.add_work(entry, work)
     return out
 
 
