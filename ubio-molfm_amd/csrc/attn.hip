@@ -418,7 +418,7 @@ __device__ __forceinline__ void tp_transpose(const float (&g)[kNT], float (&dA)[
 // column j are its key-CSR edges.  w_g and dqk_g hold the group's 32 heads per
 // edge ([E][32]), written by the row pass of the same group.
 template <int R, typename TS, bool kSlots, int kMode>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attn_bwd_col_grp(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(TS) == 4 ? 2 : 3))) void k_attn_bwd_col_grp(
     e2v2_attn_args A, const TS* __restrict__ G, const float* __restrict__ w_g, const float* __restrict__ dqk_g,
     float* __restrict__ dv_out, float* __restrict__ dk_out, int grp) {
   constexpr bool kZ = kMode & kModeZero;
