@@ -281,14 +281,16 @@ int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset,
 /* Per-edge values of a "plain"-layout table ([pairs][n_nodes][4][nc], nc channels): out [E][nc] =
    f_c(dist[e]) for the pair (atom_type[edge_row[e]], atom_type[col[e]]), the quintic Hermite interpolant.
    Replaces the per-edge RadialProfile calls of the QKdot gates, rad_func_m0(x_edge) (e2former.py:278)
-   and fc_easy(x_edge)[:, H:] (e2former.py:293-294). */
+   and fc_easy(x_edge)[:, H:] (e2former.py:293-294).  e_end (device int32, or NULL for n_edges): the
+   number of real edges, read on the device (the query CSR's row_ptr[n_rows]); slots e >= *e_end of a
+   capacity build are not read and get out[e][:] = 0. */
 int e2v2_radial_eval(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
                      const int32_t* atom_type, const int32_t* edge_row, const int32_t* col, const float* dist,
-                     int64_t n_edges, float* out, hipStream_t s);
-/* ddist [E] = sum_c grad[e][c] f_c'(dist[e]) (fixed summation order). */
+                     int64_t n_edges, const int32_t* e_end, float* out, hipStream_t s);
+/* ddist [E] = sum_c grad[e][c] f_c'(dist[e]) (fixed summation order); ddist[e] = 0 for e >= *e_end. */
 int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
                          const int32_t* atom_type, const int32_t* edge_row, const int32_t* col, const float* dist,
-                         int64_t n_edges, const float* grad, float* ddist, hipStream_t s);
+                         int64_t n_edges, const int32_t* e_end, const float* grad, float* ddist, hipStream_t s);
 /* x0 [E][3][C] = sum_{m in l} Y[e][m] xn[m][row(e)][C] for l = 0, 1, 2 (Y [E][9], xn [9][n_rows][C]
    m-major, edges of a row contiguous by row_ptr [n_rows + 1], C <= 256): the x_0_extra of QKdot_alpha
    (e2former.py:271-276, Y the normalised spherical harmonics) and of QKdotS_alpha (e2former.py:288-296,

@@ -101,6 +101,7 @@ def test_calculator_host_path_wraps_and_batches(pkg, cuda):
                   np.zeros(len(mol["pos"])))
     calc = calculator.E2FormerCalculator(model=m, head_name="omol25", charge=5, multiplicity=3, device=str(cuda))
     out = calc.calculate_batch([a1, a2])
+    table = calculator.head_ref_energy("omol25")          # added by default (add_ref_energy=True)
     assert isinstance(out[0]["energy"], float) and isinstance(out[0]["forces"], np.ndarray)
     wrapped = calculator.hard_wrap(pw, w["cell"][0], [True] * 3).astype(np.float32)
     frac = wrapped.astype(np.float64) @ np.linalg.inv(np.asarray(w["cell"][0], np.float64))
@@ -109,10 +110,67 @@ def test_calculator_host_path_wraps_and_batches(pkg, cuda):
         e_ref, f_ref = _oracle(om, sysd, [q], [1])
         r = out[0] if a is a1 else out[1]
         n = len(sysd["pos"])
-        de = abs(r["energy"] - float(e_ref[0])) / n
+        de = abs(r["energy"] - (float(e_ref[0]) + float(table[np.asarray(sysd["Z"])].sum()))) / n
         rel = float(np.linalg.norm(r["forces"] - f_ref.numpy()) / f_ref.norm())
         print(f"[calculator host] N={n} |dE|/atom={de:.3e} force relL2={rel:.3e}", flush=True)
         assert de < 1e-5 and rel < 1e-4
+
+
+@pytest.mark.parametrize("head", ["omol25", "svp"])
+def test_calculator_from_yaml_and_checkpoint(pkg, cuda, tmp_path, head):
+    """The model lifecycle of model_interface.py:172-245: the calculator built
+    from a flattened yaml (config_path = its directory, which holds exactly one
+    yaml) and a {"model": state_dict} checkpoint (loaded with weights_only) on a
+    two-head model; the head's energy plus the head's reference energies
+    (atom_reference * unit, molfm/data/utils.py, added by default) against the
+    oracle with the same weights plus the table sum, 1e-5 eV/atom and 1e-4
+    force rel-L2.  svp exercises the kcal/mol -> eV unit and its own head."""
+    import yaml
+    from ubio_molfm_amd import calculator, model, systems
+    from oracle.model import MolfmAtomic as OracleModel
+    args = model.default_args(heads=("omol25", "svp"))
+    raw = dict(backbone="e2former", backbone_config=dict(args.backbone_config), dataset_name_list="omol25,svp",
+               head_cfg_str="", AutoGradForce=True)
+    raw["backbone_config"].pop("name")
+    cfg_dir = tmp_path / "run"
+    cfg_dir.mkdir()
+    (cfg_dir / "config.yaml").write_text(yaml.safe_dump(raw))
+    torch.manual_seed(21)
+    src = model.MolfmAtomic(calculator.model_args_from_config(raw))
+    torch.save({"model": src.state_dict()}, cfg_dir / "ckpt.pt")
+    calc = calculator.E2FormerCalculator(config_path=str(cfg_dir), checkpoint_path=str(cfg_dir / "ckpt.pt"),
+                                         head_name=head, device=str(cuda))
+    assert calc.config_file == str(cfg_dir / "config.yaml") and calc.add_ref_energy
+    om = OracleModel(head_names=("omol25", "svp")).eval()
+    om.load_state_dict(src.state_dict(), strict=True)
+    s = systems.organics_batch(n_mol=1, nmin=14, nmax=18, seed=22)
+    sysin = dict(positions=np.asarray(s["pos"], np.float64), numbers=np.asarray(s["Z"]), cell=np.zeros((3, 3)),
+                 pbc=np.zeros(3, bool), charge=np.zeros(len(s["pos"])))
+    r = calc.calculate_batch([sysin])[0]
+    bd = systems.to_padded(s)
+    bd["charge"] = torch.zeros(1, dtype=torch.int32)
+    bd["multiplicity"] = torch.ones(1, dtype=torch.int32)
+    o = om(bd, head=head)
+    table = calculator.head_ref_energy(head)
+    ref_sum = float(table[np.asarray(s["Z"])].sum())
+    n = len(s["pos"])
+    de = abs(r["energy"] - (float(o["pred_energy"][0]) + ref_sum)) / n
+    fr = o["pred_forces"].detach()[bd["atom_masks"]].double()
+    rel = float(np.linalg.norm(r["forces"] - fr.numpy()) / fr.norm())
+    print(f"[calculator yaml+ckpt {head}] ref sum {ref_sum:.3f} eV |dE|/atom={de:.3e} force relL2={rel:.3e}",
+          flush=True)
+    assert abs(ref_sum) > 100.0
+    assert de < 1e-5 and rel < 1e-4
+    # config_name picks one of several yamls; without it the directory must hold exactly one
+    (cfg_dir / "other.yaml").write_text(yaml.safe_dump(raw))
+    with pytest.raises(ValueError, match="exactly one yaml"):
+        calculator.E2FormerCalculator(config_path=str(cfg_dir), checkpoint_path=str(cfg_dir / "ckpt.pt"),
+                                      head_name=head, device=str(cuda))
+    calc2 = calculator.E2FormerCalculator(config_path=str(cfg_dir), config_name="config.yaml",
+                                          checkpoint_path=str(cfg_dir / "ckpt.pt"), head_name=head,
+                                          device=str(cuda), add_ref_energy=False)
+    r2 = calc2.calculate_batch([sysin])[0]
+    assert abs(r2["energy"] - (r["energy"] - ref_sum)) / n < 1e-5
 
 
 def test_neighbor_info_reference_dict(pkg, cuda):
@@ -217,3 +275,28 @@ def test_md_capacity_builds_match_exact_and_recover_from_overflow(pkg, cuda):
     assert torch.equal(ref.x, small.x) and torch.equal(ref.p, small.p) and torch.equal(ref.f, small.f)
     assert ref.edge_counts == lag.edge_counts == small.edge_counts
     assert lag.redone == 0 and small.redone == 2
+
+
+@pytest.mark.parametrize("tp", ["QKdot_alpha", "QKdotS_alpha"])
+def test_md_capacity_builds_qkdot_gates(pkg, cuda, tp):
+    """Capacity builds with the QKdot gates, whose per-edge kernels
+    (e2v2_radial_eval and its backward) run over every edge slot: slots past the
+    real edges (never written by the build) are bounded on the device by
+    row_ptr[N] and not read, and the trajectory equals that of exact builds
+    bitwise over 4 steps."""
+    from ubio_molfm_amd import md, model, systems
+    torch.manual_seed(16)
+    args = model.default_args()
+    args.backbone_config.update(tp_type=tp)
+    m = model.MolfmAtomic(args).eval().to(cuda)
+    s = systems.small_water(8, 6.2, seed=9)
+    ref = md.VelocityVerlet(m, s, cuda, dt_fs=1.0, T=300.0, seed=2, lagged=False)
+    lag = md.VelocityVerlet(m, s, cuda, dt_fs=1.0, T=300.0, seed=2)
+    for _ in range(4):
+        ref.step(); lag.step()
+    lag.sync()
+    nl = lag.last_nl
+    real = int(nl.row_ptr[-1])
+    print(f"[md capacity {tp}] slots {nl.n_edges} edges {real} redone {lag.redone}", flush=True)
+    assert nl.stats is not None and nl.n_edges > real
+    assert torch.equal(ref.x, lag.x) and torch.equal(ref.p, lag.p) and torch.equal(ref.f, lag.f)

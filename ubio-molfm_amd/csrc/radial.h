@@ -40,8 +40,10 @@ struct RadialTab {
 
 // Offset (floats) of node n of the interval holding d for pair p, and the
 // fraction t in [0, 1] (d / h, its floor and fraction are exact in fp32).
+// u is clamped to [0, n_nodes - 2] (a NaN distance gives the last interval), so no
+// distance reads outside the pair's nodes.
 __device__ __forceinline__ int64_t radial_node(const RadialTab& R, int pair, float d, float& t) {
-  const float u = fminf(d * R.inv_h, (float)(R.n_nodes - 2));
+  const float u = fmaxf(fminf(d * R.inv_h, (float)(R.n_nodes - 2)), 0.0f);
   const float fn = floorf(u);
   t = u - fn;
   return ((int64_t)pair * R.n_nodes + (int64_t)fn) * (4 * R.nc);
@@ -51,7 +53,7 @@ __device__ __forceinline__ int64_t radial_node(const RadialTab& R, int pair, flo
 // table ([pairs][n_slices][nodes][4][w]) of slice `slice`, and the fraction t.
 __device__ __forceinline__ int64_t radial_node_sliced(const RadialTab& R, int pair, int slice, int n_slices, int w,
                                                       float d, float& t) {
-  const float u = fminf(d * R.inv_h, (float)(R.n_nodes - 2));
+  const float u = fmaxf(fminf(d * R.inv_h, (float)(R.n_nodes - 2)), 0.0f);
   const float fn = floorf(u);
   t = u - fn;
   return (((int64_t)pair * n_slices + slice) * R.n_nodes + (int64_t)fn) * (4 * w);

@@ -280,17 +280,29 @@ __global__ __launch_bounds__(kRH) void k_radial_check(e2v2_radial_net W, const f
 // wavefront per edge, lanes over channels.  The forward interpolates rows 0..2
 // (values), the backward rows 1..3 (h-scaled derivatives) and sums
 // grad[e][c] f_c'(d) over the channels in a fixed order (lane partials, then a
-// butterfly), so the result does not depend on the launch.
+// butterfly), so the result does not depend on the launch.  e_end (NULL: n_edges)
+// bounds the edges on the device: in a capacity build the slots from row_ptr[n_rows]
+// on hold no edge (their row, column and distance were never written), and they
+// get zeros without reading them.
 constexpr int kEvWaves = 4;
+
+__device__ __forceinline__ bool past_end(int64_t e, const int32_t* __restrict__ e_end) {
+  return e_end != nullptr && e >= (int64_t)*e_end;
+}
 
 __global__ __launch_bounds__(64 * kEvWaves) void k_radial_eval(RadialTab R, const int32_t* __restrict__ atom_type,
                                                                const int32_t* __restrict__ edge_row,
                                                                const int32_t* __restrict__ col,
                                                                const float* __restrict__ dist, int64_t n_edges,
+                                                               const int32_t* __restrict__ e_end,
                                                                float* __restrict__ out) {
   const int64_t e = (int64_t)blockIdx.x * kEvWaves + (threadIdx.x >> 6);
   if (e >= n_edges) return;
   const int lane = threadIdx.x & 63;
+  if (past_end(e, e_end)) {
+    for (int c = lane; c < R.nc; c += 64) out[e * R.nc + c] = 0.f;
+    return;
+  }
   const int pair = atom_type[edge_row[e]] * R.n_types + atom_type[col[e]];
   float t;
   const float* a = R.tab + radial_node(R, pair, dist[e], t);
@@ -305,11 +317,16 @@ __global__ __launch_bounds__(64 * kEvWaves) void k_radial_eval_bwd(RadialTab R, 
                                                                    const int32_t* __restrict__ edge_row,
                                                                    const int32_t* __restrict__ col,
                                                                    const float* __restrict__ dist, int64_t n_edges,
+                                                                   const int32_t* __restrict__ e_end,
                                                                    const float* __restrict__ grad,
                                                                    float* __restrict__ ddist) {
   const int64_t e = (int64_t)blockIdx.x * kEvWaves + (threadIdx.x >> 6);
   if (e >= n_edges) return;
   const int lane = threadIdx.x & 63;
+  if (past_end(e, e_end)) {
+    if (lane == 0) ddist[e] = 0.f;
+    return;
+  }
   const int pair = atom_type[edge_row[e]] * R.n_types + atom_type[col[e]];
   float t;
   const float* a = R.tab + radial_node(R, pair, dist[e], t);
@@ -409,7 +426,8 @@ static int radial_eval_check(const float* tab, int32_t n_types, int32_t n_nodes,
 
 E2V2_API int e2v2_radial_eval(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
                               const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
-                              const float* dist, int64_t n_edges, float* out, hipStream_t s) {
+                              const float* dist, int64_t n_edges, const int32_t* e_end, float* out,
+                              hipStream_t s) {
   if (int rc = radial_eval_check(tab, n_types, n_nodes, h, nc, atom_type, edge_row, col, dist, n_edges,
                                  "radial_eval"))
     return rc;
@@ -417,15 +435,15 @@ E2V2_API int e2v2_radial_eval(const float* tab, int32_t n_types, int32_t n_nodes
   E2V2_REQUIRE(out, "radial_eval: out is NULL");
   const RadialTab R{tab, n_types, n_nodes, nc, 1.0f / h};
   hipLaunchKernelGGL(k_radial_eval, dim3((unsigned)((n_edges + kEvWaves - 1) / kEvWaves)), dim3(64 * kEvWaves), 0, s,
-                     R, atom_type, edge_row, col, dist, n_edges, out);
+                     R, atom_type, edge_row, col, dist, n_edges, e_end, out);
   E2V2_LAUNCHED("k_radial_eval");
   return 0;
 }
 
 E2V2_API int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
                                   const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
-                                  const float* dist, int64_t n_edges, const float* grad, float* ddist,
-                                  hipStream_t s) {
+                                  const float* dist, int64_t n_edges, const int32_t* e_end, const float* grad,
+                                  float* ddist, hipStream_t s) {
   if (int rc = radial_eval_check(tab, n_types, n_nodes, h, nc, atom_type, edge_row, col, dist, n_edges,
                                  "radial_eval_bwd"))
     return rc;
@@ -433,7 +451,7 @@ E2V2_API int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, int32_t n_n
   E2V2_REQUIRE(grad && ddist, "radial_eval_bwd: grad or ddist is NULL");
   const RadialTab R{tab, n_types, n_nodes, nc, 1.0f / h};
   hipLaunchKernelGGL(k_radial_eval_bwd, dim3((unsigned)((n_edges + kEvWaves - 1) / kEvWaves)), dim3(64 * kEvWaves),
-                     0, s, R, atom_type, edge_row, col, dist, n_edges, grad, ddist);
+                     0, s, R, atom_type, edge_row, col, dist, n_edges, e_end, grad, ddist);
   E2V2_LAUNCHED("k_radial_eval_bwd");
   return 0;
 }

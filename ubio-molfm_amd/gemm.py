@@ -141,6 +141,12 @@ def gemm(a, pw: PackedWeight, out: torch.Tensor, widx: Optional[Sequence[int]] =
         sg, k1, k2 = gate
         if sg.dtype != torch.float32 or sg.dim() != 2 or sg.stride(1) != 1 or sg.shape[0] != _as3(out).shape[1]:
             raise ValueError("gemm: gate logits must be fp32 [m, ld] with contiguous rows")
+        # the logit columns read (k of them per weight index) must lie inside the view, not merely inside
+        # its row stride: a narrowed view s[:, :w] of a wider tensor would read past its own columns
+        nb = _as3(out).shape[0]
+        top = max(int(g.widx[b]) for b in range(1, nb)) + 1 if nb > 1 else 0
+        if pw.k * max(top, 1) > sg.shape[1]:
+            raise ValueError(f"gemm: gate logits of {sg.shape[1]} columns, the batches read {pw.k * max(top, 1)}")
         _lib.call("e2v2_gemm_s3_gated", _lib.C.byref(g), _lib.vp(sg.data_ptr()), _lib.i64(sg.stride(0)),
                   _lib.f32(k1), _lib.f32(k2), st)
     else:

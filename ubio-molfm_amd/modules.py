@@ -1370,8 +1370,9 @@ class E2AttentionArbOrder_sparse(nn.Module):
         if self.tp_type == "QKdot_alpha":
             x0 = ShContractFn.apply(_sh_integral(ctx.dvec), xd, nl).reshape(E, -1)    # [E, 3 Cd]
             return _linear(x0 * rad, self.fc_m0)
-        sv = self.sum_vec.detach()
-        if not torch.equal(sv.cpu(), self._sum_vec_blocks()):
+        # checked once per version of sum_vec (a host readback), not on every evaluation
+        if not cached(self, "sum_vec_ok", (self.sum_vec,),
+                      lambda: torch.equal(self.sum_vec.detach().cpu(), self._sum_vec_blocks())):
             raise NotImplementedError("QKdotS_alpha: sum_vec must keep its l-block indicator values")
         x0 = ShContractFn.apply(_raw_sh(ctx.dvec), xd, nl).reshape(E, -1)[:, :H]     # [E, H]
         dl = self.direction_linear

@@ -378,8 +378,10 @@ class RadialEvalFn(torch.autograd.Function):
 
 
 def _radial_eval_args(nl: NeighborList, atom_type, table: RadialTable, dist):
+    # e_end = row_ptr[N] on the device: a capacity build's slots past the real edges are not read
+    e_end = _lib.vp(nl.row_ptr.data_ptr() + 4 * nl.n_atoms) if nl.n_edges else None
     return (_p(table.tab), _lib.i32(table.n_types), _lib.i32(table.n_nodes), _lib.f32(table.h),
-            _lib.i32(table.nc), _p(atom_type), _p(nl.edge_row), _p(nl.col), _p(dist), _lib.i64(nl.n_edges))
+            _lib.i32(table.nc), _p(atom_type), _p(nl.edge_row), _p(nl.col), _p(dist), _lib.i64(nl.n_edges), e_end)
 
 
 class ShContractFn(torch.autograd.Function):
