@@ -142,14 +142,18 @@ PROJ_FLOPS["e2v2_qk_proj_bwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
 SPLIT_PRODUCTS = 6
 SPLIT_ENTRIES = ("e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3", "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated")
 
-KERNELS_OF = {"e2v2_attn_fwd": ["k_attn_fwd_sl"],
-              "e2v2_attn_bwd": ["k_attn_bwd_row_sl", "k_attn_bwd_col_grp", "k_edge_part_sum"],
-              "e2v2_deg_fwd": ["k_deg_fwd_sl"], "e2v2_deg_bwd": ["k_deg_bwd_sl", "k_edge_part_sum"],
-              "e2v2_nbr_count": ["k_nbr_count"],
-              "e2v2_qk_proj_fwd": ["k_qk_proj_fwd"], "e2v2_qk_proj_bwd": ["k_qk_proj_bwd"],
-              "e2v2_qk_proj_fwd_s3": ["k_qk_s3_fwd"], "e2v2_qk_proj_bwd_s3": ["k_qk_s3_bwd"],
-              "e2v2_gemm_s3": ["k_gemm_s3"], "e2v2_gemm_s3_grouped": ["k_gemm_s3_grp"],
-              "e2v2_gemm_s3_gated": ["k_gemm_s3_gate"]}
+# Kernels of each library entry point with their dispatches per call: e2v2_attn_bwd runs the row pass and
+# the column pass once per head group (4 groups) and one partial sum.  k_edge_part_sum serves both the
+# attention and the degree backward with the same [8][E][4] -> [E][4] shape, so its mean per dispatch is
+# that of either.
+KERNELS_OF = {"e2v2_attn_fwd": [("k_attn_fwd_sl", 1)],
+              "e2v2_attn_bwd": [("k_attn_bwd_row_sl", 4), ("k_attn_bwd_col_grp", 4), ("k_edge_part_sum", 1)],
+              "e2v2_deg_fwd": [("k_deg_fwd_sl", 1)], "e2v2_deg_bwd": [("k_deg_bwd_sl", 1), ("k_edge_part_sum", 1)],
+              "e2v2_nbr_count": [("k_nbr_count", 1)],
+              "e2v2_qk_proj_fwd": [("k_qk_proj_fwd", 1)], "e2v2_qk_proj_bwd": [("k_qk_proj_bwd", 1)],
+              "e2v2_qk_proj_fwd_s3": [("k_qk_s3_fwd", 1)], "e2v2_qk_proj_bwd_s3": [("k_qk_s3_bwd", 1)],
+              "e2v2_gemm_s3": [("k_gemm_s3", 1)], "e2v2_gemm_s3_grouped": [("k_gemm_s3_grp", 1)],
+              "e2v2_gemm_s3_gated": [("k_gemm_s3_gate", 1)]}
 
 
 def expanded_nodes(nl) -> int:
@@ -167,21 +171,33 @@ def expanded_nodes(nl) -> int:
     return N + int(torch.unique(keys).numel())
 
 
-def traffic_from_profile(entry, bf16=False, config=4):
-    """HBM-side bytes per call of a library entry point (sum over its kernels)
-    from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the fp32
-    configs[3] workload (--config 4), calibrated against a plain copy; None when
-    the entry point, its precision or the workload is not covered by the summary."""
-    path = ROOT / "profiles" / "hbm_traffic_cfg4_md10k.txt"
-    ks = KERNELS_OF.get(entry)
-    if ks is None or not path.exists() or bf16 or config != 4:
-        return None
-    found = {}
+TRAFFIC_PROFILE = ROOT / "profiles" / "hbm_traffic_cfg4_md10k.txt"
+
+
+def profile_traffic_per_dispatch(path=TRAFFIC_PROFILE):
+    """{kernel: HBM-side bytes per dispatch} of a committed FETCH_SIZE/WRITE_SIZE
+    summary (its traffic_GB column, already scaled by the copy calibration)."""
+    out = {}
     for line in path.read_text().splitlines():
         parts = line.split()
-        if parts and parts[0] in ks and len(parts) == 4:
-            found[parts[0]] = float(parts[3]) * 1e9
-    return sum(found.values()) if len(found) == len(ks) else None
+        if len(parts) == 4 and not line.startswith("#") and parts[0] != "kernel":
+            out[parts[0]] = float(parts[3]) * 1e9
+    return out
+
+
+def traffic_from_profile(entry, bf16=False, config=4):
+    """HBM-side bytes per call of a library entry point: the sum over its kernels
+    of bytes per dispatch times dispatches per call, from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary of the fp32 configs[3] workload (--config 4),
+    calibrated against a plain copy; None when the entry point, its precision or
+    the workload is not covered by the summary."""
+    ks = KERNELS_OF.get(entry)
+    if ks is None or not TRAFFIC_PROFILE.exists() or bf16 or config != 4:
+        return None
+    per = profile_traffic_per_dispatch()
+    if any(k not in per for k, _ in ks):
+        return None
+    return sum(per[k] * n for k, n in ks)
 
 
 def _cpu_model() -> str:
@@ -194,19 +210,52 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(pkg, config: int = 4, sample: str = "default"):
+# host memory the restated path needs for one evaluation of configs[3]'s own 10,000-atom system
+# (~100 GB measured, with margin), and what that evaluation takes on 16 host threads (~60 s)
+FULL_CFG4_HOST_BYTES = 128 * 2**30
+
+
+def mem_available() -> int:
+    """MemAvailable of /proc/meminfo in bytes (0 when unreadable)."""
+    try:
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemAvailable:"):
+                return int(line.split()[1]) * 1024
+    except (OSError, ValueError, IndexError):
+        pass
+    return 0
+
+
+def cpu_sample_choice(config: int, sample: str, avail: int):
+    """(full system?, reason) of the CPU baseline's sample: "auto" times
+    configs[3]'s own system when the host has the memory for it, else the
+    2,000-atom sample of its recipe."""
+    if config != 4:
+        return config in (1, 2, 3), "the configuration's own system"
+    if sample == "full":
+        return True, "requested with --cpu-sample full"
+    if sample == "default":
+        return False, "requested with --cpu-sample default"
+    if avail >= FULL_CFG4_HOST_BYTES:
+        return True, f"MemAvailable {avail / 2**30:.0f} GiB covers the ~100 GB the full system needs"
+    return False, (f"MemAvailable {avail / 2**30:.0f} GiB is below the {FULL_CFG4_HOST_BYTES / 2**30:.0f} GiB "
+                   "the full 10,000-atom system needs, so a 2,000-atom sample of its recipe is timed")
+
+
+def cpu_baseline(pkg, config: int = 4, sample: str = "auto"):
     """The restated reference path (oracle/, torch CPU fp32; the attention's QK
     and value aggregation edge-chunked above 2^18 edges) timed on all host cores
     in this process's affinity, after a warm-up on a 12-atom cell, with the exact
-    cell-list neighbour list.  Samples of each workload (default):
+    cell-list neighbour list.  Samples of each workload:
     config 1: the full 648-atom water box, one evaluation;
     config 2: the full 64-molecule batch, graph by graph;
     config 3: the full 1,500-atom system, one evaluation;
-    config 4: a 2,000-atom periodic water/protein mix built by its recipe (same
-    density and element ratios), one evaluation;
-    config 5: not run (hours per evaluation on the host), None.
-    ``sample="full"`` evaluates configs[3]'s own 10,000-atom system once
-    (minutes of host time and ~100 GB of RAM)."""
+    config 4: configs[3]'s own 10,000-atom system, one evaluation (~60 s on 16
+    threads, ~100 GB of RAM) when MemAvailable covers it ("auto", the default, or
+    "full"); otherwise ("default", or too little memory) a 2,000-atom periodic
+    water/protein mix built by its recipe (same density and element ratios), one
+    evaluation;
+    config 5: not run (hours per evaluation on the host), None."""
     import numpy as np
     import torch
     from ubio_molfm_amd import systems
@@ -219,12 +268,15 @@ def cpu_baseline(pkg, config: int = 4, sample: str = "default"):
     torch.manual_seed(0)
     om = OracleModel().eval()
     energy_forces_with_neighbors(om, systems.small_water(4, 5.5, seed=1))
-    if config == 3 or (config == 4 and sample == "full"):
+    full, why = cpu_sample_choice(config, sample, mem_available())
+    print(f"[cpu baseline] configs[{config - 1}]: {'full system' if full else 'sample'} ({why})",
+          file=sys.stderr, flush=True)
+    if config == 3 or (config == 4 and full):
         graphs = [systems.CONFIGS[config]()]
-        what = f"the full configs[{config - 1}] system ({len(graphs[0]['pos'])} atoms, {{e}} edges)"
+        what = f"the full configs[{config - 1}] system ({len(graphs[0]['pos'])} atoms, {{e}} edges; {why})"
     elif config == 4:
         graphs = [systems.solvated_chains(2000, seed=0)]
-        what = f"2,000-atom periodic water/protein mix (configs[{config - 1}] recipe, {{e}} edges)"
+        what = f"2,000-atom periodic water/protein mix (configs[{config - 1}] recipe, {{e}} edges; {why})"
     elif config == 1:
         graphs = [systems.CONFIGS[1]()]
         what = "the full configs[0] water box (648 atoms, {e} edges)"
@@ -269,9 +321,10 @@ def main():
     ap.add_argument("--exact-nbr", action="store_true",
                     help="MD: exact neighbour builds with one count readback per step instead of capacity builds "
                          "checked one step later")
-    ap.add_argument("--cpu-sample", choices=["default", "full"], default="default",
-                    help="CPU baseline sample: a bounded sample of the workload (default) or, for configs 3 "
-                         "and 4, the configuration's own system (one evaluation)")
+    ap.add_argument("--cpu-sample", choices=["auto", "default", "full"], default="auto",
+                    help="CPU baseline sample of configs[3]: its own 10,000-atom system when the host's "
+                         "MemAvailable covers it, else a 2,000-atom sample (auto); always the sample (default); "
+                         "always the full system (full)")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one plain 256 MiB device copy first (scale reference for FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()

@@ -31,12 +31,56 @@ def test_attention_bytes_split_by_activation_type():
     assert bench.deg_fwd_table_bytes(E) == 4 * E * 768 * 6 and bench.deg_bwd_table_bytes(E) == 4 * E * 768 * 8
 
 
+def _trace_calls():
+    """{kernel: dispatches} of the committed kernel trace of the same workload."""
+    calls = {}
+    for line in (ROOT / "profiles" / "kernel_trace_cfg4_md10k.txt").read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 5 and not line.startswith("#") and parts[0].isdigit():
+            calls[parts[4]] = int(parts[0])
+    return calls
+
+
+def test_profile_traffic_counts_every_dispatch_of_a_call():
+    """The traffic of e2v2_attn_bwd per call, rebuilt from the two committed
+    profiles on their own: dispatches per call from the kernel trace (one degree
+    embedding and four attention layers per evaluation; k_edge_part_sum also runs
+    once per degree backward) times the traffic per dispatch of the PMC summary.
+    bench.py must agree within 1%; counting each kernel once (the old error)
+    would report under half of it."""
+    calls = _trace_calls()
+    per = bench.profile_traffic_per_dispatch()
+    n_eval = calls["k_deg_fwd_sl"]
+    n_attn = 4 * n_eval
+    assert calls["k_attn_fwd_sl"] == n_attn
+    disp = {k: calls[k] / n_attn for k in ("k_attn_bwd_row_sl", "k_attn_bwd_col_grp")}
+    disp["k_edge_part_sum"] = (calls["k_edge_part_sum"] - calls["k_deg_bwd_sl"]) / n_attn
+    rebuilt = sum(per[k] * n for k, n in disp.items())
+    got = bench.traffic_from_profile("e2v2_attn_bwd")
+    assert abs(got - rebuilt) <= 0.01 * rebuilt, (got, rebuilt, disp)
+    assert got > 1.5 * sum(per[k] for k in disp)
+    fwd = bench.traffic_from_profile("e2v2_attn_fwd")
+    assert abs(fwd - per["k_attn_fwd_sl"] * calls["k_attn_fwd_sl"] / n_attn) <= 0.01 * fwd
+
+
 def test_profile_traffic_only_for_the_profiled_workload():
     t = bench.traffic_from_profile("e2v2_attn_bwd")
     assert t is not None and t > 1e9
     assert bench.traffic_from_profile("e2v2_attn_bwd", bf16=True) is None
     assert bench.traffic_from_profile("e2v2_attn_bwd", False, 5) is None
     assert bench.traffic_from_profile("e2v2_not_an_entry") is None
+
+
+def test_cpu_sample_choice_follows_host_memory():
+    """configs[3]'s CPU baseline times the full system when MemAvailable covers
+    it and says why it falls back to the 2,000-atom sample otherwise."""
+    big, small = 200 * 2**30, 64 * 2**30
+    assert bench.cpu_sample_choice(4, "auto", big)[0] is True
+    full, why = bench.cpu_sample_choice(4, "auto", small)
+    assert full is False and "64 GiB" in why and "2,000-atom" in why
+    assert bench.cpu_sample_choice(4, "full", small)[0] is True
+    assert bench.cpu_sample_choice(4, "default", big)[0] is False
+    assert bench.cpu_sample_choice(3, "auto", small)[0] is True
 
 
 def test_more_than_one_gpu_exits_with_message():
