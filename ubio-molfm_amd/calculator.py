@@ -23,16 +23,21 @@ the model lifecycle of src/molfm/interface/model_interface.py:64-281:
     periodic systems wrapped into the primary cell first (:239-246, ASE's
     ``wrap`` with eps = 1e-7), charge = sum of the initial charges and
     multiplicity 1 (interface/data_utils.py:20-33), numpy / float back;
-* per-atom reference energies: with ``add_ref_energy`` the sum of
-  ``ref_energy[Z]`` is added per system (:187-189, :258-262).  The per-head
-  tables come from the reference's data module (molfm/data/utils.py
-  ``get_data_defult_config``), which is not part of this package: pass the
-  table as ``ref_energy`` (eV per atomic number).  The sum is formed on the
-  host in float64 (deterministic; the energy is then float64, as the
-  reference's float32 + float64 sum is).
+* per-atom reference energies: with ``add_ref_energy`` (the default) the sum
+  of ``ref_energy[Z]`` is added per system (:187-192, :255-260), where
+  ``ref_energy = atom_reference * unit`` of the head (model_interface.py:208-223):
+  the per-head tables of molfm/data/utils.py ``get_data_defult_config``,
+  shipped as data in ``atom_reference.json`` and matched on ``head_name``
+  as that function does (``startswith("svp")``, ``startswith("tzvpd")``,
+  ``== "oc20"``, ``== "omol25"``, ``== "oc22"`` on the lower-cased name, in that
+  order; any other name: zeros, unit 1).  An explicit ``ref_energy`` (eV per
+  atomic number) replaces the head's table.  The sum is formed on the host in
+  float64 (deterministic; the energy is then float64, as the reference's
+  float32 + float64 sum is).
 """
 from __future__ import annotations
 
+import json
 import os
 from pathlib import Path
 from types import SimpleNamespace
@@ -45,6 +50,29 @@ import yaml
 from .model import MolfmAtomic, default_args
 
 ALL_CHANGES = ["positions", "numbers", "cell", "pbc", "initial_charges", "initial_magmoms"]
+
+_ATOM_REF = None
+
+
+def atom_reference(head_name: str):
+    """(atom_reference [n] float64, unit) of a head: the first table of
+    ``atom_reference.json`` whose test matches ``head_name.lower()``
+    (molfm/data/utils.py:17-289), else the default (zeros, unit 1)."""
+    global _ATOM_REF
+    if _ATOM_REF is None:
+        _ATOM_REF = json.loads((Path(__file__).resolve().parent / "atom_reference.json").read_text())
+    name = str(head_name).lower()
+    for h in _ATOM_REF["heads"]:
+        if (h["match"] == "startswith" and name.startswith(h["key"])) or (h["match"] == "eq" and name == h["key"]):
+            return np.asarray(h["atom_reference"], np.float64), float(h["unit"])
+    d = _ATOM_REF["default"]
+    return np.asarray(d["atom_reference"], np.float64), float(d["unit"])
+
+
+def head_ref_energy(head_name: str) -> np.ndarray:
+    """ref_energy = atom_reference * unit of the head (model_interface.py:222), eV per Z."""
+    ref, unit = atom_reference(head_name)
+    return ref * unit
 
 
 def resolve_config_file(config_path: Optional[str], config_name: Optional[str],
@@ -181,7 +209,12 @@ class E2FormerCalculator:
         self.recompute_budget = recompute_budget
         self.config_file = None
         self.model = None
-        self.ref_energy = None if ref_energy is None else np.asarray(_np(ref_energy, np.float64), np.float64)
+        if ref_energy is not None:
+            self.ref_energy = np.asarray(_np(ref_energy, np.float64), np.float64)
+        elif head_name is not None:
+            self.ref_energy = head_ref_energy(head_name)
+        else:
+            self.ref_energy = None
         if model is not None:
             self.model = model.eval().to(self.device).requires_grad_(False)
         elif auto_setup:
@@ -276,6 +309,9 @@ class E2FormerCalculator:
         ref = None
         if self.add_ref_energy and self.ref_energy is not None:
             zs = Zt.cpu().numpy()
+            if zs.size and (zs.min() < 0 or zs.max() >= len(self.ref_energy)):
+                raise IndexError(f"reference energies of head {self.head_name!r} cover Z < {len(self.ref_energy)}, "
+                                 f"got Z = {int(zs.max())}")
             ref = np.array([self.ref_energy[zs[ptr[g]:ptr[g + 1]]].sum() for g in range(B)], np.float64)
         out = []
         for g in range(B):
