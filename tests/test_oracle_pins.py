@@ -385,3 +385,93 @@ def test_so2_grouped_layout_is_a_permutation():
                 assert a[t] == start + m * cnt * 256 and ld[t] == cnt * 256 and col[t] == p * 256
                 t += 1
     assert t == 20
+
+
+# --------------------------------------------------------------------------- decoder composition (e2former.py:1052-1117)
+
+def _identity_blocks(dec):
+    """Zero every block's last projections (the attention's proj_first /
+    proj_zero and the FFN's slinear_2, weights and biases): with the pre-norm
+    residual form x -> x + ga(norm_1(x)), x -> x + ffn(norm_ffn(x)) every block
+    is then the identity map, whatever the attention and FFN compute inside."""
+    blocks = list(dec.blocks) + list(getattr(dec, "long_blocks", []))
+    with torch.no_grad():
+        for blk in blocks:
+            proj = blk.ga.proj_zero if hasattr(blk.ga, "proj_zero") else blk.ga.proj_first
+            for lin in (proj, blk.ffn.slinear_2):
+                lin.weight.zero_()
+                lin.bias.zero_()
+
+
+def _randomise_norms(dec, gen):
+    """Affine weights and biases of the decoder's RMS norms away from (1, 0), so
+    that each norm is a distinct map."""
+    with torch.no_grad():
+        for name in ("norm_final", "pre_norm_node", "norm_cluster"):
+            if hasattr(dec, name):
+                n = getattr(dec, name)
+                n.affine_weight.copy_(0.5 + torch.rand(n.affine_weight.shape, generator=gen))
+                n.affine_bias.copy_(torch.randn(n.affine_bias.shape, generator=gen))
+
+
+def _decoder_io(m, bd):
+    """(degree embedding output [N, 9, C], decoder output of the real atoms)."""
+    got = {}
+    dec = m.decoder.decoder
+    h1 = dec.edge_deg_embed_dense.register_forward_hook(lambda mod, i, o: got.__setitem__("deg", o))
+    h2 = dec.register_forward_hook(lambda mod, i, o: got.__setitem__("out", o[2]))
+    try:
+        with torch.no_grad():
+            m(bd, need_force=False)
+    finally:
+        h1.remove(); h2.remove()
+    return got["deg"], got["out"][bd["atom_masks"]]
+
+
+def test_decoder_with_identity_blocks_is_norm_final_of_degree_embedding():
+    """With every block the identity, the decoder output equals
+    norm_final(degree embedding) (e2former.py:1052-1087, 1119-1120).  Catches a
+    residual taken after norm_1 or norm_ffn (the output would carry that norm),
+    a missing residual (the output would be norm_final(0)), the sys embedding
+    added outside the normed input, and a norm_final skipped or applied twice."""
+    from ubio_molfm_amd import systems
+    torch.manual_seed(41)
+    m = om.MolfmAtomic(num_layers=2).eval()
+    dec = m.decoder.decoder
+    _identity_blocks(dec)
+    _randomise_norms(dec, torch.Generator().manual_seed(42))
+    s = systems.small_water(4, 5.5, seed=43)
+    bd = systems.to_padded(s)
+    bd["charge"] = torch.tensor([1], dtype=torch.int32)
+    bd["multiplicity"] = torch.tensor([2], dtype=torch.int32)
+    deg, out = _decoder_io(m, bd)
+    with torch.no_grad():
+        expect = dec.norm_final(deg)
+    assert deg.abs().max() > 1e-3
+    assert torch.allclose(out, expect, rtol=1e-5, atol=1e-6), float((out - expect).abs().max())
+    assert (out - deg).abs().max() > 1e-2
+
+
+def test_cluster_decoder_with_identity_blocks():
+    """with_cluster="node" and identity blocks: the output equals
+    final_linear(cat[short, norm_cluster(pre_norm_node(short))]) with
+    short = the degree embedding (e2former.py:1088-1117); no norm_final after
+    final_linear.  Catches the [short, long] order swapped, pre_norm_node or
+    norm_cluster dropped or exchanged, and a stray norm_final after
+    final_linear."""
+    from ubio_molfm_amd import systems
+    torch.manual_seed(44)
+    m = om.MolfmAtomic(num_layers=2, with_cluster="node", long_range_layers=1).eval()
+    dec = m.decoder.decoder
+    _identity_blocks(dec)
+    _randomise_norms(dec, torch.Generator().manual_seed(45))
+    s = systems.organics_batch(n_mol=2, nmin=8, nmax=12, seed=46)
+    bd = systems.to_padded(s)
+    deg, out = _decoder_io(m, bd)
+    with torch.no_grad():
+        long = dec.norm_cluster(dec.pre_norm_node(deg))
+        expect = dec.final_linear(torch.cat([deg, long], dim=-1))
+        swapped = dec.final_linear(torch.cat([long, deg], dim=-1))
+    assert torch.allclose(out, expect, rtol=1e-5, atol=1e-6), float((out - expect).abs().max())
+    assert (expect - swapped).abs().max() > 1e-2
+    assert (expect - dec.norm_final(expect)).abs().max() > 1e-2
