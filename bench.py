@@ -138,8 +138,10 @@ PROJ_FLOPS["e2v2_qk_proj_fwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
 PROJ_FLOPS["e2v2_qk_proj_bwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
 PROJ_FLOPS["e2v2_qk_proj_fwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
 PROJ_FLOPS["e2v2_qk_proj_bwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
-# fp32 GEMMs on the split kernels execute six bf16 MFMA products per fp32 multiply-add
+# fp32 GEMMs on the split kernels execute six bf16 MFMA products per fp32 multiply-add; the bf16 mode runs
+# the same kernels on one-piece packs (bf16 operands): one product
 SPLIT_PRODUCTS = 6
+SPLIT_PRODUCTS_BF16 = 1
 SPLIT_ENTRIES = ("e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3", "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated")
 
 # Kernels of each library entry point with their dispatches per call: e2v2_attn_bwd runs the row pass and
@@ -403,14 +405,18 @@ def main():
                        impl_gbs=round(b_imp / sec / 1e9, 1), impl_frac=round(b_imp / sec / 1e9 / HBM_PEAK_GBS, 4),
                        impl_table_bytes_per_launch=b_tab)
         elif k in SPLIT_ENTRIES:
-            # fp32 GEMMs executed as six bf16 MFMA products each: the executed bf16 rate against the bf16
-            # peak (frac, comparable with SQ_VALU_MFMA_BUSY), and the fp32 work rate beside the fp32 peak
+            # fp32 GEMMs executed as six bf16 MFMA products each (one in the bf16 mode): the executed bf16
+            # rate against the bf16 peak (frac, comparable with SQ_VALU_MFMA_BUSY), and in fp32 the fp32 work
+            # rate beside the fp32 peak
             fl = PROJ_FLOPS[k](N) if k in PROJ_FLOPS else v["work"] / v["count"]
             tf = fl / sec / 1e12
-            ent.update(bound="mfma", flops_per_launch=fl, executed_flops_per_launch=SPLIT_PRODUCTS * fl,
-                       achieved_tflops=round(SPLIT_PRODUCTS * tf, 2), peak_tflops=BF16_PEAK_TFLOPS,
-                       frac=round(SPLIT_PRODUCTS * tf / BF16_PEAK_TFLOPS, 4),
-                       fp32_equivalent_tflops=round(tf, 2), fp32_equivalent_over_fp32_peak=round(tf / FP32_PEAK_TFLOPS, 4))
+            prod = SPLIT_PRODUCTS_BF16 if bf16 else SPLIT_PRODUCTS
+            ent.update(bound="mfma", flops_per_launch=fl, executed_flops_per_launch=prod * fl,
+                       achieved_tflops=round(prod * tf, 2), peak_tflops=BF16_PEAK_TFLOPS,
+                       frac=round(prod * tf / BF16_PEAK_TFLOPS, 4))
+            if not bf16:
+                ent.update(fp32_equivalent_tflops=round(tf, 2),
+                           fp32_equivalent_over_fp32_peak=round(tf / FP32_PEAK_TFLOPS, 4))
         elif k in PROJ_FLOPS:
             tf = PROJ_FLOPS[k](N) / sec / 1e12
             pk = BF16_PEAK_TFLOPS if k.endswith("_bf16") else FP32_PEAK_TFLOPS

@@ -461,11 +461,11 @@ int e2v2_ln_silu_bwd(const float* x, const float* g, const float* b, const float
  * b: n_w weights packed by e2v2_gemm_pack; c (and r, which may equal c): fp32 with row / batch strides.
  * Requires n % 128 == 0, k % 16 == 0, 1 <= batch <= 16, 0 <= widx[b] < n_w <= 16. */
 typedef struct {
-  const float* a;
+  const void* a;        /* fp32, or bf16 when a_bf16 */
   int64_t lda, a_bs;
   const void* b;
   int n_w;
-  float* c;
+  void* c;              /* fp32, or bf16 when c_bf16 */
   int64_t ldc, c_bs;
   const float* r;
   int64_t ldr, r_bs;
@@ -474,6 +474,9 @@ typedef struct {
   int bias_batches;
   int m, n, k, batch;
   int widx[16];
+  int pieces;           /* operand pieces of b's packing: 3 (fp32 GEMM) or 1 (bf16 operands, fp32 accumulation) */
+  int a_bf16;           /* 1: a is bf16 in memory (with pieces = 1; lda % 8 == 0) */
+  int c_bf16;           /* 1: c is written as bf16 (rounded once from the fp32 result) */
 } e2v2_gemm_args;
 int e2v2_gemm_s3(const e2v2_gemm_args* args, hipStream_t s);
 /* Up to four independent GEMMs (each as e2v2_gemm_s3, with its own shapes, operands and packed weight) in one
@@ -490,9 +493,11 @@ int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hipStream_t
  * kernel followed by e2v2_gemm_s3. */
 int e2v2_gemm_s3_gated(const e2v2_gemm_args* args, const float* s, int64_t ld_s, float k1, float k2, hipStream_t st);
 /* Pack n_w weights W_w[j][k] = w[w w_stride + j ld_n + k ld_k] (j < n, k < k; so W or W^T of a row-major matrix
- * without a copy) into e2v2_gemm_packed_bytes(n_w, n, k) bytes at packed (16-byte aligned); the bytes needed,
- * or -1 for an unsupported shape. */
-int64_t e2v2_gemm_packed_bytes(int n_w, int n, int k);
+ * without a copy) into e2v2_gemm_packed_bytes(n_w, n, k, pieces) bytes at packed (16-byte aligned); the bytes
+ * needed, or -1 for an unsupported shape.  pieces 3: the exact three-piece split; pieces 1: the bf16 rounding
+ * alone, for the bf16 mode's GEMMs (bf16 operands, fp32 accumulation: one MFMA product, the A operand rounded
+ * to bf16 as it is read, or read as bf16 with a_bf16). */
+int64_t e2v2_gemm_packed_bytes(int n_w, int n, int k, int pieces);
 /* The Q/K projection with its m-contraction (as e2v2_qk_proj_fwd / _bwd above) on the split GEMM.  Pairs
  * p < 2 hid: (q_a, q_b) columns p of the stacked w for p < hid, else (k_a, k_b) columns p - hid.
  *   fwd: wp = the three per-l [4 hid][C] weights packed with their columns in the tile-paired order (128-column
@@ -504,11 +509,11 @@ int64_t e2v2_gemm_packed_bytes(int n_w, int n, int k);
  *        ([C][4 hid + cv]).
  * Requires hid % 64 == 0, C % 16 (fwd) / % 128 (bwd), cv % 16 == 0; operands 16-byte aligned. */
 int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bias, float* y, float* hq, float* hk, int n,
-                        int hid, int c, hipStream_t s);
+                        int hid, int c, int pieces, hipStream_t s);
 int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* ghk, const void* wp, const float* gv,
-                        float* gx, int n, int hid, int c, int cv, hipStream_t s);
-int e2v2_gemm_pack(const float* w, int64_t ld_n, int64_t ld_k, int64_t w_stride, int n_w, int n, int k, void* packed,
-                   hipStream_t s);
+                        float* gx, int n, int hid, int c, int cv, int pieces, hipStream_t s);
+int e2v2_gemm_pack(const float* w, int64_t ld_n, int64_t ld_k, int64_t w_stride, int n_w, int n, int k, int pieces,
+                   void* packed, hipStream_t s);
 
 /* ---- positions --------------------------------------------------------- */
 int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,

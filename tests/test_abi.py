@@ -78,15 +78,21 @@ def test_split_gemm_host_checks(pkg):
     the host, before any HIP call."""
     from ubio_molfm_amd import _lib
     lib = _lib.load()
-    assert lib.e2v2_gemm_packed_bytes(3, 256, 64) == 3 * 2 * 2 * 3 * 512 * 16
-    assert lib.e2v2_gemm_packed_bytes(1, 100, 64) == -1 and lib.e2v2_gemm_packed_bytes(1, 128, 40) == -1
+    assert lib.e2v2_gemm_packed_bytes(3, 256, 64, 3) == 3 * 2 * 2 * 3 * 512 * 16
+    assert lib.e2v2_gemm_packed_bytes(3, 256, 64, 1) == 3 * 2 * 2 * 1 * 512 * 16
+    assert lib.e2v2_gemm_packed_bytes(1, 100, 64, 3) == -1 and lib.e2v2_gemm_packed_bytes(1, 128, 40, 3) == -1
+    assert lib.e2v2_gemm_packed_bytes(1, 128, 64, 2) == -1
     g = _lib.GemmArgs()
     g.a = g.b = g.c = 16                 # never dereferenced: the checks fail first
-    g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w = 64, 128, 10, 128, 64, 2, 1
+    g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w, g.pieces = 64, 128, 10, 128, 64, 2, 1, 3
     g.widx[1] = 1                         # only weight 0 exists
     assert lib.e2v2_gemm_s3(_lib.C.byref(g), None) != 0 and b"widx[1]" in lib.e2v2_last_error()
     g.widx[1], g.n = 0, 100
     assert lib.e2v2_gemm_s3(_lib.C.byref(g), None) != 0 and b"multiple of 128" in lib.e2v2_last_error()
+    g.n, g.a_bf16 = 128, 1               # a bf16 A needs the one-piece packing
+    assert lib.e2v2_gemm_s3(_lib.C.byref(g), None) != 0 and b"one piece" in lib.e2v2_last_error()
+    g.pieces, g.lda = 1, 68              # bf16 rows of 16 bytes: lda % 8 == 0
+    assert lib.e2v2_gemm_s3(_lib.C.byref(g), None) != 0 and b"lda % 8" in lib.e2v2_last_error()
 
 
 def test_grouped_gemm_host_checks(pkg):
@@ -97,9 +103,12 @@ def test_grouped_gemm_host_checks(pkg):
     arr = (_lib.GemmArgs * 4)()
     for g in arr:
         g.a = g.b = g.c = 16                 # never dereferenced: the checks fail first
-        g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w = 64, 128, 10, 128, 64, 1, 1
+        g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w, g.pieces = 64, 128, 10, 128, 64, 1, 1, 3
     assert lib.e2v2_gemm_s3_grouped(arr, 0, None) != 0 and b"groups" in lib.e2v2_last_error()
     assert lib.e2v2_gemm_s3_grouped(arr, 5, None) != 0 and b"groups" in lib.e2v2_last_error()
+    arr[1].pieces = 1                        # the groups of one launch share the operand pieces
+    assert lib.e2v2_gemm_s3_grouped(arr, 3, None) != 0 and b"share the operand pieces" in lib.e2v2_last_error()
+    arr[1].pieces = 3
     arr[2].k = 40
     assert lib.e2v2_gemm_s3_grouped(arr, 3, None) != 0 and b"multiple of 16" in lib.e2v2_last_error()
 
@@ -111,7 +120,7 @@ def test_gated_gemm_host_checks(pkg):
     lib = _lib.load()
     g = _lib.GemmArgs()
     g.a = g.b = g.c = 16                 # never dereferenced: the checks fail first
-    g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w = 64, 128, 10, 128, 64, 3, 3
+    g.lda, g.ldc, g.m, g.n, g.k, g.batch, g.n_w, g.pieces = 64, 128, 10, 128, 64, 3, 3, 3
     g.widx[0], g.widx[1], g.widx[2] = 0, 1, 2
     f = _lib.C.c_float
     assert lib.e2v2_gemm_s3_gated(_lib.C.byref(g), _lib.C.c_void_p(16), _lib.C.c_int64(128), f(1.0), f(1.0),

@@ -260,3 +260,109 @@ def test_list_operands_either_order(pkg, cuda):
         out = torch.empty(2, m, n, device=cuda)
         gemm.gemm(xs, pw, out, list(order), bias=bias[list(order)].contiguous(), bias_batches=2)
         assert torch.equal(out[0], refs[order[0]]) and torch.equal(out[1], refs[order[1]])
+
+
+# --------------------------------------------------------------------------- one-piece packs: the bf16 mode
+
+def _bf(t):
+    return t.to(torch.bfloat16).double()
+
+
+@pytest.mark.parametrize("a_dtype,c_dtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+                                             (torch.float32, torch.bfloat16), (torch.bfloat16, torch.bfloat16)])
+def test_bf16_gemm_against_float64_on_rounded_operands(pkg, cuda, a_dtype, c_dtype):
+    """One-piece packs (the bf16 mode's GEMMs: bf16 operands, fp32 accumulation):
+    A read as fp32 and rounded to bf16 as the kernel reads it, or read as bf16;
+    the result against the float64 product of the bf16-rounded operands, within
+    fp32 accumulation error (8 u sqrt(k) of the GEMM's own scale), plus one bf16
+    rounding when C is written as bf16.  A bias on batch 0, a residual and three
+    weights over five batches."""
+    from ubio_molfm_amd import gemm
+    g = torch.Generator().manual_seed(11)
+    batch, m, n, k = 5, 333, 256, 768
+    a = _wide_range((batch, m, k), g, spread=4.0)
+    w = _wide_range((3, n, k), g, spread=4.0) / k
+    bias = torch.randn(n, generator=g)
+    widx = [0, 1, 2, 1, 0]
+    pw = gemm.pack(w.to(cuda), pieces=1)
+    assert pw.pieces == 1
+    out = torch.empty(batch, m, n, device=cuda, dtype=c_dtype)
+    res = None
+    if c_dtype == torch.float32:
+        res = torch.randn(batch, m, n, generator=g)
+        out.copy_(res.to(cuda))
+    gemm.gemm(a.to(cuda).to(a_dtype), pw, out, widx, bias=bias.to(cuda), bias_batches=1,
+              res=None if res is None else out)
+    a64, w64 = _bf(a), _bf(w[widx])
+    b64 = torch.zeros(batch, 1, n, dtype=torch.float64)
+    b64[0, 0] = bias.double()
+    err = _scaled_err(out.float(), a64, w64, res64=None if res is None else res.double(), bias64=b64)
+    tol = 8 * U * math.sqrt(k) + (2.0 ** -8 if c_dtype == torch.bfloat16 else 0.0)
+    print(f"[bf16 gemm] A {a_dtype} C {c_dtype}: {err / U:.2f} u (tol {tol / U:.0f} u)", flush=True)
+    assert err <= tol
+    # exactly one product: the second and third pieces of either operand must not enter
+    ex = _scaled_err(out.float(), a.double(), w[widx].double(), res64=None if res is None else res.double(),
+                     bias64=b64)
+    assert ex > 8 * U * math.sqrt(k)
+
+
+def test_bf16_gemm_gated_and_grouped_match_separate_launches(pkg, cuda):
+    """The gated and the grouped forms on one-piece packs equal, bitwise, the gate
+    kernel followed by the plain GEMM and the separate launches of the same
+    problems (the same products in the same order)."""
+    from ubio_molfm_amd import gemm, modules, _lib
+    g = torch.Generator().manual_seed(12)
+    n_rows, C = 700, 256
+    h = torch.randn(9, n_rows, C, generator=g).to(cuda)
+    sc = torch.randn(n_rows, 3 * C, generator=g).to(cuda)
+    w2 = (torch.randn(3, C, C, generator=g) / 16).to(cuda)
+    pw = gemm.pack(w2, pieces=1)
+    widx = modules._m_degrees(2)
+    k1, k2 = modules.SILU_NORM, modules.SIGMOID_NORM
+    y_g = torch.empty(9, n_rows, C, device=cuda)
+    gemm.gemm(h, pw, y_g, widx, gate=(sc, k1, k2))
+    gated = torch.empty_like(h)
+    _lib.call("e2v2_gate_fwd", _lib.vp(sc.data_ptr()), _lib.vp(h.data_ptr()), _lib.vp(gated.data_ptr()),
+              _lib.i32(n_rows), _lib.f32(k1), _lib.f32(k2), _lib.vp(torch.cuda.current_stream().cuda_stream))
+    y_s = torch.empty_like(y_g)
+    gemm.gemm(gated, pw, y_s, widx)
+    assert torch.equal(y_g, y_s)
+    a1 = torch.randn(2, 300, 512, generator=g).to(cuda).to(torch.bfloat16)
+    a2 = torch.randn(3, 500, 256, generator=g).to(cuda).to(torch.bfloat16)
+    p1 = gemm.pack((torch.randn(2, 256, 512, generator=g) / 16).to(cuda), pieces=1)
+    p2 = gemm.pack((torch.randn(1, 384, 256, generator=g) / 16).to(cuda), pieces=1)
+    o1 = torch.empty(2, 300, 256, device=cuda)
+    o2 = torch.empty(3, 500, 384, device=cuda, dtype=torch.bfloat16)
+    gemm.gemm_grouped([{"a": a1, "pw": p1, "out": o1}, {"a": a2, "pw": p2, "out": o2, "widx": [0, 0, 0]}])
+    r1, r2 = torch.empty_like(o1), torch.empty_like(o2)
+    gemm.gemm(a1, p1, r1)
+    gemm.gemm(a2, p2, r2, [0, 0, 0])
+    assert torch.equal(o1, r1) and torch.equal(o2, r2)
+    with pytest.raises(ValueError):                                   # a bf16 A needs a one-piece packing
+        gemm.gemm(a1[0], gemm.pack((torch.randn(256, 512, generator=g)).to(cuda)), o1[0])
+
+
+def test_qk_proj_one_piece_against_float64(pkg, cuda):
+    """The Q/K projection kernels on one-piece packs: forward against float64 of
+    the bf16-rounded weights and input (the input rounded in the kernel), at
+    fp32 accumulation error."""
+    from ubio_molfm_amd import gemm
+    torch.manual_seed(9)
+    n, hid, C, Cv = 300, 512, 256, 256
+    W = torch.randn(3, 4 * hid, C, device=cuda) / 16
+    b = torch.randn(4 * hid, device=cuda)
+    Wv = torch.randn(3, Cv, C, device=cuda) / 16
+    P = gemm.pack_qk(W, b, Wv, pieces=1)
+    x = torch.randn(9, n, C, device=cuda)
+    hq, hk, _ = gemm.qk_forward(x, P)
+    idx = torch.tensor([0, 1, 1, 1, 2, 2, 2, 2, 2])
+    x64, W64 = _bf(x.cpu()), _bf(W.cpu())
+    y = torch.einsum("mnc,moc->mno", x64, W64[idx])
+    y[0] += b.cpu().double()
+    ref = [torch.stack([(y[a:c, :, o0:o0 + hid] * y[a:c, :, o1:o1 + hid]).sum(0)
+                        for (a, c) in ((0, 1), (1, 4), (4, 9))], 1).reshape(n, 3 * hid)
+           for (o0, o1) in ((0, hid), (2 * hid, 3 * hid))]
+    for got, r in zip((hq, hk), ref):
+        rel = float((got.cpu().double() - r).norm() / r.norm())
+        print(f"[qk one-piece] rel {rel:.2e}", flush=True)
+        assert rel < 2e-5

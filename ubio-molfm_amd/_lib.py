@@ -80,7 +80,8 @@ class DegArgs(C.Structure):
 class GemmArgs(C.Structure):
     _fields_ = [("a", vp), ("lda", i64), ("a_bs", i64), ("b", vp), ("n_w", i32), ("c", vp), ("ldc", i64), ("c_bs", i64),
                 ("r", vp), ("ldr", i64), ("r_bs", i64), ("bias", vp), ("bias_bs", i64), ("bias_batches", i32),
-                ("m", i32), ("n", i32), ("k", i32), ("batch", i32), ("widx", i32 * 16)]
+                ("m", i32), ("n", i32), ("k", i32), ("batch", i32), ("widx", i32 * 16), ("pieces", i32),
+                ("a_bf16", i32), ("c_bf16", i32)]
 
 
 _lib = None
@@ -103,7 +104,7 @@ def load():
     lib.e2v2_deg_bwd_workspace.restype = C.c_size_t
     lib.e2v2_deg_bwd_workspace.argtypes = [C.c_int64]
     lib.e2v2_gemm_packed_bytes.restype = C.c_int64
-    lib.e2v2_gemm_packed_bytes.argtypes = [C.c_int32, C.c_int32, C.c_int32]
+    lib.e2v2_gemm_packed_bytes.argtypes = [C.c_int32, C.c_int32, C.c_int32, C.c_int32]
     _lib = lib
     return lib
 

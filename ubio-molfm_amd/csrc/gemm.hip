@@ -59,11 +59,17 @@ constexpr int kGAr = kGK / 4;                       // A granules (4 fp32) per r
 constexpr int kGBc = kGK / 8;                       // B granules (8 bf16) per column, piece and stage
 constexpr int kGAg = kGM * kGAr;                    // A granules per stage: 512
 constexpr int kGBg = kGN * kGBc;                    // granules per B piece and stage: 256
-constexpr int kGStage = 16 * (kGAg + 3 * kGBg);     // bytes per LDS buffer: 20 KB
-constexpr int kGBStage = 3 * kGBg;                  // packed granules per (weight, column tile, stage)
-constexpr int kGAi = kGAg / 64, kGBi = kGBStage / 64;   // wave-wide LDS-direct loads per stage: 8 (A), 12 (B)
+constexpr int kGAi = kGAg / 64;                     // wave-wide LDS-direct loads of an fp32 A stage: 8
+// Operand pieces kP: 3 (the exact split above, six products) or 1 (bf16 operands: x0 alone, one product,
+// the bf16 mode's GEMM).  A kept as bf16 in memory (kAB) is its own single piece: 8 bf16 per granule, two
+// granules per row and stage (4 KB).
+__host__ __device__ constexpr int a_stage_bytes(bool kAB) { return kAB ? kGM * kGK * 2 : 16 * kGAg; }
+__host__ __device__ constexpr int g_stage_bytes(int kP, bool kAB) { return a_stage_bytes(kAB) + 16 * kP * kGBg; }
+__host__ __device__ constexpr int b_stage_granules(int kP) { return kP * kGBg; }   // per (weight, column tile, stage)
+constexpr int kGStage = g_stage_bytes(3, false);    // largest LDS buffer: 20 KB
 
 __device__ __forceinline__ int a_slot(int r, int g) { return r * kGAr + (g ^ ((r >> 2) & 3)); }       // granules
+__device__ __forceinline__ int abf_slot(int r, int g) { return r * 2 + (g ^ ((r >> 3) & 1)); }       // bf16 A
 __host__ __device__ __forceinline__ int b_slot(int c, int g) { return c * kGBc + (g ^ ((c >> 3) & 1)); }
 
 // Row of accumulator register r of a 32x32 tile for this lane (column = lane & 31).
@@ -94,6 +100,17 @@ __device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, bf1
   for (int k = 0; k < 3; ++k) p[k] = __builtin_bit_cast(bf16x8, (uint32x4){u[k][0], u[k][1], u[k][2], u[k][3]});
 }
 
+// Eight fp32 values -> their bf16 roundings (the first piece alone).
+__device__ __forceinline__ void round8(const floatx4& x0, const floatx4& x1, bf16x8 (&p)[1]) {
+  p[0] = __builtin_bit_cast(bf16x8, (uint32x4){pk_bf16(x0[0], x0[1]), pk_bf16(x0[2], x0[3]),
+                                               pk_bf16(x1[0], x1[1]), pk_bf16(x1[2], x1[3])});
+}
+template <int kP>
+__device__ __forceinline__ void split_pieces(const floatx4& x0, const floatx4& x1, bf16x8 (&p)[kP]) {
+  if constexpr (kP == 3) split8(x0, x1, p);
+  else round8(x0, x1, p);
+}
+
 // LDS-direct load offsets of an fp32 A tile of 128 rows (row stride lda floats):
 // this wavefront's two loads per stage (ii = wv, wv + 4) fill LDS granules
 // 64 ii .. +63, i.e. rows 16 ii + lane / 4, slot lane % 4, from the source
@@ -117,29 +134,53 @@ __device__ __forceinline__ void load_a(__amdgpu_buffer_rsrc_t r, const uint32_t 
   for (int i = 0; i < kGAi / 4; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(As + (wv + 4 * i) * 1024), 16, voff[i] + koff, 0, 0, 0);
 }
-// The packed B stage ks (contiguous 12 KB from the weight's column-tile base).
+// bf16 A (row stride lda elements): this wavefront's one load per stage fills LDS granules 64 wv .. +63,
+// i.e. rows 32 wv + lane / 2, slot lane % 2, from the source granule that belongs there (byte offset from
+// the tile's first row; the stage's k offset is 32 ks bytes).
+__device__ __forceinline__ uint32_t abf_offset(int wv, int lane, int lda) {
+  const int r = 32 * wv + (lane >> 1), sl = lane & 1;
+  return (uint32_t)(r * lda + 8 * (sl ^ ((r >> 3) & 1))) * 2u;
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc_bf(const __bf16* base, int row0, int m, int ld) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(base + (size_t)row0 * ld), (short)0,
+                                           (int)((uint32_t)(m - row0) * (uint32_t)ld * 2u), 0x00020000);
+}
+// The packed B stage ks (kP 4 KB pieces, contiguous from the weight's column-tile base).
+template <int kP>
 __device__ __forceinline__ void load_b(__amdgpu_buffer_rsrc_t r, int ks, char* Bs, int wv, int lane) {
-  const uint32_t bst = (uint32_t)ks * kGBStage * 16u;
+  const uint32_t bst = (uint32_t)ks * b_stage_granules(kP) * 16u;
 #pragma unroll
-  for (int i = 0; i < kGBi / 4; ++i)
+  for (int i = 0; i < kP; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(Bs + (wv + 4 * i) * 1024), 16,
                                              bst + (uint32_t)((wv + 4 * i) * 1024 + 16 * lane), 0, 0, 0);
 }
+template <int kP>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t b_rsrc(const void* packed, int w, int n_nt, int nt, int nks) {
-  const char* base = static_cast<const char*>(packed) + ((size_t)w * n_nt + nt) * (size_t)nks * kGBStage * 16;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nks * kGBStage * 16, 0x00020000);
+  const size_t stage = (size_t)b_stage_granules(kP) * 16;
+  const char* base = static_cast<const char*>(packed) + ((size_t)w * n_nt + nt) * (size_t)nks * stage;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)(nks * stage), 0x00020000);
 }
 
+// A fragment of one stage for this lane (row 32 wv + lane % 32, k 8 (lane / 32) .. +7): eight fp32 values
+// (x0, x1) to split into the pieces, or, for a bf16 A, the granule itself (b).
+struct AFrag {
+  floatx4 x0, x1;
+  bf16x8 b;
+};
+
 // The pipelined K loop of every kernel here: stage ks sits in LDS buffer ks & 1
-// (A at offset 0, the three B pieces at 16 kGAg, any extra region after them);
+// (A at offset 0, the kP B pieces after it, any extra region after them);
 // stage ks + 2 is loaded into it (load(ks, buf)) once every wavefront has read
-// it.  read_a(ks, buf, x0, x1) gives this lane's eight fp32 A values of stage ks
-// (row 32 wv + lane % 32, k 8 (lane / 32) .. +7); they are split while the 24
-// MFMAs of the previous stage run.  The wavefront accumulates rows 32 wv .. +31
-// of the tile over all 128 columns (four 32x32 tiles j).
-template <typename Load, typename ReadA>
+// it.  read_a(ks, buf, f) gives this lane's A fragment of stage ks; it is split
+// (or rounded, kP = 1) while the MFMAs of the previous stage run: 24 for kP = 3
+// (B by piece: b0 with a0, a1, a2; b1 with a0, a1; b2 with a0), 4 for kP = 1.
+// The wavefront accumulates rows 32 wv .. +31 of the tile over all 128 columns
+// (four 32x32 tiles j).
+template <int kP, bool kAB, typename Load, typename ReadA>
 __device__ __forceinline__ void kloop(const char* lds, int stage_bytes, int nks, int lane, Load&& load,
                                       ReadA&& read_a, floatx16 (&acc)[4]) {
+  static_assert(kP == 1 || kP == 3, "one or three operand pieces");
+  static_assert(!kAB || kP == 1, "a bf16 A operand is one piece");
   const int h = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -149,18 +190,22 @@ __device__ __forceinline__ void kloop(const char* lds, int stage_bytes, int nks,
   if (nks > 1) load(1, 1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  bf16x8 a_cur[3];
+  bf16x8 a_cur[kP];
+  auto pieces = [&](const AFrag& f) {
+    if constexpr (kAB) a_cur[0] = f.b;
+    else split_pieces<kP>(f.x0, f.x1, a_cur);
+  };
   {
-    floatx4 x0, x1;
-    read_a(0, 0, x0, x1);
-    split8(x0, x1, a_cur);
+    AFrag f;
+    read_a(0, 0, f);
+    pieces(f);
   }
   for (int ks = 0; ks < nks; ++ks) {
     const int buf = ks & 1;
-    const bf16x8* Bs = reinterpret_cast<const bf16x8*>(lds + buf * stage_bytes + kGAg * 16);
-    bf16x8 b[3][4];
+    const bf16x8* Bs = reinterpret_cast<const bf16x8*>(lds + buf * stage_bytes + a_stage_bytes(kAB));
+    bf16x8 b[kP][4];
 #pragma unroll
-    for (int p = 0; p < 3; ++p)
+    for (int p = 0; p < kP; ++p)
 #pragma unroll
       for (int j = 0; j < 4; ++j) b[p][j] = Bs[p * kGBg + b_slot(32 * j + (lane & 31), h)];
     if (ks + 1 < nks) {
@@ -169,15 +214,20 @@ __device__ __forceinline__ void kloop(const char* lds, int stage_bytes, int nks,
       if (ks + 2 < nks) load(ks + 2, buf);
     }
     // (after the last stage this reads the other buffer's stale contents: values never used)
-    floatx4 x0, x1;
-    read_a(ks + 1, buf ^ 1, x0, x1);
-    constexpr int kPa[6] = {0, 1, 2, 0, 1, 0}, kPb[6] = {0, 0, 0, 1, 1, 2};
+    AFrag f;
+    read_a(ks + 1, buf ^ 1, f);
+    if constexpr (kP == 3) {
+      constexpr int kPa[6] = {0, 1, 2, 0, 1, 0}, kPb[6] = {0, 0, 0, 1, 1, 2};
 #pragma unroll
-    for (int q = 0; q < 6; ++q)
+      for (int q = 0; q < 6; ++q)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_cur[kPa[q]], b[kPb[q]][j], acc[j], 0, 0, 0);
-    split8(x0, x1, a_cur);
+        for (int j = 0; j < 4; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_cur[kPa[q]], b[kPb[q]][j], acc[j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_cur[0], b[0][j], acc[j], 0, 0, 0);
+    }
+    pieces(f);
   }
 }
 
@@ -195,19 +245,28 @@ struct GateOp {
   float k1, k2;
 };
 
-// One 128 x 128 output tile (batch-major, then row tile, then column tile).
-template <bool kGate>
+// One 128 x 128 output tile (batch-major, then row tile, then column tile).  kP operand pieces; kAB: A is
+// bf16 in memory (G.a_bf16); C is written as bf16 when G.c_bf16 (rounded once, from the fp32 sum).
+template <int kP, bool kAB, bool kGate>
 __device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, char* lds, const GateOp& gt) {
+  static_assert(!(kAB && kGate), "the gated operand is fp32");
+  constexpr int SB = g_stage_bytes(kP, kAB);
   const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
   const int n_mt = (G.m + kGM - 1) / kGM, n_nt = G.n / kGN;
   const int nt = tile % n_nt, mt = (tile / n_nt) % n_mt, bi = tile / (n_nt * n_mt);
   const int row0 = mt * kGM, nks = G.k / kGK;
   const bool g0 = kGate && bi == 0;                      // batch 0 of a gated call: silu of the logits
   const int lda = g0 ? (int)gt.ld : (int)G.lda;
-  const __amdgpu_buffer_rsrc_t ar = rows_rsrc(g0 ? gt.s : G.a + (int64_t)bi * G.a_bs, row0, G.m, lda);
+  __amdgpu_buffer_rsrc_t ar;
   uint32_t a_voff[kGAi / 4];
-  a_offsets(wv, lane, lda, a_voff);
-  const __amdgpu_buffer_rsrc_t br = b_rsrc(G.b, G.widx[bi], n_nt, nt, nks);
+  if constexpr (kAB) {
+    ar = rows_rsrc_bf(static_cast<const __bf16*>(G.a) + (int64_t)bi * G.a_bs, row0, G.m, lda);
+    a_voff[0] = abf_offset(wv, lane, lda);
+  } else {
+    ar = rows_rsrc(g0 ? gt.s : static_cast<const float*>(G.a) + (int64_t)bi * G.a_bs, row0, G.m, lda);
+    a_offsets(wv, lane, lda, a_voff);
+  }
+  const __amdgpu_buffer_rsrc_t br = b_rsrc<kP>(G.b, G.widx[bi], n_nt, nt, nks);
   const int ra = wv * 32 + (lane & 31);
   // gate logits of this lane's A values (row ra, k 8 h .. +7 of each stage), one stage ahead
   // (32-bit byte offsets from the uniform base: (m + 128) ld_s 4 < 2^31 is checked by the host)
@@ -222,32 +281,42 @@ __device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, cha
     mv1 = *reinterpret_cast<const floatx4*>(sb + moff + 16u);
   }
   floatx16 acc[4];
-  kloop(lds, kGStage, nks, lane,
+  kloop<kP, kAB>(lds, SB, nks, lane,
         [&](int ks, int buf) {
-          load_a(ar, a_voff, (uint32_t)(ks * kGK) * 4u, lds + buf * kGStage, wv);
-          load_b(br, ks, lds + buf * kGStage + kGAg * 16, wv, lane);
+          if constexpr (kAB) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void*)(lds + buf * SB + wv * 1024), 16,
+                                                     a_voff[0] + (uint32_t)(ks * kGK) * 2u, 0, 0, 0);
+          } else {
+            load_a(ar, a_voff, (uint32_t)(ks * kGK) * 4u, lds + buf * SB, wv);
+          }
+          load_b<kP>(br, ks, lds + buf * SB + a_stage_bytes(kAB), wv, lane);
         },
-        [&](int ks, int buf, floatx4& x0, floatx4& x1) {
-          const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * kGStage);
-          x0 = As[a_slot(ra, 2 * h)];
-          x1 = As[a_slot(ra, 2 * h + 1)];
-          if constexpr (kGate) {
-            if (g0) {
+        [&](int ks, int buf, AFrag& f) {
+          if constexpr (kAB) {
+            f.b = reinterpret_cast<const bf16x8*>(lds + buf * SB)[abf_slot(ra, h)];
+            return;
+          } else {
+            const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * SB);
+            f.x0 = As[a_slot(ra, 2 * h)];
+            f.x1 = As[a_slot(ra, 2 * h + 1)];
+            if constexpr (kGate) {
+              if (g0) {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                x0[e] = silu(x0[e]) * gt.k1;
-                x1[e] = silu(x1[e]) * gt.k1;
-              }
-            } else {
+                for (int e = 0; e < 4; ++e) {
+                  f.x0[e] = silu(f.x0[e]) * gt.k1;
+                  f.x1[e] = silu(f.x1[e]) * gt.k1;
+                }
+              } else {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                x0[e] = sigmoidf_(mv0[e]) * gt.k2 * x0[e];
-                x1[e] = sigmoidf_(mv1[e]) * gt.k2 * x1[e];
-              }
-              if (mok && ks + 1 < nks) {
-                const uint32_t o = moff + (uint32_t)(ks + 1) * (kGK * 4u);
-                mv0 = *reinterpret_cast<const floatx4*>(sb + o);
-                mv1 = *reinterpret_cast<const floatx4*>(sb + o + 16u);
+                for (int e = 0; e < 4; ++e) {
+                  f.x0[e] = sigmoidf_(mv0[e]) * gt.k2 * f.x0[e];
+                  f.x1[e] = sigmoidf_(mv1[e]) * gt.k2 * f.x1[e];
+                }
+                if (mok && ks + 1 < nks) {
+                  const uint32_t o = moff + (uint32_t)(ks + 1) * (kGK * 4u);
+                  mv0 = *reinterpret_cast<const floatx4*>(sb + o);
+                  mv1 = *reinterpret_cast<const floatx4*>(sb + o + 16u);
+                }
               }
             }
           }
@@ -256,7 +325,8 @@ __device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, cha
 
   // epilogue: C = acc (+ bias) (+ R)
   const bool with_bias = G.bias && bi < G.bias_batches;
-  float* cb = G.c + (int64_t)bi * G.c_bs;
+  float* cb = static_cast<float*>(G.c) + (G.c_bf16 ? 0 : (int64_t)bi * G.c_bs);
+  __bf16* cbh = static_cast<__bf16*>(G.c) + (G.c_bf16 ? (int64_t)bi * G.c_bs : 0);
   const float* rb = G.r ? G.r + (int64_t)bi * G.r_bs : nullptr;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -269,33 +339,39 @@ __device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, cha
         float v = acc[j][r];
         if (with_bias) v += bv;
         if (rb) v += rb[(size_t)row * G.ldr + col];
-        cb[(size_t)row * G.ldc + col] = v;
+        if (G.c_bf16)
+          cbh[(size_t)row * G.ldc + col] = (__bf16)v;
+        else
+          cb[(size_t)row * G.ldc + col] = v;
       }
     }
   }
 }
 
+template <int kP, bool kAB>
 __global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(kP, kAB)];
   const int n_tiles = gemm_tiles(G);
   const int tile = xcd_row(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
-  gemm_tile<false>(G, tile, lds, GateOp{});
+  gemm_tile<kP, kAB, false>(G, tile, lds, GateOp{});
 }
 
+template <int kP>
 __global__ __launch_bounds__(kGT, 3) void k_gemm_s3_gate(e2v2_gemm_args G, GateOp gt) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(kP, false)];
   const int n_tiles = gemm_tiles(G);
   const int tile = xcd_row(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
-  gemm_tile<true>(G, tile, lds, gt);
+  gemm_tile<kP, false, true>(G, tile, lds, gt);
 }
 
 // Independent GEMMs in one launch: group g owns workgroups block0[g] ..
 // block0[g + 1] - 1 (xcd_grid of its tile count, in the order given, so the
 // caller puts the longest tiles first), its tiles spread over the XCDs as in a
 // launch of its own.  The group is selected with constant indices so that its
-// arguments stay in the kernel-argument segment.
+// arguments stay in the kernel-argument segment.  The groups share the operand
+// pieces and A's storage type (the output's may differ).
 constexpr int kGGroups = 4;
 struct GemmGroups {
   e2v2_gemm_args g[kGGroups];
@@ -303,15 +379,16 @@ struct GemmGroups {
   int n;
 };
 
+template <int kP, bool kAB>
 __global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp(GemmGroups P) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(kP, kAB)];
   const int b = blockIdx.x;
 #pragma unroll
   for (int gi = 0; gi < kGGroups; ++gi) {
     if (gi < P.n && b >= P.block0[gi] && b < P.block0[gi + 1]) {
       const int n_tiles = gemm_tiles(P.g[gi]);
       const int tile = xcd_row(b - P.block0[gi], n_tiles);
-      if (tile < n_tiles) gemm_tile<false>(P.g[gi], tile, lds, GateOp{});
+      if (tile < n_tiles) gemm_tile<kP, kAB, false>(P.g[gi], tile, lds, GateOp{});
       return;
     }
   }
@@ -331,11 +408,13 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp(GemmGroups P) {
 // so that within every 16-k stage of the backward the partner of column k is k ^ 8.
 __device__ __forceinline__ int pair_pos(int p, int ab) { return 16 * (p >> 3) + 8 * ab + (p & 7); }
 
+template <int kP>
 __global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ x, const void* __restrict__ wp,
                                                       const float* __restrict__ bias, float* __restrict__ y,
                                                       float* __restrict__ hq, float* __restrict__ hk, int n,
                                                       int hid, int c) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kGStage];
+  constexpr int SB = g_stage_bytes(kP, false);
+  __shared__ __attribute__((aligned(16))) char lds[2 * SB];
   const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
   const int n_mt = (n + kGM - 1) / kGM, n_pt = 2 * hid / 64, tiles = n_mt * n_pt;
   // three groups of xcd_grid(tiles) workgroups, l = 2, 1, 0 (5, 3, 1 m-rows): long tiles first
@@ -345,7 +424,7 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ 
   const int mt = tile / n_pt, pt = tile % n_pt, row0 = mt * kGM, nks = c / kGK, O = 4 * hid;
   uint32_t a_voff[kGAi / 4];
   a_offsets(wv, lane, c, a_voff);
-  const __amdgpu_buffer_rsrc_t br = b_rsrc(wp, L, n_pt, pt, nks);
+  const __amdgpu_buffer_rsrc_t br = b_rsrc<kP>(wp, L, n_pt, pt, nks);
   const int ra = wv * 32 + (lane & 31);
   float s[2][16];
 #pragma unroll
@@ -356,15 +435,15 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ 
     if (m != L * L) __syncthreads();      // every wavefront is done with the previous row's LDS stages
     const __amdgpu_buffer_rsrc_t ar = rows_rsrc(x + (size_t)m * n * c, row0, n, c);
     floatx16 acc[4];
-    kloop(lds, kGStage, nks, lane,
+    kloop<kP, false>(lds, SB, nks, lane,
           [&](int ks, int buf) {
-            load_a(ar, a_voff, (uint32_t)(ks * kGK) * 4u, lds + buf * kGStage, wv);
-            load_b(br, ks, lds + buf * kGStage + kGAg * 16, wv, lane);
+            load_a(ar, a_voff, (uint32_t)(ks * kGK) * 4u, lds + buf * SB, wv);
+            load_b<kP>(br, ks, lds + buf * SB + kGAg * 16, wv, lane);
           },
-          [&](int, int buf, floatx4& x0, floatx4& x1) {
-            const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * kGStage);
-            x0 = As[a_slot(ra, 2 * h)];
-            x1 = As[a_slot(ra, 2 * h + 1)];
+          [&](int, int buf, AFrag& f) {
+            const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * SB);
+            f.x0 = As[a_slot(ra, 2 * h)];
+            f.x1 = As[a_slot(ra, 2 * h + 1)];
           },
           acc);
     float* ym = y + (size_t)m * n * O;
@@ -405,13 +484,15 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ 
 // pieces, granule g of row r in slot g ^ ((r / 8) & 1)).  The packed weight is
 // [W_l (rows in the paired order) ; Wv_l]^T per l: the value projection's input
 // gradient enters as cv / 16 further stages with A = gv[m].
-constexpr int kGStageQ = kGStage + 128 * 8 * 4;      // + the G tile: 24 KB
+__host__ __device__ constexpr int qk_bwd_stage_bytes(int kP) { return g_stage_bytes(kP, false) + 128 * 8 * 4; }
 __device__ __forceinline__ int g_slot(int r, int g) { return r * 2 + (g ^ ((r >> 3) & 1)); }
 
+template <int kP>
 __global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const float* __restrict__ y, const float* __restrict__ ghq,
                                                       const float* __restrict__ ghk, const void* __restrict__ wp,
                                                       const float* __restrict__ gv, float* __restrict__ gx, int n,
                                                       int hid, int c, int cv) {
+  constexpr int SB = g_stage_bytes(kP, false), kGStageQ = qk_bwd_stage_bytes(kP);   // + the G tile: 4 KB
   __shared__ __attribute__((aligned(16))) char lds[2 * kGStageQ];
   const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
   const int n_mt = (n + kGM - 1) / kGM, n_ct = c / kGN, tiles = 9 * n_mt * n_ct;
@@ -427,37 +508,38 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const float* __restrict__ 
   const __amdgpu_buffer_rsrc_t yr = rows_rsrc(y + (size_t)m * n * O, row0, n, O);
   const __amdgpu_buffer_rsrc_t vr = gv ? rows_rsrc(gv + (size_t)m * n * cv, row0, n, cv) : yr;
   const __amdgpu_buffer_rsrc_t qr = rows_rsrc(ghq, row0, n, 3 * hid), kr = rows_rsrc(ghk, row0, n, 3 * hid);
-  const char* wbase = static_cast<const char*>(wp) + ((size_t)l * n_ct + ct) * (size_t)nks_w * kGBStage * 16;
+  constexpr int kBS = b_stage_granules(kP) * 16;
+  const char* wbase = static_cast<const char*>(wp) + ((size_t)l * n_ct + ct) * (size_t)nks_w * kBS;
   const __amdgpu_buffer_rsrc_t br =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wbase), (short)0, nks_w * kGBStage * 16, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wbase), (short)0, nks_w * kBS, 0x00020000);
   // G tile load: one instruction per wavefront, LDS granules 64 wv .. +63 = rows 32 wv + lane / 2, slot lane % 2
   const int g_r = 32 * wv + (lane >> 1);
   const uint32_t g_voff = (uint32_t)(g_r * 3 * hid + 4 * ((lane & 1) ^ ((g_r >> 3) & 1))) * 4u;
   const int ra = wv * 32 + (lane & 31);
   floatx16 acc[4];
-  kloop(lds, kGStageQ, nks, lane,
+  kloop<kP, false>(lds, kGStageQ, nks, lane,
         [&](int ks, int buf) {
           char* As = lds + buf * kGStageQ;
           if (ks < nk1) {
             load_a(yr, y_voff, (uint32_t)(ks * kGK) * 4u, As, wv);
             const int p0 = 8 * ks;                                     // first pair of the stage
             const uint32_t goff = (uint32_t)(l * hid + (p0 < hid ? p0 : p0 - hid)) * 4u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(p0 < hid ? qr : kr, (lds_void*)(As + kGStage + wv * 1024), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(p0 < hid ? qr : kr, (lds_void*)(As + SB + wv * 1024), 16,
                                                      g_voff + goff, 0, 0, 0);
           } else {
             load_a(vr, v_voff, (uint32_t)((ks - nk1) * kGK) * 4u, As, wv);
           }
-          load_b(br, ks, As + kGAg * 16, wv, lane);
+          load_b<kP>(br, ks, As + kGAg * 16, wv, lane);
         },
-        [&](int ks, int buf, floatx4& x0, floatx4& x1) {
+        [&](int ks, int buf, AFrag& f) {
           const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * kGStageQ);
           if (ks < nk1) {
-            const floatx4* Gs = reinterpret_cast<const floatx4*>(lds + buf * kGStageQ + kGStage);
-            x0 = As[a_slot(ra, 2 - 2 * h)] * Gs[g_slot(ra, 0)];
-            x1 = As[a_slot(ra, 3 - 2 * h)] * Gs[g_slot(ra, 1)];
+            const floatx4* Gs = reinterpret_cast<const floatx4*>(lds + buf * kGStageQ + SB);
+            f.x0 = As[a_slot(ra, 2 - 2 * h)] * Gs[g_slot(ra, 0)];
+            f.x1 = As[a_slot(ra, 3 - 2 * h)] * Gs[g_slot(ra, 1)];
           } else {
-            x0 = As[a_slot(ra, 2 * h)];
-            x1 = As[a_slot(ra, 2 * h + 1)];
+            f.x0 = As[a_slot(ra, 2 * h)];
+            f.x1 = As[a_slot(ra, 2 * h + 1)];
           }
         },
         acc);
@@ -474,9 +556,10 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const float* __restrict__ 
 }
 
 // Pack: one thread per (weight, column tile, stage, LDS granule): the granule's
-// eight k of its column, split into the three pieces.
+// eight k of its column, split into the three pieces (or rounded to the first alone).
 __global__ __launch_bounds__(256) void k_gemm_pack(const float* __restrict__ w, int64_t ld_n, int64_t ld_k,
-                                                   int64_t w_stride, int n_w, int n, int k, bf16x8* __restrict__ out) {
+                                                   int64_t w_stride, int n_w, int n, int k, int pieces,
+                                                   bf16x8* __restrict__ out) {
   const int n_nt = n / kGN, nks = k / kGK;
   const int64_t total = (int64_t)n_w * n_nt * nks * kGBg;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -493,32 +576,39 @@ __global__ __launch_bounds__(256) void k_gemm_pack(const float* __restrict__ w, 
     x0[i] = src[i * ld_k];
     x1[i] = src[(4 + i) * ld_k];
   }
-  bf16x8 p[3];
-  split8(x0, x1, p);
-  bf16x8* dst = out + st * kGBStage + q;
-  dst[0] = p[0];
-  dst[kGBg] = p[1];
-  dst[2 * kGBg] = p[2];
+  bf16x8* dst = out + st * b_stage_granules(pieces) + q;
+  if (pieces == 3) {
+    bf16x8 p[3];
+    split8(x0, x1, p);
+    dst[0] = p[0];
+    dst[kGBg] = p[1];
+    dst[2 * kGBg] = p[2];
+  } else {
+    bf16x8 p[1];
+    round8(x0, x1, p);
+    dst[0] = p[0];
+  }
 }
 }  // namespace
 }  // namespace e2v2
 
-E2V2_API int64_t e2v2_gemm_packed_bytes(int n_w, int n, int k) {
+E2V2_API int64_t e2v2_gemm_packed_bytes(int n_w, int n, int k, int pieces) {
   using namespace e2v2;
-  if (n_w <= 0 || n <= 0 || k <= 0 || n % kGN || k % kGK) return -1;
-  return (int64_t)n_w * (n / kGN) * (k / kGK) * kGBStage * 16;
+  if (n_w <= 0 || n <= 0 || k <= 0 || n % kGN || k % kGK || (pieces != 1 && pieces != 3)) return -1;
+  return (int64_t)n_w * (n / kGN) * (k / kGK) * b_stage_granules(pieces) * 16;
 }
 
 E2V2_API int e2v2_gemm_pack(const float* w, int64_t ld_n, int64_t ld_k, int64_t w_stride, int n_w, int n, int k,
-                            void* packed, hipStream_t s) {
+                            int pieces, void* packed, hipStream_t s) {
   using namespace e2v2;
+  E2V2_REQUIRE(pieces == 1 || pieces == 3, "gemm_pack: %d pieces (1 or 3)", pieces);
   E2V2_REQUIRE(n_w > 0 && n_w <= 16, "gemm_pack: %d weights (1 .. 16)", n_w);
   E2V2_REQUIRE(n > 0 && n % kGN == 0, "gemm_pack: n=%d must be a positive multiple of %d", n, kGN);
   E2V2_REQUIRE(k > 0 && k % kGK == 0, "gemm_pack: k=%d must be a positive multiple of %d", k, kGK);
   E2V2_REQUIRE(w && packed, "gemm_pack: null pointer");
   const int64_t total = (int64_t)n_w * (n / kGN) * (k / kGK) * kGBg;
   hipLaunchKernelGGL(k_gemm_pack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, w, ld_n, ld_k, w_stride, n_w,
-                     n, k, static_cast<bf16x8*>(packed));
+                     n, k, pieces, static_cast<bf16x8*>(packed));
   E2V2_LAUNCHED("k_gemm_pack");
   return 0;
 }
@@ -530,11 +620,17 @@ int check_gemm_args(const e2v2_gemm_args& G) {
   E2V2_REQUIRE(G.m >= 0 && G.n > 0 && G.n % kGN == 0 && G.k > 0 && G.k % kGK == 0,
                "gemm_s3: m=%d, n=%d (multiple of %d), k=%d (multiple of %d)", G.m, G.n, kGN, G.k, kGK);
   E2V2_REQUIRE(G.a && G.b && G.c, "gemm_s3: null operand");
-  E2V2_REQUIRE(G.lda >= G.k && G.lda % 4 == 0 && ((uintptr_t)G.a & 15) == 0,
-               "gemm_s3: A needs lda >= k, lda %% 4 == 0 and 16-byte alignment");
+  E2V2_REQUIRE((G.pieces == 1 || G.pieces == 3) && (G.a_bf16 == 0 || G.a_bf16 == 1) &&
+                   (G.c_bf16 == 0 || G.c_bf16 == 1) && (!G.a_bf16 || G.pieces == 1),
+               "gemm_s3: %d pieces with a_bf16 %d, c_bf16 %d (a bf16 A needs one piece)", G.pieces, G.a_bf16,
+               G.c_bf16);
+  const int ea = G.a_bf16 ? 2 : 4;                     // bytes per A element; granules of 16 bytes
+  E2V2_REQUIRE(G.lda >= G.k && G.lda % (16 / ea) == 0 && ((uintptr_t)G.a & 15) == 0,
+               "gemm_s3: A needs lda >= k, 16-byte rows (lda %% %d == 0) and 16-byte alignment", 16 / ea);
   E2V2_REQUIRE(G.ldc >= G.n && (!G.r || G.ldr >= G.n), "gemm_s3: ldc / ldr below n");
-  E2V2_REQUIRE((uint64_t)(G.m + kGM) * (uint64_t)G.lda * 4u < (1ull << 31), "gemm_s3: A batch too large (m=%d)", G.m);
-  E2V2_REQUIRE((uint64_t)(G.k / kGK) * kGBStage * 16u < (1ull << 31), "gemm_s3: k=%d too large", G.k);
+  E2V2_REQUIRE((uint64_t)(G.m + kGM) * (uint64_t)G.lda * ea < (1ull << 31), "gemm_s3: A batch too large (m=%d)", G.m);
+  E2V2_REQUIRE((uint64_t)(G.k / kGK) * b_stage_granules(G.pieces) * 16u < (1ull << 31), "gemm_s3: k=%d too large",
+               G.k);
   E2V2_REQUIRE(G.n_w > 0 && G.n_w <= 16, "gemm_s3: n_w=%d (1 .. 16)", G.n_w);
   for (int b = 0; b < G.batch; ++b)
     E2V2_REQUIRE(G.widx[b] >= 0 && G.widx[b] < G.n_w, "gemm_s3: widx[%d]=%d outside 0 .. %d", b, G.widx[b], G.n_w - 1);
@@ -550,7 +646,13 @@ E2V2_API int e2v2_gemm_s3(const e2v2_gemm_args* g, hipStream_t s) {
   const e2v2_gemm_args& G = *g;
   if (int rc = check_gemm_args(G)) return rc;
   if (G.m == 0) return 0;
-  hipLaunchKernelGGL(k_gemm_s3, dim3(xcd_grid(host_tiles(G))), dim3(kGT), 0, s, G);
+  const dim3 grid(xcd_grid(host_tiles(G)));
+  if (G.pieces == 3)
+    hipLaunchKernelGGL((k_gemm_s3<3, false>), grid, dim3(kGT), 0, s, G);
+  else if (G.a_bf16)
+    hipLaunchKernelGGL((k_gemm_s3<1, true>), grid, dim3(kGT), 0, s, G);
+  else
+    hipLaunchKernelGGL((k_gemm_s3<1, false>), grid, dim3(kGT), 0, s, G);
   E2V2_LAUNCHED("k_gemm_s3");
   return 0;
 }
@@ -563,13 +665,19 @@ E2V2_API int e2v2_gemm_s3_gated(const e2v2_gemm_args* g, const float* s, int64_t
   if (int rc = check_gemm_args(G)) return rc;
   E2V2_REQUIRE(s && ((uintptr_t)s & 15) == 0 && ld_s % 4 == 0,
                "gemm_s3_gated: the gate logits need 16-byte alignment and ld_s %% 4 == 0");
+  E2V2_REQUIRE(!G.a_bf16, "gemm_s3_gated: the gated operand is fp32");
   for (int b = 0; b < G.batch; ++b)
     E2V2_REQUIRE((int64_t)G.k * (G.widx[b] + 1) <= ld_s, "gemm_s3_gated: batch %d reads logit columns past ld_s=%lld",
                  b, (long long)ld_s);
   E2V2_REQUIRE((uint64_t)(G.m + kGM) * (uint64_t)ld_s * 4u < (1ull << 31), "gemm_s3_gated: logits too large (m=%d)",
                G.m);
   if (G.m == 0) return 0;
-  hipLaunchKernelGGL(k_gemm_s3_gate, dim3(xcd_grid(host_tiles(G))), dim3(kGT), 0, st, G, GateOp{s, ld_s, k1, k2});
+  if (G.pieces == 3)
+    hipLaunchKernelGGL((k_gemm_s3_gate<3>), dim3(xcd_grid(host_tiles(G))), dim3(kGT), 0, st, G,
+                       GateOp{s, ld_s, k1, k2});
+  else
+    hipLaunchKernelGGL((k_gemm_s3_gate<1>), dim3(xcd_grid(host_tiles(G))), dim3(kGT), 0, st, G,
+                       GateOp{s, ld_s, k1, k2});
   E2V2_LAUNCHED("k_gemm_s3_gate");
   return 0;
 }
@@ -582,6 +690,8 @@ E2V2_API int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hi
   P.block0[0] = 0;
   for (int i = 0; i < n_groups; ++i) {
     if (int rc = check_gemm_args(groups[i])) return rc;
+    E2V2_REQUIRE(groups[i].pieces == groups[0].pieces && groups[i].a_bf16 == groups[0].a_bf16,
+                 "gemm_s3_grouped: the groups must share the operand pieces and A's storage type");
     P.g[i] = groups[i];
     P.block0[i + 1] = P.block0[i] + xcd_grid(host_tiles(groups[i]));
     E2V2_REQUIRE(P.block0[i + 1] >= P.block0[i], "gemm_s3_grouped: too many tiles");
@@ -589,7 +699,13 @@ E2V2_API int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hi
   for (int i = n_groups; i < kGGroups; ++i) P.block0[i + 1] = P.block0[n_groups];
   P.n = n_groups;
   if (P.block0[n_groups] == 0) return 0;
-  hipLaunchKernelGGL(k_gemm_s3_grp, dim3(P.block0[n_groups]), dim3(kGT), 0, s, P);
+  const dim3 grid(P.block0[n_groups]);
+  if (groups[0].pieces == 3)
+    hipLaunchKernelGGL((k_gemm_s3_grp<3, false>), grid, dim3(kGT), 0, s, P);
+  else if (groups[0].a_bf16)
+    hipLaunchKernelGGL((k_gemm_s3_grp<1, true>), grid, dim3(kGT), 0, s, P);
+  else
+    hipLaunchKernelGGL((k_gemm_s3_grp<1, false>), grid, dim3(kGT), 0, s, P);
   E2V2_LAUNCHED("k_gemm_s3_grp");
   return 0;
 }
@@ -598,8 +714,9 @@ E2V2_API int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hi
 // wp: the three per-l weights packed with their columns in the tile-paired order
 // (n = 4 hid, k = c), bias [4 hid] in the same order (m = 0 rows only; may be NULL).
 E2V2_API int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bias, float* y, float* hq, float* hk,
-                                 int n, int hid, int c, hipStream_t s) {
+                                 int n, int hid, int c, int pieces, hipStream_t s) {
   using namespace e2v2;
+  E2V2_REQUIRE(pieces == 1 || pieces == 3, "qk_proj_fwd_s3: %d pieces (1 or 3)", pieces);
   E2V2_REQUIRE(hid > 0 && hid % 64 == 0, "qk_proj_fwd_s3: hid=%d must be a positive multiple of 64", hid);
   E2V2_REQUIRE(c > 0 && c % kGK == 0, "qk_proj_fwd_s3: C=%d must be a positive multiple of %d", c, kGK);
   E2V2_REQUIRE(x && wp && y && hq && hk, "qk_proj_fwd_s3: null operand");
@@ -608,7 +725,10 @@ E2V2_API int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bi
                    (uint64_t)(n + kGM) * 4u * hid < (1ull << 32), "qk_proj_fwd_s3: n=%d too large", n);
   if (n == 0) return 0;
   const int tiles = ((n + kGM - 1) / kGM) * (2 * hid / 64);
-  hipLaunchKernelGGL(k_qk_s3_fwd, dim3(3 * xcd_grid(tiles)), dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
+  if (pieces == 3)
+    hipLaunchKernelGGL((k_qk_s3_fwd<3>), dim3(3 * xcd_grid(tiles)), dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
+  else
+    hipLaunchKernelGGL((k_qk_s3_fwd<1>), dim3(3 * xcd_grid(tiles)), dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
   E2V2_LAUNCHED("k_qk_s3_fwd");
   return 0;
 }
@@ -617,8 +737,9 @@ E2V2_API int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bi
 // gv [9][n][cv]; wp: per l the packed [W_l (rows in the paired order) ; Wv_l]^T
 // (n = c, k = 4 hid + cv).
 E2V2_API int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* ghk, const void* wp, const float* gv,
-                                 float* gx, int n, int hid, int c, int cv, hipStream_t s) {
+                                 float* gx, int n, int hid, int c, int cv, int pieces, hipStream_t s) {
   using namespace e2v2;
+  E2V2_REQUIRE(pieces == 1 || pieces == 3, "qk_proj_bwd_s3: %d pieces (1 or 3)", pieces);
   E2V2_REQUIRE(hid > 0 && hid % 64 == 0, "qk_proj_bwd_s3: hid=%d must be a positive multiple of 64", hid);
   E2V2_REQUIRE(c > 0 && c % kGN == 0, "qk_proj_bwd_s3: C=%d must be a positive multiple of %d", c, kGN);
   E2V2_REQUIRE(cv > 0 && cv % kGK == 0, "qk_proj_bwd_s3: Cv=%d must be a positive multiple of %d", cv, kGK);
@@ -629,7 +750,10 @@ E2V2_API int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* 
                    (uint64_t)(n + kGM) * (uint64_t)cv * 4u < (1ull << 31), "qk_proj_bwd_s3: n=%d too large", n);
   if (n == 0) return 0;
   const int tiles = 9 * ((n + kGM - 1) / kGM) * (c / kGN);
-  hipLaunchKernelGGL(k_qk_s3_bwd, dim3(xcd_grid(tiles)), dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
+  if (pieces == 3)
+    hipLaunchKernelGGL((k_qk_s3_bwd<3>), dim3(xcd_grid(tiles)), dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
+  else
+    hipLaunchKernelGGL((k_qk_s3_bwd<1>), dim3(xcd_grid(tiles)), dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
   E2V2_LAUNCHED("k_qk_s3_bwd");
   return 0;
 }

@@ -8,6 +8,11 @@ MFMA rate.  Weights are split and packed once per weight version
 (``e2v2_gemm_pack``, into the kernel's LDS image per 128-column tile and 16-k
 stage); activations are split inside the kernel.
 
+The bf16 mode runs the same kernels on one-piece packs (``pack(..., pieces=1)``:
+the bf16 rounding of the weight alone): bf16 operands (the A operand rounded as it
+is read, or read as bf16), one MFMA product, fp32 accumulation; the output can be
+written as bf16 for the attention kernels that gather it.
+
 Layers that use it (reference paths): SO3_Linear_e2former
 (src/molfm/models/e2former/module_utils.py:2010-2052), FeedForwardNetwork_s3
 (module_utils.py:2755-2797), forward_linear + proj_first
@@ -27,25 +32,29 @@ TILE_N, TILE_K, MAX_BATCH = 128, 16, 16
 
 
 class PackedWeight:
-    """n_w fp32 weights W_w [n, k] split and packed for ``e2v2_gemm_s3``."""
-    __slots__ = ("buf", "n_w", "n", "k")
+    """n_w fp32 weights W_w [n, k] split into ``pieces`` bf16 pieces (3: the exact
+    split, 1: the bf16 rounding alone) and packed for ``e2v2_gemm_s3``."""
+    __slots__ = ("buf", "n_w", "n", "k", "pieces")
 
-    def __init__(self, buf, n_w, n, k):
-        self.buf, self.n_w, self.n, self.k = buf, n_w, n, k
+    def __init__(self, buf, n_w, n, k, pieces=3):
+        self.buf, self.n_w, self.n, self.k, self.pieces = buf, n_w, n, k, pieces
 
 
 def supported(n: int, k: int) -> bool:
     return n > 0 and k > 0 and n % TILE_N == 0 and k % TILE_K == 0
 
 
-def pack(w: torch.Tensor, transpose: bool = False) -> PackedWeight:
+def pack(w: torch.Tensor, transpose: bool = False, pieces: int = 3) -> PackedWeight:
     """Pack w [n_w, n, k] (W_w = w[w]) or, with ``transpose``, w [n_w, k, n]
-    (W_w = w[w]^T, read without a copy); a 2-D w is one weight.  fp32 on the GPU."""
+    (W_w = w[w]^T, read without a copy); a 2-D w is one weight.  fp32 on the GPU
+    (a bf16 weight is widened exactly).  pieces = 1 packs bf16(W) alone."""
     w = w.detach()
     if w.dim() == 2:
         w = w.unsqueeze(0)
-    if w.dtype != torch.float32 or not w.is_cuda:
-        raise ValueError("gemm.pack: fp32 weights on the GPU")
+    if w.dtype == torch.bfloat16:
+        w = w.float()
+    if w.dtype != torch.float32 or not w.is_cuda or pieces not in (1, 3):
+        raise ValueError("gemm.pack: fp32 weights on the GPU, 1 or 3 pieces")
     w = w.contiguous()
     n_w = w.shape[0]
     if transpose:
@@ -56,12 +65,12 @@ def pack(w: torch.Tensor, transpose: bool = False) -> PackedWeight:
         ld_n, ld_k = k, 1
     if not supported(n, k) or not 0 < n_w <= MAX_BATCH:
         raise ValueError(f"gemm.pack: unsupported shape n_w={n_w} n={n} k={k}")
-    nbytes = int(_lib.load().e2v2_gemm_packed_bytes(n_w, n, k))
+    nbytes = int(_lib.load().e2v2_gemm_packed_bytes(n_w, n, k, pieces))
     buf = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=w.device)
     _lib.call("e2v2_gemm_pack", _lib.vp(w.data_ptr()), _lib.i64(ld_n), _lib.i64(ld_k), _lib.i64(w.stride(0)),
-              _lib.i32(n_w), _lib.i32(n), _lib.i32(k), _lib.vp(buf.data_ptr()),
+              _lib.i32(n_w), _lib.i32(n), _lib.i32(k), _lib.i32(pieces), _lib.vp(buf.data_ptr()),
               _lib.vp(torch.cuda.current_stream(w.device).cuda_stream))
-    return PackedWeight(buf, n_w, n, k)
+    return PackedWeight(buf, n_w, n, k, pieces)
 
 
 def _as3(t: torch.Tensor) -> torch.Tensor:
@@ -74,17 +83,21 @@ def _batch_view(a):
     bs of either sign); holder is what must stay referenced until the launch is enqueued."""
     if isinstance(a, (list, tuple)):
         t0 = a[0]
+        el = t0.element_size()
         for t in a:
-            if (t.dim() != 2 or t.shape != t0.shape or t.stride() != t0.stride() or t.dtype != torch.float32
-                    or t.stride(1) != 1 or t.stride(0) % 4 or t.data_ptr() % 16):
-                raise ValueError("gemm: batch matrices must share shape and a 16-byte aligned row layout")
+            if (t.dim() != 2 or t.shape != t0.shape or t.stride() != t0.stride() or t.dtype != t0.dtype
+                    or t0.dtype not in (torch.float32, torch.bfloat16)
+                    or t.stride(1) != 1 or (t.stride(0) * el) % 16 or t.data_ptr() % 16):
+                raise ValueError("gemm: batch matrices must share shape, dtype and a 16-byte aligned row layout")
         steps = {(a[b + 1].data_ptr() - a[b].data_ptr()) for b in range(len(a) - 1)}
-        if len(steps) > 1 or any(d % 4 for d in steps):
+        if len(steps) > 1 or any(d % el for d in steps):
             raise ValueError("gemm: batch matrices must be evenly spaced in memory")
-        bs = steps.pop() // 4 if steps else 0
+        bs = steps.pop() // el if steps else 0
         return t0.data_ptr(), t0.stride(0), bs, len(a), t0.shape[0], t0.shape[1], a
     a3 = _as3(a)
-    if a3.stride(2) != 1 or a3.stride(1) % 4 or a3.data_ptr() % 16:
+    if a3.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("gemm: A must be fp32 or bf16")
+    if a3.stride(2) != 1 or (a3.stride(1) * a3.element_size()) % 16 or a3.data_ptr() % 16:
         a3 = a3.contiguous()
     return a3.data_ptr(), a3.stride(1), a3.stride(0), a3.shape[0], a3.shape[1], a3.shape[2], a3
 
@@ -95,8 +108,13 @@ def _args(a, pw: PackedWeight, out: torch.Tensor, widx=None, bias=None, bias_bat
     o3 = _as3(out)
     r3 = None if res is None else _as3(res)
     a_ptr, lda, a_bs, batch, m, k, holder = _batch_view(a)
-    if k != pw.k or o3.shape != (batch, m, pw.n) or o3.dtype != torch.float32:
+    a_bf16 = (a[0] if isinstance(a, (list, tuple)) else a).dtype == torch.bfloat16
+    if k != pw.k or o3.shape != (batch, m, pw.n) or o3.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError(f"gemm: a [{batch}, {m}, {k}] / out {tuple(o3.shape)} do not fit W [{pw.n}, {pw.k}]")
+    if a_bf16 and pw.pieces != 1:
+        raise ValueError("gemm: a bf16 A operand needs a one-piece (bf16) packed weight")
+    if r3 is not None and r3.dtype != torch.float32:
+        raise ValueError("gemm: the residual is fp32")
     if o3.stride(2) != 1 or (r3 is not None and (r3.shape != o3.shape or r3.stride(2) != 1)):
         raise ValueError("gemm: operands need a contiguous last dimension")
     widx = list(range(batch)) if widx is None else list(widx)
@@ -105,6 +123,7 @@ def _args(a, pw: PackedWeight, out: torch.Tensor, widx=None, bias=None, bias_bat
     if m == 0:
         return None, 0.0, holder
     g = _lib.GemmArgs()
+    g.pieces, g.a_bf16, g.c_bf16 = pw.pieces, int(a_bf16), int(o3.dtype == torch.bfloat16)
     g.a, g.lda, g.a_bs = a_ptr, lda, a_bs
     g.b, g.n_w = pw.buf.data_ptr(), pw.n_w
     g.c, g.ldc, g.c_bs = o3.data_ptr(), o3.stride(1), o3.stride(0)
@@ -222,7 +241,7 @@ def qk_supported(hid: int, c: int, cv: int) -> bool:
     return hid > 0 and hid % 64 == 0 and c > 0 and c % TILE_N == 0 and cv > 0 and cv % TILE_K == 0
 
 
-def pack_qk(W: torch.Tensor, bias: Optional[torch.Tensor], Wv: torch.Tensor) -> QKPacks:
+def pack_qk(W: torch.Tensor, bias: Optional[torch.Tensor], Wv: torch.Tensor, pieces: int = 3) -> QKPacks:
     """W [3, 4 hid, C] (stacked query and key weights), bias [4 hid] or None, Wv
     [3, Cv, C] (the value projection, whose input gradient the backward adds)."""
     W = W.detach().float()
@@ -234,9 +253,9 @@ def pack_qk(W: torch.Tensor, bias: Optional[torch.Tensor], Wv: torch.Tensor) -> 
     fi = torch.as_tensor(fwd, device=W.device)
     bi = torch.as_tensor(bwd, device=W.device)
     P = QKPacks()
-    P.fwd = pack(W[:, fi, :].contiguous())
+    P.fwd = pack(W[:, fi, :].contiguous(), pieces=pieces)
     P.bias = None if bias is None else bias.detach().float()[fi].contiguous()
-    P.bwd = pack(torch.cat([W[:, bi, :], Wv], dim=1).contiguous(), transpose=True)
+    P.bwd = pack(torch.cat([W[:, bi, :], Wv], dim=1).contiguous(), transpose=True, pieces=pieces)
     P.hid, P.c, P.cv = hid, c, cv
     return P
 
@@ -251,7 +270,7 @@ def qk_forward(x: torch.Tensor, P: QKPacks):
     st = _lib.vp(torch.cuda.current_stream(x.device).cuda_stream)
     _lib.call("e2v2_qk_proj_fwd_s3", _lib.vp(x.data_ptr()), _lib.vp(P.fwd.buf.data_ptr()),
               _lib.vp(0 if P.bias is None else P.bias.data_ptr()), _lib.vp(y.data_ptr()), _lib.vp(hq.data_ptr()),
-              _lib.vp(hk.data_ptr()), _lib.i32(n), _lib.i32(P.hid), _lib.i32(c), st)
+              _lib.vp(hk.data_ptr()), _lib.i32(n), _lib.i32(P.hid), _lib.i32(c), _lib.i32(P.fwd.pieces), st)
     return hq, hk, y
 
 
@@ -264,5 +283,5 @@ def qk_backward(y: torch.Tensor, ghq: torch.Tensor, ghk: torch.Tensor, gv: Optio
     st = _lib.vp(torch.cuda.current_stream(y.device).cuda_stream)
     _lib.call("e2v2_qk_proj_bwd_s3", _lib.vp(y.data_ptr()), _lib.vp(ghq.data_ptr()), _lib.vp(ghk.data_ptr()),
               _lib.vp(P.bwd.buf.data_ptr()), _lib.vp(0 if gv is None else gv.data_ptr()), _lib.vp(gx.data_ptr()),
-              _lib.i32(n), _lib.i32(P.hid), _lib.i32(P.c), _lib.i32(P.cv), st)
+              _lib.i32(n), _lib.i32(P.hid), _lib.i32(P.c), _lib.i32(P.cv), _lib.i32(P.bwd.pieces), st)
     return gx

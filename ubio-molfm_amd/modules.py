@@ -136,27 +136,33 @@ class MRowWeight:
     for one batched GEMM over the (lmax+1)^2 m-rows (one launch instead of lmax+1,
     fewer partial tiles): ``fwd`` [M, Cin, O] and ``bwd`` [M, O, Cin]; in bf16 the
     per-l transpose ``wt`` [lmax+1, Cin, O] (B operand of the fused projection's backward).
-    In fp32, ``s3f()`` / ``s3b()``: the per-l weights packed for the split GEMM
-    (W_l for y = x W_l^T, W_l^T for the input gradient), packed on first use."""
+    ``s3f()`` / ``s3b()``: the per-l weights packed for the split GEMM (W_l for
+    y = x W_l^T, W_l^T for the input gradient), packed on first use: the exact
+    three-piece split of an fp32 weight, the bf16 weight itself as one piece (the
+    bf16 mode's GEMMs, bf16 operands with fp32 accumulation)."""
     __slots__ = ("w", "fwd", "bwd", "wt", "_s3f", "_s3b")
 
     def __init__(self, w, fwd=None, bwd=None, wt=None):
         self.w, self.fwd, self.bwd, self.wt = w, fwd, bwd, wt
         self._s3f = self._s3b = None
 
+    @property
+    def pieces(self) -> int:
+        return 1 if self.w.dtype == BF16 else 3
+
     def split_ok(self) -> bool:
         w = self.w
-        return (split_gemm_on() and w.dtype == torch.float32 and w.is_cuda
+        return ((w.dtype == BF16 or (split_gemm_on() and w.dtype == torch.float32)) and w.is_cuda
                 and s3gemm.supported(w.shape[1], w.shape[2]) and s3gemm.supported(w.shape[2], w.shape[1]))
 
     def s3f(self):
         if self._s3f is None:
-            self._s3f = s3gemm.pack(self.w)
+            self._s3f = s3gemm.pack(self.w, pieces=self.pieces)
         return self._s3f
 
     def s3b(self):
         if self._s3b is None:
-            self._s3b = s3gemm.pack(self.w, transpose=True)
+            self._s3b = s3gemm.pack(self.w, transpose=True, pieces=self.pieces)
         return self._s3b
 
 
@@ -395,7 +401,9 @@ class SO2OutFn(torch.autograd.Function):
         res = None if res is None else res.contiguous()
         O = Wc[0][3].shape[1]
         y = so2.new_empty(9, N, O, dtype=torch.float32)
-        split = all(e[5] is not None for e in Wc) and so2.dtype == torch.float32
+        # fp32 rows on three-piece packs, or the bf16 mode's one-piece packs (bf16 or fp32 rows)
+        split = all(e[5] is not None for e in Wc) and (so2.dtype == torch.float32 or
+                                                       all(e[5].pieces == 1 for e in Wc))
         problems = []
         for (l3, cnt, start, W, _, PF, _) in Wc:
             K = W.shape[0]
@@ -423,7 +431,8 @@ class SO2OutFn(torch.autograd.Function):
         N = ctx.N
         O = gy.shape[2]
         gso2 = gy.new_empty(ctx.shape, dtype=ctx.so2_dtype)
-        split = all(e[6] is not None for e in ctx.Wc) and ctx.so2_dtype == torch.float32
+        split = all(e[6] is not None for e in ctx.Wc) and (ctx.so2_dtype == torch.float32 or
+                                                           all(e[6].pieces == 1 for e in ctx.Wc))
         problems = []
         for (l3, cnt, start, _, WT, _, PB) in ctx.Wc:
             K = WT.shape[1]
@@ -614,16 +623,18 @@ class AttnProjS3Fn(torch.autograd.Function):
         return gx, None, None, None, None
 
 
-def head_pair_packs(fq: nn.Sequential, fk: nn.Sequential, owner):
+def head_pair_packs(fq: nn.Sequential, fk: nn.Sequential, owner, bf16: bool = False):
     """Operands of QKHeadsS3Fn for two final_linear stacks (Linear, LayerNorm,
     SiLU, Linear) of the same shapes: each Linear's two weights stacked and packed
-    for the forward and (transposed) for the input gradient, the biases as
-    [2, n], the LayerNorm parameters per head.  Cached on ``owner`` per weight
-    version; None when the split GEMM does not apply."""
+    for the forward and (transposed) for the input gradient (one bf16 piece in
+    the bf16 mode), the biases as [2, n], the LayerNorm parameters per head.
+    Cached on ``owner`` per weight version; None when the split GEMM does not
+    apply."""
     w1, w2 = fq[0].weight, fq[3].weight
-    if not (split_gemm_on() and w1.is_cuda and w1.dtype == torch.float32
+    if not ((bf16 or split_gemm_on()) and w1.is_cuda and w1.dtype == torch.float32
             and all(s3gemm.supported(*w.shape) and s3gemm.supported(*w.shape[::-1]) for w in (w1, w2))):
         return None
+    pc = 1 if bf16 else 3
     params = [p for f in (fq, fk) for i in (0, 1, 3) for p in (f[i].weight, f[i].bias)]
 
     def build():
@@ -631,11 +642,11 @@ def head_pair_packs(fq: nn.Sequential, fk: nn.Sequential, owner):
         W2 = torch.stack([fq[3].weight.detach(), fk[3].weight.detach()]).float().contiguous()
         ln = [(f[1].weight.detach().float().contiguous(), f[1].bias.detach().float().contiguous(),
                float(f[1].eps)) for f in (fq, fk)]
-        return {"p1f": s3gemm.pack(W1), "p1b": s3gemm.pack(W1, transpose=True),
+        return {"p1f": s3gemm.pack(W1, pieces=pc), "p1b": s3gemm.pack(W1, transpose=True, pieces=pc),
                 "b1": torch.stack([fq[0].bias.detach(), fk[0].bias.detach()]).float().contiguous(),
-                "p2f": s3gemm.pack(W2), "p2b": s3gemm.pack(W2, transpose=True),
+                "p2f": s3gemm.pack(W2, pieces=pc), "p2b": s3gemm.pack(W2, transpose=True, pieces=pc),
                 "b2": torch.stack([fq[3].bias.detach(), fk[3].bias.detach()]).float().contiguous(), "ln": ln}
-    return cached(owner, "head_pair_s3", params, build)
+    return cached(owner, "head_pair_bf16" if bf16 else "head_pair_s3", params, build)
 
 
 def _ln_silu(x, ln: nn.LayerNorm):
@@ -722,14 +733,16 @@ class DenseS3Fn(torch.autograd.Function):
         return gx, None, None
 
 
-def dense_packs(lin: nn.Linear):
-    """Split-GEMM packs (W, W^T) of an nn.Linear's weight (cached per version), or
-    None when the split GEMM does not apply."""
+def dense_packs(lin: nn.Linear, bf16: bool = False):
+    """Split-GEMM packs (W, W^T) of an nn.Linear's weight (cached per version; one
+    bf16 piece in the bf16 mode), or None when the split GEMM does not apply."""
     w = lin.weight
-    if not (split_gemm_on() and w.is_cuda and w.dtype == torch.float32
+    if not ((bf16 or split_gemm_on()) and w.is_cuda and w.dtype == torch.float32
             and s3gemm.supported(w.shape[0], w.shape[1]) and s3gemm.supported(w.shape[1], w.shape[0])):
         return None
-    return cached(lin, "s3_packs", (w,), lambda: (s3gemm.pack(w.detach()), s3gemm.pack(w.detach(), transpose=True)))
+    pc = 1 if bf16 else 3
+    return cached(lin, "s3_packs_bf16" if bf16 else "s3_packs", (w,),
+                  lambda: (s3gemm.pack(w.detach(), pieces=pc), s3gemm.pack(w.detach(), transpose=True, pieces=pc)))
 
 
 def _linear(x, lin: nn.Linear):
@@ -880,7 +893,7 @@ class Gate_s3(nn.Module):
         nn.init.uniform_(self.gates.weight, -bound, bound)
 
     def forward(self, x, bf16: bool = False):
-        packs = None if bf16 else dense_packs(self.gates)
+        packs = dense_packs(self.gates, bf16)
         return GateFn.apply(x, gemm_weight(self.gates, "weight", bf16), self.gates.bias.detach(), SILU_NORM,
                             SIGMOID_NORM, packs)
 
@@ -932,7 +945,7 @@ class FeedForwardNetwork_s3(nn.Module):
             h = self.slinear_1(x, bf16)
             s2 = self.slinear_2
             W2op = mrow_weight(s2, "weight", s2.weight, bf16, s2.lmax)
-            gpacks = None if bf16 else dense_packs(self.gate.gates)
+            gpacks = dense_packs(self.gate.gates, bf16)
             if gpacks is not None and W2op.split_ok() and h.dtype == torch.float32 and h.shape[2] == s2.weight.shape[2]:
                 return GatedLinearS3Fn.apply(h, gpacks, self.gate.gates.bias.detach(), SILU_NORM, SIGMOID_NORM, W2op,
                                              s2.bias.detach(), s2.lmax, res)
@@ -1243,25 +1256,28 @@ class E2AttentionArbOrder_sparse(nn.Module):
         w, b = cached(self, "qk", params, build)
         return mrow_weight(self, "qk", w, bf16, self.lmax), b
 
-    def qk_s3_packs(self):
+    def qk_s3_packs(self, bf16: bool = False):
         """The split-GEMM packs of the Q/K projection (query and key weights, their
         bias, and the sliced value projection whose input gradient the backward
-        adds), or None when the split GEMM does not apply (cached per version)."""
+        adds; one bf16 piece in the bf16 mode), or None when the split GEMM does
+        not apply (cached per version)."""
         Wop, b = self.qk_weights(False)
         wv, _ = self.value_weights_sliced()
         W = Wop.w
-        if not (split_gemm_on() and W.is_cuda and W.dtype == torch.float32
+        if not ((bf16 or split_gemm_on()) and W.is_cuda and W.dtype == torch.float32
                 and s3gemm.qk_supported(W.shape[1] // 4, W.shape[2], wv.shape[1])):
             return None
         pv = self.proj_value
         params = (self.query_linear.weight, self.query_linear.weight2, self.query_linear.bias,
                   self.key_linear.weight, self.key_linear.weight2, self.key_linear.bias, pv.weight, pv.bias)
-        return cached(self, "qk_s3", params, lambda: s3gemm.pack_qk(W, b, wv))
+        return cached(self, "qk_bf16" if bf16 else "qk_s3", params,
+                      lambda: s3gemm.pack_qk(W, b, wv, pieces=1 if bf16 else 3))
 
-    def qk_head_packs(self):
-        """Split-GEMM packs of the query and key final_linear (cached per version),
-        or None when the split GEMM does not apply."""
-        return head_pair_packs(self.query_linear.final_linear, self.key_linear.final_linear, self)
+    def qk_head_packs(self, bf16: bool = False):
+        """Split-GEMM packs of the query and key final_linear (cached per version;
+        one bf16 piece in the bf16 mode), or None when the split GEMM does not
+        apply."""
+        return head_pair_packs(self.query_linear.final_linear, self.key_linear.final_linear, self, bf16)
 
     def value_weights_sliced(self):
         """proj_value's weight and bias with the output channels in the attention
@@ -1441,9 +1457,9 @@ class E2AttentionArbOrder_sparse(nn.Module):
         pv = self.proj_value  # its GEMMs run inside QKProjFn (one input gradient)
         wv, bv = self.value_weights_sliced()
         with record_function("query key linear function"):
-            s3 = None if bf16 else self.qk_s3_packs()
+            s3 = self.qk_s3_packs(bf16)
             Wvop = mrow_weight(pv, "weight_sl", wv, bf16, pv.lmax)
-            heads = None if bf16 else self.qk_head_packs()
+            heads = self.qk_head_packs(bf16)
             if s3 is not None and heads is not None and Wvop.split_ok():
                 q, k, v = AttnProjS3Fn.apply(x, s3, heads, Wvop, bv)
                 q, k = q.reshape(N, H, -1), k.reshape(N, H, -1)
@@ -1475,13 +1491,14 @@ class E2AttentionArbOrder_sparse(nn.Module):
 
 def _so2_packs(W: torch.Tensor, bf16: bool):
     """(forward, backward) split-GEMM packs of an SO2OutFn operand W [K, O] (y = A W,
-    gA = gy W^T), or (None, None) in bf16 mode, with the split GEMM off, or for an
-    unsupported shape."""
+    gA = gy W^T; one bf16 piece in the bf16 mode), or (None, None) with the fp32
+    split GEMM off or for an unsupported shape."""
     K, O = W.shape
-    if bf16 or not split_gemm_on() or not W.is_cuda or not (s3gemm.supported(O, K) and s3gemm.supported(K, O)):
+    if (not bf16 and not split_gemm_on()) or not W.is_cuda or not (s3gemm.supported(O, K) and s3gemm.supported(K, O)):
         return (None, None)
     W = W.float().contiguous()
-    return (s3gemm.pack(W, transpose=True), s3gemm.pack(W))
+    pc = 1 if bf16 else 3
+    return (s3gemm.pack(W, transpose=True, pieces=pc), s3gemm.pack(W, pieces=pc))
 
 
 def _env_of(poly: str, min_dist: float):
