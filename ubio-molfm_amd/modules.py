@@ -23,7 +23,8 @@ from torch.profiler import record_function
 from . import so3
 from . import _lib
 from . import gemm as s3gemm
-from .ops import AttentionFn, DegreeEmbedFn, RadialCache, RadialEvalFn, ShContractFn
+from .ops import AttentionFn, DegreeEmbedFn, RadialCache, RadialEvalFn, ShContractFn, attention_backward, \
+    attention_forward
 
 
 def _e3nn_normalize2mom(f) -> float:
@@ -535,9 +536,10 @@ class LNSiLUFn(torch.autograd.Function):
         return gx, None, None, None
 
 
-def _heads_tail(h1, P):
+def _heads_tail(h1, P, out_dtype=torch.float32):
     """LayerNorm + SiLU of each head's first Linear output h1 [2, N, hid] and the
-    second Linear (one two-batch launch): (out [2, N, n_out], LayerNorm stats)."""
+    second Linear (one two-batch launch): (out [2, N, n_out] in out_dtype, LayerNorm
+    stats)."""
     N = h1.shape[1]
     a = torch.empty_like(h1)
     st = h1.new_empty(2, N, 2)
@@ -545,7 +547,7 @@ def _heads_tail(h1, P):
         g, be, eps = P["ln"][b]
         _lib.call("e2v2_ln_silu_fwd", _dp(h1[b]), _dp(g), _dp(be), _dp(a[b]), _dp(st[b]), _lib.i32(N),
                   _lib.i32(h1.shape[2]), _lib.f32(eps), _stream())
-    out = h1.new_empty(2, N, P["p2f"].n)
+    out = h1.new_empty(2, N, P["p2f"].n, dtype=out_dtype)
     s3gemm.gemm(a, P["p2f"], out, [0, 1], bias=P["b2"], bias_batches=2)
     return out, st
 
@@ -621,6 +623,53 @@ class AttnProjS3Fn(torch.autograd.Function):
         gh = _heads_backward(h1, st, gq, gk, ctx.P)
         gx = s3gemm.qk_backward(y, gh[0], gh[1], None if gv is None else gv.contiguous(), ctx.s3)
         return gx, None, None, None, None
+
+
+class AttnBlockBF16Fn(torch.autograd.Function):
+    """The bf16 mode's attention from the layer input to the SO(2) rows in one
+    autograd node: the node projections of AttnProjS3Fn on one-piece packs, whose
+    GEMMs write q, k and v as bf16 (the storage the attention kernels gather), then
+    the attention kernels (AttentionFn).  q, k, v never cross an autograd edge, so
+    their fp32 gradients from the attention backward reach the projections'
+    backward GEMMs unrounded and no cast kernel runs either way.  Inputs with
+    gradients: x, dvec, dist and the external gate."""
+
+    @staticmethod
+    def forward(ctx, x, dvec, dist, ext_gate, s3, P, Wvop, bv, nl, atom_type, table, rc: float, q_div: float,
+                zero_order: bool, env):
+        if not (x.is_cuda and dvec.is_cuda):
+            raise RuntimeError("the e2v2 HIP path needs GPU tensors (no CPU fallback)")
+        x = x.contiguous()
+        N = x.shape[1]
+        hq, hk, y = s3gemm.qk_forward(x, s3)
+        h1 = x.new_empty(2, N, P["p1f"].n)
+        v = x.new_empty(x.shape[0], N, Wvop.w.shape[1], dtype=BF16)
+        s3gemm.gemm_grouped([
+            {"a": [hq, hk], "pw": P["p1f"], "out": h1, "widx": [0, 1], "bias": P["b1"], "bias_batches": 2},
+            {"a": x, "pw": Wvop.s3f(), "out": v, "widx": _m_degrees(Wvop.w.shape[0] - 1), "bias": bv}])
+        qk, st = _heads_tail(h1, P, BF16)
+        H = 128
+        q, k = qk[0].reshape(N, H, -1), qk[1].reshape(N, H, -1)
+        out, mrow, srow, cnt, q, k, v, ext_gate = attention_forward(q, k, v, nl, atom_type, table, rc, q_div, BF16,
+                                                                    zero_order, env, ext_gate)
+        ctx.save_for_backward(y, h1, st, q, k, v, out, mrow, srow, cnt, ext_gate)
+        ctx.s3, ctx.P, ctx.nl, ctx.atom_type, ctx.table = s3, P, nl, atom_type, table
+        ctx.rc, ctx.q_div, ctx.zero_order, ctx.env = rc, q_div, zero_order, env
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        if torch.is_grad_enabled():
+            raise NotImplementedError("the HIP E2Former path implements first-order input gradients only "
+                                      "(create_graph=True / double backward is not supported)")
+        y, h1, st, q, k, v, out, mrow, srow, cnt, ext_gate = ctx.saved_tensors
+        dq, dk, dv, ddv, dd, dgate = attention_backward(gout, q, k, v, out, mrow, srow, cnt, ext_gate, ctx.nl,
+                                                        ctx.atom_type, ctx.table, ctx.rc, ctx.q_div, ctx.zero_order,
+                                                        ctx.env)
+        N = h1.shape[1]
+        gh = _heads_backward(h1, st, dq.reshape(N, -1), dk.reshape(N, -1), ctx.P)
+        gx = s3gemm.qk_backward(y, gh[0], gh[1], dv, ctx.s3)
+        return (gx, ddv, dd, dgate) + (None,) * 11
 
 
 def head_pair_packs(fq: nn.Sequential, fk: nn.Sequential, owner, bf16: bool = False):
@@ -1460,7 +1509,11 @@ class E2AttentionArbOrder_sparse(nn.Module):
             s3 = self.qk_s3_packs(bf16)
             Wvop = mrow_weight(pv, "weight_sl", wv, bf16, pv.lmax)
             heads = self.qk_head_packs(bf16)
-            if s3 is not None and heads is not None and Wvop.split_ok():
+            # bf16 mode: projections and attention as one autograd node (AttnBlockBF16Fn, below)
+            block_bf16 = bf16 and s3 is not None and heads is not None and Wvop.split_ok()
+            if block_bf16:
+                pass
+            elif s3 is not None and heads is not None and Wvop.split_ok():
                 q, k, v = AttnProjS3Fn.apply(x, s3, heads, Wvop, bv)
                 q, k = q.reshape(N, H, -1), k.reshape(N, H, -1)
             elif heads is not None:
@@ -1477,9 +1530,14 @@ class E2AttentionArbOrder_sparse(nn.Module):
         zero = self.attn_type == "zero-order"
         with record_function("qk attention"):
             gate = None if self.tp_type == "QK_alpha" else self.qkdot_gate(x, ctx)
-            so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table, ctx.rc,
-                                    math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32, zero,
-                                    (ctx.env_kind, ctx.env_lo), gate)
+            if block_bf16:
+                so2 = AttnBlockBF16Fn.apply(x, ctx.dvec, ctx.dist, gate, s3, heads, Wvop, bv, ctx.nl, ctx.atom_type,
+                                            table, ctx.rc, math.sqrt(self.attn_scalar_head), zero,
+                                            (ctx.env_kind, ctx.env_lo))
+            else:
+                so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table, ctx.rc,
+                                        math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32, zero,
+                                        (ctx.env_kind, ctx.env_lo), gate)
         if zero:
             with record_function("zero-order"):
                 return SO2OutFn.apply(so2.view(-1), res, self.zero_out_weights(bf16), self.proj_zero.bias.detach(),

@@ -276,6 +276,54 @@ def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: f
     return a
 
 
+def attention_forward(q, k, v, nl: NeighborList, atom_type, table: RadialTable, rc: float, q_div: float,
+                      act_dtype=torch.float32, zero_order: bool = False, env=(0, 0.0), ext_gate=None):
+    """e2v2_attn_fwd: (out, mrow, srow, cnt, q, k, v, ext_gate), the last four in the
+    storage the kernels read (what ``attention_backward`` takes back)."""
+    if act_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"attention activations must be float32 or bfloat16, got {act_dtype}")
+    dev = q.device
+    N = nl.n_atoms
+    q = q.to(act_dtype).contiguous(); k = k.to(act_dtype).contiguous(); v = v.to(act_dtype).contiguous()
+    bf = int(act_dtype == torch.bfloat16)
+    if ext_gate is not None:
+        ext_gate = ext_gate.float().contiguous()
+    args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env, ext_gate)
+    if zero_order:
+        out = torch.empty(9, N, 256, dtype=act_dtype, device=dev)
+    else:
+        out = torch.empty(20 * N * 256, dtype=act_dtype, device=dev)   # l3-grouped rows
+    mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
+    srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
+    cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
+    _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _p(out), _p(mrow), _p(srow), _p(cnt), _stream(q))
+    return out, mrow, srow, cnt, q, k, v, ext_gate
+
+
+def attention_backward(gout, q, k, v, out, mrow, srow, cnt, ext_gate, nl: NeighborList, atom_type,
+                       table: RadialTable, rc: float, q_div: float, zero_order: bool = False, env=(0, 0.0)):
+    """e2v2_attn_bwd on the state of ``attention_forward``: (dq, dk, dv, ddvec [E, 3],
+    ddist [E], dL/dgate or None), all fp32."""
+    dev = q.device
+    E = nl.n_edges
+    bf = int(q.dtype == torch.bfloat16)
+    gout = gout.to(out.dtype).contiguous()
+    dgate = None if ext_gate is None else torch.empty(E, 128, dtype=torch.float32, device=dev)
+    args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env, ext_gate, dgate)
+    f = dict(dtype=torch.float32, device=dev)
+    ddv = torch.empty(max(E, 1), 3, **f)
+    dd = torch.empty(max(E, 1), **f)
+    dq = torch.empty(q.shape, **f); dk = torch.empty(k.shape, **f); dv = torch.empty(v.shape, **f)
+    # workspace of this call (per-edge weights handed from the row pass to the column pass, per-slice
+    # partial edge gradients), freed when the call returns
+    nb = int(_lib.load().e2v2_attn_bwd_workspace(E))
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
+    _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(ddv),
+              _p(dd), _p(dq), _p(dk), _p(dv), _p(ws), _lib.C.c_size_t(ws.numel()), _stream(gout))
+    del ws
+    return dq, dk, dv, ddv[:E], dd[:E], dgate
+
+
 class AttentionFn(torch.autograd.Function):
     """Edge part of E2AttentionArbOrder_sparse.forward (e2former.py:238-433) up to
     the SO(2) product's forward_linear: returns the 20 l3-sequential rows of
@@ -299,25 +347,10 @@ class AttentionFn(torch.autograd.Function):
         [E, 128]: the gate of every (edge, head) (the QKdot variants' gates, in the
         edge order of nl); the table then only supplies the inputhead."""
         _need_cuda(q, k, v, dvec, dist)
-        if act_dtype not in (torch.float32, torch.bfloat16):
-            raise ValueError(f"attention activations must be float32 or bfloat16, got {act_dtype}")
-        dev = q.device
-        N = nl.n_atoms
-        q = q.to(act_dtype).contiguous(); k = k.to(act_dtype).contiguous(); v = v.to(act_dtype).contiguous()
-        bf = int(act_dtype == torch.bfloat16)
-        if ext_gate is not None:
-            ext_gate = ext_gate.float().contiguous()
-        args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env, ext_gate)
-        if zero_order:
-            out = torch.empty(9, N, 256, dtype=act_dtype, device=dev)
-        else:
-            out = torch.empty(20 * N * 256, dtype=act_dtype, device=dev)   # l3-grouped rows
-        mrow = torch.empty(N, 128, dtype=torch.float32, device=dev)
-        srow = torch.empty(N, 128, dtype=torch.float32, device=dev)
-        cnt = torch.empty(N, 128, dtype=torch.int32, device=dev)
-        _lib.call("e2v2_attn_fwd", _lib.C.byref(args), _p(out), _p(mrow), _p(srow), _p(cnt), _stream(q))
+        out, mrow, srow, cnt, q, k, v, ext_gate = attention_forward(q, k, v, nl, atom_type, table, rc, q_div,
+                                                                    act_dtype, zero_order, env, ext_gate)
         ctx.save_for_backward(q, k, v, out, mrow, srow, cnt, ext_gate)
-        ctx.nl, ctx.atom_type, ctx.table, ctx.rc, ctx.q_div, ctx.bf = nl, atom_type, table, rc, q_div, bf
+        ctx.nl, ctx.atom_type, ctx.table, ctx.rc, ctx.q_div = nl, atom_type, table, rc, q_div
         ctx.zero_order, ctx.env = zero_order, env
         return out
 
@@ -325,25 +358,10 @@ class AttentionFn(torch.autograd.Function):
     def backward(ctx, gout):
         _no_double_backward()
         q, k, v, out, mrow, srow, cnt, ext_gate = ctx.saved_tensors
-        nl = ctx.nl
-        dev = q.device
-        E = nl.n_edges
-        gout = gout.to(out.dtype).contiguous()
-        dgate = None if ext_gate is None else torch.empty(E, 128, dtype=torch.float32, device=dev)
-        args = attn_args(nl, q, k, v, ctx.atom_type, ctx.table, ctx.q_div, ctx.rc, ctx.bf, ctx.zero_order, ctx.env,
-                         ext_gate, dgate)
-        f = dict(dtype=torch.float32, device=dev)
-        ddv = torch.empty(max(E, 1), 3, **f)
-        dd = torch.empty(max(E, 1), **f)
-        dq = torch.empty(q.shape, **f); dk = torch.empty(k.shape, **f); dv = torch.empty(v.shape, **f)
-        # workspace of this call (per-edge weights handed from the row pass to the column pass, per-slice
-        # partial edge gradients), freed when the call returns
-        nb = int(_lib.load().e2v2_attn_bwd_workspace(E))
-        ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
-        _lib.call("e2v2_attn_bwd", _lib.C.byref(args), _p(gout), _p(out), _p(mrow), _p(srow), _p(cnt), _p(ddv),
-                  _p(dd), _p(dq), _p(dk), _p(dv), _p(ws), _lib.C.c_size_t(ws.numel()), _stream(gout))
-        del ws
-        return dq, dk, dv, ddv[:E], dd[:E], None, None, None, None, None, None, None, None, dgate
+        dq, dk, dv, ddv, dd, dgate = attention_backward(gout, q, k, v, out, mrow, srow, cnt, ext_gate, ctx.nl,
+                                                        ctx.atom_type, ctx.table, ctx.rc, ctx.q_div, ctx.zero_order,
+                                                        ctx.env)
+        return dq, dk, dv, ddv, dd, None, None, None, None, None, None, None, None, dgate
 
 
 class RadialEvalFn(torch.autograd.Function):
