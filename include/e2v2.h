@@ -227,9 +227,10 @@ int e2v2_outer_bwd(const float* grad, int n_rows, const float* sh, const float* 
 /* A RadialProfile [256 + 2 n_emb -> 128 -> LayerNorm -> SiLU -> 128 -> LayerNorm -> SiLU -> 256] over
    x_edge = [rbf(d), tgt[z_i], src[z_j]] is, for one pair of atom types, a function of the edge distance d
    alone.  Its table, for a set of n_types atom types (type slot a has atomic number type_z[a]), holds per
-   type pair p = a * n_types + b (a: the query atom's type, b: the source atom's) and node n (d = n h, h a
-   power of two) four rows of nc channels: row k = h^k d^k f / dd^k (k = 0..3), float64-built by exact
-   Taylor-series propagation through every op.  Layout tab[p][n][k][nc]; a profile's 256 output
+   table slot p of a type pair (a, b) (a: the query atom's type, b: the source atom's; the slots the caller
+   chose, see e2v2_radial_table) and node n (d = n h, h a power of two) four rows of nc channels: row
+   k = h^k d^k f / dd^k (k = 0..3), float64-built by exact Taylor-series propagation through every op.
+   Layout tab[p][n][k][nc]; a profile's 256 output
    channels are placed in each row by an e2v2_radial_layout.  The edge kernels interpolate rows 0..2
    (value) and rows 1..3 (derivative) with quintic Hermite polynomials, and read the tables in these
    layouts:
@@ -242,7 +243,9 @@ int e2v2_outer_bwd(const float* grad, int n_rows, const float* sh, const float* 
        slice_width 96};
      contiguous (any other caller): channel c of profile m at 256 m + c;
        layout {col0 256 m, split 256, block 256, block_stride 0, split_stride 0, slice_width 0}. */
-#define E2V2_MAX_TYPES 32
+#define E2V2_MAX_TYPES 256
+/* table slots per launch (one per type pair an edge can join) */
+#define E2V2_MAX_PAIRS 65535
 typedef struct e2v2_radial_net {
   const float* w1;  int32_t ld_w1;    /* Linear1 weight [128][ld_w1], ld_w1 = 256 + 2 n_emb     */
   int32_t n_emb;                      /* width of the type embeddings                           */
@@ -267,16 +270,21 @@ int e2v2_radial_table_size(float rc, float rbf_coeff, int32_t refine, int32_t* n
 typedef struct e2v2_radial_layout {
   int32_t col0, split, block, block_stride, split_stride, slice_width;
 } e2v2_radial_layout;
-/* Build one profile's channels of tab (device type_z [n_types], rbf_offset [256] = mu). */
+/* Build one profile's channels of tab (device type_z [n_types], rbf_offset [256] = mu) for n_pairs table
+   slots: slot p holds the type pair pair_ab[p] = a n_types + b (device int32), or, with pair_ab NULL,
+   n_pairs = n_types^2 slots in the order p = a n_types + b.  Callers give a slot to every pair that an edge
+   can join (e.g. the products of each graph's own type set) and map pairs to slots with pair_slot
+   [n_types^2] (slot, or -1) in the edge kernels' arguments. */
 int e2v2_radial_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff, const int32_t* type_z,
-                      int32_t n_types, int32_t n_nodes, float h, float* tab, int32_t nc,
-                      const e2v2_radial_layout* layout, hipStream_t s);
+                      int32_t n_types, const int32_t* pair_ab, int32_t n_pairs, int32_t n_nodes, float h, float* tab,
+                      int32_t nc, const e2v2_radial_layout* layout, hipStream_t s);
 /* Interpolation error of one profile's table at every interval midpoint against the float64 profile:
    err (uint32 [4], zeroed by the caller) receives the float bits of max |f - f~|, max |f|,
    max h |f' - f~'|, max h |f'|. */
 int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
-                            const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h, const float* tab,
-                            int32_t nc, const e2v2_radial_layout* layout, uint32_t* err, hipStream_t s);
+                            const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
+                            int32_t n_nodes, float h, const float* tab, int32_t nc, const e2v2_radial_layout* layout,
+                            uint32_t* err, hipStream_t s);
 
 /* Per-edge values of a "plain"-layout table ([pairs][n_nodes][4][nc], nc channels): out [E][nc] =
    f_c(dist[e]) for the pair (atom_type[edge_row[e]], atom_type[col[e]]), the quintic Hermite interpolant.
@@ -284,13 +292,14 @@ int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset,
    and fc_easy(x_edge)[:, H:] (e2former.py:293-294).  e_end (device int32, or NULL for n_edges): the
    number of real edges, read on the device (the query CSR's row_ptr[n_rows]); slots e >= *e_end of a
    capacity build are not read and get out[e][:] = 0. */
-int e2v2_radial_eval(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
-                     const int32_t* atom_type, const int32_t* edge_row, const int32_t* col, const float* dist,
-                     int64_t n_edges, const int32_t* e_end, float* out, hipStream_t s);
+int e2v2_radial_eval(const float* tab, int32_t n_types, const int32_t* pair_slot, int32_t n_nodes, float h,
+                     int32_t nc, const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
+                     const float* dist, int64_t n_edges, const int32_t* e_end, float* out, hipStream_t s);
 /* ddist [E] = sum_c grad[e][c] f_c'(dist[e]) (fixed summation order); ddist[e] = 0 for e >= *e_end. */
-int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
-                         const int32_t* atom_type, const int32_t* edge_row, const int32_t* col, const float* dist,
-                         int64_t n_edges, const int32_t* e_end, const float* grad, float* ddist, hipStream_t s);
+int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, const int32_t* pair_slot, int32_t n_nodes, float h,
+                         int32_t nc, const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
+                         const float* dist, int64_t n_edges, const int32_t* e_end, const float* grad, float* ddist,
+                         hipStream_t s);
 /* x0 [E][3][C] = sum_{m in l} Y[e][m] xn[m][row(e)][C] for l = 0, 1, 2 (Y [E][9], xn [9][n_rows][C]
    m-major, edges of a row contiguous by row_ptr [n_rows + 1], C <= 256): the x_0_extra of QKdot_alpha
    (e2former.py:271-276, Y the normalised spherical harmonics) and of QKdotS_alpha (e2former.py:288-296,
@@ -347,6 +356,8 @@ typedef struct e2v2_attn_args {
      gate's distance derivative out of ddist */
   const float* ext_gate;
   float* ext_dgate;
+  /* type pair -> table slot [n_types^2] (device int32; NULL: slot a n_types + b, all pairs in the table) */
+  const int32_t* pair_slot;
 } e2v2_attn_args;
 
 /* v [9][N][C] is m-major (row r of every atom contiguous), channels in slice order.  out holds the 20
@@ -387,6 +398,7 @@ typedef struct e2v2_deg_args {
   float rtab_h;
   float avg;                     /* avg_aggregate_num                               */
   float rc, env_a, env_b, env_c;
+  const int32_t* pair_slot;      /* type pair -> table slot [n_types^2], or NULL (all pairs) */
 } e2v2_deg_args;
 
 /* x0 [9][N][C] m-major */

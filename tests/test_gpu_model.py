@@ -230,3 +230,36 @@ def test_translation_and_rotation_invariance(pkg, cuda):
     qt = torch.as_tensor(q, dtype=torch.float32, device=cuda)
     assert torch.allclose(e1, e2, rtol=1e-5, atol=1e-5)
     assert float((f1 @ qt.T - f2).norm() / f1.norm()) < 1e-4
+
+
+def test_model_more_than_32_elements(pkg, cuda):
+    """A ragged batch of 8 molecules with 40 distinct atomic numbers (five per
+    molecule, no element shared; the reference embeds any Z < 256,
+    e2former.py:127-128, 659-660) against the oracle, 1e-5 eV/atom and 1e-4
+    force rel-L2.  The radial tables hold only the 8 x 25 = 200 type pairs that
+    an edge can join (each molecule's own elements), not 40^2 = 1600."""
+    import time
+    from ubio_molfm_amd import modules, systems
+    s = systems.organics_batch(n_mol=8, nmin=10, nmax=18, seed=31)
+    ptr = np.asarray(s["graph_ptr"])
+    elems = np.random.default_rng(32).permutation(np.arange(1, 87))[:40]
+    Z = np.empty_like(s["Z"])
+    rng = np.random.default_rng(33)
+    for g in range(8):
+        own = elems[5 * g:5 * g + 5]
+        n = ptr[g + 1] - ptr[g]
+        Z[ptr[g]:ptr[g + 1]] = np.concatenate([own, rng.choice(own, size=n - 5)])
+    s = dict(s, Z=Z)
+    _, key, _ = modules.atom_type_slots(torch.as_tensor(Z, device=cuda), ptr)
+    assert len(key[0]) == 40 and key[1] is not None and len(key[1]) == 200
+    m, om = _pair(cuda, seed=34)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    _compare(m, om, s, cuda, "40-elements")
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tabs = [blk.ga._radial.table for blk in m.decoder.decoder.blocks] + [m.decoder.decoder.edge_deg_embed_dense._radial.table]
+    mb = sum(t.tab.numel() * 4 for t in tabs) / 2 ** 20
+    assert all(t.n_pairs == 200 for t in tabs)
+    print(f"[40 elements] {len(tabs)} tables of 200 type pairs: {mb:.0f} MiB, first evaluation (tables built) "
+          f"{dt:.2f} s", flush=True)

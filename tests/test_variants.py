@@ -83,3 +83,19 @@ def test_non_softmax_weights_rejected(pkg, tp):
     from ubio_molfm_amd import model
     with pytest.raises(NotImplementedError):
         model.MolfmAtomic(_cfg(tp_type=tp))
+
+
+def test_type_pairs_are_the_products_of_each_graph_type_set(pkg):
+    """atom_type_slots: the radial tables' type pairs are the union over graphs
+    of each graph's own (a, b) products (edges never leave their graph); every
+    pair for a single graph or when the union covers all T^2 (then None)."""
+    import torch
+    from ubio_molfm_amd import modules
+    Z = torch.tensor([1, 6, 1, 8, 8, 16, 1, 6])
+    ptr = [0, 3, 6, 8]                      # {1, 6}, {8, 16}, {1, 6}
+    tz, (key, pairs), slot = modules.atom_type_slots(Z, ptr)
+    assert key == (1, 6, 8, 16) and tz.tolist() == [1, 6, 8, 16] and slot.tolist() == [0, 1, 0, 2, 2, 3, 0, 1]
+    assert pairs == ((0, 0), (0, 1), (1, 0), (1, 1), (2, 2), (2, 3), (3, 2), (3, 3))
+    assert modules.atom_type_slots(Z)[1][1] is None                          # no graphs: all pairs
+    assert modules.atom_type_slots(Z, [0, 8])[1][1] is None                  # one graph
+    assert modules.atom_type_slots(torch.tensor([1, 6, 6, 1]), [0, 2, 4])[1][1] is None   # union = all pairs

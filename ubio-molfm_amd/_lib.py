@@ -68,13 +68,15 @@ class AttnArgs(C.Structure):
                 ("dvec", vp), ("dist", vp), ("q", vp), ("k", vp), ("v", vp), ("rtab", vp), ("atom_type", vp),
                 ("n_types", i32), ("rtab_n", i32), ("rtab_h", f32), ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32),
                 ("col_span", i32), ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp),
-                ("zero_order", i32), ("env_kind", i32), ("env_lo", f32), ("ext_gate", vp), ("ext_dgate", vp)]
+                ("zero_order", i32), ("env_kind", i32), ("env_lo", f32), ("ext_gate", vp), ("ext_dgate", vp),
+                ("pair_slot", vp)]
 
 
 class DegArgs(C.Structure):
     _fields_ = [("n_rows", i32), ("n_edges", i64), ("channels", i32), ("row_ptr", vp), ("dvec", vp),
                 ("dist", vp), ("col", vp), ("rtab", vp), ("atom_type", vp), ("n_types", i32), ("rtab_n", i32),
-                ("rtab_h", f32), ("avg", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32)]
+                ("rtab_h", f32), ("avg", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32),
+                ("pair_slot", vp)]
 
 
 class GemmArgs(C.Structure):

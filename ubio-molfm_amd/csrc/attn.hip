@@ -66,6 +66,7 @@ constexpr int kTabC = 2 * kH;
 __device__ __forceinline__ RadialTab make_tab(const e2v2_attn_args& A) {
   RadialTab R;
   R.tab = A.rtab; R.n_types = A.n_types; R.n_nodes = A.rtab_n; R.nc = kTabC; R.inv_h = 1.0f / A.rtab_h;
+  R.pair_slot = A.pair_slot;
   return R;
 }
 
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
       cg[lane] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], p);
       crR[lane] = 1.0f / fmaxf(d, 1e-6f);
       float tt;
-      ctoff[lane] = radial_node_sliced(R, ti * R.n_types + A.atom_type[j], s, kSl, kSlC, d, tt);
+      ctoff[lane] = radial_node_sliced(R, tab_pair(R, ti, A.atom_type[j]), s, kSl, kSlC, d, tt);
       const Hermite5 Hw = hermite5(tt);
       chw[0][lane] = Hw.a0; chw[1][lane] = Hw.a1; chw[2][lane] = Hw.a2;
       chw[3][lane] = Hw.b0; chw[4][lane] = Hw.b1; chw[5][lane] = Hw.b2;
@@ -776,7 +777,7 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
       const int j = A.col[e];
       er_b[lane] = make_float4(A.dvec[3 * e], A.dvec[3 * e + 1], A.dvec[3 * e + 2], __int_as_float(j));
       float tt;
-      er_toff[lane] = radial_node_sliced(R, ti * R.n_types + A.atom_type[j], s, kSl, kSlC, d, tt);
+      er_toff[lane] = radial_node_sliced(R, tab_pair(R, ti, A.atom_type[j]), s, kSl, kSlC, d, tt);
       const Hermite5 Hw = hermite5(tt);
       er_hw[0][lane] = Hw.a0; er_hw[1][lane] = Hw.a1; er_hw[2][lane] = Hw.a2;
       er_hw[3][lane] = Hw.b0; er_hw[4][lane] = Hw.b1; er_hw[5][lane] = Hw.b2;

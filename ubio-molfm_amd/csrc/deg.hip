@@ -33,6 +33,7 @@ __device__ __forceinline__ int l_of(int m) { return m == 0 ? 0 : (m < 4 ? 1 : 2)
 __device__ __forceinline__ RadialTab make_deg_tab(const e2v2_deg_args& A) {
   RadialTab R;
   R.tab = A.rtab; R.n_types = A.n_types; R.n_nodes = A.rtab_n; R.nc = kDegC; R.inv_h = 1.0f / A.rtab_h;
+  R.pair_slot = A.pair_slot;
   return R;
 }
 
@@ -88,7 +89,7 @@ __device__ __forceinline__ void deg_chunk(const e2v2_deg_args& A, const Envelope
     env.eval(d, p, dp);
     C.p[t] = p; C.dp[t] = dp;
     float tt;
-    C.toff[t] = radial_node_sliced(R, ti * R.n_types + A.atom_type[A.col[e]], s, kDSl, kDRow, d, tt);
+    C.toff[t] = radial_node_sliced(R, tab_pair(R, ti, A.atom_type[A.col[e]]), s, kDSl, kDRow, d, tt);
     const Hermite5 H = hermite5(tt);
     C.hw[0][t] = H.a0; C.hw[1][t] = H.a1; C.hw[2][t] = H.a2;
     C.hw[3][t] = H.b0; C.hw[4][t] = H.b1; C.hw[5][t] = H.b2;

@@ -31,12 +31,21 @@ __device__ __forceinline__ Hermite5 hermite5(float t) {
   return H;
 }
 
-// Table of one kernel launch: tab [n_types^2][n_nodes][4][nc]
+// Table of one kernel launch: tab [n_pairs][n_nodes][4][nc]; pair_slot [n_types^2] maps the type pair
+// (a, b) = (query atom's type, source atom's type) to its table slot (NULL: slot a n_types + b, all pairs)
 struct RadialTab {
   const float* tab;
   int32_t n_types, n_nodes, nc;
   float inv_h;   // 1 / h (exact: h is a power of two)
+  const int32_t* pair_slot = nullptr;
 };
+
+// Table slot of the type pair (a, b).  The host builds a slot for every pair that an edge can join (the
+// products of each graph's own type set); a pair without one (no such edge exists) reads slot 0.
+__device__ __forceinline__ int tab_pair(const RadialTab& R, int a, int b) {
+  const int ab = a * R.n_types + b;
+  return R.pair_slot ? max(R.pair_slot[ab], 0) : ab;
+}
 
 // Offset (floats) of node n of the interval holding d for pair p, and the
 // fraction t in [0, 1] (d / h, its floor and fraction are exact in fp32).

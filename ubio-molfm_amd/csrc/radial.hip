@@ -214,12 +214,15 @@ __device__ __forceinline__ void jet_rows(const Jet& y, double h, double (&r)[4])
 }
 
 // one block per (node, pair); writes the profile's 256 channels of rows k = 0..3 at their layout positions
+// (pair slot p holds the type pair pair_ab[p] = a n_types + b; pair_ab NULL: p itself)
 __global__ __launch_bounds__(kRH) void k_radial_table(e2v2_radial_net W, const float* __restrict__ mu, double coeff,
-                                                      const int32_t* __restrict__ type_z, int n_types, int n_nodes,
+                                                      const int32_t* __restrict__ type_z, int n_types,
+                                                      const int32_t* __restrict__ pair_ab, int n_nodes,
                                                       double h, float* __restrict__ tab, int nc,
                                                       e2v2_radial_layout Lo) {
   const int n = blockIdx.x, p = blockIdx.y;
-  const int za = type_z[p / n_types], zb = type_z[p % n_types];
+  const int ab = pair_ab ? pair_ab[p] : p;
+  const int za = type_z[ab / n_types], zb = type_z[ab % n_types];
   Jet y[2];
   profile_jets(W, mu, coeff, za, zb, (double)n * h, y);
 #pragma unroll
@@ -236,11 +239,13 @@ __global__ __launch_bounds__(kRH) void k_radial_table(e2v2_radial_net W, const f
 // err[1] = max |f|, err[2] = max h |f' - f~'|, err[3] = max h |f'| (float bits; non-negative
 // floats order like their bit patterns, so the unsigned atomic max is exact and deterministic).
 __global__ __launch_bounds__(kRH) void k_radial_check(e2v2_radial_net W, const float* __restrict__ mu, double coeff,
-                                                      const int32_t* __restrict__ type_z, int n_types, int n_nodes,
+                                                      const int32_t* __restrict__ type_z, int n_types,
+                                                      const int32_t* __restrict__ pair_ab, int n_nodes,
                                                       double h, const float* __restrict__ tab, int nc,
                                                       e2v2_radial_layout Lo, uint32_t* __restrict__ err) {
   const int n = blockIdx.x, p = blockIdx.y;
-  const int za = type_z[p / n_types], zb = type_z[p % n_types];
+  const int ab = pair_ab ? pair_ab[p] : p;
+  const int za = type_z[ab / n_types], zb = type_z[ab % n_types];
   Jet y[2];
   profile_jets(W, mu, coeff, za, zb, ((double)n + 0.5) * h, y);
   const Hermite5 H = hermite5(0.5f);
@@ -303,7 +308,7 @@ __global__ __launch_bounds__(64 * kEvWaves) void k_radial_eval(RadialTab R, cons
     for (int c = lane; c < R.nc; c += 64) out[e * R.nc + c] = 0.f;
     return;
   }
-  const int pair = atom_type[edge_row[e]] * R.n_types + atom_type[col[e]];
+  const int pair = tab_pair(R, atom_type[edge_row[e]], atom_type[col[e]]);
   float t;
   const float* a = R.tab + radial_node(R, pair, dist[e], t);
   const float* b = a + 4 * R.nc;
@@ -327,7 +332,7 @@ __global__ __launch_bounds__(64 * kEvWaves) void k_radial_eval_bwd(RadialTab R, 
     if (lane == 0) ddist[e] = 0.f;
     return;
   }
-  const int pair = atom_type[edge_row[e]] * R.n_types + atom_type[col[e]];
+  const int pair = tab_pair(R, atom_type[edge_row[e]], atom_type[col[e]]);
   float t;
   const float* a = R.tab + radial_node(R, pair, dist[e], t);
   const float* b = a + 4 * R.nc;
@@ -388,29 +393,43 @@ static int check_layout(const e2v2_radial_layout* Lo, int32_t nc, const char* wh
   return 0;
 }
 
+// pair slots: n_pairs of them, pair_ab [n_pairs] (device) the type pair a n_types + b of each, or NULL for all
+// n_types^2 pairs in order
+static int check_pairs(int32_t n_types, const int32_t* pair_ab, int32_t n_pairs, const char* who) {
+  E2V2_REQUIRE(n_types >= 1 && n_types <= E2V2_MAX_TYPES, "%s: %d atom types (1 .. %d)", who, n_types,
+               E2V2_MAX_TYPES);
+  E2V2_REQUIRE(n_pairs >= 1 && n_pairs <= E2V2_MAX_PAIRS && (pair_ab || n_pairs == n_types * n_types),
+               "%s: %d table pairs for %d types (1 .. %d; all n_types^2 without a pair list)", who, n_pairs, n_types,
+               E2V2_MAX_PAIRS);
+  return 0;
+}
+
 E2V2_API int e2v2_radial_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
-                               const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h, float* tab,
-                               int32_t nc, const e2v2_radial_layout* layout, hipStream_t s) {
+                               const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
+                               int32_t n_nodes, float h, float* tab, int32_t nc, const e2v2_radial_layout* layout,
+                               hipStream_t s) {
   if (int rc = check_net(net, "radial_table")) return rc;
-  E2V2_REQUIRE(rbf_offset && type_z && tab && n_types >= 1 && n_types <= E2V2_MAX_TYPES && n_nodes >= 2 && h > 0.f,
+  if (int rc = check_pairs(n_types, pair_ab, n_pairs, "radial_table")) return rc;
+  E2V2_REQUIRE(rbf_offset && type_z && tab && n_nodes >= 2 && h > 0.f,
                "radial_table: bad arguments (n_types %d, n_nodes %d)", n_types, n_nodes);
   if (int rc = check_layout(layout, nc, "radial_table")) return rc;
-  hipLaunchKernelGGL(k_radial_table, dim3((unsigned)n_nodes, (unsigned)(n_types * n_types)), dim3(kRH), 0, s, *net,
-                     rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, *layout);
+  hipLaunchKernelGGL(k_radial_table, dim3((unsigned)n_nodes, (unsigned)n_pairs), dim3(kRH), 0, s, *net,
+                     rbf_offset, (double)rbf_coeff, type_z, n_types, pair_ab, n_nodes, (double)h, tab, nc, *layout);
   E2V2_LAUNCHED("k_radial_table");
   return 0;
 }
 
 E2V2_API int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
-                                     const int32_t* type_z, int32_t n_types, int32_t n_nodes, float h,
-                                     const float* tab, int32_t nc, const e2v2_radial_layout* layout, uint32_t* err,
-                                     hipStream_t s) {
+                                     const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
+                                     int32_t n_nodes, float h, const float* tab, int32_t nc,
+                                     const e2v2_radial_layout* layout, uint32_t* err, hipStream_t s) {
   if (int rc = check_net(net, "radial_table_check")) return rc;
-  E2V2_REQUIRE(rbf_offset && type_z && tab && err && n_types >= 1 && n_types <= E2V2_MAX_TYPES && n_nodes >= 2,
-               "radial_table_check: bad arguments");
+  if (int rc = check_pairs(n_types, pair_ab, n_pairs, "radial_table_check")) return rc;
+  E2V2_REQUIRE(rbf_offset && type_z && tab && err && n_nodes >= 2, "radial_table_check: bad arguments");
   if (int rc = check_layout(layout, nc, "radial_table_check")) return rc;
-  hipLaunchKernelGGL(k_radial_check, dim3((unsigned)(n_nodes - 1), (unsigned)(n_types * n_types)), dim3(kRH), 0, s,
-                     *net, rbf_offset, (double)rbf_coeff, type_z, n_types, n_nodes, (double)h, tab, nc, *layout, err);
+  hipLaunchKernelGGL(k_radial_check, dim3((unsigned)(n_nodes - 1), (unsigned)n_pairs), dim3(kRH), 0, s,
+                     *net, rbf_offset, (double)rbf_coeff, type_z, n_types, pair_ab, n_nodes, (double)h, tab, nc,
+                     *layout, err);
   E2V2_LAUNCHED("k_radial_check");
   return 0;
 }
@@ -424,8 +443,8 @@ static int radial_eval_check(const float* tab, int32_t n_types, int32_t n_nodes,
   return 0;
 }
 
-E2V2_API int e2v2_radial_eval(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
-                              const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
+E2V2_API int e2v2_radial_eval(const float* tab, int32_t n_types, const int32_t* pair_slot, int32_t n_nodes, float h,
+                              int32_t nc, const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
                               const float* dist, int64_t n_edges, const int32_t* e_end, float* out,
                               hipStream_t s) {
   if (int rc = radial_eval_check(tab, n_types, n_nodes, h, nc, atom_type, edge_row, col, dist, n_edges,
@@ -433,23 +452,23 @@ E2V2_API int e2v2_radial_eval(const float* tab, int32_t n_types, int32_t n_nodes
     return rc;
   if (n_edges == 0) return 0;
   E2V2_REQUIRE(out, "radial_eval: out is NULL");
-  const RadialTab R{tab, n_types, n_nodes, nc, 1.0f / h};
+  const RadialTab R{tab, n_types, n_nodes, nc, 1.0f / h, pair_slot};
   hipLaunchKernelGGL(k_radial_eval, dim3((unsigned)((n_edges + kEvWaves - 1) / kEvWaves)), dim3(64 * kEvWaves), 0, s,
                      R, atom_type, edge_row, col, dist, n_edges, e_end, out);
   E2V2_LAUNCHED("k_radial_eval");
   return 0;
 }
 
-E2V2_API int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,
-                                  const int32_t* atom_type, const int32_t* edge_row, const int32_t* col,
-                                  const float* dist, int64_t n_edges, const int32_t* e_end, const float* grad,
-                                  float* ddist, hipStream_t s) {
+E2V2_API int e2v2_radial_eval_bwd(const float* tab, int32_t n_types, const int32_t* pair_slot, int32_t n_nodes,
+                                  float h, int32_t nc, const int32_t* atom_type, const int32_t* edge_row,
+                                  const int32_t* col, const float* dist, int64_t n_edges, const int32_t* e_end,
+                                  const float* grad, float* ddist, hipStream_t s) {
   if (int rc = radial_eval_check(tab, n_types, n_nodes, h, nc, atom_type, edge_row, col, dist, n_edges,
                                  "radial_eval_bwd"))
     return rc;
   if (n_edges == 0) return 0;
   E2V2_REQUIRE(grad && ddist, "radial_eval_bwd: grad or ddist is NULL");
-  const RadialTab R{tab, n_types, n_nodes, nc, 1.0f / h};
+  const RadialTab R{tab, n_types, n_nodes, nc, 1.0f / h, pair_slot};
   hipLaunchKernelGGL(k_radial_eval_bwd, dim3((unsigned)((n_edges + kEvWaves - 1) / kEvWaves)), dim3(64 * kEvWaves),
                      0, s, R, atom_type, edge_row, col, dist, n_edges, e_end, grad, ddist);
   E2V2_LAUNCHED("k_radial_eval_bwd");

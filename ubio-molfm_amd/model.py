@@ -105,16 +105,16 @@ class E2FormerBackbone(nn.Module):
             raise ValueError(f"compute_dtype must be 'fp32' or 'bf16', got {dtype!r}")
         self.compute_bf16 = name in ("bf16", "bfloat16")
 
-    def type_slots(self, Z: torch.Tensor):
-        """(type_z [T] int32: the atomic numbers present, ascending; type_key: the
-        same as a host tuple; slot [N] int32: each atom's index into type_z).  One
-        host readback per new Z tensor; repeated calls with the same live tensor
-        (an MD loop) reuse the result."""
+    def type_slots(self, Z: torch.Tensor, graph_ptr=None):
+        """``modules.atom_type_slots`` of Z and its graphs: (type_z, type_key, slot).
+        One host readback per new Z tensor; repeated calls with the same live tensor
+        and graphs (an MD loop) reuse the result."""
+        gkey = None if graph_ptr is None else np.asarray(graph_ptr, np.int64).tobytes()
         cached = self._types
-        if cached is not None and cached[0]() is Z and cached[1] == Z._version:
-            return cached[2]
-        out = atom_type_slots(Z)
-        self._types = (weakref.ref(Z), Z._version, out)
+        if cached is not None and cached[0]() is Z and cached[1] == Z._version and cached[2] == gkey:
+            return cached[3]
+        out = atom_type_slots(Z, graph_ptr)
+        self._types = (weakref.ref(Z), Z._version, gkey, out)
         return out
 
     # -- flat interface -------------------------------------------------------
@@ -126,7 +126,7 @@ class E2FormerBackbone(nn.Module):
         identity when ``reorder`` is False).  grid_box, nbr_capacity (the capacity
         build, no host readback): see ``build_neighbors``."""
         perm = None
-        type_z, type_key, slot = self.type_slots(Z)
+        type_z, type_key, slot = self.type_slots(Z, graph_ptr)
         if reorder and nl is None:
             perm = spatial_order(pos.detach(), graph_ptr)
             pos = pos[perm]

@@ -1134,7 +1134,9 @@ class SmoothLeakyReLU(nn.Module):
 class EdgeContext:
     """Per-evaluation edge data shared by every layer: the neighbour list, the edge
     geometry, each atom's type slot (atom_type [N], into type_z [T], the atomic
-    numbers present; type_key the host tuple of type_z) for the radial tables, and
+    numbers present; type_key = (host tuple of type_z, the type-slot pairs the
+    radial tables hold or None for all T^2), see ``atom_type_slots``) for the
+    radial tables, and
     the distance envelope of the attention weights (poly_dist): env_kind 0 the
     polynomial on [0, rc] (module_utils.py:1946-1954), 1 the smooth bell on
     [env_lo, rc] (module_utils.py:1956-1985), the long-range list's "poly_bell"."""
@@ -1143,6 +1145,7 @@ class EdgeContext:
                  bf16: bool = False, env_kind: int = 0, env_lo: float = 0.0):
         self.nl, self.dvec, self.dist = nl, dvec, dist
         self.atom_type, self.type_z, self.type_key = atom_type, type_z, type_key
+        self.pairs = type_key[1]
         self.rbf_offset = rbf.offset.float().contiguous()
         self.rbf_coeff = float(rbf.coeff)
         self.rc = rc
@@ -1152,17 +1155,41 @@ class EdgeContext:
         self.env_kind, self.env_lo = int(env_kind), float(env_lo)
 
 
-def atom_type_slots(Z: torch.Tensor):
-    """(type_z [T] int32: the atomic numbers present, ascending; type_key: the
-    same as a host tuple; slot [N] int32: each atom's index into type_z).  One
+def atom_type_slots(Z: torch.Tensor, graph_ptr=None):
+    """(type_z [T] int32: the atomic numbers present, ascending; type_key =
+    (the same as a host tuple, pairs); slot [N] int32: each atom's index into
+    type_z).  pairs: the ordered type-slot pairs (a, b) an edge can join, the
+    union over the graphs (graph_ptr [B+1], host) of the products of each graph's
+    own type set, since edges never leave their graph; None when that is every
+    pair (one graph, or no graph_ptr): the radial tables then hold all T^2.  One
     host read."""
-    zs = torch.unique(Z.long())
-    key = tuple(int(z) for z in zs.cpu())
+    Zl = Z.long()
+    ptr = None if graph_ptr is None else np.asarray(graph_ptr, np.int64)
+    if ptr is None or len(ptr) <= 2:
+        codes = torch.unique(Zl).cpu().numpy()
+        gz = None
+    else:
+        B = len(ptr) - 1
+        gid = torch.repeat_interleave(torch.arange(B, device=Z.device), torch.as_tensor(np.diff(ptr), device=Z.device))
+        codes = torch.unique(gid * 1024 + Zl).cpu().numpy()
+        gz = (codes // 1024, codes % 1024)
+        codes = np.unique(gz[1])
+    key = tuple(int(z) for z in codes)
     if key and (key[0] < 0 or key[-1] > 255):
         raise ValueError(f"atomic numbers must lie in [0, 255], got {key[0]}..{key[-1]}")
+    T = len(key)
+    pairs = None
+    if gz is not None:
+        idx = {z: a for a, z in enumerate(key)}
+        per = {}
+        for g, z in zip(gz[0].tolist(), gz[1].tolist()):
+            per.setdefault(g, []).append(idx[z])
+        ps = sorted({(a, b) for sl in per.values() for a in sl for b in sl})
+        pairs = None if len(ps) == T * T else tuple(ps)
+    zs = torch.as_tensor(np.asarray(key, np.int64), device=Z.device)
     lut = torch.zeros(256, dtype=torch.int32, device=Z.device)
-    lut[zs] = torch.arange(len(key), dtype=torch.int32, device=Z.device)
-    return zs.to(torch.int32).contiguous(), key, lut[Z.long()].contiguous()
+    lut[zs] = torch.arange(T, dtype=torch.int32, device=Z.device)
+    return zs.to(torch.int32).contiguous(), (key, pairs), lut[Zl].contiguous()
 
 
 _REF_CTX_KEY = "_e2v2_edge_context"
@@ -1430,7 +1457,8 @@ class E2AttentionArbOrder_sparse(nn.Module):
         E, H = nl.n_edges, self.num_attn_heads
         xd = self.dot_linear(x, ctx.bf16)                                     # [9, N, Cd]
         tab = self._radial_m0.get(self._m0_profiles(), self.target_embedding, self.source_embedding,
-                                  ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="plain")
+                                  ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="plain",
+                                  pairs=ctx.pairs)
         rad = RadialEvalFn.apply(ctx.dist, nl, ctx.atom_type, tab)
         if self.tp_type == "QKdot_alpha":
             x0 = ShContractFn.apply(_sh_integral(ctx.dvec), xd, nl).reshape(E, -1)    # [E, 3 Cd]
@@ -1526,7 +1554,8 @@ class E2AttentionArbOrder_sparse(nn.Module):
                 k = self.key_linear.head(hk, bf16).reshape(N, H, -1)
         with record_function("rbf function-a"):   # fc_easy as a distance table, built once per weight version
             table = self._radial.get([self._attn_profile()], self.target_embedding, self.source_embedding,
-                                     ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="attn")
+                                     ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="attn",
+                                     pairs=ctx.pairs)
         zero = self.attn_type == "zero-order"
         with record_function("qk attention"):
             gate = None if self.tp_type == "QK_alpha" else self.qkdot_gate(x, ctx)
@@ -1651,7 +1680,8 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
 
     def forward_fused(self, ctx: EdgeContext):
         table = self._radial.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
-                                 ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="deg")
+                                 ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="deg",
+                                 pairs=ctx.pairs)
         # the edge spherical harmonics ("e3nn sph") are formed inside the degree kernels
         with record_function("e3nn sph"):
             return DegreeEmbedFn.apply(ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table,

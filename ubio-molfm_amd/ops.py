@@ -11,6 +11,7 @@ from __future__ import annotations
 import math
 from typing import List, Optional
 
+import numpy as np
 import torch
 from torch import nn
 
@@ -81,6 +82,12 @@ class RadialTable:
     (one host readback per build).  The coarsest passing table keeps the edge
     kernels' table reads in L2.
 
+    ``pairs`` (host sequence of (a, b) type-slot pairs, a the query atom's) chooses
+    the type pairs the table holds, one slot each in the order given; None: all
+    T^2 pairs (slot a T + b).  Every pair an edge can join must have a slot (the
+    products of each graph's own type set, ``atom_type_slots``); the kernels map a
+    pair to its slot through ``pair_slot`` [T^2] (slot or -1).
+
     ``layout`` places the channels: "plain" (rows [pairs][nodes][4][nc], profile
     m at 256 m + c), "attn" (one fc_easy profile in the attention kernels' slice
     order, gate and inputhead of head h at 32 (h // 16) + h % 16 and 16 positions
@@ -96,16 +103,33 @@ class RadialTable:
 
     def __init__(self, nets, tgt: nn.Embedding, src: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
                  rc: float, type_z: torch.Tensor, tol_value: float = 1e-6, tol_deriv: float = 1e-5,
-                 max_refine: int = 3, layout: str = "plain", min_refine: int = -1):
+                 max_refine: int = 3, layout: str = "plain", min_refine: int = -1, pairs=None):
         dev = type_z.device
         if layout not in self.LAYOUTS or (layout == "attn" and len(nets) != 1) or (layout == "deg" and len(nets) != 3):
             raise ValueError(f"radial table layout {layout!r} does not fit {len(nets)} profiles")
         self.layout = layout
         self._layouts = [_lib.RadialLayout(*self.LAYOUTS[layout](m)) for m in range(len(nets))]
         self.nc = 256 * len(nets)
-        self.n_types = int(type_z.numel())
-        if self.n_types < 1 or self.n_types > MAX_TYPES:
-            raise NotImplementedError(f"{self.n_types} atom types: the radial tables hold at most {MAX_TYPES}")
+        self.n_types = T = int(type_z.numel())
+        if T < 1 or T > MAX_TYPES:
+            raise NotImplementedError(f"{T} atom types: atomic numbers index embeddings of {MAX_TYPES} entries")
+        if pairs is None:
+            self.pairs = None
+            self.n_pairs = T * T
+            self.pair_slot = self.pair_ab = None
+        else:
+            pairs = [(int(a), int(b)) for a, b in pairs]
+            if not pairs or len(set(pairs)) != len(pairs) or any(not (0 <= a < T and 0 <= b < T) for a, b in pairs):
+                raise ValueError(f"radial table pairs must be distinct type-slot pairs of {T} types")
+            if len(pairs) > MAX_PAIRS:
+                raise NotImplementedError(f"{len(pairs)} type pairs: a table holds at most {MAX_PAIRS}")
+            self.pairs = tuple(pairs)
+            self.n_pairs = len(pairs)
+            slot = np.full(T * T, -1, np.int32)
+            ab = np.array([a * T + b for a, b in pairs], np.int32)
+            slot[ab] = np.arange(len(pairs), dtype=np.int32)
+            self.pair_slot = torch.as_tensor(slot, device=dev)
+            self.pair_ab = torch.as_tensor(ab, device=dev)
         with torch.no_grad():
             self._keep = [t.detach().float().contiguous() for t in (tgt.weight, src.weight, rbf_offset)]
             tgt_w, src_w, mu = self._keep
@@ -117,11 +141,12 @@ class RadialTable:
             _lib.call("e2v2_radial_table_size", _lib.f32(rc), _lib.f32(rbf_coeff), _lib.i32(refine), _lib.C.byref(n),
                       _lib.C.byref(h))
             self.n_nodes, self.h = n.value, h.value
-            self.tab = torch.empty(self.n_types ** 2, self.n_nodes, 4, self.nc, dtype=torch.float32, device=dev)
+            self.tab = torch.empty(self.n_pairs, self.n_nodes, 4, self.nc, dtype=torch.float32, device=dev)
             err = torch.zeros(len(nets), 4, dtype=torch.int32, device=dev)
             for m, W in enumerate(self._structs):
                 args = (_lib.C.byref(W), _p(mu), _lib.f32(rbf_coeff), _p(self.type_z), _lib.i32(self.n_types),
-                        _lib.i32(self.n_nodes), _lib.f32(self.h))
+                        _lib.vp(self.pair_slot_ptr(self.pair_ab)), _lib.i32(self.n_pairs), _lib.i32(self.n_nodes),
+                        _lib.f32(self.h))
                 lo = _lib.C.byref(self._layouts[m])
                 _lib.call("e2v2_radial_table", *args, _p(self.tab), _lib.i32(self.nc), lo, st)
                 _lib.call("e2v2_radial_table_check", *args, _p(self.tab), _lib.i32(self.nc), lo,
@@ -134,6 +159,11 @@ class RadialTable:
         else:
             raise RuntimeError(f"radial table: interpolation error {self.value_err:.2e} (value) / "
                                f"{self.deriv_err:.2e} (derivative) above tolerance after {max_refine} refinements")
+
+    def pair_slot_ptr(self, t="slot"):
+        """Device address of the pair -> slot map (or of ``t``), None for all pairs."""
+        t = self.pair_slot if isinstance(t, str) else t
+        return None if t is None else t.data_ptr()
 
     def _net(self, net: nn.Sequential, tgt_w: torch.Tensor, src_w: torch.Tensor) -> _lib.RadialNet:
         lin1, ln1, lin2, ln2, lin3 = net[0], net[1], net[3], net[4], net[6]
@@ -154,7 +184,8 @@ class RadialTable:
                               src_w.data_ptr())
 
 
-MAX_TYPES = 32
+MAX_TYPES = 256
+MAX_PAIRS = 65535
 
 
 def _version_key(params):
@@ -170,12 +201,14 @@ class RadialCache:
         self.table: Optional[RadialTable] = None
 
     def get(self, nets, tgt_emb: nn.Embedding, src_emb: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
-            rc: float, type_z: torch.Tensor, type_key: tuple, layout: str = "plain"):
+            rc: float, type_z: torch.Tensor, type_key: tuple, layout: str = "plain", pairs=None):
+        """type_key: the host key of the type set (and of ``pairs``, the table's type pairs)."""
         params = [p for n in nets for p in n.parameters()] + [tgt_emb.weight, src_emb.weight, rbf_offset]
-        key = (_version_key(params), float(rbf_coeff), float(rc), type_key, layout)
+        key = (_version_key(params), float(rbf_coeff), float(rc), type_key, pairs, layout)
         if key != self.key:
             self.table = None
-            self.table = RadialTable(nets, tgt_emb, src_emb, rbf_offset, rbf_coeff, rc, type_z, layout=layout)
+            self.table = RadialTable(nets, tgt_emb, src_emb, rbf_offset, rbf_coeff, rc, type_z, layout=layout,
+                                     pairs=pairs)
             self.key = key
         return self.table
 
@@ -244,7 +277,7 @@ def deg_args(nl: NeighborList, atom_type: torch.Tensor, table: RadialTable, avg:
         raise ValueError("the degree embedding needs the table of its three profiles in slices (layout 'deg')")
     return _lib.DegArgs(nl.n_atoms, nl.n_edges, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
                         nl.col.data_ptr(), table.tab.data_ptr(), atom_type.data_ptr(), table.n_types, table.n_nodes,
-                        table.h, float(avg), float(rc), ENV_A, ENV_B, ENV_C)
+                        table.h, float(avg), float(rc), ENV_A, ENV_B, ENV_C, table.pair_slot_ptr())
 
 
 def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: float, rc: float, bf: int,
@@ -263,6 +296,7 @@ def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: f
                       ENV_B, ENV_C, int(bf))
     a.zero_order = int(bool(zero_order))
     a.env_kind, a.env_lo = int(env[0]), float(env[1])
+    a.pair_slot = table.pair_slot_ptr()
     if ext_gate is not None:
         if ext_gate.shape != (nl.n_edges, 128) or ext_gate.dtype != torch.float32 or not ext_gate.is_contiguous():
             raise ValueError(f"ext_gate must be a contiguous float32 [{nl.n_edges}, 128] tensor")
@@ -398,8 +432,9 @@ class RadialEvalFn(torch.autograd.Function):
 def _radial_eval_args(nl: NeighborList, atom_type, table: RadialTable, dist):
     # e_end = row_ptr[N] on the device: a capacity build's slots past the real edges are not read
     e_end = _lib.vp(nl.row_ptr.data_ptr() + 4 * nl.n_atoms) if nl.n_edges else None
-    return (_p(table.tab), _lib.i32(table.n_types), _lib.i32(table.n_nodes), _lib.f32(table.h),
-            _lib.i32(table.nc), _p(atom_type), _p(nl.edge_row), _p(nl.col), _p(dist), _lib.i64(nl.n_edges), e_end)
+    return (_p(table.tab), _lib.i32(table.n_types), _lib.vp(table.pair_slot_ptr()), _lib.i32(table.n_nodes),
+            _lib.f32(table.h), _lib.i32(table.nc), _p(atom_type), _p(nl.edge_row), _p(nl.col), _p(dist),
+            _lib.i64(nl.n_edges), e_end)
 
 
 class ShContractFn(torch.autograd.Function):
