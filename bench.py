@@ -327,6 +327,11 @@ def main():
                     help="CPU baseline sample of configs[3]: its own 10,000-atom system when the host's "
                          "MemAvailable covers it, else a 2,000-atom sample (auto); always the sample (default); "
                          "always the full system (full)")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay each step as one HIP graph (captured after one eager step) instead of launching "
+                         "its kernels from Python; measured equal in time at configs 1, 3 and 4")
+    ap.add_argument("--kernel-steps", type=int, default=5,
+                    help="eager steps after the timed region whose library calls are timed with HIP events")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one plain 256 MiB device copy first (scale reference for FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -353,37 +358,45 @@ def main():
     sysd = systems.CONFIGS[args.config]()
     N = len(sysd["pos"])
     mode = args.mode or ("eval" if args.config == 5 else "md")
-    integ = md.VelocityVerlet(m, sysd, dev, dt_fs=1.0, T=300.0, seed=0, lagged=not args.exact_nbr)
-    if mode == "eval":
-        integ.step = lambda: integ.__setattr__("e", integ.forces()[0])
-        integ.kinetic = lambda: 0.0
+    graph = args.graph and not args.exact_nbr
+    integ = md.VelocityVerlet(m, sysd, dev, dt_fs=1.0, T=300.0, seed=0, lagged=not args.exact_nbr, graph=graph,
+                              evaluate_only=mode == "eval")
     integ.e, integ.f = integ.forces()          # setup: forces at t = 0
-    for _ in range(args.warmup):
+    # warm-up (with a graph: at least the eager steps and the step that captures it, so that the timed
+    # region only launches the graph)
+    warmup = max(args.warmup, integ.WARM_STEPS + 1) if graph else args.warmup
+    for _ in range(warmup):
         integ.step()
+    integ.sync()
     torch.cuda.synchronize()
+    kinetic = (lambda: 0.0) if mode == "eval" else integ.kinetic
+    e_start = integ.e.sum().item() + kinetic()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        integ.step()
+    integ.sync()                             # the last step's neighbour counters (lagged check)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    edges = integ.edge_counts[-args.steps:]
+    e_end = integ.e.sum().item() + kinetic()
+    captures = integ.captures
+    # per-kernel durations: HIP events around each library call of a few more steps run eagerly (the
+    # kernels a graph replays are the same launches; replays do not pass through the Python wrappers)
     timer = _lib.KernelTimer(["e2v2_attn_fwd", "e2v2_attn_bwd",
                               "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill",
                               "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd", "e2v2_qk_proj_fwd_bf16",
                               "e2v2_qk_proj_bwd_bf16", "e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3",
                               "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated"])
-    edges = []
-    e_start = integ.e.sum().item() + integ.kinetic()
+    integ.use_graph = False
     _lib.set_timer(timer)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(min(args.steps, args.kernel_steps)):
         integ.step()
-    if mode == "md":
-        integ.sync()                         # the last step's neighbour counters (lagged check)
+    integ.sync()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
     _lib.set_timer(None)
     if mode == "md":
-        edges = integ.edge_counts[-args.steps:]
         integ.forces()                       # untimed exact build: the list expanded_nodes reads
-    else:
-        edges = [integ.n_edges] * args.steps
-    e_end = integ.e.sum().item() + integ.kinetic()
     dt = t1 - t0
     ms = dt / args.steps * 1e3
     E_mean = float(np.mean(edges))
@@ -455,8 +468,11 @@ def main():
         "metric": "attn edges/s fwd+force-bwd & MD atom-steps/s at 10k atoms; % HBM roofline",
         "value": E_mean * args.steps / dt,
         "unit": "edges/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "n_gpus": 1, "steps": args.steps, "warmup": warmup, "ms_per_step": ms,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "hip_graph": {"used": graph, "captures": captures, "warmup_steps": warmup,
+                      "kernel_timing": f"HIP events around each library call of {min(args.steps, args.kernel_steps)} "
+                                       "eager steps after the timed region"},
         "dtype": "bf16 GEMM operands, f32 accumulate" if bf16 else "f32",
         "data": "synthetic (seeded generator, random-init weights)",
         "config": {"workload": f"configs[{args.config - 1}] {sysd['name']}: {N} atoms, rc 6 A, "

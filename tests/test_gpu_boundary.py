@@ -300,3 +300,36 @@ def test_md_capacity_builds_qkdot_gates(pkg, cuda, tp):
     print(f"[md capacity {tp}] slots {nl.n_edges} edges {real} redone {lag.redone}", flush=True)
     assert nl.stats is not None and nl.n_edges > real
     assert torch.equal(ref.x, lag.x) and torch.equal(ref.p, lag.p) and torch.equal(ref.f, lag.f)
+
+
+def test_md_hip_graph_matches_eager_bitwise(pkg, cuda):
+    """graph=True: after one eager step each step is one launch of the captured
+    step graph.  Every replay (with the eager run's work and synchronisations
+    between them) equals the eager capacity-build trajectory bitwise in positions,
+    momenta, forces and energies over 6 steps; a capacity too small for the list,
+    set after step 3, overflows inside the graph, is detected before the next
+    launch, redone from the graph's backup with an exact build and captured again.
+    evaluate_only: graphed evaluations at fixed positions equal eager ones."""
+    from ubio_molfm_amd import md, systems
+    m, _ = _pair(cuda, seed=14)
+    s = systems.small_water(8, 6.2, seed=9)
+    ref = md.VelocityVerlet(m, s, cuda, dt_fs=1.0, T=300.0, seed=2)
+    gr = md.VelocityVerlet(m, s, cuda, dt_fs=1.0, T=300.0, seed=2, graph=True)
+    for k in range(6):
+        ref.step(); gr.step()
+        ref.sync(); gr.sync()
+        same = [torch.equal(a, b) for a, b in ((ref.x, gr.x), (ref.p, gr.p), (ref.f, gr.f), (ref.e, gr.e))]
+        print(f"[md graph step {k}] launches {gr.graph_launches} captures {gr.captures} redone {gr.redone} "
+              f"bitwise {same}", flush=True)
+        assert all(same)
+        if k == 3:
+            gr.capacity = (gr.n_edges - 10, gr.capacity[1])             # the next (graphed) build overflows
+    assert gr.graph_launches == 5 and gr.redone == 1 and gr.captures == 3
+    assert ref.edge_counts == gr.edge_counts
+    ev = md.VelocityVerlet(m, s, cuda, seed=2, evaluate_only=True)
+    eg = md.VelocityVerlet(m, s, cuda, seed=2, evaluate_only=True, graph=True)
+    for k in range(4):
+        ev.step(); eg.step()
+    ev.sync(); eg.sync()
+    assert eg.graph_launches == 3 and torch.equal(ev.f, eg.f) and torch.equal(ev.e, eg.e)
+    assert torch.equal(ev.x, eg.x) and torch.equal(eg.x, torch.as_tensor(np.asarray(s["pos"], np.float64), device=cuda))

@@ -25,6 +25,17 @@ time the device has long finished that build; a step whose list overflowed is
 recomputed from its saved starting state with an exact build (bitwise the same
 result, since the capacity only pads the edge arrays).  ``sync()`` resolves the
 last step; until then the state after ``step()`` is provisional.
+
+With ``graph=True`` the step (capacity neighbour build, energy, autograd forces,
+FixCom and the Verlet updates: about 300 kernels) is captured once, after one
+eager step, as a HIP graph that advances a static state in place, after copying it to a backup
+inside the same graph; each step is then one graph launch.  The build's counters
+land in a static pinned buffer and are checked before the next launch (waiting
+for the previous step only); an overflowing step is redone from the backup with
+an exact build and the graph is captured again for the new capacity.  The
+replayed kernels are those of the eager step, so the trajectory is bitwise the
+same.  ``evaluate_only=True`` makes a step an energy + force evaluation at fixed
+positions (the benchmark's eval mode), graphed the same way.
 """
 from __future__ import annotations
 
@@ -113,7 +124,8 @@ class VelocityVerlet:
     # capacity of the next build: the last count plus this fraction and a fixed margin
     CAP_FRAC, CAP_EDGES, CAP_ROW = 0.04, 4096, 64
 
-    def __init__(self, model, sysd, device, dt_fs=1.0, T=300.0, seed=0, fixcm=True, wrap=True, lagged=True):
+    def __init__(self, model, sysd, device, dt_fs=1.0, T=300.0, seed=0, fixcm=True, wrap=True, lagged=True,
+                 graph=False, evaluate_only=False):
         self.model = model
         self.sys = sysd
         self.dev = device
@@ -146,6 +158,14 @@ class VelocityVerlet:
         self.pending = None           # (pinned counters, event, state before the step) of the last one
         self.edge_counts = []         # edges of every step's build, in order (complete after sync())
         self.redone = 0               # steps recomputed after an overflowing capacity build
+        self.evaluate_only = evaluate_only
+        # HIP-graph mode: capacity builds only; the first WARM_STEPS steps run eagerly
+        self.use_graph = graph and self.lagged
+        self.graph = None             # (CUDAGraph, capacity) of the captured step
+        self._gstate = self._gbackup = self._gstats = self._gevent = None
+        self.graph_launches = 0
+        self.captures = 0
+        self._eager_steps = 0
 
     @property
     def v(self) -> torch.Tensor:
@@ -196,6 +216,7 @@ class VelocityVerlet:
     def sync(self):
         """Resolve the last step (after it the state is final)."""
         self._resolve()
+        self._resolve_graph()
 
     def forces(self):
         return self.forces_at(self.x)
@@ -203,29 +224,108 @@ class VelocityVerlet:
     def kinetic(self):
         return 0.5 * float((self.p * self.p / self.m).sum())
 
+    WARM_STEPS = 1                    # eager steps before the graph is captured
+
     def step(self):
+        if self.use_graph and self._eager_steps >= self.WARM_STEPS:
+            return self._graph_step()
         self._resolve()
         if self.f is None:
             self.e, self.f = self.forces()
         self._advance(self.capacity if self.lagged else None)
+        self._eager_steps += 1
         return self.e
+
+    def _verlet(self, x, p, f, capacity):
+        """(x', p', e', f') of one step from (x, p, f), fresh tensors: the NVE
+        velocity-Verlet update with FixCom, or with ``evaluate_only`` the energy and
+        forces at x (x, p returned as they are)."""
+        if self.evaluate_only:
+            e_new, f_new = self.forces_at(x, capacity)
+            return x, p, e_new, f_new
+        m, dt, c1 = self.m, self.dt, 0.5 * self.dt
+        fc = fixcom_forces(f, m, self.mmsum) if self.fixcm else f
+        # x + dt (p / m + c1 f / m)
+        x_new = torch.addcmul(x, self.inv_m, p, value=dt).addcmul_(self.inv_m, fc, value=dt * c1)
+        if self.fixcm:
+            x_new = fixcom_positions(x, x_new, m, self.msum)
+        e_new, f_new = self.forces_at(x_new, capacity)
+        fn = fixcom_forces(f_new, m, self.mmsum) if self.fixcm else f_new
+        # ((x_new - x) / dt + c1 fn / m) m
+        p_new = torch.addcmul(fn * c1, x_new - x, m, value=1.0 / dt)
+        if self.fixcm:
+            p_new = fixcom_momenta(p_new, m, self.msum)
+        return x_new, p_new, e_new, f_new
 
     def _advance(self, capacity):
         state = (self.x, self.p, self.e, self.f)
-        m, dt, c1 = self.m, self.dt, 0.5 * self.dt
-        f = fixcom_forces(self.f, m, self.mmsum) if self.fixcm else self.f
-        # x + dt (p / m + c1 f / m)
-        x_new = torch.addcmul(self.x, self.inv_m, self.p, value=dt).addcmul_(self.inv_m, f, value=dt * c1)
-        if self.fixcm:
-            x_new = fixcom_positions(self.x, x_new, m, self.msum)
-        e_new, f_new = self.forces_at(x_new, capacity)
+        x_new, p_new, e_new, f_new = self._verlet(self.x, self.p, self.f, capacity)
         if capacity is not None:
             self.pending = (self.last_nl.stats_host, self.last_nl.stats_event, state)
         else:
             self.edge_counts.append(self.n_edges)
-        fn = fixcom_forces(f_new, m, self.mmsum) if self.fixcm else f_new
-        # ((x_new - x) / dt + c1 fn / m) m
-        p_new = torch.addcmul(fn * c1, x_new - self.x, m, value=1.0 / dt)
-        if self.fixcm:
-            p_new = fixcom_momenta(p_new, m, self.msum)
         self.x, self.p, self.e, self.f = x_new, p_new, e_new, f_new
+
+    # -- HIP graph of one step ------------------------------------------------------
+    def _capture(self):
+        """Capture one step at the current capacity: the graph copies the static
+        state to the backup, runs the step (capacity build, counters copied to the
+        static pinned buffer) and writes the new state over the static one.  Capture
+        records the kernels without running them."""
+        self.graph = None
+        state = tuple(t.clone() for t in (self.x, self.p, self.e, self.f))
+        backup = tuple(torch.empty_like(t) for t in state)
+        stats = torch.zeros(4, dtype=torch.int32, pin_memory=True)
+        cap = (self.capacity[0], self.capacity[1], stats)
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for b, t in zip(backup, state):
+                b.copy_(t)
+            x, p, e, f = state
+            new = self._verlet(x, p, f, cap)
+            for t, n in zip(state, new):
+                if n is not t:
+                    t.copy_(n)
+        self.graph = (g, self.capacity)
+        self._gstate, self._gbackup, self._gstats = state, backup, stats
+        self.x, self.p, self.e, self.f = state
+        self.captures += 1
+
+    def _graph_step(self):
+        self._resolve()
+        self._resolve_graph()
+        if self.graph is None or self.graph[1] != self.capacity:
+            self._capture()
+        self.graph[0].replay()
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.dev))
+        self._gevent = ev
+        self.graph_launches += 1
+        return self.e
+
+    def _resolve_graph(self):
+        """Check the last graph launch's neighbour counters (waits for that launch);
+        redo an overflowing step from the backup with an exact build."""
+        ev = self._gevent
+        if ev is None:
+            return
+        self._gevent = None
+        ev.synchronize()
+        E, longest, outside, overflow = (int(v) for v in self._gstats.tolist())
+        if outside or overflow:
+            state = self._gstate
+            for t, b in zip(state, self._gbackup):
+                t.copy_(b)
+            self.redone += 1
+            x, p, e, f = state
+            new = self._verlet(x, p, f, None)            # exact build: sets n_edges and the capacity
+            for t, n in zip(state, new):
+                if n is not t:
+                    t.copy_(n)
+            self.edge_counts.append(self.n_edges)
+            return
+        self.n_edges = E
+        self.edge_counts.append(E)
+        if E > self.capacity[0] - self.CAP_EDGES // 2 or longest > self.capacity[1] - self.CAP_ROW // 2:
+            self._size_from(E, longest)                    # captured again at the next step

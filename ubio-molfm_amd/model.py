@@ -90,7 +90,7 @@ class E2FormerBackbone(nn.Module):
         self.max_neighbors = self.decoder.max_neighbors
         self.max_radius = float(self.decoder.max_radius)
         self.cells_per_direction = int(kwargs.get("pbc_expanded_num_cell_per_direction", 4))
-        self._types = None
+        self._types = []
         self.set_compute_dtype(kwargs.get("compute_dtype", "fp32"))
 
     def set_compute_dtype(self, dtype) -> None:
@@ -110,11 +110,13 @@ class E2FormerBackbone(nn.Module):
         One host readback per new Z tensor; repeated calls with the same live tensor
         and graphs (an MD loop) reuse the result."""
         gkey = None if graph_ptr is None else np.asarray(graph_ptr, np.int64).tobytes()
-        cached = self._types
-        if cached is not None and cached[0]() is Z and cached[1] == Z._version and cached[2] == gkey:
-            return cached[3]
+        # the last few live Z tensors (several integrators may share one model)
+        self._types = [c for c in self._types if c[0]() is not None]
+        for c in self._types:
+            if c[0]() is Z and c[1] == Z._version and c[2] == gkey:
+                return c[3]
         out = atom_type_slots(Z, graph_ptr)
-        self._types = (weakref.ref(Z), Z._version, gkey, out)
+        self._types = (self._types + [(weakref.ref(Z), Z._version, gkey, out)])[-4:]
         return out
 
     # -- flat interface -------------------------------------------------------
@@ -123,8 +125,9 @@ class E2FormerBackbone(nn.Module):
         """pos [N,3] (may require grad), Z [N] on the GPU; graph_ptr/cell/pbc on the host.
         Returns (node_irreps [N,9,C], neighbour list, perm): rows of node_irreps and
         the neighbour list refer to atoms ``perm`` (Morton order within each graph;
-        identity when ``reorder`` is False).  grid_box, nbr_capacity (the capacity
-        build, no host readback): see ``build_neighbors``."""
+        identity when ``reorder`` is False).  grid_box, nbr_capacity = (edges,
+        longest row[, pinned int32 [4] counter buffer]) (the capacity build, no host
+        readback): see ``build_neighbors``."""
         perm = None
         type_z, type_key, slot = self.type_slots(Z, graph_ptr)
         if reorder and nl is None:
@@ -133,7 +136,9 @@ class E2FormerBackbone(nn.Module):
             slot = slot[perm]
         if nl is None:
             nl = build_neighbors(pos.detach(), graph_ptr, cell, pbc, self.max_radius, 1e-4, self.max_neighbors,
-                                 self.cells_per_direction, grid_box=grid_box, capacity=nbr_capacity)
+                                 self.cells_per_direction, grid_box=grid_box,
+                                 capacity=None if nbr_capacity is None else tuple(nbr_capacity[:2]),
+                                 stats_host=None if nbr_capacity is None or len(nbr_capacity) < 3 else nbr_capacity[2])
         dvec, dist = EdgeGeometryFn.apply(pos, nl)
         ctx = EdgeContext(nl, dvec, dist, slot.contiguous(), type_z, type_key, self.decoder.rbf, self.max_radius,
                           self.compute_bf16)

@@ -223,7 +223,7 @@ def make_plan(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float 
 def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: float = 1e-4,
                     max_neighbors: Optional[int] = None, cells_per_direction: int = 4,
                     grid_box=None, src_include: Optional[torch.Tensor] = None,
-                    capacity: Optional[tuple] = None) -> NeighborList:
+                    capacity: Optional[tuple] = None, stats_host: Optional[torch.Tensor] = None) -> NeighborList:
     """pos [N,3] fp32 on the GPU (graphs contiguous); graph_ptr [B+1], cells
     [B,3,3], pbcs [B,3] on the host.  grid_box [2,B,3] (optional, host): per-graph
     (lo, hi) corners of the bin grid that contain every atom, e.g. the cell of
@@ -239,7 +239,10 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
     returned list carries ``stats`` = {E, longest row, atom outside the grid box,
     overflow} on the device, and the caller must check (later, asynchronously) that
     entries 2 and 3 are zero, else rebuild: the list is then truncated.  Needs a
-    grid box, no max_neighbors."""
+    grid box, no max_neighbors.  stats_host (pinned int32 [4], optional): the
+    caller's buffer the counters are copied into (no event is recorded: the caller
+    synchronises, e.g. after replaying a captured graph); without it a buffer and
+    an event are made here."""
     if not pos.is_cuda:
         raise RuntimeError("build_neighbors runs on the GPU only (pos must be a CUDA/HIP tensor)")
     dev = pos.device
@@ -265,10 +268,13 @@ def build_neighbors(pos: torch.Tensor, graph_ptr, cells, pbcs, rc: float, rmin: 
         _lib.call("e2v2_nbr_cap", _lib.vp(row_ptr.data_ptr()), _lib.i32(N), _lib.i64(E), _lib.i32(max_row),
                   _lib.vp(stats.data_ptr()), _lib.vp(stream))
         # the counters are final here: start their copy to the host now, not after the evaluation
-        stats_host = torch.empty(4, dtype=torch.int32, pin_memory=True)
+        stats_event = None
+        if stats_host is None:
+            stats_host = torch.empty(4, dtype=torch.int32, pin_memory=True)
+            stats_event = torch.cuda.Event()
         stats_host.copy_(stats, non_blocking=True)
-        stats_event = torch.cuda.Event()
-        stats_event.record(torch.cuda.current_stream(dev))
+        if stats_event is not None:
+            stats_event.record(torch.cuda.current_stream(dev))
         outside = 0
     else:
         E, max_row, outside = (int(x) for x in stats[:3].cpu())
