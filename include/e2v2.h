@@ -358,6 +358,10 @@ typedef struct e2v2_attn_args {
   float* ext_dgate;
   /* type pair -> table slot [n_types^2] (device int32; NULL: slot a n_types + b, all pairs in the table) */
   const int32_t* pair_slot;
+  /* weight form (e2former.py:329-360): 0 the segmented softmax alpha = exp(a - max) p ih / (sum + 1e-3);
+     1 alpha = softplus(a) ih p (tp_type "+softplus"); 2 alpha = sigmoid(a) ih p ("+sigmoid"), with
+     a = gate q.k / sqrt(D).  Forms 1 and 2 have no row statistics: mrow holds 0 and srow 0. */
+  int32_t weight_act;
 } e2v2_attn_args;
 
 /* v [9][N][C] is m-major (row r of every atom contiguous), channels in slice order.  out holds the 20

@@ -317,6 +317,14 @@ def segment_alpha(logit, poly, inputhead, qi, n_rows):
     return e * inputhead / (asum[qi] + 1e-3)
 
 
+def act_alpha(logit, poly, inputhead, act):
+    """The non-softmax weights of ``e2former.py:329-332`` (tp_type "+softplus" /
+    "+sigmoid"): alpha = act(a) * inputhead * p, no row statistics; softplus is
+    torch's (beta 1, threshold 20)."""
+    f = torch.nn.functional.softplus(logit) if act == "softplus" else torch.sigmoid(logit)
+    return f * inputhead * poly.unsqueeze(-1)
+
+
 def e3nn_sh(l, vec, normalize=True):
     """``e3nn.o3.spherical_harmonics(l, vec, normalize)`` with its default
     normalization="integral" (e2former.py:274): the raw polynomials of the unit
@@ -336,6 +344,8 @@ class E2AttentionArbOrder_sparse(nn.Module):
         super().__init__()
         self.attn_type = attn_type
         self.tp_type = tp_type.split("+")[0]
+        # e2former.py:123-124: substring tests on the whole tp_type, softplus first
+        self.weight_act = "softplus" if "softplus" in tp_type else "sigmoid" if "sigmoid" in tp_type else None
         self.num_attn_heads, self.attn_scalar_head, self.lmax = num_attn_heads, attn_scalar_head, lmax
         self.node_embed_dim = 128
         self.source_embedding = nn.Embedding(atom_type_cnt, 128)
@@ -405,7 +415,10 @@ class E2AttentionArbOrder_sparse(nn.Module):
             qk = sparse_ops.sparse_qk(q_scaled, key, qi, nj)
         else:
             qk = torch.sum(q_scaled[qi] * key[nj], dim=-1)
-        alpha = segment_alpha(gate * qk, poly_dist, inputhead, qi, f_N1)
+        if self.weight_act:                                 # e2former.py:329-332
+            alpha = act_alpha(gate * qk, poly_dist, inputhead, self.weight_act)
+        else:
+            alpha = segment_alpha(gate * qk, poly_dist, inputhead, qi, f_N1)
         value = self.proj_value(x)[bd["f_outcell_index"]]
         alpha_div_r = alpha / edge_dis.unsqueeze(-1).clamp_min(1e-6)
 

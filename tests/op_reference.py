@@ -8,6 +8,8 @@ Each one restates the reference's own torch formulation of the op:
 * ``attn0_ref`` zero-order aggregation of e2former.py:393-416 (value reshaped to
                 [M, 9 C / H, H]: channel c weighted by head c mod H), with the
                 polynomial or the bell envelope (module_utils.py:1946-1985)
+Both take the weight form ``act``: None for the segmented softmax, "softplus" /
+"sigmoid" for alpha = act(a) ih p (e2former.py:329-332).
 """
 import math
 
@@ -31,18 +33,26 @@ def mlp_ref(d, zi, zj, net, tgt_w, src_w, offset, coeff):
     return net(x)
 
 
-def attn_ref(q, k, v, dvec, dist, row, col, gi, T, rc, N):
-    E = row.shape[0]
+def weights(a, p, ih, row, N, act=None):
+    """alpha [E, H] of the logits a, envelope p [E] and inputhead ih."""
+    if act == "softplus":
+        return torch.nn.functional.softplus(a) * ih * p.unsqueeze(-1)
+    if act == "sigmoid":
+        return torch.sigmoid(a) * ih * p.unsqueeze(-1)
+    H = a.shape[1]
+    rh = row.view(-1, 1).expand(-1, H)
+    amax = torch.full((N, H), -torch.inf, dtype=a.dtype).scatter_reduce(0, rh, a, "amax", include_self=True)
+    e = torch.exp(a - amax[row]) * p.unsqueeze(-1)
+    s = torch.zeros((N, H), dtype=a.dtype).scatter_add(0, rh, e)
+    return e * ih / (s[row] + 1e-3)
+
+
+def attn_ref(q, k, v, dvec, dist, row, col, gi, T, rc, N, act=None):
     H = q.shape[1]
     qs = q / math.sqrt(q.shape[-1])
     qk = (qs[row] * k[col]).sum(-1)
     gate, ih = gi[:, :H], gi[:, H:]
-    a = gate * qk
-    rh = row.view(-1, 1).expand(-1, H)
-    amax = torch.full((N, H), -torch.inf, dtype=a.dtype).scatter_reduce(0, rh, a, "amax", include_self=True)
-    e = torch.exp(a - amax[row]) * envelope(dist, rc).unsqueeze(-1)
-    s = torch.zeros((N, H), dtype=a.dtype).scatter_add(0, rh, e)
-    alpha = e * ih / (s[row] + 1e-3)
+    alpha = weights(gate * qk, envelope(dist, rc), ih, row, N, act)
     w = alpha / dist.clamp_min(1e-6).unsqueeze(-1)
     C = v.shape[-1]
     wc = w[:, torch.arange(C) % H]                       # [E, C]
@@ -78,19 +88,15 @@ def bell(d, lo, hi):
     return (1 - t * t) ** 2
 
 
-def attn0_ref(q, k, v, dist, row, col, gi, env, N):
+def attn0_ref(q, k, v, dist, row, col, gi, env, N, act=None):
     """Zero-order aggregation: out[i, r, c] = sum over edges (i, j) of
-    alpha_e,(c mod H) v[j, r, c], alpha the row softmax with the envelope env(d)."""
+    alpha_e,(c mod H) v[j, r, c], alpha the row softmax (or the act form) with
+    the envelope env(d)."""
     H = q.shape[1]
     qs = q / math.sqrt(q.shape[-1])
     qk = (qs[row] * k[col]).sum(-1)
     gate, ih = gi[:, :H], gi[:, H:]
-    a = gate * qk
-    rh = row.view(-1, 1).expand(-1, H)
-    amax = torch.full((N, H), -torch.inf, dtype=a.dtype).scatter_reduce(0, rh, a, "amax", include_self=True)
-    e = torch.exp(a - amax[row]) * env(dist).unsqueeze(-1)
-    s = torch.zeros((N, H), dtype=a.dtype).scatter_add(0, rh, e)
-    alpha = e * ih / (s[row] + 1e-3)
+    alpha = weights(gate * qk, env(dist), ih, row, N, act)
     C = v.shape[-1]
     contrib = v[col] * alpha[:, torch.arange(C) % H].unsqueeze(1)     # [E, 9, C]
     return torch.zeros((N, v.shape[1], C), dtype=contrib.dtype).index_add(0, row, contrib)

@@ -101,6 +101,24 @@ def test_model_qkdot_variants(pkg, cuda, tp):
     _compare(m, om, systems.small_water(8, 6.2, seed=9), cuda, f"{tp}")
 
 
+@pytest.mark.parametrize("tp, cfg", [
+    ("QK_alpha+softplus", dict(attn_type="so2-first-order+zero-order")),
+    ("QK_alpha+sigmoid", dict()),
+    ("QKdot_alpha+sigmoid", dict(with_cluster="node_bell", long_range_layers=1)),
+])
+def test_model_act_weights(pkg, cuda, tp, cfg):
+    """tp_type "+softplus" / "+sigmoid" (alpha = act(gate q.k) inputhead p,
+    e2former.py:123-124,329-332) through the whole model against the oracle,
+    base gates: first- and zero-order blocks, and the QKdot gate with the bell
+    cluster blocks (zero order, bell envelope, caller's gate)."""
+    from ubio_molfm_amd import systems
+    m, om = _pair_variant(cuda, 16, tp_type=tp, **cfg)
+    assert m.decoder.decoder.blocks[0].ga.weight_act == tp.split("+")[1]
+    sysd = systems.organics_batch(n_mol=3, nmin=10, nmax=24, seed=11) if cfg.get("with_cluster") else \
+        systems.small_water(8, 6.2, seed=10)
+    _compare(m, om, sysd, cuda, tp)
+
+
 def test_model_qkdot_cluster_bell(pkg, cuda):
     """QKdot_alpha with the bell cluster blocks (the long-range blocks take the
     same tp_type, e2former.py:906-919) on a ragged batch."""
@@ -131,6 +149,17 @@ def test_model_organics_cfg2_bf16(pkg, cuda):
     m, om = _pair(cuda, seed=6)
     m.decoder.set_compute_dtype("bf16")
     _compare(m, om, systems.CONFIGS[2](), cuda, "cfg2-bf16", tol_e=1e-3, tol_f=2e-2)
+
+
+def test_model_sigmoid_weights_bf16(pkg, cuda):
+    """The bf16 mode (projections and attention in one autograd node) with
+    "+sigmoid" weights on a ragged organic batch against the fp32 oracle, the
+    bf16 tolerance of config 2 (1e-3 eV/atom, 2e-2 relative L2 on forces)."""
+    from ubio_molfm_amd import systems
+    m, om = _pair_variant(cuda, 17, tp_type="QK_alpha+sigmoid")
+    m.decoder.set_compute_dtype("bf16")
+    _compare(m, om, systems.organics_batch(n_mol=6, nmin=10, nmax=30, seed=12), cuda, "sigmoid-bf16",
+             tol_e=1e-3, tol_f=2e-2)
 
 
 def test_reference_interface_padded(pkg, cuda):

@@ -244,17 +244,19 @@ def test_attention_bf16_storage(pkg, cuda, clusters):
         assert e < 1e-2, (name, e)
 
 
-@pytest.mark.parametrize("env", ["poly", "bell"])
-@pytest.mark.parametrize("act", ["fp32", "bf16"])
-def test_zero_order_attention(pkg, cuda, env, act):
+@pytest.mark.parametrize("env, act, form", [("poly", "fp32", None), ("bell", "fp32", None), ("poly", "bf16", None),
+                                            ("bell", "bf16", None), ("bell", "fp32", "softplus"),
+                                            ("poly", "fp32", "sigmoid"), ("bell", "bf16", "sigmoid")])
+def test_zero_order_attention(pkg, cuda, env, act, form):
     """The zero-order attention of the long-range blocks through AttentionFn
     (e2v2_attn_fwd / e2v2_attn_bwd with zero_order set) on the long-range list
     (12 A, lower cutoff 0.1 A, sources O only), against the float64 reference
     with the profile evaluated per edge: the polynomial envelope on [0, 12] or
-    the bell on [0.1, 12].  The output does not depend on dvec: its gradient is
-    exactly zero; the distance gradient carries the envelope, the profile and
-    the softmax.  fp32: forward 2e-5, gradients 1e-4; bf16 storage (inputs and
-    output gradient rounded to bf16 on both sides): 4e-3 and 1e-2."""
+    the bell on [0.1, 12]; the segmented softmax or the softplus / sigmoid
+    weights.  The output does not depend on dvec: its gradient is exactly zero;
+    the distance gradient carries the envelope, the profile and the weights.
+    fp32: forward 2e-5, gradients 1e-4; bf16 storage (inputs and output
+    gradient rounded to bf16 on both sides): 4e-3 and 1e-2."""
     from ubio_molfm_amd import modules, neighbors, ops, systems
     rc, lo = 12.0, 0.1
     bf = act == "bf16"
@@ -264,7 +266,7 @@ def test_zero_order_attention(pkg, cuda, env, act):
     inc = torch.as_tensor(np.asarray(s["Z"]) != 1, device=cuda)
     nl = neighbors.build_neighbors(pos, s["graph_ptr"], s["cell"], s["pbc"], rc, lo, src_include=inc)
     N, E = nl.n_atoms, nl.n_edges
-    print(f"[attn zero-order {env} {act}] N={N} E={E}", flush=True)
+    print(f"[attn zero-order {env} {act} {form}] N={N} E={E}", flush=True)
     q, k, v = _attn_inputs(nl, cuda, seed=12)
     G = torch.randn(N, 9, 256, generator=torch.Generator().manual_seed(13))
     if bf:
@@ -284,7 +286,8 @@ def test_zero_order_attention(pkg, cuda, env, act):
     dist = nl.dist.clone().requires_grad_(True)
     qd = q.to(cuda).requires_grad_(True); kd = k.to(cuda).requires_grad_(True)
     vd = v.permute(1, 0, 2).to(cuda)[:, :, P].contiguous().requires_grad_(True)
-    out = ops.AttentionFn.apply(qd, kd, vd, dvec, dist, nl, slot, tab, rc, math.sqrt(8.0), adt, True, env_t)
+    out = ops.AttentionFn.apply(qd, kd, vd, dvec, dist, nl, slot, tab, rc, math.sqrt(8.0), adt, True, env_t, None,
+                                form or "softmax")
     assert out.shape == (9, N, 256)
     Gd = G.permute(1, 0, 2).to(cuda)[:, :, P].contiguous()
     out.backward(Gd.to(out.dtype))
@@ -293,12 +296,12 @@ def test_zero_order_attention(pkg, cuda, env, act):
     leaves = [t.double().requires_grad_(True) for t in (q, k, v, nl.dist.cpu())]
     gi = mlp_ref(leaves[3], Z[row], Z[col], net64, tw, sw, rb.offset.double(), float(np.float32(rb.coeff)))
     env_fn = (lambda d: bell(d, lo, rc)) if env == "bell" else (lambda d: envelope(d, rc))
-    ref = attn0_ref(*leaves[:3], leaves[3], row, col, gi, env_fn, N)
+    ref = attn0_ref(*leaves[:3], leaves[3], row, col, gi, env_fn, N, form)
     e_f = relerr(out.float()[:, :, Pinv].permute(1, 0, 2), ref)
     grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
     errs = dict(q=relerr(qd.grad, grads[0]), k=relerr(kd.grad, grads[1]),
                 v=relerr(vd.grad[:, :, Pinv].permute(1, 0, 2), grads[2]), dist=relerr(dist.grad, grads[3]))
-    print(f"[attn zero-order {env} {act}] fwd rel {e_f:.2e} bwd {errs}", flush=True)
+    print(f"[attn zero-order {env} {act} {form}] fwd rel {e_f:.2e} bwd {errs}", flush=True)
     assert torch.count_nonzero(dvec.grad) == 0
     assert e_f < (4e-3 if bf else 2e-5)
     for name, e in errs.items():
@@ -350,6 +353,60 @@ def test_attention_external_gate(pkg, cuda):
                 v=relerr(vd.grad[:, :, Pinv].permute(1, 0, 2), grads[2]), dvec=relerr(dvec.grad, grads[3]),
                 dist=relerr(dist.grad, grads[4]), gate=relerr(gd.grad, grads[5]))
     print(f"[attn ext gate] fwd rel {e_f:.2e} bwd {errs}", flush=True)
+    assert e_f < 2e-5
+    for name, e in errs.items():
+        assert e < 1e-4, (name, e)
+
+
+@pytest.mark.parametrize("form, ext", [("softplus", False), ("sigmoid", False), ("sigmoid", True)])
+def test_attention_act_weights(pkg, cuda, form, ext):
+    """The first-order attention with tp_type's "+softplus" / "+sigmoid" weights
+    alpha = act(gate q.k) ih p (e2former.py:329-332: no row maximum or sum),
+    the gate from the table or from the caller: forward and gradients through
+    AttentionFn against the float64 reference.  fp32: forward 2e-5, gradients
+    1e-4."""
+    from ubio_molfm_amd import modules, ops, so3
+    s, pos, nl = _graph(pkg, cuda, seed=6)
+    N, E = nl.n_atoms, nl.n_edges
+    print(f"[attn {form} ext={ext}] N={N} E={E}", flush=True)
+    q, k, v = _attn_inputs(nl, cuda, seed=21)
+    gate = torch.randn(E, 128, generator=torch.Generator().manual_seed(22), dtype=torch.float64)
+    G = torch.randn(N, 20, 256, generator=torch.Generator().manual_seed(23))
+    rb = modules.GaussianSmearing(256, 6.0, 2.0)
+    prof = _profile(24, 512)
+    tgt, src = _embeddings(25, 256, 128)
+    net64 = copy.deepcopy(prof).double().net
+    tw, sw = tgt.weight.detach().double().clone(), src.weight.detach().double().clone()
+    type_z, slot = _types(pkg, cuda, s["Z"])
+    tab = ops.RadialTable([prof.to(cuda).net], tgt.to(cuda), src.to(cuda), rb.offset.to(cuda), rb.coeff, 6.0, type_z,
+                          layout="attn")
+    P = modules.slice_perm(cuda)
+    Pinv = torch.argsort(P)
+    dvec = nl.dvec.clone().requires_grad_(True)
+    dist = nl.dist.clone().requires_grad_(True)
+    qd = q.to(cuda).requires_grad_(True); kd = k.to(cuda).requires_grad_(True)
+    vd = v.permute(1, 0, 2).to(cuda)[:, :, P].contiguous().requires_grad_(True)
+    gd = gate.float().to(cuda).requires_grad_(True) if ext else None
+    out = ops.AttentionFn.apply(qd, kd, vd, dvec, dist, nl, slot, tab, 6.0, math.sqrt(8.0), torch.float32, False,
+                                (0, 0.0), gd, form)
+    out.backward(ops.so2_grouped(G.permute(1, 0, 2).to(cuda)[:, :, P].contiguous()))
+    T = torch.as_tensor(so3.cartesian_tp_table())
+    row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()
+    Z = torch.as_tensor(np.asarray(s["Z"]))
+    leaves = [t.double().requires_grad_(True) for t in (q, k, v, nl.dvec.cpu(), nl.dist.cpu())]
+    gi = mlp_ref(leaves[4], Z[row], Z[col], net64, tw, sw, rb.offset.double(), float(np.float32(rb.coeff)))
+    if ext:
+        leaves.append(gate.clone().requires_grad_(True))
+        gi = torch.cat([leaves[5], gi[:, 128:]], dim=1)
+    ref = attn_ref(*leaves[:5], row, col, gi, T, 6.0, N, form)
+    e_f = relerr(ops.so2_rows(out.detach(), N)[:, :, Pinv].permute(1, 0, 2), ref)
+    grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
+    errs = dict(q=relerr(qd.grad, grads[0]), k=relerr(kd.grad, grads[1]),
+                v=relerr(vd.grad[:, :, Pinv].permute(1, 0, 2), grads[2]), dvec=relerr(dvec.grad, grads[3]),
+                dist=relerr(dist.grad, grads[4]))
+    if ext:
+        errs["gate"] = relerr(gd.grad, grads[5])
+    print(f"[attn {form} ext={ext}] fwd rel {e_f:.2e} bwd {errs}", flush=True)
     assert e_f < 2e-5
     for name, e in errs.items():
         assert e < 1e-4, (name, e)

@@ -248,6 +248,64 @@ def test_zero_order_attention_head_of_channel():
         assert torch.allclose(out[row], expect, rtol=1e-13, atol=1e-15), row
 
 
+@pytest.mark.parametrize("form, f0", [("softplus", math.log(2.0)), ("sigmoid", 0.5)])
+def test_act_weights_zero_order_unnormalised(form, f0):
+    """tp_type "+softplus" / "+sigmoid" (e2former.py:329-332) on the zero-order
+    attention of three atoms, atom 0 with two neighbours, proj_value and
+    proj_zero the identity, gate 0 (logit 0: softplus ln 2, sigmoid 1/2) and
+    inputhead 1 on head h0 only: row 0 is f0 (p1 v1 + p2 v2) in the channels of
+    h0, a plain sum over the row.  Catches: a row normalisation left in (the
+    softmax's (p1 v1 + p2 v2) / (p1 + p2 + 1e-3)), the envelope or the inputhead
+    dropped (every head would then pass), sigmoid and softplus swapped."""
+    torch.manual_seed(5)
+    H, C = 4, 8
+    ga = om.E2AttentionArbOrder_sparse(C=C, attn_weight_input_dim=6, num_attn_heads=H, attn_scalar_head=2,
+                                       attn_type="zero-order", tp_type="QK_alpha+" + form).double()
+    assert ga.weight_act == form
+    with torch.no_grad():
+        for lin in (ga.proj_value, ga.proj_zero):
+            lin.weight.copy_(torch.eye(C, dtype=D64).expand(3, C, C))
+            lin.bias.zero_()
+        last = ga.fc_easy.net[-1]
+        last.weight.zero_()
+        last.bias.zero_()
+        h0 = 2
+        last.bias[H + h0] = 1.0
+    Z = torch.tensor([8, 6, 1])
+    pos = torch.tensor([[0.0, 0.0, 0.0], [0.0, 0.0, 2.5], [1.7, 0.0, 0.0]], dtype=D64)
+    qi, nj = torch.tensor([0, 0, 1, 2]), torch.tensor([1, 2, 0, 0])
+    vec = pos[qi] - pos[nj]
+    dist = vec.norm(dim=-1)
+    poly = om.polynomial(dist, 6.0)
+    rbf = om.GaussianSmearing(6, cutoff=6.0).double()(dist)
+    x = torch.randn(3, 9, C, dtype=D64)
+    bd = dict(query_idx=qi, neighbor_idx=nj, f_outcell_index=torch.arange(3), f_exp_node_pos=pos)
+    out, _ = ga(pos, x, dist, vec, rbf, Z, poly, bd)
+    chans = torch.tensor([h0, h0 + H])
+    p = poly.tolist()
+    expect = torch.zeros(3, 9, C, dtype=D64)
+    expect[0][:, chans] = f0 * (p[0] * x[1][:, chans] + p[1] * x[2][:, chans])
+    expect[1][:, chans] = f0 * p[2] * x[0][:, chans]
+    expect[2][:, chans] = f0 * p[3] * x[0][:, chans]
+    assert torch.allclose(out, expect, rtol=1e-13, atol=1e-15)
+
+
+def test_act_weights_slopes_and_softplus_threshold():
+    """d alpha / d a at a = 0 is 1/2 (softplus) and 1/4 (sigmoid) times ih p;
+    softplus is the identity above 20 (torch's threshold) and tends to e^a at
+    large negative a.  Catches the derivative of the wrong form and a softplus
+    of the wrong base or sign."""
+    a = torch.tensor([[0.0], [0.0]], dtype=D64, requires_grad=True)
+    p = torch.tensor([0.5, 1.0], dtype=D64)
+    ih = torch.tensor([[2.0], [3.0]], dtype=D64)
+    for form, slope in (("softplus", 0.5), ("sigmoid", 0.25)):
+        (g,) = torch.autograd.grad(om.act_alpha(a, p, ih, form).sum(), a)
+        assert torch.allclose(g[:, 0], slope * ih[:, 0] * p, rtol=1e-15, atol=0)
+    big = torch.tensor([[25.0], [-30.0]], dtype=torch.float32)
+    sp = om.act_alpha(big, torch.ones(2), torch.ones(2, 1), "softplus")[:, 0]
+    assert float(sp[0]) == 25.0 and abs(float(sp[1]) / math.exp(-30.0) - 1.0) < 1e-6
+
+
 def test_chunked_sparse_ops_equal_fallbacks(monkeypatch):
     """The edge-chunked QK / value aggregation (used by the oracle above
     CHUNKED_EDGES edges, e.g. for the CPU baseline at 10k atoms) give the same

@@ -78,11 +78,20 @@ def test_qkdot_variants_state_dict_names(pkg, tp):
     m.load_state_dict(om.state_dict(), strict=True)
 
 
-@pytest.mark.parametrize("tp", ["QK_alpha+softplus", "QK_alpha+sigmoid", "QKdot_alpha+softplus"])
-def test_non_softmax_weights_rejected(pkg, tp):
+@pytest.mark.parametrize("tp, form", [("QK_alpha+softplus", "softplus"), ("QK_alpha+sigmoid", "sigmoid"),
+                                      ("QKdot_alpha+softplus", "softplus"), ("QKdotS_alpha+sigmoid", "sigmoid"),
+                                      ("QK_alpha+sigmoid+softplus", "softplus"), ("QK_alpha", "softmax")])
+def test_weight_forms_parsed_like_the_reference(pkg, tp, form):
+    """e2former.py:123-124: substring tests on the whole tp_type, softplus
+    taking precedence; the parameters are those of the base tp_type, so state
+    dicts load both ways."""
     from ubio_molfm_amd import model
-    with pytest.raises(NotImplementedError):
-        model.MolfmAtomic(_cfg(tp_type=tp))
+    from oracle.model import MolfmAtomic as OracleModel
+    m = model.MolfmAtomic(_cfg(tp_type=tp))
+    assert all(b.ga.weight_act == form for b in m.decoder.decoder.blocks)
+    om = OracleModel(tp_type=tp)
+    assert all(b.ga.weight_act == (None if form == "softmax" else form) for b in om.decoder.decoder.blocks)
+    om.load_state_dict(m.state_dict(), strict=True)
 
 
 def test_type_pairs_are_the_products_of_each_graph_type_set(pkg):

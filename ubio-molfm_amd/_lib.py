@@ -69,7 +69,7 @@ class AttnArgs(C.Structure):
                 ("n_types", i32), ("rtab_n", i32), ("rtab_h", f32), ("q_div", f32), ("rc", f32), ("env_a", f32), ("env_b", f32), ("env_c", f32), ("act_bf16", i32),
                 ("col_span", i32), ("col_slot_member", vp), ("col_slot_edge", vp), ("col_n_slots", vp),
                 ("zero_order", i32), ("env_kind", i32), ("env_lo", f32), ("ext_gate", vp), ("ext_dgate", vp),
-                ("pair_slot", vp)]
+                ("pair_slot", vp), ("weight_act", i32)]
 
 
 class DegArgs(C.Structure):

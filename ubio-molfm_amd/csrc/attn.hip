@@ -52,8 +52,31 @@ __device__ __forceinline__ int pos_head(int p) { return ((p >> 5) << 4) | (p & 1
 // 2 g + 1).  Lane l of a wave owns position 64 g + l, and dims 4 (l % 2) .. +3
 // of head 32 g + l / 2 for dk.
 constexpr int kGroups = 4, kGroupHeads = kH / kGroups, kGroupC = kC / kGroups;
-// kernel variants (template bits): zero-order aggregation, bell envelope, the caller's gate
-constexpr int kModeZero = 1, kModeBell = 2, kModeExt = 4;
+// kernel variants (template bits): zero-order aggregation, bell envelope, the caller's gate, and the weight
+// form: the segmented softmax (neither bit), or alpha = act(a) ih p with act softplus or sigmoid
+// (tp_type "+softplus" / "+sigmoid", e2former.py:123-124, 329-334: no row maximum or sum)
+constexpr int kModeZero = 1, kModeBell = 2, kModeExt = 4, kModeSoftplus = 8, kModeSigmoid = 16;
+constexpr int kModeAct = kModeSoftplus | kModeSigmoid;
+
+// The non-softmax weight activations and their derivatives: softplus as torch's F.softplus (beta 1,
+// threshold 20: the identity above it), the logistic sigmoid.
+template <int kAct>
+__device__ __forceinline__ void weight_act(float a, float& f, float& df) {
+  if constexpr (kAct == kModeSoftplus) {
+    if (a > 20.f) {
+      f = a;
+      df = 1.f;
+    } else {
+      const float e = expf(a);
+      f = log1pf(e);
+      df = e / (1.f + e);
+    }
+  } else {
+    const float sg = 1.f / (1.f + expf(-a));
+    f = sg;
+    df = sg * (1.f - sg);
+  }
+}
 __device__ __forceinline__ Envelope make_env(const e2v2_attn_args& A) {
   Envelope E;
   E.rc = A.rc; E.a = A.env_a; E.b = A.env_b; E.c = A.env_c;
@@ -176,6 +199,7 @@ template <typename TS, int kMode>
 __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __restrict__ out, float* __restrict__ mrow,
                                                     float* __restrict__ srow, int32_t* __restrict__ cnt) {
   constexpr bool kZ = kMode & kModeZero, kBell = kMode & kModeBell, kExt = kMode & kModeExt;
+  constexpr int kAct = kMode & kModeAct;
   constexpr int CH = 32;               // edges per chunk
   __shared__ uint32_t ckof[CH];        // byte offsets of the edge's k row (head 16 s) and v rows (position 32 s)
   __shared__ uint32_t cvof[CH];
@@ -287,6 +311,16 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
         lapply(k, Xa);
       }
     }
+    if constexpr (kAct != 0) {
+      // alpha = act(a) ih p: no statistics, nothing to rescale
+      for (int el = sub; el < nc; el += 4) {
+        float f, df;
+        weight_act<kAct>(a_s[el][hh], f, df);
+        const float ee = f * cg[el].w;
+        coef_s[el][hh] = kZ ? ee * coef_s[el][hh] : (ee * coef_s[el][hh]) * crR[el];
+      }
+      if (sub == 0) sc_s[hh] = 1.f;
+    } else {
     // online softmax of head h over the chunk (each lane reads back the logits it wrote)
     float cm = -INFINITY;
     for (int el = sub; el < nc; el += 4) cm = fmaxf(cm, a_s[el][hh]);
@@ -311,6 +345,7 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
     s_run = s_run * sc + ls;
     m_run = m_new;
     if (sub == 0) sc_s[hh] = sc;
+    }
     __syncthreads();
     // value aggregation of position 32 s + u over the edges of parity par
     const float scu = sc_s[hu];
@@ -374,7 +409,7 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
       acc[r][0] += red[3 * r][u]; acc[r][1] += red[3 * r + 1][u]; acc[r][2] += red[3 * r + 2][u];
     }
     // this lane (sub = u / 16, hh = u % 16) holds the statistics of head 16 s + hu
-    const float inv = 1.0f / (s_run + kEps);
+    const float inv = kAct ? 1.0f : 1.0f / (s_run + kEps);   // (no normalisation for the act forms)
     if constexpr (kZ) {
       // zero order: the aggregated rows themselves, m-major [9][N][C]
       const size_t os = (size_t)A.n_rows * kC;
@@ -393,7 +428,7 @@ __global__ __launch_bounds__(64) void k_attn_fwd_sl(e2v2_attn_args A, TS* __rest
     }
   }
   if (lane < kSlH) {
-    mrow[(size_t)i * kH + h] = m_run;
+    mrow[(size_t)i * kH + h] = kAct ? 0.f : m_run;
     srow[(size_t)i * kH + h] = s_run;
     cnt[(size_t)i * kH + h] = c_run;
   }
@@ -613,6 +648,7 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
                                                         float* __restrict__ dq, float* __restrict__ w_out,
                                                         float* __restrict__ dqk_out, int grp) {
   constexpr bool kZ = kMode & kModeZero, kBell = kMode & kModeBell, kExt = kMode & kModeExt;
+  constexpr int kAct = kMode & kModeAct;
   constexpr int CH = 64;
   __shared__ float4 er_a[CH];      // p, dp/dd, 1/max(d, 1e-6), d
   __shared__ float4 er_b[CH];      // dvec, column (int bits)
@@ -651,12 +687,15 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
       g1[z] = f32(G[rz + p1]);
     }
     // D_h = sum over the head's two channels and the output rows, summed as the first channel then the second
+    // (the softmax row term; the act forms have none)
     float d0 = 0.f, d1 = 0.f;
+    if constexpr (kAct == 0) {
 #pragma unroll
-    for (int z = 0; z < NG; ++z) {
-      const size_t rz = row_at(z);
-      d0 = fmaf(g0[z], f32(O[rz + p0]), d0);
-      d1 = fmaf(g1[z], f32(O[rz + p1]), d1);
+      for (int z = 0; z < NG; ++z) {
+        const size_t rz = row_at(z);
+        d0 = fmaf(g0[z], f32(O[rz + p0]), d0);
+        d1 = fmaf(g1[z], f32(O[rz + p1]), d1);
+      }
     }
     const float Dh = d1 + d0;
     if constexpr (kZ) {
@@ -670,12 +709,16 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
       tp_transpose(g0, dA0);
       tp_transpose(g1, dA1);
     }
-    m = mrow[(size_t)i * kH + h];
-    const float sr = srow[(size_t)i * kH + h];
-    const int cn = cnt[(size_t)i * kH + h];
-    inv = 1.0f / (sr + kEps);
-    dsum = Dh * inv;
-    dmc = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
+    if constexpr (kAct != 0) {
+      m = 0.f; inv = 1.f; dsum = 0.f; dmc = 0.f;
+    } else {
+      m = mrow[(size_t)i * kH + h];
+      const float sr = srow[(size_t)i * kH + h];
+      const int cn = cnt[(size_t)i * kH + h];
+      inv = 1.0f / (sr + kEps);
+      dsum = Dh * inv;
+      dmc = cn > 0 ? (-Dh * kEps * inv) / (float)cn : 0.f;
+    }
   }
   float qs[kD];
   load_qs<TS>(A, i, h, qs);
@@ -728,7 +771,14 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
     for (int q = 0; q < kD; ++q) kf[q] = f32(X.k[q]);
     const float qk = half_dot(qs, kf) + half_dot(qs + 4, kf + 4);
     const float a = gate * qk;
-    const float ex = fexp(a - m);
+    // softmax: ex = exp(a - m), d ex/da = ex; act forms: ex = act(a), d ex/da = act'(a)
+    float ex, dex;
+    if constexpr (kAct != 0) {
+      weight_act<kAct>(a, ex, dex);
+    } else {
+      ex = fexp(a - m);
+      dex = ex;
+    }
     const float ee = ex * pe;
     const float alpha = (ee * ih) * inv;
     const float w = kZ ? alpha : alpha * rR;
@@ -750,8 +800,8 @@ __global__ __launch_bounds__(64) void k_attn_bwd_row_sl(e2v2_attn_args A, const 
     const float dR = (!kZ && d > 1e-6f) ? -dalpha * alpha * rR : 0.f;
     const float dih = dalpha * ee * inv;
     const float de = dalpha * ih * inv - dsum;
-    float da = de * ee;
-    if (a == m) da += dmc;
+    float da = de * (dex * pe);
+    if (kAct == 0 && a == m) da += dmc;
     const float dpv = de * ex;
     const float dqk = da * gate;
     ntstore(w, w_out + e * kGroupHeads + hg);
@@ -824,19 +874,32 @@ using namespace e2v2;
 
 // kernel variant of the arguments (combinations checked by check_table): the bell only with zero order
 static int kernel_mode(const e2v2_attn_args& A) {
-  return (A.zero_order ? kModeZero : 0) | (A.env_kind ? kModeBell : 0) | (A.ext_gate ? kModeExt : 0);
+  return (A.zero_order ? kModeZero : 0) | (A.env_kind ? kModeBell : 0) | (A.ext_gate ? kModeExt : 0) |
+         (A.weight_act == 1 ? kModeSoftplus : A.weight_act == 2 ? kModeSigmoid : 0);
 }
 
-// Calls f(integral_constant<int, mode>) for the instantiated variants 0, 1, 3, 4, 5, 7.
+// Calls f(integral_constant<int, mode>) for the instantiated variants: {0, Z, Z|B, E, E|Z, E|Z|B} with each of
+// the three weight forms.
+template <int kA, typename F>
+static int with_shape(int mode, F&& f) {
+  switch (mode & ~kModeAct) {
+    case 0: return f(std::integral_constant<int, kA>{});
+    case kModeZero: return f(std::integral_constant<int, kA | kModeZero>{});
+    case kModeZero | kModeBell: return f(std::integral_constant<int, kA | kModeZero | kModeBell>{});
+    case kModeExt: return f(std::integral_constant<int, kA | kModeExt>{});
+    case kModeExt | kModeZero: return f(std::integral_constant<int, kA | kModeExt | kModeZero>{});
+    case kModeExt | kModeZero | kModeBell:
+      return f(std::integral_constant<int, kA | kModeExt | kModeZero | kModeBell>{});
+    default: return ::e2v2::set_error(-1, "attention variant %d is not built", mode);
+  }
+}
+
 template <typename F>
 static int with_mode(int mode, F&& f) {
-  switch (mode) {
-    case 0: return f(std::integral_constant<int, 0>{});
-    case kModeZero: return f(std::integral_constant<int, kModeZero>{});
-    case kModeZero | kModeBell: return f(std::integral_constant<int, kModeZero | kModeBell>{});
-    case kModeExt: return f(std::integral_constant<int, kModeExt>{});
-    case kModeExt | kModeZero: return f(std::integral_constant<int, kModeExt | kModeZero>{});
-    case kModeExt | kModeZero | kModeBell: return f(std::integral_constant<int, kModeExt | kModeZero | kModeBell>{});
+  switch (mode & kModeAct) {
+    case 0: return with_shape<0>(mode, f);
+    case kModeSoftplus: return with_shape<kModeSoftplus>(mode, f);
+    case kModeSigmoid: return with_shape<kModeSigmoid>(mode, f);
     default: return ::e2v2::set_error(-1, "attention variant %d is not built", mode);
   }
 }
@@ -846,6 +909,8 @@ static int check_table(const e2v2_attn_args& A, const char* who) {
                    (A.env_kind == 0 || (A.zero_order == 1 && A.env_lo >= 0.f && A.env_lo < A.rc)),
                "%s: zero_order %d with envelope kind %d (lo %g, rc %g) is not supported (the bell envelope is "
                "built for the zero-order layers)", who, A.zero_order, A.env_kind, (double)A.env_lo, (double)A.rc);
+  E2V2_REQUIRE(A.weight_act >= 0 && A.weight_act <= 2, "%s: weight form %d (0 softmax, 1 softplus, 2 sigmoid)",
+               who, A.weight_act);
   E2V2_REQUIRE(A.rtab && A.atom_type && A.n_types >= 1 && A.n_types <= E2V2_MAX_TYPES && A.rtab_n >= 2 &&
                    A.rtab_h > 0.f,
                "%s: needs the fc_easy table and atom types (n_types %d, rtab_n %d)", who, A.n_types, A.rtab_n);

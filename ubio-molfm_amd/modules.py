@@ -636,7 +636,7 @@ class AttnBlockBF16Fn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, dvec, dist, ext_gate, s3, P, Wvop, bv, nl, atom_type, table, rc: float, q_div: float,
-                zero_order: bool, env):
+                zero_order: bool, env, weight_act: str = "softmax"):
         if not (x.is_cuda and dvec.is_cuda):
             raise RuntimeError("the e2v2 HIP path needs GPU tensors (no CPU fallback)")
         x = x.contiguous()
@@ -651,10 +651,10 @@ class AttnBlockBF16Fn(torch.autograd.Function):
         H = 128
         q, k = qk[0].reshape(N, H, -1), qk[1].reshape(N, H, -1)
         out, mrow, srow, cnt, q, k, v, ext_gate = attention_forward(q, k, v, nl, atom_type, table, rc, q_div, BF16,
-                                                                    zero_order, env, ext_gate)
+                                                                    zero_order, env, ext_gate, weight_act)
         ctx.save_for_backward(y, h1, st, q, k, v, out, mrow, srow, cnt, ext_gate)
         ctx.s3, ctx.P, ctx.nl, ctx.atom_type, ctx.table = s3, P, nl, atom_type, table
-        ctx.rc, ctx.q_div, ctx.zero_order, ctx.env = rc, q_div, zero_order, env
+        ctx.rc, ctx.q_div, ctx.zero_order, ctx.env, ctx.weight_act = rc, q_div, zero_order, env, weight_act
         return out
 
     @staticmethod
@@ -665,11 +665,11 @@ class AttnBlockBF16Fn(torch.autograd.Function):
         y, h1, st, q, k, v, out, mrow, srow, cnt, ext_gate = ctx.saved_tensors
         dq, dk, dv, ddv, dd, dgate = attention_backward(gout, q, k, v, out, mrow, srow, cnt, ext_gate, ctx.nl,
                                                         ctx.atom_type, ctx.table, ctx.rc, ctx.q_div, ctx.zero_order,
-                                                        ctx.env)
+                                                        ctx.env, ctx.weight_act)
         N = h1.shape[1]
         gh = _heads_backward(h1, st, dq.reshape(N, -1), dk.reshape(N, -1), ctx.P)
         gx = s3gemm.qk_backward(y, gh[0], gh[1], dv, ctx.s3)
-        return (gx, ddv, dd, dgate) + (None,) * 11
+        return (gx, ddv, dd, dgate) + (None,) * 12
 
 
 def head_pair_packs(fq: nn.Sequential, fk: nn.Sequential, owner, bf16: bool = False):
@@ -1266,7 +1266,9 @@ class E2AttentionArbOrder_sparse(nn.Module):
     (proj_zero on the alpha-weighted sum of the neighbours' values,
     e2former.py:199-204,411-416) and tp_type QK_alpha, QKdot_alpha (gate from
     the spherical harmonics of the edge against dot_linear of the query node,
-    e2former.py:143-154,270-283) or QKdotS_alpha (e2former.py:155-167,284-300).
+    e2former.py:143-154,270-283) or QKdotS_alpha (e2former.py:155-167,284-300),
+    each with the segmented softmax or, with "+softplus" / "+sigmoid" in
+    tp_type, alpha = act(gate q.k) inputhead p (e2former.py:123-124,329-332).
     The QKdot gates are formed per edge (e2v2_sh_contract, e2v2_radial_eval,
     the gate's small dense layers) and handed to the attention kernels as their
     gate; the inputhead stays a table inside the kernels."""
@@ -1278,6 +1280,8 @@ class E2AttentionArbOrder_sparse(nn.Module):
         self.num_attn_heads, self.attn_scalar_head, self.lmax = num_attn_heads, attn_scalar_head, lmax
         self.node_embed_dim = 128
         self.attn_type, self.tp_type = attn_type, tp_type.split("+")[0]
+        # the weight form: substring tests on the whole tp_type, softplus first (e2former.py:123-124, 329-332)
+        self.weight_act = "softplus" if "softplus" in tp_type else "sigmoid" if "sigmoid" in tp_type else "softmax"
         self.source_embedding = nn.Embedding(atom_type_cnt, 128)
         self.target_embedding = nn.Embedding(atom_type_cnt, 128)
         nn.init.uniform_(self.source_embedding.weight.data, -0.001, 0.001)
@@ -1562,11 +1566,11 @@ class E2AttentionArbOrder_sparse(nn.Module):
             if block_bf16:
                 so2 = AttnBlockBF16Fn.apply(x, ctx.dvec, ctx.dist, gate, s3, heads, Wvop, bv, ctx.nl, ctx.atom_type,
                                             table, ctx.rc, math.sqrt(self.attn_scalar_head), zero,
-                                            (ctx.env_kind, ctx.env_lo))
+                                            (ctx.env_kind, ctx.env_lo), self.weight_act)
             else:
                 so2 = AttentionFn.apply(q, k, v, ctx.dvec, ctx.dist, ctx.nl, ctx.atom_type, table, ctx.rc,
                                         math.sqrt(q.shape[-1]), BF16 if bf16 else torch.float32, zero,
-                                        (ctx.env_kind, ctx.env_lo), gate)
+                                        (ctx.env_kind, ctx.env_lo), gate, self.weight_act)
         if zero:
             with record_function("zero-order"):
                 return SO2OutFn.apply(so2.view(-1), res, self.zero_out_weights(bf16), self.proj_zero.bias.detach(),
@@ -1792,7 +1796,6 @@ def check_supported(C, lmax, heads, head_dim, n_basis, irreps_head, norm_layer, 
     ok = (C == 256 and lmax == 2 and heads == 128 and head_dim == 8 and n_basis == 256 and hc * heads == C
           and hl == lmax and norm_layer in ("rms_norm_sh", "rms_norm_sh_BL")
           and tp_type.split("+")[0] in ("QK_alpha", "QKdot_alpha", "QKdotS_alpha")
-          and "softplus" not in tp_type and "sigmoid" not in tp_type
           and all(a in ("so2-first-order", "zero-order") for a in attn_type.split("+"))
           and len(attn_type.split("+")) <= 2 and ("s3" in ffn_type or "default" in ffn_type)
           and basis_type == "gaussiansmear" and "wolayernorm" not in edge_embedtype)
@@ -1800,7 +1803,7 @@ def check_supported(C, lmax, heads, head_dim, n_basis, irreps_head, norm_layer, 
         raise NotImplementedError(
             "the MI355X path implements the E2Former-V2 production configuration: irreps 256x0e+256x1e+256x2e, "
             "irreps_head 2x0e+2x1e+2x2e, 128 heads, attn_scalar_head 8, 256 basis, rms_norm_sh, tp_type QK_alpha / "
-            "QKdot_alpha / QKdotS_alpha (softmax weights), attn_type so2-first-order / zero-order (or 'a+b' of the "
+            "QKdot_alpha / QKdotS_alpha (softmax, +softplus or +sigmoid weights), attn_type so2-first-order / zero-order (or 'a+b' of the "
             "two), ffn s3")
     if "node" not in str(with_cluster) and str(with_cluster) not in ("False", "false", "0", "None", "none"):
         raise ValueError("Only with_cluster='node*' is restored in this release tree. "

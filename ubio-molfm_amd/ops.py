@@ -280,13 +280,20 @@ def deg_args(nl: NeighborList, atom_type: torch.Tensor, table: RadialTable, avg:
                         table.h, float(avg), float(rc), ENV_A, ENV_B, ENV_C, table.pair_slot_ptr())
 
 
+WEIGHT_ACTS = {"softmax": 0, "softplus": 1, "sigmoid": 2}
+
+
 def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: float, rc: float, bf: int,
-              zero_order: bool = False, env=(0, 0.0), ext_gate=None, ext_dgate=None):
+              zero_order: bool = False, env=(0, 0.0), ext_gate=None, ext_dgate=None, weight_act: str = "softmax"):
     """e2v2_attn_args over the neighbour list (with its column clusters when built).
     zero_order selects the zero-order aggregation; env = (kind, lower end): kind 0
     the polynomial envelope on [0, rc], 1 the smooth bell on [lower end, rc];
     ext_gate [E, 128] fp32 (or None) replaces the table's gate rows, ext_dgate
-    [E, 128] receives its gradient in the backward."""
+    [E, 128] receives its gradient in the backward; weight_act the weight form
+    ("softmax", or "softplus" / "sigmoid" of tp_type's "+softplus" / "+sigmoid",
+    e2former.py:329-332)."""
+    if weight_act not in WEIGHT_ACTS:
+        raise ValueError(f"weight form {weight_act!r} is not one of {sorted(WEIGHT_ACTS)}")
     if table.nc != 256 or table.layout != "attn":
         raise ValueError("the attention needs the table of its fc_easy profile in slice order (layout 'attn')")
     a = _lib.AttnArgs(nl.n_atoms, nl.n_edges, 128, 8, 256, nl.row_ptr.data_ptr(), nl.col.data_ptr(),
@@ -297,6 +304,7 @@ def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: f
     a.zero_order = int(bool(zero_order))
     a.env_kind, a.env_lo = int(env[0]), float(env[1])
     a.pair_slot = table.pair_slot_ptr()
+    a.weight_act = WEIGHT_ACTS[weight_act]
     if ext_gate is not None:
         if ext_gate.shape != (nl.n_edges, 128) or ext_gate.dtype != torch.float32 or not ext_gate.is_contiguous():
             raise ValueError(f"ext_gate must be a contiguous float32 [{nl.n_edges}, 128] tensor")
@@ -311,7 +319,8 @@ def attn_args(nl: NeighborList, q, k, v, atom_type, table: RadialTable, q_div: f
 
 
 def attention_forward(q, k, v, nl: NeighborList, atom_type, table: RadialTable, rc: float, q_div: float,
-                      act_dtype=torch.float32, zero_order: bool = False, env=(0, 0.0), ext_gate=None):
+                      act_dtype=torch.float32, zero_order: bool = False, env=(0, 0.0), ext_gate=None,
+                      weight_act: str = "softmax"):
     """e2v2_attn_fwd: (out, mrow, srow, cnt, q, k, v, ext_gate), the last four in the
     storage the kernels read (what ``attention_backward`` takes back)."""
     if act_dtype not in (torch.float32, torch.bfloat16):
@@ -322,7 +331,8 @@ def attention_forward(q, k, v, nl: NeighborList, atom_type, table: RadialTable, 
     bf = int(act_dtype == torch.bfloat16)
     if ext_gate is not None:
         ext_gate = ext_gate.float().contiguous()
-    args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env, ext_gate)
+    args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env, ext_gate,
+                     weight_act=weight_act)
     if zero_order:
         out = torch.empty(9, N, 256, dtype=act_dtype, device=dev)
     else:
@@ -335,7 +345,8 @@ def attention_forward(q, k, v, nl: NeighborList, atom_type, table: RadialTable, 
 
 
 def attention_backward(gout, q, k, v, out, mrow, srow, cnt, ext_gate, nl: NeighborList, atom_type,
-                       table: RadialTable, rc: float, q_div: float, zero_order: bool = False, env=(0, 0.0)):
+                       table: RadialTable, rc: float, q_div: float, zero_order: bool = False, env=(0, 0.0),
+                       weight_act: str = "softmax"):
     """e2v2_attn_bwd on the state of ``attention_forward``: (dq, dk, dv, ddvec [E, 3],
     ddist [E], dL/dgate or None), all fp32."""
     dev = q.device
@@ -343,7 +354,7 @@ def attention_backward(gout, q, k, v, out, mrow, srow, cnt, ext_gate, nl: Neighb
     bf = int(q.dtype == torch.bfloat16)
     gout = gout.to(out.dtype).contiguous()
     dgate = None if ext_gate is None else torch.empty(E, 128, dtype=torch.float32, device=dev)
-    args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env, ext_gate, dgate)
+    args = attn_args(nl, q, k, v, atom_type, table, q_div, rc, bf, zero_order, env, ext_gate, dgate, weight_act)
     f = dict(dtype=torch.float32, device=dev)
     ddv = torch.empty(max(E, 1), 3, **f)
     dd = torch.empty(max(E, 1), **f)
@@ -374,18 +385,21 @@ class AttentionFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, dvec, dist, nl: NeighborList, atom_type, table: RadialTable, rc: float,
-                q_div: float, act_dtype=torch.float32, zero_order: bool = False, env=(0, 0.0), ext_gate=None):
+                q_div: float, act_dtype=torch.float32, zero_order: bool = False, env=(0, 0.0), ext_gate=None,
+                weight_act: str = "softmax"):
         """act_dtype: storage of q, k, v and of the output rows (torch.float32, or
         torch.bfloat16 in the bf16 mode: half the gather traffic, fp32 math).
         env: the distance envelope (kind, lower end), see attn_args.  ext_gate
         [E, 128]: the gate of every (edge, head) (the QKdot variants' gates, in the
-        edge order of nl); the table then only supplies the inputhead."""
+        edge order of nl); the table then only supplies the inputhead.  weight_act:
+        the weight form, see attn_args."""
         _need_cuda(q, k, v, dvec, dist)
         out, mrow, srow, cnt, q, k, v, ext_gate = attention_forward(q, k, v, nl, atom_type, table, rc, q_div,
-                                                                    act_dtype, zero_order, env, ext_gate)
+                                                                    act_dtype, zero_order, env, ext_gate,
+                                                                    weight_act)
         ctx.save_for_backward(q, k, v, out, mrow, srow, cnt, ext_gate)
         ctx.nl, ctx.atom_type, ctx.table, ctx.rc, ctx.q_div = nl, atom_type, table, rc, q_div
-        ctx.zero_order, ctx.env = zero_order, env
+        ctx.zero_order, ctx.env, ctx.weight_act = zero_order, env, weight_act
         return out
 
     @staticmethod
@@ -394,8 +408,8 @@ class AttentionFn(torch.autograd.Function):
         q, k, v, out, mrow, srow, cnt, ext_gate = ctx.saved_tensors
         dq, dk, dv, ddv, dd, dgate = attention_backward(gout, q, k, v, out, mrow, srow, cnt, ext_gate, ctx.nl,
                                                         ctx.atom_type, ctx.table, ctx.rc, ctx.q_div, ctx.zero_order,
-                                                        ctx.env)
-        return dq, dk, dv, ddv, dd, None, None, None, None, None, None, None, None, dgate
+                                                        ctx.env, ctx.weight_act)
+        return dq, dk, dv, ddv, dd, None, None, None, None, None, None, None, None, dgate, None
 
 
 class RadialEvalFn(torch.autograd.Function):
