@@ -1,0 +1,196 @@
+"""The training path (``second_order``): in training mode the backbone's forces
+are taken with create_graph=True and differentiated again, as the reference's
+force training does (head.py:305-328 with AutoGradForce).  The loss
+L = sum F . G + sum e g (random G, g) is differentiated with respect to
+parameters of every kind (radial profiles, embeddings, SO(3) linears, the Q/K
+projections, the SO(2) output linears, norms, the energy head), compared with
+the float64 oracle's double backward on the same state dict, and to the
+positions (a Hessian-vector product), compared with central differences of the
+oracle's L in float64 along random directions (the oracle's own second
+derivative in the positions passes through its Wigner frames, whose double
+backward is not finite at every atom).  Gates: energies 1e-5 eV/atom, forces
+1e-4 relative L2 (as the eval path), parameter gradients 5e-4 relative L2 per
+tensor (fp32 against float64 through two differentiations), directional
+position derivatives 1e-3 relative."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+PARAMS = [
+    "decoder.decoder.edge_deg_embed_dense.gbf_projs.1.net.0.weight",
+    "decoder.decoder.edge_deg_embed_dense.source_embedding.weight",
+    "decoder.decoder.blocks.0.ga.fc_easy.net.6.weight",
+    "decoder.decoder.blocks.0.ga.query_linear.weight",
+    "decoder.decoder.blocks.0.ga.key_linear.final_linear.3.weight",
+    "decoder.decoder.blocks.1.ga.proj_value.weight",
+    "decoder.decoder.blocks.1.ga.target_embedding.weight",
+    "decoder.decoder.blocks.2.ffn.gate.gates.weight",
+    "decoder.decoder.blocks.3.norm_1.affine_weight",
+    "decoder.decoder.blocks.3.ffn.slinear_2.bias",
+    "decoder.decoder.norm_final.affine_bias",
+    "head.energy_heads.omol25.mlp.0.weight",
+]
+
+
+def _pair(cuda, seed, **cfg):
+    from ubio_molfm_amd import model
+    from oracle.model import MolfmAtomic as OracleModel
+    torch.manual_seed(seed)
+    args = model.default_args()
+    args.backbone_config.update(cfg)
+    m = model.MolfmAtomic(args).to(cuda)
+    om = OracleModel(**cfg)
+    om.load_state_dict({k: v.cpu() for k, v in m.state_dict().items()}, strict=True)
+    # the zero-initialised biases and unit norms would leave some second-order terms at zero
+    g = torch.Generator().manual_seed(seed + 100)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if p.requires_grad and ("bias" in name or "affine" in name):
+                p.add_(0.05 * torch.randn(p.shape, generator=g).to(cuda))
+    om.load_state_dict({k: v.cpu() for k, v in m.state_dict().items()}, strict=True)
+    return m.train(), om.double().train()
+
+
+def _to(bd, dev, dtype):
+    return {k: (v.to(dev, dtype) if torch.is_tensor(v) and v.is_floating_point() else
+                (v.to(dev) if torch.is_tensor(v) else v)) for k, v in bd.items()}
+
+
+def _oracle_ef(om, bd, create_graph):
+    pos = bd["pos"]
+    out = om.decoder(dict(bd))
+    e, _ = om.head(out, bd, "omol25")
+    f = -torch.autograd.grad(e, pos, torch.ones_like(e), create_graph=create_graph)[0]
+    return e, f
+
+
+def _second_order(m, bd, names, G, ge, dev, dtype, oracle=False):
+    """(energy, forces of the real atoms, {name: dL/dparam}, dL/dpos or None) with
+    L = sum F . G + sum e ge, forces taken with create_graph=True."""
+    bd = _to(bd, dev, dtype)
+    pos = bd["pos"].clone().requires_grad_(True)
+    bd["pos"] = pos
+    mask = bd["atom_masks"]
+    if oracle:
+        e, f = _oracle_ef(m, bd, True)
+    else:
+        res = m(bd)
+        e, f = res["pred_energy"], res["pred_forces"]
+    fr = f[mask]
+    loss = (fr * G.to(dev, dtype)).sum() + (e * ge.to(dev, dtype)).sum()
+    params = dict(m.named_parameters())
+    wrt = [params[n] for n in names] + ([] if oracle else [pos])
+    gs = torch.autograd.grad(loss, wrt)
+    return e.detach(), fr.detach(), dict(zip(names, gs[:len(names)])), None if oracle else gs[-1][mask]
+
+
+def _oracle_loss(om, bd, G, ge):
+    """L of the oracle at the positions of bd (float64, first order only)."""
+    bd = dict(bd)
+    bd["pos"] = bd["pos"].clone().requires_grad_(True)
+    e, f = _oracle_ef(om, bd, False)
+    return float((f[bd["atom_masks"]] * G).sum() + (e.detach() * ge).sum())
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def _case(cuda, sysd, seed, label, names=PARAMS, charge=None, **cfg):
+    from ubio_molfm_amd import systems
+    m, om = _pair(cuda, seed, **cfg)
+    bd = systems.to_padded(sysd)
+    if charge is not None:
+        B = len(sysd["graph_ptr"]) - 1
+        bd["charge"] = torch.full((B,), charge[0], dtype=torch.long)
+        bd["multiplicity"] = torch.full((B,), charge[1], dtype=torch.long)
+    n = int(bd["atom_masks"].sum())
+    g = torch.Generator().manual_seed(seed + 7)
+    G = torch.randn(n, 3, generator=g, dtype=torch.float64)
+    ge = torch.randn(len(sysd["graph_ptr"]) - 1, generator=g, dtype=torch.float64)
+    names = [k for k in names if k in dict(m.named_parameters())]
+    e, f, gp, gx = _second_order(m, bd, names, G, ge, cuda, torch.float32)
+    e0, f0, gp0, _ = _second_order(om, bd, names, G, ge, "cpu", torch.float64, oracle=True)
+    natoms = torch.as_tensor(np.diff(sysd["graph_ptr"]), dtype=torch.float64)
+    de = float(((e.cpu().double() - e0) / natoms).abs().max())
+    errs = {k: _rel(gp[k], gp0[k]) for k in names}
+    # dL/dpos along random directions against central differences of the oracle's L
+    bd64 = _to(bd, "cpu", torch.float64)
+    mask = bd64["atom_masks"]
+    h, fd, ad = 1e-4, [], []
+    for _ in range(3):
+        u = torch.zeros_like(bd64["pos"])
+        u[mask] = torch.randn(n, 3, generator=g, dtype=torch.float64)
+        lp = _oracle_loss(om, dict(bd64, pos=bd64["pos"] + h * u), G, ge)
+        lm = _oracle_loss(om, dict(bd64, pos=bd64["pos"] - h * u), G, ge)
+        fd.append((lp - lm) / (2 * h))
+        ad.append(float((gx.cpu().double() * u[mask]).sum()))
+    errs["pos"] = _rel(torch.tensor(ad), torch.tensor(fd))
+    worst = max(errs, key=errs.get)
+    print(f"[train {label}] N={n} |dE|/atom={de:.2e} force relL2={_rel(f, f0):.2e} second order: worst "
+          f"{worst} {errs[worst]:.2e}, pos {errs['pos']:.2e} (directional {ad} vs {fd})", flush=True)
+    assert de < 1e-5 and _rel(f, f0) < 1e-4
+    for k in names:
+        assert gp0[k].abs().max() > 0, k
+        assert errs[k] < 5e-4, (k, errs[k])
+    assert errs["pos"] < 1e-3
+
+
+def test_training_second_order_water(pkg, cuda):
+    """Base model (QK_alpha, first-order SO(2) product) on a periodic water cell
+    with charge / multiplicity: the shift of each periodic edge is a constant of
+    the positions."""
+    from ubio_molfm_amd import systems
+    _case(cuda, systems.small_water(8, 6.2, seed=21), 31, "water", charge=(1, 2))
+
+
+def test_training_second_order_variants(pkg, cuda):
+    """QKdot_alpha with sigmoid weights and one bell cluster block (zero-order
+    aggregation, the long-range list) on a ragged organic batch, plus the
+    QKdot gate's own parameters (norm_final is not used with the cluster
+    blocks, e2former.py:1088-1117)."""
+    from ubio_molfm_amd import systems
+    names = [k for k in PARAMS if "norm_final" not in k] + ["decoder.decoder.blocks.0.ga.rad_func_m0.net.3.weight",
+                      "decoder.decoder.blocks.0.ga.fc_m0.weight",
+                      "decoder.decoder.blocks.0.ga.dot_linear.weight",
+                      "decoder.decoder.long_blocks.0.ga.proj_zero.weight",
+                      "decoder.decoder.final_linear.weight",
+                      "decoder.decoder.norm_cluster.affine_weight"]
+    _case(cuda, systems.organics_batch(n_mol=2, nmin=8, nmax=14, seed=22), 32, "qkdot-sigmoid-cluster", names,
+          tp_type="QKdot_alpha+sigmoid", with_cluster="node_bell", long_range_layers=1)
+
+
+def test_training_second_order_qkdots_softplus(pkg, cuda):
+    """QKdotS_alpha with softplus weights and zero-order short blocks
+    ("so2-first-order+zero-order")."""
+    from ubio_molfm_amd import systems
+    names = PARAMS + ["decoder.decoder.blocks.1.ga.direction_linear.0.weight",
+                      "decoder.decoder.blocks.3.ga.proj_zero.weight"]
+    _case(cuda, systems.small_water(6, 5.6, seed=23), 33, "qkdots-softplus", names,
+          tp_type="QKdotS_alpha+softplus", attn_type="so2-first-order+zero-order")
+
+
+def test_eval_mode_keeps_the_fused_path(pkg, cuda):
+    """eval(): the fused kernels run (their backward is first order, so a
+    create_graph=True differentiation raises instead of silently dropping the
+    second-order terms); train() on the same model gives the same energy and
+    forces through the training path."""
+    from ubio_molfm_amd import systems
+    m, _ = _pair(cuda, 34)
+    s = systems.small_water(4, 5.5, seed=24)
+    pos = torch.as_tensor(s["pos"], device=cuda)
+    Z = torch.as_tensor(s["Z"], device=cuda)
+    m.eval()
+    e_eval, f_eval, _ = m.energy_forces_flat(pos, Z, s["graph_ptr"], s["cell"], s["pbc"])
+    m.train()
+    e_tr, f_tr, _ = m.energy_forces_flat(pos, Z, s["graph_ptr"], s["cell"], s["pbc"])
+    assert f_tr.requires_grad and not f_eval.requires_grad
+    assert _rel(e_tr, e_eval) < 1e-5 and _rel(f_tr, f_eval) < 1e-4
+    m.eval()
+    p = pos.clone().requires_grad_(True)
+    e, _ = m.energy_flat(p, Z, s["graph_ptr"], s["cell"], s["pbc"])
+    with pytest.raises(NotImplementedError):
+        torch.autograd.grad(e.sum(), p, create_graph=True)

@@ -22,6 +22,7 @@ import torch
 from torch import nn
 
 from . import _lib
+from . import second_order
 from .modules import E2former, EdgeContext, atom_type_slots, parse_irreps
 from .neighbors import build_neighbors
 from .ops import EdgeGeometryFn
@@ -127,7 +128,10 @@ class E2FormerBackbone(nn.Module):
         the neighbour list refer to atoms ``perm`` (Morton order within each graph;
         identity when ``reorder`` is False).  grid_box, nbr_capacity = (edges,
         longest row[, pinned int32 [4] counter buffer]) (the capacity build, no host
-        readback): see ``build_neighbors``."""
+        readback): see ``build_neighbors``.  In training mode the decoder runs the
+        twice-differentiable training path (``second_order``): gradients reach
+        every parameter, and forces taken with create_graph=True can be
+        differentiated again."""
         perm = None
         type_z, type_key, slot = self.type_slots(Z, graph_ptr)
         if reorder and nl is None:
@@ -139,7 +143,8 @@ class E2FormerBackbone(nn.Module):
                                  self.cells_per_direction, grid_box=grid_box,
                                  capacity=None if nbr_capacity is None else tuple(nbr_capacity[:2]),
                                  stats_host=None if nbr_capacity is None or len(nbr_capacity) < 3 else nbr_capacity[2])
-        dvec, dist = EdgeGeometryFn.apply(pos, nl)
+        train = self.training
+        dvec, dist = (nl.dvec, nl.dist) if train else EdgeGeometryFn.apply(pos, nl)
         ctx = EdgeContext(nl, dvec, dist, slot.contiguous(), type_z, type_key, self.decoder.rbf, self.max_radius,
                           self.compute_bf16)
         long_ctx = None
@@ -154,6 +159,8 @@ class E2FormerBackbone(nn.Module):
                                             dim=-1)).reshape(B, -1)
             counts = torch.as_tensor(np.diff(np.asarray(graph_ptr)), device=pos.device)
             sys_node = torch.repeat_interleave(sys_emb, counts, dim=0)
+        if train:
+            return second_order.decoder_forward(self.decoder, ctx, pos, sys_node, long_ctx), nl, perm
         return self.decoder.forward_flat(ctx, sys_node, long_ctx), nl, perm
 
     def long_range_context(self, pos, Z, graph_ptr, cell, pbc, slot, type_z, type_key) -> EdgeContext:
@@ -168,7 +175,7 @@ class E2FormerBackbone(nn.Module):
         mx = None if self.max_neighbors is None else int(2.5 * self.max_neighbors)
         nl = build_neighbors(pos.detach(), graph_ptr, cell, pbc, hi, lo, mx, self.cells_per_direction,
                              src_include=include.contiguous())
-        dvec, dist = EdgeGeometryFn.apply(pos, nl)
+        dvec, dist = (nl.dvec, nl.dist) if self.training else EdgeGeometryFn.apply(pos, nl)
         kind, env_lo = dec.long_envelope()
         return EdgeContext(nl, dvec, dist, slot.contiguous(), type_z, type_key, dec.rbf_long, hi, self.compute_bf16,
                            kind, env_lo)
@@ -273,12 +280,11 @@ class MLP_energy_head(nn.Module):
 
 
 class GradientHead(nn.Module):
-    """head.py:305-328: forces = -dE/dpos (first order in eval)."""
+    """head.py:305-328: forces = -dE/dpos, with create_graph in training mode
+    (the backbone then runs its twice-differentiable training path)."""
 
     def forward(self, pos, pred_energy):
-        if self.training:
-            raise NotImplementedError("training-mode (create_graph) forces are not supported by the HIP path")
-        return -torch.autograd.grad(pred_energy, pos, torch.ones_like(pred_energy))[0]
+        return -torch.autograd.grad(pred_energy, pos, torch.ones_like(pred_energy), create_graph=self.training)[0]
 
 
 class MDEnergyForceMultiHead(nn.Module):
@@ -340,6 +346,9 @@ class MolfmAtomic(nn.Module):
         pos = pos.detach().float().requires_grad_(True)
         energy, nl = self.energy_flat(pos, Z, graph_ptr, cell, pbc, head, charge, multiplicity, grid_box=grid_box,
                                       nbr_capacity=nbr_capacity)
+        if self.training:   # forces that can be differentiated again (the training path)
+            forces = -torch.autograd.grad(energy, pos, torch.ones_like(energy), create_graph=True)[0]
+            return energy, forces, nl
         forces = -torch.autograd.grad(energy, pos, torch.ones_like(energy))[0]
         return energy.detach(), forces, nl
 

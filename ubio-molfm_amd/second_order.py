@@ -1,0 +1,315 @@
+"""The training path: a twice-differentiable forward of the E2former decoder
+for force training (``create_graph=True``: the reference's training step with
+``AutoGradForce``, src/molfm/pipeline/head.py:305-328, differentiates the forces
+once more through its second-order Triton classes,
+triton_dr/triton_sparse_qk_autograd.py:754-836,
+sparse_v_agg_edge_index_cblocked_bench.py:361-425,
+edge_degree_outer_autograd.py:259-296).
+
+The fused attention and degree kernels give first-order input gradients only.
+In training mode (``module.train()``) the backbone instead composes each layer
+from the op-level HIP functions of ``sparse_ops`` -- the segment QK dot, the
+alpha sum, the value aggregation and the degree outer product, each with
+second- and higher-order gradients -- and PyTorch ops for the per-node and
+per-edge dense parts, as the reference composes them
+(e2former.py:223-436, 623-753, 958-1145 with ``use_triton``), so gradients of
+the forces reach every parameter and the positions.  The first-order SO(2)
+product runs in its Cartesian form (the sum over the 9 value rows and the three
+components of the edge vector with the coupling table of ``so3``; the identity
+with the node-frame product is pinned in the tests), as three value
+aggregations with weights w * dvec[:, k].  The radial profiles are evaluated per
+edge (no distance tables: their parameters receive gradients).  fp32 only.
+
+Every edge operation still runs on the GPU through libe2v2.so; nothing here
+falls back to the CPU."""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import so3
+from . import sparse_ops
+from .ops import ENV_A, ENV_B, ENV_C
+
+_EXPAND = {}
+_CART = {}
+
+
+def _expand(lmax: int, device) -> torch.Tensor:
+    """Degree l of each of the (lmax + 1)^2 m-rows."""
+    key = (lmax, str(device))
+    if key not in _EXPAND:
+        _EXPAND[key] = torch.tensor([l for l in range(lmax + 1) for _ in range(2 * l + 1)], device=device)
+    return _EXPAND[key]
+
+
+def _cartesian(device) -> torch.Tensor:
+    """The Cartesian coupling table T [20, 9, 3] of the first-order product."""
+    key = str(device)
+    if key not in _CART:
+        _CART[key] = torch.as_tensor(np.asarray(so3.cartesian_tp_table(), np.float32), device=device)
+    return _CART[key]
+
+
+# --------------------------------------------------------------------------- per-node layers (m-major [9, N, C])
+
+def so3_linear(mod, x: torch.Tensor) -> torch.Tensor:
+    """SO3_Linear_e2former (module_utils.py:2010-2052): row m times W_l(m)^T, the
+    bias on row 0."""
+    w = mod.weight.index_select(0, _expand(mod.lmax, x.device))          # [9, Cout, Cin]
+    out = torch.matmul(x, w.transpose(1, 2))
+    return torch.cat([out[:1] + mod.bias, out[1:]], dim=0)
+
+
+def so3_linear2scalar(mod, x: torch.Tensor) -> torch.Tensor:
+    """SO3_Linear2Scalar_e2former (module_utils.py:2198-2272): two SO(3) linears
+    (the bias on the first one's row 0), their m-contraction per degree, then
+    final_linear."""
+    e = _expand(mod.lmax, x.device)
+    a = torch.matmul(x, mod.weight.index_select(0, e).transpose(1, 2))
+    a = torch.cat([a[:1] + mod.bias.reshape(-1), a[1:]], dim=0)
+    b = torch.matmul(x, mod.weight2.index_select(0, e).transpose(1, 2))
+    h = torch.cat([(a[l * l:(l + 1) ** 2] * b[l * l:(l + 1) ** 2]).sum(0) for l in range(mod.lmax + 1)], dim=-1)
+    return mod.final_linear(h)
+
+
+def rms_norm(mod, x: torch.Tensor) -> torch.Tensor:
+    """EquivariantRMSNormArraySphericalHarmonicsV2_BL (module_utils.py:1663-1772):
+    row 0 centred over the channels, the degree-balanced mean square over rows
+    and channels, the affine weight of each row's degree, the bias on row 0."""
+    f0 = x[:1] - x[:1].mean(dim=2, keepdim=True)
+    f = torch.cat([f0, x[1:]], dim=0)
+    bw = mod.balance_degree_weight.view(-1, 1, 1).to(x.dtype)
+    fn = (f.pow(2) * bw).sum(0, keepdim=True).mean(dim=2, keepdim=True)
+    fn = (fn + mod.eps).pow(-0.5)
+    w = mod.affine_weight.index_select(0, _expand(mod.lmax, x.device)).unsqueeze(1)
+    out = f * (fn * w)
+    return torch.cat([out[:1] + mod.affine_bias, out[1:]], dim=0)
+
+
+def gate_s3(mod, x: torch.Tensor, silu_norm: float, sigmoid_norm: float) -> torch.Tensor:
+    """Gate_s3 (module_utils.py:2694-2746): logits from row 0, SiLU on row 0,
+    the sigmoid of each degree's logits on its rows."""
+    C = mod.sphere_channels
+    sc = mod.gates(x[0])
+    rows = [F.silu(sc[:, :C]) * silu_norm]
+    for m in range(1, x.shape[0]):
+        l = int(math.isqrt(m))
+        rows.append(torch.sigmoid(sc[:, l * C:(l + 1) * C]) * sigmoid_norm * x[m])
+    return torch.stack(rows, dim=0)
+
+
+def ffn(mod, x: torch.Tensor, silu_norm: float, sigmoid_norm: float) -> torch.Tensor:
+    """FeedForwardNetwork_s3 (module_utils.py:2755-2797)."""
+    return so3_linear(mod.slinear_2, gate_s3(mod.gate, so3_linear(mod.slinear_1, x), silu_norm, sigmoid_norm))
+
+
+# --------------------------------------------------------------------------- edges
+
+class TrainEdges:
+    """The edge inputs of one neighbour list for the training path: query row
+    and source atom of every edge (query-row order), the edge vector and distance
+    as differentiable functions of the positions, each atom's atomic number, the
+    Gaussian basis and cutoff, the envelope, and the segment metadata of the
+    sparse ops built from the neighbour list's own CSRs (no sort)."""
+
+    def __init__(self, ctx, pos: torch.Tensor):
+        nl = ctx.nl
+        N, E = nl.n_atoms, nl.n_edges
+        self.nl, self.rc, self.N, self.E = nl, float(ctx.rc), N, E
+        self.row32, self.col32 = nl.edge_row[:E].contiguous(), nl.col[:E].contiguous()
+        self.qi, self.nj = self.row32.long(), self.col32.long()
+        # the cell shift of each edge, a constant: dvec = pos_i - pos_j + off
+        base = pos[self.qi] - pos[self.nj]
+        off = (nl.dvec[:E] - base.detach()).detach()
+        self.dvec = base + off
+        self.dist = self.dvec.norm(dim=-1)
+        self.Z = ctx.type_z.long()[ctx.atom_type.long()]
+        self.offset, self.coeff = ctx.rbf_offset, float(ctx.rbf_coeff)
+        self.env_kind, self.env_lo = ctx.env_kind, ctx.env_lo
+        eid = torch.arange(E, dtype=torch.int32, device=pos.device)
+        key_eid = nl.key_eid[:E].contiguous()
+        # (query row_ptr, partner rows, edge ids) then the same by key: the 6-tuple of
+        # prepare_sparse_qk_edge_index_metadata for an edge list in row order
+        self.md = (nl.row_ptr, self.col32, eid, nl.key_ptr, self.row32.index_select(0, key_eid.long()), key_eid)
+
+    def rbf(self) -> torch.Tensor:
+        """GaussianSmearing (module_utils.py:1853-1869) of the distances."""
+        return torch.exp(self.coeff * (self.dist.view(-1, 1) - self.offset.view(1, -1)).pow(2))
+
+    def envelope(self) -> torch.Tensor:
+        """polynomial(d, rc) (module_utils.py:1946-1954) or, for the long-range
+        list of with_cluster "node_bell", smooth_polynomial_bell(d, lo, rc)
+        (module_utils.py:1956-1985)."""
+        d = self.dist
+        if self.env_kind == 0:
+            r = d / self.rc
+            return torch.where(r < 1, 1 + r ** 5 * (ENV_A + r * (ENV_B + ENV_C * r)), torch.zeros_like(r))
+        lo, hi = self.env_lo, max(self.rc, self.env_lo + 1e-8)
+        t = torch.clamp((2 * d - (lo + hi)) / (hi - lo), -1.0, 1.0)
+        return (1.0 - t * t) ** 2
+
+    def edge_input(self, tgt_emb, src_emb, rbf: torch.Tensor) -> torch.Tensor:
+        """x_edge = [rbf(d), tgt[z_i], src[z_j]] (e2former.py:258-266, 709-733)."""
+        return torch.cat([rbf, tgt_emb(self.Z)[self.qi], src_emb(self.Z)[self.nj]], dim=-1)
+
+    def qk(self, q: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
+        return sparse_ops.sparse_qk_edge_index_triton(q, k, self.row32, self.col32, metadata=self.md)
+
+    def v_agg(self, value: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
+        """value [N, Cv, H], alpha [E, H] -> [N, Cv, H]."""
+        return sparse_ops.sparse_v_agg_edge_index_triton_cblocked(value, alpha, self.row32, self.col32, self.N,
+                                                                 metadata=self.md)
+
+    def row_sum(self, alpha: torch.Tensor) -> torch.Tensor:
+        return sparse_ops.sparse_alpha_sum_edge_index_triton(alpha, self.row32, self.N,
+                                                            metadata=(self.nl.row_ptr, self.md[2]))
+
+    def outer(self, sh: torch.Tensor, fea: torch.Tensor) -> torch.Tensor:
+        return sparse_ops.edge_degree_outer_triton(sh, fea, self.row32, self.N,
+                                                  metadata=(self.nl.row_ptr, None, self.md[2], None, None, None))
+
+
+def attention_weights(logit, p, ih, edges: TrainEdges, form: str) -> torch.Tensor:
+    """alpha [E, H] (e2former.py:327-364): the segmented softmax with the row
+    maximum by scatter_reduce(amax) (its gradient split over ties) and the
+    +1e-3 in the denominator, or the softplus / sigmoid forms."""
+    if form == "softplus":
+        return F.softplus(logit) * ih * p.unsqueeze(-1)
+    if form == "sigmoid":
+        return torch.sigmoid(logit) * ih * p.unsqueeze(-1)
+    H = logit.shape[1]
+    idx = edges.qi.view(-1, 1).expand(-1, H)
+    amax = torch.full((edges.N, H), -torch.inf, dtype=logit.dtype, device=logit.device)
+    amax = amax.scatter_reduce(0, idx, logit, reduce="amax", include_self=True)
+    e = torch.exp(logit - amax[edges.qi]) * p.unsqueeze(-1)
+    s = edges.row_sum(e)
+    return e * ih / (s[edges.qi] + 1e-3)
+
+
+def _sh_integral(v: torch.Tensor) -> torch.Tensor:
+    from .modules import _sh_integral as f
+    return f(v)
+
+
+def _raw_sh(v: torch.Tensor) -> torch.Tensor:
+    from .modules import _raw_sh as f
+    return f(v)
+
+
+def qkdot_gate(ga, x: torch.Tensor, edges: TrainEdges, x_edge: torch.Tensor):
+    """(gate, inputhead) of the QKdot variants (e2former.py:270-300)."""
+    H = ga.num_attn_heads
+    xd = so3_linear(ga.dot_linear, x)                                        # [9, N, Cd]
+    xq = xd.index_select(1, edges.qi)                                        # [9, E, Cd]
+    if ga.tp_type == "QKdot_alpha":
+        Y = _sh_integral(edges.dvec)                                         # [E, 9]
+        x0 = torch.cat([(Y[:, l * l:(l + 1) ** 2].t().unsqueeze(-1) * xq[l * l:(l + 1) ** 2]).sum(0)
+                        for l in range(ga.lmax + 1)], dim=-1)                # [E, 3 Cd]
+        gate = ga.fc_m0(x0 * ga.rad_func_m0(x_edge))
+        return gate, ga.fc_easy(x_edge).reshape(-1, H)
+    lxs = _raw_sh(edges.dvec)                                                # [E, 9]
+    x0 = torch.einsum("lec,el,ls->esc", xq, lxs, ga.sum_vec.to(xq.dtype)).reshape(xq.shape[1], -1)[:, :H]
+    eg = ga.fc_easy(x_edge)
+    return ga.direction_linear(x0 * eg[:, H:]), eg[:, :H]
+
+
+def so2_forward_linear(tp, so2: torch.Tensor) -> torch.Tensor:
+    """SO2_TP_givenl2.forward_linear (so2_tensor_product.py:276-290) on the 20
+    l3-sequential rows [20, N, C]: per output degree its cnt paths side by side
+    through out_linear, times path_norm; rows scaled by any loaded CG_weight
+    path scale first."""
+    sc = tp.path_scales()
+    if sc is not None:
+        so2 = so2 * sc.view(-1, 1, 1).to(so2.dtype)
+    N = so2.shape[1]
+    outs, st = [], 0
+    for idx, (l3, cnt) in enumerate(tp.l3_sequential):
+        nr = 2 * l3 + 1
+        blk = so2[st:st + cnt * nr].reshape(cnt, nr, N, -1).permute(1, 2, 0, 3).reshape(nr, N, -1)
+        outs.append(tp.out_linear[idx](blk))
+        st += cnt * nr
+    return torch.cat(outs, dim=0) * tp.path_norm.view(-1, 1, 1).to(so2.dtype)
+
+
+def attention(ga, x: torch.Tensor, edges: TrainEdges, rbf: torch.Tensor) -> torch.Tensor:
+    """E2AttentionArbOrder_sparse.forward (e2former.py:223-436) on x [9, N, C]."""
+    N, H = x.shape[1], ga.num_attn_heads
+    q = so3_linear2scalar(ga.query_linear, x).reshape(N, H, -1)
+    k = so3_linear2scalar(ga.key_linear, x).reshape(N, H, -1)
+    x_edge = edges.edge_input(ga.target_embedding, ga.source_embedding, rbf)
+    if ga.tp_type == "QK_alpha":
+        eg = ga.fc_easy(x_edge)
+        gate, ih = eg[:, :H], eg[:, H:]
+    else:
+        gate, ih = qkdot_gate(ga, x, edges, x_edge)
+    qk = edges.qk(q / math.sqrt(q.shape[-1]), k)
+    alpha = attention_weights(gate * qk, edges.envelope(), ih, edges, ga.weight_act)
+    alpha = ga.alpha_dropout(alpha)
+    v = so3_linear(ga.proj_value, x)                                         # [9, N, C]
+    C = v.shape[-1]
+    vh = v.permute(1, 0, 2).reshape(N, -1, H)                                # channel c -> head c mod H
+    if ga.attn_type == "zero-order":
+        agg = edges.v_agg(vh, alpha).reshape(N, -1, C).permute(1, 0, 2)      # [9, N, C]
+        return so3_linear(ga.proj_zero, agg)
+    w = alpha / edges.dist.clamp_min(1e-6).unsqueeze(-1)
+    T = _cartesian(x.device)
+    so2 = 0
+    for kk in range(3):
+        a = edges.v_agg(vh, w * edges.dvec[:, kk:kk + 1]).reshape(N, -1, C)  # [N, 9, C]
+        so2 = so2 + torch.einsum("tr,nrc->tnc", T[:, :, kk], a)
+    return so3_linear(ga.proj_first, so2_forward_linear(ga.first_order_tp.so2_tp, so2))
+
+
+def degree_embedding(mod, edges: TrainEdges, rbf: torch.Tensor) -> torch.Tensor:
+    """EdgeDegreeEmbeddingNetwork_higherorder.forward (e2former.py:689-753):
+    per degree the profile times the envelope, its outer product with the
+    unit-vector spherical harmonics reduced over each row, / avg."""
+    emb = edges.edge_input(mod.target_embedding, mod.source_embedding, rbf)
+    u = F.normalize(edges.dvec, dim=-1)
+    lxs = _raw_sh(u)
+    p = edges.envelope().view(-1, 1)
+    rows = []
+    for l in range(mod.lmax + 1):
+        fea = mod.gbf_projs[l](emb) * p
+        rows.append(edges.outer(lxs[:, l * l:(l + 1) ** 2].contiguous(), fea))   # [N, 2l+1, C]
+    return torch.cat(rows, dim=1).permute(1, 0, 2) / mod.avg_aggregate_num
+
+
+def block(blk, x: torch.Tensor, edges: TrainEdges, rbf: torch.Tensor, sys_node, norms) -> torch.Tensor:
+    """TransBlock.forward (e2former.py:600-620): pre-norm residual attention and FFN."""
+    h = rms_norm(blk.norm_1, x)
+    if sys_node is not None:
+        h = torch.cat([(h[0] + sys_node).unsqueeze(0), h[1:]], dim=0)
+    x = x + attention(blk.ga, h, edges, rbf)
+    return x + ffn(blk.ffn, rms_norm(blk.norm_ffn, x), *norms)
+
+
+def decoder_forward(dec, ctx, pos: torch.Tensor, sys_node: Optional[torch.Tensor] = None, long_ctx=None):
+    """E2former's decoder (e2former.py:958-1145) on the training path: node
+    irreps [9, N, C] as twice-differentiable functions of pos and the parameters."""
+    from .modules import SILU_NORM, SIGMOID_NORM
+    if ctx.bf16:
+        raise NotImplementedError("the training path runs in fp32 (set_compute_dtype('fp32'))")
+    norms = (SILU_NORM, SIGMOID_NORM)
+    edges = TrainEdges(ctx, pos)
+    rbf = edges.rbf()
+    x = degree_embedding(dec.edge_deg_embed_dense, edges, rbf)
+    for blk in dec.blocks:
+        x = block(blk, x, edges, rbf, sys_node, norms)
+    if not dec.cluster:
+        return rms_norm(dec.norm_final, x)
+    if long_ctx is None:
+        raise ValueError("cluster_neighbor_info is required when with_cluster contains 'node'.")
+    short = x
+    x = rms_norm(dec.pre_norm_node, x)
+    long_edges = TrainEdges(long_ctx, pos)
+    rbf_l = long_edges.rbf()
+    for blk in dec.long_blocks:
+        x = block(blk, x, long_edges, rbf_l, sys_node, norms)
+    x = rms_norm(dec.norm_cluster, x)
+    return so3_linear(dec.final_linear, torch.cat([short, x], dim=-1))

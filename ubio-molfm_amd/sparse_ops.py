@@ -21,8 +21,10 @@ sum and the row gather are each other's gradients; the degree outer product and
 its gradient close the same way), so second- and higher-order gradients follow
 the reference's ``*_Backward_Fn`` classes without separate kernels.
 
-The model's own attention and degree-embedding paths do not use these: they
-run fused (ops.attention / ops.degree_embed)."""
+The model's own attention and degree-embedding paths run fused
+(ops.AttentionFn / ops.DegreeEmbedFn) in evaluation mode; in training mode they
+are composed from these functions (``second_order``) so that forces can be
+differentiated again."""
 from __future__ import annotations
 
 import ctypes as C
