@@ -531,6 +531,42 @@ int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* ghk, cons
 int e2v2_gemm_pack(const float* w, int64_t ld_n, int64_t ld_k, int64_t w_stride, int n_w, int n, int k, int pieces,
                    void* packed, hipStream_t s);
 
+/* ---- QKdot_alpha gate ------------------------------------------------- */
+/* The gate of tp_type QKdot_alpha (e2former.py:270-283) without per-edge channel tensors:
+ *   gate[e][h] = bias[h] + sum_k A[e][k] W[h][k],   k < 768 = 3 x 256,
+ *   A[e][256 l + c] = x0[e][l][c] rad[e][256 l + c],  x0[e][l][c] = sum_{m in l} Y[e][m] xd[m][i(e)][c],
+ * with W the fc_m0 weight [128][768], Y [E][9] the edge's normalised spherical harmonics l <= 2, xd [9][N][256]
+ * the query atoms' dot_linear output (m-major) and rad the rad_func_m0 profile (768 channels, "plain" table
+ * layout [pairs][rtab_n][4][768], type pairs as in e2v2_attn_args).  A is formed as the GEMM reads it.  The
+ * backward takes dL/dgate [E][128] and writes dL/dY [E][9], dL/ddist [E] (through rad) and dL/dxd
+ * [9][N][256] (per-row sums in a fixed order, no atomics; atoms without edges get zeros); dL/dA is formed per
+ * 128-edge tile in LDS and never stored.  Edges past *e_end (a device count, or NULL) give a zero gate and
+ * zero gradients.  Operands fp32 and 16-byte aligned; W packed by e2v2_gemm_pack (forward: W as [128][768],
+ * backward: W^T as [768][128]) with `pieces` 3 (fp32 accuracy) or 1 (bf16 mode). */
+typedef struct e2v2_qkdot_args {
+  int32_t n_rows;
+  int64_t n_edges;
+  const int32_t* row_ptr;        /* [N+1] query CSR                                 */
+  const int32_t* edge_row;       /* [E]                                             */
+  const int32_t* col;            /* [E] source atom                                 */
+  const float* dist;             /* [E]                                             */
+  const int32_t* e_end;          /* device count of valid edges, or NULL            */
+  const float* Y;                /* [E][9]                                          */
+  const float* xd;               /* [9][N][256]                                     */
+  const float* rtab;             /* rad_func_m0 table, plain layout, 768 channels   */
+  const int32_t* atom_type;
+  int32_t n_types, rtab_n;
+  float rtab_h;
+  const int32_t* pair_slot;
+  int32_t pieces;
+} e2v2_qkdot_args;
+int e2v2_qkdot_gate_fwd(const e2v2_qkdot_args* args, const void* w_packed, const float* bias, float* gate,
+                        hipStream_t s);
+/* Bytes of device workspace e2v2_qkdot_gate_bwd needs (per-tile partial sums, alive during the call). */
+size_t e2v2_qkdot_gate_bwd_workspace(int64_t n_edges);
+int e2v2_qkdot_gate_bwd(const e2v2_qkdot_args* args, const void* wt_packed, const float* dgate, float* dY,
+                        float* ddist, float* dxd, void* workspace, size_t workspace_bytes, hipStream_t s);
+
 /* ---- positions --------------------------------------------------------- */
 int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,
                      const float* dvec, const float* dist, const float* ddvec, const float* ddist, float* dpos,

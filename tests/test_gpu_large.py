@@ -45,10 +45,12 @@ def test_neighbors_cfg5_bit_exact(pkg, cuda):
     _nbr_exact(pkg, cuda, systems.CONFIGS[5](), "cfg5")
 
 
-def _model(cuda, seed=21):
+def _model(cuda, seed=21, **cfg):
     from ubio_molfm_amd import model
     torch.manual_seed(seed)
-    return model.MolfmAtomic(model.default_args()).eval().to(cuda).requires_grad_(False)
+    args = model.default_args()
+    args.backbone_config.update(cfg)
+    return model.MolfmAtomic(args).eval().to(cuda).requires_grad_(False)
 
 
 def _ef(m, pos, s, cell=None):
@@ -135,7 +137,8 @@ def test_cfg5_bf16_against_fp32_and_memory(pkg, cuda):
     assert peak16 < 288.0
 
 
-def test_cfg3_no_edge_channel_tensors(pkg, cuda):
+@pytest.mark.parametrize("tp", ["QK_alpha", "QKdot_alpha"])
+def test_cfg3_no_edge_channel_tensors(pkg, cuda, tp):
     """Linear memory without per-edge channel tensors (configs[2], 1,500 atoms,
     ~127k edges, fp32): every tensor created during one energy + force
     evaluation (forward and backward, logged at the ATen level by a dispatch
@@ -143,11 +146,15 @@ def test_cfg3_no_edge_channel_tensors(pkg, cuda):
     least E x 128 x 4 bytes must be node-level (N among its first two
     dimensions); the backward entry points' per-call workspaces stay within 384
     bytes per edge, and the attention workspace itself is among the logged
-    tensors (the log sees the backward's allocations)."""
+    tensors (the log sees the backward's allocations).  QKdot_alpha: its gate
+    (e2former.py:270-283) is formed by the fused gate GEMM; the only per-edge
+    tensors of channel width are the [E, 128] gate the attention kernels take
+    (ext_gate) and its gradient -- nothing of the 768-wide edge operand -- and the
+    gate backward's workspace stays within 384 bytes per edge."""
     from torch.utils._python_dispatch import TorchDispatchMode
     from ubio_molfm_amd import _lib, systems
     s = systems.CONFIGS[3]()
-    m = _model(cuda, seed=23)
+    m = _model(cuda, seed=23, tp_type=tp)
     pos = torch.as_tensor(s["pos"], device=cuda)
     N = pos.shape[0]
     _ef(m, pos, s)                                   # warm-up: tables and weight caches
@@ -169,17 +176,23 @@ def test_cfg3_no_edge_channel_tensors(pkg, cuda):
     E = nl.n_edges
     peak = torch.cuda.max_memory_allocated(cuda) - base
     lim = 128 * 4 * E
-    big = [(sh, b) for sh, b in created if b >= lim and N not in sh[:2]]
+    gate_shape = (E, 128)
+    big = [(sh, b) for sh, b in created if b >= lim and N not in sh[:2] and not (tp != "QK_alpha" and sh == gate_shape)]
+    n_gate = sum(1 for sh, _ in created if sh == gate_shape)
     edge_level = [b for sh, b in created if sh and sh[0] == E]
     lib = _lib.load()
     nb_attn = int(lib.e2v2_attn_bwd_workspace(E))
     ws_attn = nb_attn / E
     ws_deg = int(lib.e2v2_deg_bwd_workspace(E)) / E
-    print(f"[cfg3 memory] N={N} E={E} tensors logged={len(created)} activation peak={peak / 1e9:.3f} GB "
+    ws_qk = int(lib.e2v2_qkdot_gate_bwd_workspace(E)) / E
+    print(f"[cfg3 memory {tp}] N={N} E={E} tensors logged={len(created)} activation peak={peak / 1e9:.3f} GB "
           f"({peak / E:.0f} B/edge, {peak / N / 1e3:.0f} KB/atom) widest [E,...] tensor="
-          f"{max(edge_level) / E if edge_level else 0:.0f} B/edge, workspaces attn {ws_attn:.0f} deg {ws_deg:.0f} B/edge",
-          flush=True)
+          f"{max(edge_level) / E if edge_level else 0:.0f} B/edge, [E, 128] gate tensors {n_gate}, workspaces attn "
+          f"{ws_attn:.0f} deg {ws_deg:.0f} qkdot gate {ws_qk:.0f} B/edge", flush=True)
     assert len(created) > 100
     assert any(b == nb_attn for _, b in created), "the backward's allocations are not in the log"
     assert not big, big[:5]
-    assert ws_attn <= 384 and ws_deg <= 128
+    assert ws_attn <= 384 and ws_deg <= 128 and ws_qk <= 384
+    assert max(edge_level) <= lim
+    if tp == "QKdot_alpha":
+        assert n_gate >= 2 * len(m.decoder.decoder.blocks)   # the gate and its gradient in every layer

@@ -442,6 +442,76 @@ def test_radial_eval_per_edge(pkg, cuda):
     assert ev < 2e-6 and ed < 1e-5
 
 
+@pytest.mark.parametrize("pieces, ragged", [(3, False), (3, True), (1, False)])
+def test_qkdot_gate_fused(pkg, cuda, pieces, ragged):
+    """e2v2_qkdot_gate_fwd / _bwd (QKdotGateFn): gate = fc_m0(x0 * rad) with
+    x0[e, l] = sum_{m in l} Y[e, m] xd[m, row(e)] and rad the three 256-channel
+    profiles at every edge, against float64 (profiles evaluated per edge); the
+    gradients to Y, xd (per-row sums over rows that cross the 128-edge tiles, and
+    zero for atoms without edges) and dist (through rad).  pieces 3 (fp32): gate
+    2e-6 of the scale, gradients 1e-5; pieces 1 (the bf16 mode: W and the edge
+    operand rounded to bf16): 1e-2.  "ragged": 150 atoms in a ball of radius
+    2.9 A (rows of 149 edges, so rows span up to three 128-edge tiles) plus two
+    isolated atoms, an edge count that is not a multiple of 128."""
+    from ubio_molfm_amd import gemm as s3gemm, modules, neighbors, ops
+    if ragged:
+        rng = np.random.default_rng(61)
+        u = rng.normal(size=(152, 3))
+        p = u / np.linalg.norm(u, axis=1, keepdims=True) * 2.9 * rng.uniform(0, 1, size=(152, 1)) ** (1 / 3)
+        p[150] = [100.0, 0.0, 0.0]
+        p[151] = [0.0, -100.0, 0.0]
+        s = dict(pos=p.astype(np.float32), Z=rng.choice([1, 6, 8], size=152), graph_ptr=np.array([0, 152]),
+                 cell=np.zeros((1, 3, 3), np.float32), pbc=np.zeros((1, 3), bool))
+        nl = neighbors.build_neighbors(torch.as_tensor(s["pos"], device=cuda), s["graph_ptr"], s["cell"], s["pbc"],
+                                       6.0)
+        deg = np.diff(nl.row_ptr.cpu().numpy())
+        assert deg[150] == 0 and deg[151] == 0 and nl.n_edges % 128 != 0 and deg.max() > 128
+    else:
+        s, pos, nl = _graph(pkg, cuda, seed=8)
+    N, E = nl.n_atoms, nl.n_edges
+    print(f"[qkdot gate pieces={pieces} ragged={ragged}] N={N} E={E}", flush=True)
+    gen = torch.Generator().manual_seed(70 + pieces)
+    rb = modules.GaussianSmearing(256, 6.0, 2.0)
+    profs = [_profile(71 + m, 512) for m in range(3)]
+    tgt, src = _embeddings(74, 256, 128)
+    tw, sw = tgt.weight.detach().double().clone(), src.weight.detach().double().clone()
+    type_z, slot = _types(pkg, cuda, s["Z"])
+    tab = ops.RadialTable([copy.deepcopy(p).to(cuda).net for p in profs], tgt.to(cuda), src.to(cuda),
+                          rb.offset.to(cuda), rb.coeff, 6.0, type_z, layout="plain")
+    fc = torch.nn.Linear(768, 128)
+    with torch.no_grad():
+        fc.weight.normal_(0.0, 0.05, generator=gen); fc.bias.normal_(0.0, 0.1, generator=gen)
+    W = fc.weight.detach().to(cuda)
+    packs = (s3gemm.pack(W, pieces=pieces), s3gemm.pack(W, transpose=True, pieces=pieces))
+    Y = torch.randn(E, 9, generator=gen); xd = torch.randn(9, N, 256, generator=gen)
+    G = torch.randn(E, 128, generator=gen)
+    if pieces == 1:
+        W = W.to(torch.bfloat16).float()
+    dist = nl.dist.clone().requires_grad_(True)
+    Yd = Y.to(cuda).requires_grad_(True); xdd = xd.to(cuda).requires_grad_(True)
+    gate = ops.QKdotGateFn.apply(dist, Yd, xdd, nl, slot, tab, packs, fc.bias.detach().to(cuda))
+    gate.backward(G.to(cuda))
+    row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()
+    Z = torch.as_tensor(np.asarray(s["Z"]))
+    d64 = nl.dist.cpu().double().requires_grad_(True)
+    Y64, x64 = Y.double().requires_grad_(True), xd.double().requires_grad_(True)
+    rad = torch.cat([mlp_ref(d64, Z[row], Z[col], copy.deepcopy(p).double().net, tw, sw, rb.offset.double(),
+                             float(np.float32(rb.coeff))) for p in profs], dim=1)
+    blocks = [(0, 1), (1, 4), (4, 9)]
+    x0 = torch.cat([torch.einsum("em,mec->ec", Y64[:, a:b], x64[a:b][:, row]) for a, b in blocks], dim=1)
+    ref = (x0 * rad) @ W.cpu().double().t() + fc.bias.detach().double()
+    gY, gx, gd = torch.autograd.grad((ref * G.double()).sum(), [Y64, x64, d64])
+    ev = float((gate.detach().cpu().double() - ref).abs().max() / ref.abs().max())
+    errs = dict(dY=relerr(Yd.grad, gY), dxd=relerr(xdd.grad, gx), ddist=relerr(dist.grad, gd))
+    print(f"[qkdot gate pieces={pieces} ragged={ragged}] gate {ev:.2e} {errs}", flush=True)
+    tol_v, tol_g = (2e-6, 1e-5) if pieces == 3 else (1e-2, 1e-2)
+    assert ev < tol_v
+    for name, e in errs.items():
+        assert e < tol_g, (name, e)
+    if ragged:
+        assert torch.count_nonzero(xdd.grad[:, 150:]) == 0
+
+
 @pytest.mark.parametrize("C", [256, 43])
 def test_sh_contract(pkg, cuda, C):
     """e2v2_sh_contract / _bwd: x0[e, l] = sum_{m in l} Y[e, m] xn[m, row(e)] and

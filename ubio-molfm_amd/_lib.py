@@ -26,6 +26,7 @@ EXPORTS = [
     "e2v2_gather_rows", "e2v2_outer_reduce", "e2v2_outer_bwd",
     "e2v2_radial_eval", "e2v2_radial_eval_bwd", "e2v2_sh_contract", "e2v2_sh_contract_bwd",
     "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated", "e2v2_gemm_pack", "e2v2_gemm_packed_bytes", "e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3",
+    "e2v2_qkdot_gate_fwd", "e2v2_qkdot_gate_bwd", "e2v2_qkdot_gate_bwd_workspace",
 ]
 
 
@@ -72,6 +73,12 @@ class AttnArgs(C.Structure):
                 ("pair_slot", vp), ("weight_act", i32)]
 
 
+class QkdotArgs(C.Structure):
+    _fields_ = [("n_rows", i32), ("n_edges", i64), ("row_ptr", vp), ("edge_row", vp), ("col", vp), ("dist", vp),
+                ("e_end", vp), ("Y", vp), ("xd", vp), ("rtab", vp), ("atom_type", vp), ("n_types", i32),
+                ("rtab_n", i32), ("rtab_h", f32), ("pair_slot", vp), ("pieces", i32)]
+
+
 class DegArgs(C.Structure):
     _fields_ = [("n_rows", i32), ("n_edges", i64), ("channels", i32), ("row_ptr", vp), ("dvec", vp),
                 ("dist", vp), ("col", vp), ("rtab", vp), ("atom_type", vp), ("n_types", i32), ("rtab_n", i32),
@@ -105,6 +112,8 @@ def load():
     lib.e2v2_attn_bwd_workspace.argtypes = [C.c_int64]
     lib.e2v2_deg_bwd_workspace.restype = C.c_size_t
     lib.e2v2_deg_bwd_workspace.argtypes = [C.c_int64]
+    lib.e2v2_qkdot_gate_bwd_workspace.restype = C.c_size_t
+    lib.e2v2_qkdot_gate_bwd_workspace.argtypes = [C.c_int64]
     lib.e2v2_gemm_packed_bytes.restype = C.c_int64
     lib.e2v2_gemm_packed_bytes.argtypes = [C.c_int32, C.c_int32, C.c_int32, C.c_int32]
     _lib = lib

@@ -13,7 +13,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libe2v2.so"
-SOURCES = ["api.hip", "nbr.hip", "radial.hip", "attn.hip", "deg.hip", "node.hip", "proj.hip", "sparse.hip", "gemm.hip"]
+SOURCES = ["api.hip", "nbr.hip", "radial.hip", "attn.hip", "deg.hip", "node.hip", "proj.hip", "sparse.hip", "gemm.hip", "qkdot.hip"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 

@@ -23,8 +23,8 @@ from torch.profiler import record_function
 from . import so3
 from . import _lib
 from . import gemm as s3gemm
-from .ops import AttentionFn, DegreeEmbedFn, RadialCache, RadialEvalFn, ShContractFn, attention_backward, \
-    attention_forward
+from .ops import AttentionFn, DegreeEmbedFn, QKdotGateFn, RadialCache, RadialEvalFn, ShContractFn, \
+    attention_backward, attention_forward
 
 
 def _e3nn_normalize2mom(f) -> float:
@@ -1463,10 +1463,16 @@ class E2AttentionArbOrder_sparse(nn.Module):
         tab = self._radial_m0.get(self._m0_profiles(), self.target_embedding, self.source_embedding,
                                   ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="plain",
                                   pairs=ctx.pairs)
-        rad = RadialEvalFn.apply(ctx.dist, nl, ctx.atom_type, tab)
         if self.tp_type == "QKdot_alpha":
+            packs = dense_packs(self.fc_m0, ctx.bf16)
+            if packs is not None and xd.shape[2] == 256 and H == 128 and tab.nc == 768:
+                # the 768-wide edge operand is formed inside the gate GEMM (no per-edge channel tensor)
+                return QKdotGateFn.apply(ctx.dist, _sh_integral(ctx.dvec), xd, nl, ctx.atom_type, tab, packs,
+                                         self.fc_m0.bias.detach())
+            rad = RadialEvalFn.apply(ctx.dist, nl, ctx.atom_type, tab)
             x0 = ShContractFn.apply(_sh_integral(ctx.dvec), xd, nl).reshape(E, -1)    # [E, 3 Cd]
             return _linear(x0 * rad, self.fc_m0)
+        rad = RadialEvalFn.apply(ctx.dist, nl, ctx.atom_type, tab)
         # checked once per version of sum_vec (a host readback), not on every evaluation
         if not cached(self, "sum_vec_ok", (self.sum_vec,),
                       lambda: torch.equal(self.sum_vec.detach().cpu(), self._sum_vec_blocks())):

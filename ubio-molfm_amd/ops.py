@@ -451,6 +451,65 @@ def _radial_eval_args(nl: NeighborList, atom_type, table: RadialTable, dist):
             _lib.i64(nl.n_edges), e_end)
 
 
+class QKdotGateFn(torch.autograd.Function):
+    """The gate [E, 128] of tp_type QKdot_alpha (e2former.py:270-283):
+    fc_m0(cat_l(sum_{m in l} Y[e, m] xd[m, row(e)]) * rad_func_m0(x_edge)) with
+    the profile read from its 768-channel "plain" table and the 768-wide edge
+    operand formed inside the GEMM (e2v2_qkdot_gate_fwd / _bwd): no per-edge
+    tensor wider than the gate exists in either direction.  Y [E, 9] (the edge's
+    normalised spherical harmonics), xd [9, N, 256] (dot_linear of the layer
+    input), packs = (fc_m0.weight packed, its transpose packed) of one piece
+    count, bias [128].  Gradients to dist, Y and xd."""
+
+    @staticmethod
+    def forward(ctx, dist, Y, xd, nl: NeighborList, atom_type, table: RadialTable, packs, bias):
+        _need_cuda(dist, Y, xd)
+        if table.layout != "plain" or table.nc != 768:
+            raise ValueError("QKdotGateFn needs the 768-channel rad_func_m0 table in the 'plain' layout")
+        if packs[0].n != 128 or packs[0].k != 768 or packs[1].n != 768 or packs[1].k != 128 or \
+                packs[0].pieces != packs[1].pieces:
+            raise ValueError("QKdotGateFn: fc_m0 must be Linear(768, 128), packed both ways with one piece count")
+        E, N = nl.n_edges, nl.n_atoms
+        Y = Y.float().contiguous()
+        xd = xd.float().contiguous()
+        if Y.shape != (E, 9) or xd.shape != (9, N, 256):
+            raise ValueError(f"QKdotGateFn: Y {tuple(Y.shape)}, xd {tuple(xd.shape)} for {E} edges and {N} atoms")
+        dist = dist.float().contiguous()
+        bias = bias.float().contiguous()
+        args = _qkdot_args(nl, atom_type, table, dist, Y, xd, packs[0].pieces)
+        gate = torch.empty(E, 128, dtype=torch.float32, device=dist.device)
+        _lib.call("e2v2_qkdot_gate_fwd", _lib.C.byref(args), _p(packs[0].buf), _p(bias), _p(gate), _stream(dist))
+        ctx.save_for_backward(dist, Y, xd)
+        ctx.nl, ctx.atom_type, ctx.table, ctx.packs = nl, atom_type, table, packs
+        return gate
+
+    @staticmethod
+    def backward(ctx, dgate):
+        _no_double_backward()
+        dist, Y, xd = ctx.saved_tensors
+        nl = ctx.nl
+        dgate = dgate.float().contiguous()
+        args = _qkdot_args(nl, ctx.atom_type, ctx.table, dist, Y, xd, ctx.packs[0].pieces)
+        dY = torch.empty_like(Y)
+        ddist = torch.empty_like(dist)
+        dxd = torch.empty_like(xd)
+        nb = int(_lib.load().e2v2_qkdot_gate_bwd_workspace(nl.n_edges))
+        ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dist.device)
+        _lib.call("e2v2_qkdot_gate_bwd", _lib.C.byref(args), _p(ctx.packs[1].buf), _p(dgate), _p(dY), _p(ddist),
+                  _p(dxd), _p(ws), _lib.C.c_size_t(ws.numel()), _stream(dgate))
+        del ws
+        return ddist, dY, dxd, None, None, None, None, None
+
+
+def _qkdot_args(nl: NeighborList, atom_type, table: RadialTable, dist, Y, xd, pieces: int):
+    # e_end = row_ptr[N] on the device: a capacity build's slots past the real edges are not read
+    e_end = _lib.vp(nl.row_ptr.data_ptr() + 4 * nl.n_atoms) if nl.n_edges else None
+    return _lib.QkdotArgs(nl.n_atoms, nl.n_edges, nl.row_ptr.data_ptr(), nl.edge_row.data_ptr(), nl.col.data_ptr(),
+                          dist.data_ptr(), e_end, Y.data_ptr(), xd.data_ptr(), table.tab.data_ptr(),
+                          atom_type.data_ptr(), table.n_types, table.n_nodes, table.h, table.pair_slot_ptr(),
+                          int(pieces))
+
+
 class ShContractFn(torch.autograd.Function):
     """x0 [E, 3, C] with x0[e, l] = sum_{m in l} Y[e, m] xn[m, row(e)] (e2v2_sh_contract):
     the per-edge x_0_extra of the QKdot gates (e2former.py:271-276, 288-296).  Y
