@@ -139,6 +139,9 @@ PROJ_FLOPS["e2v2_qk_proj_fwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
 PROJ_FLOPS["e2v2_qk_proj_bwd_bf16"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
 PROJ_FLOPS["e2v2_qk_proj_fwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_fwd"]
 PROJ_FLOPS["e2v2_qk_proj_bwd_s3"] = PROJ_FLOPS["e2v2_qk_proj_bwd"]
+# the QKdot_alpha gate GEMM (768 -> 128 per edge), forward and input gradient: per launch 2 E 768 128
+EDGE_GEMM_FLOPS = {"e2v2_qkdot_gate_fwd": lambda E: 2.0 * E * 768 * 128,
+                   "e2v2_qkdot_gate_bwd": lambda E: 2.0 * E * 768 * 128}
 # fp32 GEMMs on the split kernels execute six bf16 MFMA products per fp32 multiply-add; the bf16 mode runs
 # the same kernels on one-piece packs (bf16 operands): one product
 SPLIT_PRODUCTS = 6
@@ -333,6 +336,10 @@ def main():
                          "its kernels from Python; measured equal in time at configs 1, 3 and 4")
     ap.add_argument("--kernel-steps", type=int, default=5,
                     help="eager steps after the timed region whose library calls are timed with HIP events")
+    ap.add_argument("--tp-type", default="QK_alpha",
+                    help="tp_type of the model (variant lines: QKdot_alpha, QKdotS_alpha, +softplus / +sigmoid)")
+    ap.add_argument("--with-cluster", default="False",
+                    help="with_cluster of the model (variant lines: node, node_bell: two long-range blocks)")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one plain 256 MiB device copy first (scale reference for FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -352,7 +359,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     torch.manual_seed(0)
-    m = model.MolfmAtomic(model.default_args()).eval().to(dev).requires_grad_(False)
+    margs = model.default_args()
+    margs.backbone_config.update(tp_type=args.tp_type, with_cluster=args.with_cluster)
+    m = model.MolfmAtomic(margs).eval().to(dev).requires_grad_(False)
     dtype = args.dtype or ("bf16" if args.config in (2, 5) else "fp32")
     m.decoder.set_compute_dtype(dtype)
     bf16 = dtype == "bf16"
@@ -388,7 +397,8 @@ def main():
                               "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill",
                               "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd", "e2v2_qk_proj_fwd_bf16",
                               "e2v2_qk_proj_bwd_bf16", "e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3",
-                              "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated"])
+                              "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated",
+                              "e2v2_qkdot_gate_fwd", "e2v2_qkdot_gate_bwd"])
     integ.use_graph = False
     _lib.set_timer(timer)
     for _ in range(min(args.steps, args.kernel_steps)):
@@ -431,6 +441,13 @@ def main():
             if not bf16:
                 ent.update(fp32_equivalent_tflops=round(tf, 2),
                            fp32_equivalent_over_fp32_peak=round(tf / FP32_PEAK_TFLOPS, 4))
+        elif k in EDGE_GEMM_FLOPS:
+            fl = EDGE_GEMM_FLOPS[k](E_mean)
+            tf = fl / sec / 1e12
+            prod = SPLIT_PRODUCTS_BF16 if bf16 else SPLIT_PRODUCTS
+            ent.update(bound="mfma", flops_per_launch=fl, executed_flops_per_launch=prod * fl,
+                       achieved_tflops=round(prod * tf, 2), peak_tflops=BF16_PEAK_TFLOPS,
+                       frac=round(prod * tf / BF16_PEAK_TFLOPS, 4))
         elif k in PROJ_FLOPS:
             tf = PROJ_FLOPS[k](N) / sec / 1e12
             pk = BF16_PEAK_TFLOPS if k.endswith("_bf16") else FP32_PEAK_TFLOPS
@@ -440,14 +457,17 @@ def main():
     # headline: the library entry point with the largest total time, at its algorithmic work per launch
     name = max(stats.items(), key=lambda kv: kv[1]["total_ms"])[0]
     ent = per_kernel[name]
+    # the traffic profile and the CPU baseline cover the default model (QK_alpha, no cluster blocks)
+    default_model = args.tp_type == "QK_alpha" and args.with_cluster in ("False", "false", "0", "None", "none")
+    cfg_traffic = args.config if default_model else -1
     if ent.get("bound") == "hbm":
         roof = {"bound": "hbm", "achieved": ent["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": ent["frac"], "traffic": traffic_from_profile(name, bf16, args.config), "kernel": name,
+                "frac": ent["frac"], "traffic": traffic_from_profile(name, bf16, cfg_traffic), "kernel": name,
                 "algorithmic_bytes_per_launch": ent["bytes_per_launch"], "expanded_nodes": M}
     else:
         pk = ent.get("peak_tflops", FP32_PEAK_TFLOPS)
         roof = {"bound": "mfma", "achieved": ent.get("achieved_tflops"), "peak": pk, "unit": "TFLOP/s",
-                "frac": ent.get("frac"), "traffic": traffic_from_profile(name, bf16, args.config), "kernel": name}
+                "frac": ent.get("frac"), "traffic": traffic_from_profile(name, bf16, cfg_traffic), "kernel": name}
     # stack: whole evaluation against the MFMA roofline; HBM-bound kernels time-weighted
     stack_tf = stack_flops(N, E_mean) / (ms * 1e-3) / 1e12
     hb = [k for k in COMPULSORY if k in stats]
@@ -463,7 +483,7 @@ def main():
                                          "frac": round(hb_alg / hb_time / 1e9 / HBM_PEAK_GBS, 4),
                                          "impl_frac": round(hb_imp / hb_time / 1e9 / HBM_PEAK_GBS, 4)}
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and default_model:
         cpu = cpu_baseline(pkg, args.config, args.cpu_sample)
     out = {
         "metric": "attn edges/s fwd+force-bwd & MD atom-steps/s at 10k atoms; % HBM roofline",
@@ -480,7 +500,8 @@ def main():
                                + ("NVE velocity-Verlet 1 fs, neighbour rebuild every step, energy+forces"
                                   if mode == "md" else "repeated energy+force evaluations (neighbour build "
                                                        "included)") + f", {dtype}",
-                   "atoms": N, "edges_per_step": E_mean, "layers": 4, "parallelism": "single GPU"},
+                   "atoms": N, "edges_per_step": E_mean, "layers": 4, "parallelism": "single GPU",
+                   "tp_type": args.tp_type, "with_cluster": args.with_cluster},
         "atom_steps_per_s": N * args.steps / dt,
         "mode": mode,
         "peak_memory_gb": peak_gb,

@@ -4,13 +4,14 @@
 // as one GEMM per direction whose edge-side operand is never stored.
 //
 // Forward (k_qkdot_fwd): gate = A W^T + b on the split GEMM of gemm_core.h (128 edges x 128 heads per
-// workgroup, K = 768 in 48 stages of 16).  A lane forms its own A fragment (one edge, eight channels of
-// the stage) in registers: rad from the six table rows of its distance interval (quintic Hermite, the
-// Hermite weights and the table node formed once per edge) and x0 from the 2l + 1 rows of xd of the
-// query atom, then splits it into the bf16 pieces; only W goes through LDS.
+// workgroup, K = 768 in 48 stages of 16).  A is built in LDS 32 channels at a time (double-buffered, one
+// chunk ahead of the MFMAs): rad from the six table rows of each edge's distance interval (quintic
+// Hermite; the table node and Hermite weights formed once per edge) and x0 from the 2l + 1 rows of xd of
+// the query atom, eight lanes per edge so that every load reads whole 128-byte runs; the K loop then
+// splits each lane's fragment into the bf16 pieces as in gemm_core.h.
 //
 // Backward (k_qkdot_bwd): per (128-edge tile, 128-channel column tile) the GEMM dA = dgate W (K = 128)
-// lands in LDS; thread pairs then walk the tile edge by edge (rad, its distance derivative and x0
+// lands in LDS; groups of 16 lanes then walk the tile edge by edge (rad, its distance derivative and x0
 // recomputed as in the forward) and form dx0 = dA rad (written back in place of dA), the edge's
 // dL/ddist = sum dA x0 rad' and dL/dY_m = sum dx0 xd_m over the tile's channels (one partial per column
 // tile and edge); threads per channel then sum Y_m dx0 over the edges of each query row in edge order
@@ -52,90 +53,156 @@ __device__ __forceinline__ QkEdge qk_edge(const e2v2_qkdot_args& A, const Radial
   return q;
 }
 
-// x0 of the eight channels at p (channel offset within the degree) for degree L: sum over its 2L + 1 rows.
-template <int L>
-__device__ __forceinline__ void qk_x0(const float* xr, size_t xm, const float (&Y)[9], floatx4& x0, floatx4& x1) {
-  x0 = floatx4{0.f, 0.f, 0.f, 0.f};
-  x1 = floatx4{0.f, 0.f, 0.f, 0.f};
+// Edge setup of a 128-edge tile in LDS (thread t < 128 for edge e0 + t): table node offset, Hermite
+// weights, Y and the query row (-1 past the valid edges).
+struct QkTileEdges {
+  int64_t toff[kGM];
+  float H[kGM][6];
+  float Y[kGM][9];
+  int row[kGM];
+};
+
+__device__ __forceinline__ void qk_tile_setup(const e2v2_qkdot_args& A, const RadialTab& R, int64_t e0,
+                                              int64_t e_lim, int t, QkTileEdges& S) {
+  if (t >= kGM) return;
+  const int64_t e = e0 + t;
+  if (e < e_lim) {
+    const QkEdge q = qk_edge(A, R, e);
+    S.toff[t] = q.toff;
+    S.H[t][0] = q.H.a0; S.H[t][1] = q.H.a1; S.H[t][2] = q.H.a2;
+    S.H[t][3] = q.H.b0; S.H[t][4] = q.H.b1; S.H[t][5] = q.H.b2;
 #pragma unroll
-  for (int j = 0; j < 2 * L + 1; ++j) {
-    const float* p = xr + (size_t)(L * L + j) * xm;
-    const floatx4 a = ld4(p), b = ld4(p + 4);
-    const float y = Y[L * L + j];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      x0[q] = fmaf(y, a[q], x0[q]);
-      x1[q] = fmaf(y, b[q], x1[q]);
-    }
+    for (int m = 0; m < 9; ++m) S.Y[t][m] = A.Y[e * 9 + m];
+    S.row[t] = A.edge_row[e];
+  } else {
+    S.row[t] = -1;
   }
 }
+
+__device__ __forceinline__ Hermite5 qk_h(const QkTileEdges& S, int er) {
+  Hermite5 H;
+  H.a0 = S.H[er][0]; H.a1 = S.H[er][1]; H.a2 = S.H[er][2];
+  H.b0 = S.H[er][3]; H.b1 = S.H[er][4]; H.b2 = S.H[er][5];
+  return H;
+}
+
+// Forward A values of edge er, channels k .. k + 3 (k = 256 L + c within the 768): x0 of degree L times rad.
+template <int L>
+__device__ __forceinline__ floatx4 qk_a4(const RadialTab& R, const QkTileEdges& S, const float* xd, size_t xm,
+                                         int er, int k) {
+  const int c = k - L * kQC;
+  const float* p = R.tab + S.toff[er] + k;
+  const floatx4 f0 = ld4(p), f1 = ld4(p + kQK), f2 = ld4(p + 2 * kQK);
+  const floatx4 g0 = ld4(p + 4 * kQK), g1 = ld4(p + 5 * kQK), g2 = ld4(p + 6 * kQK);
+  const float* xr = xd + (size_t)S.row[er] * kQC + c;
+  floatx4 xv[2 * L + 1];
+#pragma unroll
+  for (int j = 0; j < 2 * L + 1; ++j) xv[j] = ld4(xr + (size_t)(L * L + j) * xm);
+  const Hermite5 H = qk_h(S, er);
+  floatx4 a;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float x0 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2 * L + 1; ++j) x0 = fmaf(S.Y[er][L * L + j], xv[j][u], x0);
+    a[u] = x0 * herm_value(H, f0[u], f1[u], f2[u], g0[u], g1[u], g2[u]);
+  }
+  return a;
+}
+
+// The forward's A operand is built in LDS 32 channels (two stages) at a time, double-buffered: eight lanes per
+// edge row (lane j: channels 4 j .. 4 j + 3), so that every load instruction reads whole 128-byte runs of the
+// table and xd rows; granules are stored in the A slot order of the K loop (a_slot).
+constexpr int kQCh = 32;                                    // channels per A chunk
+constexpr int kQChG = kGM * kQCh / 4;                       // granules per chunk: 1024 (16 KB)
 
 template <int kP>
 __global__ __launch_bounds__(kGT, 2) void k_qkdot_fwd(e2v2_qkdot_args A, const void* __restrict__ wp,
                                                         const float* __restrict__ bias, float* __restrict__ gate) {
-  constexpr int SB = g_stage_bytes(kP, false);
-  constexpr int nks = kQK / kGK;
-  __shared__ __attribute__((aligned(16))) char lds[2 * SB];
+  constexpr int BS = 16 * kP * kGBg;                        // one B stage: kP pieces of 4 KB
+  constexpr int nks = kQK / kGK;                            // 48
+  __shared__ __attribute__((aligned(16))) char bl[2 * BS];
+  __shared__ floatx4 Ac[2][kQChG];
+  __shared__ QkTileEdges S;
   const int64_t E = A.n_edges;
   const int n_tiles = (int)((E + kGM - 1) / kGM);
   const int tile = xcd_row(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
   const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5;
   const int64_t e0 = (int64_t)tile * kGM;
-  const int ra = wv * 32 + (lane & 31);
-  const int64_t e = e0 + ra;
-  const bool ok = e < qk_e_lim(A);
-  const RadialTab R{A.rtab, A.n_types, A.rtab_n, kQK, 1.0f / A.rtab_h, A.pair_slot};
-  QkEdge q{};
-  float Y[9];
-  const float* xr = A.xd;
-  if (ok) {
-    q = qk_edge(A, R, e);
-#pragma unroll
-    for (int m = 0; m < 9; ++m) Y[m] = A.Y[e * 9 + m];
-    xr = A.xd + (size_t)A.edge_row[e] * kQC;
-  } else {
-#pragma unroll
-    for (int m = 0; m < 9; ++m) Y[m] = 0.f;
-  }
-  const size_t xm = (size_t)A.n_rows * kQC;
-  const float* tb = R.tab + q.toff + 8 * h;
-  const __amdgpu_buffer_rsrc_t br = b_rsrc<kP>(wp, 0, 1, 0, nks);
-  floatx16 acc[4];
-  kloop<kP, false>(lds, SB, nks, lane,
-        [&](int ks, int buf) { load_b<kP>(br, ks, lds + buf * SB + a_stage_bytes(false), wv, lane); },
-        [&](int ks, int buf, AFrag& f) {
-          f.x0 = floatx4{0.f, 0.f, 0.f, 0.f};
-          f.x1 = floatx4{0.f, 0.f, 0.f, 0.f};
-          if (!ok || ks >= nks) return;
-          const int l = ks >> 4;                           // 16 stages per degree
-          const int c = ((ks & 15) << 4) + 8 * h;          // this lane's eight channels within the degree
-          // rad: rows 0..2 at node n (ta) and n + 1 (ta + 4 rows)
-          const float* ta = tb + l * kQC + ((ks & 15) << 4);
-          floatx4 r0, r1;
-#pragma unroll
-          for (int half = 0; half < 2; ++half) {
-            const float* p = ta + 4 * half;
-            const floatx4 f0 = ld4(p), f1 = ld4(p + kQK), f2 = ld4(p + 2 * kQK);
-            const floatx4 g0 = ld4(p + 4 * kQK), g1 = ld4(p + 5 * kQK), g2 = ld4(p + 6 * kQK);
-            floatx4 v;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = herm_value(q.H, f0[u], f1[u], f2[u], g0[u], g1[u], g2[u]);
-            if (half == 0) r0 = v; else r1 = v;
-          }
-          floatx4 x0, x1;
-          const float* xp = xr + c;
-          if (l == 0) qk_x0<0>(xp, xm, Y, x0, x1);
-          else if (l == 1) qk_x0<1>(xp, xm, Y, x0, x1);
-          else qk_x0<2>(xp, xm, Y, x0, x1);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            f.x0[u] = x0[u] * r0[u];
-            f.x1[u] = x1[u] * r1[u];
-          }
-        },
-        acc);
   const int64_t e_lim = qk_e_lim(A);
+  const RadialTab R{A.rtab, A.n_types, A.rtab_n, kQK, 1.0f / A.rtab_h, A.pair_slot};
+  const size_t xm = (size_t)A.n_rows * kQC;
+  const __amdgpu_buffer_rsrc_t br = b_rsrc<kP>(wp, 0, 1, 0, nks);
+  qk_tile_setup(A, R, e0, e_lim, t, S);
+  // chunk c (stages 2c, 2c + 1) into buffer b
+  auto build = [&](int c, int b) {
+    const int j = t & 7, k = c * kQCh + 4 * j, L = k / kQC;
+#pragma unroll 2
+    for (int pass = 0; pass < kGM / 32; ++pass) {
+      const int er = (t >> 3) + 32 * pass;
+      floatx4 a = {0.f, 0.f, 0.f, 0.f};
+      if (S.row[er] >= 0) {
+        if (L == 0) a = qk_a4<0>(R, S, A.xd, xm, er, k);
+        else if (L == 1) a = qk_a4<1>(R, S, A.xd, xm, er, k);
+        else a = qk_a4<2>(R, S, A.xd, xm, er, k);
+      }
+      Ac[b][(j >> 2) * kGAg + a_slot(er, j & 3)] = a;     // stage j / 4 of the chunk, granule j % 4 of the row
+    }
+  };
+  const int ra = wv * 32 + (lane & 31);
+  auto read_a = [&](int ks, AFrag& f) {
+    const floatx4* As = Ac[(ks >> 1) & 1] + (ks & 1) * kGAg;
+    f.x0 = As[a_slot(ra, 2 * h)];
+    f.x1 = As[a_slot(ra, 2 * h + 1)];
+  };
+  floatx16 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+  __syncthreads();                                          // the tile setup
+  load_b<kP>(br, 0, bl, wv, lane);
+  load_b<kP>(br, 1, bl + BS, wv, lane);
+  build(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  bf16x8 a_cur[kP];
+  {
+    AFrag f;
+    read_a(0, f);
+    split_pieces<kP>(f.x0, f.x1, a_cur);
+  }
+  for (int ks = 0; ks < nks; ++ks) {
+    const bf16x8* Bs = reinterpret_cast<const bf16x8*>(bl + (ks & 1) * BS);
+    bf16x8 b[kP][4];
+#pragma unroll
+    for (int p = 0; p < kP; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[p][j] = Bs[p * kGBg + b_slot(32 * j + (lane & 31), h)];
+    if (ks + 1 < nks) {
+      __builtin_amdgcn_s_waitcnt(0);    // stage ks + 1 landed; this wavefront's reads of B buffer ks & 1 are done
+      __syncthreads();
+      if (ks + 2 < nks) load_b<kP>(br, ks + 2, bl + (ks & 1) * BS, wv, lane);
+      // chunk (ks + 2) / 2 into the buffer of chunk ks / 2 - 1, whose last reader ran before this barrier; the
+      // next iteration's barrier orders these writes before the first read (stage ks + 2)
+      if ((ks & 1) == 0 && ks + 2 < nks) build((ks + 2) >> 1, ((ks + 2) >> 1) & 1);
+    }
+    AFrag f;
+    if (ks + 1 < nks) read_a(ks + 1, f);
+    if constexpr (kP == 3) {
+      constexpr int kPa[6] = {0, 1, 2, 0, 1, 0}, kPb[6] = {0, 0, 0, 1, 1, 2};
+#pragma unroll
+      for (int q = 0; q < 6; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_cur[kPa[q]], b[kPb[q]][j], acc[j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_cur[0], b[0][j], acc[j], 0, 0, 0);
+    }
+    if (ks + 1 < nks) split_pieces<kP>(f.x0, f.x1, a_cur);
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int col = 32 * j + (lane & 31);
@@ -148,41 +215,38 @@ __global__ __launch_bounds__(kGT, 2) void k_qkdot_fwd(e2v2_qkdot_args A, const v
   }
 }
 
-// Phase 1 of the backward for one edge and degree L: this thread's 64 channels (8 groups of 8) of column tile
-// ct.  D holds dA of the edge row; dx0 replaces it.  Returns dL/ddist and dL/dY of the degree's rows.
+// Phase 1 of the backward for one edge and degree L, one lane of the edge's 16: channels 4 j .. 4 j + 3 and
+// 64 + 4 j .. + 3 of column tile ct (each load instruction reads 256 contiguous bytes of a row per 16 lanes).
+// D holds dA of the edge row; dx0 replaces it.  Adds this lane's share of dL/ddist and dL/dY of the degree.
 template <int L>
-__device__ __forceinline__ void qk_bwd_edge(const e2v2_qkdot_args& A, const RadialTab& R, const QkEdge& q,
-                                            const float (&Y)[9], const float* xr, size_t xm, int cb, int c0,
+__device__ __forceinline__ void qk_bwd_edge(const RadialTab& R, int64_t toff, const Hermite5& H,
+                                            const float (&Y)[9], const float* xr, size_t xm, int cb, int j,
                                             float* D, float& dd, float (&dY)[5]) {
-#pragma unroll 1
-  for (int g = 0; g < 8; ++g) {
-    const int cc = c0 + 8 * g;                                  // channel within the column tile
-    const float* ta = R.tab + q.toff + L * kQC + cb + cc;       // node n row 0
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int cc = 64 * half + 4 * j;                           // channel within the column tile
+    const float* p = R.tab + toff + L * kQC + cb + cc;          // node n row 0
+    const floatx4 f0 = ld4(p), f1 = ld4(p + kQK), f2 = ld4(p + 2 * kQK), f3 = ld4(p + 3 * kQK);
+    const floatx4 g0 = ld4(p + 4 * kQK), g1 = ld4(p + 5 * kQK), g2 = ld4(p + 6 * kQK), g3 = ld4(p + 7 * kQK);
+    floatx4 xv[2 * L + 1];
+#pragma unroll
+    for (int k = 0; k < 2 * L + 1; ++k) xv[k] = ld4(xr + (size_t)(L * L + k) * xm + cb + cc);
     floatx4* dp = reinterpret_cast<floatx4*>(D + cc);
+    const floatx4 da = *dp;
+    floatx4 dx;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const float* p = ta + 4 * half;
-      const floatx4 f0 = ld4(p), f1 = ld4(p + kQK), f2 = ld4(p + 2 * kQK), f3 = ld4(p + 3 * kQK);
-      const floatx4 g0 = ld4(p + 4 * kQK), g1 = ld4(p + 5 * kQK), g2 = ld4(p + 6 * kQK), g3 = ld4(p + 7 * kQK);
-      floatx4 xv[2 * L + 1];
+    for (int u = 0; u < 4; ++u) {
+      const float rad = herm_value(H, f0[u], f1[u], f2[u], g0[u], g1[u], g2[u]);
+      const float rd = herm_value(H, f1[u], f2[u], f3[u], g1[u], g2[u], g3[u]) * R.inv_h;
+      float x0 = 0.f;
 #pragma unroll
-      for (int j = 0; j < 2 * L + 1; ++j) xv[j] = ld4(xr + (size_t)(L * L + j) * xm + cb + cc + 4 * half);
-      const floatx4 da = dp[half];
-      floatx4 dx;
+      for (int k = 0; k < 2 * L + 1; ++k) x0 = fmaf(Y[L * L + k], xv[k][u], x0);
+      dx[u] = da[u] * rad;
+      dd = fmaf(da[u] * x0, rd, dd);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float rad = herm_value(q.H, f0[u], f1[u], f2[u], g0[u], g1[u], g2[u]);
-        const float rd = herm_value(q.H, f1[u], f2[u], f3[u], g1[u], g2[u], g3[u]) * R.inv_h;
-        float x0 = 0.f;
-#pragma unroll
-        for (int j = 0; j < 2 * L + 1; ++j) x0 = fmaf(Y[L * L + j], xv[j][u], x0);
-        dx[u] = da[u] * rad;
-        dd = fmaf(da[u] * x0, rd, dd);
-#pragma unroll
-        for (int j = 0; j < 2 * L + 1; ++j) dY[j] = fmaf(dx[u], xv[j][u], dY[j]);
-      }
-      dp[half] = dx;
+      for (int k = 0; k < 2 * L + 1; ++k) dY[k] = fmaf(dx[u], xv[k][u], dY[k]);
     }
+    *dp = dx;
   }
 }
 
@@ -224,6 +288,8 @@ __global__ __launch_bounds__(kGT, 2) void k_qkdot_bwd(e2v2_qkdot_args A, const v
   constexpr int kLds = 2 * SB > kGM * kQDl * 4 ? 2 * SB : kGM * kQDl * 4;
   __shared__ __attribute__((aligned(16))) char lds[kLds];
   __shared__ float Ys[kGM][9];
+  __shared__ float Hs[kGM][6];
+  __shared__ int64_t Ts[kGM];
   __shared__ int rows[kGM];
   const int64_t E = A.n_edges;
   const int n_et = (int)((E + kGM - 1) / kGM);
@@ -260,42 +326,58 @@ __global__ __launch_bounds__(kGT, 2) void k_qkdot_bwd(e2v2_qkdot_args A, const v
     for (int r = 0; r < 16; ++r) D[(wv * 32 + acc_row(r, lane)) * kQDl + 32 * j + (lane & 31)] = acc[j][r];
   __syncthreads();
 
-  // phase 1: thread pair (2 er, 2 er + 1) on edge e0 + er, 64 channels each
+  // phase 1: the tile's edges in turn, 16 lanes per edge (edge setup formed once per edge, in LDS)
   const int64_t e_lim = qk_e_lim(A);
   const int l = ct >> 1, cb = (ct & 1) * kGN;
   const RadialTab R{A.rtab, A.n_types, A.rtab_n, kQK, 1.0f / A.rtab_h, A.pair_slot};
   const size_t xm = (size_t)A.n_rows * kQC;
-  {
-    const int er = t >> 1, hf = t & 1;
-    const int64_t e = e0 + er;
-    float dd = 0.f, dY[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  if (t < kGM) {
+    const int64_t e = e0 + t;
     if (e < e_lim) {
       const QkEdge q = qk_edge(A, R, e);
-      float Y[9];
+      Ts[t] = q.toff;
+      Hs[t][0] = q.H.a0; Hs[t][1] = q.H.a1; Hs[t][2] = q.H.a2;
+      Hs[t][3] = q.H.b0; Hs[t][4] = q.H.b1; Hs[t][5] = q.H.b2;
 #pragma unroll
-      for (int m = 0; m < 9; ++m) Y[m] = A.Y[e * 9 + m];
-      const int i = A.edge_row[e];
-      if (hf == 0) {
-        rows[er] = i;
-#pragma unroll
-        for (int m = 0; m < 9; ++m) Ys[er][m] = Y[m];
-      }
-      const float* xr = A.xd + (size_t)i * kQC;
-      float* Dr = D + er * kQDl;
-      if (l == 0) qk_bwd_edge<0>(A, R, q, Y, xr, xm, cb, 64 * hf, Dr, dd, dY);
-      else if (l == 1) qk_bwd_edge<1>(A, R, q, Y, xr, xm, cb, 64 * hf, Dr, dd, dY);
-      else qk_bwd_edge<2>(A, R, q, Y, xr, xm, cb, 64 * hf, Dr, dd, dY);
-    } else if (hf == 0) {
-      rows[er] = -1;
+      for (int m = 0; m < 9; ++m) Ys[t][m] = A.Y[e * 9 + m];
+      rows[t] = A.edge_row[e];
+    } else {
+      rows[t] = -1;
     }
-    dd += __shfl_xor(dd, 1, 64);
+  }
+  __syncthreads();
+  {
+    const int j = t & 15;
+#pragma unroll 1
+    for (int er = t >> 4; er < kGM; er += kGT / 16) {
+      const int64_t e = e0 + er;
+      float dd = 0.f, dY[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+      if (e < e_lim) {
+        Hermite5 H;
+        H.a0 = Hs[er][0]; H.a1 = Hs[er][1]; H.a2 = Hs[er][2];
+        H.b0 = Hs[er][3]; H.b1 = Hs[er][4]; H.b2 = Hs[er][5];
+        float Y[9];
 #pragma unroll
-    for (int j = 0; j < 5; ++j) dY[j] += __shfl_xor(dY[j], 1, 64);
-    if (hf == 0 && e < E) {
-      float* pp = part + ((size_t)ct * E + e) * kQPart;
-      pp[0] = dd;
+        for (int m = 0; m < 9; ++m) Y[m] = Ys[er][m];
+        const float* xr = A.xd + (size_t)rows[er] * kQC;
+        float* Dr = D + er * kQDl;
+        if (l == 0) qk_bwd_edge<0>(R, Ts[er], H, Y, xr, xm, cb, j, Dr, dd, dY);
+        else if (l == 1) qk_bwd_edge<1>(R, Ts[er], H, Y, xr, xm, cb, j, Dr, dd, dY);
+        else qk_bwd_edge<2>(R, Ts[er], H, Y, xr, xm, cb, j, Dr, dd, dY);
+      }
+      // sums over the edge's 16 lanes (a fixed butterfly order)
 #pragma unroll
-      for (int j = 0; j < 5; ++j) pp[1 + j] = dY[j];
+      for (int o = 8; o >= 1; o >>= 1) {
+        dd += __shfl_xor(dd, o, 64);
+#pragma unroll
+        for (int k = 0; k < 5; ++k) dY[k] += __shfl_xor(dY[k], o, 64);
+      }
+      if (j == 0 && e < E) {
+        float* pp = part + ((size_t)ct * E + e) * kQPart;
+        pp[0] = dd;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) pp[1 + k] = dY[k];
+      }
     }
   }
   __syncthreads();
