@@ -523,11 +523,13 @@ int64_t e2v2_gemm_packed_bytes(int n_w, int n, int k, int pieces);
  *   bwd: gx [9][N][C] = gy W (+ gv Wv when gv != NULL, gv [9][N][cv]), gy the contraction's gradient formed
  *        from y, ghq, ghk as the operand is read; wp = per l the packed [W rows in y's order ; Wv_l]^T
  *        ([C][4 hid + cv]).
+ * y_bf16 = 1 (one piece only, the bf16 mode): y is stored as bf16 (rounded once; the forward's contraction uses
+ * the fp32 sums) and read as bf16 by the backward: half the memory the backward keeps per layer.
  * Requires hid % 64 == 0, C % 16 (fwd) / % 128 (bwd), cv % 16 == 0; operands 16-byte aligned. */
-int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bias, float* y, float* hq, float* hk, int n,
-                        int hid, int c, int pieces, hipStream_t s);
-int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* ghk, const void* wp, const float* gv,
-                        float* gx, int n, int hid, int c, int cv, int pieces, hipStream_t s);
+int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bias, void* y, float* hq, float* hk, int n,
+                        int hid, int c, int pieces, int y_bf16, hipStream_t s);
+int e2v2_qk_proj_bwd_s3(const void* y, const float* ghq, const float* ghk, const void* wp, const float* gv,
+                        float* gx, int n, int hid, int c, int cv, int pieces, int y_bf16, hipStream_t s);
 int e2v2_gemm_pack(const float* w, int64_t ld_n, int64_t ld_k, int64_t w_stride, int n_w, int n, int k, int pieces,
                    void* packed, hipStream_t s);
 

@@ -366,3 +366,48 @@ def test_qk_proj_one_piece_against_float64(pkg, cuda):
         rel = float((got.cpu().double() - r).norm() / r.norm())
         print(f"[qk one-piece] rel {rel:.2e}", flush=True)
         assert rel < 2e-5
+
+
+def test_qk_proj_one_piece_bf16_y_backward(pkg, cuda):
+    """One-piece packs keep y as bf16 (the bf16 mode): y within one bf16 rounding
+    of the float64 product, hq / hk from the fp32 sums as before, and the input
+    gradient equal, at fp32 accumulation error, to float64 GEMMs of exactly the
+    operands the kernel forms: the contraction gradient g * y(partner) from the
+    stored bf16 y, multiplied in fp32 and rounded to bf16, the value gradient
+    and both weights rounded to bf16."""
+    from ubio_molfm_amd import gemm
+    torch.manual_seed(10)
+    n, hid, C, Cv = 300, 512, 256, 256
+    W = torch.randn(3, 4 * hid, C, device=cuda) / 16
+    b = torch.randn(4 * hid, device=cuda)
+    Wv = torch.randn(3, Cv, C, device=cuda) / 16
+    P = gemm.pack_qk(W, b, Wv, pieces=1)
+    x = torch.randn(9, n, C, device=cuda)
+    hq, hk, y = gemm.qk_forward(x, P)
+    assert y.dtype == torch.bfloat16
+    hq32, hk32, y32 = gemm.qk_forward(x, P, y_bf16=False)
+    assert torch.equal(hq, hq32) and torch.equal(hk, hk32) and torch.equal(y, y32.to(torch.bfloat16))
+    _, bwd_order = gemm.qk_orders(hid)
+    ym = torch.empty(9, n, 4 * hid, dtype=torch.float32, device=cuda)
+    ym[:, :, torch.as_tensor(bwd_order, device=cuda)] = y.float()      # W's column order
+    idx = torch.tensor([0, 1, 1, 1, 2, 2, 2, 2, 2])
+    yd = torch.einsum("mnc,moc->mno", _bf(x.cpu()), _bf(W.cpu())[idx])
+    yd[0] += b.cpu().double()
+    assert float((ym.cpu().double() - yd).abs().max() / yd.abs().max()) < 4e-3
+    ghq = torch.randn(n, 3 * hid, device=cuda); ghk = torch.randn(n, 3 * hid, device=cuda)
+    gv = torch.randn(9, n, Cv, device=cuda)
+    gx = gemm.qk_backward(y, ghq, ghk, gv, P)
+    lm = [0, 1, 1, 1, 2, 2, 2, 2, 2]
+    gy = torch.empty(9, n, 4 * hid, dtype=torch.float32)
+    yc = ym.cpu()
+    for m in range(9):
+        l = lm[m]
+        gq, gk = ghq.cpu()[:, l * hid:(l + 1) * hid], ghk.cpu()[:, l * hid:(l + 1) * hid]
+        qa, qb, ka, kb = yc[m].split(hid, dim=1)
+        gy[m] = torch.cat([qb * gq, qa * gq, kb * gk, ka * gk], dim=1)     # fp32 products, as the kernel forms them
+    gy = gy.to(torch.bfloat16).double()
+    ref = torch.einsum("mno,mok->mnk", gy, _bf(W.cpu())[idx]) + \
+        torch.einsum("mnj,mjk->mnk", _bf(gv.cpu()), _bf(Wv.cpu())[idx])
+    rel = float((gx.cpu().double() - ref).norm() / ref.norm())
+    print(f"[qk one-piece bf16 y] gx rel {rel:.2e}", flush=True)
+    assert rel < 2e-5

@@ -224,9 +224,9 @@ __global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp(GemmGroups P) {
 // so that within every 16-k stage of the backward the partner of column k is k ^ 8.
 __device__ __forceinline__ int pair_pos(int p, int ab) { return 16 * (p >> 3) + 8 * ab + (p & 7); }
 
-template <int kP>
+template <int kP, bool kYB>
 __global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ x, const void* __restrict__ wp,
-                                                      const float* __restrict__ bias, float* __restrict__ y,
+                                                      const float* __restrict__ bias, void* __restrict__ y,
                                                       float* __restrict__ hq, float* __restrict__ hk, int n,
                                                       int hid, int c) {
   constexpr int SB = g_stage_bytes(kP, false);
@@ -262,7 +262,10 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ 
             f.x1 = As[a_slot(ra, 2 * h + 1)];
           },
           acc);
-    float* ym = y + (size_t)m * n * O;
+    // y kept for the backward: fp32, or bf16 (kYB, the bf16 mode: rounded once; the contraction below uses
+    // the fp32 sums)
+    float* ym = static_cast<float*>(y) + (kYB ? 0 : (size_t)m * n * O);
+    __bf16* ymb = static_cast<__bf16*>(y) + (kYB ? (size_t)m * n * O : 0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int p = 64 * pt + 32 * (j & 1) + (lane & 31), ab = j >> 1;
@@ -272,7 +275,12 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ 
       for (int r = 0; r < 16; ++r) {
         const int row = row0 + wv * 32 + acc_row(r, lane);
         acc[j][r] += bv;
-        if (row < n) ym[(size_t)row * O + col] = acc[j][r];
+        if (row < n) {
+          if constexpr (kYB)
+            ymb[(size_t)row * O + col] = (__bf16)acc[j][r];
+          else
+            ym[(size_t)row * O + col] = acc[j][r];
+        }
       }
     }
 #pragma unroll
@@ -303,8 +311,8 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_fwd(const float* __restrict__ 
 __host__ __device__ constexpr int qk_bwd_stage_bytes(int kP) { return g_stage_bytes(kP, false) + 128 * 8 * 4; }
 __device__ __forceinline__ int g_slot(int r, int g) { return r * 2 + (g ^ ((r >> 3) & 1)); }
 
-template <int kP>
-__global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const float* __restrict__ y, const float* __restrict__ ghq,
+template <int kP, bool kYB>
+__global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const void* __restrict__ y, const float* __restrict__ ghq,
                                                       const float* __restrict__ ghk, const void* __restrict__ wp,
                                                       const float* __restrict__ gv, float* __restrict__ gx, int n,
                                                       int hid, int c, int cv) {
@@ -321,7 +329,10 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const float* __restrict__ 
   uint32_t y_voff[kGAi / 4], v_voff[kGAi / 4];
   a_offsets(wv, lane, O, y_voff);
   a_offsets(wv, lane, cv, v_voff);
-  const __amdgpu_buffer_rsrc_t yr = rows_rsrc(y + (size_t)m * n * O, row0, n, O);
+  const uint32_t yb_voff = abf_offset(wv, lane, O);      // bf16 y: one granule (8 values) per lane and stage
+  const __amdgpu_buffer_rsrc_t yr =
+      kYB ? rows_rsrc_bf(static_cast<const __bf16*>(y) + (size_t)m * n * O, row0, n, O)
+          : rows_rsrc(static_cast<const float*>(y) + (size_t)m * n * O, row0, n, O);
   const __amdgpu_buffer_rsrc_t vr = gv ? rows_rsrc(gv + (size_t)m * n * cv, row0, n, cv) : yr;
   const __amdgpu_buffer_rsrc_t qr = rows_rsrc(ghq, row0, n, 3 * hid), kr = rows_rsrc(ghk, row0, n, 3 * hid);
   constexpr int kBS = b_stage_granules(kP) * 16;
@@ -337,7 +348,11 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const float* __restrict__ 
         [&](int ks, int buf) {
           char* As = lds + buf * kGStageQ;
           if (ks < nk1) {
-            load_a(yr, y_voff, (uint32_t)(ks * kGK) * 4u, As, wv);
+            if constexpr (kYB)
+              __builtin_amdgcn_raw_ptr_buffer_load_lds(yr, (lds_void*)(As + wv * 1024), 16,
+                                                       yb_voff + (uint32_t)(ks * kGK) * 2u, 0, 0, 0);
+            else
+              load_a(yr, y_voff, (uint32_t)(ks * kGK) * 4u, As, wv);
             const int p0 = 8 * ks;                                     // first pair of the stage
             const uint32_t goff = (uint32_t)(l * hid + (p0 < hid ? p0 : p0 - hid)) * 4u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(p0 < hid ? qr : kr, (lds_void*)(As + SB + wv * 1024), 16,
@@ -351,8 +366,19 @@ __global__ __launch_bounds__(kGT, 2) void k_qk_s3_bwd(const float* __restrict__ 
           const floatx4* As = reinterpret_cast<const floatx4*>(lds + buf * kGStageQ);
           if (ks < nk1) {
             const floatx4* Gs = reinterpret_cast<const floatx4*>(lds + buf * kGStageQ + SB);
-            f.x0 = As[a_slot(ra, 2 - 2 * h)] * Gs[g_slot(ra, 0)];
-            f.x1 = As[a_slot(ra, 3 - 2 * h)] * Gs[g_slot(ra, 1)];
+            if constexpr (kYB) {
+              // the partner's eight bf16 values (the other half of the stage: granule 1 - h), widened exactly
+              const bf16x8 yb = reinterpret_cast<const bf16x8*>(lds + buf * kGStageQ)[abf_slot(ra, 1 - h)];
+              const floatx4 g0 = Gs[g_slot(ra, 0)], g1 = Gs[g_slot(ra, 1)];
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                f.x0[u] = (float)yb[u] * g0[u];
+                f.x1[u] = (float)yb[4 + u] * g1[u];
+              }
+            } else {
+              f.x0 = As[a_slot(ra, 2 - 2 * h)] * Gs[g_slot(ra, 0)];
+              f.x1 = As[a_slot(ra, 3 - 2 * h)] * Gs[g_slot(ra, 1)];
+            }
           } else {
             f.x0 = As[a_slot(ra, 2 * h)];
             f.x1 = As[a_slot(ra, 2 * h + 1)];
@@ -529,10 +555,12 @@ E2V2_API int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hi
 // hq, hk [n][3 hid] and the kept y [9][n][4 hid] (paired order) from x [9][n][c];
 // wp: the three per-l weights packed with their columns in the tile-paired order
 // (n = 4 hid, k = c), bias [4 hid] in the same order (m = 0 rows only; may be NULL).
-E2V2_API int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bias, float* y, float* hq, float* hk,
-                                 int n, int hid, int c, int pieces, hipStream_t s) {
+E2V2_API int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bias, void* y, float* hq, float* hk,
+                                 int n, int hid, int c, int pieces, int y_bf16, hipStream_t s) {
   using namespace e2v2;
   E2V2_REQUIRE(pieces == 1 || pieces == 3, "qk_proj_fwd_s3: %d pieces (1 or 3)", pieces);
+  E2V2_REQUIRE(y_bf16 == 0 || (y_bf16 == 1 && pieces == 1), "qk_proj_fwd_s3: bf16 y (%d) with one piece only",
+               y_bf16);
   E2V2_REQUIRE(hid > 0 && hid % 64 == 0, "qk_proj_fwd_s3: hid=%d must be a positive multiple of 64", hid);
   E2V2_REQUIRE(c > 0 && c % kGK == 0, "qk_proj_fwd_s3: C=%d must be a positive multiple of %d", c, kGK);
   E2V2_REQUIRE(x && wp && y && hq && hk, "qk_proj_fwd_s3: null operand");
@@ -541,10 +569,13 @@ E2V2_API int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bi
                    (uint64_t)(n + kGM) * 4u * hid < (1ull << 32), "qk_proj_fwd_s3: n=%d too large", n);
   if (n == 0) return 0;
   const int tiles = ((n + kGM - 1) / kGM) * (2 * hid / 64);
+  const dim3 grid(3 * xcd_grid(tiles));
   if (pieces == 3)
-    hipLaunchKernelGGL((k_qk_s3_fwd<3>), dim3(3 * xcd_grid(tiles)), dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
+    hipLaunchKernelGGL((k_qk_s3_fwd<3, false>), grid, dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
+  else if (y_bf16)
+    hipLaunchKernelGGL((k_qk_s3_fwd<1, true>), grid, dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
   else
-    hipLaunchKernelGGL((k_qk_s3_fwd<1>), dim3(3 * xcd_grid(tiles)), dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
+    hipLaunchKernelGGL((k_qk_s3_fwd<1, false>), grid, dim3(kGT), 0, s, x, wp, bias, y, hq, hk, n, hid, c);
   E2V2_LAUNCHED("k_qk_s3_fwd");
   return 0;
 }
@@ -552,10 +583,12 @@ E2V2_API int e2v2_qk_proj_fwd_s3(const float* x, const void* wp, const float* bi
 // gx [9][n][c] from y (paired order), ghq, ghk [n][3 hid] and, when gv != NULL,
 // gv [9][n][cv]; wp: per l the packed [W_l (rows in the paired order) ; Wv_l]^T
 // (n = c, k = 4 hid + cv).
-E2V2_API int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* ghk, const void* wp, const float* gv,
-                                 float* gx, int n, int hid, int c, int cv, int pieces, hipStream_t s) {
+E2V2_API int e2v2_qk_proj_bwd_s3(const void* y, const float* ghq, const float* ghk, const void* wp, const float* gv,
+                                 float* gx, int n, int hid, int c, int cv, int pieces, int y_bf16, hipStream_t s) {
   using namespace e2v2;
   E2V2_REQUIRE(pieces == 1 || pieces == 3, "qk_proj_bwd_s3: %d pieces (1 or 3)", pieces);
+  E2V2_REQUIRE(y_bf16 == 0 || (y_bf16 == 1 && pieces == 1), "qk_proj_bwd_s3: bf16 y (%d) with one piece only",
+               y_bf16);
   E2V2_REQUIRE(hid > 0 && hid % 64 == 0, "qk_proj_bwd_s3: hid=%d must be a positive multiple of 64", hid);
   E2V2_REQUIRE(c > 0 && c % kGN == 0, "qk_proj_bwd_s3: C=%d must be a positive multiple of %d", c, kGN);
   E2V2_REQUIRE(cv > 0 && cv % kGK == 0, "qk_proj_bwd_s3: Cv=%d must be a positive multiple of %d", cv, kGK);
@@ -566,10 +599,13 @@ E2V2_API int e2v2_qk_proj_bwd_s3(const float* y, const float* ghq, const float* 
                    (uint64_t)(n + kGM) * (uint64_t)cv * 4u < (1ull << 31), "qk_proj_bwd_s3: n=%d too large", n);
   if (n == 0) return 0;
   const int tiles = 9 * ((n + kGM - 1) / kGM) * (c / kGN);
+  const dim3 grid(xcd_grid(tiles));
   if (pieces == 3)
-    hipLaunchKernelGGL((k_qk_s3_bwd<3>), dim3(xcd_grid(tiles)), dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
+    hipLaunchKernelGGL((k_qk_s3_bwd<3, false>), grid, dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
+  else if (y_bf16)
+    hipLaunchKernelGGL((k_qk_s3_bwd<1, true>), grid, dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
   else
-    hipLaunchKernelGGL((k_qk_s3_bwd<1>), dim3(xcd_grid(tiles)), dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
+    hipLaunchKernelGGL((k_qk_s3_bwd<1, false>), grid, dim3(kGT), 0, s, y, ghq, ghk, wp, gv, gx, n, hid, c, cv);
   E2V2_LAUNCHED("k_qk_s3_bwd");
   return 0;
 }

@@ -260,28 +260,38 @@ def pack_qk(W: torch.Tensor, bias: Optional[torch.Tensor], Wv: torch.Tensor, pie
     return P
 
 
-def qk_forward(x: torch.Tensor, P: QKPacks):
-    """(hq, hk [N, 3 hid], y [9, N, 4 hid] in the backward order) from x [9, N, C]."""
+def qk_forward(x: torch.Tensor, P: QKPacks, y_bf16: Optional[bool] = None):
+    """(hq, hk [N, 3 hid], y [9, N, 4 hid] in the backward order) from x [9, N, C];
+    y_bf16: y kept as bf16 for the backward (default: with one-piece packs, the
+    bf16 mode)."""
     x = x.contiguous()
     _, n, c = x.shape
-    y = x.new_empty(9, n, 4 * P.hid)
+    if y_bf16 is None:
+        y_bf16 = P.fwd.pieces == 1
+    if y_bf16 and P.fwd.pieces != 1:
+        raise ValueError("qk_forward: a bf16 y needs one-piece packs")
+    y = x.new_empty(9, n, 4 * P.hid, dtype=torch.bfloat16 if y_bf16 else torch.float32)
     hq = x.new_empty(n, 3 * P.hid)
     hk = x.new_empty(n, 3 * P.hid)
     st = _lib.vp(torch.cuda.current_stream(x.device).cuda_stream)
     _lib.call("e2v2_qk_proj_fwd_s3", _lib.vp(x.data_ptr()), _lib.vp(P.fwd.buf.data_ptr()),
               _lib.vp(0 if P.bias is None else P.bias.data_ptr()), _lib.vp(y.data_ptr()), _lib.vp(hq.data_ptr()),
-              _lib.vp(hk.data_ptr()), _lib.i32(n), _lib.i32(P.hid), _lib.i32(c), _lib.i32(P.fwd.pieces), st)
+              _lib.vp(hk.data_ptr()), _lib.i32(n), _lib.i32(P.hid), _lib.i32(c), _lib.i32(P.fwd.pieces),
+              _lib.i32(int(y_bf16)), st)
     return hq, hk, y
 
 
 def qk_backward(y: torch.Tensor, ghq: torch.Tensor, ghk: torch.Tensor, gv: Optional[torch.Tensor], P: QKPacks):
-    """gx [9, N, C] (with gv [9, N, Cv] W_v added when gv is given)."""
+    """gx [9, N, C] (with gv [9, N, Cv] W_v added when gv is given); y fp32, or bf16
+    from qk_forward(y_bf16=True)."""
     n = y.shape[1]
-    gx = y.new_empty(9, n, P.c)
+    gx = y.new_empty(9, n, P.c, dtype=torch.float32)
+    y_bf16 = y.dtype == torch.bfloat16
     ghq, ghk = ghq.contiguous(), ghk.contiguous()
     gv = None if gv is None else gv.float().contiguous()
     st = _lib.vp(torch.cuda.current_stream(y.device).cuda_stream)
     _lib.call("e2v2_qk_proj_bwd_s3", _lib.vp(y.data_ptr()), _lib.vp(ghq.data_ptr()), _lib.vp(ghk.data_ptr()),
               _lib.vp(P.bwd.buf.data_ptr()), _lib.vp(0 if gv is None else gv.data_ptr()), _lib.vp(gx.data_ptr()),
-              _lib.i32(n), _lib.i32(P.hid), _lib.i32(P.c), _lib.i32(P.cv), _lib.i32(P.bwd.pieces), st)
+              _lib.i32(n), _lib.i32(P.hid), _lib.i32(P.c), _lib.i32(P.cv), _lib.i32(P.bwd.pieces),
+              _lib.i32(int(y_bf16)), st)
     return gx
