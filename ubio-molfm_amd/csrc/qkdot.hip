@@ -11,8 +11,9 @@
 // splits each lane's fragment into the bf16 pieces as in gemm_core.h.
 //
 // Backward (k_qkdot_bwd): per (128-edge tile, 128-channel column tile) the GEMM dA = dgate W (K = 128)
-// lands in LDS; groups of 16 lanes then walk the tile edge by edge (rad, its distance derivative and x0
-// recomputed as in the forward) and form dx0 = dA rad (written back in place of dA), the edge's
+// lands in registers and, one 64-channel half at a time, in LDS; groups of 16 lanes then walk the tile edge
+// by edge (rad, its distance derivative and x0 recomputed as in the forward) and form dx0 = dA rad (written
+// back in place of dA), the edge's
 // dL/ddist = sum dA x0 rad' and dL/dY_m = sum dx0 xd_m over the tile's channels (one partial per column
 // tile and edge); threads per channel then sum Y_m dx0 over the edges of each query row in edge order
 // (dL/dxd).  A row that lies inside the tile is written directly; a row that crosses a tile boundary
@@ -31,7 +32,6 @@ constexpr int kQH = 128;            // heads: the forward's N, the backward's K
 constexpr int kQSide = 9 * kQC;     // partial dL/dxd of one boundary row: [9][256]
 constexpr int kQCt = kQK / kGN;     // column tiles of the backward: 6 (two per degree)
 constexpr int kQPart = 6;           // per (column tile, edge): dL/ddist, then dL/dY of the tile's degree
-constexpr int kQDl = kGN + 4;       // row stride (floats) of the dA tile in LDS
 
 __device__ __forceinline__ int64_t qk_e_lim(const e2v2_qkdot_args& A) {
   return A.e_end ? min(A.n_edges, (int64_t)*A.e_end) : A.n_edges;
@@ -215,64 +215,63 @@ __global__ __launch_bounds__(kGT, 2) void k_qkdot_fwd(e2v2_qkdot_args A, const v
   }
 }
 
-// Phase 1 of the backward for one edge and degree L, one lane of the edge's 16: channels 4 j .. 4 j + 3 and
-// 64 + 4 j .. + 3 of column tile ct (each load instruction reads 256 contiguous bytes of a row per 16 lanes).
-// D holds dA of the edge row; dx0 replaces it.  Adds this lane's share of dL/ddist and dL/dY of the degree.
+// Phase 1 of the backward for one edge and degree L, one lane of the edge's 16: channels c .. c + 3 of the
+// degree (each load instruction reads 256 contiguous bytes of a row per 16 lanes).  D points at the edge's
+// dA values of those channels; dx0 replaces them.  Adds this lane's share of dL/ddist and dL/dY.
 template <int L>
 __device__ __forceinline__ void qk_bwd_edge(const RadialTab& R, int64_t toff, const Hermite5& H,
-                                            const float (&Y)[9], const float* xr, size_t xm, int cb, int j,
-                                            float* D, float& dd, float (&dY)[5]) {
+                                            const float (&Y)[9], const float* xr, size_t xm, int c, float* D,
+                                            float& dd, float (&dY)[5]) {
+  const float* p = R.tab + toff + L * kQC + c;                  // node n row 0
+  const floatx4 f0 = ld4(p), f1 = ld4(p + kQK), f2 = ld4(p + 2 * kQK), f3 = ld4(p + 3 * kQK);
+  const floatx4 g0 = ld4(p + 4 * kQK), g1 = ld4(p + 5 * kQK), g2 = ld4(p + 6 * kQK), g3 = ld4(p + 7 * kQK);
+  floatx4 xv[2 * L + 1];
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const int cc = 64 * half + 4 * j;                           // channel within the column tile
-    const float* p = R.tab + toff + L * kQC + cb + cc;          // node n row 0
-    const floatx4 f0 = ld4(p), f1 = ld4(p + kQK), f2 = ld4(p + 2 * kQK), f3 = ld4(p + 3 * kQK);
-    const floatx4 g0 = ld4(p + 4 * kQK), g1 = ld4(p + 5 * kQK), g2 = ld4(p + 6 * kQK), g3 = ld4(p + 7 * kQK);
-    floatx4 xv[2 * L + 1];
+  for (int k = 0; k < 2 * L + 1; ++k) xv[k] = ld4(xr + (size_t)(L * L + k) * xm + c);
+  floatx4* dp = reinterpret_cast<floatx4*>(D);
+  const floatx4 da = *dp;
+  floatx4 dx;
 #pragma unroll
-    for (int k = 0; k < 2 * L + 1; ++k) xv[k] = ld4(xr + (size_t)(L * L + k) * xm + cb + cc);
-    floatx4* dp = reinterpret_cast<floatx4*>(D + cc);
-    const floatx4 da = *dp;
-    floatx4 dx;
+  for (int u = 0; u < 4; ++u) {
+    const float rad = herm_value(H, f0[u], f1[u], f2[u], g0[u], g1[u], g2[u]);
+    const float rd = herm_value(H, f1[u], f2[u], f3[u], g1[u], g2[u], g3[u]) * R.inv_h;
+    float x0 = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float rad = herm_value(H, f0[u], f1[u], f2[u], g0[u], g1[u], g2[u]);
-      const float rd = herm_value(H, f1[u], f2[u], f3[u], g1[u], g2[u], g3[u]) * R.inv_h;
-      float x0 = 0.f;
+    for (int k = 0; k < 2 * L + 1; ++k) x0 = fmaf(Y[L * L + k], xv[k][u], x0);
+    dx[u] = da[u] * rad;
+    dd = fmaf(da[u] * x0, rd, dd);
 #pragma unroll
-      for (int k = 0; k < 2 * L + 1; ++k) x0 = fmaf(Y[L * L + k], xv[k][u], x0);
-      dx[u] = da[u] * rad;
-      dd = fmaf(da[u] * x0, rd, dd);
-#pragma unroll
-      for (int k = 0; k < 2 * L + 1; ++k) dY[k] = fmaf(dx[u], xv[k][u], dY[k]);
-    }
-    *dp = dx;
+    for (int k = 0; k < 2 * L + 1; ++k) dY[k] = fmaf(dx[u], xv[k][u], dY[k]);
   }
+  *dp = dx;
 }
 
-// Phase 2 for degree L: sums over the edges of each row of Y_m dx0 for channel cc, m-rows [m0, m1) of L.
+constexpr int kQDh = 64 + 4;        // row stride (floats) of a 64-channel half of the dA tile in LDS
+
+// Phase 2 for degree L: sums over the edges of each row of Y_m dx0 for channel cd of the LDS half tile
+// (degree channel c), m-rows mg and mg + 4 of L's 2 L + 1.
 template <int L>
 __device__ __forceinline__ void qk_bwd_rows(const e2v2_qkdot_args& A, const float* D, const float (*Ys)[9],
-                                            const int* rows, int n_valid, int64_t e0, int et, int cb, int cc, int m0,
-                                            int m1, float* __restrict__ side, float* __restrict__ dxd) {
-  float acc[3] = {0.f, 0.f, 0.f};
+                                            const int* rows, int n_valid, int64_t e0, int et, int cd, int c, int mg,
+                                            float* __restrict__ side, float* __restrict__ dxd) {
+  constexpr int M = 2 * L + 1;
+  float acc[2] = {0.f, 0.f};
   const size_t xm = (size_t)A.n_rows * kQC;
   for (int er = 0; er < n_valid; ++er) {
     const int r = rows[er];
-    const float d = D[er * kQDl + cc];
+    const float d = D[er * kQDh + cd];
 #pragma unroll
-    for (int k = 0; k < 3; ++k)
-      if (m0 + k < m1) acc[k] = fmaf(Ys[er][L * L + m0 + k], d, acc[k]);
+    for (int k = 0; k < 2; ++k)
+      if (mg + 4 * k < M) acc[k] = fmaf(Ys[er][L * L + mg + 4 * k], d, acc[k]);
     if (er + 1 == n_valid || rows[er + 1] != r) {
       const bool whole = A.row_ptr[r] >= e0 && A.row_ptr[r + 1] <= e0 + n_valid;
-      float* out = whole ? dxd + xm * (size_t)(L * L) + (size_t)r * kQC + cb + cc
-                         : side + ((size_t)et * 2 + (r == rows[0] ? 0 : 1)) * kQSide + (size_t)(L * L) * kQC + cb +
-                               cc;
+      float* out = whole ? dxd + xm * (size_t)(L * L) + (size_t)r * kQC + c
+                         : side + ((size_t)et * 2 + (r == rows[0] ? 0 : 1)) * kQSide + (size_t)(L * L) * kQC + c;
       const size_t ms = whole ? xm : (size_t)kQC;
 #pragma unroll
-      for (int k = 0; k < 3; ++k)
-        if (m0 + k < m1) {
-          out[(size_t)(m0 + k) * ms] = acc[k];
+      for (int k = 0; k < 2; ++k)
+        if (mg + 4 * k < M) {
+          out[(size_t)(mg + 4 * k) * ms] = acc[k];
           acc[k] = 0.f;
         }
     }
@@ -280,17 +279,19 @@ __device__ __forceinline__ void qk_bwd_rows(const e2v2_qkdot_args& A, const floa
 }
 
 template <int kP>
-__global__ __launch_bounds__(kGT, 2) void k_qkdot_bwd(e2v2_qkdot_args A, const void* __restrict__ wtp,
+__global__ __launch_bounds__(kGT, 3) void k_qkdot_bwd(e2v2_qkdot_args A, const void* __restrict__ wtp,
                                                         const float* __restrict__ dgate, float* __restrict__ part,
                                                         float* __restrict__ side, float* __restrict__ dxd) {
   constexpr int SB = g_stage_bytes(kP, false);
   constexpr int nks = kQH / kGK;
-  constexpr int kLds = 2 * SB > kGM * kQDl * 4 ? 2 * SB : kGM * kQDl * 4;
+  // the stage buffers of the GEMM, then (reused) one 64-channel half of the dA tile
+  constexpr int kLds = 2 * SB > kGM * kQDh * 4 ? 2 * SB : kGM * kQDh * 4;
   __shared__ __attribute__((aligned(16))) char lds[kLds];
   __shared__ float Ys[kGM][9];
   __shared__ float Hs[kGM][6];
   __shared__ int64_t Ts[kGM];
   __shared__ int rows[kGM];
+  __shared__ float Pl[kGM][kQPart];   // the first half's per-edge partials
   const int64_t E = A.n_edges;
   const int n_et = (int)((E + kGM - 1) / kGM);
   const int tile = xcd_row(blockIdx.x, n_et * kQCt);
@@ -318,15 +319,8 @@ __global__ __launch_bounds__(kGT, 2) void k_qkdot_bwd(e2v2_qkdot_args A, const v
           f.x1 = As[a_slot(ra, 2 * h + 1)];
         },
         acc);
-  __syncthreads();   // every wavefront is past its last read of the stage buffers
-  float* D = reinterpret_cast<float*>(lds);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) D[(wv * 32 + acc_row(r, lane)) * kQDl + 32 * j + (lane & 31)] = acc[j][r];
-  __syncthreads();
 
-  // phase 1: the tile's edges in turn, 16 lanes per edge (edge setup formed once per edge, in LDS)
+  // edge setup, once per edge in LDS
   const int64_t e_lim = qk_e_lim(A);
   const int l = ct >> 1, cb = (ct & 1) * kGN;
   const RadialTab R{A.rtab, A.n_types, A.rtab_n, kQK, 1.0f / A.rtab_h, A.pair_slot};
@@ -345,8 +339,21 @@ __global__ __launch_bounds__(kGT, 2) void k_qkdot_bwd(e2v2_qkdot_args A, const v
       rows[t] = -1;
     }
   }
-  __syncthreads();
-  {
+  const int64_t nv = e_lim - e0;
+  const int n_valid = nv <= 0 ? 0 : (nv < kGM ? (int)nv : kGM);
+  float* D = reinterpret_cast<float*>(lds);
+  // the tile's two 64-channel halves in turn (accumulator tiles j = 2 hf, 2 hf + 1)
+  auto run_half = [&](auto hfc) {
+    constexpr int hf = decltype(hfc)::value;
+    __syncthreads();   // the stage buffers (hf 0) or the previous half (hf 1) are no longer read
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        D[(wv * 32 + acc_row(r, lane)) * kQDh + 32 * jj + (lane & 31)] = acc[2 * hf + jj][r];
+    __syncthreads();
+    const int ch = cb + 64 * hf;                 // first channel of the half within the degree
+    // phase 1: the tile's edges in turn, 16 lanes per edge, four channels per lane
     const int j = t & 15;
 #pragma unroll 1
     for (int er = t >> 4; er < kGM; er += kGT / 16) {
@@ -360,10 +367,10 @@ __global__ __launch_bounds__(kGT, 2) void k_qkdot_bwd(e2v2_qkdot_args A, const v
 #pragma unroll
         for (int m = 0; m < 9; ++m) Y[m] = Ys[er][m];
         const float* xr = A.xd + (size_t)rows[er] * kQC;
-        float* Dr = D + er * kQDl;
-        if (l == 0) qk_bwd_edge<0>(R, Ts[er], H, Y, xr, xm, cb, j, Dr, dd, dY);
-        else if (l == 1) qk_bwd_edge<1>(R, Ts[er], H, Y, xr, xm, cb, j, Dr, dd, dY);
-        else qk_bwd_edge<2>(R, Ts[er], H, Y, xr, xm, cb, j, Dr, dd, dY);
+        float* Dr = D + er * kQDh + 4 * j;
+        if (l == 0) qk_bwd_edge<0>(R, Ts[er], H, Y, xr, xm, ch + 4 * j, Dr, dd, dY);
+        else if (l == 1) qk_bwd_edge<1>(R, Ts[er], H, Y, xr, xm, ch + 4 * j, Dr, dd, dY);
+        else qk_bwd_edge<2>(R, Ts[er], H, Y, xr, xm, ch + 4 * j, Dr, dd, dY);
       }
       // sums over the edge's 16 lanes (a fixed butterfly order)
 #pragma unroll
@@ -372,27 +379,30 @@ __global__ __launch_bounds__(kGT, 2) void k_qkdot_bwd(e2v2_qkdot_args A, const v
 #pragma unroll
         for (int k = 0; k < 5; ++k) dY[k] += __shfl_xor(dY[k], o, 64);
       }
-      if (j == 0 && e < E) {
-        float* pp = part + ((size_t)ct * E + e) * kQPart;
-        pp[0] = dd;
+      if (j == 0) {
+        if constexpr (hf == 0) {
+          Pl[er][0] = dd;
 #pragma unroll
-        for (int k = 0; k < 5; ++k) pp[1 + k] = dY[k];
+          for (int k = 0; k < 5; ++k) Pl[er][1 + k] = dY[k];
+        } else if (e < E) {
+          float* pp = part + ((size_t)ct * E + e) * kQPart;
+          pp[0] = Pl[er][0] + dd;
+#pragma unroll
+          for (int k = 0; k < 5; ++k) pp[1 + k] = Pl[er][1 + k] + dY[k];
+        }
       }
     }
-  }
-  __syncthreads();
-
-  // phase 2: channel cc of the column tile, m-rows of the degree split between the two thread halves
-  const int64_t nv = e_lim - e0;
-  const int n_valid = nv <= 0 ? 0 : (nv < kGM ? (int)nv : kGM);
-  const int cc = t & (kGN - 1), grp = t >> 7;
-  const int M = 2 * l + 1, mh = (M + 1) / 2;
-  const int m0 = grp ? mh : 0, m1 = grp ? M : mh;
-  if (m0 < m1 && n_valid > 0) {
-    if (l == 0) qk_bwd_rows<0>(A, D, Ys, rows, n_valid, e0, et, cb, cc, m0, m1, side, dxd);
-    else if (l == 1) qk_bwd_rows<1>(A, D, Ys, rows, n_valid, e0, et, cb, cc, m0, m1, side, dxd);
-    else qk_bwd_rows<2>(A, D, Ys, rows, n_valid, e0, et, cb, cc, m0, m1, side, dxd);
-  }
+    __syncthreads();
+    // phase 2: channel cd of the half, m-rows mg and mg + 4 of the degree
+    const int cd = t & 63, mg = t >> 6;
+    if (mg < 2 * l + 1 && n_valid > 0) {
+      if (l == 0) qk_bwd_rows<0>(A, D, Ys, rows, n_valid, e0, et, cd, ch + cd, mg, side, dxd);
+      else if (l == 1) qk_bwd_rows<1>(A, D, Ys, rows, n_valid, e0, et, cd, ch + cd, mg, side, dxd);
+      else qk_bwd_rows<2>(A, D, Ys, rows, n_valid, e0, et, cd, ch + cd, mg, side, dxd);
+    }
+  };
+  run_half(std::integral_constant<int, 0>{});
+  run_half(std::integral_constant<int, 1>{});
 }
 
 // Rows of dL/dxd that the tiles did not write: atoms without edges get zeros, rows that cross a tile boundary
