@@ -61,6 +61,33 @@ struct GateOp {
   float k1, k2;
 };
 
+// Epilogue of a tile: C = acc (+ bias) (+ R), fp32 or bf16 (rounded once).
+__device__ __forceinline__ void gemm_store(const e2v2_gemm_args& G, int bi, int nt, int row0, int wv, int lane,
+                                           const floatx16 (&acc)[4]) {
+  const bool with_bias = G.bias && bi < G.bias_batches;
+  float* cb = static_cast<float*>(G.c) + (G.c_bf16 ? 0 : (int64_t)bi * G.c_bs);
+  __bf16* cbh = static_cast<__bf16*>(G.c) + (G.c_bf16 ? (int64_t)bi * G.c_bs : 0);
+  const float* rb = G.r ? G.r + (int64_t)bi * G.r_bs : nullptr;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int col = nt * kGN + 32 * j + (lane & 31);
+    const float bv = with_bias ? G.bias[(int64_t)bi * G.bias_bs + col] : 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + wv * 32 + acc_row(r, lane);
+      if (row < G.m) {
+        float v = acc[j][r];
+        if (with_bias) v += bv;
+        if (rb) v += rb[(size_t)row * G.ldr + col];
+        if (G.c_bf16)
+          cbh[(size_t)row * G.ldc + col] = (__bf16)v;
+        else
+          cb[(size_t)row * G.ldc + col] = v;
+      }
+    }
+  }
+}
+
 // One 128 x 128 output tile (batch-major, then row tile, then column tile).  kP operand pieces; kAB: A is
 // bf16 in memory (G.a_bf16); C is written as bf16 when G.c_bf16 (rounded once, from the fp32 sum).
 template <int kP, bool kAB, bool kGate>
@@ -139,38 +166,47 @@ __device__ __forceinline__ void gemm_tile(const e2v2_gemm_args& G, int tile, cha
         },
         acc);
 
-  // epilogue: C = acc (+ bias) (+ R)
-  const bool with_bias = G.bias && bi < G.bias_batches;
-  float* cb = static_cast<float*>(G.c) + (G.c_bf16 ? 0 : (int64_t)bi * G.c_bs);
-  __bf16* cbh = static_cast<__bf16*>(G.c) + (G.c_bf16 ? (int64_t)bi * G.c_bs : 0);
-  const float* rb = G.r ? G.r + (int64_t)bi * G.r_bs : nullptr;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = nt * kGN + 32 * j + (lane & 31);
-    const float bv = with_bias ? G.bias[(int64_t)bi * G.bias_bs + col] : 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = row0 + wv * 32 + acc_row(r, lane);
-      if (row < G.m) {
-        float v = acc[j][r];
-        if (with_bias) v += bv;
-        if (rb) v += rb[(size_t)row * G.ldr + col];
-        if (G.c_bf16)
-          cbh[(size_t)row * G.ldc + col] = (__bf16)v;
-        else
-          cb[(size_t)row * G.ldc + col] = v;
-      }
-    }
-  }
+  gemm_store(G, bi, nt, row0, wv, lane, acc);
 }
 
-template <int kP, bool kAB>
-__global__ __launch_bounds__(kGT, 3) void k_gemm_s3(e2v2_gemm_args G) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(kP, kAB)];
+// One tile of an fp32-A GEMM on kloop_r (A into registers two stages ahead, B through three LDS buffers of
+// 12 KB (kP = 3): 36 KB and at most 128 VGPRs, four workgroups per CU).
+template <int kP>
+__device__ __forceinline__ void gemm_tile_r(const e2v2_gemm_args& G, int tile) {
+  constexpr int BB = b_stage_bytes(kP);
+  __shared__ __attribute__((aligned(16))) char B0[BB];
+  __shared__ __attribute__((aligned(16))) char B1[BB];
+  __shared__ __attribute__((aligned(16))) char B2[BB];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n_mt = (G.m + kGM - 1) / kGM, n_nt = G.n / kGN;
+  const int nt = tile % n_nt, mt = (tile / n_nt) % n_mt, bi = tile / (n_nt * n_mt);
+  const int row0 = mt * kGM, nks = G.k / kGK;
+  const __amdgpu_buffer_rsrc_t ar =
+      rows_rsrc(static_cast<const float*>(G.a) + (int64_t)bi * G.a_bs, row0, G.m, (int)G.lda);
+  const __amdgpu_buffer_rsrc_t br = b_rsrc<kP>(G.b, G.widx[bi], n_nt, nt, nks);
+  const uint32_t aoff = (uint32_t)((wv * 32 + (lane & 31)) * (int)G.lda + 8 * (lane >> 5)) * 4u;
+  floatx16 acc[4];
+  kloop_r<kP>(B0, B1, B2, nks, lane,
+              [&](int ks, char* Bs) { load_b<kP>(br, ks, Bs, wv, lane); },
+              [&](int ks, floatx4 (&x)[2]) { load_a_regs(ar, aoff, ks, x); }, acc);
+  gemm_store(G, bi, nt, row0, wv, lane, acc);
+}
+
+// fp32 A (kP = 3, or 1 in the bf16 mode with an fp32 operand)
+template <int kP>
+__global__ __launch_bounds__(kGT, 4) void k_gemm_s3(e2v2_gemm_args G) {
   const int n_tiles = gemm_tiles(G);
   const int tile = xcd_row(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
-  gemm_tile<kP, kAB, false>(G, tile, lds, GateOp{});
+  gemm_tile_r<kP>(G, tile);
+}
+// bf16 A (the bf16 mode), on kloop
+__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_abf(e2v2_gemm_args G) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(1, true)];
+  const int n_tiles = gemm_tiles(G);
+  const int tile = xcd_row(blockIdx.x, n_tiles);
+  if (tile >= n_tiles) return;
+  gemm_tile<1, true, false>(G, tile, lds, GateOp{});
 }
 
 template <int kP>
@@ -195,16 +231,28 @@ struct GemmGroups {
   int n;
 };
 
-template <int kP, bool kAB>
-__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp(GemmGroups P) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(kP, kAB)];
+template <int kP>
+__global__ __launch_bounds__(kGT, 4) void k_gemm_s3_grp(GemmGroups P) {
   const int b = blockIdx.x;
 #pragma unroll
   for (int gi = 0; gi < kGGroups; ++gi) {
     if (gi < P.n && b >= P.block0[gi] && b < P.block0[gi + 1]) {
       const int n_tiles = gemm_tiles(P.g[gi]);
       const int tile = xcd_row(b - P.block0[gi], n_tiles);
-      if (tile < n_tiles) gemm_tile<kP, kAB, false>(P.g[gi], tile, lds, GateOp{});
+      if (tile < n_tiles) gemm_tile_r<kP>(P.g[gi], tile);
+      return;
+    }
+  }
+}
+__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp_abf(GemmGroups P) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(1, true)];
+  const int b = blockIdx.x;
+#pragma unroll
+  for (int gi = 0; gi < kGGroups; ++gi) {
+    if (gi < P.n && b >= P.block0[gi] && b < P.block0[gi + 1]) {
+      const int n_tiles = gemm_tiles(P.g[gi]);
+      const int tile = xcd_row(b - P.block0[gi], n_tiles);
+      if (tile < n_tiles) gemm_tile<1, true, false>(P.g[gi], tile, lds, GateOp{});
       return;
     }
   }
@@ -490,11 +538,11 @@ E2V2_API int e2v2_gemm_s3(const e2v2_gemm_args* g, hipStream_t s) {
   if (G.m == 0) return 0;
   const dim3 grid(xcd_grid(host_tiles(G)));
   if (G.pieces == 3)
-    hipLaunchKernelGGL((k_gemm_s3<3, false>), grid, dim3(kGT), 0, s, G);
+    hipLaunchKernelGGL((k_gemm_s3<3>), grid, dim3(kGT), 0, s, G);
   else if (G.a_bf16)
-    hipLaunchKernelGGL((k_gemm_s3<1, true>), grid, dim3(kGT), 0, s, G);
+    hipLaunchKernelGGL(k_gemm_s3_abf, grid, dim3(kGT), 0, s, G);
   else
-    hipLaunchKernelGGL((k_gemm_s3<1, false>), grid, dim3(kGT), 0, s, G);
+    hipLaunchKernelGGL((k_gemm_s3<1>), grid, dim3(kGT), 0, s, G);
   E2V2_LAUNCHED("k_gemm_s3");
   return 0;
 }
@@ -543,11 +591,11 @@ E2V2_API int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hi
   if (P.block0[n_groups] == 0) return 0;
   const dim3 grid(P.block0[n_groups]);
   if (groups[0].pieces == 3)
-    hipLaunchKernelGGL((k_gemm_s3_grp<3, false>), grid, dim3(kGT), 0, s, P);
+    hipLaunchKernelGGL((k_gemm_s3_grp<3>), grid, dim3(kGT), 0, s, P);
   else if (groups[0].a_bf16)
-    hipLaunchKernelGGL((k_gemm_s3_grp<1, true>), grid, dim3(kGT), 0, s, P);
+    hipLaunchKernelGGL(k_gemm_s3_grp_abf, grid, dim3(kGT), 0, s, P);
   else
-    hipLaunchKernelGGL((k_gemm_s3_grp<1, false>), grid, dim3(kGT), 0, s, P);
+    hipLaunchKernelGGL((k_gemm_s3_grp<1>), grid, dim3(kGT), 0, s, P);
   E2V2_LAUNCHED("k_gemm_s3_grp");
   return 0;
 }

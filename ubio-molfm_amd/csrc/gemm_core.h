@@ -2,6 +2,8 @@
 // three-piece split of eight fp32 values, the LDS-direct operand loads and slot swizzles, and the
 // pipelined K loop.  The scheme itself is described at the top of gemm.hip.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/e2v2.h"
 
@@ -190,6 +192,87 @@ __device__ __forceinline__ void kloop(const char* lds, int stage_bytes, int nks,
     pieces(f);
   }
 }
+
+// The K loop of the fp32-A GEMMs whose A rows belong to one wavefront each (a wavefront's 32 rows are read by
+// no other): A goes from memory straight into registers (load_a(ks, x): this lane's eight values of stage ks,
+// row 32 wv + lane % 32, k 8 (lane / 32) .. +7), two stages ahead in a ring of three; the kP B pieces go
+// through three LDS buffers (B0, B1, B2: separate objects, so that the compiler's waits for the LDS-direct
+// loads of one buffer do not hold the reads of another), filled by load_b(ks, buffer) two stages ahead.  Per
+// stage: wait for the stage's own loads (vmcnt: the next stage's kP + 2 may stay in flight), one barrier
+// (every wavefront's share of the stage has landed and every wavefront is done with the buffer of stage
+// ks - 1, which the loads of stage ks + 2 then fill), the B fragments from LDS, the split of A, the MFMAs.
+// The steady state issues a stage's loads in every step (no branch between the loads and the waits); the
+// last stages run with the loads past the end left out.  The products and their order are those of kloop.
+template <int kP, typename LoadB, typename LoadA>
+__device__ __forceinline__ void kloop_r(char* B0, char* B1, char* B2, int nks, int lane, LoadB&& load_b_,
+                                        LoadA&& load_a_, floatx16 (&acc)[4]) {
+  static_assert(kP == 1 || kP == 3, "one or three operand pieces");
+  const int h = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+  floatx4 av[3][2];
+  auto load = [&](int ks, auto slot) {
+    constexpr int sl = decltype(slot)::value;
+    load_b_(ks, sl == 0 ? B0 : sl == 1 ? B1 : B2);
+    load_a_(ks, av[sl]);
+  };
+  auto step = [&](int ks, auto slot, auto steady) {
+    constexpr int sl = decltype(slot)::value, sl2 = (sl + 2) % 3;
+    constexpr bool kU = decltype(steady)::value;
+    // s_waitcnt immediate (gfx9): vmcnt in bits 3:0 (and 15:14), expcnt 6:4 and lgkmcnt 11:8 at their
+    // maxima (no wait).  Per stage a wavefront issues kP LDS-direct B loads and two A loads.
+    if (kU || ks + 1 < nks) __builtin_amdgcn_s_waitcnt(0x0F70 | (kP + 2));   // vmcnt(kP + 2)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                                // vmcnt(0)
+    // a plain s_barrier: __syncthreads()'s release fence would also wait for the loads of stage ks + 1
+    asm volatile("s_barrier" ::: "memory");
+    if (kU || ks + 2 < nks) load(ks + 2, std::integral_constant<int, sl2>{});
+    const bf16x8* Bs = reinterpret_cast<const bf16x8*>(sl == 0 ? B0 : sl == 1 ? B1 : B2);
+    bf16x8 b[kP][4];
+#pragma unroll
+    for (int p = 0; p < kP; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[p][j] = Bs[p * kGBg + b_slot(32 * j + (lane & 31), h)];
+    bf16x8 a[kP];
+    split_pieces<kP>(av[sl][0], av[sl][1], a);
+    if constexpr (kP == 3) {
+      constexpr int kPa[6] = {0, 1, 2, 0, 1, 0}, kPb[6] = {0, 0, 0, 1, 1, 2};
+#pragma unroll
+      for (int q = 0; q < 6; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kPa[q]], b[kPb[q]][j], acc[j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0][j], acc[j], 0, 0, 0);
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  load(0, I0{});
+  if (nks > 1) load(1, I1{});
+  int ks = 0;
+  for (; ks + 5 <= nks; ks += 3) {   // every step here issues stage ks + 2 <= nks - 1
+    step(ks, I0{}, std::true_type{});
+    step(ks + 1, I1{}, std::true_type{});
+    step(ks + 2, I2{}, std::true_type{});
+  }
+  for (; ks < nks; ks += 3) {
+    step(ks, I0{}, std::false_type{});
+    if (ks + 1 < nks) step(ks + 1, I1{}, std::false_type{});
+    if (ks + 2 < nks) step(ks + 2, I2{}, std::false_type{});
+  }
+}
+// This lane's eight A values of stage ks from a buffer resource over the tile's rows (rows past m read as
+// zero): byte offset aoff of the lane's row and k 8 (lane / 32), plus 64 bytes per stage.
+__device__ __forceinline__ void load_a_regs(__amdgpu_buffer_rsrc_t r, uint32_t aoff, int ks, floatx4 (&x)[2]) {
+  const uint32_t o = aoff + (uint32_t)ks * (kGK * 4u);
+  x[0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
+  x[1] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, o + 16u, 0, 0));
+}
+constexpr int b_stage_bytes(int kP) { return 16 * kP * kGBg; }
 
 }  // namespace
 }  // namespace e2v2
