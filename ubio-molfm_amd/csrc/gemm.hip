@@ -192,21 +192,23 @@ __device__ __forceinline__ void gemm_tile_r(const e2v2_gemm_args& G, int tile) {
   gemm_store(G, bi, nt, row0, wv, lane, acc);
 }
 
-// fp32 A (kP = 3, or 1 in the bf16 mode with an fp32 operand)
-template <int kP>
+// fp32 A, three pieces
 __global__ __launch_bounds__(kGT, 4) void k_gemm_s3(e2v2_gemm_args G) {
   const int n_tiles = gemm_tiles(G);
   const int tile = xcd_row(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
-  gemm_tile_r<kP>(G, tile);
+  gemm_tile_r<3>(G, tile);
 }
-// bf16 A (the bf16 mode), on kloop
-__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_abf(e2v2_gemm_args G) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(1, true)];
+// one piece (the bf16 mode), A fp32 or bf16 (kAB), on kloop: with one MFMA product per stage these GEMMs are
+// bound by their operand and output traffic, and the two-buffer loop at up to five workgroups per CU was
+// measured faster for an fp32 A than kloop_r (55.8 against 64.1 us per call at cfg 4)
+template <bool kAB>
+__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_p1(e2v2_gemm_args G) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(1, kAB)];
   const int n_tiles = gemm_tiles(G);
   const int tile = xcd_row(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
-  gemm_tile<1, true, false>(G, tile, lds, GateOp{});
+  gemm_tile<1, kAB, false>(G, tile, lds, GateOp{});
 }
 
 template <int kP>
@@ -231,7 +233,6 @@ struct GemmGroups {
   int n;
 };
 
-template <int kP>
 __global__ __launch_bounds__(kGT, 4) void k_gemm_s3_grp(GemmGroups P) {
   const int b = blockIdx.x;
 #pragma unroll
@@ -239,20 +240,21 @@ __global__ __launch_bounds__(kGT, 4) void k_gemm_s3_grp(GemmGroups P) {
     if (gi < P.n && b >= P.block0[gi] && b < P.block0[gi + 1]) {
       const int n_tiles = gemm_tiles(P.g[gi]);
       const int tile = xcd_row(b - P.block0[gi], n_tiles);
-      if (tile < n_tiles) gemm_tile_r<kP>(P.g[gi], tile);
+      if (tile < n_tiles) gemm_tile_r<3>(P.g[gi], tile);
       return;
     }
   }
 }
-__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp_abf(GemmGroups P) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(1, true)];
+template <bool kAB>
+__global__ __launch_bounds__(kGT, 3) void k_gemm_s3_grp_p1(GemmGroups P) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * g_stage_bytes(1, kAB)];
   const int b = blockIdx.x;
 #pragma unroll
   for (int gi = 0; gi < kGGroups; ++gi) {
     if (gi < P.n && b >= P.block0[gi] && b < P.block0[gi + 1]) {
       const int n_tiles = gemm_tiles(P.g[gi]);
       const int tile = xcd_row(b - P.block0[gi], n_tiles);
-      if (tile < n_tiles) gemm_tile<1, true, false>(P.g[gi], tile, lds, GateOp{});
+      if (tile < n_tiles) gemm_tile<1, kAB, false>(P.g[gi], tile, lds, GateOp{});
       return;
     }
   }
@@ -538,11 +540,11 @@ E2V2_API int e2v2_gemm_s3(const e2v2_gemm_args* g, hipStream_t s) {
   if (G.m == 0) return 0;
   const dim3 grid(xcd_grid(host_tiles(G)));
   if (G.pieces == 3)
-    hipLaunchKernelGGL((k_gemm_s3<3>), grid, dim3(kGT), 0, s, G);
+    hipLaunchKernelGGL(k_gemm_s3, grid, dim3(kGT), 0, s, G);
   else if (G.a_bf16)
-    hipLaunchKernelGGL(k_gemm_s3_abf, grid, dim3(kGT), 0, s, G);
+    hipLaunchKernelGGL((k_gemm_s3_p1<true>), grid, dim3(kGT), 0, s, G);
   else
-    hipLaunchKernelGGL((k_gemm_s3<1>), grid, dim3(kGT), 0, s, G);
+    hipLaunchKernelGGL((k_gemm_s3_p1<false>), grid, dim3(kGT), 0, s, G);
   E2V2_LAUNCHED("k_gemm_s3");
   return 0;
 }
@@ -591,11 +593,11 @@ E2V2_API int e2v2_gemm_s3_grouped(const e2v2_gemm_args* groups, int n_groups, hi
   if (P.block0[n_groups] == 0) return 0;
   const dim3 grid(P.block0[n_groups]);
   if (groups[0].pieces == 3)
-    hipLaunchKernelGGL((k_gemm_s3_grp<3>), grid, dim3(kGT), 0, s, P);
+    hipLaunchKernelGGL(k_gemm_s3_grp, grid, dim3(kGT), 0, s, P);
   else if (groups[0].a_bf16)
-    hipLaunchKernelGGL(k_gemm_s3_grp_abf, grid, dim3(kGT), 0, s, P);
+    hipLaunchKernelGGL((k_gemm_s3_grp_p1<true>), grid, dim3(kGT), 0, s, P);
   else
-    hipLaunchKernelGGL((k_gemm_s3_grp<1>), grid, dim3(kGT), 0, s, P);
+    hipLaunchKernelGGL((k_gemm_s3_grp_p1<false>), grid, dim3(kGT), 0, s, P);
   E2V2_LAUNCHED("k_gemm_s3_grp");
   return 0;
 }
