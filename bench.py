@@ -164,16 +164,18 @@ KERNELS_OF = {"e2v2_attn_fwd": [("k_attn_fwd_sl", 1)],
 
 def expanded_nodes(nl) -> int:
     """M of the reference formulation: the real atoms plus the distinct periodic
-    images (atom, nonzero cell shift) that carry edges."""
+    images (atom, nonzero cell shift) that carry edges.  Only the real edges
+    (row_ptr[N] of them) are read: a capacity build's slots past them hold no edge."""
     import numpy as np
     import torch
     N = nl.n_atoms
-    if nl.n_edges == 0:
+    e_real = int(nl.row_ptr[N]) if nl.n_edges else 0
+    if e_real == 0:
         return N
     zero = torch.as_tensor(np.asarray(nl.shift_ptr[:-1], np.int64), device=nl.col.device)
-    sidx = nl.shift_idx.long()
+    sidx = nl.shift_idx[:e_real].long()
     img = ~torch.isin(sidx, zero)
-    keys = sidx[img] * N + nl.col.long()[img]
+    keys = sidx[img] * N + nl.col[:e_real].long()[img]
     return N + int(torch.unique(keys).numel())
 
 

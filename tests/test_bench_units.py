@@ -113,5 +113,27 @@ def test_expanded_nodes_counts_distinct_images():
     from types import SimpleNamespace
     col = torch.tensor([1, 1, 2, 0, 1, 2, 2], dtype=torch.int32)
     sidx = torch.tensor([0, 3, 3, 0, 3, 5, 5], dtype=torch.int32)
-    nl = SimpleNamespace(n_atoms=3, n_edges=7, col=col, shift_idx=sidx, shift_ptr=np.array([0, 27]))
+    nl = SimpleNamespace(n_atoms=3, n_edges=7, col=col, shift_idx=sidx, shift_ptr=np.array([0, 27]),
+                         row_ptr=torch.tensor([0, 2, 5, 7], dtype=torch.int32))
     assert bench.expanded_nodes(nl) == 3 + 3          # (3,1), (3,2), (5,2)
+
+
+def test_expanded_nodes_counts_real_edges_only():
+    """M = N + distinct (atom, nonzero shift) images over the real edges; the slots of
+    a capacity build past row_ptr[N] hold stale values and must not count."""
+    import types
+
+    import numpy as np
+    import torch
+    N = 4
+    # two graphs' shift tables: rows 0..2 for graph 0 (row 0 the zero shift), 3..4 for graph 1
+    shift_ptr = np.array([0, 3, 5])
+    row_ptr = torch.tensor([0, 2, 3, 5, 6], dtype=torch.int32)
+    col = torch.tensor([1, 1, 0, 3, 3, 2] + [0, 1, 2, 3], dtype=torch.int32)
+    sidx = torch.tensor([0, 1, 2, 4, 4, 3] + [1, 2, 1, 4], dtype=torch.int32)
+    nl = types.SimpleNamespace(n_atoms=N, n_edges=10, row_ptr=row_ptr, col=col, shift_idx=sidx,
+                               shift_ptr=shift_ptr)
+    # real images: (1, shift 1), (0, shift 2), (3, shift 4); shifts 0 and 3 are zero shifts
+    assert bench.expanded_nodes(nl) == N + 3
+    nl.n_edges = 0
+    assert bench.expanded_nodes(nl) == N
