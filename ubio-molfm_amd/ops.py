@@ -476,6 +476,9 @@ class QKdotGateFn(torch.autograd.Function):
             raise ValueError(f"QKdotGateFn: Y {tuple(Y.shape)}, xd {tuple(xd.shape)} for {E} edges and {N} atoms")
         dist = dist.float().contiguous()
         bias = bias.float().contiguous()
+        if dist.shape != (E,) or bias.shape != (128,) or atom_type.dtype != torch.int32 or atom_type.numel() < N:
+            raise ValueError(f"QKdotGateFn: dist {tuple(dist.shape)} (needs [{E}]), bias {tuple(bias.shape)} "
+                             f"(needs [128]), atom_type {atom_type.dtype} [{atom_type.numel()}] (int32, {N} atoms)")
         args = _qkdot_args(nl, atom_type, table, dist, Y, xd, packs[0].pieces)
         gate = torch.empty(E, 128, dtype=torch.float32, device=dist.device)
         _lib.call("e2v2_qkdot_gate_fwd", _lib.C.byref(args), _p(packs[0].buf), _p(bias), _p(gate), _stream(dist))
