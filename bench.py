@@ -313,15 +313,74 @@ def cpu_baseline(pkg, config: int = 4, sample: str = "auto"):
     return out
 
 
+def train_line(args, dev):
+    """One JSON line for force-training steps: the model in training mode (the backbone composed from the
+    second-order op-level kernels, forces taken with create_graph=True), loss = mean e^2 / atom + mean |F|^2
+    (zero targets: the work, not the fit, is measured), backward to every parameter through the forces,
+    one Adam step; positions fixed, the neighbour list rebuilt inside every forward as in training."""
+    import numpy as np
+    import torch
+    from ubio_molfm_amd import model, neighbors, systems
+    torch.manual_seed(0)
+    margs = model.default_args()
+    margs.backbone_config.update(tp_type=args.tp_type, with_cluster=args.with_cluster)
+    m = model.MolfmAtomic(margs).to(dev).train()
+    sysd = systems.CONFIGS[args.config]()
+    N = len(sysd["pos"])
+    bd = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in systems.to_padded(sysd).items()}
+    mask = bd["atom_masks"]
+    nl = neighbors.build_neighbors(torch.as_tensor(sysd["pos"], device=dev), sysd["graph_ptr"], sysd["cell"],
+                                   sysd["pbc"], 6.0)
+    E = nl.n_edges
+    opt = torch.optim.Adam(m.parameters(), lr=1e-5)
+
+    def step():
+        b = dict(bd)
+        b["pos"] = bd["pos"].clone().requires_grad_(True)
+        res = m(b)
+        e, f = res["pred_energy"], res["pred_forces"]
+        loss = (e / mask.sum(-1)).pow(2).mean() + f[mask].pow(2).sum(-1).mean()
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = dt / args.steps * 1e3
+    print(json.dumps({
+        "metric": "force-training steps: edges/s (energy + forces with create_graph + parameter backward + Adam)",
+        "value": E * args.steps / dt, "unit": "edges/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded generator, random-init weights, zero targets)",
+        "config": {"workload": f"configs[{args.config - 1}] {sysd['name']}: {N} atoms, rc 6 A, force training "
+                               f"(model.train(): second-order composition), fixed positions",
+                   "atoms": N, "edges_per_step": E, "layers": 4, "parallelism": "single GPU",
+                   "tp_type": args.tp_type, "with_cluster": args.with_cluster},
+        "mode": "train", "atom_steps_per_s": N * args.steps / dt, "final_loss": float(loss),
+        "peak_memory_gb": torch.cuda.max_memory_allocated(dev) / 1e9,
+        "roofline": None, "cpu_baseline": None}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=4)
-    ap.add_argument("--mode", choices=["md", "eval"], default=None,
+    ap.add_argument("--mode", choices=["md", "eval", "train"], default=None,
                     help="md: NVE velocity-Verlet steps (default for configs 1-4); eval: repeated energy+force "
-                         "evaluations at fixed positions (default for config 5)")
+                         "evaluations at fixed positions (default for config 5); train: force-training steps "
+                         "(energy, forces with create_graph, loss on both, backward to every parameter, one Adam "
+                         "step) of the model in training mode at fixed positions (a separate line, not the "
+                         "headline metric)")
     ap.add_argument("--dtype", choices=["fp32", "bf16"], default=None,
                     help="GEMM operand precision (default: bf16 for configs 2 and 5, as they are specified, "
                          "else fp32); accumulation, activations and reductions are fp32 in both")
@@ -360,6 +419,9 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.mode == "train":
+        train_line(args, dev)
+        return
     torch.manual_seed(0)
     margs = model.default_args()
     margs.backbone_config.update(tp_type=args.tp_type, with_cluster=args.with_cluster)
