@@ -35,23 +35,65 @@ __device__ __forceinline__ bool slot_ok(const e2v2_segments& S, int c, int e) {
   return c >= 0 && c < S.n_cols && e >= 0 && (int64_t)e < S.n_edges;
 }
 
+// Slots of one row staged in LDS (edge id and partner row, -1 for a skipped slot) when the row has at most
+// kSegStage of them; longer rows read the slot arrays directly.
+constexpr int kSegStage = 512;
+
+__device__ __forceinline__ bool stage_row(const e2v2_segments& S, const SegRow& R, bool with_col, int* se, int* sc) {
+  const int np = R.p1 - R.p0;
+  if (np > kSegStage) return false;
+  for (int t = threadIdx.x; t < np; t += kSegThreads) {
+    const int p = R.p0 + t;
+    const int e = S.alpha_index[p], c = with_col ? S.col_index[p] : 0;
+    const bool ok = e >= 0 && (int64_t)e < S.n_edges && (!with_col || (c >= 0 && c < S.n_cols));
+    se[t] = ok ? e : -1;
+    sc[t] = ok ? c : 0;
+  }
+  __syncthreads();
+  return true;
+}
+
 // out[alpha_index[p], h] = sum_d A[r, h, d] B[col_index[p], h, d] for the slots p of row r
 __global__ __launch_bounds__(kSegThreads) void k_seg_dot(e2v2_segments S, const float* __restrict__ A, int64_t sa_r,
                                                          int64_t sa_h, int64_t sa_d, const float* __restrict__ B,
                                                          int64_t sb_r, int64_t sb_h, int64_t sb_d, int H, int D,
                                                          float* __restrict__ out, int64_t so_e, int64_t so_h) {
+  __shared__ int se[kSegStage], sc[kSegStage];
   const int r = blockIdx.x;
   const SegRow R = seg_row(S, r);
+  const bool staged = stage_row(S, R, true, se, sc);
   const unsigned n = (unsigned)(R.p1 - R.p0) * (unsigned)H;
   const float* a = A + (int64_t)r * sa_r;
+  // unit-stride rows of 16-byte aligned groups of four: float4 loads (the same products, summed in d order)
+  const bool v4 = sa_d == 1 && sb_d == 1 && (D & 3) == 0 && ((sa_r | sa_h | sb_r | sb_h) & 3) == 0 &&
+                  (((uintptr_t)A | (uintptr_t)B) & 15) == 0;
   for (unsigned idx = threadIdx.x; idx < n; idx += kSegThreads) {
-    const int p = R.p0 + (int)(idx / (unsigned)H), h = (int)(idx % (unsigned)H);
-    const int c = S.col_index[p], e = S.alpha_index[p];
-    if (!slot_ok(S, c, e)) continue;
+    const int k = (int)(idx / (unsigned)H), h = (int)(idx % (unsigned)H);
+    int c, e;
+    if (staged) {
+      e = se[k];
+      c = sc[k];
+      if (e < 0) continue;
+    } else {
+      const int p = R.p0 + k;
+      c = S.col_index[p];
+      e = S.alpha_index[p];
+      if (!slot_ok(S, c, e)) continue;
+    }
     const float* b = B + (int64_t)c * sb_r + (int64_t)h * sb_h;
     const float* ah = a + (int64_t)h * sa_h;
     float s = 0.f;
-    for (int d = 0; d < D; ++d) s = fmaf(ah[d * sa_d], b[d * sb_d], s);
+    if (v4) {
+      for (int d = 0; d < D; d += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(ah + d), y = *reinterpret_cast<const float4*>(b + d);
+        s = fmaf(x.x, y.x, s);
+        s = fmaf(x.y, y.y, s);
+        s = fmaf(x.z, y.z, s);
+        s = fmaf(x.w, y.w, s);
+      }
+    } else {
+      for (int d = 0; d < D; ++d) s = fmaf(ah[d * sa_d], b[d * sb_d], s);
+    }
     out[(int64_t)e * so_e + (int64_t)h * so_h] = s;
   }
 }
@@ -63,21 +105,51 @@ __global__ __launch_bounds__(kSegThreads) void k_seg_reduce(e2v2_segments S, con
                                                             int64_t sx_r, int64_t sx_h, int64_t sx_d, int H, int D,
                                                             bool h_fast, float* __restrict__ out, int64_t so_r,
                                                             int64_t so_h, int64_t so_d) {
+  __shared__ int se[kSegStage], sc[kSegStage];
   const int r = blockIdx.x;
   const SegRow R = seg_row(S, r);
+  const bool staged = stage_row(S, R, X != nullptr, se, sc);
+  const int np = R.p1 - R.p0;
   for (int idx = threadIdx.x; idx < H * D; idx += kSegThreads) {
     const int h = h_fast ? idx % H : idx / D, d = h_fast ? idx / H : idx % D;
+    const float* wh = W + (int64_t)h * sw_h;
+    const float* xh = X ? X + (int64_t)h * sx_h + (int64_t)d * sx_d : nullptr;
     float s = 0.f;
-    for (int p = R.p0; p < R.p1; ++p) {
-      const int e = S.alpha_index[p];
-      if (e < 0 || (int64_t)e >= S.n_edges) continue;
-      const float w = W[(int64_t)e * sw_e + (int64_t)h * sw_h];
-      if (X) {
-        const int c = S.col_index[p];
-        if (c < 0 || c >= S.n_cols) continue;
-        s = fmaf(w, X[(int64_t)c * sx_r + (int64_t)h * sx_h + (int64_t)d * sx_d], s);
-      } else {
-        s += w;
+    if (staged) {
+      // four slots' loads in flight at a time (a skipped slot loads nothing and adds nothing); the sum keeps
+      // slot order
+      int k = 0;
+      for (; k + 4 <= np; k += 4) {
+        int e[4];
+        float w[4], x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          e[u] = se[k + u];
+          w[u] = e[u] >= 0 ? wh[(int64_t)e[u] * sw_e] : 0.f;
+          x[u] = (xh && e[u] >= 0) ? xh[(int64_t)sc[k + u] * sx_r] : 1.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (e[u] >= 0) s = xh ? fmaf(w[u], x[u], s) : s + w[u];
+      }
+      for (; k < np; ++k) {
+        const int e = se[k];
+        if (e < 0) continue;
+        const float w = wh[(int64_t)e * sw_e];
+        s = xh ? fmaf(w, xh[(int64_t)sc[k] * sx_r], s) : s + w;
+      }
+    } else {
+      for (int p = R.p0; p < R.p1; ++p) {
+        const int e = S.alpha_index[p];
+        if (e < 0 || (int64_t)e >= S.n_edges) continue;
+        const float w = wh[(int64_t)e * sw_e];
+        if (X) {
+          const int c = S.col_index[p];
+          if (c < 0 || c >= S.n_cols) continue;
+          s = fmaf(w, xh[(int64_t)c * sx_r], s);
+        } else {
+          s += w;
+        }
       }
     }
     out[(int64_t)r * so_r + (int64_t)h * so_h + (int64_t)d * so_d] = s;
