@@ -62,7 +62,8 @@ def deg_compulsory(N, M, E, act=4):
 
 
 COMPULSORY = {"e2v2_attn_fwd": attn_fwd_compulsory, "e2v2_attn_bwd": attn_bwd_compulsory,
-              "e2v2_deg_fwd": deg_compulsory, "e2v2_deg_bwd": deg_compulsory}
+              "e2v2_deg_fwd": deg_compulsory, "e2v2_deg_bwd": deg_compulsory,
+              "e2v2_deg_hidden_fwd": deg_compulsory, "e2v2_deg_hidden_bwd": deg_compulsory}
 
 
 # Bytes the implementation's kernels read and write per launch, split into node / edge-list traffic
@@ -117,10 +118,35 @@ def deg_bwd_table_bytes(E):
     return 4.0 * E * 768 * 8
 
 
+# The degree embedding through the profiles' hidden channels (the model's path): 384 table channels instead of
+# 768, hs [9][N][144] written; the backward reads grad_h [9][N][128] and grad_s [9][N].  Its per-node GEMMs
+# (144 -> 256 and 256 -> 128 per m-row) are e2v2_gemm_s3 calls, its bias-column gradient e2v2_deg_bias_grad.
+DEG_HIDDEN_SLICES = 4   # 32 hidden channels of each profile per slice
+
+
+def deg_hidden_fwd_bytes(N, E, act=4):
+    return 4.0 * (DEG_HIDDEN_SLICES * E * 6 + N * 9 * 144) + deg_hidden_fwd_table_bytes(E)
+
+
+def deg_hidden_fwd_table_bytes(E):
+    return 4.0 * E * 384 * 6
+
+
+def deg_hidden_bwd_bytes(N, E, act=4):
+    S = DEG_HIDDEN_SLICES
+    return 4.0 * (S * E * 6 + N * 9 * 129 + S * E * 4 + S * E * 4 + E * 4) + deg_hidden_bwd_table_bytes(E)
+
+
+def deg_hidden_bwd_table_bytes(E):
+    return 4.0 * E * 384 * 8
+
+
 IMPL_BYTES = {"e2v2_attn_fwd": attn_fwd_bytes, "e2v2_attn_bwd": attn_bwd_bytes, "e2v2_deg_fwd": deg_fwd_bytes,
-              "e2v2_deg_bwd": deg_bwd_bytes}
+              "e2v2_deg_bwd": deg_bwd_bytes, "e2v2_deg_hidden_fwd": deg_hidden_fwd_bytes,
+              "e2v2_deg_hidden_bwd": deg_hidden_bwd_bytes}
 TABLE_BYTES = {"e2v2_attn_fwd": attn_fwd_table_bytes, "e2v2_attn_bwd": attn_bwd_table_bytes,
-               "e2v2_deg_fwd": deg_fwd_table_bytes, "e2v2_deg_bwd": deg_bwd_table_bytes}
+               "e2v2_deg_fwd": deg_fwd_table_bytes, "e2v2_deg_bwd": deg_bwd_table_bytes,
+               "e2v2_deg_hidden_fwd": deg_hidden_fwd_table_bytes, "e2v2_deg_hidden_bwd": deg_hidden_bwd_table_bytes}
 BYTES_OF = IMPL_BYTES
 
 
@@ -155,6 +181,9 @@ SPLIT_ENTRIES = ("e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3", "e2v2_gemm_s3", "
 KERNELS_OF = {"e2v2_attn_fwd": [("k_attn_fwd_sl", 1)],
               "e2v2_attn_bwd": [("k_attn_bwd_row_sl", 4), ("k_attn_bwd_col_grp", 4), ("k_edge_part_sum", 1)],
               "e2v2_deg_fwd": [("k_deg_fwd_sl", 1)], "e2v2_deg_bwd": [("k_deg_bwd_sl", 1), ("k_edge_part_sum", 1)],
+              "e2v2_deg_hidden_fwd": [("k_degh_fwd_sl", 1)],
+              "e2v2_deg_hidden_bwd": [("k_degh_bwd_sl", 1), ("k_edge_part_sum", 1)],
+              "e2v2_deg_bias_grad": [("k_deg_bias_grad", 1)],
               "e2v2_nbr_count": [("k_nbr_count", 1)],
               "e2v2_qk_proj_fwd": [("k_qk_proj_fwd", 1)], "e2v2_qk_proj_bwd": [("k_qk_proj_bwd", 1)],
               "e2v2_qk_proj_fwd_s3": [("k_qk_s3_fwd", 1)], "e2v2_qk_proj_bwd_s3": [("k_qk_s3_bwd", 1)],
@@ -458,7 +487,8 @@ def main():
     # per-kernel durations: HIP events around each library call of a few more steps run eagerly (the
     # kernels a graph replays are the same launches; replays do not pass through the Python wrappers)
     timer = _lib.KernelTimer(["e2v2_attn_fwd", "e2v2_attn_bwd",
-                              "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_nbr_count", "e2v2_nbr_fill",
+                              "e2v2_deg_fwd", "e2v2_deg_bwd", "e2v2_deg_hidden_fwd", "e2v2_deg_hidden_bwd",
+                              "e2v2_deg_bias_grad", "e2v2_nbr_count", "e2v2_nbr_fill",
                               "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd", "e2v2_qk_proj_fwd_bf16",
                               "e2v2_qk_proj_bwd_bf16", "e2v2_qk_proj_fwd_s3", "e2v2_qk_proj_bwd_s3",
                               "e2v2_gemm_s3", "e2v2_gemm_s3_grouped", "e2v2_gemm_s3_gated",

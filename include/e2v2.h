@@ -286,6 +286,24 @@ int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset,
                             int32_t n_nodes, float h, const float* tab, int32_t nc, const e2v2_radial_layout* layout,
                             uint32_t* err, hipStream_t s);
 
+/* The same table of a profile's 128 hidden channels (the output of its second SiLU, the input of its last
+   Linear, module_utils.py:2159-2172), placed by the layout as channels o = 0..127: a profile's output is
+   W3 h + b3 of the hidden channels h, so a sum over edges of outputs times edge factors equals W3 times the
+   sum of hidden channels times the same factors plus b3 times the sum of the factors (the degree
+   embedding, e2v2_deg_hidden_fwd).  The check's errors (err as for e2v2_radial_table_check) are those of the
+   output W3 h~ + b3 formed in float64 from the interpolated h~ and h~', against the float64 output: the
+   same tolerances as a table of the outputs.  Degree-embedding layout (nc = 384, profiles l = 0, 1, 2):
+   hidden channel o of profile l at 96 (o / 32) + 32 l + o % 32, stored slice-major (four slices);
+   layout {col0 32 l, split 128, block 32, block_stride 96, split_stride 0, slice_width 96}. */
+int e2v2_radial_hidden_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                             const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
+                             int32_t n_nodes, float h, float* tab, int32_t nc, const e2v2_radial_layout* layout,
+                             hipStream_t s);
+int e2v2_radial_hidden_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                                   const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
+                                   int32_t n_nodes, float h, const float* tab, int32_t nc,
+                                   const e2v2_radial_layout* layout, uint32_t* err, hipStream_t s);
+
 /* Per-edge values of a "plain"-layout table ([pairs][n_nodes][4][nc], nc channels): out [E][nc] =
    f_c(dist[e]) for the pair (atom_type[edge_row[e]], atom_type[col[e]]), the quintic Hermite interpolant.
    Replaces the per-edge RadialProfile calls of the QKdot gates, rad_func_m0(x_edge) (e2former.py:278)
@@ -413,6 +431,21 @@ size_t e2v2_deg_bwd_workspace(int64_t n_edges);
    derivative from the table); workspace: e2v2_deg_bwd_workspace(E) bytes, 16-byte aligned */
 int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* ddvec, float* ddist, void* workspace,
                  size_t workspace_bytes, hipStream_t s);
+
+/* The degree embedding through the gbf_projs hidden channels (e2former.py:728-748 with the last Linear of
+   each profile, module_utils.py:2159-2172, moved past the sum over edges):
+     hs[m][i][k] = (1/avg) sum_e Y_m(e) p(e) h_l(m),k(e)   (k < 128),
+     hs[m][i][128] = (1/avg) sum_e Y_m(e) p(e),   hs[m][i][129..143] = 0,
+   hs [9][N][144] m-major; then x0[m] = hs[m] [W3_l | b3_l | 0]^T (a per-node GEMM, 144 -> 256) is the
+   output of e2v2_deg_fwd.  args.rtab is the hidden table (e2v2_radial_hidden_table, degree layout, nc 384)
+   and args.channels = 128. */
+int e2v2_deg_hidden_fwd(const e2v2_deg_args* args, float* hs, hipStream_t s);
+/* grad_h [9][N][128] = grad_x0[m] W3_l and grad_s [9][N] = grad_x0[m] . b3_l (unscaled: the kernel applies
+   1/avg) -> ddvec [E,3], ddist [E]; workspace: e2v2_deg_bwd_workspace(E) bytes, 16-byte aligned. */
+int e2v2_deg_hidden_bwd(const e2v2_deg_args* args, const float* grad_h, const float* grad_s, float* ddvec,
+                        float* ddist, void* workspace, size_t workspace_bytes, hipStream_t s);
+/* grad_s [9][n] = sum_c grad_x0[m][i][c] b3[l(m)][c] (grad_x0 [9][n][256] m-major, b3 [3][256]; fixed order). */
+int e2v2_deg_bias_grad(const float* grad_x0, const float* b3, int32_t n, float* grad_s, hipStream_t s);
 
 /* ---- per-node kernels (node layout m-major: x[9][N][256]) --------------- */
 /* rms_norm_sh: EquivariantRMSNormArraySphericalHarmonicsV2_BL

@@ -578,6 +578,53 @@ def test_degree_forward_backward(pkg, cuda):
         assert e < 1e-4, (k_, e)
 
 
+def test_degree_hidden_table_forward_backward(pkg, cuda):
+    """Degree embedding through the profiles' hidden channels (layout "degh":
+    kernel sums of the interpolated hidden channels, then the per-node split GEMM
+    with [W3 | b3], and in the backward the transposed GEMM and the bias column's
+    gradient) via ops.DegreeEmbedFn, against the float64 per-edge profiles; and
+    against the output-table kernels ("deg") on the same graph.  The hidden table
+    meets the output tolerances (1e-6 value, 1e-5 derivative) through its check."""
+    from ubio_molfm_amd import _lib, modules, ops
+    s, pos, nl = _graph(pkg, cuda, seed=5)
+    N, E = nl.n_atoms, nl.n_edges
+    rb = modules.GaussianSmearing(256, 6.0, 2.0)
+    profs = [_profile(20 + l, 768) for l in range(3)]
+    tgt, src = _embeddings(23, 300, 256)
+    nets64 = [copy.deepcopy(p_).double().net for p_ in profs]
+    assert all(float(n[6].bias.abs().max()) > 1e-3 for n in nets64)   # the bias column carries a term
+    tw, sw = tgt.weight.detach().double().clone(), src.weight.detach().double().clone()
+    type_z, slot = _types(pkg, cuda, s["Z"])
+    nets = [p_.to(cuda).net for p_ in profs]
+    tabh = ops.RadialTable(nets, tgt.to(cuda), src.to(cuda), rb.offset.to(cuda), rb.coeff, 6.0, type_z,
+                           layout="degh")
+    assert tabh.nc == 384 and tabh.value_err <= 1e-6 and tabh.deriv_err <= 1e-5, (tabh.value_err, tabh.deriv_err)
+    row = nl.edge_row.long().cpu(); col = nl.col.long().cpu()
+    Z = torch.as_tensor(np.asarray(s["Z"]))
+    leaves = [nl.dvec.cpu().double().requires_grad_(True), nl.dist.cpu().double().requires_grad_(True)]
+    coeff = float(np.float32(rb.coeff))
+    fea = torch.cat([mlp_ref(leaves[1], Z[row], Z[col], n64, tw, sw, rb.offset.double(), coeff) for n64 in nets64],
+                    dim=-1)
+    ref = deg_ref(leaves[0], leaves[1], row, fea, 23.01, 6.0, N)
+    G = torch.randn(N, 9, 256, generator=torch.Generator().manual_seed(9))
+    grads = torch.autograd.grad((ref * G.double()).sum(), leaves)
+    outs = {}
+    for lay, tab in (("degh", tabh), ("deg", ops.RadialTable(nets, tgt.to(cuda), src.to(cuda), rb.offset.to(cuda),
+                                                              rb.coeff, 6.0, type_z, layout="deg"))):
+        dvec = nl.dvec.clone().requires_grad_(True); dist = nl.dist.clone().requires_grad_(True)
+        x0 = ops.DegreeEmbedFn.apply(dvec, dist, nl, slot, tab, 23.01, 6.0)
+        x0.backward(G.permute(1, 0, 2).contiguous().to(cuda))
+        outs[lay] = (x0.detach().permute(1, 0, 2), dvec.grad, dist.grad)
+        errs = dict(fwd=relerr(outs[lay][0], ref), dvec=relerr(dvec.grad, grads[0]), dist=relerr(dist.grad, grads[1]))
+        print(f"[deg {lay}] E={E} {errs}", flush=True)
+        assert errs["fwd"] < 2e-5, (lay, errs)
+        for k_, e in errs.items():
+            assert e < 1e-4, (lay, k_, e)
+    cross = [relerr(a_, b_.double().cpu()) for a_, b_ in zip(outs["degh"], outs["deg"])]
+    print(f"[deg degh vs deg] {cross}", flush=True)
+    assert max(cross) < 1e-4, cross
+
+
 def test_morton_keys(pkg, cuda):
     """e2v2_morton_keys against a numpy restatement (fp32 quantisation, 10-bit
     interleave), one graph and a ragged batch of three graphs."""

@@ -16,8 +16,9 @@ EXPORTS = [
     "e2v2_last_error", "e2v2_version", "e2v2_fill_i32", "e2v2_fill_f32", "e2v2_scan_i32",
     "e2v2_nbr_bin", "e2v2_nbr_count", "e2v2_nbr_count_noalloc", "e2v2_nbr_fill", "e2v2_nbr_cap", "e2v2_nbr_topk", "e2v2_csr_transpose", "e2v2_cluster_slots",
     "e2v2_morton_keys", "e2v2_radial_table_size", "e2v2_radial_table", "e2v2_radial_table_check",
+    "e2v2_radial_hidden_table", "e2v2_radial_hidden_table_check",
     "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_attn_bwd_workspace", "e2v2_deg_fwd", "e2v2_deg_bwd",
-    "e2v2_deg_bwd_workspace",
+    "e2v2_deg_bwd_workspace", "e2v2_deg_hidden_fwd", "e2v2_deg_hidden_bwd", "e2v2_deg_bias_grad",
     "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd",
     "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd", "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd",

@@ -11,8 +11,8 @@
 namespace e2v2 {
 
 int set_error(int code, const char* fmt, ...);
-// ddv[e] = sum_s part[s][e].xyz, dd[e] = sum_s part[s][e].w over 8 slices in slice order (deg.hip)
-int launch_edge_part_sum(const float* part, int64_t n_edges, float* ddv, float* dd, hipStream_t st);
+// ddv[e] = sum_s part[s][e].xyz, dd[e] = sum_s part[s][e].w over n_sl (<= 8) slices in slice order (deg.hip)
+int launch_edge_part_sum(const float* part, int64_t n_edges, float* ddv, float* dd, hipStream_t st, int n_sl = 8);
 
 #define E2V2_TRY_HIP(expr)                                                          \
   do {                                                                              \

@@ -18,6 +18,7 @@ namespace e2v2 {
 
 constexpr int kDC = 256;
 constexpr int kDegC = 3 * kDC;   // channels per table row: profiles l = 0, 1, 2
+constexpr int kDH = 128, kDHs = kDH + 16;   // hidden channels; row of hs: the hidden sums, the bias column, zeros
 
 // dY/du for u = (x, y, z) given dL/dY -> dL/du
 __device__ __forceinline__ void raw_sh2_bwd(float x, float y, float z, const float (&g)[9], float& gx, float& gy,
@@ -30,9 +31,11 @@ __device__ __forceinline__ void raw_sh2_bwd(float x, float y, float z, const flo
 
 __device__ __forceinline__ int l_of(int m) { return m == 0 ? 0 : (m < 4 ? 1 : 2); }
 
+template <bool kHid = false>
 __device__ __forceinline__ RadialTab make_deg_tab(const e2v2_deg_args& A) {
   RadialTab R;
-  R.tab = A.rtab; R.n_types = A.n_types; R.n_nodes = A.rtab_n; R.nc = kDegC; R.inv_h = 1.0f / A.rtab_h;
+  R.tab = A.rtab; R.n_types = A.n_types; R.n_nodes = A.rtab_n; R.nc = kHid ? 3 * kDH : kDegC;
+  R.inv_h = 1.0f / A.rtab_h;
   R.pair_slot = A.pair_slot;
   return R;
 }
@@ -44,17 +47,29 @@ __device__ __forceinline__ RadialTab make_deg_tab(const e2v2_deg_args& A) {
 // stored slice-major, [pairs][8][nodes][4][96], column 32 l + u holding channel
 // 32 s + u of profile l.  Lane (sub, q) = (lane / 8, lane % 8) owns channels
 // 32 s + 4 q .. + 3 (16-byte table loads) and the row's edges sub, sub + 8, ...
-constexpr int kDSl = 8, kDSlC = kDC / kDSl, kDRow = 3 * kDSlC, kDNode = 4 * kDRow;
+// The hidden-channel table (kHid: the profiles' 128 hidden channels) has four
+// slices of 32 channels per profile ([pairs][4][nodes][4][96]), slice s on the
+// XCDs s and s + 4, the same lane mapping.
+constexpr int kDSl = 8, kDSlC = kDC / kDSl;
+template <bool kHid>
+struct DegSl {
+  static constexpr int NS = kHid ? 4 : kDSl;             // slices
+  static constexpr int W = kDSlC;                         // channels of one profile per slice
+  static constexpr int Row = 3 * W, Node = 4 * Row;      // floats per table row / node of a slice
+  static constexpr int Q = W / 4, Sub = kWave / Q;       // lanes per edge, edges in flight per wavefront
+};
 
 // Four consecutive channels of one profile from rows r0 .. r0 + 2 at both nodes
 // (p: the profile's columns of the lower node): the quintic Hermite interpolant.
+template <int kRow>
 __device__ __forceinline__ floatx4 deg_interp(const float* p, const Hermite5& H, int r0) {
-  const floatx4 f0 = *reinterpret_cast<const floatx4*>(p + r0 * kDRow);
-  const floatx4 f1 = *reinterpret_cast<const floatx4*>(p + (r0 + 1) * kDRow);
-  const floatx4 f2 = *reinterpret_cast<const floatx4*>(p + (r0 + 2) * kDRow);
-  const floatx4 g0 = *reinterpret_cast<const floatx4*>(p + kDNode + r0 * kDRow);
-  const floatx4 g1 = *reinterpret_cast<const floatx4*>(p + kDNode + (r0 + 1) * kDRow);
-  const floatx4 g2 = *reinterpret_cast<const floatx4*>(p + kDNode + (r0 + 2) * kDRow);
+  constexpr int kNode = 4 * kRow;
+  const floatx4 f0 = *reinterpret_cast<const floatx4*>(p + r0 * kRow);
+  const floatx4 f1 = *reinterpret_cast<const floatx4*>(p + (r0 + 1) * kRow);
+  const floatx4 f2 = *reinterpret_cast<const floatx4*>(p + (r0 + 2) * kRow);
+  const floatx4 g0 = *reinterpret_cast<const floatx4*>(p + kNode + r0 * kRow);
+  const floatx4 g1 = *reinterpret_cast<const floatx4*>(p + kNode + (r0 + 1) * kRow);
+  const floatx4 g2 = *reinterpret_cast<const floatx4*>(p + kNode + (r0 + 2) * kRow);
   floatx4 v;
 #pragma unroll
   for (int u = 0; u < 4; ++u) v[u] = herm_value(H, f0[u], f1[u], f2[u], g0[u], g1[u], g2[u]);
@@ -71,6 +86,7 @@ struct DegChunk {
   float hw[6][64];       // quintic Hermite weights of the fraction in the node interval
 };
 
+template <int kRow, int kNS = kDSl>
 __device__ __forceinline__ void deg_chunk(const e2v2_deg_args& A, const Envelope& env, const RadialTab& R, int ti,
                                           int s, int64_t e0, int nc, DegChunk& C) {
   const int t = threadIdx.x;
@@ -89,7 +105,7 @@ __device__ __forceinline__ void deg_chunk(const e2v2_deg_args& A, const Envelope
     env.eval(d, p, dp);
     C.p[t] = p; C.dp[t] = dp;
     float tt;
-    C.toff[t] = radial_node_sliced(R, tab_pair(R, ti, A.atom_type[A.col[e]]), s, kDSl, kDRow, d, tt);
+    C.toff[t] = radial_node_sliced(R, tab_pair(R, ti, A.atom_type[A.col[e]]), s, kNS, kRow, d, tt);
     const Hermite5 H = hermite5(tt);
     C.hw[0][t] = H.a0; C.hw[1][t] = H.a1; C.hw[2][t] = H.a2;
     C.hw[3][t] = H.b0; C.hw[4][t] = H.b1; C.hw[5][t] = H.b2;
@@ -109,35 +125,44 @@ __device__ __forceinline__ Envelope deg_env(const e2v2_deg_args& A) {
   return env;
 }
 
-// Forward: x0[m][i][c] = (1/avg) sum_e Y_m(e) p(e) fea_l(m)(e)[c]; the eight edge
-// subsets are added by lane swaps (lane ^ 8, ^ 16, ^ 32, a fixed order).
-__global__ __launch_bounds__(64) void k_deg_fwd_sl(e2v2_deg_args A, float* __restrict__ x0) {
+// Forward: x0[m][i][c] = (1/avg) sum_e Y_m(e) p(e) fea_l(m)(e)[c]; the edge
+// subsets of the lanes are added by lane swaps (lane ^ Q, ^ 2 Q, ..., ^ 32: a
+// fixed order).  kHid: the same sums of the hidden channels into hs [9][N][144]
+// (row: 128 hidden sums, then (1/avg) sum_e Y_m p and 15 zeros, written by slice 0:
+// lanes q = 0..3 of sub 0).
+template <bool kHid>
+__device__ __forceinline__ void deg_fwd_body(const e2v2_deg_args& A, float* __restrict__ out) {
+  using S = DegSl<kHid>;
   constexpr int CH = 64;
   __shared__ DegChunk C;
-  const int s = blockIdx.x % kDSl, i = blockIdx.x / kDSl;
+  const int s = blockIdx.x % S::NS, i = blockIdx.x / S::NS;
   if (i >= A.n_rows) return;
-  const int lane = threadIdx.x, sub = lane >> 3, q = lane & 7;
+  const int lane = threadIdx.x, sub = lane / S::Q, q = lane % S::Q;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   const Envelope env = deg_env(A);
-  const RadialTab R = make_deg_tab(A);
+  const RadialTab R = make_deg_tab<kHid>(A);
   const int ti = A.atom_type[i];
   floatx4 acc[9];
+  float sacc[9];   // kHid: sum of Y_m p (the bias column)
 #pragma unroll
-  for (int m = 0; m < 9; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < 9; ++m) {
+    acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+    sacc[m] = 0.f;
+  }
   for (int c0 = 0; c0 < n; c0 += CH) {
     const int nc = min(CH, n - c0);
-    deg_chunk(A, env, R, ti, s, (int64_t)b + c0, nc, C);
+    deg_chunk<S::Row, S::NS>(A, env, R, ti, s, (int64_t)b + c0, nc, C);
     __syncthreads();
-    for (int el = sub; el < nc; el += 8) {
+    for (int el = sub; el < nc; el += S::Sub) {
       const float* tb = R.tab + C.toff[el] + 4 * q;
       const Hermite5 H = chunk_hermite(C, el);
       const float p = C.p[el];
       float Y[9];
 #pragma unroll
       for (int m = 0; m < 9; ++m) Y[m] = C.Y[m][el];
-      const floatx4 fa = deg_interp(tb, H, 0);
-      const floatx4 fb = deg_interp(tb + kDSlC, H, 0);
-      const floatx4 fc = deg_interp(tb + 2 * kDSlC, H, 0);
+      const floatx4 fa = deg_interp<S::Row>(tb, H, 0);
+      const floatx4 fb = deg_interp<S::Row>(tb + S::W, H, 0);
+      const floatx4 fc = deg_interp<S::Row>(tb + 2 * S::W, H, 0);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float f0 = fa[u] * p, f1 = fb[u] * p, f2 = fc[u] * p;
@@ -147,6 +172,10 @@ __global__ __launch_bounds__(64) void k_deg_fwd_sl(e2v2_deg_args A, float* __res
 #pragma unroll
         for (int m = 4; m < 9; ++m) acc[m][u] = fmaf(Y[m], f2, acc[m][u]);
       }
+      if constexpr (kHid) {
+#pragma unroll
+        for (int m = 0; m < 9; ++m) sacc[m] = fmaf(Y[m], p, sacc[m]);
+      }
     }
     __syncthreads();
   }
@@ -155,21 +184,35 @@ __global__ __launch_bounds__(64) void k_deg_fwd_sl(e2v2_deg_args A, float* __res
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       float v = acc[m][u];
-      v += __shfl_xor(v, 8, kWave);
-      v += __shfl_xor(v, 16, kWave);
-      v += __shfl_xor(v, 32, kWave);
+#pragma unroll
+      for (int o = S::Q; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
       acc[m][u] = v;
+    }
+    if constexpr (kHid) {
+#pragma unroll
+      for (int o = S::Q; o < kWave; o <<= 1) sacc[m] += __shfl_xor(sacc[m], o, kWave);
     }
   }
   if (sub == 0) {
+    constexpr int ld = kHid ? kDHs : kDC;
 #pragma unroll
     for (int m = 0; m < 9; ++m) {
       floatx4 o;
 #pragma unroll
       for (int u = 0; u < 4; ++u) o[u] = acc[m][u] / A.avg;
-      *reinterpret_cast<floatx4*>(x0 + ((size_t)m * A.n_rows + i) * kDC + kDSlC * s + 4 * q) = o;
+      float* row = out + ((size_t)m * A.n_rows + i) * ld;
+      *reinterpret_cast<floatx4*>(row + S::W * s + 4 * q) = o;
+      if (kHid && s == 0 && q < 4)   // columns 128 + 4 q .. + 3: the bias column (q = 0) and zeros
+        *reinterpret_cast<floatx4*>(row + kDH + 4 * q) = floatx4{q == 0 ? sacc[m] / A.avg : 0.f, 0.f, 0.f, 0.f};
     }
   }
+}
+
+__global__ __launch_bounds__(64) void k_deg_fwd_sl(e2v2_deg_args A, float* __restrict__ x0) {
+  deg_fwd_body<false>(A, x0);
+}
+__global__ __launch_bounds__(64) void k_degh_fwd_sl(e2v2_deg_args A, float* __restrict__ hs) {
+  deg_fwd_body<true>(A, hs);
 }
 
 // Sum over each group of 8 lanes (lanes 8 k .. 8 k + 7), left in every lane of the
@@ -181,35 +224,48 @@ __device__ __forceinline__ float sum8(float v) {
   return v;
 }
 
+// Sum over each quad of lanes (lanes 4 k .. 4 k + 3), left in every lane of the quad (fixed order).
+__device__ __forceinline__ float sum4(float v) {
+  v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+  return v;
+}
+
 // Backward: per edge and slice, dfea_l[c] = p/avg sum_{m in l} Y_m G0[m][i][c];
 // dL/dd = sum_{l,c} dfea_l[c] (p' fea_l[c] / p + fea_l'[c]) (envelope and profile
-// derivative) and dL/dY -> dL/ddvec.  The 8 lanes of an edge add their channel
-// quads' sums (sum8) and lane q = 0 writes the slice's partial part[s][e] =
+// derivative) and dL/dY -> dL/ddvec.  The Q lanes of an edge add their channel
+// quads' sums and lane q = 0 writes the slice's partial part[s][e] =
 // (dL/ddvec, dL/dd); e2v2_deg_bwd adds the 8 partials of every edge in slice order.
-__global__ __launch_bounds__(64) void k_deg_bwd_sl(e2v2_deg_args A, const float* __restrict__ G0,
-                                                   float4* __restrict__ part) {
-  constexpr int CH = 64;
+// kHid: G0 is grad_h [9][N][128] over the hidden channels, and slice 0 adds the
+// bias column's terms from grad_s [9][N] (a channel of value 1 and derivative 0).
+template <bool kHid>
+__device__ __forceinline__ void deg_bwd_body(const e2v2_deg_args& A, const float* __restrict__ G0,
+                                             const float* __restrict__ GS, float4* __restrict__ part) {
+  using S = DegSl<kHid>;
+  constexpr int CH = 64, ld = kHid ? kDH : kDC;
   __shared__ DegChunk C;
-  const int s = blockIdx.x % kDSl, i = blockIdx.x / kDSl;
+  const int s = blockIdx.x % S::NS, i = blockIdx.x / S::NS;
   if (i >= A.n_rows) return;
-  const int lane = threadIdx.x, sub = lane >> 3, q = lane & 7;
+  const int lane = threadIdx.x, sub = lane / S::Q, q = lane % S::Q;
   const int b = A.row_ptr[i], n = A.row_ptr[i + 1] - b;
   const Envelope env = deg_env(A);
-  const RadialTab R = make_deg_tab(A);
+  const RadialTab R = make_deg_tab<kHid>(A);
   const int ti = A.atom_type[i];
-  const int c = kDSlC * s + 4 * q;
+  const int c = S::W * s + 4 * q;
   floatx4 g[9];
+  float gs[9];
 #pragma unroll
   for (int m = 0; m < 9; ++m) {
-    const floatx4 v = *reinterpret_cast<const floatx4*>(G0 + ((size_t)m * A.n_rows + i) * kDC + c);
+    const floatx4 v = *reinterpret_cast<const floatx4*>(G0 + ((size_t)m * A.n_rows + i) * ld + c);
 #pragma unroll
     for (int u = 0; u < 4; ++u) g[m][u] = v[u] / A.avg;
+    gs[m] = (kHid && s == 0) ? GS[(size_t)m * A.n_rows + i] / A.avg : 0.f;
   }
   for (int c0 = 0; c0 < n; c0 += CH) {
     const int nc = min(CH, n - c0);
-    deg_chunk(A, env, R, ti, s, (int64_t)b + c0, nc, C);
+    deg_chunk<S::Row, S::NS>(A, env, R, ti, s, (int64_t)b + c0, nc, C);
     __syncthreads();
-    for (int el = sub; el < nc; el += 8) {
+    for (int el = sub; el < nc; el += S::Sub) {
       const float* tb = R.tab + C.toff[el] + 4 * q;
       const Hermite5 H = chunk_hermite(C, el);
       const float p = C.p[el];
@@ -223,8 +279,8 @@ __global__ __launch_bounds__(64) void k_deg_bwd_sl(e2v2_deg_args A, const float*
       // one degree block l (rows m0 .. m0 + 2l) at compile-time indices (the arrays stay in registers)
       auto block = [&](auto lc) {
         constexpr int l = decltype(lc)::value, m0 = l * l, m1 = (l + 1) * (l + 1);
-        const floatx4 f = deg_interp(tb + l * kDSlC, H, 0);
-        const floatx4 fd = deg_interp(tb + l * kDSlC, H, 1);
+        const floatx4 f = deg_interp<S::Row>(tb + l * S::W, H, 0);
+        const floatx4 fd = deg_interp<S::Row>(tb + l * S::W, H, 1);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           float dl = 0.f;
@@ -240,11 +296,19 @@ __global__ __launch_bounds__(64) void k_deg_bwd_sl(e2v2_deg_args A, const float*
       block(std::integral_constant<int, 0>{});
       block(std::integral_constant<int, 1>{});
       block(std::integral_constant<int, 2>{});
-      s_val = sum8(s_val);
-      s_der = sum8(s_der);
+      auto sumq = [](float v) { return S::Q == 8 ? sum8(v) : sum4(v); };
+      s_val = sumq(s_val);
+      s_der = sumq(s_der);
 #pragma unroll
-      for (int m = 1; m < 9; ++m) dsh[m] = sum8(dsh[m]);
+      for (int m = 1; m < 9; ++m) dsh[m] = sumq(dsh[m]);
       if (q == 0) {
+        if (kHid && s == 0) {   // the bias column: value 1, no distance derivative
+#pragma unroll
+          for (int m = 0; m < 9; ++m) {
+            s_val = fmaf(Y[m], gs[m], s_val);
+            dsh[m] = fmaf(gs[m], p, dsh[m]);
+          }
+        }
         const float ux = C.u[0][el], uy = C.u[1][el], uz = C.u[2][el], nrm = C.nrm[el];
         float gx, gy, gz;
         raw_sh2_bwd(ux, uy, uz, dsh, gx, gy, gz);
@@ -259,14 +323,41 @@ __global__ __launch_bounds__(64) void k_deg_bwd_sl(e2v2_deg_args A, const float*
   }
 }
 
-// dL/d dvec and dL/dd of every edge: the 8 slices' partials part[s][e] added in slice order.
+__global__ __launch_bounds__(64) void k_deg_bwd_sl(e2v2_deg_args A, const float* __restrict__ G0,
+                                                   float4* __restrict__ part) {
+  deg_bwd_body<false>(A, G0, nullptr, part);
+}
+__global__ __launch_bounds__(64) void k_degh_bwd_sl(e2v2_deg_args A, const float* __restrict__ GH,
+                                                    const float* __restrict__ GS, float4* __restrict__ part) {
+  deg_bwd_body<true>(A, GH, GS, part);
+}
+
+// grad_s[m][i] = sum_c grad_x0[m][i][c] b3[l(m)][c]: one wavefront per (m, i), four channels per lane, then a
+// fixed-order wave sum.
+__global__ __launch_bounds__(256) void k_deg_bias_grad(const float* __restrict__ gx0, const float* __restrict__ b3,
+                                                       int n, float* __restrict__ gs) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);   // row m n + i of [9 n]
+  if (r >= 9 * (int64_t)n) return;
+  const int lane = threadIdx.x & 63, m = (int)(r / n);
+  const floatx4 x = *reinterpret_cast<const floatx4*>(gx0 + r * kDC + 4 * lane);
+  const floatx4 w = *reinterpret_cast<const floatx4*>(b3 + l_of(m) * kDC + 4 * lane);
+  float v = x[0] * w[0];
+  v = fmaf(x[1], w[1], v);
+  v = fmaf(x[2], w[2], v);
+  v = fmaf(x[3], w[3], v);
+  v = wave_sum(v);
+  if (lane == 0) gs[r] = v;
+}
+
+// dL/d dvec and dL/dd of every edge: the slices' partials part[s][e] (n_sl = 8 or 4) added in slice order.
 __global__ __launch_bounds__(256) void k_edge_part_sum(const float4* __restrict__ part, int64_t n_edges,
-                                                       float* __restrict__ ddv, float* __restrict__ dd) {
+                                                       float* __restrict__ ddv, float* __restrict__ dd, int n_sl) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= n_edges) return;
   float4 a = part[e];
 #pragma unroll
   for (int s = 1; s < kDSl; ++s) {
+    if (s >= n_sl) break;
     const float4 v = part[(int64_t)s * n_edges + e];
     a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
   }
@@ -276,10 +367,10 @@ __global__ __launch_bounds__(256) void k_edge_part_sum(const float4* __restrict_
   dd[e] = a.w;
 }
 
-int launch_edge_part_sum(const float* part, int64_t n_edges, float* ddv, float* dd, hipStream_t st) {
+int launch_edge_part_sum(const float* part, int64_t n_edges, float* ddv, float* dd, hipStream_t st, int n_sl) {
   if (n_edges <= 0) return 0;
   hipLaunchKernelGGL(k_edge_part_sum, dim3((unsigned)((n_edges + 255) / 256)), dim3(256), 0, st,
-                     reinterpret_cast<const float4*>(part), n_edges, ddv, dd);
+                     reinterpret_cast<const float4*>(part), n_edges, ddv, dd, n_sl);
   E2V2_LAUNCHED("k_edge_part_sum");
   return 0;
 }
@@ -324,8 +415,8 @@ __global__ __launch_bounds__(64 * kPosWaves) void k_edge_to_pos(int n_atoms, con
 
 using namespace e2v2;
 
-static int check_deg_table(const e2v2_deg_args& A, const char* who) {
-  E2V2_REQUIRE(A.channels == kDC, "%s: built for C=%d, got %d", who, kDC, A.channels);
+static int check_deg_table(const e2v2_deg_args& A, const char* who, int channels = kDC) {
+  E2V2_REQUIRE(A.channels == channels, "%s: built for %d channels, got %d", who, channels, A.channels);
   E2V2_REQUIRE(A.rtab && A.atom_type && A.col && A.n_types >= 1 && A.n_types <= E2V2_MAX_TYPES && A.rtab_n >= 2 &&
                    A.rtab_h > 0.f && (double)A.rc * (1.0 / A.rtab_h) <= (double)(A.rtab_n - 1),
                "%s: needs the gbf_projs table covering the cutoff and the atom types (n_types %d, rtab_n %d)", who,
@@ -360,7 +451,46 @@ E2V2_API int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float
   float4* part = static_cast<float4*>(workspace);
   hipLaunchKernelGGL(k_deg_bwd_sl, dim3((unsigned)A.n_rows * kDSl), dim3(kWave), 0, s, A, grad_x0, part);
   E2V2_LAUNCHED("k_deg_bwd_sl");
-  return launch_edge_part_sum(reinterpret_cast<const float*>(part), A.n_edges, ddvec, ddist, s);
+  return launch_edge_part_sum(reinterpret_cast<const float*>(part), A.n_edges, ddvec, ddist, s, kDSl);
+}
+
+E2V2_API int e2v2_deg_hidden_fwd(const e2v2_deg_args* args, float* hs, hipStream_t s) {
+  E2V2_REQUIRE(args && hs, "deg_hidden_fwd: null argument");
+  const e2v2_deg_args& A = *args;
+  if (int rc = check_deg_table(A, "deg_hidden_fwd", kDH)) return rc;
+  if (A.n_rows == 0) return 0;
+  hipLaunchKernelGGL(k_degh_fwd_sl, dim3((unsigned)A.n_rows * DegSl<true>::NS), dim3(kWave), 0, s, A, hs);
+  E2V2_LAUNCHED("k_degh_fwd_sl");
+  return 0;
+}
+
+E2V2_API int e2v2_deg_hidden_bwd(const e2v2_deg_args* args, const float* grad_h, const float* grad_s, float* ddvec,
+                                 float* ddist, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  E2V2_REQUIRE(args, "deg_hidden_bwd: null arguments");
+  const e2v2_deg_args& A = *args;
+  if (int rc = check_deg_table(A, "deg_hidden_bwd", kDH)) return rc;
+  if (A.n_rows == 0) return 0;
+  E2V2_REQUIRE(grad_h && grad_s && ddvec && ddist, "deg_hidden_bwd: null operand");
+  const size_t need = e2v2_deg_bwd_workspace(A.n_edges);
+  E2V2_REQUIRE(workspace_bytes >= need && (need == 0 || workspace) &&
+                   reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "deg_hidden_bwd: workspace of %zu bytes (16-byte aligned) needed, got %zu", need, workspace_bytes);
+  float4* part = static_cast<float4*>(workspace);
+  hipLaunchKernelGGL(k_degh_bwd_sl, dim3((unsigned)A.n_rows * DegSl<true>::NS), dim3(kWave), 0, s, A, grad_h,
+                     grad_s, part);
+  E2V2_LAUNCHED("k_degh_bwd_sl");
+  return launch_edge_part_sum(reinterpret_cast<const float*>(part), A.n_edges, ddvec, ddist, s, DegSl<true>::NS);
+}
+
+E2V2_API int e2v2_deg_bias_grad(const float* grad_x0, const float* b3, int32_t n, float* grad_s, hipStream_t s) {
+  E2V2_REQUIRE(n >= 0 && n < (1 << 27), "deg_bias_grad: n=%d", n);
+  if (n == 0) return 0;
+  E2V2_REQUIRE(grad_x0 && b3 && grad_s && ((uintptr_t)grad_x0 & 15) == 0 && ((uintptr_t)b3 & 15) == 0,
+               "deg_bias_grad: null or unaligned operand (16 bytes)");
+  const int64_t rows = 9 * (int64_t)n;
+  hipLaunchKernelGGL(k_deg_bias_grad, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, grad_x0, b3, n, grad_s);
+  E2V2_LAUNCHED("k_deg_bias_grad");
+  return 0;
 }
 
 E2V2_API int e2v2_edge_to_pos(int n_atoms, const int32_t* row_ptr, const int32_t* key_ptr, const int32_t* key_eid,

@@ -131,9 +131,10 @@ __device__ __forceinline__ Jet jlayernorm(const Jet& x, double g, double b, doub
   return n;
 }
 
-// Output jets of one profile at d = d0 (type pair (ta, tb)) for channels t and t + 128.
+// Output jets of one profile at d = d0 (type pair (ta, tb)) for channels t and t + 128, and hid, the jet of
+// hidden channel t (the second SiLU's output, the last Linear's input).
 __device__ void profile_jets(const e2v2_radial_net& W, const float* __restrict__ mu, double coeff, int za, int zb,
-                             double d0, Jet (&out)[2]) {
+                             double d0, Jet (&out)[2], Jet& hid) {
   __shared__ double rbf_s[kNB][4];
   __shared__ double hid_s[kRH][4];
   __shared__ double red[kRH][4];
@@ -174,6 +175,7 @@ __device__ void profile_jets(const e2v2_radial_net& W, const float* __restrict__
   }
   __syncthreads();
   const Jet s2 = jsilu(jlayernorm(z, (double)W.g2[t], (double)W.be2[t], red));
+  hid = s2;
 #pragma unroll
   for (int q = 0; q < 4; ++q) hid_s[t][q] = s2.c[q];
   __syncthreads();
@@ -213,8 +215,10 @@ __device__ __forceinline__ void jet_rows(const Jet& y, double h, double (&r)[4])
   r[3] = h * h * h * 6.0 * y.c[3];
 }
 
-// one block per (node, pair); writes the profile's 256 channels of rows k = 0..3 at their layout positions
-// (pair slot p holds the type pair pair_ab[p] = a n_types + b; pair_ab NULL: p itself)
+// one block per (node, pair); writes the profile's 256 output channels (kHid: its 128 hidden channels, the last
+// Linear's input) of rows k = 0..3 at their layout positions (pair slot p holds the type pair
+// pair_ab[p] = a n_types + b; pair_ab NULL: p itself)
+template <bool kHid>
 __global__ __launch_bounds__(kRH) void k_radial_table(e2v2_radial_net W, const float* __restrict__ mu, double coeff,
                                                       const int32_t* __restrict__ type_z, int n_types,
                                                       const int32_t* __restrict__ pair_ab, int n_nodes,
@@ -223,12 +227,12 @@ __global__ __launch_bounds__(kRH) void k_radial_table(e2v2_radial_net W, const f
   const int n = blockIdx.x, p = blockIdx.y;
   const int ab = pair_ab ? pair_ab[p] : p;
   const int za = type_z[ab / n_types], zb = type_z[ab % n_types];
-  Jet y[2];
-  profile_jets(W, mu, coeff, za, zb, (double)n * h, y);
+  Jet y[2], hid;
+  profile_jets(W, mu, coeff, za, zb, (double)n * h, y, hid);
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
+  for (int hh = 0; hh < (kHid ? 1 : 2); ++hh) {
     double r[4];
-    jet_rows(y[hh], h, r);
+    jet_rows(kHid ? hid : y[hh], h, r);
     const int o = layout_pos(Lo, threadIdx.x + hh * kRH);
 #pragma unroll
     for (int k = 0; k < 4; ++k) tab[tab_index(Lo, p, n_nodes, n, k, nc, o)] = (float)r[k];
@@ -238,29 +242,58 @@ __global__ __launch_bounds__(kRH) void k_radial_table(e2v2_radial_net W, const f
 // Interpolation error at the midpoint of every node interval: err[0] = max |f - f~|,
 // err[1] = max |f|, err[2] = max h |f' - f~'|, err[3] = max h |f'| (float bits; non-negative
 // floats order like their bit patterns, so the unsigned atomic max is exact and deterministic).
+// kHid: the table holds the hidden channels; the error is that of the profile's output formed from them,
+// f~ = W3 h~ + b3 (in float64 from the fp32 interpolants h~, h~'), against the float64 output.
+template <bool kHid>
 __global__ __launch_bounds__(kRH) void k_radial_check(e2v2_radial_net W, const float* __restrict__ mu, double coeff,
                                                       const int32_t* __restrict__ type_z, int n_types,
                                                       const int32_t* __restrict__ pair_ab, int n_nodes,
                                                       double h, const float* __restrict__ tab, int nc,
                                                       e2v2_radial_layout Lo, uint32_t* __restrict__ err) {
+  __shared__ float hv_s[kRH], hd_s[kRH];
   const int n = blockIdx.x, p = blockIdx.y;
   const int ab = pair_ab ? pair_ab[p] : p;
   const int za = type_z[ab / n_types], zb = type_z[ab % n_types];
-  Jet y[2];
-  profile_jets(W, mu, coeff, za, zb, ((double)n + 0.5) * h, y);
+  Jet y[2], hid;
+  profile_jets(W, mu, coeff, za, zb, ((double)n + 0.5) * h, y, hid);
   const Hermite5 H = hermite5(0.5f);
-  float e_v = 0.f, m_v = 0.f, e_d = 0.f, m_d = 0.f;
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const int o = layout_pos(Lo, threadIdx.x + hh * kRH);
+  if constexpr (kHid) {
+    const int o = layout_pos(Lo, threadIdx.x);
     float a[4], b[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       a[k] = tab[tab_index(Lo, p, n_nodes, n, k, nc, o)];
       b[k] = tab[tab_index(Lo, p, n_nodes, n + 1, k, nc, o)];
     }
-    const float v = herm_value(H, a[0], a[1], a[2], b[0], b[1], b[2]);
-    const float dv = herm_value(H, a[1], a[2], a[3], b[1], b[2], b[3]);
+    hv_s[threadIdx.x] = herm_value(H, a[0], a[1], a[2], b[0], b[1], b[2]);
+    hd_s[threadIdx.x] = herm_value(H, a[1], a[2], a[3], b[1], b[2], b[3]);
+    __syncthreads();
+  }
+  float e_v = 0.f, m_v = 0.f, e_d = 0.f, m_d = 0.f;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    float v, dv;
+    if constexpr (kHid) {
+      const int oc = threadIdx.x + hh * kRH;
+      const float* w3 = W.w3 + (size_t)oc * kRH;
+      double sv = (double)W.b3[oc], sd = 0.0;
+      for (int j = 0; j < kRH; ++j) {
+        sv += (double)w3[j] * (double)hv_s[j];
+        sd += (double)w3[j] * (double)hd_s[j];
+      }
+      v = (float)sv;
+      dv = (float)sd;
+    } else {
+      const int o = layout_pos(Lo, threadIdx.x + hh * kRH);
+      float a[4], b[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        a[k] = tab[tab_index(Lo, p, n_nodes, n, k, nc, o)];
+        b[k] = tab[tab_index(Lo, p, n_nodes, n + 1, k, nc, o)];
+      }
+      v = herm_value(H, a[0], a[1], a[2], b[0], b[1], b[2]);
+      dv = herm_value(H, a[1], a[2], a[3], b[1], b[2], b[3]);
+    }
     e_v = fmaxf(e_v, (float)fabs((double)v - y[hh].c[0]));
     m_v = fmaxf(m_v, (float)fabs(y[hh].c[0]));
     e_d = fmaxf(e_d, (float)fabs((double)dv - h * y[hh].c[1]));
@@ -373,16 +406,17 @@ E2V2_API int e2v2_radial_table_size(float rc, float rbf_coeff, int32_t refine, i
   return 0;
 }
 
-// Every output channel of the profile lands inside the row, at a distinct position.
-static int check_layout(const e2v2_radial_layout* Lo, int32_t nc, const char* who) {
+// Every channel of the profile (n_ch: its 256 outputs or 128 hidden channels) lands inside the row, at a
+// distinct position.
+static int check_layout(const e2v2_radial_layout* Lo, int32_t nc, const char* who, int n_ch = kRO) {
   E2V2_REQUIRE(Lo, "%s: no channel layout", who);
-  E2V2_REQUIRE(nc >= kRO && nc <= 4 * kRO && Lo->split >= 1 && kRO % Lo->split == 0 && Lo->block >= 1 &&
+  E2V2_REQUIRE(nc >= n_ch && nc <= 4 * kRO && Lo->split >= 1 && n_ch % Lo->split == 0 && Lo->block >= 1 &&
                    Lo->split % Lo->block == 0 && Lo->col0 >= 0 && Lo->block_stride >= 0 && Lo->split_stride >= 0 &&
                    Lo->slice_width >= 0 && (Lo->slice_width == 0 || nc % Lo->slice_width == 0),
                "%s: bad channel layout (nc %d, col0 %d, split %d, block %d, slice width %d)", who, nc, Lo->col0,
                Lo->split, Lo->block, Lo->slice_width);
   uint64_t used[4 * kRO / 64] = {};
-  for (int o = 0; o < kRO; ++o) {
+  for (int o = 0; o < n_ch; ++o) {
     const int64_t p = (int64_t)Lo->col0 + (int64_t)((o % Lo->split) / Lo->block) * Lo->block_stride +
                       (int64_t)(o / Lo->split) * Lo->split_stride + o % Lo->block;
     E2V2_REQUIRE(p >= 0 && p < nc, "%s: channel %d maps to position %lld outside rows of %d", who, o, (long long)p,
@@ -404,34 +438,68 @@ static int check_pairs(int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
   return 0;
 }
 
+template <bool kHid>
+static int radial_table_launch(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                               const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
+                               int32_t n_nodes, float h, float* tab, int32_t nc, const e2v2_radial_layout* layout,
+                               hipStream_t s, const char* who) {
+  if (int rc = check_net(net, who)) return rc;
+  if (int rc = check_pairs(n_types, pair_ab, n_pairs, who)) return rc;
+  E2V2_REQUIRE(rbf_offset && type_z && tab && n_nodes >= 2 && h > 0.f, "%s: bad arguments (n_types %d, n_nodes %d)",
+               who, n_types, n_nodes);
+  if (int rc = check_layout(layout, nc, who, kHid ? kRH : kRO)) return rc;
+  hipLaunchKernelGGL(k_radial_table<kHid>, dim3((unsigned)n_nodes, (unsigned)n_pairs), dim3(kRH), 0, s, *net,
+                     rbf_offset, (double)rbf_coeff, type_z, n_types, pair_ab, n_nodes, (double)h, tab, nc, *layout);
+  E2V2_LAUNCHED("k_radial_table");
+  return 0;
+}
+
+template <bool kHid>
+static int radial_check_launch(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                               const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
+                               int32_t n_nodes, float h, const float* tab, int32_t nc,
+                               const e2v2_radial_layout* layout, uint32_t* err, hipStream_t s, const char* who) {
+  if (int rc = check_net(net, who)) return rc;
+  if (int rc = check_pairs(n_types, pair_ab, n_pairs, who)) return rc;
+  E2V2_REQUIRE(rbf_offset && type_z && tab && err && n_nodes >= 2, "%s: bad arguments", who);
+  if (int rc = check_layout(layout, nc, who, kHid ? kRH : kRO)) return rc;
+  hipLaunchKernelGGL(k_radial_check<kHid>, dim3((unsigned)(n_nodes - 1), (unsigned)n_pairs), dim3(kRH), 0, s,
+                     *net, rbf_offset, (double)rbf_coeff, type_z, n_types, pair_ab, n_nodes, (double)h, tab, nc,
+                     *layout, err);
+  E2V2_LAUNCHED("k_radial_check");
+  return 0;
+}
+
 E2V2_API int e2v2_radial_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
                                const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
                                int32_t n_nodes, float h, float* tab, int32_t nc, const e2v2_radial_layout* layout,
                                hipStream_t s) {
-  if (int rc = check_net(net, "radial_table")) return rc;
-  if (int rc = check_pairs(n_types, pair_ab, n_pairs, "radial_table")) return rc;
-  E2V2_REQUIRE(rbf_offset && type_z && tab && n_nodes >= 2 && h > 0.f,
-               "radial_table: bad arguments (n_types %d, n_nodes %d)", n_types, n_nodes);
-  if (int rc = check_layout(layout, nc, "radial_table")) return rc;
-  hipLaunchKernelGGL(k_radial_table, dim3((unsigned)n_nodes, (unsigned)n_pairs), dim3(kRH), 0, s, *net,
-                     rbf_offset, (double)rbf_coeff, type_z, n_types, pair_ab, n_nodes, (double)h, tab, nc, *layout);
-  E2V2_LAUNCHED("k_radial_table");
-  return 0;
+  return radial_table_launch<false>(net, rbf_offset, rbf_coeff, type_z, n_types, pair_ab, n_pairs, n_nodes, h, tab,
+                                    nc, layout, s, "radial_table");
 }
 
 E2V2_API int e2v2_radial_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
                                      const int32_t* type_z, int32_t n_types, const int32_t* pair_ab, int32_t n_pairs,
                                      int32_t n_nodes, float h, const float* tab, int32_t nc,
                                      const e2v2_radial_layout* layout, uint32_t* err, hipStream_t s) {
-  if (int rc = check_net(net, "radial_table_check")) return rc;
-  if (int rc = check_pairs(n_types, pair_ab, n_pairs, "radial_table_check")) return rc;
-  E2V2_REQUIRE(rbf_offset && type_z && tab && err && n_nodes >= 2, "radial_table_check: bad arguments");
-  if (int rc = check_layout(layout, nc, "radial_table_check")) return rc;
-  hipLaunchKernelGGL(k_radial_check, dim3((unsigned)(n_nodes - 1), (unsigned)n_pairs), dim3(kRH), 0, s,
-                     *net, rbf_offset, (double)rbf_coeff, type_z, n_types, pair_ab, n_nodes, (double)h, tab, nc,
-                     *layout, err);
-  E2V2_LAUNCHED("k_radial_check");
-  return 0;
+  return radial_check_launch<false>(net, rbf_offset, rbf_coeff, type_z, n_types, pair_ab, n_pairs, n_nodes, h, tab,
+                                    nc, layout, err, s, "radial_table_check");
+}
+
+E2V2_API int e2v2_radial_hidden_table(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                                      const int32_t* type_z, int32_t n_types, const int32_t* pair_ab,
+                                      int32_t n_pairs, int32_t n_nodes, float h, float* tab, int32_t nc,
+                                      const e2v2_radial_layout* layout, hipStream_t s) {
+  return radial_table_launch<true>(net, rbf_offset, rbf_coeff, type_z, n_types, pair_ab, n_pairs, n_nodes, h, tab,
+                                   nc, layout, s, "radial_hidden_table");
+}
+
+E2V2_API int e2v2_radial_hidden_table_check(const e2v2_radial_net* net, const float* rbf_offset, float rbf_coeff,
+                                            const int32_t* type_z, int32_t n_types, const int32_t* pair_ab,
+                                            int32_t n_pairs, int32_t n_nodes, float h, const float* tab, int32_t nc,
+                                            const e2v2_radial_layout* layout, uint32_t* err, hipStream_t s) {
+  return radial_check_launch<true>(net, rbf_offset, rbf_coeff, type_z, n_types, pair_ab, n_pairs, n_nodes, h, tab,
+                                   nc, layout, err, s, "radial_hidden_table_check");
 }
 
 static int radial_eval_check(const float* tab, int32_t n_types, int32_t n_nodes, float h, int32_t nc,

@@ -1690,7 +1690,7 @@ class EdgeDegreeEmbeddingNetwork_higherorder(nn.Module):
 
     def forward_fused(self, ctx: EdgeContext):
         table = self._radial.get([p.net for p in self.gbf_projs], self.target_embedding, self.source_embedding,
-                                 ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="deg",
+                                 ctx.rbf_offset, ctx.rbf_coeff, ctx.rc, ctx.type_z, ctx.type_key, layout="degh",
                                  pairs=ctx.pairs)
         # the edge spherical harmonics ("e3nn sph") are formed inside the degree kernels
         with record_function("e3nn sph"):

@@ -15,7 +15,7 @@ import numpy as np
 import torch
 from torch import nn
 
-from . import _lib, so3
+from . import _lib, gemm, so3
 from .neighbors import NeighborList
 
 ENV_EXPONENT = 5
@@ -91,25 +91,37 @@ class RadialTable:
     ``layout`` places the channels: "plain" (rows [pairs][nodes][4][nc], profile
     m at 256 m + c), "attn" (one fc_easy profile in the attention kernels' slice
     order, gate and inputhead of head h at 32 (h // 16) + h % 16 and 16 positions
-    on, stored slice-major [pairs][8][nodes][4][32]) or "deg" (three profiles,
+    on, stored slice-major [pairs][8][nodes][4][32]), "deg" (three profiles,
     channel c of profile l at 96 (c // 32) + 32 l + c % 32, stored slice-major
-    [pairs][8][nodes][4][96])."""
+    [pairs][8][nodes][4][96]) or "degh": the three profiles' 128 hidden channels
+    (the last Linear's input; e2v2_radial_hidden_table), hidden channel k of
+    profile l at 96 (k // 32) + 32 l + k % 32, stored slice-major
+    [pairs][4][nodes][4][96].  The hidden table is checked on the profile's output
+    W3 h~ + b3, with the same tolerances, and keeps the packed last Linears for the
+    degree embedding's per-node GEMMs (``w3_pack``: [W3_l | b3_l | 0] as a
+    144 -> 256 weight, ``w3t_pack``: W3_l^T, ``b3``: [3, 256])."""
 
     LAYOUTS = {
         "plain": lambda m: (256 * m, 256, 256, 0, 0, 0),
         "attn": lambda m: (0, 128, 16, 32, 16, 32),
         "deg": lambda m: (32 * m, 256, 32, 96, 0, 96),
+        "degh": lambda m: (32 * m, 128, 32, 96, 0, 96),
     }
+    HIDDEN = ("degh",)
 
     def __init__(self, nets, tgt: nn.Embedding, src: nn.Embedding, rbf_offset: torch.Tensor, rbf_coeff: float,
                  rc: float, type_z: torch.Tensor, tol_value: float = 1e-6, tol_deriv: float = 1e-5,
                  max_refine: int = 3, layout: str = "plain", min_refine: int = -1, pairs=None):
         dev = type_z.device
-        if layout not in self.LAYOUTS or (layout == "attn" and len(nets) != 1) or (layout == "deg" and len(nets) != 3):
+        if (layout not in self.LAYOUTS or (layout == "attn" and len(nets) != 1)
+                or (layout in ("deg", "degh") and len(nets) != 3)):
             raise ValueError(f"radial table layout {layout!r} does not fit {len(nets)} profiles")
         self.layout = layout
+        hidden = layout in self.HIDDEN
         self._layouts = [_lib.RadialLayout(*self.LAYOUTS[layout](m)) for m in range(len(nets))]
-        self.nc = 256 * len(nets)
+        self.nc = (128 if hidden else 256) * len(nets)
+        build, check = (("e2v2_radial_hidden_table", "e2v2_radial_hidden_table_check") if hidden
+                        else ("e2v2_radial_table", "e2v2_radial_table_check"))
         self.n_types = T = int(type_z.numel())
         if T < 1 or T > MAX_TYPES:
             raise NotImplementedError(f"{T} atom types: atomic numbers index embeddings of {MAX_TYPES} entries")
@@ -148,9 +160,8 @@ class RadialTable:
                         _lib.vp(self.pair_slot_ptr(self.pair_ab)), _lib.i32(self.n_pairs), _lib.i32(self.n_nodes),
                         _lib.f32(self.h))
                 lo = _lib.C.byref(self._layouts[m])
-                _lib.call("e2v2_radial_table", *args, _p(self.tab), _lib.i32(self.nc), lo, st)
-                _lib.call("e2v2_radial_table_check", *args, _p(self.tab), _lib.i32(self.nc), lo,
-                          _lib.vp(err[m].data_ptr()), st)
+                _lib.call(build, *args, _p(self.tab), _lib.i32(self.nc), lo, st)
+                _lib.call(check, *args, _p(self.tab), _lib.i32(self.nc), lo, _lib.vp(err[m].data_ptr()), st)
             e = err.cpu().view(torch.float32).double()
             self.value_err = float((e[:, 0] / e[:, 1].clamp_min(1e-30)).max())
             self.deriv_err = float((e[:, 2] / e[:, 3].clamp_min(1e-30)).max())
@@ -159,6 +170,16 @@ class RadialTable:
         else:
             raise RuntimeError(f"radial table: interpolation error {self.value_err:.2e} (value) / "
                                f"{self.deriv_err:.2e} (derivative) above tolerance after {max_refine} refinements")
+        if hidden:
+            with torch.no_grad():
+                w3 = torch.stack([n[6].weight.detach().float() for n in nets])          # [3, 256, 128]
+                b3 = torch.stack([n[6].bias.detach().float() for n in nets])            # [3, 256]
+                wb = torch.zeros(len(nets), 256, 144, dtype=torch.float32, device=dev)
+                wb[:, :, :128] = w3
+                wb[:, :, 128] = b3
+                self.w3_pack = gemm.pack(wb)                    # hs [.., 144] -> x0 [.., 256]
+                self.w3t_pack = gemm.pack(w3, transpose=True)   # grad_x0 [.., 256] -> grad_h [.., 128]
+                self.b3 = b3.contiguous()
 
     def pair_slot_ptr(self, t="slot"):
         """Device address of the pair -> slot map (or of ``t``), None for all pairs."""
@@ -240,44 +261,72 @@ class EdgeGeometryFn(torch.autograd.Function):
 
 
 class DegreeEmbedFn(torch.autograd.Function):
-    """EdgeDegreeEmbeddingNetwork_higherorder.forward (e2former.py:689-753): the three
-    gbf_projs profiles interpolated from their table inside the kernels; nothing per
-    edge is saved."""
+    """EdgeDegreeEmbeddingNetwork_higherorder.forward (e2former.py:689-753) with its
+    three gbf_projs profiles (module_utils.py:2151-2178) split at their last Linear:
+    the kernels sum the interpolated hidden channels times Y_m p over each row's
+    edges (hs [9, N, 144]: 128 hidden sums, the sum of Y_m p, zeros), and one
+    per-node split GEMM applies [W3_l | b3_l] (x0 = hs W^T, 144 -> 256 per degree l).
+    The backward runs the transposed GEMM (grad_h = grad_x0 W3_l) and the bias
+    column's grad_s = grad_x0 . b3_l before the edge kernel.  A "deg" table (the
+    profiles' outputs) runs e2v2_deg_fwd / e2v2_deg_bwd directly.  Nothing per edge
+    is saved."""
+
+    WIDX = (0, 1, 1, 1, 2, 2, 2, 2, 2)   # profile of each m-row
 
     @staticmethod
     def forward(ctx, dvec, dist, nl: NeighborList, atom_type, table: RadialTable, avg: float, rc: float):
         _need_cuda(dvec, dist)
         dev = dvec.device
         dargs = deg_args(nl, atom_type, table, avg, rc)
-        x0 = torch.empty(9, nl.n_atoms, 256, dtype=torch.float32, device=dev)   # m-major
-        _lib.call("e2v2_deg_fwd", _lib.C.byref(dargs), _p(x0), _stream(x0))
+        N = nl.n_atoms
+        x0 = torch.empty(9, N, 256, dtype=torch.float32, device=dev)   # m-major
+        if table.layout == "degh":
+            hs = torch.empty(9, N, 144, dtype=torch.float32, device=dev)
+            _lib.call("e2v2_deg_hidden_fwd", _lib.C.byref(dargs), _p(hs), _stream(hs))
+            if N:
+                gemm.gemm(hs, table.w3_pack, x0, DegreeEmbedFn.WIDX)
+            del hs
+        else:
+            _lib.call("e2v2_deg_fwd", _lib.C.byref(dargs), _p(x0), _stream(x0))
         ctx.nl, ctx.atom_type, ctx.table, ctx.avg, ctx.rc = nl, atom_type, table, avg, rc
         return x0
 
     @staticmethod
     def backward(ctx, gx0):
         _no_double_backward()
-        nl = ctx.nl
+        nl, table = ctx.nl, ctx.table
         dev = nl.dvec.device
-        E = nl.n_edges
+        E, N = nl.n_edges, nl.n_atoms
         gx0 = gx0.float().contiguous()
-        dargs = deg_args(nl, ctx.atom_type, ctx.table, ctx.avg, ctx.rc)
+        dargs = deg_args(nl, ctx.atom_type, table, ctx.avg, ctx.rc)
         ddv = torch.empty(max(E, 1), 3, dtype=torch.float32, device=dev)
         dd = torch.empty(max(E, 1), dtype=torch.float32, device=dev)
         nb = int(_lib.load().e2v2_deg_bwd_workspace(E))     # per-slice partials of this call
         ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
-        _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(ddv), _p(dd), _p(ws), _lib.C.c_size_t(ws.numel()),
-                  _stream(gx0))
+        if table.layout == "degh":
+            gh = torch.empty(9, N, 128, dtype=torch.float32, device=dev)
+            gs = torch.empty(9, max(N, 1), dtype=torch.float32, device=dev)
+            if N:
+                gemm.gemm(gx0, table.w3t_pack, gh, DegreeEmbedFn.WIDX)
+            _lib.call("e2v2_deg_bias_grad", _p(gx0), _p(table.b3), _lib.i32(N), _p(gs), _stream(gx0))
+            _lib.call("e2v2_deg_hidden_bwd", _lib.C.byref(dargs), _p(gh), _p(gs), _p(ddv), _p(dd), _p(ws),
+                      _lib.C.c_size_t(ws.numel()), _stream(gx0))
+            del gh, gs
+        else:
+            _lib.call("e2v2_deg_bwd", _lib.C.byref(dargs), _p(gx0), _p(ddv), _p(dd), _p(ws),
+                      _lib.C.c_size_t(ws.numel()), _stream(gx0))
         del ws
         return ddv[:E], dd[:E], None, None, None, None, None
 
 
 def deg_args(nl: NeighborList, atom_type: torch.Tensor, table: RadialTable, avg: float, rc: float):
-    if table.nc != 768 or table.layout != "deg":
-        raise ValueError("the degree embedding needs the table of its three profiles in slices (layout 'deg')")
-    return _lib.DegArgs(nl.n_atoms, nl.n_edges, 256, nl.row_ptr.data_ptr(), nl.dvec.data_ptr(), nl.dist.data_ptr(),
-                        nl.col.data_ptr(), table.tab.data_ptr(), atom_type.data_ptr(), table.n_types, table.n_nodes,
-                        table.h, float(avg), float(rc), ENV_A, ENV_B, ENV_C, table.pair_slot_ptr())
+    if not ((table.layout == "deg" and table.nc == 768) or (table.layout == "degh" and table.nc == 384)):
+        raise ValueError("the degree embedding needs the table of its three profiles in slices (layout 'deg', "
+                         "or 'degh' for their hidden channels)")
+    return _lib.DegArgs(nl.n_atoms, nl.n_edges, 128 if table.layout == "degh" else 256, nl.row_ptr.data_ptr(),
+                        nl.dvec.data_ptr(), nl.dist.data_ptr(), nl.col.data_ptr(), table.tab.data_ptr(),
+                        atom_type.data_ptr(), table.n_types, table.n_nodes, table.h, float(avg), float(rc), ENV_A,
+                        ENV_B, ENV_C, table.pair_slot_ptr())
 
 
 WEIGHT_ACTS = {"softmax": 0, "softplus": 1, "sigmoid": 2}
