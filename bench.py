@@ -68,8 +68,8 @@ COMPULSORY = {"e2v2_attn_fwd": attn_fwd_compulsory, "e2v2_attn_bwd": attn_bwd_co
 
 # Bytes the implementation's kernels read and write per launch, split into node / edge-list traffic
 # and the radial-table reads (rows of the per-type-pair distance tables, mostly served by the L2 and
-# the Infinity Cache: an attention layer's table is 16 pairs x 386 nodes x 4 KB = 25 MB at configs[3],
-# spacing 2^-6 A).
+# the Infinity Cache: an attention layer's table is 16 pairs x 770 nodes x 4 KB = 50 MB at configs[3],
+# spacing 2^-7 A, the first spacing at which the bench model's tables pass their check).
 # The forward and the backward row pass run one wavefront per (row, 16-head slice): every slice reads
 # the edge list (col, dvec, dist, source type: 6 words per edge) once, 8 times in all.
 SLICES = 8
