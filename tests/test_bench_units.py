@@ -29,6 +29,10 @@ def test_attention_bytes_split_by_activation_type():
     # the degree kernels read and write fp32 in both modes
     assert bench.deg_fwd_bytes(N, E, 2) == bench.deg_fwd_bytes(N, E)
     assert bench.deg_fwd_table_bytes(E) == 4 * E * 768 * 6 and bench.deg_bwd_table_bytes(E) == 4 * E * 768 * 8
+    # the hidden-channel form reads half the table channels (3 x 128), over 4 slices, and writes hs [9][N][144]
+    assert bench.deg_hidden_fwd_table_bytes(E) == 4 * E * 384 * 6
+    assert bench.deg_hidden_bwd_table_bytes(E) == 4 * E * 384 * 8
+    assert bench.deg_hidden_fwd_bytes(N, E) == 4 * (4 * E * 6 + N * 9 * 144) + 4 * E * 384 * 6
 
 
 def _trace_calls():
@@ -50,11 +54,13 @@ def test_profile_traffic_counts_every_dispatch_of_a_call():
     would report under half of it."""
     calls = _trace_calls()
     per = bench.profile_traffic_per_dispatch()
-    n_eval = calls["k_deg_fwd_sl"]
+    # the degree embedding's kernels: the hidden-channel form (the model's path) or the output-table form
+    deg_f, deg_b = ("k_degh_fwd_sl", "k_degh_bwd_sl") if "k_degh_fwd_sl" in calls else ("k_deg_fwd_sl", "k_deg_bwd_sl")
+    n_eval = calls[deg_f]
     n_attn = 4 * n_eval
     assert calls["k_attn_fwd_sl"] == n_attn
     disp = {k: calls[k] / n_attn for k in ("k_attn_bwd_row_sl", "k_attn_bwd_col_grp")}
-    disp["k_edge_part_sum"] = (calls["k_edge_part_sum"] - calls["k_deg_bwd_sl"]) / n_attn
+    disp["k_edge_part_sum"] = (calls["k_edge_part_sum"] - calls[deg_b]) / n_attn
     rebuilt = sum(per[k] * n for k, n in disp.items())
     got = bench.traffic_from_profile("e2v2_attn_bwd")
     assert abs(got - rebuilt) <= 0.01 * rebuilt, (got, rebuilt, disp)
