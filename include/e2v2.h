@@ -436,11 +436,11 @@ int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float* ddvec, 
    each profile, module_utils.py:2159-2172, moved past the sum over edges):
      hs[m][i][k] = (1/avg) sum_e Y_m(e) p(e) h_l(m),k(e)   (k < 128),
      hs[m][i][128] = (1/avg) sum_e Y_m(e) p(e),   hs[m][i][129..143] = 0,
-   hs [9][N][144] m-major; then x0[m] = hs[m] [W3_l | b3_l | 0]^T (a per-node GEMM, 144 -> 256) is the
+   hs [9][N][144] m-major (16-byte aligned); then x0[m] = hs[m] [W3_l | b3_l | 0]^T (a per-node GEMM, 144 -> 256) is the
    output of e2v2_deg_fwd.  args.rtab is the hidden table (e2v2_radial_hidden_table, degree layout, nc 384)
    and args.channels = 128. */
 int e2v2_deg_hidden_fwd(const e2v2_deg_args* args, float* hs, hipStream_t s);
-/* grad_h [9][N][128] = grad_x0[m] W3_l and grad_s [9][N] = grad_x0[m] . b3_l (unscaled: the kernel applies
+/* grad_h [9][N][128] (16-byte aligned) = grad_x0[m] W3_l and grad_s [9][N] = grad_x0[m] . b3_l (unscaled: the kernel applies
    1/avg) -> ddvec [E,3], ddist [E]; workspace: e2v2_deg_bwd_workspace(E) bytes, 16-byte aligned. */
 int e2v2_deg_hidden_bwd(const e2v2_deg_args* args, const float* grad_h, const float* grad_s, float* ddvec,
                         float* ddist, void* workspace, size_t workspace_bytes, hipStream_t s);

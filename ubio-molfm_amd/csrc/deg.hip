@@ -455,7 +455,7 @@ E2V2_API int e2v2_deg_bwd(const e2v2_deg_args* args, const float* grad_x0, float
 }
 
 E2V2_API int e2v2_deg_hidden_fwd(const e2v2_deg_args* args, float* hs, hipStream_t s) {
-  E2V2_REQUIRE(args && hs, "deg_hidden_fwd: null argument");
+  E2V2_REQUIRE(args && hs && ((uintptr_t)hs & 15) == 0, "deg_hidden_fwd: null argument or hs not 16-byte aligned");
   const e2v2_deg_args& A = *args;
   if (int rc = check_deg_table(A, "deg_hidden_fwd", kDH)) return rc;
   if (A.n_rows == 0) return 0;
@@ -470,7 +470,8 @@ E2V2_API int e2v2_deg_hidden_bwd(const e2v2_deg_args* args, const float* grad_h,
   const e2v2_deg_args& A = *args;
   if (int rc = check_deg_table(A, "deg_hidden_bwd", kDH)) return rc;
   if (A.n_rows == 0) return 0;
-  E2V2_REQUIRE(grad_h && grad_s && ddvec && ddist, "deg_hidden_bwd: null operand");
+  E2V2_REQUIRE(grad_h && grad_s && ddvec && ddist && ((uintptr_t)grad_h & 15) == 0,
+               "deg_hidden_bwd: null operand or grad_h not 16-byte aligned");
   const size_t need = e2v2_deg_bwd_workspace(A.n_edges);
   E2V2_REQUIRE(workspace_bytes >= need && (need == 0 || workspace) &&
                    reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
