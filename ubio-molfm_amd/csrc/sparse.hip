@@ -18,6 +18,7 @@
 namespace e2v2 {
 
 constexpr int kSegThreads = 256;
+constexpr int kSegMaxD = 16;   // d per thread of the h-fast segmented reduction
 
 struct SegRow {
   int p0, p1;
@@ -92,7 +93,19 @@ __global__ __launch_bounds__(kSegThreads) void k_seg_dot(e2v2_segments S, const 
         s = fmaf(x.w, y.w, s);
       }
     } else {
-      for (int d = 0; d < D; ++d) s = fmaf(ah[d * sa_d], b[d * sb_d], s);
+      // four d steps' loads issued before their products (the same order of the sum)
+      int d = 0;
+      for (; d + 4 <= D; d += 4) {
+        float x[4], y[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          x[u] = ah[(int64_t)(d + u) * sa_d];
+          y[u] = b[(int64_t)(d + u) * sb_d];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s = fmaf(x[u], y[u], s);
+      }
+      for (; d < D; ++d) s = fmaf(ah[(int64_t)d * sa_d], b[(int64_t)d * sb_d], s);
     }
     out[(int64_t)e * so_e + (int64_t)h * so_h] = s;
   }
@@ -110,6 +123,49 @@ __global__ __launch_bounds__(kSegThreads) void k_seg_reduce(e2v2_segments S, con
   const SegRow R = seg_row(S, r);
   const bool staged = stage_row(S, R, X != nullptr, se, sc);
   const int np = R.p1 - R.p0;
+  // h-fast X with H dividing the block: thread (g, h) = (t / H, t % H) owns d = g, g + G, ... (G = 256 / H,
+  // at most kSegMaxD of them) and loads W[e, h] once per slot for all of them; the sums keep slot order
+  const int G = (X && h_fast && kSegThreads % H == 0) ? kSegThreads / H : 0;
+  if (staged && G > 0 && (D + G - 1) / G <= kSegMaxD) {
+    const int t = threadIdx.x, h = t % H, g = t / H;
+    const int nd = g < D ? (D - g + G - 1) / G : 0;
+    const float* wh = W + (int64_t)h * sw_h;
+    const float* xh = X + (int64_t)h * sx_h + (int64_t)g * sx_d;
+    const int64_t xs = (int64_t)G * sx_d;
+    float acc[kSegMaxD];
+#pragma unroll
+    for (int j = 0; j < kSegMaxD; ++j) acc[j] = 0.f;
+    int k = 0;
+    for (; k + 2 <= np; k += 2) {   // two slots' loads in flight
+      float w[2], x[2][kSegMaxD];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int e = se[k + u];
+        w[u] = e >= 0 ? wh[(int64_t)e * sw_e] : 0.f;
+        const float* xr = xh + (int64_t)sc[k + u] * sx_r;
+#pragma unroll
+        for (int j = 0; j < kSegMaxD; ++j) x[u][j] = (e >= 0 && j < nd) ? xr[j * xs] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (se[k + u] < 0) continue;
+#pragma unroll
+        for (int j = 0; j < kSegMaxD; ++j)
+          if (j < nd) acc[j] = fmaf(w[u], x[u][j], acc[j]);
+      }
+    }
+    if (k < np && se[k] >= 0) {
+      const float w = wh[(int64_t)se[k] * sw_e];
+      const float* xr = xh + (int64_t)sc[k] * sx_r;
+#pragma unroll
+      for (int j = 0; j < kSegMaxD; ++j)
+        if (j < nd) acc[j] = fmaf(w, xr[j * xs], acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < kSegMaxD; ++j)
+      if (j < nd) out[(int64_t)r * so_r + (int64_t)h * so_h + (int64_t)(g + j * G) * so_d] = acc[j];
+    return;
+  }
   for (int idx = threadIdx.x; idx < H * D; idx += kSegThreads) {
     const int h = h_fast ? idx % H : idx / D, d = h_fast ? idx / H : idx % D;
     const float* wh = W + (int64_t)h * sw_h;
