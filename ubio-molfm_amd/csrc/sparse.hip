@@ -19,6 +19,7 @@ namespace e2v2 {
 
 constexpr int kSegThreads = 256;
 constexpr int kSegMaxD = 16;   // d per thread of the h-fast segmented reduction
+constexpr int kSegMaxA = 24;   // d of a segmented dot held in registers
 
 struct SegRow {
   int p0, p1;
@@ -65,6 +66,38 @@ __global__ __launch_bounds__(kSegThreads) void k_seg_dot(e2v2_segments S, const 
   const bool staged = stage_row(S, R, true, se, sc);
   const unsigned n = (unsigned)(R.p1 - R.p0) * (unsigned)H;
   const float* a = A + (int64_t)r * sa_r;
+  // H dividing the block: thread t keeps head t % H for every slot it takes (t / H, + 256 / H, ...), so its
+  // A row stays in registers; each slot's B row is loaded whole before the products (summed in d order)
+  if (kSegThreads % H == 0 && D <= kSegMaxA) {
+    const int h = (int)threadIdx.x % H, ks = kSegThreads / H, np = R.p1 - R.p0;
+    const float* ah = a + (int64_t)h * sa_h;
+    float ar[kSegMaxA];
+#pragma unroll
+    for (int j = 0; j < kSegMaxA; ++j) ar[j] = j < D ? ah[(int64_t)j * sa_d] : 0.f;
+    for (int k = (int)threadIdx.x / H; k < np; k += ks) {
+      int c, e;
+      if (staged) {
+        e = se[k];
+        c = sc[k];
+        if (e < 0) continue;
+      } else {
+        const int p = R.p0 + k;
+        c = S.col_index[p];
+        e = S.alpha_index[p];
+        if (!slot_ok(S, c, e)) continue;
+      }
+      const float* b = B + (int64_t)c * sb_r + (int64_t)h * sb_h;
+      float y[kSegMaxA];
+#pragma unroll
+      for (int j = 0; j < kSegMaxA; ++j) y[j] = j < D ? b[(int64_t)j * sb_d] : 0.f;
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < kSegMaxA; ++j)
+        if (j < D) s = fmaf(ar[j], y[j], s);
+      out[(int64_t)e * so_e + (int64_t)h * so_h] = s;
+    }
+    return;
+  }
   // unit-stride rows of 16-byte aligned groups of four: float4 loads (the same products, summed in d order)
   const bool v4 = sa_d == 1 && sb_d == 1 && (D & 3) == 0 && ((sa_r | sa_h | sb_r | sb_h) & 3) == 0 &&
                   (((uintptr_t)A | (uintptr_t)B) & 15) == 0;
