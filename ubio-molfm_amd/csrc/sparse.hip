@@ -290,6 +290,37 @@ __global__ void k_outer_dsh(const float* __restrict__ g, int n_rows, const float
   dsh[t] = s;
 }
 
+// The same, one wavefront per edge for H <= 256 channels in groups of four and L <= kOuterL: lane t owns
+// channels 4 t .. 4 t + 3 of fea[e] (loaded once) and of each g row; per l the lanes' partial dots are added
+// by a fixed-order wave sum.
+constexpr int kOuterL = 9, kOuterWaves = 4;
+__global__ __launch_bounds__(64 * kOuterWaves) void k_outer_dsh_w(const float* __restrict__ g, int n_rows,
+                                                                 const float* __restrict__ fea,
+                                                                 const int32_t* __restrict__ qidx, int64_t n_edges,
+                                                                 int L, int H, float* __restrict__ dsh) {
+  const int64_t e = (int64_t)blockIdx.x * kOuterWaves + (threadIdx.x >> 6);
+  if (e >= n_edges) return;
+  const int lane = threadIdx.x & 63, c = 4 * lane;
+  const int q = qidx[e];
+  const bool ok = q >= 0 && q < n_rows, in = c < H;
+  float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (ok && in) f = *reinterpret_cast<const float4*>(fea + e * H + c);
+#pragma unroll
+  for (int l = 0; l < kOuterL; ++l) {
+    if (l >= L) break;
+    float v = 0.f;
+    if (ok && in) {
+      const float4 x = *reinterpret_cast<const float4*>(g + ((int64_t)q * L + l) * H + c);
+      v = x.x * f.x;
+      v = fmaf(x.y, f.y, v);
+      v = fmaf(x.z, f.z, v);
+      v = fmaf(x.w, f.w, v);
+    }
+    v = wave_sum(v);
+    if (lane == 0) dsh[e * L + l] = v;
+  }
+}
+
 // dfea[e, h] = sum_l g[q[e], l, h] sh[e, l]  (q[e] outside [0, n_rows): 0)
 __global__ void k_outer_dfea(const float* __restrict__ g, int n_rows, const float* __restrict__ sh,
                              const int32_t* __restrict__ qidx, int64_t n_edges, int L, int H,
@@ -501,9 +532,15 @@ E2V2_API int e2v2_outer_bwd(const float* grad, int n_rows, const float* sh, cons
   E2V2_REQUIRE(grad && query_index && (dsh == nullptr || fea) && (dfea == nullptr || sh),
                "outer_bwd: null operand");
   if (dsh) {
-    hipLaunchKernelGGL(k_outer_dsh, dim3(blocks_of(n_edges * L, 256)), dim3(256), 0, s, grad, n_rows, fea,
-                       query_index, n_edges, L, H, dsh);
-    E2V2_LAUNCHED("k_outer_dsh");
+    if (H <= 256 && H % 4 == 0 && L <= kOuterL && ((uintptr_t)grad & 15) == 0 && ((uintptr_t)fea & 15) == 0) {
+      hipLaunchKernelGGL(k_outer_dsh_w, dim3(blocks_of(n_edges, kOuterWaves)), dim3(64 * kOuterWaves), 0, s, grad,
+                         n_rows, fea, query_index, n_edges, L, H, dsh);
+      E2V2_LAUNCHED("k_outer_dsh_w");
+    } else {
+      hipLaunchKernelGGL(k_outer_dsh, dim3(blocks_of(n_edges * L, 256)), dim3(256), 0, s, grad, n_rows, fea,
+                         query_index, n_edges, L, H, dsh);
+      E2V2_LAUNCHED("k_outer_dsh");
+    }
   }
   if (dfea) {
     hipLaunchKernelGGL(k_outer_dfea, dim3(blocks_of(n_edges * H, 256)), dim3(256), 0, s, grad, n_rows, sh,
