@@ -947,24 +947,45 @@ class Gate_s3(nn.Module):
                             SIGMOID_NORM, packs)
 
 
-class GatedLinearS3Fn(torch.autograd.Function):
-    """Gate_s3 followed by the FFN's second SO3_Linear_e2former
-    (module_utils.py:2694-2746, 2755-2797) on the split GEMMs, fp32: the gate logits
-    sc = h[0] Wg^T + bg, then y = res + gate(sc, h) W2 (+ b2 on row 0) with the gate
-    applied while the GEMM reads its operand (``e2v2_gemm_s3_gated``), so the gated
-    activation is never written.  The backward is GateFn's and SO3LinearFn's.  Input
-    gradients only."""
+class GateFold:
+    """Gate_s3's logit Linear folded into the FFN's first SO3 linear: the logits are
+    sc = h[0] Wg^T + bg with h[0] = x[0] W1_0^T + b1 (the l = 0 row carries the bias),
+    so sc = x[0] F^T + bs with F = Wg W1_0 [768, 256] and bs = Wg b1 + bg, formed in
+    float64 once per weight version.  ``f``: F packed for sc = x[0] F^T; ``bk``: F^T
+    packed for the logits' input gradient gsc F (``pieces`` as the FFN's other packs: 3 in
+    fp32, 1 — the bf16 rounding of F — in the bf16 mode); ``b``: bs in fp32."""
+    __slots__ = ("f", "bk", "b")
+
+    def __init__(self, Wg, bg, W1_0, b1, pieces: int = 3):
+        F = (Wg.detach().double() @ W1_0.detach().double()).float().contiguous()
+        self.b = (Wg.detach().double() @ b1.detach().double() + bg.detach().double()).float().contiguous()
+        self.f = s3gemm.pack(F, pieces=pieces)
+        self.bk = s3gemm.pack(F, transpose=True, pieces=pieces)
+
+
+class FFNS3Fn(torch.autograd.Function):
+    """FeedForwardNetwork_s3 (module_utils.py:2755-2797) with Gate_s3 (:2694-2746) on the
+    split GEMMs, fp32: one grouped launch forms h = x W1^T (+ b1 on row 0) and the gate
+    logits sc = x[0] F^T + bs (GateFold), then y = res + gate(sc, h) W2^T (+ b2 on row 0)
+    with the gate applied while the GEMM reads its operand (``e2v2_gemm_s3_gated``: the
+    gated activation is never written).  Backward: gy = gout W2, the gate kernel
+    (gsc and gh[1:]; h[0] enters only through the logits), and one grouped launch for
+    gx[0] = gsc F and gx[1:] = gh[1:] W1.  Input gradients only."""
 
     @staticmethod
-    def forward(ctx, h, gpacks, bg, k1: float, k2: float, W2op, b2, lmax: int, res=None):
-        h = h.contiguous()
-        sc = h.new_empty(h.shape[1], gpacks[0].n)
-        s3gemm.gemm(h[0], gpacks[0], sc, bias=bg)
-        y = h.new_empty(h.shape[0], h.shape[1], W2op.w.shape[1])
+    def forward(ctx, x, W1op, b1, fold: GateFold, k1: float, k2: float, W2op, b2, lmax: int, res=None):
+        x = x.contiguous()
+        N = x.shape[1]
+        f32 = dict(dtype=torch.float32, device=x.device)
+        h = torch.empty(x.shape[0], N, W1op.w.shape[1], **f32)
+        sc = torch.empty(N, fold.f.n, **f32)
+        s3gemm.gemm_grouped([dict(a=x, pw=W1op.s3f(), out=h, widx=_m_degrees(lmax), bias=b1, bias_batches=1),
+                             dict(a=x[0], pw=fold.f, out=sc, bias=fold.b)])
+        y = torch.empty(x.shape[0], N, W2op.w.shape[1], **f32)
         s3gemm.gemm(h, W2op.s3f(), y, _m_degrees(lmax), bias=b2, bias_batches=1,
                     res=None if res is None else res.contiguous(), gate=(sc, k1, k2))
         ctx.save_for_backward(sc, h)
-        ctx.gpacks, ctx.k, ctx.W2op, ctx.lmax, ctx.has_res = gpacks, (k1, k2), W2op, lmax, res is not None
+        ctx.W1op, ctx.fold, ctx.k, ctx.W2op, ctx.lmax, ctx.has_res = W1op, fold, (k1, k2), W2op, lmax, res is not None
         return y
 
     @staticmethod
@@ -976,8 +997,10 @@ class GatedLinearS3Fn(torch.autograd.Function):
         gsc = torch.empty_like(sc); gh = torch.empty_like(h)
         _lib.call("e2v2_gate_bwd", _dp(sc), _dp(h), _dp(gy), _dp(gsc), _dp(gh), _lib.i32(h.shape[1]),
                   _lib.f32(ctx.k[0]), _lib.f32(ctx.k[1]), _stream())
-        s3gemm.gemm(gsc, ctx.gpacks[1], gh[0])        # the gate kernel leaves gh[0] = 0
-        return gh, None, None, None, None, None, None, None, (gout if ctx.has_res else None)
+        gx = gh.new_empty(gh.shape[0], gh.shape[1], ctx.W1op.w.shape[2])
+        s3gemm.gemm_grouped([dict(a=gsc, pw=ctx.fold.bk, out=gx[0]),            # K = 768 first
+                             dict(a=gh[1:], pw=ctx.W1op.s3b(), out=gx[1:], widx=_m_degrees(ctx.lmax)[1:])])
+        return gx, None, None, None, None, None, None, None, None, (gout if ctx.has_res else None)
 
 
 class FeedForwardNetwork_s3(nn.Module):
@@ -991,13 +1014,19 @@ class FeedForwardNetwork_s3(nn.Module):
 
     def forward(self, x, res=None, bf16: bool = False, **kw):
         with record_function("FeedForwardFunction"):
-            h = self.slinear_1(x, bf16)
-            s2 = self.slinear_2
+            s1, s2, g = self.slinear_1, self.slinear_2, self.gate.gates
+            W1op = mrow_weight(s1, "weight", s1.weight, bf16, s1.lmax)
             W2op = mrow_weight(s2, "weight", s2.weight, bf16, s2.lmax)
-            gpacks = dense_packs(self.gate.gates, bf16)
-            if gpacks is not None and W2op.split_ok() and h.dtype == torch.float32 and h.shape[2] == s2.weight.shape[2]:
-                return GatedLinearS3Fn.apply(h, gpacks, self.gate.gates.bias.detach(), SILU_NORM, SIGMOID_NORM, W2op,
-                                             s2.bias.detach(), s2.lmax, res)
+            if (x.dtype == torch.float32 and W1op.split_ok() and W2op.split_ok()
+                    and dense_packs(g, bf16) is not None and s1.lmax == s2.lmax == self.gate.lmax
+                    and g.weight.shape == (s1.out_features * (s1.lmax + 1), s1.out_features)
+                    and s1.out_features == s2.in_features):
+                pc = W1op.pieces
+                fold = cached(self, "gate_fold_bf16" if bf16 else "gate_fold", (g.weight, g.bias, s1.weight, s1.bias),
+                              lambda: GateFold(g.weight, g.bias, s1.weight[0], s1.bias, pc))
+                return FFNS3Fn.apply(x, W1op, s1.bias.detach(), fold, SILU_NORM, SIGMOID_NORM, W2op,
+                                     s2.bias.detach(), s2.lmax, res)
+            h = s1(x, bf16)
             h = self.gate(h, bf16)
             return SO3LinearFn.apply(h, W2op, s2.bias.detach(), s2.lmax, res)
 
