@@ -153,9 +153,11 @@ class TrainEdges:
         t = torch.clamp((2 * d - (lo + hi)) / (hi - lo), -1.0, 1.0)
         return (1.0 - t * t) ** 2
 
-    def edge_input(self, tgt_emb, src_emb, rbf: torch.Tensor) -> torch.Tensor:
-        """x_edge = [rbf(d), tgt[z_i], src[z_j]] (e2former.py:258-266, 709-733)."""
-        return torch.cat([rbf, tgt_emb(self.Z)[self.qi], src_emb(self.Z)[self.nj]], dim=-1)
+    def edge_input(self, tgt_emb, src_emb, rbf: torch.Tensor) -> "EdgeInput":
+        """x_edge = [rbf(d), tgt[z_i], src[z_j]] (e2former.py:258-266, 709-733), applied to
+        radial profiles without being formed (EdgeInput)."""
+        return EdgeInput(self, tgt_emb, src_emb, rbf)
+
 
     def qk(self, q: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
         return sparse_ops.sparse_qk_edge_index_triton(q, k, self.row32, self.col32, metadata=self.md)
@@ -172,6 +174,31 @@ class TrainEdges:
     def outer(self, sh: torch.Tensor, fea: torch.Tensor) -> torch.Tensor:
         return sparse_ops.edge_degree_outer_triton(sh, fea, self.row32, self.N,
                                                   metadata=(self.nl.row_ptr, None, self.md[2], None, None, None))
+
+
+class EdgeInput:
+    """x_edge = [rbf(d), tgt[z_i], src[z_j]] as the input of RadialProfile nets
+    (module_utils.py:2151-2178) without the [E, 256 + 2 n_emb] tensor: the first
+    Linear's type blocks act on the embedding rows per atom and are gathered per edge,
+    W x_edge + b = W_rbf rbf + (tgt[Z] W_t^T)[i] + (src[Z] W_s^T)[j] + b (the same sum,
+    fp32 rounding of another association); the rest of the net follows unchanged, so
+    every parameter (the embeddings included) keeps its gradients to any order."""
+
+    def __init__(self, edges, tgt_emb, src_emb, rbf: torch.Tensor):
+        self.edges, self.tgt, self.src, self.rbf = edges, tgt_emb, src_emb, rbf
+
+    def __call__(self, prof) -> torch.Tensor:
+        net = prof.net
+        lin1 = net[0]
+        K, ne = self.rbf.shape[1], self.tgt.weight.shape[1]
+        W = lin1.weight
+        e = self.edges
+        ht = self.tgt(e.Z) @ W[:, K:K + ne].t()                  # [N, hidden] per atom
+        hs = self.src(e.Z) @ W[:, K + ne:K + 2 * ne].t()
+        h = self.rbf @ W[:, :K].t() + ht[e.qi] + hs[e.nj]
+        if lin1.bias is not None:
+            h = h + lin1.bias
+        return net[1:](h)
 
 
 def attention_weights(logit, p, ih, edges: TrainEdges, form: str) -> torch.Tensor:
@@ -201,7 +228,7 @@ def _raw_sh(v: torch.Tensor) -> torch.Tensor:
     return f(v)
 
 
-def qkdot_gate(ga, x: torch.Tensor, edges: TrainEdges, x_edge: torch.Tensor):
+def qkdot_gate(ga, x: torch.Tensor, edges: TrainEdges, x_edge: EdgeInput):
     """(gate, inputhead) of the QKdot variants (e2former.py:270-300)."""
     H = ga.num_attn_heads
     xd = so3_linear(ga.dot_linear, x)                                        # [9, N, Cd]
@@ -210,11 +237,11 @@ def qkdot_gate(ga, x: torch.Tensor, edges: TrainEdges, x_edge: torch.Tensor):
         Y = _sh_integral(edges.dvec)                                         # [E, 9]
         x0 = torch.cat([(Y[:, l * l:(l + 1) ** 2].t().unsqueeze(-1) * xq[l * l:(l + 1) ** 2]).sum(0)
                         for l in range(ga.lmax + 1)], dim=-1)                # [E, 3 Cd]
-        gate = ga.fc_m0(x0 * ga.rad_func_m0(x_edge))
-        return gate, ga.fc_easy(x_edge).reshape(-1, H)
+        gate = ga.fc_m0(x0 * x_edge(ga.rad_func_m0))
+        return gate, x_edge(ga.fc_easy).reshape(-1, H)
     lxs = _raw_sh(edges.dvec)                                                # [E, 9]
     x0 = torch.einsum("lec,el,ls->esc", xq, lxs, ga.sum_vec.to(xq.dtype)).reshape(xq.shape[1], -1)[:, :H]
-    eg = ga.fc_easy(x_edge)
+    eg = x_edge(ga.fc_easy)
     return ga.direction_linear(x0 * eg[:, H:]), eg[:, :H]
 
 
@@ -243,7 +270,7 @@ def attention(ga, x: torch.Tensor, edges: TrainEdges, rbf: torch.Tensor) -> torc
     k = so3_linear2scalar(ga.key_linear, x).reshape(N, H, -1)
     x_edge = edges.edge_input(ga.target_embedding, ga.source_embedding, rbf)
     if ga.tp_type == "QK_alpha":
-        eg = ga.fc_easy(x_edge)
+        eg = x_edge(ga.fc_easy)
         gate, ih = eg[:, :H], eg[:, H:]
     else:
         gate, ih = qkdot_gate(ga, x, edges, x_edge)
@@ -275,7 +302,7 @@ def degree_embedding(mod, edges: TrainEdges, rbf: torch.Tensor) -> torch.Tensor:
     p = edges.envelope().view(-1, 1)
     rows = []
     for l in range(mod.lmax + 1):
-        fea = mod.gbf_projs[l](emb) * p
+        fea = emb(mod.gbf_projs[l]) * p
         rows.append(edges.outer(lxs[:, l * l:(l + 1) ** 2].contiguous(), fea))   # [N, 2l+1, C]
     return torch.cat(rows, dim=1).permute(1, 0, 2) / mod.avg_aggregate_num
 
