@@ -495,6 +495,18 @@ int e2v2_ln_silu_fwd(const float* x, const float* g, const float* b, float* y, f
                      hipStream_t s);
 int e2v2_ln_silu_bwd(const float* x, const float* g, const float* b, const float* stats, const float* gy, float* gx,
                      int n, int w, hipStream_t s);
+/* Training-path LayerNorm + SiLU of the RadialProfile nets (module_utils.py:2151-2178: the nn.LayerNorm +
+   nn.SiLU pairs, whose gradients torch composes for each autograd order).  With stats from e2v2_ln_silu_fwd:
+   _bwd_param returns the input gradient gx and the affine gradients as per-block partial sums
+   part_g / part_b [n_part][w] (the caller sums the n_part rows); _bwd2 differentiates that first-order
+   pass once more: given the upstream gradients qx [n][w], qg [w], qb [w] of (gx, dg, db) (each may be NULL:
+   zero) it returns dgy, dx [n][w] and the partial sums of the affine gradients.  w in {64, 128, 192, 256,
+   384, 512}; 0 < n_part <= 65535 blocks of 4 wavefronts (one row per wavefront). */
+int e2v2_ln_silu_bwd_param(const float* x, const float* g, const float* b, const float* stats, const float* gy,
+                           float* gx, float* part_g, float* part_b, int n, int w, int n_part, hipStream_t s);
+int e2v2_ln_silu_bwd2(const float* x, const float* g, const float* b, const float* stats, const float* gy,
+                      const float* qx, const float* qg, const float* qb, float* dgy, float* dx, float* part_g,
+                      float* part_b, int n, int w, int n_part, hipStream_t s);
 
 /* ---- per-node dense layers: fp32 GEMMs on bf16 MFMA by the exact three-piece split ----
  * Replaces the GEMMs (forward and input gradient) of SO3_Linear_e2former (module_utils.py:2010-2052) and so of

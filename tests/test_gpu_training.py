@@ -31,6 +31,10 @@ PARAMS = [
     "decoder.decoder.blocks.3.ffn.slinear_2.bias",
     "decoder.decoder.norm_final.affine_bias",
     "head.energy_heads.omol25.mlp.0.weight",
+    "decoder.decoder.blocks.0.ga.fc_easy.net.1.weight",
+    "decoder.decoder.blocks.2.ga.fc_easy.net.4.bias",
+    "decoder.decoder.edge_deg_embed_dense.gbf_projs.0.net.1.bias",
+    "decoder.decoder.blocks.1.ga.query_linear.final_linear.1.weight",
 ]
 
 
@@ -171,6 +175,45 @@ def test_training_second_order_qkdots_softplus(pkg, cuda):
                       "decoder.decoder.blocks.3.ga.proj_zero.weight"]
     _case(cuda, systems.small_water(6, 5.6, seed=23), 33, "qkdots-softplus", names,
           tp_type="QKdotS_alpha+softplus", attn_type="so2-first-order+zero-order")
+
+
+@pytest.mark.parametrize("w", [64, 128, 192, 512])
+def test_ln_silu_second_order(pkg, cuda, w):
+    """ln_silu (the fused LayerNorm + SiLU of the radial nets on the training
+    path) against float64 layer_norm + silu: values and the first-order
+    gradients of x, g, b (1e-5 relative L2), then the gradients of
+    L = <gx, R0> + <dg, R1> + <db, R2> in x, g, b and the upstream gy (every
+    term of the second-order pass; 1e-4 relative L2, fp32 against float64
+    through two differentiations).  Rows not a multiple of the 4 rows per
+    block, more rows than wavefronts (each strides over several)."""
+    from ubio_molfm_amd import second_order as so
+    torch.manual_seed(w)
+    n = 4 * 2048 * 2 + 3 if w == 128 else 997
+    ln = torch.nn.LayerNorm(w).to(cuda)
+    with torch.no_grad():
+        ln.weight.normal_(1.0, 0.3)
+        ln.bias.normal_(0.0, 0.5)
+    x = torch.randn(n, w, device=cuda) * 1.5 + 0.3
+    gy = torch.randn(n, w, device=cuda)
+    R = [torch.randn(n, w, device=cuda), torch.randn(w, device=cuda), torch.randn(w, device=cuda)]
+
+    def run(f, g, b, dtype):
+        xx = x.to(dtype).requires_grad_(True)
+        gg = gy.to(dtype).requires_grad_(True)
+        y = f(xx)
+        gx, dg, db = torch.autograd.grad(y, (xx, g, b), gg, create_graph=True)
+        L = (gx * R[0].to(dtype)).sum() + (dg * R[1].to(dtype)).sum() + (db * R[2].to(dtype)).sum()
+        return [y, gx, dg, db] + list(torch.autograd.grad(L, (xx, g, b, gg)))
+
+    got = run(lambda t: so.ln_silu(ln, t), ln.weight, ln.bias, torch.float32)
+    g64 = ln.weight.detach().double().requires_grad_(True)
+    b64 = ln.bias.detach().double().requires_grad_(True)
+    ref = run(lambda t: torch.nn.functional.silu(torch.nn.functional.layer_norm(t, (w,), g64, b64, ln.eps)),
+              g64, b64, torch.float64)
+    names = ["y", "gx", "dg", "db", "d2x", "d2g", "d2b", "d2gy"]
+    for k, (a, r) in enumerate(zip(got, ref)):
+        err = _rel(a.double(), r)
+        assert err < (1e-5 if k < 4 else 1e-4), (names[k], err)
 
 
 def test_eval_mode_keeps_the_fused_path(pkg, cuda):

@@ -6,6 +6,8 @@
 //    sc[N][3C] = gates(x[0]).
 // Backward passes return input gradients only (weights are constants for force
 // evaluation) and recompute the statistics.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/e2v2.h"
 
@@ -347,6 +349,204 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ x
     if (q < nq) o[q * 64 + lane] = rstd * (dn[q] - m1 - nv[q] * m2);
 }
 }  // namespace e2v2
+
+// ---- LayerNorm + SiLU of the RadialProfile nets on the training path
+// (module_utils.py:2151-2178: Linear -> LayerNorm -> SiLU per hidden layer), where
+// the forces are differentiated once more: the first-order pass also returns the
+// affine parameters' gradients, and the second-order pass differentiates that
+// first-order pass.  Per row (z = xh g + b, xh = (x - mean) rstd, s = sigmoid(z),
+// s1 = silu'(z) = s (1 + z (1 - s)), s2 = silu''(z) = s (1 - s) (2 + z (1 - 2 s))):
+//   first order   gz = gy s1, u = gz g, gx = rstd (u - <u> - xh <u xh>),
+//                 dg = sum_rows gz xh, db = sum_rows gz;
+//   second order  (upstream qx, qg, qb on gx, dg, db; <.> the row mean over w)
+//                 A = rstd (qx - <qx> - xh <qx xh>), P = g A + qg xh + qb,
+//                 dgy = P s1, Z = P gy s2, c = <u xh>, m = <qx xh>,
+//                 R = sum qx (u - <u> - xh c),
+//                 X = -rstd (c qx + m u) + qg gz + Z g,
+//                 dx = rstd (X - <X> - xh <X xh>) - R rstd^2 xh / w,
+//                 d(g) = sum_rows (gz A + Z xh), d(b) = sum_rows Z.
+// One wavefront per row, rows strided over n_part blocks of 4 wavefronts; each
+// block writes its parameter sums to row blockIdx.x of part_* [n_part][w] (summed
+// over blocks by the caller: the order is fixed, so results repeat bitwise).
+namespace e2v2 {
+template <int NQ>
+__device__ __forceinline__ void ln_block_partials(float (&acc_a)[NQ], float (&acc_b)[NQ], float* part_a,
+                                                  float* part_b) {
+  constexpr int W = NQ * 64;
+  __shared__ float red[2][4][W];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    red[0][wave][q * 64 + lane] = acc_a[q];
+    red[1][wave][q * 64 + lane] = acc_b[q];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 2 * W; i += 256) {
+    const int k = i / W, c = i % W;
+    const float v = ((red[k][0][c] + red[k][1][c]) + red[k][2][c]) + red[k][3][c];
+    (k ? part_b : part_a)[(size_t)blockIdx.x * W + c] = v;
+  }
+}
+
+template <int NQ>
+__global__ __launch_bounds__(256) void k_ln_silu_bwd_param(const float* __restrict__ x, const float* __restrict__ g,
+                                                           const float* __restrict__ b,
+                                                           const float* __restrict__ stats,
+                                                           const float* __restrict__ gy, float* __restrict__ gx,
+                                                           float* __restrict__ part_g, float* __restrict__ part_b,
+                                                           int n) {
+  constexpr int W = NQ * 64;
+  const int lane = threadIdx.x & 63;
+  float gc[NQ], bc[NQ], ag[NQ], ab[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    gc[q] = g[q * 64 + lane];
+    bc[q] = b[q * 64 + lane];
+    ag[q] = 0.f;
+    ab[q] = 0.f;
+  }
+  for (int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6); row < n; row += gridDim.x * 4) {
+    const float mean = stats[2 * (size_t)row], rstd = stats[2 * (size_t)row + 1];
+    const float* xr = x + (size_t)row * W;
+    const float* gr = gy + (size_t)row * W;
+    float xh[NQ], u[NQ];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = q * 64 + lane;
+      xh[q] = (xr[c] - mean) * rstd;
+      const float z = xh[q] * gc[q] + bc[q];
+      const float sg = 1.0f / (1.0f + expf(-z));
+      const float gz = gr[c] * sg * (1.0f + z * (1.0f - sg));
+      ag[q] = fmaf(gz, xh[q], ag[q]);
+      ab[q] += gz;
+      u[q] = gz * gc[q];
+      s1 += u[q];
+      s2 = fmaf(u[q], xh[q], s2);
+    }
+    const float m1 = wave_sum(s1) / (float)W, m2 = wave_sum(s2) / (float)W;
+    float* o = gx + (size_t)row * W;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) o[q * 64 + lane] = rstd * (u[q] - m1 - xh[q] * m2);
+  }
+  ln_block_partials<NQ>(ag, ab, part_g, part_b);
+}
+
+template <int NQ>
+__global__ __launch_bounds__(256) void k_ln_silu_bwd2(const float* __restrict__ x, const float* __restrict__ g,
+                                                      const float* __restrict__ b, const float* __restrict__ stats,
+                                                      const float* __restrict__ gy, const float* __restrict__ qx,
+                                                      const float* __restrict__ qg, const float* __restrict__ qb,
+                                                      float* __restrict__ dgy, float* __restrict__ dx,
+                                                      float* __restrict__ part_g, float* __restrict__ part_b, int n) {
+  constexpr int W = NQ * 64;
+  constexpr float kInvW = 1.0f / (float)W;
+  const int lane = threadIdx.x & 63;
+  float gc[NQ], bc[NQ], qgc[NQ], qbc[NQ], ag[NQ], ab[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int c = q * 64 + lane;
+    gc[q] = g[c];
+    bc[q] = b[c];
+    qgc[q] = qg ? qg[c] : 0.f;
+    qbc[q] = qb ? qb[c] : 0.f;
+    ag[q] = 0.f;
+    ab[q] = 0.f;
+  }
+  for (int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6); row < n; row += gridDim.x * 4) {
+    const float mean = stats[2 * (size_t)row], rstd = stats[2 * (size_t)row + 1];
+    const size_t base = (size_t)row * W;
+    float xh[NQ], gz[NQ], u[NQ], qv[NQ], s1d[NQ], gzs2[NQ];
+    float su = 0.f, sux = 0.f, sq = 0.f, sqx = 0.f, squ = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = q * 64 + lane;
+      xh[q] = (x[base + c] - mean) * rstd;
+      const float z = xh[q] * gc[q] + bc[q];
+      const float sg = 1.0f / (1.0f + expf(-z));
+      const float gyv = gy[base + c];
+      s1d[q] = sg * (1.0f + z * (1.0f - sg));
+      gz[q] = gyv * s1d[q];
+      gzs2[q] = gyv * (sg * (1.0f - sg) * (2.0f + z * (1.0f - 2.0f * sg)));
+      u[q] = gz[q] * gc[q];
+      qv[q] = qx ? qx[base + c] : 0.f;
+      su += u[q];
+      sux = fmaf(u[q], xh[q], sux);
+      sq += qv[q];
+      sqx = fmaf(qv[q], xh[q], sqx);
+      squ = fmaf(qv[q], u[q], squ);
+    }
+    su = wave_sum(su);
+    sux = wave_sum(sux);
+    sq = wave_sum(sq);
+    sqx = wave_sum(sqx);
+    squ = wave_sum(squ);
+    const float ubar = su * kInvW, c_ = sux * kInvW, qbar = sq * kInvW, m = sqx * kInvW;
+    const float R = squ - ubar * sq - c_ * sqx;
+    float X[NQ];
+    float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = q * 64 + lane;
+      const float A = rstd * (qv[q] - qbar - xh[q] * m);
+      const float P = gc[q] * A + qgc[q] * xh[q] + qbc[q];
+      dgy[base + c] = P * s1d[q];
+      const float Z = P * gzs2[q];
+      X[q] = -rstd * (c_ * qv[q] + m * u[q]) + qgc[q] * gz[q] + Z * gc[q];
+      ag[q] += gz[q] * A + Z * xh[q];
+      ab[q] += Z;
+      t1 += X[q];
+      t2 = fmaf(X[q], xh[q], t2);
+    }
+    const float mX = wave_sum(t1) * kInvW, mXx = wave_sum(t2) * kInvW;
+    const float rr = R * rstd * rstd * kInvW;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) dx[base + q * 64 + lane] = rstd * (X[q] - mX - xh[q] * mXx) - rr * xh[q];
+  }
+  ln_block_partials<NQ>(ag, ab, part_g, part_b);
+}
+
+template <typename F>
+int ln_width_dispatch(int w, F&& f) {
+  switch (w) {
+    case 64: return f(std::integral_constant<int, 1>{});
+    case 128: return f(std::integral_constant<int, 2>{});
+    case 192: return f(std::integral_constant<int, 3>{});
+    case 256: return f(std::integral_constant<int, 4>{});
+    case 384: return f(std::integral_constant<int, 6>{});
+    case 512: return f(std::integral_constant<int, 8>{});
+    default: return -1;
+  }
+}
+}  // namespace e2v2
+
+E2V2_API int e2v2_ln_silu_bwd_param(const float* x, const float* g, const float* b, const float* stats,
+                                    const float* gy, float* gx, float* part_g, float* part_b, int n, int w,
+                                    int n_part, hipStream_t s) {
+  E2V2_REQUIRE(n >= 0 && n_part > 0 && n_part <= 65535, "ln_silu_bwd_param: n %d, n_part %d", n, n_part);
+  const int rc = e2v2::ln_width_dispatch(w, [&](auto nq) {
+    hipLaunchKernelGGL(e2v2::k_ln_silu_bwd_param<decltype(nq)::value>, dim3((unsigned)n_part), dim3(256), 0, s, x,
+                       g, b, stats, gy, gx, part_g, part_b, n);
+    return 0;
+  });
+  E2V2_REQUIRE(rc == 0, "ln_silu_bwd_param: width %d (64, 128, 192, 256, 384 or 512)", w);
+  E2V2_LAUNCHED("k_ln_silu_bwd_param");
+  return 0;
+}
+
+E2V2_API int e2v2_ln_silu_bwd2(const float* x, const float* g, const float* b, const float* stats, const float* gy,
+                               const float* qx, const float* qg, const float* qb, float* dgy, float* dx,
+                               float* part_g, float* part_b, int n, int w, int n_part, hipStream_t s) {
+  E2V2_REQUIRE(n >= 0 && n_part > 0 && n_part <= 65535, "ln_silu_bwd2: n %d, n_part %d", n, n_part);
+  const int rc = e2v2::ln_width_dispatch(w, [&](auto nq) {
+    hipLaunchKernelGGL(e2v2::k_ln_silu_bwd2<decltype(nq)::value>, dim3((unsigned)n_part), dim3(256), 0, s, x, g, b,
+                       stats, gy, qx, qg, qb, dgy, dx, part_g, part_b, n);
+    return 0;
+  });
+  E2V2_REQUIRE(rc == 0, "ln_silu_bwd2: width %d (64, 128, 192, 256, 384 or 512)", w);
+  E2V2_LAUNCHED("k_ln_silu_bwd2");
+  return 0;
+}
 
 E2V2_API int e2v2_ln_silu_fwd(const float* x, const float* g, const float* b, float* y, float* stats, int n, int w,
                               float eps, hipStream_t s) {

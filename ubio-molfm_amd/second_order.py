@@ -29,14 +29,17 @@ from typing import Optional
 
 import numpy as np
 import torch
+import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _lib
 from . import so3
 from . import sparse_ops
 from .ops import ENV_A, ENV_B, ENV_C
 
 _EXPAND = {}
 _CART = {}
+_ROW0 = {}
 
 
 def _expand(lmax: int, device) -> torch.Tensor:
@@ -45,6 +48,114 @@ def _expand(lmax: int, device) -> torch.Tensor:
     if key not in _EXPAND:
         _EXPAND[key] = torch.tensor([l for l in range(lmax + 1) for _ in range(2 * l + 1)], device=device)
     return _EXPAND[key]
+
+
+def _row0(n: int, ref: torch.Tensor) -> torch.Tensor:
+    """[n, 1, 1] indicator of the degree-0 row in ref's dtype and device.  A bias
+    on row 0 is added as row0 * bias over all rows (rows 1.. gain an exact
+    zero), so neither pass of the double backward slices or concatenates the
+    [n, N, C] tensor."""
+    key = (n, ref.dtype, str(ref.device))
+    if key not in _ROW0:
+        m = torch.zeros(n, 1, 1, dtype=ref.dtype)
+        m[0] = 1
+        _ROW0[key] = m.to(ref.device)
+    return _ROW0[key]
+
+
+_LN_WIDTHS = (64, 128, 192, 256, 384, 512)
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else _lib.vp(t.data_ptr())
+
+
+def _ln_parts(n: int) -> int:
+    """Blocks (rows of the parameter partial sums) of the LayerNorm + SiLU gradient passes."""
+    return max(1, min((n + 3) // 4, 2048))
+
+
+class _LNSiLUFn(torch.autograd.Function):
+    """silu(LayerNorm(x) * g + b) on rows x [n, w] (a RadialProfile's nn.LayerNorm +
+    nn.SiLU, module_utils.py:2151-2178) through e2v2_ln_silu_fwd; its backward is
+    _LNSiLUGradFn, itself differentiable once more, so the forces' parameter and
+    position gradients come from two fused kernels instead of torch's composed
+    double backward of layer_norm and silu."""
+
+    @staticmethod
+    def forward(ctx, x, g, b, eps: float):
+        n, w = x.shape
+        y = torch.empty_like(x)
+        st = x.new_empty(n, 2)
+        _lib.call("e2v2_ln_silu_fwd", _p(x), _p(g), _p(b), _p(y), _p(st), _lib.i32(n), _lib.i32(w), _lib.f32(eps),
+                  sparse_ops._stream(x.device))
+        ctx.save_for_backward(x, g, b, st)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, g, b, st = ctx.saved_tensors
+        gx, gg, gb = _LNSiLUGradFn.apply(gy, x, g, b, st)
+        return gx, gg, gb, None
+
+
+class _LNSiLUGradFn(torch.autograd.Function):
+    """(gx, dg, db) of _LNSiLUFn given gy (e2v2_ln_silu_bwd_param); its backward is
+    the second-order pass e2v2_ln_silu_bwd2 (mean and rstd enter as constants: the
+    kernel differentiates through them analytically)."""
+
+    @staticmethod
+    def forward(ctx, gy, x, g, b, st):
+        gy = gy.contiguous()
+        n, w = x.shape
+        npart = _ln_parts(n)
+        gx = torch.empty_like(x)
+        pg, pb = x.new_empty(npart, w), x.new_empty(npart, w)
+        _lib.call("e2v2_ln_silu_bwd_param", _p(x), _p(g), _p(b), _p(st), _p(gy), _p(gx), _p(pg), _p(pb),
+                  _lib.i32(n), _lib.i32(w), _lib.i32(npart), sparse_ops._stream(x.device))
+        ctx.save_for_backward(gy, x, g, b, st)
+        ctx.set_materialize_grads(False)
+        return gx, pg.sum(0), pb.sum(0)
+
+    @staticmethod
+    def backward(ctx, qx, qg, qb):
+        gy, x, g, b, st = ctx.saved_tensors
+        n, w = x.shape
+        npart = _ln_parts(n)
+        qx = None if qx is None else qx.contiguous()
+        qg = None if qg is None else qg.contiguous()
+        qb = None if qb is None else qb.contiguous()
+        dgy, dx = torch.empty_like(x), torch.empty_like(x)
+        pg, pb = x.new_empty(npart, w), x.new_empty(npart, w)
+        _lib.call("e2v2_ln_silu_bwd2", _p(x), _p(g), _p(b), _p(st), _p(gy), _p(qx), _p(qg), _p(qb), _p(dgy),
+                  _p(dx), _p(pg), _p(pb), _lib.i32(n), _lib.i32(w), _lib.i32(npart), sparse_ops._stream(x.device))
+        return dgy, dx, pg.sum(0), pb.sum(0), None
+
+
+def ln_silu(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
+    """silu(ln(x)) over the last dimension through _LNSiLUFn."""
+    w = x.shape[-1]
+    sparse_ops._need_gpu(x)
+    if (x.dtype != torch.float32 or tuple(ln.normalized_shape) != (w,) or w not in _LN_WIDTHS
+            or ln.weight is None or ln.bias is None):
+        raise ValueError(f"ln_silu: fp32 rows of width {_LN_WIDTHS} with an affine LayerNorm, got "
+                         f"{tuple(x.shape)} {x.dtype}")
+    y = _LNSiLUFn.apply(x.reshape(-1, w).contiguous(), ln.weight, ln.bias, float(ln.eps))
+    return y.view(x.shape)
+
+
+def run_seq(mods, h: torch.Tensor) -> torch.Tensor:
+    """nn.Sequential over mods with each nn.LayerNorm + nn.SiLU pair as ln_silu."""
+    mods = list(mods) if isinstance(mods, (nn.Sequential, list, tuple)) else [mods]
+    i = 0
+    while i < len(mods):
+        if isinstance(mods[i], nn.LayerNorm) and i + 1 < len(mods) and isinstance(mods[i + 1], nn.SiLU):
+            h = ln_silu(mods[i], h)
+            i += 2
+        else:
+            h = mods[i](h)
+            i += 1
+    return h
 
 
 def _cartesian(device) -> torch.Tensor:
@@ -62,7 +173,7 @@ def so3_linear(mod, x: torch.Tensor) -> torch.Tensor:
     bias on row 0."""
     w = mod.weight.index_select(0, _expand(mod.lmax, x.device))          # [9, Cout, Cin]
     out = torch.matmul(x, w.transpose(1, 2))
-    return torch.cat([out[:1] + mod.bias, out[1:]], dim=0)
+    return out + _row0(out.shape[0], out) * mod.bias.reshape(-1)
 
 
 def so3_linear2scalar(mod, x: torch.Tensor) -> torch.Tensor:
@@ -71,36 +182,35 @@ def so3_linear2scalar(mod, x: torch.Tensor) -> torch.Tensor:
     final_linear."""
     e = _expand(mod.lmax, x.device)
     a = torch.matmul(x, mod.weight.index_select(0, e).transpose(1, 2))
-    a = torch.cat([a[:1] + mod.bias.reshape(-1), a[1:]], dim=0)
+    a = a + _row0(a.shape[0], a) * mod.bias.reshape(-1)
     b = torch.matmul(x, mod.weight2.index_select(0, e).transpose(1, 2))
-    h = torch.cat([(a[l * l:(l + 1) ** 2] * b[l * l:(l + 1) ** 2]).sum(0) for l in range(mod.lmax + 1)], dim=-1)
-    return mod.final_linear(h)
+    ab = (a * b).split([2 * l + 1 for l in range(mod.lmax + 1)], dim=0)
+    return run_seq(mod.final_linear, torch.cat([p.sum(0) for p in ab], dim=-1))
 
 
 def rms_norm(mod, x: torch.Tensor) -> torch.Tensor:
     """EquivariantRMSNormArraySphericalHarmonicsV2_BL (module_utils.py:1663-1772):
     row 0 centred over the channels, the degree-balanced mean square over rows
     and channels, the affine weight of each row's degree, the bias on row 0."""
-    f0 = x[:1] - x[:1].mean(dim=2, keepdim=True)
-    f = torch.cat([f0, x[1:]], dim=0)
+    r0 = _row0(x.shape[0], x)
+    f = x - x.mean(dim=2, keepdim=True) * r0
     bw = mod.balance_degree_weight.view(-1, 1, 1).to(x.dtype)
     fn = (f.pow(2) * bw).sum(0, keepdim=True).mean(dim=2, keepdim=True)
     fn = (fn + mod.eps).pow(-0.5)
     w = mod.affine_weight.index_select(0, _expand(mod.lmax, x.device)).unsqueeze(1)
-    out = f * (fn * w)
-    return torch.cat([out[:1] + mod.affine_bias, out[1:]], dim=0)
+    return f * (fn * w) + r0 * mod.affine_bias.reshape(-1)
 
 
 def gate_s3(mod, x: torch.Tensor, silu_norm: float, sigmoid_norm: float) -> torch.Tensor:
     """Gate_s3 (module_utils.py:2694-2746): logits from row 0, SiLU on row 0,
     the sigmoid of each degree's logits on its rows."""
-    C = mod.sphere_channels
-    sc = mod.gates(x[0])
-    rows = [F.silu(sc[:, :C]) * silu_norm]
-    for m in range(1, x.shape[0]):
-        l = int(math.isqrt(m))
-        rows.append(torch.sigmoid(sc[:, l * C:(l + 1) * C]) * sigmoid_norm * x[m])
-    return torch.stack(rows, dim=0)
+    C, n, N = mod.sphere_channels, x.shape[0], x.shape[1]
+    lmax = math.isqrt(n) - 1
+    x0, xr = x.split([1, n - 1], dim=0)
+    s0, sr = mod.gates(x0.squeeze(0)).split([C, lmax * C], dim=1)
+    g = torch.sigmoid(sr).view(N, lmax, C).transpose(0, 1)                # [lmax, N, C]
+    g = g.index_select(0, _expand(lmax, x.device)[1:] - 1)                # row m <- its degree
+    return torch.cat([(F.silu(s0) * silu_norm).unsqueeze(0), g * sigmoid_norm * xr], dim=0)
 
 
 def ffn(mod, x: torch.Tensor, silu_norm: float, sigmoid_norm: float) -> torch.Tensor:
@@ -198,7 +308,7 @@ class EdgeInput:
         h = self.rbf @ W[:, :K].t() + ht[e.qi] + hs[e.nj]
         if lin1.bias is not None:
             h = h + lin1.bias
-        return net[1:](h)
+        return run_seq(net[1:], h)
 
 
 def attention_weights(logit, p, ih, edges: TrainEdges, form: str) -> torch.Tensor:
@@ -241,8 +351,8 @@ def qkdot_gate(ga, x: torch.Tensor, edges: TrainEdges, x_edge: EdgeInput):
         return gate, x_edge(ga.fc_easy).reshape(-1, H)
     lxs = _raw_sh(edges.dvec)                                                # [E, 9]
     x0 = torch.einsum("lec,el,ls->esc", xq, lxs, ga.sum_vec.to(xq.dtype)).reshape(xq.shape[1], -1)[:, :H]
-    eg = x_edge(ga.fc_easy)
-    return ga.direction_linear(x0 * eg[:, H:]), eg[:, :H]
+    ih, eg = x_edge(ga.fc_easy).split([H, x0.shape[1]], dim=1)
+    return run_seq(ga.direction_linear, x0 * eg), ih
 
 
 def so2_forward_linear(tp, so2: torch.Tensor) -> torch.Tensor:
@@ -254,12 +364,12 @@ def so2_forward_linear(tp, so2: torch.Tensor) -> torch.Tensor:
     if sc is not None:
         so2 = so2 * sc.view(-1, 1, 1).to(so2.dtype)
     N = so2.shape[1]
-    outs, st = [], 0
-    for idx, (l3, cnt) in enumerate(tp.l3_sequential):
+    outs = []
+    parts = so2.split([cnt * (2 * l3 + 1) for l3, cnt in tp.l3_sequential], dim=0)
+    for idx, ((l3, cnt), part) in enumerate(zip(tp.l3_sequential, parts)):
         nr = 2 * l3 + 1
-        blk = so2[st:st + cnt * nr].reshape(cnt, nr, N, -1).permute(1, 2, 0, 3).reshape(nr, N, -1)
+        blk = part.reshape(cnt, nr, N, -1).permute(1, 2, 0, 3).reshape(nr, N, -1)
         outs.append(tp.out_linear[idx](blk))
-        st += cnt * nr
     return torch.cat(outs, dim=0) * tp.path_norm.view(-1, 1, 1).to(so2.dtype)
 
 
@@ -271,7 +381,7 @@ def attention(ga, x: torch.Tensor, edges: TrainEdges, rbf: torch.Tensor) -> torc
     x_edge = edges.edge_input(ga.target_embedding, ga.source_embedding, rbf)
     if ga.tp_type == "QK_alpha":
         eg = x_edge(ga.fc_easy)
-        gate, ih = eg[:, :H], eg[:, H:]
+        gate, ih = eg.split([H, eg.shape[1] - H], dim=1)
     else:
         gate, ih = qkdot_gate(ga, x, edges, x_edge)
     qk = edges.qk(q / math.sqrt(q.shape[-1]), k)
@@ -285,9 +395,9 @@ def attention(ga, x: torch.Tensor, edges: TrainEdges, rbf: torch.Tensor) -> torc
         return so3_linear(ga.proj_zero, agg)
     w = alpha / edges.dist.clamp_min(1e-6).unsqueeze(-1)
     T = _cartesian(x.device)
-    so2 = 0
+    so2, dv = 0, edges.dvec.unbind(1)
     for kk in range(3):
-        a = edges.v_agg(vh, w * edges.dvec[:, kk:kk + 1]).reshape(N, -1, C)  # [N, 9, C]
+        a = edges.v_agg(vh, w * dv[kk].unsqueeze(-1)).reshape(N, -1, C)     # [N, 9, C]
         so2 = so2 + torch.einsum("tr,nrc->tnc", T[:, :, kk], a)
     return so3_linear(ga.proj_first, so2_forward_linear(ga.first_order_tp.so2_tp, so2))
 
@@ -311,7 +421,7 @@ def block(blk, x: torch.Tensor, edges: TrainEdges, rbf: torch.Tensor, sys_node, 
     """TransBlock.forward (e2former.py:600-620): pre-norm residual attention and FFN."""
     h = rms_norm(blk.norm_1, x)
     if sys_node is not None:
-        h = torch.cat([(h[0] + sys_node).unsqueeze(0), h[1:]], dim=0)
+        h = h + _row0(h.shape[0], h) * sys_node
     x = x + attention(blk.ga, h, edges, rbf)
     return x + ffn(blk.ffn, rms_norm(blk.norm_ffn, x), *norms)
 
