@@ -132,6 +132,79 @@ class _LNSiLUGradFn(torch.autograd.Function):
         return dgy, dx, pg.sum(0), pb.sum(0), None
 
 
+_EDGE_ROWS = 16384   # rows from which a Linear takes the split-K weight gradient
+
+
+def _will_run(node) -> bool:
+    """Whether the running backward needs the gradient flowing into node (False
+    only when the engine reports that it will not execute it: autograd.grad of
+    other inputs, as the forces' first differentiation)."""
+    if node is None:
+        return False
+    try:
+        return bool(torch._C._will_engine_execute_node(node))
+    except (AttributeError, RuntimeError):
+        return True
+
+
+def _splitk_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a^T b for a [E, m], b [E, n] with E >> m, n: s batched partial products
+    over row blocks, summed (one GEMM with K = E leaves most of the chip idle)."""
+    a, b = a.contiguous(), b.contiguous()
+    E = a.shape[0]
+    s = max(1, min(32, E // 2048))
+    if s == 1:
+        return a.t() @ b
+    E0 = E // s * s
+    out = torch.bmm(a[:E0].view(s, E0 // s, -1).transpose(1, 2), b[:E0].view(s, E0 // s, -1)).sum(0)
+    if E0 < E:
+        out = out + a[E0:].t() @ b[E0:]
+    return out
+
+
+class _EdgeLinearFn(torch.autograd.Function):
+    """y = x W^T (+ b) on per-edge rows x [E, k] (the nn.Linear layers of the
+    RadialProfile nets, module_utils.py:2151-2178) with gradients of any order:
+    the input gradient is this function again (gy W), the weight gradient the
+    split-K _EdgeWGradFn, skipped when the running backward does not need it."""
+
+    @staticmethod
+    def forward(ctx, x, W, b):
+        ctx.save_for_backward(x, W)
+        ctx.has_b = b is not None
+        return torch.addmm(b, x, W.t()) if b is not None else x @ W.t()
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, W = ctx.saved_tensors
+        nxt = ctx.next_functions
+        gx = _EdgeLinearFn.apply(gy, W.t(), None) if ctx.needs_input_grad[0] else None
+        gW = _EdgeWGradFn.apply(gy, x) if ctx.needs_input_grad[1] and _will_run(nxt[1][0]) else None
+        gb = gy.sum(0) if ctx.has_b and ctx.needs_input_grad[2] and _will_run(nxt[2][0]) else None
+        return gx, gW, gb
+
+
+class _EdgeWGradFn(torch.autograd.Function):
+    """a^T b over the edge rows (split-K); gradients b Q^T and a Q."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        ctx.save_for_backward(a, b)
+        return _splitk_tn(a, b)
+
+    @staticmethod
+    def backward(ctx, Q):
+        a, b = ctx.saved_tensors
+        ga = _EdgeLinearFn.apply(b, Q, None) if ctx.needs_input_grad[0] else None
+        gb = _EdgeLinearFn.apply(a, Q.t(), None) if ctx.needs_input_grad[1] else None
+        return ga, gb
+
+
+def edge_linear(lin: nn.Linear, x: torch.Tensor) -> torch.Tensor:
+    """lin(x) on per-edge rows through _EdgeLinearFn."""
+    return _EdgeLinearFn.apply(x, lin.weight, lin.bias)
+
+
 def ln_silu(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
     """silu(ln(x)) over the last dimension through _LNSiLUFn."""
     w = x.shape[-1]
@@ -145,13 +218,17 @@ def ln_silu(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
 
 
 def run_seq(mods, h: torch.Tensor) -> torch.Tensor:
-    """nn.Sequential over mods with each nn.LayerNorm + nn.SiLU pair as ln_silu."""
+    """nn.Sequential over mods with each nn.LayerNorm + nn.SiLU pair as ln_silu and
+    each nn.Linear on at least _EDGE_ROWS rows as edge_linear."""
     mods = list(mods) if isinstance(mods, (nn.Sequential, list, tuple)) else [mods]
     i = 0
     while i < len(mods):
         if isinstance(mods[i], nn.LayerNorm) and i + 1 < len(mods) and isinstance(mods[i + 1], nn.SiLU):
             h = ln_silu(mods[i], h)
             i += 2
+        elif isinstance(mods[i], nn.Linear) and h.dim() == 2 and h.shape[0] >= _EDGE_ROWS:
+            h = edge_linear(mods[i], h)
+            i += 1
         else:
             h = mods[i](h)
             i += 1
@@ -269,6 +346,14 @@ class TrainEdges:
         return EdgeInput(self, tgt_emb, src_emb, rbf)
 
 
+    def gather_q(self, x: torch.Tensor) -> torch.Tensor:
+        """x [N, F] -> x[qi] [E, F] (gradient: the sum over each query row's edges)."""
+        return sparse_ops.sparse_gather_edge_index(x, self.row32, self.N, (self.md[0], self.md[2]))
+
+    def gather_k(self, x: torch.Tensor) -> torch.Tensor:
+        """x [N, F] -> x[nj] [E, F] (gradient: the sum over each source atom's edges)."""
+        return sparse_ops.sparse_gather_edge_index(x, self.col32, self.N, (self.md[3], self.md[5]))
+
     def qk(self, q: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
         return sparse_ops.sparse_qk_edge_index_triton(q, k, self.row32, self.col32, metadata=self.md)
 
@@ -305,9 +390,7 @@ class EdgeInput:
         e = self.edges
         ht = self.tgt(e.Z) @ W[:, K:K + ne].t()                  # [N, hidden] per atom
         hs = self.src(e.Z) @ W[:, K + ne:K + 2 * ne].t()
-        h = self.rbf @ W[:, :K].t() + ht[e.qi] + hs[e.nj]
-        if lin1.bias is not None:
-            h = h + lin1.bias
+        h = _EdgeLinearFn.apply(self.rbf, W[:, :K], lin1.bias) + e.gather_q(ht) + e.gather_k(hs)
         return run_seq(net[1:], h)
 
 
@@ -323,9 +406,9 @@ def attention_weights(logit, p, ih, edges: TrainEdges, form: str) -> torch.Tenso
     idx = edges.qi.view(-1, 1).expand(-1, H)
     amax = torch.full((edges.N, H), -torch.inf, dtype=logit.dtype, device=logit.device)
     amax = amax.scatter_reduce(0, idx, logit, reduce="amax", include_self=True)
-    e = torch.exp(logit - amax[edges.qi]) * p.unsqueeze(-1)
+    e = torch.exp(logit - edges.gather_q(amax)) * p.unsqueeze(-1)
     s = edges.row_sum(e)
-    return e * ih / (s[edges.qi] + 1e-3)
+    return e * ih / (edges.gather_q(s) + 1e-3)
 
 
 def _sh_integral(v: torch.Tensor) -> torch.Tensor:

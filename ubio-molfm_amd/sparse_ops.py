@@ -353,6 +353,23 @@ def sparse_alpha_sum_edge_index_triton(alpha, query_index, num_queries, metadata
 sparse_alpha_sum_edge_index = sparse_alpha_sum_edge_index_triton
 
 
+def sparse_gather_edge_index(x, index, num_rows, metadata):
+    """x [num_rows, F] -> out [E, F], out[e] = x[index[e]], whose gradient sums
+    the edges of each row by the segments metadata = (row_ptr, edge ids in
+    segment order) of index (e2v2_gather_rows forward, e2v2_seg_reduce backward,
+    each the other's gradient to any order): the per-edge gathers of the
+    RadialProfile input (e2former.py:258-266, the tgt[z_i] and src[z_j] blocks)
+    without torch's sort-based index backward."""
+    _need_gpu(x, index)
+    if x.ndim != 2 or x.shape[0] != num_rows:
+        raise ValueError(f"x {tuple(x.shape)} must be [{num_rows}, F]")
+    row_ptr, alpha_index = metadata
+    A = _AlphaLayout(row_ptr, alpha_index, index, num_rows, index.numel())
+    if torch.is_grad_enabled() and x.requires_grad:
+        return _GatherRowsFn.apply(x.float(), A).to(x.dtype)
+    return _gather_rows(A, x).to(x.dtype)
+
+
 # ---------------------------------------------------------------------------
 # edge_degree_outer_triton (edge_degree_outer_autograd.py:299-375)
 # ---------------------------------------------------------------------------
