@@ -408,7 +408,7 @@ def attention_weights(logit, p, ih, edges: TrainEdges, form: str) -> torch.Tenso
     amax = amax.scatter_reduce(0, idx, logit, reduce="amax", include_self=True)
     e = torch.exp(logit - edges.gather_q(amax)) * p.unsqueeze(-1)
     s = edges.row_sum(e)
-    return e * ih / (edges.gather_q(s) + 1e-3)
+    return e * ih * edges.gather_q(1.0 / (s + 1e-3))       # the reciprocal per row, not per edge
 
 
 def _sh_integral(v: torch.Tensor) -> torch.Tensor:
@@ -476,11 +476,10 @@ def attention(ga, x: torch.Tensor, edges: TrainEdges, rbf: torch.Tensor) -> torc
     if ga.attn_type == "zero-order":
         agg = edges.v_agg(vh, alpha).reshape(N, -1, C).permute(1, 0, 2)      # [9, N, C]
         return so3_linear(ga.proj_zero, agg)
-    w = alpha / edges.dist.clamp_min(1e-6).unsqueeze(-1)
     T = _cartesian(x.device)
-    so2, dv = 0, edges.dvec.unbind(1)
+    so2, u = 0, (edges.dvec / edges.dist.clamp_min(1e-6).unsqueeze(-1)).unbind(1)   # alpha / d * dvec_k
     for kk in range(3):
-        a = edges.v_agg(vh, w * dv[kk].unsqueeze(-1)).reshape(N, -1, C)     # [N, 9, C]
+        a = edges.v_agg(vh, alpha * u[kk].unsqueeze(-1)).reshape(N, -1, C)    # [N, 9, C]
         so2 = so2 + torch.einsum("tr,nrc->tnc", T[:, :, kk], a)
     return so3_linear(ga.proj_first, so2_forward_linear(ga.first_order_tp.so2_tp, so2))
 
