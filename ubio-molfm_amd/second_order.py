@@ -205,25 +205,35 @@ def edge_linear(lin: nn.Linear, x: torch.Tensor) -> torch.Tensor:
     return _EdgeLinearFn.apply(x, lin.weight, lin.bias)
 
 
+def ln_silu_fusable(ln: nn.LayerNorm, x: torch.Tensor) -> bool:
+    """Whether _LNSiLUFn takes silu(ln(x)): fp32 GPU rows of a width the kernels
+    are built for and an affine LayerNorm over that width with fp32 parameters."""
+    w = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.float32 and tuple(ln.normalized_shape) == (w,) and w in _LN_WIDTHS
+            and ln.weight is not None and ln.bias is not None and ln.weight.dtype == torch.float32
+            and ln.bias.dtype == torch.float32 and ln.weight.is_contiguous() and ln.bias.is_contiguous())
+
+
 def ln_silu(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
     """silu(ln(x)) over the last dimension through _LNSiLUFn."""
-    w = x.shape[-1]
     sparse_ops._need_gpu(x)
-    if (x.dtype != torch.float32 or tuple(ln.normalized_shape) != (w,) or w not in _LN_WIDTHS
-            or ln.weight is None or ln.bias is None):
-        raise ValueError(f"ln_silu: fp32 rows of width {_LN_WIDTHS} with an affine LayerNorm, got "
+    if not ln_silu_fusable(ln, x):
+        raise ValueError(f"ln_silu: fp32 rows of width {_LN_WIDTHS} with an fp32 affine LayerNorm, got "
                          f"{tuple(x.shape)} {x.dtype}")
+    w = x.shape[-1]
     y = _LNSiLUFn.apply(x.reshape(-1, w).contiguous(), ln.weight, ln.bias, float(ln.eps))
     return y.view(x.shape)
 
 
 def run_seq(mods, h: torch.Tensor) -> torch.Tensor:
-    """nn.Sequential over mods with each nn.LayerNorm + nn.SiLU pair as ln_silu and
-    each nn.Linear on at least _EDGE_ROWS rows as edge_linear."""
+    """nn.Sequential over mods with each nn.LayerNorm + nn.SiLU pair as ln_silu (where
+    ln_silu_fusable; other widths run the two modules) and each nn.Linear on at
+    least _EDGE_ROWS rows as edge_linear."""
     mods = list(mods) if isinstance(mods, (nn.Sequential, list, tuple)) else [mods]
     i = 0
     while i < len(mods):
-        if isinstance(mods[i], nn.LayerNorm) and i + 1 < len(mods) and isinstance(mods[i + 1], nn.SiLU):
+        if (isinstance(mods[i], nn.LayerNorm) and i + 1 < len(mods) and isinstance(mods[i + 1], nn.SiLU)
+                and ln_silu_fusable(mods[i], h)):
             h = ln_silu(mods[i], h)
             i += 2
         elif isinstance(mods[i], nn.Linear) and h.dim() == 2 and h.shape[0] >= _EDGE_ROWS:
