@@ -458,6 +458,18 @@ int e2v2_add_rmsnorm_fwd(const float* x, const float* delta, const float* w, con
 /* gx = d(rms_norm_sh)/dx^T gy (+ gres when gres is not NULL: the gradient of a residual branch that reads x) */
 int e2v2_rmsnorm_bwd(const float* x, const float* w, const float* gy, const float* gres, float* gx, int n, float eps,
                      hipStream_t s);
+/* rms_norm_sh on the training path (the reference's norm under torch's double backward, e2former.py:600-620
+   with AutoGradForce's create_graph=True).  _bwd_param: gx as e2v2_rmsnorm_bwd plus the affine gradients as
+   per-workgroup partial sums part [n_part][4][256] (rows dw_0, dw_1, dw_2, db; the caller sums the n_part
+   blocks).  _bwd2: the derivative of that first-order pass given the upstream gradients qx [9][n][256],
+   qw [3][256], qb [256] of (gx, dw, db) (each may be NULL: zero): dgy, dx [9][n][256] and the partial sums of
+   the weight gradient part [n_part][3][256] (the bias does not enter the first-order pass).
+   0 < n_part <= 65535 workgroups, nodes strided over them. */
+int e2v2_rmsnorm_bwd_param(const float* x, const float* w, const float* gy, float* gx, float* part, int n, int n_part,
+                           float eps, hipStream_t s);
+int e2v2_rmsnorm_bwd2(const float* x, const float* w, const float* gy, const float* qx, const float* qw,
+                      const float* qb, float* dgy, float* dx, float* part, int n, int n_part, float eps,
+                      hipStream_t s);
 /* Gate_s3 activation (module_utils.py:2694-2746) from gate logits sc [N][768];
  * k1, k2 = normalize2mom constants of SiLU and sigmoid */
 int e2v2_gate_fwd(const float* sc, const float* x, float* y, int n, float k1, float k2, hipStream_t s);

@@ -216,6 +216,43 @@ def test_ln_silu_second_order(pkg, cuda, w):
         assert err < (1e-5 if k < 4 else 1e-4), (names[k], err)
 
 
+def test_rms_norm_second_order(pkg, cuda):
+    """The fused rms_norm_sh of the training path (e2v2_rmsnorm_fwd / _bwd_param /
+    _bwd2) against the float64 composition on the CPU: values and the first-order
+    gradients of x, the affine weight and bias (1e-5 relative L2), then the
+    gradients of L = <gx, R0> + <dw, R1> + <db, R2> in x, the weight and the
+    upstream gy (1e-4).  More nodes than workgroups (1,024): some workgroups
+    stride over two nodes."""
+    import copy
+    from ubio_molfm_amd import modules
+    from ubio_molfm_amd import second_order as so
+    torch.manual_seed(5)
+    mod = modules.EquivariantRMSNormArraySphericalHarmonicsV2_BL(2, 256).to(cuda)
+    with torch.no_grad():
+        mod.affine_weight.normal_(1.0, 0.3)
+        mod.affine_bias.normal_(0.0, 0.5)
+    N = 1500 + 37
+    x = torch.randn(9, N, 256, device=cuda) * 1.3
+    x[0] += 0.7
+    gy = torch.randn_like(x)
+    R = [torch.randn_like(x), torch.randn(3, 256, device=cuda), torch.randn(256, device=cuda)]
+
+    def run(m, dtype, dev):
+        xx = x.to(dev, dtype).requires_grad_(True)
+        gg = gy.to(dev, dtype).requires_grad_(True)
+        y = so.rms_norm(m, xx)
+        gx, dw, db = torch.autograd.grad(y, (xx, m.affine_weight, m.affine_bias), gg, create_graph=True)
+        L = sum((t * r.to(dev, dtype)).sum() for t, r in zip((gx, dw, db), R))
+        return [y, gx, dw, db] + list(torch.autograd.grad(L, (xx, m.affine_weight, gg)))
+
+    got = run(mod, torch.float32, cuda)
+    ref = run(copy.deepcopy(mod).double().cpu(), torch.float64, "cpu")
+    names = ["y", "gx", "dw", "db", "d2x", "d2w", "d2gy"]
+    for k, (a, r) in enumerate(zip(got, ref)):
+        err = _rel(a, r)
+        assert err < (1e-5 if k < 4 else 1e-4), (names[k], err)
+
+
 def test_eval_mode_keeps_the_fused_path(pkg, cuda):
     """eval(): the fused kernels run (their backward is first order, so a
     create_graph=True differentiation raises instead of silently dropping the

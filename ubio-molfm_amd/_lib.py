@@ -19,7 +19,7 @@ EXPORTS = [
     "e2v2_radial_hidden_table", "e2v2_radial_hidden_table_check",
     "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_attn_bwd_workspace", "e2v2_deg_fwd", "e2v2_deg_bwd",
     "e2v2_deg_bwd_workspace", "e2v2_deg_hidden_fwd", "e2v2_deg_hidden_bwd", "e2v2_deg_bias_grad",
-    "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_gate_fwd",
+    "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_rmsnorm_bwd_param", "e2v2_rmsnorm_bwd2", "e2v2_gate_fwd",
     "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd", "e2v2_ln_silu_bwd_param", "e2v2_ln_silu_bwd2",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd", "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd",
     "e2v2_qk_proj_fwd_bf16", "e2v2_qk_proj_bwd_bf16",

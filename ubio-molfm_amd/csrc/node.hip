@@ -155,9 +155,168 @@ __global__ void k_gate_bwd(const float* __restrict__ sc, const float* __restrict
   gs[2 * kNC + c] = a2 * k2 * sg2 * (1.0f - sg2);
 }
 
+// ---- rms_norm_sh on the training path, where the forces are differentiated once more.  Per node
+// (f = x with row 0 centred over the channels, r = (S + eps)^-1/2, S = <bal f^2> over the channels and
+// summed over the rows, P = gy w, C = 256):
+//   first order   gx = centred_0(r P - (r^3 / C) (sum P f) bal f), dw_l = sum_nodes sum_{m in l} gy f r,
+//                 db = sum_nodes gy_0;
+//   second order  (upstream qx, qw, qb on gx, dw, db; q = centred_0(qx), Qw = qw of the row's degree,
+//                 A = sum q P, B = sum q bal f, G = sum P f, T = sum gy Qw f, k = r^3 / C)
+//                 u = r q - k B f,  dgy = w u + r Qw f + [m = 0] qb,  d(w)_l = sum_nodes sum_{m in l} gy u,
+//                 dx = centred_0(-k (P B + G q bal) + r gy Qw - (A - 3 r^2 G B / C + T) k bal f).
+// One workgroup per node (thread = channel), nodes strided over n_part workgroups; each writes its
+// parameter sums to part [n_part][4 or 3][256] (summed over workgroups by the caller, in fixed order).
+template <int K>
+__device__ __forceinline__ void block_sums256(float (&v)[K], float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = wave_sum(v[k]);
+  __syncthreads();
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) red[wave * K + k] = v[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = red[k] + red[K + k] + red[2 * K + k] + red[3 * K + k];
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd_param(const float* __restrict__ x, const float* __restrict__ w,
+                                                           const float* __restrict__ gy, float* __restrict__ gx,
+                                                           float* __restrict__ part, int n, float eps) {
+  __shared__ float red[4];
+  const int c = threadIdx.x;
+  const size_t st = (size_t)n * kNC;
+  float aw[3] = {0.f, 0.f, 0.f}, ab = 0.f;
+  for (int i = blockIdx.x; i < n; i += gridDim.x) {
+    const float* xp = x + (size_t)i * kNC + c;
+    const float* gp = gy + (size_t)i * kNC + c;
+    float f[9], g[9];
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      f[m] = xp[m * st];
+      g[m] = gp[m * st];
+    }
+    ab += g[0];
+    const float mean0 = block_sum256(f[0], red) * (1.0f / kNC);
+    f[0] -= mean0;
+    float ss = 0.f, dr = 0.f;
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      ss = fmaf(bal(m), f[m] * f[m], ss);
+      dr = fmaf(g[m] * w[lof(m) * kNC + c], f[m], dr);
+    }
+    const float S = block_sum256(ss, red) * (1.0f / kNC);
+    const float DR = block_sum256(dr, red);
+    const float r = 1.0f / sqrtf(S + eps);
+    const float dS = -0.5f * r * r * r * DR;
+    float gf[9];
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      aw[lof(m)] = fmaf(g[m], f[m] * r, aw[lof(m)]);
+      gf[m] = (g[m] * w[lof(m) * kNC + c]) * r + dS * 2.0f * bal(m) * f[m] * (1.0f / kNC);
+    }
+    const float gmean0 = block_sum256(gf[0], red) * (1.0f / kNC);
+    gf[0] -= gmean0;
+    float* op = gx + (size_t)i * kNC + c;
+#pragma unroll
+    for (int m = 0; m < 9; ++m) op[m * st] = gf[m];
+  }
+  float* pp = part + (size_t)blockIdx.x * 4 * kNC + c;
+  pp[0] = aw[0];
+  pp[kNC] = aw[1];
+  pp[2 * kNC] = aw[2];
+  pp[3 * kNC] = ab;
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd2(const float* __restrict__ x, const float* __restrict__ w,
+                                                      const float* __restrict__ gy, const float* __restrict__ qx,
+                                                      const float* __restrict__ qw, const float* __restrict__ qb,
+                                                      float* __restrict__ dgy, float* __restrict__ dx,
+                                                      float* __restrict__ part, int n, float eps) {
+  __shared__ float red[4 * 4];
+  const int c = threadIdx.x;
+  const size_t st = (size_t)n * kNC;
+  float wc[3], qwc[3], aw[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    wc[l] = w[l * kNC + c];
+    qwc[l] = qw ? qw[l * kNC + c] : 0.f;
+  }
+  const float qbc = qb ? qb[c] : 0.f;
+  for (int i = blockIdx.x; i < n; i += gridDim.x) {
+    const size_t base = (size_t)i * kNC + c;
+    float f[9], g[9], q[9];
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      f[m] = x[base + m * st];
+      g[m] = gy[base + m * st];
+      q[m] = qx ? qx[base + m * st] : 0.f;
+    }
+    float mv[2] = {f[0], q[0]};
+    block_sums256<2>(mv, red);
+    f[0] -= mv[0] * (1.0f / kNC);
+    q[0] -= mv[1] * (1.0f / kNC);
+    float sv[4] = {0.f, 0.f, 0.f, 0.f};   // S, then A, B, G, T
+    float ss = 0.f;
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      const int l = lof(m);
+      const float P = g[m] * wc[l];
+      ss = fmaf(bal(m), f[m] * f[m], ss);
+      sv[0] = fmaf(q[m], P, sv[0]);
+      sv[1] = fmaf(q[m] * bal(m), f[m], sv[1]);
+      sv[2] = fmaf(P, f[m], sv[2]);
+      sv[3] = fmaf(g[m] * qwc[l], f[m], sv[3]);
+    }
+    block_sums256<4>(sv, red);
+    const float S = block_sum256(ss, red) * (1.0f / kNC);
+    const float r = 1.0f / sqrtf(S + eps);
+    const float A = sv[0], B = sv[1], G = sv[2], T = sv[3];
+    const float k3 = r * r * r * (1.0f / kNC);
+    const float dLdr = A - 3.0f * r * r * (1.0f / kNC) * G * B + T;
+    float Gf[9];
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      const int l = lof(m);
+      const float P = g[m] * wc[l];
+      const float u = r * q[m] - k3 * B * f[m];
+      dgy[base + m * st] = wc[l] * u + r * qwc[l] * f[m] + (m == 0 ? qbc : 0.f);
+      aw[l] = fmaf(g[m], u, aw[l]);
+      Gf[m] = -k3 * (P * B + G * q[m] * bal(m)) + r * g[m] * qwc[l] - dLdr * k3 * bal(m) * f[m];
+    }
+    const float gm0 = block_sum256(Gf[0], red) * (1.0f / kNC);
+    Gf[0] -= gm0;
+#pragma unroll
+    for (int m = 0; m < 9; ++m) dx[base + m * st] = Gf[m];
+  }
+  float* pp = part + (size_t)blockIdx.x * 3 * kNC + c;
+  pp[0] = aw[0];
+  pp[kNC] = aw[1];
+  pp[2 * kNC] = aw[2];
+}
+
 }  // namespace e2v2
 
 using namespace e2v2;
+
+E2V2_API int e2v2_rmsnorm_bwd_param(const float* x, const float* w, const float* gy, float* gx, float* part, int n,
+                                    int n_part, float eps, hipStream_t s) {
+  E2V2_REQUIRE(n >= 0 && n_part > 0 && n_part <= 65535, "rmsnorm_bwd_param: n %d, n_part %d", n, n_part);
+  hipLaunchKernelGGL(e2v2::k_rmsnorm_bwd_param, dim3((unsigned)n_part), dim3(256), 0, s, x, w, gy, gx, part, n, eps);
+  E2V2_LAUNCHED("k_rmsnorm_bwd_param");
+  return 0;
+}
+
+E2V2_API int e2v2_rmsnorm_bwd2(const float* x, const float* w, const float* gy, const float* qx, const float* qw,
+                               const float* qb, float* dgy, float* dx, float* part, int n, int n_part, float eps,
+                               hipStream_t s) {
+  E2V2_REQUIRE(n >= 0 && n_part > 0 && n_part <= 65535, "rmsnorm_bwd2: n %d, n_part %d", n, n_part);
+  hipLaunchKernelGGL(e2v2::k_rmsnorm_bwd2, dim3((unsigned)n_part), dim3(256), 0, s, x, w, gy, qx, qw, qb, dgy, dx,
+                     part, n, eps);
+  E2V2_LAUNCHED("k_rmsnorm_bwd2");
+  return 0;
+}
 
 E2V2_API int e2v2_rmsnorm_fwd(const float* x, const float* w, const float* b, float* y, int n, float eps,
                               hipStream_t s) {

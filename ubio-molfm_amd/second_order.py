@@ -275,10 +275,74 @@ def so3_linear2scalar(mod, x: torch.Tensor) -> torch.Tensor:
     return run_seq(mod.final_linear, torch.cat([p.sum(0) for p in ab], dim=-1))
 
 
+class _RMSNormFn(torch.autograd.Function):
+    """rms_norm_sh on x [9, N, 256] (e2v2_rmsnorm_fwd; the module's balance weights
+    are the kernels' 1 / ((2l + 1)(lmax + 1))); its backward is _RMSNormGradFn,
+    differentiable once more, in place of the composed norm's double backward."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, eps: float):
+        n = x.shape[1]
+        y = torch.empty_like(x)
+        _lib.call("e2v2_rmsnorm_fwd", _p(x), _p(w), _p(b), _p(y), _lib.i32(n), _lib.f32(eps),
+                  sparse_ops._stream(x.device))
+        ctx.save_for_backward(x, w)
+        ctx.eps = eps
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        gx, gw, gb = _RMSNormGradFn.apply(gy, x, w, ctx.eps)
+        return gx, gw, gb, None
+
+
+def _rms_parts(n: int) -> int:
+    return max(1, min(n, 1024))
+
+
+class _RMSNormGradFn(torch.autograd.Function):
+    """(gx, dw, db) of _RMSNormFn given gy (e2v2_rmsnorm_bwd_param); its backward
+    is e2v2_rmsnorm_bwd2."""
+
+    @staticmethod
+    def forward(ctx, gy, x, w, eps: float):
+        gy = gy.contiguous()
+        n = x.shape[1]
+        npart = _rms_parts(n)
+        gx = torch.empty_like(x)
+        part = x.new_empty(npart, 4, x.shape[2])
+        _lib.call("e2v2_rmsnorm_bwd_param", _p(x), _p(w), _p(gy), _p(gx), _p(part), _lib.i32(n), _lib.i32(npart),
+                  _lib.f32(eps), sparse_ops._stream(x.device))
+        ctx.save_for_backward(gy, x, w)
+        ctx.eps = eps
+        ctx.set_materialize_grads(False)
+        p = part.sum(0)
+        return gx, p[:3].contiguous(), p[3].contiguous()
+
+    @staticmethod
+    def backward(ctx, qx, qw, qb):
+        gy, x, w = ctx.saved_tensors
+        n = x.shape[1]
+        npart = _rms_parts(n)
+        qx = None if qx is None else qx.contiguous()
+        qw = None if qw is None else qw.contiguous()
+        qb = None if qb is None else qb.contiguous()
+        dgy, dx = torch.empty_like(x), torch.empty_like(x)
+        part = x.new_empty(npart, 3, x.shape[2])
+        _lib.call("e2v2_rmsnorm_bwd2", _p(x), _p(w), _p(gy), _p(qx), _p(qw), _p(qb), _p(dgy), _p(dx), _p(part),
+                  _lib.i32(n), _lib.i32(npart), _lib.f32(ctx.eps), sparse_ops._stream(x.device))
+        return dgy, dx, part.sum(0), None
+
+
 def rms_norm(mod, x: torch.Tensor) -> torch.Tensor:
     """EquivariantRMSNormArraySphericalHarmonicsV2_BL (module_utils.py:1663-1772):
     row 0 centred over the channels, the degree-balanced mean square over rows
-    and channels, the affine weight of each row's degree, the bias on row 0."""
+    and channels, the affine weight of each row's degree, the bias on row 0.
+    fp32 GPU rows [9, N, 256] run _RMSNormFn; other inputs the composition below."""
+    if (x.is_cuda and x.dtype == torch.float32 and x.dim() == 3 and tuple(x.shape[::2]) == (9, 256)
+            and mod.lmax == 2 and mod.affine_weight.dtype == torch.float32 and mod.affine_weight.is_contiguous()):
+        return _RMSNormFn.apply(x.contiguous(), mod.affine_weight, mod.affine_bias, float(mod.eps))
     r0 = _row0(x.shape[0], x)
     f = x - x.mean(dim=2, keepdim=True) * r0
     bw = mod.balance_degree_weight.view(-1, 1, 1).to(x.dtype)
