@@ -475,6 +475,11 @@ int e2v2_rmsnorm_bwd2(const float* x, const float* w, const float* gy, const flo
 int e2v2_gate_fwd(const float* sc, const float* x, float* y, int n, float k1, float k2, hipStream_t s);
 int e2v2_gate_bwd(const float* sc, const float* x, const float* gy, float* gsc, float* gx, int n, float k1,
                   float k2, hipStream_t s);
+/* Derivative of e2v2_gate_bwd for the training path's second differentiation (torch's double backward of
+   Gate_s3's silu / sigmoid products): given the upstream gradients qsc [N][768] on gsc and qx [9][N][256] on gx
+   (each may be NULL: zero), dgy, dx [9][N][256] and dsc [N][768]. */
+int e2v2_gate_bwd2(const float* sc, const float* x, const float* gy, const float* qsc, const float* qx, float* dgy,
+                   float* dsc, float* dx, int n, float k1, float k2, hipStream_t s);
 
 /* Q/K scalarisation of SO3_Linear2Scalar_e2former (module_utils.py:2241-2266):
  * y [9][N][4 hid] = (q_a | q_b | k_a | k_b) -> hq, hk [N][3 hid], h[l hid + c] = sum_{m in l} a b */

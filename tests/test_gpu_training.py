@@ -253,6 +253,38 @@ def test_rms_norm_second_order(pkg, cuda):
         assert err < (1e-5 if k < 4 else 1e-4), (names[k], err)
 
 
+def test_gate_second_order(pkg, cuda):
+    """The fused Gate_s3 activations of the training path (e2v2_gate_fwd / _bwd /
+    _bwd2) against the float64 composition on the CPU: values, first-order
+    gradients of x and the gate Linear's weight (1e-5 relative L2), and the
+    gradients of L = <gx, R0> + <dWg, R1> in x, the weight and the upstream gy
+    (1e-4)."""
+    import copy
+    from ubio_molfm_amd import modules
+    from ubio_molfm_amd import second_order as so
+    torch.manual_seed(6)
+    mod = modules.Gate_s3(256, 2).to(cuda)
+    N = 700
+    x = torch.randn(9, N, 256, device=cuda)
+    gy = torch.randn_like(x)
+    R = [torch.randn_like(x), torch.randn_like(mod.gates.weight)]
+
+    def run(m, dtype, dev):
+        xx = x.to(dev, dtype).requires_grad_(True)
+        gg = gy.to(dev, dtype).requires_grad_(True)
+        y = so.gate_s3(m, xx, 1.679, 1.842)
+        gx, dW = torch.autograd.grad(y, (xx, m.gates.weight), gg, create_graph=True)
+        L = (gx * R[0].to(dev, dtype)).sum() + (dW * R[1].to(dev, dtype)).sum()
+        return [y, gx, dW] + list(torch.autograd.grad(L, (xx, m.gates.weight, gg)))
+
+    got = run(mod, torch.float32, cuda)
+    ref = run(copy.deepcopy(mod).double().cpu(), torch.float64, "cpu")
+    names = ["y", "gx", "dW", "d2x", "d2W", "d2gy"]
+    for k, (a, r) in enumerate(zip(got, ref)):
+        err = _rel(a, r)
+        assert err < (1e-5 if k < 3 else 1e-4), (names[k], err)
+
+
 def test_eval_mode_keeps_the_fused_path(pkg, cuda):
     """eval(): the fused kernels run (their backward is first order, so a
     create_graph=True differentiation raises instead of silently dropping the

@@ -20,7 +20,7 @@ EXPORTS = [
     "e2v2_attn_fwd", "e2v2_attn_bwd", "e2v2_attn_bwd_workspace", "e2v2_deg_fwd", "e2v2_deg_bwd",
     "e2v2_deg_bwd_workspace", "e2v2_deg_hidden_fwd", "e2v2_deg_hidden_bwd", "e2v2_deg_bias_grad",
     "e2v2_edge_to_pos", "e2v2_rmsnorm_fwd", "e2v2_add_rmsnorm_fwd", "e2v2_rmsnorm_bwd", "e2v2_rmsnorm_bwd_param", "e2v2_rmsnorm_bwd2", "e2v2_gate_fwd",
-    "e2v2_gate_bwd", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd", "e2v2_ln_silu_bwd_param", "e2v2_ln_silu_bwd2",
+    "e2v2_gate_bwd", "e2v2_gate_bwd2", "e2v2_ln_silu_fwd", "e2v2_ln_silu_bwd", "e2v2_ln_silu_bwd_param", "e2v2_ln_silu_bwd2",
     "e2v2_pairdot_fwd", "e2v2_pairdot_bwd", "e2v2_qk_proj_fwd", "e2v2_qk_proj_bwd",
     "e2v2_qk_proj_fwd_bf16", "e2v2_qk_proj_bwd_bf16",
     "e2v2_segment_metadata", "e2v2_pair_count", "e2v2_pair_emit", "e2v2_seg_dot", "e2v2_seg_reduce",

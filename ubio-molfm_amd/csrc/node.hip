@@ -155,6 +155,49 @@ __global__ void k_gate_bwd(const float* __restrict__ sc, const float* __restrict
   gs[2 * kNC + c] = a2 * k2 * sg2 * (1.0f - sg2);
 }
 
+// Derivative of the Gate_s3 backward (k_gate_bwd) for the training path's second differentiation:
+// given the upstream gradients qsc [N][768] on gsc and qx [9][N][256] on gx (each may be NULL: zero),
+// with s_l the logits of degree l at (i, c), sg_l = sigmoid(s_l), sg'_l = sg_l (1 - sg_l),
+// sg''_l = sg'_l (1 - 2 sg_l), silu'(s) = sg (1 + s (1 - sg)), silu''(s) = sg (1 - sg) (2 + s (1 - 2 sg)):
+//   dgy_0 = q_0 k1 silu'(s_0),   dgy_m = k2 (q_l sg'_l x_m + qx_m sg_l)   (m >= 1, l = l(m)),
+//   dx_0 = 0,                     dx_m = k2 q_l sg'_l gy_m,
+//   dsc_0 = q_0 k1 silu''(s_0) gy_0,   dsc_l = k2 (q_l sg''_l sum_{m in l} gy_m x_m + sg'_l sum_{m in l} qx_m gy_m).
+__global__ void k_gate_bwd2(const float* __restrict__ sc, const float* __restrict__ x, const float* __restrict__ gy,
+                            const float* __restrict__ qsc, const float* __restrict__ qx, float* __restrict__ dgy,
+                            float* __restrict__ dsc, float* __restrict__ dx, int n, float k1, float k2) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)n * kNC) return;
+  const int i = (int)(idx / kNC), c = (int)(idx % kNC);
+  const size_t st = (size_t)n * kNC;
+  const size_t srow = (size_t)i * 3 * kNC;
+  float sl[3], sg[3], d1[3], q[3];
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    sl[l] = sc[srow + l * kNC + c];
+    sg[l] = sigmoidf_(sl[l]);
+    d1[l] = sg[l] * (1.0f - sg[l]);
+    q[l] = qsc ? qsc[srow + l * kNC + c] : 0.f;
+  }
+  const float g0 = gy[idx];
+  dgy[idx] = q[0] * k1 * (sg[0] * (1.0f + sl[0] * (1.0f - sg[0])));
+  dx[idx] = 0.f;
+  dsc[srow + c] = q[0] * k1 * (d1[0] * (2.0f + sl[0] * (1.0f - 2.0f * sg[0]))) * g0;
+  float gxs[3] = {0.f, 0.f, 0.f}, qgs[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 1; m < 9; ++m) {
+    const int l = m < 4 ? 1 : 2;
+    const float g = gy[idx + m * st], xv = x[idx + m * st];
+    const float qv = qx ? qx[idx + m * st] : 0.f;
+    dgy[idx + m * st] = k2 * (q[l] * d1[l] * xv + qv * sg[l]);
+    dx[idx + m * st] = k2 * q[l] * d1[l] * g;
+    gxs[l] = fmaf(g, xv, gxs[l]);
+    qgs[l] = fmaf(qv, g, qgs[l]);
+  }
+#pragma unroll
+  for (int l = 1; l < 3; ++l)
+    dsc[srow + l * kNC + c] = k2 * (q[l] * (d1[l] * (1.0f - 2.0f * sg[l])) * gxs[l] + d1[l] * qgs[l]);
+}
+
 // ---- rms_norm_sh on the training path, where the forces are differentiated once more.  Per node
 // (f = x with row 0 centred over the channels, r = (S + eps)^-1/2, S = <bal f^2> over the channels and
 // summed over the rows, P = gy w, C = 256):
@@ -299,6 +342,17 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd2(const float* __restrict__ 
 }  // namespace e2v2
 
 using namespace e2v2;
+
+E2V2_API int e2v2_gate_bwd2(const float* sc, const float* x, const float* gy, const float* qsc, const float* qx,
+                            float* dgy, float* dsc, float* dx, int n, float k1, float k2, hipStream_t s) {
+  E2V2_REQUIRE(n >= 0, "gate_bwd2: n %d", n);
+  if (n == 0) return 0;
+  const int64_t tot = (int64_t)n * e2v2::kNC;
+  hipLaunchKernelGGL(e2v2::k_gate_bwd2, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, sc, x, gy, qsc, qx, dgy,
+                     dsc, dx, n, k1, k2);
+  E2V2_LAUNCHED("k_gate_bwd2");
+  return 0;
+}
 
 E2V2_API int e2v2_rmsnorm_bwd_param(const float* x, const float* w, const float* gy, float* gx, float* part, int n,
                                     int n_part, float eps, hipStream_t s) {

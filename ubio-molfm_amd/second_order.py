@@ -352,12 +352,61 @@ def rms_norm(mod, x: torch.Tensor) -> torch.Tensor:
     return f * (fn * w) + r0 * mod.affine_bias.reshape(-1)
 
 
+class _GateActFn(torch.autograd.Function):
+    """Gate_s3's activations on x [9, N, 256] from the logits sc [N, 768]
+    (e2v2_gate_fwd); backward _GateActGradFn, differentiable once more."""
+
+    @staticmethod
+    def forward(ctx, sc, x, k1: float, k2: float):
+        y = torch.empty_like(x)
+        _lib.call("e2v2_gate_fwd", _p(sc), _p(x), _p(y), _lib.i32(x.shape[1]), _lib.f32(k1), _lib.f32(k2),
+                  sparse_ops._stream(x.device))
+        ctx.save_for_backward(sc, x)
+        ctx.k = (k1, k2)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        sc, x = ctx.saved_tensors
+        gsc, gx = _GateActGradFn.apply(gy, sc, x, *ctx.k)
+        return gsc, gx, None, None
+
+
+class _GateActGradFn(torch.autograd.Function):
+    """(gsc, gx) of _GateActFn given gy (e2v2_gate_bwd); backward e2v2_gate_bwd2."""
+
+    @staticmethod
+    def forward(ctx, gy, sc, x, k1: float, k2: float):
+        gy = gy.contiguous()
+        gsc, gx = torch.empty_like(sc), torch.empty_like(x)
+        _lib.call("e2v2_gate_bwd", _p(sc), _p(x), _p(gy), _p(gsc), _p(gx), _lib.i32(x.shape[1]), _lib.f32(k1),
+                  _lib.f32(k2), sparse_ops._stream(x.device))
+        ctx.save_for_backward(gy, sc, x)
+        ctx.k = (k1, k2)
+        ctx.set_materialize_grads(False)
+        return gsc, gx
+
+    @staticmethod
+    def backward(ctx, qsc, qx):
+        gy, sc, x = ctx.saved_tensors
+        qsc = None if qsc is None else qsc.contiguous()
+        qx = None if qx is None else qx.contiguous()
+        dgy, dsc, dx = torch.empty_like(x), torch.empty_like(sc), torch.empty_like(x)
+        _lib.call("e2v2_gate_bwd2", _p(sc), _p(x), _p(gy), _p(qsc), _p(qx), _p(dgy), _p(dsc), _p(dx),
+                  _lib.i32(x.shape[1]), _lib.f32(ctx.k[0]), _lib.f32(ctx.k[1]), sparse_ops._stream(x.device))
+        return dgy, dsc, dx, None, None
+
+
 def gate_s3(mod, x: torch.Tensor, silu_norm: float, sigmoid_norm: float) -> torch.Tensor:
     """Gate_s3 (module_utils.py:2694-2746): logits from row 0, SiLU on row 0,
-    the sigmoid of each degree's logits on its rows."""
+    the sigmoid of each degree's logits on its rows.  fp32 GPU rows [9, N, 256]
+    take the activations through _GateActFn; other inputs the composition."""
     C, n, N = mod.sphere_channels, x.shape[0], x.shape[1]
     lmax = math.isqrt(n) - 1
     x0, xr = x.split([1, n - 1], dim=0)
+    if x.is_cuda and x.dtype == torch.float32 and n == 9 and C == 256 and x.shape[2] == 256:
+        sc = mod.gates(x0.squeeze(0)).contiguous()
+        return _GateActFn.apply(sc, x.contiguous(), float(silu_norm), float(sigmoid_norm))
     s0, sr = mod.gates(x0.squeeze(0)).split([C, lmax * C], dim=1)
     g = torch.sigmoid(sr).view(N, lmax, C).transpose(0, 1)                # [lmax, N, C]
     g = g.index_select(0, _expand(lmax, x.device)[1:] - 1)                # row m <- its degree
