@@ -517,6 +517,31 @@ class EdgeInput:
         return run_seq(net[1:], h)
 
 
+class _RowMaxFn(torch.autograd.Function):
+    """m[i, h] = max over the edges of row i of logit[e, h] (scatter_reduce amax from
+    -inf, e2former.py:335-347), with scatter_reduce's gradient -- g[i, h] split evenly
+    over the edges that attain the maximum -- composed from the segment gather and
+    row sum, so its own derivative comes from those ops (the tie mask is piecewise
+    constant in the logits)."""
+
+    @staticmethod
+    def forward(ctx, logit, edges):
+        H = logit.shape[1]
+        m = torch.full((edges.N, H), -torch.inf, dtype=logit.dtype, device=logit.device)
+        m = m.scatter_reduce(0, edges.qi.view(-1, 1).expand(-1, H), logit, reduce="amax", include_self=True)
+        ctx.save_for_backward(logit, m)
+        ctx.edges = edges
+        return m
+
+    @staticmethod
+    def backward(ctx, g):
+        logit, m = ctx.saved_tensors
+        edges = ctx.edges
+        tie = (logit == edges.gather_q(m)).to(logit.dtype)
+        cnt = edges.row_sum(tie).clamp_min(1.0)
+        return edges.gather_q(g / cnt) * tie, None
+
+
 def attention_weights(logit, p, ih, edges: TrainEdges, form: str) -> torch.Tensor:
     """alpha [E, H] (e2former.py:327-364): the segmented softmax with the row
     maximum by scatter_reduce(amax) (its gradient split over ties) and the
@@ -525,10 +550,7 @@ def attention_weights(logit, p, ih, edges: TrainEdges, form: str) -> torch.Tenso
         return F.softplus(logit) * ih * p.unsqueeze(-1)
     if form == "sigmoid":
         return torch.sigmoid(logit) * ih * p.unsqueeze(-1)
-    H = logit.shape[1]
-    idx = edges.qi.view(-1, 1).expand(-1, H)
-    amax = torch.full((edges.N, H), -torch.inf, dtype=logit.dtype, device=logit.device)
-    amax = amax.scatter_reduce(0, idx, logit, reduce="amax", include_self=True)
+    amax = _RowMaxFn.apply(logit, edges)
     e = torch.exp(logit - edges.gather_q(amax)) * p.unsqueeze(-1)
     s = edges.row_sum(e)
     return e * ih * edges.gather_q(1.0 / (s + 1e-3))       # the reciprocal per row, not per edge
