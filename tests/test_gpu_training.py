@@ -285,6 +285,56 @@ def test_gate_second_order(pkg, cuda):
         assert err < (1e-5 if k < 3 else 1e-4), (names[k], err)
 
 
+def test_row_max_ties_match_scatter_reduce(pkg, cuda):
+    """The softmax row maximum of the training path (_RowMaxFn: scatter_reduce amax
+    forward, its tie-split gradient composed from the segment gather and row sum)
+    against torch's scatter_reduce on logits with many exact ties, rows of 0-7
+    edges: the maximum, the first-order gradient and the gradient of
+    <d logit, R> in the upstream g."""
+    from ubio_molfm_amd import sparse_ops
+    from ubio_molfm_amd import second_order as so
+    g = torch.Generator().manual_seed(8)
+    N, H = 300, 16
+    deg = torch.randint(0, 8, (N,), generator=g)
+    qi = torch.repeat_interleave(torch.arange(N), deg).to(cuda)
+    E = qi.numel()
+    logit = torch.randint(-3, 3, (E, H), generator=g).float().to(cuda)
+
+    class Edges:
+        def __init__(self):
+            self.qi, self.N, self.row32 = qi, N, qi.int()
+            self.row_ptr = torch.cat([torch.zeros(1, dtype=torch.long), deg.cumsum(0)]).int().to(cuda)
+            self.eid = torch.arange(E, dtype=torch.int32, device=cuda)
+
+        def gather_q(self, x):
+            return sparse_ops.sparse_gather_edge_index(x, self.row32, self.N, (self.row_ptr, self.eid))
+
+        def row_sum(self, a):
+            return sparse_ops.sparse_alpha_sum_edge_index_triton(a, self.row32, self.N,
+                                                                metadata=(self.row_ptr, self.eid))
+
+    up = torch.randn(N, H, device=cuda)
+    R = torch.randn(E, H, device=cuda)
+
+    def run(f):
+        x = logit.clone().requires_grad_(True)
+        gg = up.clone().requires_grad_(True)
+        m = f(x)
+        gx, = torch.autograd.grad(m, x, gg, create_graph=True)
+        d2, = torch.autograd.grad((gx * R).sum(), gg)
+        return m.detach(), gx.detach(), d2
+
+    def ref(x):
+        m = torch.full((N, H), -torch.inf, device=cuda)
+        return m.scatter_reduce(0, qi.view(-1, 1).expand(-1, H), x, reduce="amax", include_self=True)
+
+    got, want = run(lambda x: so._RowMaxFn.apply(x, Edges())), run(ref)
+    rows = deg.to(cuda) > 0
+    assert torch.equal(got[0][rows], want[0][rows])
+    for a, b in zip(got[1:], want[1:]):
+        assert torch.allclose(a, b, rtol=1e-6, atol=1e-7)
+
+
 def test_eval_mode_keeps_the_fused_path(pkg, cuda):
     """eval(): the fused kernels run (their backward is first order, so a
     create_graph=True differentiation raises instead of silently dropping the
