@@ -570,7 +570,8 @@ def qkdot_gate(ga, x: torch.Tensor, edges: TrainEdges, x_edge: EdgeInput):
     """(gate, inputhead) of the QKdot variants (e2former.py:270-300)."""
     H = ga.num_attn_heads
     xd = so3_linear(ga.dot_linear, x)                                        # [9, N, Cd]
-    xq = xd.index_select(1, edges.qi)                                        # [9, E, Cd]
+    L9, N, Cd = xd.shape
+    xq = edges.gather_q(xd.permute(1, 0, 2).reshape(N, L9 * Cd)).view(-1, L9, Cd).permute(1, 0, 2)  # [9, E, Cd]
     if ga.tp_type == "QKdot_alpha":
         Y = _sh_integral(edges.dvec)                                         # [E, 9]
         x0 = torch.cat([(Y[:, l * l:(l + 1) ** 2].t().unsqueeze(-1) * xq[l * l:(l + 1) ** 2]).sum(0)
